@@ -1,0 +1,164 @@
+"""Python binding of libnnh (include/nnh.h) for tests and benchmarks.
+
+The product is the C ABI in lib/libnnh.so; this module only loads it with ctypes and passes device
+pointers of torch tensors (torch is used for device memory and streams). Every call raises NnhError
+(ShapeError for nn-cpp's TensorShapeError) when the library returns a non-zero status, and the module
+refuses to run at all when the library is missing: there is no fallback path.
+"""
+import ctypes as C
+import os
+
+PKG_ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+LIB_PATH = os.path.join(PKG_ROOT, "lib", "libnnh.so")
+REPO_ROOT = os.path.dirname(PKG_ROOT)
+HEADER_PATH = os.path.join(REPO_ROOT, "include", "nnh.h")
+
+OK, ERR_INVALID, ERR_SHAPE, ERR_ALIAS, ERR_HIP = 0, 1, 2, 3, 4
+BIAS_NONE, BIAS_COL, BIAS_ROW = 0, 1, 2
+MAX_BATCH_DIMS = 4
+
+
+class NnhError(RuntimeError):
+    def __init__(self, code, msg):
+        super().__init__(f"nnh error {code}: {msg}")
+        self.code = code
+
+
+class ShapeError(NnhError):
+    """nn-cpp's TensorShapeError."""
+
+
+class Batch(C.Structure):
+    _fields_ = [("ndim", C.c_int), ("shape", C.c_size_t * MAX_BATCH_DIMS),
+                ("stride_a", C.c_ssize_t * MAX_BATCH_DIMS), ("stride_b", C.c_ssize_t * MAX_BATCH_DIMS),
+                ("stride_c", C.c_ssize_t * MAX_BATCH_DIMS)]
+
+
+class Epilogue(C.Structure):
+    _fields_ = [("bias_mode", C.c_int), ("relu", C.c_int), ("bias", C.c_void_p), ("alive", C.c_void_p)]
+
+
+_lib = None
+_sz = C.c_size_t
+_vp = C.c_void_p
+_szp = C.POINTER(C.c_size_t)
+
+
+def _declare(L):
+    gemm = [C.c_int, C.c_int, _sz, _sz, _sz, _vp, _sz, _vp, _sz, _vp, _sz, C.c_int]
+    L.nnh_last_error.restype = C.c_char_p
+    L.nnh_version.restype = C.c_char_p
+    L.nnh_sgemm.argtypes = gemm + [_vp]
+    L.nnh_sgemm_batched.argtypes = gemm + [C.POINTER(Batch), C.POINTER(Epilogue), _vp]
+    L.nnh_sgemm_config.argtypes = gemm + [C.POINTER(Batch), C.POINTER(Epilogue), C.c_int, _vp]
+    L.nnh_gemm_config_name.restype = C.c_char_p
+    L.nnh_matmul_shape.argtypes = [_szp, C.c_int, _szp, C.c_int, C.c_int, C.c_int, _szp, C.POINTER(C.c_int)]
+    L.nnh_matmul.argtypes = [_vp, _szp, C.c_int, _vp, _szp, C.c_int, C.c_int, C.c_int, _vp, _vp]
+    for name, args in _EXTRA_DECLS.items():
+        if hasattr(L, name):
+            getattr(L, name).argtypes = args
+
+
+_EXTRA_DECLS = {}
+
+
+def lib():
+    """The loaded library; raises if it has not been built (no fallback exists)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} is missing: build it with `make -C nn-cpp_amd` "
+                               "(or __graft_entry__.build()); nnh has no CPU fallback")
+        L = C.CDLL(LIB_PATH)
+        _declare(L)
+        _lib = L
+    return _lib
+
+
+def check(rc):
+    if rc != OK:
+        msg = lib().nnh_last_error().decode()
+        raise (ShapeError if rc == ERR_SHAPE else NnhError)(rc, msg)
+
+
+def header_functions():
+    """Names of every function include/nnh.h declares."""
+    import re
+    text = open(HEADER_PATH).read()
+    return sorted(set(re.findall(r"\b(nnh_[a-z0-9_]+)\s*\(", text)))
+
+
+# ---- torch plumbing ----
+
+def _stream(stream):
+    import torch
+    if stream is None:
+        stream = torch.cuda.current_stream()
+    return C.c_void_p(stream.cuda_stream)
+
+
+def _ptr(t, offset=0):
+    if t is None:
+        return None
+    import torch
+    assert t.dtype == torch.float32 or t.dtype == torch.uint8, t.dtype
+    assert t.is_cuda, "nnh works on device tensors"
+    return C.c_void_p(t.data_ptr() + offset * t.element_size())
+
+
+def make_batch(shape=(), sa=(), sb=(), sc=()):
+    b = Batch()
+    b.ndim = len(shape)
+    for i, d in enumerate(shape):
+        b.shape[i], b.stride_a[i], b.stride_b[i], b.stride_c[i] = d, sa[i], sb[i], sc[i]
+    return b
+
+
+def make_epilogue(bias_mode=BIAS_NONE, bias=None, relu=False, alive=None):
+    e = Epilogue()
+    e.bias_mode = bias_mode
+    e.relu = int(bool(relu))
+    e.bias = _ptr(bias).value if bias is not None else None
+    e.alive = _ptr(alive).value if alive is not None else None
+    return e
+
+
+def sgemm(ta, tb, m, n, k, a, lda, b, ldb, c, ldc, accumulate=False, stream=None):
+    """nn::kernels::sgemm on device tensors a, b, c (their first element is the matrix origin)."""
+    check(lib().nnh_sgemm(int(ta), int(tb), m, n, k, _ptr(a), lda, _ptr(b), ldb, _ptr(c), ldc, int(accumulate),
+                          _stream(stream)))
+
+
+def sgemm_batched(ta, tb, m, n, k, a, lda, b, ldb, c, ldc, accumulate=False, batch=None, epilogue=None,
+                  config=-1, stream=None):
+    bp = C.byref(batch) if batch is not None else None
+    ep = C.byref(epilogue) if epilogue is not None else None
+    check(lib().nnh_sgemm_config(int(ta), int(tb), m, n, k, _ptr(a), lda, _ptr(b), ldb, _ptr(c), ldc,
+                                 int(accumulate), bp, ep, int(config), _stream(stream)))
+
+
+def gemm_configs():
+    L = lib()
+    return [L.nnh_gemm_config_name(i).decode() for i in range(L.nnh_gemm_config_count())]
+
+
+def matmul_shape(a_shape, b_shape, ta=False, tb=False):
+    ash = (C.c_size_t * max(1, len(a_shape)))(*a_shape)
+    bsh = (C.c_size_t * max(1, len(b_shape)))(*b_shape)
+    out = (C.c_size_t * 16)()
+    nd = C.c_int(0)
+    check(lib().nnh_matmul_shape(ash, len(a_shape), bsh, len(b_shape), int(ta), int(tb), out, C.byref(nd)))
+    return tuple(out[i] for i in range(nd.value))
+
+
+def matmul(a, b, ta=False, tb=False, stream=None):
+    """nn::matmul(a, b, ta, tb) on contiguous device tensors; returns a new tensor."""
+    import torch
+    assert a.is_contiguous() and b.is_contiguous()
+    shape = matmul_shape(a.shape, b.shape, ta, tb)
+    out = torch.empty(shape, dtype=torch.float32, device=a.device)
+    ash = (C.c_size_t * a.dim())(*a.shape)
+    bsh = (C.c_size_t * b.dim())(*b.shape)
+    check(lib().nnh_matmul(_ptr(a), ash, a.dim(), _ptr(b), bsh, b.dim(), int(ta), int(tb), _ptr(out),
+                           _stream(stream)))
+    return out

@@ -1,0 +1,194 @@
+// gemm.hip - instantiations, depth-cut reduction and launch logic of the fp32 MFMA GEMM.
+#include "gemm.hpp"
+
+#include <algorithm>
+#include <mutex>
+
+namespace nnh {
+
+namespace {
+
+__device__ __forceinline__ float finish(float v, int64_t row, int64_t col, int64_t off, const Epilogue& ep,
+                                        unsigned char* alive) {
+	if (ep.bias_mode == kBiasCol) v = v + ep.bias[col];
+	else if (ep.bias_mode == kBiasRow) v = v + ep.bias[row];
+	if (ep.relu) {
+		const bool on = v > 0.0f;
+		if (alive) alive[off] = on ? 1 : 0;
+		v = on ? v : 0.0f;
+	}
+	return v;
+}
+
+// Depth-cut second pass (gemm.cpp:475-484): acc = piece 0, then += each later piece in order;
+// C = acc, or C = C + acc when accumulating. One thread per element, no atomics.
+__global__ void __launch_bounds__(256) reduce_pieces_kernel(const float* __restrict__ part, int pieces, int m, int n,
+                                                            float* c, int64_t ldc, int accumulate, BatchDesc batch,
+                                                            int64_t batch_count, Epilogue ep) {
+	const int64_t mn = (int64_t)m * n;
+	const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+	if (idx >= mn * batch_count) return;
+	const int64_t bi = idx / mn, e = idx % mn;
+	const int64_t row = e / n, col = e % n;
+	const float* pp = part + bi * pieces * mn + e;
+	float acc = pp[0];
+	for (int q = 1; q < pieces; ++q) acc = acc + pp[q * mn];
+	int64_t oa, ob, oc = 0;
+	if (batch.ndim > 0) batch_offsets(batch, bi, oa, ob, oc);
+	const int64_t off = row * ldc + col;
+	float* cp = c + oc;
+	float v = accumulate ? cp[off] + acc : acc;
+	cp[off] = finish(v, row, col, off, ep, ep.alive ? ep.alive + oc : nullptr);
+}
+
+using KernelFn = void (*)(const GemmArgs);
+
+struct Config {
+	const char* name;
+	int bm, bn, bk;
+	int lds_bytes[4];      // per (ta, tb)
+	KernelFn fn[4][2];     // [ta*2 + tb][edge]
+};
+
+template <int BM, int BN, int BK, int WM, int WN>
+Config make_config(const char* name) {
+	Config c{};
+	c.name = name;
+	c.bm = BM;
+	c.bn = BN;
+	c.bk = BK;
+#define NNH_SET(TA, TB)                                                                                  \
+	c.lds_bytes[TA * 2 + TB] = TileShape<BM, BN, BK, WM, WN, TA, TB>::kLdsFloats * (int)sizeof(float);   \
+	c.fn[TA * 2 + TB][0] = sgemm_tile_kernel<BM, BN, BK, WM, WN, TA, TB, false>;                         \
+	c.fn[TA * 2 + TB][1] = sgemm_tile_kernel<BM, BN, BK, WM, WN, TA, TB, true>;
+	NNH_SET(false, false)
+	NNH_SET(false, true)
+	NNH_SET(true, false)
+	NNH_SET(true, true)
+#undef NNH_SET
+	return c;
+}
+
+const Config* configs() {
+	static const Config table[] = {
+		make_config<256, 128, 16, 128, 64>("256x128x16_w128x64"),
+		make_config<128, 128, 32, 64, 64>("128x128x32_w64x64"),
+		make_config<64, 128, 32, 64, 32>("64x128x32_w64x32"),
+	};
+	return table;
+}
+constexpr int kNumConfigs = 3;
+
+// Raises each kernel's dynamic LDS limit once per device (gfx950 has 160 KiB per CU).
+hipError_t prepare_device() {
+	static std::mutex mu;
+	static bool done[64] = {};
+	int dev = 0;
+	hipError_t e = hipGetDevice(&dev);
+	if (e != hipSuccess) return e;
+	if (dev < 0 || dev >= 64) return hipErrorInvalidDevice;
+	std::lock_guard<std::mutex> lock(mu);
+	if (done[dev]) return hipSuccess;
+	const Config* cfg = configs();
+	for (int i = 0; i < kNumConfigs; ++i)
+		for (int f = 0; f < 4; ++f)
+			for (int edge = 0; edge < 2; ++edge) {
+				e = hipFuncSetAttribute(reinterpret_cast<const void*>(cfg[i].fn[f][edge]),
+				                        hipFuncAttributeMaxDynamicSharedMemorySize, cfg[i].lds_bytes[f]);
+				if (e != hipSuccess) return e;
+			}
+	done[dev] = true;
+	return hipSuccess;
+}
+
+int pick_config(const GemmCall& g) {
+	const Config* cfg = configs();
+	// largest tile that still gives every CU at least one workgroup
+	for (int i = 0; i < kNumConfigs; ++i) {
+		const int64_t tiles = ((g.m + cfg[i].bm - 1) / cfg[i].bm) * ((g.n + cfg[i].bn - 1) / cfg[i].bn) * g.batch_count;
+		if (tiles >= 256) return i;
+	}
+	return kNumConfigs - 1;
+}
+
+}  // namespace
+
+bool depth_cut(int64_t m, int64_t n, int64_t k) {
+	return !(m == 0 || n == 0 || m * n > (int64_t(1) << 16) || k < 4 * 128 || m * n * k < (int64_t(1) << 20));
+}
+
+int64_t gemm_workspace_floats(const GemmCall& g) {
+	if (!depth_cut(g.m, g.n, g.k)) return 0;
+	const int64_t pieces = (g.k + 127) / 128;
+	return pieces * g.m * g.n * g.batch_count;
+}
+
+int gemm_config_count() { return kNumConfigs; }
+const char* gemm_config_name(int config) {
+	return (config >= 0 && config < kNumConfigs) ? configs()[config].name : "";
+}
+
+hipError_t gemm_launch(const GemmCall& g, hipStream_t s, int config, float* workspace) {
+	if (g.m == 0 || g.n == 0 || g.batch_count == 0) return hipSuccess;
+	hipError_t e = prepare_device();
+	if (e != hipSuccess) return e;
+	if (config < 0 || config >= kNumConfigs) config = pick_config(g);
+	const Config& cf = configs()[config];
+
+	GemmArgs p{};
+	p.a = g.a;
+	p.b = g.b;
+	p.c = g.c;
+	p.lda = g.lda;
+	p.ldb = g.ldb;
+	p.ldc = g.ldc;
+	p.m = (int)g.m;
+	p.n = (int)g.n;
+	p.k = (int)g.k;
+	p.accumulate = g.accumulate;
+	p.tiles_m = (int)((g.m + cf.bm - 1) / cf.bm);
+	p.tiles_n = (int)((g.n + cf.bn - 1) / cf.bn);
+	p.batch_count = (int)g.batch_count;
+	p.batch = g.batch;
+	p.ep = g.ep;
+	const bool cut = depth_cut(g.m, g.n, g.k);
+	p.pieces = cut ? (int)((g.k + 127) / 128) : 1;
+	p.piece_k = cut ? 128 : (int)std::max<int64_t>(g.k, 1);
+	bool vec_ok = (g.lda % 4 == 0) && (g.ldb % 4 == 0) && (reinterpret_cast<uintptr_t>(g.a) % 16 == 0) &&
+	              (reinterpret_cast<uintptr_t>(g.b) % 16 == 0);
+	for (int d = 0; d < g.batch.ndim; ++d) vec_ok = vec_ok && g.batch.sa[d] % 4 == 0 && g.batch.sb[d] % 4 == 0;
+	p.vec_ok = vec_ok ? 1 : 0;
+	const bool interior = vec_ok && g.m % cf.bm == 0 && g.n % cf.bn == 0 && g.k % cf.bk == 0 && g.k > 0;
+
+	float* part = nullptr;
+	bool own = false;
+	if (cut) {
+		const int64_t need = gemm_workspace_floats(g);
+		if (workspace) {
+			part = workspace;
+		} else {
+			e = hipMallocAsync(reinterpret_cast<void**>(&part), need * sizeof(float), s);
+			if (e != hipSuccess) return e;
+			own = true;
+		}
+		p.partial = part;
+	}
+	const int64_t blocks = (int64_t)p.tiles_m * p.tiles_n * p.pieces * p.batch_count;
+	if (blocks > 0x7fffffff) return hipErrorInvalidConfiguration;
+	const int f = (g.ta ? 2 : 0) + (g.tb ? 1 : 0);
+	hipLaunchKernelGGL(cf.fn[f][interior ? 0 : 1], dim3((unsigned)blocks), dim3(256), cf.lds_bytes[f], s, p);
+	e = hipGetLastError();
+	if (e == hipSuccess && cut) {
+		const int64_t total = g.m * g.n * g.batch_count;
+		hipLaunchKernelGGL(reduce_pieces_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, part,
+		                   p.pieces, p.m, p.n, g.c, g.ldc, g.accumulate, g.batch, g.batch_count, g.ep);
+		e = hipGetLastError();
+	}
+	if (own) {
+		hipError_t e2 = hipFreeAsync(part, s);
+		if (e == hipSuccess) e = e2;
+	}
+	return e;
+}
+
+}  // namespace nnh

@@ -1,0 +1,44 @@
+// gemm.hpp - host-side launch API of the fp32 MFMA GEMM (internal to libnnh; the public C ABI is
+// include/nnh.h).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "gemm_tile.hpp"
+
+namespace nnh {
+
+// One GEMM, or a batch of GEMMs sharing m, n, k and leading dimensions, in nn::kernels::sgemm's
+// terms (include/nn/kernels/gemm.hpp:36-59): C = op(A) op(B) (+ C when accumulate), then the epilogue.
+struct GemmCall {
+	int ta = 0, tb = 0;
+	int64_t m = 0, n = 0, k = 0;
+	const float* a = nullptr;
+	int64_t lda = 0;
+	const float* b = nullptr;
+	int64_t ldb = 0;
+	float* c = nullptr;
+	int64_t ldc = 0;
+	int accumulate = 0;
+	BatchDesc batch{};        // ndim 0: a single matrix
+	int64_t batch_count = 1;
+	Epilogue ep{};
+};
+
+// nn-cpp's depth-cut rule (src/kernels/gemm.cpp:453-458): small output, long depth -> 128-deep pieces
+// summed in piece order. Applies per matrix.
+bool depth_cut(int64_t m, int64_t n, int64_t k);
+
+// Floats of workspace a call needs (0 when it takes no depth cut).
+int64_t gemm_workspace_floats(const GemmCall& g);
+
+// Launches on stream s. Kernel configuration: -1 picks one by shape; results never depend on it.
+// Workspace for a depth cut comes from workspace (if non-null, at least gemm_workspace_floats) or
+// else from the stream-ordered allocator.
+hipError_t gemm_launch(const GemmCall& g, hipStream_t s, int config = -1, float* workspace = nullptr);
+
+int gemm_config_count();
+const char* gemm_config_name(int config);
+
+}  // namespace nnh

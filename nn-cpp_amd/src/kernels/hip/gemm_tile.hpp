@@ -1,0 +1,327 @@
+// gemm_tile.hpp - the fp32 MFMA tile GEMM for gfx950 (CDNA4), shared by every GEMM-shaped op.
+//
+// Numerical contract (what makes the results identical to nn-cpp's NN_NATIVE sgemm):
+//   nn::kernels::sgemm's AVX2 microkernel computes each C element as a sequential fused
+//   multiply-add chain over the depth, starting at +0 (src/kernels/gemm.cpp:232-244); depth
+//   blocks of 256 store and reload the running sum unchanged (gemm.cpp:225-231, 371).
+//   On gfx950, v_mfma_f32_32x32x1_2b_f32 computes exactly fma(a, b, c) per output element
+//   (single rounding, denormals kept): measured against fmaf on 520k outputs, all equal.
+//   This kernel issues one such MFMA per depth index k, in increasing k, starting from +0,
+//   so every element is the same fma chain. The k order never depends on the tile shape,
+//   the grid, ld, alignment, batch or stream: results are a pure function of the inputs.
+//   With accumulate, the old C is added after the first min(K, 256) steps (Store::kAdd then
+//   Store::kContinue, gemm.cpp:245-252), exactly as the reference does.
+//
+// Tiling: 256 threads = 4 waves. A workgroup owns a BM x BN tile of C; wave w owns a WM x WN
+// sub-tile. One MFMA covers 64 rows x 32 columns (two 32x32 blocks: A lanes 0-31 and 32-63
+// carry 64 distinct rows, B lanes 32-63 repeat lanes 0-31's 32 columns).
+// Operands go global -> registers -> LDS (double buffered, one barrier per depth tile).
+// LDS layouts follow the global layout so that every global load and LDS store is 16 bytes:
+//   K-contiguous operands (A when !TA, B when TB) are stored [row][BK+4] and read as one
+//   ds_read_b128 giving 4 consecutive k; M/N-contiguous operands are stored [BK][rows] and read
+//   as 4 ds_read_b32 (one per k).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace nnh {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x32 __attribute__((ext_vector_type(32)));
+
+constexpr int kMaxBatchDims = 4;
+constexpr int kAccAfter = 256;  // nn-cpp's kKC (gemm.hpp:33): where an accumulating product adds old C
+
+// Batch addressing: up to 4 batch dims, element strides per dim for A, B, C (0 = broadcast).
+struct BatchDesc {
+	int ndim;
+	int64_t shape[kMaxBatchDims];
+	int64_t sa[kMaxBatchDims], sb[kMaxBatchDims], sc[kMaxBatchDims];
+};
+
+enum BiasMode : int { kBiasNone = 0, kBiasCol = 1, kBiasRow = 2 };
+
+// Applied to each finished element v (after any accumulate): v = v + bias; then, with relu,
+// alive = v > 0, v = alive ? v : 0 (src/autograd/ops.cpp:726-730, 1396-1409).
+struct Epilogue {
+	int bias_mode;
+	int relu;
+	const float* bias;
+	unsigned char* alive;  // optional, addressed like C
+};
+
+struct GemmArgs {
+	const float* a;
+	const float* b;
+	float* c;
+	int64_t lda, ldb, ldc;
+	int m, n, k;
+	int accumulate;
+	int tiles_m, tiles_n;
+	int batch_count;
+	int pieces;        // > 1: depth cut, each piece writes partial[(batch*pieces + piece)][m][n]
+	int piece_k;       // depth of one piece
+	int vec_ok;        // lda, ldb, strides multiples of 4 and a, b 16-byte aligned
+	float* partial;
+	BatchDesc batch;
+	Epilogue ep;
+};
+
+__device__ __forceinline__ void batch_offsets(const BatchDesc& d, int64_t bi, int64_t& oa, int64_t& ob,
+                                              int64_t& oc) {
+	oa = ob = oc = 0;
+	for (int i = d.ndim - 1; i >= 0; --i) {
+		const int64_t idx = bi % d.shape[i];
+		bi /= d.shape[i];
+		oa += idx * d.sa[i];
+		ob += idx * d.sb[i];
+		oc += idx * d.sc[i];
+	}
+}
+
+// Loads an R x CC row-major tile (CC % 4 == 0) starting at g: 16-byte loads, zeros outside
+// rows_valid x cols_valid when EDGE.
+template <int R, int CC, bool EDGE>
+__device__ __forceinline__ void load_tile(const float* __restrict__ g, int64_t ld, int rows_valid,
+                                          int cols_valid, bool vec_ok, f32x4* out, int tid) {
+	constexpr int kVecPerRow = CC / 4;
+	constexpr int kPer = R * CC / 4 / 256;
+	static_assert(kPer * 256 * 4 == R * CC, "tile must split evenly over 256 threads");
+#pragma unroll
+	for (int i = 0; i < kPer; ++i) {
+		const int idx = tid + 256 * i;
+		const int r = idx / kVecPerRow;
+		const int c = (idx % kVecPerRow) * 4;
+		if (!EDGE) {
+			out[i] = *reinterpret_cast<const f32x4*>(g + r * ld + c);
+		} else {
+			const bool row_in = r < rows_valid;
+			if (row_in && c + 3 < cols_valid && vec_ok) {
+				out[i] = *reinterpret_cast<const f32x4*>(g + r * ld + c);
+			} else {
+				f32x4 v;
+#pragma unroll
+				for (int e = 0; e < 4; ++e) v[e] = (row_in && c + e < cols_valid) ? g[r * ld + c + e] : 0.0f;
+				out[i] = v;
+			}
+		}
+	}
+}
+
+template <int R, int CC, int S>
+__device__ __forceinline__ void store_tile(float* lds, const f32x4* v, int tid) {
+	constexpr int kVecPerRow = CC / 4;
+	constexpr int kPer = R * CC / 4 / 256;
+#pragma unroll
+	for (int i = 0; i < kPer; ++i) {
+		const int idx = tid + 256 * i;
+		const int r = idx / kVecPerRow;
+		const int c = (idx % kVecPerRow) * 4;
+		*reinterpret_cast<f32x4*>(lds + r * S + c) = v[i];
+	}
+}
+
+template <int BM, int BN, int BK, int WM, int WN, bool TA, bool TB>
+struct TileShape {
+	static constexpr int kWavesN = BN / WN;
+	static_assert((BM / WM) * (BN / WN) == 4, "4 waves per workgroup");
+	static_assert(WM % 64 == 0 && WN % 32 == 0, "one MFMA covers 64 x 32");
+	static_assert(kAccAfter % BK == 0 && BK % 4 == 0, "depth tile must divide 256");
+	static constexpr int I = WM / 64, J = WN / 32;
+	// LDS strides (floats). K-major tiles get 4 floats of padding so that 64 lanes reading 16 bytes
+	// from 64 consecutive rows spread over the banks.
+	static constexpr int SA = TA ? BM : BK + 4;
+	static constexpr int SB = TB ? BK + 4 : BN;
+	static constexpr int kASize = TA ? BK * SA : BM * SA;
+	static constexpr int kBSize = TB ? BN * SB : BK * SB;
+	static constexpr int kStage = kASize + kBSize;
+	static constexpr int kLdsFloats = 2 * kStage;
+	static constexpr int LA = BM * BK / 4 / 256;
+	static constexpr int LB = BN * BK / 4 / 256;
+};
+
+// Maps the hardware workgroup id to a logical tile id so that consecutive logical ids (which share
+// A rows and B columns) run on the same XCD and therefore share its L2. Workgroups are dispatched to
+// the 8 XCDs round-robin by id.
+__device__ __forceinline__ int xcd_remap(int bid, int total) {
+	const int per = total / 8;
+	if (bid < per * 8) return (bid % 8) * per + bid / 8;
+	return bid;
+}
+
+template <int BM, int BN, int BK, int WM, int WN, bool TA, bool TB, bool EDGE>
+__global__ void __launch_bounds__(256) sgemm_tile_kernel(const GemmArgs p) {
+	using S = TileShape<BM, BN, BK, WM, WN, TA, TB>;
+	constexpr int I = S::I, J = S::J;
+	extern __shared__ __align__(16) float lds[];
+
+	const int tid = threadIdx.x;
+	const int lane = tid & 63;
+	const int wave = tid >> 6;
+	const int wm0 = (wave / S::kWavesN) * WM;
+	const int wn0 = (wave % S::kWavesN) * WN;
+
+	// ---- which tile, piece and batch matrix ----
+	const int tiles = p.tiles_m * p.tiles_n;
+	const int total = tiles * p.pieces * p.batch_count;
+	const int lid = xcd_remap(blockIdx.x, total);
+	const int t = lid % tiles;
+	const int rest = lid / tiles;
+	const int piece = rest % p.pieces;
+	const int bi = rest / p.pieces;
+	// grouped order: 8 tile-rows at a time, column-major inside the group
+	constexpr int G = 8;
+	const int group = t / (G * p.tiles_n);
+	const int first_m = group * G;
+	const int gsize = min(G, p.tiles_m - first_m);
+	const int in_group = t % (G * p.tiles_n);
+	const int tm = first_m + in_group % gsize;
+	const int tn = in_group / gsize;
+	const int m0 = tm * BM, n0 = tn * BN;
+
+	int64_t oa = 0, ob = 0, oc = 0;
+	if (p.batch.ndim > 0) batch_offsets(p.batch, bi, oa, ob, oc);
+	const float* __restrict__ A = p.a + oa;
+	const float* __restrict__ B = p.b + ob;
+
+	const int k_lo = piece * p.piece_k;
+	const int k_hi = min(p.k, k_lo + p.piece_k);
+	const int kr = k_hi - k_lo;
+	const int nkt = (kr + BK - 1) / BK;
+	// accumulate: old C joins the chain after the first min(K, 256) steps (whole product only)
+	const bool acc_mode = p.accumulate && p.pieces == 1;
+	const int acc_tile = (p.k > kAccAfter) ? kAccAfter / BK - 1 : -1;
+
+	f32x32 acc[I][J];
+#pragma unroll
+	for (int i = 0; i < I; ++i)
+#pragma unroll
+		for (int j = 0; j < J; ++j)
+#pragma unroll
+			for (int r = 0; r < 32; ++r) acc[i][j][r] = 0.0f;
+
+	const bool vec_ok = p.vec_ok != 0;
+	f32x4 ra[S::LA], rb[S::LB];
+	auto load = [&](int kt) {
+		const int k0 = k_lo + kt * BK;
+		if (!TA)  // A stored m x k: tile BM rows x BK
+			load_tile<BM, BK, EDGE>(A + (int64_t)m0 * p.lda + k0, p.lda, p.m - m0, k_hi - k0, vec_ok, ra, tid);
+		else      // A stored k x m: tile BK rows x BM
+			load_tile<BK, BM, EDGE>(A + (int64_t)k0 * p.lda + m0, p.lda, k_hi - k0, p.m - m0, vec_ok, ra, tid);
+		if (TB)   // B stored n x k
+			load_tile<BN, BK, EDGE>(B + (int64_t)n0 * p.ldb + k0, p.ldb, p.n - n0, k_hi - k0, vec_ok, rb, tid);
+		else      // B stored k x n
+			load_tile<BK, BN, EDGE>(B + (int64_t)k0 * p.ldb + n0, p.ldb, k_hi - k0, p.n - n0, vec_ok, rb, tid);
+	};
+	auto store = [&](int buf) {
+		float* As = lds + buf * S::kStage;
+		float* Bs = As + S::kASize;
+		if (!TA) store_tile<BM, BK, S::SA>(As, ra, tid);
+		else store_tile<BK, BM, S::SA>(As, ra, tid);
+		if (TB) store_tile<BN, BK, S::SB>(Bs, rb, tid);
+		else store_tile<BK, BN, S::SB>(Bs, rb, tid);
+	};
+
+	// C element (i, j, r) of this lane: row and column inside the workgroup tile
+	auto c_row = [&](int i, int r) { return wm0 + 64 * i + 32 * (r >> 4) + 8 * ((r & 15) >> 2) + 4 * (lane >> 5) + (r & 3); };
+	auto c_col = [&](int j) { return wn0 + 32 * j + (lane & 31); };
+
+	if (nkt > 0) {
+		load(0);
+		store(0);
+		__syncthreads();
+	}
+	for (int kt = 0; kt < nkt; ++kt) {
+		const int cur = kt & 1;
+		if (kt + 1 < nkt) load(kt + 1);
+		const float* As = lds + cur * S::kStage;
+		const float* Bs = As + S::kASize;
+#pragma unroll
+		for (int kk = 0; kk < BK; kk += 4) {
+			f32x4 af[I], bf[J];
+#pragma unroll
+			for (int i = 0; i < I; ++i) {
+				const int row = wm0 + 64 * i + lane;
+				if (!TA) {
+					af[i] = *reinterpret_cast<const f32x4*>(As + row * S::SA + kk);
+				} else {
+#pragma unroll
+					for (int e = 0; e < 4; ++e) af[i][e] = As[(kk + e) * S::SA + row];
+				}
+			}
+#pragma unroll
+			for (int j = 0; j < J; ++j) {
+				const int col = wn0 + 32 * j + (lane & 31);
+				if (TB) {
+					bf[j] = *reinterpret_cast<const f32x4*>(Bs + col * S::SB + kk);
+				} else {
+#pragma unroll
+					for (int e = 0; e < 4; ++e) bf[j][e] = Bs[(kk + e) * S::SB + col];
+				}
+			}
+#pragma unroll
+			for (int e = 0; e < 4; ++e)
+#pragma unroll
+				for (int i = 0; i < I; ++i)
+#pragma unroll
+					for (int j = 0; j < J; ++j)
+						acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x1f32(af[i][e], bf[j][e], acc[i][j], 0, 0, 0);
+		}
+		if (kt + 1 < nkt) store(cur ^ 1);
+		if (acc_mode && kt == acc_tile) {
+			// Store::kAdd after the first depth block: c_old + running sum
+#pragma unroll
+			for (int i = 0; i < I; ++i)
+#pragma unroll
+				for (int j = 0; j < J; ++j)
+#pragma unroll
+					for (int r = 0; r < 32; ++r) {
+						const int row = m0 + c_row(i, r), col = n0 + c_col(j);
+						if (!EDGE || (row < p.m && col < p.n))
+							acc[i][j][r] = p.c[oc + (int64_t)row * p.ldc + col] + acc[i][j][r];
+					}
+		}
+		__syncthreads();
+	}
+
+	// ---- epilogue ----
+	if (p.pieces > 1) {
+		float* part = p.partial + ((int64_t)bi * p.pieces + piece) * (int64_t)p.m * p.n;
+#pragma unroll
+		for (int i = 0; i < I; ++i)
+#pragma unroll
+			for (int j = 0; j < J; ++j)
+#pragma unroll
+				for (int r = 0; r < 32; ++r) {
+					const int row = m0 + c_row(i, r), col = n0 + c_col(j);
+					if (!EDGE || (row < p.m && col < p.n)) part[(int64_t)row * p.n + col] = acc[i][j][r];
+				}
+		return;
+	}
+	const bool add_old_at_end = acc_mode && p.k <= kAccAfter;
+	float* __restrict__ Cp = p.c + oc;
+	unsigned char* alive = p.ep.alive ? p.ep.alive + oc : nullptr;
+#pragma unroll
+	for (int i = 0; i < I; ++i)
+#pragma unroll
+		for (int j = 0; j < J; ++j)
+#pragma unroll
+			for (int r = 0; r < 32; ++r) {
+				const int row = m0 + c_row(i, r), col = n0 + c_col(j);
+				if (EDGE && (row >= p.m || col >= p.n)) continue;
+				const int64_t off = (int64_t)row * p.ldc + col;
+				float v = acc[i][j][r];
+				if (add_old_at_end) v = (p.k > 0) ? Cp[off] + v : Cp[off];
+				if (p.ep.bias_mode == kBiasCol) v = v + p.ep.bias[col];
+				else if (p.ep.bias_mode == kBiasRow) v = v + p.ep.bias[row];
+				if (p.ep.relu) {
+					const bool on = v > 0.0f;
+					if (alive) alive[off] = on ? 1 : 0;
+					v = on ? v : 0.0f;
+				}
+				Cp[off] = v;
+			}
+}
+
+}  // namespace nnh

@@ -1,0 +1,362 @@
+"""ctypes access to the CPU checker (oracle/lib/liboracle.so) and to nn-cpp itself (oracle/_ref/libnnref.so).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg,
+never by the product package. All arrays are numpy float32 (row-major); results are returned as new
+arrays so a caller never aliases the checker's buffers.
+"""
+import ctypes as C
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ORACLE_SO = os.path.join(HERE, "lib", "liboracle.so")
+REF_SO = os.path.join(HERE, "_ref", "libnnref.so")
+
+_f = C.POINTER(C.c_float)
+_d = C.POINTER(C.c_double)
+_u8 = C.POINTER(C.c_ubyte)
+_sz = C.c_size_t
+_szp = C.POINTER(C.c_size_t)
+
+
+def _fp(a):
+    if a is None:
+        return None
+    assert a.dtype == np.float32 and a.flags["C_CONTIGUOUS"], (a.dtype, a.flags)
+    return a.ctypes.data_as(_f)
+
+
+def _dp(a):
+    if a is None:
+        return None
+    assert a.dtype == np.float64 and a.flags["C_CONTIGUOUS"]
+    return a.ctypes.data_as(_d)
+
+
+def _bp(a):
+    if a is None:
+        return None
+    assert a.dtype == np.uint8 and a.flags["C_CONTIGUOUS"]
+    return a.ctypes.data_as(_u8)
+
+
+class Oracle:
+    """The C restatement (bit-exact emulation of nn-cpp's NN_NATIVE arithmetic) and fp64 closed forms."""
+
+    def __init__(self, path=ORACLE_SO):
+        if not os.path.exists(path):
+            raise FileNotFoundError(f"{path} missing: run `make -C oracle` (or __graft_entry__.build())")
+        L = self.lib = C.CDLL(path)
+        gemm = [C.c_int, C.c_int, _sz, _sz, _sz, _f, _sz, _f, _sz, _f, _sz, C.c_int]
+        for name in ("oracle_sgemm", "oracle_sgemm_naive"):
+            getattr(L, name).argtypes = gemm
+            getattr(L, name).restype = None
+        L.oracle_sgemm_at.argtypes = [C.c_int, C.c_int, _sz, _sz, _sz, _f, _sz, _f, _sz, C.c_int, _szp, _szp, _f,
+                                      _sz, _f]
+        L.oracle_depth_cut.argtypes = [_sz, _sz, _sz]
+        L.oracle_depth_cut.restype = C.c_int
+        L.oracle_sgemm_f64.argtypes = [C.c_int, C.c_int, _sz, _sz, _sz, _f, _sz, _f, _sz, _f, _sz, C.c_int, _d, _d]
+        L.oracle_sum_axis0.argtypes = [_f, _sz, _sz, _f]
+        L.oracle_lane_sum.argtypes = [_f, _sz]
+        L.oracle_lane_sum.restype = C.c_float
+        L.oracle_linear_forward.argtypes = [_f, _sz, _sz, _f, _sz, _f, _f]
+        L.oracle_linear_backward.argtypes = [_f, _f, _f, _sz, _sz, _sz, _szp, C.c_int, _f, C.c_int, _f, C.c_int,
+                                             _f, C.c_int]
+        L.oracle_relu.argtypes = [_f, _f, _sz]
+        L.oracle_im2col_sample.argtypes = [_f, _f, _sz, _sz, _sz, _sz, _sz, _sz, _sz]
+        L.oracle_col2im_sample_add.argtypes = [_f, _f, _sz, _sz, _sz, _sz, _sz, _sz, _sz]
+        L.oracle_conv2d_forward.argtypes = [_f, _sz, _sz, _sz, _sz, _f, _sz, _sz, _sz, _f, _sz, _sz, C.c_int, _f, _u8]
+        L.oracle_conv2d_backward.argtypes = [_f, _f, _f, _u8, _sz, _sz, _sz, _sz, _sz, _sz, _sz, _sz, _sz, _f,
+                                             C.c_int, _f, _f]
+        L.oracle_conv2d_f64.argtypes = [_f, _sz, _sz, _sz, _sz, _f, _sz, _sz, _sz, _f, _sz, _sz, _d, _d]
+        L.oracle_masked_softmax_row.argtypes = [_f, _f, _sz, _sz, _f, C.c_int, C.c_float]
+        L.oracle_attention_forward.argtypes = [_f, _f, _f, _sz, _sz, _sz, _sz, _sz, _f, C.c_int, _f, _f]
+        L.oracle_attention_backward.argtypes = [_f, _f, _f, _f, _f, _sz, _sz, _sz, _sz, _sz, _f, C.c_int,
+                                                _f, C.c_int, _f, C.c_int, _f, C.c_int]
+        L.oracle_scaled_masked_softmax.argtypes = [_f, _sz, _sz, _sz, _sz, C.c_float, _f, C.c_int, _f]
+        L.oracle_attention_f64.argtypes = [_f, _f, _f, _sz, _sz, _sz, _sz, _sz, _f, C.c_int, _d, _d]
+        L.oracle_mt19937_uniform.argtypes = [C.c_uint, C.c_float, C.c_float, _f, _sz]
+
+    # -- GEMM --
+    def sgemm(self, ta, tb, m, n, k, a, lda, b, ldb, c, ldc, acc, naive=False):
+        """Returns a copy of c updated by nn::kernels::sgemm's arithmetic (or the naive fp32 triple loop)."""
+        out = np.array(c, dtype=np.float32, copy=True)
+        fn = self.lib.oracle_sgemm_naive if naive else self.lib.oracle_sgemm
+        fn(int(ta), int(tb), m, n, k, _fp(a), lda, _fp(b), ldb, _fp(out), ldc, int(acc))
+        return out
+
+    def sgemm_at(self, ta, tb, m, n, k, a, lda, b, ldb, acc, rows, cols, c_old=None):
+        """sgemm's value at elements (rows[t], cols[t]); c_old holds those elements before the call."""
+        rows = np.ascontiguousarray(rows, np.uint64)
+        cols = np.ascontiguousarray(cols, np.uint64)
+        cnt = rows.size
+        cold = np.ascontiguousarray(c_old if c_old is not None else np.zeros(cnt), np.float32)
+        out = np.empty(cnt, np.float32)
+        self.lib.oracle_sgemm_at(int(ta), int(tb), m, n, k, _fp(a), lda, _fp(b), ldb, int(acc),
+                                 rows.ctypes.data_as(_szp), cols.ctypes.data_as(_szp), _fp(cold), cnt, _fp(out))
+        return out
+
+    def depth_cut(self, m, n, k):
+        return bool(self.lib.oracle_depth_cut(m, n, k))
+
+    def sgemm_f64(self, ta, tb, m, n, k, a, lda, b, ldb, c, ldc, acc):
+        """fp64 op(A) op(B) (+ C) as a dense m x n array, with the magnitude sum |a||b| (+|c|)."""
+        out = np.zeros((m, n), np.float64)
+        mag = np.zeros((m, n), np.float64)
+        cin = c if c is not None else np.zeros(1, np.float32)
+        self.lib.oracle_sgemm_f64(int(ta), int(tb), m, n, k, _fp(a), lda, _fp(b), ldb, _fp(cin), ldc, int(acc),
+                                  _dp(out), _dp(mag))
+        return out, mag
+
+    # -- reductions --
+    def sum_axis0(self, src):
+        src = np.ascontiguousarray(src, np.float32)
+        rows, inner = src.shape[0], int(np.prod(src.shape[1:], dtype=np.int64))
+        out = np.empty(src.shape[1:], np.float32)
+        self.lib.oracle_sum_axis0(_fp(src), rows, inner, _fp(out))
+        return out
+
+    def lane_sum(self, p):
+        p = np.ascontiguousarray(p, np.float32)
+        return np.float32(self.lib.oracle_lane_sum(_fp(p), p.size))
+
+    # -- linear --
+    def linear_forward(self, x, w, bias):
+        K = x.shape[-1]
+        M = x.size // K
+        n = w.shape[0]
+        y = np.empty(x.shape[:-1] + (n,), np.float32)
+        self.lib.oracle_linear_forward(_fp(x), M, K, _fp(w), n, _fp(bias), _fp(y))
+        return y
+
+    def linear_backward(self, g, x, w, dx=None, dx_first=True, dw=None, dw_first=True, db=None, db_first=True,
+                        want=(True, True, True)):
+        K = x.shape[-1]
+        M = x.size // K
+        n = w.shape[0]
+        lead = (C.c_size_t * max(1, x.ndim - 1))(*x.shape[:-1])
+        dx = (np.array(dx, np.float32) if dx is not None else np.zeros(x.shape, np.float32)) if want[0] else None
+        dw = (np.array(dw, np.float32) if dw is not None else np.zeros(w.shape, np.float32)) if want[1] else None
+        db = (np.array(db, np.float32) if db is not None else np.zeros((n,), np.float32)) if want[2] else None
+        self.lib.oracle_linear_backward(_fp(g), _fp(x), _fp(w), M, K, n, lead, x.ndim - 1, _fp(dx), int(dx_first),
+                                        _fp(dw), int(dw_first), _fp(db), int(db_first))
+        return dx, dw, db
+
+    def relu(self, x):
+        y = np.empty_like(x)
+        self.lib.oracle_relu(_fp(x), _fp(y), x.size)
+        return y
+
+    # -- conv --
+    @staticmethod
+    def conv_out(H, W, kh, kw, stride, pad):
+        return (H + 2 * pad - kh) // stride + 1, (W + 2 * pad - kw) // stride + 1
+
+    def im2col(self, x, kh, kw, stride, pad):
+        N, Cin, H, W = x.shape
+        ho, wo = self.conv_out(H, W, kh, kw, stride, pad)
+        col = np.empty((N, Cin * kh * kw, ho * wo), np.float32)
+        for n in range(N):
+            xs = np.ascontiguousarray(x[n])
+            cs = np.empty((Cin * kh * kw, ho * wo), np.float32)
+            self.lib.oracle_im2col_sample(_fp(xs), _fp(cs), Cin, H, W, kh, kw, stride, pad)
+            col[n] = cs
+        return col
+
+    def col2im_add(self, col, dx, kh, kw, stride, pad):
+        dx = np.array(dx, np.float32, copy=True)
+        N, Cin, H, W = dx.shape
+        for n in range(N):
+            cs = np.ascontiguousarray(col[n])
+            xs = np.ascontiguousarray(dx[n])
+            self.lib.oracle_col2im_sample_add(_fp(cs), _fp(xs), Cin, H, W, kh, kw, stride, pad)
+            dx[n] = xs
+        return dx
+
+    def conv2d_forward(self, x, w, bias, stride, pad, fuse_relu):
+        N, Cin, H, W = x.shape
+        Cout, _, kh, kw = w.shape
+        ho, wo = self.conv_out(H, W, kh, kw, stride, pad)
+        y = np.empty((N, Cout, ho, wo), np.float32)
+        alive = np.zeros((N, Cout, ho, wo), np.uint8)
+        self.lib.oracle_conv2d_forward(_fp(x), N, Cin, H, W, _fp(w), Cout, kh, kw, _fp(bias), stride, pad,
+                                       int(fuse_relu), _fp(y), _bp(alive))
+        return y, alive
+
+    def conv2d_backward(self, g, x, w, alive, stride, pad, dx=None, dx_first=True):
+        N, Cin, H, W = x.shape
+        Cout, _, kh, kw = w.shape
+        dx = np.array(dx, np.float32) if dx is not None else np.zeros(x.shape, np.float32)
+        dw = np.zeros(w.shape, np.float32)
+        db = np.zeros((Cout,), np.float32)
+        self.lib.oracle_conv2d_backward(_fp(g), _fp(x), _fp(w), _bp(alive), N, Cin, H, W, Cout, kh, kw, stride, pad,
+                                        _fp(dx), int(dx_first), _fp(dw), _fp(db))
+        return dx, dw, db
+
+    def conv2d_f64(self, x, w, bias, stride, pad):
+        N, Cin, H, W = x.shape
+        Cout, _, kh, kw = w.shape
+        ho, wo = self.conv_out(H, W, kh, kw, stride, pad)
+        y = np.empty((N, Cout, ho, wo), np.float64)
+        mag = np.empty_like(y)
+        self.lib.oracle_conv2d_f64(_fp(x), N, Cin, H, W, _fp(w), Cout, kh, kw, _fp(bias), stride, pad, _dp(y), _dp(mag))
+        return y, mag
+
+    # -- attention --
+    def attention_forward(self, q, k, v, heads, pad=None, causal=False):
+        N, Tq, D = q.shape
+        Tk = k.shape[1]
+        out = np.empty((N, Tq, D), np.float32)
+        probs = np.empty((N, heads, Tq, Tk), np.float32)
+        self.lib.oracle_attention_forward(_fp(q), _fp(k), _fp(v), N, Tq, Tk, D, heads, _fp(pad), int(causal),
+                                          _fp(out), _fp(probs))
+        return out, probs
+
+    def attention_backward(self, g, q, k, v, probs, heads, pad=None, causal=False):
+        N, Tq, D = q.shape
+        Tk = k.shape[1]
+        dq, dk, dv = (np.zeros(q.shape, np.float32), np.zeros(k.shape, np.float32), np.zeros(v.shape, np.float32))
+        self.lib.oracle_attention_backward(_fp(g), _fp(q), _fp(k), _fp(v), _fp(probs), N, Tq, Tk, D, heads, _fp(pad),
+                                           int(causal), _fp(dq), 1, _fp(dk), 1, _fp(dv), 1)
+        return dq, dk, dv
+
+    def scaled_masked_softmax(self, x, scale, pad=None, causal=False):
+        N, H, Tq, Tk = x.shape
+        y = np.empty_like(x)
+        self.lib.oracle_scaled_masked_softmax(_fp(x), N, H, Tq, Tk, scale, _fp(pad), int(causal), _fp(y))
+        return y
+
+    def attention_f64(self, q, k, v, heads, pad=None, causal=False):
+        N, Tq, D = q.shape
+        Tk = k.shape[1]
+        out = np.empty((N, Tq, D), np.float64)
+        probs = np.empty((N, heads, Tq, Tk), np.float64)
+        self.lib.oracle_attention_f64(_fp(q), _fp(k), _fp(v), N, Tq, Tk, D, heads, _fp(pad), int(causal),
+                                      _dp(out), _dp(probs))
+        return out, probs
+
+    def mt19937_uniform(self, seed, lo, hi, count):
+        out = np.empty(count, np.float32)
+        self.lib.oracle_mt19937_uniform(seed, lo, hi, _fp(out), count)
+        return out
+
+
+class Reference:
+    """nn-cpp itself (its unmodified sources compiled by oracle/Makefile), through oracle/ref_shim.cpp."""
+
+    def __init__(self, path=REF_SO):
+        if not os.path.exists(path):
+            raise FileNotFoundError(f"{path} missing: run `make -C oracle ref` where /root/reference exists")
+        L = self.lib = C.CDLL(path)
+        L.nnref_set_threads.argtypes = [_sz]
+        L.nnref_num_threads.restype = _sz
+        L.nnref_uses_avx2.restype = C.c_int
+        L.nnref_sgemm.argtypes = [C.c_int, C.c_int, _sz, _sz, _sz, _f, _sz, _f, _sz, _f, _sz, C.c_int]
+        L.nnref_matmul.argtypes = [_f, _szp, C.c_int, _f, _szp, C.c_int, C.c_int, C.c_int, _f, _sz, _szp,
+                                   C.POINTER(C.c_int)]
+        L.nnref_linear_forward.argtypes = [_f, _szp, C.c_int, _f, _sz, _f, _f]
+        L.nnref_linear_backward.argtypes = [_f, _szp, C.c_int, _f, _sz, _f, _f, _f, _f, _f]
+        L.nnref_conv2d_forward.argtypes = [_f, _sz, _sz, _sz, _sz, _f, _sz, _sz, _sz, _f, C.c_int, C.c_int, C.c_int, _f]
+        L.nnref_conv2d_backward.argtypes = [_f, _sz, _sz, _sz, _sz, _f, _sz, _sz, _sz, _f, C.c_int, C.c_int, C.c_int,
+                                            _f, _f, _f, _f]
+        L.nnref_attention_forward.argtypes = [_f, _f, _f, _sz, _sz, _sz, _sz, _sz, _f, C.c_int, _f]
+        L.nnref_attention_backward.argtypes = [_f, _f, _f, _sz, _sz, _sz, _sz, _sz, _f, C.c_int, _f, _f, _f, _f]
+        L.nnref_scaled_masked_softmax.argtypes = [_f, _sz, _sz, _sz, _sz, C.c_float, _f, C.c_int, _f]
+
+    def set_threads(self, n):
+        self.lib.nnref_set_threads(n)
+
+    def num_threads(self):
+        return int(self.lib.nnref_num_threads())
+
+    def uses_avx2(self):
+        return bool(self.lib.nnref_uses_avx2())
+
+    def sgemm(self, ta, tb, m, n, k, a, lda, b, ldb, c, ldc, acc):
+        out = np.array(c, dtype=np.float32, copy=True)
+        self.lib.nnref_sgemm(int(ta), int(tb), m, n, k, _fp(a), lda, _fp(b), ldb, _fp(out), ldc, int(acc))
+        return out
+
+    def sgemm_inplace(self, ta, tb, m, n, k, a, lda, b, ldb, c, ldc, acc):
+        self.lib.nnref_sgemm(int(ta), int(tb), m, n, k, _fp(a), lda, _fp(b), ldb, _fp(c), ldc, int(acc))
+
+    def matmul(self, a, b, ta=False, tb=False):
+        a = np.ascontiguousarray(a, np.float32)
+        b = np.ascontiguousarray(b, np.float32)
+        ash = (C.c_size_t * a.ndim)(*a.shape)
+        bsh = (C.c_size_t * b.ndim)(*b.shape)
+        cap = max(1, (a.size + 1) * (b.size + 1))
+        cap = min(cap, 1 << 26)
+        out = np.empty(cap, np.float32)
+        osh = (C.c_size_t * 8)()
+        ond = C.c_int(0)
+        rc = self.lib.nnref_matmul(_fp(a), ash, a.ndim, _fp(b), bsh, b.ndim, int(ta), int(tb), _fp(out), cap, osh,
+                                   C.byref(ond))
+        if rc != 0:
+            return rc, None
+        shape = tuple(osh[i] for i in range(ond.value))
+        return 0, out[: int(np.prod(shape, dtype=np.int64))].reshape(shape).copy()
+
+    def linear_forward(self, x, w, bias):
+        xs = (C.c_size_t * x.ndim)(*x.shape)
+        y = np.empty(x.shape[:-1] + (w.shape[0],), np.float32)
+        rc = self.lib.nnref_linear_forward(_fp(x), xs, x.ndim, _fp(w), w.shape[0], _fp(bias), _fp(y))
+        assert rc == 0, rc
+        return y
+
+    def linear_backward(self, x, w, bias, g):
+        xs = (C.c_size_t * x.ndim)(*x.shape)
+        dx, dw, db = np.empty_like(x), np.empty_like(w), np.empty_like(bias)
+        rc = self.lib.nnref_linear_backward(_fp(x), xs, x.ndim, _fp(w), w.shape[0], _fp(bias), _fp(g), _fp(dx),
+                                            _fp(dw), _fp(db))
+        assert rc == 0, rc
+        return dx, dw, db
+
+    def conv2d_forward(self, x, w, bias, stride, pad, fuse_relu):
+        N, Cin, H, W = x.shape
+        Cout, _, kh, kw = w.shape
+        ho, wo = Oracle.conv_out(H, W, kh, kw, stride, pad)
+        y = np.empty((N, Cout, ho, wo), np.float32)
+        rc = self.lib.nnref_conv2d_forward(_fp(x), N, Cin, H, W, _fp(w), Cout, kh, kw, _fp(bias), stride, pad,
+                                           int(fuse_relu), _fp(y))
+        assert rc == 0, rc
+        return y
+
+    def conv2d_backward(self, x, w, bias, stride, pad, fuse_relu, g):
+        N, Cin, H, W = x.shape
+        Cout, _, kh, kw = w.shape
+        dx, dw, db = np.empty_like(x), np.empty_like(w), np.empty_like(bias)
+        rc = self.lib.nnref_conv2d_backward(_fp(x), N, Cin, H, W, _fp(w), Cout, kh, kw, _fp(bias), stride, pad,
+                                            int(fuse_relu), _fp(g), _fp(dx), _fp(dw), _fp(db))
+        assert rc == 0, rc
+        return dx, dw, db
+
+    def attention_forward(self, q, k, v, heads, pad=None, causal=False):
+        N, Tq, D = q.shape
+        Tk = k.shape[1]
+        out = np.empty((N, Tq, D), np.float32)
+        rc = self.lib.nnref_attention_forward(_fp(q), _fp(k), _fp(v), N, Tq, Tk, D, heads, _fp(pad), int(causal),
+                                              _fp(out))
+        assert rc == 0, rc
+        return out
+
+    def attention_backward(self, q, k, v, heads, g, pad=None, causal=False):
+        N, Tq, D = q.shape
+        Tk = k.shape[1]
+        dq, dk, dv = np.empty_like(q), np.empty_like(k), np.empty_like(v)
+        rc = self.lib.nnref_attention_backward(_fp(q), _fp(k), _fp(v), N, Tq, Tk, D, heads, _fp(pad), int(causal),
+                                               _fp(g), _fp(dq), _fp(dk), _fp(dv))
+        assert rc == 0, rc
+        return dq, dk, dv
+
+    def scaled_masked_softmax(self, x, scale, pad=None, causal=False):
+        N, H, Tq, Tk = x.shape
+        y = np.empty_like(x)
+        rc = self.lib.nnref_scaled_masked_softmax(_fp(x), N, H, Tq, Tk, scale, _fp(pad), int(causal), _fp(y))
+        assert rc == 0, rc
+        return y
+
+
+def reference_available():
+    return os.path.exists(REF_SO)

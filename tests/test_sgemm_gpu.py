@@ -1,0 +1,200 @@
+"""Parity of nnh_sgemm (the replacement of nn::kernels::sgemm) with nn-cpp, on the GPU.
+
+Mirrors tests/test_kernels.cpp of the reference (sizes x flags x accumulate, block boundaries, zero sizes,
+leading-dimension padding with sentinels, Inf/NaN, determinism, the depth cut), but the bar is higher:
+every output must be BIT-IDENTICAL to the oracle, which restates nn-cpp's NN_NATIVE arithmetic and is
+itself pinned bit for bit to nn-cpp's compiled sources (tests/test_oracle.py). Full BASELINE sizes are
+checked on sampled elements (the oracle recomputes each sampled element's whole depth chain).
+"""
+import numpy as np
+import pytest
+
+from helpers import SENTINEL, Problem, bits_equal, first_diff, gpu_sgemm, oracle_sgemm, within_fp64_bound
+from nnh import synth
+
+pytestmark = pytest.mark.gpu
+
+
+def check(oracle, p, acc, config=-1):
+    got = gpu_sgemm(p, acc, config)
+    want = oracle_sgemm(oracle, p, acc)
+    assert bits_equal(got, want), f"ta={p.ta} tb={p.tb} m={p.m} n={p.n} k={p.k} acc={acc}: {first_diff(got, want)}"
+    return got
+
+
+def test_sizes_and_flags(gpu, oracle):
+    """test_kernels.cpp:293-331: sizes {1,7,33,257}^3 x trans_a x trans_b x accumulate."""
+    sizes = (1, 7, 33, 257)
+    seed = 4000
+    for ta in (0, 1):
+        for tb in (0, 1):
+            for acc in (0, 1):
+                for m in sizes:
+                    for n in sizes:
+                        for k in sizes:
+                            check(oracle, Problem(ta, tb, m, n, k, 0, seed), acc)
+                            seed += 1
+
+
+def test_block_boundaries(gpu, oracle):
+    """Past each of the reference's block sizes (kMC=96, kKC=256, kNC=1024; test_kernels.cpp:169-178) and
+    past each of this kernel's tile sizes (64/128/256 rows, 128 columns, 16/32 deep)."""
+    cases = [(96 + 5, 7, 33), (7, 33, 256 + 5), (7, 1024 + 5, 33), (7, 1024 + 5, 256 + 5),
+             (257, 129, 17), (129, 129, 33), (255, 127, 31), (65, 300, 64), (300, 200, 100), (512, 384, 48)]
+    seed = 1000
+    for ta in (0, 1):
+        for tb in (0, 1):
+            for acc in (0, 1):
+                for m, n, k in cases:
+                    check(oracle, Problem(ta, tb, m, n, k, 0, seed), acc)
+                    seed += 1
+
+
+def test_zero_size_dimensions(gpu):
+    """test_kernels.cpp:180-201: m or n == 0 touches nothing; k == 0 zero-fills, or leaves C when
+    accumulating; nothing outside m x n is written."""
+    import torch
+
+    import nnh
+    for m, n, k in ((0, 5, 4), (3, 0, 4), (3, 5, 0)):
+        for acc in (0, 1):
+            ldc = 6
+            a = torch.ones(16, device="cuda")
+            b = torch.ones(32, device="cuda")
+            c = np.full((4, ldc), SENTINEL, np.float32)
+            c[:m, :n] = 2.0
+            cd = torch.from_numpy(c).cuda()
+            nnh.sgemm(0, 0, m, n, k, a, k if k else 1, b, n if n else 1, cd, ldc, acc)
+            got = cd.cpu().numpy()
+            want = np.full((4, ldc), SENTINEL, np.float32)
+            want[:m, :n] = 2.0 if acc else 0.0
+            assert bits_equal(got, want), (m, n, k, acc)
+
+
+def test_leading_dimensions_wider_than_width(gpu, oracle):
+    """test_kernels.cpp:203-209 (sentinel padding stays untouched, bitwise), plus larger and odd pads that
+    break 16-byte alignment of rows."""
+    seed = 2000
+    for ta in (0, 1):
+        for tb in (0, 1):
+            for acc in (0, 1):
+                for (m, n, k, pad) in ((7, 33, 33, 3), (200, 300, 100, 5), (128, 128, 64, 1), (256, 256, 256, 4)):
+                    check(oracle, Problem(ta, tb, m, n, k, pad, seed), acc)
+                    seed += 1
+
+
+def test_inf_and_nan_propagate(gpu, oracle):
+    """test_kernels.cpp:211-231: op(A)(2,0) = +Inf, row 0 of op(B) cycles +1, -1, 0 (so row 2 of C holds
+    +Inf, -Inf and NaN), op(B)(5,3) = NaN (column 3 of C is NaN)."""
+    seed = 3000
+    for ta in (0, 1):
+        for tb in (0, 1):
+            for acc in (0, 1):
+                p = Problem(ta, tb, 7, 33, 17, 0, seed)
+                seed += 1
+                if ta:
+                    p.a[0, 2] = np.inf
+                else:
+                    p.a[2, 0] = np.inf
+                for j in range(p.n):
+                    v = 1.0 if j % 3 == 0 else (-1.0 if j % 3 == 1 else 0.0)
+                    if tb:
+                        p.b[j, 0] = v
+                    else:
+                        p.b[0, j] = v
+                if tb:
+                    p.b[3, 5] = np.nan
+                else:
+                    p.b[5, 3] = np.nan
+                got = check(oracle, p, acc)
+                assert np.isnan(got[2, 2]) and np.isposinf(got[2, 0]) and np.isneginf(got[2, 1])
+                assert np.all(np.isnan(got[:, 3]))
+
+
+def test_deterministic_repeat(gpu):
+    """test_kernels.cpp:333-341, and repeated large launches: bitwise identical run to run."""
+    for (ta, tb, m, n, k, pad, seed) in ((0, 1, 101, 75, 300, 2, 5000), (0, 0, 1024, 1024, 1024, 0, 5001),
+                                         (1, 0, 300, 1000, 700, 3, 5002)):
+        p = Problem(ta, tb, m, n, k, pad, seed)
+        for acc in (0, 1):
+            first = gpu_sgemm(p, acc)
+            for _ in range(2):
+                assert bits_equal(gpu_sgemm(p, acc), first)
+
+
+def test_depth_cut(gpu, oracle):
+    """test_kernels.cpp:406-435: small m x n with a long depth is cut into 128-deep pieces summed in order;
+    the shapes just under the thresholds take the ordinary path."""
+    cases = [(64, 64, 1024), (40, 48, 2 * 256 + 77), (7, 300, 3 * 256), (64, 64, 2 * 256 - 1), (300, 300, 512)]
+    seed = 30000
+    for ta in (0, 1):
+        for tb in (0, 1):
+            for acc in (0, 1):
+                for m, n, k in cases:
+                    check(oracle, Problem(ta, tb, m, n, k, 3, seed), acc)
+                    seed += 1
+
+
+def test_accumulate_adds_old_c_after_first_depth_block(gpu, oracle):
+    """With accumulate, nn-cpp adds the old C after the first 256 depth steps (Store::kAdd, then
+    kContinue): exercised at depths around 256 and 512, with and without the depth cut."""
+    seed = 40000
+    for k in (1, 255, 256, 257, 300, 511, 512, 513, 1000):
+        for (m, n) in ((129, 129), (300, 300)):
+            for ta, tb in ((0, 0), (1, 1)):
+                check(oracle, Problem(ta, tb, m, n, k, 1, seed), 1)
+                seed += 1
+
+
+def test_every_tile_configuration_gives_the_same_bits(gpu, oracle):
+    """The depth order of each element is independent of the kernel's tiling, so every configuration
+    returns the oracle's bits."""
+    import nnh
+    n_cfg = len(nnh.gemm_configs())
+    seed = 50000
+    for (ta, tb, m, n, k, pad) in ((0, 0, 256, 256, 256, 0), (1, 1, 300, 200, 77, 1), (0, 1, 64, 512, 600, 0),
+                                   (1, 0, 512, 64, 2048, 0)):
+        p = Problem(ta, tb, m, n, k, pad, seed)
+        seed += 1
+        for acc in (0, 1):
+            want = oracle_sgemm(oracle, p, acc)
+            for cfg in range(n_cfg):
+                got = gpu_sgemm(p, acc, config=cfg)
+                assert bits_equal(got, want), (cfg, p.args(), acc, first_diff(got, want))
+
+
+@pytest.mark.parametrize("ta,tb", [(0, 0), (1, 0), (0, 1)])
+def test_baseline_config1_512(gpu, oracle, ta, tb):
+    """512^3 from seed 0 (A filled first, then B, uniform [-1, 1]); NN, A^T B, A B^T.
+    Whole output bit-identical to nn-cpp, and within 4 K 2^-24 sum|a||b| of the fp64 product."""
+    n = 512
+    a, b = synth.uniform_operands(0, [(n, n), (n, n)])
+    p = Problem(ta, tb, n, n, n, 0, 0)
+    p.a, p.b = np.ascontiguousarray(a), np.ascontiguousarray(b)
+    p.c = np.zeros((n, n), np.float32)
+    got = check(oracle, p, 0)
+    assert within_fp64_bound(got, p, 0, oracle)
+
+
+@pytest.mark.parametrize("m,n,k", [(1024, 1024, 1024), (2048, 2048, 2048), (4096, 4096, 4096),
+                                   (8192, 8192, 8192), (64, 4096, 4096), (4096, 4096, 64)])
+def test_baseline_config5_sampled(gpu, oracle, m, n, k):
+    """BASELINE config 5 at full size, seed 4: 512 sampled elements (corners, edges, random) bit-identical
+    to nn-cpp's arithmetic, repeated launches bitwise equal."""
+    import torch
+
+    import nnh
+    a, b = synth.uniform_operands(4, [(m, k), (k, n)])
+    da, db = torch.from_numpy(a).cuda(), torch.from_numpy(b).cuda()
+    dc = torch.empty((m, n), device="cuda")
+    nnh.sgemm(0, 0, m, n, k, da, k, db, n, dc, n, 0)
+    dc2 = torch.empty_like(dc)
+    nnh.sgemm(0, 0, m, n, k, da, k, db, n, dc2, n, 0)
+    torch.cuda.synchronize()
+    assert torch.equal(dc.view(torch.int32), dc2.view(torch.int32))
+    rng = np.random.default_rng(m * 7 + n * 3 + k)
+    rows = np.concatenate([[0, 0, m - 1, m - 1, m // 2], rng.integers(0, m, 507)])
+    cols = np.concatenate([[0, n - 1, 0, n - 1, n // 2], rng.integers(0, n, 507)])
+    got = dc.cpu().numpy()[rows, cols]
+    want = oracle.sgemm_at(0, 0, m, n, k, a, k, b, n, 0, rows, cols)
+    assert got.tobytes() == want.tobytes(), first_diff(got, want)
