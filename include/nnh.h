@@ -101,6 +101,36 @@ int nnh_matmul_shape(const size_t* a_shape, int a_ndim, const size_t* b_shape, i
 int nnh_matmul(const float* a, const size_t* a_shape, int a_ndim, const float* b, const size_t* b_shape, int b_ndim,
                int trans_a, int trans_b, float* out, void* stream);
 
+/*
+ * nn::linear forward (src/autograd/ops.cpp:714-730): y[M x n] = x[M x K] w[n x K]^T, then + bias[n] per
+ * column, in one kernel. relu != 0 also applies the ReLU node that follows a Linear in the reference
+ * (ops.cpp:775-782) in the same epilogue: y = v > 0 ? v : 0 (bit-identical to linear then relu).
+ */
+int nnh_linear_forward(const float* x, size_t M, size_t K, const float* w, size_t n, const float* bias, int relu,
+                       float* y, void* stream);
+
+/*
+ * nn::linear backward (ops.cpp:731-744) for upstream gradient g of shape lead[0..nlead-1] x n, where x has
+ * shape lead x K: dx = g w (sgemm F,F), dw = g^T x (sgemm T,F), db = g summed over every leading axis by
+ * Tensor::sum(0), one axis at a time (ops.cpp:35-53). Each *_first selects nn-cpp's first-write rule for a
+ * fresh gradient buffer (value.cpp:60-64): overwrite (db: s + 0.0f) instead of accumulate. Any of dx, dw,
+ * db may be NULL (that input needs no gradient).
+ */
+int nnh_linear_backward(const float* g, const float* x, const float* w, const size_t* lead, int nlead, size_t K,
+                        size_t n, float* dx, int dx_first, float* dw, int dw_first, float* db, int db_first,
+                        void* stream);
+
+/* nn::relu forward (ops.cpp:775-782): y = x > 0 ? x : 0. */
+int nnh_relu_forward(const float* x, float* y, size_t count, void* stream);
+
+/* nn::relu backward (ops.cpp:783-792): term = x > 0 ? g : 0; first: dx = term + 0.0f, else dx += term.
+ * x may be the forward output instead of its input (y > 0 exactly where x > 0). */
+int nnh_relu_backward(const float* x, const float* g, float* dx, int first, size_t count, void* stream);
+
+/* Tensor::sum(0) of a {rows, inner} tensor (src/tensor.cpp:422-456): s_j = sum of src[a][j] over a in order,
+ * from +0. combine 0: dst = s; 1: dst = s + 0.0f (a fresh gradient); 2: dst += s. */
+int nnh_tensor_sum0(const float* src, size_t rows, size_t inner, float* dst, int combine, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

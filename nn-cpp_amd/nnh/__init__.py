@@ -59,7 +59,13 @@ def _declare(L):
             getattr(L, name).argtypes = args
 
 
-_EXTRA_DECLS = {}
+_EXTRA_DECLS = {
+    "nnh_linear_forward": [_vp, _sz, _sz, _vp, _sz, _vp, C.c_int, _vp, _vp],
+    "nnh_linear_backward": [_vp, _vp, _vp, _szp, C.c_int, _sz, _sz, _vp, C.c_int, _vp, C.c_int, _vp, C.c_int, _vp],
+    "nnh_relu_forward": [_vp, _vp, _sz, _vp],
+    "nnh_relu_backward": [_vp, _vp, _vp, C.c_int, _sz, _vp],
+    "nnh_tensor_sum0": [_vp, _sz, _sz, _vp, C.c_int, _vp],
+}
 
 
 def lib():
@@ -162,3 +168,39 @@ def matmul(a, b, ta=False, tb=False, stream=None):
     check(lib().nnh_matmul(_ptr(a), ash, a.dim(), _ptr(b), bsh, b.dim(), int(ta), int(tb), _ptr(out),
                            _stream(stream)))
     return out
+
+
+def linear_forward(x, w, bias, relu=False, stream=None):
+    """nn::linear (optionally followed by nn::relu) on device tensors; returns y."""
+    import torch
+    K = x.shape[-1]
+    M = x.numel() // K if K else int(torch.tensor(x.shape[:-1]).prod())
+    n = w.shape[0]
+    y = torch.empty(tuple(x.shape[:-1]) + (n,), dtype=torch.float32, device=x.device)
+    check(lib().nnh_linear_forward(_ptr(x), M, K, _ptr(w), n, _ptr(bias), int(relu), _ptr(y), _stream(stream)))
+    return y
+
+
+def linear_backward(g, x, w, dx=None, dx_first=True, dw=None, dw_first=True, db=None, db_first=True, stream=None):
+    """nn::linear's backward into the given gradient buffers (any may be None)."""
+    lead = (C.c_size_t * (x.dim() - 1))(*x.shape[:-1])
+    check(lib().nnh_linear_backward(_ptr(g), _ptr(x), _ptr(w), lead, x.dim() - 1, x.shape[-1], w.shape[0],
+                                    _ptr(dx), int(dx_first), _ptr(dw), int(dw_first), _ptr(db), int(db_first),
+                                    _stream(stream)))
+
+
+def relu_forward(x, stream=None):
+    import torch
+    y = torch.empty_like(x)
+    check(lib().nnh_relu_forward(_ptr(x), _ptr(y), x.numel(), _stream(stream)))
+    return y
+
+
+def relu_backward(x, g, dx, first=True, stream=None):
+    check(lib().nnh_relu_backward(_ptr(x), _ptr(g), _ptr(dx), int(first), x.numel(), _stream(stream)))
+
+
+def tensor_sum0(src, dst, combine=0, stream=None):
+    rows = src.shape[0]
+    inner = src.numel() // rows if rows else dst.numel()
+    check(lib().nnh_tensor_sum0(_ptr(src), rows, inner, _ptr(dst), int(combine), _stream(stream)))

@@ -1,5 +1,6 @@
 // gemm.hip - instantiations, depth-cut reduction and launch logic of the fp32 MFMA GEMM.
 #include "gemm.hpp"
+#include "gemm_config.hpp"
 
 #include <algorithm>
 #include <mutex>
@@ -41,43 +42,14 @@ __global__ void __launch_bounds__(256) reduce_pieces_kernel(const float* __restr
 	cp[off] = finish(v, row, col, off, ep, ep.alive ? ep.alive + oc : nullptr);
 }
 
-using KernelFn = void (*)(const GemmArgs);
-
-struct Config {
-	const char* name;
-	int bm, bn, bk;
-	int lds_bytes[4];      // per (ta, tb)
-	KernelFn fn[4][2];     // [ta*2 + tb][edge]
-};
-
-template <int BM, int BN, int BK, int WM, int WN>
-Config make_config(const char* name) {
-	Config c{};
-	c.name = name;
-	c.bm = BM;
-	c.bn = BN;
-	c.bk = BK;
-#define NNH_SET(TA, TB)                                                                                  \
-	c.lds_bytes[TA * 2 + TB] = TileShape<BM, BN, BK, WM, WN, TA, TB>::kLdsFloats * (int)sizeof(float);   \
-	c.fn[TA * 2 + TB][0] = sgemm_tile_kernel<BM, BN, BK, WM, WN, TA, TB, false>;                         \
-	c.fn[TA * 2 + TB][1] = sgemm_tile_kernel<BM, BN, BK, WM, WN, TA, TB, true>;
-	NNH_SET(false, false)
-	NNH_SET(false, true)
-	NNH_SET(true, false)
-	NNH_SET(true, true)
-#undef NNH_SET
-	return c;
-}
-
 const Config* configs() {
 	static const Config table[] = {
-		make_config<256, 128, 16, 128, 64>("256x128x16_w128x64"),
-		make_config<128, 128, 32, 64, 64>("128x128x32_w64x64"),
-		make_config<64, 128, 32, 64, 32>("64x128x32_w64x32"),
+		config_64x128x32(), config_128x128x32(), config_64x256x32(), config_128x64x32(),
+		config_128x256x16(), config_256x128x16(), config_64x128x64(), config_128x128x16(),
 	};
 	return table;
 }
-constexpr int kNumConfigs = 3;
+constexpr int kNumConfigs = 8;
 
 // Raises each kernel's dynamic LDS limit once per device (gfx950 has 160 KiB per CU).
 hipError_t prepare_device() {
@@ -101,14 +73,16 @@ hipError_t prepare_device() {
 	return hipSuccess;
 }
 
+// Choice by measured throughput on MI355X (tile sweep over the BASELINE shapes): 128 x 128 tiles once there
+// are two workgroups per CU of them (16-deep stages for A B, 32-deep when an operand is transposed), then
+// 128 x 64, then 64 x 128 for small products. Results never depend on the choice.
+enum { kCfg64x128x32 = 0, kCfg128x128x32 = 1, kCfg128x64x32 = 3, kCfg128x128x16 = 7 };
+
 int pick_config(const GemmCall& g) {
-	const Config* cfg = configs();
-	// largest tile that still gives every CU at least one workgroup
-	for (int i = 0; i < kNumConfigs; ++i) {
-		const int64_t tiles = ((g.m + cfg[i].bm - 1) / cfg[i].bm) * ((g.n + cfg[i].bn - 1) / cfg[i].bn) * g.batch_count;
-		if (tiles >= 256) return i;
-	}
-	return kNumConfigs - 1;
+	auto tiles = [&](int bm, int bn) { return ((g.m + bm - 1) / bm) * ((g.n + bn - 1) / bn) * g.batch_count; };
+	if (tiles(128, 128) >= 512) return (!g.ta && !g.tb) ? kCfg128x128x16 : kCfg128x128x32;
+	if (tiles(128, 64) >= 512) return kCfg128x64x32;
+	return kCfg64x128x32;
 }
 
 }  // namespace

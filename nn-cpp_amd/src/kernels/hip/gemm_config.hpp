@@ -1,0 +1,46 @@
+// gemm_config.hpp - one compiled tile configuration of the MFMA GEMM: its 8 kernels (4 operand layouts x
+// interior/edge) and their LDS sizes. Each configuration is instantiated in its own gemm_cfg_*.hip.
+#pragma once
+
+#include "gemm_tile.hpp"
+
+namespace nnh {
+
+using KernelFn = void (*)(const GemmArgs);
+
+struct Config {
+	const char* name;
+	int bm, bn, bk;
+	int lds_bytes[4];   // per operand layout (ta * 2 + tb)
+	KernelFn fn[4][2];  // [ta * 2 + tb][edge]
+};
+
+template <int BM, int BN, int BK, int WM, int WN, int WPE>
+Config make_config(const char* name) {
+	Config c{};
+	c.name = name;
+	c.bm = BM;
+	c.bn = BN;
+	c.bk = BK;
+#define NNH_SET(TA, TB)                                                                                  \
+	c.lds_bytes[TA * 2 + TB] = TileShape<BM, BN, BK, WM, WN, TA, TB>::kLdsFloats * (int)sizeof(float);   \
+	c.fn[TA * 2 + TB][0] = sgemm_tile_kernel<BM, BN, BK, WM, WN, WPE, TA, TB, false>;                         \
+	c.fn[TA * 2 + TB][1] = sgemm_tile_kernel<BM, BN, BK, WM, WN, WPE, TA, TB, true>;
+	NNH_SET(false, false)
+	NNH_SET(false, true)
+	NNH_SET(true, false)
+	NNH_SET(true, true)
+#undef NNH_SET
+	return c;
+}
+
+Config config_64x128x32();
+Config config_128x128x32();
+Config config_64x256x32();
+Config config_128x64x32();
+Config config_128x256x16();
+Config config_256x128x16();
+Config config_64x128x64();
+Config config_128x128x16();
+
+}  // namespace nnh

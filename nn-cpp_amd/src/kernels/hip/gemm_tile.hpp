@@ -150,8 +150,8 @@ __device__ __forceinline__ int xcd_remap(int bid, int total) {
 	return bid;
 }
 
-template <int BM, int BN, int BK, int WM, int WN, bool TA, bool TB, bool EDGE>
-__global__ void __launch_bounds__(256) sgemm_tile_kernel(const GemmArgs p) {
+template <int BM, int BN, int BK, int WM, int WN, int WPE, bool TA, bool TB, bool EDGE>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE))) sgemm_tile_kernel(const GemmArgs p) {
 	using S = TileShape<BM, BN, BK, WM, WN, TA, TB>;
 	constexpr int I = S::I, J = S::J;
 	extern __shared__ __align__(16) float lds[];
@@ -224,68 +224,91 @@ __global__ void __launch_bounds__(256) sgemm_tile_kernel(const GemmArgs p) {
 	};
 
 	// C element (i, j, r) of this lane: row and column inside the workgroup tile
-	auto c_row = [&](int i, int r) { return wm0 + 64 * i + 32 * (r >> 4) + 8 * ((r & 15) >> 2) + 4 * (lane >> 5) + (r & 3); };
-	auto c_col = [&](int j) { return wn0 + 32 * j + (lane & 31); };
+	auto c_row = [&](int i, int r, int ln) { return wm0 + 64 * i + 32 * (r >> 4) + 8 * ((r & 15) >> 2) + 4 * (ln >> 5) + (r & 3); };
+	auto c_col = [&](int j, int ln) { return wn0 + 32 * j + (ln & 31); };
 
-	if (nkt > 0) {
-		load(0);
-		store(0);
-		__syncthreads();
-	}
-	for (int kt = 0; kt < nkt; ++kt) {
-		const int cur = kt & 1;
-		if (kt + 1 < nkt) load(kt + 1);
-		const float* As = lds + cur * S::kStage;
+	// One depth tile from LDS buffer buf: fragments for depth group kk+4 are read while the MFMAs of
+	// group kk run (two register sets), and each element's chain advances one k per MFMA, in order.
+	auto read_frags = [&](const float* As, const float* Bs, int kk, f32x4* af, f32x4* bf) {
+#pragma unroll
+		for (int i = 0; i < I; ++i) {
+			const int row = wm0 + 64 * i + lane;
+			if (!TA) {
+				af[i] = *reinterpret_cast<const f32x4*>(As + row * S::SA + kk);
+			} else {
+#pragma unroll
+				for (int e = 0; e < 4; ++e) af[i][e] = As[(kk + e) * S::SA + row];
+			}
+		}
+#pragma unroll
+		for (int j = 0; j < J; ++j) {
+			const int col = wn0 + 32 * j + (lane & 31);
+			if (TB) {
+				bf[j] = *reinterpret_cast<const f32x4*>(Bs + col * S::SB + kk);
+			} else {
+#pragma unroll
+				for (int e = 0; e < 4; ++e) bf[j][e] = Bs[(kk + e) * S::SB + col];
+			}
+		}
+	};
+	auto mma_tile = [&](int buf) {
+		const float* As = lds + buf * S::kStage;
 		const float* Bs = As + S::kASize;
+		f32x4 af[2][I], bf[2][J];
+		read_frags(As, Bs, 0, af[0], bf[0]);
 #pragma unroll
 		for (int kk = 0; kk < BK; kk += 4) {
-			f32x4 af[I], bf[J];
-#pragma unroll
-			for (int i = 0; i < I; ++i) {
-				const int row = wm0 + 64 * i + lane;
-				if (!TA) {
-					af[i] = *reinterpret_cast<const f32x4*>(As + row * S::SA + kk);
-				} else {
-#pragma unroll
-					for (int e = 0; e < 4; ++e) af[i][e] = As[(kk + e) * S::SA + row];
-				}
-			}
-#pragma unroll
-			for (int j = 0; j < J; ++j) {
-				const int col = wn0 + 32 * j + (lane & 31);
-				if (TB) {
-					bf[j] = *reinterpret_cast<const f32x4*>(Bs + col * S::SB + kk);
-				} else {
-#pragma unroll
-					for (int e = 0; e < 4; ++e) bf[j][e] = Bs[(kk + e) * S::SB + col];
-				}
-			}
+			const int cur = (kk >> 2) & 1;
+			// issue the next group's LDS reads before this group's MFMAs, so their latency is hidden;
+			// the scheduling fences stop the compiler from sinking them back next to their uses
+			if (kk + 4 < BK) read_frags(As, Bs, kk + 4, af[cur ^ 1], bf[cur ^ 1]);
+			__builtin_amdgcn_sched_barrier(0);
 #pragma unroll
 			for (int e = 0; e < 4; ++e)
 #pragma unroll
 				for (int i = 0; i < I; ++i)
 #pragma unroll
 					for (int j = 0; j < J; ++j)
-						acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x1f32(af[i][e], bf[j][e], acc[i][j], 0, 0, 0);
+						acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x1f32(af[cur][i][e], bf[cur][j][e], acc[i][j], 0, 0, 0);
+			__builtin_amdgcn_sched_barrier(0);
 		}
-		if (kt + 1 < nkt) store(cur ^ 1);
-		if (acc_mode && kt == acc_tile) {
-			// Store::kAdd after the first depth block: c_old + running sum
-#pragma unroll
-			for (int i = 0; i < I; ++i)
-#pragma unroll
-				for (int j = 0; j < J; ++j)
-#pragma unroll
-					for (int r = 0; r < 32; ++r) {
-						const int row = m0 + c_row(i, r), col = n0 + c_col(j);
-						if (!EDGE || (row < p.m && col < p.n))
-							acc[i][j][r] = p.c[oc + (int64_t)row * p.ldc + col] + acc[i][j][r];
-					}
-		}
+	};
+	auto step = [&](int kt) {
+		if (kt + 1 < nkt) load(kt + 1);
+		mma_tile(kt & 1);
+		if (kt + 1 < nkt) store((kt + 1) & 1);
+		__syncthreads();
+	};
+
+	if (nkt > 0) {
+		load(0);
+		store(0);
 		__syncthreads();
 	}
+	// With accumulate, old C joins the chain after the first 256 steps; the loop is split there so the
+	// accumulators never leave the matrix-core registers inside a loop.
+	const bool add_mid = acc_mode && acc_tile >= 0;
+	const int n1 = add_mid ? acc_tile + 1 : nkt;
+	for (int kt = 0; kt < n1; ++kt) step(kt);
+	if (add_mid) {
+		int lane_m = lane;
+		asm volatile("" : "+v"(lane_m));
+#pragma unroll
+		for (int i = 0; i < I; ++i)
+#pragma unroll
+			for (int j = 0; j < J; ++j)
+#pragma unroll
+				for (int r = 0; r < 32; ++r) {
+					const int row = m0 + c_row(i, r, lane_m), col = n0 + c_col(j, lane_m);
+					if (!EDGE || (row < p.m && col < p.n))
+						acc[i][j][r] = p.c[oc + (int64_t)row * p.ldc + col] + acc[i][j][r];
+				}
+	}
+	for (int kt = n1; kt < nkt; ++kt) step(kt);
 
-	// ---- epilogue ----
+	// ---- epilogue ---- (the fenced lane keeps the store addresses from being computed before the loop)
+	int lane_e = lane;
+	asm volatile("" : "+v"(lane_e));
 	if (p.pieces > 1) {
 		float* part = p.partial + ((int64_t)bi * p.pieces + piece) * (int64_t)p.m * p.n;
 #pragma unroll
@@ -294,7 +317,7 @@ __global__ void __launch_bounds__(256) sgemm_tile_kernel(const GemmArgs p) {
 			for (int j = 0; j < J; ++j)
 #pragma unroll
 				for (int r = 0; r < 32; ++r) {
-					const int row = m0 + c_row(i, r), col = n0 + c_col(j);
+					const int row = m0 + c_row(i, r, lane_e), col = n0 + c_col(j, lane_e);
 					if (!EDGE || (row < p.m && col < p.n)) part[(int64_t)row * p.n + col] = acc[i][j][r];
 				}
 		return;
@@ -305,10 +328,13 @@ __global__ void __launch_bounds__(256) sgemm_tile_kernel(const GemmArgs p) {
 #pragma unroll
 	for (int i = 0; i < I; ++i)
 #pragma unroll
-		for (int j = 0; j < J; ++j)
+		for (int j = 0; j < J; ++j) {
+			// one 64 x 32 block at a time: bounds the registers the epilogue keeps live
+			__builtin_amdgcn_sched_barrier(0);
+			const int col = n0 + c_col(j, lane_e);
 #pragma unroll
 			for (int r = 0; r < 32; ++r) {
-				const int row = m0 + c_row(i, r), col = n0 + c_col(j);
+				const int row = m0 + c_row(i, r, lane_e);
 				if (EDGE && (row >= p.m || col >= p.n)) continue;
 				const int64_t off = (int64_t)row * p.ldc + col;
 				float v = acc[i][j][r];
@@ -322,6 +348,7 @@ __global__ void __launch_bounds__(256) sgemm_tile_kernel(const GemmArgs p) {
 				}
 				Cp[off] = v;
 			}
+		}
 }
 
 }  // namespace nnh

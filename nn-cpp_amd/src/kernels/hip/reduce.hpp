@@ -1,0 +1,14 @@
+// reduce.hpp - launchers of the memory-bound kernels in reduce.hip (internal to libnnh).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace nnh {
+
+// dst[j] (combine 0: =, 1: = s + 0.0f, 2: +=) s_j = sum over rows a, in order from +0, of src[a * inner + j].
+hipError_t sum_rows(const float* src, int64_t rows, int64_t inner, float* dst, int combine, hipStream_t s);
+hipError_t relu_forward(const float* x, float* y, int64_t count, hipStream_t s);
+hipError_t relu_backward(const float* x, const float* g, float* dst, int64_t count, int first, hipStream_t s);
+
+}  // namespace nnh

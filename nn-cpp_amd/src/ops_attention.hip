@@ -1,0 +1,150 @@
+// ops_attention.hip - extern "C" entry points of nn::attention and nn::scaled_masked_softmax (include/nnh.h).
+//
+// Forward (src/autograd/ops.cpp:1226-1261) as three launches over all (sample, head) pairs at once:
+//   probs = Q_h K_h^T   (batched sgemm F,T with two-level batch addressing n*T*D + h*Dh, row stride D)
+//   probs = masked_softmax_row(probs) per row
+//   out_h = probs V_h   (batched sgemm F,F into column block h*Dh, row stride D)
+// Backward (ops.cpp:1263-1295): dP = G_h V_h^T, dV (+)= P^T G_h, dS = softmax backward, dQ (+)= dS K_h,
+// dK (+)= dS^T Q_h. Heads write disjoint column blocks, so batching the heads keeps, for every element, the
+// reference's order of contributions (dV, then dQ, then dK, which matters when q, k and v are one node).
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+
+#include "abi_common.hpp"
+#include "kernels/hip/softmax.hpp"
+#include "nnh.h"
+
+using namespace nnh;
+
+namespace {
+
+struct AttnGeom {
+	size_t N, Tq, Tk, D, H, Dh;
+	float scale;
+};
+
+int check_attention(size_t N, size_t Tq, size_t Tk, size_t D, size_t heads, int causal, AttnGeom& a) {
+	// ops.cpp:1228-1236
+	if (heads == 0 || D % heads != 0 || Tq == 0 || Tk == 0 || (causal && Tq != Tk))
+		return fail(NNH_ERR_SHAPE, "attention: heads must divide D, sequences non-empty, causal needs Tq == Tk");
+	a = AttnGeom{N, Tq, Tk, D, heads, D / heads, 1.0f / std::sqrt(static_cast<float>(D / heads))};
+	if ((int64_t)Tk > softmax_max_row_length())
+		return fail(NNH_ERR_INVALID, "attention: key length beyond the row softmax's LDS capacity");
+	return NNH_OK;
+}
+
+// (sample, head) batch over {N, T, D} operands: head h of sample n starts at n*T*D + h*Dh
+nnh_batch head_batch(const AttnGeom& a, size_t ta_rows, size_t tb_rows, bool a_is_probs, bool c_is_probs,
+                     size_t tc_rows) {
+	nnh_batch b{};
+	b.ndim = 2;
+	b.shape[0] = a.N;
+	b.shape[1] = a.H;
+	const ptrdiff_t pp = (ptrdiff_t)(a.Tq * a.Tk);
+	b.stride_a[0] = a_is_probs ? (ptrdiff_t)a.H * pp : (ptrdiff_t)(ta_rows * a.D);
+	b.stride_a[1] = a_is_probs ? pp : (ptrdiff_t)a.Dh;
+	b.stride_b[0] = (ptrdiff_t)(tb_rows * a.D);
+	b.stride_b[1] = (ptrdiff_t)a.Dh;
+	b.stride_c[0] = c_is_probs ? (ptrdiff_t)a.H * pp : (ptrdiff_t)(tc_rows * a.D);
+	b.stride_c[1] = c_is_probs ? pp : (ptrdiff_t)a.Dh;
+	return b;
+}
+
+int gemm(int ta, int tb, size_t m, size_t n, size_t k, const float* A, size_t lda, const float* B, size_t ldb,
+         float* Cm, size_t ldc, int acc, const nnh_batch& batch, void* stream) {
+	GemmCall g;
+	int rc = build_gemm(ta, tb, m, n, k, A, lda, B, ldb, Cm, ldc, acc, &batch, nullptr, g);
+	if (rc != NNH_OK) return rc;
+	return run_gemm(g, stream, -1);
+}
+
+}  // namespace
+
+extern "C" {
+
+int nnh_attention_forward(const float* q, const float* k, const float* v, size_t N, size_t Tq, size_t Tk, size_t D,
+                          size_t heads, const float* key_padding_mask, int causal, float* out, float* probs,
+                          void* stream) {
+	AttnGeom a;
+	int rc = check_attention(N, Tq, Tk, D, heads, causal, a);
+	if (rc != NNH_OK) return rc;
+	if (N == 0) return NNH_OK;
+	if (!q || !k || !v || !out || !probs) return fail(NNH_ERR_INVALID, "attention: null pointer");
+	hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+	// S = Q_h K_h^T into probs (ops.cpp:1256)
+	rc = gemm(0, 1, Tq, Tk, a.Dh, q, D, k, D, probs, Tk, 0, head_batch(a, Tq, Tk, false, true, 0), stream);
+	if (rc != NNH_OK) return rc;
+	rc = hip_status(softmax_rows(probs, probs, (int64_t)(N * heads * Tq), (int)Tk, (int)Tq, (int)heads, a.scale,
+	                             key_padding_mask, causal, s),
+	                "attention softmax");
+	if (rc != NNH_OK) return rc;
+	// O_h = P V_h into column block h (ops.cpp:1259)
+	nnh_batch bo = head_batch(a, 0, Tk, true, false, Tq);
+	return gemm(0, 0, Tq, a.Dh, Tk, probs, Tk, v, D, out, D, 0, bo, stream);
+}
+
+int nnh_attention_backward(const float* g, const float* q, const float* k, const float* v, const float* probs,
+                           size_t N, size_t Tq, size_t Tk, size_t D, size_t heads, const float* key_padding_mask,
+                           int causal, float* dq, int dq_first, float* dk, int dk_first, float* dv, int dv_first,
+                           void* stream) {
+	AttnGeom a;
+	int rc = check_attention(N, Tq, Tk, D, heads, causal, a);
+	if (rc != NNH_OK) return rc;
+	if (N == 0 || (!dq && !dk && !dv)) return NNH_OK;
+	if (!g || !q || !k || !v || !probs) return fail(NNH_ERR_INVALID, "attention backward: null pointer");
+	hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+	float* ds = nullptr;
+	const size_t ds_floats = N * heads * Tq * Tk;
+	rc = hip_status(hipMallocAsync(reinterpret_cast<void**>(&ds), ds_floats * sizeof(float), s), "attention workspace");
+	if (rc != NNH_OK) return rc;
+	// dP = G_h V_h^T (ops.cpp:1286)
+	rc = gemm(0, 1, Tq, Tk, a.Dh, g, D, v, D, ds, Tk, 0, head_batch(a, Tq, Tk, false, true, 0), stream);
+	// dV (+)= P^T G_h (ops.cpp:1287): A = probs stored Tq x Tk, read transposed
+	if (rc == NNH_OK && dv) {
+		nnh_batch b = head_batch(a, 0, Tq, true, false, Tk);
+		rc = gemm(1, 0, Tk, a.Dh, Tq, probs, Tk, g, D, dv, D, !dv_first, b, stream);
+	}
+	if (rc == NNH_OK && (dq || dk))
+		rc = hip_status(softmax_backward_rows(probs, ds, ds, (int64_t)(N * heads * Tq), (int)Tk, (int)Tq, (int)heads,
+		                                      a.scale, key_padding_mask, causal, 0, s),
+		                "attention softmax backward");
+	// dQ (+)= dS K_h (ops.cpp:1291)
+	if (rc == NNH_OK && dq) {
+		nnh_batch b = head_batch(a, 0, Tk, true, false, Tq);
+		rc = gemm(0, 0, Tq, a.Dh, Tk, ds, Tk, k, D, dq, D, !dq_first, b, stream);
+	}
+	// dK (+)= dS^T Q_h (ops.cpp:1292)
+	if (rc == NNH_OK && dk) {
+		nnh_batch b = head_batch(a, 0, Tq, true, false, Tk);
+		rc = gemm(1, 0, Tk, a.Dh, Tq, ds, Tk, q, D, dk, D, !dk_first, b, stream);
+	}
+	const int rc2 = hip_status(hipFreeAsync(ds, s), "attention workspace");
+	return rc != NNH_OK ? rc : rc2;
+}
+
+int nnh_scaled_masked_softmax_forward(const float* x, size_t N, size_t H, size_t Tq, size_t Tk, float scale,
+                                      const float* key_padding_mask, int causal, float* y, void* stream) {
+	if (Tk == 0) return fail(NNH_ERR_SHAPE, "scaled_masked_softmax: empty rows");  // ops.cpp:1300
+	if (N == 0 || H == 0 || Tq == 0) return NNH_OK;
+	if (!x || !y) return fail(NNH_ERR_INVALID, "null pointer");
+	if ((int64_t)Tk > softmax_max_row_length()) return fail(NNH_ERR_INVALID, "row too long for the row softmax");
+	return hip_status(softmax_rows(x, y, (int64_t)(N * H * Tq), (int)Tk, (int)Tq, (int)H, scale, key_padding_mask,
+	                               causal, reinterpret_cast<hipStream_t>(stream)),
+	                  "scaled_masked_softmax");
+}
+
+int nnh_scaled_masked_softmax_backward(const float* y, const float* g, size_t N, size_t H, size_t Tq, size_t Tk,
+                                       float scale, const float* key_padding_mask, int causal, float* dx, int first,
+                                       void* stream) {
+	if (Tk == 0) return fail(NNH_ERR_SHAPE, "scaled_masked_softmax: empty rows");
+	if (N == 0 || H == 0 || Tq == 0) return NNH_OK;
+	if (!y || !g || !dx) return fail(NNH_ERR_INVALID, "null pointer");
+	if ((int64_t)Tk > softmax_max_row_length()) return fail(NNH_ERR_INVALID, "row too long for the row softmax");
+	return hip_status(softmax_backward_rows(y, g, dx, (int64_t)(N * H * Tq), (int)Tk, (int)Tq, (int)H, scale,
+	                                        key_padding_mask, causal, first ? 1 : 2,
+	                                        reinterpret_cast<hipStream_t>(stream)),
+	                  "scaled_masked_softmax backward");
+}
+
+}  // extern "C"

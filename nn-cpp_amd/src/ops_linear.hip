@@ -1,0 +1,115 @@
+// ops_linear.hip - extern "C" entry points of nn::linear and the ReLU node (include/nnh.h).
+#include <hip/hip_runtime.h>
+
+#include <vector>
+
+#include "abi_common.hpp"
+#include "kernels/hip/reduce.hpp"
+#include "nnh.h"
+
+using namespace nnh;
+
+namespace {
+
+bool product_fits(const size_t* dims, int n, size_t& out) {
+	size_t p = 1;
+	for (int i = 0; i < n; ++i) {
+		if (dims[i] != 0 && p > SIZE_MAX / dims[i]) return false;
+		p *= dims[i];
+	}
+	out = p;
+	return true;
+}
+
+}  // namespace
+
+extern "C" {
+
+int nnh_linear_forward(const float* x, size_t M, size_t K, const float* w, size_t n, const float* bias, int relu,
+                       float* y, void* stream) {
+	if (M > 0 && n > 0 && !bias) return fail(NNH_ERR_INVALID, "bias is null");
+	nnh_epilogue ep{NNH_BIAS_COL, relu ? 1 : 0, bias, nullptr};
+	GemmCall g;
+	// Y = X W^T (ops.cpp:725): sgemm(F, T, M, n, K, x, K, w, K, y, n, false), then + bias (726-730)
+	int rc = build_gemm(0, 1, M, n, K, x, K, w, K, y, n, 0, nullptr, &ep, g);
+	if (rc != NNH_OK) return rc;
+	return run_gemm(g, stream, -1);
+}
+
+int nnh_linear_backward(const float* g, const float* x, const float* w, const size_t* lead, int nlead, size_t K,
+                        size_t n, float* dx, int dx_first, float* dw, int dw_first, float* db, int db_first,
+                        void* stream) {
+	if (nlead < 1 || !lead) return fail(NNH_ERR_SHAPE, "linear input needs at least 2 dimensions");
+	size_t M = 0;
+	if (!product_fits(lead, nlead, M)) return fail(NNH_ERR_INVALID, "input size overflows");
+	hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+	GemmCall call;
+	if (dx) {  // dX = G W (ops.cpp:737)
+		int rc = build_gemm(0, 0, M, K, n, g, n, w, K, dx, K, !dx_first, nullptr, nullptr, call);
+		if (rc != NNH_OK) return rc;
+		rc = run_gemm(call, stream, -1);
+		if (rc != NNH_OK) return rc;
+	}
+	if (dw) {  // dW = G^T X (ops.cpp:741)
+		int rc = build_gemm(1, 0, n, K, M, g, n, x, K, dw, K, !dw_first, nullptr, nullptr, call);
+		if (rc != NNH_OK) return rc;
+		rc = run_gemm(call, stream, -1);
+		if (rc != NNH_OK) return rc;
+	}
+	if (db && n > 0) {
+		// accumulate_grad(bias, G): Tensor::sum(0) once per leading axis (ops.cpp:35-53), then stored as
+		// s + 0.0f into a fresh gradient or added (ops.cpp:85-99)
+		if (M > 0 && !g) return fail(NNH_ERR_INVALID, "G is null");
+		if (ranges_overlap(db, n * 4, g, (uint64_t)M * n * 4)) return fail(NNH_ERR_ALIAS, "db overlaps G");
+		const int combine = db_first ? 1 : 2;
+		if (nlead == 1) return hip_status(sum_rows(g, (int64_t)lead[0], (int64_t)n, db, combine, s), "bias gradient");
+		// suffix[d] = n * prod(lead[d+1 ..]): the row length left after reducing axes 0..d
+		std::vector<size_t> suffix(nlead);
+		suffix[nlead - 1] = n;
+		for (int d = nlead - 2; d >= 0; --d) suffix[d] = suffix[d + 1] * lead[d + 1];
+		float* tmp[2] = {nullptr, nullptr};
+		hipError_t e = hipSuccess;
+		const float* cur = g;
+		for (int d = 0; d < nlead && e == hipSuccess; ++d) {
+			if (d == nlead - 1) {
+				e = sum_rows(cur, (int64_t)lead[d], (int64_t)n, db, combine, s);
+				break;
+			}
+			float*& out = tmp[d & 1];
+			if (!out) e = hipMallocAsync(reinterpret_cast<void**>(&out), (suffix[0] ? suffix[0] : 1) * sizeof(float), s);
+			if (e != hipSuccess) break;
+			e = sum_rows(cur, (int64_t)lead[d], (int64_t)suffix[d], out, 0, s);
+			cur = out;
+		}
+		for (float* t : tmp)
+			if (t) {
+				hipError_t e2 = hipFreeAsync(t, s);
+				if (e == hipSuccess) e = e2;
+			}
+		return hip_status(e, "bias gradient");
+	}
+	return NNH_OK;
+}
+
+int nnh_relu_forward(const float* x, float* y, size_t count, void* stream) {
+	if (count == 0) return NNH_OK;
+	if (!x || !y) return fail(NNH_ERR_INVALID, "null pointer");
+	return hip_status(relu_forward(x, y, (int64_t)count, reinterpret_cast<hipStream_t>(stream)), "relu forward");
+}
+
+int nnh_relu_backward(const float* x, const float* g, float* dx, int first, size_t count, void* stream) {
+	if (count == 0) return NNH_OK;
+	if (!x || !g || !dx) return fail(NNH_ERR_INVALID, "null pointer");
+	return hip_status(relu_backward(x, g, dx, (int64_t)count, first, reinterpret_cast<hipStream_t>(stream)),
+	                  "relu backward");
+}
+
+int nnh_tensor_sum0(const float* src, size_t rows, size_t inner, float* dst, int combine, void* stream) {
+	if (inner == 0) return NNH_OK;
+	if (!dst || (rows > 0 && !src)) return fail(NNH_ERR_INVALID, "null pointer");
+	if (combine < 0 || combine > 2) return fail(NNH_ERR_INVALID, "combine must be 0, 1 or 2");
+	return hip_status(sum_rows(src, (int64_t)rows, (int64_t)inner, dst, combine, reinterpret_cast<hipStream_t>(stream)),
+	                  "sum0");
+}
+
+}  // extern "C"

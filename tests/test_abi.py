@@ -1,0 +1,87 @@
+"""The C ABI without a GPU: the library loads, exports every function include/nnh.h declares, and rejects
+invalid calls on the host before touching the device (no compute call is made here)."""
+import ctypes as C
+
+import pytest
+
+import nnh
+
+
+def test_library_exports_every_declared_function():
+    L = nnh.lib()
+    names = nnh.header_functions()
+    assert "nnh_sgemm" in names and len(names) >= 8
+    missing = [n for n in names if not hasattr(L, n)]
+    assert not missing, missing
+
+
+def test_version_and_configs():
+    assert b"gfx950" in nnh.lib().nnh_version()
+    assert len(nnh.gemm_configs()) >= 1
+
+
+def _sgemm(*args):
+    return nnh.lib().nnh_sgemm(*args)
+
+
+FAKE_A, FAKE_B, FAKE_C = 0x10000000, 0x20000000, 0x30000000  # host-side address checks only
+
+
+def test_invalid_arguments_are_rejected_on_the_host():
+    L = nnh.lib()
+    # null operands with k > 0
+    assert _sgemm(0, 0, 4, 4, 4, None, 4, C.c_void_p(FAKE_B), 4, C.c_void_p(FAKE_C), 4, 0, None) == nnh.ERR_INVALID
+    assert _sgemm(0, 0, 4, 4, 4, C.c_void_p(FAKE_A), 4, C.c_void_p(FAKE_B), 4, None, 4, 0, None) == nnh.ERR_INVALID
+    # leading dimensions too small for the stored layouts
+    assert _sgemm(0, 0, 4, 5, 6, C.c_void_p(FAKE_A), 5, C.c_void_p(FAKE_B), 5, C.c_void_p(FAKE_C), 5, 0, None) == nnh.ERR_INVALID
+    assert _sgemm(1, 0, 4, 5, 6, C.c_void_p(FAKE_A), 3, C.c_void_p(FAKE_B), 5, C.c_void_p(FAKE_C), 5, 0, None) == nnh.ERR_INVALID
+    assert _sgemm(0, 1, 4, 5, 6, C.c_void_p(FAKE_A), 6, C.c_void_p(FAKE_B), 5, C.c_void_p(FAKE_C), 5, 0, None) == nnh.ERR_INVALID
+    assert _sgemm(0, 0, 4, 5, 6, C.c_void_p(FAKE_A), 6, C.c_void_p(FAKE_B), 5, C.c_void_p(FAKE_C), 4, 0, None) == nnh.ERR_INVALID
+    assert b"ldc" in L.nnh_last_error()
+    # sizes beyond the kernel's 32-bit index range
+    assert _sgemm(0, 0, 1 << 31, 4, 4, C.c_void_p(FAKE_A), 4, C.c_void_p(FAKE_B), 4, C.c_void_p(FAKE_C), 4, 0, None) == nnh.ERR_INVALID
+
+
+def test_output_aliasing_an_input_is_rejected():
+    """include/nn/kernels/gemm.hpp:37-39: C must not alias A or B."""
+    assert _sgemm(0, 0, 4, 4, 4, C.c_void_p(FAKE_A), 4, C.c_void_p(FAKE_B), 4, C.c_void_p(FAKE_A + 16), 4, 0, None) == nnh.ERR_ALIAS
+    assert _sgemm(0, 0, 4, 4, 4, C.c_void_p(FAKE_A), 4, C.c_void_p(FAKE_B), 4, C.c_void_p(FAKE_B - 16), 4, 0, None) == nnh.ERR_ALIAS
+
+
+def test_empty_products_touch_nothing_and_need_no_device():
+    """m == 0 or n == 0 returns before any device work (gemm.cpp:344); null pointers are then fine."""
+    assert _sgemm(0, 0, 0, 5, 4, None, 4, None, 5, None, 5, 0, None) == nnh.OK
+    assert _sgemm(0, 0, 3, 0, 4, None, 4, None, 1, None, 1, 1, None) == nnh.OK
+
+
+def test_matmul_shapes_follow_the_reference():
+    """tests/test_tensor.cpp:385-392 and 444-450: result shapes and TensorShapeError cases."""
+    assert nnh.matmul_shape((2, 3), (3, 2)) == (2, 2)
+    assert nnh.matmul_shape((0, 3), (3, 2)) == (0, 2)
+    assert nnh.matmul_shape((2, 0), (0, 3)) == (2, 3)
+    assert nnh.matmul_shape((2, 3), (3, 0)) == (2, 0)
+    assert nnh.matmul_shape((3, 4), (3, 5), True, False) == (4, 5)
+    assert nnh.matmul_shape((4, 7, 33), (33, 5)) == (4, 7, 5)          # fold path
+    assert nnh.matmul_shape((1, 7, 33), (4, 33, 5)) == (4, 7, 5)       # broadcast
+    assert nnh.matmul_shape((2, 1, 9, 7), (1, 3, 6, 9), True, True) == (2, 3, 7, 6)
+    for a, b, ta, tb in (((3, 4), (3, 5), 0, 0), ((3, 4), (3, 5), 0, 1), ((3,), (3, 5), 0, 0),
+                         ((2, 3, 4), (3, 4, 5), 0, 0), ((2, 3), (4, 2), 0, 0)):
+        with pytest.raises(nnh.ShapeError):
+            nnh.matmul_shape(a, b, ta, tb)
+
+
+def test_matmul_shapes_and_errors_match_nncpp(ref):
+    """Result shapes and shape errors agree with nn::matmul itself over random shape combinations."""
+    import numpy as np
+    rng = np.random.default_rng(11)
+    for _ in range(300):
+        an, bn = int(rng.integers(1, 5)), int(rng.integers(1, 5))
+        dims = lambda n: tuple(int(d) for d in rng.choice([1, 2, 3], n))
+        a_shape, b_shape = dims(an), dims(bn)
+        ta, tb = bool(rng.integers(0, 2)), bool(rng.integers(0, 2))
+        rc, out = ref.matmul(np.ones(a_shape, np.float32), np.ones(b_shape, np.float32), ta, tb)
+        try:
+            got = nnh.matmul_shape(a_shape, b_shape, ta, tb)
+            assert rc == 0 and out.shape == got, (a_shape, b_shape, ta, tb)
+        except nnh.ShapeError:
+            assert rc == 2, (a_shape, b_shape, ta, tb)

@@ -1,0 +1,161 @@
+"""Parity of nn::matmul (Tensor batched matmul), nn::linear and the ReLU node on the GPU.
+
+Golden vectors are nn-cpp's own outputs (tests/golden/reference_vectors.npz, written from its compiled
+sources); every comparison is bitwise. BASELINE config 2 (3-layer MLP, forward and backward) is checked
+against the oracle at full size.
+"""
+import numpy as np
+import pytest
+
+from helpers import first_diff
+from nnh import synth
+
+pytestmark = pytest.mark.gpu
+
+
+def dev(a):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def host(t):
+    import torch
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def same(got, want, what):
+    assert got.shape == want.shape, (what, got.shape, want.shape)
+    assert got.tobytes() == want.tobytes(), f"{what}: {first_diff(got, want)}"
+
+
+# ------------------------------------------------------------------ matmul
+
+def test_matmul_golden(gpu):
+    import golden_cases as gc
+
+    import nnh
+    g = np.load(gc.__file__.replace("golden_cases.py", "reference_vectors.npz"))
+    for name, spec in gc.MATMUL_CASES:
+        a, b, ta, tb = gc.matmul_inputs(spec)
+        same(host(nnh.matmul(dev(a), dev(b), ta, tb)), g[f"matmul/{name}"], name)
+
+
+def test_matmul_hand_values(gpu):
+    """tests/test_tensor.cpp:365-392."""
+    import nnh
+    a = np.array([[1, 2, 3], [4, 5, 6]], np.float32)
+    b = np.array([[7, 8], [9, 10], [11, 12]], np.float32)
+    assert host(nnh.matmul(dev(a), dev(b))).tolist() == [[58, 64], [139, 154]]
+    ab = np.array([1, 0, 0, 1, 2, 0, 0, 2], np.float32).reshape(2, 2, 2)
+    c = host(nnh.matmul(dev(ab), dev(np.ones((2, 2, 2), np.float32))))
+    assert c[0, 0, 0] == 1.0 and c[1, 0, 0] == 2.0
+    import torch
+    e = nnh.matmul(torch.zeros((0, 3), device="cuda"), torch.zeros((3, 2), device="cuda"))
+    assert tuple(e.shape) == (0, 2)
+    e = host(nnh.matmul(torch.zeros((2, 0), device="cuda"), torch.zeros((0, 3), device="cuda")))
+    assert e.shape == (2, 3) and np.all(e == 0.0)
+    assert tuple(nnh.matmul(torch.zeros((2, 3), device="cuda"), torch.zeros((3, 0), device="cuda")).shape) == (2, 0)
+
+
+def test_matmul_flags_match_oracle(gpu, oracle):
+    """test_tensor.cpp:403-442's check_flags shapes, every flag combination, bit-exact with the oracle."""
+    import nnh
+    from test_oracle import oracle_matmul
+    rng = np.random.default_rng(1)
+    for a_shape, b_shape in (((7, 33), (33, 5)), ((4, 7, 33), (4, 33, 5)), ((1, 7, 33), (4, 33, 5)),
+                             ((4, 7, 33), (33, 5)), ((2, 3, 65, 129), (1, 3, 129, 70))):
+        for f in range(4):
+            ta, tb = bool(f & 1), bool(f & 2)
+            a = rng.uniform(-1, 1, a_shape).astype(np.float32)
+            b = rng.uniform(-1, 1, b_shape).astype(np.float32)
+            sa = np.ascontiguousarray(np.swapaxes(a, -1, -2)) if ta else a
+            sb = np.ascontiguousarray(np.swapaxes(b, -1, -2)) if tb else b
+            got = host(nnh.matmul(dev(sa), dev(sb), ta, tb))
+            same(got, oracle_matmul(oracle, sa, sb, ta, tb), (a_shape, b_shape, ta, tb))
+
+
+def test_matmul_shape_error(gpu):
+    import nnh
+    with pytest.raises(nnh.ShapeError):
+        import torch
+        nnh.matmul(torch.zeros((2, 3), device="cuda"), torch.zeros((4, 2), device="cuda"))
+
+
+# ------------------------------------------------------------------ linear
+
+def test_linear_golden(gpu):
+    import golden_cases as gc
+    import torch
+
+    import nnh
+    g = np.load(gc.__file__.replace("golden_cases.py", "reference_vectors.npz"))
+    for name, spec in gc.LINEAR_CASES:
+        x, w, bias, gr = gc.linear_inputs(spec)
+        same(host(nnh.linear_forward(dev(x), dev(w), dev(bias))), g[f"linear/{name}/y"], name)
+        # nn-cpp's leaves accumulate into zero-filled gradients (first == false)
+        dx, dw, db = (torch.zeros(s, device="cuda") for s in (x.shape, w.shape, bias.shape))
+        nnh.linear_backward(dev(gr), dev(x), dev(w), dx, False, dw, False, db, False)
+        for key, t in (("dx", dx), ("dw", dw), ("db", db)):
+            same(host(t), g[f"linear/{name}/{key}"], (name, key))
+
+
+def test_linear_first_write_overwrites(gpu, oracle):
+    """A fresh gradient is overwritten (sgemm without accumulate; bias s + 0.0f): garbage in the buffer
+    must not leak into the result."""
+    import torch
+
+    import nnh
+    x, w, gr = (synth.mt19937_uniform(s, n).reshape(sh) for s, n, sh in
+                ((7, 300 * 70, (300, 70)), (8, 40 * 70, (40, 70)), (9, 300 * 40, (300, 40))))
+    dx, dw, db = (torch.full(s, float("nan"), device="cuda") for s in (x.shape, w.shape, (40,)))
+    nnh.linear_backward(dev(gr), dev(x), dev(w), dx, True, dw, True, db, True)
+    want = oracle.linear_backward(gr, x, w, dx_first=True, dw_first=True, db_first=True)
+    for t, wv, key in zip((dx, dw, db), want, ("dx", "dw", "db")):
+        same(host(t), wv, key)
+
+
+def test_relu_node(gpu, oracle):
+    import torch
+
+    import nnh
+    x = synth.mt19937_uniform(5, 10007)
+    x[::97] = 0.0
+    x[1::101] = -0.0
+    y = host(nnh.relu_forward(dev(x)))
+    same(y, oracle.relu(x), "relu forward")
+    g = synth.mt19937_uniform(6, 10007)
+    for first in (True, False):
+        d0 = synth.mt19937_uniform(7, 10007)
+        d = dev(d0)
+        nnh.relu_backward(dev(x), dev(g), d, first)
+        term = np.where(x > 0, g, np.float32(0)).astype(np.float32)
+        want = (term + np.float32(0)) if first else (d0 + term)
+        same(host(d), want.astype(np.float32), f"relu backward first={first}")
+
+
+def test_baseline_config2_mlp(gpu, oracle):
+    """X[256 x 784] ~ U[0,1], layers 784->512->256->10 with weights {out, in} ~ U(+-1/sqrt(in))
+    (nn-cpp's Linear init bound), zero biases, y = ReLU(X W^T + b) per layer; backward of each layer with
+    dY ~ N(0,1): dX = dY W, dW = dY^T X, db. Everything bit-identical to nn-cpp's arithmetic."""
+    import torch
+
+    import nnh
+    dims = [784, 512, 256, 10]
+    x = synth.mt19937_uniform(1, 256 * 784, 0.0, 1.0).reshape(256, 784)
+    acts = [x]
+    for li in range(3):
+        fan_in, fan_out = dims[li], dims[li + 1]
+        bound = float(1.0 / np.sqrt(fan_in))
+        w = synth.mt19937_uniform(100 + li, fan_out * fan_in, -bound, bound).reshape(fan_out, fan_in)
+        b = np.zeros(fan_out, np.float32)
+        y_gpu = host(nnh.linear_forward(dev(acts[-1]), dev(w), dev(b), relu=True))
+        y_ref = oracle.relu(oracle.linear_forward(acts[-1], w, b))
+        same(y_gpu, y_ref, f"layer {li} forward")
+        gy = synth.normal(200 + li, (256, fan_out))
+        dx, dw, db = (torch.zeros(s, device="cuda") for s in ((256, fan_in), w.shape, b.shape))
+        nnh.linear_backward(dev(gy), dev(acts[-1]), dev(w), dx, True, dw, True, db, True)
+        want = oracle.linear_backward(gy, acts[-1], w, dx_first=True, dw_first=True, db_first=True)
+        for t, wv, key in zip((dx, dw, db), want, ("dx", "dw", "db")):
+            same(host(t), wv, f"layer {li} {key}")
+        acts.append(y_ref)

@@ -1,0 +1,332 @@
+"""Pins the oracle (CPU, no GPU): the C restatement of nn-cpp must be right before it can judge the GPU.
+
+Each restated function is checked against at least one of: nn-cpp's own outputs (golden vectors written from
+its compiled sources, and the compiled library itself when present), hand values from the reference's
+tests, exact integer arithmetic, an fp64 closed form with the north-star bound, or an algebraic identity
+(transposes, adjointness). The checks are chosen so a dropped term, a swapped index or a wrong flag fails.
+"""
+import os
+
+import numpy as np
+import pytest
+
+from nnh import synth
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+GOLDEN = os.path.join(HERE, "golden", "reference_vectors.npz")
+
+
+def golden():
+    import sys
+    sys.path.insert(0, os.path.join(HERE, "golden"))
+    import golden_cases
+    return golden_cases, np.load(GOLDEN, allow_pickle=False)
+
+
+# ---------------------------------------------------------------- inputs
+
+def test_mt19937_raw_stream_is_the_standard_one():
+    """[rand.predef]: the 10000th output of a default-constructed std::mt19937 (seed 5489) is 4123659995."""
+    assert int(synth.mt19937_raw(5489, 10000)[-1]) == 4123659995
+
+
+@pytest.mark.parametrize("seed,lo,hi", [(0, -1.0, 1.0), (1, 0.0, 1.0), (4, -1.0, 1.0), (2, -0.3, 0.3), (99, -2.0, 2.0)])
+def test_uniform_stream_matches_libstdcxx(oracle, seed, lo, hi):
+    """nnh.synth reproduces std::uniform_real_distribution<float> over std::mt19937 bit for bit."""
+    assert synth.mt19937_uniform(seed, 200000, lo, hi).tobytes() == oracle.mt19937_uniform(seed, lo, hi, 200000).tobytes()
+
+
+# ---------------------------------------------------------------- golden vectors (nn-cpp's own outputs)
+
+def test_golden_sgemm(oracle):
+    gc, g = golden()
+    for name, spec in gc.SGEMM_CASES:
+        ta, tb, m, n, k, acc, pad, seed = spec
+        a, lda, b, ldb, c, ldc = gc.sgemm_inputs(*spec)
+        got = oracle.sgemm(ta, tb, m, n, k, a, lda, b, ldb, c, ldc, acc)
+        assert got.tobytes() == g[f"sgemm/{name}"].tobytes(), name
+
+
+def test_golden_linear(oracle):
+    gc, g = golden()
+    for name, spec in gc.LINEAR_CASES:
+        x, w, bias, gr = gc.linear_inputs(spec)
+        assert oracle.linear_forward(x, w, bias).tobytes() == g[f"linear/{name}/y"].tobytes(), name
+        # leaves accumulate into zeroed gradients (first == false), as in a training step
+        dx, dw, db = oracle.linear_backward(gr, x, w, dx_first=False, dw_first=False, db_first=False)
+        for key, arr in (("dx", dx), ("dw", dw), ("db", db)):
+            assert arr.tobytes() == g[f"linear/{name}/{key}"].tobytes(), (name, key)
+
+
+def test_golden_conv(oracle):
+    gc, g = golden()
+    for name, spec in gc.CONV_CASES:
+        x, w, bias, gr, stride, pad, relu = gc.conv_inputs(spec)
+        y, alive = oracle.conv2d_forward(x, w, bias, stride, pad, relu)
+        assert y.tobytes() == g[f"conv/{name}/y"].tobytes(), name
+        dx, dw, db = oracle.conv2d_backward(gr, x, w, alive if relu else None, stride, pad)
+        for key, arr in (("dx", dx), ("dw", dw), ("db", db)):
+            assert arr.tobytes() == g[f"conv/{name}/{key}"].tobytes(), (name, key)
+
+
+def test_golden_attention(oracle):
+    gc, g = golden()
+    for name, spec in gc.ATTENTION_CASES:
+        q, k, v, heads, mask, causal, gr = gc.attention_inputs(spec)
+        out, probs = oracle.attention_forward(q, k, v, heads, mask, causal)
+        assert out.tobytes() == g[f"attention/{name}/out"].tobytes(), name
+        dq, dk, dv = oracle.attention_backward(gr, q, k, v, probs, heads, mask, causal)
+        for key, arr in (("dq", dq), ("dk", dk), ("dv", dv)):
+            assert arr.tobytes() == g[f"attention/{name}/{key}"].tobytes(), (name, key)
+
+
+def test_golden_matmul_against_batched_sgemm(oracle):
+    """nn::matmul's batching (broadcast, fold) as per-matrix oracle sgemm calls reproduces nn-cpp's bits."""
+    gc, g = golden()
+    for name, spec in gc.MATMUL_CASES:
+        a, b, ta, tb = gc.matmul_inputs(spec)
+        want = g[f"matmul/{name}"]
+        assert oracle_matmul(oracle, a, b, ta, tb).tobytes() == want.tobytes(), name
+
+
+def oracle_matmul(oracle, a, b, ta, tb):
+    """nn::matmul (src/tensor.cpp:571-641) composed from oracle sgemm calls."""
+    a_rows, a_cols = a.shape[-2:]
+    b_rows, b_cols = b.shape[-2:]
+    m, k = (a_cols, a_rows) if ta else (a_rows, a_cols)
+    n = b_rows if tb else b_cols
+    if b.ndim == 2 and not ta and a.ndim > 2:
+        M = a.size // a_cols
+        out = np.zeros(a.shape[:-1] + (n,), np.float32)
+        return oracle.sgemm(0, tb, M, n, k, a, a_cols, b, b_cols, out.reshape(M, n), n, 0).reshape(out.shape)
+    batch = np.broadcast_shapes(a.shape[:-2], b.shape[:-2])
+    out = np.zeros(batch + (m, n), np.float32)
+    ab = np.broadcast_to(a, batch + a.shape[-2:])
+    bb = np.broadcast_to(b, batch + b.shape[-2:])
+    for idx in np.ndindex(*batch):
+        out[idx] = oracle.sgemm(ta, tb, m, n, k, np.ascontiguousarray(ab[idx]), a_cols, np.ascontiguousarray(bb[idx]),
+                                b_cols, out[idx], n, 0)
+    return out
+
+
+# ---------------------------------------------------------------- the compiled reference itself
+
+def test_oracle_sgemm_matches_nncpp_sweep(oracle, ref):
+    """Random sweep of shapes, flags, accumulate and ld padding, including depth-cut shapes: bit-identical."""
+    rng = np.random.default_rng(7)
+    sizes = (1, 2, 7, 33, 64, 129, 257)
+    cases = [(int(rng.choice(sizes)), int(rng.choice(sizes)), int(rng.choice(sizes))) for _ in range(24)]
+    cases += [(64, 64, 1024), (40, 48, 589), (7, 300, 768), (64, 64, 511), (300, 300, 512), (5, 9, 1100)]
+    seed = 100
+    for (m, n, k) in cases:
+        for ta in (0, 1):
+            for tb in (0, 1):
+                for acc in (0, 1):
+                    spec = (ta, tb, m, n, k, acc, int(rng.integers(0, 4)), seed)
+                    seed += 1
+                    import golden_cases as gc
+                    a, lda, b, ldb, c, ldc = gc.sgemm_inputs(*spec)
+                    x = oracle.sgemm(ta, tb, m, n, k, a, lda, b, ldb, c, ldc, acc)
+                    y = ref.sgemm(ta, tb, m, n, k, a, lda, b, ldb, c, ldc, acc)
+                    assert x.tobytes() == y.tobytes(), spec
+
+
+def test_oracle_ops_match_nncpp(oracle, ref):
+    rng = np.random.default_rng(8)
+    for _ in range(4):
+        M, K, n = (int(v) for v in rng.integers(1, 80, 3))
+        x, w, bias, g = (rng.uniform(-1, 1, s).astype(np.float32) for s in ((M, K), (n, K), (n,), (M, n)))
+        assert oracle.linear_forward(x, w, bias).tobytes() == ref.linear_forward(x, w, bias).tobytes()
+        got = oracle.linear_backward(g, x, w, dx_first=False, dw_first=False, db_first=False)
+        for p, q in zip(got, ref.linear_backward(x, w, bias, g)):
+            assert p.tobytes() == q.tobytes()
+    for (N, Cin, H, W, Cout, kk, s, p_) in ((2, 3, 11, 9, 5, 3, 1, 1), (3, 1, 8, 8, 4, 2, 2, 0)):
+        x = rng.uniform(-1, 1, (N, Cin, H, W)).astype(np.float32)
+        w = rng.uniform(-1, 1, (Cout, Cin, kk, kk)).astype(np.float32)
+        bias = rng.uniform(-1, 1, Cout).astype(np.float32)
+        for relu in (0, 1):
+            y, alive = oracle.conv2d_forward(x, w, bias, s, p_, relu)
+            assert y.tobytes() == ref.conv2d_forward(x, w, bias, s, p_, relu).tobytes()
+    for causal in (0, 1):
+        q, k, v = (rng.standard_normal((2, 9, 12)).astype(np.float32) for _ in range(3))
+        out, _ = oracle.attention_forward(q, k, v, 3, None, causal)
+        assert out.tobytes() == ref.attention_forward(q, k, v, 3, None, causal).tobytes()
+        x = rng.standard_normal((2, 3, 9, 9)).astype(np.float32)
+        assert oracle.scaled_masked_softmax(x, 0.25, None, causal).tobytes() == \
+            ref.scaled_masked_softmax(x, 0.25, None, causal).tobytes()
+
+
+# ---------------------------------------------------------------- hand values from the reference's tests
+
+def test_hand_values_matmul(oracle):
+    """tests/test_tensor.cpp:365-383."""
+    a = np.array([[1, 2, 3], [4, 5, 6]], np.float32)
+    b = np.array([[7, 8], [9, 10], [11, 12]], np.float32)
+    got = oracle.sgemm(0, 0, 2, 2, 3, a, 3, b, 2, np.zeros((2, 2), np.float32), 2, 0)
+    assert got.tolist() == [[58.0, 64.0], [139.0, 154.0]]
+    ab = np.array([1, 0, 0, 1, 2, 0, 0, 2], np.float32).reshape(2, 2, 2)
+    bb = np.ones((2, 2, 2), np.float32)
+    c = oracle_matmul(oracle, ab, bb, 0, 0)
+    assert c[0, 0, 0] == 1.0 and c[1, 0, 0] == 2.0
+
+
+def test_hand_values_linear(oracle):
+    """tests/test_nn.cpp:44-65: 1*3 + 2*4 + 0.5, and x W^T + b = 4.5, 9, 8.5, 16."""
+    y = oracle.linear_forward(np.array([[3, 4]], np.float32), np.array([[1, 2]], np.float32), np.array([0.5], np.float32))
+    assert y.tolist() == [[11.5]]
+    w = np.array([[1, 2, 3], [4, 5, 6]], np.float32)
+    y = oracle.linear_forward(np.array([[1, 0, 1], [0, 1, 2]], np.float32), w, np.array([0.5, -1.0], np.float32))
+    assert y.tolist() == [[4.5, 9.0], [8.5, 16.0]]
+
+
+def test_hand_values_conv(oracle):
+    """tests/test_autograd.cpp:374-382: identity-diagonal 2x2 kernel over 1..9 gives 1+5 and 5+9."""
+    x = np.arange(1, 10, dtype=np.float32).reshape(1, 1, 3, 3)
+    w = np.array([1, 0, 0, 1], np.float32).reshape(1, 1, 2, 2)
+    y, _ = oracle.conv2d_forward(x, w, np.zeros(1, np.float32), 1, 0, 0)
+    assert y.shape == (1, 1, 2, 2) and y[0, 0, 0, 0] == 6.0 and y[0, 0, 1, 1] == 14.0
+
+
+def test_hand_values_attention(oracle):
+    """tests/test_transformer.cpp:149-176 (identity projections, one head, Dh = 2): softmax of x_i.x_j/sqrt(2)
+    weights over the rows of x; and 269-276's fully masked row, which is exactly the mean of V."""
+    x = np.array([1, 0, 0, 2], np.float32).reshape(1, 2, 2)
+    out, _ = oracle.attention_forward(x, x, x, 1)
+    s = np.float32(np.sqrt(2.0))
+    for i in range(2):
+        s0 = (x[0, i, 0] * x[0, 0, 0] + x[0, i, 1] * x[0, 0, 1]) / s
+        s1 = (x[0, i, 0] * x[0, 1, 0] + x[0, i, 1] * x[0, 1, 1]) / s
+        e0, e1 = np.exp(s0), np.exp(s1)
+        for c in range(2):
+            want = (e0 * x[0, 0, c] + e1 * x[0, 1, c]) / (e0 + e1)
+            assert abs(out[0, i, c] - want) <= 1e-5 * abs(want) + 1e-7
+    xs = synth.mt19937_uniform(3, 2 * 4 * 4).reshape(2, 4, 4)
+    none = np.array([[0, 0, 0, 0], [1, 1, 1, 1]], np.float32)
+    out, probs = oracle.attention_forward(xs, xs, xs, 2, none, False)
+    assert np.all(np.isfinite(out))
+    assert np.allclose(out[0], np.broadcast_to(xs[0].mean(axis=0), (4, 4)), rtol=1e-5, atol=1e-6)
+
+
+# ---------------------------------------------------------------- closed forms and identities
+
+@pytest.mark.parametrize("ta,tb,acc", [(0, 0, 0), (1, 0, 1), (0, 1, 0), (1, 1, 1)])
+def test_integer_products_are_exact(oracle, ta, tb, acc):
+    """Small integers keep every partial sum exact (|sum| < 2^24), so any correct order gives the exact
+    integer product: pins indexing, transposes, ld handling and the accumulate rule, depth cut included."""
+    rng = np.random.default_rng(ta * 4 + tb * 2 + acc)
+    for (m, n, k, pad) in ((7, 33, 17, 0), (64, 64, 1024, 3), (33, 5, 300, 1)):
+        A = rng.integers(-4, 5, (m, k)).astype(np.float32)
+        B = rng.integers(-4, 5, (k, n)).astype(np.float32)
+        C0 = rng.integers(-100, 100, (m, n)).astype(np.float32)
+        a = np.zeros(((k, m + pad) if ta else (m, k + pad)), np.float32)
+        b = np.zeros(((n, k + pad) if tb else (k, n + pad)), np.float32)
+        if ta:
+            a[:, :m] = A.T
+        else:
+            a[:, :k] = A
+        if tb:
+            b[:, :k] = B.T
+        else:
+            b[:, :n] = B
+        c = np.zeros((m, n + pad), np.float32)
+        c[:, :n] = C0
+        got = oracle.sgemm(ta, tb, m, n, k, a, a.shape[1], b, b.shape[1], c, n + pad, acc)
+        exact = A.astype(np.int64) @ B.astype(np.int64) + (C0.astype(np.int64) if acc else 0)
+        assert np.array_equal(got[:, :n].astype(np.int64), exact)
+        assert np.all(got[:, n:] == 0.0)
+
+
+def test_sgemm_within_north_star_bound_of_fp64(oracle):
+    """|oracle - exact| <= 4 K 2^-24 sum|a||b| for random inputs (tolerance of BASELINE.json north_star)."""
+    import golden_cases as gc
+    for spec in ((0, 0, 65, 47, 600, 0, 1, 5), (1, 1, 64, 64, 1024, 1, 0, 6), (0, 1, 200, 100, 300, 1, 2, 7)):
+        ta, tb, m, n, k, acc, pad, seed = spec
+        a, lda, b, ldb, c, ldc = gc.sgemm_inputs(*spec)
+        got = oracle.sgemm(ta, tb, m, n, k, a, lda, b, ldb, c, ldc, acc)
+        exact, mag = oracle.sgemm_f64(ta, tb, m, n, k, a, lda, b, ldb, c, ldc, acc)
+        assert np.all(np.abs(got[:, :n] - exact) <= 4 * k * 2.0 ** -24 * mag)
+
+
+def test_sgemm_at_matches_full_product(oracle):
+    import golden_cases as gc
+    for spec in ((0, 0, 70, 90, 700, 1, 0, 9), (1, 0, 64, 64, 1024, 0, 2, 10), (0, 1, 33, 40, 20, 1, 1, 11)):
+        ta, tb, m, n, k, acc, pad, seed = spec
+        a, lda, b, ldb, c, ldc = gc.sgemm_inputs(*spec)
+        full = oracle.sgemm(ta, tb, m, n, k, a, lda, b, ldb, c, ldc, acc)
+        rows = np.arange(m).repeat(n)
+        cols = np.tile(np.arange(n), m)
+        got = oracle.sgemm_at(ta, tb, m, n, k, a, lda, b, ldb, acc, rows, cols, c[rows, cols])
+        assert got.tobytes() == np.ascontiguousarray(full[:, :n]).reshape(-1).tobytes()
+
+
+def test_depth_cut_predicate(oracle):
+    """gemm.cpp:456-458 thresholds, at the cases of test_kernels.cpp:414."""
+    assert oracle.depth_cut(64, 64, 1024) and oracle.depth_cut(40, 48, 589) and oracle.depth_cut(7, 300, 768)
+    assert not oracle.depth_cut(64, 64, 511) and not oracle.depth_cut(300, 300, 512)
+    assert not oracle.depth_cut(4096, 4096, 4096) and not oracle.depth_cut(64, 4096, 4096)
+    assert not oracle.depth_cut(32, 9, 784)  # conv1 dW: m n k < 2^20
+
+
+def test_im2col_definition_and_col2im_adjoint(oracle):
+    """im2col equals the window definition; col2im is its adjoint: <im2col x, y> = <x, col2im y> (fp64)."""
+    rng = np.random.default_rng(3)
+    for (N, Cin, H, W, kk, s, p) in ((2, 3, 7, 6, 3, 2, 1), (1, 2, 5, 5, 4, 3, 3), (3, 1, 28, 28, 3, 1, 1)):
+        x = rng.uniform(-1, 1, (N, Cin, H, W)).astype(np.float32)
+        col = oracle.im2col(x, kk, kk, s, p)
+        ho, wo = oracle.conv_out(H, W, kk, kk, s, p)
+        xp = np.pad(x, ((0, 0), (0, 0), (p, p), (p, p)))
+        for c in range(Cin):
+            for i in range(kk):
+                for j in range(kk):
+                    win = xp[:, c, i:i + s * ho:s, j:j + s * wo:s][:, :ho, :wo].reshape(N, -1)
+                    assert np.array_equal(col[:, (c * kk + i) * kk + j], win)
+        y = rng.uniform(-1, 1, col.shape).astype(np.float32)
+        back = oracle.col2im_add(y, np.zeros_like(x), kk, kk, s, p)
+        lhs = float(np.sum(col.astype(np.float64) * y))
+        rhs = float(np.sum(x.astype(np.float64) * back))
+        assert abs(lhs - rhs) <= 1e-4 * (1 + abs(lhs))
+
+
+def test_conv_close_to_fp64_direct_convolution(oracle):
+    """test_autograd.cpp:420-448's direct-convolution reference, in fp64, with the north-star style bound."""
+    rng = np.random.default_rng(4)
+    for (N, Cin, H, W, Cout, kk, s, p) in ((7, 2, 9, 6, 3, 3, 2, 1), (3, 2, 33, 5, 2, 4, 3, 3), (2, 32, 14, 14, 8, 3, 1, 1)):
+        x = rng.uniform(-1, 1, (N, Cin, H, W)).astype(np.float32)
+        w = rng.uniform(-1, 1, (Cout, Cin, kk, kk)).astype(np.float32)
+        b = rng.uniform(-1, 1, Cout).astype(np.float32)
+        y, _ = oracle.conv2d_forward(x, w, b, s, p, 0)
+        exact, mag = oracle.conv2d_f64(x, w, b, s, p)
+        K = Cin * kk * kk
+        assert np.all(np.abs(y - exact) <= 4 * (K + 1) * 2.0 ** -24 * mag)
+
+
+def test_attention_close_to_fp64(oracle):
+    rng = np.random.default_rng(5)
+    for causal in (0, 1):
+        q, k, v = (rng.standard_normal((2, 16, 32)).astype(np.float32) for _ in range(3))
+        mask = np.ones((2, 16), np.float32)
+        mask[1, 11:] = 0
+        out, probs = oracle.attention_forward(q, k, v, 4, mask, causal)
+        eo, ep = oracle.attention_f64(q, k, v, 4, mask, causal)
+        assert np.allclose(probs, ep, rtol=1e-5, atol=1e-6)
+        assert np.allclose(out, eo, rtol=1e-4, atol=1e-5)
+        if causal:
+            tri = np.triu(np.ones((16, 16), bool), 1)
+            assert np.all(probs[:, :, tri] == 0.0)
+
+
+def test_lane_sum_and_sum_axis0(oracle):
+    """lane_sum's 8-lane order (ops.cpp:804-812) and Tensor::sum(0)'s row order differ from naive sums in
+    their bits but not in value; integers make them exact."""
+    p = np.arange(1, 100, dtype=np.float32)
+    assert oracle.lane_sum(p) == np.float32(4950)
+    x = np.arange(12, dtype=np.float32).reshape(4, 3)
+    assert oracle.sum_axis0(x).tolist() == [18.0, 22.0, 26.0]
+    v = synth.mt19937_uniform(1, 803)
+    a = np.zeros(8, np.float32)
+    for i in range(0, 800, 8):
+        a += v[i:i + 8]
+    t = ((a[0] + a[1]) + (a[2] + a[3])) + ((a[4] + a[5]) + (a[6] + a[7]))
+    for i in range(800, 803):
+        t = np.float32(t + v[i])
+    assert oracle.lane_sum(v) == t
