@@ -87,6 +87,183 @@ def cpu_baseline(a, b, m, n, k, budget_s=12.0, max_runs=30):
     }
 
 
+# ---------------------------------------------------------------------------------------------------------------
+# --report: every BASELINE.json config, absolute throughput and roofline fraction, nn-cpp's CPU path beside it
+
+def _gpu_time_ms(fn, warmup=3, reps=20):
+    """Average duration of fn() (one or more launches on torch's current stream) from HIP events."""
+    import torch
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        fn()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / reps
+
+
+def _cpu_time_ms(fn, budget_s=3.0, max_runs=15):
+    """nn-cpp's method (apps/bench/runner.cpp:80-96): a warm-up, then the median of timed runs (bounded)."""
+    fn()
+    times, t_start = [], time.perf_counter()
+    while len(times) < max_runs and (time.perf_counter() - t_start) < budget_s:
+        t0 = time.perf_counter()
+        fn()
+        times.append((time.perf_counter() - t0) * 1e3)
+    return statistics.median(times)
+
+
+def report():
+    import numpy as np
+    import torch
+
+    import nnh
+    from nnh import synth
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    from pyoracle import Reference, reference_available
+    ref = Reference() if reference_available() else None
+    threads = max(1, min(16, len(os.sched_getaffinity(0))))
+    if ref:
+        ref.set_threads(threads)
+    dev = torch.device("cuda:0")
+    d = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+    rows = []
+
+    def row(cfg, what, ms, flops=None, nbytes=None, bound="mfma", cpu_ms=None):
+        tflops = flops / (ms * 1e-3) / 1e12 if flops else None
+        gbps = nbytes / (ms * 1e-3) / 1e9 if nbytes else None
+        frac = (tflops / PEAK_FP32_MFMA_TFLOPS) if bound == "mfma" else (gbps / PEAK_HBM_GBPS)
+        rows.append({"config": cfg, "what": what, "ms": ms, "tflops": tflops, "gbps": gbps, "bound": bound,
+                     "roofline_frac": frac, "cpu_ms": cpu_ms, "speedup_vs_cpu": (cpu_ms / ms) if cpu_ms else None})
+        log(f"[{cfg}] {what}: {ms:.4f} ms" + (f", {tflops:.2f} TFLOP/s" if tflops else "") +
+            (f", {gbps:.1f} GB/s" if gbps else "") + f", {frac * 100:.1f}% of {bound} peak" +
+            (f"; nn-cpp CPU {cpu_ms:.3f} ms" if cpu_ms else ""))
+
+    # config 1: 512^3, NN / TN / NT, seed 0
+    n = 512
+    a, b = synth.uniform_operands(0, [(n, n), (n, n)])
+    da, db, dc = d(a), d(b), torch.empty((n, n), device=dev)
+    c = np.empty((n, n), np.float32)
+    for ta, tb, name in ((0, 0, "C=A B"), (1, 0, "C=A^T B"), (0, 1, "C=A B^T")):
+        ms = _gpu_time_ms(lambda: nnh.sgemm(ta, tb, n, n, n, da, n, db, n, dc, n))
+        cpu = _cpu_time_ms(lambda: ref.sgemm_inplace(ta, tb, n, n, n, a, n, b, n, c, n, 0)) if ref else None
+        row(1, f"sgemm 512^3 {name}", ms, flops=2.0 * n ** 3, cpu_ms=cpu)
+
+    # config 2: MLP 256 x 784 -> 512 -> 256 -> 10, forward (linear + ReLU) and backward (dX, dW, db)
+    dims = [784, 512, 256, 10]
+    x = synth.mt19937_uniform(1, 256 * 784, 0.0, 1.0).reshape(256, 784)
+    ws = [synth.mt19937_uniform(100 + i, dims[i + 1] * dims[i], -1 / np.sqrt(dims[i]), 1 / np.sqrt(dims[i]))
+          .reshape(dims[i + 1], dims[i]) for i in range(3)]
+    bs = [np.zeros(dims[i + 1], np.float32) for i in range(3)]
+    gys = [synth.normal(200 + i, (256, dims[i + 1])) for i in range(3)]
+    dws, dbs, dgs = [d(w) for w in ws], [d(bb) for bb in bs], [d(g) for g in gys]
+    acts = [d(x)]
+    for i in range(3):
+        acts.append(nnh.linear_forward(acts[-1], dws[i], dbs[i], relu=True))
+    grads = [(torch.empty((256, dims[i]), device=dev), torch.empty(ws[i].shape, device=dev),
+              torch.empty(dims[i + 1], device=dev)) for i in range(3)]
+
+    def mlp_fwd():
+        h = acts[0]
+        for i in range(3):
+            h = nnh.linear_forward(h, dws[i], dbs[i], relu=True)
+
+    def mlp_bwd():
+        for i in range(3):
+            nnh.linear_backward(dgs[i], acts[i], dws[i], *[v for pair in zip(grads[i], (True,) * 3) for v in pair])
+
+    fwd_flops = sum(2.0 * 256 * dims[i] * dims[i + 1] for i in range(3))
+    cpu = None
+    if ref:
+        hx = [x] + [None] * 3
+
+        def cpu_fwd():
+            h = x
+            for i in range(3):
+                h = np.maximum(ref.linear_forward(h, ws[i], bs[i]), np.float32(0))
+        cpu = _cpu_time_ms(cpu_fwd)
+    row(2, "MLP forward (3 x linear+ReLU)", _gpu_time_ms(mlp_fwd), flops=fwd_flops, cpu_ms=cpu)
+    cpu = None
+    if ref:
+        hacts = [x]
+        for i in range(3):
+            hacts.append(np.maximum(ref.linear_forward(hacts[-1], ws[i], bs[i]), np.float32(0)))
+        cpu = _cpu_time_ms(lambda: [ref.linear_backward(hacts[i], ws[i], bs[i], gys[i]) for i in range(3)])
+    row(2, "MLP backward (dX, dW, db per layer)", _gpu_time_ms(mlp_bwd), flops=2 * fwd_flops, cpu_ms=cpu)
+
+    # config 3: conv2d_relu, batch 128: conv1 1->32 on 28x28 (memory-bound), conv2 32->64 on 14x14
+    xc = synth.mt19937_uniform(2, 128 * 28 * 28, 0.0, 1.0).reshape(128, 1, 28, 28)
+    w1 = (synth.normal(21, (32, 1, 3, 3)) * np.float32(np.sqrt(2.0 / 9))).astype(np.float32)
+    w2 = (synth.normal(22, (64, 32, 3, 3)) * np.float32(np.sqrt(2.0 / 288))).astype(np.float32)
+    b1, b2 = np.zeros(32, np.float32), np.zeros(64, np.float32)
+    dxc, dw1, dw2, db1, db2 = d(xc), d(w1), d(w2), d(b1), d(b2)
+    y1, al1 = nnh.conv2d_forward(dxc, dw1, db1, 1, 1, True)
+    x2 = torch.nn.functional.max_pool2d(y1, 2).contiguous()
+    hx2 = x2.cpu().numpy()
+    conv1_bytes = 4 * (xc.size + w1.size + b1.size + 128 * 32 * 784)
+    cpu = _cpu_time_ms(lambda: ref.conv2d_forward(xc, w1, b1, 1, 1, 1)) if ref else None
+    row(3, "conv1 conv2d_relu fwd (1->32, 28x28, b128)", _gpu_time_ms(lambda: nnh.conv2d_forward(dxc, dw1, db1, 1, 1, True)),
+        flops=2.0 * 128 * 32 * 784 * 9, nbytes=conv1_bytes, bound="hbm", cpu_ms=cpu)
+    cpu = _cpu_time_ms(lambda: ref.conv2d_forward(hx2, w2, b2, 1, 1, 1)) if ref else None
+    row(3, "conv2 conv2d_relu fwd (32->64, 14x14, b128)", _gpu_time_ms(lambda: nnh.conv2d_forward(x2, dw2, db2, 1, 1, True)),
+        flops=2.0 * 128 * 64 * 196 * 288, nbytes=4 * (hx2.size + w2.size + 64 + 128 * 64 * 196), cpu_ms=cpu)
+    y2, al2 = nnh.conv2d_forward(x2, dw2, db2, 1, 1, True)
+    g2 = d(synth.normal(32, tuple(y2.shape)))
+    gx2, gw2, gb2 = torch.empty_like(x2), torch.empty_like(dw2), torch.empty_like(db2)
+    cpu = None
+    if ref:
+        hg2 = g2.cpu().numpy()
+        cpu = _cpu_time_ms(lambda: ref.conv2d_backward(hx2, w2, b2, 1, 1, 1, hg2))
+    row(3, "conv2 conv2d_relu bwd (dx, dW, db)",
+        _gpu_time_ms(lambda: nnh.conv2d_backward(g2, x2, dw2, al2, 1, 1, gx2, True, gw2, True, gb2, True)),
+        flops=2 * 2.0 * 128 * 64 * 196 * 288, cpu_ms=cpu)
+
+    # config 4: attention 32 x 8 heads x 256 x 64 (+ causal); probs stored, as the reference does
+    q, k, v = (synth.normal(3 + i, (32, 256, 512)) for i in range(3))
+    dq_, dk_, dv_ = d(q), d(k), d(v)
+    att_flops = 2 * 2.0 * 32 * 8 * 256 * 256 * 64
+    for causal in (False, True):
+        cpu = _cpu_time_ms(lambda: ref.attention_forward(q, k, v, 8, None, causal), budget_s=4.0, max_runs=5) if ref else None
+        row(4, "attention fwd" + (" causal" if causal else ""),
+            _gpu_time_ms(lambda: nnh.attention_forward(dq_, dk_, dv_, 8, None, causal)), flops=att_flops, cpu_ms=cpu)
+    out, probs = nnh.attention_forward(dq_, dk_, dv_, 8, None, False)
+    ga = d(synth.normal(7, (32, 256, 512)))
+    gq, gk, gv = torch.empty_like(dq_), torch.empty_like(dk_), torch.empty_like(dv_)
+    cpu = None
+    if ref:
+        hg = ga.cpu().numpy()
+        cpu = _cpu_time_ms(lambda: ref.attention_backward(q, k, v, 8, hg), budget_s=4.0, max_runs=3)
+    row(4, "attention bwd (dQ, dK, dV)",
+        _gpu_time_ms(lambda: nnh.attention_backward(ga, dq_, dk_, dv_, probs, 8, None, False, gq, True, gk, True, gv, True)),
+        flops=2 * att_flops, cpu_ms=cpu)
+
+    # config 5: roofline sweep, seed 4
+    for (m, n_, k_) in ((1024, 1024, 1024), (2048, 2048, 2048), (4096, 4096, 4096), (8192, 8192, 8192),
+                        (64, 4096, 4096), (4096, 4096, 64)):
+        a, b = synth.uniform_operands(4, [(m, k_), (k_, n_)])
+        da, db, dc = d(a), d(b), torch.empty((m, n_), device=dev)
+        c = np.empty((m, n_), np.float32)
+        reps = 5 if m * n_ * k_ >= 8192 ** 3 else 20
+        cpu = _cpu_time_ms(lambda: ref.sgemm_inplace(0, 0, m, n_, k_, a, k_, b, n_, c, n_, 0),
+                           budget_s=6.0, max_runs=5) if ref else None
+        row(5, f"sgemm {m}x{n_}x{k_}", _gpu_time_ms(lambda: nnh.sgemm(0, 0, m, n_, k_, da, k_, db, n_, dc, n_), reps=reps),
+            flops=2.0 * m * n_ * k_, cpu_ms=cpu)
+
+    lines = [f"GPU: {torch.cuda.get_device_name(0)}; nn-cpp CPU baseline: NN_NATIVE AVX2 build, {threads} threads on "
+             f"{cpu_model()}", "",
+             "| cfg | workload | GPU ms | TFLOP/s | GB/s | bound | % of roofline | nn-cpp CPU ms | GPU speedup |",
+             "|---|---|---|---|---|---|---|---|---|"]
+    for r in rows:
+        f = lambda v, fmt: (fmt % v) if v is not None else "-"
+        lines.append(f"| {r['config']} | {r['what']} | {r['ms']:.4f} | {f(r['tflops'], '%.2f')} | {f(r['gbps'], '%.0f')} | "
+                     f"{r['bound']} | {r['roofline_frac'] * 100:.1f}% | {f(r['cpu_ms'], '%.3f')} | "
+                     f"{f(r['speedup_vs_cpu'], '%.0fx')} |")
+    print("\n".join(lines), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -94,11 +271,16 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--size", type=int, default=4096)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--report", action="store_true", help="every BASELINE config as a markdown table (not the "
+                    "driver's JSON line)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (this build has no multi-GPU path); --gpus {args.gpus} is not "
               "supported", file=sys.stderr)
         sys.exit(2)
+    if args.report:
+        report()
+        return
 
     import numpy as np
     import torch

@@ -131,6 +131,66 @@ int nnh_relu_backward(const float* x, const float* g, float* dx, int first, size
  * from +0. combine 0: dst = s; 1: dst = s + 0.0f (a fresh gradient); 2: dst += s. */
 int nnh_tensor_sum0(const float* src, size_t rows, size_t inner, float* dst, int combine, void* stream);
 
+/*
+ * nn::attention forward (src/autograd/ops.cpp:1226-1261): q {N, Tq, D}, k and v {N, Tk, D}, `heads` heads of
+ * Dh = D / heads columns. probs {N, heads, Tq, Tk} receives the softmax probabilities (kept for the backward
+ * pass, as the reference does); out {N, Tq, D}. key_padding_mask {N, Tk} (0 marks a padded key) may be NULL.
+ * Shape rules as the reference: NNH_ERR_SHAPE unless heads divides D, Tq, Tk > 0 and (causal => Tq == Tk).
+ */
+int nnh_attention_forward(const float* q, const float* k, const float* v, size_t N, size_t Tq, size_t Tk, size_t D,
+                          size_t heads, const float* key_padding_mask, int causal, float* out, float* probs,
+                          void* stream);
+
+/*
+ * nn::attention backward (ops.cpp:1263-1295) for upstream gradient g {N, Tq, D} and the forward's probs. Each of
+ * dq, dk, dv may be NULL; *_first selects the fresh-gradient rule (overwrite instead of accumulate). When q, k and
+ * v are one tensor, pass one gradient buffer three times with dv_first as its freshness and dq_first = dk_first = 0.
+ */
+int nnh_attention_backward(const float* g, const float* q, const float* k, const float* v, const float* probs,
+                           size_t N, size_t Tq, size_t Tk, size_t D, size_t heads, const float* key_padding_mask,
+                           int causal, float* dq, int dq_first, float* dk, int dk_first, float* dv, int dv_first,
+                           void* stream);
+
+/* nn::scaled_masked_softmax forward (ops.cpp:1298-1322) over x {N, H, Tq, Tk}; x may equal y. */
+int nnh_scaled_masked_softmax_forward(const float* x, size_t N, size_t H, size_t Tq, size_t Tk, float scale,
+                                      const float* key_padding_mask, int causal, float* y, void* stream);
+
+/* Its backward (ops.cpp:1323-1342): first: dx = masked ? 0 : term + 0.0f; else dx += term where not masked. */
+int nnh_scaled_masked_softmax_backward(const float* y, const float* g, size_t N, size_t H, size_t Tq, size_t Tk,
+                                       float scale, const float* key_padding_mask, int causal, float* dx, int first,
+                                       void* stream);
+
+/*
+ * nn::conv2d / nn::conv2d_relu forward (src/autograd/ops.cpp:1345-1410, 1466-1472): x {N, Cin, H, W},
+ * w {Cout, Cin, kh, kw}, bias {Cout}, y {N, Cout, Ho, Wo} with Ho = (H + 2 padding - kh) / stride + 1.
+ * fuse_relu applies the folded ReLU: v = acc + b; alive = v > 0; y = alive ? v : 0, and alive (optional, one
+ * byte per output, laid out like y) receives the flags the backward pass masks with.
+ * Shape rules as the reference: NNH_ERR_SHAPE for stride <= 0, padding < 0 or a kernel wider than the padded
+ * input.
+ */
+int nnh_conv2d_forward(const float* x, size_t N, size_t Cin, size_t H, size_t W, const float* w, size_t Cout,
+                       size_t kh, size_t kw, const float* bias, int stride, int padding, int fuse_relu, float* y,
+                       unsigned char* alive, void* stream);
+
+/*
+ * Its backward (ops.cpp:1418-1463) for upstream gradient g {N, Cout, Ho, Wo}: g is masked by alive when given
+ * (the fused ReLU), db = per-sample lane sums summed over samples in order, dw = per-sample g col^T summed
+ * over samples in order, dx = col2im(W^T g). *_first: the gradient is fresh (dx zero-filled first, dw and db
+ * stored rather than added). Any of dx, dw, db may be NULL.
+ */
+int nnh_conv2d_backward(const float* g, const float* x, const float* w, const unsigned char* alive, size_t N,
+                        size_t Cin, size_t H, size_t W, size_t Cout, size_t kh, size_t kw, int stride, int padding,
+                        float* dx, int dx_first, float* dw, int dw_first, float* db, int db_first, void* stream);
+
+/* im2col_sample over a batch (ops.cpp:188-212): col {N, Cin*kh*kw, Ho*Wo}, zeros where a tap is padding. */
+int nnh_im2col(const float* x, size_t N, size_t Cin, size_t H, size_t W, size_t kh, size_t kw, int stride, int padding,
+               float* col, void* stream);
+
+/* col2im_sample_add over a batch (ops.cpp:224-243): dx {N, Cin, H, W} += the column entries of each element's taps,
+ * in the reference's order; first zero-fills dx first. */
+int nnh_col2im_add(const float* col, size_t N, size_t Cin, size_t H, size_t W, size_t kh, size_t kw, int stride,
+                   int padding, float* dx, int first, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -10,6 +10,7 @@ import os
 
 PKG_ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 LIB_PATH = os.path.join(PKG_ROOT, "lib", "libnnh.so")
+HOST_LIB_PATH = os.path.join(PKG_ROOT, "lib", "libnn_gemm_hip.so")
 REPO_ROOT = os.path.dirname(PKG_ROOT)
 HEADER_PATH = os.path.join(REPO_ROOT, "include", "nnh.h")
 
@@ -65,6 +66,16 @@ _EXTRA_DECLS = {
     "nnh_relu_forward": [_vp, _vp, _sz, _vp],
     "nnh_relu_backward": [_vp, _vp, _vp, C.c_int, _sz, _vp],
     "nnh_tensor_sum0": [_vp, _sz, _sz, _vp, C.c_int, _vp],
+    "nnh_attention_forward": [_vp, _vp, _vp, _sz, _sz, _sz, _sz, _sz, _vp, C.c_int, _vp, _vp, _vp],
+    "nnh_attention_backward": [_vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, _sz, _sz, _vp, C.c_int, _vp, C.c_int, _vp,
+                               C.c_int, _vp, C.c_int, _vp],
+    "nnh_scaled_masked_softmax_forward": [_vp, _sz, _sz, _sz, _sz, C.c_float, _vp, C.c_int, _vp, _vp],
+    "nnh_scaled_masked_softmax_backward": [_vp, _vp, _sz, _sz, _sz, _sz, C.c_float, _vp, C.c_int, _vp, C.c_int, _vp],
+    "nnh_conv2d_forward": [_vp, _sz, _sz, _sz, _sz, _vp, _sz, _sz, _sz, _vp, C.c_int, C.c_int, C.c_int, _vp, _vp, _vp],
+    "nnh_conv2d_backward": [_vp, _vp, _vp, _vp, _sz, _sz, _sz, _sz, _sz, _sz, _sz, C.c_int, C.c_int, _vp, C.c_int,
+                            _vp, C.c_int, _vp, C.c_int, _vp],
+    "nnh_im2col": [_vp, _sz, _sz, _sz, _sz, _sz, _sz, C.c_int, C.c_int, _vp, _vp],
+    "nnh_col2im_add": [_vp, _sz, _sz, _sz, _sz, _sz, _sz, C.c_int, C.c_int, _vp, C.c_int, _vp],
 }
 
 
@@ -204,3 +215,109 @@ def tensor_sum0(src, dst, combine=0, stream=None):
     rows = src.shape[0]
     inner = src.numel() // rows if rows else dst.numel()
     check(lib().nnh_tensor_sum0(_ptr(src), rows, inner, _ptr(dst), int(combine), _stream(stream)))
+
+
+def attention_forward(q, k, v, heads, mask=None, causal=False, stream=None):
+    """nn::attention forward on device tensors; returns (out, probs)."""
+    import torch
+    N, Tq, D = q.shape
+    Tk = k.shape[1]
+    out = torch.empty((N, Tq, D), dtype=torch.float32, device=q.device)
+    probs = torch.empty((N, heads, Tq, Tk), dtype=torch.float32, device=q.device)
+    check(lib().nnh_attention_forward(_ptr(q), _ptr(k), _ptr(v), N, Tq, Tk, D, heads, _ptr(mask), int(causal),
+                                      _ptr(out), _ptr(probs), _stream(stream)))
+    return out, probs
+
+
+def attention_backward(g, q, k, v, probs, heads, mask=None, causal=False, dq=None, dq_first=True, dk=None,
+                       dk_first=True, dv=None, dv_first=True, stream=None):
+    N, Tq, D = q.shape
+    Tk = k.shape[1]
+    check(lib().nnh_attention_backward(_ptr(g), _ptr(q), _ptr(k), _ptr(v), _ptr(probs), N, Tq, Tk, D, heads,
+                                       _ptr(mask), int(causal), _ptr(dq), int(dq_first), _ptr(dk), int(dk_first),
+                                       _ptr(dv), int(dv_first), _stream(stream)))
+
+
+def scaled_masked_softmax_forward(x, scale, mask=None, causal=False, stream=None):
+    import torch
+    N, H, Tq, Tk = x.shape
+    y = torch.empty_like(x)
+    check(lib().nnh_scaled_masked_softmax_forward(_ptr(x), N, H, Tq, Tk, float(scale), _ptr(mask), int(causal),
+                                                  _ptr(y), _stream(stream)))
+    return y
+
+
+def scaled_masked_softmax_backward(y, g, dx, scale, mask=None, causal=False, first=True, stream=None):
+    N, H, Tq, Tk = y.shape
+    check(lib().nnh_scaled_masked_softmax_backward(_ptr(y), _ptr(g), N, H, Tq, Tk, float(scale), _ptr(mask),
+                                                   int(causal), _ptr(dx), int(first), _stream(stream)))
+
+
+def conv_out(H, W, kh, kw, stride, pad):
+    """conv2d_output_size (ops.cpp:135-139); (0, 0) for geometry the library rejects."""
+    if stride <= 0 or pad < 0 or kh > H + 2 * pad or kw > W + 2 * pad:
+        return 0, 0
+    return (H + 2 * pad - kh) // stride + 1, (W + 2 * pad - kw) // stride + 1
+
+
+def conv2d_forward(x, w, bias, stride, pad, fuse_relu, want_alive=True, stream=None):
+    """nn::conv2d (fuse_relu=False) or nn::conv2d_relu; returns (y, alive or None)."""
+    import torch
+    N, Cin, H, W = x.shape
+    Cout, _, kh, kw = w.shape
+    ho, wo = conv_out(H, W, kh, kw, stride, pad)
+    y = torch.empty((N, Cout, max(ho, 0), max(wo, 0)), dtype=torch.float32, device=x.device)
+    alive = torch.empty(y.shape, dtype=torch.uint8, device=x.device) if (fuse_relu and want_alive) else None
+    check(lib().nnh_conv2d_forward(_ptr(x), N, Cin, H, W, _ptr(w), Cout, kh, kw, _ptr(bias), int(stride), int(pad),
+                                   int(fuse_relu), _ptr(y), _ptr(alive), _stream(stream)))
+    return y, alive
+
+
+def conv2d_backward(g, x, w, alive, stride, pad, dx=None, dx_first=True, dw=None, dw_first=True, db=None,
+                    db_first=True, stream=None):
+    N, Cin, H, W = x.shape
+    Cout, _, kh, kw = w.shape
+    check(lib().nnh_conv2d_backward(_ptr(g), _ptr(x), _ptr(w), _ptr(alive), N, Cin, H, W, Cout, kh, kw, int(stride),
+                                    int(pad), _ptr(dx), int(dx_first), _ptr(dw), int(dw_first), _ptr(db),
+                                    int(db_first), _stream(stream)))
+
+
+def im2col(x, kh, kw, stride, pad, stream=None):
+    import torch
+    N, Cin, H, W = x.shape
+    ho, wo = conv_out(H, W, kh, kw, stride, pad)
+    col = torch.empty((N, Cin * kh * kw, ho * wo), dtype=torch.float32, device=x.device)
+    check(lib().nnh_im2col(_ptr(x), N, Cin, H, W, kh, kw, int(stride), int(pad), _ptr(col), _stream(stream)))
+    return col
+
+
+def col2im_add(col, dx, kh, kw, stride, pad, first=False, stream=None):
+    N, Cin, H, W = dx.shape
+    check(lib().nnh_col2im_add(_ptr(col), N, Cin, H, W, kh, kw, int(stride), int(pad), _ptr(dx), int(first),
+                               _stream(stream)))
+
+
+_host_lib = None
+
+
+def host_lib():
+    """libnn_gemm_hip.so: the drop-in nn::kernels::sgemm (host pointers) built on libnnh."""
+    global _host_lib
+    if _host_lib is None:
+        if not os.path.exists(HOST_LIB_PATH):
+            raise RuntimeError(f"{HOST_LIB_PATH} is missing: build it with `make -C nn-cpp_amd`")
+        L = C.CDLL(HOST_LIB_PATH)
+        L.nnh_sgemm_host.argtypes = [C.c_int, C.c_int, _sz, _sz, _sz, _vp, _sz, _vp, _sz, _vp, _sz, C.c_int]
+        _host_lib = L
+    return _host_lib
+
+
+def sgemm_host(ta, tb, m, n, k, a, lda, b, ldb, c, ldc, accumulate=False):
+    """nn::kernels::sgemm's exact signature on host numpy arrays (C updated in place)."""
+    import numpy as np
+    for arr in (a, b, c):
+        assert arr.dtype == np.float32 and arr.flags["C_CONTIGUOUS"]
+    rc = host_lib().nnh_sgemm_host(int(ta), int(tb), m, n, k, a.ctypes.data, lda, b.ctypes.data, ldb, c.ctypes.data,
+                                   ldc, int(accumulate))
+    if rc != OK:
+        raise NnhError(rc, "nn::kernels::sgemm (HIP) failed")

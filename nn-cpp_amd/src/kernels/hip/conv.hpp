@@ -1,0 +1,22 @@
+// conv.hpp - launchers of the convolution kernels (internal to libnnh).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace nnh {
+
+// One convolution's geometry (ConvGeometry, src/autograd/ops.cpp:164-176): input cin x h x w, kernel kh x kw,
+// stride, zero padding, output ho x wo.
+struct ConvGeom {
+	int cin, h, w, kh, kw, stride, pad, ho, wo;
+};
+
+hipError_t im2col(const float* x, float* col, const ConvGeom& g, int64_t samples, hipStream_t s);
+hipError_t col2im(const float* col, float* dx, const ConvGeom& g, int64_t samples, int first, hipStream_t s);
+hipError_t conv_direct(const float* x, const float* w, const float* bias, float* y, unsigned char* alive,
+                       const ConvGeom& g, int64_t samples, int cout, int relu, hipStream_t s);
+hipError_t mask_grad(const float* g, const unsigned char* alive, float* out, int64_t total, hipStream_t s);
+hipError_t lane_sums(const float* src, int64_t rows, int64_t n, float* dst, hipStream_t s);
+
+}  // namespace nnh

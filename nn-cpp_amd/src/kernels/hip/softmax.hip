@@ -13,8 +13,22 @@
 
 namespace nnh {
 
-// exp as std::exp(float) gives it on the reference host (glibc expf): computed in double and rounded once.
-__device__ __forceinline__ float exp_ref(float x) { return (float)exp((double)x); }
+// The correctly rounded e^x for the softmax's arguments (x <= 0 or NaN): exp in double, rounded once to float.
+// An exhaustive scan of every float in [-104.5, 0] (tests/golden/exp_scan.c, quad precision) finds exactly
+// four inputs whose e^x lies within 8 double ulps of a float rounding midpoint, where the last bits of a
+// double exp could decide the rounding; their correctly rounded results are given directly. Every other
+// input lies farther than 8 ulps from a midpoint, so any double exp accurate to a few ulps rounds right.
+// (nn-cpp's std::exp is glibc's expf, which is within 0.502 ulp and differs from this on 97052 of those
+// 1.12e9 inputs, always by one ulp; that is the only arithmetic difference of the attention path.)
+__device__ __forceinline__ float exp_ref(float x) {
+	switch (__float_as_uint(x)) {
+		case 0xb3000000u: return __uint_as_float(0x3f800000u);  // -0x1p-25       -> 1
+		case 0xbae0e25cu: return __uint_as_float(0x3f7f8fa7u);  // -0x1.c1c4b8p-10 -> 0x1.ff1f4ep-1
+		case 0xbbf0edf1u: return __uint_as_float(0x3f7e1fe9u);  // -0x1.e1dbe2p-8  -> 0x1.fc3fd2p-1
+		case 0xc16912cdu: return __uint_as_float(0x34fd331bu);  // -0x1.d2259ap+3  -> 0x1.fa6636p-22
+		default: return (float)exp((double)x);
+	}
+}
 
 namespace {
 

@@ -1,0 +1,201 @@
+// ops_conv.hip - extern "C" entry points of nn::conv2d / nn::conv2d_relu, im2col and col2im (include/nnh.h).
+//
+// Forward (src/autograd/ops.cpp:1345-1410): a short depth (K = Cin*kh*kw <= kDirectMaxK, a network's first
+// layer) runs as a direct convolution fused with bias/ReLU, memory-bound; a longer depth is im2col into a
+// workspace and one batched MFMA GEMM W[Cout x K] col_n[K x hw] over all samples with the bias/ReLU/alive
+// epilogue. Both give each output the reference's fma chain over k = (c, ph, pw) in order.
+// Backward (ops.cpp:1418-1463): g masked by alive; db = per-sample lane_sum, then summed in sample order;
+// dW_n = g_n col_n^T (batched sgemm F,T), summed in sample order; dcol_n = W^T g_n (batched sgemm T,F), then
+// col2im in gather form into a zero-filled (fresh) or existing dx.
+#include <hip/hip_runtime.h>
+
+#include <vector>
+
+#include "abi_common.hpp"
+#include "kernels/hip/conv.hpp"
+#include "kernels/hip/reduce.hpp"
+#include "nnh.h"
+
+using namespace nnh;
+
+namespace {
+
+constexpr size_t kDirectMaxK = 32;
+
+int conv_geometry(size_t N, size_t Cin, size_t H, size_t W, size_t Cout, size_t kh, size_t kw, int stride,
+                  int padding, ConvGeom& g) {
+	(void)N;
+	(void)Cout;
+	// ops.cpp:1350-1365
+	if (stride <= 0 || padding < 0) return fail(NNH_ERR_SHAPE, "conv2d: stride must be positive, padding >= 0");
+	if (kh > H + 2 * (size_t)padding || kw > W + 2 * (size_t)padding)
+		return fail(NNH_ERR_SHAPE, "conv2d: kernel larger than the padded input");
+	const size_t lim = 1u << 30;
+	if (Cin > lim || H > lim || W > lim || kh > lim || kw > lim) return fail(NNH_ERR_INVALID, "conv2d: size too large");
+	g.cin = (int)Cin;
+	g.h = (int)H;
+	g.w = (int)W;
+	g.kh = (int)kh;
+	g.kw = (int)kw;
+	g.stride = stride;
+	g.pad = padding;
+	g.ho = (int)((H + 2 * (size_t)padding - kh) / (size_t)stride + 1);  // ops.cpp:135-139
+	g.wo = (int)((W + 2 * (size_t)padding - kw) / (size_t)stride + 1);
+	return NNH_OK;
+}
+
+struct Workspace {
+	hipStream_t s;
+	std::vector<void*> bufs;
+	hipError_t err = hipSuccess;
+	explicit Workspace(hipStream_t st) : s(st) {}
+	template <typename T>
+	T* get(size_t count) {
+		void* p = nullptr;
+		if (err != hipSuccess) return nullptr;
+		err = hipMallocAsync(&p, (count ? count : 1) * sizeof(T), s);
+		if (err != hipSuccess) return nullptr;
+		bufs.push_back(p);
+		return static_cast<T*>(p);
+	}
+	hipError_t release() {
+		hipError_t e = err;
+		for (void* p : bufs) {
+			hipError_t e2 = hipFreeAsync(p, s);
+			if (e == hipSuccess) e = e2;
+		}
+		bufs.clear();
+		return e;
+	}
+};
+
+}  // namespace
+
+extern "C" {
+
+int nnh_conv2d_forward(const float* x, size_t N, size_t Cin, size_t H, size_t W, const float* w, size_t Cout,
+                       size_t kh, size_t kw, const float* bias, int stride, int padding, int fuse_relu, float* y,
+                       unsigned char* alive, void* stream) {
+	ConvGeom g;
+	int rc = conv_geometry(N, Cin, H, W, Cout, kh, kw, stride, padding, g);
+	if (rc != NNH_OK) return rc;
+	const size_t hw = (size_t)g.ho * g.wo, K = Cin * kh * kw;
+	if (N == 0 || Cout == 0 || hw == 0) return NNH_OK;
+	if (!x || !w || !bias || !y) return fail(NNH_ERR_INVALID, "conv2d: null pointer");
+	if (ranges_overlap(y, N * Cout * hw * 4, x, N * Cin * H * W * 4)) return fail(NNH_ERR_ALIAS, "conv2d: y overlaps x");
+	hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+	unsigned char* al = fuse_relu ? alive : nullptr;
+	if (K <= kDirectMaxK)
+		return hip_status(conv_direct(x, w, bias, y, al, g, (int64_t)N, (int)Cout, fuse_relu ? 1 : 0, s), "conv2d direct");
+	Workspace ws(s);
+	float* col = ws.get<float>(N * K * hw);
+	if (!col) return hip_status(ws.release(), "conv2d workspace");
+	rc = hip_status(im2col(x, col, g, (int64_t)N, s), "im2col");
+	if (rc == NNH_OK) {
+		// Y_n = W col_n (ops.cpp:1395), W shared by every sample
+		nnh_batch b{};
+		b.ndim = 1;
+		b.shape[0] = N;
+		b.stride_a[0] = 0;
+		b.stride_b[0] = (ptrdiff_t)(K * hw);
+		b.stride_c[0] = (ptrdiff_t)(Cout * hw);
+		nnh_epilogue ep{NNH_BIAS_ROW, fuse_relu ? 1 : 0, bias, al};
+		GemmCall call;
+		rc = build_gemm(0, 0, Cout, hw, K, w, K, col, hw, y, hw, 0, &b, &ep, call);
+		if (rc == NNH_OK) rc = run_gemm(call, stream, -1);
+	}
+	const int rc2 = hip_status(ws.release(), "conv2d workspace");
+	return rc != NNH_OK ? rc : rc2;
+}
+
+int nnh_conv2d_backward(const float* g, const float* x, const float* w, const unsigned char* alive, size_t N,
+                        size_t Cin, size_t H, size_t W, size_t Cout, size_t kh, size_t kw, int stride, int padding,
+                        float* dx, int dx_first, float* dw, int dw_first, float* db, int db_first, void* stream) {
+	ConvGeom geo;
+	int rc = conv_geometry(N, Cin, H, W, Cout, kh, kw, stride, padding, geo);
+	if (rc != NNH_OK) return rc;
+	const size_t hw = (size_t)geo.ho * geo.wo, K = Cin * kh * kw;
+	hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+	if (!dx && !dw && !db) return NNH_OK;
+	if (N == 0) {
+		// no samples: dx is empty, and dW, db receive a sum over zero samples (zeros), stored or added
+		if (dw) rc = hip_status(sum_rows(nullptr, 0, (int64_t)(Cout * K), dw, dw_first ? 0 : 2, s), "conv2d dw");
+		if (rc == NNH_OK && db) rc = hip_status(sum_rows(nullptr, 0, (int64_t)Cout, db, db_first ? 0 : 2, s), "conv2d db");
+		return rc;
+	}
+	if (!g || !x || !w) return fail(NNH_ERR_INVALID, "conv2d backward: null pointer");
+	Workspace ws(s);
+	const float* gm = g;
+	if (alive) {  // ops.cpp:1439-1443
+		float* m = ws.get<float>(N * Cout * hw);
+		if (!m) return hip_status(ws.release(), "conv2d workspace");
+		rc = hip_status(mask_grad(g, alive, m, (int64_t)(N * Cout * hw), s), "conv2d mask");
+		gm = m;
+	}
+	if (rc == NNH_OK && db) {  // ops.cpp:1445, 1461
+		float* gb = ws.get<float>(N * Cout);
+		rc = gb ? hip_status(lane_sums(gm, (int64_t)(N * Cout), (int64_t)hw, gb, s), "conv2d db")
+		        : hip_status(ws.err, "conv2d workspace");
+		if (rc == NNH_OK) rc = hip_status(sum_rows(gb, (int64_t)N, (int64_t)Cout, db, db_first ? 0 : 2, s), "conv2d db");
+	}
+	float* col = nullptr;
+	if (rc == NNH_OK && (dw || dx)) {
+		col = ws.get<float>(N * K * hw);
+		if (!col) rc = hip_status(ws.err, "conv2d workspace");
+	}
+	if (rc == NNH_OK && dw) {  // ops.cpp:1448-1449, 1462
+		float* gw = ws.get<float>(N * Cout * K);
+		if (!gw) rc = hip_status(ws.err, "conv2d workspace");
+		if (rc == NNH_OK) rc = hip_status(im2col(x, col, geo, (int64_t)N, s), "im2col");
+		if (rc == NNH_OK) {
+			nnh_batch b{};
+			b.ndim = 1;
+			b.shape[0] = N;
+			b.stride_a[0] = (ptrdiff_t)(Cout * hw);
+			b.stride_b[0] = (ptrdiff_t)(K * hw);
+			b.stride_c[0] = (ptrdiff_t)(Cout * K);
+			GemmCall call;
+			rc = build_gemm(0, 1, Cout, K, hw, gm, hw, col, hw, gw, K, 0, &b, nullptr, call);
+			if (rc == NNH_OK) rc = run_gemm(call, stream, -1);
+		}
+		if (rc == NNH_OK)
+			rc = hip_status(sum_rows(gw, (int64_t)N, (int64_t)(Cout * K), dw, dw_first ? 0 : 2, s), "conv2d dw");
+	}
+	if (rc == NNH_OK && dx) {  // ops.cpp:1452-1455
+		nnh_batch b{};
+		b.ndim = 1;
+		b.shape[0] = N;
+		b.stride_a[0] = 0;
+		b.stride_b[0] = (ptrdiff_t)(Cout * hw);
+		b.stride_c[0] = (ptrdiff_t)(K * hw);
+		GemmCall call;
+		rc = build_gemm(1, 0, K, hw, Cout, w, K, gm, hw, col, hw, 0, &b, nullptr, call);
+		if (rc == NNH_OK) rc = run_gemm(call, stream, -1);
+		if (rc == NNH_OK) rc = hip_status(col2im(col, dx, geo, (int64_t)N, dx_first ? 1 : 0, s), "col2im");
+	}
+	const int rc2 = hip_status(ws.release(), "conv2d workspace");
+	return rc != NNH_OK ? rc : rc2;
+}
+
+int nnh_im2col(const float* x, size_t N, size_t Cin, size_t H, size_t W, size_t kh, size_t kw, int stride, int padding,
+               float* col, void* stream) {
+	ConvGeom g;
+	int rc = conv_geometry(N, Cin, H, W, 1, kh, kw, stride, padding, g);
+	if (rc != NNH_OK) return rc;
+	const size_t total = N * Cin * kh * kw * (size_t)g.ho * g.wo;
+	if (total == 0) return NNH_OK;
+	if (!x || !col) return fail(NNH_ERR_INVALID, "im2col: null pointer");
+	return hip_status(im2col(x, col, g, (int64_t)N, reinterpret_cast<hipStream_t>(stream)), "im2col");
+}
+
+int nnh_col2im_add(const float* col, size_t N, size_t Cin, size_t H, size_t W, size_t kh, size_t kw, int stride,
+                   int padding, float* dx, int first, void* stream) {
+	ConvGeom g;
+	int rc = conv_geometry(N, Cin, H, W, 1, kh, kw, stride, padding, g);
+	if (rc != NNH_OK) return rc;
+	if (N * Cin * H * W == 0) return NNH_OK;
+	if (!col || !dx) return fail(NNH_ERR_INVALID, "col2im: null pointer");
+	return hip_status(col2im(col, dx, g, (int64_t)N, first, reinterpret_cast<hipStream_t>(stream)), "col2im");
+}
+
+}  // extern "C"

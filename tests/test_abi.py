@@ -15,6 +15,14 @@ def test_library_exports_every_declared_function():
     assert not missing, missing
 
 
+def test_host_library_exports_its_header():
+    import re
+    text = open(nnh.HEADER_PATH.replace("nnh.h", "nnh_host.h")).read()
+    names = sorted(set(re.findall(r"\b(nnh_[a-z0-9_]+)\s*\(", text)))
+    L = nnh.host_lib()
+    assert names and not [n for n in names if not hasattr(L, n)]
+
+
 def test_version_and_configs():
     assert b"gfx950" in nnh.lib().nnh_version()
     assert len(nnh.gemm_configs()) >= 1

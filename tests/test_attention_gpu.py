@@ -1,0 +1,253 @@
+"""Parity of nn::attention (forward and backward) and nn::scaled_masked_softmax on the GPU.
+
+Every step except one is bit-identical to nn-cpp: the GEMMs (QK^T, PV and the four backward products), the
+scale, the masks, the max scan, the in-order row sum, the division and the softmax backward. The exception is
+exp: nn-cpp's std::exp(float) is glibc's expf, which is not correctly rounded (maximum error about 0.502 ulp),
+while the GPU computes exp in double and rounds once (the correctly rounded value). So:
+  * against the oracle with the correctly rounded exp (oracle exp mode 1): bitwise, at every shape;
+  * against nn-cpp itself (golden vectors, oracle exp mode 0): within the stated tolerance (probabilities
+    within 4 ulp, outputs and gradients within 4 K 2^-24 of their magnitude sums).
+Shapes: the reference's test cases and BASELINE config 4 (32 x 8 heads x 256 x 64, and its causal variant).
+"""
+import contextlib
+import numpy as np
+import pytest
+
+from helpers import first_diff
+from nnh import synth
+
+pytestmark = pytest.mark.gpu
+
+
+def dev(a):
+    import torch
+    return None if a is None else torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def host(t):
+    import torch
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def same(got, want, what):
+    assert got.shape == want.shape, (what, got.shape, want.shape)
+    assert got.tobytes() == want.tobytes(), f"{what}: {first_diff(got, want)}"
+
+
+@contextlib.contextmanager
+def correctly_rounded_exp(oracle):
+    oracle.set_exp_mode(1)
+    try:
+        yield oracle
+    finally:
+        oracle.set_exp_mode(0)
+
+
+def ulps(a, b):
+    """Distance in float32 units in the last place (finite, same-sign values)."""
+    ai = a.astype(np.float32).view(np.int32).astype(np.int64)
+    bi = b.astype(np.float32).view(np.int32).astype(np.int64)
+    return np.abs(ai - bi)
+
+
+def close_to_nncpp(got, want, depth, what):
+    """|got - want| <= 4 depth 2^-24 max|want| (+ 1e-30): the north-star bound with sum |p||v| <= max |v|."""
+    bound = 4.0 * depth * 2.0 ** -24 * float(np.max(np.abs(want))) + 1e-30
+    err = float(np.max(np.abs(got.astype(np.float64) - want.astype(np.float64))))
+    assert err <= bound, f"{what}: max error {err} > {bound}"
+
+
+def golden():
+    import golden_cases as gc
+    return gc, np.load(gc.__file__.replace("golden_cases.py", "reference_vectors.npz"))
+
+
+def test_attention_golden_forward_backward(gpu, oracle):
+    import torch
+
+    import nnh
+    gc, g = golden()
+    for name, spec in gc.ATTENTION_CASES:
+        q, k, v, heads, mask, causal, gr = gc.attention_inputs(spec)
+        out, probs = nnh.attention_forward(dev(q), dev(k), dev(v), heads, dev(mask), causal)
+        # nn-cpp's leaves accumulate into zero-filled gradients (first == false)
+        dq, dk, dv = (torch.zeros(t.shape, device="cuda") for t in (q, k, v))
+        nnh.attention_backward(dev(gr), dev(q), dev(k), dev(v), probs, heads, dev(mask), causal, dq, False, dk, False,
+                               dv, False)
+        with correctly_rounded_exp(oracle):
+            wo, wp = oracle.attention_forward(q, k, v, heads, mask, causal)
+            wq, wk, wv = oracle.attention_backward(gr, q, k, v, wp, heads, mask, causal)
+        same(host(out), wo, (name, "out"))
+        same(host(probs), wp, (name, "probs"))
+        for key, t, w in (("dq", dq, wq), ("dk", dk, wk), ("dv", dv, wv)):
+            same(host(t), w, (name, key))
+            close_to_nncpp(host(t), g[f"attention/{name}/{key}"], spec[2] * 4, (name, key, "vs nn-cpp"))
+        close_to_nncpp(host(out), g[f"attention/{name}/out"], spec[2], (name, "out vs nn-cpp"))
+
+
+def composed(q, k, v, heads, mask, causal):
+    """test_autograd.cpp:1533-1540: split heads, matmul_bt, scaled_masked_softmax, matmul, merge heads,
+    every step through this library."""
+    import nnh
+    N, Tq, D = q.shape
+    Tk = k.shape[1]
+    Dh = D // heads
+
+    def split(x, T):
+        return x.reshape(N, T, heads, Dh).transpose(1, 2).contiguous()
+
+    s = nnh.matmul(split(q, Tq), split(k, Tk), False, True)
+    w = nnh.scaled_masked_softmax_forward(s, np.float32(1.0) / np.sqrt(np.float32(Dh)), mask, causal)
+    o = nnh.matmul(w, split(v, Tk))
+    return o.transpose(1, 2).contiguous().reshape(N, Tq, D), w
+
+
+def test_attention_gives_the_bits_of_the_composed_ops(gpu):
+    """test_autograd.cpp:1597-1620 on this backend: the fused op equals the composition of matmul_bt,
+    scaled_masked_softmax and matmul, bit for bit (the per-element depth order never depends on the caller)."""
+    import nnh
+    mask = np.array([[1, 1, 1, 1, 0], [1, 1, 1, 1, 1], [1, 1, 0, 0, 0]], np.float32)
+    for tq, tk, causal, padded in ((5, 5, True, False), (5, 5, True, True), (4, 5, False, True), (5, 5, False, False)):
+        q = dev(synth.mt19937_uniform(1, 3 * tq * 8).reshape(3, tq, 8))
+        k = dev(synth.mt19937_uniform(2, 3 * tk * 8).reshape(3, tk, 8))
+        v = dev(synth.mt19937_uniform(3, 3 * tk * 8).reshape(3, tk, 8))
+        m = dev(mask) if padded else None
+        out, probs = nnh.attention_forward(q, k, v, 4, m, causal)
+        co, cw = composed(q, k, v, 4, m, causal)
+        same(host(out), host(co), (tq, tk, causal, padded))
+        same(host(probs), host(cw), ("probs", tq, tk, causal, padded))
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_baseline_config4(gpu, oracle, causal):
+    """batch 32, 8 heads, seq 256, head_dim 64, Q, K, V ~ N(0, 1) (seed 3); scale 1/8.
+    Bitwise with the correctly rounded exp; against nn-cpp's glibc expf: probabilities within 4 ulp, output
+    within the north-star bound; causal rows hold exact zeros past the diagonal."""
+    import nnh
+    N, T, D, H = 32, 256, 512, 8
+    q, k, v = (synth.normal(3 + i, (N, T, D)) for i in range(3))
+    out, probs = nnh.attention_forward(dev(q), dev(k), dev(v), H, None, causal)
+    out, probs = host(out), host(probs)
+    with correctly_rounded_exp(oracle):
+        cr_out, cr_probs = oracle.attention_forward(q, k, v, H, None, causal)
+    same(probs, cr_probs, "probs")
+    same(out, cr_out, "out")
+    ref_out, ref_probs = oracle.attention_forward(q, k, v, H, None, causal)
+    d = ulps(probs, ref_probs)
+    assert int(d.max()) <= 4, f"probabilities differ from nn-cpp's by up to {int(d.max())} ulp"
+    close_to_nncpp(out, ref_out, T, "out vs nn-cpp")
+    if causal:
+        tri = np.triu(np.ones((T, T), bool), 1)
+        assert np.all(probs[:, :, tri] == 0.0)
+
+
+def test_attention_backward_matches_oracle(gpu, oracle):
+    import torch
+
+    import nnh
+    N, T, D, H = 4, 256, 512, 8
+    q, k, v, g = (synth.normal(30 + i, (N, T, D)) for i in range(4))
+    mask = np.ones((N, T), np.float32)
+    mask[1, 200:] = 0
+    for causal in (False, True):
+        out, probs = nnh.attention_forward(dev(q), dev(k), dev(v), H, dev(mask), causal)
+        dq, dk, dv = (torch.full((N, T, D), float("nan"), device="cuda") for _ in range(3))
+        nnh.attention_backward(dev(g), dev(q), dev(k), dev(v), probs, H, dev(mask), causal, dq, True, dk, True, dv,
+                               True)
+        with correctly_rounded_exp(oracle):
+            _, want_probs = oracle.attention_forward(q, k, v, H, mask, causal)
+            want = oracle.attention_backward(g, q, k, v, want_probs, H, mask, causal)
+        for t, w, key in zip((dq, dk, dv), want, ("dq", "dk", "dv")):
+            same(host(t), w, (key, causal))
+
+
+def test_self_attention_gradient_sums_the_three_roles(gpu, oracle):
+    """One node as query, key and value (test_autograd.cpp:1591-1594): dV is stored first, dQ and dK add."""
+    import nnh
+    x = synth.mt19937_uniform(44, 2 * 7 * 12).reshape(2, 7, 12)
+    g = synth.mt19937_uniform(45, 2 * 7 * 12).reshape(2, 7, 12)
+    dx_, gx = dev(x), dev(g)
+    out, probs = nnh.attention_forward(dx_, dx_, dx_, 3, None, True)
+    grad = dev(np.full(x.shape, np.nan, np.float32))
+    nnh.attention_backward(gx, dx_, dx_, dx_, probs, 3, None, True, grad, False, grad, False, grad, True)
+    want = np.zeros_like(x)
+    L = oracle.lib
+    from pyoracle import _fp
+    with correctly_rounded_exp(oracle):
+        _, p = oracle.attention_forward(x, x, x, 3, None, True)
+    L.oracle_attention_backward(_fp(g), _fp(x), _fp(x), _fp(x), _fp(p), 2, 7, 7, 12, 3, None, 1, _fp(want), 0,
+                                _fp(want), 0, _fp(want), 1)
+    same(host(grad), want, "self-attention gradient")
+
+
+def test_attention_hand_reference_and_masks(gpu):
+    """test_transformer.cpp:149-176 (one head, identity projections) and 232-276 (a fully masked row is
+    finite: exactly the mean of V)."""
+    import nnh
+    x = np.array([1, 0, 0, 2], np.float32).reshape(1, 2, 2)
+    out, _ = nnh.attention_forward(dev(x), dev(x), dev(x), 1)
+    out = host(out)
+    s = np.float32(np.sqrt(2.0))
+    for i in range(2):
+        s0 = (x[0, i, 0] * x[0, 0, 0] + x[0, i, 1] * x[0, 0, 1]) / s
+        s1 = (x[0, i, 0] * x[0, 1, 0] + x[0, i, 1] * x[0, 1, 1]) / s
+        e0, e1 = np.exp(s0), np.exp(s1)
+        for c in range(2):
+            want = (e0 * x[0, 0, c] + e1 * x[0, 1, c]) / (e0 + e1)
+            assert abs(out[0, i, c] - want) <= 1e-5 * abs(want) + 1e-7
+    xs = synth.mt19937_uniform(3, 32).reshape(2, 4, 4)
+    none = np.array([[0, 0, 0, 0], [1, 1, 1, 1]], np.float32)
+    o, _ = nnh.attention_forward(dev(xs), dev(xs), dev(xs), 2, dev(none), False)
+    o = host(o)
+    assert np.all(np.isfinite(o))
+    assert np.allclose(o[0], np.broadcast_to(xs[0].mean(axis=0), (4, 4)), rtol=1e-5, atol=1e-6)
+
+
+def test_scaled_masked_softmax_matches_oracle(gpu, oracle):
+    import nnh
+    x = synth.normal(9, (2, 3, 33, 40))
+    mask = np.ones((2, 40), np.float32)
+    mask[0, 35:] = 0
+    for causal, m in ((False, None), (False, mask), (True, None)):
+        if causal:
+            x = synth.normal(10, (2, 3, 40, 40))
+        y = nnh.scaled_masked_softmax_forward(dev(x), 0.3, dev(m), causal)
+        with correctly_rounded_exp(oracle):
+            same(host(y), oracle.scaled_masked_softmax(x, np.float32(0.3), m, causal), ("forward", causal))
+        assert int(ulps(host(y), oracle.scaled_masked_softmax(x, np.float32(0.3), m, causal)).max()) <= 4
+    x = synth.normal(11, (2, 3, 17, 17))
+    y = oracle.scaled_masked_softmax(x, np.float32(0.5), None, True)
+    gr = synth.normal(12, y.shape)
+    for first in (True, False):
+        d0 = synth.normal(13, y.shape)
+        d = dev(d0)
+        nnh.scaled_masked_softmax_backward(dev(y), dev(gr), d, 0.5, None, True, first)
+        want = d0.copy()
+        for r in range(2 * 3 * 17):
+            n, i = r // (3 * 17), r % 17
+            yy, gg = y.reshape(-1, 17)[r], gr.reshape(-1, 17)[r]
+            dot = np.float32(0)
+            for j in range(17):
+                dot = np.float32(dot + np.float32(gg[j] * yy[j]))
+            for j in range(17):
+                masked = j > i
+                term = np.float32(np.float32(0.5) * np.float32(yy[j] * np.float32(gg[j] - dot)))
+                if first:
+                    want.reshape(-1, 17)[r, j] = np.float32(0) if masked else np.float32(term + np.float32(0))
+                elif not masked:
+                    want.reshape(-1, 17)[r, j] = np.float32(want.reshape(-1, 17)[r, j] + term)
+        same(host(d), want, ("backward", first))
+
+
+def test_attention_shape_errors(gpu):
+    """test_autograd.cpp:1634-1640: heads must divide D; causal needs Tq == Tk."""
+    import torch
+
+    import nnh
+    q = torch.zeros((2, 4, 6), device="cuda")
+    with pytest.raises(nnh.ShapeError):
+        nnh.attention_forward(q, q, q, 4)
+    k5 = torch.zeros((2, 5, 6), device="cuda")
+    with pytest.raises(nnh.ShapeError):
+        nnh.attention_forward(q, k5, k5, 2, None, True)

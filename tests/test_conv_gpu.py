@@ -1,0 +1,132 @@
+"""Parity of nn::conv2d / nn::conv2d_relu (forward and backward), im2col and col2im on the GPU.
+
+Bitwise against nn-cpp's golden outputs and against the oracle at BASELINE config 3 (batch 128: conv1 1->32 on
+28x28, conv2 32->64 on 14x14 after 2x2 max-pooling), on both forward paths (direct for a short depth, im2col +
+MFMA GEMM for a long one).
+"""
+import numpy as np
+import pytest
+
+from helpers import first_diff
+from nnh import synth
+
+pytestmark = pytest.mark.gpu
+
+
+def dev(a):
+    import torch
+    return None if a is None else torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def host(t):
+    import torch
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def same(got, want, what):
+    assert got.shape == want.shape, (what, got.shape, want.shape)
+    assert got.tobytes() == want.tobytes(), f"{what}: {first_diff(got, want)}"
+
+
+def test_conv_golden(gpu):
+    import golden_cases as gc
+    import torch
+
+    import nnh
+    g = np.load(gc.__file__.replace("golden_cases.py", "reference_vectors.npz"))
+    for name, spec in gc.CONV_CASES:
+        x, w, bias, gr, stride, pad, relu = gc.conv_inputs(spec)
+        y, alive = nnh.conv2d_forward(dev(x), dev(w), dev(bias), stride, pad, relu)
+        same(host(y), g[f"conv/{name}/y"], name)
+        # nn-cpp's leaves add into zero-filled gradients
+        dx, dw, db = (torch.zeros(t.shape, device="cuda") for t in (x, w, bias))
+        nnh.conv2d_backward(dev(gr), dev(x), dev(w), alive, stride, pad, dx, False, dw, False, db, False)
+        for key, t in (("dx", dx), ("dw", dw), ("db", db)):
+            same(host(t), g[f"conv/{name}/{key}"], (name, key))
+
+
+def maxpool2(y):
+    N, C, H, W = y.shape
+    return y.reshape(N, C, H // 2, 2, W // 2, 2).max(axis=(3, 5))
+
+
+def config3():
+    """x ~ U[0,1] (seed 2); conv weights ~ N(0, sqrt(2 / fan_in)) (Kaiming-normal), zero biases."""
+    x = synth.mt19937_uniform(2, 128 * 28 * 28, 0.0, 1.0).reshape(128, 1, 28, 28)
+    w1 = (synth.normal(21, (32, 1, 3, 3)) * np.float32(np.sqrt(2.0 / 9))).astype(np.float32)
+    w2 = (synth.normal(22, (64, 32, 3, 3)) * np.float32(np.sqrt(2.0 / 288))).astype(np.float32)
+    return x, w1, w2
+
+
+@pytest.mark.parametrize("layer", [1, 2])
+def test_baseline_config3(gpu, oracle, layer):
+    import torch
+
+    import nnh
+    x, w1, w2 = config3()
+    b1, b2 = np.zeros(32, np.float32), np.zeros(64, np.float32)
+    y1, a1 = oracle.conv2d_forward(x, w1, b1, 1, 1, 1)
+    if layer == 1:
+        xin, w, b, want_y, want_a = x, w1, b1, y1, a1
+    else:
+        xin = np.ascontiguousarray(maxpool2(y1))
+        w, b = w2, b2
+        want_y, want_a = oracle.conv2d_forward(xin, w, b, 1, 1, 1)
+    y, alive = nnh.conv2d_forward(dev(xin), dev(w), dev(b), 1, 1, True)
+    same(host(y), want_y, f"conv{layer} forward")
+    same(host(alive), want_a, f"conv{layer} alive")
+    gr = synth.normal(30 + layer, want_y.shape)
+    dx, dw, db = (torch.full(t.shape, float("nan"), device="cuda") for t in (xin, w, b))
+    nnh.conv2d_backward(dev(gr), dev(xin), dev(w), alive, 1, 1, dx, True, dw, True, db, True)
+    wdx, wdw, wdb = oracle.conv2d_backward(gr, xin, w, want_a, 1, 1, dx_first=True)
+    same(host(dx), wdx, f"conv{layer} dx")
+    same(host(dw), wdw, f"conv{layer} dw")
+    same(host(db), wdb, f"conv{layer} db")
+
+
+def test_direct_and_gemm_paths_match_the_oracle(gpu, oracle):
+    """K = Cin*kh*kw <= 32 takes the direct kernel, longer depths im2col + GEMM; both are the reference's chain."""
+    import nnh
+    for (N, Cin, H, W, Cout, kk, s, p) in ((3, 3, 11, 9, 40, 3, 1, 1), (3, 4, 11, 9, 40, 3, 1, 1),
+                                            (2, 1, 8, 8, 5, 5, 2, 2), (2, 8, 8, 8, 70, 5, 2, 2), (5, 2, 7, 6, 3, 2, 3, 0)):
+        x = synth.mt19937_uniform(N * 100 + Cin, N * Cin * H * W).reshape(N, Cin, H, W)
+        w = synth.mt19937_uniform(Cout + 7, Cout * Cin * kk * kk).reshape(Cout, Cin, kk, kk)
+        b = synth.mt19937_uniform(Cout + 8, Cout)
+        for relu in (False, True):
+            y, alive = nnh.conv2d_forward(dev(x), dev(w), dev(b), s, p, relu)
+            wy, wa = oracle.conv2d_forward(x, w, b, s, p, relu)
+            same(host(y), wy, (N, Cin, Cout, kk, s, p, relu))
+            if relu:
+                same(host(alive), wa, "alive")
+
+
+def test_im2col_col2im(gpu, oracle):
+    import torch
+
+    import nnh
+    for (N, Cin, H, W, kk, s, p) in ((2, 3, 7, 6, 3, 2, 1), (1, 2, 5, 5, 4, 3, 3), (3, 1, 28, 28, 3, 1, 1)):
+        x = synth.mt19937_uniform(N + H, N * Cin * H * W).reshape(N, Cin, H, W)
+        col = nnh.im2col(dev(x), kk, kk, s, p)
+        same(host(col), oracle.im2col(x, kk, kk, s, p), ("im2col", N, Cin, H, W, kk, s, p))
+        y = synth.mt19937_uniform(N + W + 1, col.numel()).reshape(tuple(col.shape))
+        base = synth.mt19937_uniform(N + W + 2, x.size).reshape(x.shape)
+        for first in (True, False):
+            d = dev(base)
+            nnh.col2im_add(dev(y), d, kk, kk, s, p, first)
+            want = oracle.col2im_add(y, np.zeros_like(x) if first else base, kk, kk, s, p)
+            same(host(d), want, ("col2im", first))
+
+
+def test_conv_shape_errors(gpu):
+    """ops.cpp:1350-1365: stride > 0, padding >= 0, kernel within the padded input."""
+    import torch
+
+    import nnh
+    x = torch.zeros((1, 1, 3, 3), device="cuda")
+    w = torch.zeros((1, 1, 5, 5), device="cuda")
+    b = torch.zeros(1, device="cuda")
+    with pytest.raises(nnh.ShapeError):
+        nnh.conv2d_forward(x, w, b, 1, 0, False)
+    with pytest.raises(nnh.ShapeError):
+        nnh.conv2d_forward(x, torch.zeros((1, 1, 2, 2), device="cuda"), b, 0, 0, False)
