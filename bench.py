@@ -51,7 +51,7 @@ def cpu_model():
     return "unknown CPU"
 
 
-def cpu_baseline(a, b, m, n, k, budget_s=12.0, max_runs=30):
+def cpu_baseline(a, b, m, n, k, budget_s=15.0, max_runs=400):
     """nn-cpp's own sgemm (oracle/_ref) on the same host buffers, reference method: warm-up, then the median of
     timed runs (apps/bench/runner.cpp:80-96), bounded to about budget_s seconds of CPU work."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
@@ -267,12 +267,14 @@ def report():
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=40)
     ap.add_argument("--size", type=int, default=4096)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--report", action="store_true", help="every BASELINE config as a markdown table (not the "
                     "driver's JSON line)")
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
+                    help="only run 5 device-to-device copies of MIB MiB (calibrates rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (this build has no multi-GPU path); --gpus {args.gpus} is not "
@@ -280,6 +282,16 @@ def main():
         sys.exit(2)
     if args.report:
         report()
+        return
+    if args.copy_probe:
+        import torch
+        nbytes = args.copy_probe << 20
+        src = torch.ones(nbytes // 4, device="cuda:0")
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"copy probe: 5 copies of {nbytes} bytes ({nbytes / 1024:.0f} KiB read + written per copy)")
         return
 
     import numpy as np
