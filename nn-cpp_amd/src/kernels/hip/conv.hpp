@@ -16,6 +16,11 @@ hipError_t im2col(const float* x, float* col, const ConvGeom& g, int64_t samples
 hipError_t col2im(const float* col, float* dx, const ConvGeom& g, int64_t samples, int first, hipStream_t s);
 hipError_t conv_direct(const float* x, const float* w, const float* bias, float* y, unsigned char* alive,
                        const ConvGeom& g, int64_t samples, int cout, int relu, hipStream_t s);
+// The direct kernel's vectorised form (stride 1, "same" width, w % 4 == 0, aligned buffers), with an explicit
+// number of output channels per lane (4 or 8); conv_direct uses it whenever conv_same_quad_ok holds.
+bool conv_same_quad_ok(const float* x, const float* y, const unsigned char* alive, const ConvGeom& g, int64_t samples);
+hipError_t conv_same_quad(const float* x, const float* w, const float* bias, float* y, unsigned char* alive,
+                          const ConvGeom& g, int64_t samples, int cout, int relu, int cg, hipStream_t s);
 hipError_t mask_grad(const float* g, const unsigned char* alive, float* out, int64_t total, hipStream_t s);
 hipError_t lane_sums(const float* src, int64_t rows, int64_t n, float* dst, hipStream_t s);
 

@@ -130,3 +130,49 @@ def test_conv_shape_errors(gpu):
         nnh.conv2d_forward(x, w, b, 1, 0, False)
     with pytest.raises(nnh.ShapeError):
         nnh.conv2d_forward(x, torch.zeros((1, 1, 2, 2), device="cuda"), b, 0, 0, False)
+
+
+def test_same_width_quad_path(gpu, oracle):
+    """Stride 1, kw = 2 pad + 1, W % 4 == 0 takes the 4-pixels-per-lane direct kernel: every pad 0..4, several
+    input channels, Cout not a multiple of the channel group, kh != kw, rows that straddle waves (W = 28: a wave
+    of 64 lanes ends mid-row), and an unaligned y (the scalar kernel then)."""
+    import torch
+
+    import nnh
+    # (the direct kernels take depths Cin*kh*kw <= 32; pads 3 and 4 reach them with one-row kernels)
+    cases = ((4, 1, 28, 28, 32, 3, 3, 1), (3, 2, 9, 12, 7, 1, 1, 0), (2, 1, 10, 8, 19, 5, 5, 2),
+             (2, 1, 13, 20, 9, 1, 7, 3), (1, 2, 12, 16, 5, 1, 9, 4), (3, 2, 11, 24, 6, 5, 3, 1),
+             (2, 3, 6, 4, 12, 1, 3, 1))
+    for (N, Cin, H, W, Cout, kh, kw, p) in cases:
+        x = synth.mt19937_uniform(N * 31 + W, N * Cin * H * W).reshape(N, Cin, H, W)
+        w = synth.mt19937_uniform(Cout * 3 + kh, Cout * Cin * kh * kw).reshape(Cout, Cin, kh, kw)
+        b = synth.mt19937_uniform(Cout + 9, Cout)
+        for relu in (False, True):
+            y, alive = nnh.conv2d_forward(dev(x), dev(w), dev(b), 1, p, relu)
+            wy, wa = oracle.conv2d_forward(x, w, b, 1, p, relu)
+            same(host(y), wy, (N, Cin, H, W, Cout, kh, kw, p, relu))
+            if relu:
+                same(host(alive), wa, ("alive", N, Cin, H, W, Cout, kh, kw, p))
+    # Inf, NaN and -0 weights: a padding tap is fma(w, 0, acc), so an infinite weight makes the border NaN
+    N, Cin, H, W, Cout = 2, 1, 8, 8, 4
+    x = synth.mt19937_uniform(5, N * H * W).reshape(N, Cin, H, W)
+    x[0, 0, 3, 3] = -0.0
+    w = synth.mt19937_uniform(6, Cout * 9).reshape(Cout, Cin, 3, 3)
+    w[0, 0, 0, 0], w[1, 0, 2, 2], w[2, 0, 1, 1], w[3, 0, 1, 0] = np.inf, np.nan, -0.0, -np.inf
+    b = np.array([0.0, -0.0, 1.0, -1.0], np.float32)
+    for relu in (False, True):
+        y, alive = nnh.conv2d_forward(dev(x), dev(w), dev(b), 1, 1, relu)
+        wy, wa = oracle.conv2d_forward(x, w, b, 1, 1, relu)
+        same(host(y), wy, ("special values", relu))
+    # an output view that is not 16-byte aligned falls back to the scalar kernel with the same bits
+    x = synth.mt19937_uniform(8, 2 * 1 * 12 * 12).reshape(2, 1, 12, 12)
+    w = synth.mt19937_uniform(9, 5 * 9).reshape(5, 1, 3, 3)
+    b = synth.mt19937_uniform(10, 5)
+    buf = torch.zeros(2 * 5 * 144 + 1, device="cuda")
+    yv = buf[1:]
+    dx, dw, db = dev(x), dev(w), dev(b)  # held until the kernel has run
+    rc = nnh.lib().nnh_conv2d_forward(nnh._ptr(dx), 2, 1, 12, 12, nnh._ptr(dw), 5, 3, 3, nnh._ptr(db), 1, 1,
+                                      1, nnh._ptr(yv), None, nnh._stream(None))
+    nnh.check(rc)
+    wy, _ = oracle.conv2d_forward(x, w, b, 1, 1, True)
+    same(host(yv).reshape(wy.shape), wy, "unaligned y")
