@@ -10,6 +10,7 @@ before timing starts. Prints one JSON line on stdout (diagnostics go to stderr).
 
 roofline.achieved = 2 M N K / (average kernel duration from HIP events recorded on the launch stream);
 roofline.traffic comes from the committed rocprofv3 PMC summary (profiles/sgemm_4096_pmc.md) when present.
+fused_op = the metric's "fused-op GB/s": conv2d_relu forward of config 3's memory-bound first layer.
 cpu_baseline = nn-cpp's NN_NATIVE AVX2 sgemm (oracle/_ref, compiled from the reference's own sources) on the
 same inputs, on the host's cores (at most 16 threads), median of a bounded number of runs.
 """
@@ -87,21 +88,82 @@ def cpu_baseline(a, b, m, n, k, budget_s=15.0, max_runs=400):
     }
 
 
+def fused_op_conv1():
+    """The metric's fused-op figure: nn::conv2d_relu forward of BASELINE config 3's first layer (x [128,1,28,28]
+    U[0,1] seed 2, W [32,1,3,3] Kaiming-normal, zero bias, stride 1, pad 1), the memory-bound direct kernel
+    with its bias/ReLU/alive epilogue. Algorithmic bytes: x + W + b read once, y written once (the alive flags
+    are extra traffic, not counted). Device time from device_time_ms."""
+    import numpy as np
+    import torch
+
+    import nnh
+    from nnh import synth
+    dev = torch.device("cuda:0")
+    xc = synth.mt19937_uniform(2, 128 * 28 * 28, 0.0, 1.0).reshape(128, 1, 28, 28)
+    w1 = (synth.normal(21, (32, 1, 3, 3)) * np.float32(np.sqrt(2.0 / 9))).astype(np.float32)
+    dx, dw, db = (torch.from_numpy(np.ascontiguousarray(t)).to(dev) for t in (xc, w1, np.zeros(32, np.float32)))
+    y = torch.empty((128, 32, 28, 28), device=dev)
+    alive = torch.empty((128, 32, 28, 28), dtype=torch.uint8, device=dev)
+    lib, stream = nnh.lib(), torch.cuda.current_stream()
+
+    def step(al):
+        nnh.check(lib.nnh_conv2d_forward(nnh._ptr(dx), 128, 1, 28, 28, nnh._ptr(dw), 32, 3, 3, nnh._ptr(db), 1, 1, 1,
+                                         nnh._ptr(y), nnh._ptr(al), nnh._stream(stream)))
+
+    nbytes = 4 * (xc.size + w1.size + 32 + y.numel())
+    ms = device_time_ms(lambda: step(alive), reps=200)
+    ms_no_alive = device_time_ms(lambda: step(None), reps=200)
+    gbps = nbytes / (ms * 1e-3) / 1e9
+    log(f"conv1 conv2d_relu: {ms * 1e3:.2f} us with alive flags ({gbps:.0f} GB/s), "
+        f"{ms_no_alive * 1e3:.2f} us without")
+    return {"workload": "conv2d_relu forward, BASELINE config 3 conv1: x [128,1,28,28] -> y [128,32,28,28], 3x3 s1 p1, "
+                        "with alive flags", "value": round(gbps, 1), "unit": "GB/s", "us_per_launch": round(ms * 1e3, 3),
+            "algorithmic_bytes": nbytes, "roofline": {"bound": "hbm", "peak": PEAK_HBM_GBPS, "unit": "GB/s",
+                                                      "frac": round(gbps / PEAK_HBM_GBPS, 4)},
+            "without_alive_flags": {"us_per_launch": round(ms_no_alive * 1e3, 3),
+                                    "value": round(nbytes / (ms_no_alive * 1e-3) / 1e9, 1)}}
+
+
 # ---------------------------------------------------------------------------------------------------------------
 # --report: every BASELINE.json config, absolute throughput and roofline fraction, nn-cpp's CPU path beside it
 
-def _gpu_time_ms(fn, warmup=3, reps=20):
-    """Average duration of fn() (one or more launches on torch's current stream) from HIP events."""
+def device_time_ms(fn, reps=50, warmup_s=0.05, stream=None):
+    """Average device time of one fn() (one or more launches on torch's current stream), without the
+    Python caller's issue time: a bounded device-side delay (nnh.bench_delay) holds the stream while the
+    host queues `reps` calls, then HIP events recorded on that stream around the calls time them back to
+    back. Warm-up runs fn() for at least warmup_s of wall time so the clocks have ramped."""
     import torch
-    for _ in range(warmup):
+
+    import nnh
+    stream = stream or torch.cuda.current_stream()
+    t_end = time.perf_counter() + warmup_s
+    n = 0
+    while n < 3 or time.perf_counter() < t_end:
         fn()
+        n += 1
     torch.cuda.synchronize()
+    h0 = time.perf_counter()
+    for _ in range(10):
+        fn()
+    issue_per_call = (time.perf_counter() - h0) / 10
+    torch.cuda.synchronize()
+    delay_us = min(1.5e6, 1000.0 + 3.0 * reps * issue_per_call * 1e6)
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for _ in range(reps):
-        fn()
-    e1.record()
-    torch.cuda.synchronize()
+    for attempt in range(4):
+        nnh.bench_delay(delay_us, stream)
+        e0.record(stream)
+        h0 = time.perf_counter()
+        for _ in range(reps):
+            fn()
+        issued = time.perf_counter() - h0
+        e1.record(stream)
+        torch.cuda.synchronize()
+        if issued * 1e6 <= delay_us:
+            break
+        # the host fell behind the delay, so the events also timed host gaps: measure again with a longer delay
+        delay_us = min(1.5e6, 2.0 * issued * 1e6 + 1000.0)
+    else:
+        log(f"  (host issue {issued * 1e6:.0f} us outlasted the {delay_us:.0f} us delay: the time includes host gaps)")
     return e0.elapsed_time(e1) / reps
 
 
@@ -148,7 +210,7 @@ def report():
     da, db, dc = d(a), d(b), torch.empty((n, n), device=dev)
     c = np.empty((n, n), np.float32)
     for ta, tb, name in ((0, 0, "C=A B"), (1, 0, "C=A^T B"), (0, 1, "C=A B^T")):
-        ms = _gpu_time_ms(lambda: nnh.sgemm(ta, tb, n, n, n, da, n, db, n, dc, n))
+        ms = device_time_ms(lambda: nnh.sgemm(ta, tb, n, n, n, da, n, db, n, dc, n))
         cpu = _cpu_time_ms(lambda: ref.sgemm_inplace(ta, tb, n, n, n, a, n, b, n, c, n, 0)) if ref else None
         row(1, f"sgemm 512^3 {name}", ms, flops=2.0 * n ** 3, cpu_ms=cpu)
 
@@ -185,14 +247,14 @@ def report():
             for i in range(3):
                 h = np.maximum(ref.linear_forward(h, ws[i], bs[i]), np.float32(0))
         cpu = _cpu_time_ms(cpu_fwd)
-    row(2, "MLP forward (3 x linear+ReLU)", _gpu_time_ms(mlp_fwd), flops=fwd_flops, cpu_ms=cpu)
+    row(2, "MLP forward (3 x linear+ReLU)", device_time_ms(mlp_fwd), flops=fwd_flops, cpu_ms=cpu)
     cpu = None
     if ref:
         hacts = [x]
         for i in range(3):
             hacts.append(np.maximum(ref.linear_forward(hacts[-1], ws[i], bs[i]), np.float32(0)))
         cpu = _cpu_time_ms(lambda: [ref.linear_backward(hacts[i], ws[i], bs[i], gys[i]) for i in range(3)])
-    row(2, "MLP backward (dX, dW, db per layer)", _gpu_time_ms(mlp_bwd), flops=2 * fwd_flops, cpu_ms=cpu)
+    row(2, "MLP backward (dX, dW, db per layer)", device_time_ms(mlp_bwd), flops=2 * fwd_flops, cpu_ms=cpu)
 
     # config 3: conv2d_relu, batch 128: conv1 1->32 on 28x28 (memory-bound), conv2 32->64 on 14x14
     xc = synth.mt19937_uniform(2, 128 * 28 * 28, 0.0, 1.0).reshape(128, 1, 28, 28)
@@ -205,10 +267,21 @@ def report():
     hx2 = x2.cpu().numpy()
     conv1_bytes = 4 * (xc.size + w1.size + b1.size + 128 * 32 * 784)
     cpu = _cpu_time_ms(lambda: ref.conv2d_forward(xc, w1, b1, 1, 1, 1)) if ref else None
-    row(3, "conv1 conv2d_relu fwd (1->32, 28x28, b128)", _gpu_time_ms(lambda: nnh.conv2d_forward(dxc, dw1, db1, 1, 1, True)),
+    row(3, "conv1 conv2d_relu fwd (1->32, 28x28, b128)", device_time_ms(lambda: nnh.conv2d_forward(dxc, dw1, db1, 1, 1, True)),
         flops=2.0 * 128 * 32 * 784 * 9, nbytes=conv1_bytes, bound="hbm", cpu_ms=cpu)
+    row(3, "conv1 conv2d_relu fwd, no alive flags (backward masks with y > 0)",
+        device_time_ms(lambda: nnh.conv2d_forward(dxc, dw1, db1, 1, 1, True, want_alive=False)),
+        flops=2.0 * 128 * 32 * 784 * 9, nbytes=conv1_bytes, bound="hbm")
+    # not a BASELINE config: the same layer at batch 2048 shows the kernel's streaming rate once launch and
+    # drain latency (about 4 us for any 13 MB launch on this GPU) no longer dominate
+    xbig = dxc.repeat(16, 1, 1, 1)
+    row("3*", "conv1 conv2d_relu fwd at batch 2048 (steady state)",
+        device_time_ms(lambda: nnh.conv2d_forward(xbig, dw1, db1, 1, 1, True), reps=20),
+        flops=16 * 2.0 * 128 * 32 * 784 * 9, nbytes=16 * (conv1_bytes - 4 * (w1.size + b1.size)) + 4 * (w1.size + b1.size),
+        bound="hbm")
+    del xbig
     cpu = _cpu_time_ms(lambda: ref.conv2d_forward(hx2, w2, b2, 1, 1, 1)) if ref else None
-    row(3, "conv2 conv2d_relu fwd (32->64, 14x14, b128)", _gpu_time_ms(lambda: nnh.conv2d_forward(x2, dw2, db2, 1, 1, True)),
+    row(3, "conv2 conv2d_relu fwd (32->64, 14x14, b128)", device_time_ms(lambda: nnh.conv2d_forward(x2, dw2, db2, 1, 1, True)),
         flops=2.0 * 128 * 64 * 196 * 288, nbytes=4 * (hx2.size + w2.size + 64 + 128 * 64 * 196), cpu_ms=cpu)
     y2, al2 = nnh.conv2d_forward(x2, dw2, db2, 1, 1, True)
     g2 = d(synth.normal(32, tuple(y2.shape)))
@@ -218,7 +291,7 @@ def report():
         hg2 = g2.cpu().numpy()
         cpu = _cpu_time_ms(lambda: ref.conv2d_backward(hx2, w2, b2, 1, 1, 1, hg2))
     row(3, "conv2 conv2d_relu bwd (dx, dW, db)",
-        _gpu_time_ms(lambda: nnh.conv2d_backward(g2, x2, dw2, al2, 1, 1, gx2, True, gw2, True, gb2, True)),
+        device_time_ms(lambda: nnh.conv2d_backward(g2, x2, dw2, al2, 1, 1, gx2, True, gw2, True, gb2, True)),
         flops=2 * 2.0 * 128 * 64 * 196 * 288, cpu_ms=cpu)
 
     # config 4: attention 32 x 8 heads x 256 x 64 (+ causal); probs stored, as the reference does
@@ -228,7 +301,7 @@ def report():
     for causal in (False, True):
         cpu = _cpu_time_ms(lambda: ref.attention_forward(q, k, v, 8, None, causal), budget_s=4.0, max_runs=5) if ref else None
         row(4, "attention fwd" + (" causal" if causal else ""),
-            _gpu_time_ms(lambda: nnh.attention_forward(dq_, dk_, dv_, 8, None, causal)), flops=att_flops, cpu_ms=cpu)
+            device_time_ms(lambda: nnh.attention_forward(dq_, dk_, dv_, 8, None, causal)), flops=att_flops, cpu_ms=cpu)
     out, probs = nnh.attention_forward(dq_, dk_, dv_, 8, None, False)
     ga = d(synth.normal(7, (32, 256, 512)))
     gq, gk, gv = torch.empty_like(dq_), torch.empty_like(dk_), torch.empty_like(dv_)
@@ -237,7 +310,7 @@ def report():
         hg = ga.cpu().numpy()
         cpu = _cpu_time_ms(lambda: ref.attention_backward(q, k, v, 8, hg), budget_s=4.0, max_runs=3)
     row(4, "attention bwd (dQ, dK, dV)",
-        _gpu_time_ms(lambda: nnh.attention_backward(ga, dq_, dk_, dv_, probs, 8, None, False, gq, True, gk, True, gv, True)),
+        device_time_ms(lambda: nnh.attention_backward(ga, dq_, dk_, dv_, probs, 8, None, False, gq, True, gk, True, gv, True)),
         flops=2 * att_flops, cpu_ms=cpu)
 
     # config 5: roofline sweep, seed 4
@@ -249,7 +322,7 @@ def report():
         reps = 5 if m * n_ * k_ >= 8192 ** 3 else 20
         cpu = _cpu_time_ms(lambda: ref.sgemm_inplace(0, 0, m, n_, k_, a, k_, b, n_, c, n_, 0),
                            budget_s=6.0, max_runs=5) if ref else None
-        row(5, f"sgemm {m}x{n_}x{k_}", _gpu_time_ms(lambda: nnh.sgemm(0, 0, m, n_, k_, da, k_, db, n_, dc, n_), reps=reps),
+        row(5, f"sgemm {m}x{n_}x{k_}", device_time_ms(lambda: nnh.sgemm(0, 0, m, n_, k_, da, k_, db, n_, dc, n_), reps=reps),
             flops=2.0 * m * n_ * k_, cpu_ms=cpu)
 
     lines = [f"GPU: {torch.cuda.get_device_name(0)}; nn-cpp CPU baseline: NN_NATIVE AVX2 build, {threads} threads on "
@@ -271,6 +344,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=40)
     ap.add_argument("--size", type=int, default=4096)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-fused-op", action="store_true", help="skip the conv1 fused conv2d_relu GB/s figure")
     ap.add_argument("--report", action="store_true", help="every BASELINE config as a markdown table (not the "
                     "driver's JSON line)")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
@@ -329,6 +403,7 @@ def main():
     log(f"sgemm {m}^3: {kernel_ms:.4f} ms/launch (HIP events), {achieved:.2f} TFLOP/s per launch, "
         f"{value:.2f} TFLOP/s wall over {args.steps} steps")
 
+    fused = None if args.no_fused_op else fused_op_conv1()
     cpu = None if args.no_cpu_baseline else cpu_baseline(a, b, m, n, k)
     if cpu:
         log(f"cpu baseline: {cpu['value']} TFLOP/s ({cpu['sample']})")
@@ -352,6 +427,7 @@ def main():
         "roofline": {"bound": "mfma", "achieved": round(achieved, 3), "peak": PEAK_FP32_MFMA_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP32_MFMA_TFLOPS, 4), "traffic": traffic},
         "cpu_baseline": cpu,
+        "fused_op": fused,
     }
     print(json.dumps(out), flush=True)
 

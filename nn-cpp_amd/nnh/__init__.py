@@ -11,6 +11,7 @@ import os
 PKG_ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 LIB_PATH = os.path.join(PKG_ROOT, "lib", "libnnh.so")
 HOST_LIB_PATH = os.path.join(PKG_ROOT, "lib", "libnn_gemm_hip.so")
+BENCH_LIB_PATH = os.path.join(PKG_ROOT, "lib", "libnnh_bench.so")
 REPO_ROOT = os.path.dirname(PKG_ROOT)
 HEADER_PATH = os.path.join(REPO_ROOT, "include", "nnh.h")
 
@@ -295,6 +296,24 @@ def col2im_add(col, dx, kh, kw, stride, pad, first=False, stream=None):
     N, Cin, H, W = dx.shape
     check(lib().nnh_col2im_add(_ptr(col), N, Cin, H, W, kh, kw, int(stride), int(pad), _ptr(dx), int(first),
                                _stream(stream)))
+
+
+_bench_lib = None
+
+
+def bench_delay(microseconds, stream=None):
+    """Occupies the stream for `microseconds` of device time (libnnh_bench.so, a measurement helper): calls
+    queued behind it then run back to back, so events around them time the device, not the Python caller."""
+    global _bench_lib
+    if _bench_lib is None:
+        if not os.path.exists(BENCH_LIB_PATH):
+            raise RuntimeError(f"{BENCH_LIB_PATH} is missing: build it with `make -C nn-cpp_amd`")
+        L = C.CDLL(BENCH_LIB_PATH)
+        L.nnh_bench_delay.argtypes = [C.c_double, _vp]
+        _bench_lib = L
+    rc = _bench_lib.nnh_bench_delay(float(microseconds), _stream(stream))
+    if rc != 0:
+        raise NnhError(ERR_HIP, f"nnh_bench_delay: HIP error {rc}")
 
 
 _host_lib = None

@@ -46,10 +46,11 @@ const Config* configs() {
 	static const Config table[] = {
 		config_64x128x32(), config_128x128x32(), config_64x256x32(), config_128x64x32(),
 		config_128x256x16(), config_256x128x16(), config_64x128x64(), config_128x128x16(),
+		config_32x32x32_mf4(), config_64x64x32_mf4(), config_64x64x32_mf16(), config_128x64x32_mf16(),
 	};
 	return table;
 }
-constexpr int kNumConfigs = 8;
+constexpr int kNumConfigs = 12;
 
 // Raises each kernel's dynamic LDS limit once per device (gfx950 has 160 KiB per CU).
 hipError_t prepare_device() {
@@ -80,16 +81,27 @@ hipError_t prepare_device() {
 	return hipSuccess;
 }
 
-// Choice by measured throughput on MI355X (tile sweep over the BASELINE shapes): 128 x 128 tiles once there
-// are two workgroups per CU of them (16-deep stages for A B, 32-deep when an operand is transposed), then
-// 128 x 64, then 64 x 128 for small products. Results never depend on the choice.
-enum { kCfg64x128x32 = 0, kCfg128x128x32 = 1, kCfg128x64x32 = 3, kCfg128x128x16 = 7 };
+// Choice by measured device time on MI355X (every configuration on every BASELINE shape). Each output element
+// is a K-long chain of dependent MFMAs, and a dependent chain step costs about 64 cycles with 32x32x1 and 44
+// with 16x16x1 or 4x4x1, whose instructions also issue faster. Large products fill the GPU with 128 x 128 or
+// 128 x 64 tiles of 32x32x1 units (16-deep stages for A B, 32-deep when an operand is transposed); a million
+// outputs or more use 64 x 64 workgroups of 16x16x1 units; smaller products use 32 x 32 workgroups of 4x4x1
+// units, one wave per 16 x 16 block, so that as many chains as possible advance at once. Results never
+// depend on the choice.
+enum {
+	kCfg128x128x32 = 1,
+	kCfg128x64x32 = 3,
+	kCfg128x128x16 = 7,
+	kCfg32x32x32Mf4 = 8,
+	kCfg64x64x32Mf16 = 10,
+};
 
 int pick_config(const GemmCall& g) {
-	auto tiles = [&](int bm, int bn) { return ((g.m + bm - 1) / bm) * ((g.n + bn - 1) / bn) * g.batch_count; };
-	if (tiles(128, 128) >= 512) return (!g.ta && !g.tb) ? kCfg128x128x16 : kCfg128x128x32;
-	if (tiles(128, 64) >= 512) return kCfg128x64x32;
-	return kCfg64x128x32;
+	const double outputs = (double)g.m * (double)g.n * (double)g.batch_count;
+	if (outputs >= 512.0 * 128 * 128) return (!g.ta && !g.tb) ? kCfg128x128x16 : kCfg128x128x32;
+	if (g.m >= 128 && outputs >= 512.0 * 128 * 64) return kCfg128x64x32;
+	if (outputs >= 1024.0 * 1024) return kCfg64x64x32Mf16;
+	return kCfg32x32x32Mf4;
 }
 
 }  // namespace

@@ -15,7 +15,7 @@ struct Config {
 	KernelFn fn[4][2];  // [ta * 2 + tb][edge]
 };
 
-template <int BM, int BN, int BK, int WM, int WN, int WPE>
+template <int BM, int BN, int BK, int WM, int WN, int WPE, int MF = kMf32>
 Config make_config(const char* name) {
 	Config c{};
 	c.name = name;
@@ -23,9 +23,9 @@ Config make_config(const char* name) {
 	c.bn = BN;
 	c.bk = BK;
 #define NNH_SET(TA, TB)                                                                                  \
-	c.lds_bytes[TA * 2 + TB] = TileShape<BM, BN, BK, WM, WN, TA, TB>::kLdsFloats * (int)sizeof(float);   \
-	c.fn[TA * 2 + TB][0] = sgemm_tile_kernel<BM, BN, BK, WM, WN, WPE, TA, TB, false>;                         \
-	c.fn[TA * 2 + TB][1] = sgemm_tile_kernel<BM, BN, BK, WM, WN, WPE, TA, TB, true>;
+	c.lds_bytes[TA * 2 + TB] = TileShape<BM, BN, BK, WM, WN, MF, TA, TB>::kLdsFloats * (int)sizeof(float); \
+	c.fn[TA * 2 + TB][0] = sgemm_tile_kernel<BM, BN, BK, WM, WN, WPE, MF, TA, TB, false>;                     \
+	c.fn[TA * 2 + TB][1] = sgemm_tile_kernel<BM, BN, BK, WM, WN, WPE, MF, TA, TB, true>;
 	NNH_SET(false, false)
 	NNH_SET(false, true)
 	NNH_SET(true, false)
@@ -42,5 +42,10 @@ Config config_128x256x16();
 Config config_256x128x16();
 Config config_64x128x64();
 Config config_128x128x16();
+// short-latency MFMAs (4x4x1, 16x16x1) for products too small or too skinny to fill the GPU with 32x32 units
+Config config_32x32x32_mf4();
+Config config_64x64x32_mf4();
+Config config_64x64x32_mf16();
+Config config_128x64x32_mf16();
 
 }  // namespace nnh

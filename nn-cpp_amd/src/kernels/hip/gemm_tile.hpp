@@ -4,17 +4,26 @@
 //   nn::kernels::sgemm's AVX2 microkernel computes each C element as a sequential fused
 //   multiply-add chain over the depth, starting at +0 (src/kernels/gemm.cpp:232-244); depth
 //   blocks of 256 store and reload the running sum unchanged (gemm.cpp:225-231, 371).
-//   On gfx950, v_mfma_f32_32x32x1_2b_f32 computes exactly fma(a, b, c) per output element
-//   (single rounding, denormals kept): measured against fmaf on 520k outputs, all equal.
-//   This kernel issues one such MFMA per depth index k, in increasing k, starting from +0,
+//   On gfx950 the k = 1 fp32 MFMAs compute exactly fma(a, b, c) per output element (single
+//   rounding, denormals kept; see below). This kernel issues one MFMA per depth index k, in
+//   increasing k, starting from +0,
 //   so every element is the same fma chain. The k order never depends on the tile shape,
 //   the grid, ld, alignment, batch or stream: results are a pure function of the inputs.
 //   With accumulate, the old C is added after the first min(K, 256) steps (Store::kAdd then
 //   Store::kContinue, gemm.cpp:245-252), exactly as the reference does.
 //
+// The three k = 1 fp32 MFMAs of gfx950 all compute exactly fma(a, b, c) per element (measured against fmaf on
+// 1-8 million outputs each, special values included); they differ in latency per chain step, which bounds
+// products whose grid cannot fill the GPU (each element is a K-long dependent chain):
+//   32x32x1_2b: 2048 fmas, 16 passes; 16x16x1_4b: 1024 fmas, 8 passes; 4x4x1_16b: 256 fmas, 2 passes.
+// Large products use 32x32x1 (the most reuse per LDS read); small and skinny ones use the shorter ones.
+//
 // Tiling: 256 threads = 4 waves. A workgroup owns a BM x BN tile of C; wave w owns a WM x WN
-// sub-tile. One MFMA covers 64 rows x 32 columns (two 32x32 blocks: A lanes 0-31 and 32-63
-// carry 64 distinct rows, B lanes 32-63 repeat lanes 0-31's 32 columns).
+// sub-tile made of MFMA units (Mfma<MF>::UM x UN each):
+//   32x32x1_2b: unit 64 x 32 (two 32x32 blocks: A lanes 0-31 and 32-63 carry 64 distinct rows,
+//               B lanes 32-63 repeat lanes 0-31's 32 columns);
+//   16x16x1_4b: unit 64 x 16 (four 16x16 blocks stacked along M, sharing their 16 columns);
+//   4x4x1_16b:  unit 16 x 16 (sixteen 4x4 blocks as a 4 x 4 grid).
 // Operands go global -> registers -> LDS (double buffered, one barrier per depth tile).
 // LDS layouts follow the global layout so that every global load and LDS store is 16 bytes:
 //   K-contiguous operands (A when !TA, B when TB) are stored [row][BK+4] and read as one
@@ -28,7 +37,48 @@
 namespace nnh {
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x32 __attribute__((ext_vector_type(32)));
+
+enum MfmaKind : int { kMf32 = 0, kMf16 = 1, kMf4 = 2 };
+
+// Per MFMA kind: the unit tile, which row of A (column of B) lane l supplies, and where accumulator
+// register r of lane l sits in the unit (lane layouts measured on gfx950).
+template <int MF>
+struct Mfma;
+
+template <>
+struct Mfma<kMf32> {
+	static constexpr int UM = 64, UN = 32, NV = 32;
+	using Acc = f32x32;
+	__device__ static int arow(int l) { return l; }
+	__device__ static int bcol(int l) { return l & 31; }
+	__device__ static int crow(int r, int l) { return 32 * (r >> 4) + 8 * ((r & 15) >> 2) + 4 * (l >> 5) + (r & 3); }
+	__device__ static int ccol(int l) { return l & 31; }
+	__device__ static Acc mma(float a, float b, const Acc& c) { return __builtin_amdgcn_mfma_f32_32x32x1f32(a, b, c, 0, 0, 0); }
+};
+
+template <>
+struct Mfma<kMf16> {
+	static constexpr int UM = 64, UN = 16, NV = 16;
+	using Acc = f32x16;
+	__device__ static int arow(int l) { return l; }
+	__device__ static int bcol(int l) { return l & 15; }
+	__device__ static int crow(int r, int l) { return 16 * (r >> 2) + 4 * (l >> 4) + (r & 3); }
+	__device__ static int ccol(int l) { return l & 15; }
+	__device__ static Acc mma(float a, float b, const Acc& c) { return __builtin_amdgcn_mfma_f32_16x16x1f32(a, b, c, 0, 0, 0); }
+};
+
+template <>
+struct Mfma<kMf4> {
+	static constexpr int UM = 16, UN = 16, NV = 4;
+	using Acc = f32x4;
+	__device__ static int arow(int l) { return 4 * (l >> 4) + (l & 3); }
+	__device__ static int bcol(int l) { return 4 * ((l >> 2) & 3) + (l & 3); }
+	__device__ static int crow(int r, int l) { return 4 * (l >> 4) + r; }
+	__device__ static int ccol(int l) { return 4 * ((l >> 2) & 3) + (l & 3); }
+	__device__ static Acc mma(float a, float b, const Acc& c) { return __builtin_amdgcn_mfma_f32_4x4x1f32(a, b, c, 0, 0, 0); }
+};
 
 constexpr int kMaxBatchDims = 4;
 constexpr int kAccAfter = 256;  // nn-cpp's kKC (gemm.hpp:33): where an accumulating product adds old C
@@ -122,13 +172,13 @@ __device__ __forceinline__ void store_tile(float* lds, const f32x4* v, int tid) 
 	}
 }
 
-template <int BM, int BN, int BK, int WM, int WN, bool TA, bool TB>
+template <int BM, int BN, int BK, int WM, int WN, int MF, bool TA, bool TB>
 struct TileShape {
 	static constexpr int kWavesN = BN / WN;
 	static_assert((BM / WM) * (BN / WN) == 4, "4 waves per workgroup");
-	static_assert(WM % 64 == 0 && WN % 32 == 0, "one MFMA covers 64 x 32");
+	static_assert(WM % Mfma<MF>::UM == 0 && WN % Mfma<MF>::UN == 0, "wave tile must be whole MFMA units");
 	static_assert(kAccAfter % BK == 0 && BK % 4 == 0, "depth tile must divide 256");
-	static constexpr int I = WM / 64, J = WN / 32;
+	static constexpr int I = WM / Mfma<MF>::UM, J = WN / Mfma<MF>::UN;
 	// LDS strides (floats). K-major tiles get 4 floats of padding so that 64 lanes reading 16 bytes
 	// from 64 consecutive rows spread over the banks.
 	static constexpr int SA = TA ? BM : BK + 4;
@@ -150,9 +200,10 @@ __device__ __forceinline__ int xcd_remap(int bid, int total) {
 	return bid;
 }
 
-template <int BM, int BN, int BK, int WM, int WN, int WPE, bool TA, bool TB, bool EDGE>
+template <int BM, int BN, int BK, int WM, int WN, int WPE, int MF, bool TA, bool TB, bool EDGE>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE))) sgemm_tile_kernel(const GemmArgs p) {
-	using S = TileShape<BM, BN, BK, WM, WN, TA, TB>;
+	using S = TileShape<BM, BN, BK, WM, WN, MF, TA, TB>;
+	using U = Mfma<MF>;
 	constexpr int I = S::I, J = S::J;
 	extern __shared__ __align__(16) float lds[];
 
@@ -193,13 +244,13 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE)))
 	const bool acc_mode = p.accumulate && p.pieces == 1;
 	const int acc_tile = (p.k > kAccAfter) ? kAccAfter / BK - 1 : -1;
 
-	f32x32 acc[I][J];
+	typename U::Acc acc[I][J];
 #pragma unroll
 	for (int i = 0; i < I; ++i)
 #pragma unroll
 		for (int j = 0; j < J; ++j)
 #pragma unroll
-			for (int r = 0; r < 32; ++r) acc[i][j][r] = 0.0f;
+			for (int r = 0; r < U::NV; ++r) acc[i][j][r] = 0.0f;
 
 	const bool vec_ok = p.vec_ok != 0;
 	f32x4 ra[S::LA], rb[S::LB];
@@ -224,15 +275,15 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE)))
 	};
 
 	// C element (i, j, r) of this lane: row and column inside the workgroup tile
-	auto c_row = [&](int i, int r, int ln) { return wm0 + 64 * i + 32 * (r >> 4) + 8 * ((r & 15) >> 2) + 4 * (ln >> 5) + (r & 3); };
-	auto c_col = [&](int j, int ln) { return wn0 + 32 * j + (ln & 31); };
+	auto c_row = [&](int i, int r, int ln) { return wm0 + U::UM * i + U::crow(r, ln); };
+	auto c_col = [&](int j, int ln) { return wn0 + U::UN * j + U::ccol(ln); };
 
 	// One depth tile from LDS buffer buf: fragments for depth group kk+4 are read while the MFMAs of
 	// group kk run (two register sets), and each element's chain advances one k per MFMA, in order.
 	auto read_frags = [&](const float* As, const float* Bs, int kk, f32x4* af, f32x4* bf) {
 #pragma unroll
 		for (int i = 0; i < I; ++i) {
-			const int row = wm0 + 64 * i + lane;
+			const int row = wm0 + U::UM * i + U::arow(lane);
 			if (!TA) {
 				af[i] = *reinterpret_cast<const f32x4*>(As + row * S::SA + kk);
 			} else {
@@ -242,7 +293,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE)))
 		}
 #pragma unroll
 		for (int j = 0; j < J; ++j) {
-			const int col = wn0 + 32 * j + (lane & 31);
+			const int col = wn0 + U::UN * j + U::bcol(lane);
 			if (TB) {
 				bf[j] = *reinterpret_cast<const f32x4*>(Bs + col * S::SB + kk);
 			} else {
@@ -269,7 +320,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE)))
 				for (int i = 0; i < I; ++i)
 #pragma unroll
 					for (int j = 0; j < J; ++j)
-						acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x1f32(af[cur][i][e], bf[cur][j][e], acc[i][j], 0, 0, 0);
+						acc[i][j] = U::mma(af[cur][i][e], bf[cur][j][e], acc[i][j]);
 			__builtin_amdgcn_sched_barrier(0);
 		}
 	};
@@ -298,7 +349,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE)))
 #pragma unroll
 			for (int j = 0; j < J; ++j)
 #pragma unroll
-				for (int r = 0; r < 32; ++r) {
+				for (int r = 0; r < U::NV; ++r) {
 					const int row = m0 + c_row(i, r, lane_m), col = n0 + c_col(j, lane_m);
 					if (!EDGE || (row < p.m && col < p.n))
 						acc[i][j][r] = p.c[oc + (int64_t)row * p.ldc + col] + acc[i][j][r];
@@ -316,7 +367,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE)))
 #pragma unroll
 			for (int j = 0; j < J; ++j)
 #pragma unroll
-				for (int r = 0; r < 32; ++r) {
+				for (int r = 0; r < U::NV; ++r) {
 					const int row = m0 + c_row(i, r, lane_e), col = n0 + c_col(j, lane_e);
 					if (!EDGE || (row < p.m && col < p.n)) part[(int64_t)row * p.n + col] = acc[i][j][r];
 				}
@@ -329,11 +380,11 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE)))
 	for (int i = 0; i < I; ++i)
 #pragma unroll
 		for (int j = 0; j < J; ++j) {
-			// one 64 x 32 block at a time: bounds the registers the epilogue keeps live
+			// one MFMA unit at a time: bounds the registers the epilogue keeps live
 			__builtin_amdgcn_sched_barrier(0);
 			const int col = n0 + c_col(j, lane_e);
 #pragma unroll
-			for (int r = 0; r < 32; ++r) {
+			for (int r = 0; r < U::NV; ++r) {
 				const int row = m0 + c_row(i, r, lane_e);
 				if (EDGE && (row >= p.m || col >= p.n)) continue;
 				const int64_t off = (int64_t)row * p.ldc + col;
