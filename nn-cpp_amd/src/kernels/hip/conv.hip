@@ -1,6 +1,7 @@
 // conv.hip - convolution kernels around the GEMM, each reproducing nn-cpp's operation order
 // (src/autograd/ops.cpp:119-243 geometry and im2col, 1345-1472 conv2d_impl).
 #include "conv.hpp"
+#include "fastdiv.hpp"
 
 namespace nnh {
 
@@ -102,23 +103,6 @@ __global__ void __launch_bounds__(256) conv_direct_kernel(const float* __restric
 		}
 		y[o] = v;
 	}
-}
-
-// Unsigned division by a runtime constant d as a multiply and a shift (round-up method): exact for every
-// numerator below 2^31.
-struct FastDiv {
-	unsigned d, m, s;
-};
-
-inline FastDiv make_fastdiv(unsigned d) {
-	unsigned s = 0;
-	while ((1ull << s) < d) ++s;
-	const unsigned m = (unsigned)((((1ull << s) - d) << 32) / d + 1);
-	return FastDiv{d, m, s};
-}
-
-__device__ __forceinline__ unsigned fdiv(unsigned q, const FastDiv& f) {
-	return (__umulhi(q, f.m) + q) >> f.s;
 }
 
 // Direct convolution for the common first-layer shape: stride 1, "same" width (kw = 2*PAD + 1, so wo == w),

@@ -5,34 +5,64 @@
 //   m = v_0, then m = (m < v_j) ? v_j : m       (std::max)
 //   p_j = exp(v_j - m) for j < live (live = i + 1 when causal), exactly 0 beyond
 //   sum = ((0 + p_0) + p_1) + ...  in j order;  p_j = p_j / sum
-// The elementwise steps run on every lane; the two order-sensitive steps (the max scan and the sum) run
-// one thread per row over the row held in LDS, so the bits match the reference's serial loops.
+// A block holds up to 64 rows in LDS. Loads and stores are batched 16-byte accesses; the elementwise steps
+// run on every lane. The max is a wave reduction that reproduces std::max's scan exactly (see row_max); the
+// sum, whose rounding depends on its order, runs one lane per row in j order, as the reference's loop does.
 #include "softmax.hpp"
+#include "fastdiv.hpp"
 
 #include <math.h>
 
 namespace nnh {
 
-// The correctly rounded e^x for the softmax's arguments (x <= 0 or NaN): exp in double, rounded once to float.
-// An exhaustive scan of every float in [-104.5, 0] (tests/golden/exp_scan.c, quad precision) finds exactly
-// four inputs whose e^x lies within 8 double ulps of a float rounding midpoint, where the last bits of a
-// double exp could decide the rounding; their correctly rounded results are given directly. Every other
-// input lies farther than 8 ulps from a midpoint, so any double exp accurate to a few ulps rounds right.
-// (nn-cpp's std::exp is glibc's expf, which is within 0.502 ulp and differs from this on 97052 of those
-// 1.12e9 inputs, always by one ulp; that is the only arithmetic difference of the attention path.)
-__device__ __forceinline__ float exp_ref(float x) {
-	switch (__float_as_uint(x)) {
-		case 0xb3000000u: return __uint_as_float(0x3f800000u);  // -0x1p-25       -> 1
-		case 0xbae0e25cu: return __uint_as_float(0x3f7f8fa7u);  // -0x1.c1c4b8p-10 -> 0x1.ff1f4ep-1
-		case 0xbbf0edf1u: return __uint_as_float(0x3f7e1fe9u);  // -0x1.e1dbe2p-8  -> 0x1.fc3fd2p-1
-		case 0xc16912cdu: return __uint_as_float(0x34fd331bu);  // -0x1.d2259ap+3  -> 0x1.fa6636p-22
-		default: return (float)exp((double)x);
+// std::exp(float) in nn-cpp is glibc's expf (ops.cpp:1199). glibc (2.28 and later) implements it with the
+// published algorithm of ARM's optimized-routines (expf by Szabolcs Nagy): e^x = 2^(k/32) 2^(r/32) with
+// k = round(x 32/ln2) and |r| <= 1/2, 2^(k/32) from a 32-entry table, 2^(r/32) from a cubic, all in double, then
+// rounded once to float. x86-64 glibc runs the build of it compiled with FMA, which fuses the reduction steps.
+// This restatement of that algorithm (same constants, same fused steps, same special cases) returns glibc's
+// expf bit for bit on every one of the 2^32 float inputs (tests/golden/expf_glibc_check.c), so the attention
+// path has no arithmetic difference from the reference.
+// kExp2Table[i] = bits of 2^(i/32) rounded to the nearest double, minus i << 47 (tests/golden/expf_table.py).
+__constant__ unsigned long long kExp2Table[32] = {  // copied into LDS by each block
+	0x3ff0000000000000ull, 0x3fefd9b0d3158574ull, 0x3fefb5586cf9890full, 0x3fef9301d0125b51ull,
+	0x3fef72b83c7d517bull, 0x3fef54873168b9aaull, 0x3fef387a6e756238ull, 0x3fef1e9df51fdee1ull,
+	0x3fef06fe0a31b715ull, 0x3feef1a7373aa9cbull, 0x3feedea64c123422ull, 0x3feece086061892dull,
+	0x3feebfdad5362a27ull, 0x3feeb42b569d4f82ull, 0x3feeab07dd485429ull, 0x3feea47eb03a5585ull,
+	0x3feea09e667f3bcdull, 0x3fee9f75e8ec5f74ull, 0x3feea11473eb0187ull, 0x3feea589994cce13ull,
+	0x3feeace5422aa0dbull, 0x3feeb737b0cdc5e5ull, 0x3feec49182a3f090ull, 0x3feed503b23e255dull,
+	0x3feee89f995ad3adull, 0x3feeff76f2fb5e47ull, 0x3fef199bdd85529cull, 0x3fef3720dcef9069ull,
+	0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull,
+};
+
+__device__ __forceinline__ float expf_glibc(float x, const unsigned long long* table) {
+	const unsigned abstop = (__float_as_uint(x) >> 20) & 0x7ffu;
+	if (abstop >= 0x42bu) {  // |x| >= 88, infinity or NaN
+		if (__float_as_uint(x) == 0xff800000u) return 0.0f;
+		if (abstop >= 0x7f8u) return x + x;
+		if (x > 0x1.62e42ep6f) return __builtin_inff();  // e^x overflows
+		if (x < -0x1.9fe368p6f) return 0.0f;             // e^x below half the smallest subnormal
 	}
+	constexpr double kInvLn2N = 0x1.71547652b82fep+0 * 32, kShift = 0x1.8p+52;
+	constexpr double kC0 = 0x1.c6af84b912394p-5 / 32 / 32 / 32, kC1 = 0x1.ebfce50fac4f3p-3 / 32 / 32,
+	                 kC2 = 0x1.62e42ff0c52d6p-1 / 32;
+	const double xd = x;
+	double kd = __builtin_fma(kInvLn2N, xd, kShift);  // k + kShift, rounded to an integer by the addition
+	const unsigned long long ki = (unsigned long long)__double_as_longlong(kd);
+	kd -= kShift;
+	const double r = __builtin_fma(kInvLn2N, xd, -kd);
+	const double s = __longlong_as_double((long long)(table[ki & 31] + (ki << 47)));
+	const double z = __builtin_fma(kC0, r, kC1), r2 = r * r;
+	double y = __builtin_fma(kC2, r, 1.0);
+	y = __builtin_fma(z, r2, y);
+	return (float)(y * s);
 }
 
 namespace {
 
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
 constexpr int kThreads = 256;
+constexpr int kUnroll = 8;  // 16-byte loads each thread keeps in flight
 
 struct RowGeom {
 	int64_t rows;     // total rows
@@ -42,68 +72,208 @@ struct RowGeom {
 	float scale;
 	const float* pad; // {N, Tk} key padding mask (0 marks a padded key) or null
 	int causal;
+	FastDiv fq, fhq;  // division by tq and by heads * tq (rows < 2^31)
 };
 
-__device__ __forceinline__ float masked_value(float s, const RowGeom& g, const float* ph, int64_t i, int j) {
+__device__ __forceinline__ int query_index(const RowGeom& g, int64_t row) {
+	return (int)((unsigned)row - fdiv((unsigned)row, g.fq) * (unsigned)g.tq);
+}
+
+__device__ __forceinline__ const float* pad_row(const RowGeom& g, int64_t row) {
+	return g.pad ? g.pad + (int64_t)fdiv((unsigned)row, g.fhq) * g.tk : nullptr;
+}
+
+__device__ __forceinline__ float masked_value(float s, const RowGeom& g, int64_t row, int j) {
 	float v = s * g.scale;
-	if (ph && ph[j] == 0.0f) v = -1e9f;
-	if (g.causal && j > i) v = -2e9f;
+	if (g.pad && pad_row(g, row)[j] == 0.0f) v = -1e9f;
+	if (g.causal && j > query_index(g, row)) v = -2e9f;
 	return v;
 }
 
-// rb rows per block (dynamic), row stride tk + 1 in LDS (odd: a thread walking its own row and its
-// neighbours walking theirs hit different banks).
-__global__ void __launch_bounds__(kThreads) softmax_rows_kernel(const float* in, float* out, RowGeom g, int rb) {
-	extern __shared__ float sm[];
+__device__ __forceinline__ int live_keys(const RowGeom& g, int64_t row) {
+	return g.causal ? min(g.tk, query_index(g, row) + 1) : g.tk;
+}
+
+// Copies rows r0 .. r0+nr-1 of src (row length tk) into LDS rows of stride ld, applying f(value, row, j).
+// 16-byte loads when vec (tk % 4 == 0, src 16-byte aligned), kUnroll of them in flight per thread.
+template <typename F>
+__device__ __forceinline__ void load_rows(const float* src, float* sm, int64_t r0, int nr, int tk, int ld,
+                                          bool vec, FastDiv per_row, F f) {
 	const int tid = threadIdx.x;
+	if (vec) {
+		const unsigned total = (unsigned)(nr * (tk / 4));
+		const f32x4* s4 = reinterpret_cast<const f32x4*>(src + r0 * tk);
+		for (unsigned base = tid; base < total; base += kThreads * kUnroll) {
+			f32x4 v[kUnroll];
+#pragma unroll
+			for (int u = 0; u < kUnroll; ++u) {
+				const unsigned e = base + u * kThreads;
+				if (e < total) v[u] = s4[e];
+			}
+#pragma unroll
+			for (int u = 0; u < kUnroll; ++u) {
+				const unsigned e = base + u * kThreads;
+				if (e < total) {
+					const unsigned r = fdiv(e, per_row);
+					const int j = (int)(e - r * per_row.d) * 4;
+#pragma unroll
+					for (int c = 0; c < 4; ++c) sm[r * ld + j + c] = f(v[u][c], r0 + r, j + c);
+				}
+			}
+		}
+	} else {
+		const unsigned total = (unsigned)(nr * tk);
+		const float* s1 = src + r0 * tk;
+		for (unsigned base = tid; base < total; base += kThreads * kUnroll) {
+			float v[kUnroll];
+#pragma unroll
+			for (int u = 0; u < kUnroll; ++u) {
+				const unsigned e = base + u * kThreads;
+				if (e < total) v[u] = s1[e];
+			}
+#pragma unroll
+			for (int u = 0; u < kUnroll; ++u) {
+				const unsigned e = base + u * kThreads;
+				if (e < total) {
+					const unsigned r = fdiv(e, per_row);
+					const int j = (int)(e - r * per_row.d);
+					sm[r * ld + j] = f(v[u], r0 + r, j);
+				}
+			}
+		}
+	}
+}
+
+// std::max scan of the reference (m = o_0, then m = (m < o_j) ? o_j : m) over a row: the scan returns NaN when
+// o_0 is NaN (no comparison with NaN is true, so m stays), otherwise the largest non-NaN value (a NaN o_j never
+// replaces m). fmaxf ignores NaN operands, so fmaxf over the row in any order gives that largest value; the
+// kernel keeps four independent chains per lane. The sign of a zero maximum does not matter (v - m and exp see
+// the same value for m = +0 or -0).
+
+// The row softmax, rb rows per block. VEC (tk % 4 == 0, 16-byte aligned rows): LDS rows of stride tk + 4 and
+// 16-byte accesses everywhere (the stride puts the 16-byte reads of lanes walking different rows on different
+// banks); otherwise stride tk + 1 and 4-byte accesses.
+template <bool VEC>
+__global__ void __launch_bounds__(kThreads) softmax_rows_kernel(const float* in, float* out, RowGeom g, int rb,
+                                                                FastDiv per_row) {
+	extern __shared__ float sm[];
+	__shared__ unsigned long long table[32];
+	const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
 	const int64_t r0 = (int64_t)blockIdx.x * rb;
 	const int nr = (int)min<int64_t>(rb, g.rows - r0);
-	const int ld = g.tk + 1;
-	float* rowmax = sm + rb * ld;
-	float* rowsum = rowmax + rb;
-	// A: load, scale and mask
-	for (int e = tid; e < nr * g.tk; e += kThreads) {
-		const int r = e / g.tk, j = e % g.tk;
-		const int64_t row = r0 + r;
-		const int64_t i = row % g.tq;
-		const float* ph = g.pad ? g.pad + (row / ((int64_t)g.heads * g.tq)) * g.tk : nullptr;
-		sm[r * ld + j] = masked_value(in[row * g.tk + j], g, ph, i, j);
-	}
-	__syncthreads();
-	// B: the max scan, one thread per row
-	if (tid < nr) {
-		const float* o = sm + tid * ld;
-		float m = o[0];
-		for (int j = 1; j < g.tk; ++j) {
-			const float v = o[j];
-			m = (m < v) ? v : m;
+	const int ld = VEC ? g.tk + 4 : g.tk + 1;
+	float* rowsum = sm + rb * ld;
+	float* rowmax = rowsum + rb;
+	if (tid < 32) table[tid] = kExp2Table[tid];
+	// A: load (every load issued before the first use), scale and mask
+	if (VEC) {
+		const unsigned total = (unsigned)(nr * (g.tk / 4));
+		const f32x4* s4 = reinterpret_cast<const f32x4*>(in + r0 * g.tk);
+		for (unsigned base = tid; base < total; base += kThreads * 2 * kUnroll) {
+			f32x4 v[2 * kUnroll];
+#pragma unroll
+			for (int u = 0; u < 2 * kUnroll; ++u) {
+				const unsigned e = base + u * kThreads;
+				if (e < total) v[u] = s4[e];
+			}
+#pragma unroll
+			for (int u = 0; u < 2 * kUnroll; ++u) {
+				const unsigned e = base + u * kThreads;
+				if (e < total) {
+					const unsigned r = fdiv(e, per_row);
+					const int j = (int)(e - r * per_row.d) * 4;
+					f32x4 w;
+#pragma unroll
+					for (int c = 0; c < 4; ++c) w[c] = masked_value(v[u][c], g, r0 + r, j + c);
+					*reinterpret_cast<f32x4*>(sm + r * ld + j) = w;
+				}
+			}
 		}
-		rowmax[tid] = m;
+	} else {
+		load_rows(in, sm, r0, nr, g.tk, ld, false, per_row,
+		          [&](float s, int64_t row, int j) { return masked_value(s, g, row, j); });
 	}
 	__syncthreads();
-	// C: exponentials (exact zeros past the causal limit)
-	for (int e = tid; e < nr * g.tk; e += kThreads) {
-		const int r = e / g.tk, j = e % g.tk;
-		const int64_t i = (r0 + r) % g.tq;
-		const int live = g.causal ? (int)min<int64_t>(g.tk, i + 1) : g.tk;
-		float* p = sm + r * ld + j;
-		*p = (j < live) ? exp_ref(*p - rowmax[r]) : 0.0f;
+	// B: the max of each row, one lane per row (rows spread over the four waves)
+	{
+		const int r = lane * 4 + wave;
+		if (r < nr) {
+			const float* o = sm + r * ld;
+			float m0 = __builtin_nanf(""), m1 = m0, m2 = m0, m3 = m0;
+			int j = 0;
+			if (VEC) {
+				for (; j + 4 <= g.tk; j += 4) {
+					const f32x4 v = *reinterpret_cast<const f32x4*>(o + j);
+					m0 = fmaxf(m0, v[0]);
+					m1 = fmaxf(m1, v[1]);
+					m2 = fmaxf(m2, v[2]);
+					m3 = fmaxf(m3, v[3]);
+				}
+			}
+			for (; j < g.tk; ++j) m0 = fmaxf(m0, o[j]);
+			const float m = fmaxf(fmaxf(m0, m1), fmaxf(m2, m3));
+			const float first = o[0];
+			rowmax[r] = (first != first) ? first : m;  // std::max's scan: see row_max
+		}
 	}
 	__syncthreads();
-	// D: the sum in j order, one thread per row
-	if (tid < nr) {
-		const float* o = sm + tid * ld;
-		const int64_t i = (r0 + tid) % g.tq;
-		const int live = g.causal ? (int)min<int64_t>(g.tk, i + 1) : g.tk;
-		float s = 0.0f;
-		for (int j = 0; j < live; ++j) s += o[j];
-		rowsum[tid] = s;
+	// B': the exponentials, a row per wave at a time (exact zeros past the causal limit)
+	for (int r = wave; r < nr; r += kThreads / 64) {
+		float* o = sm + r * ld;
+		const float m = rowmax[r];
+		const int live = live_keys(g, r0 + r);
+		if (VEC) {
+			for (int j = 4 * lane; j < g.tk; j += 256) {
+				f32x4 v = *reinterpret_cast<const f32x4*>(o + j);
+#pragma unroll
+				for (int c = 0; c < 4; ++c) v[c] = (j + c < live) ? expf_glibc(v[c] - m, table) : 0.0f;
+				*reinterpret_cast<f32x4*>(o + j) = v;
+			}
+		} else {
+			for (int j = lane; j < g.tk; j += 64) o[j] = (j < live) ? expf_glibc(o[j] - m, table) : 0.0f;
+		}
 	}
 	__syncthreads();
-	// E: normalise and store
-	for (int e = tid; e < nr * g.tk; e += kThreads) {
-		const int r = e / g.tk, j = e % g.tk;
-		out[(r0 + r) * g.tk + j] = sm[r * ld + j] / rowsum[r];
+	// C: the sum in j order, one lane per row
+	{
+		const int r = lane * 4 + wave;
+		if (r < nr) {
+			const float* o = sm + r * ld;
+			const int live = live_keys(g, r0 + r);
+			float s = 0.0f;
+			int j = 0;
+			if (VEC) {
+				for (; j + 4 <= live; j += 4) {
+					const f32x4 v = *reinterpret_cast<const f32x4*>(o + j);
+					s += v[0];
+					s += v[1];
+					s += v[2];
+					s += v[3];
+				}
+			}
+			for (; j < live; ++j) s += o[j];
+			rowsum[r] = s;
+		}
+	}
+	__syncthreads();
+	// D: normalise and store
+	if (VEC) {
+		const unsigned total = (unsigned)(nr * (g.tk / 4));
+		f32x4* o4 = reinterpret_cast<f32x4*>(out + r0 * g.tk);
+		for (unsigned e = tid; e < total; e += kThreads) {
+			const unsigned r = fdiv(e, per_row);
+			const int j = (int)(e - r * per_row.d) * 4;
+			const f32x4 v = *reinterpret_cast<const f32x4*>(sm + r * ld + j);
+			const float s = rowsum[r];
+			o4[e] = f32x4{v[0] / s, v[1] / s, v[2] / s, v[3] / s};
+		}
+	} else {
+		const unsigned total = (unsigned)(nr * g.tk);
+		for (unsigned e = tid; e < total; e += kThreads) {
+			const unsigned r = fdiv(e, per_row);
+			const int j = (int)(e - r * per_row.d);
+			out[r0 * g.tk + e] = sm[r * ld + j] / rowsum[r];
+		}
 	}
 }
 
@@ -114,38 +284,43 @@ __global__ void __launch_bounds__(kThreads) softmax_rows_kernel(const float* in,
 // mode 1 (standalone, fresh gradient): same as mode 0
 // mode 2 (standalone, accumulate): out_j += term_j where not masked
 __global__ void __launch_bounds__(kThreads) softmax_backward_rows_kernel(const float* y, const float* gin, float* out,
-                                                                         RowGeom g, int rb, int mode) {
+                                                                         RowGeom g, int rb, int mode, int vec,
+                                                                         FastDiv per_row_vec, FastDiv per_row) {
 	extern __shared__ float sm[];
-	const int tid = threadIdx.x;
+	const int tid = threadIdx.x, wave = tid >> 6;
 	const int64_t r0 = (int64_t)blockIdx.x * rb;
 	const int nr = (int)min<int64_t>(rb, g.rows - r0);
 	const int ld = g.tk + 1;
 	float* sy = sm;
 	float* sg = sm + rb * ld;
 	float* dot = sg + rb * ld;
-	for (int e = tid; e < nr * g.tk; e += kThreads) {
-		const int r = e / g.tk, j = e % g.tk;
-		sy[r * ld + j] = y[(r0 + r) * g.tk + j];
-		sg[r * ld + j] = gin[(r0 + r) * g.tk + j];
-	}
+	const FastDiv pr = vec ? per_row_vec : per_row;
+	load_rows(y, sy, r0, nr, g.tk, ld, vec != 0, pr, [](float v, int64_t, int) { return v; });
+	load_rows(gin, sg, r0, nr, g.tk, ld, vec != 0, pr, [](float v, int64_t, int) { return v; });
 	__syncthreads();
-	if (tid < nr) {
-		float d = 0.0f;
-		for (int j = 0; j < g.tk; ++j) {
-			const float t = sg[tid * ld + j] * sy[tid * ld + j];
-			d = d + t;
+	{
+		const int r = (tid & 63) * 4 + wave;
+		if (r < nr) {
+			const float* a = sy + r * ld;
+			const float* b = sg + r * ld;
+			float d = 0.0f;
+#pragma unroll 8
+			for (int j = 0; j < g.tk; ++j) {
+				const float t = b[j] * a[j];
+				d = d + t;
+			}
+			dot[r] = d;
 		}
-		dot[tid] = d;
 	}
 	__syncthreads();
-	for (int e = tid; e < nr * g.tk; e += kThreads) {
-		const int r = e / g.tk, j = e % g.tk;
+	const unsigned total = (unsigned)(nr * g.tk);
+	for (unsigned e = tid; e < total; e += kThreads) {
+		const unsigned r = fdiv(e, per_row);
+		const int j = (int)(e - r * per_row.d);
 		const int64_t row = r0 + r;
-		const int64_t i = row % g.tq;
-		const float* ph = g.pad ? g.pad + (row / ((int64_t)g.heads * g.tq)) * g.tk : nullptr;
-		const bool masked = (ph && ph[j] == 0.0f) || (g.causal && j > i);
+		const bool masked = (g.pad && pad_row(g, row)[j] == 0.0f) || (g.causal && j > query_index(g, row));
 		const float term = g.scale * (sy[r * ld + j] * (sg[r * ld + j] - dot[r]));
-		float* o = out + row * g.tk + j;
+		float* o = out + r0 * g.tk + e;
 		if (mode == 2) {
 			if (!masked) *o = *o + term;
 		} else {
@@ -157,11 +332,11 @@ __global__ void __launch_bounds__(kThreads) softmax_backward_rows_kernel(const f
 constexpr int kMaxLdsBytes = 160 * 1024;
 
 int rows_per_block(int tk, int arrays) {
-	// arrays row buffers of (tk + 1) floats plus 2 per-row scalars, within the CU's LDS
-	const int per_row = (arrays * (tk + 1) + 2) * 4;
+	// arrays row buffers of (tk + 4) floats plus 2 per-row scalars, within the CU's LDS (less the exp table)
+	const int per_row = (arrays * (tk + 4) + 2) * 4;
 	int rb = 64;
 	while (rb > 1 && rb * per_row > kMaxLdsBytes / 2) rb /= 2;  // leave room for two blocks per CU
-	if (rb * per_row > kMaxLdsBytes) return 0;
+	if (rb * per_row > kMaxLdsBytes - 1024) return 0;
 	return rb;
 }
 
@@ -169,19 +344,37 @@ hipError_t set_lds_limit(const void* fn, int bytes) {
 	return hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
 }
 
+RowGeom row_geom(int64_t rows, int tk, int tq, int heads, float scale, const float* pad, int causal) {
+	const unsigned q = tq > 0 ? (unsigned)tq : 1u, hq = q * (heads > 0 ? (unsigned)heads : 1u);
+	return RowGeom{rows, tk, tq, heads, scale, pad, causal, make_fastdiv(q), make_fastdiv(hq)};
+}
+
+bool vec_ok(int tk, const void* a, const void* b) {
+	return tk % 4 == 0 && reinterpret_cast<uintptr_t>(a) % 16 == 0 && reinterpret_cast<uintptr_t>(b) % 16 == 0;
+}
+
 }  // namespace
 
 hipError_t softmax_rows(const float* in, float* out, int64_t rows, int tk, int tq, int heads, float scale,
                         const float* pad, int causal, hipStream_t s) {
 	if (rows == 0 || tk == 0) return hipSuccess;
-	const int rb = rows_per_block(tk, 1);
+	const int rb = min(32, rows_per_block(tk, 1));  // 32 rows (33 KB at tk = 256): four blocks share a CU
 	if (rb == 0) return hipErrorInvalidValue;
-	RowGeom g{rows, tk, tq, heads, scale, pad, causal};
-	const int lds = (rb * (tk + 1) + 2 * rb) * 4;
-	hipError_t e = set_lds_limit(reinterpret_cast<const void*>(softmax_rows_kernel), lds);
+	if (rows >= ((int64_t)1 << 31) || (int64_t)rb * tk >= ((int64_t)1 << 31)) return hipErrorInvalidValue;
+	const RowGeom g = row_geom(rows, tk, tq, heads, scale, pad, causal);
+	const bool vec = vec_ok(tk, in, out);
+	const int lds = (rb * (tk + (vec ? 4 : 1)) + 2 * rb) * 4;
+	const void* fn = vec ? reinterpret_cast<const void*>(softmax_rows_kernel<true>)
+	                     : reinterpret_cast<const void*>(softmax_rows_kernel<false>);
+	hipError_t e = set_lds_limit(fn, lds);
 	if (e != hipSuccess) return e;
-	hipLaunchKernelGGL(softmax_rows_kernel, dim3((unsigned)((rows + rb - 1) / rb)), dim3(kThreads), lds, s, in, out,
-	                   g, rb);
+	const dim3 grid((unsigned)((rows + rb - 1) / rb));
+	if (vec)
+		hipLaunchKernelGGL(softmax_rows_kernel<true>, grid, dim3(kThreads), lds, s, in, out, g, rb,
+		                   make_fastdiv((unsigned)(tk / 4)));
+	else
+		hipLaunchKernelGGL(softmax_rows_kernel<false>, grid, dim3(kThreads), lds, s, in, out, g, rb,
+		                   make_fastdiv((unsigned)tk));
 	return hipGetLastError();
 }
 
@@ -190,12 +383,15 @@ hipError_t softmax_backward_rows(const float* y, const float* g_in, float* out, 
 	if (rows == 0 || tk == 0) return hipSuccess;
 	const int rb = rows_per_block(tk, 2);
 	if (rb == 0) return hipErrorInvalidValue;
-	RowGeom g{rows, tk, tq, heads, scale, pad, causal};
+	if (rows >= ((int64_t)1 << 31) || (int64_t)rb * tk >= ((int64_t)1 << 31)) return hipErrorInvalidValue;
+	const RowGeom g = row_geom(rows, tk, tq, heads, scale, pad, causal);
 	const int lds = (2 * rb * (tk + 1) + rb) * 4;
 	hipError_t e = set_lds_limit(reinterpret_cast<const void*>(softmax_backward_rows_kernel), lds);
 	if (e != hipSuccess) return e;
+	const int vec = vec_ok(tk, y, g_in) ? 1 : 0;
 	hipLaunchKernelGGL(softmax_backward_rows_kernel, dim3((unsigned)((rows + rb - 1) / rb)), dim3(kThreads), lds, s, y,
-	                   g_in, out, g, rb, mode);
+	                   g_in, out, g, rb, mode, vec, make_fastdiv((unsigned)(tk / 4 > 0 ? tk / 4 : 1)),
+	                   make_fastdiv((unsigned)tk));
 	return hipGetLastError();
 }
 

@@ -369,12 +369,8 @@ void oracle_conv2d_f64(const float* x, size_t N, size_t Cin, size_t H, size_t W,
 
 static inline float std_max(float a, float b) { return (a < b) ? b : a; }  /* std::max(a, b) */
 
-/* exp of the softmax: mode 0 is glibc's expf, what the reference's std::exp(float) calls (ops.cpp:1199);
- * mode 1 is exp computed in double and rounded once, the correctly rounded value. glibc's expf has a
- * maximum error of about 0.502 ulp, so the two differ (by one ulp) on a small fraction of inputs. */
-static int g_exp_mode = 0;
-void oracle_set_exp_mode(int mode) { g_exp_mode = mode; }
-static inline float softmax_exp(float x) { return g_exp_mode ? (float)exp((double)x) : expf(x); }
+/* exp of the softmax: the C library's expf, which is what the reference's std::exp(float) calls (ops.cpp:1199). */
+static inline float softmax_exp(float x) { return expf(x); }
 
 /* masked_softmax_row (ops.cpp:1183-1204). */
 void oracle_masked_softmax_row(const float* row, float* o, size_t Tk, size_t i, const float* ph, int causal,

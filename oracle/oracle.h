@@ -62,7 +62,6 @@ void oracle_conv2d_f64(const float* x, size_t N, size_t Cin, size_t H, size_t W,
                        double* mag);
 
 /* ---- attention (src/autograd/ops.cpp:1169-1343) ---- */
-void oracle_set_exp_mode(int mode);  /* 0: glibc expf (the reference), 1: exp in double rounded once */
 void oracle_masked_softmax_row(const float* row, float* o, size_t Tk, size_t i, const float* ph, int causal,
                                float scale_by);
 void oracle_masked_softmax_row_backward(const float* y, float* g, size_t Tk, size_t i, const float* ph,

@@ -78,11 +78,6 @@ class Oracle:
         L.oracle_scaled_masked_softmax.argtypes = [_f, _sz, _sz, _sz, _sz, C.c_float, _f, C.c_int, _f]
         L.oracle_attention_f64.argtypes = [_f, _f, _f, _sz, _sz, _sz, _sz, _sz, _f, C.c_int, _d, _d]
         L.oracle_mt19937_uniform.argtypes = [C.c_uint, C.c_float, C.c_float, _f, _sz]
-        L.oracle_set_exp_mode.argtypes = [C.c_int]
-
-    def set_exp_mode(self, mode):
-        """0: glibc expf, as nn-cpp's std::exp; 1: exp computed in double and rounded once (correctly rounded)."""
-        self.lib.oracle_set_exp_mode(int(mode))
 
     # -- GEMM --
     def sgemm(self, ta, tb, m, n, k, a, lda, b, ldb, c, ldc, acc, naive=False):

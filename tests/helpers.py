@@ -58,6 +58,24 @@ def bits_equal(x, y):
     return x.shape == y.shape and x.tobytes() == y.tobytes()
 
 
+def assert_same(got, want, what, nan_equal=False):
+    """Bit-for-bit equality of two arrays (with nan_equal, any NaN matches any NaN). The comparison is made
+    before the assert, so a failure reports the first difference instead of a diff of the raw bytes."""
+    assert got.shape == want.shape, (what, got.shape, want.shape)
+    if got.dtype == np.float32 and want.dtype == np.float32:
+        diff = got.view(np.uint32) != want.view(np.uint32)
+        if nan_equal:
+            diff &= ~(np.isnan(got) & np.isnan(want))
+    else:
+        diff = got != want
+    bad = np.nonzero(diff)
+    ok = len(bad[0]) == 0
+    if not ok:
+        idx = tuple(int(v[0]) for v in bad)
+        msg = f"{what}: {len(bad[0])} differ, first at {idx}: got {got[idx]!r} want {want[idx]!r}"
+    assert ok, msg
+
+
 def first_diff(x, y):
     d = np.nonzero(x.view(np.uint32) != y.view(np.uint32))
     if len(d[0]) == 0:

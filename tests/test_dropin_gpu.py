@@ -9,7 +9,7 @@ import os
 import numpy as np
 import pytest
 
-from helpers import first_diff
+from helpers import assert_same
 from nnh import synth
 
 pytestmark = pytest.mark.gpu
@@ -28,7 +28,7 @@ def refs(gpu):
 
 
 def same(got, want, what):
-    assert got.shape == want.shape and got.tobytes() == want.tobytes(), f"{what}: {first_diff(got, want)}"
+    assert_same(got, want, what)
 
 
 def test_sgemm_symbol_is_the_gpu_one(refs):

@@ -7,7 +7,7 @@ against the oracle at full size.
 import numpy as np
 import pytest
 
-from helpers import first_diff
+from helpers import assert_same
 from nnh import synth
 
 pytestmark = pytest.mark.gpu
@@ -25,8 +25,7 @@ def host(t):
 
 
 def same(got, want, what):
-    assert got.shape == want.shape, (what, got.shape, want.shape)
-    assert got.tobytes() == want.tobytes(), f"{what}: {first_diff(got, want)}"
+    assert_same(got, want, what)
 
 
 # ------------------------------------------------------------------ matmul
