@@ -203,6 +203,119 @@ __global__ void __launch_bounds__(256) conv_same_quad_kernel(const float* __rest
 	}
 }
 
+// Index arithmetic of the fast im2col / col2im kernels: 32-bit division by the geometry as multiply-shifts.
+struct ConvDiv {
+	FastDiv hw4;   // quads per column row (hw / 4)
+	FastDiv k;     // rows of a sample's columns (cin * kh * kw)
+	FastDiv khkw;  // kh * kw
+	FastDiv kw, wo, w, h, cin, stride;
+};
+
+// im2col with four consecutive column entries per thread (hw % 4 == 0): one 16-byte store, four cached loads.
+// Same values as im2col_kernel.
+__global__ void __launch_bounds__(256) im2col_quad_kernel(const float* __restrict__ x, float* __restrict__ col,
+                                                          ConvGeom g, ConvDiv d, unsigned total4) {
+	const unsigned e = blockIdx.x * 256 + threadIdx.x;
+	if (e >= total4) return;
+	const unsigned row = fdiv(e, d.hw4);  // n * K + kk
+	const unsigned p0 = (e - row * d.hw4.d) * 4;
+	const unsigned n = fdiv(row, d.k);
+	const unsigned kk = row - n * d.k.d;
+	const unsigned c = fdiv(kk, d.khkw);
+	const unsigned rem = kk - c * d.khkw.d;
+	const unsigned ph = fdiv(rem, d.kw);
+	const int pw = (int)(rem - ph * d.kw.d);
+	const float* xp = x + ((int64_t)n * g.cin + c) * g.h * g.w;
+	f32x4 v;
+#pragma unroll
+	for (int i = 0; i < 4; ++i) {
+		const unsigned p = p0 + i;
+		const unsigned oh = fdiv(p, d.wo);
+		const int ow = (int)(p - oh * d.wo.d);
+		const int ih = (int)oh * g.stride + (int)ph - g.pad, iw = ow * g.stride + pw - g.pad;
+		v[i] = (ih >= 0 && ih < g.h && iw >= 0 && iw < g.w) ? xp[ih * g.w + iw] : 0.0f;
+	}
+	*reinterpret_cast<f32x4*>(col + (int64_t)e * 4) = v;
+}
+
+// col2im_kernel with 32-bit index arithmetic (total < 2^31): the same gather in (ph, pw) order.
+__global__ void __launch_bounds__(256) col2im_fast_kernel(const float* __restrict__ col, float* __restrict__ dx,
+                                                          ConvGeom g, ConvDiv d, unsigned total, int first) {
+	const unsigned e = blockIdx.x * 256 + threadIdx.x;
+	if (e >= total) return;
+	const unsigned t0 = fdiv(e, d.w);
+	const int iw = (int)(e - t0 * d.w.d);
+	const unsigned t1 = fdiv(t0, d.h);
+	const int ih = (int)(t0 - t1 * d.h.d);
+	const unsigned n = fdiv(t1, d.cin);
+	const int c = (int)(t1 - n * d.cin.d);
+	const int hw = g.ho * g.wo;
+	const float* cn = col + (int64_t)n * d.k.d * hw;
+	float acc = first ? 0.0f : dx[e];
+	for (int ph = 0; ph < g.kh; ++ph) {
+		const int th = ih + g.pad - ph;
+		if (th < 0) continue;
+		const unsigned qh = fdiv((unsigned)th, d.stride);
+		if ((int)(qh * d.stride.d) != th || (int)qh >= g.ho) continue;
+		for (int pw = 0; pw < g.kw; ++pw) {
+			const int tw = iw + g.pad - pw;
+			if (tw < 0) continue;
+			const unsigned qw = fdiv((unsigned)tw, d.stride);
+			if ((int)(qw * d.stride.d) != tw || (int)qw >= g.wo) continue;
+			acc = acc + cn[((c * g.kh + ph) * g.kw + pw) * hw + (int)qh * g.wo + (int)qw];
+		}
+	}
+	dx[e] = acc;
+}
+
+// The ReLU's gradient mask on four elements per thread (count % 4 == 0, 16-byte aligned g and out).
+__global__ void __launch_bounds__(256) mask4_kernel(const float* __restrict__ g, const unsigned* __restrict__ alive,
+                                                    float* __restrict__ out, unsigned total4) {
+	const unsigned e = blockIdx.x * 256 + threadIdx.x;
+	if (e >= total4) return;
+	const f32x4 v = reinterpret_cast<const f32x4*>(g)[e];
+	const unsigned a = alive[e];
+	f32x4 o;
+#pragma unroll
+	for (int i = 0; i < 4; ++i) o[i] = ((a >> (8 * i)) & 0xffu) ? v[i] : 0.0f;
+	reinterpret_cast<f32x4*>(out)[e] = o;
+}
+
+// lane_sum (ops.cpp:804-812) with eight lanes per row: lane k of a row's group computes the reference's partial
+// sum a[k] (elements k, k+8, ... of the full groups of eight, in order, from +0); the group's first lane
+// combines them as ((a0 + a1) + (a2 + a3)) + ((a4 + a5) + (a6 + a7)) and adds the tail in order.
+__global__ void __launch_bounds__(256) lane_sum8_kernel(const float* __restrict__ src, unsigned rows, int n,
+                                                        float* __restrict__ dst) {
+	const unsigned gid = blockIdx.x * 256 + threadIdx.x;
+	const unsigned row = gid >> 3;
+	const int k = (int)(gid & 7);
+	const bool valid = row < rows;
+	const float* p = src + (int64_t)(valid ? row : 0) * n;
+	const int full = n & ~7;
+	float a = 0.0f;
+	if (valid) {
+		// eight loads in flight ahead of the dependent additions
+		int i = k;
+		for (; i + 56 < full; i += 64) {
+			float v[8];
+#pragma unroll
+			for (int u = 0; u < 8; ++u) v[u] = p[i + 8 * u];
+#pragma unroll
+			for (int u = 0; u < 8; ++u) a = a + v[u];
+		}
+		for (; i < full; i += 8) a = a + p[i];
+	}
+	const int base = (int)(threadIdx.x & 63) & ~7;
+	float part[8];
+#pragma unroll
+	for (int j = 0; j < 8; ++j) part[j] = __shfl(a, base + j);
+	if (valid && k == 0) {
+		float t = ((part[0] + part[1]) + (part[2] + part[3])) + ((part[4] + part[5]) + (part[6] + part[7]));
+		for (int i = full; i < n; ++i) t = t + p[i];
+		dst[row] = t;
+	}
+}
+
 // The ReLU's gradient mask (ops.cpp:1439-1443): out = alive ? g : 0.
 __global__ void __launch_bounds__(256) mask_kernel(const float* __restrict__ g, const unsigned char* __restrict__ alive,
                                                    float* __restrict__ out, int64_t total) {
@@ -229,17 +342,48 @@ __global__ void __launch_bounds__(256) lane_sum_kernel(const float* __restrict__
 
 }  // namespace
 
+namespace {
+
+ConvDiv conv_div(const ConvGeom& g) {
+	const unsigned hw = (unsigned)(g.ho * g.wo);
+	ConvDiv d;
+	d.hw4 = make_fastdiv(hw / 4 > 0 ? hw / 4 : 1);
+	d.k = make_fastdiv((unsigned)(g.cin * g.kh * g.kw));
+	d.khkw = make_fastdiv((unsigned)(g.kh * g.kw));
+	d.kw = make_fastdiv((unsigned)g.kw);
+	d.wo = make_fastdiv((unsigned)g.wo);
+	d.w = make_fastdiv((unsigned)g.w);
+	d.h = make_fastdiv((unsigned)g.h);
+	d.cin = make_fastdiv((unsigned)g.cin);
+	d.stride = make_fastdiv((unsigned)g.stride);
+	return d;
+}
+
+constexpr int64_t kFast = (int64_t)1 << 31;  // the 32-bit index kernels take fewer elements than this
+
+}  // namespace
+
 hipError_t im2col(const float* x, float* col, const ConvGeom& g, int64_t samples, hipStream_t s) {
-	const int64_t total = samples * g.cin * g.kh * g.kw * (int64_t)g.ho * g.wo;
+	const int64_t hw = (int64_t)g.ho * g.wo;
+	const int64_t total = samples * g.cin * g.kh * g.kw * hw;
 	if (total == 0) return hipSuccess;
-	hipLaunchKernelGGL(im2col_kernel, dim3(blocks_for(total)), dim3(256), 0, s, x, col, g, total);
+	if (hw % 4 == 0 && total < kFast && reinterpret_cast<uintptr_t>(col) % 16 == 0) {
+		const unsigned total4 = (unsigned)(total / 4);
+		hipLaunchKernelGGL(im2col_quad_kernel, dim3(blocks_for(total4)), dim3(256), 0, s, x, col, g, conv_div(g), total4);
+	} else {
+		hipLaunchKernelGGL(im2col_kernel, dim3(blocks_for(total)), dim3(256), 0, s, x, col, g, total);
+	}
 	return hipGetLastError();
 }
 
 hipError_t col2im(const float* col, float* dx, const ConvGeom& g, int64_t samples, int first, hipStream_t s) {
 	const int64_t total = samples * g.cin * (int64_t)g.h * g.w;
 	if (total == 0) return hipSuccess;
-	hipLaunchKernelGGL(col2im_kernel, dim3(blocks_for(total)), dim3(256), 0, s, col, dx, g, total, first);
+	if (total < kFast && samples * g.cin * g.kh * g.kw * (int64_t)g.ho * g.wo < kFast)
+		hipLaunchKernelGGL(col2im_fast_kernel, dim3(blocks_for(total)), dim3(256), 0, s, col, dx, g, conv_div(g),
+		                   (unsigned)total, first);
+	else
+		hipLaunchKernelGGL(col2im_kernel, dim3(blocks_for(total)), dim3(256), 0, s, col, dx, g, total, first);
 	return hipGetLastError();
 }
 
@@ -323,13 +467,23 @@ hipError_t conv_direct(const float* x, const float* w, const float* bias, float*
 
 hipError_t mask_grad(const float* g, const unsigned char* alive, float* out, int64_t total, hipStream_t s) {
 	if (total == 0) return hipSuccess;
-	hipLaunchKernelGGL(mask_kernel, dim3(blocks_for(total)), dim3(256), 0, s, g, alive, out, total);
+	if (total % 4 == 0 && total < kFast && reinterpret_cast<uintptr_t>(g) % 16 == 0 &&
+	    reinterpret_cast<uintptr_t>(out) % 16 == 0 && reinterpret_cast<uintptr_t>(alive) % 4 == 0) {
+		const unsigned total4 = (unsigned)(total / 4);
+		hipLaunchKernelGGL(mask4_kernel, dim3(blocks_for(total4)), dim3(256), 0, s, g,
+		                   reinterpret_cast<const unsigned*>(alive), out, total4);
+	} else {
+		hipLaunchKernelGGL(mask_kernel, dim3(blocks_for(total)), dim3(256), 0, s, g, alive, out, total);
+	}
 	return hipGetLastError();
 }
 
 hipError_t lane_sums(const float* src, int64_t rows, int64_t n, float* dst, hipStream_t s) {
 	if (rows == 0) return hipSuccess;
-	hipLaunchKernelGGL(lane_sum_kernel, dim3(blocks_for(rows)), dim3(256), 0, s, src, rows, n, dst);
+	if (rows * 8 < kFast && n < kFast)
+		hipLaunchKernelGGL(lane_sum8_kernel, dim3(blocks_for(rows * 8)), dim3(256), 0, s, src, (unsigned)rows, (int)n, dst);
+	else
+		hipLaunchKernelGGL(lane_sum_kernel, dim3(blocks_for(rows)), dim3(256), 0, s, src, rows, n, dst);
 	return hipGetLastError();
 }
 

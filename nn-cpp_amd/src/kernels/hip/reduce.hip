@@ -6,6 +6,8 @@ namespace nnh {
 
 namespace {
 
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
 // Tensor::sum(0) of a {rows, inner} tensor (src/tensor.cpp:422-456): a zero-filled output, then the
 // rows added in order. One thread per column: consecutive threads read consecutive addresses.
 // combine: 0 store s, 1 store s + 0.0f (first gradient write, ops.cpp:64-73), 2 dst += s.
@@ -28,6 +30,71 @@ __global__ void __launch_bounds__(256) sum_rows_kernel(const float* __restrict__
 	if (combine == 0) dst[j] = s;
 	else if (combine == 1) dst[j] = s + 0.0f;
 	else dst[j] = dst[j] + s;
+}
+
+// The same sum with the rows staged through LDS: a block owns 64 columns; for each chunk of up to kChunk rows
+// all 256 threads load the chunk at once (16-byte loads when the rows allow), then one lane per column adds
+// the chunk's rows in order onto its running sum. Same bits as sum_rows_kernel, without one memory latency
+// per few rows.
+constexpr int kSumCols = 64, kChunk = 128;
+
+__global__ void __launch_bounds__(256) sum_rows_lds_kernel(const float* __restrict__ src, int rows, int inner,
+                                                           float* __restrict__ dst, int combine, int vec) {
+	__shared__ __align__(16) float tile[kChunk][kSumCols];
+	const int tid = threadIdx.x;
+	const int c0 = blockIdx.x * kSumCols;
+	const int ncol = min(kSumCols, inner - c0);
+	float s = 0.0f;
+	for (int a0 = 0; a0 < rows; a0 += kChunk) {
+		const int nr = min(kChunk, rows - a0);
+		if (vec) {  // 16 float4 per row of the tile; inner % 4 == 0, so a column block is whole float4s
+			constexpr int kPer = kChunk * kSumCols / 4 / 256;
+			f32x4 v[kPer];
+#pragma unroll
+			for (int u = 0; u < kPer; ++u) {
+				const int idx = tid + 256 * u, r = idx >> 4, q = (idx & 15) * 4;
+				if (r < nr && q < ncol) v[u] = *reinterpret_cast<const f32x4*>(src + (int64_t)(a0 + r) * inner + c0 + q);
+			}
+#pragma unroll
+			for (int u = 0; u < kPer; ++u) {
+				const int idx = tid + 256 * u, r = idx >> 4, q = (idx & 15) * 4;
+				if (r < nr && q < ncol) *reinterpret_cast<f32x4*>(&tile[r][q]) = v[u];
+			}
+		} else {
+			constexpr int kPer = kChunk * kSumCols / 256;
+			float v[kPer];
+#pragma unroll
+			for (int u = 0; u < kPer; ++u) {
+				const int idx = tid + 256 * u, r = idx >> 6, c = idx & 63;
+				if (r < nr && c < ncol) v[u] = src[(int64_t)(a0 + r) * inner + c0 + c];
+			}
+#pragma unroll
+			for (int u = 0; u < kPer; ++u) {
+				const int idx = tid + 256 * u, r = idx >> 6, c = idx & 63;
+				if (r < nr && c < ncol) tile[r][c] = v[u];
+			}
+		}
+		__syncthreads();
+		if (tid < ncol) {
+			// sixteen LDS reads in flight ahead of the dependent additions
+			int r = 0;
+			for (; r + 16 <= nr; r += 16) {
+				float v[16];
+#pragma unroll
+				for (int u = 0; u < 16; ++u) v[u] = tile[r + u][tid];
+#pragma unroll
+				for (int u = 0; u < 16; ++u) s = s + v[u];
+			}
+			for (; r < nr; ++r) s = s + tile[r][tid];
+		}
+		__syncthreads();
+	}
+	if (tid < ncol) {
+		float* d = dst + c0 + tid;
+		if (combine == 0) *d = s;
+		else if (combine == 1) *d = s + 0.0f;
+		else *d = *d + s;
+	}
 }
 
 // relu forward (ops.cpp:775-782): y = x > 0 ? x : 0
@@ -57,7 +124,13 @@ inline unsigned blocks_for(int64_t n) { return (unsigned)((n + 255) / 256); }
 
 hipError_t sum_rows(const float* src, int64_t rows, int64_t inner, float* dst, int combine, hipStream_t s) {
 	if (inner == 0) return hipSuccess;
-	hipLaunchKernelGGL(sum_rows_kernel, dim3(blocks_for(inner)), dim3(256), 0, s, src, rows, inner, dst, combine);
+	if (rows < ((int64_t)1 << 31) && inner < ((int64_t)1 << 31)) {
+		const int vec = (inner % 4 == 0 && reinterpret_cast<uintptr_t>(src) % 16 == 0) ? 1 : 0;
+		hipLaunchKernelGGL(sum_rows_lds_kernel, dim3((unsigned)((inner + kSumCols - 1) / kSumCols)), dim3(256), 0, s,
+		                   src, (int)rows, (int)inner, dst, combine, vec);
+	} else {
+		hipLaunchKernelGGL(sum_rows_kernel, dim3(blocks_for(inner)), dim3(256), 0, s, src, rows, inner, dst, combine);
+	}
 	return hipGetLastError();
 }
 

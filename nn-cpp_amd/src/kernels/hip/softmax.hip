@@ -202,6 +202,18 @@ __global__ void __launch_bounds__(kThreads) softmax_rows_kernel(const float* in,
 			float m0 = __builtin_nanf(""), m1 = m0, m2 = m0, m3 = m0;
 			int j = 0;
 			if (VEC) {
+				for (; j + 16 <= g.tk; j += 16) {  // four 16-byte reads in flight
+					f32x4 v[4];
+#pragma unroll
+					for (int u = 0; u < 4; ++u) v[u] = *reinterpret_cast<const f32x4*>(o + j + 4 * u);
+#pragma unroll
+					for (int u = 0; u < 4; ++u) {
+						m0 = fmaxf(m0, v[u][0]);
+						m1 = fmaxf(m1, v[u][1]);
+						m2 = fmaxf(m2, v[u][2]);
+						m3 = fmaxf(m3, v[u][3]);
+					}
+				}
 				for (; j + 4 <= g.tk; j += 4) {
 					const f32x4 v = *reinterpret_cast<const f32x4*>(o + j);
 					m0 = fmaxf(m0, v[0]);
@@ -243,6 +255,18 @@ __global__ void __launch_bounds__(kThreads) softmax_rows_kernel(const float* in,
 			float s = 0.0f;
 			int j = 0;
 			if (VEC) {
+				for (; j + 16 <= live; j += 16) {  // four 16-byte reads in flight, additions in order
+					f32x4 v[4];
+#pragma unroll
+					for (int u = 0; u < 4; ++u) v[u] = *reinterpret_cast<const f32x4*>(o + j + 4 * u);
+#pragma unroll
+					for (int u = 0; u < 4; ++u) {
+						s += v[u][0];
+						s += v[u][1];
+						s += v[u][2];
+						s += v[u][3];
+					}
+				}
 				for (; j + 4 <= live; j += 4) {
 					const f32x4 v = *reinterpret_cast<const f32x4*>(o + j);
 					s += v[0];
@@ -283,29 +307,83 @@ __global__ void __launch_bounds__(kThreads) softmax_rows_kernel(const float* in,
 // mode 0 (attention): out_j = masked ? 0 : term_j + 0.0f
 // mode 1 (standalone, fresh gradient): same as mode 0
 // mode 2 (standalone, accumulate): out_j += term_j where not masked
+template <bool VEC>
 __global__ void __launch_bounds__(kThreads) softmax_backward_rows_kernel(const float* y, const float* gin, float* out,
-                                                                         RowGeom g, int rb, int mode, int vec,
-                                                                         FastDiv per_row_vec, FastDiv per_row) {
+                                                                         RowGeom g, int rb, int mode, FastDiv per_row) {
 	extern __shared__ float sm[];
-	const int tid = threadIdx.x, wave = tid >> 6;
+	const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
 	const int64_t r0 = (int64_t)blockIdx.x * rb;
 	const int nr = (int)min<int64_t>(rb, g.rows - r0);
-	const int ld = g.tk + 1;
+	const int ld = VEC ? g.tk + 4 : g.tk + 1;
 	float* sy = sm;
 	float* sg = sm + rb * ld;
 	float* dot = sg + rb * ld;
-	const FastDiv pr = vec ? per_row_vec : per_row;
-	load_rows(y, sy, r0, nr, g.tk, ld, vec != 0, pr, [](float v, int64_t, int) { return v; });
-	load_rows(gin, sg, r0, nr, g.tk, ld, vec != 0, pr, [](float v, int64_t, int) { return v; });
+	// A: both rows into LDS, every load issued before the first use
+	if (VEC) {
+		const unsigned total = (unsigned)(nr * (g.tk / 4));
+		const f32x4* y4 = reinterpret_cast<const f32x4*>(y + r0 * g.tk);
+		const f32x4* g4 = reinterpret_cast<const f32x4*>(gin + r0 * g.tk);
+		for (unsigned base = tid; base < total; base += kThreads * kUnroll) {
+			f32x4 vy[kUnroll], vg[kUnroll];
+#pragma unroll
+			for (int u = 0; u < kUnroll; ++u) {
+				const unsigned e = base + u * kThreads;
+				if (e < total) {
+					vy[u] = y4[e];
+					vg[u] = g4[e];
+				}
+			}
+#pragma unroll
+			for (int u = 0; u < kUnroll; ++u) {
+				const unsigned e = base + u * kThreads;
+				if (e < total) {
+					const unsigned r = fdiv(e, per_row);
+					const int j = (int)(e - r * per_row.d) * 4;
+					*reinterpret_cast<f32x4*>(sy + r * ld + j) = vy[u];
+					*reinterpret_cast<f32x4*>(sg + r * ld + j) = vg[u];
+				}
+			}
+		}
+	} else {
+		load_rows(y, sy, r0, nr, g.tk, ld, false, per_row, [](float v, int64_t, int) { return v; });
+		load_rows(gin, sg, r0, nr, g.tk, ld, false, per_row, [](float v, int64_t, int) { return v; });
+	}
 	__syncthreads();
+	// the dot product in j order (product rounded, then added), one lane per row
 	{
-		const int r = (tid & 63) * 4 + wave;
+		const int r = lane * 4 + wave;
 		if (r < nr) {
 			const float* a = sy + r * ld;
 			const float* b = sg + r * ld;
 			float d = 0.0f;
-#pragma unroll 8
-			for (int j = 0; j < g.tk; ++j) {
+			int j = 0;
+			if (VEC) {
+				for (; j + 16 <= g.tk; j += 16) {  // eight 16-byte reads in flight, additions in order
+					f32x4 va[4], vb[4];
+#pragma unroll
+					for (int u = 0; u < 4; ++u) {
+						va[u] = *reinterpret_cast<const f32x4*>(a + j + 4 * u);
+						vb[u] = *reinterpret_cast<const f32x4*>(b + j + 4 * u);
+					}
+#pragma unroll
+					for (int u = 0; u < 4; ++u)
+#pragma unroll
+						for (int c = 0; c < 4; ++c) {
+							const float t = vb[u][c] * va[u][c];
+							d = d + t;
+						}
+				}
+				for (; j + 4 <= g.tk; j += 4) {
+					const f32x4 va = *reinterpret_cast<const f32x4*>(a + j);
+					const f32x4 vb = *reinterpret_cast<const f32x4*>(b + j);
+#pragma unroll
+					for (int c = 0; c < 4; ++c) {
+						const float t = vb[c] * va[c];
+						d = d + t;
+					}
+				}
+			}
+			for (; j < g.tk; ++j) {
 				const float t = b[j] * a[j];
 				d = d + t;
 			}
@@ -313,18 +391,33 @@ __global__ void __launch_bounds__(kThreads) softmax_backward_rows_kernel(const f
 		}
 	}
 	__syncthreads();
-	const unsigned total = (unsigned)(nr * g.tk);
-	for (unsigned e = tid; e < total; e += kThreads) {
-		const unsigned r = fdiv(e, per_row);
-		const int j = (int)(e - r * per_row.d);
+	// the terms, a row per wave at a time
+	for (int r = wave; r < nr; r += kThreads / 64) {
 		const int64_t row = r0 + r;
-		const bool masked = (g.pad && pad_row(g, row)[j] == 0.0f) || (g.causal && j > query_index(g, row));
-		const float term = g.scale * (sy[r * ld + j] * (sg[r * ld + j] - dot[r]));
-		float* o = out + r0 * g.tk + e;
-		if (mode == 2) {
-			if (!masked) *o = *o + term;
+		const float* ph = g.pad ? pad_row(g, row) : nullptr;
+		const int i = g.causal ? query_index(g, row) : 0;
+		const float dr = dot[r];
+		float* o = out + row * g.tk;
+		auto term = [&](int j, float yv, float gv, float old) {
+			const bool masked = (ph && ph[j] == 0.0f) || (g.causal && j > i);
+			const float t = g.scale * (yv * (gv - dr));
+			if (mode == 2) return masked ? old : old + t;
+			return masked ? 0.0f : t + 0.0f;
+		};
+		if (VEC) {
+			for (int j = 4 * lane; j < g.tk; j += 256) {
+				const f32x4 vy = *reinterpret_cast<const f32x4*>(sy + r * ld + j);
+				const f32x4 vg = *reinterpret_cast<const f32x4*>(sg + r * ld + j);
+				f32x4 old = {0.0f, 0.0f, 0.0f, 0.0f};
+				if (mode == 2) old = *reinterpret_cast<const f32x4*>(o + j);
+				f32x4 res;
+#pragma unroll
+				for (int c = 0; c < 4; ++c) res[c] = term(j + c, vy[c], vg[c], old[c]);
+				*reinterpret_cast<f32x4*>(o + j) = res;
+			}
 		} else {
-			*o = masked ? 0.0f : term + 0.0f;
+			for (int j = lane; j < g.tk; j += 64)
+				o[j] = term(j, sy[r * ld + j], sg[r * ld + j], mode == 2 ? o[j] : 0.0f);
 		}
 	}
 }
@@ -381,17 +474,23 @@ hipError_t softmax_rows(const float* in, float* out, int64_t rows, int tk, int t
 hipError_t softmax_backward_rows(const float* y, const float* g_in, float* out, int64_t rows, int tk, int tq,
                                  int heads, float scale, const float* pad, int causal, int mode, hipStream_t s) {
 	if (rows == 0 || tk == 0) return hipSuccess;
-	const int rb = rows_per_block(tk, 2);
+	const int rb = min(16, rows_per_block(tk, 2));  // 16 rows (33 KB at tk = 256): four blocks share a CU
 	if (rb == 0) return hipErrorInvalidValue;
 	if (rows >= ((int64_t)1 << 31) || (int64_t)rb * tk >= ((int64_t)1 << 31)) return hipErrorInvalidValue;
 	const RowGeom g = row_geom(rows, tk, tq, heads, scale, pad, causal);
-	const int lds = (2 * rb * (tk + 1) + rb) * 4;
-	hipError_t e = set_lds_limit(reinterpret_cast<const void*>(softmax_backward_rows_kernel), lds);
+	const bool vec = vec_ok(tk, y, g_in) && reinterpret_cast<uintptr_t>(out) % 16 == 0;
+	const int lds = (2 * rb * (tk + (vec ? 4 : 1)) + rb) * 4;
+	const void* fn = vec ? reinterpret_cast<const void*>(softmax_backward_rows_kernel<true>)
+	                     : reinterpret_cast<const void*>(softmax_backward_rows_kernel<false>);
+	hipError_t e = set_lds_limit(fn, lds);
 	if (e != hipSuccess) return e;
-	const int vec = vec_ok(tk, y, g_in) ? 1 : 0;
-	hipLaunchKernelGGL(softmax_backward_rows_kernel, dim3((unsigned)((rows + rb - 1) / rb)), dim3(kThreads), lds, s, y,
-	                   g_in, out, g, rb, mode, vec, make_fastdiv((unsigned)(tk / 4 > 0 ? tk / 4 : 1)),
-	                   make_fastdiv((unsigned)tk));
+	const dim3 grid((unsigned)((rows + rb - 1) / rb));
+	if (vec)
+		hipLaunchKernelGGL(softmax_backward_rows_kernel<true>, grid, dim3(kThreads), lds, s, y, g_in, out, g, rb, mode,
+		                   make_fastdiv((unsigned)(tk / 4)));
+	else
+		hipLaunchKernelGGL(softmax_backward_rows_kernel<false>, grid, dim3(kThreads), lds, s, y, g_in, out, g, rb, mode,
+		                   make_fastdiv((unsigned)tk));
 	return hipGetLastError();
 }
 

@@ -158,3 +158,29 @@ def test_baseline_config2_mlp(gpu, oracle):
         for t, wv, key in zip((dx, dw, db), want, ("dx", "dw", "db")):
             same(host(t), wv, f"layer {li} {key}")
         acts.append(y_ref)
+
+
+def test_tensor_sum0_every_shape_and_combine(gpu, oracle):
+    """Tensor::sum(0) (src/tensor.cpp:422-456): rows added in order from +0. Row counts around the kernel's
+    128-row chunks, widths that are not multiples of 4 or of its 64-column blocks, an unaligned source (the 4-byte
+    path), and the three combines: store, store s + 0.0f (a fresh gradient: -0 becomes +0), add."""
+    import torch
+
+    import nnh
+    seed = 900
+    for rows in (0, 1, 7, 127, 128, 129, 300):
+        for inner in (1, 3, 10, 64, 65, 130, 512):
+            src = synth.mt19937_uniform(seed, max(rows * inner, 1), -1.0, 1.0)[: rows * inner].reshape(rows, inner)
+            seed += 1
+            if rows:
+                src[0, 0] = -0.0  # a one-row column sum of -0 is -0 stored, +0 with combine 1
+            base = synth.mt19937_uniform(seed, inner, -1.0, 1.0)
+            s = oracle.sum_axis0(src) if rows else np.zeros(inner, np.float32)
+            for offset in (0, 1):
+                buf = torch.zeros(rows * inner + offset + 1, device="cuda")
+                view = buf[offset: offset + rows * inner]
+                view.copy_(torch.from_numpy(src.reshape(-1)))
+                for combine, want in ((0, s), (1, s + np.float32(0.0)), (2, base + s)):
+                    dst = torch.from_numpy(base.copy()).cuda()
+                    nnh.tensor_sum0(view.reshape(rows, inner) if rows else view.reshape(0, inner), dst, combine)
+                    same(host(dst), want.astype(np.float32), (rows, inner, offset, combine))
