@@ -88,6 +88,29 @@ def cpu_baseline(a, b, m, n, k, budget_s=15.0, max_runs=400):
     }
 
 
+def floor():
+    """What a single launch costs on this GPU, beside the conv1 figure: an empty one-wave kernel (nnh.bench_delay
+    with no delay), torch fills of conv1's output size (12.85 MB) and of eight times it, and copies of the same
+    sizes, each timed as device_time_ms does. Prints a markdown table."""
+    import torch
+
+    import nnh
+    dev = torch.device("cuda:0")
+    ny = 128 * 32 * 784
+    small, big = torch.empty(ny, device=dev), torch.empty(8 * ny, device=dev)
+    src_small, src_big = torch.ones(ny // 2, device=dev), torch.ones(4 * ny, device=dev)
+    rows = [("empty one-wave kernel (bench_delay 0)", lambda: nnh.bench_delay(0.0), 0),
+            ("fill 12.85 MB (conv1's y)", lambda: small.fill_(1.0), 4 * ny),
+            ("copy 6.4 MB -> 6.4 MB", lambda: small[: ny // 2].copy_(src_small), 4 * ny),
+            ("fill 102.8 MB", lambda: big.fill_(1.0), 32 * ny),
+            ("copy 51.4 MB -> 51.4 MB", lambda: big[: 4 * ny].copy_(src_big), 32 * ny)]
+    print("| launch | us | GB/s | % of 8 TB/s |\n|---|---|---|---|")
+    for name, fn, nbytes in rows:
+        ms = device_time_ms(fn, reps=200)
+        gbps = nbytes / (ms * 1e-3) / 1e9 if nbytes else 0.0
+        print(f"| {name} | {ms * 1e3:.2f} | {gbps:.0f} | {gbps / PEAK_HBM_GBPS * 100:.1f}% |", flush=True)
+
+
 def fused_op_conv1():
     """The metric's fused-op figure: nn::conv2d_relu forward of BASELINE config 3's first layer (x [128,1,28,28]
     U[0,1] seed 2, W [32,1,3,3] Kaiming-normal, zero bias, stride 1, pad 1), the memory-bound direct kernel
@@ -147,9 +170,9 @@ def device_time_ms(fn, reps=50, warmup_s=0.05, stream=None):
         fn()
     issue_per_call = (time.perf_counter() - h0) / 10
     torch.cuda.synchronize()
-    delay_us = min(1.5e6, 1000.0 + 3.0 * reps * issue_per_call * 1e6)
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    for attempt in range(4):
+    for attempt in range(5):
+        delay_us = min(1.5e6, 1000.0 + 3.0 * reps * issue_per_call * 1e6)
         nnh.bench_delay(delay_us, stream)
         e0.record(stream)
         h0 = time.perf_counter()
@@ -160,8 +183,10 @@ def device_time_ms(fn, reps=50, warmup_s=0.05, stream=None):
         torch.cuda.synchronize()
         if issued * 1e6 <= delay_us:
             break
-        # the host fell behind the delay, so the events also timed host gaps: measure again with a longer delay
-        delay_us = min(1.5e6, 2.0 * issued * 1e6 + 1000.0)
+        # The host fell behind the delay (a long queue of launches and stream-ordered allocations behind a held
+        # stream slows the caller down), so the events also timed host gaps: measure again with fewer calls.
+        issue_per_call = issued / reps
+        reps = max(4, reps // 4)
     else:
         log(f"  (host issue {issued * 1e6:.0f} us outlasted the {delay_us:.0f} us delay: the time includes host gaps)")
     return e0.elapsed_time(e1) / reps
@@ -178,7 +203,7 @@ def _cpu_time_ms(fn, budget_s=3.0, max_runs=15):
     return statistics.median(times)
 
 
-def report():
+def report(with_cpu=True):
     import numpy as np
     import torch
 
@@ -186,7 +211,7 @@ def report():
     from nnh import synth
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     from pyoracle import Reference, reference_available
-    ref = Reference() if reference_available() else None
+    ref = Reference() if (with_cpu and reference_available()) else None
     threads = max(1, min(16, len(os.sched_getaffinity(0))))
     if ref:
         ref.set_threads(threads)
@@ -347,6 +372,7 @@ def main():
     ap.add_argument("--no-fused-op", action="store_true", help="skip the conv1 fused conv2d_relu GB/s figure")
     ap.add_argument("--report", action="store_true", help="every BASELINE config as a markdown table (not the "
                     "driver's JSON line)")
+    ap.add_argument("--floor", action="store_true", help="launch-cost floor of this GPU: empty kernel, fills, copies")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="only run 5 device-to-device copies of MIB MiB (calibrates rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     args = ap.parse_args()
@@ -355,7 +381,10 @@ def main():
               "supported", file=sys.stderr)
         sys.exit(2)
     if args.report:
-        report()
+        report(with_cpu=not args.no_cpu_baseline)
+        return
+    if args.floor:
+        floor()
         return
     if args.copy_probe:
         import torch

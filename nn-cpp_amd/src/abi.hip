@@ -36,8 +36,14 @@ bool ranges_overlap(const void* p0, uint64_t bytes0, const void* p1, uint64_t by
 
 // Validates one (batched) GEMM in nn::kernels::sgemm's terms and fills g. Returns NNH_OK or an error.
 int build_gemm(int ta, int tb, size_t m, size_t n, size_t k, const float* a, size_t lda, const float* b, size_t ldb,
-               float* c, size_t ldc, int accumulate, const nnh_batch* batch, const nnh_epilogue* ep, GemmCall& g) {
+               float* c, size_t ldc, int accumulate, const nnh_batch* batch, const nnh_epilogue* ep, GemmCall& g,
+               const ColGather* gather) {
 	g = GemmCall{};
+	if (gather) {
+		if (ta) return fail(NNH_ERR_INVALID, "a gathered B needs an untransposed A");
+		g.gather = true;
+		g.col = *gather;
+	}
 	const size_t kIntMax = INT_MAX;
 	if (m > kIntMax || n > kIntMax || k > kIntMax) return fail(NNH_ERR_INVALID, "m, n and k must be below 2^31");
 	g.ta = ta ? 1 : 0;
@@ -91,9 +97,11 @@ int build_gemm(int ta, int tb, size_t m, size_t n, size_t k, const float* a, siz
 		const size_t a_rows = ta ? k : m, a_cols = ta ? m : k;
 		const size_t b_rows = tb ? n : k, b_cols = tb ? k : n;
 		if (lda < a_cols) return fail(NNH_ERR_INVALID, "lda smaller than the stored row length of A");
-		if (ldb < b_cols) return fail(NNH_ERR_INVALID, "ldb smaller than the stored row length of B");
+		if (!gather && ldb < b_cols) return fail(NNH_ERR_INVALID, "ldb smaller than the stored row length of B");
 		const uint64_t a_extent = (uint64_t)(max_oa + (int64_t)(a_rows - 1) * (int64_t)lda + (int64_t)a_cols) * 4;
-		const uint64_t b_extent = (uint64_t)(max_ob + (int64_t)(b_rows - 1) * (int64_t)ldb + (int64_t)b_cols) * 4;
+		const uint64_t b_extent =
+			gather ? (uint64_t)(max_ob + (int64_t)gather->cin * gather->h * gather->w) * 4
+			       : (uint64_t)(max_ob + (int64_t)(b_rows - 1) * (int64_t)ldb + (int64_t)b_cols) * 4;
 		if (ranges_overlap(c, c_extent, a, a_extent) || ranges_overlap(c, c_extent, b, b_extent))
 			return fail(NNH_ERR_ALIAS, "C overlaps A or B");
 	}

@@ -15,8 +15,11 @@ extern thread_local std::string g_last_error;
 int fail(int code, const std::string& msg);
 int hip_status(hipError_t e, const char* what);
 bool ranges_overlap(const void* p0, uint64_t bytes0, const void* p1, uint64_t bytes1);
+// gather: B is each sample's im2col columns read from the convolution input b (then ldb is unused and B's
+// extent is one sample's input per batch step); null for an ordinary B.
 int build_gemm(int ta, int tb, size_t m, size_t n, size_t k, const float* a, size_t lda, const float* b, size_t ldb,
-               float* c, size_t ldc, int accumulate, const nnh_batch* batch, const nnh_epilogue* ep, GemmCall& g);
+               float* c, size_t ldc, int accumulate, const nnh_batch* batch, const nnh_epilogue* ep, GemmCall& g,
+               const ColGather* gather = nullptr);
 int run_gemm(const GemmCall& g, void* stream, int config);
 
 // How nn::matmul(a, b, trans_a, trans_b) (src/tensor.cpp:571-641) maps onto one (batched) GEMM.

@@ -65,9 +65,11 @@ hipError_t prepare_device() {
 	const Config* cfg = configs();
 	for (int i = 0; i < kNumConfigs; ++i)
 		for (int f = 0; f < 4; ++f)
-			for (int edge = 0; edge < 2; ++edge) {
-				e = hipFuncSetAttribute(reinterpret_cast<const void*>(cfg[i].fn[f][edge]),
-				                        hipFuncAttributeMaxDynamicSharedMemorySize, cfg[i].lds_bytes[f]);
+			for (int edge = 0; edge < 3; ++edge) {
+				if (edge == 2 && f >= 2) continue;  // gather kernels: A not transposed
+				const KernelFn fn = edge < 2 ? cfg[i].fn[f][edge] : cfg[i].gather_fn[f];
+				e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize,
+				                        cfg[i].lds_bytes[f]);
 				if (e != hipSuccess) return e;
 			}
 	// Workspaces (depth-cut partials, im2col columns, attention's dS) come from the device's stream-ordered pool;
@@ -144,12 +146,16 @@ hipError_t gemm_launch(const GemmCall& g, hipStream_t s, int config, float* work
 	p.batch_count = (int)g.batch_count;
 	p.batch = g.batch;
 	p.ep = g.ep;
+	p.col = g.col;
+	if (g.gather && g.ta) return hipErrorInvalidValue;
 	const bool cut = depth_cut(g.m, g.n, g.k);
 	p.pieces = cut ? (int)((g.k + 127) / 128) : 1;
 	p.piece_k = cut ? 128 : (int)std::max<int64_t>(g.k, 1);
-	bool vec_ok = (g.lda % 4 == 0) && (g.ldb % 4 == 0) && (reinterpret_cast<uintptr_t>(g.a) % 16 == 0) &&
-	              (reinterpret_cast<uintptr_t>(g.b) % 16 == 0);
-	for (int d = 0; d < g.batch.ndim; ++d) vec_ok = vec_ok && g.batch.sa[d] % 4 == 0 && g.batch.sb[d] % 4 == 0;
+	// 16-byte operand loads need 16-byte rows and strides (a gathered B is read element by element)
+	bool vec_ok = (g.lda % 4 == 0) && (reinterpret_cast<uintptr_t>(g.a) % 16 == 0) &&
+	              (g.gather || ((g.ldb % 4 == 0) && (reinterpret_cast<uintptr_t>(g.b) % 16 == 0)));
+	for (int d = 0; d < g.batch.ndim; ++d)
+		vec_ok = vec_ok && g.batch.sa[d] % 4 == 0 && (g.gather || g.batch.sb[d] % 4 == 0);
 	p.vec_ok = vec_ok ? 1 : 0;
 	const bool interior = vec_ok && g.m % cf.bm == 0 && g.n % cf.bn == 0 && g.k % cf.bk == 0 && g.k > 0;
 
@@ -169,7 +175,8 @@ hipError_t gemm_launch(const GemmCall& g, hipStream_t s, int config, float* work
 	const int64_t blocks = (int64_t)p.tiles_m * p.tiles_n * p.pieces * p.batch_count;
 	if (blocks > 0x7fffffff) return hipErrorInvalidConfiguration;
 	const int f = (g.ta ? 2 : 0) + (g.tb ? 1 : 0);
-	hipLaunchKernelGGL(cf.fn[f][interior ? 0 : 1], dim3((unsigned)blocks), dim3(256), cf.lds_bytes[f], s, p);
+	const KernelFn fn = g.gather ? cf.gather_fn[g.tb ? 1 : 0] : cf.fn[f][interior ? 0 : 1];
+	hipLaunchKernelGGL(fn, dim3((unsigned)blocks), dim3(256), cf.lds_bytes[f], s, p);
 	e = hipGetLastError();
 	if (e == hipSuccess && cut) {
 		const int64_t total = g.m * g.n * g.batch_count;

@@ -24,6 +24,8 @@ struct GemmCall {
 	BatchDesc batch{};        // ndim 0: a single matrix
 	int64_t batch_count = 1;
 	Epilogue ep{};
+	bool gather = false;      // B is each sample's im2col columns, read from the convolution input b (ColGather)
+	ColGather col{};
 };
 
 // nn-cpp's depth-cut rule (src/kernels/gemm.cpp:453-458): small output, long depth -> 128-deep pieces

@@ -13,6 +13,7 @@ struct Config {
 	int bm, bn, bk;
 	int lds_bytes[4];   // per operand layout (ta * 2 + tb)
 	KernelFn fn[4][2];  // [ta * 2 + tb][edge]
+	KernelFn gather_fn[2];  // B gathered as im2col columns (ColGather), A not transposed: [tb]
 };
 
 template <int BM, int BN, int BK, int WM, int WN, int WPE, int MF = kMf32>
@@ -31,6 +32,8 @@ Config make_config(const char* name) {
 	NNH_SET(true, false)
 	NNH_SET(true, true)
 #undef NNH_SET
+	c.gather_fn[0] = sgemm_tile_kernel<BM, BN, BK, WM, WN, WPE, MF, false, false, true, true>;
+	c.gather_fn[1] = sgemm_tile_kernel<BM, BN, BK, WM, WN, WPE, MF, false, true, true, true>;
 	return c;
 }
 

@@ -34,6 +34,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "fastdiv.hpp"
+
 namespace nnh {
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -101,6 +103,15 @@ struct Epilogue {
 	unsigned char* alive;  // optional, addressed like C
 };
 
+// Implicit im2col (src/autograd/ops.cpp:188-212): B is a sample's column matrix col[k][p] of a convolution,
+// read straight from its input x instead of a materialised buffer. Row k = (c, ph, pw) = (c * kh + ph) * kw + pw,
+// column p = (oh, ow) = oh * wo + ow; the entry is x[c][oh * stride + ph - pad][ow * stride + pw - pad], or 0 in
+// the padding. The batch's B stride steps from one sample's x to the next.
+struct ColGather {
+	int cin, h, w, kh, kw, stride, pad, ho, wo;
+	FastDiv khkw, kw_div, wo_div;
+};
+
 struct GemmArgs {
 	const float* a;
 	const float* b;
@@ -116,6 +127,7 @@ struct GemmArgs {
 	float* partial;
 	BatchDesc batch;
 	Epilogue ep;
+	ColGather col;     // used by the GB (gather) kernels only
 };
 
 __device__ __forceinline__ void batch_offsets(const BatchDesc& d, int64_t bi, int64_t& oa, int64_t& ob,
@@ -172,6 +184,55 @@ __device__ __forceinline__ void store_tile(float* lds, const f32x4* v, int tid) 
 	}
 }
 
+// Loads of a sample's column matrix (rows kk, columns p; zeros outside the matrix or in the convolution's
+// padding) from its input x, in the register layout of load_tile for an R x CC tile: thread tid's slot i covers
+// row (tid + 256 i) / (CC / 4) and the four columns from 4 ((tid + 256 i) % (CC / 4)). Because 256 is a
+// multiple of CC / 4, a thread's columns are the same in every slot and every tile. ColCols holds their
+// (oh, ow) geometry and ColRow a row's (c, ph, pw): the caller computes whichever side of the tile stays
+// fixed over the depth loop once, and the other per tile.
+struct ColCols {
+	int ihb[4], iwb[4];  // oh * stride - pad, ow * stride - pad; ihb = INT_MIN/2 marks a column past the matrix
+};
+struct ColRow {
+	int64_t xoff;  // c * h * w; -1 marks a row past the matrix
+	int ph, pw;
+};
+
+__device__ __forceinline__ ColCols col_cols(const ColGather& cg, int p0, int cols_valid) {
+	ColCols cc;
+#pragma unroll
+	for (int e = 0; e < 4; ++e) {
+		const unsigned pp = (unsigned)(p0 + e);
+		const unsigned oh = fdiv(pp, cg.wo_div);
+		const int ow = (int)(pp - oh * cg.wo_div.d);
+		const bool ok = e < cols_valid;
+		cc.ihb[e] = ok ? (int)oh * cg.stride - cg.pad : -(1 << 30);
+		cc.iwb[e] = ow * cg.stride - cg.pad;
+	}
+	return cc;
+}
+
+__device__ __forceinline__ ColRow col_row(const ColGather& cg, int kk, bool valid) {
+	const unsigned ci = fdiv((unsigned)kk, cg.khkw);
+	const unsigned rem = (unsigned)kk - ci * cg.khkw.d;
+	const unsigned ph = fdiv(rem, cg.kw_div);
+	return ColRow{valid ? (int64_t)ci * cg.h * cg.w : (int64_t)-1, (int)ph, (int)(rem - ph * cg.kw_div.d)};
+}
+
+__device__ __forceinline__ f32x4 col_values(const float* __restrict__ x, const ColGather& cg, const ColRow& r,
+                                            const ColCols& cc) {
+	f32x4 v = {0.0f, 0.0f, 0.0f, 0.0f};
+	if (r.xoff >= 0) {
+		const float* xc = x + r.xoff;
+#pragma unroll
+		for (int e = 0; e < 4; ++e) {
+			const int ih = cc.ihb[e] + r.ph, iw = cc.iwb[e] + r.pw;
+			if (ih >= 0 && ih < cg.h && iw >= 0 && iw < cg.w) v[e] = xc[ih * cg.w + iw];
+		}
+	}
+	return v;
+}
+
 template <int BM, int BN, int BK, int WM, int WN, int MF, bool TA, bool TB>
 struct TileShape {
 	static constexpr int kWavesN = BN / WN;
@@ -200,8 +261,9 @@ __device__ __forceinline__ int xcd_remap(int bid, int total) {
 	return bid;
 }
 
-template <int BM, int BN, int BK, int WM, int WN, int WPE, int MF, bool TA, bool TB, bool EDGE>
+template <int BM, int BN, int BK, int WM, int WN, int WPE, int MF, bool TA, bool TB, bool EDGE, bool GB = false>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE))) sgemm_tile_kernel(const GemmArgs p) {
+	static_assert(!GB || (!TA && EDGE), "the implicit im2col operand is B, loaded with bounds checks");
 	using S = TileShape<BM, BN, BK, WM, WN, MF, TA, TB>;
 	using U = Mfma<MF>;
 	constexpr int I = S::I, J = S::J;
@@ -254,16 +316,47 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE)))
 
 	const bool vec_ok = p.vec_ok != 0;
 	f32x4 ra[S::LA], rb[S::LB];
+	// implicit im2col: the side of each thread's B slots that is fixed over the depth loop (NN: its columns p,
+	// NT: its rows kk), computed once
+	constexpr int kGV = TB ? BK / 4 : BN / 4;  // 16-byte groups per row of the B tile
+	ColCols gcols{};
+	ColRow grows[S::LB];
+	if constexpr (GB) {
+		const int c = (tid % kGV) * 4;
+		if constexpr (!TB) {
+			gcols = col_cols(p.col, n0 + c, p.n - n0 - c);
+		} else {
+#pragma unroll
+			for (int i = 0; i < S::LB; ++i) {
+				const int r = (tid + 256 * i) / kGV;
+				grows[i] = col_row(p.col, n0 + r, r < p.n - n0);
+			}
+		}
+	}
 	auto load = [&](int kt) {
 		const int k0 = k_lo + kt * BK;
 		if (!TA)  // A stored m x k: tile BM rows x BK
 			load_tile<BM, BK, EDGE>(A + (int64_t)m0 * p.lda + k0, p.lda, p.m - m0, k_hi - k0, vec_ok, ra, tid);
 		else      // A stored k x m: tile BK rows x BM
 			load_tile<BK, BM, EDGE>(A + (int64_t)k0 * p.lda + m0, p.lda, k_hi - k0, p.m - m0, vec_ok, ra, tid);
-		if (TB)   // B stored n x k
+		if constexpr (GB) {  // B = a sample's im2col columns, gathered from x
+			const int c = (tid % kGV) * 4;
+			if constexpr (TB) {  // rows kk fixed, columns p = depth
+				const ColCols cc = col_cols(p.col, k0 + c, k_hi - k0 - c);
+#pragma unroll
+				for (int i = 0; i < S::LB; ++i) rb[i] = col_values(B, p.col, grows[i], cc);
+			} else {  // rows kk = depth, columns p fixed
+#pragma unroll
+				for (int i = 0; i < S::LB; ++i) {
+					const int r = (tid + 256 * i) / kGV;
+					rb[i] = col_values(B, p.col, col_row(p.col, k0 + r, r < k_hi - k0), gcols);
+				}
+			}
+		} else if constexpr (TB) {  // B stored n x k
 			load_tile<BN, BK, EDGE>(B + (int64_t)n0 * p.ldb + k0, p.ldb, p.n - n0, k_hi - k0, vec_ok, rb, tid);
-		else      // B stored k x n
+		} else {  // B stored k x n
 			load_tile<BK, BN, EDGE>(B + (int64_t)k0 * p.ldb + n0, p.ldb, k_hi - k0, p.n - n0, vec_ok, rb, tid);
+		}
 	};
 	auto store = [&](int buf) {
 		float* As = lds + buf * S::kStage;

@@ -1,12 +1,16 @@
 // ops_conv.hip - extern "C" entry points of nn::conv2d / nn::conv2d_relu, im2col and col2im (include/nnh.h).
 //
 // Forward (src/autograd/ops.cpp:1345-1410): a short depth (K = Cin*kh*kw <= kDirectMaxK, a network's first
-// layer) runs as a direct convolution fused with bias/ReLU, memory-bound; a longer depth is im2col into a
-// workspace and one batched MFMA GEMM W[Cout x K] col_n[K x hw] over all samples with the bias/ReLU/alive
-// epilogue. Both give each output the reference's fma chain over k = (c, ph, pw) in order.
+// layer) runs as a direct convolution fused with bias/ReLU, memory-bound; a longer depth is one batched MFMA
+// GEMM W[Cout x K] col_n[K x hw] over all samples with the bias/ReLU/alive epilogue, whose B tiles are gathered
+// from x (implicit im2col: the column matrix is never stored). Both give each output the reference's fma
+// chain over k = (c, ph, pw) in order.
 // Backward (ops.cpp:1418-1463): g masked by alive; db = per-sample lane_sum, then summed in sample order;
-// dW_n = g_n col_n^T (batched sgemm F,T), summed in sample order; dcol_n = W^T g_n (batched sgemm T,F), then
-// col2im in gather form into a zero-filled (fresh) or existing dx.
+// dW_n = g_n col_n^T (batched sgemm F,T, col_n gathered from x), summed in sample order; dcol_n = W^T g_n
+// (batched sgemm T,F into a workspace), then col2im in gather form into a zero-filled (fresh) or existing dx.
+// A fresh dW or db is stored as the sum s, where the reference adds s to a zero-filled gradient (0 + s): the
+// two agree because every such sum starts at +0 (fma chains, lane sums and Tensor::sum(0) alike) and so is
+// never -0.
 #include <hip/hip_runtime.h>
 
 #include <vector>
@@ -41,7 +45,26 @@ int conv_geometry(size_t N, size_t Cin, size_t H, size_t W, size_t Cout, size_t 
 	g.pad = padding;
 	g.ho = (int)((H + 2 * (size_t)padding - kh) / (size_t)stride + 1);  // ops.cpp:135-139
 	g.wo = (int)((W + 2 * (size_t)padding - kw) / (size_t)stride + 1);
+	if (Cin * H * W >= ((size_t)1 << 31) || (size_t)g.ho * g.wo >= ((size_t)1 << 31) || Cin * kh * kw >= ((size_t)1 << 31))
+		return fail(NNH_ERR_INVALID, "conv2d: a sample is too large");
 	return NNH_OK;
+}
+
+ColGather col_gather(const ConvGeom& g) {
+	ColGather c;
+	c.cin = g.cin;
+	c.h = g.h;
+	c.w = g.w;
+	c.kh = g.kh;
+	c.kw = g.kw;
+	c.stride = g.stride;
+	c.pad = g.pad;
+	c.ho = g.ho;
+	c.wo = g.wo;
+	c.khkw = make_fastdiv((unsigned)(g.kh * g.kw));
+	c.kw_div = make_fastdiv((unsigned)g.kw);
+	c.wo_div = make_fastdiv((unsigned)g.wo);
+	return c;
 }
 
 struct Workspace {
@@ -87,25 +110,19 @@ int nnh_conv2d_forward(const float* x, size_t N, size_t Cin, size_t H, size_t W,
 	unsigned char* al = fuse_relu ? alive : nullptr;
 	if (K <= kDirectMaxK)
 		return hip_status(conv_direct(x, w, bias, y, al, g, (int64_t)N, (int)Cout, fuse_relu ? 1 : 0, s), "conv2d direct");
-	Workspace ws(s);
-	float* col = ws.get<float>(N * K * hw);
-	if (!col) return hip_status(ws.release(), "conv2d workspace");
-	rc = hip_status(im2col(x, col, g, (int64_t)N, s), "im2col");
-	if (rc == NNH_OK) {
-		// Y_n = W col_n (ops.cpp:1395), W shared by every sample
-		nnh_batch b{};
-		b.ndim = 1;
-		b.shape[0] = N;
-		b.stride_a[0] = 0;
-		b.stride_b[0] = (ptrdiff_t)(K * hw);
-		b.stride_c[0] = (ptrdiff_t)(Cout * hw);
-		nnh_epilogue ep{NNH_BIAS_ROW, fuse_relu ? 1 : 0, bias, al};
-		GemmCall call;
-		rc = build_gemm(0, 0, Cout, hw, K, w, K, col, hw, y, hw, 0, &b, &ep, call);
-		if (rc == NNH_OK) rc = run_gemm(call, stream, -1);
-	}
-	const int rc2 = hip_status(ws.release(), "conv2d workspace");
-	return rc != NNH_OK ? rc : rc2;
+	// Y_n = W col_n (ops.cpp:1395), W shared by every sample, col_n gathered from x_n
+	nnh_batch b{};
+	b.ndim = 1;
+	b.shape[0] = N;
+	b.stride_a[0] = 0;
+	b.stride_b[0] = (ptrdiff_t)(Cin * H * W);
+	b.stride_c[0] = (ptrdiff_t)(Cout * hw);
+	nnh_epilogue ep{NNH_BIAS_ROW, fuse_relu ? 1 : 0, bias, al};
+	const ColGather cg = col_gather(g);
+	GemmCall call;
+	rc = build_gemm(0, 0, Cout, hw, K, w, K, x, hw, y, hw, 0, &b, &ep, call, &cg);
+	if (rc != NNH_OK) return rc;
+	return run_gemm(call, stream, -1);
 }
 
 int nnh_conv2d_backward(const float* g, const float* x, const float* w, const unsigned char* alive, size_t N,
@@ -138,28 +155,28 @@ int nnh_conv2d_backward(const float* g, const float* x, const float* w, const un
 		        : hip_status(ws.err, "conv2d workspace");
 		if (rc == NNH_OK) rc = hip_status(sum_rows(gb, (int64_t)N, (int64_t)Cout, db, db_first ? 0 : 2, s), "conv2d db");
 	}
-	float* col = nullptr;
-	if (rc == NNH_OK && (dw || dx)) {
-		col = ws.get<float>(N * K * hw);
-		if (!col) rc = hip_status(ws.err, "conv2d workspace");
-	}
-	if (rc == NNH_OK && dw) {  // ops.cpp:1448-1449, 1462
+	if (rc == NNH_OK && dw) {  // ops.cpp:1448-1449, 1462: dW_n = g_n col_n^T with col_n gathered from x_n
 		float* gw = ws.get<float>(N * Cout * K);
 		if (!gw) rc = hip_status(ws.err, "conv2d workspace");
-		if (rc == NNH_OK) rc = hip_status(im2col(x, col, geo, (int64_t)N, s), "im2col");
 		if (rc == NNH_OK) {
 			nnh_batch b{};
 			b.ndim = 1;
 			b.shape[0] = N;
 			b.stride_a[0] = (ptrdiff_t)(Cout * hw);
-			b.stride_b[0] = (ptrdiff_t)(K * hw);
+			b.stride_b[0] = (ptrdiff_t)(Cin * H * W);
 			b.stride_c[0] = (ptrdiff_t)(Cout * K);
+			const ColGather cg = col_gather(geo);
 			GemmCall call;
-			rc = build_gemm(0, 1, Cout, K, hw, gm, hw, col, hw, gw, K, 0, &b, nullptr, call);
+			rc = build_gemm(0, 1, Cout, K, hw, gm, hw, x, hw, gw, K, 0, &b, nullptr, call, &cg);
 			if (rc == NNH_OK) rc = run_gemm(call, stream, -1);
 		}
 		if (rc == NNH_OK)
 			rc = hip_status(sum_rows(gw, (int64_t)N, (int64_t)(Cout * K), dw, dw_first ? 0 : 2, s), "conv2d dw");
+	}
+	float* col = nullptr;
+	if (rc == NNH_OK && dx) {
+		col = ws.get<float>(N * K * hw);
+		if (!col) rc = hip_status(ws.err, "conv2d workspace");
 	}
 	if (rc == NNH_OK && dx) {  // ops.cpp:1452-1455
 		nnh_batch b{};

@@ -85,10 +85,15 @@ def test_baseline_config3(gpu, oracle, layer):
 
 
 def test_direct_and_gemm_paths_match_the_oracle(gpu, oracle):
-    """K = Cin*kh*kw <= 32 takes the direct kernel, longer depths im2col + GEMM; both are the reference's chain."""
+    """K = Cin*kh*kw <= 32 takes the direct kernel, longer depths one GEMM whose B tiles are gathered from x
+    (implicit im2col); both are the reference's chain. Backward (mask, db, dW with gathered columns, dcol and
+    col2im) on every case; the last case's forward product takes nn-cpp's depth cut (m n <= 2^16, K = 576)."""
+    import torch
+
     import nnh
     for (N, Cin, H, W, Cout, kk, s, p) in ((3, 3, 11, 9, 40, 3, 1, 1), (3, 4, 11, 9, 40, 3, 1, 1),
-                                            (2, 1, 8, 8, 5, 5, 2, 2), (2, 8, 8, 8, 70, 5, 2, 2), (5, 2, 7, 6, 3, 2, 3, 0)):
+                                            (2, 1, 8, 8, 5, 5, 2, 2), (2, 8, 8, 8, 70, 5, 2, 2), (5, 2, 7, 6, 3, 2, 3, 0),
+                                            (2, 64, 8, 8, 64, 3, 1, 1)):
         x = synth.mt19937_uniform(N * 100 + Cin, N * Cin * H * W).reshape(N, Cin, H, W)
         w = synth.mt19937_uniform(Cout + 7, Cout * Cin * kk * kk).reshape(Cout, Cin, kk, kk)
         b = synth.mt19937_uniform(Cout + 8, Cout)
@@ -98,6 +103,12 @@ def test_direct_and_gemm_paths_match_the_oracle(gpu, oracle):
             same(host(y), wy, (N, Cin, Cout, kk, s, p, relu))
             if relu:
                 same(host(alive), wa, "alive")
+        gr = synth.mt19937_uniform(Cout + 9, wy.size).reshape(wy.shape)
+        dx, dw, db = torch.empty(x.shape, device="cuda"), torch.empty(w.shape, device="cuda"), torch.empty(Cout, device="cuda")
+        nnh.conv2d_backward(dev(gr), dev(x), dev(w), alive, s, p, dx, True, dw, True, db, True)
+        wdx, wdw, wdb = oracle.conv2d_backward(gr, x, w, wa, s, p, dx_first=True)
+        for got, want, key in ((dx, wdx, "dx"), (dw, wdw, "dw"), (db, wdb, "db")):
+            same(host(got), want, (key, N, Cin, Cout, kk, s, p))
 
 
 def test_im2col_col2im(gpu, oracle):
