@@ -1,0 +1,335 @@
+// attention.hip - nn::attention's forward (src/autograd/ops.cpp:1226-1261) as one kernel for head width 64.
+//
+// A workgroup owns 64 query rows of one (sample, head) pair and runs the reference's three steps for them
+// with the score rows resident in LDS:
+//   1. S = Q_h K_h^T: each element the fma chain over d = 0..63 from +0 (sgemm F,T, ops.cpp:1256). Wave w
+//      takes keys 64w..64w+63 against the 64 queries as two 32x32x1 MFMA chains computing S^T (the product
+//      fma(k, q, acc) is the reference's fma(q, k, acc)); lane l holds key row 64w + l in registers (the
+//      MFMA's A operand), the queries come from LDS.
+//   2. masked_softmax_row (ops.cpp:1183-1204) over the 64 rows: scale and mask, std::max's scan, glibc's
+//      expf, the sum over live keys in key order, the division; the probabilities go to `probs` (kept for the
+//      backward pass) and stay in LDS.
+//   3. O_h = P V_h: each element the fma chain over the keys j = 0..Tk-1 from +0 (sgemm F,F, ops.cpp:1259),
+//      every key included (a zero probability still meets its V entry). Wave w takes output columns
+//      16w..16w+15 as one 16x16x1 MFMA chain over the 64 rows; P comes from LDS, V from global memory a
+//      chunk of keys ahead.
+// Same bits as the three-launch path (batched GEMM, row softmax, batched GEMM): both sgemm shapes are below
+// nn-cpp's depth cut (k = 64 and k = Tk <= 256), so every element is a single chain.
+// Two workgroups share a CU (about 67 KB of LDS each at Tk = 256), so one's MFMA phases can overlap the other's
+// VALU phases.
+#include "attention.hpp"
+
+#include "gemm_tile.hpp"
+#include "softmax_row.hpp"
+
+namespace nnh {
+
+namespace {
+
+constexpr int kRows = 64;          // query rows per workgroup
+constexpr int kDh = 64;            // head width
+constexpr int kKLd = kDh + 4;      // LDS row stride of the queries (16-byte reads of 16 lanes hit distinct banks)
+constexpr int kMaxKeys = 256;     // four waves of 64 keys
+constexpr int kVChunk = 16;        // keys of V each lane keeps in flight
+
+struct FusedArgs {
+	const float* q;
+	const float* k;
+	const float* v;
+	float* out;
+	float* probs;
+	const float* pad;  // {N, Tk}, 0 marks a padded key; or null
+	int heads, tq, tk, d;
+	int qblocks, total;
+	int causal;
+	float scale;
+	FastDiv quads;     // division by tk / 4
+};
+
+inline int lds_floats_p(int tk) { return kRows * (tk + 4); }
+
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) attention_fused_kernel(const FusedArgs a) {
+	extern __shared__ __align__(16) float sm[];
+	__shared__ unsigned long long table[32];
+	__shared__ float rowmax[kRows], rowsum[kRows];
+	__shared__ double rowinv[kRows];
+	const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+	const int lid = xcd_remap(blockIdx.x, a.total);  // the query blocks of one head share an XCD's L2
+	const int nh = lid / a.qblocks, qb = lid - nh * a.qblocks;
+	const int n = nh / a.heads, h = nh - n * a.heads;
+	const int i0 = qb * kRows, nq = min(kRows, a.tq - i0);
+	const int tk = a.tk, ldp = tk + 4;
+	const float* qp = a.q + ((int64_t)n * a.tq + i0) * a.d + h * kDh;
+	const float* kp = a.k + (int64_t)n * tk * a.d + h * kDh;
+	const float* vp = a.v + (int64_t)n * tk * a.d + h * kDh;
+	const float* padrow = a.pad ? a.pad + (int64_t)n * tk : nullptr;
+	if (tid < 32) table[tid] = kExp2Table[tid];
+
+	// 0. the 64 query rows into LDS (coalesced, stride kKLd; the score rows reuse this LDS later), key row
+	// 64w + lane into registers. Loads are unconditional (indices clamped into range) so that all are in flight
+	// before the first wait; values past the end are never used.
+	const bool keys_here = 64 * wave < tk;
+	f32x4 kv[kDh / 4];
+	if (keys_here) {
+		const float* kr = kp + (int64_t)min(64 * wave + lane, tk - 1) * a.d;
+#pragma unroll
+		for (int u = 0; u < kDh / 4; ++u) kv[u] = *reinterpret_cast<const f32x4*>(kr + 4 * u);
+	}
+	{
+		f32x4 qs[kRows * kDh / 4 / 256];
+#pragma unroll
+		for (int u = 0; u < kRows * kDh / 4 / 256; ++u) {
+			const int row = (tid >> 4) + 16 * u;
+			qs[u] = *reinterpret_cast<const f32x4*>(qp + (int64_t)min(row, nq - 1) * a.d + 4 * (tid & 15));
+		}
+#pragma unroll
+		for (int u = 0; u < kRows * kDh / 4 / 256; ++u)
+			*reinterpret_cast<f32x4*>(sm + ((tid >> 4) + 16 * u) * kKLd + 4 * (tid & 15)) = qs[u];
+	}
+	__syncthreads();
+
+	// 1. S^T for keys 64w + l against queries 32u + (l & 31), u = 0, 1
+	using M32 = Mfma<kMf32>;
+	M32::Acc s0, s1;
+#pragma unroll
+	for (int r = 0; r < M32::NV; ++r) s0[r] = s1[r] = 0.0f;
+	if (keys_here) {
+		const float* qb0 = sm + (lane & 31) * kKLd;
+		const float* qb1 = qb0 + 32 * kKLd;
+#pragma unroll
+		for (int d4 = 0; d4 < kDh / 4; ++d4) {
+			const f32x4 b0 = *reinterpret_cast<const f32x4*>(qb0 + 4 * d4);
+			const f32x4 b1 = *reinterpret_cast<const f32x4*>(qb1 + 4 * d4);
+#pragma unroll
+			for (int c = 0; c < 4; ++c) {
+				s0 = M32::mma(kv[d4][c], b0[c], s0);
+				s1 = M32::mma(kv[d4][c], b1[c], s1);
+			}
+		}
+	}
+	__syncthreads();  // the queries are dead: the score rows take their LDS
+
+	// 2a. scaled and masked scores into LDS rows of stride tk + 4 (ops.cpp:1186-1191). Accumulator registers
+	// 4t .. 4t+3 hold four consecutive keys of one query: one 16-byte store each.
+	f32x4* sm4 = reinterpret_cast<f32x4*>(sm);
+	const int ldp4 = ldp / 4;
+	if (keys_here) {
+		const bool masked = padrow != nullptr || a.causal;
+#pragma unroll
+		for (int t = 0; t < M32::NV / 4; ++t) {
+			const int j = 64 * wave + M32::crow(4 * t, lane);
+#pragma unroll
+			for (int u = 0; u < 2; ++u) {
+				const int row = 32 * u + M32::ccol(lane);
+				f32x4 val;
+#pragma unroll
+				for (int c = 0; c < 4; ++c) val[c] = (u ? s1[4 * t + c] : s0[4 * t + c]) * a.scale;
+				if (masked) {  // uniform
+					const f32x4 pd = padrow ? *reinterpret_cast<const f32x4*>(padrow + min(j, tk - 4)) : f32x4{1, 1, 1, 1};
+#pragma unroll
+					for (int c = 0; c < 4; ++c) {
+						val[c] = pd[c] == 0.0f ? -1e9f : val[c];
+						val[c] = a.causal && j + c > i0 + row ? -2e9f : val[c];
+					}
+				}
+				if (row < nq && j < tk) sm4[row * ldp4 + j / 4] = val;  // tk % 4 == 0: the quad is whole
+			}
+		}
+	}
+	__syncthreads();
+
+	// 2b. the row maxima: std::max's scan is v_0 when v_0 is NaN, else the largest non-NaN value, which fmaxf
+	// gives in any order (a zero maximum's sign cannot change v - m or its exp). Four lanes per row.
+	{
+		const int row = 16 * wave + (lane >> 2), q = lane & 3;
+		float m = __builtin_nanf("");
+		if (row < nq) {
+			const float* o = sm + row * ldp;
+			for (int j = 4 * q; j < tk; j += 16) {
+				const f32x4 x = *reinterpret_cast<const f32x4*>(o + j);
+				m = fmaxf(m, fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])));
+			}
+		}
+		m = fmaxf(m, __shfl_xor(m, 1));
+		m = fmaxf(m, __shfl_xor(m, 2));
+		if (row < nq && q == 0) {
+			const float first = sm[row * ldp];
+			rowmax[row] = first != first ? first : m;
+		}
+	}
+	__syncthreads();
+
+	// 2c. p_j = exp(v_j - m) for the live keys, exact zeros past the causal limit (ops.cpp:1197-1201); kExpQuads
+	// quads per thread at a time so that their table reads and double-precision chains overlap
+	constexpr int kExpQuads = 4;
+	const unsigned quads = (unsigned)(nq * (tk / 4));
+	for (unsigned e0 = tid; e0 < quads; e0 += 256 * kExpQuads) {
+		f32x4 x[kExpQuads];
+		float* o[kExpQuads];
+		int live[kExpQuads], j[kExpQuads];
+		float m[kExpQuads];
+#pragma unroll
+		for (int h2 = 0; h2 < kExpQuads; ++h2) {
+			const unsigned e = min(e0 + 256 * h2, quads - 1);  // a repeated quad is computed, stored once
+			const unsigned row = fdiv(e, a.quads);
+			j[h2] = (int)(e - row * a.quads.d) * 4;
+			o[h2] = sm + row * ldp + j[h2];
+			x[h2] = *reinterpret_cast<const f32x4*>(o[h2]);
+			m[h2] = rowmax[row];
+			live[h2] = a.causal ? min(tk, i0 + (int)row + 1) : tk;
+		}
+		float ex[4 * kExpQuads];
+#pragma unroll
+		for (int h2 = 0; h2 < kExpQuads; ++h2)
+#pragma unroll
+			for (int c = 0; c < 4; ++c) ex[4 * h2 + c] = x[h2][c] - m[h2];
+		expf_glibc_n(ex, table);
+#pragma unroll
+		for (int h2 = 0; h2 < kExpQuads; ++h2) {
+#pragma unroll
+			for (int c = 0; c < 4; ++c) x[h2][c] = j[h2] + c < live[h2] ? ex[4 * h2 + c] : 0.0f;
+			if (h2 == 0 || e0 + 256 * h2 < quads) *reinterpret_cast<f32x4*>(o[h2]) = x[h2];
+		}
+	}
+	__syncthreads();
+
+	// 2d. the sum over the live keys in key order from +0, one lane per row (ops.cpp:1198-1200)
+	{
+		const int row = 16 * wave + lane;
+		if (lane < 16 && row < nq) {
+			const float* o = sm + row * ldp;
+			const int live = a.causal ? min(tk, i0 + row + 1) : tk;
+			float s = 0.0f;
+			int j = 0;
+			for (; j + 16 <= live; j += 16) {
+				f32x4 x[4];
+#pragma unroll
+				for (int u = 0; u < 4; ++u) x[u] = *reinterpret_cast<const f32x4*>(o + j + 4 * u);
+#pragma unroll
+				for (int u = 0; u < 4; ++u) {
+					s += x[u][0];
+					s += x[u][1];
+					s += x[u][2];
+					s += x[u][3];
+				}
+			}
+			for (; j < live; ++j) s += o[j];
+			rowsum[row] = s;
+			rowinv[row] = 1.0 / (double)s;
+		}
+	}
+	__syncthreads();
+
+	// 2e. p_j / sum into probs and back into LDS (ops.cpp:1203)
+	{
+		float* pr = a.probs + ((int64_t)nh * a.tq + i0) * tk;
+		for (unsigned e = tid; e < quads; e += 256) {
+			const unsigned row = fdiv(e, a.quads);
+			const int j = (int)(e - row * a.quads.d) * 4;
+			float* o = sm + row * ldp + j;
+			const f32x4 x = *reinterpret_cast<const f32x4*>(o);
+			float y[4] = {x[0], x[1], x[2], x[3]};
+			div_n_by_row_sum(y, rowsum[row], rowinv[row]);
+			const f32x4 y4 = {y[0], y[1], y[2], y[3]};
+			*reinterpret_cast<f32x4*>(o) = y4;
+			*reinterpret_cast<f32x4*>(pr + (int64_t)row * tk + j) = y4;
+		}
+	}
+	__syncthreads();
+
+	// 3. O columns 16w .. 16w+15 for the 64 rows: the chain over every key in order
+	using M16 = Mfma<kMf16>;
+	M16::Acc o;
+#pragma unroll
+	for (int r = 0; r < M16::NV; ++r) o[r] = 0.0f;
+	{
+		const f32x4* prow4 = sm4 + M16::arow(lane) * ldp4;  // rows past nq hold stale values, never stored
+		const int vlane = 16 * wave + M16::bcol(lane);
+		// V entries of keys j0 .. j0+kVChunk-1 for this lane's column; rows past tk are clamped to the last key
+		// (loaded, never used), so every load is issued unconditionally with a uniform row address.
+		auto load_v = [&](float (&dst)[kVChunk], int j0) {
+#pragma unroll
+			for (int u = 0; u < kVChunk; ++u) dst[u] = (vp + (int64_t)min(j0 + u, tk - 1) * a.d)[vlane];
+		};
+		// P quads of keys j0 .. j0+kVChunk-1 (quads past tk, in a partial chunk, read a stale in-row value)
+		auto load_p = [&](f32x4 (&dst)[kVChunk / 4], int j0) {
+#pragma unroll
+			for (int u4 = 0; u4 < kVChunk / 4; ++u4) dst[u4] = prow4[min(j0 + 4 * u4, tk - 4) / 4];
+		};
+		auto steps = [&](const f32x4 (&p)[kVChunk / 4], const float (&src)[kVChunk], int j0, bool whole) {
+#pragma unroll
+			for (int u4 = 0; u4 < kVChunk / 4; ++u4) {
+				if (whole || j0 + 4 * u4 < tk) {  // tk % 4 == 0: whole quads only, no step past the last key
+#pragma unroll
+					for (int c = 0; c < 4; ++c) o = M16::mma(p[u4][c], src[4 * u4 + c], o);
+				}
+			}
+		};
+		float v0[kVChunk], v1[kVChunk];
+		f32x4 p0[kVChunk / 4], p1[kVChunk / 4];
+		load_v(v0, 0);
+		load_v(v1, kVChunk);
+		load_p(p0, 0);
+		int j0 = 0;
+		for (; j0 + 2 * kVChunk <= tk; j0 += 2 * kVChunk) {  // V two chunks ahead, P one chunk ahead
+			load_p(p1, j0 + kVChunk);
+			steps(p0, v0, j0, true);
+			load_v(v0, j0 + 2 * kVChunk);
+			load_p(p0, j0 + 2 * kVChunk);
+			steps(p1, v1, j0 + kVChunk, true);
+			load_v(v1, j0 + 3 * kVChunk);
+		}
+		if (j0 < tk) {
+			load_p(p1, j0 + kVChunk);
+			steps(p0, v0, j0, false);
+			if (j0 + kVChunk < tk) steps(p1, v1, j0 + kVChunk, false);
+		}
+	}
+	float* op = a.out + ((int64_t)n * a.tq + i0) * a.d + h * kDh + 16 * wave + M16::ccol(lane);
+#pragma unroll
+	for (int r = 0; r < M16::NV; ++r) {
+		const int row = M16::crow(r, lane);
+		if (row < nq) op[(int64_t)row * a.d] = o[r];
+	}
+}
+
+}  // namespace
+
+bool attention_fused_ok(int64_t tq, int64_t tk, int64_t dh, int64_t d, const void* q, const void* k, const void* v,
+                        const void* out, const void* probs, const void* pad) {
+	auto al = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
+	return dh == kDh && tk >= 1 && tk <= kMaxKeys && tk % 4 == 0 && d % 4 == 0 && tq >= 1 && tq < (1 << 24) &&
+	       al(q) && al(k) && al(v) && al(out) && al(probs) && (pad == nullptr || al(pad));
+}
+
+hipError_t attention_fused_forward(const float* q, const float* k, const float* v, int64_t n, int64_t tq, int64_t tk,
+                                   int64_t d, int64_t heads, const float* pad, int causal, float scale, float* out,
+                                   float* probs, hipStream_t s) {
+	const int64_t qblocks = (tq + kRows - 1) / kRows, total = n * heads * qblocks;
+	if (total == 0) return hipSuccess;
+	if (total >= ((int64_t)1 << 31) || n * heads * tq * tk >= ((int64_t)1 << 62)) return hipErrorInvalidValue;
+	FusedArgs a;
+	a.q = q;
+	a.k = k;
+	a.v = v;
+	a.out = out;
+	a.probs = probs;
+	a.pad = pad;
+	a.heads = (int)heads;
+	a.tq = (int)tq;
+	a.tk = (int)tk;
+	a.d = (int)d;
+	a.qblocks = (int)qblocks;
+	a.total = (int)total;
+	a.causal = causal ? 1 : 0;
+	a.scale = scale;
+	a.quads = make_fastdiv((unsigned)(tk / 4));
+	const int lds = 4 * max(kRows * kKLd, lds_floats_p((int)tk));
+	hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(attention_fused_kernel),
+	                                   hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+	if (e != hipSuccess) return e;
+	hipLaunchKernelGGL(attention_fused_kernel, dim3((unsigned)total), dim3(256), lds, s, a);
+	return hipGetLastError();
+}
+
+}  // namespace nnh

@@ -4,58 +4,17 @@
 //   v_j = s_j * scale; padded key -> -1e9; causal j > i -> -2e9
 //   m = v_0, then m = (m < v_j) ? v_j : m       (std::max)
 //   p_j = exp(v_j - m) for j < live (live = i + 1 when causal), exactly 0 beyond
-//   sum = ((0 + p_0) + p_1) + ...  in j order;  p_j = p_j / sum
+//   sum = ((0 + p_0) + p_1) + ...  in j order;  p_j = p_j / sum  (as div_by_row_sum: the same rounding)
 // A block holds up to 64 rows in LDS. Loads and stores are batched 16-byte accesses; the elementwise steps
 // run on every lane. The max is a wave reduction that reproduces std::max's scan exactly (see row_max); the
 // sum, whose rounding depends on its order, runs one lane per row in j order, as the reference's loop does.
 #include "softmax.hpp"
+#include "softmax_row.hpp"
 #include "fastdiv.hpp"
 
 #include <math.h>
 
 namespace nnh {
-
-// std::exp(float) in nn-cpp is glibc's expf (ops.cpp:1199). glibc (2.28 and later) implements it with the
-// published algorithm of ARM's optimized-routines (expf by Szabolcs Nagy): e^x = 2^(k/32) 2^(r/32) with
-// k = round(x 32/ln2) and |r| <= 1/2, 2^(k/32) from a 32-entry table, 2^(r/32) from a cubic, all in double, then
-// rounded once to float. x86-64 glibc runs the build of it compiled with FMA, which fuses the reduction steps.
-// This restatement of that algorithm (same constants, same fused steps, same special cases) returns glibc's
-// expf bit for bit on every one of the 2^32 float inputs (tests/golden/expf_glibc_check.c), so the attention
-// path has no arithmetic difference from the reference.
-// kExp2Table[i] = bits of 2^(i/32) rounded to the nearest double, minus i << 47 (tests/golden/expf_table.py).
-__constant__ unsigned long long kExp2Table[32] = {  // copied into LDS by each block
-	0x3ff0000000000000ull, 0x3fefd9b0d3158574ull, 0x3fefb5586cf9890full, 0x3fef9301d0125b51ull,
-	0x3fef72b83c7d517bull, 0x3fef54873168b9aaull, 0x3fef387a6e756238ull, 0x3fef1e9df51fdee1ull,
-	0x3fef06fe0a31b715ull, 0x3feef1a7373aa9cbull, 0x3feedea64c123422ull, 0x3feece086061892dull,
-	0x3feebfdad5362a27ull, 0x3feeb42b569d4f82ull, 0x3feeab07dd485429ull, 0x3feea47eb03a5585ull,
-	0x3feea09e667f3bcdull, 0x3fee9f75e8ec5f74ull, 0x3feea11473eb0187ull, 0x3feea589994cce13ull,
-	0x3feeace5422aa0dbull, 0x3feeb737b0cdc5e5ull, 0x3feec49182a3f090ull, 0x3feed503b23e255dull,
-	0x3feee89f995ad3adull, 0x3feeff76f2fb5e47ull, 0x3fef199bdd85529cull, 0x3fef3720dcef9069ull,
-	0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull,
-};
-
-__device__ __forceinline__ float expf_glibc(float x, const unsigned long long* table) {
-	const unsigned abstop = (__float_as_uint(x) >> 20) & 0x7ffu;
-	if (abstop >= 0x42bu) {  // |x| >= 88, infinity or NaN
-		if (__float_as_uint(x) == 0xff800000u) return 0.0f;
-		if (abstop >= 0x7f8u) return x + x;
-		if (x > 0x1.62e42ep6f) return __builtin_inff();  // e^x overflows
-		if (x < -0x1.9fe368p6f) return 0.0f;             // e^x below half the smallest subnormal
-	}
-	constexpr double kInvLn2N = 0x1.71547652b82fep+0 * 32, kShift = 0x1.8p+52;
-	constexpr double kC0 = 0x1.c6af84b912394p-5 / 32 / 32 / 32, kC1 = 0x1.ebfce50fac4f3p-3 / 32 / 32,
-	                 kC2 = 0x1.62e42ff0c52d6p-1 / 32;
-	const double xd = x;
-	double kd = __builtin_fma(kInvLn2N, xd, kShift);  // k + kShift, rounded to an integer by the addition
-	const unsigned long long ki = (unsigned long long)__double_as_longlong(kd);
-	kd -= kShift;
-	const double r = __builtin_fma(kInvLn2N, xd, -kd);
-	const double s = __longlong_as_double((long long)(table[ki & 31] + (ki << 47)));
-	const double z = __builtin_fma(kC0, r, kC1), r2 = r * r;
-	double y = __builtin_fma(kC2, r, 1.0);
-	y = __builtin_fma(z, r2, y);
-	return (float)(y * s);
-}
 
 namespace {
 
@@ -158,6 +117,7 @@ __global__ void __launch_bounds__(kThreads) softmax_rows_kernel(const float* in,
                                                                 FastDiv per_row) {
 	extern __shared__ float sm[];
 	__shared__ unsigned long long table[32];
+	__shared__ double rowinv[64];
 	const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
 	const int64_t r0 = (int64_t)blockIdx.x * rb;
 	const int nr = (int)min<int64_t>(rb, g.rows - r0);
@@ -237,12 +197,17 @@ __global__ void __launch_bounds__(kThreads) softmax_rows_kernel(const float* in,
 		if (VEC) {
 			for (int j = 4 * lane; j < g.tk; j += 256) {
 				f32x4 v = *reinterpret_cast<const f32x4*>(o + j);
+				float e[4] = {v[0] - m, v[1] - m, v[2] - m, v[3] - m};
+				expf_glibc_n(e, table);
 #pragma unroll
-				for (int c = 0; c < 4; ++c) v[c] = (j + c < live) ? expf_glibc(v[c] - m, table) : 0.0f;
+				for (int c = 0; c < 4; ++c) v[c] = j + c < live ? e[c] : 0.0f;
 				*reinterpret_cast<f32x4*>(o + j) = v;
 			}
 		} else {
-			for (int j = lane; j < g.tk; j += 64) o[j] = (j < live) ? expf_glibc(o[j] - m, table) : 0.0f;
+			for (int j = lane; j < g.tk; j += 64) {
+				const float e = expf_glibc(o[j] - m, table);
+				o[j] = j < live ? e : 0.0f;
+			}
 		}
 	}
 	__syncthreads();
@@ -277,6 +242,7 @@ __global__ void __launch_bounds__(kThreads) softmax_rows_kernel(const float* in,
 			}
 			for (; j < live; ++j) s += o[j];
 			rowsum[r] = s;
+			rowinv[r] = 1.0 / (double)s;
 		}
 	}
 	__syncthreads();
@@ -289,14 +255,17 @@ __global__ void __launch_bounds__(kThreads) softmax_rows_kernel(const float* in,
 			const int j = (int)(e - r * per_row.d) * 4;
 			const f32x4 v = *reinterpret_cast<const f32x4*>(sm + r * ld + j);
 			const float s = rowsum[r];
-			o4[e] = f32x4{v[0] / s, v[1] / s, v[2] / s, v[3] / s};
+			const double ri = rowinv[r];
+			float q[4] = {v[0], v[1], v[2], v[3]};
+			div_n_by_row_sum(q, s, ri);
+			o4[e] = f32x4{q[0], q[1], q[2], q[3]};
 		}
 	} else {
 		const unsigned total = (unsigned)(nr * g.tk);
 		for (unsigned e = tid; e < total; e += kThreads) {
 			const unsigned r = fdiv(e, per_row);
 			const int j = (int)(e - r * per_row.d);
-			out[r0 * g.tk + e] = sm[r * ld + j] / rowsum[r];
+			out[r0 * g.tk + e] = div_by_row_sum(sm[r * ld + j], rowsum[r], rowinv[r]);
 		}
 	}
 }

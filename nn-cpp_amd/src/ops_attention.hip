@@ -1,6 +1,7 @@
 // ops_attention.hip - extern "C" entry points of nn::attention and nn::scaled_masked_softmax (include/nnh.h).
 //
-// Forward (src/autograd/ops.cpp:1226-1261) as three launches over all (sample, head) pairs at once:
+// Forward (src/autograd/ops.cpp:1226-1261): for heads of width 64 and Tk <= 256, one fused kernel per 64 query
+// rows (kernels/hip/attention.hip). Otherwise three launches over all (sample, head) pairs at once:
 //   probs = Q_h K_h^T   (batched sgemm F,T with two-level batch addressing n*T*D + h*Dh, row stride D)
 //   probs = masked_softmax_row(probs) per row
 //   out_h = probs V_h   (batched sgemm F,F into column block h*Dh, row stride D)
@@ -12,6 +13,7 @@
 #include <cmath>
 
 #include "abi_common.hpp"
+#include "kernels/hip/attention.hpp"
 #include "kernels/hip/softmax.hpp"
 #include "nnh.h"
 
@@ -72,6 +74,10 @@ int nnh_attention_forward(const float* q, const float* k, const float* v, size_t
 	if (N == 0) return NNH_OK;
 	if (!q || !k || !v || !out || !probs) return fail(NNH_ERR_INVALID, "attention: null pointer");
 	hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+	if (attention_fused_ok((int64_t)Tq, (int64_t)Tk, (int64_t)a.Dh, (int64_t)D, q, k, v, out, probs, key_padding_mask))
+		return hip_status(attention_fused_forward(q, k, v, (int64_t)N, (int64_t)Tq, (int64_t)Tk, (int64_t)D,
+		                                          (int64_t)heads, key_padding_mask, causal, a.scale, out, probs, s),
+		                  "attention forward");
 	// S = Q_h K_h^T into probs (ops.cpp:1256)
 	rc = gemm(0, 1, Tq, Tk, a.Dh, q, D, k, D, probs, Tk, 0, head_batch(a, Tq, Tk, false, true, 0), stream);
 	if (rc != NNH_OK) return rc;

@@ -1,6 +1,6 @@
 /*
  * expf_glibc_check.c - checks the restatement of glibc's expf that the GPU softmax uses (expf_glibc in
- * nn-cpp_amd/src/kernels/hip/softmax.hip) against the C library's own expf, which is what nn-cpp's
+ * nn-cpp_amd/src/kernels/hip/softmax_row.hpp) against the C library's own expf, which is what nn-cpp's
  * std::exp(float) calls (src/autograd/ops.cpp:1199).
  *
  * The algorithm is ARM optimized-routines' expf (Szabolcs Nagy), which glibc 2.28+ ships: k = round(x 32/ln2)

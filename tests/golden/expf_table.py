@@ -1,4 +1,4 @@
-"""The 32-entry table of the softmax's exp (kExp2Table in nn-cpp_amd/src/kernels/hip/softmax.hip), from its
+"""The 32-entry table of the softmax's exp (kExp2Table in nn-cpp_amd/src/kernels/hip/softmax_row.hpp), from its
 definition: entry i = bits of 2^(i/32) rounded to the nearest double, minus i << 47 (mod 2^64). 2^(i/32) is
 evaluated with 60-digit decimal arithmetic and converted by Python's correctly rounded float().
 

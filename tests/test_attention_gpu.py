@@ -107,6 +107,112 @@ def test_baseline_config4(gpu, oracle, causal):
         assert np.all(probs[:, :, tri] == 0.0)
 
 
+# Head width 64, Tk <= 256, Tk % 4 == 0: the fused forward kernel (one workgroup per 64 query rows). Ragged query
+# blocks, key counts that do not fill a wave's 64 keys, causal rows, padded keys.
+FUSED_SHAPES = [  # (N, Tq, Tk, heads, causal, masked)
+    (2, 1, 4, 1, False, False),
+    (2, 37, 36, 2, False, True),
+    (1, 64, 64, 1, True, False),
+    (2, 100, 100, 2, True, True),
+    (1, 130, 252, 3, False, True),
+    (2, 256, 256, 2, True, True),
+]
+# The three-launch path: key count not a multiple of 4, more than 256 keys, head width 32.
+UNFUSED_SHAPES = [  # (N, Tq, Tk, heads, Dh, causal, masked)
+    (2, 50, 37, 2, 64, False, True),
+    (1, 40, 260, 1, 64, False, False),
+    (2, 70, 70, 4, 32, True, True),
+]
+
+
+def attention_case(seed, N, Tq, Tk, D, masked):
+    q = synth.normal(seed, (N, Tq, D))
+    k = synth.normal(seed + 1, (N, Tk, D))
+    v = synth.normal(seed + 2, (N, Tk, D))
+    mask = None
+    if masked:
+        mask = np.ones((N, Tk), np.float32)
+        mask[0, Tk // 2:] = 0
+        if N > 1:
+            mask[1, ::3] = 0
+    return q, k, v, mask
+
+
+@pytest.mark.parametrize("shape", FUSED_SHAPES)
+def test_fused_forward_matches_oracle(gpu, oracle, shape):
+    import nnh
+    N, Tq, Tk, H, causal, masked = shape
+    q, k, v, mask = attention_case(60 + Tq, N, Tq, Tk, 64 * H, masked)
+    out, probs = nnh.attention_forward(dev(q), dev(k), dev(v), H, dev(mask), causal)
+    want_out, want_probs = oracle.attention_forward(q, k, v, H, mask, causal)
+    same(host(probs), want_probs, (shape, "probs"))
+    same(host(out), want_out, (shape, "out"))
+
+
+@pytest.mark.parametrize("shape", UNFUSED_SHAPES)
+def test_unfused_forward_matches_oracle(gpu, oracle, shape):
+    import nnh
+    N, Tq, Tk, H, Dh, causal, masked = shape
+    q, k, v, mask = attention_case(80 + Tq, N, Tq, Tk, Dh * H, masked)
+    out, probs = nnh.attention_forward(dev(q), dev(k), dev(v), H, dev(mask), causal)
+    want_out, want_probs = oracle.attention_forward(q, k, v, H, mask, causal)
+    same(host(probs), want_probs, (shape, "probs"))
+    same(host(out), want_out, (shape, "out"))
+
+
+def test_fused_forward_special_values(gpu, oracle):
+    """Inf and NaN in Q, K and V: the fused kernel's chains, max scan and division propagate them as nn-cpp does
+    (NaN payloads aside)."""
+    import nnh
+    N, T, H = 2, 96, 2
+    q, k, v, _ = attention_case(90, N, T, T, 64 * H, False)
+    q[0, 3, 5] = np.inf
+    k[0, 7, 70] = -np.inf
+    k[1, 0, 1] = np.nan
+    v[0, 11, 2] = np.nan
+    v[1, 50, 64] = np.inf
+    for causal in (False, True):
+        out, probs = nnh.attention_forward(dev(q), dev(k), dev(v), H, None, causal)
+        want_out, want_probs = oracle.attention_forward(q, k, v, H, None, causal)
+        assert_same(host(probs), want_probs, ("probs", causal), nan_equal=True)
+        assert_same(host(out), want_out, ("out", causal), nan_equal=True)
+
+
+def division_rows(T):
+    """Score rows [0, 0, 0, 0, 0, 0, x, -1e4]: six keys at the maximum, so the sum is 6 and p_6 / 6 for x in the
+    subnormal range of exp hits exact midpoints between subnormal floats (p = 3 M 2^-149 with M odd)."""
+    x = np.linspace(-103.9, -87.4, T, dtype=np.float32)
+    rows = np.zeros((T, 8), np.float32)
+    rows[:, 6] = x
+    rows[:, 7] = -1e4
+    return rows
+
+
+def test_softmax_division_at_subnormal_midpoints(gpu, oracle):
+    """Both softmax kernels (the fused attention and the row softmax) against the oracle's float division on rows
+    whose quotients are subnormal, some exactly halfway between two floats."""
+    import nnh
+    T, H = 4096, 1
+    rows = division_rows(T)
+    y = nnh.scaled_masked_softmax_forward(dev(rows.reshape(1, 1, T, 8)), 1.0, None, False)
+    assert_same(host(y), oracle.scaled_masked_softmax(rows.reshape(1, 1, T, 8), np.float32(1.0), None, False),
+                "row softmax")
+    # attention with S = Q K^T equal to 8 * rows: q_i = [1, 8 x_i, 0...], k_j picks a column (scale 1/8)
+    N, Tq = T // 256, 256
+    q = np.zeros((N, Tq, 64), np.float32)
+    q[..., 0] = 1
+    q[..., 1] = (8 * rows[:, 6]).reshape(N, Tq)
+    k = np.zeros((N, 8, 64), np.float32)
+    k[:, 6, 1] = 1
+    k[:, 7, 0] = -8e4
+    v = synth.normal(5, (N, 8, 64))
+    out, probs = nnh.attention_forward(dev(q), dev(k), dev(v), H, None, False)
+    want_out, want_probs = oracle.attention_forward(q, k, v, H, None, False)
+    assert (want_probs[..., 6] < 2 ** -126).all() and (want_probs[..., 6] > 0).any()
+    same(host(probs), want_probs, "attention probs")
+    same(host(out), want_out, "attention out")
+
+
 def test_attention_backward_matches_oracle(gpu, oracle):
     import torch
 

@@ -339,7 +339,7 @@ def test_lane_sum_and_sum_axis0(oracle):
 
 GOLDEN_DIR = os.path.join(HERE, "golden")
 SOFTMAX_SRC = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "nn-cpp_amd", "src", "kernels",
-                           "hip", "softmax.hip")
+                           "hip", "softmax_row.hpp")
 
 
 def test_expf_table_is_its_definition():
