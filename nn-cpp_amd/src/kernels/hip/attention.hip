@@ -48,6 +48,57 @@ struct FusedArgs {
 
 inline int lds_floats_p(int tk) { return kRows * (tk + 4); }
 
+using M32 = Mfma<kMf32>;
+using M16 = Mfma<kMf16>;
+
+// Phases 0 and 1, shared by the forward and the backward: (R K^T)^T for the 64 rows of R (row stride d, nr of
+// them valid) against the keys of K (row stride d, tk valid). Wave w takes keys 64w + l (lane l holds key row
+// 64w + l in registers: the MFMA's A operand) against rows 32u + (l & 31), u = 0, 1 (staged in LDS with
+// coalesced loads, read as the B operand), each element the fma chain over d = 0..63 from +0. Ends with a
+// barrier after which the LDS is free.
+__device__ __forceinline__ void rows_times_keys(const float* rp, int nr, const float* kp, int tk, int d, float* sm,
+                                                M32::Acc& s0, M32::Acc& s1) {
+	const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+	const bool keys_here = 64 * wave < tk;
+	// loads are unconditional (indices clamped into range) so that all are in flight before the first wait;
+	// values past the end are never used
+	f32x4 kv[kDh / 4];
+	if (keys_here) {
+		const float* kr = kp + (int64_t)min(64 * wave + lane, tk - 1) * d;
+#pragma unroll
+		for (int u = 0; u < kDh / 4; ++u) kv[u] = *reinterpret_cast<const f32x4*>(kr + 4 * u);
+	}
+	{
+		f32x4 rs[kRows * kDh / 4 / 256];
+#pragma unroll
+		for (int u = 0; u < kRows * kDh / 4 / 256; ++u) {
+			const int row = (tid >> 4) + 16 * u;
+			rs[u] = *reinterpret_cast<const f32x4*>(rp + (int64_t)min(row, nr - 1) * d + 4 * (tid & 15));
+		}
+#pragma unroll
+		for (int u = 0; u < kRows * kDh / 4 / 256; ++u)
+			*reinterpret_cast<f32x4*>(sm + ((tid >> 4) + 16 * u) * kKLd + 4 * (tid & 15)) = rs[u];
+	}
+	__syncthreads();
+#pragma unroll
+	for (int r = 0; r < M32::NV; ++r) s0[r] = s1[r] = 0.0f;
+	if (keys_here) {
+		const float* rb0 = sm + (lane & 31) * kKLd;
+		const float* rb1 = rb0 + 32 * kKLd;
+#pragma unroll
+		for (int d4 = 0; d4 < kDh / 4; ++d4) {
+			const f32x4 b0 = *reinterpret_cast<const f32x4*>(rb0 + 4 * d4);
+			const f32x4 b1 = *reinterpret_cast<const f32x4*>(rb1 + 4 * d4);
+#pragma unroll
+			for (int c = 0; c < 4; ++c) {
+				s0 = M32::mma(kv[d4][c], b0[c], s0);
+				s1 = M32::mma(kv[d4][c], b1[c], s1);
+			}
+		}
+	}
+	__syncthreads();  // the staged rows are dead
+}
+
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) attention_fused_kernel(const FusedArgs a) {
 	extern __shared__ __align__(16) float sm[];
 	__shared__ unsigned long long table[32];
@@ -65,49 +116,11 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) a
 	const float* padrow = a.pad ? a.pad + (int64_t)n * tk : nullptr;
 	if (tid < 32) table[tid] = kExp2Table[tid];
 
-	// 0. the 64 query rows into LDS (coalesced, stride kKLd; the score rows reuse this LDS later), key row
-	// 64w + lane into registers. Loads are unconditional (indices clamped into range) so that all are in flight
-	// before the first wait; values past the end are never used.
+	// 0, 1. S^T for keys 64w + l against queries 32u + (l & 31), u = 0, 1 (fma(k, q, acc) is the reference's
+	// fma(q, k, acc))
 	const bool keys_here = 64 * wave < tk;
-	f32x4 kv[kDh / 4];
-	if (keys_here) {
-		const float* kr = kp + (int64_t)min(64 * wave + lane, tk - 1) * a.d;
-#pragma unroll
-		for (int u = 0; u < kDh / 4; ++u) kv[u] = *reinterpret_cast<const f32x4*>(kr + 4 * u);
-	}
-	{
-		f32x4 qs[kRows * kDh / 4 / 256];
-#pragma unroll
-		for (int u = 0; u < kRows * kDh / 4 / 256; ++u) {
-			const int row = (tid >> 4) + 16 * u;
-			qs[u] = *reinterpret_cast<const f32x4*>(qp + (int64_t)min(row, nq - 1) * a.d + 4 * (tid & 15));
-		}
-#pragma unroll
-		for (int u = 0; u < kRows * kDh / 4 / 256; ++u)
-			*reinterpret_cast<f32x4*>(sm + ((tid >> 4) + 16 * u) * kKLd + 4 * (tid & 15)) = qs[u];
-	}
-	__syncthreads();
-
-	// 1. S^T for keys 64w + l against queries 32u + (l & 31), u = 0, 1
-	using M32 = Mfma<kMf32>;
 	M32::Acc s0, s1;
-#pragma unroll
-	for (int r = 0; r < M32::NV; ++r) s0[r] = s1[r] = 0.0f;
-	if (keys_here) {
-		const float* qb0 = sm + (lane & 31) * kKLd;
-		const float* qb1 = qb0 + 32 * kKLd;
-#pragma unroll
-		for (int d4 = 0; d4 < kDh / 4; ++d4) {
-			const f32x4 b0 = *reinterpret_cast<const f32x4*>(qb0 + 4 * d4);
-			const f32x4 b1 = *reinterpret_cast<const f32x4*>(qb1 + 4 * d4);
-#pragma unroll
-			for (int c = 0; c < 4; ++c) {
-				s0 = M32::mma(kv[d4][c], b0[c], s0);
-				s1 = M32::mma(kv[d4][c], b1[c], s1);
-			}
-		}
-	}
-	__syncthreads();  // the queries are dead: the score rows take their LDS
+	rows_times_keys(qp, nq, kp, tk, a.d, sm, s0, s1);
 
 	// 2a. scaled and masked scores into LDS rows of stride tk + 4 (ops.cpp:1186-1191). Accumulator registers
 	// 4t .. 4t+3 hold four consecutive keys of one query: one 16-byte store each.
@@ -238,7 +251,6 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) a
 	__syncthreads();
 
 	// 3. O columns 16w .. 16w+15 for the 64 rows: the chain over every key in order
-	using M16 = Mfma<kMf16>;
 	M16::Acc o;
 #pragma unroll
 	for (int r = 0; r < M16::NV; ++r) o[r] = 0.0f;
@@ -293,6 +305,136 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) a
 	}
 }
 
+
+struct DScoresArgs {
+	const float* g;      // upstream gradient {N, Tq, D}
+	const float* v;
+	const float* probs;  // the forward's {N, heads, Tq, Tk}
+	float* ds;           // {N, heads, Tq, Tk}
+	const float* pad;
+	int heads, tq, tk, d;
+	int qblocks, total;
+	int causal;
+	float scale;
+};
+
+// The first half of nn::attention's backward for 64 query rows of one (sample, head) pair (ops.cpp:1286-1290):
+//   dP = G_h V_h^T                     each element the fma chain over d = 0..63 from +0 (sgemm F,T)
+//   dot_i = sum_j dP_ij * y_ij         the products rounded, then added in key order from +0
+//   dS_ij = masked ? 0 : scale * (y_ij * (dP_ij - dot_i)) + 0     (masked_softmax_row_backward, ops.cpp:1216-1224)
+// dP stays in the MFMA accumulators (wave w holds keys 64w..64w+63 of the 64 rows, four consecutive keys per
+// four registers); y is loaded in the same layout; only the products dP y go through LDS, where one lane per
+// row adds them in key order. dS is written to HBM for the dQ and dK products.
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) attention_dscores_kernel(const DScoresArgs a) {
+	extern __shared__ __align__(16) float sm[];
+	__shared__ float rowdot[kRows];
+	const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+	const int lid = xcd_remap(blockIdx.x, a.total);
+	const int nh = lid / a.qblocks, qb = lid - nh * a.qblocks;
+	const int n = nh / a.heads, h = nh - n * a.heads;
+	const int i0 = qb * kRows, nq = min(kRows, a.tq - i0);
+	const int tk = a.tk, ldp4 = (tk + 4) / 4;
+	const float* gp = a.g + ((int64_t)n * a.tq + i0) * a.d + h * kDh;
+	const float* vp = a.v + (int64_t)n * tk * a.d + h * kDh;
+	const float* yp = a.probs + ((int64_t)nh * a.tq + i0) * tk;
+	float* dsp = a.ds + ((int64_t)nh * a.tq + i0) * tk;
+	const float* padrow = a.pad ? a.pad + (int64_t)n * tk : nullptr;
+	f32x4* sm4 = reinterpret_cast<f32x4*>(sm);
+
+	// dP^T for keys 64w + l against rows 32u + (l & 31)
+	const bool keys_here = 64 * wave < tk;
+	M32::Acc s0, s1;
+	rows_times_keys(gp, nq, vp, tk, a.d, sm, s0, s1);
+
+	// y in the accumulator layout: quad t of unit u is y[32u + ccol][64w + crow(4t) .. +3] (rows and keys clamped
+	// into range; values outside are never used)
+	constexpr int kQ = M32::NV / 4;
+	f32x4 y[2][kQ];
+	if (keys_here) {
+#pragma unroll
+		for (int u = 0; u < 2; ++u) {
+			const int row = min(32 * u + M32::ccol(lane), nq - 1);
+#pragma unroll
+			for (int t = 0; t < kQ; ++t) {
+				const int j = min(64 * wave + M32::crow(4 * t, lane), tk - 4);
+				y[u][t] = *reinterpret_cast<const f32x4*>(yp + (int64_t)row * tk + j);
+			}
+		}
+		// the products dP y, rounded, into LDS rows of stride tk + 4 (tk % 4 == 0: every quad is whole)
+#pragma unroll
+		for (int u = 0; u < 2; ++u) {
+			const int row = 32 * u + M32::ccol(lane);
+#pragma unroll
+			for (int t = 0; t < kQ; ++t) {
+				const int j = 64 * wave + M32::crow(4 * t, lane);
+				f32x4 prod;
+#pragma unroll
+				for (int c = 0; c < 4; ++c) prod[c] = (u ? s1[4 * t + c] : s0[4 * t + c]) * y[u][t][c];
+				if (row < nq && j < tk) sm4[row * ldp4 + j / 4] = prod;
+			}
+		}
+	}
+	__syncthreads();
+
+	// dot_i: one lane per row, every key in order from +0
+	{
+		const int row = 16 * wave + lane;
+		if (lane < 16 && row < nq) {
+			const f32x4* o = sm4 + row * ldp4;
+			float dot = 0.0f;
+			int q = 0;
+			for (; q + 4 <= tk / 4; q += 4) {
+				f32x4 x[4];
+#pragma unroll
+				for (int u = 0; u < 4; ++u) x[u] = o[q + u];
+#pragma unroll
+				for (int u = 0; u < 4; ++u) {
+					dot += x[u][0];
+					dot += x[u][1];
+					dot += x[u][2];
+					dot += x[u][3];
+				}
+			}
+			for (; q < tk / 4; ++q) {
+				const f32x4 x = o[q];
+				dot += x[0];
+				dot += x[1];
+				dot += x[2];
+				dot += x[3];
+			}
+			rowdot[row] = dot;
+		}
+	}
+	__syncthreads();
+
+	// dS from the registers
+	if (keys_here) {
+		const bool masked = padrow != nullptr || a.causal;
+#pragma unroll
+		for (int u = 0; u < 2; ++u) {
+			const int row = 32 * u + M32::ccol(lane);
+			const float dot = rowdot[min(row, nq - 1)];
+#pragma unroll
+			for (int t = 0; t < kQ; ++t) {
+				const int j = 64 * wave + M32::crow(4 * t, lane);
+				f32x4 r;
+#pragma unroll
+				for (int c = 0; c < 4; ++c) {
+					const float dp = u ? s1[4 * t + c] : s0[4 * t + c];
+					r[c] = a.scale * (y[u][t][c] * (dp - dot)) + 0.0f;
+				}
+				if (masked) {  // uniform
+					const f32x4 pd = padrow ? *reinterpret_cast<const f32x4*>(padrow + min(j, tk - 4)) : f32x4{1, 1, 1, 1};
+#pragma unroll
+					for (int c = 0; c < 4; ++c)
+						r[c] = pd[c] == 0.0f || (a.causal && j + c > i0 + row) ? 0.0f : r[c];
+				}
+				if (row < nq && j < tk) *reinterpret_cast<f32x4*>(dsp + (int64_t)row * tk + j) = r;
+			}
+		}
+	}
+}
+
 }  // namespace
 
 bool attention_fused_ok(int64_t tq, int64_t tk, int64_t dh, int64_t d, const void* q, const void* k, const void* v,
@@ -329,6 +471,34 @@ hipError_t attention_fused_forward(const float* q, const float* k, const float* 
 	                                   hipFuncAttributeMaxDynamicSharedMemorySize, lds);
 	if (e != hipSuccess) return e;
 	hipLaunchKernelGGL(attention_fused_kernel, dim3((unsigned)total), dim3(256), lds, s, a);
+	return hipGetLastError();
+}
+
+hipError_t attention_fused_dscores(const float* g, const float* v, const float* probs, int64_t n, int64_t tq, int64_t tk,
+                                   int64_t d, int64_t heads, const float* pad, int causal, float scale, float* ds,
+                                   hipStream_t s) {
+	const int64_t qblocks = (tq + kRows - 1) / kRows, total = n * heads * qblocks;
+	if (total == 0) return hipSuccess;
+	if (total >= ((int64_t)1 << 31) || n * heads * tq * tk >= ((int64_t)1 << 62)) return hipErrorInvalidValue;
+	DScoresArgs a;
+	a.g = g;
+	a.v = v;
+	a.probs = probs;
+	a.ds = ds;
+	a.pad = pad;
+	a.heads = (int)heads;
+	a.tq = (int)tq;
+	a.tk = (int)tk;
+	a.d = (int)d;
+	a.qblocks = (int)qblocks;
+	a.total = (int)total;
+	a.causal = causal ? 1 : 0;
+	a.scale = scale;
+	const int lds = 4 * max(kRows * kKLd, lds_floats_p((int)tk));
+	hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(attention_dscores_kernel),
+	                                   hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+	if (e != hipSuccess) return e;
+	hipLaunchKernelGGL(attention_dscores_kernel, dim3((unsigned)total), dim3(256), lds, s, a);
 	return hipGetLastError();
 }
 

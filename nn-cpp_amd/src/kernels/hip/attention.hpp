@@ -17,4 +17,10 @@ hipError_t attention_fused_forward(const float* q, const float* k, const float* 
                                    int64_t d, int64_t heads, const float* pad, int causal, float scale, float* out,
                                    float* probs, hipStream_t s);
 
+// The first half of nn::attention's backward (ops.cpp:1286-1290) for the same shapes: dP = G_h V_h^T and the
+// softmax backward, ds {n, heads, tq, tk} = dL/d(scores), bit for bit the reference's.
+hipError_t attention_fused_dscores(const float* g, const float* v, const float* probs, int64_t n, int64_t tq, int64_t tk,
+                                   int64_t d, int64_t heads, const float* pad, int causal, float scale, float* ds,
+                                   hipStream_t s);
+
 }  // namespace nnh

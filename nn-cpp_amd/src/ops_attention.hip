@@ -6,7 +6,7 @@
 //   probs = masked_softmax_row(probs) per row
 //   out_h = probs V_h   (batched sgemm F,F into column block h*Dh, row stride D)
 // Backward (ops.cpp:1263-1295): dP = G_h V_h^T, dV (+)= P^T G_h, dS = softmax backward, dQ (+)= dS K_h,
-// dK (+)= dS^T Q_h. Heads write disjoint column blocks, so batching the heads keeps, for every element, the
+// dK (+)= dS^T Q_h; for the fused forward's shapes dP and dS come from one kernel (dP never leaves the chip). Heads write disjoint column blocks, so batching the heads keeps, for every element, the
 // reference's order of contributions (dV, then dQ, then dK, which matters when q, k and v are one node).
 #include <hip/hip_runtime.h>
 
@@ -104,14 +104,20 @@ int nnh_attention_backward(const float* g, const float* q, const float* k, const
 	const size_t ds_floats = N * heads * Tq * Tk;
 	rc = hip_status(hipMallocAsync(reinterpret_cast<void**>(&ds), ds_floats * sizeof(float), s), "attention workspace");
 	if (rc != NNH_OK) return rc;
-	// dP = G_h V_h^T (ops.cpp:1286)
-	rc = gemm(0, 1, Tq, Tk, a.Dh, g, D, v, D, ds, Tk, 0, head_batch(a, Tq, Tk, false, true, 0), stream);
+	const bool fused = (dq || dk) && attention_fused_ok((int64_t)Tq, (int64_t)Tk, (int64_t)a.Dh, (int64_t)D, g, v, v, ds,
+	                                                    probs, key_padding_mask);
+	if (fused)  // dP = G_h V_h^T and the softmax backward in one kernel (ops.cpp:1286, 1289-1290)
+		rc = hip_status(attention_fused_dscores(g, v, probs, (int64_t)N, (int64_t)Tq, (int64_t)Tk, (int64_t)D,
+		                                        (int64_t)heads, key_padding_mask, causal, a.scale, ds, s),
+		                "attention backward");
+	else  // dP = G_h V_h^T (ops.cpp:1286)
+		rc = gemm(0, 1, Tq, Tk, a.Dh, g, D, v, D, ds, Tk, 0, head_batch(a, Tq, Tk, false, true, 0), stream);
 	// dV (+)= P^T G_h (ops.cpp:1287): A = probs stored Tq x Tk, read transposed
 	if (rc == NNH_OK && dv) {
 		nnh_batch b = head_batch(a, 0, Tq, true, false, Tk);
 		rc = gemm(1, 0, Tk, a.Dh, Tq, probs, Tk, g, D, dv, D, !dv_first, b, stream);
 	}
-	if (rc == NNH_OK && (dq || dk))
+	if (rc == NNH_OK && (dq || dk) && !fused)
 		rc = hip_status(softmax_backward_rows(probs, ds, ds, (int64_t)(N * heads * Tq), (int)Tk, (int)Tq, (int)heads,
 		                                      a.scale, key_padding_mask, causal, 0, s),
 		                "attention softmax backward");

@@ -160,9 +160,42 @@ def test_unfused_forward_matches_oracle(gpu, oracle, shape):
     same(host(out), want_out, (shape, "out"))
 
 
+def backward_case(oracle, q, k, v, mask, H, causal, seed):
+    """dQ, dK, dV from the library (fresh gradients) and from the oracle, for upstream gradient N(0, 1)."""
+    import torch
+
+    import nnh
+    g = synth.normal(seed, q.shape)
+    _, probs = oracle.attention_forward(q, k, v, H, mask, causal)
+    dq, dk, dv = (torch.full(t.shape, float("nan"), device="cuda") for t in (q, k, v))
+    nnh.attention_backward(dev(g), dev(q), dev(k), dev(v), dev(probs), H, dev(mask), causal, dq, True, dk, True, dv,
+                           True)
+    want = oracle.attention_backward(g, q, k, v, probs, H, mask, causal)
+    return (host(dq), host(dk), host(dv)), want
+
+
+@pytest.mark.parametrize("shape", FUSED_SHAPES)
+def test_fused_backward_matches_oracle(gpu, oracle, shape):
+    """The fused dP + softmax backward kernel (same shapes as the fused forward), then dQ, dK, dV."""
+    N, Tq, Tk, H, causal, masked = shape
+    q, k, v, mask = attention_case(70 + Tq, N, Tq, Tk, 64 * H, masked)
+    got, want = backward_case(oracle, q, k, v, mask, H, causal, 75 + Tq)
+    for t, w, key in zip(got, want, ("dq", "dk", "dv")):
+        same(t, w, (shape, key))
+
+
+@pytest.mark.parametrize("shape", UNFUSED_SHAPES)
+def test_unfused_backward_matches_oracle(gpu, oracle, shape):
+    N, Tq, Tk, H, Dh, causal, masked = shape
+    q, k, v, mask = attention_case(85 + Tq, N, Tq, Tk, Dh * H, masked)
+    got, want = backward_case(oracle, q, k, v, mask, H, causal, 87 + Tq)
+    for t, w, key in zip(got, want, ("dq", "dk", "dv")):
+        same(t, w, (shape, key))
+
+
 def test_fused_forward_special_values(gpu, oracle):
-    """Inf and NaN in Q, K and V: the fused kernel's chains, max scan and division propagate them as nn-cpp does
-    (NaN payloads aside)."""
+    """Inf and NaN in Q, K and V: the fused kernels' chains, max scan, division and softmax backward propagate them
+    as nn-cpp does (NaN payloads aside)."""
     import nnh
     N, T, H = 2, 96, 2
     q, k, v, _ = attention_case(90, N, T, T, 64 * H, False)
@@ -176,6 +209,9 @@ def test_fused_forward_special_values(gpu, oracle):
         want_out, want_probs = oracle.attention_forward(q, k, v, H, None, causal)
         assert_same(host(probs), want_probs, ("probs", causal), nan_equal=True)
         assert_same(host(out), want_out, ("out", causal), nan_equal=True)
+        got, want = backward_case(oracle, q, k, v, None, H, causal, 95)
+        for t, w, key in zip(got, want, ("dq", "dk", "dv")):
+            assert_same(t, w, (key, causal), nan_equal=True)
 
 
 def division_rows(T):
