@@ -112,9 +112,9 @@ int build_gemm(int ta, int tb, size_t m, size_t n, size_t k, const float* a, siz
 	return NNH_OK;
 }
 
-int run_gemm(const GemmCall& g, void* stream, int config) {
+int run_gemm(const GemmCall& g, void* stream, int config, float* workspace) {
 	if (g.m == 0 || g.n == 0 || g.batch_count == 0) return NNH_OK;
-	return hip_status(gemm_launch(g, reinterpret_cast<hipStream_t>(stream), config), "sgemm launch");
+	return hip_status(gemm_launch(g, reinterpret_cast<hipStream_t>(stream), config, workspace), "sgemm launch");
 }
 
 }  // namespace nnh

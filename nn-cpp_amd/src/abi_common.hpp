@@ -20,7 +20,9 @@ bool ranges_overlap(const void* p0, uint64_t bytes0, const void* p1, uint64_t by
 int build_gemm(int ta, int tb, size_t m, size_t n, size_t k, const float* a, size_t lda, const float* b, size_t ldb,
                float* c, size_t ldc, int accumulate, const nnh_batch* batch, const nnh_epilogue* ep, GemmCall& g,
                const ColGather* gather = nullptr);
-int run_gemm(const GemmCall& g, void* stream, int config);
+// workspace: depth-cut partials (at least gemm_workspace_floats(g)), required when the caller holds the
+// stream's StreamWorkspace; otherwise null.
+int run_gemm(const GemmCall& g, void* stream, int config, float* workspace = nullptr);
 
 // How nn::matmul(a, b, trans_a, trans_b) (src/tensor.cpp:571-641) maps onto one (batched) GEMM.
 struct MatmulPlan {

@@ -1,5 +1,9 @@
 // gemm.hip - instantiations, depth-cut reduction and launch logic of the fp32 MFMA GEMM.
 #include "gemm.hpp"
+
+#include <optional>
+
+#include "workspace.hpp"
 #include "gemm_config.hpp"
 
 #include <algorithm>
@@ -112,11 +116,13 @@ bool depth_cut(int64_t m, int64_t n, int64_t k) {
 	return !(m == 0 || n == 0 || m * n > (int64_t(1) << 16) || k < 4 * 128 || m * n * k < (int64_t(1) << 20));
 }
 
-int64_t gemm_workspace_floats(const GemmCall& g) {
-	if (!depth_cut(g.m, g.n, g.k)) return 0;
-	const int64_t pieces = (g.k + 127) / 128;
-	return pieces * g.m * g.n * g.batch_count;
+int64_t gemm_workspace_floats(int64_t m, int64_t n, int64_t k, int64_t batch_count) {
+	if (!depth_cut(m, n, k)) return 0;
+	const int64_t pieces = (k + 127) / 128;
+	return pieces * m * n * batch_count;
 }
+
+int64_t gemm_workspace_floats(const GemmCall& g) { return gemm_workspace_floats(g.m, g.n, g.k, g.batch_count); }
 
 int gemm_config_count() { return kNumConfigs; }
 const char* gemm_config_name(int config) {
@@ -160,15 +166,14 @@ hipError_t gemm_launch(const GemmCall& g, hipStream_t s, int config, float* work
 	const bool interior = vec_ok && g.m % cf.bm == 0 && g.n % cf.bn == 0 && g.k % cf.bk == 0 && g.k > 0;
 
 	float* part = nullptr;
-	bool own = false;
+	std::optional<StreamWorkspace> ws;
 	if (cut) {
-		const int64_t need = gemm_workspace_floats(g);
 		if (workspace) {
 			part = workspace;
 		} else {
-			e = hipMallocAsync(reinterpret_cast<void**>(&part), need * sizeof(float), s);
-			if (e != hipSuccess) return e;
-			own = true;
+			ws.emplace(s, (size_t)gemm_workspace_floats(g) * sizeof(float));
+			if (ws->error() != hipSuccess) return ws->error();
+			part = ws->at<float>(0);
 		}
 		p.partial = part;
 	}
@@ -183,10 +188,6 @@ hipError_t gemm_launch(const GemmCall& g, hipStream_t s, int config, float* work
 		hipLaunchKernelGGL(reduce_pieces_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, part,
 		                   p.pieces, p.m, p.n, g.c, g.ldc, g.accumulate, g.batch, g.batch_count, g.ep);
 		e = hipGetLastError();
-	}
-	if (own) {
-		hipError_t e2 = hipFreeAsync(part, s);
-		if (e == hipSuccess) e = e2;
 	}
 	return e;
 }

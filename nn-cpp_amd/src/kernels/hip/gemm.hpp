@@ -34,10 +34,11 @@ bool depth_cut(int64_t m, int64_t n, int64_t k);
 
 // Floats of workspace a call needs (0 when it takes no depth cut).
 int64_t gemm_workspace_floats(const GemmCall& g);
+int64_t gemm_workspace_floats(int64_t m, int64_t n, int64_t k, int64_t batch_count);
 
 // Launches on stream s. Kernel configuration: -1 picks one by shape; results never depend on it.
-// Workspace for a depth cut comes from workspace (if non-null, at least gemm_workspace_floats) or
-// else from the stream-ordered allocator.
+// Workspace for a depth cut comes from workspace (if non-null, at least gemm_workspace_floats) or else from
+// the stream's StreamWorkspace (so a caller holding that one must pass workspace).
 hipError_t gemm_launch(const GemmCall& g, hipStream_t s, int config = -1, float* workspace = nullptr);
 
 int gemm_config_count();

@@ -10,11 +10,14 @@
 // reference's order of contributions (dV, then dQ, then dK, which matters when q, k and v are one node).
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 
 #include "abi_common.hpp"
 #include "kernels/hip/attention.hpp"
+#include "kernels/hip/gemm.hpp"
 #include "kernels/hip/softmax.hpp"
+#include "workspace.hpp"
 #include "nnh.h"
 
 using namespace nnh;
@@ -54,11 +57,11 @@ nnh_batch head_batch(const AttnGeom& a, size_t ta_rows, size_t tb_rows, bool a_i
 }
 
 int gemm(int ta, int tb, size_t m, size_t n, size_t k, const float* A, size_t lda, const float* B, size_t ldb,
-         float* Cm, size_t ldc, int acc, const nnh_batch& batch, void* stream) {
+         float* Cm, size_t ldc, int acc, const nnh_batch& batch, void* stream, float* partials = nullptr) {
 	GemmCall g;
 	int rc = build_gemm(ta, tb, m, n, k, A, lda, B, ldb, Cm, ldc, acc, &batch, nullptr, g);
 	if (rc != NNH_OK) return rc;
-	return run_gemm(g, stream, -1);
+	return run_gemm(g, stream, -1, partials);
 }
 
 }  // namespace
@@ -100,10 +103,18 @@ int nnh_attention_backward(const float* g, const float* q, const float* k, const
 	if (N == 0 || (!dq && !dk && !dv)) return NNH_OK;
 	if (!g || !q || !k || !v || !probs) return fail(NNH_ERR_INVALID, "attention backward: null pointer");
 	hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-	float* ds = nullptr;
-	const size_t ds_floats = N * heads * Tq * Tk;
-	rc = hip_status(hipMallocAsync(reinterpret_cast<void**>(&ds), ds_floats * sizeof(float), s), "attention workspace");
-	if (rc != NNH_OK) return rc;
+	// one workspace: dS, then the depth-cut partials the dV, dQ and dK products share (they run in turn)
+	WorkspacePlan plan;
+	const size_t off_ds = plan.add(N * heads * Tq * Tk * sizeof(float));
+	const int64_t nb = (int64_t)(N * heads);
+	const int64_t part = std::max({gemm_workspace_floats((int64_t)Tk, (int64_t)a.Dh, (int64_t)Tq, nb),
+	                               gemm_workspace_floats((int64_t)Tq, (int64_t)a.Dh, (int64_t)Tk, nb),
+	                               gemm_workspace_floats((int64_t)Tq, (int64_t)Tk, (int64_t)a.Dh, nb)});
+	const size_t off_part = part ? plan.add((size_t)part * sizeof(float)) : 0;
+	StreamWorkspace ws(s, plan.total);
+	if (ws.error() != hipSuccess) return hip_status(ws.error(), "attention workspace");
+	float* ds = ws.at<float>(off_ds);
+	float* partials = part ? ws.at<float>(off_part) : nullptr;
 	const bool fused = (dq || dk) && attention_fused_ok((int64_t)Tq, (int64_t)Tk, (int64_t)a.Dh, (int64_t)D, g, v, v, ds,
 	                                                    probs, key_padding_mask);
 	if (fused)  // dP = G_h V_h^T and the softmax backward in one kernel (ops.cpp:1286, 1289-1290)
@@ -111,11 +122,11 @@ int nnh_attention_backward(const float* g, const float* q, const float* k, const
 		                                        (int64_t)heads, key_padding_mask, causal, a.scale, ds, s),
 		                "attention backward");
 	else  // dP = G_h V_h^T (ops.cpp:1286)
-		rc = gemm(0, 1, Tq, Tk, a.Dh, g, D, v, D, ds, Tk, 0, head_batch(a, Tq, Tk, false, true, 0), stream);
+		rc = gemm(0, 1, Tq, Tk, a.Dh, g, D, v, D, ds, Tk, 0, head_batch(a, Tq, Tk, false, true, 0), stream, partials);
 	// dV (+)= P^T G_h (ops.cpp:1287): A = probs stored Tq x Tk, read transposed
 	if (rc == NNH_OK && dv) {
 		nnh_batch b = head_batch(a, 0, Tq, true, false, Tk);
-		rc = gemm(1, 0, Tk, a.Dh, Tq, probs, Tk, g, D, dv, D, !dv_first, b, stream);
+		rc = gemm(1, 0, Tk, a.Dh, Tq, probs, Tk, g, D, dv, D, !dv_first, b, stream, partials);
 	}
 	if (rc == NNH_OK && (dq || dk) && !fused)
 		rc = hip_status(softmax_backward_rows(probs, ds, ds, (int64_t)(N * heads * Tq), (int)Tk, (int)Tq, (int)heads,
@@ -124,15 +135,14 @@ int nnh_attention_backward(const float* g, const float* q, const float* k, const
 	// dQ (+)= dS K_h (ops.cpp:1291)
 	if (rc == NNH_OK && dq) {
 		nnh_batch b = head_batch(a, 0, Tk, true, false, Tq);
-		rc = gemm(0, 0, Tq, a.Dh, Tk, ds, Tk, k, D, dq, D, !dq_first, b, stream);
+		rc = gemm(0, 0, Tq, a.Dh, Tk, ds, Tk, k, D, dq, D, !dq_first, b, stream, partials);
 	}
 	// dK (+)= dS^T Q_h (ops.cpp:1292)
 	if (rc == NNH_OK && dk) {
 		nnh_batch b = head_batch(a, 0, Tq, true, false, Tk);
-		rc = gemm(1, 0, Tk, a.Dh, Tq, ds, Tk, q, D, dk, D, !dk_first, b, stream);
+		rc = gemm(1, 0, Tk, a.Dh, Tq, ds, Tk, q, D, dk, D, !dk_first, b, stream, partials);
 	}
-	const int rc2 = hip_status(hipFreeAsync(ds, s), "attention workspace");
-	return rc != NNH_OK ? rc : rc2;
+	return rc;
 }
 
 int nnh_scaled_masked_softmax_forward(const float* x, size_t N, size_t H, size_t Tq, size_t Tk, float scale,

@@ -13,11 +13,14 @@
 // never -0.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <vector>
 
 #include "abi_common.hpp"
 #include "kernels/hip/conv.hpp"
+#include "kernels/hip/gemm.hpp"
 #include "kernels/hip/reduce.hpp"
+#include "workspace.hpp"
 #include "nnh.h"
 
 using namespace nnh;
@@ -66,31 +69,6 @@ ColGather col_gather(const ConvGeom& g) {
 	c.wo_div = make_fastdiv((unsigned)g.wo);
 	return c;
 }
-
-struct Workspace {
-	hipStream_t s;
-	std::vector<void*> bufs;
-	hipError_t err = hipSuccess;
-	explicit Workspace(hipStream_t st) : s(st) {}
-	template <typename T>
-	T* get(size_t count) {
-		void* p = nullptr;
-		if (err != hipSuccess) return nullptr;
-		err = hipMallocAsync(&p, (count ? count : 1) * sizeof(T), s);
-		if (err != hipSuccess) return nullptr;
-		bufs.push_back(p);
-		return static_cast<T*>(p);
-	}
-	hipError_t release() {
-		hipError_t e = err;
-		for (void* p : bufs) {
-			hipError_t e2 = hipFreeAsync(p, s);
-			if (e == hipSuccess) e = e2;
-		}
-		bufs.clear();
-		return e;
-	}
-};
 
 }  // namespace
 
@@ -141,44 +119,47 @@ int nnh_conv2d_backward(const float* g, const float* x, const float* w, const un
 		return rc;
 	}
 	if (!g || !x || !w) return fail(NNH_ERR_INVALID, "conv2d backward: null pointer");
-	Workspace ws(s);
+	// one workspace: the masked gradient, per-sample bias and weight gradients, dcol, and the depth-cut partials
+	// of the two GEMMs (which run one after the other and share them)
+	WorkspacePlan plan;
+	const size_t off_m = alive ? plan.add(N * Cout * hw * 4) : 0;
+	const size_t off_gb = db ? plan.add(N * Cout * 4) : 0;
+	const size_t off_gw = dw ? plan.add(N * Cout * K * 4) : 0;
+	const size_t off_col = dx ? plan.add(N * K * hw * 4) : 0;
+	const int64_t part = std::max(dw ? gemm_workspace_floats((int64_t)Cout, (int64_t)K, (int64_t)hw, (int64_t)N) : 0,
+	                              dx ? gemm_workspace_floats((int64_t)K, (int64_t)hw, (int64_t)Cout, (int64_t)N) : 0);
+	const size_t off_part = part ? plan.add((size_t)part * 4) : 0;
+	StreamWorkspace ws(s, plan.total);
+	if (ws.error() != hipSuccess) return hip_status(ws.error(), "conv2d workspace");
+	float* partials = part ? ws.at<float>(off_part) : nullptr;
 	const float* gm = g;
 	if (alive) {  // ops.cpp:1439-1443
-		float* m = ws.get<float>(N * Cout * hw);
-		if (!m) return hip_status(ws.release(), "conv2d workspace");
+		float* m = ws.at<float>(off_m);
 		rc = hip_status(mask_grad(g, alive, m, (int64_t)(N * Cout * hw), s), "conv2d mask");
 		gm = m;
 	}
 	if (rc == NNH_OK && db) {  // ops.cpp:1445, 1461
-		float* gb = ws.get<float>(N * Cout);
-		rc = gb ? hip_status(lane_sums(gm, (int64_t)(N * Cout), (int64_t)hw, gb, s), "conv2d db")
-		        : hip_status(ws.err, "conv2d workspace");
+		float* gb = ws.at<float>(off_gb);
+		rc = hip_status(lane_sums(gm, (int64_t)(N * Cout), (int64_t)hw, gb, s), "conv2d db");
 		if (rc == NNH_OK) rc = hip_status(sum_rows(gb, (int64_t)N, (int64_t)Cout, db, db_first ? 0 : 2, s), "conv2d db");
 	}
 	if (rc == NNH_OK && dw) {  // ops.cpp:1448-1449, 1462: dW_n = g_n col_n^T with col_n gathered from x_n
-		float* gw = ws.get<float>(N * Cout * K);
-		if (!gw) rc = hip_status(ws.err, "conv2d workspace");
-		if (rc == NNH_OK) {
-			nnh_batch b{};
-			b.ndim = 1;
-			b.shape[0] = N;
-			b.stride_a[0] = (ptrdiff_t)(Cout * hw);
-			b.stride_b[0] = (ptrdiff_t)(Cin * H * W);
-			b.stride_c[0] = (ptrdiff_t)(Cout * K);
-			const ColGather cg = col_gather(geo);
-			GemmCall call;
-			rc = build_gemm(0, 1, Cout, K, hw, gm, hw, x, hw, gw, K, 0, &b, nullptr, call, &cg);
-			if (rc == NNH_OK) rc = run_gemm(call, stream, -1);
-		}
+		float* gw = ws.at<float>(off_gw);
+		nnh_batch b{};
+		b.ndim = 1;
+		b.shape[0] = N;
+		b.stride_a[0] = (ptrdiff_t)(Cout * hw);
+		b.stride_b[0] = (ptrdiff_t)(Cin * H * W);
+		b.stride_c[0] = (ptrdiff_t)(Cout * K);
+		const ColGather cg = col_gather(geo);
+		GemmCall call;
+		rc = build_gemm(0, 1, Cout, K, hw, gm, hw, x, hw, gw, K, 0, &b, nullptr, call, &cg);
+		if (rc == NNH_OK) rc = run_gemm(call, stream, -1, partials);
 		if (rc == NNH_OK)
 			rc = hip_status(sum_rows(gw, (int64_t)N, (int64_t)(Cout * K), dw, dw_first ? 0 : 2, s), "conv2d dw");
 	}
-	float* col = nullptr;
-	if (rc == NNH_OK && dx) {
-		col = ws.get<float>(N * K * hw);
-		if (!col) rc = hip_status(ws.err, "conv2d workspace");
-	}
 	if (rc == NNH_OK && dx) {  // ops.cpp:1452-1455
+		float* col = ws.at<float>(off_col);
 		nnh_batch b{};
 		b.ndim = 1;
 		b.shape[0] = N;
@@ -187,11 +168,10 @@ int nnh_conv2d_backward(const float* g, const float* x, const float* w, const un
 		b.stride_c[0] = (ptrdiff_t)(K * hw);
 		GemmCall call;
 		rc = build_gemm(1, 0, K, hw, Cout, w, K, gm, hw, col, hw, 0, &b, nullptr, call);
-		if (rc == NNH_OK) rc = run_gemm(call, stream, -1);
+		if (rc == NNH_OK) rc = run_gemm(call, stream, -1, partials);
 		if (rc == NNH_OK) rc = hip_status(col2im(col, dx, geo, (int64_t)N, dx_first ? 1 : 0, s), "col2im");
 	}
-	const int rc2 = hip_status(ws.release(), "conv2d workspace");
-	return rc != NNH_OK ? rc : rc2;
+	return rc;
 }
 
 int nnh_im2col(const float* x, size_t N, size_t Cin, size_t H, size_t W, size_t kh, size_t kw, int stride, int padding,

@@ -6,6 +6,7 @@
 #include "abi_common.hpp"
 #include "kernels/hip/reduce.hpp"
 #include "nnh.h"
+#include "workspace.hpp"
 
 using namespace nnh;
 
@@ -67,25 +68,21 @@ int nnh_linear_backward(const float* g, const float* x, const float* w, const si
 		std::vector<size_t> suffix(nlead);
 		suffix[nlead - 1] = n;
 		for (int d = nlead - 2; d >= 0; --d) suffix[d] = suffix[d + 1] * lead[d + 1];
-		float* tmp[2] = {nullptr, nullptr};
-		hipError_t e = hipSuccess;
+		WorkspacePlan plan;
+		const size_t tmp_bytes = (suffix[0] ? suffix[0] : 1) * sizeof(float);
+		const size_t off[2] = {plan.add(tmp_bytes), plan.add(tmp_bytes)};
+		StreamWorkspace ws(s, plan.total);
+		hipError_t e = ws.error();
 		const float* cur = g;
 		for (int d = 0; d < nlead && e == hipSuccess; ++d) {
 			if (d == nlead - 1) {
 				e = sum_rows(cur, (int64_t)lead[d], (int64_t)n, db, combine, s);
 				break;
 			}
-			float*& out = tmp[d & 1];
-			if (!out) e = hipMallocAsync(reinterpret_cast<void**>(&out), (suffix[0] ? suffix[0] : 1) * sizeof(float), s);
-			if (e != hipSuccess) break;
+			float* out = ws.at<float>(off[d & 1]);
 			e = sum_rows(cur, (int64_t)lead[d], (int64_t)suffix[d], out, 0, s);
 			cur = out;
 		}
-		for (float* t : tmp)
-			if (t) {
-				hipError_t e2 = hipFreeAsync(t, s);
-				if (e == hipSuccess) e = e2;
-			}
 		return hip_status(e, "bias gradient");
 	}
 	return NNH_OK;

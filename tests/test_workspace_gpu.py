@@ -1,0 +1,166 @@
+"""The library's per-(device, stream) workspace (nn-cpp_amd/src/workspace.hpp): calls that need scratch memory
+(conv2d and attention backward, depth-cut GEMMs, multi-axis bias gradients) reuse one buffer per stream.
+
+Each case runs with the device held behind a bounded delay, so that the host is ahead of the device, as in a
+training loop: calls must not wait for the device on the host, successive calls on one stream must not disturb
+each other's results, the buffer must grow when a larger call comes, and work on two streams, or from two host
+threads on one stream, must not share scratch memory. Results are compared bit for bit with the same calls run
+alone (which the op tests compare with nn-cpp).
+"""
+import threading
+import time
+
+import numpy as np
+import pytest
+
+from helpers import assert_same
+from nnh import synth
+
+pytestmark = pytest.mark.gpu
+
+
+def dev(a):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def conv_case(seed, N, Cin, H, Cout):
+    import nnh
+    import torch
+    x = dev(synth.mt19937_uniform(seed, N * Cin * H * H).reshape(N, Cin, H, H))
+    w = dev(synth.normal(seed + 1, (Cout, Cin, 3, 3)))
+    b = torch.zeros(Cout, device="cuda")
+    y, alive = nnh.conv2d_forward(x, w, b, 1, 1, True)
+    g = dev(synth.normal(seed + 2, tuple(y.shape)))
+    return x, w, alive, g
+
+
+def conv_backward(case, stream=None):
+    import nnh
+    import torch
+    x, w, alive, g = case
+    dx, dw, db = torch.empty_like(x), torch.empty_like(w), torch.empty(w.shape[0], device="cuda")
+    nnh.conv2d_backward(g, x, w, alive, 1, 1, dx, True, dw, True, db, True, stream=stream)
+    return dx, dw, db
+
+
+def reference(case):
+    import torch
+    out = conv_backward(case)
+    torch.cuda.synchronize()
+    return [t.cpu().numpy() for t in out]
+
+
+def test_calls_queued_behind_the_device_do_not_wait_and_stay_correct(gpu):
+    """40 conv backward calls (two shapes, alternating, so each call overwrites the scratch data of the one before
+    it) enqueued while the device is 150 ms behind: the host must finish enqueueing long before the device gets to
+    them (the stream-ordered free made the host wait for the device on every call), and every result must be
+    bit-identical to the call run alone."""
+    import nnh
+    import torch
+    small, big = conv_case(10, 16, 8, 14, 16), conv_case(20, 64, 32, 14, 64)
+    want = {id(small): reference(small), id(big): reference(big)}
+    conv_backward(big)  # the buffer already has the larger size: no growth during the timed loop
+    torch.cuda.synchronize()
+    nnh.bench_delay(150000)
+    t0 = time.perf_counter()
+    outs = [(c, conv_backward(c)) for c in [small, big] * 20]
+    enqueue = time.perf_counter() - t0
+    torch.cuda.synchronize()
+    assert enqueue < 0.1, f"40 calls took {enqueue * 1e3:.1f} ms to enqueue: the host waited for the device"
+    for i, (c, got) in enumerate(outs):
+        for t, w_, name in zip(got, want[id(c)], ("dx", "dw", "db")):
+            assert_same(t.cpu().numpy(), w_, (i, name))
+
+
+def test_buffer_grows_between_calls(gpu):
+    """Small, then larger, then small again, all queued behind the device: the larger call grows the buffer."""
+    import nnh
+    import torch
+    cases = [conv_case(30 + 10 * i, n, c, 14, c) for i, (n, c) in enumerate(((4, 4), (128, 32), (8, 8), (256, 32)))]
+    want = [reference(c) for c in cases]
+    nnh.bench_delay(50000)
+    outs = [conv_backward(c) for c in cases]
+    torch.cuda.synchronize()
+    for i, (got, w_) in enumerate(zip(outs, want)):
+        for t, ww, name in zip(got, w_, ("dx", "dw", "db")):
+            assert_same(t.cpu().numpy(), ww, (i, name))
+
+
+def test_two_streams_get_separate_buffers(gpu):
+    """Alternating calls on two streams, both held behind delays, run concurrently on the device."""
+    import nnh
+    import torch
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    a, b = conv_case(50, 32, 16, 14, 32), conv_case(60, 32, 16, 14, 32)
+    wa, wb = reference(a), reference(b)
+    torch.cuda.synchronize()
+    nnh.bench_delay(30000, stream=s1)
+    nnh.bench_delay(30000, stream=s2)
+    outs = []
+    for _ in range(6):
+        outs.append((conv_backward(a, s1), wa))
+        outs.append((conv_backward(b, s2), wb))
+    torch.cuda.synchronize()
+    for i, (got, w_) in enumerate(outs):
+        for t, ww, name in zip(got, w_, ("dx", "dw", "db")):
+            assert_same(t.cpu().numpy(), ww, (i, name))
+
+
+def test_two_threads_on_one_stream(gpu):
+    """Two host threads calling on the same stream at once: each call keeps the buffer while it enqueues."""
+    import nnh
+    import torch
+    s = torch.cuda.Stream()
+    a, b = conv_case(70, 32, 16, 14, 32), conv_case(80, 32, 16, 14, 32)
+    wa, wb = reference(a), reference(b)
+    torch.cuda.synchronize()
+    nnh.bench_delay(30000, stream=s)
+    outs = {0: [], 1: []}
+
+    def worker(i, case):
+        torch.cuda.set_device(0)
+        for _ in range(8):
+            outs[i].append(conv_backward(case, s))
+
+    threads = [threading.Thread(target=worker, args=(0, a)), threading.Thread(target=worker, args=(1, b))]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    torch.cuda.synchronize()
+    for i, w_ in ((0, wa), (1, wb)):
+        assert len(outs[i]) == 8
+        for j, got in enumerate(outs[i]):
+            for t, ww, name in zip(got, w_, ("dx", "dw", "db")):
+                assert_same(t.cpu().numpy(), ww, (i, j, name))
+
+
+def test_attention_backward_and_depth_cut_gemm_queued(gpu, oracle):
+    """The attention backward (dS in the workspace) and a depth-cut GEMM (partials in the workspace) queued
+    alternately behind the device, against the oracle."""
+    import nnh
+    import torch
+    N, T, D, H = 2, 64, 128, 2
+    q, k, v, g = (synth.normal(200 + i, (N, T, D)) for i in range(4))
+    _, probs = oracle.attention_forward(q, k, v, H, None, False)
+    want = oracle.attention_backward(g, q, k, v, probs, H, None, False)
+    m, n, kk = 64, 64, 1024  # m n <= 2^16, k >= 512, m n k >= 2^20: nn-cpp's depth cut
+    A = synth.mt19937_uniform(210, m * kk).reshape(m, kk) * 2 - 1
+    B = synth.mt19937_uniform(211, kk * n).reshape(kk, n) * 2 - 1
+    wc = oracle.sgemm(0, 0, m, n, kk, A, kk, B, n, np.zeros((m, n), np.float32), n, False)
+    dq_, dk_, dv_, dp, da, db_ = dev(q), dev(k), dev(v), dev(probs), dev(A), dev(B)
+    dg = dev(g)
+    nnh.bench_delay(50000)
+    outs = []
+    for _ in range(4):
+        grads = [torch.empty((N, T, D), device="cuda") for _ in range(3)]
+        nnh.attention_backward(dg, dq_, dk_, dv_, dp, H, None, False, grads[0], True, grads[1], True, grads[2], True)
+        c = torch.empty((m, n), device="cuda")
+        nnh.sgemm(0, 0, m, n, kk, da, kk, db_, n, c, n)
+        outs.append((grads, c))
+    torch.cuda.synchronize()
+    for i, (grads, c) in enumerate(outs):
+        for t, w_, name in zip(grads, want, ("dq", "dk", "dv")):
+            assert_same(t.cpu().numpy(), w_, (i, name))
+        assert_same(c.cpu().numpy(), wc, (i, "sgemm depth cut"))
