@@ -316,6 +316,61 @@ __global__ void __launch_bounds__(256) lane_sum8_kernel(const float* __restrict_
 	}
 }
 
+// The ReLU's gradient mask and lane_sum of each masked row in one pass (ops.cpp:1439-1445): out = alive ? g : 0,
+// and dst[row] = lane_sum(out row), with lane_sum8_kernel's arrangement (eight lanes per row, lane k the
+// reference's partial a[k]).
+__global__ void __launch_bounds__(256) mask_lane_sum8_kernel(const float* __restrict__ g,
+                                                             const unsigned char* __restrict__ alive,
+                                                             float* __restrict__ out, unsigned rows, int n,
+                                                             float* __restrict__ dst) {
+	const unsigned gid = blockIdx.x * 256 + threadIdx.x;
+	const unsigned row = gid >> 3;
+	const int k = (int)(gid & 7);
+	const bool valid = row < rows;
+	const int64_t off = (int64_t)(valid ? row : 0) * n;
+	const float* p = g + off;
+	const unsigned char* al = alive + off;
+	float* o = out + off;
+	const int full = n & ~7;
+	float a = 0.0f;
+	if (valid) {
+		int i = k;
+		for (; i + 56 < full; i += 64) {  // eight elements in flight ahead of the dependent additions
+			float v[8];
+			unsigned char f[8];
+#pragma unroll
+			for (int u = 0; u < 8; ++u) {
+				v[u] = p[i + 8 * u];
+				f[u] = al[i + 8 * u];
+			}
+#pragma unroll
+			for (int u = 0; u < 8; ++u) {
+				const float m = f[u] ? v[u] : 0.0f;
+				o[i + 8 * u] = m;
+				a = a + m;
+			}
+		}
+		for (; i < full; i += 8) {
+			const float m = al[i] ? p[i] : 0.0f;
+			o[i] = m;
+			a = a + m;
+		}
+	}
+	const int base = (int)(threadIdx.x & 63) & ~7;
+	float part[8];
+#pragma unroll
+	for (int j = 0; j < 8; ++j) part[j] = __shfl(a, base + j);
+	if (valid && k == 0) {
+		float t = ((part[0] + part[1]) + (part[2] + part[3])) + ((part[4] + part[5]) + (part[6] + part[7]));
+		for (int i = full; i < n; ++i) {
+			const float m = al[i] ? p[i] : 0.0f;
+			o[i] = m;
+			t = t + m;
+		}
+		dst[row] = t;
+	}
+}
+
 // The ReLU's gradient mask (ops.cpp:1439-1443): out = alive ? g : 0.
 __global__ void __launch_bounds__(256) mask_kernel(const float* __restrict__ g, const unsigned char* __restrict__ alive,
                                                    float* __restrict__ out, int64_t total) {
@@ -475,6 +530,18 @@ hipError_t mask_grad(const float* g, const unsigned char* alive, float* out, int
 	} else {
 		hipLaunchKernelGGL(mask_kernel, dim3(blocks_for(total)), dim3(256), 0, s, g, alive, out, total);
 	}
+	return hipGetLastError();
+}
+
+hipError_t masked_lane_sums(const float* g, const unsigned char* alive, float* out, int64_t rows, int64_t n, float* dst,
+                            hipStream_t s) {
+	if (rows == 0) return hipSuccess;
+	if (rows * 8 >= kFast || n >= kFast || rows * n >= kFast) {  // the two passes, with 64-bit indexing
+		hipError_t e = mask_grad(g, alive, out, rows * n, s);
+		return e != hipSuccess ? e : lane_sums(out, rows, n, dst, s);
+	}
+	hipLaunchKernelGGL(mask_lane_sum8_kernel, dim3(blocks_for(rows * 8)), dim3(256), 0, s, g, alive, out, (unsigned)rows,
+	                   (int)n, dst);
 	return hipGetLastError();
 }
 

@@ -22,6 +22,9 @@ bool conv_same_quad_ok(const float* x, const float* y, const unsigned char* aliv
 hipError_t conv_same_quad(const float* x, const float* w, const float* bias, float* y, unsigned char* alive,
                           const ConvGeom& g, int64_t samples, int cout, int relu, int cg, hipStream_t s);
 hipError_t mask_grad(const float* g, const unsigned char* alive, float* out, int64_t total, hipStream_t s);
+// mask_grad and lane_sums in one pass: out = alive ? g : 0 over rows x n, dst[row] = lane_sum of out's row.
+hipError_t masked_lane_sums(const float* g, const unsigned char* alive, float* out, int64_t rows, int64_t n, float* dst,
+                            hipStream_t s);
 hipError_t lane_sums(const float* src, int64_t rows, int64_t n, float* dst, hipStream_t s);
 
 }  // namespace nnh

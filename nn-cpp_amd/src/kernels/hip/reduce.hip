@@ -32,61 +32,82 @@ __global__ void __launch_bounds__(256) sum_rows_kernel(const float* __restrict__
 	else dst[j] = dst[j] + s;
 }
 
-// The same sum with the rows staged through LDS: a block owns 64 columns; for each chunk of up to kChunk rows
-// all 256 threads load the chunk at once (16-byte loads when the rows allow), then one lane per column adds
-// the chunk's rows in order onto its running sum. Same bits as sum_rows_kernel, without one memory latency
-// per few rows.
-constexpr int kSumCols = 64, kChunk = 128;
+// The same sum, staged through LDS: a block owns kSumCols columns; all 256 threads load a chunk of up to
+// kSumChunk rows at once (16-byte loads when the rows allow), then kSumCols lanes of the first wave add the chunk's
+// rows in order onto their running sums, while the next chunk's loads are already in flight. Narrow blocks give
+// many blocks (one column's chain is serial, so the parallelism is the number of columns). Same bits as
+// sum_rows_kernel.
+constexpr int kSumCols = 16, kSumChunk = 256;
+constexpr int kSumPer = kSumCols * kSumChunk / 256;  // floats each thread loads per chunk
+
+__device__ __forceinline__ void sum_chunk_load(const float* __restrict__ src, int rows, int inner, int c0, int ncol,
+                                               int r0, int vec, float (&v)[kSumPer]) {
+	const int tid = threadIdx.x;
+	if (vec) {  // inner % 4 == 0 and 16-byte aligned: four threads per row, 16 bytes each
+#pragma unroll
+		for (int u = 0; u < kSumPer / 4; ++u) {
+			const int idx = tid + 256 * u, r = min(r0 + (idx >> 2), rows - 1), q = 4 * (idx & 3);
+			const f32x4 x = *reinterpret_cast<const f32x4*>(src + (int64_t)r * inner + c0 + min(q, ncol - 4));
+#pragma unroll
+			for (int c = 0; c < 4; ++c) v[4 * u + c] = x[c];
+		}
+	} else {
+#pragma unroll
+		for (int u = 0; u < kSumPer; ++u) {
+			const int idx = tid + 256 * u, r = min(r0 + (idx >> 4), rows - 1), c = min(idx & 15, ncol - 1);
+			v[u] = src[(int64_t)r * inner + c0 + c];
+		}
+	}
+}
+
+__device__ __forceinline__ void sum_chunk_store(float (*tile)[kSumCols], int vec, const float (&v)[kSumPer]) {
+	const int tid = threadIdx.x;
+	if (vec) {
+#pragma unroll
+		for (int u = 0; u < kSumPer / 4; ++u) {
+			const int idx = tid + 256 * u;
+			*reinterpret_cast<f32x4*>(&tile[idx >> 2][4 * (idx & 3)]) = f32x4{v[4 * u], v[4 * u + 1], v[4 * u + 2], v[4 * u + 3]};
+		}
+	} else {
+#pragma unroll
+		for (int u = 0; u < kSumPer; ++u) {
+			const int idx = tid + 256 * u;
+			tile[idx >> 4][idx & 15] = v[u];
+		}
+	}
+}
 
 __global__ void __launch_bounds__(256) sum_rows_lds_kernel(const float* __restrict__ src, int rows, int inner,
                                                            float* __restrict__ dst, int combine, int vec) {
-	__shared__ __align__(16) float tile[kChunk][kSumCols];
+	__shared__ __align__(16) float tile[2][kSumChunk][kSumCols];
 	const int tid = threadIdx.x;
 	const int c0 = blockIdx.x * kSumCols;
 	const int ncol = min(kSumCols, inner - c0);
+	// 16-byte loads need whole quads of columns in this block (the clamp above keeps them in the row)
+	const int vec_here = vec && ncol % 4 == 0;
 	float s = 0.0f;
-	for (int a0 = 0; a0 < rows; a0 += kChunk) {
-		const int nr = min(kChunk, rows - a0);
-		if (vec) {  // 16 float4 per row of the tile; inner % 4 == 0, so a column block is whole float4s
-			constexpr int kPer = kChunk * kSumCols / 4 / 256;
-			f32x4 v[kPer];
-#pragma unroll
-			for (int u = 0; u < kPer; ++u) {
-				const int idx = tid + 256 * u, r = idx >> 4, q = (idx & 15) * 4;
-				if (r < nr && q < ncol) v[u] = *reinterpret_cast<const f32x4*>(src + (int64_t)(a0 + r) * inner + c0 + q);
-			}
-#pragma unroll
-			for (int u = 0; u < kPer; ++u) {
-				const int idx = tid + 256 * u, r = idx >> 4, q = (idx & 15) * 4;
-				if (r < nr && q < ncol) *reinterpret_cast<f32x4*>(&tile[r][q]) = v[u];
-			}
-		} else {
-			constexpr int kPer = kChunk * kSumCols / 256;
-			float v[kPer];
-#pragma unroll
-			for (int u = 0; u < kPer; ++u) {
-				const int idx = tid + 256 * u, r = idx >> 6, c = idx & 63;
-				if (r < nr && c < ncol) v[u] = src[(int64_t)(a0 + r) * inner + c0 + c];
-			}
-#pragma unroll
-			for (int u = 0; u < kPer; ++u) {
-				const int idx = tid + 256 * u, r = idx >> 6, c = idx & 63;
-				if (r < nr && c < ncol) tile[r][c] = v[u];
-			}
-		}
-		__syncthreads();
+	float v[kSumPer];
+	if (rows > 0) {
+		sum_chunk_load(src, rows, inner, c0, ncol, 0, vec_here, v);
+		sum_chunk_store(tile[0], vec_here, v);
+	}
+	__syncthreads();
+	for (int r0 = 0, b = 0; r0 < rows; r0 += kSumChunk, b ^= 1) {
+		const bool next = r0 + kSumChunk < rows;
+		if (next) sum_chunk_load(src, rows, inner, c0, ncol, r0 + kSumChunk, vec_here, v);  // in flight meanwhile
 		if (tid < ncol) {
-			// sixteen LDS reads in flight ahead of the dependent additions
+			const int nr = min(kSumChunk, rows - r0);
 			int r = 0;
-			for (; r + 16 <= nr; r += 16) {
-				float v[16];
+			for (; r + 16 <= nr; r += 16) {  // sixteen LDS reads ahead of the dependent additions
+				float x[16];
 #pragma unroll
-				for (int u = 0; u < 16; ++u) v[u] = tile[r + u][tid];
+				for (int u = 0; u < 16; ++u) x[u] = tile[b][r + u][tid];
 #pragma unroll
-				for (int u = 0; u < 16; ++u) s = s + v[u];
+				for (int u = 0; u < 16; ++u) s = s + x[u];
 			}
-			for (; r < nr; ++r) s = s + tile[r][tid];
+			for (; r < nr; ++r) s = s + tile[b][r][tid];
 		}
+		if (next) sum_chunk_store(tile[b ^ 1], vec_here, v);
 		__syncthreads();
 	}
 	if (tid < ncol) {

@@ -133,16 +133,17 @@ int nnh_conv2d_backward(const float* g, const float* x, const float* w, const un
 	if (ws.error() != hipSuccess) return hip_status(ws.error(), "conv2d workspace");
 	float* partials = part ? ws.at<float>(off_part) : nullptr;
 	const float* gm = g;
-	if (alive) {  // ops.cpp:1439-1443
+	float* gb = db ? ws.at<float>(off_gb) : nullptr;
+	if (alive) {  // ops.cpp:1439-1443, with the per-sample bias sums of ops.cpp:1445 in the same pass
 		float* m = ws.at<float>(off_m);
-		rc = hip_status(mask_grad(g, alive, m, (int64_t)(N * Cout * hw), s), "conv2d mask");
+		rc = db ? hip_status(masked_lane_sums(g, alive, m, (int64_t)(N * Cout), (int64_t)hw, gb, s), "conv2d mask, db")
+		        : hip_status(mask_grad(g, alive, m, (int64_t)(N * Cout * hw), s), "conv2d mask");
 		gm = m;
-	}
-	if (rc == NNH_OK && db) {  // ops.cpp:1445, 1461
-		float* gb = ws.at<float>(off_gb);
+	} else if (db) {  // ops.cpp:1445
 		rc = hip_status(lane_sums(gm, (int64_t)(N * Cout), (int64_t)hw, gb, s), "conv2d db");
-		if (rc == NNH_OK) rc = hip_status(sum_rows(gb, (int64_t)N, (int64_t)Cout, db, db_first ? 0 : 2, s), "conv2d db");
 	}
+	if (rc == NNH_OK && db)  // ops.cpp:1461
+		rc = hip_status(sum_rows(gb, (int64_t)N, (int64_t)Cout, db, db_first ? 0 : 2, s), "conv2d db");
 	if (rc == NNH_OK && dw) {  // ops.cpp:1448-1449, 1462: dW_n = g_n col_n^T with col_n gathered from x_n
 		float* gw = ws.at<float>(off_gw);
 		nnh_batch b{};
