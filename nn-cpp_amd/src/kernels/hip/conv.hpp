@@ -23,6 +23,12 @@ hipError_t conv_same_quad(const float* x, const float* w, const float* bias, flo
                           const ConvGeom& g, int64_t samples, int cout, int relu, int cg, hipStream_t s);
 hipError_t mask_grad(const float* g, const unsigned char* alive, float* out, int64_t total, hipStream_t s);
 // mask_grad and lane_sums in one pass: out = alive ? g : 0 over rows x n, dst[row] = lane_sum of out's row.
+// dx of nn::conv2d's backward from the masked output gradient gm {samples, cout, Ho*Wo} (ops.cpp:1452-1455): the
+// per-sample dcol = W^T gm and col2im in one kernel, dcol kept in LDS (same bits). first: dx = 0 + taps, else
+// dx += taps. conv_dx_fused_ok tells whether the geometry fits (Ho*Wo <= 256).
+bool conv_dx_fused_ok(const ConvGeom& g, int64_t samples, int cout);
+hipError_t conv_dx_fused(const float* gm, const float* w, float* dx, const ConvGeom& g, int64_t samples, int cout,
+                         int first, hipStream_t s);
 hipError_t masked_lane_sums(const float* g, const unsigned char* alive, float* out, int64_t rows, int64_t n, float* dst,
                             hipStream_t s);
 hipError_t lane_sums(const float* src, int64_t rows, int64_t n, float* dst, hipStream_t s);

@@ -1,0 +1,241 @@
+// conv_dx.hip - the input gradient of nn::conv2d without the column matrix in HBM (ops.cpp:1452-1455).
+//
+// The reference computes, per sample, dcol = W^T g (sgemm T,F: each element the fma chain over the output
+// channels co = 0..Cout-1 from +0) and then col2im: each dx element, starting from 0 (a fresh gradient) or its old
+// value, adds its taps in (ph, pw) order. One workgroup here owns one sample and a group of CG input channels:
+//   1. dcol rows k = (c, ph, pw) of its channels for every output position, as 16x16x1 MFMA chains over co:
+//      wave w owns positions 64w..64w+63 (the MFMA's A operand: the masked gradient g[co][p], read from global
+//      memory one row per step), against up to 80 rows k in five 16-wide units (B operand: W[co][k], staged in LDS
+//      a chunk of 64 output channels at a time); the chains never leave the accumulators across chunks.
+//   2. The dcol tile goes to LDS, and each dx element of the group gathers its taps from there, in (ph, pw) order.
+// Same bits as the batched GEMM + col2im path, with no dcol in HBM. Taken when a sample's output positions fit the
+// four waves (Ho*Wo <= 256) and the group's rows fit LDS; otherwise the caller uses that path.
+#include "conv.hpp"
+
+#include <algorithm>
+
+#include "gemm_tile.hpp"
+
+namespace nnh {
+
+namespace {
+
+constexpr int kDxRows = 80;      // dcol rows per workgroup (five 16-wide MFMA units)
+constexpr int kDxCo = 64;        // output channels of W staged per chunk
+constexpr int kDxWLd = kDxCo + 4;
+constexpr int kDxPos = 256;      // output positions: four waves of 64
+constexpr int kDxLdsBytes = 80 * 1024;
+constexpr int kDxACh = 16;       // gradient rows each lane keeps in flight
+
+using M16 = Mfma<kMf16>;
+
+struct DxArgs {
+	const float* g;   // masked output gradient {N, Cout, hw}
+	const float* w;   // {Cout, K}
+	float* dx;        // {N, Cin, H, W}
+	ConvGeom geo;
+	int cout, cg, groups, total, first;
+	int hwp;          // LDS row stride of the dcol tile (a multiple of 4, > hw)
+	FastDiv plane, width, stride;  // division by H*W, W and the stride
+};
+
+// The taps of a 3x3, stride-1 convolution, unrolled: the same order and the same additions as gather_taps
+__device__ __forceinline__ float gather_taps_3x3(const float* tile, const DxArgs& a, int c, int ih, int iw, float v) {
+	const ConvGeom& G = a.geo;
+#pragma unroll
+	for (int ph = 0; ph < 3; ++ph) {
+		const int qh = ih + G.pad - ph;
+		const bool row_ok = qh >= 0 && qh < G.ho;
+		const float* trow = tile + (c * 9 + ph * 3) * a.hwp + qh * G.wo;
+#pragma unroll
+		for (int pw = 0; pw < 3; ++pw) {
+			const int qw = iw + G.pad - pw;
+			if (row_ok && qw >= 0 && qw < G.wo) v = v + trow[pw * a.hwp + qw];
+		}
+	}
+	return v;
+}
+
+// The taps of dx element (ih, iw) of channel c from the dcol tile, in (ph, pw) order (col2im_fast_kernel's gather)
+template <bool STRIDE1>
+__device__ __forceinline__ float gather_taps(const float* tile, const DxArgs& a, int c, int ih, int iw, float v) {
+	const ConvGeom& G = a.geo;
+	for (int ph = 0; ph < G.kh; ++ph) {
+		const int th = ih + G.pad - ph;
+		int qh = th;
+		if (th < 0) continue;
+		if (!STRIDE1) {
+			qh = (int)fdiv((unsigned)th, a.stride);
+			if (qh * G.stride != th) continue;
+		}
+		if (qh >= G.ho) continue;
+		const float* trow = tile + (c * G.kh + ph) * G.kw * a.hwp + qh * G.wo;
+		for (int pw = 0; pw < G.kw; ++pw) {
+			const int tw = iw + G.pad - pw;
+			int qw = tw;
+			if (tw < 0) continue;
+			if (!STRIDE1) {
+				qw = (int)fdiv((unsigned)tw, a.stride);
+				if (qw * G.stride != tw) continue;
+			}
+			if (qw >= G.wo) continue;
+			v = v + trow[pw * a.hwp + qw];
+		}
+	}
+	return v;
+}
+
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) conv_dx_fused_kernel(const DxArgs a) {
+	extern __shared__ __align__(16) float sm[];
+	const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+	const ConvGeom& G = a.geo;
+	const int khkw = G.kh * G.kw, hw = G.ho * G.wo, K = G.cin * khkw;
+	const int lid = xcd_remap(blockIdx.x, a.total);  // the channel groups of one sample share an XCD's L2
+	const int n = lid / a.groups, grp = lid - n * a.groups;
+	const int c0 = grp * a.cg, cg = min(a.cg, G.cin - c0), rows = cg * khkw, k0 = c0 * khkw;
+	float* wl = sm;                          // [kDxRows][kDxWLd]: W^T for a chunk of output channels
+	float* tile = sm + kDxRows * kDxWLd;     // [cg * khkw][hwp]: the group's dcol rows
+	const float* gn = a.g + (int64_t)n * a.cout * hw;
+
+	// 1. the chains
+	M16::Acc acc[kDxRows / 16];
+#pragma unroll
+	for (int u = 0; u < kDxRows / 16; ++u)
+#pragma unroll
+		for (int r = 0; r < M16::NV; ++r) acc[u][r] = 0.0f;
+	const int pos = min(64 * wave + M16::arow(lane), hw - 1);  // positions past hw compute values never stored
+	const bool pos_here = 64 * wave < hw;
+	// gradient rows co .. co+kDxACh-1 at this lane's position (rows clamped into range, never used past cout)
+	auto load_g = [&](float (&dst)[kDxACh], int co) {
+#pragma unroll
+		for (int u = 0; u < kDxACh; ++u) dst[u] = gn[(int64_t)min(co + u, a.cout - 1) * hw + pos];
+	};
+	for (int cc = 0; cc < a.cout; cc += kDxCo) {
+		const int nco = min(kDxCo, a.cout - cc);
+		// W[cc + j][k0 + k] into wl[k][j] (rows past the group and channels past cout read as 0); every load is
+		// issued (at an index clamped into range) before the first store
+		{
+			constexpr int kPer = kDxRows * kDxCo / 256;
+			float wv[kPer];
+#pragma unroll
+			for (int u = 0; u < kPer; ++u) {
+				const int idx = tid + 256 * u, j = idx / kDxRows, k = idx - j * kDxRows;
+				wv[u] = a.w[(int64_t)(cc + min(j, nco - 1)) * K + k0 + min(k, rows - 1)];
+			}
+#pragma unroll
+			for (int u = 0; u < kPer; ++u) {
+				const int idx = tid + 256 * u, j = idx / kDxRows, k = idx - j * kDxRows;
+				wl[k * kDxWLd + j] = (k < rows && j < nco) ? wv[u] : 0.0f;
+			}
+		}
+		__syncthreads();
+		if (pos_here) {
+			float g0[kDxACh], g1[kDxACh];
+			load_g(g0, cc);
+			load_g(g1, cc + kDxACh);
+			auto steps = [&](const float (&gv)[kDxACh], int j0) {
+#pragma unroll
+				for (int q = 0; q < kDxACh / 4; ++q) {
+					const int j = j0 + 4 * q;
+					if (j < nco) {  // whole quads of channels, then single steps for a ragged end
+						f32x4 b[kDxRows / 16];
+#pragma unroll
+						for (int u = 0; u < kDxRows / 16; ++u)
+							b[u] = *reinterpret_cast<const f32x4*>(wl + (16 * u + M16::bcol(lane)) * kDxWLd + j);
+#pragma unroll
+						for (int e = 0; e < 4; ++e)
+							if (j + e < nco)
+#pragma unroll
+								for (int u = 0; u < kDxRows / 16; ++u)
+									acc[u] = M16::mma(gv[4 * q + e], b[u][e], acc[u]);
+					}
+				}
+			};
+			for (int j0 = 0; j0 < nco; j0 += 2 * kDxACh) {  // two chunks of gradient rows in flight
+				steps(g0, j0);
+				load_g(g0, cc + j0 + 2 * kDxACh);
+				steps(g1, j0 + kDxACh);
+				load_g(g1, cc + j0 + 3 * kDxACh);
+			}
+		}
+		__syncthreads();  // wl is rewritten by the next chunk
+	}
+
+	// 2a. the dcol rows into LDS: registers 4t .. 4t+3 of unit u hold row 16u + (l & 15) at four consecutive
+	// positions
+	if (pos_here) {
+#pragma unroll
+		for (int u = 0; u < kDxRows / 16; ++u) {
+			const int k = 16 * u + M16::ccol(lane);
+#pragma unroll
+			for (int t = 0; t < M16::NV / 4; ++t) {
+				const int p0 = 64 * wave + M16::crow(4 * t, lane);
+				if (k < rows && p0 < hw)
+					*reinterpret_cast<f32x4*>(tile + k * a.hwp + p0) =
+					    f32x4{acc[u][4 * t], acc[u][4 * t + 1], acc[u][4 * t + 2], acc[u][4 * t + 3]};
+			}
+		}
+	}
+	__syncthreads();
+
+	// 2b. col2im for the group's channels: every dx element adds its taps in (ph, pw) order
+	const int plane = G.h * G.w;
+	float* dxn = a.dx + ((int64_t)n * G.cin + c0) * plane;
+	for (int e = tid; e < cg * plane; e += 256) {
+		const int c = (int)fdiv((unsigned)e, a.plane), rem = e - c * plane;
+		const int ih = (int)fdiv((unsigned)rem, a.width), iw = rem - ih * G.w;
+		const float v0 = a.first ? 0.0f : dxn[e];
+		dxn[e] = G.stride != 1                 ? gather_taps<false>(tile, a, c, ih, iw, v0)
+		         : (G.kh == 3 && G.kw == 3) ? gather_taps_3x3(tile, a, c, ih, iw, v0)
+		                                    : gather_taps<true>(tile, a, c, ih, iw, v0);
+	}
+}
+
+int dx_hwp(const ConvGeom& g) { return (g.ho * g.wo + 3) / 4 * 4 + 4; }
+
+int dx_lds_bytes(const ConvGeom& g, int cg) { return (kDxRows * kDxWLd + cg * g.kh * g.kw * dx_hwp(g)) * 4; }
+
+// Input channels per workgroup: as many as the 80 MFMA rows hold, fewer if the dcol tile would not fit LDS
+int dx_group(const ConvGeom& g) {
+	int cg = std::min(kDxRows / (g.kh * g.kw), g.cin);
+	while (cg > 0 && dx_lds_bytes(g, cg) > kDxLdsBytes) --cg;
+	return cg;
+}
+
+}  // namespace
+
+bool conv_dx_fused_ok(const ConvGeom& g, int64_t samples, int cout) {
+	const int64_t hw = (int64_t)g.ho * g.wo;
+	if (hw < 1 || hw > kDxPos || cout < 1 || g.kh * g.kw > kDxRows) return false;
+	const int cg = dx_group(g);
+	if (cg < 1) return false;
+	const int64_t groups = (g.cin + cg - 1) / cg;
+	return samples * groups < ((int64_t)1 << 31) && samples * cout * hw < ((int64_t)1 << 40);
+}
+
+hipError_t conv_dx_fused(const float* gm, const float* w, float* dx, const ConvGeom& g, int64_t samples, int cout,
+                         int first, hipStream_t s) {
+	if (!conv_dx_fused_ok(g, samples, cout)) return hipErrorInvalidValue;
+	DxArgs a;
+	a.g = gm;
+	a.w = w;
+	a.dx = dx;
+	a.geo = g;
+	a.cout = cout;
+	a.cg = dx_group(g);
+	a.groups = (g.cin + a.cg - 1) / a.cg;
+	a.total = (int)(samples * a.groups);
+	a.first = first;
+	a.hwp = dx_hwp(g);
+	a.plane = make_fastdiv((unsigned)(g.h * g.w));
+	a.width = make_fastdiv((unsigned)g.w);
+	a.stride = make_fastdiv((unsigned)g.stride);
+	const int lds = dx_lds_bytes(g, a.cg);
+	hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(conv_dx_fused_kernel),
+	                                   hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+	if (e != hipSuccess) return e;
+	hipLaunchKernelGGL(conv_dx_fused_kernel, dim3((unsigned)a.total), dim3(256), lds, s, a);
+	return hipGetLastError();
+}
+
+}  // namespace nnh

@@ -7,7 +7,8 @@
 // chain over k = (c, ph, pw) in order.
 // Backward (ops.cpp:1418-1463): g masked by alive; db = per-sample lane_sum, then summed in sample order;
 // dW_n = g_n col_n^T (batched sgemm F,T, col_n gathered from x), summed in sample order; dcol_n = W^T g_n
-// (batched sgemm T,F into a workspace), then col2im in gather form into a zero-filled (fresh) or existing dx.
+// then col2im in gather form into a zero-filled (fresh) or existing dx: one kernel with dcol in LDS when a
+// sample's output positions fit it (conv_dx.hip), else a batched sgemm T,F into the workspace and col2im.
 // A fresh dW or db is stored as the sum s, where the reference adds s to a zero-filled gradient (0 + s): the
 // two agree because every such sum starts at +0 (fma chains, lane sums and Tensor::sum(0) alike) and so is
 // never -0.
@@ -125,9 +126,11 @@ int nnh_conv2d_backward(const float* g, const float* x, const float* w, const un
 	const size_t off_m = alive ? plan.add(N * Cout * hw * 4) : 0;
 	const size_t off_gb = db ? plan.add(N * Cout * 4) : 0;
 	const size_t off_gw = dw ? plan.add(N * Cout * K * 4) : 0;
-	const size_t off_col = dx ? plan.add(N * K * hw * 4) : 0;
-	const int64_t part = std::max(dw ? gemm_workspace_floats((int64_t)Cout, (int64_t)K, (int64_t)hw, (int64_t)N) : 0,
-	                              dx ? gemm_workspace_floats((int64_t)K, (int64_t)hw, (int64_t)Cout, (int64_t)N) : 0);
+	const bool dx_fused = dx && conv_dx_fused_ok(geo, (int64_t)N, (int)Cout);
+	const size_t off_col = dx && !dx_fused ? plan.add(N * K * hw * 4) : 0;
+	const int64_t part =
+	    std::max(dw ? gemm_workspace_floats((int64_t)Cout, (int64_t)K, (int64_t)hw, (int64_t)N) : 0,
+	             dx && !dx_fused ? gemm_workspace_floats((int64_t)K, (int64_t)hw, (int64_t)Cout, (int64_t)N) : 0);
 	const size_t off_part = part ? plan.add((size_t)part * 4) : 0;
 	StreamWorkspace ws(s, plan.total);
 	if (ws.error() != hipSuccess) return hip_status(ws.error(), "conv2d workspace");
@@ -159,7 +162,9 @@ int nnh_conv2d_backward(const float* g, const float* x, const float* w, const un
 		if (rc == NNH_OK)
 			rc = hip_status(sum_rows(gw, (int64_t)N, (int64_t)(Cout * K), dw, dw_first ? 0 : 2, s), "conv2d dw");
 	}
-	if (rc == NNH_OK && dx) {  // ops.cpp:1452-1455
+	if (rc == NNH_OK && dx && dx_fused) {  // ops.cpp:1452-1455, dcol kept on chip
+		rc = hip_status(conv_dx_fused(gm, w, dx, geo, (int64_t)N, (int)Cout, dx_first ? 1 : 0, s), "conv2d dx");
+	} else if (rc == NNH_OK && dx) {  // ops.cpp:1452-1455
 		float* col = ws.at<float>(off_col);
 		nnh_batch b{};
 		b.ndim = 1;

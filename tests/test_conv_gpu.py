@@ -111,6 +111,43 @@ def test_direct_and_gemm_paths_match_the_oracle(gpu, oracle):
             same(host(got), want, (key, N, Cin, Cout, kk, s, p))
 
 
+# dx with dcol kept on chip (Ho*Wo <= 256): input-channel groups that do not divide Cin, Cout over several 64-wide
+# chunks with a ragged end, strides, rectangular and large kernels, output planes that do not fill a wave; and
+# Ho*Wo > 256, which takes the batched GEMM and col2im. (N, Cin, H, W, Cout, kh, kw, stride, pad)
+DX_CASES = [
+    (2, 13, 14, 14, 64, 3, 3, 1, 1),    # config 3 conv2's plane; 13 channels: groups of 8 and 5
+    (3, 9, 9, 7, 150, 3, 3, 1, 1),      # Cout 150: chunks of 64, 64 and 22
+    (2, 5, 11, 11, 7, 5, 5, 2, 2),      # stride 2, 25 taps: 3 channels per group
+    (2, 4, 6, 10, 33, 2, 3, 1, 0),      # rectangular kernel, no padding
+    (1, 3, 16, 16, 20, 9, 9, 1, 4),     # 81 taps: one channel per group does not fit 80 rows
+    (2, 6, 17, 17, 24, 3, 3, 1, 1),     # 289 outputs: the GEMM + col2im path
+]
+
+
+@pytest.mark.parametrize("case", DX_CASES)
+def test_conv_backward_dx_paths(gpu, oracle, case):
+    """dx, fresh and accumulated onto an existing gradient, bitwise against the oracle (dW and db too)."""
+    import torch
+
+    import nnh
+    N, Cin, H, W, Cout, kh, kw, s, p = case
+    x = synth.mt19937_uniform(N * 31 + Cin, N * Cin * H * W).reshape(N, Cin, H, W)
+    w = synth.normal(Cout + 17, (Cout, Cin, kh, kw))
+    b = synth.mt19937_uniform(Cout + 18, Cout)
+    y, alive = nnh.conv2d_forward(dev(x), dev(w), dev(b), s, p, True)
+    _, wa = oracle.conv2d_forward(x, w, b, s, p, True)
+    gr = synth.normal(Cout + 19, tuple(y.shape))
+    old = synth.normal(Cout + 20, x.shape)
+    for first in (True, False):
+        dx = dev(old) if not first else torch.full(x.shape, float("nan"), device="cuda")
+        dw, db = torch.empty(w.shape, device="cuda"), torch.empty(Cout, device="cuda")
+        nnh.conv2d_backward(dev(gr), dev(x), dev(w), alive, s, p, dx, first, dw, True, db, True)
+        wdx, wdw, wdb = oracle.conv2d_backward(gr, x, w, wa, s, p, dx=None if first else old, dx_first=first)
+        same(host(dx), wdx, ("dx", case, first))
+        same(host(dw), wdw, ("dw", case))
+        same(host(db), wdb, ("db", case))
+
+
 def test_im2col_col2im(gpu, oracle):
     import torch
 
