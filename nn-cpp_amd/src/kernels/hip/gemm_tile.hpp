@@ -219,16 +219,18 @@ __device__ __forceinline__ ColRow col_row(const ColGather& cg, int kk, bool vali
 	return ColRow{valid ? (int64_t)ci * cg.h * cg.w : (int64_t)-1, (int)ph, (int)(rem - ph * cg.kw_div.d)};
 }
 
+// Every load is issued, at an index clamped into the channel image (so the code has no branches and the loads
+// of a tile are in flight together); padding and entries past the matrix are then replaced by 0.
 __device__ __forceinline__ f32x4 col_values(const float* __restrict__ x, const ColGather& cg, const ColRow& r,
                                             const ColCols& cc) {
-	f32x4 v = {0.0f, 0.0f, 0.0f, 0.0f};
-	if (r.xoff >= 0) {
-		const float* xc = x + r.xoff;
+	f32x4 v;
+	const float* xc = x + (r.xoff >= 0 ? r.xoff : 0);
 #pragma unroll
-		for (int e = 0; e < 4; ++e) {
-			const int ih = cc.ihb[e] + r.ph, iw = cc.iwb[e] + r.pw;
-			if (ih >= 0 && ih < cg.h && iw >= 0 && iw < cg.w) v[e] = xc[ih * cg.w + iw];
-		}
+	for (int e = 0; e < 4; ++e) {
+		const int ih = cc.ihb[e] + r.ph, iw = cc.iwb[e] + r.pw;
+		const bool in = r.xoff >= 0 && ih >= 0 && ih < cg.h && iw >= 0 && iw < cg.w;
+		const float t = xc[min(max(ih, 0), cg.h - 1) * cg.w + min(max(iw, 0), cg.w - 1)];
+		v[e] = in ? t : 0.0f;
 	}
 	return v;
 }
