@@ -203,7 +203,101 @@ def _cpu_time_ms(fn, budget_s=3.0, max_runs=15):
     return statistics.median(times)
 
 
+U32 = 2.0 ** -24  # unit roundoff of fp32
+
+
+def _host(t):
+    return t.detach().cpu().numpy()
+
+
+def _repeat_runs(run, times=3):
+    """Runs the op `times` times (run() returns its output tensors); whether every run left the same bits, and the
+    outputs of the first run on the host."""
+    import numpy as np
+    import torch
+    first, same = None, True
+    for _ in range(times):
+        outs = run()
+        torch.cuda.synchronize()
+        cur = [np.array(_host(t), copy=True) for t in outs]
+        if first is None:
+            first = cur
+        else:
+            same = same and all(np.array_equal(a.view(np.uint32), b.view(np.uint32)) for a, b in zip(first, cur))
+    return same, first
+
+
+def _vs_cpu(got, want):
+    """Largest |GPU - nn-cpp| over the outputs, and whether every bit agrees."""
+    import numpy as np
+    bitwise = all(np.array_equal(g.view(np.uint32), w.view(np.uint32)) for g, w in zip(got, want))
+    diff = max(float(np.max(np.abs(g.astype(np.float64) - w.astype(np.float64)))) if g.size else 0.0
+               for g, w in zip(got, want))
+    return diff, bitwise
+
+
+def _vs_f64(got, want, mag=None, terms=None):
+    """Largest |GPU - fp64| and, given the magnitude sum mag = sum |a||b| and the number of product terms per
+    output, the largest error as a fraction of the a-priori bound 4 terms 2^-24 mag (any summation order)."""
+    import numpy as np
+    err = np.abs(got.astype(np.float64) - want)
+    worst = float(err.max()) if err.size else 0.0
+    if mag is None:
+        return worst, None
+    bound = 4.0 * terms * U32 * mag
+    ratio = np.where(bound > 0, err / np.where(bound > 0, bound, 1.0), np.where(err > 0, np.inf, 0.0))
+    return worst, float(ratio.max()) if ratio.size else 0.0
+
+
+def _conv_f64(x, w, b, pad):
+    """Stride-1 convolution in fp64 and its magnitude sum, tap by tap."""
+    import numpy as np
+    N, C, H, W = x.shape
+    O, _, kh, kw = w.shape
+    ho, wo = H + 2 * pad - kh + 1, W + 2 * pad - kw + 1
+    xp = np.pad(x.astype(np.float64), ((0, 0), (0, 0), (pad, pad), (pad, pad)))
+    w64 = w.astype(np.float64)
+    y = np.zeros((N, O, ho, wo))
+    mag = np.zeros_like(y)
+    for i in range(kh):
+        for j in range(kw):
+            win = xp[:, :, i:i + ho, j:j + wo]
+            y += np.einsum("nchw,oc->nohw", win, w64[:, :, i, j], optimize=True)
+            mag += np.einsum("nchw,oc->nohw", np.abs(win), np.abs(w64[:, :, i, j]), optimize=True)
+    y += b.astype(np.float64)[None, :, None, None]
+    mag += np.abs(b.astype(np.float64))[None, :, None, None]
+    return y, mag
+
+
+def _heads(t, heads):
+    import numpy as np
+    N, T, D = t.shape
+    return t.astype(np.float64).reshape(N, T, heads, D // heads).transpose(0, 2, 1, 3)
+
+
+def _attention_f64(q, k, v, g, heads, causal):
+    """Attention forward (out) and backward (dq, dk, dv) in fp64, per head, with the softmax taken exactly."""
+    import numpy as np
+    N, T, D = q.shape
+    scale = 1.0 / np.sqrt(D // heads)
+    qh, kh, vh, gh = (_heads(t, heads) for t in (q, k, v, g))
+    s = (qh @ kh.transpose(0, 1, 3, 2)) * scale
+    if causal:
+        s = np.where(np.triu(np.ones((T, k.shape[1]), bool), 1), -np.inf, s)
+    p = np.exp(s - s.max(-1, keepdims=True))
+    p /= p.sum(-1, keepdims=True)
+    merge = lambda t: t.transpose(0, 2, 1, 3).reshape(N, -1, D)
+    out = merge(p @ vh)
+    dp = gh @ vh.transpose(0, 1, 3, 2)
+    ds = p * (dp - (dp * p).sum(-1, keepdims=True)) * scale
+    return out, (merge(ds @ kh), merge(ds.transpose(0, 1, 3, 2) @ qh), merge(p.transpose(0, 1, 3, 2) @ gh))
+
+
 def report(with_cpu=True):
+    """Every BASELINE.json config on the GPU: time, TFLOP/s or GB/s, roofline fraction, nn-cpp's CPU time, and three
+    checks of the outputs: bit equality over 3 repeated GPU runs, the largest difference from nn-cpp's CPU output
+    on the same inputs (0 = bit for bit), and the largest error against fp64, also as a fraction of the bound
+    4 K 2^-24 (|A||B|)_ij where the op is one product per output (K terms, any order)."""
     import numpy as np
     import torch
 
@@ -219,15 +313,33 @@ def report(with_cpu=True):
     d = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)
     rows = []
 
-    def row(cfg, what, ms, flops=None, nbytes=None, bound="mfma", cpu_ms=None):
+    def row(cfg, what, ms, flops=None, nbytes=None, bound="mfma", cpu_ms=None, repeat=None, cpu_diff=None,
+            f64=None):
         tflops = flops / (ms * 1e-3) / 1e12 if flops else None
         gbps = nbytes / (ms * 1e-3) / 1e9 if nbytes else None
         frac = (tflops / PEAK_FP32_MFMA_TFLOPS) if bound == "mfma" else (gbps / PEAK_HBM_GBPS)
         rows.append({"config": cfg, "what": what, "ms": ms, "tflops": tflops, "gbps": gbps, "bound": bound,
-                     "roofline_frac": frac, "cpu_ms": cpu_ms, "speedup_vs_cpu": (cpu_ms / ms) if cpu_ms else None})
+                     "roofline_frac": frac, "cpu_ms": cpu_ms, "speedup_vs_cpu": (cpu_ms / ms) if cpu_ms else None,
+                     "repeat": repeat, "cpu_diff": cpu_diff, "f64": f64})
         log(f"[{cfg}] {what}: {ms:.4f} ms" + (f", {tflops:.2f} TFLOP/s" if tflops else "") +
             (f", {gbps:.1f} GB/s" if gbps else "") + f", {frac * 100:.1f}% of {bound} peak" +
-            (f"; nn-cpp CPU {cpu_ms:.3f} ms" if cpu_ms else ""))
+            (f"; nn-cpp CPU {cpu_ms:.3f} ms" if cpu_ms else "") +
+            (f"; repeats bitwise {repeat}" if repeat is not None else "") +
+            (f"; vs nn-cpp {cpu_diff[0]:.3g} (bitwise {cpu_diff[1]})" if cpu_diff else "") +
+            (f"; vs fp64 {f64[0]:.3g}" + (f" = {f64[1]:.3g} of the bound" if f64[1] is not None else "")
+             if f64 else ""))
+
+    def worst(pairs):
+        """Combines (abs error, fraction of bound) pairs over several outputs."""
+        return (max(p[0] for p in pairs),
+                None if any(p[1] is None for p in pairs) else max(p[1] for p in pairs))
+
+    def gemm_f64(got, a, b, rows_of=None):
+        """fp64 A B (on a sample of rows for large m) against the GPU's C."""
+        a64, b64 = a.astype(np.float64), b.astype(np.float64)
+        if rows_of is not None:
+            a64, got = a64[rows_of], got[rows_of]
+        return _vs_f64(got, a64 @ b64, np.abs(a64) @ np.abs(b64), a.shape[1])
 
     # config 1: 512^3, NN / TN / NT, seed 0
     n = 512
@@ -235,9 +347,13 @@ def report(with_cpu=True):
     da, db, dc = d(a), d(b), torch.empty((n, n), device=dev)
     c = np.empty((n, n), np.float32)
     for ta, tb, name in ((0, 0, "C=A B"), (1, 0, "C=A^T B"), (0, 1, "C=A B^T")):
-        ms = device_time_ms(lambda: nnh.sgemm(ta, tb, n, n, n, da, n, db, n, dc, n))
+        run = lambda: nnh.sgemm(ta, tb, n, n, n, da, n, db, n, dc, n)
+        ms = device_time_ms(run)
         cpu = _cpu_time_ms(lambda: ref.sgemm_inplace(ta, tb, n, n, n, a, n, b, n, c, n, 0)) if ref else None
-        row(1, f"sgemm 512^3 {name}", ms, flops=2.0 * n ** 3, cpu_ms=cpu)
+        same, (got,) = _repeat_runs(lambda: (run(), dc)[1:])
+        row(1, f"sgemm 512^3 {name}", ms, flops=2.0 * n ** 3, cpu_ms=cpu, repeat=same,
+            cpu_diff=_vs_cpu([got], [c]) if ref else None,
+            f64=gemm_f64(got, a.T if ta else a, b.T if tb else b))
 
     # config 2: MLP 256 x 784 -> 512 -> 256 -> 10, forward (linear + ReLU) and backward (dX, dW, db)
     dims = [784, 512, 256, 10]
@@ -254,32 +370,51 @@ def report(with_cpu=True):
               torch.empty(dims[i + 1], device=dev)) for i in range(3)]
 
     def mlp_fwd():
-        h = acts[0]
+        h, hs = acts[0], []
         for i in range(3):
             h = nnh.linear_forward(h, dws[i], dbs[i], relu=True)
+            hs.append(h)
+        return hs
 
     def mlp_bwd():
         for i in range(3):
             nnh.linear_backward(dgs[i], acts[i], dws[i], *[v for pair in zip(grads[i], (True,) * 3) for v in pair])
+        return [t for gr in grads for t in gr]
 
     fwd_flops = sum(2.0 * 256 * dims[i] * dims[i + 1] for i in range(3))
-    cpu = None
+    cpu, hacts = None, [x]
     if ref:
-        hx = [x] + [None] * 3
+        for i in range(3):
+            hacts.append(np.maximum(ref.linear_forward(hacts[-1], ws[i], bs[i]), np.float32(0)))
 
         def cpu_fwd():
             h = x
             for i in range(3):
                 h = np.maximum(ref.linear_forward(h, ws[i], bs[i]), np.float32(0))
         cpu = _cpu_time_ms(cpu_fwd)
-    row(2, "MLP forward (3 x linear+ReLU)", device_time_ms(mlp_fwd), flops=fwd_flops, cpu_ms=cpu)
-    cpu = None
+    ms = device_time_ms(mlp_fwd)
+    same, hs = _repeat_runs(mlp_fwd)
+    # each layer against fp64 from the GPU's own input to it (ReLU is 1-Lipschitz; the bias is one more term)
+    ins = [x] + hs[:2]
+    f64 = worst([_vs_f64(hs[i], np.maximum(ins[i].astype(np.float64) @ ws[i].T.astype(np.float64) + bs[i], 0),
+                         np.abs(ins[i].astype(np.float64)) @ np.abs(ws[i].T.astype(np.float64)) + np.abs(bs[i]),
+                         dims[i] + 1) for i in range(3)])
+    row(2, "MLP forward (3 x linear+ReLU)", ms, flops=fwd_flops, cpu_ms=cpu, repeat=same,
+        cpu_diff=_vs_cpu(hs, hacts[1:]) if ref else None, f64=f64)
+    cpu, want = None, None
     if ref:
-        hacts = [x]
-        for i in range(3):
-            hacts.append(np.maximum(ref.linear_forward(hacts[-1], ws[i], bs[i]), np.float32(0)))
+        want = [t for i in range(3) for t in ref.linear_backward(hacts[i], ws[i], bs[i], gys[i])]
         cpu = _cpu_time_ms(lambda: [ref.linear_backward(hacts[i], ws[i], bs[i], gys[i]) for i in range(3)])
-    row(2, "MLP backward (dX, dW, db per layer)", device_time_ms(mlp_bwd), flops=2 * fwd_flops, cpu_ms=cpu)
+    ms = device_time_ms(mlp_bwd)
+    same, got = _repeat_runs(mlp_bwd)
+    pairs = []
+    for i in range(3):
+        g64, x64, w64 = gys[i].astype(np.float64), _host(acts[i]).astype(np.float64), ws[i].astype(np.float64)
+        pairs += [_vs_f64(got[3 * i], g64 @ w64, np.abs(g64) @ np.abs(w64), dims[i + 1]),
+                  _vs_f64(got[3 * i + 1], g64.T @ x64, np.abs(g64.T) @ np.abs(x64), 256),
+                  _vs_f64(got[3 * i + 2], g64.sum(0), np.abs(g64).sum(0), 256)]
+    row(2, "MLP backward (dX, dW, db per layer)", ms, flops=2 * fwd_flops, cpu_ms=cpu, repeat=same,
+        cpu_diff=_vs_cpu(got, want) if ref else None, f64=worst(pairs))
 
     # config 3: conv2d_relu, batch 128: conv1 1->32 on 28x28 (memory-bound), conv2 32->64 on 14x14
     xc = synth.mt19937_uniform(2, 128 * 28 * 28, 0.0, 1.0).reshape(128, 1, 28, 28)
@@ -290,13 +425,23 @@ def report(with_cpu=True):
     y1, al1 = nnh.conv2d_forward(dxc, dw1, db1, 1, 1, True)
     x2 = torch.nn.functional.max_pool2d(y1, 2).contiguous()
     hx2 = x2.cpu().numpy()
+
+    def conv_checks(run, x_, w_, b_, terms):
+        same, (got,) = _repeat_runs(run)
+        y64, mag = _conv_f64(x_, w_, b_, 1)
+        cmp = _vs_cpu([got], [ref.conv2d_forward(x_, w_, b_, 1, 1, 1)]) if ref else None
+        return dict(repeat=same, cpu_diff=cmp, f64=_vs_f64(got, np.maximum(y64, 0), mag, terms))
+
     conv1_bytes = 4 * (xc.size + w1.size + b1.size + 128 * 32 * 784)
     cpu = _cpu_time_ms(lambda: ref.conv2d_forward(xc, w1, b1, 1, 1, 1)) if ref else None
-    row(3, "conv1 conv2d_relu fwd (1->32, 28x28, b128)", device_time_ms(lambda: nnh.conv2d_forward(dxc, dw1, db1, 1, 1, True)),
-        flops=2.0 * 128 * 32 * 784 * 9, nbytes=conv1_bytes, bound="hbm", cpu_ms=cpu)
-    row(3, "conv1 conv2d_relu fwd, no alive flags (backward masks with y > 0)",
-        device_time_ms(lambda: nnh.conv2d_forward(dxc, dw1, db1, 1, 1, True, want_alive=False)),
-        flops=2.0 * 128 * 32 * 784 * 9, nbytes=conv1_bytes, bound="hbm")
+    run = lambda: nnh.conv2d_forward(dxc, dw1, db1, 1, 1, True)
+    row(3, "conv1 conv2d_relu fwd (1->32, 28x28, b128)", device_time_ms(run),
+        flops=2.0 * 128 * 32 * 784 * 9, nbytes=conv1_bytes, bound="hbm", cpu_ms=cpu,
+        **conv_checks(lambda: run()[:1], xc, w1, b1, 10))
+    run = lambda: nnh.conv2d_forward(dxc, dw1, db1, 1, 1, True, want_alive=False)
+    row(3, "conv1 conv2d_relu fwd, no alive flags (backward masks with y > 0)", device_time_ms(run),
+        flops=2.0 * 128 * 32 * 784 * 9, nbytes=conv1_bytes, bound="hbm",
+        **conv_checks(lambda: run()[:1], xc, w1, b1, 10))
     # not a BASELINE config: the same layer at batch 2048 shows the kernel's streaming rate once launch and
     # drain latency (about 4 us for any 13 MB launch on this GPU) no longer dominate
     xbig = dxc.repeat(16, 1, 1, 1)
@@ -306,39 +451,72 @@ def report(with_cpu=True):
         bound="hbm")
     del xbig
     cpu = _cpu_time_ms(lambda: ref.conv2d_forward(hx2, w2, b2, 1, 1, 1)) if ref else None
-    row(3, "conv2 conv2d_relu fwd (32->64, 14x14, b128)", device_time_ms(lambda: nnh.conv2d_forward(x2, dw2, db2, 1, 1, True)),
-        flops=2.0 * 128 * 64 * 196 * 288, nbytes=4 * (hx2.size + w2.size + 64 + 128 * 64 * 196), cpu_ms=cpu)
+    run = lambda: nnh.conv2d_forward(x2, dw2, db2, 1, 1, True)
+    row(3, "conv2 conv2d_relu fwd (32->64, 14x14, b128)", device_time_ms(run),
+        flops=2.0 * 128 * 64 * 196 * 288, nbytes=4 * (hx2.size + w2.size + 64 + 128 * 64 * 196), cpu_ms=cpu,
+        **conv_checks(lambda: run()[:1], hx2, w2, b2, 289))
     y2, al2 = nnh.conv2d_forward(x2, dw2, db2, 1, 1, True)
-    g2 = d(synth.normal(32, tuple(y2.shape)))
+    hg2 = synth.normal(32, tuple(y2.shape))
+    g2 = d(hg2)
     gx2, gw2, gb2 = torch.empty_like(x2), torch.empty_like(dw2), torch.empty_like(db2)
-    cpu = None
+    cpu, want = None, None
     if ref:
-        hg2 = g2.cpu().numpy()
+        want = list(ref.conv2d_backward(hx2, w2, b2, 1, 1, 1, hg2))
         cpu = _cpu_time_ms(lambda: ref.conv2d_backward(hx2, w2, b2, 1, 1, 1, hg2))
-    row(3, "conv2 conv2d_relu bwd (dx, dW, db)",
-        device_time_ms(lambda: nnh.conv2d_backward(g2, x2, dw2, al2, 1, 1, gx2, True, gw2, True, gb2, True)),
-        flops=2 * 2.0 * 128 * 64 * 196 * 288, cpu_ms=cpu)
+    run = lambda: nnh.conv2d_backward(g2, x2, dw2, al2, 1, 1, gx2, True, gw2, True, gb2, True)
+    ms = device_time_ms(run)
+    same, got = _repeat_runs(lambda: (run(), gx2, gw2, gb2)[1:])
+    # fp64 gradients of the masked output gradient gm: dx is the transposed convolution (Cout kh kw terms),
+    # dW correlates gm with the padded input (N Ho Wo terms), db sums gm
+    gm = hg2.astype(np.float64) * (_host(y2) > 0)
+    xp = np.pad(hx2.astype(np.float64), ((0, 0), (0, 0), (1, 1), (1, 1)))
+    dx64, dxmag = np.zeros(xp.shape), np.zeros(xp.shape)
+    dw64, dwmag = np.zeros(w2.shape), np.zeros(w2.shape)
+    for i in range(3):
+        for j in range(3):
+            win = xp[:, :, i:i + 14, j:j + 14]
+            dw64[:, :, i, j] = np.einsum("nohw,nchw->oc", gm, win, optimize=True)
+            dwmag[:, :, i, j] = np.einsum("nohw,nchw->oc", np.abs(gm), np.abs(win), optimize=True)
+            dx64[:, :, i:i + 14, j:j + 14] += np.einsum("nohw,oc->nchw", gm, w2[:, :, i, j].astype(np.float64),
+                                                        optimize=True)
+            dxmag[:, :, i:i + 14, j:j + 14] += np.einsum("nohw,oc->nchw", np.abs(gm),
+                                                         np.abs(w2[:, :, i, j].astype(np.float64)), optimize=True)
+    f64 = worst([_vs_f64(got[0], dx64[:, :, 1:15, 1:15], dxmag[:, :, 1:15, 1:15], 64 * 9),
+                 _vs_f64(got[1], dw64, dwmag, 128 * 196),
+                 _vs_f64(got[2], gm.sum((0, 2, 3)), np.abs(gm).sum((0, 2, 3)), 128 * 196)])
+    row(3, "conv2 conv2d_relu bwd (dx, dW, db)", ms, flops=2 * 2.0 * 128 * 64 * 196 * 288, cpu_ms=cpu,
+        repeat=same, cpu_diff=_vs_cpu(got, want) if ref else None, f64=f64)
 
     # config 4: attention 32 x 8 heads x 256 x 64 (+ causal); probs stored, as the reference does
     q, k, v = (synth.normal(3 + i, (32, 256, 512)) for i in range(3))
+    hg = synth.normal(7, (32, 256, 512))
     dq_, dk_, dv_ = d(q), d(k), d(v)
     att_flops = 2 * 2.0 * 32 * 8 * 256 * 256 * 64
+    out64, grads64 = _attention_f64(q, k, v, hg, 8, False)
     for causal in (False, True):
         cpu = _cpu_time_ms(lambda: ref.attention_forward(q, k, v, 8, None, causal), budget_s=4.0, max_runs=5) if ref else None
-        row(4, "attention fwd" + (" causal" if causal else ""),
-            device_time_ms(lambda: nnh.attention_forward(dq_, dk_, dv_, 8, None, causal)), flops=att_flops, cpu_ms=cpu)
+        run = lambda: nnh.attention_forward(dq_, dk_, dv_, 8, None, causal)
+        ms = device_time_ms(run)
+        same, (got,) = _repeat_runs(lambda: run()[:1])
+        want64 = out64 if not causal else _attention_f64(q, k, v, hg, 8, True)[0]
+        row(4, "attention fwd" + (" causal" if causal else ""), ms, flops=att_flops, cpu_ms=cpu, repeat=same,
+            cpu_diff=_vs_cpu([got], [ref.attention_forward(q, k, v, 8, None, causal)]) if ref else None,
+            f64=_vs_f64(got, want64))
     out, probs = nnh.attention_forward(dq_, dk_, dv_, 8, None, False)
-    ga = d(synth.normal(7, (32, 256, 512)))
+    ga = d(hg)
     gq, gk, gv = torch.empty_like(dq_), torch.empty_like(dk_), torch.empty_like(dv_)
-    cpu = None
+    cpu, want = None, None
     if ref:
-        hg = ga.cpu().numpy()
+        want = list(ref.attention_backward(q, k, v, 8, hg))
         cpu = _cpu_time_ms(lambda: ref.attention_backward(q, k, v, 8, hg), budget_s=4.0, max_runs=3)
-    row(4, "attention bwd (dQ, dK, dV)",
-        device_time_ms(lambda: nnh.attention_backward(ga, dq_, dk_, dv_, probs, 8, None, False, gq, True, gk, True, gv, True)),
-        flops=2 * att_flops, cpu_ms=cpu)
+    run = lambda: nnh.attention_backward(ga, dq_, dk_, dv_, probs, 8, None, False, gq, True, gk, True, gv, True)
+    ms = device_time_ms(run)
+    same, got = _repeat_runs(lambda: (run(), gq, gk, gv)[1:])
+    row(4, "attention bwd (dQ, dK, dV)", ms, flops=2 * att_flops, cpu_ms=cpu, repeat=same,
+        cpu_diff=_vs_cpu(got, want) if ref else None, f64=worst([_vs_f64(g_, w_) for g_, w_ in zip(got, grads64)]))
+    del out64, grads64
 
-    # config 5: roofline sweep, seed 4
+    # config 5: roofline sweep, seed 4; fp64 on 256 evenly spaced rows when m >= 2048
     for (m, n_, k_) in ((1024, 1024, 1024), (2048, 2048, 2048), (4096, 4096, 4096), (8192, 8192, 8192),
                         (64, 4096, 4096), (4096, 4096, 64)):
         a, b = synth.uniform_operands(4, [(m, k_), (k_, n_)])
@@ -347,18 +525,27 @@ def report(with_cpu=True):
         reps = 5 if m * n_ * k_ >= 8192 ** 3 else 20
         cpu = _cpu_time_ms(lambda: ref.sgemm_inplace(0, 0, m, n_, k_, a, k_, b, n_, c, n_, 0),
                            budget_s=6.0, max_runs=5) if ref else None
-        row(5, f"sgemm {m}x{n_}x{k_}", device_time_ms(lambda: nnh.sgemm(0, 0, m, n_, k_, da, k_, db, n_, dc, n_), reps=reps),
-            flops=2.0 * m * n_ * k_, cpu_ms=cpu)
+        run = lambda: nnh.sgemm(0, 0, m, n_, k_, da, k_, db, n_, dc, n_)
+        ms = device_time_ms(run, reps=reps)
+        same, (got,) = _repeat_runs(lambda: (run(), dc)[1:])
+        sample = np.linspace(0, m - 1, 256).astype(np.int64) if m >= 2048 else None
+        row(5, f"sgemm {m}x{n_}x{k_}", ms, flops=2.0 * m * n_ * k_, cpu_ms=cpu, repeat=same,
+            cpu_diff=_vs_cpu([got], [c]) if ref else None, f64=gemm_f64(got, a, b, sample))
+        del got, c
 
     lines = [f"GPU: {torch.cuda.get_device_name(0)}; nn-cpp CPU baseline: NN_NATIVE AVX2 build, {threads} threads on "
              f"{cpu_model()}", "",
-             "| cfg | workload | GPU ms | TFLOP/s | GB/s | bound | % of roofline | nn-cpp CPU ms | GPU speedup |",
-             "|---|---|---|---|---|---|---|---|---|"]
+             "| cfg | workload | GPU ms | TFLOP/s | GB/s | bound | % of roofline | nn-cpp CPU ms | GPU speedup | "
+             "3 GPU runs | max abs diff vs nn-cpp | max abs err vs fp64 | err / bound |",
+             "|---|---|---|---|---|---|---|---|---|---|---|---|---|"]
     for r in rows:
         f = lambda v, fmt: (fmt % v) if v is not None else "-"
+        rep = "-" if r["repeat"] is None else ("bitwise equal" if r["repeat"] else "DIFFER")
+        cd = "-" if r["cpu_diff"] is None else ("0 (bitwise)" if r["cpu_diff"][1] else "%.3g" % r["cpu_diff"][0])
+        fe = r["f64"] or (None, None)
         lines.append(f"| {r['config']} | {r['what']} | {r['ms']:.4f} | {f(r['tflops'], '%.2f')} | {f(r['gbps'], '%.0f')} | "
                      f"{r['bound']} | {r['roofline_frac'] * 100:.1f}% | {f(r['cpu_ms'], '%.3f')} | "
-                     f"{f(r['speedup_vs_cpu'], '%.0fx')} |")
+                     f"{f(r['speedup_vs_cpu'], '%.0fx')} | {rep} | {cd} | {f(fe[0], '%.3g')} | {f(fe[1], '%.3g')} |")
     print("\n".join(lines), flush=True)
 
 
