@@ -55,7 +55,7 @@ struct Mfma<kMf32> {
 	using Acc = f32x32;
 	__device__ static int arow(int l) { return l; }
 	__device__ static int bcol(int l) { return l & 31; }
-	__device__ static int crow(int r, int l) { return 32 * (r >> 4) + 8 * ((r & 15) >> 2) + 4 * (l >> 5) + (r & 3); }
+	__host__ __device__ static constexpr int crow(int r, int l) { return 32 * (r >> 4) + 8 * ((r & 15) >> 2) + 4 * (l >> 5) + (r & 3); }
 	__device__ static int ccol(int l) { return l & 31; }
 	__device__ static Acc mma(float a, float b, const Acc& c) { return __builtin_amdgcn_mfma_f32_32x32x1f32(a, b, c, 0, 0, 0); }
 };
@@ -66,7 +66,7 @@ struct Mfma<kMf16> {
 	using Acc = f32x16;
 	__device__ static int arow(int l) { return l; }
 	__device__ static int bcol(int l) { return l & 15; }
-	__device__ static int crow(int r, int l) { return 16 * (r >> 2) + 4 * (l >> 4) + (r & 3); }
+	__host__ __device__ static constexpr int crow(int r, int l) { return 16 * (r >> 2) + 4 * (l >> 4) + (r & 3); }
 	__device__ static int ccol(int l) { return l & 15; }
 	__device__ static Acc mma(float a, float b, const Acc& c) { return __builtin_amdgcn_mfma_f32_16x16x1f32(a, b, c, 0, 0, 0); }
 };
@@ -77,7 +77,7 @@ struct Mfma<kMf4> {
 	using Acc = f32x4;
 	__device__ static int arow(int l) { return 4 * (l >> 4) + (l & 3); }
 	__device__ static int bcol(int l) { return 4 * ((l >> 2) & 3) + (l & 3); }
-	__device__ static int crow(int r, int l) { return 4 * (l >> 4) + r; }
+	__host__ __device__ static constexpr int crow(int r, int l) { return 4 * (l >> 4) + r; }
 	__device__ static int ccol(int l) { return 4 * ((l >> 2) & 3) + (l & 3); }
 	__device__ static Acc mma(float a, float b, const Acc& c) { return __builtin_amdgcn_mfma_f32_4x4x1f32(a, b, c, 0, 0, 0); }
 };
@@ -235,6 +235,16 @@ __device__ __forceinline__ f32x4 col_values(const float* __restrict__ x, const C
 	return v;
 }
 
+// Whether every accumulator register r of an MFMA unit stays, for all 64 lanes, inside the pass of RP rows that
+// lane 0 puts it in (the interior epilogue stages one pass at a time).
+template <int MF>
+__host__ __device__ constexpr bool passes_split_evenly(int rp) {
+	for (int r = 0; r < Mfma<MF>::NV; ++r)
+		for (int l = 0; l < 64; ++l)
+			if (Mfma<MF>::crow(r, l) / rp != Mfma<MF>::crow(r, 0) / rp) return false;
+	return Mfma<MF>::UM % rp == 0;
+}
+
 template <int BM, int BN, int BK, int WM, int WN, int MF, bool TA, bool TB>
 struct TileShape {
 	static constexpr int kWavesN = BN / WN;
@@ -264,7 +274,7 @@ __device__ __forceinline__ int xcd_remap(int bid, int total) {
 }
 
 template <int BM, int BN, int BK, int WM, int WN, int WPE, int MF, bool TA, bool TB, bool EDGE, bool GB = false>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE))) sgemm_tile_kernel(const GemmArgs p) {
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE, WPE))) sgemm_tile_kernel(const GemmArgs p) {
 	static_assert(!GB || (!TA && EDGE), "the implicit im2col operand is B, loaded with bounds checks");
 	using S = TileShape<BM, BN, BK, WM, WN, MF, TA, TB>;
 	using U = Mfma<MF>;
@@ -471,6 +481,70 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE)))
 	const bool add_old_at_end = acc_mode && p.k <= kAccAfter;
 	float* __restrict__ Cp = p.c + oc;
 	unsigned char* alive = p.ep.alive ? p.ep.alive + oc : nullptr;
+	if constexpr (!EDGE) {
+		// Interior tiles (C 16-byte aligned, ldc a multiple of 4): each wave passes its accumulators through its own
+		// slice of the operand LDS (free after the depth loop's last barrier), RP rows of one MFMA row-block at a
+		// time, and writes C as 16-byte stores of 4 consecutive columns; the epilogue is applied per element.
+		constexpr int kPerWave = S::kLdsFloats / 4;
+		constexpr int LS = WN + 4;
+		constexpr int RP = (MF == kMf4) ? 16 : (U::UM * LS <= kPerWave ? U::UM : (U::UM / 2 * LS <= kPerWave ? U::UM / 2 : 16));
+		static_assert(RP * LS <= kPerWave, "an epilogue pass must fit in the wave's LDS slice");
+		static_assert(passes_split_evenly<MF>(RP), "a register's pass must not depend on the lane");
+		constexpr int kChunks = RP * WN / 4;        // 4-column groups in one pass
+		constexpr int kRowChunks = WN / 4;
+		float* st = lds + wave * kPerWave;
+		const bool plain = !add_old_at_end && p.ep.bias_mode == kBiasNone && !p.ep.relu;
+#pragma unroll
+		for (int i = 0; i < I; ++i)
+#pragma unroll
+			for (int pass = 0; pass < U::UM / RP; ++pass) {
+				// a register's pass does not depend on the lane: every lane-dependent row offset stays inside it
+#pragma unroll
+				for (int j = 0; j < J; ++j)
+#pragma unroll
+					for (int r = 0; r < U::NV; ++r) {
+						if (U::crow(r, 0) / RP != pass) continue;
+						st[(U::crow(r, lane_e) - pass * RP) * LS + U::UN * j + U::ccol(lane_e)] = acc[i][j][r];
+					}
+				static_assert(kChunks % 64 == 0, "a pass is a whole number of 16-byte stores per lane");
+				if (plain) {
+#pragma unroll
+					for (int t = 0; t < kChunks / 64; ++t) {
+						const int ch = lane_e + 64 * t;
+						const int lr = ch / kRowChunks, c4 = (ch % kRowChunks) * 4;
+						const int row = m0 + wm0 + U::UM * i + pass * RP + lr, col = n0 + wn0 + c4;
+						*reinterpret_cast<f32x4*>(Cp + (int64_t)row * p.ldc + col) =
+							*reinterpret_cast<const f32x4*>(st + lr * LS + c4);
+					}
+					continue;
+				}
+#pragma unroll
+				for (int t = 0; t < kChunks / 64; ++t) {
+					const int ch = lane_e + 64 * t;
+					const int lr = ch / kRowChunks, c4 = (ch % kRowChunks) * 4;
+					f32x4 v = *reinterpret_cast<const f32x4*>(st + lr * LS + c4);
+					const int row = m0 + wm0 + U::UM * i + pass * RP + lr, col = n0 + wn0 + c4;
+					const int64_t off = (int64_t)row * p.ldc + col;
+					if (add_old_at_end) {
+						const f32x4 old = *reinterpret_cast<const f32x4*>(Cp + off);
+#pragma unroll
+						for (int e = 0; e < 4; ++e) v[e] = (p.k > 0) ? old[e] + v[e] : old[e];
+					}
+#pragma unroll
+					for (int e = 0; e < 4; ++e) {
+						if (p.ep.bias_mode == kBiasCol) v[e] = v[e] + p.ep.bias[col + e];
+						else if (p.ep.bias_mode == kBiasRow) v[e] = v[e] + p.ep.bias[row];
+						if (p.ep.relu) {
+							const bool on = v[e] > 0.0f;
+							if (alive) alive[off + e] = on ? 1 : 0;
+							v[e] = on ? v[e] : 0.0f;
+						}
+					}
+					*reinterpret_cast<f32x4*>(Cp + off) = v;
+				}
+			}
+		return;
+	}
 #pragma unroll
 	for (int i = 0; i < I; ++i)
 #pragma unroll
