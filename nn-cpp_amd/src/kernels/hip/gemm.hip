@@ -69,9 +69,10 @@ hipError_t prepare_device() {
 	const Config* cfg = configs();
 	for (int i = 0; i < kNumConfigs; ++i)
 		for (int f = 0; f < 4; ++f)
-			for (int edge = 0; edge < 3; ++edge) {
+			for (int edge = 0; edge < 5; ++edge) {
 				if (edge == 2 && f >= 2) continue;  // gather kernels: A not transposed
-				const KernelFn fn = edge < 2 ? cfg[i].fn[f][edge] : cfg[i].gather_fn[f];
+				if (edge >= 3 && f != 2) continue;  // row-sum kernels: transposed A, plain B
+				const KernelFn fn = edge < 2 ? cfg[i].fn[f][edge] : edge == 2 ? cfg[i].gather_fn[f] : cfg[i].rowsum_fn[edge - 3];
 				e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize,
 				                        cfg[i].lds_bytes[f]);
 				if (e != hipSuccess) return e;
@@ -158,6 +159,9 @@ hipError_t gemm_launch(const GemmCall& g, hipStream_t s, int config, float* work
 	p.col = g.col;
 	if (g.gather && g.ta) return hipErrorInvalidValue;
 	const bool cut = depth_cut(g.m, g.n, g.k);
+	if (g.rowsum && (cut || g.batch_count != 1 || g.gather || !g.ta || g.tb)) return hipErrorInvalidValue;
+	p.rowsum = g.rowsum;
+	p.rowsum_combine = g.rowsum_combine;
 	p.pieces = cut ? (int)((g.k + 127) / 128) : 1;
 	p.piece_k = cut ? 128 : (int)std::max<int64_t>(g.k, 1);
 	// 16-byte operand loads need 16-byte rows and strides (a gathered B is read element by element)
@@ -186,7 +190,7 @@ hipError_t gemm_launch(const GemmCall& g, hipStream_t s, int config, float* work
 	const int64_t blocks = (int64_t)p.tiles_m * p.tiles_n * p.pieces * p.batch_count;
 	if (blocks > 0x7fffffff) return hipErrorInvalidConfiguration;
 	const int f = (g.ta ? 2 : 0) + (g.tb ? 1 : 0);
-	const KernelFn fn = g.gather ? cf.gather_fn[g.tb ? 1 : 0] : cf.fn[f][interior ? 0 : 1];
+	const KernelFn fn = g.gather ? cf.gather_fn[g.tb ? 1 : 0] : g.rowsum ? cf.rowsum_fn[interior ? 0 : 1] : cf.fn[f][interior ? 0 : 1];
 	hipLaunchKernelGGL(fn, dim3((unsigned)blocks), dim3(256), cf.lds_bytes[f], s, p);
 	e = hipGetLastError();
 	if (e == hipSuccess && cut) {

@@ -26,6 +26,8 @@ struct GemmCall {
 	Epilogue ep{};
 	bool gather = false;      // B is each sample's im2col columns, read from the convolution input b (ColGather)
 	ColGather col{};
+	float* rowsum = nullptr;  // optional row sums of op(A) (GemmArgs::rowsum); A transposed, B not, one matrix, no depth cut
+	int rowsum_combine = 0;
 };
 
 // nn-cpp's depth-cut rule (src/kernels/gemm.cpp:453-458): small output, long depth -> 128-deep pieces

@@ -14,6 +14,7 @@ struct Config {
 	int lds_bytes[4];   // per operand layout (ta * 2 + tb)
 	KernelFn fn[4][2];  // [ta * 2 + tb][edge]
 	KernelFn gather_fn[2];  // B gathered as im2col columns (ColGather), A not transposed: [tb]
+	KernelFn rowsum_fn[2];  // transposed A, plain B, with row sums of op(A) (GemmArgs::rowsum): [edge]
 };
 
 template <int BM, int BN, int BK, int WM, int WN, int WPE, int MF = kMf32>
@@ -34,6 +35,8 @@ Config make_config(const char* name) {
 #undef NNH_SET
 	c.gather_fn[0] = sgemm_tile_kernel<BM, BN, BK, WM, WN, WPE, MF, false, false, true, true>;
 	c.gather_fn[1] = sgemm_tile_kernel<BM, BN, BK, WM, WN, WPE, MF, false, true, true, true>;
+	c.rowsum_fn[0] = sgemm_tile_kernel<BM, BN, BK, WM, WN, WPE, MF, true, false, false, false, true>;
+	c.rowsum_fn[1] = sgemm_tile_kernel<BM, BN, BK, WM, WN, WPE, MF, true, false, true, false, true>;
 	return c;
 }
 

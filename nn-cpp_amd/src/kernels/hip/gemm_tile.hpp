@@ -128,6 +128,11 @@ struct GemmArgs {
 	BatchDesc batch;
 	Epilogue ep;
 	ColGather col;     // used by the GB (gather) kernels only
+	// optional: rowsum[i] = the sum of row i of op(A) over k, in k order from +0 (Tensor::sum(0) of A's
+	// transpose, tensor.cpp:422-456), computed by the first column tile; transposed A, single matrix, no depth cut.
+	// combine: 0 store s, 1 store s + 0.0f, 2 rowsum[i] += s
+	float* rowsum;
+	int rowsum_combine;
 };
 
 __device__ __forceinline__ void batch_offsets(const BatchDesc& d, int64_t bi, int64_t& oa, int64_t& ob,
@@ -273,9 +278,12 @@ __device__ __forceinline__ int xcd_remap(int bid, int total) {
 	return bid;
 }
 
-template <int BM, int BN, int BK, int WM, int WN, int WPE, int MF, bool TA, bool TB, bool EDGE, bool GB = false>
+template <int BM, int BN, int BK, int WM, int WN, int WPE, int MF, bool TA, bool TB, bool EDGE, bool GB = false,
+          bool RS = false>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE, WPE))) sgemm_tile_kernel(const GemmArgs p) {
 	static_assert(!GB || (!TA && EDGE), "the implicit im2col operand is B, loaded with bounds checks");
+	static_assert(!RS || (TA && !TB && !GB), "row sums are compiled for the weight-gradient layout only");
+	static_assert(!RS || (BM & (BM - 1)) == 0, "row sums index rows as tid % BM");
 	using S = TileShape<BM, BN, BK, WM, WN, MF, TA, TB>;
 	using U = Mfma<MF>;
 	constexpr int I = S::I, J = S::J;
@@ -407,17 +415,33 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE, W
 			}
 		}
 	};
+	// Row sums of op(A) (see GemmArgs::rowsum; RS kernels, the weight-gradient layout): every thread folds row
+	// tid % BM of each depth tile in k order, four values per MFMA group, read with that group's fragments, with
+	// no branch; the first column tile's threads tid < BM store them. Depth past k is zero-filled by the edge
+	// loader, and adding +0 leaves the sum unchanged (it starts at +0, so it is never -0).
+	float rsum = 0.0f;
+	auto read_rowsum = [&](const float* As, int kk) {
+		f32x4 v;
+#pragma unroll
+		for (int e = 0; e < 4; ++e) v[e] = As[(kk + e) * S::SA + (tid & (BM - 1))];
+		return v;
+	};
 	auto mma_tile = [&](int buf) {
 		const float* As = lds + buf * S::kStage;
 		const float* Bs = As + S::kASize;
 		f32x4 af[2][I], bf[2][J];
+		[[maybe_unused]] f32x4 rs[2];
 		read_frags(As, Bs, 0, af[0], bf[0]);
+		if constexpr (RS) rs[0] = read_rowsum(As, 0);
 #pragma unroll
 		for (int kk = 0; kk < BK; kk += 4) {
 			const int cur = (kk >> 2) & 1;
 			// issue the next group's LDS reads before this group's MFMAs, so their latency is hidden;
 			// the scheduling fences stop the compiler from sinking them back next to their uses
-			if (kk + 4 < BK) read_frags(As, Bs, kk + 4, af[cur ^ 1], bf[cur ^ 1]);
+			if (kk + 4 < BK) {
+				read_frags(As, Bs, kk + 4, af[cur ^ 1], bf[cur ^ 1]);
+				if constexpr (RS) rs[cur ^ 1] = read_rowsum(As, kk + 4);
+			}
 			__builtin_amdgcn_sched_barrier(0);
 #pragma unroll
 			for (int e = 0; e < 4; ++e)
@@ -426,6 +450,10 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE, W
 #pragma unroll
 					for (int j = 0; j < J; ++j)
 						acc[i][j] = U::mma(af[cur][i][e], bf[cur][j][e], acc[i][j]);
+			if constexpr (RS) {
+#pragma unroll
+				for (int e = 0; e < 4; ++e) rsum = rsum + rs[cur][e];
+			}
 			__builtin_amdgcn_sched_barrier(0);
 		}
 	};
@@ -461,6 +489,10 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE, W
 				}
 	}
 	for (int kt = n1; kt < nkt; ++kt) step(kt);
+	if (RS && p.rowsum != nullptr && tn == 0 && p.pieces == 1 && tid < BM && m0 + tid < p.m) {
+		float* d = p.rowsum + m0 + tid;
+		*d = p.rowsum_combine == 0 ? rsum : (p.rowsum_combine == 1 ? rsum + 0.0f : *d + rsum);
+	}
 
 	// ---- epilogue ---- (the fenced lane keeps the store addresses from being computed before the loop)
 	int lane_e = lane;

@@ -51,13 +51,22 @@ int nnh_linear_backward(const float* g, const float* x, const float* w, const si
 		rc = run_gemm(call, stream, -1);
 		if (rc != NNH_OK) return rc;
 	}
+	// db of a 2-D gradient is one Tensor::sum(0): each column of G folded over the rows in order from +0, which is
+	// the row sum of op(A) = G^T over k in the dW product, so that product computes it on the way
+	const bool db_in_dw = dw && db && nlead == 1 && M > 0 && K > 0 && n > 0 && !depth_cut((int64_t)n, (int64_t)K, (int64_t)M) &&
+	                      !ranges_overlap(db, n * 4, dw, (uint64_t)n * K * 4) && !ranges_overlap(db, n * 4, g, (uint64_t)M * n * 4) &&
+	                      !ranges_overlap(db, n * 4, x, (uint64_t)M * K * 4);
 	if (dw) {  // dW = G^T X (ops.cpp:741)
 		int rc = build_gemm(1, 0, n, K, M, g, n, x, K, dw, K, !dw_first, nullptr, nullptr, call);
 		if (rc != NNH_OK) return rc;
+		if (db_in_dw) {
+			call.rowsum = db;
+			call.rowsum_combine = db_first ? 1 : 2;
+		}
 		rc = run_gemm(call, stream, -1);
 		if (rc != NNH_OK) return rc;
 	}
-	if (db && n > 0) {
+	if (db && n > 0 && !db_in_dw) {
 		// accumulate_grad(bias, G): Tensor::sum(0) once per leading axis (ops.cpp:35-53), then stored as
 		// s + 0.0f into a fresh gradient or added (ops.cpp:85-99)
 		if (M > 0 && !g) return fail(NNH_ERR_INVALID, "G is null");

@@ -114,6 +114,45 @@ def test_linear_first_write_overwrites(gpu, oracle):
         same(host(t), wv, key)
 
 
+def test_linear_bias_gradient_in_weight_product(gpu, oracle):
+    """db of a 2-D gradient is folded inside the dW = G^T X product (the row sums of op(A), in k order from +0);
+    other cases keep the separate Tensor::sum(0). Both combines (store s + 0.0f, add to the old db), edge and
+    interior tiles, several row tiles, depths that are not a multiple of the depth tile, weight gradients large
+    enough for the 64 x 64 and 128 x 128 tile configurations, a product that takes nn-cpp's depth cut (db
+    computed apart: 32 x 64 outputs, 1024 deep), a 3-D gradient (two sums), and special values in G."""
+    import torch
+
+    import nnh
+    cases = [  # (batch rows M, in K, out n, leading shape)
+        (300, 70, 40, None), (256, 784, 512, None), (256, 256, 10, None), (64, 128, 96, None),
+        (37, 33, 129, None), (1024, 64, 32, None), (64, 1024, 1024, None), (16, 2048, 4096, None),
+        (6, 50, 70, (2, 3)),
+    ]
+    for ci, (M, K, n, lead) in enumerate(cases):
+        x = synth.mt19937_uniform(1000 + ci, M * K).reshape(M, K)
+        w = synth.mt19937_uniform(1100 + ci, n * K).reshape(n, K)
+        gr = synth.normal(1200 + ci, (M, n))
+        if ci == 4:
+            gr[3, 0] = np.inf
+            gr[5, 1] = np.nan
+            gr[:, 2] = -0.0
+            gr[7, 3], gr[9, 3] = np.inf, -np.inf
+        shape_x = (lead + (K,)) if lead else (M, K)
+        shape_g = (lead + (n,)) if lead else (M, n)
+        for first in (True, False):
+            dx0 = synth.mt19937_uniform(1300 + ci, M * K).reshape(shape_x)
+            dw0 = synth.mt19937_uniform(1400 + ci, n * K).reshape(n, K)
+            db0 = synth.mt19937_uniform(1500 + ci, n)
+            dx, dw, db = dev(dx0), dev(dw0), dev(db0)
+            nnh.linear_backward(dev(gr.reshape(shape_g)), dev(x.reshape(shape_x)), dev(w), dx, first, dw, first,
+                                db, first)
+            want = oracle.linear_backward(gr.reshape(shape_g), x.reshape(shape_x), w, dx=dx0.copy(), dx_first=first,
+                                          dw=dw0.copy(), dw_first=first, db=db0.copy(), db_first=first)
+            # a NaN made by the arithmetic (inf - inf) has no defined sign bit: x86 and the GPU differ there
+            for t, wv, key in zip((dx, dw, db), want, ("dx", "dw", "db")):
+                assert_same(host(t), wv, (M, K, n, lead, first, key), nan_equal=(ci == 4))
+
+
 def test_relu_node(gpu, oracle):
     import torch
 
