@@ -89,6 +89,8 @@ int nnh_conv2d_forward(const float* x, size_t N, size_t Cin, size_t H, size_t W,
 	unsigned char* al = fuse_relu ? alive : nullptr;
 	if (K <= kDirectMaxK)
 		return hip_status(conv_direct(x, w, bias, y, al, g, (int64_t)N, (int)Cout, fuse_relu ? 1 : 0, s), "conv2d direct");
+	if (conv_fwd3_ok(g, (int64_t)N, (int)Cout, y, al))
+		return hip_status(conv_fwd3(x, w, bias, y, al, g, (int64_t)N, (int)Cout, fuse_relu ? 1 : 0, s), "conv2d 3x3");
 	// Y_n = W col_n (ops.cpp:1395), W shared by every sample, col_n gathered from x_n
 	nnh_batch b{};
 	b.ndim = 1;

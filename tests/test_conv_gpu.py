@@ -179,6 +179,55 @@ def test_conv_shape_errors(gpu):
         nnh.conv2d_forward(x, torch.zeros((1, 1, 2, 2), device="cuda"), b, 0, 0, False)
 
 
+def test_conv3x3_lds_path(gpu, oracle):
+    """3x3, stride 1, padding 1 on planes up to 14 x 14 with Cout a multiple of 32 and H*W a multiple of 4 runs
+    as MFMA chains over the input held in LDS: tiny and rectangular planes, one to fifty input channels, several
+    32-channel groups, ReLU on and off, special values in x, w and the bias. A product that takes nn-cpp's depth
+    cut (Cin = 60: K = 540, 32 x 64 outputs), H*W = 49 and an unaligned y take the GEMM path instead: same bits."""
+    import torch
+
+    import nnh
+    cases = [(2, 32, 14, 14, 64), (3, 1, 2, 2, 32), (2, 7, 12, 10, 96), (1, 50, 14, 14, 32), (2, 3, 9, 4, 32),
+             (1, 60, 8, 8, 32), (2, 3, 7, 7, 32)]
+    for ci, (N, Cin, H, W, Cout) in enumerate(cases):
+        x = synth.mt19937_uniform(300 + ci, N * Cin * H * W).reshape(N, Cin, H, W) * 2 - 1
+        w = synth.normal(310 + ci, (Cout, Cin, 3, 3))
+        b = synth.mt19937_uniform(320 + ci, Cout) - np.float32(0.5)
+        for relu in (False, True):
+            y, alive = nnh.conv2d_forward(dev(x), dev(w), dev(b), 1, 1, relu)
+            wy, wa = oracle.conv2d_forward(x, w, b, 1, 1, relu)
+            same(host(y), wy, (N, Cin, H, W, Cout, relu))
+            if relu:
+                same(host(alive), wa, ("alive", N, Cin, H, W, Cout))
+    # special values: an infinite or NaN weight or input, -0 inputs and biases; a padding tap is fma(w, 0, acc)
+    N, Cin, H, W, Cout = 2, 5, 14, 14, 64
+    x = synth.mt19937_uniform(330, N * Cin * H * W).reshape(N, Cin, H, W)
+    x[0, 1, 5, 5], x[1, 2, 0, 0], x[1, 3, 13, 13], x[0, 4, 7, 2] = np.inf, np.nan, -0.0, -np.inf
+    w = synth.normal(331, (Cout, Cin, 3, 3))
+    w[3, 0, 0, 0], w[17, 2, 1, 1], w[40, 4, 2, 2], w[63, 1, 0, 2] = np.inf, np.nan, -0.0, -np.inf
+    b = synth.mt19937_uniform(332, Cout)
+    b[5], b[6] = -0.0, 0.0
+    for relu in (False, True):
+        y, alive = nnh.conv2d_forward(dev(x), dev(w), dev(b), 1, 1, relu)
+        wy, wa = oracle.conv2d_forward(x, w, b, 1, 1, relu)
+        same(host(y), wy, ("special values", relu))
+        if relu:
+            same(host(alive), wa, "special values alive")
+    # an output view that is not 16-byte aligned: the GEMM path
+    N, Cin, H, W, Cout = 2, 4, 14, 14, 32
+    x = synth.mt19937_uniform(340, N * Cin * H * W).reshape(N, Cin, H, W)
+    w = synth.normal(341, (Cout, Cin, 3, 3))
+    b = synth.mt19937_uniform(342, Cout)
+    buf = torch.zeros(N * Cout * H * W + 1, device="cuda")
+    yv = buf[1:]
+    dx, dw, db = dev(x), dev(w), dev(b)  # held until the kernel has run
+    rc = nnh.lib().nnh_conv2d_forward(nnh._ptr(dx), N, Cin, H, W, nnh._ptr(dw), Cout, 3, 3, nnh._ptr(db), 1, 1,
+                                      0, nnh._ptr(yv), None, nnh._stream(None))
+    nnh.check(rc)
+    wy, _ = oracle.conv2d_forward(x, w, b, 1, 1, False)
+    same(host(yv).reshape(wy.shape), wy, "unaligned y")
+
+
 def test_same_width_quad_path(gpu, oracle):
     """Stride 1, kw = 2 pad + 1, W % 4 == 0 takes the 4-pixels-per-lane direct kernel: every pad 0..4, several
     input channels, Cout not a multiple of the channel group, kh != kw, rows that straddle waves (W = 28: a wave
