@@ -20,6 +20,15 @@ hipError_t col2im(const float* col, float* dx, const ConvGeom& g, int64_t sample
 bool conv_fwd3_ok(const ConvGeom& g, int64_t samples, int cout, const float* y, const unsigned char* alive);
 hipError_t conv_fwd3(const float* x, const float* w, const float* bias, float* y, unsigned char* alive,
                      const ConvGeom& g, int64_t samples, int cout, int relu, hipStream_t s);
+// The per-sample weight gradients dW_n = g_n col_n^T of the same convolutions (conv_dw3.hip; Cout a multiple of
+// 64, K = Cin*9 <= 384, hw % 4 == 0, 16-byte aligned gradient), into gw {N, Cout, K}: whether it takes them, and
+// the launch. With alive (4-byte aligned), the gradient is masked as it is read and the masked gradient is written
+// to gmo (16-byte aligned); with gb, gb {N, Cout} receives the per-sample bias gradients (lane sums of the masked
+// rows).
+bool conv_dw3_ok(const ConvGeom& g, int64_t samples, int cout, const float* gr, const unsigned char* alive,
+                 const float* gmo);
+hipError_t conv_dw3(const float* gr, const unsigned char* alive, float* gmo, float* gb, const float* x, float* gw,
+                    const ConvGeom& g, int64_t samples, int cout, hipStream_t s);
 hipError_t conv_direct(const float* x, const float* w, const float* bias, float* y, unsigned char* alive,
                        const ConvGeom& g, int64_t samples, int cout, int relu, hipStream_t s);
 // The direct kernel's vectorised form (stride 1, "same" width, w % 4 == 0, aligned buffers), with an explicit

@@ -48,7 +48,7 @@ struct F3Args {
 template <int CH>  // most input channels in one staging half
 __global__ void __launch_bounds__(256) conv_fwd3_kernel(const F3Args a) {
 	extern __shared__ __align__(16) float sm[];
-	const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+	const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
 	const int n = blockIdx.x / a.groups, co0 = (blockIdx.x - n * a.groups) * kF3Co;
 	const int K = a.cin * 9, hw = a.height * a.width;
 	float* xs = sm;                       // [cin][16][16], zero outside the image
@@ -85,16 +85,17 @@ __global__ void __launch_bounds__(256) conv_fwd3_kernel(const F3Args a) {
 	auto store_half = [&](int cb, int ce) {
 		const int x0 = cb * kF3Plane, nx = (ce - cb) * kF3Plane;
 		const int nw = (ce - cb) * 9 * kF3Co;
+		// nx is a multiple of 256, so slot u is in range for every thread exactly when 256 u < nx (uniform); for W
+		// the test is uniform whenever the whole round is in range
 #pragma unroll
 		for (int u = 0; u < kX; ++u)
-			if (tid + 256 * u < nx) xs[x0 + tid + 256 * u] = xv[u];
+			if (256 * u < nx) xs[x0 + tid + 256 * u] = xv[u];
 #pragma unroll
 		for (int u = 0; u < kW; ++u) {
 			const int e = tid + 256 * u;
-			if (e < nw) {
-				const int j = (int)fdiv((unsigned)e, a.spandiv[cb == 0 ? 0 : 1]), kk = e - j * (ce - cb) * 9;
-				ws[(cb * 9 + kk) * kF3WLd + j] = wv[u];
-			}
+			const int j = (int)fdiv((unsigned)e, a.spandiv[cb == 0 ? 0 : 1]), kk = e - j * (ce - cb) * 9;
+			if (256 * (u + 1) <= nw) ws[(cb * 9 + kk) * kF3WLd + j] = wv[u];
+			else if (e < nw) ws[(cb * 9 + kk) * kF3WLd + j] = wv[u];
 		}
 	};
 	load_half(0, c1);

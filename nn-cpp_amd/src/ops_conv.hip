@@ -137,20 +137,24 @@ int nnh_conv2d_backward(const float* g, const float* x, const float* w, const un
 	StreamWorkspace ws(s, plan.total);
 	if (ws.error() != hipSuccess) return hip_status(ws.error(), "conv2d workspace");
 	float* partials = part ? ws.at<float>(off_part) : nullptr;
-	const float* gm = g;
+	float* m = alive ? ws.at<float>(off_m) : nullptr;
 	float* gb = db ? ws.at<float>(off_gb) : nullptr;
-	if (alive) {  // ops.cpp:1439-1443, with the per-sample bias sums of ops.cpp:1445 in the same pass
-		float* m = ws.at<float>(off_m);
+	float* gw = dw ? ws.at<float>(off_gw) : nullptr;
+	const float* gm = alive ? m : g;
+	// 3x3, stride 1, padding 1 on small planes: one kernel takes the mask (ops.cpp:1439-1443), the per-sample bias
+	// sums (1445) and the per-sample weight gradients (1448-1449) with its operands in LDS
+	const bool dw3 = dw && conv_dw3_ok(geo, (int64_t)N, (int)Cout, g, alive, m);
+	if (dw3) {
+		rc = hip_status(conv_dw3(g, alive, m, gb, x, gw, geo, (int64_t)N, (int)Cout, s), "conv2d mask, db, dw 3x3");
+	} else if (alive) {  // ops.cpp:1439-1443, with the per-sample bias sums of ops.cpp:1445 in the same pass
 		rc = db ? hip_status(masked_lane_sums(g, alive, m, (int64_t)(N * Cout), (int64_t)hw, gb, s), "conv2d mask, db")
 		        : hip_status(mask_grad(g, alive, m, (int64_t)(N * Cout * hw), s), "conv2d mask");
-		gm = m;
 	} else if (db) {  // ops.cpp:1445
 		rc = hip_status(lane_sums(gm, (int64_t)(N * Cout), (int64_t)hw, gb, s), "conv2d db");
 	}
 	if (rc == NNH_OK && db)  // ops.cpp:1461
 		rc = hip_status(sum_rows(gb, (int64_t)N, (int64_t)Cout, db, db_first ? 0 : 2, s), "conv2d db");
-	if (rc == NNH_OK && dw) {  // ops.cpp:1448-1449, 1462: dW_n = g_n col_n^T with col_n gathered from x_n
-		float* gw = ws.at<float>(off_gw);
+	if (rc == NNH_OK && dw && !dw3) {  // ops.cpp:1448-1449: dW_n = g_n col_n^T with col_n gathered from x_n
 		nnh_batch b{};
 		b.ndim = 1;
 		b.shape[0] = N;
@@ -161,9 +165,9 @@ int nnh_conv2d_backward(const float* g, const float* x, const float* w, const un
 		GemmCall call;
 		rc = build_gemm(0, 1, Cout, K, hw, gm, hw, x, hw, gw, K, 0, &b, nullptr, call, &cg);
 		if (rc == NNH_OK) rc = run_gemm(call, stream, -1, partials);
-		if (rc == NNH_OK)
-			rc = hip_status(sum_rows(gw, (int64_t)N, (int64_t)(Cout * K), dw, dw_first ? 0 : 2, s), "conv2d dw");
 	}
+	if (rc == NNH_OK && dw)  // ops.cpp:1462
+		rc = hip_status(sum_rows(gw, (int64_t)N, (int64_t)(Cout * K), dw, dw_first ? 0 : 2, s), "conv2d dw");
 	if (rc == NNH_OK && dx && dx_fused) {  // ops.cpp:1452-1455, dcol kept on chip
 		rc = hip_status(conv_dx_fused(gm, w, dx, geo, (int64_t)N, (int)Cout, dx_first ? 1 : 0, s), "conv2d dx");
 	} else if (rc == NNH_OK && dx) {  // ops.cpp:1452-1455

@@ -228,6 +228,60 @@ def test_conv3x3_lds_path(gpu, oracle):
     same(host(yv).reshape(wy.shape), wy, "unaligned y")
 
 
+def test_conv3x3_weight_gradient_lds_path(gpu, oracle):
+    """The per-sample weight gradients of 3x3, stride 1, padding 1 convolutions on planes up to 14 x 14 with Cout
+    a multiple of 64 run as MFMA chains over the gradient rows and the padded input held in LDS, then the ordered
+    sum over samples: several 64-channel groups, one to 42 input channels (a ragged last group of 16 k), tiny and
+    rectangular planes, with and without the ReLU mask, accumulating gradients, special values. The same kernel
+    masks the gradient (the masked gradient then feeds dx) and takes the per-sample bias sums, so dx and db are
+    checked too, also with only some of the three gradients asked for. Cout = 32, planes whose size is not a
+    multiple of 4 and a gradient that is not 16-byte aligned take the gathered GEMM instead."""
+    import torch
+
+    import nnh
+    cases = [(3, 32, 14, 14, 64, True), (2, 1, 2, 2, 64, False), (2, 7, 12, 11, 128, True), (1, 42, 14, 14, 64, True),
+             (3, 5, 9, 4, 64, False), (2, 3, 14, 14, 32, True), (2, 3, 7, 7, 64, True), (2, 4, 6, 6, 64, False)]
+    for ci, (N, Cin, H, W, Cout, relu) in enumerate(cases):
+        x = synth.mt19937_uniform(400 + ci, N * Cin * H * W).reshape(N, Cin, H, W) * 2 - 1
+        w = synth.normal(410 + ci, (Cout, Cin, 3, 3))
+        b = synth.mt19937_uniform(420 + ci, Cout) - np.float32(0.5)
+        if ci == 2:
+            x[0, 1, 3, 3], x[1, 6, 11, 10], x[1, 0, 0, 0] = np.inf, -0.0, np.nan
+        y, alive = nnh.conv2d_forward(dev(x), dev(w), dev(b), 1, 1, relu)
+        wy, wa = oracle.conv2d_forward(x, w, b, 1, 1, relu)
+        same(host(y), wy, ("forward", ci))
+        gr = synth.normal(430 + ci, wy.shape)
+        for first in (True, False):
+            dx0 = synth.mt19937_uniform(440 + ci, x.size).reshape(x.shape)
+            dw0 = synth.mt19937_uniform(450 + ci, w.size).reshape(w.shape)
+            db0 = synth.mt19937_uniform(460 + ci, Cout)
+            dx, dw, db = dev(dx0), dev(dw0), dev(db0)
+            gd = dev(gr)
+            if ci == 7:  # the gradient one float past a 16-byte boundary
+                gd = torch.empty(gr.size + 1, dtype=torch.float32, device="cuda")[1:].view(gr.shape).copy_(gd)
+            nnh.conv2d_backward(gd, dev(x), dev(w), alive if relu else None, 1, 1, dx, first, dw, first, db, first)
+            wdx, wdw, wdb = oracle.conv2d_backward(gr, x, w, wa if relu else None, 1, 1, dx=None if first else dx0,
+                                                   dx_first=first)
+            if not first:
+                wdw, wdb = dw0 + wdw, db0 + wdb
+            else:
+                wdw, wdb = wdw + np.float32(0), wdb + np.float32(0)
+            for got, want, key in ((dx, wdx, "dx"), (dw, wdw, "dw"), (db, wdb, "db")):
+                assert_same(host(got), want.astype(np.float32), (ci, N, Cin, H, W, Cout, relu, first, key),
+                            nan_equal=(ci == 2))
+        # a subset of the gradients: dW alone, dW and db without dx, dx and db without dW
+        wdx, wdw, wdb = oracle.conv2d_backward(gr, x, w, wa if relu else None, 1, 1)
+        for want_dx, want_dw, want_db in ((False, True, False), (False, True, True), (True, False, True)):
+            dx = dev(np.zeros(x.shape, np.float32)) if want_dx else None
+            dw = dev(np.zeros(w.shape, np.float32)) if want_dw else None
+            db = dev(np.zeros(Cout, np.float32)) if want_db else None
+            nnh.conv2d_backward(dev(gr), dev(x), dev(w), alive if relu else None, 1, 1, dx, True, dw, True, db, True)
+            for got, want, key in ((dx, wdx, "dx"), (dw, wdw + np.float32(0), "dw"), (db, wdb + np.float32(0), "db")):
+                if got is not None:
+                    assert_same(host(got), want.astype(np.float32),
+                                (ci, N, Cin, H, W, Cout, relu, want_dx, want_dw, want_db, key), nan_equal=(ci == 2))
+
+
 def test_same_width_quad_path(gpu, oracle):
     """Stride 1, kw = 2 pad + 1, W % 4 == 0 takes the 4-pixels-per-lane direct kernel: every pad 0..4, several
     input channels, Cout not a multiple of the channel group, kh != kw, rows that straddle waves (W = 28: a wave
