@@ -77,11 +77,21 @@ __device__ __forceinline__ void sum_chunk_store(float (*tile)[kSumCols], int vec
 	}
 }
 
-__global__ void __launch_bounds__(256) sum_rows_lds_kernel(const float* __restrict__ src, int rows, int inner,
-                                                           float* __restrict__ dst, int combine, int vec) {
+// One column sum: the source {rows, inner}, the destination and its combine rule, and whether 16-byte loads apply.
+struct SumJob {
+	const float* src;
+	float* dst;
+	int rows, inner, combine, vec;
+};
+
+// The columns block * kSumCols .. + kSumCols - 1 of one job.
+__device__ __forceinline__ void sum_rows_block(const SumJob& job, int block) {
 	__shared__ __align__(16) float tile[2][kSumChunk][kSumCols];
+	const float* __restrict__ src = job.src;
+	float* __restrict__ dst = job.dst;
+	const int rows = job.rows, inner = job.inner, combine = job.combine, vec = job.vec;
 	const int tid = threadIdx.x;
-	const int c0 = blockIdx.x * kSumCols;
+	const int c0 = block * kSumCols;
 	const int ncol = min(kSumCols, inner - c0);
 	// 16-byte loads need whole quads of columns in this block (the clamp above keeps them in the row)
 	const int vec_here = vec && ncol % 4 == 0;
@@ -118,6 +128,15 @@ __global__ void __launch_bounds__(256) sum_rows_lds_kernel(const float* __restri
 	}
 }
 
+__global__ void __launch_bounds__(256) sum_rows_lds_kernel(const SumJob job) { sum_rows_block(job, blockIdx.x); }
+
+// Two independent column sums in one launch: blocks below blocks0 take the first job, the rest the second.
+__global__ void __launch_bounds__(256) sum_rows_pair_kernel(const SumJob job0, const SumJob job1, int blocks0) {
+	const int b = blockIdx.x;
+	if (b < blocks0) sum_rows_block(job0, b);
+	else sum_rows_block(job1, b - blocks0);
+}
+
 // relu forward (ops.cpp:775-782): y = x > 0 ? x : 0
 __global__ void __launch_bounds__(256) relu_forward_kernel(const float* __restrict__ x, float* __restrict__ y,
                                                            int64_t count) {
@@ -143,15 +162,41 @@ inline unsigned blocks_for(int64_t n) { return (unsigned)((n + 255) / 256); }
 
 }  // namespace
 
+namespace {
+
+bool lds_sum_fits(int64_t rows, int64_t inner) { return rows < ((int64_t)1 << 31) && inner < ((int64_t)1 << 31); }
+
+SumJob sum_job(const float* src, int64_t rows, int64_t inner, float* dst, int combine) {
+	const int vec = (inner % 4 == 0 && reinterpret_cast<uintptr_t>(src) % 16 == 0) ? 1 : 0;
+	return SumJob{src, dst, (int)rows, (int)inner, combine, vec};
+}
+
+unsigned sum_blocks(int64_t inner) { return (unsigned)((inner + kSumCols - 1) / kSumCols); }
+
+}  // namespace
+
 hipError_t sum_rows(const float* src, int64_t rows, int64_t inner, float* dst, int combine, hipStream_t s) {
 	if (inner == 0) return hipSuccess;
-	if (rows < ((int64_t)1 << 31) && inner < ((int64_t)1 << 31)) {
-		const int vec = (inner % 4 == 0 && reinterpret_cast<uintptr_t>(src) % 16 == 0) ? 1 : 0;
-		hipLaunchKernelGGL(sum_rows_lds_kernel, dim3((unsigned)((inner + kSumCols - 1) / kSumCols)), dim3(256), 0, s,
-		                   src, (int)rows, (int)inner, dst, combine, vec);
+	if (lds_sum_fits(rows, inner)) {
+		hipLaunchKernelGGL(sum_rows_lds_kernel, dim3(sum_blocks(inner)), dim3(256), 0, s,
+		                   sum_job(src, rows, inner, dst, combine));
 	} else {
 		hipLaunchKernelGGL(sum_rows_kernel, dim3(blocks_for(inner)), dim3(256), 0, s, src, rows, inner, dst, combine);
 	}
+	return hipGetLastError();
+}
+
+hipError_t sum_rows_pair(const float* src0, int64_t rows0, int64_t inner0, float* dst0, int combine0,
+                         const float* src1, int64_t rows1, int64_t inner1, float* dst1, int combine1, hipStream_t s) {
+	const int64_t blocks = (int64_t)sum_blocks(inner0) + sum_blocks(inner1);
+	if (inner0 == 0 || inner1 == 0 || !lds_sum_fits(rows0, inner0) || !lds_sum_fits(rows1, inner1) ||
+	    blocks > 0x7fffffff) {
+		const hipError_t e = sum_rows(src0, rows0, inner0, dst0, combine0, s);
+		return e != hipSuccess ? e : sum_rows(src1, rows1, inner1, dst1, combine1, s);
+	}
+	hipLaunchKernelGGL(sum_rows_pair_kernel, dim3((unsigned)blocks), dim3(256), 0, s,
+	                   sum_job(src0, rows0, inner0, dst0, combine0), sum_job(src1, rows1, inner1, dst1, combine1),
+	                   (int)sum_blocks(inner0));
 	return hipGetLastError();
 }
 

@@ -8,6 +8,9 @@ namespace nnh {
 
 // dst[j] (combine 0: =, 1: = s + 0.0f, 2: +=) s_j = sum over rows a, in order from +0, of src[a * inner + j].
 hipError_t sum_rows(const float* src, int64_t rows, int64_t inner, float* dst, int combine, hipStream_t s);
+// Two independent sum_rows in one launch (the same bits as two calls).
+hipError_t sum_rows_pair(const float* src0, int64_t rows0, int64_t inner0, float* dst0, int combine0,
+                         const float* src1, int64_t rows1, int64_t inner1, float* dst1, int combine1, hipStream_t s);
 hipError_t relu_forward(const float* x, float* y, int64_t count, hipStream_t s);
 hipError_t relu_backward(const float* x, const float* g, float* dst, int64_t count, int first, hipStream_t s);
 

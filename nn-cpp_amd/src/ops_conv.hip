@@ -152,8 +152,6 @@ int nnh_conv2d_backward(const float* g, const float* x, const float* w, const un
 	} else if (db) {  // ops.cpp:1445
 		rc = hip_status(lane_sums(gm, (int64_t)(N * Cout), (int64_t)hw, gb, s), "conv2d db");
 	}
-	if (rc == NNH_OK && db)  // ops.cpp:1461
-		rc = hip_status(sum_rows(gb, (int64_t)N, (int64_t)Cout, db, db_first ? 0 : 2, s), "conv2d db");
 	if (rc == NNH_OK && dw && !dw3) {  // ops.cpp:1448-1449: dW_n = g_n col_n^T with col_n gathered from x_n
 		nnh_batch b{};
 		b.ndim = 1;
@@ -166,8 +164,15 @@ int nnh_conv2d_backward(const float* g, const float* x, const float* w, const un
 		rc = build_gemm(0, 1, Cout, K, hw, gm, hw, x, hw, gw, K, 0, &b, nullptr, call, &cg);
 		if (rc == NNH_OK) rc = run_gemm(call, stream, -1, partials);
 	}
-	if (rc == NNH_OK && dw)  // ops.cpp:1462
+	// the sample-order sums (ops.cpp:1461-1462), in one launch when both are asked for
+	if (rc == NNH_OK && db && dw)
+		rc = hip_status(sum_rows_pair(gw, (int64_t)N, (int64_t)(Cout * K), dw, dw_first ? 0 : 2, gb, (int64_t)N,
+		                              (int64_t)Cout, db, db_first ? 0 : 2, s),
+		                "conv2d dw, db");
+	else if (rc == NNH_OK && dw)
 		rc = hip_status(sum_rows(gw, (int64_t)N, (int64_t)(Cout * K), dw, dw_first ? 0 : 2, s), "conv2d dw");
+	else if (rc == NNH_OK && db)
+		rc = hip_status(sum_rows(gb, (int64_t)N, (int64_t)Cout, db, db_first ? 0 : 2, s), "conv2d db");
 	if (rc == NNH_OK && dx && dx_fused) {  // ops.cpp:1452-1455, dcol kept on chip
 		rc = hip_status(conv_dx_fused(gm, w, dx, geo, (int64_t)N, (int)Cout, dx_first ? 1 : 0, s), "conv2d dx");
 	} else if (rc == NNH_OK && dx) {  // ops.cpp:1452-1455
