@@ -287,6 +287,45 @@ def test_self_attention_gradient_sums_the_three_roles(gpu, oracle):
     same(host(grad), want, "self-attention gradient")
 
 
+def test_head64_dq_dk_accumulate_subsets_and_one_node(gpu, oracle):
+    """dQ and dK of head width 64 after the fused dS kernel: accumulating into old gradients, with only one of the
+    two asked for, and with q, k and v one node (dV stored first, then dQ and dK added: the reference's order),
+    over ragged 64-row blocks, padded keys and causal rows."""
+    import nnh
+    from pyoracle import _fp
+    L = oracle.lib
+    N, T, H = 2, 100, 2
+    D = 64 * H
+    q, k, v, mask = attention_case(120, N, T, T, D, True)
+    g = synth.normal(125, (N, T, D))
+    for causal in (False, True):
+        _, p = oracle.attention_forward(q, k, v, H, mask, causal)
+        for want_dq, want_dk in ((True, True), (True, False), (False, True)):
+            dq0, dk0 = synth.normal(126, q.shape), synth.normal(127, k.shape)
+            dq, dk = (dev(dq0) if want_dq else None), (dev(dk0) if want_dk else None)
+            nnh.attention_backward(dev(g), dev(q), dev(k), dev(v), dev(p), H, dev(mask), causal, dq, False, dk, False,
+                                   None, True)
+            wq, wk = dq0.copy(), dk0.copy()
+            L.oracle_attention_backward(_fp(g), _fp(q), _fp(k), _fp(v), _fp(p), N, T, T, D, H, _fp(mask), int(causal),
+                                        _fp(wq) if want_dq else None, 0, _fp(wk) if want_dk else None, 0, None, 1)
+            if want_dq:
+                same(host(dq), wq, (causal, "dq accumulated"))
+            if want_dk:
+                same(host(dk), wk, (causal, "dk accumulated"))
+        # one node: x is query, key and value
+        x = q
+        _, px = oracle.attention_forward(x, x, x, H, mask, causal)
+        for dv_first, dq_first, dk_first in ((True, False, False), (False, False, False), (False, True, False)):
+            old = synth.normal(128, x.shape)
+            grad = dev(old)
+            nnh.attention_backward(dev(g), dev(x), dev(x), dev(x), dev(px), H, dev(mask), causal, grad, dq_first, grad,
+                                   dk_first, grad, dv_first)
+            want = old.copy()
+            L.oracle_attention_backward(_fp(g), _fp(x), _fp(x), _fp(x), _fp(px), N, T, T, D, H, _fp(mask), int(causal),
+                                        _fp(want), int(dq_first), _fp(want), int(dk_first), _fp(want), int(dv_first))
+            same(host(grad), want, (causal, dv_first, dq_first, dk_first, "one node"))
+
+
 def test_attention_hand_reference_and_masks(gpu):
     """test_transformer.cpp:149-176 (one head, identity projections) and 232-276 (a fully masked row is
     finite: exactly the mean of V)."""
