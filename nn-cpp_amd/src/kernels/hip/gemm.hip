@@ -67,7 +67,7 @@ hipError_t prepare_device() {
 	std::lock_guard<std::mutex> lock(mu);
 	if (done[dev]) return hipSuccess;
 	const Config* cfg = configs();
-	for (int i = 0; i < kNumConfigs; ++i)
+	for (int i = 0; i < kNumConfigs; ++i) {
 		for (int f = 0; f < 4; ++f)
 			for (int edge = 0; edge < 5; ++edge) {
 				if (edge == 2 && f >= 2) continue;  // gather kernels: A not transposed
@@ -77,6 +77,14 @@ hipError_t prepare_device() {
 				                        cfg[i].lds_bytes[f]);
 				if (e != hipSuccess) return e;
 			}
+		for (int p = 0; p < 8; ++p) {
+			const PairFn fn = cfg[i].pair_fn[p >> 2][(p >> 1) & 1][p & 1];
+			if (!fn) continue;
+			e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize,
+			                        std::max(cfg[i].lds_bytes[0], cfg[i].lds_bytes[2]));
+			if (e != hipSuccess) return e;
+		}
+	}
 	// Workspaces (depth-cut partials, im2col columns, attention's dS) come from the device's stream-ordered pool;
 	// keep freed blocks in the pool instead of returning them at every synchronisation, so repeated calls reuse them.
 	hipMemPool_t pool = nullptr;
@@ -114,6 +122,44 @@ int pick_config(const GemmCall& g) {
 	return kCfg32x32x32Mf4;
 }
 
+// The kernel arguments of one product on configuration cf; cut: the product takes nn-cpp's depth cut (the
+// caller supplies p.partial); interior: every tile is whole and 16-byte aligned (the kernels without bounds checks).
+GemmArgs make_args(const GemmCall& g, const Config& cf, bool& cut, bool& interior) {
+	GemmArgs p{};
+	p.a = g.a;
+	p.b = g.b;
+	p.c = g.c;
+	p.lda = g.lda;
+	p.ldb = g.ldb;
+	p.ldc = g.ldc;
+	p.m = (int)g.m;
+	p.n = (int)g.n;
+	p.k = (int)g.k;
+	p.accumulate = g.accumulate;
+	p.tiles_m = (int)((g.m + cf.bm - 1) / cf.bm);
+	p.tiles_n = (int)((g.n + cf.bn - 1) / cf.bn);
+	p.batch_count = (int)g.batch_count;
+	p.batch = g.batch;
+	p.ep = g.ep;
+	p.col = g.col;
+	cut = depth_cut(g.m, g.n, g.k);
+	p.rowsum = g.rowsum;
+	p.rowsum_combine = g.rowsum_combine;
+	p.pieces = cut ? (int)((g.k + 127) / 128) : 1;
+	p.piece_k = cut ? 128 : (int)std::max<int64_t>(g.k, 1);
+	// 16-byte operand loads need 16-byte rows and strides (a gathered B is read element by element)
+	bool vec_ok = (g.lda % 4 == 0) && (reinterpret_cast<uintptr_t>(g.a) % 16 == 0) &&
+	              (g.gather || ((g.ldb % 4 == 0) && (reinterpret_cast<uintptr_t>(g.b) % 16 == 0)));
+	for (int d = 0; d < g.batch.ndim; ++d)
+		vec_ok = vec_ok && g.batch.sa[d] % 4 == 0 && (g.gather || g.batch.sb[d] % 4 == 0);
+	p.vec_ok = vec_ok ? 1 : 0;
+	// interior kernels also write C with 16-byte stores
+	bool c_vec = (g.ldc % 4 == 0) && (reinterpret_cast<uintptr_t>(g.c) % 16 == 0);
+	for (int d = 0; d < g.batch.ndim; ++d) c_vec = c_vec && g.batch.sc[d] % 4 == 0;
+	interior = vec_ok && c_vec && g.m % cf.bm == 0 && g.n % cf.bn == 0 && g.k % cf.bk == 0 && g.k > 0;
+	return p;
+}
+
 }  // namespace
 
 bool depth_cut(int64_t m, int64_t n, int64_t k) {
@@ -140,40 +186,11 @@ hipError_t gemm_launch(const GemmCall& g, hipStream_t s, int config, float* work
 	if (config < 0 || config >= kNumConfigs) config = pick_config(g);
 	const Config& cf = configs()[config];
 
-	GemmArgs p{};
-	p.a = g.a;
-	p.b = g.b;
-	p.c = g.c;
-	p.lda = g.lda;
-	p.ldb = g.ldb;
-	p.ldc = g.ldc;
-	p.m = (int)g.m;
-	p.n = (int)g.n;
-	p.k = (int)g.k;
-	p.accumulate = g.accumulate;
-	p.tiles_m = (int)((g.m + cf.bm - 1) / cf.bm);
-	p.tiles_n = (int)((g.n + cf.bn - 1) / cf.bn);
-	p.batch_count = (int)g.batch_count;
-	p.batch = g.batch;
-	p.ep = g.ep;
-	p.col = g.col;
 	if (g.gather && g.ta) return hipErrorInvalidValue;
-	const bool cut = depth_cut(g.m, g.n, g.k);
-	if (g.rowsum && (cut || g.batch_count != 1 || g.gather || !g.ta || g.tb)) return hipErrorInvalidValue;
-	p.rowsum = g.rowsum;
-	p.rowsum_combine = g.rowsum_combine;
-	p.pieces = cut ? (int)((g.k + 127) / 128) : 1;
-	p.piece_k = cut ? 128 : (int)std::max<int64_t>(g.k, 1);
-	// 16-byte operand loads need 16-byte rows and strides (a gathered B is read element by element)
-	bool vec_ok = (g.lda % 4 == 0) && (reinterpret_cast<uintptr_t>(g.a) % 16 == 0) &&
-	              (g.gather || ((g.ldb % 4 == 0) && (reinterpret_cast<uintptr_t>(g.b) % 16 == 0)));
-	for (int d = 0; d < g.batch.ndim; ++d)
-		vec_ok = vec_ok && g.batch.sa[d] % 4 == 0 && (g.gather || g.batch.sb[d] % 4 == 0);
-	p.vec_ok = vec_ok ? 1 : 0;
-	// interior kernels also write C with 16-byte stores
-	bool c_vec = (g.ldc % 4 == 0) && (reinterpret_cast<uintptr_t>(g.c) % 16 == 0);
-	for (int d = 0; d < g.batch.ndim; ++d) c_vec = c_vec && g.batch.sc[d] % 4 == 0;
-	const bool interior = vec_ok && c_vec && g.m % cf.bm == 0 && g.n % cf.bn == 0 && g.k % cf.bk == 0 && g.k > 0;
+	if (g.rowsum && (depth_cut(g.m, g.n, g.k) || g.batch_count != 1 || g.gather || !g.ta || g.tb))
+		return hipErrorInvalidValue;
+	bool cut = false, interior = false;
+	GemmArgs p = make_args(g, cf, cut, interior);
 
 	float* part = nullptr;
 	std::optional<StreamWorkspace> ws;
@@ -199,6 +216,32 @@ hipError_t gemm_launch(const GemmCall& g, hipStream_t s, int config, float* work
 		                   p.pieces, p.m, p.n, g.c, g.ldc, g.accumulate, g.batch, g.batch_count, g.ep);
 		e = hipGetLastError();
 	}
+	return e;
+}
+
+hipError_t gemm_launch_pair(const GemmCall& g0, const GemmCall& g1, hipStream_t s, bool& launched) {
+	launched = false;
+	// g0 = A B and g1 = A^T B (row sums allowed), single matrices, no depth cut, both on one configuration that
+	// has the pair kernels
+	if (g0.ta || g0.tb || g0.gather || g0.rowsum || !g1.ta || g1.tb || g1.gather) return hipSuccess;
+	if (g0.batch_count != 1 || g1.batch_count != 1 || g0.batch.ndim != 0 || g1.batch.ndim != 0) return hipSuccess;
+	if (g0.m == 0 || g0.n == 0 || g1.m == 0 || g1.n == 0) return hipSuccess;
+	if (depth_cut(g0.m, g0.n, g0.k) || depth_cut(g1.m, g1.n, g1.k)) return hipSuccess;
+	const int c0 = pick_config(g0), c1 = pick_config(g1);
+	if (c0 != c1) return hipSuccess;
+	const Config& cf = configs()[c0];
+	bool cut0 = false, cut1 = false, in0 = false, in1 = false;
+	const GemmArgs p0 = make_args(g0, cf, cut0, in0), p1 = make_args(g1, cf, cut1, in1);
+	const PairFn fn = cf.pair_fn[in0 ? 0 : 1][in1 ? 0 : 1][g1.rowsum ? 1 : 0];
+	if (!fn) return hipSuccess;
+	const int64_t b0 = (int64_t)p0.tiles_m * p0.tiles_n, b1 = (int64_t)p1.tiles_m * p1.tiles_n;
+	if (b0 + b1 > 0x7fffffff) return hipSuccess;
+	hipError_t e = prepare_device();
+	if (e != hipSuccess) return e;
+	hipLaunchKernelGGL(fn, dim3((unsigned)(b0 + b1)), dim3(256), std::max(cf.lds_bytes[0], cf.lds_bytes[2]), s, p0, p1,
+	                   (int)b0);
+	e = hipGetLastError();
+	launched = e == hipSuccess;
 	return e;
 }
 

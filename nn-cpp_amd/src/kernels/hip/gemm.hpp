@@ -42,6 +42,10 @@ int64_t gemm_workspace_floats(int64_t m, int64_t n, int64_t k, int64_t batch_cou
 // Workspace for a depth cut comes from workspace (if non-null, at least gemm_workspace_floats) or else from
 // the stream's StreamWorkspace (so a caller holding that one must pass workspace).
 hipError_t gemm_launch(const GemmCall& g, hipStream_t s, int config = -1, float* workspace = nullptr);
+// A B (g0) and A^T B (g1, row sums allowed) in one launch when both are single matrices without a depth cut and
+// pick the same small-tile configuration; launched tells whether it did (otherwise nothing was launched and the
+// caller runs them in turn). The caller guarantees that neither product writes what the other reads or writes.
+hipError_t gemm_launch_pair(const GemmCall& g0, const GemmCall& g1, hipStream_t s, bool& launched);
 
 int gemm_config_count();
 const char* gemm_config_name(int config);

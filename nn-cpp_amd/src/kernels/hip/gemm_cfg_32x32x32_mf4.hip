@@ -2,5 +2,5 @@
 #include "gemm_config.hpp"
 
 namespace nnh {
-Config config_32x32x32_mf4() { return make_config<32, 32, 32, 16, 16, 4, kMf4>("32x32x32_w16x16_mf4"); }
+Config config_32x32x32_mf4() { return make_config<32, 32, 32, 16, 16, 4, kMf4, true>("32x32x32_w16x16_mf4"); }
 }  // namespace nnh

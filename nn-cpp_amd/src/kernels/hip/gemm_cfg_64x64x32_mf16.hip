@@ -2,5 +2,5 @@
 #include "gemm_config.hpp"
 
 namespace nnh {
-Config config_64x64x32_mf16() { return make_config<64, 64, 32, 64, 16, 4, kMf16>("64x64x32_w64x16_mf16"); }
+Config config_64x64x32_mf16() { return make_config<64, 64, 32, 64, 16, 4, kMf16, true>("64x64x32_w64x16_mf16"); }
 }  // namespace nnh

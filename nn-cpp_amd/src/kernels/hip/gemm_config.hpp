@@ -7,6 +7,7 @@
 namespace nnh {
 
 using KernelFn = void (*)(const GemmArgs);
+using PairFn = void (*)(const GemmArgs, const GemmArgs, int);
 
 struct Config {
 	const char* name;
@@ -15,9 +16,12 @@ struct Config {
 	KernelFn fn[4][2];  // [ta * 2 + tb][edge]
 	KernelFn gather_fn[2];  // B gathered as im2col columns (ColGather), A not transposed: [tb]
 	KernelFn rowsum_fn[2];  // transposed A, plain B, with row sums of op(A) (GemmArgs::rowsum): [edge]
+	// A B and A^T B (with row sums or not) in one launch, compiled for the small-tile configurations only (null
+	// otherwise): [edge of the first][edge of the second][row sums]
+	PairFn pair_fn[2][2][2];
 };
 
-template <int BM, int BN, int BK, int WM, int WN, int WPE, int MF = kMf32>
+template <int BM, int BN, int BK, int WM, int WN, int WPE, int MF = kMf32, bool PAIR = false>
 Config make_config(const char* name) {
 	Config c{};
 	c.name = name;
@@ -37,6 +41,18 @@ Config make_config(const char* name) {
 	c.gather_fn[1] = sgemm_tile_kernel<BM, BN, BK, WM, WN, WPE, MF, false, true, true, true>;
 	c.rowsum_fn[0] = sgemm_tile_kernel<BM, BN, BK, WM, WN, WPE, MF, true, false, false, false, true>;
 	c.rowsum_fn[1] = sgemm_tile_kernel<BM, BN, BK, WM, WN, WPE, MF, true, false, true, false, true>;
+	if constexpr (PAIR) {
+#define NNH_PAIR(E0, E1, R) c.pair_fn[E0][E1][R] = sgemm_pair_kernel<BM, BN, BK, WM, WN, WPE, MF, E0, E1, R>;
+		NNH_PAIR(false, false, false)
+		NNH_PAIR(false, false, true)
+		NNH_PAIR(false, true, false)
+		NNH_PAIR(false, true, true)
+		NNH_PAIR(true, false, false)
+		NNH_PAIR(true, false, true)
+		NNH_PAIR(true, true, false)
+		NNH_PAIR(true, true, true)
+#undef NNH_PAIR
+	}
 	return c;
 }
 

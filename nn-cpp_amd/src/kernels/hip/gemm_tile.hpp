@@ -278,9 +278,9 @@ __device__ __forceinline__ int xcd_remap(int bid, int total) {
 	return bid;
 }
 
-template <int BM, int BN, int BK, int WM, int WN, int WPE, int MF, bool TA, bool TB, bool EDGE, bool GB = false,
-          bool RS = false>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE, WPE))) sgemm_tile_kernel(const GemmArgs p) {
+// One workgroup's tile of a product; block is the workgroup's index among the product's workgroups.
+template <int BM, int BN, int BK, int WM, int WN, int MF, bool TA, bool TB, bool EDGE, bool GB = false, bool RS = false>
+__device__ __forceinline__ void sgemm_tile_body(const GemmArgs& p, int block) {
 	static_assert(!GB || (!TA && EDGE), "the implicit im2col operand is B, loaded with bounds checks");
 	static_assert(!RS || (TA && !TB && !GB), "row sums are compiled for the weight-gradient layout only");
 	static_assert(!RS || (BM & (BM - 1)) == 0, "row sums index rows as tid % BM");
@@ -298,7 +298,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE, W
 	// ---- which tile, piece and batch matrix ----
 	const int tiles = p.tiles_m * p.tiles_n;
 	const int total = tiles * p.pieces * p.batch_count;
-	const int lid = xcd_remap(blockIdx.x, total);
+	const int lid = xcd_remap(block, total);
 	const int t = lid % tiles;
 	const int rest = lid / tiles;
 	const int piece = rest % p.pieces;
@@ -601,6 +601,23 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE, W
 				Cp[off] = v;
 			}
 		}
+}
+
+template <int BM, int BN, int BK, int WM, int WN, int WPE, int MF, bool TA, bool TB, bool EDGE, bool GB = false,
+          bool RS = false>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE, WPE))) sgemm_tile_kernel(const GemmArgs p) {
+	sgemm_tile_body<BM, BN, BK, WM, WN, MF, TA, TB, EDGE, GB, RS>(p, (int)blockIdx.x);
+}
+
+// Two independent products in one launch: A B (p0, workgroups below blocks0) and A^T B, with or without row sums
+// (p1, the rest). A Linear backward's dX and dW are such a pair; when both are small, their tiles then run side by
+// side instead of one product after the other. Each product's elements are computed exactly as in its own launch.
+template <int BM, int BN, int BK, int WM, int WN, int WPE, int MF, bool EDGE0, bool EDGE1, bool RS1>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
+sgemm_pair_kernel(const GemmArgs p0, const GemmArgs p1, int blocks0) {
+	const int b = (int)blockIdx.x;
+	if (b < blocks0) sgemm_tile_body<BM, BN, BK, WM, WN, MF, false, false, EDGE0>(p0, b);
+	else sgemm_tile_body<BM, BN, BK, WM, WN, MF, true, false, EDGE1, false, RS1>(p1, b - blocks0);
 }
 
 }  // namespace nnh

@@ -44,27 +44,47 @@ int nnh_linear_backward(const float* g, const float* x, const float* w, const si
 	size_t M = 0;
 	if (!product_fits(lead, nlead, M)) return fail(NNH_ERR_INVALID, "input size overflows");
 	hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-	GemmCall call;
-	if (dx) {  // dX = G W (ops.cpp:737)
-		int rc = build_gemm(0, 0, M, K, n, g, n, w, K, dx, K, !dx_first, nullptr, nullptr, call);
-		if (rc != NNH_OK) return rc;
-		rc = run_gemm(call, stream, -1);
-		if (rc != NNH_OK) return rc;
-	}
 	// db of a 2-D gradient is one Tensor::sum(0): each column of G folded over the rows in order from +0, which is
 	// the row sum of op(A) = G^T over k in the dW product, so that product computes it on the way
 	const bool db_in_dw = dw && db && nlead == 1 && M > 0 && K > 0 && n > 0 && !depth_cut((int64_t)n, (int64_t)K, (int64_t)M) &&
 	                      !ranges_overlap(db, n * 4, dw, (uint64_t)n * K * 4) && !ranges_overlap(db, n * 4, g, (uint64_t)M * n * 4) &&
 	                      !ranges_overlap(db, n * 4, x, (uint64_t)M * K * 4);
+	GemmCall cx, cw;
+	if (dx) {  // dX = G W (ops.cpp:737)
+		const int rc = build_gemm(0, 0, M, K, n, g, n, w, K, dx, K, !dx_first, nullptr, nullptr, cx);
+		if (rc != NNH_OK) return rc;
+	}
 	if (dw) {  // dW = G^T X (ops.cpp:741)
-		int rc = build_gemm(1, 0, n, K, M, g, n, x, K, dw, K, !dw_first, nullptr, nullptr, call);
+		const int rc = build_gemm(1, 0, n, K, M, g, n, x, K, dw, K, !dw_first, nullptr, nullptr, cw);
 		if (rc != NNH_OK) return rc;
 		if (db_in_dw) {
-			call.rowsum = db;
-			call.rowsum_combine = db_first ? 1 : 2;
+			cw.rowsum = db;
+			cw.rowsum_combine = db_first ? 1 : 2;
 		}
-		rc = run_gemm(call, stream, -1);
-		if (rc != NNH_OK) return rc;
+	}
+	// the two products in one launch when neither writes what the other reads or writes (the reference runs dX
+	// first; with disjoint buffers the order cannot show)
+	bool paired = false;
+	if (dx && dw && M > 0 && K > 0 && n > 0) {
+		const uint64_t bx = (uint64_t)M * K * 4, bw = (uint64_t)n * K * 4, bg = (uint64_t)M * n * 4;
+		const bool apart = !ranges_overlap(dx, bx, g, bg) && !ranges_overlap(dx, bx, w, bw) &&
+		                   !ranges_overlap(dx, bx, x, bx) && !ranges_overlap(dx, bx, dw, bw) &&
+		                   !ranges_overlap(dw, bw, w, bw) && (!db_in_dw || (!ranges_overlap(db, n * 4, dx, bx) &&
+		                                                                    !ranges_overlap(db, n * 4, w, bw)));
+		if (apart) {
+			const int rc = hip_status(gemm_launch_pair(cx, cw, s, paired), "linear backward");
+			if (rc != NNH_OK) return rc;
+		}
+	}
+	if (!paired) {
+		if (dx) {
+			const int rc = run_gemm(cx, stream, -1);
+			if (rc != NNH_OK) return rc;
+		}
+		if (dw) {
+			const int rc = run_gemm(cw, stream, -1);
+			if (rc != NNH_OK) return rc;
+		}
 	}
 	if (db && n > 0 && !db_in_dw) {
 		// accumulate_grad(bias, G): Tensor::sum(0) once per leading axis (ops.cpp:35-53), then stored as

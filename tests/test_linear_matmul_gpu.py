@@ -153,6 +153,54 @@ def test_linear_bias_gradient_in_weight_product(gpu, oracle):
                 assert_same(host(t), wv, (M, K, n, lead, first, key), nan_equal=(ci == 4))
 
 
+def test_linear_backward_dx_dw_in_one_launch(gpu, oracle):
+    """dX = G W and dW = G^T X of one Linear run in one launch when both pick the same small-tile configuration
+    (4x4x1 and 16x16x1 tiles, interior and edge, with and without db inside dW). Buffers that overlap keep the
+    reference's order, dX then dW: dx overlapping dw ends with dW's values where they meet, and dx on x itself
+    makes dW read the new dX."""
+    import torch
+
+    import nnh
+    cases = [(256, 784, 512), (256, 512, 256), (256, 256, 10), (1024, 1024, 1024), (96, 64, 64)]
+    for ci, (M, K, n) in enumerate(cases):
+        x = synth.mt19937_uniform(1600 + ci, M * K).reshape(M, K)
+        w = synth.mt19937_uniform(1700 + ci, n * K).reshape(n, K)
+        gr = synth.normal(1800 + ci, (M, n))
+        for first, with_db in ((True, True), (False, True), (False, False)):
+            dx0 = synth.mt19937_uniform(1900 + ci, M * K).reshape(M, K)
+            dw0 = synth.mt19937_uniform(2000 + ci, n * K).reshape(n, K)
+            db0 = synth.mt19937_uniform(2100 + ci, n)
+            dx, dw = dev(dx0), dev(dw0)
+            db = dev(db0) if with_db else None
+            nnh.linear_backward(dev(gr), dev(x), dev(w), dx, first, dw, first, db, first)
+            want = oracle.linear_backward(gr, x, w, dx=dx0.copy(), dx_first=first, dw=dw0.copy(), dw_first=first,
+                                          db=db0.copy(), db_first=first)
+            for t, wv, key in zip((dx, dw, db), want, ("dx", "dw", "db")):
+                if t is not None:
+                    same(host(t), wv, (M, K, n, first, with_db, key))
+    # overlapping buffers: one allocation holds dx, and dw starts inside it
+    M, K, n = 256, 512, 256
+    x = synth.mt19937_uniform(2200, M * K).reshape(M, K)
+    w = synth.mt19937_uniform(2201, n * K).reshape(n, K)
+    gr = synth.normal(2202, (M, n))
+    want_dx, want_dw, _ = oracle.linear_backward(gr, x, w, dx_first=True, dw_first=True, db_first=True)
+    buf = torch.zeros(M * K + n * K // 2, device="cuda")
+    dx, dw = buf[:M * K].view(M, K), buf[M * K - n * K // 2:].view(n, K)
+    nnh.linear_backward(dev(gr), dev(x), dev(w), dx, True, dw, True, None, True)
+    mem = np.zeros(M * K + n * K // 2, np.float32)
+    mem[:M * K] = want_dx.ravel()
+    mem[M * K - n * K // 2:] = want_dw.ravel()
+    same(host(buf), mem, "dx overlapped by dw")
+    # dx is x: dW = G^T (new dX)
+    xd = dev(x)
+    dw = torch.zeros((n, K), device="cuda")
+    nnh.linear_backward(dev(gr), xd, dev(w), xd, True, dw, True, None, True)
+    new_x = want_dx
+    _, want_dw2, _ = oracle.linear_backward(gr, new_x, w, dx_first=True, dw_first=True, db_first=True)
+    same(host(xd), want_dx, "dx written over x")
+    same(host(dw), want_dw2, "dw from the new x")
+
+
 def test_relu_node(gpu, oracle):
     import torch
 
