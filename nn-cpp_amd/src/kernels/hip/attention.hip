@@ -172,36 +172,46 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) a
 	}
 	__syncthreads();
 
-	// 2c. p_j = exp(v_j - m) for the live keys, exact zeros past the causal limit (ops.cpp:1197-1201); kExpQuads
-	// quads per thread at a time so that their table reads and double-precision chains overlap
-	constexpr int kExpQuads = 4;
-	const unsigned quads = (unsigned)(nq * (tk / 4));
-	for (unsigned e0 = tid; e0 < quads; e0 += 256 * kExpQuads) {
-		f32x4 x[kExpQuads];
-		float* o[kExpQuads];
-		int live[kExpQuads], j[kExpQuads];
-		float m[kExpQuads];
+	// 2c. p_j = exp(v_j - m) for the live keys, exact zeros past the causal limit (ops.cpp:1197-1201). Lane l takes
+	// row l, wave w the quads of keys w, w + 4, ..., kExpQuads of them at a time so that their table reads and
+	// double-precision chains overlap. Keys past a row's causal limit take exp(0) in place of exp(-2e9 - m), whose
+	// result is replaced by an exact zero, which keeps waves out of exp's special-case path (padded keys stay live
+	// and go through exp). Quads past the block's last live key are zero for every row: a wave stores them without
+	// computing anything.
+	{
+		constexpr int kExpQuads = 4;
+		const int row = lane, nq4 = tk / 4;
+		const float m = rowmax[min(row, nq - 1)];
+		const int live = a.causal ? min(tk, i0 + row + 1) : tk;
+		const int block_live = a.causal ? min(tk, i0 + nq) : tk;  // keys any row of the block reaches
+		f32x4* orow = sm4 + row * ldp4;
+		for (int q0 = wave; q0 < nq4; q0 += 4 * kExpQuads) {
+			if (4 * q0 >= block_live) {  // uniform: this and every later quad of the wave is dead for all rows
+				if (row < nq) {
 #pragma unroll
-		for (int h2 = 0; h2 < kExpQuads; ++h2) {
-			const unsigned e = min(e0 + 256 * h2, quads - 1);  // a repeated quad is computed, stored once
-			const unsigned row = fdiv(e, a.quads);
-			j[h2] = (int)(e - row * a.quads.d) * 4;
-			o[h2] = sm + row * ldp + j[h2];
-			x[h2] = *reinterpret_cast<const f32x4*>(o[h2]);
-			m[h2] = rowmax[row];
-			live[h2] = a.causal ? min(tk, i0 + (int)row + 1) : tk;
-		}
-		float ex[4 * kExpQuads];
+					for (int h2 = 0; h2 < kExpQuads; ++h2)
+						if (q0 + 4 * h2 < nq4) orow[q0 + 4 * h2] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+				}
+				continue;
+			}
+			f32x4 x[kExpQuads];
 #pragma unroll
-		for (int h2 = 0; h2 < kExpQuads; ++h2)
+			for (int h2 = 0; h2 < kExpQuads; ++h2) x[h2] = orow[min(q0 + 4 * h2, nq4 - 1)];
+			float ex[4 * kExpQuads];
 #pragma unroll
-			for (int c = 0; c < 4; ++c) ex[4 * h2 + c] = x[h2][c] - m[h2];
-		expf_glibc_n(ex, table);
+			for (int h2 = 0; h2 < kExpQuads; ++h2)
 #pragma unroll
-		for (int h2 = 0; h2 < kExpQuads; ++h2) {
+				for (int c = 0; c < 4; ++c) ex[4 * h2 + c] = 4 * (q0 + 4 * h2) + c < live ? x[h2][c] - m : 0.0f;
+			expf_glibc_n(ex, table);
+			if (row < nq) {
 #pragma unroll
-			for (int c = 0; c < 4; ++c) x[h2][c] = j[h2] + c < live[h2] ? ex[4 * h2 + c] : 0.0f;
-			if (h2 == 0 || e0 + 256 * h2 < quads) *reinterpret_cast<f32x4*>(o[h2]) = x[h2];
+				for (int h2 = 0; h2 < kExpQuads; ++h2) {
+					const int q = q0 + 4 * h2;
+#pragma unroll
+					for (int c = 0; c < 4; ++c) x[h2][c] = 4 * q + c < live ? ex[4 * h2 + c] : 0.0f;
+					if (q < nq4) orow[q] = x[h2];
+				}
+			}
 		}
 	}
 	__syncthreads();
@@ -236,6 +246,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) a
 	// 2e. p_j / sum into probs and back into LDS (ops.cpp:1203)
 	{
 		float* pr = a.probs + ((int64_t)nh * a.tq + i0) * tk;
+		const unsigned quads = (unsigned)(nq * (tk / 4));
 		for (unsigned e = tid; e < quads; e += 256) {
 			const unsigned row = fdiv(e, a.quads);
 			const int j = (int)(e - row * a.quads.d) * 4;

@@ -189,7 +189,8 @@ __global__ void __launch_bounds__(kThreads) softmax_rows_kernel(const float* in,
 		}
 	}
 	__syncthreads();
-	// B': the exponentials, a row per wave at a time (exact zeros past the causal limit)
+	// B': the exponentials, a row per wave at a time (exact zeros past the causal limit; those keys take exp(0) in
+	// place of exp(-2e9 - m), whose result is discarded, so that waves stay out of exp's special-case path)
 	for (int r = wave; r < nr; r += kThreads / 64) {
 		float* o = sm + r * ld;
 		const float m = rowmax[r];
@@ -197,7 +198,9 @@ __global__ void __launch_bounds__(kThreads) softmax_rows_kernel(const float* in,
 		if (VEC) {
 			for (int j = 4 * lane; j < g.tk; j += 256) {
 				f32x4 v = *reinterpret_cast<const f32x4*>(o + j);
-				float e[4] = {v[0] - m, v[1] - m, v[2] - m, v[3] - m};
+				float e[4];
+#pragma unroll
+				for (int c = 0; c < 4; ++c) e[c] = j + c < live ? v[c] - m : 0.0f;
 				expf_glibc_n(e, table);
 #pragma unroll
 				for (int c = 0; c < 4; ++c) v[c] = j + c < live ? e[c] : 0.0f;
@@ -205,7 +208,7 @@ __global__ void __launch_bounds__(kThreads) softmax_rows_kernel(const float* in,
 			}
 		} else {
 			for (int j = lane; j < g.tk; j += 64) {
-				const float e = expf_glibc(o[j] - m, table);
+				const float e = expf_glibc(j < live ? o[j] - m : 0.0f, table);
 				o[j] = j < live ? e : 0.0f;
 			}
 		}
