@@ -39,20 +39,27 @@ struct DxArgs {
 	FastDiv plane, width, stride;  // division by H*W, W and the stride
 };
 
-// The taps of a 3x3, stride-1 convolution, unrolled: the same order and the same additions as gather_taps
+// The taps of a 3x3, stride-1 convolution, unrolled: the same order and the same additions as gather_taps. The
+// nine reads are unconditional (positions clamped into the row) so that all are in flight at once; a tap outside
+// the output plane is dropped by a select, which leaves the sum exactly as skipping it would.
 __device__ __forceinline__ float gather_taps_3x3(const float* tile, const DxArgs& a, int c, int ih, int iw, float v) {
 	const ConvGeom& G = a.geo;
+	float x[9];
+	bool ok[9];
 #pragma unroll
 	for (int ph = 0; ph < 3; ++ph) {
 		const int qh = ih + G.pad - ph;
 		const bool row_ok = qh >= 0 && qh < G.ho;
-		const float* trow = tile + (c * 9 + ph * 3) * a.hwp + qh * G.wo;
+		const float* trow = tile + (c * 9 + ph * 3) * a.hwp + min(max(qh, 0), G.ho - 1) * G.wo;
 #pragma unroll
 		for (int pw = 0; pw < 3; ++pw) {
 			const int qw = iw + G.pad - pw;
-			if (row_ok && qw >= 0 && qw < G.wo) v = v + trow[pw * a.hwp + qw];
+			ok[ph * 3 + pw] = row_ok && qw >= 0 && qw < G.wo;
+			x[ph * 3 + pw] = trow[pw * a.hwp + min(max(qw, 0), G.wo - 1)];
 		}
 	}
+#pragma unroll
+	for (int t = 0; t < 9; ++t) v = ok[t] ? v + x[t] : v;
 	return v;
 }
 
@@ -181,13 +188,32 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) c
 	// 2b. col2im for the group's channels: every dx element adds its taps in (ph, pw) order
 	const int plane = G.h * G.w;
 	float* dxn = a.dx + ((int64_t)n * G.cin + c0) * plane;
-	for (int e = tid; e < cg * plane; e += 256) {
-		const int c = (int)fdiv((unsigned)e, a.plane), rem = e - c * plane;
-		const int ih = (int)fdiv((unsigned)rem, a.width), iw = rem - ih * G.w;
-		const float v0 = a.first ? 0.0f : dxn[e];
-		dxn[e] = G.stride != 1                 ? gather_taps<false>(tile, a, c, ih, iw, v0)
-		         : (G.kh == 3 && G.kw == 3) ? gather_taps_3x3(tile, a, c, ih, iw, v0)
-		                                    : gather_taps<true>(tile, a, c, ih, iw, v0);
+	if (G.stride == 1 && G.kh == 3 && G.kw == 3) {  // uniform: two elements per thread at a time
+		const int total = cg * plane;
+		for (int e0 = tid; e0 < total; e0 += 512) {
+			int c[2], ih[2], iw[2];
+			float v[2];
+#pragma unroll
+			for (int h = 0; h < 2; ++h) {
+				const int e = min(e0 + 256 * h, total - 1);  // a repeated element is computed, stored once
+				c[h] = (int)fdiv((unsigned)e, a.plane);
+				const int rem = e - c[h] * plane;
+				ih[h] = (int)fdiv((unsigned)rem, a.width);
+				iw[h] = rem - ih[h] * G.w;
+				v[h] = a.first ? 0.0f : dxn[e];
+			}
+#pragma unroll
+			for (int h = 0; h < 2; ++h) v[h] = gather_taps_3x3(tile, a, c[h], ih[h], iw[h], v[h]);
+			dxn[e0] = v[0];
+			if (e0 + 256 < total) dxn[e0 + 256] = v[1];
+		}
+	} else {
+		for (int e = tid; e < cg * plane; e += 256) {
+			const int c = (int)fdiv((unsigned)e, a.plane), rem = e - c * plane;
+			const int ih = (int)fdiv((unsigned)rem, a.width), iw = rem - ih * G.w;
+			const float v0 = a.first ? 0.0f : dxn[e];
+			dxn[e] = G.stride != 1 ? gather_taps<false>(tile, a, c, ih, iw, v0) : gather_taps<true>(tile, a, c, ih, iw, v0);
+		}
 	}
 }
 
