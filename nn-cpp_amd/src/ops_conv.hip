@@ -1,14 +1,18 @@
 // ops_conv.hip - extern "C" entry points of nn::conv2d / nn::conv2d_relu, im2col and col2im (include/nnh.h).
 //
 // Forward (src/autograd/ops.cpp:1345-1410): a short depth (K = Cin*kh*kw <= kDirectMaxK, a network's first
-// layer) runs as a direct convolution fused with bias/ReLU, memory-bound; a longer depth is one batched MFMA
-// GEMM W[Cout x K] col_n[K x hw] over all samples with the bias/ReLU/alive epilogue, whose B tiles are gathered
-// from x (implicit im2col: the column matrix is never stored). Both give each output the reference's fma
-// chain over k = (c, ph, pw) in order.
+// layer) runs as a direct convolution fused with bias/ReLU, memory-bound; 3x3, stride 1, padding 1 on small
+// planes runs with the padded sample in LDS (conv_fwd3.hip); any other depth is one batched MFMA GEMM
+// W[Cout x K] col_n[K x hw] over all samples with the bias/ReLU/alive epilogue, whose B tiles are gathered from x
+// (implicit im2col: the column matrix is never stored). All give each output the reference's fma chain over
+// k = (c, ph, pw) in order.
 // Backward (ops.cpp:1418-1463): g masked by alive; db = per-sample lane_sum, then summed in sample order;
-// dW_n = g_n col_n^T (batched sgemm F,T, col_n gathered from x), summed in sample order; dcol_n = W^T g_n
-// then col2im in gather form into a zero-filled (fresh) or existing dx: one kernel with dcol in LDS when a
-// sample's output positions fit it (conv_dx.hip), else a batched sgemm T,F into the workspace and col2im.
+// dW_n = g_n col_n^T, summed in sample order; dcol_n = W^T g_n then col2im in gather form into a zero-filled
+// (fresh) or existing dx. For 3x3, stride 1, padding 1 on small planes one kernel takes the mask, the
+// per-sample db and dW_n with its operands in LDS (conv_dw3.hip); otherwise the mask and db take one pass and
+// dW_n a batched sgemm F,T with col_n gathered from x. The two sample-order sums share a launch. dx is one
+// kernel with dcol in LDS when a sample's output positions fit it (conv_dx.hip), else a batched sgemm T,F into
+// the workspace and col2im.
 // A fresh dW or db is stored as the sum s, where the reference adds s to a zero-filled gradient (0 + s): the
 // two agree because every such sum starts at +0 (fma chains, lane sums and Tensor::sum(0) alike) and so is
 // never -0.
