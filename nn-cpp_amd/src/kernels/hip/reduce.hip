@@ -37,16 +37,17 @@ __global__ void __launch_bounds__(256) sum_rows_kernel(const float* __restrict__
 // rows in order onto their running sums, while the next chunk's loads are already in flight. Narrow blocks give
 // many blocks (one column's chain is serial, so the parallelism is the number of columns). Same bits as
 // sum_rows_kernel.
-constexpr int kSumCols = 16, kSumChunk = 256;
+constexpr int kSumCols = 32, kSumChunk = 128;
+constexpr int kSumQuads = kSumCols / 4;  // 16-byte groups per row of a block
 constexpr int kSumPer = kSumCols * kSumChunk / 256;  // floats each thread loads per chunk
 
 __device__ __forceinline__ void sum_chunk_load(const float* __restrict__ src, int rows, int inner, int c0, int ncol,
                                                int r0, int vec, float (&v)[kSumPer]) {
 	const int tid = threadIdx.x;
-	if (vec) {  // inner % 4 == 0 and 16-byte aligned: four threads per row, 16 bytes each
+	if (vec) {  // inner % 4 == 0 and 16-byte aligned: kSumQuads threads per row, 16 bytes each
 #pragma unroll
 		for (int u = 0; u < kSumPer / 4; ++u) {
-			const int idx = tid + 256 * u, r = min(r0 + (idx >> 2), rows - 1), q = 4 * (idx & 3);
+			const int idx = tid + 256 * u, r = min(r0 + idx / kSumQuads, rows - 1), q = 4 * (idx % kSumQuads);
 			const f32x4 x = *reinterpret_cast<const f32x4*>(src + (int64_t)r * inner + c0 + min(q, ncol - 4));
 #pragma unroll
 			for (int c = 0; c < 4; ++c) v[4 * u + c] = x[c];
@@ -54,7 +55,7 @@ __device__ __forceinline__ void sum_chunk_load(const float* __restrict__ src, in
 	} else {
 #pragma unroll
 		for (int u = 0; u < kSumPer; ++u) {
-			const int idx = tid + 256 * u, r = min(r0 + (idx >> 4), rows - 1), c = min(idx & 15, ncol - 1);
+			const int idx = tid + 256 * u, r = min(r0 + idx / kSumCols, rows - 1), c = min(idx % kSumCols, ncol - 1);
 			v[u] = src[(int64_t)r * inner + c0 + c];
 		}
 	}
@@ -66,13 +67,13 @@ __device__ __forceinline__ void sum_chunk_store(float (*tile)[kSumCols], int vec
 #pragma unroll
 		for (int u = 0; u < kSumPer / 4; ++u) {
 			const int idx = tid + 256 * u;
-			*reinterpret_cast<f32x4*>(&tile[idx >> 2][4 * (idx & 3)]) = f32x4{v[4 * u], v[4 * u + 1], v[4 * u + 2], v[4 * u + 3]};
+			*reinterpret_cast<f32x4*>(&tile[idx / kSumQuads][4 * (idx % kSumQuads)]) = f32x4{v[4 * u], v[4 * u + 1], v[4 * u + 2], v[4 * u + 3]};
 		}
 	} else {
 #pragma unroll
 		for (int u = 0; u < kSumPer; ++u) {
 			const int idx = tid + 256 * u;
-			tile[idx >> 4][idx & 15] = v[u];
+			tile[idx / kSumCols][idx % kSumCols] = v[u];
 		}
 	}
 }
