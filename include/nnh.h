@@ -26,6 +26,7 @@ extern "C" {
 #define NNH_ERR_SHAPE 2    /* non-conformable shapes: nn-cpp's TensorShapeError */
 #define NNH_ERR_ALIAS 3    /* output overlaps an input (forbidden by include/nn/kernels/gemm.hpp:37-39) */
 #define NNH_ERR_HIP 4      /* HIP runtime error (no device, launch failure, out of memory) */
+#define NNH_ERR_WORKSPACE 5 /* the caller registered a workspace for the stream that is smaller than the call needs */
 
 #define NNH_MAX_BATCH_DIMS 4
 
@@ -52,6 +53,37 @@ typedef struct nnh_epilogue {
 	const float* bias;
 	unsigned char* alive;
 } nnh_epilogue;
+
+/*
+ * Scratch memory. Some calls need device scratch beyond their inputs and outputs (depth-cut partial sums, the
+ * convolution backward's masked gradient and per-sample sums, attention's dS). Each (device, stream) pair has one
+ * scratch buffer, used by the calls on that stream in turn. By default the library owns it: allocated on the first
+ * call that needs it, grown on demand, kept until the process ends.
+ *
+ * nnh_set_workspace registers a caller-owned device buffer of `bytes` bytes as the scratch of every call on
+ * `stream` (on the device the stream belongs to). After it, no call on that stream allocates device memory: a call
+ * that needs more than `bytes` returns NNH_ERR_WORKSPACE before launching anything. The buffer must stay valid
+ * until the work enqueued on the stream with it has finished. workspace NULL with bytes 0 gives the stream back to
+ * the library's own buffer. There is no counterpart in the reference, whose only scratch is thread-local packing
+ * buffers (src/kernels/gemm.cpp:354, 395, 416, 467).
+ *
+ * The *_workspace_size queries give, for the same shape arguments as the call, the bytes that call takes (at least
+ * what it needs: where a kernel choice depends on pointer alignment, the larger of the two).
+ */
+int nnh_set_workspace(void* stream, void* workspace, size_t bytes);
+int nnh_sgemm_workspace_size(size_t m, size_t n, size_t k, size_t batch_count, size_t* bytes);
+int nnh_matmul_workspace_size(const size_t* a_shape, int a_ndim, const size_t* b_shape, int b_ndim, int trans_a,
+                              int trans_b, size_t* bytes);
+int nnh_linear_forward_workspace_size(size_t M, size_t K, size_t n, size_t* bytes);
+int nnh_linear_backward_workspace_size(const size_t* lead, int nlead, size_t K, size_t n, int want_dx, int want_dw,
+                                       int want_db, size_t* bytes);
+int nnh_conv2d_forward_workspace_size(size_t N, size_t Cin, size_t H, size_t W, size_t Cout, size_t kh, size_t kw,
+                                      int stride, int padding, size_t* bytes);
+int nnh_conv2d_backward_workspace_size(size_t N, size_t Cin, size_t H, size_t W, size_t Cout, size_t kh, size_t kw,
+                                       int stride, int padding, int with_alive, int want_dx, int want_dw, int want_db,
+                                       size_t* bytes);
+int nnh_attention_forward_workspace_size(size_t N, size_t Tq, size_t Tk, size_t D, size_t heads, size_t* bytes);
+int nnh_attention_backward_workspace_size(size_t N, size_t Tq, size_t Tk, size_t D, size_t heads, size_t* bytes);
 
 /* Message of the calling thread's last failed call ("" if none). */
 const char* nnh_last_error(void);

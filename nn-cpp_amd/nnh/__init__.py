@@ -15,7 +15,7 @@ BENCH_LIB_PATH = os.path.join(PKG_ROOT, "lib", "libnnh_bench.so")
 REPO_ROOT = os.path.dirname(PKG_ROOT)
 HEADER_PATH = os.path.join(REPO_ROOT, "include", "nnh.h")
 
-OK, ERR_INVALID, ERR_SHAPE, ERR_ALIAS, ERR_HIP = 0, 1, 2, 3, 4
+OK, ERR_INVALID, ERR_SHAPE, ERR_ALIAS, ERR_HIP, ERR_WORKSPACE = 0, 1, 2, 3, 4, 5
 BIAS_NONE, BIAS_COL, BIAS_ROW = 0, 1, 2
 MAX_BATCH_DIMS = 4
 
@@ -75,9 +75,41 @@ _EXTRA_DECLS = {
     "nnh_conv2d_forward": [_vp, _sz, _sz, _sz, _sz, _vp, _sz, _sz, _sz, _vp, C.c_int, C.c_int, C.c_int, _vp, _vp, _vp],
     "nnh_conv2d_backward": [_vp, _vp, _vp, _vp, _sz, _sz, _sz, _sz, _sz, _sz, _sz, C.c_int, C.c_int, _vp, C.c_int,
                             _vp, C.c_int, _vp, C.c_int, _vp],
+    "nnh_set_workspace": [_vp, _vp, _sz],
+    "nnh_sgemm_workspace_size": [_sz, _sz, _sz, _sz, _szp],
+    "nnh_matmul_workspace_size": [_szp, C.c_int, _szp, C.c_int, C.c_int, C.c_int, _szp],
+    "nnh_linear_forward_workspace_size": [_sz, _sz, _sz, _szp],
+    "nnh_linear_backward_workspace_size": [_szp, C.c_int, _sz, _sz, C.c_int, C.c_int, C.c_int, _szp],
+    "nnh_conv2d_forward_workspace_size": [_sz, _sz, _sz, _sz, _sz, _sz, _sz, C.c_int, C.c_int, _szp],
+    "nnh_conv2d_backward_workspace_size": [_sz, _sz, _sz, _sz, _sz, _sz, _sz, C.c_int, C.c_int, C.c_int, C.c_int,
+                                           C.c_int, C.c_int, _szp],
+    "nnh_attention_forward_workspace_size": [_sz, _sz, _sz, _sz, _sz, _szp],
+    "nnh_attention_backward_workspace_size": [_sz, _sz, _sz, _sz, _sz, _szp],
     "nnh_im2col": [_vp, _sz, _sz, _sz, _sz, _sz, _sz, C.c_int, C.c_int, _vp, _vp],
     "nnh_col2im_add": [_vp, _sz, _sz, _sz, _sz, _sz, _sz, C.c_int, C.c_int, _vp, C.c_int, _vp],
 }
+
+
+def workspace_size(name, *args):
+    """Bytes of scratch the call nnh_<name> takes, from its nnh_<name>_workspace_size query (the call's shape
+    arguments; a list or tuple becomes a size_t array)."""
+    conv = []
+    for a in args:
+        if isinstance(a, (list, tuple)):
+            conv.append((C.c_size_t * max(1, len(a)))(*a))
+        else:
+            conv.append(a)
+    out = C.c_size_t(0)
+    check(getattr(lib(), f"nnh_{name}_workspace_size")(*conv, C.byref(out)))
+    return out.value
+
+
+def set_workspace(buf, stream=None):
+    """Registers the device tensor buf as the scratch of every call on stream (None: the library owns it again)."""
+    if buf is None:
+        check(lib().nnh_set_workspace(_stream(stream), None, 0))
+    else:
+        check(lib().nnh_set_workspace(_stream(stream), C.c_void_p(buf.data_ptr()), buf.numel() * buf.element_size()))
 
 
 def lib():
@@ -100,10 +132,15 @@ def check(rc):
 
 
 def header_functions():
-    """Names of every function include/nnh.h declares."""
+    """Names of every function the headers of libnnh declare (include/nnh*.h except nnh_host.h, which belongs to
+    the drop-in library)."""
+    import glob
     import re
-    text = open(HEADER_PATH).read()
-    return sorted(set(re.findall(r"\b(nnh_[a-z0-9_]+)\s*\(", text)))
+    names = set()
+    for path in glob.glob(os.path.join(os.path.dirname(HEADER_PATH), "nnh*.h")):
+        if os.path.basename(path) != "nnh_host.h":
+            names |= set(re.findall(r"\b(nnh_[a-z0-9_]+)\s*\(", open(path).read()))
+    return sorted(names)
 
 
 # ---- torch plumbing ----

@@ -13,6 +13,7 @@
 
 #include "abi_common.hpp"
 #include "kernels/hip/gemm.hpp"
+#include "workspace.hpp"
 
 namespace nnh {
 
@@ -114,7 +115,30 @@ int build_gemm(int ta, int tb, size_t m, size_t n, size_t k, const float* a, siz
 
 int run_gemm(const GemmCall& g, void* stream, int config, float* workspace) {
 	if (g.m == 0 || g.n == 0 || g.batch_count == 0) return NNH_OK;
+	if (!workspace) {
+		const int rc = check_workspace(stream, gemm_workspace_bytes(g));
+		if (rc != NNH_OK) return rc;
+	}
 	return hip_status(gemm_launch(g, reinterpret_cast<hipStream_t>(stream), config, workspace), "sgemm launch");
+}
+
+int check_workspace(void* stream, size_t bytes) {
+	if (bytes == 0) return NNH_OK;
+	bool external = false;
+	size_t have = 0;
+	const int rc = hip_status(stream_workspace_external(reinterpret_cast<hipStream_t>(stream), external, have),
+	                          "workspace lookup");
+	if (rc != NNH_OK) return rc;
+	if (external && have < bytes)
+		return fail(NNH_ERR_WORKSPACE, "the stream's workspace holds " + std::to_string(have) + " bytes; this call needs " +
+		                                   std::to_string(bytes));
+	return NNH_OK;
+}
+
+int put_bytes(size_t* out, size_t bytes) {
+	if (!out) return fail(NNH_ERR_INVALID, "bytes is null");
+	*out = bytes;
+	return NNH_OK;
 }
 
 }  // namespace nnh
@@ -150,6 +174,25 @@ int nnh_sgemm_config(int trans_a, int trans_b, size_t m, size_t n, size_t k, con
 	if (rc != NNH_OK) return rc;
 	if (config < -1 || config >= gemm_config_count()) return fail(NNH_ERR_INVALID, "no such kernel configuration");
 	return run_gemm(g, stream, config);
+}
+
+int nnh_set_workspace(void* stream, void* workspace, size_t bytes) {
+	if (bytes > 0 && !workspace) return fail(NNH_ERR_INVALID, "workspace is null");
+	return hip_status(set_stream_workspace(reinterpret_cast<hipStream_t>(stream), workspace, bytes), "set workspace");
+}
+
+int nnh_sgemm_workspace_size(size_t m, size_t n, size_t k, size_t batch_count, size_t* bytes) {
+	return put_bytes(bytes, gemm_workspace_bytes(m, n, k, batch_count));
+}
+
+int nnh_matmul_workspace_size(const size_t* a_shape, int a_ndim, const size_t* b_shape, int b_ndim, int trans_a,
+                              int trans_b, size_t* bytes) {
+	MatmulPlan plan;
+	const int rc = plan_matmul(a_shape, a_ndim, b_shape, b_ndim, trans_a, trans_b, plan);
+	if (rc != NNH_OK) return rc;
+	size_t count = 1;
+	for (int d = 0; d < plan.batch.ndim; ++d) count *= plan.batch.shape[d];
+	return put_bytes(bytes, gemm_workspace_bytes(plan.m, plan.n, plan.k, count));
 }
 
 int nnh_gemm_config_count(void) { return gemm_config_count(); }

@@ -21,8 +21,18 @@ int build_gemm(int ta, int tb, size_t m, size_t n, size_t k, const float* a, siz
                float* c, size_t ldc, int accumulate, const nnh_batch* batch, const nnh_epilogue* ep, GemmCall& g,
                const ColGather* gather = nullptr);
 // workspace: depth-cut partials (at least gemm_workspace_floats(g)), required when the caller holds the
-// stream's StreamWorkspace; otherwise null.
+// stream's StreamWorkspace; otherwise null (the partials then come from the stream's workspace, checked first).
 int run_gemm(const GemmCall& g, void* stream, int config, float* workspace = nullptr);
+// Bytes of stream workspace g's depth-cut partials take (0 without a depth cut).
+inline size_t gemm_workspace_bytes(const GemmCall& g) { return (size_t)gemm_workspace_floats(g) * sizeof(float); }
+inline size_t gemm_workspace_bytes(size_t m, size_t n, size_t k, size_t batch_count) {
+	return (size_t)gemm_workspace_floats((int64_t)m, (int64_t)n, (int64_t)k, (int64_t)batch_count) * sizeof(float);
+}
+// NNH_ERR_WORKSPACE when the caller registered a workspace for the stream that holds fewer than `bytes`;
+// called by every entry point before it launches anything.
+int check_workspace(void* stream, size_t bytes);
+// Stores a workspace query's answer.
+int put_bytes(size_t* out, size_t bytes);
 
 // How nn::matmul(a, b, trans_a, trans_b) (src/tensor.cpp:571-641) maps onto one (batched) GEMM.
 struct MatmulPlan {

@@ -14,6 +14,7 @@
 
 #include <algorithm>
 
+#include "gemm.hpp"
 #include "gemm_tile.hpp"
 
 namespace nnh {
@@ -233,6 +234,9 @@ int dx_group(const ConvGeom& g) {
 bool conv_dx_fused_ok(const ConvGeom& g, int64_t samples, int cout) {
 	const int64_t hw = (int64_t)g.ho * g.wo;
 	if (hw < 1 || hw > kDxPos || cout < 1 || g.kh * g.kw > kDxRows) return false;
+	// the reference's dcol product sgemm(T, F, K, hw, Cout) (ops.cpp:1452) splits into 128-deep pieces over the
+	// output channels when it takes the depth cut; this kernel runs one chain over all of them
+	if (depth_cut((int64_t)g.cin * g.kh * g.kw, hw, cout)) return false;
 	const int cg = dx_group(g);
 	if (cg < 1) return false;
 	const int64_t groups = (g.cin + cg - 1) / cg;

@@ -85,13 +85,6 @@ hipError_t prepare_device() {
 			if (e != hipSuccess) return e;
 		}
 	}
-	// Workspaces (depth-cut partials, im2col columns, attention's dS) come from the device's stream-ordered pool;
-	// keep freed blocks in the pool instead of returning them at every synchronisation, so repeated calls reuse them.
-	hipMemPool_t pool = nullptr;
-	if (hipDeviceGetDefaultMemPool(&pool, dev) == hipSuccess && pool) {
-		uint64_t keep = UINT64_MAX;
-		(void)hipMemPoolSetAttribute(pool, hipMemPoolAttrReleaseThreshold, &keep);
-	}
 	done[dev] = true;
 	return hipSuccess;
 }

@@ -64,9 +64,52 @@ int gemm(int ta, int tb, size_t m, size_t n, size_t k, const float* A, size_t ld
 	return run_gemm(g, stream, -1, partials);
 }
 
+// One workspace for nnh_attention_backward: dS, then the depth-cut partials the dV, dQ and dK products share
+// (they run in turn).
+struct BwdPlan {
+	size_t total = 0, off_ds = 0, off_part = 0;
+	int64_t part = 0;
+};
+
+BwdPlan attention_backward_plan(const AttnGeom& a) {
+	BwdPlan p;
+	if (a.N == 0) return p;
+	WorkspacePlan plan;
+	p.off_ds = plan.add(a.N * a.H * a.Tq * a.Tk * sizeof(float));
+	const int64_t nb = (int64_t)(a.N * a.H);
+	p.part = std::max({gemm_workspace_floats((int64_t)a.Tk, (int64_t)a.Dh, (int64_t)a.Tq, nb),
+	                   gemm_workspace_floats((int64_t)a.Tq, (int64_t)a.Dh, (int64_t)a.Tk, nb),
+	                   gemm_workspace_floats((int64_t)a.Tq, (int64_t)a.Tk, (int64_t)a.Dh, nb)});
+	p.off_part = p.part ? plan.add((size_t)p.part * sizeof(float)) : 0;
+	p.total = plan.total;
+	return p;
+}
+
+// Scratch of nnh_attention_forward: the depth-cut partials of the S and O products where the three-launch path
+// may run (the fused kernel needs none).
+size_t attention_forward_ws(const AttnGeom& a) {
+	if (a.N == 0) return 0;
+	const size_t nb = a.N * a.H;
+	return std::max(gemm_workspace_bytes(a.Tq, a.Tk, a.Dh, nb), gemm_workspace_bytes(a.Tq, a.Dh, a.Tk, nb));
+}
+
 }  // namespace
 
 extern "C" {
+
+int nnh_attention_forward_workspace_size(size_t N, size_t Tq, size_t Tk, size_t D, size_t heads, size_t* bytes) {
+	AttnGeom a;
+	const int rc = check_attention(N, Tq, Tk, D, heads, 0, a);
+	if (rc != NNH_OK) return rc;
+	return put_bytes(bytes, attention_forward_ws(a));
+}
+
+int nnh_attention_backward_workspace_size(size_t N, size_t Tq, size_t Tk, size_t D, size_t heads, size_t* bytes) {
+	AttnGeom a;
+	const int rc = check_attention(N, Tq, Tk, D, heads, 0, a);
+	if (rc != NNH_OK) return rc;
+	return put_bytes(bytes, attention_backward_plan(a).total);
+}
 
 int nnh_attention_forward(const float* q, const float* k, const float* v, size_t N, size_t Tq, size_t Tk, size_t D,
                           size_t heads, const float* key_padding_mask, int causal, float* out, float* probs,
@@ -77,6 +120,12 @@ int nnh_attention_forward(const float* q, const float* k, const float* v, size_t
 	if (N == 0) return NNH_OK;
 	if (!q || !k || !v || !out || !probs) return fail(NNH_ERR_INVALID, "attention: null pointer");
 	hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+	const bool fused_fwd = attention_fused_ok((int64_t)Tq, (int64_t)Tk, (int64_t)a.Dh, (int64_t)D, q, k, v, out, probs,
+	                                          key_padding_mask);
+	if (!fused_fwd) {
+		rc = check_workspace(stream, attention_forward_ws(a));
+		if (rc != NNH_OK) return rc;
+	}
 	if (attention_fused_ok((int64_t)Tq, (int64_t)Tk, (int64_t)a.Dh, (int64_t)D, q, k, v, out, probs, key_padding_mask))
 		return hip_status(attention_fused_forward(q, k, v, (int64_t)N, (int64_t)Tq, (int64_t)Tk, (int64_t)D,
 		                                          (int64_t)heads, key_padding_mask, causal, a.scale, out, probs, s),
@@ -103,18 +152,13 @@ int nnh_attention_backward(const float* g, const float* q, const float* k, const
 	if (N == 0 || (!dq && !dk && !dv)) return NNH_OK;
 	if (!g || !q || !k || !v || !probs) return fail(NNH_ERR_INVALID, "attention backward: null pointer");
 	hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-	// one workspace: dS, then the depth-cut partials the dV, dQ and dK products share (they run in turn)
-	WorkspacePlan plan;
-	const size_t off_ds = plan.add(N * heads * Tq * Tk * sizeof(float));
-	const int64_t nb = (int64_t)(N * heads);
-	const int64_t part = std::max({gemm_workspace_floats((int64_t)Tk, (int64_t)a.Dh, (int64_t)Tq, nb),
-	                               gemm_workspace_floats((int64_t)Tq, (int64_t)a.Dh, (int64_t)Tk, nb),
-	                               gemm_workspace_floats((int64_t)Tq, (int64_t)Tk, (int64_t)a.Dh, nb)});
-	const size_t off_part = part ? plan.add((size_t)part * sizeof(float)) : 0;
+	const BwdPlan plan = attention_backward_plan(a);
+	rc = check_workspace(stream, plan.total);
+	if (rc != NNH_OK) return rc;
 	StreamWorkspace ws(s, plan.total);
 	if (ws.error() != hipSuccess) return hip_status(ws.error(), "attention workspace");
-	float* ds = ws.at<float>(off_ds);
-	float* partials = part ? ws.at<float>(off_part) : nullptr;
+	float* ds = ws.at<float>(plan.off_ds);
+	float* partials = plan.part ? ws.at<float>(plan.off_part) : nullptr;
 	const bool fused = (dq || dk) && attention_fused_ok((int64_t)Tq, (int64_t)Tk, (int64_t)a.Dh, (int64_t)D, g, v, v, ds,
 	                                                    probs, key_padding_mask);
 	if (fused)  // dP = G_h V_h^T and the softmax backward in one kernel (ops.cpp:1286, 1289-1290)

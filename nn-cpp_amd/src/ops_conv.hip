@@ -75,9 +75,59 @@ ColGather col_gather(const ConvGeom& g) {
 	return c;
 }
 
+// One workspace for nnh_conv2d_backward: the masked gradient, per-sample bias and weight gradients, dcol, and
+// the depth-cut partials of the two GEMMs (which run one after the other and share them).
+struct BwdPlan {
+	size_t total = 0, off_m = 0, off_gb = 0, off_gw = 0, off_col = 0, off_part = 0;
+	int64_t part = 0;
+	bool dx_fused = false;
+};
+
+BwdPlan conv_backward_plan(const ConvGeom& geo, size_t N, size_t Cout, bool alive, bool dx, bool dw, bool db) {
+	BwdPlan p;
+	const size_t hw = (size_t)geo.ho * geo.wo, K = (size_t)geo.cin * geo.kh * geo.kw;
+	if (N == 0 || (!dx && !dw && !db)) return p;
+	WorkspacePlan plan;
+	p.off_m = alive ? plan.add(N * Cout * hw * 4) : 0;
+	p.off_gb = db ? plan.add(N * Cout * 4) : 0;
+	p.off_gw = dw ? plan.add(N * Cout * K * 4) : 0;
+	p.dx_fused = dx && conv_dx_fused_ok(geo, (int64_t)N, (int)Cout);
+	p.off_col = dx && !p.dx_fused ? plan.add(N * K * hw * 4) : 0;
+	p.part = std::max(dw ? gemm_workspace_floats((int64_t)Cout, (int64_t)K, (int64_t)hw, (int64_t)N) : 0,
+	                  dx && !p.dx_fused ? gemm_workspace_floats((int64_t)K, (int64_t)hw, (int64_t)Cout, (int64_t)N) : 0);
+	p.off_part = p.part ? plan.add((size_t)p.part * 4) : 0;
+	p.total = plan.total;
+	return p;
+}
+
+// Scratch of nnh_conv2d_forward: the depth-cut partials of the batched implicit GEMM, where that path may run
+// (the direct and LDS kernels need none).
+size_t conv_forward_ws(const ConvGeom& g, size_t N, size_t Cout) {
+	const size_t hw = (size_t)g.ho * g.wo, K = (size_t)g.cin * g.kh * g.kw;
+	if (N == 0 || Cout == 0 || hw == 0 || K <= kDirectMaxK) return 0;
+	return gemm_workspace_bytes(Cout, hw, K, N);
+}
+
 }  // namespace
 
 extern "C" {
+
+int nnh_conv2d_forward_workspace_size(size_t N, size_t Cin, size_t H, size_t W, size_t Cout, size_t kh, size_t kw,
+                                      int stride, int padding, size_t* bytes) {
+	ConvGeom g;
+	const int rc = conv_geometry(N, Cin, H, W, Cout, kh, kw, stride, padding, g);
+	if (rc != NNH_OK) return rc;
+	return put_bytes(bytes, conv_forward_ws(g, N, Cout));
+}
+
+int nnh_conv2d_backward_workspace_size(size_t N, size_t Cin, size_t H, size_t W, size_t Cout, size_t kh, size_t kw,
+                                       int stride, int padding, int with_alive, int want_dx, int want_dw, int want_db,
+                                       size_t* bytes) {
+	ConvGeom g;
+	const int rc = conv_geometry(N, Cin, H, W, Cout, kh, kw, stride, padding, g);
+	if (rc != NNH_OK) return rc;
+	return put_bytes(bytes, conv_backward_plan(g, N, Cout, with_alive, want_dx, want_dw, want_db).total);
+}
 
 int nnh_conv2d_forward(const float* x, size_t N, size_t Cin, size_t H, size_t W, const float* w, size_t Cout,
                        size_t kh, size_t kw, const float* bias, int stride, int padding, int fuse_relu, float* y,
@@ -126,24 +176,16 @@ int nnh_conv2d_backward(const float* g, const float* x, const float* w, const un
 		return rc;
 	}
 	if (!g || !x || !w) return fail(NNH_ERR_INVALID, "conv2d backward: null pointer");
-	// one workspace: the masked gradient, per-sample bias and weight gradients, dcol, and the depth-cut partials
-	// of the two GEMMs (which run one after the other and share them)
-	WorkspacePlan plan;
-	const size_t off_m = alive ? plan.add(N * Cout * hw * 4) : 0;
-	const size_t off_gb = db ? plan.add(N * Cout * 4) : 0;
-	const size_t off_gw = dw ? plan.add(N * Cout * K * 4) : 0;
-	const bool dx_fused = dx && conv_dx_fused_ok(geo, (int64_t)N, (int)Cout);
-	const size_t off_col = dx && !dx_fused ? plan.add(N * K * hw * 4) : 0;
-	const int64_t part =
-	    std::max(dw ? gemm_workspace_floats((int64_t)Cout, (int64_t)K, (int64_t)hw, (int64_t)N) : 0,
-	             dx && !dx_fused ? gemm_workspace_floats((int64_t)K, (int64_t)hw, (int64_t)Cout, (int64_t)N) : 0);
-	const size_t off_part = part ? plan.add((size_t)part * 4) : 0;
+	const BwdPlan plan = conv_backward_plan(geo, N, Cout, alive != nullptr, dx != nullptr, dw != nullptr, db != nullptr);
+	rc = check_workspace(stream, plan.total);
+	if (rc != NNH_OK) return rc;
+	const bool dx_fused = plan.dx_fused;
 	StreamWorkspace ws(s, plan.total);
 	if (ws.error() != hipSuccess) return hip_status(ws.error(), "conv2d workspace");
-	float* partials = part ? ws.at<float>(off_part) : nullptr;
-	float* m = alive ? ws.at<float>(off_m) : nullptr;
-	float* gb = db ? ws.at<float>(off_gb) : nullptr;
-	float* gw = dw ? ws.at<float>(off_gw) : nullptr;
+	float* partials = plan.part ? ws.at<float>(plan.off_part) : nullptr;
+	float* m = alive ? ws.at<float>(plan.off_m) : nullptr;
+	float* gb = db ? ws.at<float>(plan.off_gb) : nullptr;
+	float* gw = dw ? ws.at<float>(plan.off_gw) : nullptr;
 	const float* gm = alive ? m : g;
 	// 3x3, stride 1, padding 1 on small planes: one kernel takes the mask (ops.cpp:1439-1443), the per-sample bias
 	// sums (1445) and the per-sample weight gradients (1448-1449) with its operands in LDS
@@ -180,7 +222,7 @@ int nnh_conv2d_backward(const float* g, const float* x, const float* w, const un
 	if (rc == NNH_OK && dx && dx_fused) {  // ops.cpp:1452-1455, dcol kept on chip
 		rc = hip_status(conv_dx_fused(gm, w, dx, geo, (int64_t)N, (int)Cout, dx_first ? 1 : 0, s), "conv2d dx");
 	} else if (rc == NNH_OK && dx) {  // ops.cpp:1452-1455
-		float* col = ws.at<float>(off_col);
+		float* col = ws.at<float>(plan.off_col);
 		nnh_batch b{};
 		b.ndim = 1;
 		b.shape[0] = N;

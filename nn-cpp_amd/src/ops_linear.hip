@@ -1,6 +1,7 @@
 // ops_linear.hip - extern "C" entry points of nn::linear and the ReLU node (include/nnh.h).
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <vector>
 
 #include "abi_common.hpp"
@@ -22,9 +23,39 @@ bool product_fits(const size_t* dims, int n, size_t& out) {
 	return true;
 }
 
+// Scratch of nnh_linear_backward: the depth-cut partials of dX and dW, or two buffers for a bias gradient
+// reduced over several leading axes; they are taken one after the other, so the largest is what it needs.
+size_t linear_backward_ws(const size_t* lead, int nlead, size_t M, size_t K, size_t n, bool dx, bool dw, bool db) {
+	size_t bytes = 0;
+	if (dx) bytes = std::max(bytes, gemm_workspace_bytes(M, K, n, 1));
+	if (dw) bytes = std::max(bytes, gemm_workspace_bytes(n, K, M, 1));
+	if (db && n > 0 && nlead > 1) {
+		size_t row = n;
+		for (int d = 1; d < nlead; ++d) row *= lead[d];
+		WorkspacePlan plan;
+		const size_t tmp_bytes = (row ? row : 1) * sizeof(float);
+		plan.add(tmp_bytes);
+		plan.add(tmp_bytes);
+		bytes = std::max(bytes, plan.total);
+	}
+	return bytes;
+}
+
 }  // namespace
 
 extern "C" {
+
+int nnh_linear_forward_workspace_size(size_t M, size_t K, size_t n, size_t* bytes) {
+	return put_bytes(bytes, gemm_workspace_bytes(M, n, K, 1));
+}
+
+int nnh_linear_backward_workspace_size(const size_t* lead, int nlead, size_t K, size_t n, int want_dx, int want_dw,
+                                       int want_db, size_t* bytes) {
+	if (nlead < 1 || !lead) return fail(NNH_ERR_SHAPE, "linear input needs at least 2 dimensions");
+	size_t M = 0;
+	if (!product_fits(lead, nlead, M)) return fail(NNH_ERR_INVALID, "input size overflows");
+	return put_bytes(bytes, linear_backward_ws(lead, nlead, M, K, n, want_dx, want_dw, want_db));
+}
 
 int nnh_linear_forward(const float* x, size_t M, size_t K, const float* w, size_t n, const float* bias, int relu,
                        float* y, void* stream) {
@@ -44,6 +75,10 @@ int nnh_linear_backward(const float* g, const float* x, const float* w, const si
 	size_t M = 0;
 	if (!product_fits(lead, nlead, M)) return fail(NNH_ERR_INVALID, "input size overflows");
 	hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+	{
+		const int rc = check_workspace(stream, linear_backward_ws(lead, nlead, M, K, n, dx, dw, db));
+		if (rc != NNH_OK) return rc;
+	}
 	// db of a 2-D gradient is one Tensor::sum(0): each column of G folded over the rows in order from +0, which is
 	// the row sum of op(A) = G^T over k in the dW product, so that product computes it on the way
 	const bool db_in_dw = dw && db && nlead == 1 && M > 0 && K > 0 && n > 0 && !depth_cut((int64_t)n, (int64_t)K, (int64_t)M) &&

@@ -12,8 +12,10 @@ namespace {
 
 struct Slot {
 	std::mutex busy;            // held while a call enqueues work that uses the buffer
-	void* p = nullptr;
-	size_t bytes = 0;
+	void* owned = nullptr;      // the library's buffer (kept while a caller's buffer is registered)
+	size_t owned_bytes = 0;
+	void* ext = nullptr;        // the caller's buffer, when one is registered
+	size_t ext_bytes = 0;
 	hipEvent_t done = nullptr;  // recorded on the stream when the last user let go of the buffer
 	bool recorded = false;
 };
@@ -22,6 +24,17 @@ std::mutex table_mu;
 std::map<std::pair<int, hipStream_t>, Slot*> table;  // slots live until the process ends
 thread_local bool holding = false;
 
+hipError_t find_slot(hipStream_t s, Slot*& slot) {
+	hipDevice_t dev = 0;
+	const hipError_t e = hipStreamGetDevice(s, &dev);
+	if (e != hipSuccess) return e;
+	std::lock_guard<std::mutex> lock(table_mu);
+	Slot*& entry = table[{static_cast<int>(dev), s}];
+	if (!entry) entry = new Slot;
+	slot = entry;
+	return hipSuccess;
+}
+
 }  // namespace
 
 StreamWorkspace::StreamWorkspace(hipStream_t s, size_t bytes) : s_(s) {
@@ -29,16 +42,9 @@ StreamWorkspace::StreamWorkspace(hipStream_t s, size_t bytes) : s_(s) {
 		err_ = hipErrorInvalidValue;
 		return;
 	}
-	hipDevice_t dev = 0;
-	err_ = hipStreamGetDevice(s, &dev);
-	if (err_ != hipSuccess) return;
 	Slot* slot = nullptr;
-	{
-		std::lock_guard<std::mutex> lock(table_mu);
-		Slot*& e = table[{static_cast<int>(dev), s}];
-		if (!e) e = new Slot;
-		slot = e;
-	}
+	err_ = find_slot(s, slot);
+	if (err_ != hipSuccess) return;
 	slot->busy.lock();
 	slot_ = slot;
 	holding = true;
@@ -46,23 +52,31 @@ StreamWorkspace::StreamWorkspace(hipStream_t s, size_t bytes) : s_(s) {
 		err_ = hipStreamWaitEvent(s, slot->done, 0);
 		if (err_ != hipSuccess) return;
 	}
+	if (slot->ext) {  // the caller's buffer: never grown here (callers check the size before enqueueing)
+		if (bytes > slot->ext_bytes) {
+			err_ = hipErrorInvalidValue;
+			return;
+		}
+		ptr_ = slot->ext;
+		return;
+	}
 	bytes = std::max<size_t>(bytes, 256);
-	if (slot->bytes < bytes) {
-		const size_t grow = std::max(bytes, slot->bytes + slot->bytes / 2);
+	if (slot->owned_bytes < bytes) {
+		const size_t grow = std::max(bytes, slot->owned_bytes + slot->owned_bytes / 2);
 		void* p = nullptr;
 		err_ = hipMallocAsync(&p, grow, s);
 		if (err_ != hipSuccess) return;
-		if (slot->p) {
-			err_ = hipFreeAsync(slot->p, s);  // after every earlier use, in stream order
+		if (slot->owned) {
+			err_ = hipFreeAsync(slot->owned, s);  // after every earlier use, in stream order
 			if (err_ != hipSuccess) {
 				(void)hipFreeAsync(p, s);
 				return;
 			}
 		}
-		slot->p = p;
-		slot->bytes = grow;
+		slot->owned = p;
+		slot->owned_bytes = grow;
 	}
-	ptr_ = slot->p;
+	ptr_ = slot->owned;
 }
 
 StreamWorkspace::~StreamWorkspace() {
@@ -72,6 +86,29 @@ StreamWorkspace::~StreamWorkspace() {
 	slot->recorded = slot->done != nullptr && hipEventRecord(slot->done, s_) == hipSuccess;
 	holding = false;
 	slot->busy.unlock();
+}
+
+hipError_t set_stream_workspace(hipStream_t s, void* p, size_t bytes) {
+	if (holding) return hipErrorInvalidValue;
+	Slot* slot = nullptr;
+	const hipError_t e = find_slot(s, slot);
+	if (e != hipSuccess) return e;
+	std::lock_guard<std::mutex> lock(slot->busy);
+	slot->ext = bytes ? p : nullptr;
+	slot->ext_bytes = slot->ext ? bytes : 0;
+	return hipSuccess;
+}
+
+hipError_t stream_workspace_external(hipStream_t s, bool& external, size_t& bytes) {
+	Slot* slot = nullptr;
+	const hipError_t e = find_slot(s, slot);
+	external = false;
+	bytes = 0;
+	if (e != hipSuccess) return e;
+	std::lock_guard<std::mutex> lock(slot->busy);
+	external = slot->ext != nullptr;
+	bytes = slot->ext_bytes;
+	return hipSuccess;
 }
 
 }  // namespace nnh

@@ -93,3 +93,31 @@ def test_matmul_shapes_and_errors_match_nncpp(ref):
             assert rc == 0 and out.shape == got, (a_shape, b_shape, ta, tb)
         except nnh.ShapeError:
             assert rc == 2, (a_shape, b_shape, ta, tb)
+
+
+def test_workspace_queries_on_the_host():
+    """The *_workspace_size queries need no device: nn-cpp's depth cut (gemm.cpp:453-458) decides the GEMM's partials,
+    128-deep pieces of m n floats each, and the multi-step ops take the largest of their pieces."""
+    import nnh
+    assert nnh.workspace_size("sgemm", 64, 64, 4096, 1) == 32 * 64 * 64 * 4
+    assert nnh.workspace_size("sgemm", 40, 48, 1100, 3) == 9 * 40 * 48 * 4 * 3
+    assert nnh.workspace_size("sgemm", 512, 512, 512, 1) == 0          # m n > 2^16: no cut
+    assert nnh.workspace_size("sgemm", 16, 16, 2048, 1) == 0           # m n k < 2^20: no cut
+    assert nnh.workspace_size("matmul", [2, 40, 1100], 3, [1100, 48], 2, 0, 0) == 9 * 80 * 48 * 4  # folded: 80 x 48 x 1100
+    assert nnh.workspace_size("matmul", [3, 40, 1100], 3, [3, 1100, 48], 3, 0, 0) == 9 * 40 * 48 * 4 * 3
+    assert nnh.workspace_size("linear_forward", 40, 1100, 48) == 9 * 40 * 48 * 4
+    # linear backward: dW = G^T X is 48 x 1100 x 40 (no cut), dX = G W is 40 x 1100 x 48 (no cut); a 3-D input's
+    # bias gradient takes two buffers of lead[1] * n floats
+    assert nnh.workspace_size("linear_backward", [40], 1, 1100, 48, 1, 1, 1) == 0
+    assert nnh.workspace_size("linear_backward", [3, 5], 2, 20, 7, 0, 0, 1) == 2 * 256
+    # conv2d backward at config 3's conv2 (batch 128, 32 -> 64 on 14 x 14): masked gradient, per-sample db and dW
+    # (dx keeps dcol on chip for 196 positions)
+    N, Cout, hw, K = 128, 64, 196, 288
+    r = lambda b: (b + 255) // 256 * 256
+    assert nnh.workspace_size("conv2d_backward", N, 32, 14, 14, Cout, 3, 3, 1, 1, 1, 1, 1, 1) == \
+        r(N * Cout * hw * 4) + r(N * Cout * 4) + r(N * Cout * K * 4)
+    assert nnh.workspace_size("conv2d_forward", N, 1, 28, 28, 32, 3, 3, 1, 1) == 0  # direct kernel
+    # attention backward at config 4: dS, one float per score
+    assert nnh.workspace_size("attention_backward", 32, 256, 256, 512, 8) == 32 * 8 * 256 * 256 * 4
+    with pytest.raises(nnh.ShapeError):
+        nnh.workspace_size("attention_backward", 2, 4, 4, 10, 3)  # heads must divide D

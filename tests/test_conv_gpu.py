@@ -121,6 +121,7 @@ DX_CASES = [
     (2, 4, 6, 10, 33, 2, 3, 1, 0),      # rectangular kernel, no padding
     (1, 3, 16, 16, 20, 9, 9, 1, 4),     # 81 taps: one channel per group does not fit 80 rows
     (2, 6, 17, 17, 24, 3, 3, 1, 1),     # 289 outputs: the GEMM + col2im path
+    (2, 8, 8, 8, 512, 3, 3, 1, 1),      # dcol = W^T g (72 x 64 x 512) takes the depth cut: the GEMM + col2im path
 ]
 
 

@@ -164,3 +164,59 @@ def test_attention_backward_and_depth_cut_gemm_queued(gpu, oracle):
         for t, w_, name in zip(grads, want, ("dq", "dk", "dv")):
             assert_same(t.cpu().numpy(), w_, (i, name))
         assert_same(c.cpu().numpy(), wc, (i, "sgemm depth cut"))
+
+
+def test_caller_workspace_sized_by_the_query(gpu):
+    """A caller's buffer registered with nnh_set_workspace and sized by each op's *_workspace_size query gives the
+    same bits as the library's own buffer; one 256 bytes short makes the call return NNH_ERR_WORKSPACE before it
+    launches anything (the outputs keep their sentinel), and unregistering gives the stream back to the library."""
+    import nnh
+    import torch
+    s = torch.cuda.Stream()
+    conv = conv_case(41, 8, 32, 14, 64)
+    att_in = [dev(synth.normal(50 + i, (2, 64, 128))) for i in range(4)]
+    a_cut, b_cut = dev(synth.mt19937_uniform(60, 64 * 4096, -1, 1)), dev(synth.mt19937_uniform(61, 4096 * 64, -1, 1))
+    xl, wl, gl = dev(synth.normal(62, (3, 5, 20))), dev(synth.normal(63, (7, 20))), dev(synth.normal(64, (3, 5, 7)))
+
+    def run_all():
+        with torch.cuda.stream(s):
+            outs = list(conv_backward(conv, stream=s))
+            out, probs = nnh.attention_forward(*att_in[:3], 2, stream=s)
+            dq, dk, dv = (torch.full_like(att_in[0], 3.0) for _ in range(3))
+            nnh.attention_backward(att_in[3], *att_in[:3], probs, 2, None, False, dq, True, dk, True, dv, True, stream=s)
+            c = torch.full((64, 64), 3.0, device="cuda")
+            nnh.sgemm(0, 0, 64, 64, 4096, a_cut, 4096, b_cut, 64, c, 64, stream=s)
+            dxl, dwl, dbl = torch.full_like(xl, 3.0), torch.full_like(wl, 3.0), torch.full((7,), 3.0, device="cuda")
+            nnh.linear_backward(gl, xl, wl, dxl, True, dwl, True, dbl, True, stream=s)
+            outs += [out, probs, dq, dk, dv, c, dxl, dwl, dbl]
+        s.synchronize()
+        return [t.cpu().numpy() for t in outs]
+
+    want = run_all()
+    need = max(nnh.workspace_size("conv2d_backward", 8, 32, 14, 14, 64, 3, 3, 1, 1, 1, 1, 1, 1),
+               nnh.workspace_size("attention_backward", 2, 64, 64, 128, 2),
+               nnh.workspace_size("sgemm", 64, 64, 4096, 1),
+               nnh.workspace_size("linear_backward", [3, 5], 2, 20, 7, 1, 1, 1))
+    assert nnh.workspace_size("sgemm", 64, 64, 4096, 1) == 32 * 64 * 64 * 4  # 32 pieces of 128
+    buf = torch.empty(need // 4 + 1, device="cuda")
+    try:
+        nnh.set_workspace(buf, stream=s)
+        got = run_all()
+        for i, (g_, w_) in enumerate(zip(got, want)):
+            assert_same(g_, w_, ("caller workspace", i))
+        # too small for the conv backward: refused on the host, nothing written
+        conv_need = nnh.workspace_size("conv2d_backward", 8, 32, 14, 14, 64, 3, 3, 1, 1, 1, 1, 1, 1)
+        small = torch.empty((conv_need - 256) // 4, device="cuda")
+        nnh.set_workspace(small, stream=s)
+        x, w, alive, g = conv
+        dx, dw, db = torch.full_like(x, 3.0), torch.full_like(w, 3.0), torch.full((64,), 3.0, device="cuda")
+        with pytest.raises(nnh.NnhError) as err:
+            nnh.conv2d_backward(g, x, w, alive, 1, 1, dx, True, dw, True, db, True, stream=s)
+        assert err.value.code == nnh.ERR_WORKSPACE
+        s.synchronize()
+        assert bool((dx == 3.0).all()) and bool((dw == 3.0).all()) and bool((db == 3.0).all())
+    finally:
+        nnh.set_workspace(None, stream=s)
+    got = run_all()
+    for i, (g_, w_) in enumerate(zip(got, want)):
+        assert_same(g_, w_, ("library workspace again", i))
