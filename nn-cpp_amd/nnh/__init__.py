@@ -59,6 +59,8 @@ def _declare(L):
     for name, args in _EXTRA_DECLS.items():
         if hasattr(L, name):
             getattr(L, name).argtypes = args
+    if hasattr(L, "nnh_sgemm_noalloc_max_workspace"):
+        L.nnh_sgemm_noalloc_max_workspace.restype = _sz
 
 
 _EXTRA_DECLS = {
@@ -85,6 +87,7 @@ _EXTRA_DECLS = {
                                            C.c_int, C.c_int, _szp],
     "nnh_attention_forward_workspace_size": [_sz, _sz, _sz, _sz, _sz, _szp],
     "nnh_attention_backward_workspace_size": [_sz, _sz, _sz, _sz, _sz, _szp],
+    "nnh_sgemm_noalloc": [C.c_int, C.c_int, _sz, _sz, _sz, _vp, _sz, _vp, _sz, _vp, _sz, C.c_int, _vp],
     "nnh_im2col": [_vp, _sz, _sz, _sz, _sz, _sz, _sz, C.c_int, C.c_int, _vp, _vp],
     "nnh_col2im_add": [_vp, _sz, _sz, _sz, _sz, _sz, _sz, C.c_int, C.c_int, _vp, C.c_int, _vp],
 }
