@@ -1,24 +1,28 @@
 #!/usr/bin/env python3
-"""Benchmark of the fp32 GEMM hot path on one MI355X.
+"""Benchmark of nn-cpp's fp32 GEMM hot path on one MI355X.
 
-Default workload (BASELINE.json metric "fp32 GEMM TFLOP/s @4096^3"): nn::kernels::sgemm's replacement,
-C = A B with A, B 4096 x 4096 fp32 from the reference's own seeded uniform[-1, 1] stream (seed 4, A filled
-first, then B: apps/bench/runner.cpp:80-86). One step = one 4096^3 product; inputs are resident in HBM
-before timing starts. Prints one JSON line on stdout (diagnostics go to stderr).
+The JSON line's headline (BASELINE.json metric "fp32 GEMM TFLOP/s @4096^3"): nn::kernels::sgemm's replacement,
+C = A B with A, B 4096 x 4096 fp32 from the reference's own seeded uniform[-1, 1] stream (seed 4, A filled first,
+then B: apps/bench/runner.cpp:80-86). One step = one 4096^3 product; inputs are resident in HBM before timing
+starts. Before the W warm-up steps the clock is settled with launches for at least SETTLE_S seconds (it ramps
+over the first ~20 launches), reported as settle_launches.
 
-  python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+`configs` holds every BASELINE.json configuration (cfg 1-5) as rows: the op's median device time over BATCHES
+batches of back-to-back calls (stats.hpp:24-58's median and IQR/median spread), TFLOP/s or GB/s, its roofline
+fraction, whether three GPU runs and nn-cpp's own CPU output agree bit for bit, and nn-cpp's CPU time for the same
+op on the same host buffers (the reference's NN_NATIVE AVX2 build, oracle/_ref, timed in C++ as runner.cpp does:
+nn::matmul for configs 1 and 5, linear + relu for 2, conv2d_relu for 3, attention for 4; backward rows time the
+op's own backward rule), on one thread per physical core of the cores this process may use, pinned, and on one
+thread. Prints one JSON line on stdout (diagnostics go to stderr).
 
-roofline.achieved = 2 M N K / (average kernel duration from HIP events recorded on the launch stream);
-roofline.traffic comes from the committed rocprofv3 PMC summary (profiles/sgemm_4096_pmc.md) when present.
-fused_op = the metric's "fused-op GB/s": conv2d_relu forward of config 3's memory-bound first layer.
-cpu_baseline = nn-cpp's NN_NATIVE AVX2 sgemm (oracle/_ref, compiled from the reference's own sources) on the
-same inputs, on the host's cores (at most 16 threads), median of a bounded number of runs.
+  python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--no-configs] [--csv PATH]
+  python bench.py --report      # the same rows as a markdown table, with fp64 error bounds
+  python bench.py --floor       # launch-cost floor of this GPU
 """
 import argparse
 import json
 import os
 import re
-import statistics
 import sys
 import time
 
@@ -27,6 +31,8 @@ sys.path.insert(0, os.path.join(ROOT, "nn-cpp_amd"))
 
 PEAK_FP32_MFMA_TFLOPS = 157.3   # MI355X dense fp32 matrix peak (AMD spec)
 PEAK_HBM_GBPS = 8000.0          # MI355X HBM3E
+SETTLE_S = 0.5                  # clock settling before the headline's warm-up
+BATCHES = 7                     # timed batches per config row (median and spread over them)
 
 
 def log(*a):
@@ -42,6 +48,30 @@ def traffic_from_profile(name):
     return float(m.group(1)) if m else None
 
 
+# ---------------------------------------------------------------------------------------------------------------
+# statistics: apps/bench/stats.hpp (linear-interpolated quantiles)
+
+def quantile_sorted(s, q):
+    pos = q * (len(s) - 1)
+    lo = int(pos)
+    hi = min(lo + 1, len(s) - 1)
+    return s[lo] + (pos - lo) * (s[hi] - s[lo])
+
+
+def median(v):
+    return quantile_sorted(sorted(v), 0.5)
+
+
+def spread(v):
+    if len(v) < 2:
+        return 0.0
+    s = sorted(v)
+    return (quantile_sorted(s, 0.75) - quantile_sorted(s, 0.25)) / quantile_sorted(s, 0.5)
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# the host CPU (for the baseline): model, governor, one logical CPU per physical core
+
 def cpu_model():
     try:
         for line in open("/proc/cpuinfo"):
@@ -52,103 +82,29 @@ def cpu_model():
     return "unknown CPU"
 
 
-def cpu_baseline(a, b, m, n, k, budget_s=15.0, max_runs=400):
-    """nn-cpp's own sgemm (oracle/_ref) on the same host buffers, reference method: warm-up, then the median of
-    timed runs (apps/bench/runner.cpp:80-96), bounded to about budget_s seconds of CPU work."""
-    sys.path.insert(0, os.path.join(ROOT, "oracle"))
-    import numpy as np
-    from pyoracle import Reference, reference_available
-    if not reference_available():
-        log("cpu_baseline: oracle/_ref not built; skipped")
-        return None
-    ref = Reference()
+def cpu_governor():
     try:
-        avail = len(os.sched_getaffinity(0))
-    except AttributeError:
-        avail = os.cpu_count() or 1
-    threads = max(1, min(16, avail))
-    ref.set_threads(threads)
-    c = np.empty((m, n), np.float32)
-    ref.sgemm_inplace(0, 0, m, n, k, a, k, b, n, c, n, 0)  # warm-up (pool start, page faults)
-    times = []
-    t_start = time.perf_counter()
-    while len(times) < max_runs and (time.perf_counter() - t_start) < budget_s:
-        t0 = time.perf_counter()
-        ref.sgemm_inplace(0, 0, m, n, k, a, k, b, n, c, n, 0)
-        times.append(time.perf_counter() - t0)
-    med = statistics.median(times)
-    return {
-        "value": round(2.0 * m * n * k / med / 1e12, 4),
-        "unit": "TFLOP/s",
-        "cores": threads,
-        "kind": "reference",
-        "sample": (f"nn::kernels::sgemm {m}x{n}x{k} NN (nn-cpp 2.0.0 NN_NATIVE AVX2/FMA build, -O3 -mavx2 -mfma "
-                   f"-ffp-contract=off), same seed-4 inputs, {threads} threads on {cpu_model()}, median of "
-                   f"{len(times)} runs after 1 warm-up ({sum(times):.1f} s timed)"),
-    }
+        return open("/sys/devices/system/cpu/cpu0/cpufreq/scaling_governor").read().strip()
+    except OSError:
+        return "unknown"
 
 
-def floor():
-    """What a single launch costs on this GPU, beside the conv1 figure: an empty one-wave kernel (nnh.bench_delay
-    with no delay), torch fills of conv1's output size (12.85 MB) and of eight times it, and copies of the same
-    sizes, each timed as device_time_ms does. Prints a markdown table."""
-    import torch
-
-    import nnh
-    dev = torch.device("cuda:0")
-    ny = 128 * 32 * 784
-    small, big = torch.empty(ny, device=dev), torch.empty(8 * ny, device=dev)
-    src_small, src_big = torch.ones(ny // 2, device=dev), torch.ones(4 * ny, device=dev)
-    rows = [("empty one-wave kernel (bench_delay 0)", lambda: nnh.bench_delay(0.0), 0),
-            ("fill 12.85 MB (conv1's y)", lambda: small.fill_(1.0), 4 * ny),
-            ("copy 6.4 MB -> 6.4 MB", lambda: small[: ny // 2].copy_(src_small), 4 * ny),
-            ("fill 102.8 MB", lambda: big.fill_(1.0), 32 * ny),
-            ("copy 51.4 MB -> 51.4 MB", lambda: big[: 4 * ny].copy_(src_big), 32 * ny)]
-    print("| launch | us | GB/s | % of 8 TB/s |\n|---|---|---|---|")
-    for name, fn, nbytes in rows:
-        ms = device_time_ms(fn, reps=200)
-        gbps = nbytes / (ms * 1e-3) / 1e9 if nbytes else 0.0
-        print(f"| {name} | {ms * 1e3:.2f} | {gbps:.0f} | {gbps / PEAK_HBM_GBPS * 100:.1f}% |", flush=True)
-
-
-def fused_op_conv1():
-    """The metric's fused-op figure: nn::conv2d_relu forward of BASELINE config 3's first layer (x [128,1,28,28]
-    U[0,1] seed 2, W [32,1,3,3] Kaiming-normal, zero bias, stride 1, pad 1), the memory-bound direct kernel
-    with its bias/ReLU/alive epilogue. Algorithmic bytes: x + W + b read once, y written once (the alive flags
-    are extra traffic, not counted). Device time from device_time_ms."""
-    import numpy as np
-    import torch
-
-    import nnh
-    from nnh import synth
-    dev = torch.device("cuda:0")
-    xc = synth.mt19937_uniform(2, 128 * 28 * 28, 0.0, 1.0).reshape(128, 1, 28, 28)
-    w1 = (synth.normal(21, (32, 1, 3, 3)) * np.float32(np.sqrt(2.0 / 9))).astype(np.float32)
-    dx, dw, db = (torch.from_numpy(np.ascontiguousarray(t)).to(dev) for t in (xc, w1, np.zeros(32, np.float32)))
-    y = torch.empty((128, 32, 28, 28), device=dev)
-    alive = torch.empty((128, 32, 28, 28), dtype=torch.uint8, device=dev)
-    lib, stream = nnh.lib(), torch.cuda.current_stream()
-
-    def step(al):
-        nnh.check(lib.nnh_conv2d_forward(nnh._ptr(dx), 128, 1, 28, 28, nnh._ptr(dw), 32, 3, 3, nnh._ptr(db), 1, 1, 1,
-                                         nnh._ptr(y), nnh._ptr(al), nnh._stream(stream)))
-
-    nbytes = 4 * (xc.size + w1.size + 32 + y.numel())
-    ms = device_time_ms(lambda: step(alive), reps=200)
-    ms_no_alive = device_time_ms(lambda: step(None), reps=200)
-    gbps = nbytes / (ms * 1e-3) / 1e9
-    log(f"conv1 conv2d_relu: {ms * 1e3:.2f} us with alive flags ({gbps:.0f} GB/s), "
-        f"{ms_no_alive * 1e3:.2f} us without")
-    return {"workload": "conv2d_relu forward, BASELINE config 3 conv1: x [128,1,28,28] -> y [128,32,28,28], 3x3 s1 p1, "
-                        "with alive flags", "value": round(gbps, 1), "unit": "GB/s", "us_per_launch": round(ms * 1e3, 3),
-            "algorithmic_bytes": nbytes, "roofline": {"bound": "hbm", "peak": PEAK_HBM_GBPS, "unit": "GB/s",
-                                                      "frac": round(gbps / PEAK_HBM_GBPS, 4)},
-            "without_alive_flags": {"us_per_launch": round(ms_no_alive * 1e3, 3),
-                                    "value": round(nbytes / (ms_no_alive * 1e-3) / 1e9, 1)}}
+def physical_cores():
+    """One logical CPU per physical core among the CPUs this process may run on, and the allowed CPU count."""
+    allowed = sorted(os.sched_getaffinity(0))
+    first = {}
+    for c in allowed:
+        base = f"/sys/devices/system/cpu/cpu{c}/topology/"
+        try:
+            key = (int(open(base + "physical_package_id").read()), int(open(base + "core_id").read()))
+        except (OSError, ValueError):
+            key = (0, c)
+        first.setdefault(key, c)
+    return sorted(first.values()), len(allowed)
 
 
 # ---------------------------------------------------------------------------------------------------------------
-# --report: every BASELINE.json config, absolute throughput and roofline fraction, nn-cpp's CPU path beside it
+# device timing
 
 def device_time_ms(fn, reps=50, warmup_s=0.05, stream=None):
     """Average device time of one fn() (one or more launches on torch's current stream), without the
@@ -192,48 +148,19 @@ def device_time_ms(fn, reps=50, warmup_s=0.05, stream=None):
     return e0.elapsed_time(e1) / reps
 
 
-def _cpu_time_ms(fn, budget_s=3.0, max_runs=15):
-    """nn-cpp's method (apps/bench/runner.cpp:80-96): a warm-up, then the median of timed runs (bounded)."""
-    fn()
-    times, t_start = [], time.perf_counter()
-    while len(times) < max_runs and (time.perf_counter() - t_start) < budget_s:
-        t0 = time.perf_counter()
-        fn()
-        times.append((time.perf_counter() - t0) * 1e3)
-    return statistics.median(times)
+def device_times(fn, est_ms):
+    """BATCHES device-time measurements of fn (each an average over back-to-back calls); the first also warms up."""
+    reps = int(max(4, min(100, 20.0 / max(est_ms, 1e-3))))
+    out = [device_time_ms(fn, reps=reps, warmup_s=0.1)]
+    for _ in range(BATCHES - 1):
+        out.append(device_time_ms(fn, reps=reps, warmup_s=0.0))
+    return out
 
+
+# ---------------------------------------------------------------------------------------------------------------
+# fp64 checks (--report)
 
 U32 = 2.0 ** -24  # unit roundoff of fp32
-
-
-def _host(t):
-    return t.detach().cpu().numpy()
-
-
-def _repeat_runs(run, times=3):
-    """Runs the op `times` times (run() returns its output tensors); whether every run left the same bits, and the
-    outputs of the first run on the host."""
-    import numpy as np
-    import torch
-    first, same = None, True
-    for _ in range(times):
-        outs = run()
-        torch.cuda.synchronize()
-        cur = [np.array(_host(t), copy=True) for t in outs]
-        if first is None:
-            first = cur
-        else:
-            same = same and all(np.array_equal(a.view(np.uint32), b.view(np.uint32)) for a, b in zip(first, cur))
-    return same, first
-
-
-def _vs_cpu(got, want):
-    """Largest |GPU - nn-cpp| over the outputs, and whether every bit agrees."""
-    import numpy as np
-    bitwise = all(np.array_equal(g.view(np.uint32), w.view(np.uint32)) for g, w in zip(got, want))
-    diff = max(float(np.max(np.abs(g.astype(np.float64) - w.astype(np.float64)))) if g.size else 0.0
-               for g, w in zip(got, want))
-    return diff, bitwise
 
 
 def _vs_f64(got, want, mag=None, terms=None):
@@ -247,6 +174,10 @@ def _vs_f64(got, want, mag=None, terms=None):
     bound = 4.0 * terms * U32 * mag
     ratio = np.where(bound > 0, err / np.where(bound > 0, bound, 1.0), np.where(err > 0, np.inf, 0.0))
     return worst, float(ratio.max()) if ratio.size else 0.0
+
+
+def _worst(pairs):
+    return (max(p[0] for p in pairs), None if any(p[1] is None for p in pairs) else max(p[1] for p in pairs))
 
 
 def _conv_f64(x, w, b, pad):
@@ -269,10 +200,24 @@ def _conv_f64(x, w, b, pad):
     return y, mag
 
 
-def _heads(t, heads):
+def _conv_bwd_f64(gm, x, w):
+    """fp64 gradients of a stride-1, padding-1 3x3 convolution for the masked output gradient gm: dx (Cout kh kw
+    terms), dW (N Ho Wo terms), db, each with its magnitude sum."""
     import numpy as np
-    N, T, D = t.shape
-    return t.astype(np.float64).reshape(N, T, heads, D // heads).transpose(0, 2, 1, 3)
+    _, _, H, W = x.shape
+    xp = np.pad(x.astype(np.float64), ((0, 0), (0, 0), (1, 1), (1, 1)))
+    dx64, dxmag = np.zeros(xp.shape), np.zeros(xp.shape)
+    dw64, dwmag = np.zeros(w.shape), np.zeros(w.shape)
+    for i in range(3):
+        for j in range(3):
+            win = xp[:, :, i:i + H, j:j + W]
+            w64 = w[:, :, i, j].astype(np.float64)
+            dw64[:, :, i, j] = np.einsum("nohw,nchw->oc", gm, win, optimize=True)
+            dwmag[:, :, i, j] = np.einsum("nohw,nchw->oc", np.abs(gm), np.abs(win), optimize=True)
+            dx64[:, :, i:i + H, j:j + W] += np.einsum("nohw,oc->nchw", gm, w64, optimize=True)
+            dxmag[:, :, i:i + H, j:j + W] += np.einsum("nohw,oc->nchw", np.abs(gm), np.abs(w64), optimize=True)
+    return ((dx64[:, :, 1:H + 1, 1:W + 1], dxmag[:, :, 1:H + 1, 1:W + 1]), (dw64, dwmag),
+            (gm.sum((0, 2, 3)), np.abs(gm).sum((0, 2, 3))))
 
 
 def _attention_f64(q, k, v, g, heads, causal):
@@ -280,273 +225,478 @@ def _attention_f64(q, k, v, g, heads, causal):
     import numpy as np
     N, T, D = q.shape
     scale = 1.0 / np.sqrt(D // heads)
-    qh, kh, vh, gh = (_heads(t, heads) for t in (q, k, v, g))
+    hd = lambda t: t.astype(np.float64).reshape(N, T, heads, D // heads).transpose(0, 2, 1, 3)
+    qh, kh, vh, gh = hd(q), hd(k), hd(v), hd(g)
     s = (qh @ kh.transpose(0, 1, 3, 2)) * scale
     if causal:
-        s = np.where(np.triu(np.ones((T, k.shape[1]), bool), 1), -np.inf, s)
+        s = np.where(np.triu(np.ones((T, T), bool), 1), -np.inf, s)
     p = np.exp(s - s.max(-1, keepdims=True))
     p /= p.sum(-1, keepdims=True)
     merge = lambda t: t.transpose(0, 2, 1, 3).reshape(N, -1, D)
-    out = merge(p @ vh)
     dp = gh @ vh.transpose(0, 1, 3, 2)
     ds = p * (dp - (dp * p).sum(-1, keepdims=True)) * scale
-    return out, (merge(ds @ kh), merge(ds.transpose(0, 1, 3, 2) @ qh), merge(p.transpose(0, 1, 3, 2) @ gh))
+    return merge(p @ vh), (merge(ds @ kh), merge(ds.transpose(0, 1, 3, 2) @ qh), merge(p.transpose(0, 1, 3, 2) @ gh))
 
 
-def report(with_cpu=True):
-    """Every BASELINE.json config on the GPU: time, TFLOP/s or GB/s, roofline fraction, nn-cpp's CPU time, and three
-    checks of the outputs: bit equality over 3 repeated GPU runs, the largest difference from nn-cpp's CPU output
-    on the same inputs (0 = bit for bit), and the largest error against fp64, also as a fraction of the bound
-    4 K 2^-24 (|A||B|)_ij where the op is one product per output (K terms, any order)."""
+# ---------------------------------------------------------------------------------------------------------------
+# the BASELINE.json configurations as rows
+
+class Row:
+    """One measured op. gpu() launches it once on device-resident inputs (writing fixed outputs); outs() returns
+    those output tensors; cpu(ref, warmup, runs, budget) times nn-cpp's own op on the same host buffers and returns
+    (times_ms, outputs); f64(host_outs) gives (max abs error vs fp64, fraction of the error bound)."""
+
+    def __init__(self, cfg, key, workload, gpu, outs, flops, nbytes=None, bound="mfma", cpu=None, f64=None,
+                 est_ms=0.05, useful_flops=None):
+        self.cfg, self.key, self.workload = cfg, key, workload
+        self.gpu, self.outs, self.cpu, self.f64 = gpu, outs, cpu, f64
+        self.flops, self.nbytes, self.bound, self.est_ms, self.useful_flops = flops, nbytes, bound, est_ms, useful_flops
+        self.result = {}
+
+
+def build_rows(report=False):
+    """Inputs of every BASELINE.json configuration (the reference's seeded streams), resident on the GPU, and one
+    Row per measured op."""
+    import ctypes as C
+
     import numpy as np
     import torch
 
     import nnh
     from nnh import synth
-    sys.path.insert(0, os.path.join(ROOT, "oracle"))
-    from pyoracle import Reference, reference_available
-    ref = Reference() if (with_cpu and reference_available()) else None
-    threads = max(1, min(16, len(os.sched_getaffinity(0))))
-    if ref:
-        ref.set_threads(threads)
+    L = nnh.lib()
     dev = torch.device("cuda:0")
     d = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+    st = lambda: nnh._stream(None)
+    P = nnh._ptr
     rows = []
 
-    def row(cfg, what, ms, flops=None, nbytes=None, bound="mfma", cpu_ms=None, repeat=None, cpu_diff=None,
-            f64=None):
-        tflops = flops / (ms * 1e-3) / 1e12 if flops else None
-        gbps = nbytes / (ms * 1e-3) / 1e9 if nbytes else None
-        frac = (tflops / PEAK_FP32_MFMA_TFLOPS) if bound == "mfma" else (gbps / PEAK_HBM_GBPS)
-        rows.append({"config": cfg, "what": what, "ms": ms, "tflops": tflops, "gbps": gbps, "bound": bound,
-                     "roofline_frac": frac, "cpu_ms": cpu_ms, "speedup_vs_cpu": (cpu_ms / ms) if cpu_ms else None,
-                     "repeat": repeat, "cpu_diff": cpu_diff, "f64": f64})
-        log(f"[{cfg}] {what}: {ms:.4f} ms" + (f", {tflops:.2f} TFLOP/s" if tflops else "") +
-            (f", {gbps:.1f} GB/s" if gbps else "") + f", {frac * 100:.1f}% of {bound} peak" +
-            (f"; nn-cpp CPU {cpu_ms:.3f} ms" if cpu_ms else "") +
-            (f"; repeats bitwise {repeat}" if repeat is not None else "") +
-            (f"; vs nn-cpp {cpu_diff[0]:.3g} (bitwise {cpu_diff[1]})" if cpu_diff else "") +
-            (f"; vs fp64 {f64[0]:.3g}" + (f" = {f64[1]:.3g} of the bound" if f64[1] is not None else "")
-             if f64 else ""))
+    def shape_arr(s):
+        return (C.c_size_t * len(s))(*s)
 
-    def worst(pairs):
-        """Combines (abs error, fraction of bound) pairs over several outputs."""
-        return (max(p[0] for p in pairs),
-                None if any(p[1] is None for p in pairs) else max(p[1] for p in pairs))
+    def matmul_row(cfg, key, what, seed, m, n, k, ta, tb, est_ms):
+        a, b = synth.uniform_operands(seed, [(k, m) if ta else (m, k), (n, k) if tb else (k, n)])
+        da, db = d(a), d(b)
+        dc = torch.empty((m, n), device=dev)
+        ash, bsh = shape_arr(a.shape), shape_arr(b.shape)
 
-    def gemm_f64(got, a, b, rows_of=None):
-        """fp64 A B (on a sample of rows for large m) against the GPU's C."""
-        a64, b64 = a.astype(np.float64), b.astype(np.float64)
-        if rows_of is not None:
-            a64, got = a64[rows_of], got[rows_of]
-        return _vs_f64(got, a64 @ b64, np.abs(a64) @ np.abs(b64), a.shape[1])
+        def gpu():
+            nnh.check(L.nnh_matmul(P(da), ash, 2, P(db), bsh, 2, ta, tb, P(dc), st()))
 
-    # config 1: 512^3, NN / TN / NT, seed 0
-    n = 512
-    a, b = synth.uniform_operands(0, [(n, n), (n, n)])
-    da, db, dc = d(a), d(b), torch.empty((n, n), device=dev)
-    c = np.empty((n, n), np.float32)
-    for ta, tb, name in ((0, 0, "C=A B"), (1, 0, "C=A^T B"), (0, 1, "C=A B^T")):
-        run = lambda: nnh.sgemm(ta, tb, n, n, n, da, n, db, n, dc, n)
-        ms = device_time_ms(run)
-        cpu = _cpu_time_ms(lambda: ref.sgemm_inplace(ta, tb, n, n, n, a, n, b, n, c, n, 0)) if ref else None
-        same, (got,) = _repeat_runs(lambda: (run(), dc)[1:])
-        row(1, f"sgemm 512^3 {name}", ms, flops=2.0 * n ** 3, cpu_ms=cpu, repeat=same,
-            cpu_diff=_vs_cpu([got], [c]) if ref else None,
-            f64=gemm_f64(got, a.T if ta else a, b.T if tb else b))
+        def f64(h):
+            a64 = (a.T if ta else a).astype(np.float64)
+            b64 = (b.T if tb else b).astype(np.float64)
+            rows_of = np.linspace(0, m - 1, 256).astype(np.int64) if m >= 2048 else slice(None)
+            return _vs_f64(h[0][rows_of], a64[rows_of] @ b64, np.abs(a64[rows_of]) @ np.abs(b64), k)
 
-    # config 2: MLP 256 x 784 -> 512 -> 256 -> 10, forward (linear + ReLU) and backward (dX, dW, db)
+        rows.append(Row(cfg, key, what, gpu, lambda: [dc], 2.0 * m * n * k,
+                        cpu=lambda ref, w, r, bud: (lambda t, o: (t, [o]))(*ref.time_matmul(a, b, ta, tb, w, r, bud)),
+                        f64=f64, est_ms=est_ms))
+
+    # config 1: 512^3 through nn::matmul, C = A B, A^T B, A B^T (seed 0)
+    for ta, tb, name in ((0, 0, "A B"), (1, 0, "A^T B"), (0, 1, "A B^T")):
+        matmul_row(1, f"matmul512_{'t' if ta else 'n'}{'t' if tb else 'n'}", f"nn::matmul 512^3 C = {name}", 0,
+                   512, 512, 512, ta, tb, 0.01)
+
+    # config 2: MLP 256 x 784 -> 512 -> 256 -> 10, linear + ReLU per layer; backward dX, dW, db per layer (seed 1)
     dims = [784, 512, 256, 10]
-    x = synth.mt19937_uniform(1, 256 * 784, 0.0, 1.0).reshape(256, 784)
+    M = 256
+    x = synth.mt19937_uniform(1, M * 784, 0.0, 1.0).reshape(M, 784)
     ws = [synth.mt19937_uniform(100 + i, dims[i + 1] * dims[i], -1 / np.sqrt(dims[i]), 1 / np.sqrt(dims[i]))
           .reshape(dims[i + 1], dims[i]) for i in range(3)]
     bs = [np.zeros(dims[i + 1], np.float32) for i in range(3)]
-    gys = [synth.normal(200 + i, (256, dims[i + 1])) for i in range(3)]
-    dws, dbs, dgs = [d(w) for w in ws], [d(bb) for bb in bs], [d(g) for g in gys]
-    acts = [d(x)]
-    for i in range(3):
-        acts.append(nnh.linear_forward(acts[-1], dws[i], dbs[i], relu=True))
-    grads = [(torch.empty((256, dims[i]), device=dev), torch.empty(ws[i].shape, device=dev),
+    gys = [synth.normal(200 + i, (M, dims[i + 1])) for i in range(3)]
+    dws, dbs, dgs = [d(w) for w in ws], [d(b) for b in bs], [d(g) for g in gys]
+    acts = [d(x)] + [torch.empty((M, dims[i + 1]), device=dev) for i in range(3)]
+    grads = [(torch.empty((M, dims[i]), device=dev), torch.empty(ws[i].shape, device=dev),
               torch.empty(dims[i + 1], device=dev)) for i in range(3)]
+    lead = shape_arr([M])
 
     def mlp_fwd():
-        h, hs = acts[0], []
         for i in range(3):
-            h = nnh.linear_forward(h, dws[i], dbs[i], relu=True)
-            hs.append(h)
-        return hs
+            nnh.check(L.nnh_linear_forward(P(acts[i]), M, dims[i], P(dws[i]), dims[i + 1], P(dbs[i]), 1, P(acts[i + 1]),
+                                           st()))
+
+    mlp_fwd()
+    hacts = [x] + [acts[i + 1].cpu().numpy() for i in range(3)]
 
     def mlp_bwd():
         for i in range(3):
-            nnh.linear_backward(dgs[i], acts[i], dws[i], *[v for pair in zip(grads[i], (True,) * 3) for v in pair])
-        return [t for gr in grads for t in gr]
+            nnh.check(L.nnh_linear_backward(P(dgs[i]), P(acts[i]), P(dws[i]), lead, 1, dims[i], dims[i + 1],
+                                            P(grads[i][0]), 1, P(grads[i][1]), 1, P(grads[i][2]), 1, st()))
 
-    fwd_flops = sum(2.0 * 256 * dims[i] * dims[i + 1] for i in range(3))
-    cpu, hacts = None, [x]
-    if ref:
+    def mlp_fwd_f64(h):
+        ins = [x] + h[:2]
+        return _worst([_vs_f64(h[i], np.maximum(ins[i].astype(np.float64) @ ws[i].T.astype(np.float64) + bs[i], 0),
+                               np.abs(ins[i].astype(np.float64)) @ np.abs(ws[i].T.astype(np.float64)) + np.abs(bs[i]),
+                               dims[i] + 1) for i in range(3)])
+
+    def mlp_bwd_f64(h):
+        pairs = []
         for i in range(3):
-            hacts.append(np.maximum(ref.linear_forward(hacts[-1], ws[i], bs[i]), np.float32(0)))
+            g64, x64, w64 = gys[i].astype(np.float64), hacts[i].astype(np.float64), ws[i].astype(np.float64)
+            pairs += [_vs_f64(h[3 * i], g64 @ w64, np.abs(g64) @ np.abs(w64), dims[i + 1]),
+                      _vs_f64(h[3 * i + 1], g64.T @ x64, np.abs(g64.T) @ np.abs(x64), M),
+                      _vs_f64(h[3 * i + 2], g64.sum(0), np.abs(g64).sum(0), M)]
+        return _worst(pairs)
 
-        def cpu_fwd():
-            h = x
-            for i in range(3):
-                h = np.maximum(ref.linear_forward(h, ws[i], bs[i]), np.float32(0))
-        cpu = _cpu_time_ms(cpu_fwd)
-    ms = device_time_ms(mlp_fwd)
-    same, hs = _repeat_runs(mlp_fwd)
-    # each layer against fp64 from the GPU's own input to it (ReLU is 1-Lipschitz; the bias is one more term)
-    ins = [x] + hs[:2]
-    f64 = worst([_vs_f64(hs[i], np.maximum(ins[i].astype(np.float64) @ ws[i].T.astype(np.float64) + bs[i], 0),
-                         np.abs(ins[i].astype(np.float64)) @ np.abs(ws[i].T.astype(np.float64)) + np.abs(bs[i]),
-                         dims[i] + 1) for i in range(3)])
-    row(2, "MLP forward (3 x linear+ReLU)", ms, flops=fwd_flops, cpu_ms=cpu, repeat=same,
-        cpu_diff=_vs_cpu(hs, hacts[1:]) if ref else None, f64=f64)
-    cpu, want = None, None
-    if ref:
-        want = [t for i in range(3) for t in ref.linear_backward(hacts[i], ws[i], bs[i], gys[i])]
-        cpu = _cpu_time_ms(lambda: [ref.linear_backward(hacts[i], ws[i], bs[i], gys[i]) for i in range(3)])
-    ms = device_time_ms(mlp_bwd)
-    same, got = _repeat_runs(mlp_bwd)
-    pairs = []
-    for i in range(3):
-        g64, x64, w64 = gys[i].astype(np.float64), _host(acts[i]).astype(np.float64), ws[i].astype(np.float64)
-        pairs += [_vs_f64(got[3 * i], g64 @ w64, np.abs(g64) @ np.abs(w64), dims[i + 1]),
-                  _vs_f64(got[3 * i + 1], g64.T @ x64, np.abs(g64.T) @ np.abs(x64), 256),
-                  _vs_f64(got[3 * i + 2], g64.sum(0), np.abs(g64).sum(0), 256)]
-    row(2, "MLP backward (dX, dW, db per layer)", ms, flops=2 * fwd_flops, cpu_ms=cpu, repeat=same,
-        cpu_diff=_vs_cpu(got, want) if ref else None, f64=worst(pairs))
+    fwd_flops = sum(2.0 * M * dims[i] * dims[i + 1] for i in range(3))
+    rows.append(Row(2, "mlp_forward", "MLP forward: 3 x nn::linear + ReLU, 256 x 784 -> 512 -> 256 -> 10", mlp_fwd,
+                    lambda: acts[1:], fwd_flops,
+                    cpu=lambda ref, w, r, bud: ref.time_linear_relu_chain(x, ws, bs, w, r, bud), f64=mlp_fwd_f64,
+                    est_ms=0.03))
+    rows.append(Row(2, "mlp_backward", "MLP backward: nn::linear's dX, dW, db for each of the 3 layers", mlp_bwd,
+                    lambda: [t for gr in grads for t in gr], 2 * fwd_flops,
+                    cpu=lambda ref, w, r, bud: ref.time_linear_backward_layers(hacts[:3], ws, bs, gys, w, r, bud),
+                    f64=mlp_bwd_f64, est_ms=0.035))
 
-    # config 3: conv2d_relu, batch 128: conv1 1->32 on 28x28 (memory-bound), conv2 32->64 on 14x14
-    xc = synth.mt19937_uniform(2, 128 * 28 * 28, 0.0, 1.0).reshape(128, 1, 28, 28)
+    # config 3: conv2d_relu, batch 128: conv1 1 -> 32 on 28 x 28 (memory-bound), conv2 32 -> 64 on 14 x 14 after a
+    # 2 x 2 max pool (seed 2)
+    N = 128
+    xc = synth.mt19937_uniform(2, N * 28 * 28, 0.0, 1.0).reshape(N, 1, 28, 28)
     w1 = (synth.normal(21, (32, 1, 3, 3)) * np.float32(np.sqrt(2.0 / 9))).astype(np.float32)
     w2 = (synth.normal(22, (64, 32, 3, 3)) * np.float32(np.sqrt(2.0 / 288))).astype(np.float32)
     b1, b2 = np.zeros(32, np.float32), np.zeros(64, np.float32)
     dxc, dw1, dw2, db1, db2 = d(xc), d(w1), d(w2), d(b1), d(b2)
-    y1, al1 = nnh.conv2d_forward(dxc, dw1, db1, 1, 1, True)
-    x2 = torch.nn.functional.max_pool2d(y1, 2).contiguous()
+    y1, al1 = torch.empty((N, 32, 28, 28), device=dev), torch.empty((N, 32, 28, 28), dtype=torch.uint8, device=dev)
+
+    def conv_fwd(x_, w_, b_, y_, al_, dims_):
+        n_, cin, h, w__ = dims_
+        return lambda: nnh.check(L.nnh_conv2d_forward(P(x_), n_, cin, h, w__, P(w_), w_.shape[0], 3, 3, P(b_), 1, 1, 1,
+                                                      P(y_), P(al_) if al_ is not None else None, st()))
+
+    conv1 = conv_fwd(dxc, dw1, db1, y1, al1, (N, 1, 28, 28))
+    conv1()
+    x2 = torch.empty((N, 32, 14, 14), device=dev)
+    arg1 = torch.empty((N, 32, 14, 14), dtype=torch.int32, device=dev)
+
+    def pool1():
+        nnh.check(L.nnh_maxpool2d_forward(P(y1), N, 32, 28, 28, 2, 2, P(x2), C.c_void_p(arg1.data_ptr()), st()))
+
+    pool1()
     hx2 = x2.cpu().numpy()
-
-    def conv_checks(run, x_, w_, b_, terms):
-        same, (got,) = _repeat_runs(run)
-        y64, mag = _conv_f64(x_, w_, b_, 1)
-        cmp = _vs_cpu([got], [ref.conv2d_forward(x_, w_, b_, 1, 1, 1)]) if ref else None
-        return dict(repeat=same, cpu_diff=cmp, f64=_vs_f64(got, np.maximum(y64, 0), mag, terms))
-
-    conv1_bytes = 4 * (xc.size + w1.size + b1.size + 128 * 32 * 784)
-    cpu = _cpu_time_ms(lambda: ref.conv2d_forward(xc, w1, b1, 1, 1, 1)) if ref else None
-    run = lambda: nnh.conv2d_forward(dxc, dw1, db1, 1, 1, True)
-    row(3, "conv1 conv2d_relu fwd (1->32, 28x28, b128)", device_time_ms(run),
-        flops=2.0 * 128 * 32 * 784 * 9, nbytes=conv1_bytes, bound="hbm", cpu_ms=cpu,
-        **conv_checks(lambda: run()[:1], xc, w1, b1, 10))
-    run = lambda: nnh.conv2d_forward(dxc, dw1, db1, 1, 1, True, want_alive=False)
-    row(3, "conv1 conv2d_relu fwd, no alive flags (backward masks with y > 0)", device_time_ms(run),
-        flops=2.0 * 128 * 32 * 784 * 9, nbytes=conv1_bytes, bound="hbm",
-        **conv_checks(lambda: run()[:1], xc, w1, b1, 10))
-    # not a BASELINE config: the same layer at batch 2048 shows the kernel's streaming rate once launch and
-    # drain latency (about 4 us for any 13 MB launch on this GPU) no longer dominate
-    xbig = dxc.repeat(16, 1, 1, 1)
-    row("3*", "conv1 conv2d_relu fwd at batch 2048 (steady state)",
-        device_time_ms(lambda: nnh.conv2d_forward(xbig, dw1, db1, 1, 1, True), reps=20),
-        flops=16 * 2.0 * 128 * 32 * 784 * 9, nbytes=16 * (conv1_bytes - 4 * (w1.size + b1.size)) + 4 * (w1.size + b1.size),
-        bound="hbm")
-    del xbig
-    cpu = _cpu_time_ms(lambda: ref.conv2d_forward(hx2, w2, b2, 1, 1, 1)) if ref else None
-    run = lambda: nnh.conv2d_forward(x2, dw2, db2, 1, 1, True)
-    row(3, "conv2 conv2d_relu fwd (32->64, 14x14, b128)", device_time_ms(run),
-        flops=2.0 * 128 * 64 * 196 * 288, nbytes=4 * (hx2.size + w2.size + 64 + 128 * 64 * 196), cpu_ms=cpu,
-        **conv_checks(lambda: run()[:1], hx2, w2, b2, 289))
-    y2, al2 = nnh.conv2d_forward(x2, dw2, db2, 1, 1, True)
-    hg2 = synth.normal(32, tuple(y2.shape))
-    g2 = d(hg2)
+    y2, al2 = torch.empty((N, 64, 14, 14), device=dev), torch.empty((N, 64, 14, 14), dtype=torch.uint8, device=dev)
+    conv2 = conv_fwd(x2, dw2, db2, y2, al2, (N, 32, 14, 14))
+    conv2()
+    hy1, hy2 = y1.cpu().numpy(), y2.cpu().numpy()
+    hg1, hg2 = synth.normal(31, (N, 32, 28, 28)), synth.normal(32, (N, 64, 14, 14))
+    g1, g2 = d(hg1), d(hg2)
+    gx1, gw1, gb1 = torch.empty_like(dxc), torch.empty_like(dw1), torch.empty_like(db1)
     gx2, gw2, gb2 = torch.empty_like(x2), torch.empty_like(dw2), torch.empty_like(db2)
-    cpu, want = None, None
-    if ref:
-        want = list(ref.conv2d_backward(hx2, w2, b2, 1, 1, 1, hg2))
-        cpu = _cpu_time_ms(lambda: ref.conv2d_backward(hx2, w2, b2, 1, 1, 1, hg2))
-    run = lambda: nnh.conv2d_backward(g2, x2, dw2, al2, 1, 1, gx2, True, gw2, True, gb2, True)
-    ms = device_time_ms(run)
-    same, got = _repeat_runs(lambda: (run(), gx2, gw2, gb2)[1:])
-    # fp64 gradients of the masked output gradient gm: dx is the transposed convolution (Cout kh kw terms),
-    # dW correlates gm with the padded input (N Ho Wo terms), db sums gm
-    gm = hg2.astype(np.float64) * (_host(y2) > 0)
-    xp = np.pad(hx2.astype(np.float64), ((0, 0), (0, 0), (1, 1), (1, 1)))
-    dx64, dxmag = np.zeros(xp.shape), np.zeros(xp.shape)
-    dw64, dwmag = np.zeros(w2.shape), np.zeros(w2.shape)
-    for i in range(3):
-        for j in range(3):
-            win = xp[:, :, i:i + 14, j:j + 14]
-            dw64[:, :, i, j] = np.einsum("nohw,nchw->oc", gm, win, optimize=True)
-            dwmag[:, :, i, j] = np.einsum("nohw,nchw->oc", np.abs(gm), np.abs(win), optimize=True)
-            dx64[:, :, i:i + 14, j:j + 14] += np.einsum("nohw,oc->nchw", gm, w2[:, :, i, j].astype(np.float64),
-                                                        optimize=True)
-            dxmag[:, :, i:i + 14, j:j + 14] += np.einsum("nohw,oc->nchw", np.abs(gm),
-                                                         np.abs(w2[:, :, i, j].astype(np.float64)), optimize=True)
-    f64 = worst([_vs_f64(got[0], dx64[:, :, 1:15, 1:15], dxmag[:, :, 1:15, 1:15], 64 * 9),
-                 _vs_f64(got[1], dw64, dwmag, 128 * 196),
-                 _vs_f64(got[2], gm.sum((0, 2, 3)), np.abs(gm).sum((0, 2, 3)), 128 * 196)])
-    row(3, "conv2 conv2d_relu bwd (dx, dW, db)", ms, flops=2 * 2.0 * 128 * 64 * 196 * 288, cpu_ms=cpu,
-        repeat=same, cpu_diff=_vs_cpu(got, want) if ref else None, f64=f64)
 
-    # config 4: attention 32 x 8 heads x 256 x 64 (+ causal); probs stored, as the reference does
-    q, k, v = (synth.normal(3 + i, (32, 256, 512)) for i in range(3))
-    hg = synth.normal(7, (32, 256, 512))
-    dq_, dk_, dv_ = d(q), d(k), d(v)
-    att_flops = 2 * 2.0 * 32 * 8 * 256 * 256 * 64
-    out64, grads64 = _attention_f64(q, k, v, hg, 8, False)
+    def conv_bwd(g_, x_, w_, al_, dims_, outs_):
+        n_, cin, h, w__ = dims_
+        gx, gw, gb = outs_
+        return lambda: nnh.check(L.nnh_conv2d_backward(P(g_), P(x_), P(w_), P(al_), n_, cin, h, w__, w_.shape[0], 3, 3,
+                                                       1, 1, P(gx), 1, P(gw), 1, P(gb), 1, st()))
+
+    conv_cache = {}
+
+    def conv_cpu(which, ref, w, r, bud):
+        """nn-cpp's conv2d_relu forward and backward rule for one layer; both rows of a layer share one call."""
+        if (which, w, r, bud) not in conv_cache:
+            xx, ww, bb, gg = (xc, w1, b1, hg1) if which == 1 else (hx2, w2, b2, hg2)
+            conv_cache[(which, w, r, bud)] = ref.time_conv2d(xx, ww, bb, 1, 1, 1, gg, w, r, bud)
+        return conv_cache[(which, w, r, bud)]
+
+    def conv_fwd_f64(x_, w_, b_, terms):
+        return lambda h: (lambda y64, mag: _vs_f64(h[0], np.maximum(y64, 0), mag, terms))(*_conv_f64(x_, w_, b_, 1))
+
+    def conv_bwd_f64(hg, hy, x_, w_, hw):
+        def f(h):
+            (dx64, dxm), (dw64, dwm), (db64, dbm) = _conv_bwd_f64(hg.astype(np.float64) * (hy > 0), x_, w_)
+            return _worst([_vs_f64(h[0], dx64, dxm, w_.shape[0] * 9), _vs_f64(h[1], dw64, dwm, N * hw),
+                           _vs_f64(h[2], db64, dbm, N * hw)])
+        return f
+
+    conv1_bytes = 4 * (xc.size + w1.size + b1.size + N * 32 * 784)
+    conv1_flops = 2.0 * N * 32 * 784 * 9
+    rows.append(Row(3, "conv1_forward", "conv2d_relu forward, conv1: x [128,1,28,28] -> y [128,32,28,28], 3x3 s1 p1, "
+                    "with alive flags", conv1, lambda: [y1], conv1_flops, nbytes=conv1_bytes, bound="hbm",
+                    cpu=lambda ref, w, r, bud: (lambda f, b: (f[0], [f[1]]))(*conv_cpu(1, ref, w, r, bud)),
+                    f64=conv_fwd_f64(xc, w1, b1, 10), est_ms=0.006))
+    conv1_na = conv_fwd(dxc, dw1, db1, y1, None, (N, 1, 28, 28))
+    rows.append(Row(3, "conv1_forward_no_alive", "conv2d_relu forward, conv1, without alive flags (the backward masks "
+                    "with y > 0)", conv1_na, lambda: [y1], conv1_flops, nbytes=conv1_bytes, bound="hbm",
+                    f64=conv_fwd_f64(xc, w1, b1, 10), est_ms=0.006))
+    conv1_bwd_bytes = 4 * (hg1.size + xc.size + w1.size + xc.size + w1.size + b1.size)
+    rows.append(Row(3, "conv1_backward", "conv2d_relu backward, conv1: dx, dW, db (g masked by alive)",
+                    conv_bwd(g1, dxc, dw1, al1, (N, 1, 28, 28), (gx1, gw1, gb1)), lambda: [gx1, gw1, gb1],
+                    2 * conv1_flops, nbytes=conv1_bwd_bytes, bound="hbm",
+                    cpu=lambda ref, w, r, bud: (lambda f, b: (b[0], list(b[1])))(*conv_cpu(1, ref, w, r, bud)),
+                    f64=conv_bwd_f64(hg1, hy1, xc, w1, 784), est_ms=0.03))
+    hy1c = y1.cpu().numpy()
+    hgp = synth.normal(33, (N, 32, 14, 14))
+    gp, gxp = d(hgp), torch.empty_like(y1)
+    pool_cache = {}
+
+    def pool_cpu(ref, w, r, bud):
+        if (w, r, bud) not in pool_cache:
+            pool_cache[(w, r, bud)] = ref.time_maxpool2d(hy1c, 2, 2, hgp, w, r, bud)
+        return pool_cache[(w, r, bud)]
+
+    def pool1_bwd():
+        nnh.check(L.nnh_maxpool2d_backward(P(gp), C.c_void_p(arg1.data_ptr()), N, 32, 28, 28, 2, 2, P(gxp), 1, st()))
+
+    pool_bytes = 4 * (hy1c.size + hx2.size)
+    rows.append(Row(3, "pool1_forward", "maxpool2d forward 2x2 s2 on conv1's output: [128,32,28,28] -> [128,32,14,14]"
+                    " (argmax kept)", pool1, lambda: [x2, arg1], 0, nbytes=pool_bytes, bound="hbm",
+                    cpu=lambda ref, w, r, bud: (lambda f, b: (f[0], [f[1], None]))(*pool_cpu(ref, w, r, bud)),
+                    est_ms=0.005))
+    rows.append(Row(3, "pool1_backward", "maxpool2d backward 2x2 s2: dx [128,32,28,28] from g [128,32,14,14]",
+                    pool1_bwd, lambda: [gxp], 0, nbytes=pool_bytes, bound="hbm",
+                    cpu=lambda ref, w, r, bud: (lambda f, b: (b[0], [b[1]]))(*pool_cpu(ref, w, r, bud)),
+                    est_ms=0.008))
+    conv2_flops = 2.0 * N * 64 * 196 * 288
+    rows.append(Row(3, "conv2_forward", "conv2d_relu forward, conv2: x [128,32,14,14] -> y [128,64,14,14], 3x3 s1 p1",
+                    conv2, lambda: [y2], conv2_flops, nbytes=4 * (hx2.size + w2.size + 64 + N * 64 * 196),
+                    cpu=lambda ref, w, r, bud: (lambda f, b: (f[0], [f[1]]))(*conv_cpu(2, ref, w, r, bud)),
+                    f64=conv_fwd_f64(hx2, w2, b2, 289), est_ms=0.02))
+    rows.append(Row(3, "conv2_backward", "conv2d_relu backward, conv2: dx, dW, db (g masked by alive)",
+                    conv_bwd(g2, x2, dw2, al2, (N, 32, 14, 14), (gx2, gw2, gb2)), lambda: [gx2, gw2, gb2],
+                    2 * conv2_flops,
+                    cpu=lambda ref, w, r, bud: (lambda f, b: (b[0], list(b[1])))(*conv_cpu(2, ref, w, r, bud)),
+                    f64=conv_bwd_f64(hg2, hy2, hx2, w2, 196), est_ms=0.05))
+
+    # config 4: attention, batch 32, 8 heads, seq 256, head width 64 (+ causal); probs stored, as the reference does
+    Na, T, D, H = 32, 256, 512, 8
+    q, k, v = (synth.normal(3 + i, (Na, T, D)) for i in range(3))
+    hg = synth.normal(7, (Na, T, D))
+    dq_, dk_, dv_, ga = d(q), d(k), d(v), d(hg)
+    att_flops = 2 * 2.0 * Na * H * T * T * (D // H)
+    useful = 2 * 2.0 * Na * H * (T * (T + 1) // 2) * (D // H)
+    att_cache = {}
+
+    def att_cpu(causal, ref, w, r, bud):
+        if (causal, w, r, bud) not in att_cache:
+            att_cache[(causal, w, r, bud)] = ref.time_attention(q, k, v, H, causal, hg, w, r, bud)
+        return att_cache[(causal, w, r, bud)]
+
+    f64_cache = {}
+
+    def att_f64(causal):
+        if causal not in f64_cache:
+            f64_cache[causal] = _attention_f64(q, k, v, hg, H, causal)
+        return f64_cache[causal]
+
     for causal in (False, True):
-        cpu = _cpu_time_ms(lambda: ref.attention_forward(q, k, v, 8, None, causal), budget_s=4.0, max_runs=5) if ref else None
-        run = lambda: nnh.attention_forward(dq_, dk_, dv_, 8, None, causal)
-        ms = device_time_ms(run)
-        same, (got,) = _repeat_runs(lambda: run()[:1])
-        want64 = out64 if not causal else _attention_f64(q, k, v, hg, 8, True)[0]
-        row(4, "attention fwd" + (" causal" if causal else ""), ms, flops=att_flops, cpu_ms=cpu, repeat=same,
-            cpu_diff=_vs_cpu([got], [ref.attention_forward(q, k, v, 8, None, causal)]) if ref else None,
-            f64=_vs_f64(got, want64))
-    out, probs = nnh.attention_forward(dq_, dk_, dv_, 8, None, False)
-    ga = d(hg)
-    gq, gk, gv = torch.empty_like(dq_), torch.empty_like(dk_), torch.empty_like(dv_)
-    cpu, want = None, None
-    if ref:
-        want = list(ref.attention_backward(q, k, v, 8, hg))
-        cpu = _cpu_time_ms(lambda: ref.attention_backward(q, k, v, 8, hg), budget_s=4.0, max_runs=3)
-    run = lambda: nnh.attention_backward(ga, dq_, dk_, dv_, probs, 8, None, False, gq, True, gk, True, gv, True)
-    ms = device_time_ms(run)
-    same, got = _repeat_runs(lambda: (run(), gq, gk, gv)[1:])
-    row(4, "attention bwd (dQ, dK, dV)", ms, flops=2 * att_flops, cpu_ms=cpu, repeat=same,
-        cpu_diff=_vs_cpu(got, want) if ref else None, f64=worst([_vs_f64(g_, w_) for g_, w_ in zip(got, grads64)]))
-    del out64, grads64
+        out = torch.empty((Na, T, D), device=dev)
+        probs = torch.empty((Na, H, T, T), device=dev)
+        gq, gk, gv = torch.empty_like(dq_), torch.empty_like(dk_), torch.empty_like(dv_)
 
-    # config 5: roofline sweep, seed 4; fp64 on 256 evenly spaced rows when m >= 2048
-    for (m, n_, k_) in ((1024, 1024, 1024), (2048, 2048, 2048), (4096, 4096, 4096), (8192, 8192, 8192),
-                        (64, 4096, 4096), (4096, 4096, 64)):
-        a, b = synth.uniform_operands(4, [(m, k_), (k_, n_)])
-        da, db, dc = d(a), d(b), torch.empty((m, n_), device=dev)
-        c = np.empty((m, n_), np.float32)
-        reps = 5 if m * n_ * k_ >= 8192 ** 3 else 20
-        cpu = _cpu_time_ms(lambda: ref.sgemm_inplace(0, 0, m, n_, k_, a, k_, b, n_, c, n_, 0),
-                           budget_s=6.0, max_runs=5) if ref else None
-        run = lambda: nnh.sgemm(0, 0, m, n_, k_, da, k_, db, n_, dc, n_)
-        ms = device_time_ms(run, reps=reps)
-        same, (got,) = _repeat_runs(lambda: (run(), dc)[1:])
-        sample = np.linspace(0, m - 1, 256).astype(np.int64) if m >= 2048 else None
-        row(5, f"sgemm {m}x{n_}x{k_}", ms, flops=2.0 * m * n_ * k_, cpu_ms=cpu, repeat=same,
-            cpu_diff=_vs_cpu([got], [c]) if ref else None, f64=gemm_f64(got, a, b, sample))
-        del got, c
+        def fwd(out=out, probs=probs, causal=causal):
+            nnh.check(L.nnh_attention_forward(P(dq_), P(dk_), P(dv_), Na, T, T, D, H, None, causal, P(out), P(probs),
+                                              st()))
 
-    lines = [f"GPU: {torch.cuda.get_device_name(0)}; nn-cpp CPU baseline: NN_NATIVE AVX2 build, {threads} threads on "
-             f"{cpu_model()}", "",
-             "| cfg | workload | GPU ms | TFLOP/s | GB/s | bound | % of roofline | nn-cpp CPU ms | GPU speedup | "
-             "3 GPU runs | max abs diff vs nn-cpp | max abs err vs fp64 | err / bound |",
-             "|---|---|---|---|---|---|---|---|---|---|---|---|---|"]
+        def bwd(probs=probs, gq=gq, gk=gk, gv=gv, causal=causal):
+            nnh.check(L.nnh_attention_backward(P(ga), P(dq_), P(dk_), P(dv_), P(probs), Na, T, T, D, H, None, causal,
+                                               P(gq), 1, P(gk), 1, P(gv), 1, st()))
+
+        fwd()
+        tag = " causal" if causal else ""
+        rows.append(Row(4, "attention_forward" + ("_causal" if causal else ""),
+                        f"nn::attention forward{tag}: q, k, v [32,256,512], 8 heads of 64, probs stored", fwd,
+                        lambda out=out: [out], att_flops, useful_flops=useful if causal else None,
+                        cpu=lambda ref, w, r, bud, c=causal: (lambda f, b: (f[0], [f[1]]))(*att_cpu(c, ref, w, r, bud)),
+                        f64=lambda h, c=causal: _vs_f64(h[0], att_f64(c)[0]), est_ms=0.085))
+        rows.append(Row(4, "attention_backward" + ("_causal" if causal else ""),
+                        f"nn::attention backward{tag}: dQ, dK, dV", bwd, lambda gq=gq, gk=gk, gv=gv: [gq, gk, gv],
+                        2 * att_flops, useful_flops=2 * useful if causal else None,
+                        cpu=lambda ref, w, r, bud, c=causal: (lambda f, b: (b[0], list(b[1])))(*att_cpu(c, ref, w, r, bud)),
+                        f64=lambda h, c=causal: _worst([_vs_f64(g_, w_) for g_, w_ in zip(h, att_f64(c)[1])]),
+                        est_ms=0.13))
+
+    # config 5: the roofline sweep through nn::matmul (seed 4)
+    for (m5, n5, k5, est) in ((1024, 1024, 1024, 0.027), (2048, 2048, 2048, 0.16), (4096, 4096, 4096, 1.15),
+                              (8192, 8192, 8192, 9.1), (64, 4096, 4096, 0.06), (4096, 4096, 64, 0.028)):
+        matmul_row(5, f"matmul_{m5}x{n5}x{k5}", f"nn::matmul {m5}x{n5}x{k5} C = A B", 4, m5, n5, k5, 0, 0, est)
+    return rows
+
+
+def run_gpu_rows(rows):
+    """Times every row on the GPU, checks that three runs give the same bits, and keeps one run's outputs on the
+    host."""
+    import torch
     for r in rows:
-        f = lambda v, fmt: (fmt % v) if v is not None else "-"
-        rep = "-" if r["repeat"] is None else ("bitwise equal" if r["repeat"] else "DIFFER")
-        cd = "-" if r["cpu_diff"] is None else ("0 (bitwise)" if r["cpu_diff"][1] else "%.3g" % r["cpu_diff"][0])
-        fe = r["f64"] or (None, None)
-        lines.append(f"| {r['config']} | {r['what']} | {r['ms']:.4f} | {f(r['tflops'], '%.2f')} | {f(r['gbps'], '%.0f')} | "
-                     f"{r['bound']} | {r['roofline_frac'] * 100:.1f}% | {f(r['cpu_ms'], '%.3f')} | "
-                     f"{f(r['speedup_vs_cpu'], '%.0fx')} | {rep} | {cd} | {f(fe[0], '%.3g')} | {f(fe[1], '%.3g')} |")
+        times = device_times(r.gpu, r.est_ms)
+        ms = median(times)
+        res = {"ms": ms, "spread": spread(times), "runs": len(times)}
+        outs = []
+        for rep in range(3):
+            r.gpu()
+            torch.cuda.synchronize()
+            cur = [t.clone() for t in r.outs()]
+            outs.append(cur)
+        same = all(torch.equal(a.view(torch.int32), b.view(torch.int32)) for a, b in zip(outs[0], outs[1])) and \
+            all(torch.equal(a.view(torch.int32), b.view(torch.int32)) for a, b in zip(outs[0], outs[2]))
+        res["bitwise_repeat"] = bool(same)
+        r.host_outs = [t.cpu().numpy() for t in outs[0]]
+        del outs
+        if r.flops:
+            res["tflops"] = r.flops / (ms * 1e-3) / 1e12
+        if r.nbytes:
+            res["gbps"] = r.nbytes / (ms * 1e-3) / 1e9
+        achieved = res["tflops"] if r.bound == "mfma" else res["gbps"]
+        peak = PEAK_FP32_MFMA_TFLOPS if r.bound == "mfma" else PEAK_HBM_GBPS
+        res["roofline"] = {"bound": r.bound, "achieved": achieved, "peak": peak,
+                           "unit": "TFLOP/s" if r.bound == "mfma" else "GB/s", "frac": achieved / peak}
+        if r.useful_flops:
+            res["roofline"]["useful_frac"] = r.useful_flops / (ms * 1e-3) / 1e12 / PEAK_FP32_MFMA_TFLOPS
+        r.result = res
+        log(f"[cfg {r.cfg}] {r.key}: {ms * 1e3:.2f} us (spread {res['spread']:.3f}), "
+            f"{achieved:.1f} {res['roofline']['unit']} = {res['roofline']['frac'] * 100:.1f}% of {r.bound} peak, "
+            f"repeat bitwise {same}")
+
+
+def run_cpu_rows(rows, headline=None):
+    """nn-cpp's own op on the same host buffers for every row with a CPU counterpart: one thread per physical core
+    (pinned) and one thread; the last run's outputs are compared with the GPU's. Returns the baseline's setup."""
+    import numpy as np
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    from pyoracle import Reference, reference_available
+    if not reference_available():
+        log("cpu baseline: oracle/_ref not built; skipped")
+        return None
+    cores, allowed = physical_cores()
+    saved = os.sched_getaffinity(0)
+    ref = Reference()
+    setup = {"cpu": cpu_model(), "governor": cpu_governor(), "allowed_cpus": allowed, "physical_cores": len(cores),
+             "pinned_to": cores, "build": "nn-cpp 2.0.0 NN_NATIVE (g++ -O3 -mavx2 -mfma -ffp-contract=off)"}
+    log(f"cpu baseline: {setup['cpu']}, governor {setup['governor']}, {len(cores)} physical cores of {allowed} "
+        f"allowed CPUs")
+    try:
+        for threads, budget, max_runs, key in ((len(cores), 1.5, 15, "cpu_baseline"), (1, 1.0, 5, "cpu_1thread")):
+            os.sched_setaffinity(0, cores[:threads])
+            ref.set_threads(threads)
+            for r in rows + ([headline] if headline is not None and threads == len(cores) else []):
+                if r.cpu is None:
+                    continue
+                t0 = time.perf_counter()
+                # one untimed call first (page faults, the pool's start); a single run past the budget counts as it
+                times, outs = r.cpu(ref, 0, 1, 0.0)
+                warm = times[0] * 1e-3 < budget
+                if warm:
+                    times, outs = r.cpu(ref, 0, max_runs, budget)
+                ms = median(times)
+                entry = {"ms": ms, "spread": spread(times), "runs": len(times), "threads": threads,
+                         "warmup": 1 if warm else 0}
+                if r.flops:
+                    entry["tflops"] = r.flops / (ms * 1e-3) / 1e12
+                if key == "cpu_baseline" and hasattr(r, "host_outs"):
+                    pairs = [(g, w) for g, w in zip(r.host_outs, outs) if w is not None]
+                    same = all(np.array_equal(g.view(np.uint32), w.reshape(g.shape).view(np.uint32)) for g, w in pairs)
+                    diff = max(float(np.max(np.abs(g.astype(np.float64) - w.reshape(g.shape).astype(np.float64))))
+                               if g.size else 0.0 for g, w in pairs)
+                    r.result["bitwise_vs_nn_cpp"] = bool(same)
+                    r.result["maxabs_vs_nn_cpp"] = diff
+                r.result[key] = entry
+                log(f"  [{key} x{threads}] {r.key}: {ms:.3f} ms median of {len(times)} "
+                    f"({time.perf_counter() - t0:.1f} s)")
+    finally:
+        os.sched_setaffinity(0, saved)
+    return setup
+
+
+def write_csv(path, rows, setup):
+    """apps/bench/bench.cpp:112-113's columns, then the GPU columns; one line per GPU row and per CPU baseline."""
+    cols = ["config", "label", "threads", "benchmark", "size", "forward_ms", "backward_ms", "optim_ms", "total_ms",
+            "gflops", "spread", "runs", "tflops", "gbps", "roofline_bound", "roofline_frac", "maxabs_err",
+            "bitwise_repeat"]
+    lines = [",".join(cols)]
+    f = lambda v: "" if v is None else (f"{v:.6g}" if isinstance(v, float) else str(v))
+    for r in rows:
+        res = r.result
+        back = "backward" in r.key
+        size = r.key.split("_", 1)[1] if r.key.startswith("matmul") else str(r.cfg)
+        for label, ent, thr in (("gpu-mi355x", res, ""), ("native-pinned", res.get("cpu_baseline"), None),
+                                ("native-1thread", res.get("cpu_1thread"), None)):
+            if not ent:
+                continue
+            ms = ent["ms"]
+            gpu = label.startswith("gpu")
+            vals = ["gpu" if gpu else "native", label, thr if gpu else ent["threads"], r.key, size,
+                    None if back else ms, ms if back else None, None, ms,
+                    r.flops / (ms * 1e6) if r.flops else None, ent["spread"], ent["runs"],
+                    res.get("tflops") if gpu else ent.get("tflops"), res.get("gbps") if gpu else None,
+                    r.bound if gpu else None, res["roofline"]["frac"] if gpu else None,
+                    res.get("maxabs_vs_nn_cpp") if gpu else None, res.get("bitwise_repeat") if gpu else None]
+            lines.append(",".join(f(v) for v in vals))
+    with open(path, "w") as fh:
+        fh.write("\n".join(lines) + "\n")
+    log(f"csv: {path} ({len(lines) - 1} rows)")
+
+
+def row_json(r):
+    res = r.result
+    out = {"cfg": r.cfg, "key": r.key, "workload": r.workload, "ms": round(res["ms"], 6),
+           "spread": round(res["spread"], 4), "runs": res["runs"]}
+    for k in ("tflops", "gbps"):
+        if k in res:
+            out[k] = round(res[k], 3)
+    out["roofline"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in res["roofline"].items()}
+    for k in ("bitwise_repeat", "bitwise_vs_nn_cpp"):
+        if k in res:
+            out[k] = res[k]
+    for k in ("cpu_baseline", "cpu_1thread"):
+        if k in res:
+            e = res[k]
+            out[k] = {"ms": round(e["ms"], 4), "threads": e["threads"], "runs": e["runs"],
+                      "spread": round(e["spread"], 4), "speedup_gpu": round(e["ms"] / res["ms"], 1)}
+    return out
+
+
+def report(with_cpu=True):
+    """The config rows as a markdown table, with the fp64 checks (slow)."""
+    import torch
+    rows = build_rows(report=True)
+    run_gpu_rows(rows)
+    setup = run_cpu_rows(rows) if with_cpu else None
+    for r in rows:
+        if r.f64:
+            r.result["f64"] = r.f64(r.host_outs)
+    lines = [f"GPU: {torch.cuda.get_device_name(0)}; nn-cpp CPU baseline: " +
+             (f"{setup['build']}, {setup['physical_cores']} threads pinned one per physical core of {setup['cpu']} "
+              f"(governor {setup['governor']}), and 1 thread" if setup else "not run"), "",
+             "| cfg | workload | GPU ms (median) | spread | TFLOP/s | GB/s | bound | % of roofline | nn-cpp CPU ms | "
+             "nn-cpp 1-thread ms | GPU speedup | 3 GPU runs | vs nn-cpp | max abs err vs fp64 | err / bound |",
+             "|---|---|---|---|---|---|---|---|---|---|---|---|---|---|---|"]
+    f = lambda v, fmt: (fmt % v) if v is not None else "-"
+    for r in rows:
+        res = r.result
+        cb, c1 = res.get("cpu_baseline"), res.get("cpu_1thread")
+        fe = res.get("f64") or (None, None)
+        vs = "-" if "bitwise_vs_nn_cpp" not in res else ("0 (bitwise)" if res["bitwise_vs_nn_cpp"]
+                                                         else "%.3g" % res["maxabs_vs_nn_cpp"])
+        lines.append(f"| {r.cfg} | {r.workload} | {res['ms']:.4f} | {res['spread']:.3f} | {f(res.get('tflops'), '%.2f')} | "
+                     f"{f(res.get('gbps'), '%.0f')} | {r.bound} | {res['roofline']['frac'] * 100:.1f}% | "
+                     f"{f(cb['ms'] if cb else None, '%.3f')} | {f(c1['ms'] if c1 else None, '%.3f')} | "
+                     f"{f(cb['ms'] / res['ms'] if cb else None, '%.0fx')} | "
+                     f"{'bitwise equal' if res['bitwise_repeat'] else 'DIFFER'} | {vs} | {f(fe[0], '%.3g')} | "
+                     f"{f(fe[1], '%.3g')} |")
     print("\n".join(lines), flush=True)
+
+
+def floor():
+    """What a single launch costs on this GPU, beside the conv1 figure: an empty one-wave kernel (nnh.bench_delay
+    with no delay), torch fills of conv1's output size (12.85 MB) and of eight times it, and copies of the same
+    sizes, each timed as device_time_ms does. Prints a markdown table."""
+    import torch
+
+    import nnh
+    dev = torch.device("cuda:0")
+    ny = 128 * 32 * 784
+    small, big = torch.empty(ny, device=dev), torch.empty(8 * ny, device=dev)
+    src_small, src_big = torch.ones(ny // 2, device=dev), torch.ones(4 * ny, device=dev)
+    rows = [("empty one-wave kernel (bench_delay 0)", lambda: nnh.bench_delay(0.0), 0),
+            ("fill 12.85 MB (conv1's y)", lambda: small.fill_(1.0), 4 * ny),
+            ("copy 6.4 MB -> 6.4 MB", lambda: small[: ny // 2].copy_(src_small), 4 * ny),
+            ("fill 102.8 MB", lambda: big.fill_(1.0), 32 * ny),
+            ("copy 51.4 MB -> 51.4 MB", lambda: big[: 4 * ny].copy_(src_big), 32 * ny)]
+    print("| launch | us | GB/s | % of 8 TB/s |\n|---|---|---|---|")
+    for name, fn, nbytes in rows:
+        ms = device_time_ms(fn, reps=200)
+        gbps = nbytes / (ms * 1e-3) / 1e9 if nbytes else 0.0
+        print(f"| {name} | {ms * 1e3:.2f} | {gbps:.0f} | {gbps / PEAK_HBM_GBPS * 100:.1f}% |", flush=True)
 
 
 def main():
@@ -556,9 +706,10 @@ def main():
     ap.add_argument("--warmup", type=int, default=40)
     ap.add_argument("--size", type=int, default=4096)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--no-fused-op", action="store_true", help="skip the conv1 fused conv2d_relu GB/s figure")
-    ap.add_argument("--report", action="store_true", help="every BASELINE config as a markdown table (not the "
-                    "driver's JSON line)")
+    ap.add_argument("--no-configs", action="store_true", help="only the headline product (no per-config rows)")
+    ap.add_argument("--csv", default=None, help="also write the rows as CSV (the reference's bench columns + GPU ones)")
+    ap.add_argument("--report", action="store_true", help="every BASELINE config as a markdown table with fp64 "
+                    "checks (not the driver's JSON line)")
     ap.add_argument("--floor", action="store_true", help="launch-cost floor of this GPU: empty kernel, fills, copies")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="only run 5 device-to-device copies of MIB MiB (calibrates rocprofv3 FETCH_SIZE/WRITE_SIZE)")
@@ -601,6 +752,14 @@ def main():
     def step():
         nnh.sgemm(0, 0, m, n, k, da, k, db, n, dc, n, 0, stream=stream)
 
+    # settle the clock, then the driver's warm-up steps, then exactly K timed steps between two synchronisations
+    settle = 0
+    t_end = time.perf_counter() + SETTLE_S
+    while settle < 20 or time.perf_counter() < t_end:
+        step()
+        settle += 1
+        if settle % 20 == 0:
+            torch.cuda.synchronize()
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
@@ -617,13 +776,31 @@ def main():
     value = flops * args.steps / wall / 1e12
     achieved = flops / (kernel_ms * 1e-3) / 1e12
     log(f"sgemm {m}^3: {kernel_ms:.4f} ms/launch (HIP events), {achieved:.2f} TFLOP/s per launch, "
-        f"{value:.2f} TFLOP/s wall over {args.steps} steps")
+        f"{value:.2f} TFLOP/s wall over {args.steps} steps after {settle} settling launches")
+    del dc
 
-    fused = None if args.no_fused_op else fused_op_conv1()
-    cpu = None if args.no_cpu_baseline else cpu_baseline(a, b, m, n, k)
-    if cpu:
-        log(f"cpu baseline: {cpu['value']} TFLOP/s ({cpu['sample']})")
-    traffic = traffic_from_profile(f"sgemm_{m}")
+    rows = []
+    if not args.no_configs:
+        rows = build_rows()
+        run_gpu_rows(rows)
+    headline = Row(5, "headline", f"nn::kernels::sgemm {m}^3", None, None, flops,
+                   cpu=lambda ref, w, r, bud: ref.time_matmul(a, b, 0, 0, w, r, bud))
+    setup = None
+    if not args.no_cpu_baseline:
+        setup = run_cpu_rows(rows, headline)
+    if args.csv and rows:
+        write_csv(args.csv, rows, setup)
+    cpu = None
+    hb = headline.result.get("cpu_baseline")
+    if hb:
+        cpu = {"value": round(flops / (hb["ms"] * 1e-3) / 1e12, 4), "unit": "TFLOP/s", "cores": hb["threads"],
+               "kind": "reference",
+               "sample": (f"nn::matmul {m}x{n}x{k} (nn-cpp 2.0.0 NN_NATIVE AVX2/FMA build, -O3 -mavx2 -mfma "
+                          f"-ffp-contract=off) on the same seed-4 inputs, {hb['threads']} threads pinned one per "
+                          f"physical core of {setup['cpu']} (governor {setup['governor']}), median of {hb['runs']} "
+                          f"runs after {hb['warmup']} warm-up")}
+    conv1 = next((r for r in rows if r.key == "conv1_forward"), None)
+    conv1_na = next((r for r in rows if r.key == "conv1_forward_no_alive"), None)
     out = {
         "metric": "fp32 GEMM TFLOP/s @4096^3 (nn::kernels::sgemm replacement, bit-exact with nn-cpp)",
         "value": round(value, 3),
@@ -631,19 +808,29 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "settle_launches": settle,
         "ms_per_step": round(wall / args.steps * 1e3, 5),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",
-        "data": "synthetic: the reference's seeded uniform[-1,1] stream (std::mt19937(4) + "
-                "uniform_real_distribution<float>), A then B",
+        "data": "synthetic: the reference's seeded streams (std::mt19937(seed) + uniform_real_distribution<float>; "
+                "N(0,1) from numpy's PCG64 where BASELINE.json asks for normal values); both sides get the same buffers",
         "config": {"workload": f"sgemm {m}x{n}x{k} NN fp32 (BASELINE config 5)", "m": m, "n": n, "k": k,
                    "trans_a": False, "trans_b": False, "parallelism": "single GPU"},
         "roofline": {"bound": "mfma", "achieved": round(achieved, 3), "peak": PEAK_FP32_MFMA_TFLOPS,
-                     "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP32_MFMA_TFLOPS, 4), "traffic": traffic},
+                     "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP32_MFMA_TFLOPS, 4),
+                     "traffic": traffic_from_profile(f"sgemm_{m}")},
         "cpu_baseline": cpu,
-        "fused_op": fused,
+        "cpu_setup": setup,
+        "fused_op": None if conv1 is None else {
+            "workload": conv1.workload, "value": round(conv1.result["gbps"], 1), "unit": "GB/s",
+            "us_per_launch": round(conv1.result["ms"] * 1e3, 3), "algorithmic_bytes": conv1.nbytes,
+            "roofline": {"bound": "hbm", "peak": PEAK_HBM_GBPS, "unit": "GB/s",
+                         "frac": round(conv1.result["roofline"]["frac"], 4)},
+            "without_alive_flags": None if conv1_na is None else {
+                "us_per_launch": round(conv1_na.result["ms"] * 1e3, 3), "value": round(conv1_na.result["gbps"], 1)}},
+        "configs": [row_json(r) for r in rows],
     }
     print(json.dumps(out), flush=True)
 

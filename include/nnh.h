@@ -134,6 +134,20 @@ int nnh_matmul(const float* a, const size_t* a_shape, int a_ndim, const float* b
                int trans_a, int trans_b, float* out, void* stream);
 
 /*
+ * Backward of nn::matmul(a, b) (b_transposed = 0, src/autograd/ops.cpp:683-712) and nn::matmul_bt(a, b)
+ * (b_transposed = 1, ops.cpp:747-773) for upstream gradient g of the forward's output shape. With b a 2-D matrix,
+ * a's leading axes fold into M rows and each gradient is one sgemm with accumulate = !first; otherwise the
+ * gradient is a batched product reduced over broadcast axes (sum_to_shape, ops.cpp:35-53) and stored as term + 0.0f
+ * into a fresh gradient or added. da or db may be NULL; when a and b are one tensor, pass one gradient buffer twice
+ * with db_first = 0 (dA is written first). NNH_ERR_SHAPE where the forward's shapes would throw.
+ */
+int nnh_matmul_backward(const float* g, const float* a, const size_t* a_shape, int a_ndim, const float* b,
+                        const size_t* b_shape, int b_ndim, int b_transposed, float* da, int da_first, float* db,
+                        int db_first, void* stream);
+int nnh_matmul_backward_workspace_size(const size_t* a_shape, int a_ndim, const size_t* b_shape, int b_ndim,
+                                       int b_transposed, int want_da, int want_db, size_t* bytes);
+
+/*
  * nn::linear forward (src/autograd/ops.cpp:714-730): y[M x n] = x[M x K] w[n x K]^T, then + bias[n] per
  * column, in one kernel. relu != 0 also applies the ReLU node that follows a Linear in the reference
  * (ops.cpp:775-782) in the same epilogue: y = v > 0 ? v : 0 (bit-identical to linear then relu).
@@ -222,6 +236,22 @@ int nnh_im2col(const float* x, size_t N, size_t Cin, size_t H, size_t W, size_t 
  * in the reference's order; first zero-fills dx first. */
 int nnh_col2im_add(const float* col, size_t N, size_t Cin, size_t H, size_t W, size_t kh, size_t kw, int stride,
                    int padding, float* dx, int first, void* stream);
+
+/*
+ * nn::maxpool2d forward (src/autograd/ops.cpp:1609-1684): x {N, C, H, W}, windows kernel x kernel at stride
+ * `stride`, no padding; y {N, C, Ho, Wo} with Ho = (H - kernel) / stride + 1. Each window is scanned row by row from
+ * -inf, a value taken only when greater (the first maximum wins; NaN never does; a window with nothing above -inf
+ * gives -inf and offset 0). argmax (optional, one uint32 per output) receives the winner's offset inside its
+ * (n, c) plane, which the backward pass needs. NNH_ERR_SHAPE where the reference throws TensorShapeError: kernel or
+ * stride 0, a kernel larger than the plane, a plane beyond 2^32 elements.
+ */
+int nnh_maxpool2d_forward(const float* x, size_t N, size_t C, size_t H, size_t W, size_t kernel, size_t stride,
+                          float* y, unsigned int* argmax, void* stream);
+
+/* Its backward (ops.cpp:1686-1704): dx {N, C, H, W} (first: zero-filled first, as a fresh gradient) += g at each
+ * output's argmax, in output order. */
+int nnh_maxpool2d_backward(const float* g, const unsigned int* argmax, size_t N, size_t C, size_t H, size_t W,
+                           size_t kernel, size_t stride, float* dx, int first, void* stream);
 
 #ifdef __cplusplus
 }

@@ -88,6 +88,10 @@ _EXTRA_DECLS = {
     "nnh_attention_forward_workspace_size": [_sz, _sz, _sz, _sz, _sz, _szp],
     "nnh_attention_backward_workspace_size": [_sz, _sz, _sz, _sz, _sz, _szp],
     "nnh_sgemm_noalloc": [C.c_int, C.c_int, _sz, _sz, _sz, _vp, _sz, _vp, _sz, _vp, _sz, C.c_int, _vp],
+    "nnh_maxpool2d_forward": [_vp, _sz, _sz, _sz, _sz, _sz, _sz, _vp, _vp, _vp],
+    "nnh_maxpool2d_backward": [_vp, _vp, _sz, _sz, _sz, _sz, _sz, _sz, _vp, C.c_int, _vp],
+    "nnh_matmul_backward": [_vp, _vp, _szp, C.c_int, _vp, _szp, C.c_int, C.c_int, _vp, C.c_int, _vp, C.c_int, _vp],
+    "nnh_matmul_backward_workspace_size": [_szp, C.c_int, _szp, C.c_int, C.c_int, C.c_int, C.c_int, _szp],
     "nnh_im2col": [_vp, _sz, _sz, _sz, _sz, _sz, _sz, C.c_int, C.c_int, _vp, _vp],
     "nnh_col2im_add": [_vp, _sz, _sz, _sz, _sz, _sz, _sz, C.c_int, C.c_int, _vp, C.c_int, _vp],
 }
@@ -220,6 +224,14 @@ def matmul(a, b, ta=False, tb=False, stream=None):
     check(lib().nnh_matmul(_ptr(a), ash, a.dim(), _ptr(b), bsh, b.dim(), int(ta), int(tb), _ptr(out),
                            _stream(stream)))
     return out
+
+
+def matmul_backward(g, a, b, b_transposed=False, da=None, da_first=True, db=None, db_first=True, stream=None):
+    """nn::matmul / nn::matmul_bt backward into the given gradient buffers (either may be None)."""
+    ash = (C.c_size_t * a.dim())(*a.shape)
+    bsh = (C.c_size_t * b.dim())(*b.shape)
+    check(lib().nnh_matmul_backward(_ptr(g), _ptr(a), ash, a.dim(), _ptr(b), bsh, b.dim(), int(b_transposed), _ptr(da),
+                                    int(da_first), _ptr(db), int(db_first), _stream(stream)))
 
 
 def linear_forward(x, w, bias, relu=False, stream=None):

@@ -1,0 +1,171 @@
+// pool.hip - nn::maxpool2d forward and backward (src/autograd/ops.cpp:1609-1705) on NCHW planes.
+//
+// Forward: each output scans its kernel x kernel window row by row from best = -inf, at = 0, taking a value only
+// when it is greater than best (the first maximum wins, NaN never does, and a window with nothing above -inf keeps
+// offset 0 of the plane). The argmax is that offset inside the (n, c) plane, as the reference keeps it for backward.
+// Backward: the reference zero-fills a fresh plane and adds g[i] at argmax[i] for i in output order. Here each
+// input element gathers instead, visiting the windows that contain it in output order (no atomics, one writer per
+// element). Offset 0 of a plane also receives the windows that kept offset 0 without containing it, so its thread
+// walks every output of the plane in order.
+#include "pool.hpp"
+
+#include <cmath>
+
+#include "fastdiv.hpp"
+
+namespace nnh {
+
+namespace {
+
+struct PoolArgs {
+	const float* x;
+	float* y;
+	uint32_t* arg;
+	int64_t total;          // outputs
+	int h, w, ho, wo, k, s;
+	FastDiv plane_out, wo_div;
+};
+
+// One output per thread: the general window.
+__global__ void __launch_bounds__(256) maxpool_forward_kernel(const PoolArgs a) {
+	const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+	if (idx >= a.total) return;
+	const int64_t p = idx / (a.ho * a.wo);
+	const int o = (int)(idx - p * (a.ho * a.wo));
+	const int oh = (int)fdiv((unsigned)o, a.wo_div), ow = o - oh * a.wo;
+	const float* plane = a.x + p * a.h * a.w;
+	float best = -INFINITY;
+	uint32_t at = 0;
+	for (int ph = 0; ph < a.k; ++ph) {
+		const int r = oh * a.s + ph;
+		const float* row = plane + (int64_t)r * a.w + ow * a.s;
+		for (int pw = 0; pw < a.k; ++pw) {
+			const float v = row[pw];
+			if (v > best) {
+				best = v;
+				at = (uint32_t)(r * a.w + ow * a.s + pw);
+			}
+		}
+	}
+	a.y[idx] = best;
+	if (a.arg) a.arg[idx] = at;
+}
+
+// 2 x 2 windows, stride 2, W a multiple of 4 and 16-byte aligned planes: two outputs per thread from one 16-byte
+// load of each of the window's two rows; the same four comparisons in the same order per output.
+__global__ void __launch_bounds__(256) maxpool2x2_forward_kernel(const PoolArgs a) {
+	const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;  // output pair
+	const int pairs = a.wo >> 1;
+	const int64_t per_plane = (int64_t)a.ho * pairs;
+	if (idx >= a.total / 2) return;
+	const int64_t p = idx / per_plane;
+	const int q = (int)(idx - p * per_plane);
+	const int oh = q / pairs, j = q - oh * pairs;
+	const float* r0 = a.x + p * a.h * a.w + (int64_t)(2 * oh) * a.w + 4 * j;
+	const float4 u = *reinterpret_cast<const float4*>(r0);
+	const float4 v = *reinterpret_cast<const float4*>(r0 + a.w);
+	const uint32_t base = (uint32_t)(2 * oh * a.w + 4 * j);
+	float b0 = -INFINITY, b1 = -INFINITY;
+	uint32_t t0 = 0, t1 = 0;
+	if (u.x > b0) { b0 = u.x; t0 = base; }
+	if (u.y > b0) { b0 = u.y; t0 = base + 1; }
+	if (v.x > b0) { b0 = v.x; t0 = base + a.w; }
+	if (v.y > b0) { b0 = v.y; t0 = base + a.w + 1; }
+	if (u.z > b1) { b1 = u.z; t1 = base + 2; }
+	if (u.w > b1) { b1 = u.w; t1 = base + 3; }
+	if (v.z > b1) { b1 = v.z; t1 = base + a.w + 2; }
+	if (v.w > b1) { b1 = v.w; t1 = base + a.w + 3; }
+	const int64_t o = p * a.ho * a.wo + (int64_t)oh * a.wo + 2 * j;
+	*reinterpret_cast<float2*>(a.y + o) = make_float2(b0, b1);
+	if (a.arg) *reinterpret_cast<uint2*>(a.arg + o) = make_uint2(t0, t1);
+}
+
+struct PoolBwdArgs {
+	const float* g;
+	const uint32_t* arg;
+	float* dx;
+	int64_t total;  // input elements
+	int h, w, ho, wo, k, s, first;
+	FastDiv plane_in, w_div, s_div;
+};
+
+// One input element per thread: the windows containing it, in output order (ops.cpp:1693-1700).
+__global__ void __launch_bounds__(256) maxpool_backward_kernel(const PoolBwdArgs a) {
+	const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+	if (idx >= a.total) return;
+	const int64_t hw = (int64_t)a.h * a.w;
+	const int64_t p = idx / hw;
+	const int e = (int)(idx - p * hw);
+	const int out_plane = a.ho * a.wo;
+	const float* g = a.g + p * out_plane;
+	const uint32_t* arg = a.arg + p * out_plane;
+	float v = a.first ? 0.0f : a.dx[idx];
+	if (e == 0) {
+		for (int i = 0; i < out_plane; ++i)
+			if (arg[i] == 0u) v = v + g[i];
+	} else {
+		const int ih = (int)fdiv((unsigned)e, a.w_div), iw = e - ih * a.w;
+		// windows oh with oh*s <= ih <= oh*s + k - 1, oh < ho (and the same across)
+		const int oh_lo = ih >= a.k ? (int)fdiv((unsigned)(ih - a.k), a.s_div) + 1 : 0;
+		const int oh_hi = min((int)fdiv((unsigned)ih, a.s_div), a.ho - 1);
+		const int ow_lo = iw >= a.k ? (int)fdiv((unsigned)(iw - a.k), a.s_div) + 1 : 0;
+		const int ow_hi = min((int)fdiv((unsigned)iw, a.s_div), a.wo - 1);
+		for (int oh = oh_lo; oh <= oh_hi; ++oh)
+			for (int ow = ow_lo; ow <= ow_hi; ++ow) {
+				const int i = oh * a.wo + ow;
+				if (arg[i] == (uint32_t)e) v = v + g[i];
+			}
+	}
+	a.dx[idx] = v;
+}
+
+}  // namespace
+
+hipError_t maxpool2d_forward(const float* x, float* y, uint32_t* arg, int64_t planes, int h, int w, int k, int s,
+                             hipStream_t st) {
+	PoolArgs a;
+	a.x = x;
+	a.y = y;
+	a.arg = arg;
+	a.h = h;
+	a.w = w;
+	a.k = k;
+	a.s = s;
+	a.ho = (h - k) / s + 1;
+	a.wo = (w - k) / s + 1;
+	a.total = planes * a.ho * a.wo;
+	a.wo_div = make_fastdiv((unsigned)a.wo);
+	if (a.total == 0) return hipSuccess;
+	const bool quad = k == 2 && s == 2 && w % 4 == 0 && h % 2 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0 &&
+	                  reinterpret_cast<uintptr_t>(y) % 8 == 0 && reinterpret_cast<uintptr_t>(arg) % 8 == 0;
+	if (quad) {
+		const int64_t threads = a.total / 2;
+		hipLaunchKernelGGL(maxpool2x2_forward_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, st, a);
+	} else {
+		hipLaunchKernelGGL(maxpool_forward_kernel, dim3((unsigned)((a.total + 255) / 256)), dim3(256), 0, st, a);
+	}
+	return hipGetLastError();
+}
+
+hipError_t maxpool2d_backward(const float* g, const uint32_t* arg, float* dx, int64_t planes, int h, int w, int k, int s,
+                              int first, hipStream_t st) {
+	PoolBwdArgs a;
+	a.g = g;
+	a.arg = arg;
+	a.dx = dx;
+	a.h = h;
+	a.w = w;
+	a.k = k;
+	a.s = s;
+	a.first = first;
+	a.ho = (h - k) / s + 1;
+	a.wo = (w - k) / s + 1;
+	a.total = planes * h * w;
+	a.w_div = make_fastdiv((unsigned)w);
+	a.s_div = make_fastdiv((unsigned)s);
+	if (a.total == 0) return hipSuccess;
+	hipLaunchKernelGGL(maxpool_backward_kernel, dim3((unsigned)((a.total + 255) / 256)), dim3(256), 0, st, a);
+	return hipGetLastError();
+}
+
+}  // namespace nnh

@@ -174,7 +174,43 @@ SumJob sum_job(const float* src, int64_t rows, int64_t inner, float* dst, int co
 
 unsigned sum_blocks(int64_t inner) { return (unsigned)((inner + kSumCols - 1) / kSumCols); }
 
+// Tensor::sum(axis) of a tensor viewed as {pre, d, post} (src/tensor.cpp:421-456): each output [pre][post] is
+// the sum over a = 0..d-1 in order from +0. One thread per output element; combine as sum_rows_kernel.
+__global__ void __launch_bounds__(256) sum_axis_kernel(const float* __restrict__ src, int64_t pre, int64_t d,
+                                                       int64_t post, float* __restrict__ dst, int combine) {
+	const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+	if (idx >= pre * post) return;
+	const int64_t p = idx / post, j = idx - p * post;
+	const float* q = src + p * d * post + j;
+	float s = 0.0f;
+	for (int64_t a = 0; a < d; ++a) s = s + q[a * post];
+	dst[idx] = combine == 0 ? s : combine == 1 ? s + 0.0f : dst[idx] + s;
+}
+
+// add_to_grad (ops.cpp:55-82): a fresh gradient stores src + 0.0f, an existing one adds src.
+__global__ void __launch_bounds__(256) add_to_grad_kernel(float* __restrict__ dst, const float* __restrict__ src,
+                                                          int64_t count, int first) {
+	const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+	if (i >= count) return;
+	dst[i] = first ? src[i] + 0.0f : dst[i] + src[i];
+}
+
 }  // namespace
+
+hipError_t sum_axis(const float* src, int64_t pre, int64_t d, int64_t post, float* dst, int combine, hipStream_t s) {
+	const int64_t total = pre * post;
+	if (total == 0) return hipSuccess;
+	hipLaunchKernelGGL(sum_axis_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, src, pre, d, post, dst,
+	                   combine);
+	return hipGetLastError();
+}
+
+hipError_t add_to_grad(float* dst, const float* src, int64_t count, int first, hipStream_t s) {
+	if (count == 0) return hipSuccess;
+	hipLaunchKernelGGL(add_to_grad_kernel, dim3((unsigned)((count + 255) / 256)), dim3(256), 0, s, dst, src, count,
+	                   first);
+	return hipGetLastError();
+}
 
 hipError_t sum_rows(const float* src, int64_t rows, int64_t inner, float* dst, int combine, hipStream_t s) {
 	if (inner == 0) return hipSuccess;

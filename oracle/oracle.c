@@ -214,6 +214,46 @@ void oracle_relu(const float* x, float* y, size_t count) {
 	for (size_t i = 0; i < count; ++i) y[i] = x[i] > 0.0f ? x[i] : 0.0f;
 }
 
+/* ---- max pooling ---- */
+
+/* maxpool2d forward (ops.cpp:1609-1684): per window, best = -inf and at = 0, then row by row a value replaces
+ * best only when greater; at is the winner's offset inside its (n, c) plane. */
+void oracle_maxpool2d_forward(const float* x, size_t planes, size_t H, size_t W, size_t k, size_t s, float* y,
+		uint32_t* argmax) {
+	const size_t ho = (H - k) / s + 1, wo = (W - k) / s + 1;
+	for (size_t p = 0; p < planes; ++p) {
+		const float* plane = x + p * H * W;
+		for (size_t oh = 0; oh < ho; ++oh)
+			for (size_t ow = 0; ow < wo; ++ow) {
+				float best = -INFINITY;
+				uint32_t at = 0;
+				for (size_t ph = 0; ph < k; ++ph)
+					for (size_t pw = 0; pw < k; ++pw) {
+						const size_t off = (oh * s + ph) * W + ow * s + pw;
+						if (plane[off] > best) {
+							best = plane[off];
+							at = (uint32_t)off;
+						}
+					}
+				y[(p * ho + oh) * wo + ow] = best;
+				argmax[(p * ho + oh) * wo + ow] = at;
+			}
+	}
+}
+
+/* maxpool2d backward (ops.cpp:1686-1704): a fresh plane is zero-filled, then g[i] is added at argmax[i] for i in
+ * output order. */
+void oracle_maxpool2d_backward(const float* g, const uint32_t* argmax, size_t planes, size_t H, size_t W, size_t k,
+		size_t s, float* dx, int first) {
+	const size_t out_plane = ((H - k) / s + 1) * ((W - k) / s + 1);
+	for (size_t p = 0; p < planes; ++p) {
+		float* plane = dx + p * H * W;
+		if (first)
+			for (size_t i = 0; i < H * W; ++i) plane[i] = 0.0f;
+		for (size_t i = p * out_plane; i < (p + 1) * out_plane; ++i) plane[argmax[i]] += g[i];
+	}
+}
+
 /* ---- convolution ---- */
 
 /* conv2d_output_size (ops.cpp:135-139). */

@@ -15,6 +15,7 @@
 #ifndef NNH_ORACLE_H
 #define NNH_ORACLE_H
 #include <stddef.h>
+#include <stdint.h>
 #ifdef __cplusplus
 extern "C" {
 #endif
@@ -43,6 +44,12 @@ void oracle_linear_backward(const float* g, const float* x, const float* w, size
                             const size_t* lead, int nlead, float* dx, int dx_first, float* dw, int dw_first,
                             float* db, int db_first);
 void oracle_relu(const float* x, float* y, size_t count);
+
+/* ---- max pooling (src/autograd/ops.cpp:1609-1705) ---- */
+void oracle_maxpool2d_forward(const float* x, size_t planes, size_t H, size_t W, size_t k, size_t s, float* y,
+                              uint32_t* argmax);
+void oracle_maxpool2d_backward(const float* g, const uint32_t* argmax, size_t planes, size_t H, size_t W, size_t k,
+                               size_t s, float* dx, int first);
 
 /* ---- convolution (src/autograd/ops.cpp:119-243, 1345-1472) ---- */
 void oracle_conv2d_output_size(size_t h, size_t w, size_t kh, size_t kw, size_t stride, size_t padding,

@@ -78,6 +78,9 @@ class Oracle:
         L.oracle_scaled_masked_softmax.argtypes = [_f, _sz, _sz, _sz, _sz, C.c_float, _f, C.c_int, _f]
         L.oracle_attention_f64.argtypes = [_f, _f, _f, _sz, _sz, _sz, _sz, _sz, _f, C.c_int, _d, _d]
         L.oracle_mt19937_uniform.argtypes = [C.c_uint, C.c_float, C.c_float, _f, _sz]
+        _u32 = C.POINTER(C.c_uint32)
+        L.oracle_maxpool2d_forward.argtypes = [_f, _sz, _sz, _sz, _sz, _sz, _f, _u32]
+        L.oracle_maxpool2d_backward.argtypes = [_f, _u32, _sz, _sz, _sz, _sz, _sz, _f, C.c_int]
 
     # -- GEMM --
     def sgemm(self, ta, tb, m, n, k, a, lda, b, ldb, c, ldc, acc, naive=False):
@@ -237,6 +240,26 @@ class Oracle:
                                       _dp(out), _dp(probs))
         return out, probs
 
+    # -- max pooling --
+    def maxpool2d_forward(self, x, k, s):
+        """(y, argmax) of nn::maxpool2d on x {N, C, H, W}."""
+        x = np.ascontiguousarray(x, np.float32)
+        N, Cc, H, W = x.shape
+        ho, wo = (H - k) // s + 1, (W - k) // s + 1
+        y = np.empty((N, Cc, ho, wo), np.float32)
+        arg = np.empty((N, Cc, ho, wo), np.uint32)
+        self.lib.oracle_maxpool2d_forward(_fp(x), N * Cc, H, W, k, s, _fp(y), arg.ctypes.data_as(C.POINTER(C.c_uint32)))
+        return y, arg
+
+    def maxpool2d_backward(self, g, argmax, x_shape, k, s, dx=None, first=True):
+        N, Cc, H, W = x_shape
+        out = np.array(dx, np.float32, copy=True) if dx is not None else np.empty(x_shape, np.float32)
+        g = np.ascontiguousarray(g, np.float32)
+        argmax = np.ascontiguousarray(argmax, np.uint32)
+        self.lib.oracle_maxpool2d_backward(_fp(g), argmax.ctypes.data_as(C.POINTER(C.c_uint32)), N * Cc, H, W, k, s,
+                                           _fp(out), int(first))
+        return out
+
     def mt19937_uniform(self, seed, lo, hi, count):
         out = np.empty(count, np.float32)
         self.lib.oracle_mt19937_uniform(seed, lo, hi, _fp(out), count)
@@ -264,6 +287,20 @@ class Reference:
         L.nnref_attention_forward.argtypes = [_f, _f, _f, _sz, _sz, _sz, _sz, _sz, _f, C.c_int, _f]
         L.nnref_attention_backward.argtypes = [_f, _f, _f, _sz, _sz, _sz, _sz, _sz, _f, C.c_int, _f, _f, _f, _f]
         L.nnref_scaled_masked_softmax.argtypes = [_f, _sz, _sz, _sz, _sz, C.c_float, _f, C.c_int, _f]
+        L.nnref_maxpool2d.argtypes = [_f, _sz, _sz, _sz, _sz, _sz, _sz, _f, _f, _f]
+        L.nnref_time_maxpool2d.argtypes = [_f, _sz, _sz, _sz, _sz, _sz, _sz, _f, C.c_int, C.c_int, C.c_double, _d,
+                                           C.POINTER(C.c_int), _d, _f, _f]
+        L.nnref_matmul_backward.argtypes = [_f, _szp, C.c_int, _f, _szp, C.c_int, C.c_int, _f, C.c_int, _f, _f]
+        _fpp = C.POINTER(_f)
+        timing = [C.c_int, C.c_int, C.c_double, _d]
+        L.nnref_time_matmul.argtypes = [_f, _szp, C.c_int, _f, _szp, C.c_int, C.c_int, C.c_int] + timing + [_f]
+        L.nnref_time_linear_relu_chain.argtypes = [_f, _sz, _szp, C.c_int, _fpp, _fpp] + timing + [_fpp]
+        L.nnref_time_linear_backward_layers.argtypes = [_fpp, _sz, _szp, C.c_int, _fpp, _fpp, _fpp] + timing + \
+            [_fpp, _fpp, _fpp]
+        L.nnref_time_conv2d.argtypes = [_f, _sz, _sz, _sz, _sz, _f, _sz, _sz, _sz, _f, C.c_int, C.c_int, C.c_int, _f] + \
+            timing[:3] + [_d, C.POINTER(C.c_int), _d, _f, _f, _f, _f]
+        L.nnref_time_attention.argtypes = [_f, _f, _f, _sz, _sz, _sz, _sz, C.c_int, _f] + timing[:3] + \
+            [_d, C.POINTER(C.c_int), _d, _f, _f, _f, _f]
 
     def set_threads(self, n):
         self.lib.nnref_set_threads(n)
@@ -357,6 +394,116 @@ class Reference:
         rc = self.lib.nnref_scaled_masked_softmax(_fp(x), N, H, Tq, Tk, scale, _fp(pad), int(causal), _fp(y))
         assert rc == 0, rc
         return y
+
+
+    def matmul_backward(self, a, b, bt, g, repeats=1):
+        """(da, db) of nn::matmul (bt False) or nn::matmul_bt: the backward rule applied `repeats` times (fresh, then
+        added)."""
+        a, b, g = (np.ascontiguousarray(t, np.float32) for t in (a, b, g))
+        da, db = np.empty_like(a), np.empty_like(b)
+        rc = self.lib.nnref_matmul_backward(_fp(a), (C.c_size_t * a.ndim)(*a.shape), a.ndim, _fp(b),
+                                            (C.c_size_t * b.ndim)(*b.shape), b.ndim, int(bt), _fp(g), repeats,
+                                            _fp(da), _fp(db))
+        assert rc == 0, rc
+        return da, db
+
+    def maxpool2d(self, x, k, s, g=None):
+        """nn::maxpool2d's output and, given g, its input gradient (fresh)."""
+        x = np.ascontiguousarray(x, np.float32)
+        N, Cc, H, W = x.shape
+        valid = k > 0 and s > 0 and k <= H and k <= W
+        y = np.empty((N, Cc, (H - k) // s + 1, (W - k) // s + 1) if valid else (1,), np.float32)
+        dx = np.empty_like(x)
+        rc = self.lib.nnref_maxpool2d(_fp(x), N, Cc, H, W, k, s, _fp(y),
+                                      _fp(np.ascontiguousarray(g, np.float32)) if g is not None else None, _fp(dx))
+        if rc != 0:
+            return rc, None, None
+        return 0, y, (dx if g is not None else None)
+
+    # ---- timing (the CPU baseline): nn-cpp's own ops on buffers built once, apps/bench/runner.cpp's method ----
+    # Each returns (times_ms, outputs): the timed runs after `warmup` untimed ones (at least one run, at most
+    # max_runs, stopping once budget_s seconds of runs have passed) and the last run's outputs.
+
+    @staticmethod
+    def _times(buf, n):
+        assert n >= 1, "nn-cpp raised an exception"
+        return [float(buf[i]) for i in range(n)]
+
+    def time_matmul(self, a, b, ta, tb, warmup, max_runs, budget_s):
+        a = np.ascontiguousarray(a, np.float32)
+        b = np.ascontiguousarray(b, np.float32)
+        m = a.shape[-1] if ta else a.shape[-2]
+        n = b.shape[-2] if tb else b.shape[-1]
+        out = np.empty(a.shape[:-2] + (m, n), np.float32)
+        t = np.empty(max_runs, np.float64)
+        ash, bsh = (C.c_size_t * a.ndim)(*a.shape), (C.c_size_t * b.ndim)(*b.shape)
+        cnt = self.lib.nnref_time_matmul(_fp(a), ash, a.ndim, _fp(b), bsh, b.ndim, int(ta), int(tb), warmup, max_runs,
+                                         budget_s, _dp(t), _fp(out))
+        return self._times(t, cnt), out
+
+    @staticmethod
+    def _ptrs(arrs):
+        return (_f * len(arrs))(*[_fp(x) for x in arrs])
+
+    def time_linear_relu_chain(self, x, ws, bs, warmup, max_runs, budget_s):
+        dims = [x.shape[1]] + [w.shape[0] for w in ws]
+        M = x.shape[0]
+        outs = [np.empty((M, d), np.float32) for d in dims[1:]]
+        t = np.empty(max_runs, np.float64)
+        cnt = self.lib.nnref_time_linear_relu_chain(_fp(x), M, (C.c_size_t * len(dims))(*dims), len(ws), self._ptrs(ws),
+                                                    self._ptrs(bs), warmup, max_runs, budget_s, _dp(t), self._ptrs(outs))
+        return self._times(t, cnt), outs
+
+    def time_linear_backward_layers(self, xs, ws, bs, gs, warmup, max_runs, budget_s):
+        dims = [xs[0].shape[1]] + [w.shape[0] for w in ws]
+        M = xs[0].shape[0]
+        dx = [np.empty_like(x) for x in xs]
+        dw = [np.empty_like(w) for w in ws]
+        db = [np.empty_like(b) for b in bs]
+        t = np.empty(max_runs, np.float64)
+        cnt = self.lib.nnref_time_linear_backward_layers(self._ptrs(xs), M, (C.c_size_t * len(dims))(*dims), len(ws),
+                                                         self._ptrs(ws), self._ptrs(bs), self._ptrs(gs), warmup,
+                                                         max_runs, budget_s, _dp(t), self._ptrs(dx), self._ptrs(dw),
+                                                         self._ptrs(db))
+        return self._times(t, cnt), [v for i in range(len(ws)) for v in (dx[i], dw[i], db[i])]
+
+    def time_conv2d(self, x, w, bias, stride, pad, fuse_relu, g, warmup, max_runs, budget_s):
+        """Forward times and output; then, when g is given, the backward rule's times and (dx, dw, db)."""
+        N, Cin, H, W = x.shape
+        Cout, _, kh, kw = w.shape
+        ho, wo = Oracle.conv_out(H, W, kh, kw, stride, pad)
+        y = np.empty((N, Cout, ho, wo), np.float32)
+        dx, dw, db = np.empty_like(x), np.empty_like(w), np.empty_like(bias)
+        tf, tb = np.empty(max_runs, np.float64), np.empty(max_runs, np.float64)
+        nf = C.c_int(0)
+        nb = self.lib.nnref_time_conv2d(_fp(x), N, Cin, H, W, _fp(w), Cout, kh, kw, _fp(bias), stride, pad,
+                                        int(fuse_relu), _fp(g) if g is not None else None, warmup, max_runs, budget_s,
+                                        _dp(tf), C.byref(nf), _dp(tb), _fp(y), _fp(dx), _fp(dw), _fp(db))
+        fwd = (self._times(tf, nf.value), y)
+        bwd = (self._times(tb, nb), (dx, dw, db)) if g is not None else None
+        return fwd, bwd
+
+    def time_maxpool2d(self, x, k, s, g, warmup, max_runs, budget_s):
+        N, Cc, H, W = x.shape
+        y = np.empty((N, Cc, (H - k) // s + 1, (W - k) // s + 1), np.float32)
+        dx = np.empty_like(x)
+        tf, tb = np.empty(max_runs, np.float64), np.empty(max_runs, np.float64)
+        nf = C.c_int(0)
+        nb = self.lib.nnref_time_maxpool2d(_fp(x), N, Cc, H, W, k, s, _fp(g), warmup, max_runs, budget_s, _dp(tf),
+                                           C.byref(nf), _dp(tb), _fp(y), _fp(dx))
+        return (self._times(tf, nf.value), y), (self._times(tb, nb), dx)
+
+    def time_attention(self, q, k, v, heads, causal, g, warmup, max_runs, budget_s):
+        N, T, D = q.shape
+        out, dq, dk, dv = np.empty_like(q), np.empty_like(q), np.empty_like(k), np.empty_like(v)
+        tf, tb = np.empty(max_runs, np.float64), np.empty(max_runs, np.float64)
+        nf = C.c_int(0)
+        nb = self.lib.nnref_time_attention(_fp(q), _fp(k), _fp(v), N, T, D, heads, int(causal),
+                                           _fp(g) if g is not None else None, warmup, max_runs, budget_s, _dp(tf),
+                                           C.byref(nf), _dp(tb), _fp(out), _fp(dq), _fp(dk), _fp(dv))
+        fwd = (self._times(tf, nf.value), out)
+        bwd = (self._times(tb, nb), (dq, dk, dv)) if g is not None else None
+        return fwd, bwd
 
 
 def reference_available():

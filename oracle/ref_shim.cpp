@@ -12,6 +12,7 @@
 #include "nn/kernels/parallel.hpp"
 #include "nn/tensor.hpp"
 
+#include <chrono>
 #include <cstring>
 #include <exception>
 #include <stdexcept>
@@ -53,6 +54,32 @@ int guard(F f) {
 Value probe_loss(const Value& y, const float* g) {
 	Value gv = Value::leaf(make(g, y.data().shape()), false);
 	return nn::sum(nn::mul(y, gv));
+}
+
+using Clock = std::chrono::steady_clock;
+
+// apps/bench/runner.cpp's method: `warmup` untimed calls, then timed calls (steady_clock, milliseconds) until
+// max_runs of them or budget_s seconds of them, at least one. Returns the number of timed runs.
+template <typename F>
+int time_runs(F fn, int warmup, int max_runs, double budget_s, double* times) {
+	for (int i = 0; i < warmup; ++i) fn();
+	int n = 0;
+	const auto start = Clock::now();
+	while (n < max_runs) {
+		const auto t0 = Clock::now();
+		fn();
+		const auto t1 = Clock::now();
+		times[n++] = std::chrono::duration<double, std::milli>(t1 - t0).count();
+		if (std::chrono::duration<double>(t1 - start).count() >= budget_s) break;
+	}
+	return n;
+}
+
+// The backward rule of node y alone (what Value::backward runs for it), with every leaf's gradient fresh, as a
+// call with *_first set on the GPU side: the rule overwrites instead of adding.
+void run_backward_rule(const Value& y, const Tensor& g, std::initializer_list<const Value*> leaves) {
+	for (const Value* v : leaves) v->impl()->grad_fresh = true;
+	y.impl()->backward_fn(g);
 }
 
 }  // namespace
@@ -168,6 +195,186 @@ int nnref_attention_backward(const float* q, const float* k, const float* v, siz
 		put(kv.grad(), dk);
 		put(vv.grad(), dv);
 	});
+}
+
+// nn::maxpool2d (ops.cpp:1609-1705) on {N, C, H, W}: the forward output, then (when g is not null) the input
+// gradient for upstream gradient g, through the op's own backward rule with a fresh gradient.
+int nnref_maxpool2d(const float* x, size_t N, size_t C, size_t H, size_t W, size_t kernel, size_t stride, float* y,
+		const float* g, float* dx) {
+	return guard([&] {
+		const Value xv = Value::leaf(make(x, {N, C, H, W}), true);
+		const Value r = nn::maxpool2d(xv, kernel, stride);
+		put(r.data(), y);
+		if (g) {
+			run_backward_rule(r, make(g, r.data().shape()), {&xv});
+			put(xv.grad(), dx);
+		}
+	});
+}
+
+// The backward rule of nn::matmul(a, b) (bt = 0) or nn::matmul_bt(a, b) (bt = 1) for upstream gradient g, applied
+// `repeats` times: first into fresh gradients, then added (ops.cpp:683-712, 747-773). da, db receive the gradients.
+int nnref_matmul_backward(const float* a, const size_t* as, int an, const float* b, const size_t* bs, int bn, int bt,
+		const float* g, int repeats, float* da, float* db) {
+	return guard([&] {
+		const Value av = Value::leaf(make(a, shape_of(as, an)), true), bv = Value::leaf(make(b, shape_of(bs, bn)), true);
+		const Value r = bt ? nn::matmul_bt(av, bv) : nn::matmul(av, bv);
+		const Tensor gt = make(g, r.data().shape());
+		run_backward_rule(r, gt, {&av, &bv});
+		for (int i = 1; i < repeats; ++i) r.impl()->backward_fn(gt);
+		put(av.grad(), da);
+		put(bv.grad(), db);
+	});
+}
+
+// ---- timing (the CPU baseline): each returns the number of timed runs, or -1 on an exception ----
+
+// nn::matmul(a, b, ta, tb) (src/tensor.cpp:571-641) on Tensors built once, as run_matmul (runner.cpp:80-96);
+// out receives the last result.
+int nnref_time_matmul(const float* a, const size_t* as, int an, const float* b, const size_t* bs, int bn, int ta,
+		int tb, int warmup, int max_runs, double budget_s, double* times, float* out) {
+	int runs = -1;
+	guard([&] {
+		const Tensor A = make(a, shape_of(as, an)), B = make(b, shape_of(bs, bn));
+		Tensor r = Tensor::empty({0});
+		runs = time_runs([&] { r = nn::matmul(A, B, ta != 0, tb != 0); }, warmup, max_runs, budget_s, times);
+		put(r, out);
+	});
+	return runs;
+}
+
+// A chain of `layers` nn::linear + nn::relu (ops.cpp:714-793) without a graph, x {M, dims[0]}, w[i] {dims[i+1],
+// dims[i]}, b[i] {dims[i+1]}; outs[i] receives layer i's activation.
+int nnref_time_linear_relu_chain(const float* x, size_t M, const size_t* dims, int layers, const float* const* w,
+		const float* const* b, int warmup, int max_runs, double budget_s, double* times, float* const* outs) {
+	int runs = -1;
+	guard([&] {
+		nn::NoGradGuard ng;
+		const Value xv = Value::leaf(make(x, {M, dims[0]}));
+		std::vector<Value> wv, bv, hs(layers, Value::leaf(Tensor::empty({0})));
+		for (int i = 0; i < layers; ++i) {
+			wv.push_back(Value::leaf(make(w[i], {dims[i + 1], dims[i]})));
+			bv.push_back(Value::leaf(make(b[i], {dims[i + 1]})));
+		}
+		runs = time_runs([&] {
+			Value h = xv;
+			for (int i = 0; i < layers; ++i) hs[i] = h = nn::relu(nn::linear(h, wv[i], bv[i]));
+		}, warmup, max_runs, budget_s, times);
+		for (int i = 0; i < layers; ++i) put(hs[i].data(), outs[i]);
+	});
+	return runs;
+}
+
+// The backward rules of `layers` independent nn::linear nodes (ops.cpp:731-744): layer i has input x[i] {M, dims[i]},
+// weight w[i] {dims[i+1], dims[i]}, bias b[i] and upstream gradient g[i] {M, dims[i+1]}; fresh leaf gradients.
+// dx[i], dw[i], db[i] receive the last run's gradients.
+int nnref_time_linear_backward_layers(const float* const* x, size_t M, const size_t* dims, int layers,
+		const float* const* w, const float* const* b, const float* const* g, int warmup, int max_runs,
+		double budget_s, double* times, float* const* dx, float* const* dw, float* const* db) {
+	int runs = -1;
+	guard([&] {
+		std::vector<Value> xv, wv, bv, ys;
+		std::vector<Tensor> gs;
+		for (int i = 0; i < layers; ++i) {
+			xv.push_back(Value::leaf(make(x[i], {M, dims[i]}), true));
+			wv.push_back(Value::leaf(make(w[i], {dims[i + 1], dims[i]}), true));
+			bv.push_back(Value::leaf(make(b[i], {dims[i + 1]}), true));
+			ys.push_back(nn::linear(xv[i], wv[i], bv[i]));
+			gs.push_back(make(g[i], {M, dims[i + 1]}));
+		}
+		runs = time_runs([&] {
+			for (int i = 0; i < layers; ++i) run_backward_rule(ys[i], gs[i], {&xv[i], &wv[i], &bv[i]});
+		}, warmup, max_runs, budget_s, times);
+		for (int i = 0; i < layers; ++i) {
+			put(xv[i].grad(), dx[i]);
+			put(wv[i].grad(), dw[i]);
+			put(bv[i].grad(), db[i]);
+		}
+	});
+	return runs;
+}
+
+// nn::conv2d_relu / nn::conv2d (ops.cpp:1345-1472): the forward without a graph (times_fwd, y), then the node's
+// backward rule for upstream gradient g with fresh leaf gradients (times_bwd, dx, dw, db).
+int nnref_time_conv2d(const float* x, size_t N, size_t Cin, size_t H, size_t W, const float* w, size_t Cout,
+		size_t kh, size_t kw, const float* bias, int stride, int padding, int fuse_relu, const float* g, int warmup,
+		int max_runs, double budget_s, double* times_fwd, int* runs_fwd, double* times_bwd, float* y, float* dx,
+		float* dw, float* db) {
+	int runs = -1;
+	guard([&] {
+		const Value xv = Value::leaf(make(x, {N, Cin, H, W}), true), wv = Value::leaf(make(w, {Cout, Cin, kh, kw}), true);
+		const Value bv = Value::leaf(make(bias, {Cout}), true);
+		auto op = [&] { return fuse_relu ? nn::conv2d_relu(xv, wv, bv, stride, padding) : nn::conv2d(xv, wv, bv, stride, padding); };
+		{
+			nn::NoGradGuard ng;
+			Value r = Value::leaf(Tensor::empty({0}));
+			*runs_fwd = time_runs([&] { r = op(); }, warmup, max_runs, budget_s, times_fwd);
+			put(r.data(), y);
+		}
+		if (!g) {
+			runs = 0;
+			return;
+		}
+		const Value r = op();
+		const Tensor gt = make(g, r.data().shape());
+		runs = time_runs([&] { run_backward_rule(r, gt, {&xv, &wv, &bv}); }, warmup, max_runs, budget_s, times_bwd);
+		put(xv.grad(), dx);
+		put(wv.grad(), dw);
+		put(bv.grad(), db);
+	});
+	return runs;
+}
+
+// nn::attention (ops.cpp:1226-1296) without a key padding mask: the forward without a graph, then the node's
+// backward rule for g (when g is not null), as nnref_time_conv2d.
+int nnref_time_attention(const float* q, const float* k, const float* v, size_t N, size_t T, size_t D, size_t heads,
+		int causal, const float* g, int warmup, int max_runs, double budget_s, double* times_fwd, int* runs_fwd,
+		double* times_bwd, float* out, float* dq, float* dk, float* dv) {
+	int runs = -1;
+	guard([&] {
+		const Value qv = Value::leaf(make(q, {N, T, D}), true), kv = Value::leaf(make(k, {N, T, D}), true);
+		const Value vv = Value::leaf(make(v, {N, T, D}), true);
+		const Tensor none = Tensor::empty({0});
+		{
+			nn::NoGradGuard ng;
+			Value r = Value::leaf(Tensor::empty({0}));
+			*runs_fwd = time_runs([&] { r = nn::attention(qv, kv, vv, heads, none, causal != 0); }, warmup, max_runs,
+				budget_s, times_fwd);
+			put(r.data(), out);
+		}
+		if (!g) {
+			runs = 0;
+			return;
+		}
+		const Value r = nn::attention(qv, kv, vv, heads, none, causal != 0);
+		const Tensor gt = make(g, {N, T, D});
+		runs = time_runs([&] { run_backward_rule(r, gt, {&qv, &kv, &vv}); }, warmup, max_runs, budget_s, times_bwd);
+		put(qv.grad(), dq);
+		put(kv.grad(), dk);
+		put(vv.grad(), dv);
+	});
+	return runs;
+}
+
+// nn::maxpool2d (ops.cpp:1609-1705): the forward without a graph, then the node's backward rule for g.
+int nnref_time_maxpool2d(const float* x, size_t N, size_t C, size_t H, size_t W, size_t kernel, size_t stride,
+		const float* g, int warmup, int max_runs, double budget_s, double* times_fwd, int* runs_fwd, double* times_bwd,
+		float* y, float* dx) {
+	int runs = -1;
+	guard([&] {
+		const Value xv = Value::leaf(make(x, {N, C, H, W}), true);
+		{
+			nn::NoGradGuard ng;
+			Value r = Value::leaf(Tensor::empty({0}));
+			*runs_fwd = time_runs([&] { r = nn::maxpool2d(xv, kernel, stride); }, warmup, max_runs, budget_s, times_fwd);
+			put(r.data(), y);
+		}
+		const Value r = nn::maxpool2d(xv, kernel, stride);
+		const Tensor gt = make(g, r.data().shape());
+		runs = time_runs([&] { run_backward_rule(r, gt, {&xv}); }, warmup, max_runs, budget_s, times_bwd);
+		put(xv.grad(), dx);
+	});
+	return runs;
 }
 
 }  // extern "C"

@@ -111,3 +111,29 @@ def attention_inputs(spec):
     mask = np.ascontiguousarray(PAD_MASKS[Tk][:N]) if padded else None
     return (np.ascontiguousarray(q), np.ascontiguousarray(k), np.ascontiguousarray(v), heads, mask, causal,
             np.ascontiguousarray(g))
+
+
+# name, (N, C, H, W, kernel, stride, seed, specials): specials quantises the input to quarters (ties), fills one
+# window with -inf (nothing beats the start value: offset 0 keeps the gradient), one with NaN and plants a NaN
+# among ordinary values
+POOL_CASES = [
+    ("k2s2_2x3x8x8", (2, 3, 8, 8, 2, 2, 61, 0)),
+    ("k3s2_overlap_1x2x9x7_specials", (1, 2, 9, 7, 3, 2, 62, 1)),
+    ("k3s1_overlap_1x1x6x6_specials", (1, 1, 6, 6, 3, 1, 63, 1)),
+    ("k2s1_ties_1x2x5x5_specials", (1, 2, 5, 5, 2, 1, 64, 1)),
+    ("k2s2_odd_2x2x7x9", (2, 2, 7, 9, 2, 2, 65, 0)),
+    ("k2s2_specials_2x2x6x6", (2, 2, 6, 6, 2, 2, 66, 1)),
+]
+
+
+def pool_inputs(spec):
+    N, C, H, W, k, s, seed, specials = spec
+    ho, wo = (H - k) // s + 1, (W - k) // s + 1
+    x, g = synth.uniform_operands(seed, [(N, C, H, W), (N, C, ho, wo)])
+    x = np.array(x, copy=True)
+    if specials:
+        x = (np.round(x * 4) / 4).astype(np.float32)
+        x[0, 0, H - k:H, W - k:W] = -np.inf                      # the last window: nothing above -inf
+        x[-1, -1, 0:k, 0:k] = np.nan                             # the first window of the last plane: all NaN
+        x[0, -1, H // 2, W // 2] = np.nan                        # a NaN among ordinary values
+    return np.ascontiguousarray(x), np.ascontiguousarray(g), k, s

@@ -18,8 +18,8 @@ sys.path.insert(0, os.path.join(ROOT, "nn-cpp_amd"))
 sys.path.insert(0, os.path.join(ROOT, "oracle"))
 sys.path.insert(0, HERE)
 
-from golden_cases import (ATTENTION_CASES, CONV_CASES, LINEAR_CASES, MATMUL_CASES, SGEMM_CASES,  # noqa: E402
-                          attention_inputs, conv_inputs, linear_inputs, matmul_inputs, sgemm_inputs)
+from golden_cases import (ATTENTION_CASES, CONV_CASES, LINEAR_CASES, MATMUL_CASES, POOL_CASES, SGEMM_CASES,  # noqa: E402
+                          attention_inputs, conv_inputs, linear_inputs, matmul_inputs, pool_inputs, sgemm_inputs)
 from pyoracle import Reference  # noqa: E402
 
 
@@ -51,6 +51,11 @@ def main():
         out[f"attention/{name}/out"] = ref.attention_forward(q, k, v, heads, mask, causal)
         dq, dk, dv = ref.attention_backward(q, k, v, heads, g, mask, causal)
         out[f"attention/{name}/dq"], out[f"attention/{name}/dk"], out[f"attention/{name}/dv"] = dq, dk, dv
+    for name, spec in POOL_CASES:
+        x, g, k, s = pool_inputs(spec)
+        rc, y, dx = ref.maxpool2d(x, k, s, g)
+        assert rc == 0, name
+        out[f"pool/{name}/y"], out[f"pool/{name}/dx"] = y, dx
     path = os.path.join(HERE, "reference_vectors.npz")
     np.savez_compressed(path, **out)
     print(f"wrote {len(out)} arrays to {path} ({os.path.getsize(path)} bytes)")

@@ -361,3 +361,58 @@ def test_expf_restatement_equals_glibc_expf(tmp_path):
                    check=True)
     out = subprocess.run([exe, "61"], capture_output=True, text=True, timeout=300)
     assert out.returncode == 0 and out.stdout.strip().endswith(" 0 differ"), out.stdout + out.stderr
+
+
+# ---------------------------------------------------------------- max pooling (ops.cpp:1609-1705)
+
+def test_golden_maxpool(oracle):
+    """The oracle's forward and its scatter backward against nn-cpp's outputs (golden vectors), NaN, -inf windows,
+    ties and overlapping windows included; NaN compares equal to NaN."""
+    cases, gold = golden()
+    for name, spec in cases.POOL_CASES:
+        x, g, k, s = cases.pool_inputs(spec)
+        y, arg = oracle.maxpool2d_forward(x, k, s)
+        dx = oracle.maxpool2d_backward(g, arg, x.shape, k, s)
+        want_y, want_dx = gold[f"pool/{name}/y"], gold[f"pool/{name}/dx"]
+        assert np.array_equal(y, want_y, equal_nan=True) and y.tobytes() == want_y.tobytes(), name
+        assert dx.tobytes() == want_dx.tobytes(), name
+
+
+def test_maxpool_matches_nncpp(oracle, ref):
+    """Against nn-cpp's compiled maxpool2d on larger random planes (config 3's 2 x 2 pooling and an overlapping
+    window), with ties from quantised values."""
+    for (N, C, H, W, k, s, seed) in ((4, 8, 28, 28, 2, 2, 71), (2, 3, 13, 11, 3, 2, 72), (1, 2, 10, 10, 4, 3, 73)):
+        x, g = synth.uniform_operands(seed, [(N, C, H, W), (N, C, (H - k) // s + 1, (W - k) // s + 1)])
+        x = (np.round(x * 8) / 8).astype(np.float32)
+        y, arg = oracle.maxpool2d_forward(x, k, s)
+        rc, ry, rdx = ref.maxpool2d(x, k, s, g)
+        assert rc == 0
+        assert y.tobytes() == ry.tobytes()
+        assert oracle.maxpool2d_backward(g, arg, x.shape, k, s).tobytes() == rdx.tobytes()
+    # the reference's shape errors: kernel larger than the plane, zero kernel or stride
+    x = np.zeros((1, 1, 3, 3), np.float32)
+    assert ref.maxpool2d(x, 4, 1)[0] == 2 and ref.maxpool2d(x, 0, 1)[0] == 2 and ref.maxpool2d(x, 2, 0)[0] == 2
+
+
+def test_maxpool_hand_values(oracle):
+    """Worked by hand: the first maximum of a window wins a tie; a window of -inf keeps -inf and offset 0, so its
+    gradient lands on the plane's first element; NaN never wins; overlapping windows add in output order."""
+    x = np.array([[[[1, 3, 3, 0],
+                    [2, 3, 0, 5],
+                    [-np.inf, -np.inf, np.nan, 4],
+                    [-np.inf, -np.inf, 4, np.nan]]]], np.float32)
+    y, arg = oracle.maxpool2d_forward(x, 2, 2)
+    assert y.ravel().tolist() == [3, 5, -np.inf, 4]
+    assert arg.ravel().tolist() == [1, 7, 0, 11]   # (0,1) wins the tie with (1,1); NaNs skipped
+    g = np.array([10, 20, 30, 40], np.float32).reshape(1, 1, 2, 2)
+    dx = oracle.maxpool2d_backward(g, arg, x.shape, 2, 2)
+    want = np.zeros((4, 4), np.float32)
+    want[0, 0], want[0, 1], want[1, 3], want[2, 3] = 30, 10, 20, 40
+    assert dx.reshape(4, 4).tolist() == want.tolist()
+    # overlapping 2 x 2 windows at stride 1 on a 1 x 3 ramp-down row pair: both windows pick x[0, 0] ... x[.., 1]
+    x = np.array([[[[5, 4, 1], [0, 0, 0]]]], np.float32)
+    y, arg = oracle.maxpool2d_forward(x, 2, 1)
+    assert y.ravel().tolist() == [5, 4] and arg.ravel().tolist() == [0, 1]
+    dx = oracle.maxpool2d_backward(np.array([[[[1.5, 2.5]]]], np.float32), arg, x.shape, 2, 1, dx=np.ones_like(x),
+                                   first=False)
+    assert dx.ravel().tolist() == [2.5, 3.5, 1, 1, 1, 1]
