@@ -5,8 +5,8 @@
 // offset 0 of the plane). The argmax is that offset inside the (n, c) plane, as the reference keeps it for backward.
 // Backward: the reference zero-fills a fresh plane and adds g[i] at argmax[i] for i in output order. Here each
 // input element gathers instead, visiting the windows that contain it in output order (no atomics, one writer per
-// element). Offset 0 of a plane also receives the windows that kept offset 0 without containing it, so its thread
-// walks every output of the plane in order.
+// element). Offset 0 of a plane also receives the windows that kept offset 0 without containing it; when a plane
+// has such windows its thread walks every output of the plane in order.
 #include "pool.hpp"
 
 #include <cmath>
@@ -84,39 +84,49 @@ struct PoolBwdArgs {
 	const float* g;
 	const uint32_t* arg;
 	float* dx;
-	int64_t total;  // input elements
 	int h, w, ho, wo, k, s, first;
-	FastDiv plane_in, w_div, s_div;
+	FastDiv w_div, s_div;
 };
 
-// One input element per thread: the windows containing it, in output order (ops.cpp:1693-1700).
+// One (n, c) plane per workgroup (ops.cpp:1686-1704). Only the first window contains offset 0, so a later window
+// whose argmax is 0 is one where nothing beat -inf; the threads look for such windows together first. Each input
+// element then adds, in output order, g of the windows that contain it and picked it; offset 0 walks every output
+// of the plane in order when such windows exist.
 __global__ void __launch_bounds__(256) maxpool_backward_kernel(const PoolBwdArgs a) {
-	const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
-	if (idx >= a.total) return;
-	const int64_t hw = (int64_t)a.h * a.w;
-	const int64_t p = idx / hw;
-	const int e = (int)(idx - p * hw);
-	const int out_plane = a.ho * a.wo;
+	__shared__ int empty_windows;
+	const int tid = threadIdx.x;
+	const int64_t p = blockIdx.x;
+	const int hw = a.h * a.w, out_plane = a.ho * a.wo;
 	const float* g = a.g + p * out_plane;
 	const uint32_t* arg = a.arg + p * out_plane;
-	float v = a.first ? 0.0f : a.dx[idx];
-	if (e == 0) {
-		for (int i = 0; i < out_plane; ++i)
-			if (arg[i] == 0u) v = v + g[i];
-	} else {
-		const int ih = (int)fdiv((unsigned)e, a.w_div), iw = e - ih * a.w;
-		// windows oh with oh*s <= ih <= oh*s + k - 1, oh < ho (and the same across)
-		const int oh_lo = ih >= a.k ? (int)fdiv((unsigned)(ih - a.k), a.s_div) + 1 : 0;
-		const int oh_hi = min((int)fdiv((unsigned)ih, a.s_div), a.ho - 1);
-		const int ow_lo = iw >= a.k ? (int)fdiv((unsigned)(iw - a.k), a.s_div) + 1 : 0;
-		const int ow_hi = min((int)fdiv((unsigned)iw, a.s_div), a.wo - 1);
-		for (int oh = oh_lo; oh <= oh_hi; ++oh)
-			for (int ow = ow_lo; ow <= ow_hi; ++ow) {
-				const int i = oh * a.wo + ow;
-				if (arg[i] == (uint32_t)e) v = v + g[i];
-			}
+	float* dx = a.dx + p * hw;
+	if (tid == 0) empty_windows = 0;
+	__syncthreads();
+	bool found = false;
+	for (int i = tid + 1; i < out_plane; i += 256) found = found || arg[i] == 0u;
+	if (found) empty_windows = 1;  // every writer stores the same value
+	__syncthreads();
+	const bool scan0 = empty_windows != 0;
+	for (int e = tid; e < hw; e += 256) {
+		float v = a.first ? 0.0f : dx[e];
+		if (e == 0 && scan0) {
+			for (int i = 0; i < out_plane; ++i)
+				if (arg[i] == 0u) v = v + g[i];
+		} else {
+			const int ih = (int)fdiv((unsigned)e, a.w_div), iw = e - ih * a.w;
+			// windows oh with oh*s <= ih <= oh*s + k - 1, oh < ho (and the same across)
+			const int oh_lo = ih >= a.k ? (int)fdiv((unsigned)(ih - a.k), a.s_div) + 1 : 0;
+			const int oh_hi = min((int)fdiv((unsigned)ih, a.s_div), a.ho - 1);
+			const int ow_lo = iw >= a.k ? (int)fdiv((unsigned)(iw - a.k), a.s_div) + 1 : 0;
+			const int ow_hi = min((int)fdiv((unsigned)iw, a.s_div), a.wo - 1);
+			for (int oh = oh_lo; oh <= oh_hi; ++oh)
+				for (int ow = ow_lo; ow <= ow_hi; ++ow) {
+					const int i = oh * a.wo + ow;
+					if (arg[i] == (uint32_t)e) v = v + g[i];
+				}
+		}
+		dx[e] = v;
 	}
-	a.dx[idx] = v;
 }
 
 }  // namespace
@@ -160,11 +170,11 @@ hipError_t maxpool2d_backward(const float* g, const uint32_t* arg, float* dx, in
 	a.first = first;
 	a.ho = (h - k) / s + 1;
 	a.wo = (w - k) / s + 1;
-	a.total = planes * h * w;
 	a.w_div = make_fastdiv((unsigned)w);
 	a.s_div = make_fastdiv((unsigned)s);
-	if (a.total == 0) return hipSuccess;
-	hipLaunchKernelGGL(maxpool_backward_kernel, dim3((unsigned)((a.total + 255) / 256)), dim3(256), 0, st, a);
+	if (planes == 0 || (int64_t)h * w == 0) return hipSuccess;
+	if (planes > 0x7fffffff) return hipErrorInvalidConfiguration;
+	hipLaunchKernelGGL(maxpool_backward_kernel, dim3((unsigned)planes), dim3(256), 0, st, a);
 	return hipGetLastError();
 }
 

@@ -399,13 +399,15 @@ class Reference:
     def matmul_backward(self, a, b, bt, g, repeats=1):
         """(da, db) of nn::matmul (bt False) or nn::matmul_bt: the backward rule applied `repeats` times (fresh, then
         added)."""
+        same = b is None
+        b = a if same else b
         a, b, g = (np.ascontiguousarray(t, np.float32) for t in (a, b, g))
         da, db = np.empty_like(a), np.empty_like(b)
-        rc = self.lib.nnref_matmul_backward(_fp(a), (C.c_size_t * a.ndim)(*a.shape), a.ndim, _fp(b),
+        rc = self.lib.nnref_matmul_backward(_fp(a), (C.c_size_t * a.ndim)(*a.shape), a.ndim, None if same else _fp(b),
                                             (C.c_size_t * b.ndim)(*b.shape), b.ndim, int(bt), _fp(g), repeats,
                                             _fp(da), _fp(db))
         assert rc == 0, rc
-        return da, db
+        return (da, None) if same else (da, db)
 
     def maxpool2d(self, x, k, s, g=None):
         """nn::maxpool2d's output and, given g, its input gradient (fresh)."""

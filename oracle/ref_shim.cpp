@@ -217,13 +217,15 @@ int nnref_maxpool2d(const float* x, size_t N, size_t C, size_t H, size_t W, size
 int nnref_matmul_backward(const float* a, const size_t* as, int an, const float* b, const size_t* bs, int bn, int bt,
 		const float* g, int repeats, float* da, float* db) {
 	return guard([&] {
-		const Value av = Value::leaf(make(a, shape_of(as, an)), true), bv = Value::leaf(make(b, shape_of(bs, bn)), true);
+		// b null: the second operand is a itself (one node, both gradients into one buffer, written to da)
+		const Value av = Value::leaf(make(a, shape_of(as, an)), true);
+		const Value bv = b ? Value::leaf(make(b, shape_of(bs, bn)), true) : av;
 		const Value r = bt ? nn::matmul_bt(av, bv) : nn::matmul(av, bv);
 		const Tensor gt = make(g, r.data().shape());
 		run_backward_rule(r, gt, {&av, &bv});
 		for (int i = 1; i < repeats; ++i) r.impl()->backward_fn(gt);
 		put(av.grad(), da);
-		put(bv.grad(), db);
+		if (b) put(bv.grad(), db);
 	});
 }
 
