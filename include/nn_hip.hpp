@@ -1,0 +1,149 @@
+// nn_hip.hpp - nn-cpp's op surface on an MI355X, with device-resident tensors (C++17; lib/libnn_hip.so).
+//
+// The names, argument meanings, shape rules and exceptions follow nn-cpp 2.0.0's own API so that code written
+// against it reads the same:
+//   * Tensor and matmul(a, b, trans_a, trans_b)                  include/nn/tensor.hpp:47-510, 465-491
+//   * Value, NoGradGuard, grad_accum and backward                include/nn/autograd/value.hpp:41-228
+//   * matmul, linear, matmul_bt, relu, reshape, conv2d, conv2d_relu, maxpool2d, attention, scaled_masked_softmax
+//                                                                include/nn/autograd/ops.hpp:22-523
+// The difference is where the numbers live: a Tensor's storage is HBM, so a chain of ops (linear -> relu ->
+// linear, conv -> pool -> conv) never leaves the device; data crosses PCIe only in from_host / to_host. Every op
+// runs the C ABI of include/nnh.h and gives the bits nn-cpp's NN_NATIVE CPU build gives on the same inputs,
+// gradients included (each backward rule takes its gradient buffers in the reference's order and passes the
+// first-write flags of grad_accum).
+//
+// Work is enqueued on one stream (set_stream; default the null stream). Device memory comes from a caching
+// allocator: a Tensor's storage returns to it when the last Tensor sharing it is destroyed and is reused by later
+// work on the same stream, which stream order makes safe.
+// Errors: TensorShapeError where nn-cpp throws it (nnh's NNH_ERR_SHAPE), std::invalid_argument for other
+// invalid arguments, HipError for runtime failures.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <functional>
+#include <memory>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+namespace nn {
+namespace hip {
+
+class TensorShapeError : public std::runtime_error {
+public:
+	TensorShapeError() : std::runtime_error("nn::hip: tensor shape mismatch") {}
+	explicit TensorShapeError(const std::string& m) : std::runtime_error(m) {}
+};
+
+class HipError : public std::runtime_error {
+public:
+	explicit HipError(const std::string& m) : std::runtime_error(m) {}
+};
+
+// The stream every op enqueues on (setting another first waits for the current one).
+void set_stream(hipStream_t s);
+hipStream_t current_stream();
+void synchronize();
+// Device bytes the allocator holds (in use and cached), and a release of the cached ones.
+size_t allocator_bytes();
+void empty_cache();
+
+struct Block;  // a device allocation of the caching allocator
+
+// A row-major, contiguous fp32 tensor in HBM (tensor.hpp:90-413, device storage).
+class Tensor {
+public:
+	Tensor();                                                  // shape {0}
+	explicit Tensor(std::vector<size_t> shape, float value = 0.0f);  // filled with value
+	static Tensor empty(std::vector<size_t> shape);            // uninitialised (Tensor::empty, tensor.cpp:263)
+	static Tensor from_host(std::vector<size_t> shape, const float* data);
+	void to_host(float* out) const;
+	std::vector<float> to_host() const;
+
+	const std::vector<size_t>& shape() const { return shape_; }
+	size_t ndim() const { return shape_.size(); }
+	size_t size() const { return size_; }
+	float* data() const;                                       // device pointer
+	Tensor reshape(std::vector<size_t> new_shape) const;       // shares the storage
+	void zero_();
+	void fill_(float value);
+
+private:
+	std::shared_ptr<Block> storage_;
+	std::vector<size_t> shape_;
+	size_t size_ = 0;
+};
+
+// nn::matmul(a, b, trans_a, trans_b) (tensor.cpp:571-641): batched, broadcast, 2-D right operand folded.
+Tensor matmul(const Tensor& a, const Tensor& b, bool trans_a = false, bool trans_b = false);
+
+class Value;
+
+// Graph node state (value.hpp:60-84).
+struct NodeImpl {
+	Tensor data;
+	Tensor grad;
+	bool grad_fresh = false;
+	bool requires_grad = false;
+	std::vector<Value> parents;
+	std::function<void(const Tensor&)> backward_fn;
+};
+
+// Reference-counted handle to a graph node (value.hpp:86-228).
+class Value {
+public:
+	Value() = default;
+	static Value leaf(Tensor data, bool requires_grad = false);
+	static Value node(Tensor data, std::vector<Value> parents, std::function<void(const Tensor&)> backward_fn);
+	Tensor& data() const;
+	Tensor& grad() const;                     // a fresh gradient is zeroed on first read
+	Tensor& grad_accum(bool& first) const;    // value.cpp:60-64: first = the buffer holds nothing yet
+	bool requires_grad() const;
+	void zero_grad() const;
+	// Value::backward (value.cpp:80-132) for a one-element value; the overload seeds the output gradient with
+	// `seed` (the output's shape) instead of ones, for a graph whose loss is formed elsewhere.
+	void backward() const;
+	void backward(const Tensor& seed) const;
+	NodeImpl* impl() const { return impl_.get(); }
+
+private:
+	explicit Value(std::shared_ptr<NodeImpl> impl) : impl_(std::move(impl)) {}
+	std::shared_ptr<NodeImpl> impl_;
+};
+
+// Ops record no graph while one is alive on the thread (value.hpp:24-40).
+class NoGradGuard {
+public:
+	NoGradGuard();
+	~NoGradGuard();
+	NoGradGuard(const NoGradGuard&) = delete;
+	NoGradGuard& operator=(const NoGradGuard&) = delete;
+	static bool grad_enabled();
+
+private:
+	bool previous_;
+};
+
+// ops.hpp:289 / 337: differentiable matmul and matmul against a transposed right operand.
+Value matmul(const Value& a, const Value& b);
+Value matmul_bt(const Value& a, const Value& b);
+// ops.hpp:304: x W^T + b, x {..., K}, weight {N, K}, bias {N}.
+Value linear(const Value& x, const Value& weight, const Value& bias);
+Value relu(const Value& x);
+// ops.cpp:672-681: same elements, new shape (the Flatten module's op).
+Value reshape(const Value& x, std::vector<size_t> new_shape);
+// ops.hpp:392 / 402: 2-D convolution (x {N, Cin, H, W}, weight {Cout, Cin, kH, kW}, bias {Cout}), and with ReLU.
+Value conv2d(const Value& x, const Value& weight, const Value& bias, int stride, int padding);
+Value conv2d_relu(const Value& x, const Value& weight, const Value& bias, int stride, int padding);
+// ops.cpp:1609-1705: max pooling, kernel x kernel windows at `stride`.
+Value maxpool2d(const Value& x, size_t kernel_size, size_t stride);
+// ops.hpp:324: multi-head attention core; key_padding_mask {N, Tk} (0 = padded) or empty.
+Value attention(const Value& q, const Value& k, const Value& v, size_t heads, const Tensor& key_padding_mask,
+                bool causal);
+// ops.cpp:1298-1343: softmax over the last axis of {N, H, Tq, Tk} after scaling and masking.
+Value scaled_masked_softmax(const Value& x, float scale_by, const Tensor& key_padding_mask, bool causal);
+
+}  // namespace hip
+}  // namespace nn

@@ -173,6 +173,10 @@ int nnh_relu_forward(const float* x, float* y, size_t count, void* stream);
  * x may be the forward output instead of its input (y > 0 exactly where x > 0). */
 int nnh_relu_backward(const float* x, const float* g, float* dx, int first, size_t count, void* stream);
 
+/* add_to_grad (src/autograd/ops.cpp:55-82, value.cpp:60-64): a fresh gradient (first) stores src + 0.0f, an
+ * existing one adds src, element by element. The first-write rule every backward pass uses; reshape's backward. */
+int nnh_add_to_grad(float* dst, const float* src, size_t count, int first, void* stream);
+
 /* Tensor::sum(0) of a {rows, inner} tensor (src/tensor.cpp:422-456): s_j = sum of src[a][j] over a in order,
  * from +0. combine 0: dst = s; 1: dst = s + 0.0f (a fresh gradient); 2: dst += s. */
 int nnh_tensor_sum0(const float* src, size_t rows, size_t inner, float* dst, int combine, void* stream);

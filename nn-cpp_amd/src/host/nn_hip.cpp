@@ -1,0 +1,453 @@
+// nn_hip.cpp - include/nn_hip.hpp: nn-cpp's op surface over device-resident tensors, on the C ABI of include/nnh.h.
+#include "nn_hip.hpp"
+
+#include <algorithm>
+#include <cmath>
+#include <map>
+#include <mutex>
+#include <unordered_set>
+
+#include "nnh.h"
+
+namespace nn {
+namespace hip {
+
+namespace {
+
+hipStream_t g_stream = nullptr;
+
+void check(int rc) {
+	if (rc == NNH_OK) return;
+	const std::string msg = std::string("nn::hip: ") + nnh_last_error();
+	if (rc == NNH_ERR_SHAPE) throw TensorShapeError(msg);
+	if (rc == NNH_ERR_HIP) throw HipError(msg);
+	throw std::invalid_argument(msg);
+}
+
+void check_hip(hipError_t e, const char* what) {
+	if (e != hipSuccess) throw HipError(std::string("nn::hip: ") + what + ": " + hipGetErrorString(e));
+}
+
+size_t numel(const std::vector<size_t>& s) {
+	size_t n = 1;
+	for (size_t d : s) n *= d;
+	return n;
+}
+
+// Caching allocator: free blocks kept by rounded size and handed out again (all work is on g_stream, so a block
+// released after its last use was enqueued can be reused by work enqueued later).
+class Cache {
+public:
+	void* get(size_t bytes, size_t& rounded) {
+		rounded = round(bytes);
+		std::lock_guard<std::mutex> lock(mu_);
+		auto it = free_.find(rounded);
+		if (it != free_.end()) {
+			void* p = it->second;
+			free_.erase(it);
+			return p;
+		}
+		void* p = nullptr;
+		check_hip(hipMalloc(&p, rounded), "device allocation");
+		held_ += rounded;
+		return p;
+	}
+	void put(void* p, size_t rounded) {
+		std::lock_guard<std::mutex> lock(mu_);
+		free_.emplace(rounded, p);
+	}
+	size_t held() {
+		std::lock_guard<std::mutex> lock(mu_);
+		return held_;
+	}
+	void release() {
+		check_hip(hipStreamSynchronize(g_stream), "synchronize");
+		std::lock_guard<std::mutex> lock(mu_);
+		for (auto& e : free_) {
+			(void)hipFree(e.second);
+			held_ -= e.first;
+		}
+		free_.clear();
+	}
+
+private:
+	static size_t round(size_t b) {
+		if (b <= 256) return 256;
+		if (b <= (size_t(1) << 20)) return (b + 511) & ~size_t(511);
+		return (b + (size_t(1) << 20) - 1) & ~((size_t(1) << 20) - 1);
+	}
+	std::mutex mu_;
+	std::multimap<size_t, void*> free_;
+	size_t held_ = 0;
+};
+
+Cache& cache() {
+	static Cache* c = new Cache;  // kept until the process ends (the HIP runtime may be gone at static teardown)
+	return *c;
+}
+
+thread_local bool g_grad_enabled = true;
+
+std::vector<size_t> to_vec(const size_t* p, size_t n) { return std::vector<size_t>(p, p + n); }
+
+}  // namespace
+
+struct Block {
+	void* p = nullptr;
+	size_t bytes = 0;
+	explicit Block(size_t b) { p = cache().get(std::max<size_t>(b, 1), bytes); }
+	~Block() { cache().put(p, bytes); }
+	Block(const Block&) = delete;
+	Block& operator=(const Block&) = delete;
+};
+
+void set_stream(hipStream_t s) {
+	if (s == g_stream) return;
+	check_hip(hipStreamSynchronize(g_stream), "synchronize");
+	g_stream = s;
+}
+hipStream_t current_stream() { return g_stream; }
+void synchronize() { check_hip(hipStreamSynchronize(g_stream), "synchronize"); }
+size_t allocator_bytes() { return cache().held(); }
+void empty_cache() { cache().release(); }
+
+// ---- Tensor ----
+
+Tensor::Tensor() : shape_{0}, size_(0) {}
+
+Tensor::Tensor(std::vector<size_t> shape, float value) : Tensor(empty(std::move(shape))) { fill_(value); }
+
+Tensor Tensor::empty(std::vector<size_t> shape) {
+	Tensor t;
+	t.shape_ = std::move(shape);
+	t.size_ = numel(t.shape_);
+	t.storage_ = std::make_shared<Block>(t.size_ * sizeof(float));
+	return t;
+}
+
+Tensor Tensor::from_host(std::vector<size_t> shape, const float* data) {
+	Tensor t = empty(std::move(shape));
+	if (t.size_) check_hip(hipMemcpyAsync(t.data(), data, t.size_ * 4, hipMemcpyHostToDevice, g_stream), "copy in");
+	return t;
+}
+
+void Tensor::to_host(float* out) const {
+	if (size_) check_hip(hipMemcpyAsync(out, data(), size_ * 4, hipMemcpyDeviceToHost, g_stream), "copy out");
+	synchronize();
+}
+
+std::vector<float> Tensor::to_host() const {
+	std::vector<float> v(size_);
+	to_host(v.data());
+	return v;
+}
+
+float* Tensor::data() const { return storage_ ? static_cast<float*>(storage_->p) : nullptr; }
+
+Tensor Tensor::reshape(std::vector<size_t> new_shape) const {
+	if (numel(new_shape) != size_) throw TensorShapeError("nn::hip: reshape changes the element count");
+	Tensor t = *this;
+	t.shape_ = std::move(new_shape);
+	return t;
+}
+
+void Tensor::zero_() { fill_(0.0f); }
+
+void Tensor::fill_(float value) {
+	if (!size_) return;
+	if (value == 0.0f && !std::signbit(value)) {
+		// Tensor::sum(0) over no rows stores +0 everywhere: a fill kernel (no memset node if the stream is captured)
+		check(nnh_tensor_sum0(nullptr, 0, size_, data(), 0, g_stream));
+		return;
+	}
+	std::vector<float> host(size_, value);
+	check_hip(hipMemcpyAsync(data(), host.data(), size_ * 4, hipMemcpyHostToDevice, g_stream), "fill");
+	synchronize();
+}
+
+Tensor matmul(const Tensor& a, const Tensor& b, bool trans_a, bool trans_b) {
+	size_t out[16];
+	int nd = 0;
+	check(nnh_matmul_shape(a.shape().data(), (int)a.ndim(), b.shape().data(), (int)b.ndim(), trans_a, trans_b, out, &nd));
+	Tensor r = Tensor::empty(to_vec(out, nd));
+	check(nnh_matmul(a.data(), a.shape().data(), (int)a.ndim(), b.data(), b.shape().data(), (int)b.ndim(), trans_a,
+	                 trans_b, r.data(), g_stream));
+	return r;
+}
+
+// ---- Value ----
+
+NoGradGuard::NoGradGuard() : previous_(g_grad_enabled) { g_grad_enabled = false; }
+NoGradGuard::~NoGradGuard() { g_grad_enabled = previous_; }
+bool NoGradGuard::grad_enabled() { return g_grad_enabled; }
+
+Value Value::leaf(Tensor data, bool requires_grad) {
+	auto n = std::make_shared<NodeImpl>();
+	n->requires_grad = requires_grad;
+	if (requires_grad) n->grad = Tensor(data.shape(), 0.0f);  // a leaf's gradient starts as zeros (value.cpp:18-21)
+	n->data = std::move(data);
+	return Value(n);
+}
+
+Value Value::node(Tensor data, std::vector<Value> parents, std::function<void(const Tensor&)> backward_fn) {
+	if (!g_grad_enabled) return leaf(std::move(data), false);
+	auto n = std::make_shared<NodeImpl>();
+	n->data = std::move(data);
+	n->requires_grad = true;
+	n->parents = std::move(parents);
+	n->backward_fn = std::move(backward_fn);
+	return Value(n);
+}
+
+Tensor& Value::data() const { return impl_->data; }
+
+Tensor& Value::grad() const {
+	if (impl_->grad_fresh) {
+		impl_->grad.zero_();
+		impl_->grad_fresh = false;
+	}
+	return impl_->grad;
+}
+
+Tensor& Value::grad_accum(bool& first) const {
+	first = impl_->grad_fresh;
+	impl_->grad_fresh = false;
+	return impl_->grad;
+}
+
+bool Value::requires_grad() const { return impl_->requires_grad; }
+
+void Value::zero_grad() const {
+	if (impl_->grad.shape() != impl_->data.shape()) impl_->grad = Tensor(impl_->data.shape(), 0.0f);
+	else impl_->grad.zero_();
+	impl_->grad_fresh = false;
+}
+
+void Value::backward() const {
+	if (impl_->data.size() != 1) throw TensorShapeError("nn::hip: backward() needs a one-element value");
+	backward(Tensor(impl_->data.shape(), 1.0f));
+}
+
+void Value::backward(const Tensor& seed) const {
+	if (seed.shape() != impl_->data.shape()) throw TensorShapeError("nn::hip: the seed must have the output's shape");
+	// value.cpp:80-132: an iterative post-order walk, gradients sized (not zeroed) and marked fresh, the output's
+	// set, then every backward rule in reverse topological order
+	std::vector<Value> topo;
+	std::unordered_set<NodeImpl*> expanded, done;
+	std::vector<Value> stack{*this};
+	while (!stack.empty()) {
+		Value v = stack.back();
+		if (done.count(v.impl())) {
+			stack.pop_back();
+			continue;
+		}
+		if (expanded.count(v.impl())) {
+			stack.pop_back();
+			done.insert(v.impl());
+			topo.push_back(v);
+			continue;
+		}
+		expanded.insert(v.impl());
+		for (const Value& p : v.impl()->parents)
+			if (!expanded.count(p.impl())) stack.push_back(p);
+	}
+	for (const Value& v : topo)
+		if (v.impl()->backward_fn) {
+			if (v.impl()->grad.shape() != v.impl()->data.shape()) v.impl()->grad = Tensor::empty(v.impl()->data.shape());
+			v.impl()->grad_fresh = true;
+		}
+	if (impl_->grad.shape() != impl_->data.shape()) impl_->grad = Tensor::empty(impl_->data.shape());
+	if (seed.size())
+		check_hip(hipMemcpyAsync(impl_->grad.data(), seed.data(), seed.size() * 4, hipMemcpyDeviceToDevice, g_stream),
+		          "seed");
+	impl_->grad_fresh = false;
+	for (auto it = topo.rbegin(); it != topo.rend(); ++it)
+		if (it->impl()->backward_fn) it->impl()->backward_fn(it->grad());
+}
+
+// ---- ops ----
+
+namespace {
+
+float* grad_if(const Value& v, bool& first) {
+	first = false;
+	return v.requires_grad() ? v.grad_accum(first).data() : nullptr;
+}
+
+// A byte or uint32 side buffer an op keeps for its backward (conv's alive flags, pooling's argmax).
+std::shared_ptr<Block> side_buffer(size_t bytes) { return std::make_shared<Block>(bytes); }
+
+Value matmul_op(const Value& a, const Value& b, bool bt) {
+	Tensor r = matmul(a.data(), b.data(), false, bt);
+	return Value::node(std::move(r), {a, b}, [a, b, bt](const Tensor& g) {
+		bool fa = false, fb = false;
+		float* da = grad_if(a, fa);  // a first: one node passed as both operands is stored by dA, added to by dB
+		float* db = grad_if(b, fb);
+		if (!da && !db) return;
+		const Tensor& A = a.data();
+		const Tensor& B = b.data();
+		check(nnh_matmul_backward(g.data(), A.data(), A.shape().data(), (int)A.ndim(), B.data(), B.shape().data(),
+		                          (int)B.ndim(), bt, da, fa, db, fb, g_stream));
+	});
+}
+
+Value conv_op(const Value& x, const Value& w, const Value& b, int stride, int padding, bool fuse_relu) {
+	const auto& xs = x.data().shape();
+	const auto& ws = w.data().shape();
+	// ops.cpp:1347-1365
+	if (xs.size() != 4 || ws.size() != 4 || xs[1] != ws[1] || b.data().shape() != std::vector<size_t>{ws[0]})
+		throw TensorShapeError("nn::hip: conv2d shapes");
+	if (stride <= 0 || padding < 0 || ws[2] > xs[2] + 2 * (size_t)padding || ws[3] > xs[3] + 2 * (size_t)padding)
+		throw TensorShapeError("nn::hip: conv2d geometry");
+	const size_t N = xs[0], Cin = xs[1], H = xs[2], W = xs[3], Cout = ws[0], kh = ws[2], kw = ws[3];
+	const size_t ho = (H + 2 * padding - kh) / stride + 1, wo = (W + 2 * padding - kw) / stride + 1;
+	Tensor y = Tensor::empty({N, Cout, ho, wo});
+	const bool keep = fuse_relu && NoGradGuard::grad_enabled() &&
+	                  (x.requires_grad() || w.requires_grad() || b.requires_grad());
+	std::shared_ptr<Block> alive = keep ? side_buffer(y.size()) : nullptr;
+	check(nnh_conv2d_forward(x.data().data(), N, Cin, H, W, w.data().data(), Cout, kh, kw, b.data().data(), stride,
+	                         padding, fuse_relu, y.data(), alive ? static_cast<unsigned char*>(alive->p) : nullptr,
+	                         g_stream));
+	return Value::node(std::move(y), {x, w, b}, [=](const Tensor& g) {
+		// ops.cpp:1418-1463: dx taken first (grad_accum), then db and dW (grad() +=, a fresh one zeroed first,
+		// which gives the sum itself)
+		bool fx = false, fb = false, fw = false;
+		float* dx = grad_if(x, fx);
+		float* db = grad_if(b, fb);
+		float* dw = grad_if(w, fw);
+		if (!dx && !dw && !db) return;
+		check(nnh_conv2d_backward(g.data(), x.data().data(), w.data().data(),
+		                          alive ? static_cast<const unsigned char*>(alive->p) : nullptr, N, Cin, H, W, Cout, kh, kw,
+		                          stride, padding, dx, fx, dw, fw, db, fb, g_stream));
+	});
+}
+
+}  // namespace
+
+Value matmul(const Value& a, const Value& b) { return matmul_op(a, b, false); }
+Value matmul_bt(const Value& a, const Value& b) { return matmul_op(a, b, true); }
+
+Value linear(const Value& x, const Value& weight, const Value& bias) {
+	const auto& xs = x.data().shape();
+	const auto& ws = weight.data().shape();
+	// ops.cpp:717-719
+	if (xs.size() < 2 || ws.size() != 2 || xs.back() != ws[1] || bias.data().shape() != std::vector<size_t>{ws[0]})
+		throw TensorShapeError("nn::hip: linear shapes");
+	const size_t n = ws[0], K = ws[1], M = x.data().size() / std::max<size_t>(K, 1);
+	std::vector<size_t> out(xs.begin(), xs.end() - 1);
+	out.push_back(n);
+	Tensor y = Tensor::empty(out);
+	check(nnh_linear_forward(x.data().data(), K ? M : numel(std::vector<size_t>(xs.begin(), xs.end() - 1)), K,
+	                         weight.data().data(), n, bias.data().data(), 0, y.data(), g_stream));
+	return Value::node(std::move(y), {x, weight, bias}, [x, weight, bias, n, K](const Tensor& g) {
+		bool fx = false, fw = false, fb = false;
+		float* dx = grad_if(x, fx);
+		float* dw = grad_if(weight, fw);
+		float* db = grad_if(bias, fb);
+		if (!dx && !dw && !db) return;
+		const auto& xs2 = x.data().shape();
+		check(nnh_linear_backward(g.data(), x.data().data(), weight.data().data(), xs2.data(), (int)xs2.size() - 1, K, n,
+		                          dx, fx, dw, fw, db, fb, g_stream));
+	});
+}
+
+Value relu(const Value& x) {
+	Tensor y = Tensor::empty(x.data().shape());
+	check(nnh_relu_forward(x.data().data(), y.data(), y.size(), g_stream));
+	return Value::node(std::move(y), {x}, [x](const Tensor& g) {
+		bool first = false;
+		float* dx = grad_if(x, first);
+		if (dx) check(nnh_relu_backward(x.data().data(), g.data(), dx, first, g.size(), g_stream));
+	});
+}
+
+Value reshape(const Value& x, std::vector<size_t> new_shape) {
+	Tensor y = x.data().reshape(std::move(new_shape));
+	return Value::node(std::move(y), {x}, [x](const Tensor& g) {
+		bool first = false;
+		float* dx = grad_if(x, first);
+		if (dx) check(nnh_add_to_grad(dx, g.data(), g.size(), first, g_stream));
+	});
+}
+
+Value conv2d(const Value& x, const Value& weight, const Value& bias, int stride, int padding) {
+	return conv_op(x, weight, bias, stride, padding, false);
+}
+
+Value conv2d_relu(const Value& x, const Value& weight, const Value& bias, int stride, int padding) {
+	return conv_op(x, weight, bias, stride, padding, true);
+}
+
+Value maxpool2d(const Value& x, size_t kernel_size, size_t stride) {
+	const auto& xs = x.data().shape();
+	if (xs.size() != 4) throw TensorShapeError("nn::hip: maxpool2d needs {N, C, H, W}");  // ops.cpp:1610-1612
+	const size_t N = xs[0], C = xs[1], H = xs[2], W = xs[3];
+	if (kernel_size == 0 || stride == 0 || kernel_size > H || kernel_size > W)
+		throw TensorShapeError("nn::hip: maxpool2d geometry");
+	const size_t ho = (H - kernel_size) / stride + 1, wo = (W - kernel_size) / stride + 1;
+	Tensor y = Tensor::empty({N, C, ho, wo});
+	std::shared_ptr<Block> arg = side_buffer(y.size() * 4);
+	check(nnh_maxpool2d_forward(x.data().data(), N, C, H, W, kernel_size, stride, y.data(),
+	                            static_cast<unsigned int*>(arg->p), g_stream));
+	return Value::node(std::move(y), {x}, [=](const Tensor& g) {
+		bool first = false;
+		float* dx = grad_if(x, first);
+		if (dx)
+			check(nnh_maxpool2d_backward(g.data(), static_cast<const unsigned int*>(arg->p), N, C, H, W, kernel_size,
+			                             stride, dx, first, g_stream));
+	});
+}
+
+Value attention(const Value& q, const Value& k, const Value& v, size_t heads, const Tensor& key_padding_mask,
+                bool causal) {
+	const auto& qs = q.data().shape();
+	const auto& ks = k.data().shape();
+	// ops.cpp:1228-1236
+	if (qs.size() != 3 || ks.size() != 3 || v.data().shape() != ks || qs[0] != ks[0] || qs[2] != ks[2])
+		throw TensorShapeError("nn::hip: attention shapes");
+	const size_t N = qs[0], Tq = qs[1], D = qs[2], Tk = ks[1];
+	const bool mask = key_padding_mask.size() != 0;
+	if (mask && key_padding_mask.shape() != std::vector<size_t>{N, Tk})
+		throw TensorShapeError("nn::hip: attention key padding mask shape");
+	Tensor out = Tensor::empty({N, Tq, D});
+	Tensor probs = Tensor::empty({N, heads ? heads : 1, Tq, Tk});
+	const float* pm = mask ? key_padding_mask.data() : nullptr;
+	check(nnh_attention_forward(q.data().data(), k.data().data(), v.data().data(), N, Tq, Tk, D, heads, pm, causal,
+	                            out.data(), probs.data(), g_stream));
+	const Tensor keep_mask = key_padding_mask;
+	return Value::node(std::move(out), {q, k, v}, [=](const Tensor& g) {
+		// ops.cpp:1274-1278: the gradients in the order they are written, v, q, k
+		bool fv = false, fq = false, fk = false;
+		float* dv = grad_if(v, fv);
+		float* dq = grad_if(q, fq);
+		float* dk = grad_if(k, fk);
+		if (!dq && !dk && !dv) return;
+		check(nnh_attention_backward(g.data(), q.data().data(), k.data().data(), v.data().data(), probs.data(), N, Tq,
+		                             Tk, D, heads, mask ? keep_mask.data() : nullptr, causal, dq, fq, dk, fk, dv, fv,
+		                             g_stream));
+	});
+}
+
+Value scaled_masked_softmax(const Value& x, float scale_by, const Tensor& key_padding_mask, bool causal) {
+	const auto& xs = x.data().shape();
+	if (xs.size() != 4) throw TensorShapeError("nn::hip: scaled_masked_softmax needs {N, H, Tq, Tk}");
+	const size_t N = xs[0], H = xs[1], Tq = xs[2], Tk = xs[3];
+	const bool mask = key_padding_mask.size() != 0;
+	if (mask && key_padding_mask.shape() != std::vector<size_t>{N, Tk})
+		throw TensorShapeError("nn::hip: scaled_masked_softmax key padding mask shape");
+	Tensor y = Tensor::empty(xs);
+	check(nnh_scaled_masked_softmax_forward(x.data().data(), N, H, Tq, Tk, scale_by,
+	                                        mask ? key_padding_mask.data() : nullptr, causal, y.data(), g_stream));
+	const Tensor keep_mask = key_padding_mask;
+	const Tensor yk = y;
+	return Value::node(std::move(y), {x}, [=](const Tensor& g) {
+		bool first = false;
+		float* dx = grad_if(x, first);
+		if (dx)
+			check(nnh_scaled_masked_softmax_backward(yk.data(), g.data(), N, H, Tq, Tk, scale_by,
+			                                         mask ? keep_mask.data() : nullptr, causal, dx, first, g_stream));
+	});
+}
+
+}  // namespace hip
+}  // namespace nn

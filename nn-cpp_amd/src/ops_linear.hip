@@ -165,6 +165,14 @@ int nnh_relu_backward(const float* x, const float* g, float* dx, int first, size
 	                  "relu backward");
 }
 
+int nnh_add_to_grad(float* dst, const float* src, size_t count, int first, void* stream) {
+	if (count == 0) return NNH_OK;
+	if (!dst || !src) return fail(NNH_ERR_INVALID, "null pointer");
+	if (dst != src && ranges_overlap(dst, count * 4, src, count * 4)) return fail(NNH_ERR_ALIAS, "dst overlaps src");
+	return hip_status(add_to_grad(dst, src, (int64_t)count, first ? 1 : 0, reinterpret_cast<hipStream_t>(stream)),
+	                  "add_to_grad");
+}
+
 int nnh_tensor_sum0(const float* src, size_t rows, size_t inner, float* dst, int combine, void* stream) {
 	if (inner == 0) return NNH_OK;
 	if (!dst || (rows > 0 && !src)) return fail(NNH_ERR_INVALID, "null pointer");

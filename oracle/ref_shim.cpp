@@ -229,6 +229,99 @@ int nnref_matmul_backward(const float* a, const size_t* as, int an, const float*
 	});
 }
 
+// ---- graphs composed from nn-cpp's ops: the counterparts of tests/cpp/nn_hip_harness.cpp, on the CPU ----
+// Leaves start with zero gradients (Value::leaf allocates them zeroed), the backward pass is seeded with g through
+// probe_loss, exactly as the harness seeds its Value::backward.
+
+Value leaf_of(const float* p, std::vector<size_t> shape) { return Value::leaf(make(p, std::move(shape)), true); }
+
+int nnref_cnn_step(const float* x, size_t N, size_t c0, size_t side, size_t c1, size_t c2, size_t hidden,
+		size_t classes, const float* w1, const float* b1, const float* w2, const float* b2, const float* w3,
+		const float* b3, const float* w4, const float* b4, const float* g, float* logits, float* dx, float* dw1,
+		float* db1, float* dw2, float* db2, float* dw3, float* db3, float* dw4, float* db4) {
+	return guard([&] {
+		const size_t flat = c2 * (side / 4) * (side / 4);
+		const Value xv = leaf_of(x, {N, c0, side, side});
+		const Value W1 = leaf_of(w1, {c1, c0, 3, 3}), B1 = leaf_of(b1, {c1}), W2 = leaf_of(w2, {c2, c1, 3, 3});
+		const Value B2 = leaf_of(b2, {c2}), W3 = leaf_of(w3, {hidden, flat}), B3 = leaf_of(b3, {hidden});
+		const Value W4 = leaf_of(w4, {classes, hidden}), B4 = leaf_of(b4, {classes});
+		Value h = nn::maxpool2d(nn::conv2d_relu(xv, W1, B1, 1, 1), 2, 2);
+		h = nn::maxpool2d(nn::conv2d_relu(h, W2, B2, 1, 1), 2, 2);
+		h = nn::reshape(h, {N, flat});
+		const Value y = nn::linear(nn::relu(nn::linear(h, W3, B3)), W4, B4);
+		probe_loss(y, g).backward();
+		put(y.data(), logits);
+		put(xv.grad(), dx);
+		put(W1.grad(), dw1);
+		put(B1.grad(), db1);
+		put(W2.grad(), dw2);
+		put(B2.grad(), db2);
+		put(W3.grad(), dw3);
+		put(B3.grad(), db3);
+		put(W4.grad(), dw4);
+		put(B4.grad(), db4);
+	});
+}
+
+int nnref_mlp_step(const float* x, size_t M, const size_t* dims, int layers, const float* const* w,
+		const float* const* b, const float* g, float* y, float* dx, float* const* dw, float* const* db) {
+	return guard([&] {
+		const Value xv = leaf_of(x, {M, dims[0]});
+		std::vector<Value> W, B;
+		Value h = xv;
+		for (int i = 0; i < layers; ++i) {
+			W.push_back(leaf_of(w[i], {dims[i + 1], dims[i]}));
+			B.push_back(leaf_of(b[i], {dims[i + 1]}));
+			h = nn::linear(h, W[i], B[i]);
+			if (i + 1 < layers) h = nn::relu(h);
+		}
+		probe_loss(h, g).backward();
+		put(h.data(), y);
+		put(xv.grad(), dx);
+		for (int i = 0; i < layers; ++i) {
+			put(W[i].grad(), dw[i]);
+			put(B[i].grad(), db[i]);
+		}
+	});
+}
+
+int nnref_matmul_chain(const float* a, const size_t* as, const float* b, const size_t* bs, const float* c,
+		const size_t* cs, const float* g, float* y, float* da, float* db, float* dc) {
+	return guard([&] {
+		const Value A = leaf_of(a, {as[0], as[1], as[2]}), B = leaf_of(b, {bs[0], bs[1], bs[2]});
+		const Value Cv = leaf_of(c, {cs[0], cs[1]});
+		const Value r = nn::matmul_bt(nn::matmul(A, B), Cv);
+		probe_loss(r, g).backward();
+		put(r.data(), y);
+		put(A.grad(), da);
+		put(B.grad(), db);
+		put(Cv.grad(), dc);
+	});
+}
+
+int nnref_self_attention(const float* x, size_t N, size_t T, size_t D, size_t heads, int causal, const float* g,
+		float* o, float* dx) {
+	return guard([&] {
+		const Value xv = leaf_of(x, {N, T, D});
+		const Value r = nn::attention(xv, xv, xv, heads, Tensor::empty({0}), causal != 0);
+		probe_loss(r, g).backward();
+		put(r.data(), o);
+		put(xv.grad(), dx);
+	});
+}
+
+int nnref_softmax_step(const float* x, size_t N, size_t H, size_t Tq, size_t Tk, float scale, const float* pad,
+		int causal, const float* g, float* y, float* dx) {
+	return guard([&] {
+		const Value xv = leaf_of(x, {N, H, Tq, Tk});
+		const Tensor mask = pad ? make(pad, {N, Tk}) : Tensor::empty({0});
+		const Value r = nn::scaled_masked_softmax(xv, scale, mask, causal != 0);
+		probe_loss(r, g).backward();
+		put(r.data(), y);
+		put(xv.grad(), dx);
+	});
+}
+
 // ---- timing (the CPU baseline): each returns the number of timed runs, or -1 on an exception ----
 
 // nn::matmul(a, b, ta, tb) (src/tensor.cpp:571-641) on Tensors built once, as run_matmul (runner.cpp:80-96);
