@@ -444,6 +444,25 @@ void oracle_masked_softmax_row_backward(const float* y, float* g, size_t Tk, siz
 	}
 }
 
+/* scaled_masked_softmax backward over {N, H, Tq, Tk} (ops.cpp:1318-1341): per row, dot = sum of g y in j order
+ * (each product rounded, then added), term = scale (y (g - dot)); a fresh gradient stores term + 0.0f (0 where
+ * masked), an existing one adds term where not masked. */
+void oracle_scaled_masked_softmax_backward(const float* y, const float* g, size_t N, size_t H, size_t Tq, size_t Tk,
+		float scale_by, const float* pad, int causal, float* dx, int first) {
+	for (size_t r = 0; r < N * H * Tq; ++r) {
+		const size_t i = r % Tq, n = r / (H * Tq);
+		const float* ph = pad ? pad + n * Tk : NULL;
+		float dot = 0.0f;
+		for (size_t j = 0; j < Tk; ++j) dot += g[r * Tk + j] * y[r * Tk + j];
+		for (size_t j = 0; j < Tk; ++j) {
+			const int masked = (ph && ph[j] == 0.0f) || (causal && j > i);
+			const float term = scale_by * (y[r * Tk + j] * (g[r * Tk + j] - dot));
+			if (first) dx[r * Tk + j] = masked ? 0.0f : term + 0.0f;
+			else if (!masked) dx[r * Tk + j] += term;
+		}
+	}
+}
+
 /* attention forward (ops.cpp:1226-1261): per (n, h), S = Q_h K_h^T (sgemm F,T with row stride D),
  * masked softmax row by row into probs, O_h = P V_h (sgemm F,F) into column block h*Dh. */
 void oracle_attention_forward(const float* q, const float* k, const float* v, size_t N, size_t Tq, size_t Tk,

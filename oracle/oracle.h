@@ -79,6 +79,8 @@ void oracle_attention_backward(const float* g, const float* q, const float* k, c
                                const float* probs, size_t N, size_t Tq, size_t Tk, size_t D, size_t heads,
                                const float* pad, int causal, float* dq, int dq_first, float* dk, int dk_first,
                                float* dv, int dv_first);
+void oracle_scaled_masked_softmax_backward(const float* y, const float* g, size_t N, size_t H, size_t Tq, size_t Tk,
+                                           float scale_by, const float* pad, int causal, float* dx, int first);
 void oracle_scaled_masked_softmax(const float* x, size_t N, size_t H, size_t Tq, size_t Tk, float scale_by,
                                   const float* pad, int causal, float* y);
 void oracle_attention_f64(const float* q, const float* k, const float* v, size_t N, size_t Tq, size_t Tk,

@@ -76,6 +76,8 @@ class Oracle:
         L.oracle_attention_backward.argtypes = [_f, _f, _f, _f, _f, _sz, _sz, _sz, _sz, _sz, _f, C.c_int,
                                                 _f, C.c_int, _f, C.c_int, _f, C.c_int]
         L.oracle_scaled_masked_softmax.argtypes = [_f, _sz, _sz, _sz, _sz, C.c_float, _f, C.c_int, _f]
+        L.oracle_scaled_masked_softmax_backward.argtypes = [_f, _f, _sz, _sz, _sz, _sz, C.c_float, _f, C.c_int, _f,
+                                                             C.c_int]
         L.oracle_attention_f64.argtypes = [_f, _f, _f, _sz, _sz, _sz, _sz, _sz, _f, C.c_int, _d, _d]
         L.oracle_mt19937_uniform.argtypes = [C.c_uint, C.c_float, C.c_float, _f, _sz]
         _u32 = C.POINTER(C.c_uint32)
@@ -231,6 +233,14 @@ class Oracle:
         self.lib.oracle_scaled_masked_softmax(_fp(x), N, H, Tq, Tk, scale, _fp(pad), int(causal), _fp(y))
         return y
 
+    def scaled_masked_softmax_backward(self, y, g, scale, pad=None, causal=False, dx=None, first=True):
+        N, H, Tq, Tk = y.shape
+        out = np.array(dx, np.float32, copy=True) if dx is not None else np.zeros_like(y)
+        self.lib.oracle_scaled_masked_softmax_backward(_fp(np.ascontiguousarray(y, np.float32)),
+                                                       _fp(np.ascontiguousarray(g, np.float32)), N, H, Tq, Tk, scale,
+                                                       _fp(pad), int(causal), _fp(out), int(first))
+        return out
+
     def attention_f64(self, q, k, v, heads, pad=None, causal=False):
         N, Tq, D = q.shape
         Tk = k.shape[1]
@@ -277,6 +287,8 @@ class Reference:
         L.nnref_num_threads.restype = _sz
         L.nnref_uses_avx2.restype = C.c_int
         L.nnref_sgemm.argtypes = [C.c_int, C.c_int, _sz, _sz, _sz, _f, _sz, _f, _sz, _f, _sz, C.c_int]
+        L.nnref_sgemm_portable.argtypes = L.nnref_sgemm.argtypes
+        L.nnref_sgemm_unpacked.argtypes = L.nnref_sgemm.argtypes
         L.nnref_matmul.argtypes = [_f, _szp, C.c_int, _f, _szp, C.c_int, C.c_int, C.c_int, _f, _sz, _szp,
                                    C.POINTER(C.c_int)]
         L.nnref_linear_forward.argtypes = [_f, _szp, C.c_int, _f, _sz, _f, _f]
@@ -287,6 +299,7 @@ class Reference:
         L.nnref_attention_forward.argtypes = [_f, _f, _f, _sz, _sz, _sz, _sz, _sz, _f, C.c_int, _f]
         L.nnref_attention_backward.argtypes = [_f, _f, _f, _sz, _sz, _sz, _sz, _sz, _f, C.c_int, _f, _f, _f, _f]
         L.nnref_scaled_masked_softmax.argtypes = [_f, _sz, _sz, _sz, _sz, C.c_float, _f, C.c_int, _f]
+        L.nnref_module_run.argtypes = [C.c_int, C.c_uint, _f, _szp, C.c_int, _f, _f, _sz, _f, _sz, _szp, _szp]
         L.nnref_maxpool2d.argtypes = [_f, _sz, _sz, _sz, _sz, _sz, _sz, _f, _f, _f]
         L.nnref_time_maxpool2d.argtypes = [_f, _sz, _sz, _sz, _sz, _sz, _sz, _f, C.c_int, C.c_int, C.c_double, _d,
                                            C.POINTER(C.c_int), _d, _f, _f]
@@ -314,6 +327,13 @@ class Reference:
     def sgemm(self, ta, tb, m, n, k, a, lda, b, ldb, c, ldc, acc):
         out = np.array(c, dtype=np.float32, copy=True)
         self.lib.nnref_sgemm(int(ta), int(tb), m, n, k, _fp(a), lda, _fp(b), ldb, _fp(out), ldc, int(acc))
+        return out
+
+    def sgemm_variant(self, name, ta, tb, m, n, k, a, lda, b, ldb, c, ldc, acc):
+        """nn::kernels::sgemm_portable ("portable") or sgemm_unpacked ("unpacked") on a copy of c."""
+        out = np.array(c, dtype=np.float32, copy=True)
+        getattr(self.lib, f"nnref_sgemm_{name}")(int(ta), int(tb), m, n, k, _fp(a), lda, _fp(b), ldb, _fp(out), ldc,
+                                                  int(acc))
         return out
 
     def sgemm_inplace(self, ta, tb, m, n, k, a, lda, b, ldb, c, ldc, acc):
@@ -408,6 +428,16 @@ class Reference:
                                             _fp(da), _fp(db))
         assert rc == 0, rc
         return (da, None) if same else (da, db)
+
+    def module_run(self, which, seed, x, g, out_cap=1 << 20, grads_cap=1 << 22):
+        """nn-cpp module `which` (see nnref_module_run) built after manual_seed(seed): (output, all gradients)."""
+        x, g = np.ascontiguousarray(x, np.float32), np.ascontiguousarray(g, np.float32)
+        out, grads = np.empty(out_cap, np.float32), np.empty(grads_cap, np.float32)
+        n_out, n_grads = C.c_size_t(0), C.c_size_t(0)
+        rc = self.lib.nnref_module_run(which, seed, _fp(x), (C.c_size_t * x.ndim)(*x.shape), x.ndim, _fp(g), _fp(out),
+                                       out_cap, _fp(grads), grads_cap, C.byref(n_out), C.byref(n_grads))
+        assert rc == 0, rc
+        return out[: n_out.value].copy(), grads[: n_grads.value].copy()
 
     def maxpool2d(self, x, k, s, g=None):
         """nn::maxpool2d's output and, given g, its input gradient (fresh)."""

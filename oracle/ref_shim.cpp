@@ -9,12 +9,21 @@
 #include "nn/autograd/ops.hpp"
 #include "nn/autograd/value.hpp"
 #include "nn/kernels/gemm.hpp"
+#include "nn/nn/activation.hpp"
+#include "nn/nn/attention.hpp"
+#include "nn/nn/conv2d.hpp"
+#include "nn/nn/flatten.hpp"
+#include "nn/nn/linear.hpp"
+#include "nn/nn/pool2d.hpp"
+#include "nn/nn/sequential.hpp"
+#include "nn/random.hpp"
 #include "nn/kernels/parallel.hpp"
 #include "nn/tensor.hpp"
 
 #include <chrono>
 #include <cstring>
 #include <exception>
+#include <memory>
 #include <stdexcept>
 #include <vector>
 
@@ -93,6 +102,16 @@ int nnref_uses_avx2(void) { return nn::kernels::sgemm_uses_avx2() ? 1 : 0; }
 void nnref_sgemm(int ta, int tb, size_t m, size_t n, size_t k, const float* a, size_t lda, const float* b,
 		size_t ldb, float* c, size_t ldc, int accumulate) {
 	nn::kernels::sgemm(ta != 0, tb != 0, m, n, k, a, lda, b, ldb, c, ldc, accumulate != 0);
+}
+
+// The alternate kernels of include/nn/kernels/gemm.hpp:61-94 (in libnnref_hip.so they are the GPU drop-in's).
+void nnref_sgemm_portable(int ta, int tb, size_t m, size_t n, size_t k, const float* a, size_t lda, const float* b,
+		size_t ldb, float* c, size_t ldc, int accumulate) {
+	nn::kernels::sgemm_portable(ta != 0, tb != 0, m, n, k, a, lda, b, ldb, c, ldc, accumulate != 0);
+}
+void nnref_sgemm_unpacked(int ta, int tb, size_t m, size_t n, size_t k, const float* a, size_t lda, const float* b,
+		size_t ldb, float* c, size_t ldc, int accumulate) {
+	nn::kernels::sgemm_unpacked(ta != 0, tb != 0, m, n, k, a, lda, b, ldb, c, ldc, accumulate != 0);
 }
 
 // nn::matmul(a, b, ta, tb) (src/tensor.cpp:571-641). out must hold the result; its shape is returned.
@@ -319,6 +338,65 @@ int nnref_softmax_step(const float* x, size_t N, size_t H, size_t Tq, size_t Tk,
 		probe_loss(r, g).backward();
 		put(r.data(), y);
 		put(xv.grad(), dx);
+	});
+}
+
+// ---- nn-cpp's modules, unchanged (src/nn/*.cpp): the callers of the path ----
+// Builds model `which` after nn::manual_seed(seed) (so parameters come from the modules' own initialisation),
+// runs forward on x, seeds the backward pass with g through probe_loss, and returns the output (out, n_out floats)
+// and, concatenated in parameters() order followed by x's, every gradient (grads, n_grads floats).
+//   0: nn-cpp's cnn_mnist (apps/bench/workloads.cpp:113-137): Sequential of Conv2d(1,8,3,1,1), ReLU, MaxPool2d(2,2),
+//      Conv2d(8,16,3,1,1), ReLU, MaxPool2d(2,2), Flatten, Linear(784,128), ReLU, Linear(128,10); Sequential folds
+//      each Conv2d + ReLU into conv2d_relu (src/nn/sequential.cpp:16-28).
+//   1: MultiHeadAttention(64, 4 heads, causal), no dropout: the fused attention op (src/nn/attention.cpp:33-35).
+//   2: MultiHeadAttention(64, 4 heads) with dropout 0.1 in training mode: the composed path through matmul_bt,
+//      scaled_masked_softmax, dropout and a batched matmul (attention.cpp:36-47).
+//   3: Sequential of Linear(20,30), ReLU, Linear(30,5) on a 3-D input (Linear is not folded with ReLU).
+int nnref_module_run(int which, unsigned seed, const float* x, const size_t* xs, int xn, const float* g, float* out,
+		size_t out_cap, float* grads, size_t grads_cap, size_t* n_out, size_t* n_grads) {
+	return guard([&] {
+		nn::manual_seed(seed);
+		std::unique_ptr<nn::Module> m;
+		if (which == 0) {
+			auto s = std::make_unique<nn::Sequential>();
+			s->add(std::make_unique<nn::Conv2d>(1, 8, 3, 1, 1));
+			s->add(std::make_unique<nn::ReLU>());
+			s->add(std::make_unique<nn::MaxPool2d>(2, 2));
+			s->add(std::make_unique<nn::Conv2d>(8, 16, 3, 1, 1));
+			s->add(std::make_unique<nn::ReLU>());
+			s->add(std::make_unique<nn::MaxPool2d>(2, 2));
+			s->add(std::make_unique<nn::Flatten>());
+			s->add(std::make_unique<nn::Linear>(784, 128));
+			s->add(std::make_unique<nn::ReLU>());
+			s->add(std::make_unique<nn::Linear>(128, 10));
+			m = std::move(s);
+		} else if (which == 1) {
+			m = std::make_unique<nn::MultiHeadAttention>(64, 4, true);
+		} else if (which == 2) {
+			m = std::make_unique<nn::MultiHeadAttention>(64, 4, false, 0.1f);
+			m->train(true);
+		} else {
+			auto s = std::make_unique<nn::Sequential>();
+			s->add(std::make_unique<nn::Linear>(20, 30));
+			s->add(std::make_unique<nn::ReLU>());
+			s->add(std::make_unique<nn::Linear>(30, 5));
+			m = std::move(s);
+		}
+		const Value xv = Value::leaf(make(x, shape_of(xs, xn)), true);
+		const Value y = m->forward(xv);
+		probe_loss(y, g).backward();
+		if (y.data().size() > out_cap) throw std::runtime_error("capacity");
+		put(y.data(), out);
+		*n_out = y.data().size();
+		size_t off = 0;
+		std::vector<Value> ps = m->parameters();
+		ps.push_back(xv);
+		for (const Value& p : ps) {
+			if (off + p.grad().size() > grads_cap) throw std::runtime_error("capacity");
+			put(p.grad(), grads + off);
+			off += p.grad().size();
+		}
+		*n_grads = off;
 	});
 }
 

@@ -93,3 +93,61 @@ def test_host_entry_point_matches_oracle(gpu, oracle):
                 c = p.c.copy()
                 nnh.sgemm_host(ta, tb, p.m, p.n, p.k, p.a, p.lda, p.b, p.ldb, c, p.ldc, acc)
                 same(c, oracle.sgemm(ta, tb, p.m, p.n, p.k, p.a, p.lda, p.b, p.ldb, p.c, p.ldc, acc), (ta, tb, acc))
+
+
+# (model, input shape, output shape): nn-cpp's modules, unchanged, through the drop-in (see nnref_module_run)
+MODULES = [
+    (0, (32, 1, 28, 28), (32, 10)),   # cnn_mnist: Sequential folds Conv2d + ReLU into conv2d_relu
+    (1, (2, 16, 64), (2, 16, 64)),    # MultiHeadAttention, causal, no dropout: the fused attention op
+    (2, (2, 16, 64), (2, 16, 64)),    # MultiHeadAttention with dropout in training: the composed path
+    (3, (4, 6, 20), (4, 6, 5)),       # Linear on a 3-D input, ReLU, Linear
+]
+
+
+@pytest.mark.parametrize("which,xshape,yshape", MODULES)
+def test_modules_run_unchanged_through_the_dropin(refs, which, xshape, yshape):
+    """src/nn/{sequential,conv2d,linear,pool2d,activation,attention,dropout}.cpp compiled with the drop-in in place of
+    gemm.cpp: the output and every parameter's and the input's gradient bit-identical to nn-cpp's CPU build, with
+    the modules' GEMMs run on the GPU (the reference's own tests of these callers: tests/test_nn.cpp:587-651,
+    tests/test_transformer.cpp:149-276)."""
+    cpu, hip, calls = refs
+    x = synth.mt19937_uniform(30 + which, int(np.prod(xshape)), 0.0, 1.0).reshape(xshape)
+    g = synth.normal(40 + which, yshape)
+    before = calls()
+    o_cpu, g_cpu = cpu.module_run(which, 1234, x, g)
+    o_hip, g_hip = hip.module_run(which, 1234, x, g)
+    assert calls() > before, "the module's products did not reach the GPU"
+    same(o_hip, o_cpu, ("output", which))
+    same(g_hip, g_cpu, ("gradients", which))
+
+
+def test_portable_and_unpacked_kernels_through_the_dropin(refs):
+    """tests/test_kernels.cpp:157-167's sweep (sizes {1, 7, 33, 257}^3, both transposes, accumulate) for the
+    drop-in's sgemm_portable and sgemm_unpacked: the GPU computes nn-cpp's AVX2 chain for every entry point, so
+    each is bit-identical to nn-cpp's sgemm, and within the reference test's tolerance (1e-5 of sum |a b|, floor
+    1e-6; test_kernels.cpp:101-146) of nn-cpp's own portable and unpacked kernels."""
+    from helpers import Problem
+    cpu, hip, calls = refs
+    sizes = (1, 7, 33, 257)
+    seed = 1
+    for ta in (0, 1):
+        for tb in (0, 1):
+            for acc in (0, 1):
+                for m in sizes:
+                    for n in sizes:
+                        for k in sizes:
+                            p = Problem(ta, tb, m, n, k, 0, seed)
+                            seed += 1
+                            args = (ta, tb, m, n, k, p.a, p.lda, p.b, p.ldb, p.c, p.ldc, acc)
+                            want = cpu.sgemm(*args)
+                            opa, opb = (p.a.T if ta else p.a)[:m, :k], (p.b.T if tb else p.b)[:k, :n]
+                            mag = np.abs(opa.astype(np.float64)) @ np.abs(opb.astype(np.float64))
+                            if acc:
+                                mag = mag + np.abs(p.c[:m, :n])
+                            tol = np.maximum(1e-5 * mag, 1e-6)
+                            for name in ("portable", "unpacked"):
+                                got = hip.sgemm_variant(name, *args)
+                                same(got, want, (name, ta, tb, acc, m, n, k))
+                                theirs = cpu.sgemm_variant(name, *args)
+                                assert np.all(np.abs(got[:m, :n].astype(np.float64) - theirs[:m, :n]) <= tol), \
+                                    (name, ta, tb, acc, m, n, k)

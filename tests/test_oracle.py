@@ -416,3 +416,26 @@ def test_maxpool_hand_values(oracle):
     dx = oracle.maxpool2d_backward(np.array([[[[1.5, 2.5]]]], np.float32), arg, x.shape, 2, 1, dx=np.ones_like(x),
                                    first=False)
     assert dx.ravel().tolist() == [2.5, 3.5, 1, 1, 1, 1]
+
+
+def test_softmax_backward_matches_nncpp(oracle, ref):
+    """The oracle's scaled_masked_softmax backward against nn-cpp's backward rule (through its compiled library),
+    with a key padding mask and causal rows; nn-cpp's leaf gradient starts zeroed, which gives the fresh rule's bits."""
+    for (N, H, Tq, Tk, scale, masked, causal) in ((2, 3, 5, 7, 0.5, True, 0), (1, 2, 6, 6, 0.125, False, 1),
+                                                  (2, 2, 9, 9, 1.0, True, 1)):
+        x = synth.normal(120, (N, H, Tq, Tk))
+        g = synth.normal(121, (N, H, Tq, Tk))
+        pad = None
+        if masked:
+            pad = np.ones((N, Tk), np.float32)
+            pad[0, -2:] = 0
+        y = oracle.scaled_masked_softmax(x, np.float32(scale), pad, bool(causal))
+        got = oracle.scaled_masked_softmax_backward(y, g, np.float32(scale), pad, bool(causal))
+        want_y, want_dx = np.empty_like(x), np.empty_like(x)
+        fp = lambda a: None if a is None else a.ctypes.data_as(__import__("ctypes").POINTER(__import__("ctypes").c_float))
+        import ctypes as C
+        rc = ref.lib.nnref_softmax_step(fp(x), C.c_size_t(N), C.c_size_t(H), C.c_size_t(Tq), C.c_size_t(Tk),
+                                        C.c_float(scale), fp(pad), causal, fp(g), fp(want_y), fp(want_dx))
+        assert rc == 0
+        assert y.tobytes() == want_y.tobytes()
+        assert got.tobytes() == want_dx.tobytes(), (N, H, Tq, Tk)

@@ -198,3 +198,73 @@ def test_baseline_config5_sampled(gpu, oracle, m, n, k):
     got = dc.cpu().numpy()[rows, cols]
     want = oracle.sgemm_at(0, 0, m, n, k, a, k, b, n, 0, rows, cols)
     assert got.tobytes() == want.tobytes(), first_diff(got, want)
+
+
+def _subnormal_problem(ta, tb, m, n, k, seed):
+    """Operands whose products and running sums are subnormal: op(A) and op(B) entries near 2^-80 .. 2^-68
+    (products 2^-160 .. 2^-136), except at depth indices 5 and 260, where op(A) holds subnormal values (about
+    2^-135 .. 2^-130) and op(B) values in [2^-5, 1], so a subnormal operand makes a subnormal product that dominates
+    each output (a flush of subnormal inputs would lose it); signs are mixed and C holds subnormals (accumulate)."""
+    p = Problem(ta, tb, m, n, k, 2, seed)
+    rng = np.random.default_rng(seed)
+    opa = (p.a[:k, :m].T if ta else p.a[:m, :k]).astype(np.float64)
+    opb = (p.b[:n, :k].T if tb else p.b[:k, :n]).astype(np.float64)
+    opa = np.ldexp(opa, rng.integers(-80, -68, opa.shape))
+    opb = np.ldexp(opb, rng.integers(-80, -68, opb.shape))
+    for k0 in (5, 260):
+        if k0 < k:
+            opa[:, k0] = np.ldexp(np.sign(opa[:, k0]) * rng.uniform(1, 2, m), rng.integers(-135, -130, m))
+            opb[k0, :] = np.ldexp(np.sign(opb[k0, :]) * rng.uniform(1, 2, n), rng.integers(-5, 0, n))
+    opa, opb = opa.astype(np.float32), opb.astype(np.float32)
+    if ta:
+        p.a[:k, :m] = opa.T
+    else:
+        p.a[:m, :k] = opa
+    if tb:
+        p.b[:n, :k] = opb.T
+    else:
+        p.b[:k, :n] = opb
+    p.c[:m, :n] = np.ldexp(p.c[:m, :n].astype(np.float64), rng.integers(-140, -128, (m, n))).astype(np.float32)
+    return p
+
+
+@pytest.mark.parametrize("ta,tb", [(0, 0), (1, 0), (0, 1), (1, 1)])
+def test_subnormal_operands_and_sums(gpu, oracle, ta, tb):
+    """nn-cpp's AVX2 chain keeps subnormals (no flush to zero), and so must the MFMA chain: subnormal operands,
+    products and running sums, every tile configuration, with and without accumulate, bit for bit."""
+    import nnh
+    p = _subnormal_problem(ta, tb, 37, 41, 300, 77 + 2 * ta + tb)
+    vals = np.concatenate([p.a.ravel(), p.b.ravel()])
+    assert np.any((vals != 0) & (np.abs(vals) < np.finfo(np.float32).tiny))
+    for acc in (0, 1):
+        want = oracle_sgemm(oracle, p, acc)
+        out = want[: p.m, : p.n]
+        assert np.any((out != 0) & (np.abs(out) < np.finfo(np.float32).tiny)), "no subnormal result: test too weak"
+        for cfg in range(len(nnh.gemm_configs())):
+            got = gpu_sgemm(p, acc, config=cfg)
+            assert bits_equal(got, want), (cfg, acc, first_diff(got, want))
+
+
+@pytest.mark.parametrize("m,n,k", [(1024, 1024, 1024), (64, 4096, 4096), (4096, 4096, 64)])
+def test_baseline_config5_whole_output(gpu, oracle, m, n, k):
+    """BASELINE config 5 shapes, seed 4: every element bit-identical to nn-cpp (its compiled sgemm when present,
+    else the oracle), not a sample."""
+    import torch
+
+    import nnh
+    from pyoracle import Reference, reference_available
+    a, b = synth.uniform_operands(4, [(m, k), (k, n)])
+    a, b = np.ascontiguousarray(a), np.ascontiguousarray(b)
+    da, db = torch.from_numpy(a).cuda(), torch.from_numpy(b).cuda()
+    dc = torch.empty((m, n), device="cuda")
+    nnh.sgemm(0, 0, m, n, k, da, k, db, n, dc, n, 0)
+    torch.cuda.synchronize()
+    c0 = np.zeros((m, n), np.float32)
+    if reference_available():
+        r = Reference()
+        r.set_threads(8)
+        want = r.sgemm(0, 0, m, n, k, a, k, b, n, c0, n, 0)
+    else:
+        want = oracle.sgemm(0, 0, m, n, k, a, k, b, n, c0, n, 0)
+    got = dc.cpu().numpy()
+    assert bits_equal(got, want), first_diff(got, want)
