@@ -597,7 +597,77 @@ def run_cpu_rows(rows, headline=None):
     return setup
 
 
-def write_csv(path, rows, setup):
+WORKLOADS = [  # (name, model index of libnnh_workloads, batch, input shape, parameter shapes)
+    ("mlp_wide", 0, 256, (256, 784), [(1024, 784), (1024,), (1024, 1024), (1024,), (10, 1024), (10,)]),
+    ("cnn_mnist", 1, 32, (32, 1, 28, 28), [(8, 1, 3, 3), (8,), (16, 8, 3, 3), (16,), (128, 784), (128,), (10, 128),
+                                           (10,)]),
+]
+
+
+def run_workloads(with_cpu=True, seed=1, warmup=3, runs=15):
+    """nn-cpp's bench models (apps/bench/workloads.cpp:100-137): parameters reseeded from std::mt19937(seed) and the
+    input drawn from std::mt19937(seed + 1), as make_workload does; one training step's forward pass and its zero_grad
+    plus backward pass (from a fixed N(0,1) gradient of the logits; no loss, no optimizer step), timed as
+    runner.cpp:33-45 does, median of `runs` after `warmup`: on the GPU through nn::hip (libnnh_workloads.so), and
+    nn-cpp's own step on the CPU (one thread per physical core, pinned), the logits compared bit for bit."""
+    import ctypes as C
+
+    import numpy as np
+
+    from nnh import synth
+    L = C.CDLL(os.path.join(ROOT, "nn-cpp_amd", "lib", "libnnh_workloads.so"))
+    ref = None
+    if with_cpu:
+        sys.path.insert(0, os.path.join(ROOT, "oracle"))
+        from pyoracle import Reference, reference_available
+        if reference_available():
+            ref = Reference()
+    fp = lambda a: a.ctypes.data_as(C.POINTER(C.c_float))
+    dp = lambda a: a.ctypes.data_as(C.POINTER(C.c_double))
+    out = []
+    for name, model, N, xshape, shapes in WORKLOADS:
+        params = synth.reseeded_parameters(seed, shapes)
+        x = synth.mt19937_uniform(seed + 1, int(np.prod(xshape)), 0.0, 1.0).reshape(xshape)
+        g = synth.normal(seed + 2, (N, 10))
+        pp = (C.POINTER(C.c_float) * len(params))(*[fp(p) for p in params])
+        res = {"workload": name, "batch": N}
+        for side, lib, fn in (("gpu", L, "nnh_bench_workload_step"), ("cpu", ref.lib if ref else None,
+                                                                       "nnref_time_workload_step")):
+            if lib is None:
+                continue
+            fwd, bwd = np.empty(runs), np.empty(runs)
+            logits = np.empty((N, 10), np.float32)
+            if side == "cpu":
+                cores, _ = physical_cores()
+                saved = os.sched_getaffinity(0)
+                os.sched_setaffinity(0, cores)
+                ref.set_threads(len(cores))
+            try:
+                rc = getattr(lib, fn)(model, fp(x), C.c_size_t(N), pp, fp(g), warmup, runs, dp(fwd), dp(bwd), fp(logits))
+            finally:
+                if side == "cpu":
+                    os.sched_setaffinity(0, saved)
+            assert rc == 0, (name, side, rc)
+            tot = list(fwd + bwd)
+            res[side] = {"forward_ms": median(list(fwd)), "backward_ms": median(list(bwd)), "total_ms": median(tot),
+                         "spread": spread(tot), "runs": runs}
+            if side == "cpu":
+                res["cpu"]["threads"] = len(physical_cores()[0])
+            res[side + "_logits"] = logits
+        if "cpu" in res:
+            res["bitwise_vs_nn_cpp"] = bool(np.array_equal(res["gpu_logits"].view(np.uint32),
+                                                           res["cpu_logits"].view(np.uint32)))
+            res["speedup_gpu"] = res["cpu"]["total_ms"] / res["gpu"]["total_ms"]
+        for k in ("gpu_logits", "cpu_logits"):
+            res.pop(k, None)
+        log(f"[workload] {name}: GPU forward {res['gpu']['forward_ms']:.3f} ms + backward {res['gpu']['backward_ms']:.3f}"
+            f" ms" + (f"; nn-cpp CPU {res['cpu']['total_ms']:.3f} ms; logits bitwise {res['bitwise_vs_nn_cpp']}"
+                      if "cpu" in res else ""))
+        out.append(res)
+    return out
+
+
+def write_csv(path, rows, setup, workloads=()):
     """apps/bench/bench.cpp:112-113's columns, then the GPU columns; one line per GPU row and per CPU baseline."""
     cols = ["config", "label", "threads", "benchmark", "size", "forward_ms", "backward_ms", "optim_ms", "total_ms",
             "gflops", "spread", "runs", "tflops", "gbps", "roofline_bound", "roofline_frac", "maxabs_err",
@@ -620,6 +690,15 @@ def write_csv(path, rows, setup):
                     res.get("tflops") if gpu else ent.get("tflops"), res.get("gbps") if gpu else None,
                     r.bound if gpu else None, res["roofline"]["frac"] if gpu else None,
                     res.get("maxabs_vs_nn_cpp") if gpu else None, res.get("bitwise_repeat") if gpu else None]
+            lines.append(",".join(f(v) for v in vals))
+    for w in workloads:
+        for side, label in (("gpu", "gpu-mi355x"), ("cpu", "native-pinned")):
+            if side not in w:
+                continue
+            e = w[side]
+            vals = ["gpu" if side == "gpu" else "native", label, "" if side == "gpu" else e["threads"], w["workload"],
+                    str(w["batch"]), e["forward_ms"], e["backward_ms"], None, e["total_ms"], None, e["spread"],
+                    e["runs"], None, None, None, None, None, None]
             lines.append(",".join(f(v) for v in vals))
     with open(path, "w") as fh:
         fh.write("\n".join(lines) + "\n")
@@ -788,8 +867,9 @@ def main():
     setup = None
     if not args.no_cpu_baseline:
         setup = run_cpu_rows(rows, headline)
+    workloads = [] if args.no_configs else run_workloads(with_cpu=not args.no_cpu_baseline)
     if args.csv and rows:
-        write_csv(args.csv, rows, setup)
+        write_csv(args.csv, rows, setup, workloads)
     cpu = None
     hb = headline.result.get("cpu_baseline")
     if hb:
@@ -831,6 +911,9 @@ def main():
             "without_alive_flags": None if conv1_na is None else {
                 "us_per_launch": round(conv1_na.result["ms"] * 1e3, 3), "value": round(conv1_na.result["gbps"], 1)}},
         "configs": [row_json(r) for r in rows],
+        "workloads": [{k: ({kk: (round(vv, 4) if isinstance(vv, float) else vv) for kk, vv in v.items()}
+                           if isinstance(v, dict) else (round(v, 2) if isinstance(v, float) else v))
+                       for k, v in w.items()} for w in workloads],
     }
     print(json.dumps(out), flush=True)
 

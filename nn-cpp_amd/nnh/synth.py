@@ -15,12 +15,32 @@ def mt19937_raw(seed, count):
     return bg.random_raw(int(count)).astype(np.uint32)
 
 
-def mt19937_uniform(seed, count, lo=-1.0, hi=1.0):
-    u = mt19937_raw(seed, count).astype(np.float32)
-    c = u / np.float32(4294967296.0)
+def uniform_from_raw(raw, lo, hi):
+    """uniform_real_distribution<float>(lo, hi) applied to 32-bit draws raw (libstdc++'s mapping)."""
+    c = raw.astype(np.float32) / np.float32(4294967296.0)
     c = np.where(c >= np.float32(1.0), np.nextafter(np.float32(1.0), np.float32(0.0)), c).astype(np.float32)
     span = np.float32(np.float32(hi) - np.float32(lo))
     return (c * span + np.float32(lo)).astype(np.float32)
+
+
+def mt19937_uniform(seed, count, lo=-1.0, hi=1.0):
+    return uniform_from_raw(mt19937_raw(seed, count), lo, hi)
+
+
+def reseeded_parameters(seed, shapes):
+    """apps/bench/workloads.cpp:24-38 reseed_parameters: one std::mt19937(seed) stream over the parameters in order;
+    a parameter of rank < 2 becomes zeros (no draws), any other U(+-1/sqrt(size / shape[0])) in row-major order."""
+    sizes = [int(np.prod(s)) for s in shapes]
+    raw = mt19937_raw(seed, sum(n for s, n in zip(shapes, sizes) if len(s) >= 2))
+    out, off = [], 0
+    for s, n in zip(shapes, sizes):
+        if len(s) < 2:
+            out.append(np.zeros(s, np.float32))
+            continue
+        bound = np.float32(1.0) / np.sqrt(np.float32(n // s[0]))
+        out.append(np.ascontiguousarray(uniform_from_raw(raw[off:off + n], -bound, bound).reshape(s)))
+        off += n
+    return out
 
 
 def uniform_operands(seed, shapes, lo=-1.0, hi=1.0):

@@ -550,4 +550,43 @@ int nnref_time_maxpool2d(const float* x, size_t N, size_t C, size_t H, size_t W,
 	return runs;
 }
 
+// nn-cpp's side of the bench models' training step (the counterpart of nn-cpp_amd/src/bench/workloads.cpp, with
+// apps/bench/runner.cpp:33-45's clock points): the forward pass, then zero_grad and the backward pass from the
+// logits' gradient g; no loss, no optimizer step.
+int nnref_time_workload_step(int model, const float* x, size_t N, const float* const* params, const float* g,
+		int warmup, int runs, double* fwd_ms, double* bwd_ms, float* logits) {
+	return guard([&] {
+		static const std::vector<std::vector<size_t>> mlp = {{1024, 784}, {1024}, {1024, 1024}, {1024}, {10, 1024}, {10}};
+		static const std::vector<std::vector<size_t>> cnn = {{8, 1, 3, 3}, {8}, {16, 8, 3, 3}, {16}, {128, 784}, {128},
+			{10, 128}, {10}};
+		const auto& shapes = model == 0 ? mlp : cnn;
+		std::vector<Value> p;
+		for (size_t i = 0; i < shapes.size(); ++i) p.push_back(Value::leaf(make(params[i], shapes[i]), true));
+		const Value xv = Value::leaf(make(x, model == 0 ? std::vector<size_t>{N, 784} : std::vector<size_t>{N, 1, 28, 28}));
+		for (int i = 0; i < warmup + runs; ++i) {
+			const auto t0 = Clock::now();
+			Value y = Value::leaf(Tensor::empty({0}));
+			if (model == 0) {
+				Value h = nn::relu(nn::linear(xv, p[0], p[1]));
+				h = nn::relu(nn::linear(h, p[2], p[3]));
+				y = nn::linear(h, p[4], p[5]);
+			} else {
+				Value h = nn::maxpool2d(nn::conv2d_relu(xv, p[0], p[1], 1, 1), 2, 2);
+				h = nn::maxpool2d(nn::conv2d_relu(h, p[2], p[3], 1, 1), 2, 2);
+				h = nn::reshape(h, {N, 784});
+				y = nn::linear(nn::relu(nn::linear(h, p[4], p[5])), p[6], p[7]);
+			}
+			const auto t1 = Clock::now();
+			for (const Value& v : p) v.zero_grad();
+			probe_loss(y, g).backward();
+			const auto t2 = Clock::now();
+			if (i >= warmup) {
+				fwd_ms[i - warmup] = std::chrono::duration<double, std::milli>(t1 - t0).count();
+				bwd_ms[i - warmup] = std::chrono::duration<double, std::milli>(t2 - t1).count();
+			}
+			if (i + 1 == warmup + runs) put(y.data(), logits);
+		}
+	});
+}
+
 }  // extern "C"
