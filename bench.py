@@ -254,9 +254,10 @@ class Row:
         self.result = {}
 
 
-def build_rows(report=False):
+def build_rows(report=False, split=False):
     """Inputs of every BASELINE.json configuration (the reference's seeded streams), resident on the GPU, and one
-    Row per measured op."""
+    Row per measured op (split: only the GEMM-shaped rows of configs 1, 2 and 5 that the split-depth mode changes,
+    to be run in that mode)."""
     import ctypes as C
 
     import numpy as np
@@ -349,6 +350,14 @@ def build_rows(report=False):
                     lambda: [t for gr in grads for t in gr], 2 * fwd_flops,
                     cpu=lambda ref, w, r, bud: ref.time_linear_backward_layers(hacts[:3], ws, bs, gys, w, r, bud),
                     f64=mlp_bwd_f64, est_ms=0.035))
+
+    if split:  # the products the split-depth mode changes: configs 1 and 2 and the skinny config 5 product
+        matmul_row(5, "matmul_64x4096x4096", "nn::matmul 64x4096x4096 C = A B", 4, 64, 4096, 4096, 0, 0, 0.06)
+        for r in rows:
+            r.key += "_split"
+            r.workload += " [NNH_NUMERICS_SPLIT_DEPTH]"
+            r.cpu = None
+        return rows
 
     # config 3: conv2d_relu, batch 128: conv1 1 -> 32 on 28 x 28 (memory-bound), conv2 32 -> 64 on 14 x 14 after a
     # 2 x 2 max pool (seed 2)
@@ -716,6 +725,8 @@ def row_json(r):
     for k in ("bitwise_repeat", "bitwise_vs_nn_cpp"):
         if k in res:
             out[k] = res[k]
+    if "maxabs_vs_nn_cpp" in res and not res.get("bitwise_vs_nn_cpp", True):
+        out["maxabs_vs_nn_cpp"] = res["maxabs_vs_nn_cpp"]
     for k in ("cpu_baseline", "cpu_1thread"):
         if k in res:
             e = res[k]
@@ -786,6 +797,7 @@ def main():
     ap.add_argument("--size", type=int, default=4096)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-configs", action="store_true", help="only the headline product (no per-config rows)")
+    ap.add_argument("--no-split", action="store_true", help="no rows in the split-depth numerics mode")
     ap.add_argument("--csv", default=None, help="also write the rows as CSV (the reference's bench columns + GPU ones)")
     ap.add_argument("--report", action="store_true", help="every BASELINE config as a markdown table with fp64 "
                     "checks (not the driver's JSON line)")
@@ -862,6 +874,22 @@ def main():
     if not args.no_configs:
         rows = build_rows()
         run_gpu_rows(rows)
+    split_rows = []
+    if not args.no_configs and not args.no_split:
+        prev = nnh.set_numerics(nnh.NUMERICS_SPLIT_DEPTH)
+        try:
+            split_rows = build_rows(split=True)
+            run_gpu_rows(split_rows)
+        finally:
+            nnh.set_numerics(prev)
+        exact = {r.key: r for r in rows}
+        for r in split_rows:
+            e = exact.get(r.key[: -len("_split")])
+            if e is not None:
+                r.result["bitwise_vs_nn_cpp"] = all(np.array_equal(g.view(np.uint32), w.view(np.uint32))
+                                                    for g, w in zip(r.host_outs, e.host_outs))
+                r.result["maxabs_vs_nn_cpp"] = max(float(np.max(np.abs(g.astype(np.float64) - w)))
+                                                   for g, w in zip(r.host_outs, e.host_outs))
     headline = Row(5, "headline", f"nn::kernels::sgemm {m}^3", None, None, flops,
                    cpu=lambda ref, w, r, bud: ref.time_matmul(a, b, 0, 0, w, r, bud))
     setup = None
@@ -911,6 +939,7 @@ def main():
             "without_alive_flags": None if conv1_na is None else {
                 "us_per_launch": round(conv1_na.result["ms"] * 1e3, 3), "value": round(conv1_na.result["gbps"], 1)}},
         "configs": [row_json(r) for r in rows],
+        "configs_split_depth": [row_json(r) for r in split_rows],
         "workloads": [{k: ({kk: (round(vv, 4) if isinstance(vv, float) else vv) for kk, vv in v.items()}
                            if isinstance(v, dict) else (round(v, 2) if isinstance(v, float) else v))
                        for k, v in w.items()} for w in workloads],

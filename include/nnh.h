@@ -85,6 +85,20 @@ int nnh_conv2d_backward_workspace_size(size_t N, size_t Cin, size_t H, size_t W,
 int nnh_attention_forward_workspace_size(size_t N, size_t Tq, size_t Tk, size_t D, size_t heads, size_t* bytes);
 int nnh_attention_backward_workspace_size(size_t N, size_t Tq, size_t Tk, size_t D, size_t heads, size_t* bytes);
 
+/*
+ * Numerics mode (process-wide; set it before issuing work). NNH_NUMERICS_NNCPP (the default): every result is
+ * nn-cpp's bits, as described above. NNH_NUMERICS_SPLIT_DEPTH: every product with m n <= 2^18 and k >= 256 is
+ * computed the way nn-cpp's depth cut computes its products (src/kernels/gemm.cpp:453-485): 128-deep fused
+ * multiply-add chains from +0, added in piece order, then stored or added to C. Short chains let small and skinny
+ * products use the whole GPU. Results stay deterministic, a pure function of (m, n, k, trans_a, trans_b) and the
+ * inputs (so fused ops still equal their compositions), within 4 K 2^-24 sum|a||b| of the exact product, and equal
+ * to the oracle's in the same mode; they are no longer nn-cpp's bits for the products the wider rule adds.
+ */
+#define NNH_NUMERICS_NNCPP 0
+#define NNH_NUMERICS_SPLIT_DEPTH 1
+int nnh_set_numerics(int mode);
+int nnh_get_numerics(void);
+
 /* Message of the calling thread's last failed call ("" if none). */
 const char* nnh_last_error(void);
 /* Library version string. */

@@ -16,6 +16,7 @@ REPO_ROOT = os.path.dirname(PKG_ROOT)
 HEADER_PATH = os.path.join(REPO_ROOT, "include", "nnh.h")
 
 OK, ERR_INVALID, ERR_SHAPE, ERR_ALIAS, ERR_HIP, ERR_WORKSPACE = 0, 1, 2, 3, 4, 5
+NUMERICS_NNCPP, NUMERICS_SPLIT_DEPTH = 0, 1
 BIAS_NONE, BIAS_COL, BIAS_ROW = 0, 1, 2
 MAX_BATCH_DIMS = 4
 
@@ -96,6 +97,14 @@ _EXTRA_DECLS = {
     "nnh_im2col": [_vp, _sz, _sz, _sz, _sz, _sz, _sz, C.c_int, C.c_int, _vp, _vp],
     "nnh_col2im_add": [_vp, _sz, _sz, _sz, _sz, _sz, _sz, C.c_int, C.c_int, _vp, C.c_int, _vp],
 }
+
+
+def set_numerics(mode):
+    """NUMERICS_NNCPP (nn-cpp's bits) or NUMERICS_SPLIT_DEPTH (128-deep chains for small products); returns the
+    previous mode."""
+    prev = lib().nnh_get_numerics()
+    check(lib().nnh_set_numerics(int(mode)))
+    return prev
 
 
 def workspace_size(name, *args):

@@ -195,6 +195,14 @@ int nnh_matmul_workspace_size(const size_t* a_shape, int a_ndim, const size_t* b
 	return put_bytes(bytes, gemm_workspace_bytes(plan.m, plan.n, plan.k, count));
 }
 
+int nnh_set_numerics(int mode) {
+	if (mode != NNH_NUMERICS_NNCPP && mode != NNH_NUMERICS_SPLIT_DEPTH) return fail(NNH_ERR_INVALID, "no such numerics mode");
+	set_numerics(mode);
+	return NNH_OK;
+}
+
+int nnh_get_numerics(void) { return numerics(); }
+
 int nnh_gemm_config_count(void) { return gemm_config_count(); }
 
 const char* nnh_gemm_config_name(int config) { return gemm_config_name(config); }

@@ -18,6 +18,7 @@
 // Two workgroups share a CU (about 67 KB of LDS each at Tk = 256), so one's MFMA phases can overlap the other's
 // VALU phases.
 #include "attention.hpp"
+#include "gemm.hpp"
 
 #include "gemm_tile.hpp"
 #include "softmax_row.hpp"
@@ -451,6 +452,8 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) a
 bool attention_fused_ok(int64_t tq, int64_t tk, int64_t dh, int64_t d, const void* q, const void* k, const void* v,
                         const void* out, const void* probs, const void* pad) {
 	auto al = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
+	// the kernel runs S = Q K^T and O = P V as whole-depth chains: products that take the depth cut go elsewhere
+	if (depth_cut(tq, tk, dh) || depth_cut(tq, dh, tk)) return false;
 	return dh == kDh && tk >= 1 && tk <= kMaxKeys && tk % 4 == 0 && d % 4 == 0 && tq >= 1 && tq < (1 << 24) &&
 	       al(q) && al(k) && al(v) && al(out) && al(probs) && (pad == nullptr || al(pad));
 }

@@ -7,6 +7,7 @@
 #include "gemm_config.hpp"
 
 #include <algorithm>
+#include <atomic>
 #include <mutex>
 
 namespace nnh {
@@ -155,8 +156,17 @@ GemmArgs make_args(const GemmCall& g, const Config& cf, bool& cut, bool& interio
 
 }  // namespace
 
+namespace {
+std::atomic<int> g_numerics{kNumericsNnCpp};
+}  // namespace
+
+int set_numerics(int mode) { return g_numerics.exchange(mode); }
+int numerics() { return g_numerics.load(std::memory_order_relaxed); }
+
 bool depth_cut(int64_t m, int64_t n, int64_t k) {
-	return !(m == 0 || n == 0 || m * n > (int64_t(1) << 16) || k < 4 * 128 || m * n * k < (int64_t(1) << 20));
+	if (m == 0 || n == 0) return false;
+	if (numerics() == kNumericsSplitDepth && m * n <= (int64_t(1) << 18) && k >= 2 * 128) return true;
+	return !(m * n > (int64_t(1) << 16) || k < 4 * 128 || m * n * k < (int64_t(1) << 20));
 }
 
 int64_t gemm_workspace_floats(int64_t m, int64_t n, int64_t k, int64_t batch_count) {

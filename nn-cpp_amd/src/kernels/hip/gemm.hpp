@@ -30,8 +30,16 @@ struct GemmCall {
 	int rowsum_combine = 0;
 };
 
+// Numerics modes (nnh_set_numerics). kNumericsNnCpp: nn-cpp's bits. kNumericsSplitDepth: every product with
+// m n <= 2^18 and k >= 256 also takes the depth cut below, so its chains are at most 128 deep.
+constexpr int kNumericsNnCpp = 0;
+constexpr int kNumericsSplitDepth = 1;
+int set_numerics(int mode);  // returns the previous mode
+int numerics();
+
 // nn-cpp's depth-cut rule (src/kernels/gemm.cpp:453-458): small output, long depth -> 128-deep pieces
-// summed in piece order. Applies per matrix.
+// summed in piece order (and, in kNumericsSplitDepth, the wider rule above). Applies per matrix; every kernel
+// that runs a whole-depth chain declines a product this returns true for.
 bool depth_cut(int64_t m, int64_t n, int64_t k);
 
 // Floats of workspace a call needs (0 when it takes no depth cut).

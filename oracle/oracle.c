@@ -56,9 +56,16 @@ static void sgemm_flat(int ta, int tb, size_t m, size_t n, size_t k, const float
 	}
 }
 
+/* Numerics mode of the checked library: 0 nn-cpp's own rule below; 1 the split-depth rule (m n <= 2^18 and
+ * k >= 2 * kPiece also cut), under which every oracle function follows the library's NNH_NUMERICS_SPLIT_DEPTH. */
+static int g_split_depth = 0;
+void oracle_set_numerics(int mode) { g_split_depth = mode == 1; }
+
 /* The depth-cut predicate of gemm.cpp:456-458 (kDepthMaxOut = 2^16, 4 * kPiece, kDepthMinWork = 2^20). */
 int oracle_depth_cut(size_t m, size_t n, size_t k) {
-	return !(m == 0 || n == 0 || m * n > ((size_t)1 << 16) || k < 4 * KPIECE || m * n * k < ((size_t)1 << 20));
+	if (m == 0 || n == 0) return 0;
+	if (g_split_depth && m * n <= ((size_t)1 << 18) && k >= 2 * KPIECE) return 1;
+	return !(m * n > ((size_t)1 << 16) || k < 4 * KPIECE || m * n * k < ((size_t)1 << 20));
 }
 
 /* nn::kernels::sgemm (gemm.cpp:546-556 -> blocked, 453-485). */

@@ -57,6 +57,7 @@ class Oracle:
                                       _sz, _f]
         L.oracle_depth_cut.argtypes = [_sz, _sz, _sz]
         L.oracle_depth_cut.restype = C.c_int
+        L.oracle_set_numerics.argtypes = [C.c_int]
         L.oracle_sgemm_f64.argtypes = [C.c_int, C.c_int, _sz, _sz, _sz, _f, _sz, _f, _sz, _f, _sz, C.c_int, _d, _d]
         L.oracle_sum_axis0.argtypes = [_f, _sz, _sz, _f]
         L.oracle_lane_sum.argtypes = [_f, _sz]
@@ -102,6 +103,10 @@ class Oracle:
         self.lib.oracle_sgemm_at(int(ta), int(tb), m, n, k, _fp(a), lda, _fp(b), ldb, int(acc),
                                  rows.ctypes.data_as(_szp), cols.ctypes.data_as(_szp), _fp(cold), cnt, _fp(out))
         return out
+
+    def set_numerics(self, mode):
+        """0: nn-cpp's depth-cut rule; 1: the split-depth rule of the library's NNH_NUMERICS_SPLIT_DEPTH."""
+        self.lib.oracle_set_numerics(int(mode))
 
     def depth_cut(self, m, n, k):
         return bool(self.lib.oracle_depth_cut(m, n, k))

@@ -439,3 +439,47 @@ def test_softmax_backward_matches_nncpp(oracle, ref):
         assert rc == 0
         assert y.tobytes() == want_y.tobytes()
         assert got.tobytes() == want_dx.tobytes(), (N, H, Tq, Tk)
+
+
+# ---------------------------------------------------------------- the split-depth numerics mode
+
+@pytest.mark.parametrize("ta,tb,m,n,k,acc", [(0, 0, 64, 48, 300, 0), (1, 0, 33, 70, 256, 1), (0, 1, 100, 100, 784, 0),
+                                             (1, 1, 16, 512, 513, 1)])
+def test_split_depth_oracle_is_nncpp_pieces_in_order(oracle, ref, ta, tb, m, n, k, acc):
+    """In split mode a product with m n <= 2^18 and k >= 256 is nn-cpp's depth cut (gemm.cpp:466-484): each
+    128-deep slab of the depth is nn-cpp's own sgemm of that slab (a single chain from +0), the slabs are added in
+    order, then stored or added to C. Checked against nn-cpp's compiled sgemm on each slab, summed here in float32,
+    and against the fp64 bound."""
+    from helpers import Problem
+    p = Problem(ta, tb, m, n, k, 1, 5000 + m + n + k)
+    oracle.set_numerics(1)
+    try:
+        got = oracle.sgemm(ta, tb, m, n, k, p.a, p.lda, p.b, p.ldb, p.c, p.ldc, acc)
+    finally:
+        oracle.set_numerics(0)
+    opa = (p.a[:k, :m].T if ta else p.a[:m, :k])
+    opb = (p.b[:n, :k].T if tb else p.b[:k, :n])
+    total = None
+    for k0 in range(0, k, 128):
+        a_s = np.ascontiguousarray(opa[:, k0:k0 + 128])
+        b_s = np.ascontiguousarray(opb[k0:k0 + 128, :])
+        kk = a_s.shape[1]
+        piece = ref.sgemm(0, 0, m, n, kk, a_s, kk, b_s, n, np.zeros((m, n), np.float32), n, 0)
+        total = piece if total is None else (total + piece).astype(np.float32)
+    want = (p.c[:m, :n] + total).astype(np.float32) if acc else total
+    assert got[:m, :n].tobytes() == want.tobytes()
+    exact, mag = oracle.sgemm_f64(ta, tb, m, n, k, p.a, p.lda, p.b, p.ldb, p.c, p.ldc, acc)
+    assert np.all(np.abs(got[:m, :n].astype(np.float64) - exact) <= 4.0 * k * 2.0 ** -24 * mag)
+
+
+def test_split_depth_rule(oracle):
+    """The split rule widens nn-cpp's (gemm.cpp:456-458) and nothing else: m n <= 2^18 and k >= 256."""
+    oracle.set_numerics(1)
+    try:
+        assert oracle.depth_cut(512, 512, 256) and oracle.depth_cut(64, 4096, 4096) and oracle.depth_cut(256, 512, 784)
+        assert not oracle.depth_cut(512, 513, 4096)          # m n > 2^18
+        assert not oracle.depth_cut(512, 512, 255)           # one piece and a bit
+        assert oracle.depth_cut(40, 48, 1100)                # nn-cpp's own cut stays
+    finally:
+        oracle.set_numerics(0)
+    assert not oracle.depth_cut(512, 512, 256) and oracle.depth_cut(40, 48, 1100)
