@@ -55,8 +55,9 @@ typedef struct nnh_epilogue {
 } nnh_epilogue;
 
 /*
- * Scratch memory. Some calls need device scratch beyond their inputs and outputs (depth-cut partial sums, the
- * convolution backward's masked gradient and per-sample sums, attention's dS). Each (device, stream) pair has one
+ * Scratch memory. Some calls need device scratch beyond their inputs and outputs (the partial sums of a depth cut
+ * whose pieces are spread over workgroups, the convolution backward's masked gradient and per-sample sums,
+ * attention's dS). Each (device, stream) pair has one
  * scratch buffer, used by the calls on that stream in turn. By default the library owns it: allocated on the first
  * call that needs it, grown on demand, kept until the process ends.
  *

@@ -17,8 +17,9 @@ extern "C" {
 /*
  * nnh_sgemm (same arguments, same bits), with its only scratch, the depth-cut partial sums, in a static device
  * array of nnh_sgemm_noalloc_max_workspace() bytes (16 MiB) that each GPU holds until the process ends. It calls
- * no hipMalloc, hipFree or allocating library routine. A product whose partials exceed the array (m n k / 128 floats
- * or more, only for m n <= 65536 and k >= 512) returns NNH_ERR_INVALID without launching anything.
+ * no hipMalloc, hipFree or allocating library routine. Partial sums are written only by products cut into more
+ * than 16 pieces (nn-cpp's rule with k > 2048: m n k / 128 floats, rounded up to whole pieces); one whose partials
+ * exceed the array returns NNH_ERR_INVALID without launching anything.
  * All calls on one GPU share that GPU's array: calls on one stream run in order, but calls that overlap on one GPU
  * (different streams, unordered) race on it.
  */

@@ -25,8 +25,8 @@ int build_gemm(int ta, int tb, size_t m, size_t n, size_t k, const float* a, siz
 int run_gemm(const GemmCall& g, void* stream, int config, float* workspace = nullptr);
 // Bytes of stream workspace g's depth-cut partials take (0 without a depth cut).
 inline size_t gemm_workspace_bytes(const GemmCall& g) { return (size_t)gemm_workspace_floats(g) * sizeof(float); }
-inline size_t gemm_workspace_bytes(size_t m, size_t n, size_t k, size_t batch_count) {
-	return (size_t)gemm_workspace_floats((int64_t)m, (int64_t)n, (int64_t)k, (int64_t)batch_count) * sizeof(float);
+inline size_t gemm_workspace_bytes(size_t m, size_t n, size_t k, size_t batch_count, bool gather = false) {
+	return (size_t)gemm_workspace_floats((int64_t)m, (int64_t)n, (int64_t)k, (int64_t)batch_count, gather) * sizeof(float);
 }
 // NNH_ERR_WORKSPACE when the caller registered a workspace for the stream that holds fewer than `bytes`;
 // called by every entry point before it launches anything.

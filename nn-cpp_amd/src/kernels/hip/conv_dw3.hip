@@ -271,7 +271,7 @@ hipError_t conv_dw3(const float* gr, const unsigned char* alive, float* gmo, flo
 			raised[dev] = true;
 		}
 	}
-	const int hw = g.h * g.w, K = g.cin * 9;
+	const int K = g.cin * 9;
 	const int units = (K + 15) / 16;
 	const int pairs = (int)(samples * (cout / kD3Co));
 	D3Args a{gr, alive, alive ? gmo : nullptr, gb, x, gw, g.cin, g.h, g.w, cout, cout / kD3Co, (units + 1) / 2, pairs};

@@ -64,7 +64,7 @@ __global__ void __launch_bounds__(256) conv_fwd3_kernel(const F3Args a) {
 	float xv[kX], wv[kW];
 	auto load_half = [&](int cb, int ce) {
 		const int x0 = cb * kF3Plane, nx = (ce - cb) * kF3Plane;
-		const int w0 = cb * 9 * kF3Co, nw = (ce - cb) * 9 * kF3Co;
+		const int nw = (ce - cb) * 9 * kF3Co;
 #pragma unroll
 		for (int u = 0; u < kX; ++u) {
 			const int e = x0 + min(tid + 256 * u, nx - 1);

@@ -136,11 +136,12 @@ GemmArgs make_args(const GemmCall& g, const Config& cf, bool& cut, bool& interio
 	p.batch = g.batch;
 	p.ep = g.ep;
 	p.col = g.col;
-	cut = depth_cut(g.m, g.n, g.k);
+	const CutPlan plan = cut_plan(g.m, g.n, g.k);
+	cut = plan.pieces > 1;
 	p.rowsum = g.rowsum;
 	p.rowsum_combine = g.rowsum_combine;
-	p.pieces = cut ? (int)((g.k + 127) / 128) : 1;
-	p.piece_k = cut ? 128 : (int)std::max<int64_t>(g.k, 1);
+	p.pieces = cut ? (int)plan.pieces : 1;
+	p.piece_k = cut ? (int)plan.piece_k : (int)std::max<int64_t>(g.k, 1);
 	// 16-byte operand loads need 16-byte rows and strides (a gathered B is read element by element)
 	bool vec_ok = (g.lda % 4 == 0) && (reinterpret_cast<uintptr_t>(g.a) % 16 == 0) &&
 	              (g.gather || ((g.ldb % 4 == 0) && (reinterpret_cast<uintptr_t>(g.b) % 16 == 0)));
@@ -150,7 +151,8 @@ GemmArgs make_args(const GemmCall& g, const Config& cf, bool& cut, bool& interio
 	// interior kernels also write C with 16-byte stores
 	bool c_vec = (g.ldc % 4 == 0) && (reinterpret_cast<uintptr_t>(g.c) % 16 == 0);
 	for (int d = 0; d < g.batch.ndim; ++d) c_vec = c_vec && g.batch.sc[d] % 4 == 0;
-	interior = vec_ok && c_vec && g.m % cf.bm == 0 && g.n % cf.bn == 0 && g.k % cf.bk == 0 && g.k > 0;
+	interior = vec_ok && c_vec && g.m % cf.bm == 0 && g.n % cf.bn == 0 && g.k % cf.bk == 0 && g.k > 0 &&
+	           p.piece_k % cf.bk == 0;
 	return p;
 }
 
@@ -163,19 +165,33 @@ std::atomic<int> g_numerics{kNumericsNnCpp};
 int set_numerics(int mode) { return g_numerics.exchange(mode); }
 int numerics() { return g_numerics.load(std::memory_order_relaxed); }
 
-bool depth_cut(int64_t m, int64_t n, int64_t k) {
-	if (m == 0 || n == 0) return false;
-	if (numerics() == kNumericsSplitDepth && m * n <= (int64_t(1) << 18) && k >= 2 * 128) return true;
-	return !(m * n > (int64_t(1) << 16) || k < 4 * 128 || m * n * k < (int64_t(1) << 20));
+CutPlan cut_plan(int64_t m, int64_t n, int64_t k) {
+	CutPlan c;
+	if (m <= 0 || n <= 0 || k <= 0) return c;
+	if (numerics() == kNumericsSplitDepth) {
+		if (m * n > (int64_t(1) << 18) || k < 256) return c;
+		const int64_t tiles = ((m + 63) / 64) * ((n + 15) / 16);
+		const int64_t s = std::min<int64_t>(16, std::max<int64_t>(2, 4096 / tiles));
+		c.piece_k = ((k + s - 1) / s + 31) / 32 * 32;
+	} else {
+		if (m * n > (int64_t(1) << 16) || k < 4 * 128 || m * n * k < (int64_t(1) << 20)) return c;
+		c.piece_k = 128;
+	}
+	c.pieces = (k + c.piece_k - 1) / c.piece_k;
+	return c;
 }
 
-int64_t gemm_workspace_floats(int64_t m, int64_t n, int64_t k, int64_t batch_count) {
-	if (!depth_cut(m, n, k)) return 0;
-	const int64_t pieces = (k + 127) / 128;
-	return pieces * m * n * batch_count;
+bool depth_cut(int64_t m, int64_t n, int64_t k) { return cut_plan(m, n, k).pieces > 1; }
+
+int64_t gemm_workspace_floats(int64_t m, int64_t n, int64_t k, int64_t batch_count, bool gather) {
+	if (!depth_cut(m, n, k) || pieces_kernel_takes(m, n, k, batch_count, gather)) return 0;
+	return cut_plan(m, n, k).pieces * m * n * batch_count;
 }
 
-int64_t gemm_workspace_floats(const GemmCall& g) { return gemm_workspace_floats(g.m, g.n, g.k, g.batch_count); }
+int64_t gemm_workspace_floats(const GemmCall& g) {
+	if (!depth_cut(g.m, g.n, g.k) || pieces_kernel_takes(g)) return 0;
+	return cut_plan(g.m, g.n, g.k).pieces * g.m * g.n * g.batch_count;
+}
 
 int gemm_config_count() { return kNumConfigs; }
 const char* gemm_config_name(int config) {
@@ -192,6 +208,7 @@ hipError_t gemm_launch(const GemmCall& g, hipStream_t s, int config, float* work
 	if (g.gather && g.ta) return hipErrorInvalidValue;
 	if (g.rowsum && (depth_cut(g.m, g.n, g.k) || g.batch_count != 1 || g.gather || !g.ta || g.tb))
 		return hipErrorInvalidValue;
+	if (pieces_kernel_takes(g)) return gemm_pieces_launch(g, s);
 	bool cut = false, interior = false;
 	GemmArgs p = make_args(g, cf, cut, interior);
 

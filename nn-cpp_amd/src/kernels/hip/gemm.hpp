@@ -31,20 +31,38 @@ struct GemmCall {
 };
 
 // Numerics modes (nnh_set_numerics). kNumericsNnCpp: nn-cpp's bits. kNumericsSplitDepth: every product with
-// m n <= 2^18 and k >= 256 also takes the depth cut below, so its chains are at most 128 deep.
+// m n <= 2^18 and k >= 256 is cut into pieces whose depth is chosen so that the product fills the GPU (below).
 constexpr int kNumericsNnCpp = 0;
 constexpr int kNumericsSplitDepth = 1;
 int set_numerics(int mode);  // returns the previous mode
 int numerics();
 
-// nn-cpp's depth-cut rule (src/kernels/gemm.cpp:453-458): small output, long depth -> 128-deep pieces
-// summed in piece order (and, in kNumericsSplitDepth, the wider rule above). Applies per matrix; every kernel
-// that runs a whole-depth chain declines a product this returns true for.
+// How a product's depth is cut: `pieces` contiguous slices of `piece_k` depth indices (the last one shorter),
+// each a chain from +0, summed in piece order (acc = piece 0, acc += piece 1, ...), then stored or added to C.
+// pieces <= 1: no cut, one chain over the whole depth. A pure function of (m, n, k) and the numerics mode, per
+// matrix of a batch:
+//   kNumericsNnCpp: nn-cpp's rule (src/kernels/gemm.cpp:453-461): m n <= 2^16, k >= 512 and m n k >= 2^20 cut
+//     into 128-deep pieces.
+//   kNumericsSplitDepth: m n <= 2^18 and k >= 256, with T = ceil(m / 64) ceil(n / 16) tiles of 64 x 16 and
+//     s = min(16, max(2, 4096 / T)): piece_k = ceil(k / s) rounded up to a multiple of 32.
+struct CutPlan {
+	int64_t piece_k = 0;
+	int64_t pieces = 1;
+};
+CutPlan cut_plan(int64_t m, int64_t n, int64_t k);
+// cut_plan(m, n, k).pieces > 1. Every kernel that runs a whole-depth chain declines a product this is true for.
 bool depth_cut(int64_t m, int64_t n, int64_t k);
 
-// Floats of workspace a call needs (0 when it takes no depth cut).
+// Whether a depth-cut product runs as one launch of the pieces kernel (gemm_pieces.hip): not gathered, no row sums,
+// at most 16 pieces, dimensions below 2^24. Otherwise a cut product spreads its pieces over workgroups that write partial sums to the
+// workspace, and a second kernel adds them in piece order.
+bool pieces_kernel_takes(int64_t m, int64_t n, int64_t k, int64_t batch_count, bool gather_or_rowsum);
+bool pieces_kernel_takes(const GemmCall& g);  // also: leading dimensions below 2^24
+hipError_t gemm_pieces_launch(const GemmCall& g, hipStream_t s);
+
+// Floats of workspace a call needs: the partial sums of a depth cut the pieces kernel does not take, else 0.
 int64_t gemm_workspace_floats(const GemmCall& g);
-int64_t gemm_workspace_floats(int64_t m, int64_t n, int64_t k, int64_t batch_count);
+int64_t gemm_workspace_floats(int64_t m, int64_t n, int64_t k, int64_t batch_count, bool gather = false);
 
 // Launches on stream s. Kernel configuration: -1 picks one by shape; results never depend on it.
 // Workspace for a depth cut comes from workspace (if non-null, at least gemm_workspace_floats) or else from

@@ -2,7 +2,7 @@
 // capture, tight serving loops, harnesses that forbid hipMalloc).
 //
 // nnh_sgemm's only scratch is the depth-cut partial sums (one m x n partial per 128-deep piece, summed in piece
-// order by a second kernel). Here they live in `scratch`, a file-scope device array of kScratchFloats floats that
+// order by a second kernel), written by cut products whose pieces are spread over workgroups. Here they live in `scratch`, a file-scope device array of kScratchFloats floats that
 // every GPU the library runs on holds until the process ends. In host code the name `scratch` is a host-side
 // stand-in, not a device address: its address on a device comes from hipGetSymbolAddress, taken once per device
 // (with that device current) on the first call there, and only that address is passed to kernels.

@@ -93,7 +93,7 @@ BwdPlan conv_backward_plan(const ConvGeom& geo, size_t N, size_t Cout, bool aliv
 	p.off_gw = dw ? plan.add(N * Cout * K * 4) : 0;
 	p.dx_fused = dx && conv_dx_fused_ok(geo, (int64_t)N, (int)Cout);
 	p.off_col = dx && !p.dx_fused ? plan.add(N * K * hw * 4) : 0;
-	p.part = std::max(dw ? gemm_workspace_floats((int64_t)Cout, (int64_t)K, (int64_t)hw, (int64_t)N) : 0,
+	p.part = std::max(dw ? gemm_workspace_floats((int64_t)Cout, (int64_t)K, (int64_t)hw, (int64_t)N, true) : 0,
 	                  dx && !p.dx_fused ? gemm_workspace_floats((int64_t)K, (int64_t)hw, (int64_t)Cout, (int64_t)N) : 0);
 	p.off_part = p.part ? plan.add((size_t)p.part * 4) : 0;
 	p.total = plan.total;
@@ -105,7 +105,7 @@ BwdPlan conv_backward_plan(const ConvGeom& geo, size_t N, size_t Cout, bool aliv
 size_t conv_forward_ws(const ConvGeom& g, size_t N, size_t Cout) {
 	const size_t hw = (size_t)g.ho * g.wo, K = (size_t)g.cin * g.kh * g.kw;
 	if (N == 0 || Cout == 0 || hw == 0 || K <= kDirectMaxK) return 0;
-	return gemm_workspace_bytes(Cout, hw, K, N);
+	return gemm_workspace_bytes(Cout, hw, K, N, true);
 }
 
 }  // namespace

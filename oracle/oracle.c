@@ -56,16 +56,32 @@ static void sgemm_flat(int ta, int tb, size_t m, size_t n, size_t k, const float
 	}
 }
 
-/* Numerics mode of the checked library: 0 nn-cpp's own rule below; 1 the split-depth rule (m n <= 2^18 and
- * k >= 2 * kPiece also cut), under which every oracle function follows the library's NNH_NUMERICS_SPLIT_DEPTH. */
+/* Numerics mode of the checked library: 0 nn-cpp's own depth cut (below), 1 the split-depth rule, under which
+ * every oracle function follows the library's NNH_NUMERICS_SPLIT_DEPTH. */
 static int g_split_depth = 0;
 void oracle_set_numerics(int mode) { g_split_depth = mode == 1; }
 
-/* The depth-cut predicate of gemm.cpp:456-458 (kDepthMaxOut = 2^16, 4 * kPiece, kDepthMinWork = 2^20). */
+/* Depth of one piece of a cut product, or 0 when the product is not cut (one chain over the whole depth).
+ * nn-cpp (gemm.cpp:456-461): m n <= kDepthMaxOut = 2^16, k >= 4 kPiece and m n k >= kDepthMinWork = 2^20 cut
+ * into kPiece = 128-deep pieces. Split mode: m n <= 2^18 and k >= 256, with T = ceil(m / 64) ceil(n / 16) and
+ * s = min(16, max(2, 4096 / T)), pieces of ceil(k / s) rounded up to a multiple of 32. */
+size_t oracle_piece_depth(size_t m, size_t n, size_t k) {
+	if (m == 0 || n == 0 || k == 0) return 0;
+	if (g_split_depth) {
+		if (m * n > ((size_t)1 << 18) || k < 256) return 0;
+		const size_t tiles = ((m + 63) / 64) * ((n + 15) / 16);
+		size_t s = 4096 / tiles;
+		s = s < 2 ? 2 : s > 16 ? 16 : s;
+		return ((k + s - 1) / s + 31) / 32 * 32;
+	}
+	if (m * n > ((size_t)1 << 16) || k < 4 * KPIECE || m * n * k < ((size_t)1 << 20)) return 0;
+	return KPIECE;
+}
+
+/* Whether the product is cut into more than one piece. */
 int oracle_depth_cut(size_t m, size_t n, size_t k) {
-	if (m == 0 || n == 0) return 0;
-	if (g_split_depth && m * n <= ((size_t)1 << 18) && k >= 2 * KPIECE) return 1;
-	return !(m * n > ((size_t)1 << 16) || k < 4 * KPIECE || m * n * k < ((size_t)1 << 20));
+	const size_t pk = oracle_piece_depth(m, n, k);
+	return pk > 0 && pk < k;
 }
 
 /* nn::kernels::sgemm (gemm.cpp:546-556 -> blocked, 453-485). */
@@ -75,12 +91,12 @@ void oracle_sgemm(int ta, int tb, size_t m, size_t n, size_t k, const float* a, 
 		sgemm_flat(ta, tb, m, n, k, a, lda, b, ldb, c, ldc, accumulate);
 		return;
 	}
-	const size_t pieces = (k + KPIECE - 1) / KPIECE;
+	const size_t pk = oracle_piece_depth(m, n, k), pieces = (k + pk - 1) / pk;
 	for (size_t i = 0; i < m; ++i) {
 		for (size_t j = 0; j < n; ++j) {
 			float acc = 0.0f;
 			for (size_t p = 0; p < pieces; ++p) {
-				const size_t pc = p * KPIECE, kc = (k - pc < KPIECE) ? k - pc : KPIECE;
+				const size_t pc = p * pk, kc = (k - pc < pk) ? k - pc : pk;
 				float t = 0.0f;                                 /* each piece: its own overwrite product */
 				for (size_t q = pc; q < pc + kc; ++q) t = fmaf(op_a(ta, a, lda, i, q), op_b(tb, b, ldb, q, j), t);
 				acc = p == 0 ? t : acc + t;                     /* gemm.cpp:475-480, piece order */
@@ -114,9 +130,9 @@ void oracle_sgemm_at(int ta, int tb, size_t m, size_t n, size_t k, const float* 
 			v = run;
 		} else {
 			float acc = 0.0f;
-			const size_t pieces = (k + KPIECE - 1) / KPIECE;
+			const size_t pk = oracle_piece_depth(m, n, k), pieces = (k + pk - 1) / pk;
 			for (size_t p = 0; p < pieces; ++p) {
-				const size_t pc = p * KPIECE, kc = (k - pc < KPIECE) ? k - pc : KPIECE;
+				const size_t pc = p * pk, kc = (k - pc < pk) ? k - pc : pk;
 				float x = 0.0f;
 				for (size_t q = pc; q < pc + kc; ++q) x = fmaf(op_a(ta, a, lda, i, q), op_b(tb, b, ldb, q, j), x);
 				acc = p == 0 ? x : acc + x;

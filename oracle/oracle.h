@@ -24,6 +24,7 @@ extern "C" {
 void oracle_sgemm(int trans_a, int trans_b, size_t m, size_t n, size_t k, const float* a, size_t lda,
                   const float* b, size_t ldb, float* c, size_t ldc, int accumulate);
 int oracle_depth_cut(size_t m, size_t n, size_t k);
+size_t oracle_piece_depth(size_t m, size_t n, size_t k);
 void oracle_set_numerics(int mode);
 void oracle_sgemm_at(int trans_a, int trans_b, size_t m, size_t n, size_t k, const float* a, size_t lda,
                      const float* b, size_t ldb, int accumulate, const size_t* rows, const size_t* cols,

@@ -57,6 +57,8 @@ class Oracle:
                                       _sz, _f]
         L.oracle_depth_cut.argtypes = [_sz, _sz, _sz]
         L.oracle_depth_cut.restype = C.c_int
+        L.oracle_piece_depth.argtypes = [_sz, _sz, _sz]
+        L.oracle_piece_depth.restype = _sz
         L.oracle_set_numerics.argtypes = [C.c_int]
         L.oracle_sgemm_f64.argtypes = [C.c_int, C.c_int, _sz, _sz, _sz, _f, _sz, _f, _sz, _f, _sz, C.c_int, _d, _d]
         L.oracle_sum_axis0.argtypes = [_f, _sz, _sz, _f]
@@ -110,6 +112,10 @@ class Oracle:
 
     def depth_cut(self, m, n, k):
         return bool(self.lib.oracle_depth_cut(m, n, k))
+
+    def piece_depth(self, m, n, k):
+        """Depth of one piece of a cut product (0: not cut)."""
+        return int(self.lib.oracle_piece_depth(m, n, k))
 
     def sgemm_f64(self, ta, tb, m, n, k, a, lda, b, ldb, c, ldc, acc):
         """fp64 op(A) op(B) (+ C) as a dense m x n array, with the magnitude sum |a||b| (+|c|)."""

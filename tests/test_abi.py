@@ -97,15 +97,19 @@ def test_matmul_shapes_and_errors_match_nncpp(ref):
 
 def test_workspace_queries_on_the_host():
     """The *_workspace_size queries need no device: nn-cpp's depth cut (gemm.cpp:453-458) decides the GEMM's partials,
-    128-deep pieces of m n floats each, and the multi-step ops take the largest of their pieces."""
+    128-deep pieces of m n floats each where there are more than 16 pieces (up to 16, one launch adds them in LDS),
+    and the multi-step ops take the largest of their pieces."""
     import nnh
     assert nnh.workspace_size("sgemm", 64, 64, 4096, 1) == 32 * 64 * 64 * 4
-    assert nnh.workspace_size("sgemm", 40, 48, 1100, 3) == 9 * 40 * 48 * 4 * 3
+    assert nnh.workspace_size("sgemm", 40, 48, 2200, 3) == 18 * 40 * 48 * 4 * 3
     assert nnh.workspace_size("sgemm", 512, 512, 512, 1) == 0          # m n > 2^16: no cut
     assert nnh.workspace_size("sgemm", 16, 16, 2048, 1) == 0           # m n k < 2^20: no cut
-    assert nnh.workspace_size("matmul", [2, 40, 1100], 3, [1100, 48], 2, 0, 0) == 9 * 80 * 48 * 4  # folded: 80 x 48 x 1100
-    assert nnh.workspace_size("matmul", [3, 40, 1100], 3, [3, 1100, 48], 3, 0, 0) == 9 * 40 * 48 * 4 * 3
-    assert nnh.workspace_size("linear_forward", 40, 1100, 48) == 9 * 40 * 48 * 4
+    assert nnh.workspace_size("sgemm", 256, 10, 1024, 1) == 0          # 8 pieces: one launch, no partials
+    assert nnh.workspace_size("sgemm", 40, 48, 2048, 64) == 0          # 16 pieces: one launch
+    assert nnh.workspace_size("matmul", [2, 40, 2200], 3, [2200, 48], 2, 0, 0) == 18 * 80 * 48 * 4  # folded: 80 x 48
+    assert nnh.workspace_size("matmul", [3, 40, 2200], 3, [3, 2200, 48], 3, 0, 0) == 18 * 40 * 48 * 4 * 3
+    assert nnh.workspace_size("linear_forward", 40, 2200, 48) == 18 * 40 * 48 * 4
+    assert nnh.workspace_size("linear_forward", 40, 1100, 48) == 0     # 9 pieces: one launch
     # linear backward: dW = G^T X is 48 x 1100 x 40 (no cut), dX = G W is 40 x 1100 x 48 (no cut); a 3-D input's
     # bias gradient takes two buffers of lead[1] * n floats
     assert nnh.workspace_size("linear_backward", [40], 1, 1100, 48, 1, 1, 1) == 0

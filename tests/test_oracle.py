@@ -444,25 +444,27 @@ def test_softmax_backward_matches_nncpp(oracle, ref):
 # ---------------------------------------------------------------- the split-depth numerics mode
 
 @pytest.mark.parametrize("ta,tb,m,n,k,acc", [(0, 0, 64, 48, 300, 0), (1, 0, 33, 70, 256, 1), (0, 1, 100, 100, 784, 0),
-                                             (1, 1, 16, 512, 513, 1)])
+                                             (1, 1, 16, 512, 513, 1), (0, 0, 512, 512, 600, 1), (1, 0, 256, 1024, 300, 0)])
 def test_split_depth_oracle_is_nncpp_pieces_in_order(oracle, ref, ta, tb, m, n, k, acc):
-    """In split mode a product with m n <= 2^18 and k >= 256 is nn-cpp's depth cut (gemm.cpp:466-484): each
-    128-deep slab of the depth is nn-cpp's own sgemm of that slab (a single chain from +0), the slabs are added in
-    order, then stored or added to C. Checked against nn-cpp's compiled sgemm on each slab, summed here in float32,
-    and against the fp64 bound."""
+    """In split mode a product with m n <= 2^18 and k >= 256 is cut as nn-cpp's depth cut is (gemm.cpp:466-484),
+    with the split rule's piece depth: each slab of the depth is nn-cpp's own sgemm of that slab (a single chain
+    from +0, the slab too short for nn-cpp to cut), the slabs are added in order, then stored or added to C.
+    Checked against nn-cpp's compiled sgemm on each slab, summed here in float32, and against the fp64 bound."""
     from helpers import Problem
     p = Problem(ta, tb, m, n, k, 1, 5000 + m + n + k)
     oracle.set_numerics(1)
     try:
+        pk = oracle.piece_depth(m, n, k)
         got = oracle.sgemm(ta, tb, m, n, k, p.a, p.lda, p.b, p.ldb, p.c, p.ldc, acc)
     finally:
         oracle.set_numerics(0)
+    assert 0 < pk < k and not oracle.depth_cut(m, n, pk)
     opa = (p.a[:k, :m].T if ta else p.a[:m, :k])
     opb = (p.b[:n, :k].T if tb else p.b[:k, :n])
     total = None
-    for k0 in range(0, k, 128):
-        a_s = np.ascontiguousarray(opa[:, k0:k0 + 128])
-        b_s = np.ascontiguousarray(opb[k0:k0 + 128, :])
+    for k0 in range(0, k, pk):
+        a_s = np.ascontiguousarray(opa[:, k0:k0 + pk])
+        b_s = np.ascontiguousarray(opb[k0:k0 + pk, :])
         kk = a_s.shape[1]
         piece = ref.sgemm(0, 0, m, n, kk, a_s, kk, b_s, n, np.zeros((m, n), np.float32), n, 0)
         total = piece if total is None else (total + piece).astype(np.float32)
@@ -473,13 +475,31 @@ def test_split_depth_oracle_is_nncpp_pieces_in_order(oracle, ref, ta, tb, m, n, 
 
 
 def test_split_depth_rule(oracle):
-    """The split rule widens nn-cpp's (gemm.cpp:456-458) and nothing else: m n <= 2^18 and k >= 256."""
+    """The split rule: m n <= 2^18 and k >= 256; with T tiles of 64 x 16 and s = min(16, max(2, 4096 // T)), the
+    pieces are ceil(k / s) rounded up to a multiple of 32 deep. Hand-computed cases; nn-cpp's own rule returns
+    when the mode is reset."""
     oracle.set_numerics(1)
     try:
-        assert oracle.depth_cut(512, 512, 256) and oracle.depth_cut(64, 4096, 4096) and oracle.depth_cut(256, 512, 784)
-        assert not oracle.depth_cut(512, 513, 4096)          # m n > 2^18
-        assert not oracle.depth_cut(512, 512, 255)           # one piece and a bit
-        assert oracle.depth_cut(40, 48, 1100)                # nn-cpp's own cut stays
+        # (m, n, k) -> piece depth, with the tile count T and piece count target s worked out by hand
+        cases = {(512, 512, 512): 32,      # T = 8 * 32 = 256, s = 16, 32
+                 (512, 512, 256): 32,      # s = 16, 16 -> 32
+                 (64, 4096, 4096): 256,    # T = 1 * 256, s = 16, 256
+                 (256, 512, 784): 64,      # T = 4 * 32 = 128, s = 16, ceil(784 / 16) = 49 -> 64
+                 (256, 256, 512): 32,      # T = 64, s = 16, 32
+                 (256, 10, 256): 32,       # T = 4, s = 16, 16 -> 32
+                 (40, 48, 1100): 96,       # T = 3, s = 16, 69 -> 96
+                 (16, 512, 513): 64,       # T = 32, s = 16, 33 -> 64
+                 (1024, 256, 1000): 64,    # T = 16 * 16 = 256, s = 16, 63 -> 64
+                 (512, 512, 2000): 128,    # s = 16, 125 -> 128
+                 (65, 4000, 1000): 128,    # ragged: T = 2 * 250 = 500, s = 8, 125 -> 128
+                 (1, 262144, 300): 160}    # T = 16384, s = 2 (the floor), 150 -> 160
+        for (m, n, k), pk in cases.items():
+            assert oracle.piece_depth(m, n, k) == pk, (m, n, k)
+            assert oracle.depth_cut(m, n, k)
+        assert oracle.piece_depth(2048, 2048, 16) == 0                    # m n > 2^18 (also at k 16)
+        assert not oracle.depth_cut(512, 513, 4096)                       # m n > 2^18
+        assert not oracle.depth_cut(512, 512, 255)                        # k < 256
     finally:
         oracle.set_numerics(0)
     assert not oracle.depth_cut(512, 512, 256) and oracle.depth_cut(40, 48, 1100)
+    assert oracle.piece_depth(40, 48, 1100) == 128 and oracle.piece_depth(512, 512, 512) == 0

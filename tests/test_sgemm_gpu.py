@@ -268,3 +268,74 @@ def test_baseline_config5_whole_output(gpu, oracle, m, n, k):
         want = oracle.sgemm(0, 0, m, n, k, a, k, b, n, c0, n, 0)
     got = dc.cpu().numpy()
     assert bits_equal(got, want), first_diff(got, want)
+
+
+def _batched_cut_case(ta, tb, m, n, k, pad, count, seed):
+    """count matrices of A (each its own values), one B shared by all (batch stride 0), C per matrix."""
+    a_rows, a_cols = (k, m) if ta else (m, k)
+    b_rows, b_cols = (n, k) if tb else (k, n)
+    lda, ldb, ldc = a_cols + pad, b_cols + pad, n + pad
+    vals = synth.mt19937_uniform(seed, count * a_rows * a_cols + b_rows * b_cols + count * m * n, -1.0, 1.0)
+    a = np.full((count, a_rows, lda), SENTINEL, np.float32)
+    a[:, :, :a_cols] = vals[: count * a_rows * a_cols].reshape(count, a_rows, a_cols)
+    o = count * a_rows * a_cols
+    b = np.full((b_rows, ldb), SENTINEL, np.float32)
+    b[:, :b_cols] = vals[o: o + b_rows * b_cols].reshape(b_rows, b_cols)
+    o += b_rows * b_cols
+    c = np.full((count, m, ldc), SENTINEL, np.float32)
+    c[:, :, :n] = vals[o:].reshape(count, m, n)
+    return a, lda, b, ldb, c, ldc
+
+
+@pytest.mark.parametrize("ta,tb", [(0, 0), (1, 0), (0, 1), (1, 1)])
+def test_depth_cut_in_one_launch(gpu, oracle, ta, tb):
+    """Cut products of at most 16 pieces run as one launch, one wave per piece, that adds the pieces in LDS (no
+    partial sums in HBM): a batch of 64 products of 64 x 64 x 1200 (10 pieces) with B shared by the batch, 16-byte
+    and element loads, accumulate; 16 pieces (the most one launch takes); and one product of 40 x 50 x 1000
+    (8 pieces) with each bias mode and ReLU with its mask. Every element against the oracle, bit for bit."""
+    import torch
+
+    import nnh
+    m, n, k, count = 64, 64, 1200, 64
+    assert nnh.workspace_size("sgemm", m, n, k, count) == 0
+    for pad in (0, 1):
+        a, lda, b, ldb, c, ldc = _batched_cut_case(ta, tb, m, n, k, pad, count, 90000 + 10 * pad + 2 * ta + tb)
+        batch = nnh.make_batch((count,), (a[0].size,), (0,), (c[0].size,))
+        for acc in (0, 1):
+            da, db, dc = (torch.from_numpy(x).cuda() for x in (a, b, np.array(c, copy=True)))
+            nnh.sgemm_batched(ta, tb, m, n, k, da, lda, db, ldb, dc, ldc, acc, batch)
+            got = dc.cpu().numpy()
+            for i in range(count):
+                want = oracle.sgemm(ta, tb, m, n, k, np.ascontiguousarray(a[i]), lda, b, ldb,
+                                    np.ascontiguousarray(c[i]), ldc, acc)
+                assert bits_equal(got[i], want), (pad, acc, i, first_diff(got[i], want))
+    p = Problem(ta, tb, 33, 70, 2048, 1, 90500 + 2 * ta + tb)
+    assert nnh.workspace_size("sgemm", 33, 70, 2048, 1) == 0
+    for acc in (0, 1):
+        got, want = gpu_sgemm(p, acc), oracle_sgemm(oracle, p, acc)
+        assert bits_equal(got, want), ("16 pieces", acc, first_diff(got, want))
+    m, n, k = 40, 50, 1000
+    assert nnh.workspace_size("sgemm", m, n, k, 1) == 0
+    p = Problem(ta, tb, m, n, k, 0, 91000 + 2 * ta + tb)
+    bias_col = synth.mt19937_uniform(91010, n, -1.0, 1.0)
+    bias_row = synth.mt19937_uniform(91011, m, -1.0, 1.0)
+    for mode, bias in ((nnh.BIAS_NONE, None), (nnh.BIAS_COL, bias_col), (nnh.BIAS_ROW, bias_row)):
+        for relu in (False, True):
+            for acc in (0, 1):
+                dbias = torch.from_numpy(bias).cuda() if bias is not None else None
+                dalive = torch.full((m, p.ldc), 7, dtype=torch.uint8, device="cuda")
+                ep = nnh.make_epilogue(mode, dbias, relu, dalive if relu else None)
+                got = gpu_sgemm(p, acc, epilogue=ep)
+                want = oracle_sgemm(oracle, p, acc).copy()
+                v = want[:m, :n]
+                if mode == nnh.BIAS_COL:
+                    v += bias_col[None, :]
+                elif mode == nnh.BIAS_ROW:
+                    v += bias_row[:, None]
+                if relu:
+                    on = v > 0
+                    v[~on] = 0.0
+                    alive = dalive.cpu().numpy()
+                    assert np.array_equal(alive[:, :n], on.astype(np.uint8)), (mode, acc)
+                    assert np.all(alive[:, n:] == 7)
+                assert bits_equal(got, want), (mode, relu, acc, first_diff(got, want))

@@ -37,9 +37,9 @@ def host(t):
 def test_split_sgemm_matches_oracle(split, oracle, ta, tb):
     import nnh
     shapes = [(512, 512, 512), (64, 4096, 600), (256, 512, 784), (256, 10, 256), (33, 70, 300), (7, 9, 1100),
-              (512, 513, 300), (100, 100, 255)]
+              (512, 513, 300), (100, 100, 255), (512, 512, 1200)]
     for i, (m, n, k) in enumerate(shapes):
-        p = Problem(ta, tb, m, n, k, 1, 7000 + 10 * i + 2 * ta + tb)
+        p = Problem(ta, tb, m, n, k, i % 2, 7000 + 10 * i + 2 * ta + tb)
         for acc in (0, 1):
             want = oracle_sgemm(oracle, p, acc)
             got = gpu_sgemm(p, acc)

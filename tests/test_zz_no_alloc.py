@@ -25,9 +25,10 @@ def _run(fn, p, acc):
     return c.cpu().numpy()
 
 
-# (ta, tb, m, n, k): the first two take nn-cpp's depth cut (m n <= 2^16, k >= 512, m n k >= 2^20); the second is
-# smaller than the first; the last has no cut (no scratch at all)
-CASES = [(0, 0, 64, 64, 4096), (1, 0, 40, 48, 1100), (0, 1, 33, 70, 300)]
+# (ta, tb, m, n, k): the first two take nn-cpp's depth cut (m n <= 2^16, k >= 512, m n k >= 2^20) into more than 16
+# pieces, so their pieces write partial sums to the scratch; the second is smaller than the first; the third is
+# cut into 9 pieces, added in one launch without scratch; the last has no cut
+CASES = [(0, 0, 64, 64, 4096), (1, 0, 40, 48, 2200), (0, 1, 40, 48, 1100), (0, 1, 33, 70, 300)]
 
 
 def test_noalloc_matches_sgemm_on_successive_calls(gpu, oracle):
