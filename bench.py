@@ -452,6 +452,17 @@ def build_rows(report=False, split=False):
                     " (argmax kept)", pool1, lambda: [x2, arg1], 0, nbytes=pool_bytes, bound="hbm",
                     cpu=lambda ref, w, r, bud: (lambda f, b: (f[0], [f[1], None]))(*pool_cpu(ref, w, r, bud)),
                     est_ms=0.005))
+    y1f, al1f = torch.empty_like(y1), torch.empty_like(al1)
+    x2f, arg1f = torch.empty_like(x2), torch.empty_like(arg1)
+
+    def conv1_pool1():
+        nnh.check(L.nnh_conv2d_relu_maxpool2d_forward(P(dxc), N, 1, 28, 28, P(dw1), 32, 3, 3, P(db1), 1, 1, 2, 2,
+                                                      P(y1f), P(al1f), P(x2f), C.c_void_p(arg1f.data_ptr()), st()))
+
+    rows.append(Row(3, "conv1_pool1_forward", "conv2d_relu forward of conv1 and the 2x2 s2 maxpool on its output in one "
+                    "pass: y [128,32,28,28] with alive flags, pooled [128,32,14,14] with argmax",
+                    conv1_pool1, lambda: [y1f, al1f, x2f, arg1f], conv1_flops, nbytes=conv1_bytes + 4 * hx2.size,
+                    bound="hbm", est_ms=0.007))
     rows.append(Row(3, "pool1_backward", "maxpool2d backward 2x2 s2: dx [128,32,28,28] from g [128,32,14,14]",
                     pool1_bwd, lambda: [gxp], 0, nbytes=pool_bytes, bound="hbm",
                     cpu=lambda ref, w, r, bud: (lambda f, b: (b[0], [b[1]]))(*pool_cpu(ref, w, r, bud)),
@@ -722,7 +733,7 @@ def row_json(r):
         if k in res:
             out[k] = round(res[k], 3)
     out["roofline"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in res["roofline"].items()}
-    for k in ("bitwise_repeat", "bitwise_vs_nn_cpp"):
+    for k in ("bitwise_repeat", "bitwise_vs_nn_cpp", "bitwise_vs_two_ops"):
         if k in res:
             out[k] = res[k]
     if "maxabs_vs_nn_cpp" in res and not res.get("bitwise_vs_nn_cpp", True):
@@ -801,6 +812,9 @@ def main():
     ap.add_argument("--csv", default=None, help="also write the rows as CSV (the reference's bench columns + GPU ones)")
     ap.add_argument("--report", action="store_true", help="every BASELINE config as a markdown table with fp64 "
                     "checks (not the driver's JSON line)")
+    ap.add_argument("--row", default=None, metavar="KEY", help="time one configuration row only (its key, e.g. "
+                    "conv1_forward, or matmul512_nt_split in the split-depth mode) and print its JSON: the command "
+                    "the per-kernel profiles under profiles/ are taken with")
     ap.add_argument("--floor", action="store_true", help="launch-cost floor of this GPU: empty kernel, fills, copies")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="only run 5 device-to-device copies of MIB MiB (calibrates rocprofv3 FETCH_SIZE/WRITE_SIZE)")
@@ -814,6 +828,24 @@ def main():
         return
     if args.floor:
         floor()
+        return
+    if args.row:
+        import torch  # noqa: F401 (torch's HIP runtime first, as everywhere else; libnnh then shares it)
+
+        import nnh
+        split = args.row.endswith("_split")
+        prev = nnh.set_numerics(nnh.NUMERICS_SPLIT_DEPTH if split else nnh.NUMERICS_NNCPP)
+        try:
+            rows = build_rows(split=split)
+            keys = [r.key for r in rows]
+            rows = [r for r in rows if r.key == args.row]
+            if not rows:
+                print(f"bench.py: no row {args.row!r}; rows: {', '.join(keys)}", file=sys.stderr)
+                sys.exit(2)
+            run_gpu_rows(rows)
+        finally:
+            nnh.set_numerics(prev)
+        print(json.dumps(row_json(rows[0])), flush=True)
         return
     if args.copy_probe:
         import torch
@@ -871,9 +903,21 @@ def main():
     del dc
 
     rows = []
+    fill_floor_ms = None
     if not args.no_configs:
         rows = build_rows()
         run_gpu_rows(rows)
+        by_key = {r.key: r for r in rows}
+        fused = by_key.get("conv1_pool1_forward")
+        if fused is not None and "conv1_forward" in by_key and "pool1_forward" in by_key:
+            want = by_key["conv1_forward"].host_outs[:1] + [None] + by_key["pool1_forward"].host_outs
+            fused.result["bitwise_vs_two_ops"] = all(w is None or np.array_equal(g.view(np.uint8), w.view(np.uint8))
+                                                     for g, w in zip(fused.host_outs, want))
+        # the launch floor of conv1's output size on this GPU: a plain fill of y (12.85 MB)
+        ny = 128 * 32 * 28 * 28
+        fill_buf = torch.empty(ny, device=dev)
+        fill_floor_ms = median(device_times(lambda: fill_buf.fill_(1.0), 0.004))
+        del fill_buf
     split_rows = []
     if not args.no_configs and not args.no_split:
         prev = nnh.set_numerics(nnh.NUMERICS_SPLIT_DEPTH)
@@ -909,6 +953,9 @@ def main():
                           f"runs after {hb['warmup']} warm-up")}
     conv1 = next((r for r in rows if r.key == "conv1_forward"), None)
     conv1_na = next((r for r in rows if r.key == "conv1_forward_no_alive"), None)
+    pool1 = next((r for r in rows if r.key == "pool1_forward"), None)
+    conv1_pool1 = next((r for r in rows if r.key == "conv1_pool1_forward"), None)
+    fill_gbps = None if fill_floor_ms is None else 4 * 128 * 32 * 784 / (fill_floor_ms * 1e-3) / 1e9
     out = {
         "metric": "fp32 GEMM TFLOP/s @4096^3 (nn::kernels::sgemm replacement, bit-exact with nn-cpp)",
         "value": round(value, 3),
@@ -937,7 +984,16 @@ def main():
             "roofline": {"bound": "hbm", "peak": PEAK_HBM_GBPS, "unit": "GB/s",
                          "frac": round(conv1.result["roofline"]["frac"], 4)},
             "without_alive_flags": None if conv1_na is None else {
-                "us_per_launch": round(conv1_na.result["ms"] * 1e3, 3), "value": round(conv1_na.result["gbps"], 1)}},
+                "us_per_launch": round(conv1_na.result["ms"] * 1e3, 3), "value": round(conv1_na.result["gbps"], 1)},
+            "fill_floor": None if fill_floor_ms is None else {
+                "what": "torch fill of conv1's y (12.85 MB) on this GPU, the fastest a launch writing it runs",
+                "us_per_launch": round(fill_floor_ms * 1e3, 3), "value": round(fill_gbps, 1),
+                "frac_of_peak": round(fill_gbps / PEAK_HBM_GBPS, 4),
+                "conv1_frac_of_floor": round(conv1.result["gbps"] / fill_gbps, 4)},
+            "with_pool": None if conv1_pool1 is None or pool1 is None else {
+                "workload": conv1_pool1.workload, "us_per_launch": round(conv1_pool1.result["ms"] * 1e3, 3),
+                "separate_us": round((conv1.result["ms"] + pool1.result["ms"]) * 1e3, 3),
+                "bitwise_vs_two_ops": conv1_pool1.result.get("bitwise_vs_two_ops")}},
         "configs": [row_json(r) for r in rows],
         "configs_split_depth": [row_json(r) for r in split_rows],
         "workloads": [{k: ({kk: (round(vv, 4) if isinstance(vv, float) else vv) for kk, vv in v.items()}

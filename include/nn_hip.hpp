@@ -5,6 +5,7 @@
 //   * Tensor and matmul(a, b, trans_a, trans_b)                  include/nn/tensor.hpp:47-510, 465-491
 //   * Value, NoGradGuard, grad_accum and backward                include/nn/autograd/value.hpp:41-228
 //   * matmul, linear, matmul_bt, relu, reshape, conv2d, conv2d_relu, maxpool2d, attention, scaled_masked_softmax
+//     (and conv2d_relu_maxpool2d, the two ops of a first layer in one call)
 //                                                                include/nn/autograd/ops.hpp:22-523
 // The difference is where the numbers live: a Tensor's storage is HBM, so a chain of ops (linear -> relu ->
 // linear, conv -> pool -> conv) never leaves the device; data crosses PCIe only in from_host / to_host. Every op
@@ -139,6 +140,11 @@ Value conv2d(const Value& x, const Value& weight, const Value& bias, int stride,
 Value conv2d_relu(const Value& x, const Value& weight, const Value& bias, int stride, int padding);
 // ops.cpp:1609-1705: max pooling, kernel x kernel windows at `stride`.
 Value maxpool2d(const Value& x, size_t kernel_size, size_t stride);
+// maxpool2d(conv2d_relu(x, weight, bias, stride, padding), kernel_size, pool_stride): the same two graph nodes, the
+// same values and gradients, with both forwards in one pass where nnh_conv2d_relu_maxpool2d_forward fuses them (a
+// network's first layer). No counterpart in the reference, whose Sequential runs the two modules in turn.
+Value conv2d_relu_maxpool2d(const Value& x, const Value& weight, const Value& bias, int stride, int padding,
+                            size_t kernel_size, size_t pool_stride);
 // ops.hpp:324: multi-head attention core; key_padding_mask {N, Tk} (0 = padded) or empty.
 Value attention(const Value& q, const Value& k, const Value& v, size_t heads, const Tensor& key_padding_mask,
                 bool causal);

@@ -89,11 +89,13 @@ int nnh_attention_backward_workspace_size(size_t N, size_t Tq, size_t Tk, size_t
 /*
  * Numerics mode (process-wide; set it before issuing work). NNH_NUMERICS_NNCPP (the default): every result is
  * nn-cpp's bits, as described above. NNH_NUMERICS_SPLIT_DEPTH: every product with m n <= 2^18 and k >= 256 is
- * computed the way nn-cpp's depth cut computes its products (src/kernels/gemm.cpp:453-485): 128-deep fused
- * multiply-add chains from +0, added in piece order, then stored or added to C. Short chains let small and skinny
- * products use the whole GPU. Results stay deterministic, a pure function of (m, n, k, trans_a, trans_b) and the
- * inputs (so fused ops still equal their compositions), within 4 K 2^-24 sum|a||b| of the exact product, and equal
- * to the oracle's in the same mode; they are no longer nn-cpp's bits for the products the wider rule adds.
+ * computed the way nn-cpp's depth cut computes its products (src/kernels/gemm.cpp:453-485), fused multiply-add
+ * chains from +0 over consecutive slices of the depth, added in slice order, then stored or added to C, with a
+ * slice depth chosen so the product fills the GPU: with T = ceil(m / 64) ceil(n / 16) and s = min(16, max(2,
+ * 4096 / T)), ceil(k / s) rounded up to a multiple of 32. Short chains let small and skinny products use the whole
+ * GPU. Results stay deterministic, a pure function of (m, n, k) and the inputs (so fused ops still equal their
+ * compositions), within 4 K 2^-24 sum|a||b| of the exact product, and equal to the oracle's in the same mode; they
+ * are no longer nn-cpp's bits for the products the rule cuts differently from nn-cpp.
  */
 #define NNH_NUMERICS_NNCPP 0
 #define NNH_NUMERICS_SPLIT_DEPTH 1
@@ -236,6 +238,19 @@ int nnh_scaled_masked_softmax_backward(const float* y, const float* g, size_t N,
 int nnh_conv2d_forward(const float* x, size_t N, size_t Cin, size_t H, size_t W, const float* w, size_t Cout,
                        size_t kh, size_t kw, const float* bias, int stride, int padding, int fuse_relu, float* y,
                        unsigned char* alive, void* stream);
+
+/*
+ * conv2d_relu (ops.cpp:1396-1416) then maxpool2d(y, pool_kernel, pool_stride) (ops.cpp:1609-1684): y and alive as
+ * nnh_conv2d_forward with fuse_relu = 1, pooled and argmax as nnh_maxpool2d_forward on y, the same bits. A
+ * network's first layer (stride 1, "same" kh = kw = 2 padding + 1 with padding 1 or 2, W a multiple of 4, H even,
+ * Cin (kh + 1) <= 8, a 2 x 2 pool of stride 2, 16-byte aligned x and y, 8-byte aligned pooled and argmax) runs as
+ * one kernel that writes all four from registers; other shapes run the two ops in turn. alive and argmax may be
+ * NULL. No counterpart in the reference, whose Sequential runs the two modules one after the other.
+ */
+int nnh_conv2d_relu_maxpool2d_forward(const float* x, size_t N, size_t Cin, size_t H, size_t W, const float* w,
+                                      size_t Cout, size_t kh, size_t kw, const float* bias, int stride, int padding,
+                                      size_t pool_kernel, size_t pool_stride, float* y, unsigned char* alive,
+                                      float* pooled, unsigned int* argmax, void* stream);
 
 /*
  * Its backward (ops.cpp:1418-1463) for upstream gradient g {N, Cout, Ho, Wo}: g is masked by alive when given

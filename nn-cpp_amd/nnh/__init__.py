@@ -90,6 +90,8 @@ _EXTRA_DECLS = {
     "nnh_attention_backward_workspace_size": [_sz, _sz, _sz, _sz, _sz, _szp],
     "nnh_sgemm_noalloc": [C.c_int, C.c_int, _sz, _sz, _sz, _vp, _sz, _vp, _sz, _vp, _sz, C.c_int, _vp],
     "nnh_maxpool2d_forward": [_vp, _sz, _sz, _sz, _sz, _sz, _sz, _vp, _vp, _vp],
+    "nnh_conv2d_relu_maxpool2d_forward": [_vp, _sz, _sz, _sz, _sz, _vp, _sz, _sz, _sz, _vp, C.c_int, C.c_int, _sz, _sz,
+                                          _vp, _vp, _vp, _vp, _vp],
     "nnh_maxpool2d_backward": [_vp, _vp, _sz, _sz, _sz, _sz, _sz, _sz, _vp, C.c_int, _vp],
     "nnh_matmul_backward": [_vp, _vp, _szp, C.c_int, _vp, _szp, C.c_int, C.c_int, _vp, C.c_int, _vp, C.c_int, _vp],
     "nnh_matmul_backward_workspace_size": [_szp, C.c_int, _szp, C.c_int, C.c_int, C.c_int, C.c_int, _szp],
@@ -173,7 +175,7 @@ def _ptr(t, offset=0):
     if t is None:
         return None
     import torch
-    assert t.dtype == torch.float32 or t.dtype == torch.uint8, t.dtype
+    assert t.dtype in (torch.float32, torch.uint8, torch.int32), t.dtype
     assert t.is_cuda, "nnh works on device tensors"
     return C.c_void_p(t.data_ptr() + offset * t.element_size())
 
@@ -334,6 +336,38 @@ def conv2d_forward(x, w, bias, stride, pad, fuse_relu, want_alive=True, stream=N
     check(lib().nnh_conv2d_forward(_ptr(x), N, Cin, H, W, _ptr(w), Cout, kh, kw, _ptr(bias), int(stride), int(pad),
                                    int(fuse_relu), _ptr(y), _ptr(alive), _stream(stream)))
     return y, alive
+
+
+def maxpool2d_forward(x, kernel, stride, want_argmax=True, stream=None):
+    """nn::maxpool2d on a device tensor {N, C, H, W}; returns (y, argmax or None), argmax as int32 holding the uint32
+    offsets inside each (n, c) plane."""
+    import torch
+    N, Cc, H, W = x.shape
+    ho, wo = (H - kernel) // stride + 1, (W - kernel) // stride + 1
+    y = torch.empty((N, Cc, ho, wo), dtype=torch.float32, device=x.device)
+    argmax = torch.empty(y.shape, dtype=torch.int32, device=x.device) if want_argmax else None
+    check(lib().nnh_maxpool2d_forward(_ptr(x), N, Cc, H, W, kernel, stride, _ptr(y), _ptr(argmax), _stream(stream)))
+    return y, argmax
+
+
+def conv2d_relu_maxpool2d_forward(x, w, bias, stride, pad, pool_kernel, pool_stride, want_alive=True,
+                                  want_argmax=True, stream=None):
+    """nn::conv2d_relu then nn::maxpool2d on its output in one call; returns (y, alive or None, pooled, argmax or
+    None), argmax as int32 holding the uint32 offsets."""
+    import torch
+    N, Cin, H, W = x.shape
+    Cout, _, kh, kw = w.shape
+    ho, wo = conv_out(H, W, kh, kw, stride, pad)
+    y = torch.empty((N, Cout, max(ho, 0), max(wo, 0)), dtype=torch.float32, device=x.device)
+    alive = torch.empty(y.shape, dtype=torch.uint8, device=x.device) if want_alive else None
+    po, qo = (max(ho - pool_kernel, -1) // pool_stride + 1, max(wo - pool_kernel, -1) // pool_stride + 1) \
+        if pool_kernel and pool_stride else (0, 0)
+    pooled = torch.empty((N, Cout, max(po, 0), max(qo, 0)), dtype=torch.float32, device=x.device)
+    argmax = torch.empty(pooled.shape, dtype=torch.int32, device=x.device) if want_argmax else None
+    check(lib().nnh_conv2d_relu_maxpool2d_forward(_ptr(x), N, Cin, H, W, _ptr(w), Cout, kh, kw, _ptr(bias), int(stride),
+                                                  int(pad), pool_kernel, pool_stride, _ptr(y), _ptr(alive),
+                                                  _ptr(pooled), _ptr(argmax), _stream(stream)))
+    return y, alive, pooled, argmax
 
 
 def conv2d_backward(g, x, w, alive, stride, pad, dx=None, dx_first=True, dw=None, dw_first=True, db=None,

@@ -5,8 +5,9 @@
 // GEMM path) are not part of it: the backward pass starts from a given gradient of the logits.
 //   model 0, mlp_wide: Linear(784,1024) ReLU Linear(1024,1024) ReLU Linear(1024,10); params W1 b1 W2 b2 W3 b3.
 //   model 1, cnn_mnist: Conv2d(1,8,3,1,1) ReLU MaxPool2d(2,2) Conv2d(8,16,3,1,1) ReLU MaxPool2d(2,2) Flatten
-//            Linear(784,128) ReLU Linear(128,10), with Sequential's Conv2d + ReLU folding (src/nn/sequential.cpp:16-28);
-//            params conv1 w b, conv2 w b, fc1 w b, fc2 w b.
+//            Linear(784,128) ReLU Linear(128,10), with Sequential's Conv2d + ReLU folding (src/nn/sequential.cpp:16-28)
+//            and each Conv2d + ReLU + MaxPool2d run as nn::hip::conv2d_relu_maxpool2d (the same values and
+//            gradients); params conv1 w b, conv2 w b, fc1 w b, fc2 w b.
 #include <chrono>
 #include <vector>
 
@@ -37,8 +38,9 @@ Value forward(int model, const Value& x, const std::vector<Value>& p) {
 		return nn::hip::linear(h, p[4], p[5]);
 	}
 	const size_t N = x.data().shape()[0];
-	Value h = nn::hip::maxpool2d(nn::hip::conv2d_relu(x, p[0], p[1], 1, 1), 2, 2);
-	h = nn::hip::maxpool2d(nn::hip::conv2d_relu(h, p[2], p[3], 1, 1), 2, 2);
+	// each conv2d_relu -> maxpool2d pair in one call: the first layer's in one pass, the second's in turn
+	Value h = nn::hip::conv2d_relu_maxpool2d(x, p[0], p[1], 1, 1, 2, 2);
+	h = nn::hip::conv2d_relu_maxpool2d(h, p[2], p[3], 1, 1, 2, 2);
 	h = nn::hip::reshape(h, {N, 784});
 	return nn::hip::linear(nn::hip::relu(nn::hip::linear(h, p[4], p[5])), p[6], p[7]);
 }

@@ -291,7 +291,11 @@ Value matmul_op(const Value& a, const Value& b, bool bt) {
 	});
 }
 
-Value conv_op(const Value& x, const Value& w, const Value& b, int stride, int padding, bool fuse_relu) {
+struct ConvShape {
+	size_t N, Cin, H, W, Cout, kh, kw, ho, wo;
+};
+
+ConvShape conv_shape(const Value& x, const Value& w, const Value& b, int stride, int padding) {
 	const auto& xs = x.data().shape();
 	const auto& ws = w.data().shape();
 	// ops.cpp:1347-1365
@@ -299,15 +303,20 @@ Value conv_op(const Value& x, const Value& w, const Value& b, int stride, int pa
 		throw TensorShapeError("nn::hip: conv2d shapes");
 	if (stride <= 0 || padding < 0 || ws[2] > xs[2] + 2 * (size_t)padding || ws[3] > xs[3] + 2 * (size_t)padding)
 		throw TensorShapeError("nn::hip: conv2d geometry");
-	const size_t N = xs[0], Cin = xs[1], H = xs[2], W = xs[3], Cout = ws[0], kh = ws[2], kw = ws[3];
-	const size_t ho = (H + 2 * padding - kh) / stride + 1, wo = (W + 2 * padding - kw) / stride + 1;
-	Tensor y = Tensor::empty({N, Cout, ho, wo});
-	const bool keep = fuse_relu && NoGradGuard::grad_enabled() &&
-	                  (x.requires_grad() || w.requires_grad() || b.requires_grad());
-	std::shared_ptr<Block> alive = keep ? side_buffer(y.size()) : nullptr;
-	check(nnh_conv2d_forward(x.data().data(), N, Cin, H, W, w.data().data(), Cout, kh, kw, b.data().data(), stride,
-	                         padding, fuse_relu, y.data(), alive ? static_cast<unsigned char*>(alive->p) : nullptr,
-	                         g_stream));
+	ConvShape c{xs[0], xs[1], xs[2], xs[3], ws[0], ws[2], ws[3], 0, 0};
+	c.ho = (c.H + 2 * padding - c.kh) / stride + 1;
+	c.wo = (c.W + 2 * padding - c.kw) / stride + 1;
+	return c;
+}
+
+// Whether a conv node keeps its ReLU's alive flags for the backward.
+bool keeps_alive(const Value& x, const Value& w, const Value& b, bool fuse_relu) {
+	return fuse_relu && NoGradGuard::grad_enabled() && (x.requires_grad() || w.requires_grad() || b.requires_grad());
+}
+
+// The conv node over its forward's outputs y and alive.
+Value conv_node(const Value& x, const Value& w, const Value& b, int stride, int padding, const ConvShape& c, Tensor y,
+                std::shared_ptr<Block> alive) {
 	return Value::node(std::move(y), {x, w, b}, [=](const Tensor& g) {
 		// ops.cpp:1418-1463: dx taken first (grad_accum), then db and dW (grad() +=, a fresh one zeroed first,
 		// which gives the sum itself)
@@ -317,8 +326,39 @@ Value conv_op(const Value& x, const Value& w, const Value& b, int stride, int pa
 		float* dw = grad_if(w, fw);
 		if (!dx && !dw && !db) return;
 		check(nnh_conv2d_backward(g.data(), x.data().data(), w.data().data(),
-		                          alive ? static_cast<const unsigned char*>(alive->p) : nullptr, N, Cin, H, W, Cout, kh, kw,
-		                          stride, padding, dx, fx, dw, fw, db, fb, g_stream));
+		                          alive ? static_cast<const unsigned char*>(alive->p) : nullptr, c.N, c.Cin, c.H, c.W,
+		                          c.Cout, c.kh, c.kw, stride, padding, dx, fx, dw, fw, db, fb, g_stream));
+	});
+}
+
+Value conv_op(const Value& x, const Value& w, const Value& b, int stride, int padding, bool fuse_relu) {
+	const ConvShape c = conv_shape(x, w, b, stride, padding);
+	Tensor y = Tensor::empty({c.N, c.Cout, c.ho, c.wo});
+	std::shared_ptr<Block> alive = keeps_alive(x, w, b, fuse_relu) ? side_buffer(y.size()) : nullptr;
+	check(nnh_conv2d_forward(x.data().data(), c.N, c.Cin, c.H, c.W, w.data().data(), c.Cout, c.kh, c.kw,
+	                         b.data().data(), stride, padding, fuse_relu, y.data(),
+	                         alive ? static_cast<unsigned char*>(alive->p) : nullptr, g_stream));
+	return conv_node(x, w, b, stride, padding, c, std::move(y), std::move(alive));
+}
+
+// ops.cpp:1610-1617: the pooled shape, or TensorShapeError.
+std::vector<size_t> pool_shape(const std::vector<size_t>& xs, size_t kernel_size, size_t stride) {
+	if (xs.size() != 4) throw TensorShapeError("nn::hip: maxpool2d needs {N, C, H, W}");
+	if (kernel_size == 0 || stride == 0 || kernel_size > xs[2] || kernel_size > xs[3])
+		throw TensorShapeError("nn::hip: maxpool2d geometry");
+	return {xs[0], xs[1], (xs[2] - kernel_size) / stride + 1, (xs[3] - kernel_size) / stride + 1};
+}
+
+// The pool node over its forward's output y and argmax.
+Value pool_node(const Value& x, size_t kernel_size, size_t stride, Tensor y, std::shared_ptr<Block> arg) {
+	const auto& xs = x.data().shape();
+	const size_t N = xs[0], C = xs[1], H = xs[2], W = xs[3];
+	return Value::node(std::move(y), {x}, [=](const Tensor& g) {
+		bool first = false;
+		float* dx = grad_if(x, first);
+		if (dx)
+			check(nnh_maxpool2d_backward(g.data(), static_cast<const unsigned int*>(arg->p), N, C, H, W, kernel_size,
+			                             stride, dx, first, g_stream));
 	});
 }
 
@@ -380,22 +420,27 @@ Value conv2d_relu(const Value& x, const Value& weight, const Value& bias, int st
 
 Value maxpool2d(const Value& x, size_t kernel_size, size_t stride) {
 	const auto& xs = x.data().shape();
-	if (xs.size() != 4) throw TensorShapeError("nn::hip: maxpool2d needs {N, C, H, W}");  // ops.cpp:1610-1612
-	const size_t N = xs[0], C = xs[1], H = xs[2], W = xs[3];
-	if (kernel_size == 0 || stride == 0 || kernel_size > H || kernel_size > W)
-		throw TensorShapeError("nn::hip: maxpool2d geometry");
-	const size_t ho = (H - kernel_size) / stride + 1, wo = (W - kernel_size) / stride + 1;
-	Tensor y = Tensor::empty({N, C, ho, wo});
+	Tensor y = Tensor::empty(pool_shape(xs, kernel_size, stride));
 	std::shared_ptr<Block> arg = side_buffer(y.size() * 4);
-	check(nnh_maxpool2d_forward(x.data().data(), N, C, H, W, kernel_size, stride, y.data(),
+	check(nnh_maxpool2d_forward(x.data().data(), xs[0], xs[1], xs[2], xs[3], kernel_size, stride, y.data(),
 	                            static_cast<unsigned int*>(arg->p), g_stream));
-	return Value::node(std::move(y), {x}, [=](const Tensor& g) {
-		bool first = false;
-		float* dx = grad_if(x, first);
-		if (dx)
-			check(nnh_maxpool2d_backward(g.data(), static_cast<const unsigned int*>(arg->p), N, C, H, W, kernel_size,
-			                             stride, dx, first, g_stream));
-	});
+	return pool_node(x, kernel_size, stride, std::move(y), std::move(arg));
+}
+
+Value conv2d_relu_maxpool2d(const Value& x, const Value& weight, const Value& bias, int stride, int padding,
+                            size_t kernel_size, size_t pool_stride) {
+	const ConvShape c = conv_shape(x, weight, bias, stride, padding);
+	const std::vector<size_t> ys{c.N, c.Cout, c.ho, c.wo};
+	Tensor y = Tensor::empty(ys);
+	Tensor p = Tensor::empty(pool_shape(ys, kernel_size, pool_stride));
+	std::shared_ptr<Block> alive = keeps_alive(x, weight, bias, true) ? side_buffer(y.size()) : nullptr;
+	std::shared_ptr<Block> arg = side_buffer(p.size() * 4);
+	check(nnh_conv2d_relu_maxpool2d_forward(x.data().data(), c.N, c.Cin, c.H, c.W, weight.data().data(), c.Cout, c.kh,
+	                                        c.kw, bias.data().data(), stride, padding, kernel_size, pool_stride,
+	                                        y.data(), alive ? static_cast<unsigned char*>(alive->p) : nullptr, p.data(),
+	                                        static_cast<unsigned int*>(arg->p), g_stream));
+	Value conv = conv_node(x, weight, bias, stride, padding, c, std::move(y), std::move(alive));
+	return pool_node(conv, kernel_size, pool_stride, std::move(p), std::move(arg));
 }
 
 Value attention(const Value& q, const Value& k, const Value& v, size_t heads, const Tensor& key_padding_mask,

@@ -34,6 +34,12 @@ hipError_t conv_direct(const float* x, const float* w, const float* bias, float*
 // The direct kernel's vectorised form (stride 1, "same" width, w % 4 == 0, aligned buffers), with an explicit
 // number of output channels per lane (4 or 8); conv_direct uses it whenever conv_same_quad_ok holds.
 bool conv_same_quad_ok(const float* x, const float* y, const unsigned char* alive, const ConvGeom& g, int64_t samples);
+// conv2d_relu then maxpool2d(2, 2) in one pass (conv_pool.hip): whether it takes the geometry and pointers, and the
+// launch (alive and argmax may be null).
+bool conv_relu_pool2_ok(const float* x, const float* y, const unsigned char* alive, const float* pooled,
+                        const uint32_t* argmax, const ConvGeom& g, int64_t samples);
+hipError_t conv_relu_pool2(const float* x, const float* w, const float* bias, float* y, unsigned char* alive,
+                           float* pooled, uint32_t* argmax, const ConvGeom& g, int64_t samples, int cout, hipStream_t s);
 hipError_t conv_same_quad(const float* x, const float* w, const float* bias, float* y, unsigned char* alive,
                           const ConvGeom& g, int64_t samples, int cout, int relu, int cg, hipStream_t s);
 hipError_t mask_grad(const float* g, const unsigned char* alive, float* out, int64_t total, hipStream_t s);

@@ -160,6 +160,32 @@ int nnh_conv2d_forward(const float* x, size_t N, size_t Cin, size_t H, size_t W,
 	return run_gemm(call, stream, -1);
 }
 
+int nnh_conv2d_relu_maxpool2d_forward(const float* x, size_t N, size_t Cin, size_t H, size_t W, const float* w,
+                                      size_t Cout, size_t kh, size_t kw, const float* bias, int stride, int padding,
+                                      size_t pool_kernel, size_t pool_stride, float* y, unsigned char* alive,
+                                      float* pooled, unsigned int* argmax, void* stream) {
+	ConvGeom g;
+	int rc = conv_geometry(N, Cin, H, W, Cout, kh, kw, stride, padding, g);
+	if (rc != NNH_OK) return rc;
+	const size_t hw = (size_t)g.ho * g.wo;
+	const bool fused = pool_kernel == 2 && pool_stride == 2 && N > 0 && Cout > 0 && hw > 0 && x && w && bias && y &&
+	                   pooled && conv_relu_pool2_ok(x, y, alive, pooled, argmax, g, (int64_t)N);
+	if (!fused) {  // the two ops one after the other (each validates its own arguments)
+		rc = nnh_conv2d_forward(x, N, Cin, H, W, w, Cout, kh, kw, bias, stride, padding, 1, y, alive, stream);
+		if (rc != NNH_OK) return rc;
+		return nnh_maxpool2d_forward(y, N, Cout, g.ho, g.wo, pool_kernel, pool_stride, pooled, argmax, stream);
+	}
+	const uint64_t xb = (uint64_t)N * Cin * H * W * 4, yb = (uint64_t)N * Cout * hw * 4, pb = yb / 4;
+	if (ranges_overlap(y, yb, x, xb) || ranges_overlap(pooled, pb, x, xb) || ranges_overlap(pooled, pb, y, yb) ||
+	    ranges_overlap(argmax, pb, x, xb) || ranges_overlap(argmax, pb, y, yb) || ranges_overlap(argmax, pb, pooled, pb) ||
+	    ranges_overlap(alive, yb / 4, pooled, pb) || ranges_overlap(alive, yb / 4, argmax, pb) ||
+	    ranges_overlap(alive, yb / 4, y, yb) || ranges_overlap(alive, yb / 4, x, xb))
+		return fail(NNH_ERR_ALIAS, "conv2d_relu_maxpool2d: outputs overlap each other or the input");
+	return hip_status(conv_relu_pool2(x, w, bias, y, alive, pooled, argmax, g, (int64_t)N, (int)Cout,
+	                                  reinterpret_cast<hipStream_t>(stream)),
+	                  "conv2d_relu_maxpool2d");
+}
+
 int nnh_conv2d_backward(const float* g, const float* x, const float* w, const unsigned char* alive, size_t N,
                         size_t Cin, size_t H, size_t W, size_t Cout, size_t kh, size_t kw, int stride, int padding,
                         float* dx, int dx_first, float* dw, int dw_first, float* db, int db_first, void* stream) {

@@ -39,18 +39,20 @@ extern "C" {
 // src/nn/sequential.cpp:16-28): conv2d_relu(c0 -> c1, 3x3, pad 1) -> maxpool2d(2, 2) -> conv2d_relu(c1 -> c2) ->
 // maxpool2d(2, 2) -> reshape {N, c2 * (side/4)^2} -> linear(hidden) -> relu -> linear(classes); then the backward
 // pass from the logits' gradient g.
-int h_cnn_step(const float* x, size_t N, size_t c0, size_t side, size_t c1, size_t c2, size_t hidden, size_t classes,
-               const float* w1, const float* b1, const float* w2, const float* b2, const float* w3, const float* b3,
-               const float* w4, const float* b4, const float* g, float* logits, float* dx, float* dw1, float* db1,
-               float* dw2, float* db2, float* dw3, float* db3, float* dw4, float* db4) {
+static int cnn_step(bool fused, const float* x, size_t N, size_t c0, size_t side, size_t c1, size_t c2, size_t hidden,
+                    size_t classes, const float* w1, const float* b1, const float* w2, const float* b2, const float* w3,
+                    const float* b3, const float* w4, const float* b4, const float* g, float* logits, float* dx,
+                    float* dw1, float* db1, float* dw2, float* db2, float* dw3, float* db3, float* dw4, float* db4) {
 	return guard([&] {
 		const size_t flat = c2 * (side / 4) * (side / 4);
 		Value xv = param(x, {N, c0, side, side});
 		Value W1 = param(w1, {c1, c0, 3, 3}), B1 = param(b1, {c1}), W2 = param(w2, {c2, c1, 3, 3}), B2 = param(b2, {c2});
 		Value W3 = param(w3, {hidden, flat}), B3 = param(b3, {hidden}), W4 = param(w4, {classes, hidden});
 		Value B4 = param(b4, {classes});
-		Value h = nn::hip::maxpool2d(nn::hip::conv2d_relu(xv, W1, B1, 1, 1), 2, 2);
-		h = nn::hip::maxpool2d(nn::hip::conv2d_relu(h, W2, B2, 1, 1), 2, 2);
+		Value h = fused ? nn::hip::conv2d_relu_maxpool2d(xv, W1, B1, 1, 1, 2, 2)
+		                : nn::hip::maxpool2d(nn::hip::conv2d_relu(xv, W1, B1, 1, 1), 2, 2);
+		h = fused ? nn::hip::conv2d_relu_maxpool2d(h, W2, B2, 1, 1, 2, 2)
+		          : nn::hip::maxpool2d(nn::hip::conv2d_relu(h, W2, B2, 1, 1), 2, 2);
 		h = nn::hip::reshape(h, {N, flat});
 		Value y = nn::hip::linear(nn::hip::relu(nn::hip::linear(h, W3, B3)), W4, B4);
 		y.backward(Tensor::from_host({N, classes}, g));
@@ -65,6 +67,23 @@ int h_cnn_step(const float* x, size_t N, size_t c0, size_t side, size_t c1, size
 		out(W4.grad(), dw4);
 		out(B4.grad(), db4);
 	});
+}
+
+int h_cnn_step(const float* x, size_t N, size_t c0, size_t side, size_t c1, size_t c2, size_t hidden, size_t classes,
+               const float* w1, const float* b1, const float* w2, const float* b2, const float* w3, const float* b3,
+               const float* w4, const float* b4, const float* g, float* logits, float* dx, float* dw1, float* db1,
+               float* dw2, float* db2, float* dw3, float* db3, float* dw4, float* db4) {
+	return cnn_step(false, x, N, c0, side, c1, c2, hidden, classes, w1, b1, w2, b2, w3, b3, w4, b4, g, logits, dx, dw1,
+	                db1, dw2, db2, dw3, db3, dw4, db4);
+}
+
+// The same step with each conv2d_relu -> maxpool2d pair as nn::hip::conv2d_relu_maxpool2d (one pass where fusable).
+int h_cnn_step_fused(const float* x, size_t N, size_t c0, size_t side, size_t c1, size_t c2, size_t hidden,
+                     size_t classes, const float* w1, const float* b1, const float* w2, const float* b2, const float* w3,
+                     const float* b3, const float* w4, const float* b4, const float* g, float* logits, float* dx,
+                     float* dw1, float* db1, float* dw2, float* db2, float* dw3, float* db3, float* dw4, float* db4) {
+	return cnn_step(true, x, N, c0, side, c1, c2, hidden, classes, w1, b1, w2, b2, w3, b3, w4, b4, g, logits, dx, dw1,
+	                db1, dw2, db2, dw3, db3, dw4, db4);
 }
 
 // linear -> relu -> ... -> linear (the MLPs of apps/bench/workloads.cpp:100-107), backward from g.

@@ -249,14 +249,15 @@ def test_baseline_config2_mlp(gpu, oracle):
 
 def test_tensor_sum0_every_shape_and_combine(gpu, oracle):
     """Tensor::sum(0) (src/tensor.cpp:422-456): rows added in order from +0. Row counts around the kernel's
-    128-row chunks, widths that are not multiples of 4 or of its 64-column blocks, an unaligned source (the 4-byte
-    path), and the three combines: store, store s + 0.0f (a fresh gradient: -0 becomes +0), add."""
+    128-row chunks, widths that are not multiples of 4 or of its 32-column blocks (36 and 100: a last block whose
+    width is a multiple of 4 below 32, where the 16-byte path clamps its last group), an unaligned source (the
+    4-byte path), and the three combines: store, store s + 0.0f (a fresh gradient: -0 becomes +0), add."""
     import torch
 
     import nnh
     seed = 900
     for rows in (0, 1, 7, 127, 128, 129, 300):
-        for inner in (1, 3, 10, 64, 65, 130, 512):
+        for inner in (1, 3, 10, 36, 64, 65, 100, 130, 512):
             src = synth.mt19937_uniform(seed, max(rows * inner, 1), -1.0, 1.0)[: rows * inner].reshape(rows, inner)
             seed += 1
             if rows:

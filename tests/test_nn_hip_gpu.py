@@ -38,9 +38,11 @@ def uni(seed, shape, bound):
     return np.ascontiguousarray(synth.mt19937_uniform(seed, int(np.prod(shape)), -bound, bound).reshape(shape))
 
 
+@pytest.mark.parametrize("fused", [0, 1])
 @pytest.mark.parametrize("dims", [(32, 1, 28, 8, 16, 128, 10), (3, 2, 12, 5, 7, 9, 4)])
-def test_cnn_step_matches_nncpp(harness, ref, dims):
-    """nn-cpp's cnn_mnist (apps/bench/workloads.cpp:113-137): N 32, 1 x 28 x 28, conv 8 and 16, hidden 128."""
+def test_cnn_step_matches_nncpp(harness, ref, dims, fused):
+    """nn-cpp's cnn_mnist (apps/bench/workloads.cpp:113-137): N 32, 1 x 28 x 28, conv 8 and 16, hidden 128; fused:
+    each conv2d_relu -> maxpool2d pair as nn::hip::conv2d_relu_maxpool2d (the first layer in one pass)."""
     N, c0, side, c1, c2, hidden, classes = dims
     flat = c2 * (side // 4) ** 2
     shapes = [(c1, c0, 3, 3), (c1,), (c2, c1, 3, 3), (c2,), (hidden, flat), (hidden,), (classes, hidden), (classes,)]
@@ -49,7 +51,7 @@ def test_cnn_step_matches_nncpp(harness, ref, dims):
     x = np.ascontiguousarray(synth.mt19937_uniform(59, N * c0 * side * side, 0, 1).reshape(N, c0, side, side))
     g = synth.normal(58, (N, classes))
     results = []
-    for fn in (harness.h_cnn_step, ref.lib.nnref_cnn_step):
+    for fn in (harness.h_cnn_step_fused if fused else harness.h_cnn_step, ref.lib.nnref_cnn_step):
         outs = [np.empty((N, classes), np.float32), np.empty_like(x)] + [np.empty_like(p) for p in params]
         rc = fn(fp(x), _sz(N), _sz(c0), _sz(side), _sz(c1), _sz(c2), _sz(hidden), _sz(classes), *[fp(p) for p in params],
                 fp(g), *[fp(o) for o in outs])
@@ -57,7 +59,7 @@ def test_cnn_step_matches_nncpp(harness, ref, dims):
         results.append(outs)
     names = ["logits", "dx", "dw1", "db1", "dw2", "db2", "dw3", "db3", "dw4", "db4"]
     for name, got, want in zip(names, *results):
-        assert_same(got, want, (name, dims))
+        assert_same(got, want, (name, dims, fused))
 
 
 def test_mlp_step_matches_nncpp(harness, ref):

@@ -86,3 +86,47 @@ def test_maxpool_shape_errors(gpu):
     assert L.nnh_maxpool2d_forward(None, 1, 1, 3, 3, 4, 1, None, None, None) == nnh.ERR_SHAPE
     assert L.nnh_maxpool2d_forward(None, 1, 1, 3, 3, 0, 1, None, None, None) == nnh.ERR_SHAPE
     assert L.nnh_maxpool2d_forward(None, 1, 1, 3, 3, 2, 0, None, None, None) == nnh.ERR_SHAPE
+
+
+FUSED_CASES = [  # (N, Cin, H, W, Cout, k, pad, stride, pool k, pool s, seed, alive, argmax)
+    (128, 1, 28, 28, 32, 3, 1, 1, 2, 2, 91, True, True),    # config 3's conv1 -> ReLU -> pool: one kernel
+    (3, 2, 12, 8, 5, 3, 1, 1, 2, 2, 92, True, True),        # two input channels, a partial channel group
+    (2, 1, 10, 12, 7, 5, 2, 1, 2, 2, 93, False, True),      # 5 x 5, padding 2, no alive flags
+    (2, 1, 8, 4, 4, 3, 1, 1, 2, 2, 94, True, False),        # one quad per row (both halos are padding), no argmax
+    (2, 1, 9, 8, 4, 3, 1, 1, 2, 2, 95, True, True),         # H odd: the two ops in turn
+    (2, 3, 8, 8, 4, 3, 1, 1, 2, 2, 96, True, True),         # Cin (kh + 1) > 8: the two ops in turn
+    (2, 1, 8, 8, 4, 3, 1, 1, 3, 2, 97, True, True),         # a 3 x 3 pool: the two ops in turn
+]
+
+
+@pytest.mark.parametrize("case", FUSED_CASES)
+def test_conv_relu_maxpool_in_one_pass(oracle, case):
+    """nnh_conv2d_relu_maxpool2d_forward gives conv2d_relu's y and alive flags and maxpool2d's output and argmax on
+    them, bit for bit, the same as the two ops (nnh_conv2d_forward, nnh_maxpool2d_forward) and as the oracle's
+    conv2d_relu and maxpool2d; inputs include -0, NaN and -inf (the ReLU maps them to 0, windows of zeros keep their
+    first offset)."""
+    import torch
+
+    import nnh
+    N, Cin, H, W, Cout, k, pad, stride, pk, ps, seed, want_alive, want_argmax = case
+    x, wt, b = synth.uniform_operands(seed, [(N, Cin, H, W), (Cout, Cin, k, k), (Cout,)])
+    x = np.array(x, copy=True)
+    x[0, 0, 0, :3] = [np.nan, -np.inf, -0.0]
+    b = np.array(b, copy=True)
+    b[0] = -4.0  # a channel whose outputs are mostly zero after the ReLU: windows of equal zeros
+    dx_, dw_, db_ = dev(x), dev(wt), dev(b)
+    y, al, p, arg = nnh.conv2d_relu_maxpool2d_forward(dx_, dw_, db_, stride, pad, pk, ps, want_alive, want_argmax)
+    y2, al2 = nnh.conv2d_forward(dx_, dw_, db_, stride, pad, True)
+    p2, arg2 = nnh.maxpool2d_forward(y2, pk, ps)
+    torch.cuda.synchronize()
+    wy, wal = oracle.conv2d_forward(x, wt, b, stride, pad, True)
+    wp, warg = oracle.maxpool2d_forward(wy, pk, ps)
+    assert_same(y.cpu().numpy(), wy, ("y", case))
+    assert_same(y.cpu().numpy(), y2.cpu().numpy(), ("y vs two ops", case))
+    if want_alive:
+        assert np.array_equal(al.cpu().numpy(), wal), case
+    assert_same(p.cpu().numpy(), wp, ("pooled", case))
+    assert_same(p.cpu().numpy(), p2.cpu().numpy(), ("pooled vs two ops", case))
+    if want_argmax:
+        assert np.array_equal(arg.cpu().numpy().view(np.uint32), warg), case
+        assert np.array_equal(arg.cpu().numpy(), arg2.cpu().numpy()), case
