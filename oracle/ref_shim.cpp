@@ -3,8 +3,10 @@
 // oracle/_ref/libnnref.so. TEST INFRASTRUCTURE ONLY: the checker and the CPU baseline.
 //
 // Every entry point copies host buffers into nn::Tensor / nn::Value, calls the reference op and
-// copies the result back. Gradients are obtained with loss = sum(y * G) so that the op's backward
-// rule receives exactly G (sum's backward gives ones, mul's gives 1 * G).
+// copies the result back. Gradients come either from loss = sum(y * G), so that the op's backward rule receives
+// exactly G (sum's backward gives ones, mul's gives 1 * G), or from the op's backward rule called directly with G
+// on fresh leaf gradients (run_backward_rule, what Value::backward runs for that node); the nnref_time_* entry
+// points time the forward and that backward rule separately, as the reference's runner times a step.
 // Return codes: 0 ok, 2 TensorShapeError (or another shape/argument exception), 1 anything else.
 #include "nn/autograd/ops.hpp"
 #include "nn/autograd/value.hpp"
