@@ -46,7 +46,7 @@ hipError_t mask_grad(const float* g, const unsigned char* alive, float* out, int
 // mask_grad and lane_sums in one pass: out = alive ? g : 0 over rows x n, dst[row] = lane_sum of out's row.
 // dx of nn::conv2d's backward from the masked output gradient gm {samples, cout, Ho*Wo} (ops.cpp:1452-1455): the
 // per-sample dcol = W^T gm and col2im in one kernel, dcol kept in LDS (same bits). first: dx = 0 + taps, else
-// dx += taps. conv_dx_fused_ok tells whether the geometry fits (Ho*Wo <= 256).
+// dx += taps. conv_dx_fused_ok tells whether the geometry fits (Ho*Wo <= 256, or Ho*Wo <= 1024 with kh*kw <= 16).
 bool conv_dx_fused_ok(const ConvGeom& g, int64_t samples, int cout);
 hipError_t conv_dx_fused(const float* gm, const float* w, float* dx, const ConvGeom& g, int64_t samples, int cout,
                          int first, hipStream_t s);

@@ -8,8 +8,10 @@
 //      memory one row per step), against up to 80 rows k in five 16-wide units (B operand: W[co][k], staged in LDS
 //      a chunk of 64 output channels at a time); the chains never leave the accumulators across chunks.
 //   2. The dcol tile goes to LDS, and each dx element of the group gathers its taps from there, in (ph, pw) order.
-// Same bits as the batched GEMM + col2im path, with no dcol in HBM. Taken when a sample's output positions fit the
-// four waves (Ho*Wo <= 256) and the group's rows fit LDS; otherwise the caller uses that path.
+// Same bits as the batched GEMM + col2im path, with no dcol in HBM. Two shapes of workgroup: 4 waves and up to 80
+// dcol rows (Ho*Wo <= 256, a deeper layer), and 16 waves and up to 16 rows (Ho*Wo <= 1024 and kh*kw <= 16, a first
+// layer such as 28 x 28 with Cin = 1, where one row of W^T per tap is all a sample needs). Otherwise the caller uses
+// the batched GEMM + col2im path.
 #include "conv.hpp"
 
 #include <algorithm>
@@ -21,12 +23,18 @@ namespace nnh {
 
 namespace {
 
-constexpr int kDxRows = 80;      // dcol rows per workgroup (five 16-wide MFMA units)
 constexpr int kDxCo = 64;        // output channels of W staged per chunk
 constexpr int kDxWLd = kDxCo + 4;
-constexpr int kDxPos = 256;      // output positions: four waves of 64
 constexpr int kDxLdsBytes = 80 * 1024;
 constexpr int kDxACh = 16;       // gradient rows each lane keeps in flight
+
+// The two workgroup shapes: NW waves (one output position per lane, 64 NW positions) and ROWS dcol rows (16-wide
+// MFMA units).
+struct DxShape {
+	int nw, rows;
+};
+constexpr DxShape kDxDeep{4, 80};
+constexpr DxShape kDxFirst{16, 16};
 
 using M16 = Mfma<kMf16>;
 
@@ -93,7 +101,9 @@ __device__ __forceinline__ float gather_taps(const float* tile, const DxArgs& a,
 	return v;
 }
 
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) conv_dx_fused_kernel(const DxArgs a) {
+template <int NW, int kDxRows>
+__global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) conv_dx_fused_kernel(const DxArgs a) {
+	constexpr int kThreads = NW * 64;
 	extern __shared__ __align__(16) float sm[];
 	const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
 	const ConvGeom& G = a.geo;
@@ -123,16 +133,17 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) c
 		// W[cc + j][k0 + k] into wl[k][j] (rows past the group and channels past cout read as 0); every load is
 		// issued (at an index clamped into range) before the first store
 		{
-			constexpr int kPer = kDxRows * kDxCo / 256;
+			constexpr int kPer = kDxRows * kDxCo / kThreads;
+			static_assert(kPer * kThreads == kDxRows * kDxCo, "the W chunk splits evenly over the threads");
 			float wv[kPer];
 #pragma unroll
 			for (int u = 0; u < kPer; ++u) {
-				const int idx = tid + 256 * u, j = idx / kDxRows, k = idx - j * kDxRows;
+				const int idx = tid + kThreads * u, j = idx / kDxRows, k = idx - j * kDxRows;
 				wv[u] = a.w[(int64_t)(cc + min(j, nco - 1)) * K + k0 + min(k, rows - 1)];
 			}
 #pragma unroll
 			for (int u = 0; u < kPer; ++u) {
-				const int idx = tid + 256 * u, j = idx / kDxRows, k = idx - j * kDxRows;
+				const int idx = tid + kThreads * u, j = idx / kDxRows, k = idx - j * kDxRows;
 				wl[k * kDxWLd + j] = (k < rows && j < nco) ? wv[u] : 0.0f;
 			}
 		}
@@ -191,12 +202,12 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) c
 	float* dxn = a.dx + ((int64_t)n * G.cin + c0) * plane;
 	if (G.stride == 1 && G.kh == 3 && G.kw == 3) {  // uniform: two elements per thread at a time
 		const int total = cg * plane;
-		for (int e0 = tid; e0 < total; e0 += 512) {
+		for (int e0 = tid; e0 < total; e0 += 2 * kThreads) {
 			int c[2], ih[2], iw[2];
 			float v[2];
 #pragma unroll
 			for (int h = 0; h < 2; ++h) {
-				const int e = min(e0 + 256 * h, total - 1);  // a repeated element is computed, stored once
+				const int e = min(e0 + kThreads * h, total - 1);  // a repeated element is computed, stored once
 				c[h] = (int)fdiv((unsigned)e, a.plane);
 				const int rem = e - c[h] * plane;
 				ih[h] = (int)fdiv((unsigned)rem, a.width);
@@ -206,10 +217,10 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) c
 #pragma unroll
 			for (int h = 0; h < 2; ++h) v[h] = gather_taps_3x3(tile, a, c[h], ih[h], iw[h], v[h]);
 			dxn[e0] = v[0];
-			if (e0 + 256 < total) dxn[e0 + 256] = v[1];
+			if (e0 + kThreads < total) dxn[e0 + kThreads] = v[1];
 		}
 	} else {
-		for (int e = tid; e < cg * plane; e += 256) {
+		for (int e = tid; e < cg * plane; e += kThreads) {
 			const int c = (int)fdiv((unsigned)e, a.plane), rem = e - c * plane;
 			const int ih = (int)fdiv((unsigned)rem, a.width), iw = rem - ih * G.w;
 			const float v0 = a.first ? 0.0f : dxn[e];
@@ -220,39 +231,47 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) c
 
 int dx_hwp(const ConvGeom& g) { return (g.ho * g.wo + 3) / 4 * 4 + 4; }
 
-int dx_lds_bytes(const ConvGeom& g, int cg) { return (kDxRows * kDxWLd + cg * g.kh * g.kw * dx_hwp(g)) * 4; }
+int dx_lds_bytes(const ConvGeom& g, const DxShape& sh, int cg) { return (sh.rows * kDxWLd + cg * g.kh * g.kw * dx_hwp(g)) * 4; }
 
-// Input channels per workgroup: as many as the 80 MFMA rows hold, fewer if the dcol tile would not fit LDS
-int dx_group(const ConvGeom& g) {
-	int cg = std::min(kDxRows / (g.kh * g.kw), g.cin);
-	while (cg > 0 && dx_lds_bytes(g, cg) > kDxLdsBytes) --cg;
+// Input channels per workgroup: as many as the shape's MFMA rows hold, fewer if the dcol tile would not fit LDS
+int dx_group(const ConvGeom& g, const DxShape& sh) {
+	int cg = std::min(sh.rows / (g.kh * g.kw), g.cin);
+	while (cg > 0 && dx_lds_bytes(g, sh, cg) > kDxLdsBytes) --cg;
 	return cg;
+}
+
+// The workgroup shape that takes the geometry (nw 0: neither)
+DxShape dx_shape(const ConvGeom& g) {
+	const int64_t hw = (int64_t)g.ho * g.wo;
+	if (hw >= 1 && hw <= 64 * kDxDeep.nw && g.kh * g.kw <= kDxDeep.rows && dx_group(g, kDxDeep) >= 1) return kDxDeep;
+	if (hw >= 1 && hw <= 64 * kDxFirst.nw && g.kh * g.kw <= kDxFirst.rows && dx_group(g, kDxFirst) >= 1) return kDxFirst;
+	return DxShape{0, 0};
 }
 
 }  // namespace
 
 bool conv_dx_fused_ok(const ConvGeom& g, int64_t samples, int cout) {
-	const int64_t hw = (int64_t)g.ho * g.wo;
-	if (hw < 1 || hw > kDxPos || cout < 1 || g.kh * g.kw > kDxRows) return false;
-	// the reference's dcol product sgemm(T, F, K, hw, Cout) (ops.cpp:1452) splits into 128-deep pieces over the
-	// output channels when it takes the depth cut; this kernel runs one chain over all of them
-	if (depth_cut((int64_t)g.cin * g.kh * g.kw, hw, cout)) return false;
-	const int cg = dx_group(g);
-	if (cg < 1) return false;
-	const int64_t groups = (g.cin + cg - 1) / cg;
-	return samples * groups < ((int64_t)1 << 31) && samples * cout * hw < ((int64_t)1 << 40);
+	if (cout < 1) return false;
+	const DxShape sh = dx_shape(g);
+	if (sh.nw == 0) return false;
+	// the reference's dcol product sgemm(T, F, K, hw, Cout) (ops.cpp:1452) splits into pieces over the output
+	// channels when it takes the depth cut; this kernel runs one chain over all of them
+	if (depth_cut((int64_t)g.cin * g.kh * g.kw, (int64_t)g.ho * g.wo, cout)) return false;
+	const int64_t groups = (g.cin + dx_group(g, sh) - 1) / dx_group(g, sh);
+	return samples * groups < ((int64_t)1 << 31) && samples * cout * (int64_t)g.ho * g.wo < ((int64_t)1 << 40);
 }
 
 hipError_t conv_dx_fused(const float* gm, const float* w, float* dx, const ConvGeom& g, int64_t samples, int cout,
                          int first, hipStream_t s) {
 	if (!conv_dx_fused_ok(g, samples, cout)) return hipErrorInvalidValue;
+	const DxShape sh = dx_shape(g);
 	DxArgs a;
 	a.g = gm;
 	a.w = w;
 	a.dx = dx;
 	a.geo = g;
 	a.cout = cout;
-	a.cg = dx_group(g);
+	a.cg = dx_group(g, sh);
 	a.groups = (g.cin + a.cg - 1) / a.cg;
 	a.total = (int)(samples * a.groups);
 	a.first = first;
@@ -260,11 +279,17 @@ hipError_t conv_dx_fused(const float* gm, const float* w, float* dx, const ConvG
 	a.plane = make_fastdiv((unsigned)(g.h * g.w));
 	a.width = make_fastdiv((unsigned)g.w);
 	a.stride = make_fastdiv((unsigned)g.stride);
-	const int lds = dx_lds_bytes(g, a.cg);
-	hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(conv_dx_fused_kernel),
-	                                   hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+	const int lds = dx_lds_bytes(g, sh, a.cg);
+	const void* fn = sh.nw == kDxDeep.nw ? reinterpret_cast<const void*>(conv_dx_fused_kernel<kDxDeep.nw, kDxDeep.rows>)
+	                                     : reinterpret_cast<const void*>(conv_dx_fused_kernel<kDxFirst.nw, kDxFirst.rows>);
+	hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
 	if (e != hipSuccess) return e;
-	hipLaunchKernelGGL(conv_dx_fused_kernel, dim3((unsigned)a.total), dim3(256), lds, s, a);
+	if (sh.nw == kDxDeep.nw)
+		hipLaunchKernelGGL((conv_dx_fused_kernel<kDxDeep.nw, kDxDeep.rows>), dim3((unsigned)a.total), dim3(64 * sh.nw), lds,
+		                   s, a);
+	else
+		hipLaunchKernelGGL((conv_dx_fused_kernel<kDxFirst.nw, kDxFirst.rows>), dim3((unsigned)a.total), dim3(64 * sh.nw),
+		                   lds, s, a);
 	return hipGetLastError();
 }
 

@@ -120,7 +120,11 @@ DX_CASES = [
     (2, 5, 11, 11, 7, 5, 5, 2, 2),      # stride 2, 25 taps: 3 channels per group
     (2, 4, 6, 10, 33, 2, 3, 1, 0),      # rectangular kernel, no padding
     (1, 3, 16, 16, 20, 9, 9, 1, 4),     # 81 taps: one channel per group does not fit 80 rows
-    (2, 6, 17, 17, 24, 3, 3, 1, 1),     # 289 outputs: the GEMM + col2im path
+    (2, 6, 17, 17, 24, 3, 3, 1, 1),     # 289 outputs: the sixteen-wave shape, one channel per group
+    (2, 1, 28, 28, 32, 3, 3, 1, 1),     # config 3's conv1 plane (784 outputs): sixteen waves
+    (2, 2, 40, 40, 5, 3, 3, 2, 1),      # stride 2, 400 outputs: sixteen waves, the general tap gather
+    (1, 1, 30, 30, 9, 4, 4, 1, 1),      # 16 taps, 841 outputs: sixteen waves
+    (1, 2, 34, 34, 6, 3, 3, 1, 1),      # 1156 outputs: the GEMM + col2im path
     (2, 8, 8, 8, 512, 3, 3, 1, 1),      # dcol = W^T g (72 x 64 x 512) takes the depth cut: the GEMM + col2im path
 ]
 
