@@ -47,6 +47,8 @@ int build_gemm(int ta, int tb, size_t m, size_t n, size_t k, const float* a, siz
 	}
 	const size_t kIntMax = INT_MAX;
 	if (m > kIntMax || n > kIntMax || k > kIntMax) return fail(NNH_ERR_INVALID, "m, n and k must be below 2^31");
+	if (lda > kMaxElems || ldb > kMaxElems || ldc > kMaxElems)
+		return fail(NNH_ERR_INVALID, "leading dimension out of range (above 2^60)");
 	g.ta = ta ? 1 : 0;
 	g.tb = tb ? 1 : 0;
 	g.m = (int64_t)m;
@@ -59,8 +61,8 @@ int build_gemm(int ta, int tb, size_t m, size_t n, size_t k, const float* a, siz
 	g.ldb = (int64_t)ldb;
 	g.ldc = (int64_t)ldc;
 	g.accumulate = accumulate ? 1 : 0;
-	int64_t count = 1;
-	int64_t max_oa = 0, max_ob = 0, max_oc = 0;
+	// the batch's problem count and the largest offset of each operand's last problem, in elements
+	uint64_t count = 1, max_oa = 0, max_ob = 0, max_oc = 0;
 	if (batch) {
 		if (batch->ndim < 0 || batch->ndim > NNH_MAX_BATCH_DIMS) return fail(NNH_ERR_INVALID, "batch ndim must be 0..4");
 		g.batch.ndim = batch->ndim;
@@ -68,19 +70,18 @@ int build_gemm(int ta, int tb, size_t m, size_t n, size_t k, const float* a, siz
 			if (batch->shape[d] > kIntMax) return fail(NNH_ERR_INVALID, "batch dimension too large");
 			if (batch->stride_a[d] < 0 || batch->stride_b[d] < 0 || batch->stride_c[d] < 0)
 				return fail(NNH_ERR_INVALID, "batch strides must be non-negative");
+			const uint64_t span = batch->shape[d] > 0 ? batch->shape[d] - 1 : 0;
+			if (!mad_ok(count, batch->shape[d], 0, count) || !mad_ok(span, (uint64_t)batch->stride_a[d], max_oa, max_oa) ||
+			    !mad_ok(span, (uint64_t)batch->stride_b[d], max_ob, max_ob) ||
+			    !mad_ok(span, (uint64_t)batch->stride_c[d], max_oc, max_oc))
+				return fail(NNH_ERR_INVALID, "batch extent out of range (above 2^60 elements)");
 			g.batch.shape[d] = (int64_t)batch->shape[d];
 			g.batch.sa[d] = batch->stride_a[d];
 			g.batch.sb[d] = batch->stride_b[d];
 			g.batch.sc[d] = batch->stride_c[d];
-			count *= (int64_t)batch->shape[d];
-			if (batch->shape[d] > 0) {
-				max_oa += (int64_t)(batch->shape[d] - 1) * batch->stride_a[d];
-				max_ob += (int64_t)(batch->shape[d] - 1) * batch->stride_b[d];
-				max_oc += (int64_t)(batch->shape[d] - 1) * batch->stride_c[d];
-			}
 		}
 	}
-	g.batch_count = count;
+	g.batch_count = (int64_t)count;
 	if (ep) {
 		if (ep->bias_mode < NNH_BIAS_NONE || ep->bias_mode > NNH_BIAS_ROW) return fail(NNH_ERR_INVALID, "bad bias mode");
 		if (ep->bias_mode != NNH_BIAS_NONE && !ep->bias) return fail(NNH_ERR_INVALID, "bias is null");
@@ -92,18 +93,21 @@ int build_gemm(int ta, int tb, size_t m, size_t n, size_t k, const float* a, siz
 	if (m == 0 || n == 0 || count == 0) return NNH_OK;  // nothing is touched (gemm.cpp:344)
 	if (!c) return fail(NNH_ERR_INVALID, "C is null");
 	if (ldc < n) return fail(NNH_ERR_INVALID, "ldc < n");
-	const uint64_t c_extent = (uint64_t)(max_oc + (int64_t)(m - 1) * (int64_t)ldc + (int64_t)n) * sizeof(float);
+	uint64_t c_elems = 0;
+	if (!mad_ok(m - 1, ldc, max_oc + n, c_elems)) return fail(NNH_ERR_INVALID, "C's extent out of range");
+	const uint64_t c_extent = c_elems * sizeof(float);
 	if (k > 0) {
 		if (!a || !b) return fail(NNH_ERR_INVALID, "A or B is null");
 		const size_t a_rows = ta ? k : m, a_cols = ta ? m : k;
 		const size_t b_rows = tb ? n : k, b_cols = tb ? k : n;
 		if (lda < a_cols) return fail(NNH_ERR_INVALID, "lda smaller than the stored row length of A");
 		if (!gather && ldb < b_cols) return fail(NNH_ERR_INVALID, "ldb smaller than the stored row length of B");
-		const uint64_t a_extent = (uint64_t)(max_oa + (int64_t)(a_rows - 1) * (int64_t)lda + (int64_t)a_cols) * 4;
-		const uint64_t b_extent =
-			gather ? (uint64_t)(max_ob + (int64_t)gather->cin * gather->h * gather->w) * 4
-			       : (uint64_t)(max_ob + (int64_t)(b_rows - 1) * (int64_t)ldb + (int64_t)b_cols) * 4;
-		if (ranges_overlap(c, c_extent, a, a_extent) || ranges_overlap(c, c_extent, b, b_extent))
+		uint64_t a_elems = 0, b_elems = 0;
+		const bool b_ok = gather ? mad_ok((uint64_t)gather->cin * (uint64_t)gather->h, (uint64_t)gather->w, max_ob, b_elems)
+		                         : mad_ok(b_rows - 1, ldb, max_ob + b_cols, b_elems);
+		if (!mad_ok(a_rows - 1, lda, max_oa + a_cols, a_elems) || !b_ok)
+			return fail(NNH_ERR_INVALID, "A's or B's extent out of range");
+		if (ranges_overlap(c, c_extent, a, a_elems * 4) || ranges_overlap(c, c_extent, b, b_elems * 4))
 			return fail(NNH_ERR_ALIAS, "C overlaps A or B");
 	}
 	if (g.ep.bias_mode != kBiasNone) {

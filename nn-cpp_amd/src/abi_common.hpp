@@ -3,6 +3,7 @@
 #pragma once
 
 #include <cstdint>
+#include <initializer_list>
 #include <string>
 #include <vector>
 
@@ -11,10 +12,48 @@
 
 namespace nnh {
 
+// Element counts, offsets and leading dimensions above 2^60 are refused at this boundary (NNH_ERR_INVALID): no
+// device holds that many floats, and below the limit every byte count and signed offset computed from them fits
+// in 64 bits.
+constexpr uint64_t kMaxElems = (uint64_t)1 << 60;
+
+// out = a * b + c, when that is at most kMaxElems.
+inline bool mad_ok(uint64_t a, uint64_t b, uint64_t c, uint64_t& out) {
+	const unsigned __int128 r = (unsigned __int128)a * b + c;
+	if (r > kMaxElems) return false;
+	out = (uint64_t)r;
+	return true;
+}
+
+// The product of n sizes (1 for n = 0, 0 when one of them is 0), when the product of the nonzero ones is at most
+// kMaxElems: then every partial product, strides included, is too.
+inline bool count_ok(const size_t* dims, int n, uint64_t& out) {
+	uint64_t p = 1;
+	bool empty = false;
+	for (int i = 0; i < n; ++i) {
+		if (dims[i] == 0) empty = true;
+		else if (!mad_ok(p, dims[i], 0, p)) return false;
+	}
+	out = empty ? 0 : p;
+	return true;
+}
+
+inline bool count_ok(std::initializer_list<size_t> dims, uint64_t& out) {
+	return count_ok(dims.begin(), (int)dims.size(), out);
+}
+inline bool count_ok(std::initializer_list<size_t> dims) {
+	uint64_t c = 0;
+	return count_ok(dims, c);
+}
+
 extern thread_local std::string g_last_error;
 int fail(int code, const std::string& msg);
 int hip_status(hipError_t e, const char* what);
 bool ranges_overlap(const void* p0, uint64_t bytes0, const void* p1, uint64_t bytes1);
+// Overlap other than the same range twice (an op that goes element by element may write in place).
+inline bool partial_overlap(const void* p0, uint64_t bytes0, const void* p1, uint64_t bytes1) {
+	return !(p0 == p1 && bytes0 == bytes1) && ranges_overlap(p0, bytes0, p1, bytes1);
+}
 // gather: B is each sample's im2col columns read from the convolution input b (then ldb is unused and B's
 // extent is one sample's input per batch step); null for an ordinary B.
 int build_gemm(int ta, int tb, size_t m, size_t n, size_t k, const float* a, size_t lda, const float* b, size_t ldb,
@@ -31,6 +70,8 @@ inline size_t gemm_workspace_bytes(size_t m, size_t n, size_t k, size_t batch_co
 // NNH_ERR_WORKSPACE when the caller registered a workspace for the stream that holds fewer than `bytes`;
 // called by every entry point before it launches anything.
 int check_workspace(void* stream, size_t bytes);
+// maxpool2d's checks of ops.cpp:1610-1627 on one (H, W) plane, and its output plane (ho, wo).
+int maxpool_geometry(size_t H, size_t W, size_t kernel, size_t stride, size_t& ho, size_t& wo);
 // Stores a workspace query's answer.
 int put_bytes(size_t* out, size_t bytes);
 
@@ -46,6 +87,9 @@ inline int plan_matmul(const size_t* as, int an, const size_t* bs, int bn, int t
 	p = MatmulPlan{};
 	if (an < 0 || bn < 0 || (an > 0 && !as) || (bn > 0 && !bs)) return fail(NNH_ERR_INVALID, "bad shape arrays");
 	if (an < 2 || bn < 2) return fail(NNH_ERR_SHAPE, "matmul needs operands of rank 2 or more");
+	uint64_t a_count = 0, b_count = 0;
+	if (!count_ok(as, an, a_count) || !count_ok(bs, bn, b_count))
+		return fail(NNH_ERR_INVALID, "operand size out of range (above 2^60 elements)");
 	const size_t a_rows = as[an - 2], a_cols = as[an - 1], b_rows = bs[bn - 2], b_cols = bs[bn - 1];
 	const size_t m = ta ? a_cols : a_rows, k = ta ? a_rows : a_cols;
 	const size_t k2 = tb ? b_cols : b_rows, n = tb ? b_rows : b_cols;
@@ -64,6 +108,8 @@ inline int plan_matmul(const size_t* as, int an, const size_t* bs, int bn, int t
 		return NNH_OK;
 	}
 	p.m = m;
+	uint64_t out_count = 0;
+	if (!mad_ok(m, n, 0, out_count)) return fail(NNH_ERR_INVALID, "output size out of range (above 2^60 elements)");
 	// broadcast the leading axes (tensor.cpp:121-136), right-aligned
 	const int ra = an - 2, rb = bn - 2, rank = ra > rb ? ra : rb;
 	std::vector<size_t> shape(rank);
@@ -84,6 +130,8 @@ inline int plan_matmul(const size_t* as, int an, const size_t* bs, int bn, int t
 		// broadcast_offset (tensor.cpp:138-148): a source axis of size 1 contributes nothing
 		sa[i] = (ia >= 0 && as[ia] != 1) ? astr[ia] : 0;
 		sb[i] = (ib >= 0 && bs[ib] != 1) ? bstr[ib] : 0;
+		if (shape[i] != 0 && !mad_ok(out_count, shape[i], 0, out_count))
+			return fail(NNH_ERR_INVALID, "output size out of range (above 2^60 elements)");
 	}
 	{
 		int64_t s = (int64_t)(m * n);

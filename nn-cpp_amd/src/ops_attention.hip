@@ -33,6 +33,10 @@ int check_attention(size_t N, size_t Tq, size_t Tk, size_t D, size_t heads, int 
 	// ops.cpp:1228-1236
 	if (heads == 0 || D % heads != 0 || Tq == 0 || Tk == 0 || (causal && Tq != Tk))
 		return fail(NNH_ERR_SHAPE, "attention: heads must divide D, sequences non-empty, causal needs Tq == Tk");
+	const size_t lim = (size_t)1 << 31;
+	if (Tq >= lim || Tk >= lim || D >= lim || !count_ok({N, Tq, D}) || !count_ok({N, Tk, D}) ||
+	    !count_ok({N, heads, Tq, Tk}))
+		return fail(NNH_ERR_INVALID, "attention: size out of range");
 	a = AttnGeom{N, Tq, Tk, D, heads, D / heads, 1.0f / std::sqrt(static_cast<float>(D / heads))};
 	if ((int64_t)Tk > softmax_max_row_length())
 		return fail(NNH_ERR_INVALID, "attention: key length beyond the row softmax's LDS capacity");
@@ -119,6 +123,16 @@ int nnh_attention_forward(const float* q, const float* k, const float* v, size_t
 	if (rc != NNH_OK) return rc;
 	if (N == 0) return NNH_OK;
 	if (!q || !k || !v || !out || !probs) return fail(NNH_ERR_INVALID, "attention: null pointer");
+	{
+		const uint64_t qb = (uint64_t)N * Tq * D * 4, kb = (uint64_t)N * Tk * D * 4, pb = (uint64_t)N * heads * Tq * Tk * 4;
+		const uint64_t mb = (uint64_t)N * Tk * 4;
+		const void* ins[4] = {q, k, v, key_padding_mask};
+		const uint64_t in_bytes[4] = {qb, kb, kb, mb};
+		for (int i = 0; i < 4; ++i)
+			if (ranges_overlap(out, qb, ins[i], in_bytes[i]) || ranges_overlap(probs, pb, ins[i], in_bytes[i]))
+				return fail(NNH_ERR_ALIAS, "attention: an output overlaps an input");
+		if (ranges_overlap(out, qb, probs, pb)) return fail(NNH_ERR_ALIAS, "attention: out overlaps probs");
+	}
 	hipStream_t s = reinterpret_cast<hipStream_t>(stream);
 	const bool fused_fwd = attention_fused_ok((int64_t)Tq, (int64_t)Tk, (int64_t)a.Dh, (int64_t)D, q, k, v, out, probs,
 	                                          key_padding_mask);
@@ -151,6 +165,19 @@ int nnh_attention_backward(const float* g, const float* q, const float* k, const
 	if (rc != NNH_OK) return rc;
 	if (N == 0 || (!dq && !dk && !dv)) return NNH_OK;
 	if (!g || !q || !k || !v || !probs) return fail(NNH_ERR_INVALID, "attention backward: null pointer");
+	{
+		// dq, dk and dv may be one buffer (q, k and v one node); none may overlap an input
+		const uint64_t qb = (uint64_t)N * Tq * D * 4, kb = (uint64_t)N * Tk * D * 4, pb = (uint64_t)N * heads * Tq * Tk * 4;
+		const uint64_t mb = (uint64_t)N * Tk * 4;
+		const void* ins[6] = {g, q, k, v, probs, key_padding_mask};
+		const uint64_t in_bytes[6] = {qb, qb, kb, kb, pb, mb};
+		const void* outs[3] = {dq, dk, dv};
+		const uint64_t out_bytes[3] = {qb, kb, kb};
+		for (int o = 0; o < 3; ++o)
+			for (int i = 0; i < 6; ++i)
+				if (ranges_overlap(outs[o], out_bytes[o], ins[i], in_bytes[i]))
+					return fail(NNH_ERR_ALIAS, "attention backward: a gradient overlaps an input");
+	}
 	hipStream_t s = reinterpret_cast<hipStream_t>(stream);
 	const BwdPlan plan = attention_backward_plan(a);
 	rc = check_workspace(stream, plan.total);
@@ -195,6 +222,13 @@ int nnh_scaled_masked_softmax_forward(const float* x, size_t N, size_t H, size_t
 	if (N == 0 || H == 0 || Tq == 0) return NNH_OK;
 	if (!x || !y) return fail(NNH_ERR_INVALID, "null pointer");
 	if ((int64_t)Tk > softmax_max_row_length()) return fail(NNH_ERR_INVALID, "row too long for the row softmax");
+	if (Tq >= ((size_t)1 << 31) || H >= ((size_t)1 << 31) || !count_ok({N, H, Tq, Tk}))
+		return fail(NNH_ERR_INVALID, "scaled_masked_softmax: size out of range");
+	{
+		const uint64_t bytes = (uint64_t)N * H * Tq * Tk * 4;
+		if (partial_overlap(y, bytes, x, bytes) || ranges_overlap(y, bytes, key_padding_mask, (uint64_t)N * Tk * 4))
+			return fail(NNH_ERR_ALIAS, "scaled_masked_softmax: y overlaps x (other than in place) or the mask");
+	}
 	return hip_status(softmax_rows(x, y, (int64_t)(N * H * Tq), (int)Tk, (int)Tq, (int)H, scale, key_padding_mask,
 	                               causal, reinterpret_cast<hipStream_t>(stream)),
 	                  "scaled_masked_softmax");
@@ -207,6 +241,14 @@ int nnh_scaled_masked_softmax_backward(const float* y, const float* g, size_t N,
 	if (N == 0 || H == 0 || Tq == 0) return NNH_OK;
 	if (!y || !g || !dx) return fail(NNH_ERR_INVALID, "null pointer");
 	if ((int64_t)Tk > softmax_max_row_length()) return fail(NNH_ERR_INVALID, "row too long for the row softmax");
+	if (Tq >= ((size_t)1 << 31) || H >= ((size_t)1 << 31) || !count_ok({N, H, Tq, Tk}))
+		return fail(NNH_ERR_INVALID, "scaled_masked_softmax backward: size out of range");
+	{
+		const uint64_t bytes = (uint64_t)N * H * Tq * Tk * 4;
+		if (ranges_overlap(dx, bytes, y, bytes) || partial_overlap(dx, bytes, g, bytes) ||
+		    ranges_overlap(dx, bytes, key_padding_mask, (uint64_t)N * Tk * 4))
+			return fail(NNH_ERR_ALIAS, "scaled_masked_softmax backward: dx overlaps y, the mask or g (other than in place)");
+	}
 	return hip_status(softmax_backward_rows(y, g, dx, (int64_t)(N * H * Tq), (int)Tk, (int)Tq, (int)H, scale,
 	                                        key_padding_mask, causal, first ? 1 : 2,
 	                                        reinterpret_cast<hipStream_t>(stream)),

@@ -36,14 +36,13 @@ constexpr size_t kDirectMaxK = 32;
 
 int conv_geometry(size_t N, size_t Cin, size_t H, size_t W, size_t Cout, size_t kh, size_t kw, int stride,
                   int padding, ConvGeom& g) {
-	(void)N;
-	(void)Cout;
-	// ops.cpp:1350-1365
+	// ops.cpp:1350-1365 (the padded extent computed without wrapping)
 	if (stride <= 0 || padding < 0) return fail(NNH_ERR_SHAPE, "conv2d: stride must be positive, padding >= 0");
-	if (kh > H + 2 * (size_t)padding || kw > W + 2 * (size_t)padding)
-		return fail(NNH_ERR_SHAPE, "conv2d: kernel larger than the padded input");
+	const unsigned __int128 pad2 = 2 * (unsigned __int128)padding;
+	if (kh > H + pad2 || kw > W + pad2) return fail(NNH_ERR_SHAPE, "conv2d: kernel larger than the padded input");
 	const size_t lim = 1u << 30;
-	if (Cin > lim || H > lim || W > lim || kh > lim || kw > lim) return fail(NNH_ERR_INVALID, "conv2d: size too large");
+	if (Cin > lim || H > lim || W > lim || kh > lim || kw > lim || (size_t)padding > lim || Cout >= ((size_t)1 << 31))
+		return fail(NNH_ERR_INVALID, "conv2d: size too large");
 	g.cin = (int)Cin;
 	g.h = (int)H;
 	g.w = (int)W;
@@ -51,10 +50,14 @@ int conv_geometry(size_t N, size_t Cin, size_t H, size_t W, size_t Cout, size_t 
 	g.kw = (int)kw;
 	g.stride = stride;
 	g.pad = padding;
-	g.ho = (int)((H + 2 * (size_t)padding - kh) / (size_t)stride + 1);  // ops.cpp:135-139
-	g.wo = (int)((W + 2 * (size_t)padding - kw) / (size_t)stride + 1);
-	if (Cin * H * W >= ((size_t)1 << 31) || (size_t)g.ho * g.wo >= ((size_t)1 << 31) || Cin * kh * kw >= ((size_t)1 << 31))
+	const size_t ho = (H + 2 * (size_t)padding - kh) / (size_t)stride + 1;  // ops.cpp:135-139
+	const size_t wo = (W + 2 * (size_t)padding - kw) / (size_t)stride + 1;
+	if (Cin * H * W >= ((size_t)1 << 31) || ho * wo >= ((size_t)1 << 31) || Cin * kh * kw >= ((size_t)1 << 31))
 		return fail(NNH_ERR_INVALID, "conv2d: a sample is too large");
+	g.ho = (int)ho;
+	g.wo = (int)wo;
+	if (!count_ok({N, Cin, H, W}) || !count_ok({N, Cout, ho, wo}) || !count_ok({Cout, Cin, kh, kw}))
+		return fail(NNH_ERR_INVALID, "conv2d: size out of range (above 2^60 elements)");
 	return NNH_OK;
 }
 
@@ -168,19 +171,24 @@ int nnh_conv2d_relu_maxpool2d_forward(const float* x, size_t N, size_t Cin, size
 	int rc = conv_geometry(N, Cin, H, W, Cout, kh, kw, stride, padding, g);
 	if (rc != NNH_OK) return rc;
 	const size_t hw = (size_t)g.ho * g.wo;
-	const bool fused = pool_kernel == 2 && pool_stride == 2 && N > 0 && Cout > 0 && hw > 0 && x && w && bias && y &&
-	                   pooled && conv_relu_pool2_ok(x, y, alive, pooled, argmax, g, (int64_t)N);
-	if (!fused) {  // the two ops one after the other (each validates its own arguments)
+	size_t pho = 0, pwo = 0;
+	rc = maxpool_geometry((size_t)g.ho, (size_t)g.wo, pool_kernel, pool_stride, pho, pwo);
+	if (rc != NNH_OK) return rc;
+	if (N == 0 || Cout == 0 || hw == 0) return NNH_OK;
+	if (!x || !w || !bias || !y || !pooled) return fail(NNH_ERR_INVALID, "conv2d_relu_maxpool2d: null pointer");
+	const uint64_t xb = (uint64_t)N * Cin * H * W * 4, yb = (uint64_t)N * Cout * hw * 4;
+	const uint64_t pb = (uint64_t)N * Cout * pho * pwo * 4, ab = yb / 4;
+	if (ranges_overlap(y, yb, x, xb) || ranges_overlap(pooled, pb, x, xb) || ranges_overlap(pooled, pb, y, yb) ||
+	    ranges_overlap(argmax, pb, x, xb) || ranges_overlap(argmax, pb, y, yb) || ranges_overlap(argmax, pb, pooled, pb) ||
+	    ranges_overlap(alive, ab, pooled, pb) || ranges_overlap(alive, ab, argmax, pb) ||
+	    ranges_overlap(alive, ab, y, yb) || ranges_overlap(alive, ab, x, xb))
+		return fail(NNH_ERR_ALIAS, "conv2d_relu_maxpool2d: outputs overlap each other or the input");
+	const bool fused = pool_kernel == 2 && pool_stride == 2 && conv_relu_pool2_ok(x, y, alive, pooled, argmax, g, (int64_t)N);
+	if (!fused) {  // the two ops one after the other
 		rc = nnh_conv2d_forward(x, N, Cin, H, W, w, Cout, kh, kw, bias, stride, padding, 1, y, alive, stream);
 		if (rc != NNH_OK) return rc;
 		return nnh_maxpool2d_forward(y, N, Cout, g.ho, g.wo, pool_kernel, pool_stride, pooled, argmax, stream);
 	}
-	const uint64_t xb = (uint64_t)N * Cin * H * W * 4, yb = (uint64_t)N * Cout * hw * 4, pb = yb / 4;
-	if (ranges_overlap(y, yb, x, xb) || ranges_overlap(pooled, pb, x, xb) || ranges_overlap(pooled, pb, y, yb) ||
-	    ranges_overlap(argmax, pb, x, xb) || ranges_overlap(argmax, pb, y, yb) || ranges_overlap(argmax, pb, pooled, pb) ||
-	    ranges_overlap(alive, yb / 4, pooled, pb) || ranges_overlap(alive, yb / 4, argmax, pb) ||
-	    ranges_overlap(alive, yb / 4, y, yb) || ranges_overlap(alive, yb / 4, x, xb))
-		return fail(NNH_ERR_ALIAS, "conv2d_relu_maxpool2d: outputs overlap each other or the input");
 	return hip_status(conv_relu_pool2(x, w, bias, y, alive, pooled, argmax, g, (int64_t)N, (int)Cout,
 	                                  reinterpret_cast<hipStream_t>(stream)),
 	                  "conv2d_relu_maxpool2d");
@@ -202,6 +210,22 @@ int nnh_conv2d_backward(const float* g, const float* x, const float* w, const un
 		return rc;
 	}
 	if (!g || !x || !w) return fail(NNH_ERR_INVALID, "conv2d backward: null pointer");
+	{
+		const uint64_t gb_ = (uint64_t)N * Cout * hw * 4, xb = (uint64_t)N * Cin * H * W * 4, wb = (uint64_t)Cout * K * 4;
+		const uint64_t ab = gb_ / 4;
+		const void* ins[4] = {g, x, w, alive};
+		const uint64_t in_bytes[4] = {gb_, xb, wb, ab};
+		const void* outs[3] = {dx, dw, db};
+		const uint64_t out_bytes[3] = {xb, wb, (uint64_t)Cout * 4};
+		for (int o = 0; o < 3; ++o) {
+			for (int i = 0; i < 4; ++i)
+				if (ranges_overlap(outs[o], out_bytes[o], ins[i], in_bytes[i]))
+					return fail(NNH_ERR_ALIAS, "conv2d backward: a gradient overlaps an input");
+			for (int p = 0; p < o; ++p)
+				if (ranges_overlap(outs[o], out_bytes[o], outs[p], out_bytes[p]))
+					return fail(NNH_ERR_ALIAS, "conv2d backward: gradients overlap each other");
+		}
+	}
 	const BwdPlan plan = conv_backward_plan(geo, N, Cout, alive != nullptr, dx != nullptr, dw != nullptr, db != nullptr);
 	rc = check_workspace(stream, plan.total);
 	if (rc != NNH_OK) return rc;
@@ -268,9 +292,12 @@ int nnh_im2col(const float* x, size_t N, size_t Cin, size_t H, size_t W, size_t 
 	ConvGeom g;
 	int rc = conv_geometry(N, Cin, H, W, 1, kh, kw, stride, padding, g);
 	if (rc != NNH_OK) return rc;
+	if (!count_ok({N, Cin * kh * kw, (size_t)g.ho * g.wo})) return fail(NNH_ERR_INVALID, "im2col: size out of range");
 	const size_t total = N * Cin * kh * kw * (size_t)g.ho * g.wo;
 	if (total == 0) return NNH_OK;
 	if (!x || !col) return fail(NNH_ERR_INVALID, "im2col: null pointer");
+	if (ranges_overlap(col, (uint64_t)total * 4, x, (uint64_t)N * Cin * H * W * 4))
+		return fail(NNH_ERR_ALIAS, "im2col: col overlaps x");
 	return hip_status(im2col(x, col, g, (int64_t)N, reinterpret_cast<hipStream_t>(stream)), "im2col");
 }
 
@@ -279,8 +306,11 @@ int nnh_col2im_add(const float* col, size_t N, size_t Cin, size_t H, size_t W, s
 	ConvGeom g;
 	int rc = conv_geometry(N, Cin, H, W, 1, kh, kw, stride, padding, g);
 	if (rc != NNH_OK) return rc;
+	if (!count_ok({N, Cin * kh * kw, (size_t)g.ho * g.wo})) return fail(NNH_ERR_INVALID, "col2im: size out of range");
 	if (N * Cin * H * W == 0) return NNH_OK;
 	if (!col || !dx) return fail(NNH_ERR_INVALID, "col2im: null pointer");
+	if (ranges_overlap(dx, (uint64_t)N * Cin * H * W * 4, col, (uint64_t)N * Cin * kh * kw * g.ho * g.wo * 4))
+		return fail(NNH_ERR_ALIAS, "col2im: dx overlaps col");
 	return hip_status(col2im(col, dx, g, (int64_t)N, first, reinterpret_cast<hipStream_t>(stream)), "col2im");
 }
 

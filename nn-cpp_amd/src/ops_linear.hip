@@ -14,12 +14,9 @@ using namespace nnh;
 namespace {
 
 bool product_fits(const size_t* dims, int n, size_t& out) {
-	size_t p = 1;
-	for (int i = 0; i < n; ++i) {
-		if (dims[i] != 0 && p > SIZE_MAX / dims[i]) return false;
-		p *= dims[i];
-	}
-	out = p;
+	uint64_t p = 0;
+	if (!count_ok(dims, n, p)) return false;
+	out = (size_t)p;
 	return true;
 }
 
@@ -51,7 +48,8 @@ int nnh_linear_forward_workspace_size(size_t M, size_t K, size_t n, size_t* byte
 
 int nnh_linear_backward_workspace_size(const size_t* lead, int nlead, size_t K, size_t n, int want_dx, int want_dw,
                                        int want_db, size_t* bytes) {
-	if (nlead < 1 || !lead) return fail(NNH_ERR_SHAPE, "linear input needs at least 2 dimensions");
+	if (nlead > 0 && !lead) return fail(NNH_ERR_INVALID, "lead is null");
+	if (nlead < 1) return fail(NNH_ERR_SHAPE, "linear input needs at least 2 dimensions");
 	size_t M = 0;
 	if (!product_fits(lead, nlead, M)) return fail(NNH_ERR_INVALID, "input size overflows");
 	return put_bytes(bytes, linear_backward_ws(lead, nlead, M, K, n, want_dx, want_dw, want_db));
@@ -71,19 +69,19 @@ int nnh_linear_forward(const float* x, size_t M, size_t K, const float* w, size_
 int nnh_linear_backward(const float* g, const float* x, const float* w, const size_t* lead, int nlead, size_t K,
                         size_t n, float* dx, int dx_first, float* dw, int dw_first, float* db, int db_first,
                         void* stream) {
-	if (nlead < 1 || !lead) return fail(NNH_ERR_SHAPE, "linear input needs at least 2 dimensions");
+	if (nlead > 0 && !lead) return fail(NNH_ERR_INVALID, "lead is null");
+	if (nlead < 1) return fail(NNH_ERR_SHAPE, "linear input needs at least 2 dimensions");
 	size_t M = 0;
 	if (!product_fits(lead, nlead, M)) return fail(NNH_ERR_INVALID, "input size overflows");
+	if (!count_ok({M, K}) || !count_ok({M, n}) || !count_ok({n, K}))
+		return fail(NNH_ERR_INVALID, "linear: size out of range (above 2^60 elements)");
 	hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-	{
-		const int rc = check_workspace(stream, linear_backward_ws(lead, nlead, M, K, n, dx, dw, db));
-		if (rc != NNH_OK) return rc;
-	}
 	// db of a 2-D gradient is one Tensor::sum(0): each column of G folded over the rows in order from +0, which is
 	// the row sum of op(A) = G^T over k in the dW product, so that product computes it on the way
 	const bool db_in_dw = dw && db && nlead == 1 && M > 0 && K > 0 && n > 0 && !depth_cut((int64_t)n, (int64_t)K, (int64_t)M) &&
 	                      !ranges_overlap(db, n * 4, dw, (uint64_t)n * K * 4) && !ranges_overlap(db, n * 4, g, (uint64_t)M * n * 4) &&
 	                      !ranges_overlap(db, n * 4, x, (uint64_t)M * K * 4);
+	// every argument is checked before anything is enqueued
 	GemmCall cx, cw;
 	if (dx) {  // dX = G W (ops.cpp:737)
 		const int rc = build_gemm(0, 0, M, K, n, g, n, w, K, dx, K, !dx_first, nullptr, nullptr, cx);
@@ -96,6 +94,14 @@ int nnh_linear_backward(const float* g, const float* x, const float* w, const si
 			cw.rowsum = db;
 			cw.rowsum_combine = db_first ? 1 : 2;
 		}
+	}
+	if (db && n > 0 && M > 0) {
+		if (!g) return fail(NNH_ERR_INVALID, "G is null");
+		if (ranges_overlap(db, n * 4, g, (uint64_t)M * n * 4)) return fail(NNH_ERR_ALIAS, "db overlaps G");
+	}
+	{
+		const int rc = check_workspace(stream, linear_backward_ws(lead, nlead, M, K, n, dx, dw, db));
+		if (rc != NNH_OK) return rc;
 	}
 	// the two products in one launch when neither writes what the other reads or writes (the reference runs dX
 	// first; with disjoint buffers the order cannot show)
@@ -124,8 +130,6 @@ int nnh_linear_backward(const float* g, const float* x, const float* w, const si
 	if (db && n > 0 && !db_in_dw) {
 		// accumulate_grad(bias, G): Tensor::sum(0) once per leading axis (ops.cpp:35-53), then stored as
 		// s + 0.0f into a fresh gradient or added (ops.cpp:85-99)
-		if (M > 0 && !g) return fail(NNH_ERR_INVALID, "G is null");
-		if (ranges_overlap(db, n * 4, g, (uint64_t)M * n * 4)) return fail(NNH_ERR_ALIAS, "db overlaps G");
 		const int combine = db_first ? 1 : 2;
 		if (nlead == 1) return hip_status(sum_rows(g, (int64_t)lead[0], (int64_t)n, db, combine, s), "bias gradient");
 		// suffix[d] = n * prod(lead[d+1 ..]): the row length left after reducing axes 0..d
@@ -155,12 +159,17 @@ int nnh_linear_backward(const float* g, const float* x, const float* w, const si
 int nnh_relu_forward(const float* x, float* y, size_t count, void* stream) {
 	if (count == 0) return NNH_OK;
 	if (!x || !y) return fail(NNH_ERR_INVALID, "null pointer");
+	if (count > kMaxElems) return fail(NNH_ERR_INVALID, "count out of range (above 2^60)");
+	if (partial_overlap(y, count * 4, x, count * 4)) return fail(NNH_ERR_ALIAS, "y overlaps x other than in place");
 	return hip_status(relu_forward(x, y, (int64_t)count, reinterpret_cast<hipStream_t>(stream)), "relu forward");
 }
 
 int nnh_relu_backward(const float* x, const float* g, float* dx, int first, size_t count, void* stream) {
 	if (count == 0) return NNH_OK;
 	if (!x || !g || !dx) return fail(NNH_ERR_INVALID, "null pointer");
+	if (count > kMaxElems) return fail(NNH_ERR_INVALID, "count out of range (above 2^60)");
+	if (partial_overlap(dx, count * 4, g, count * 4) || partial_overlap(dx, count * 4, x, count * 4))
+		return fail(NNH_ERR_ALIAS, "dx overlaps x or g other than in place");
 	return hip_status(relu_backward(x, g, dx, (int64_t)count, first, reinterpret_cast<hipStream_t>(stream)),
 	                  "relu backward");
 }
@@ -168,6 +177,7 @@ int nnh_relu_backward(const float* x, const float* g, float* dx, int first, size
 int nnh_add_to_grad(float* dst, const float* src, size_t count, int first, void* stream) {
 	if (count == 0) return NNH_OK;
 	if (!dst || !src) return fail(NNH_ERR_INVALID, "null pointer");
+	if (count > kMaxElems) return fail(NNH_ERR_INVALID, "count out of range (above 2^60)");
 	if (dst != src && ranges_overlap(dst, count * 4, src, count * 4)) return fail(NNH_ERR_ALIAS, "dst overlaps src");
 	return hip_status(add_to_grad(dst, src, (int64_t)count, first ? 1 : 0, reinterpret_cast<hipStream_t>(stream)),
 	                  "add_to_grad");
@@ -177,6 +187,8 @@ int nnh_tensor_sum0(const float* src, size_t rows, size_t inner, float* dst, int
 	if (inner == 0) return NNH_OK;
 	if (!dst || (rows > 0 && !src)) return fail(NNH_ERR_INVALID, "null pointer");
 	if (combine < 0 || combine > 2) return fail(NNH_ERR_INVALID, "combine must be 0, 1 or 2");
+	if (!count_ok({rows, inner})) return fail(NNH_ERR_INVALID, "size out of range (above 2^60 elements)");
+	if (ranges_overlap(dst, inner * 4, src, (uint64_t)rows * inner * 4)) return fail(NNH_ERR_ALIAS, "dst overlaps src");
 	return hip_status(sum_rows(src, (int64_t)rows, (int64_t)inner, dst, combine, reinterpret_cast<hipStream_t>(stream)),
 	                  "sum0");
 }

@@ -186,6 +186,17 @@ int nnh_matmul_backward(const float* g, const float* a, const size_t* a_shape, i
 	                       db_first, p);
 	if (rc != NNH_OK) return rc;
 	if (!da && !db) return NNH_OK;
+	{
+		// da and db may be one buffer (a and b one node); neither may overlap an input
+		const uint64_t ab = numel(std::vector<size_t>(a_shape, a_shape + a_ndim)) * 4;
+		const uint64_t bb = numel(std::vector<size_t>(b_shape, b_shape + b_ndim)) * 4;
+		const uint64_t gb = numel(p.out_shape) * 4;
+		for (const float* o : {da, db}) {
+			const uint64_t ob = o == da ? ab : bb;
+			if (ranges_overlap(o, ob, g, gb) || ranges_overlap(o, ob, a, ab) || ranges_overlap(o, ob, b, bb))
+				return fail(NNH_ERR_ALIAS, "matmul backward: a gradient overlaps an input");
+		}
+	}
 	if (p.fold) {
 		// ops.cpp:688-701 (matmul: b is {K, n}) and 751-762 (matmul_bt: b is {n, K}); M = a.size / K
 		const size_t K = bt ? b_shape[1] : b_shape[0], n = bt ? b_shape[0] : b_shape[1];
@@ -196,18 +207,19 @@ int nnh_matmul_backward(const float* g, const float* a, const size_t* a_shape, i
 		nnh_matmul_backward_workspace_size(a_shape, a_ndim, b_shape, b_ndim, bt, da != nullptr, db != nullptr, &need);
 		rc = check_workspace(stream, need);
 		if (rc != NNH_OK) return rc;
-		GemmCall c;
+		GemmCall ca, cb;  // both checked before either runs
 		if (da) {
-			rc = bt ? build_gemm(0, 0, M, K, n, g, n, b, K, da, K, !da_first, nullptr, nullptr, c)
-			        : build_gemm(0, 1, M, K, n, g, n, b, n, da, K, !da_first, nullptr, nullptr, c);
-			if (rc == NNH_OK) rc = run_gemm(c, stream, -1);
+			rc = bt ? build_gemm(0, 0, M, K, n, g, n, b, K, da, K, !da_first, nullptr, nullptr, ca)
+			        : build_gemm(0, 1, M, K, n, g, n, b, n, da, K, !da_first, nullptr, nullptr, ca);
 			if (rc != NNH_OK) return rc;
 		}
 		if (db) {
-			rc = bt ? build_gemm(1, 0, n, K, M, g, n, a, K, db, K, !db_first, nullptr, nullptr, c)
-			        : build_gemm(1, 0, K, n, M, a, K, g, n, db, n, !db_first, nullptr, nullptr, c);
-			if (rc == NNH_OK) rc = run_gemm(c, stream, -1);
+			rc = bt ? build_gemm(1, 0, n, K, M, g, n, a, K, db, K, !db_first, nullptr, nullptr, cb)
+			        : build_gemm(1, 0, K, n, M, a, K, g, n, db, n, !db_first, nullptr, nullptr, cb);
+			if (rc != NNH_OK) return rc;
 		}
+		if (da) rc = run_gemm(ca, stream, -1);
+		if (rc == NNH_OK && db) rc = run_gemm(cb, stream, -1);
 		return rc;
 	}
 	rc = check_workspace(stream, p.total);

@@ -10,13 +10,14 @@
 
 using namespace nnh;
 
-namespace {
+namespace nnh {
 
 // ops.cpp:1610-1627: 4-D input, kernel and stride positive, the window inside the plane, plane offsets in 32 bits.
-int pool_geometry(size_t H, size_t W, size_t kernel, size_t stride, size_t& ho, size_t& wo) {
+int maxpool_geometry(size_t H, size_t W, size_t kernel, size_t stride, size_t& ho, size_t& wo) {
 	if (kernel == 0 || stride == 0) return fail(NNH_ERR_SHAPE, "maxpool2d: kernel and stride must be positive");
 	if (kernel > H || kernel > W) return fail(NNH_ERR_SHAPE, "maxpool2d: kernel larger than the input plane");
-	if (H * W > std::numeric_limits<uint32_t>::max()) return fail(NNH_ERR_SHAPE, "maxpool2d: plane beyond 2^32 elements");
+	if ((unsigned __int128)H * W > std::numeric_limits<uint32_t>::max())
+		return fail(NNH_ERR_SHAPE, "maxpool2d: plane beyond 2^32 elements");
 	if (H >= (1u << 30) || W >= (1u << 30) || H * W >= ((size_t)1 << 31))
 		return fail(NNH_ERR_INVALID, "maxpool2d: plane too large");
 	ho = (H - kernel) / stride + 1;  // conv2d_output_size with no padding (ops.cpp:135-139)
@@ -24,14 +25,15 @@ int pool_geometry(size_t H, size_t W, size_t kernel, size_t stride, size_t& ho, 
 	return NNH_OK;
 }
 
-}  // namespace
+}  // namespace nnh
 
 extern "C" {
 
 int nnh_maxpool2d_forward(const float* x, size_t N, size_t C, size_t H, size_t W, size_t kernel, size_t stride,
                           float* y, unsigned int* argmax, void* stream) {
+	if (!count_ok({N, C, H, W})) return fail(NNH_ERR_INVALID, "maxpool2d: size out of range (above 2^60 elements)");
 	size_t ho = 0, wo = 0;
-	int rc = pool_geometry(H, W, kernel, stride, ho, wo);
+	int rc = maxpool_geometry(H, W, kernel, stride, ho, wo);
 	if (rc != NNH_OK) return rc;
 	const size_t planes = N * C;
 	if (planes == 0) return NNH_OK;
@@ -46,8 +48,9 @@ int nnh_maxpool2d_forward(const float* x, size_t N, size_t C, size_t H, size_t W
 
 int nnh_maxpool2d_backward(const float* g, const unsigned int* argmax, size_t N, size_t C, size_t H, size_t W,
                            size_t kernel, size_t stride, float* dx, int first, void* stream) {
+	if (!count_ok({N, C, H, W})) return fail(NNH_ERR_INVALID, "maxpool2d backward: size out of range (above 2^60 elements)");
 	size_t ho = 0, wo = 0;
-	int rc = pool_geometry(H, W, kernel, stride, ho, wo);
+	int rc = maxpool_geometry(H, W, kernel, stride, ho, wo);
 	if (rc != NNH_OK) return rc;
 	const size_t planes = N * C;
 	if (planes == 0) return NNH_OK;
