@@ -9,8 +9,9 @@
 // 16 x 16 quarters, one MFMA per depth index in order. Operands stream through 32-deep slabs (a slab row is one
 // whole 128-byte line of a k-contiguous operand): the next slab's loads are in flight while the current one is
 // consumed from the wave's own LDS staging, and no load is issued past a piece's last slab (the CU's address unit
-// is shared by all 16 waves). Past a piece's end the slab is zero: fma(0, 0, acc) = acc exactly, since a chain
-// from +0 never holds -0. A finished piece goes to an LDS slot; after a barrier each thread adds the pieces in
+// is shared by all 16 waves). Past a piece's end A is +0 and B is -0: fma(+0, -0, acc) = acc + (-0) = acc exactly,
+// -0 included (a chain from +0 ends at -0 when its products round to -0). A finished piece goes to an LDS slot;
+// after a barrier each thread adds the pieces in
 // piece order for its outputs, and the store applies accumulate, bias and ReLU as the reference's does.
 #include <mutex>
 
@@ -45,19 +46,30 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const float* base) {
 }
 
 // Four elements of a row-major matrix whose element (0, 0) is the resource's base: row r, columns c .. c + 3,
-// 0 outside rows_valid x cols_valid. VEC: the caller guarantees that c < cols_valid implies c + 3 < cols_valid
-// and 16-byte alignment, so one 16-byte load serves.
-template <bool VEC>
+// 0 outside rows_valid x cols_valid (-0 with NEG: the B operand's fill, so that a step past a piece's end
+// multiplies +0 by -0 and adding that -0 product leaves every sum as it was, a piece that ended at -0 included).
+// VEC: the caller guarantees that c < cols_valid implies c + 3 < cols_valid and 16-byte alignment, so one
+// 16-byte load serves.
+template <bool VEC, bool NEG>
 __device__ __forceinline__ f32x4 load4(__amdgpu_buffer_rsrc_t res, int ld, int r, int c, int rows_valid, int cols_valid) {
+	constexpr unsigned kSign = NEG ? 0x80000000u : 0u;
 	if (VEC) {
-		const int off = (r < rows_valid && c < cols_valid) ? (r * ld + c) * 4 : kOob;
-		return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(res, off, 0, 0));
+		const bool in = r < rows_valid && c < cols_valid;
+		const int off = in ? (r * ld + c) * 4 : kOob;
+		f32x4 v = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(res, off, 0, 0));
+		if (NEG) {
+#pragma unroll
+			for (int e = 0; e < 4; ++e) v[e] = in ? v[e] : __builtin_bit_cast(float, kSign);
+		}
+		return v;
 	}
 	f32x4 v;
 #pragma unroll
 	for (int e = 0; e < 4; ++e) {
-		const int off = (r < rows_valid && c + e < cols_valid) ? (r * ld + c + e) * 4 : kOob;
+		const bool in = r < rows_valid && c + e < cols_valid;
+		const int off = in ? (r * ld + c + e) * 4 : kOob;
 		v[e] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(res, off, 0, 0));
+		if (NEG) v[e] = in ? v[e] : __builtin_bit_cast(float, kSign);
 	}
 	return v;
 }
@@ -104,10 +116,10 @@ __global__ void __launch_bounds__(kMaxPieces * 64) sgemm_pieces_kernel(const Gem
 #pragma unroll
 		for (int i = 0; i < 4; ++i) {
 			const int idx = lane + 64 * i;  // row idx / 8, columns 4 (idx % 8) .. + 3 of the 32 x 32 slab
-			if (!TA) a[i] = load4<VEC>(ares, lda, idx >> 3, (idx & 7) * 4, mv, kv);
-			else a[i] = load4<VEC>(ares, lda, idx >> 3, (idx & 7) * 4, kv, mv);
-			if (TB) b[i] = load4<VEC>(bres, ldb, idx >> 3, (idx & 7) * 4, nv, kv);
-			else b[i] = load4<VEC>(bres, ldb, idx >> 3, (idx & 7) * 4, kv, nv);
+			if (!TA) a[i] = load4<VEC, false>(ares, lda, idx >> 3, (idx & 7) * 4, mv, kv);
+			else a[i] = load4<VEC, false>(ares, lda, idx >> 3, (idx & 7) * 4, kv, mv);
+			if (TB) b[i] = load4<VEC, true>(bres, ldb, idx >> 3, (idx & 7) * 4, nv, kv);
+			else b[i] = load4<VEC, true>(bres, ldb, idx >> 3, (idx & 7) * 4, kv, nv);
 		}
 	};
 	auto store = [&](const f32x4 (&a)[4], const f32x4 (&b)[4]) {

@@ -147,11 +147,13 @@ __device__ __forceinline__ void batch_offsets(const BatchDesc& d, int64_t bi, in
 	}
 }
 
-// Loads an R x CC row-major tile (CC % 4 == 0) starting at g: 16-byte loads, zeros outside
-// rows_valid x cols_valid when EDGE.
+// Loads an R x CC row-major tile (CC % 4 == 0) starting at g: 16-byte loads, `fill` outside
+// rows_valid x cols_valid when EDGE. The B operand is filled with -0: a depth step past k then multiplies
+// +0 (A's fill) by -0, and adding that -0 product leaves every sum as it was, -0 included (adding +0 would turn a
+// chain that ended at -0 into +0).
 template <int R, int CC, bool EDGE>
 __device__ __forceinline__ void load_tile(const float* __restrict__ g, int64_t ld, int rows_valid,
-                                          int cols_valid, bool vec_ok, f32x4* out, int tid) {
+                                          int cols_valid, bool vec_ok, f32x4* out, int tid, float fill = 0.0f) {
 	constexpr int kVecPerRow = CC / 4;
 	constexpr int kPer = R * CC / 4 / 256;
 	static_assert(kPer * 256 * 4 == R * CC, "tile must split evenly over 256 threads");
@@ -169,7 +171,7 @@ __device__ __forceinline__ void load_tile(const float* __restrict__ g, int64_t l
 			} else {
 				f32x4 v;
 #pragma unroll
-				for (int e = 0; e < 4; ++e) v[e] = (row_in && c + e < cols_valid) ? g[r * ld + c + e] : 0.0f;
+				for (int e = 0; e < 4; ++e) v[e] = (row_in && c + e < cols_valid) ? g[r * ld + c + e] : fill;
 				out[i] = v;
 			}
 		}
@@ -195,8 +197,9 @@ __device__ __forceinline__ void store_tile(float* lds, const f32x4* v, int tid) 
 // multiple of CC / 4, a thread's columns are the same in every slot and every tile. ColCols holds their
 // (oh, ow) geometry and ColRow a row's (c, ph, pw): the caller computes whichever side of the tile stays
 // fixed over the depth loop once, and the other per tile.
+constexpr int kColPast = -(1 << 30);  // ColCols::ihb of a column past the matrix
 struct ColCols {
-	int ihb[4], iwb[4];  // oh * stride - pad, ow * stride - pad; ihb = INT_MIN/2 marks a column past the matrix
+	int ihb[4], iwb[4];  // oh * stride - pad, ow * stride - pad; ihb = kColPast marks a column past the matrix
 };
 struct ColRow {
 	int64_t xoff;  // c * h * w; -1 marks a row past the matrix
@@ -211,7 +214,7 @@ __device__ __forceinline__ ColCols col_cols(const ColGather& cg, int p0, int col
 		const unsigned oh = fdiv(pp, cg.wo_div);
 		const int ow = (int)(pp - oh * cg.wo_div.d);
 		const bool ok = e < cols_valid;
-		cc.ihb[e] = ok ? (int)oh * cg.stride - cg.pad : -(1 << 30);
+		cc.ihb[e] = ok ? (int)oh * cg.stride - cg.pad : kColPast;
 		cc.iwb[e] = ow * cg.stride - cg.pad;
 	}
 	return cc;
@@ -225,7 +228,8 @@ __device__ __forceinline__ ColRow col_row(const ColGather& cg, int kk, bool vali
 }
 
 // Every load is issued, at an index clamped into the channel image (so the code has no branches and the loads
-// of a tile are in flight together); padding and entries past the matrix are then replaced by 0.
+// of a tile are in flight together); the convolution's padding is then replaced by 0 (a real tap of the
+// reference's chain, fma(w, 0, acc)) and entries past the matrix by -0 (B's fill, see load_tile).
 __device__ __forceinline__ f32x4 col_values(const float* __restrict__ x, const ColGather& cg, const ColRow& r,
                                             const ColCols& cc) {
 	f32x4 v;
@@ -233,9 +237,10 @@ __device__ __forceinline__ f32x4 col_values(const float* __restrict__ x, const C
 #pragma unroll
 	for (int e = 0; e < 4; ++e) {
 		const int ih = cc.ihb[e] + r.ph, iw = cc.iwb[e] + r.pw;
-		const bool in = r.xoff >= 0 && ih >= 0 && ih < cg.h && iw >= 0 && iw < cg.w;
+		const bool past = r.xoff < 0 || cc.ihb[e] == kColPast;
+		const bool in = !past && ih >= 0 && ih < cg.h && iw >= 0 && iw < cg.w;
 		const float t = xc[min(max(ih, 0), cg.h - 1) * cg.w + min(max(iw, 0), cg.w - 1)];
-		v[e] = in ? t : 0.0f;
+		v[e] = in ? t : (past ? -0.0f : 0.0f);
 	}
 	return v;
 }
@@ -373,9 +378,9 @@ __device__ __forceinline__ void sgemm_tile_body(const GemmArgs& p, int block) {
 				}
 			}
 		} else if constexpr (TB) {  // B stored n x k
-			load_tile<BN, BK, EDGE>(B + (int64_t)n0 * p.ldb + k0, p.ldb, p.n - n0, k_hi - k0, vec_ok, rb, tid);
+			load_tile<BN, BK, EDGE>(B + (int64_t)n0 * p.ldb + k0, p.ldb, p.n - n0, k_hi - k0, vec_ok, rb, tid, -0.0f);
 		} else {  // B stored k x n
-			load_tile<BK, BN, EDGE>(B + (int64_t)k0 * p.ldb + n0, p.ldb, k_hi - k0, p.n - n0, vec_ok, rb, tid);
+			load_tile<BK, BN, EDGE>(B + (int64_t)k0 * p.ldb + n0, p.ldb, k_hi - k0, p.n - n0, vec_ok, rb, tid, -0.0f);
 		}
 	};
 	auto store = [&](int buf) {

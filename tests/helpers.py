@@ -33,6 +33,21 @@ class Problem:
         return (self.ta, self.tb, self.m, self.n, self.k)
 
 
+def underflow_problem(ta, tb, m, n, k, pad=1):
+    """Every product is -2^-160: it rounds to -0, so each chain from +0 turns into -0 at its first step and stays
+    there, and a sum of -0 pieces is -0. A depth step that adds +0 (a zero-padded tail) turns it into +0."""
+    p = Problem(ta, tb, m, n, k, pad, 1)
+    p.a[...] = np.float32(-(2.0 ** -80))
+    p.b[...] = np.float32(2.0 ** -80)
+    p.c[...] = np.float32(-0.0)
+    return p
+
+
+# Depths past tile sizes (16, 32), depth cuts with short last pieces, and split-mode shapes
+UNDERFLOW_SHAPES = [(7, 9, 17), (33, 40, 100), (65, 129, 257), (40, 48, 1100), (64, 64, 1024), (5, 9, 1100),
+                    (256, 10, 300), (100, 100, 777)]
+
+
 def gpu_sgemm(p, acc, config=-1, c=None, batch=None, epilogue=None):
     """Runs the product's sgemm on copies of p's buffers; returns the whole C buffer."""
     import torch

@@ -13,6 +13,8 @@ import sys
 import numpy as np
 import pytest
 
+from helpers import UNDERFLOW_SHAPES, underflow_problem
+
 from nnh import synth
 
 HERE = os.path.dirname(os.path.abspath(__file__))
@@ -132,6 +134,26 @@ def test_oracle_sgemm_matches_nncpp_sweep(oracle, ref):
                     x = oracle.sgemm(ta, tb, m, n, k, a, lda, b, ldb, c, ldc, acc)
                     y = ref.sgemm(ta, tb, m, n, k, a, lda, b, ldb, c, ldc, acc)
                     assert x.tobytes() == y.tobytes(), spec
+
+
+@pytest.mark.parametrize("ta,tb", [(0, 0), (1, 0), (0, 1), (1, 1)])
+def test_underflowing_chains_end_at_negative_zero(oracle, ref, ta, tb):
+    """An fma whose exact result is a nonzero negative value below half the least subnormal rounds to -0, and
+    -0 + -0 = -0: nn-cpp's outputs are -0, depth cut or not, stored or added to a -0 C; the oracle agrees bit for
+    bit, in both numerics modes (split pieces of -0 add to -0 too)."""
+    for mode in (0, 1):
+        oracle.set_numerics(mode)
+        try:
+            for m, n, k in UNDERFLOW_SHAPES:  # tile tails, depth cuts and split pieces of several lengths
+                p = underflow_problem(ta, tb, m, n, k)
+                for acc in (0, 1):
+                    got = oracle.sgemm(ta, tb, m, n, k, p.a, p.lda, p.b, p.ldb, p.c, p.ldc, acc)[:m, :n]
+                    assert np.all(got == 0) and np.all(np.signbit(got)), (mode, m, n, k, acc)
+                    if mode == 0:
+                        want = ref.sgemm(ta, tb, m, n, k, p.a, p.lda, p.b, p.ldb, p.c, p.ldc, acc)[:m, :n]
+                        assert got.tobytes() == want.tobytes(), (m, n, k, acc)
+        finally:
+            oracle.set_numerics(0)
 
 
 def test_oracle_ops_match_nncpp(oracle, ref):

@@ -9,7 +9,8 @@ checked on sampled elements (the oracle recomputes each sampled element's whole 
 import numpy as np
 import pytest
 
-from helpers import SENTINEL, Problem, bits_equal, first_diff, gpu_sgemm, oracle_sgemm, within_fp64_bound
+from helpers import (SENTINEL, UNDERFLOW_SHAPES, Problem, bits_equal, first_diff, gpu_sgemm, oracle_sgemm,
+                     underflow_problem, within_fp64_bound)
 from nnh import synth
 
 pytestmark = pytest.mark.gpu
@@ -48,6 +49,26 @@ def test_block_boundaries(gpu, oracle):
                 for m, n, k in cases:
                     check(oracle, Problem(ta, tb, m, n, k, 0, seed), acc)
                     seed += 1
+
+
+@pytest.mark.parametrize("ta,tb", [(0, 0), (1, 0), (0, 1), (1, 1)])
+def test_underflowing_chains_keep_negative_zero(gpu, oracle, ta, tb):
+    """Chains whose every product rounds to -0 end at -0 in nn-cpp (and -0 + -0 = -0 when accumulating): the
+    steps past the depth in a kernel's last depth tile or last piece must leave -0 alone, in every tile
+    configuration."""
+    import nnh
+    for m, n, k in UNDERFLOW_SHAPES:
+        p = underflow_problem(ta, tb, m, n, k)
+        for acc in (0, 1):
+            want = oracle_sgemm(oracle, p, acc)
+            assert np.all(np.signbit(want[:m, :n]))
+            got = gpu_sgemm(p, acc)
+            assert bits_equal(got, want), ((m, n, k), acc, first_diff(got, want))
+    p = underflow_problem(ta, tb, 40, 48, 100)
+    want = oracle_sgemm(oracle, p, 0)
+    for cfg in range(len(nnh.gemm_configs())):
+        got = gpu_sgemm(p, 0, config=cfg)
+        assert bits_equal(got, want), (cfg, first_diff(got, want))
 
 
 def test_zero_size_dimensions(gpu):

@@ -6,7 +6,8 @@ attention forward, the LDS convolutions) must decline such products."""
 import numpy as np
 import pytest
 
-from helpers import Problem, assert_same, bits_equal, first_diff, gpu_sgemm, oracle_sgemm, within_fp64_bound
+from helpers import (UNDERFLOW_SHAPES, Problem, assert_same, bits_equal, first_diff, gpu_sgemm, oracle_sgemm,
+                     underflow_problem, within_fp64_bound)
 from nnh import synth
 
 pytestmark = pytest.mark.gpu
@@ -50,6 +51,19 @@ def test_split_sgemm_matches_oracle(split, oracle, ta, tb):
     for cfg in range(len(nnh.gemm_configs())):
         got = gpu_sgemm(p, 0, config=cfg)
         assert bits_equal(got, oracle_sgemm(oracle, p, 0)), cfg
+
+
+@pytest.mark.parametrize("ta,tb", [(0, 0), (1, 0), (0, 1), (1, 1)])
+def test_split_underflowing_chains_keep_negative_zero(split, oracle, ta, tb):
+    """Pieces whose every product rounds to -0 are -0 and add to -0: the steps past a short last piece must
+    leave -0 alone."""
+    for m, n, k in UNDERFLOW_SHAPES + [(512, 512, 600), (64, 4096, 300)]:
+        p = underflow_problem(ta, tb, m, n, k)
+        for acc in (0, 1):
+            want = oracle_sgemm(oracle, p, acc)
+            assert np.all(np.signbit(want[:m, :n]))
+            got = gpu_sgemm(p, acc)
+            assert bits_equal(got, want), ((m, n, k), acc, first_diff(got, want))
 
 
 def test_split_linear_mlp_matches_oracle(split, oracle):
