@@ -287,6 +287,48 @@ int nnh_maxpool2d_forward(const float* x, size_t N, size_t C, size_t H, size_t W
 int nnh_maxpool2d_backward(const float* g, const unsigned int* argmax, size_t N, size_t C, size_t H, size_t W,
                            size_t kernel, size_t stride, float* dx, int first, void* stream);
 
+/*
+ * nn::batchnorm forward in training mode (src/autograd/ops.cpp:900-958): x {N, C, S} where S is the product of the
+ * axes after the channel axis (S = 1 for BatchNorm1d's {N, C}). Per channel c: mean = (float)(sum over n in order of
+ * (double)lane_sum(row (n, c)) / (N*S)), var likewise from lane_sq around the mean, inv_std = 1 / sqrt(var + eps);
+ * y = (x - mean) * (weight[c] * inv_std) + bias[c], and with fuse_relu alive = y > 0 (one byte per element, may be
+ * NULL) and y clipped at 0 (the fold of BatchNormBase::forward_relu, src/nn/batchnorm.cpp:16-23). mean, var and
+ * inv_std receive C floats each (mean and var are the statistics nn-cpp hands its running averages; mean and
+ * inv_std are what the backward pass reads); var may be NULL. N*S = 0 gives NaN statistics, as 0/0 does in the
+ * reference. Scratch: nnh_batchnorm_workspace_size.
+ */
+int nnh_batchnorm_forward(const float* x, size_t N, size_t C, size_t S, const float* weight, const float* bias,
+                          float eps, int fuse_relu, float* y, unsigned char* alive, float* mean, float* var,
+                          float* inv_std, void* stream);
+
+/* Its backward rule (ops.cpp:960-1000). alive: the forward's flags when it folded the ReLU, else NULL. dx (may be
+ * NULL) receives k * (M * g' - sum(g') - ((x - mean) * inv_std) * sum(g' (x - mean)) * inv_std) with g' the masked
+ * gradient, k = weight * inv_std / M and the two per-channel sums in double over the rows' lane sums; first stores
+ * term + 0.0f, else adds. dweight and dbias (may be NULL) have the sums added as the reference's weight.grad() +=
+ * does; *_first: the gradient is fresh (0 + sum). */
+int nnh_batchnorm_backward(const float* g, const float* x, const unsigned char* alive, const float* weight,
+                           const float* mean, const float* inv_std, size_t N, size_t C, size_t S, float* dx,
+                           int dx_first, float* dweight, int dweight_first, float* dbias, int dbias_first,
+                           void* stream);
+
+/* Scratch of either batchnorm call: two floats per (n, c) row. */
+int nnh_batchnorm_workspace_size(size_t N, size_t C, size_t S, size_t* bytes);
+
+/*
+ * nn::layernorm forward (ops.cpp:1003-1034) over R rows of D (x {..., D}, gamma and beta {D}): per row the float
+ * sum in column order, mean = sum / D, the float sum of squared deviations, inv_std = 1 / sqrt(sq / D + eps),
+ * y = (x - mean) * inv_std * gamma + beta. mean and inv_std receive R floats each (the backward pass reads them).
+ * D = 0 is refused (NNH_ERR_INVALID: the reference divides by it). No scratch.
+ */
+int nnh_layernorm_forward(const float* x, size_t R, size_t D, const float* gamma, const float* beta, float eps,
+                          float* y, float* mean, float* inv_std, void* stream);
+
+/* Its backward rule (ops.cpp:1035-1077): dx per row (first: term + 0.0f, else added); dgamma and dbeta summed over
+ * the rows in order per column and added (first: 0 + sum). Any of the three may be NULL. */
+int nnh_layernorm_backward(const float* g, const float* x, const float* gamma, const float* mean, const float* inv_std,
+                           size_t R, size_t D, float* dx, int dx_first, float* dgamma, int dgamma_first, float* dbeta,
+                           int dbeta_first, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -98,6 +98,12 @@ _EXTRA_DECLS = {
     "nnh_add_to_grad": [_vp, _vp, _sz, C.c_int, _vp],
     "nnh_im2col": [_vp, _sz, _sz, _sz, _sz, _sz, _sz, C.c_int, C.c_int, _vp, _vp],
     "nnh_col2im_add": [_vp, _sz, _sz, _sz, _sz, _sz, _sz, C.c_int, C.c_int, _vp, C.c_int, _vp],
+    "nnh_batchnorm_forward": [_vp, _sz, _sz, _sz, _vp, _vp, C.c_float, C.c_int, _vp, _vp, _vp, _vp, _vp, _vp],
+    "nnh_batchnorm_backward": [_vp, _vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, _vp, C.c_int, _vp, C.c_int, _vp, C.c_int,
+                               _vp],
+    "nnh_batchnorm_workspace_size": [_sz, _sz, _sz, _szp],
+    "nnh_layernorm_forward": [_vp, _sz, _sz, _vp, _vp, C.c_float, _vp, _vp, _vp, _vp],
+    "nnh_layernorm_backward": [_vp, _vp, _vp, _vp, _vp, _sz, _sz, _vp, C.c_int, _vp, C.c_int, _vp, C.c_int, _vp],
 }
 
 
@@ -392,6 +398,54 @@ def col2im_add(col, dx, kh, kw, stride, pad, first=False, stream=None):
     N, Cin, H, W = dx.shape
     check(lib().nnh_col2im_add(_ptr(col), N, Cin, H, W, kh, kw, int(stride), int(pad), _ptr(dx), int(first),
                                _stream(stream)))
+
+
+def batchnorm_forward(x, weight, bias, eps, fuse_relu=False, want_alive=True, stream=None):
+    """nn::batchnorm (training mode) on a device tensor {N, C, ...}; returns (y, alive or None, mean, var, inv_std)."""
+    import torch
+    N, Cc = x.shape[0], x.shape[1]
+    S = 1
+    for d in x.shape[2:]:
+        S *= d
+    y = torch.empty_like(x)
+    alive = torch.empty(x.shape, dtype=torch.uint8, device=x.device) if (fuse_relu and want_alive) else None
+    mean, var, inv = (torch.empty(Cc, dtype=torch.float32, device=x.device) for _ in range(3))
+    check(lib().nnh_batchnorm_forward(_ptr(x), N, Cc, S, _ptr(weight), _ptr(bias), float(eps), int(fuse_relu), _ptr(y),
+                                      _ptr(alive), _ptr(mean), _ptr(var), _ptr(inv), _stream(stream)))
+    return y, alive, mean, var, inv
+
+
+def batchnorm_backward(g, x, alive, weight, mean, inv_std, dx=None, dx_first=True, dw=None, dw_first=True, db=None,
+                       db_first=True, stream=None):
+    N, Cc = x.shape[0], x.shape[1]
+    S = 1
+    for d in x.shape[2:]:
+        S *= d
+    check(lib().nnh_batchnorm_backward(_ptr(g), _ptr(x), _ptr(alive), _ptr(weight), _ptr(mean), _ptr(inv_std), N, Cc,
+                                       S, _ptr(dx), int(dx_first), _ptr(dw), int(dw_first), _ptr(db), int(db_first),
+                                       _stream(stream)))
+
+
+def layernorm_forward(x, gamma, beta, eps, stream=None):
+    """nn::layernorm over the last axis of a device tensor; returns (y, mean, inv_std), one statistic per row."""
+    import torch
+    D = x.shape[-1]
+    R = x.numel() // D
+    y = torch.empty_like(x)
+    mean = torch.empty(R, dtype=torch.float32, device=x.device)
+    inv = torch.empty(R, dtype=torch.float32, device=x.device)
+    check(lib().nnh_layernorm_forward(_ptr(x), R, D, _ptr(gamma), _ptr(beta), float(eps), _ptr(y), _ptr(mean),
+                                      _ptr(inv), _stream(stream)))
+    return y, mean, inv
+
+
+def layernorm_backward(g, x, gamma, mean, inv_std, dx=None, dx_first=True, dgamma=None, dgamma_first=True,
+                       dbeta=None, dbeta_first=True, stream=None):
+    D = x.shape[-1]
+    R = x.numel() // D
+    check(lib().nnh_layernorm_backward(_ptr(g), _ptr(x), _ptr(gamma), _ptr(mean), _ptr(inv_std), R, D, _ptr(dx),
+                                       int(dx_first), _ptr(dgamma), int(dgamma_first), _ptr(dbeta), int(dbeta_first),
+                                       _stream(stream)))
 
 
 _bench_lib = None

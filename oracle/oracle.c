@@ -237,6 +237,191 @@ void oracle_relu(const float* x, float* y, size_t count) {
 	for (size_t i = 0; i < count; ++i) y[i] = x[i] > 0.0f ? x[i] : 0.0f;
 }
 
+/* ---- normalisation ---- */
+
+/* The eight-partial sums of ops.cpp:804-897 over one row, as one helper: mode 0 lane_sum(x), 1 lane_sq(x, mu),
+ * 2 lane_sum of g masked by alive (alive NULL: g itself) with lane_dot of the same g against x - mu in *dot. */
+static float lane_row(int mode, const float* x, const float* g, const unsigned char* alive, size_t n, float mu,
+		float* dot) {
+	float a[8] = {0, 0, 0, 0, 0, 0, 0, 0}, d[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+	size_t i = 0;
+	for (; i + 8 <= n; i += 8)
+		for (size_t k = 0; k < 8; ++k) {
+			if (mode == 0) {
+				a[k] += x[i + k];
+			} else if (mode == 1) {
+				const float t = x[i + k] - mu;
+				a[k] += t * t;
+			} else {
+				const float gv = alive ? (alive[i + k] ? g[i + k] : 0.0f) : g[i + k];
+				a[k] += gv;
+				d[k] += gv * (x[i + k] - mu);
+			}
+		}
+	float t = ((a[0] + a[1]) + (a[2] + a[3])) + ((a[4] + a[5]) + (a[6] + a[7]));
+	float u = ((d[0] + d[1]) + (d[2] + d[3])) + ((d[4] + d[5]) + (d[6] + d[7]));
+	for (; i < n; ++i) {
+		if (mode == 0) {
+			t += x[i];
+		} else if (mode == 1) {
+			t += (x[i] - mu) * (x[i] - mu);
+		} else {
+			const float gv = alive ? (alive[i] ? g[i] : 0.0f) : g[i];
+			t += gv;
+			u += gv * (x[i] - mu);
+		}
+	}
+	if (dot) *dot = u;
+	return t;
+}
+
+/* batchnorm forward in training mode (ops.cpp:900-958) on x {N, C, S}: per channel, in double over the samples in
+ * order, the rows' lane sums, then lane_sq around the mean; y = (x - mu) * (w * inv) + b, alive and clipping with
+ * relu. mean, var and inv_std receive C floats each (any may be NULL). */
+void oracle_batchnorm_forward(const float* x, size_t N, size_t C, size_t S, const float* w, const float* b, float eps,
+		int relu, float* y, unsigned char* alive, float* mean, float* var, float* inv_std) {
+	const size_t M = N * S;
+	for (size_t c = 0; c < C; ++c) {
+		double sum = 0.0;
+		for (size_t n = 0; n < N; ++n) sum += lane_row(0, x + (n * C + c) * S, NULL, NULL, S, 0.0f, NULL);
+		const float mu = (float)(sum / (double)M);
+		double sq = 0.0;
+		for (size_t n = 0; n < N; ++n) sq += lane_row(1, x + (n * C + c) * S, NULL, NULL, S, mu, NULL);
+		const float v = (float)(sq / (double)M);
+		const float inv = 1.0f / sqrtf(v + eps);
+		if (mean) mean[c] = mu;
+		if (var) var[c] = v;
+		if (inv_std) inv_std[c] = inv;
+		const float scale = w[c] * inv;
+		for (size_t n = 0; n < N; ++n)
+			for (size_t s = 0; s < S; ++s) {
+				const size_t i = (n * C + c) * S + s;
+				const float t = (x[i] - mu) * scale + b[c];
+				if (relu) {
+					if (alive) alive[i] = t > 0.0f;
+					y[i] = t > 0.0f ? t : 0.0f;
+				} else {
+					y[i] = t;
+				}
+			}
+	}
+}
+
+/* batchnorm backward rule (ops.cpp:960-1000): per channel sdy = sum of lane_sum(g'), sdg = sum of lane_dot(g', x,
+ * mu) in double over the samples in order (g' = g masked by alive), sdyx = sdg * inv; db += (float)sdy,
+ * dw += (float)sdyx (first: 0 + value), dx = k * (M g' - sdy - ((x - mu) * inv) * sdyx), k = w * inv / M, stored
+ * as term + 0 when first. */
+void oracle_batchnorm_backward(const float* g, const float* x, const unsigned char* alive, const float* w,
+		const float* mean, const float* inv_std, size_t N, size_t C, size_t S, float* dx, int dx_first, float* dw,
+		int dw_first, float* db, int db_first) {
+	const size_t M = N * S;
+	for (size_t c = 0; c < C; ++c) {
+		const float mu = mean[c], inv = inv_std[c];
+		double sdy = 0.0, sdg = 0.0;
+		for (size_t n = 0; n < N; ++n) {
+			const size_t base = (n * C + c) * S;
+			float dot = 0.0f;
+			sdy += lane_row(2, x + base, g + base, alive ? alive + base : NULL, S, mu, &dot);
+			sdg += dot;
+		}
+		const double sdyx = sdg * inv;
+		if (db) db[c] = db_first ? 0.0f + (float)sdy : db[c] + (float)sdy;
+		if (dw) dw[c] = dw_first ? 0.0f + (float)sdyx : dw[c] + (float)sdyx;
+		if (dx) {
+			const float k = w[c] * inv / (float)M;
+			const float fm = (float)M, av = (float)sdy, bb = (float)sdyx;
+			for (size_t n = 0; n < N; ++n)
+				for (size_t s = 0; s < S; ++s) {
+					const size_t i = (n * C + c) * S + s;
+					const float gm = alive ? (alive[i] ? g[i] : 0.0f) : g[i];
+					const float term = k * (fm * gm - av - ((x[i] - mu) * inv) * bb);
+					dx[i] = dx_first ? term + 0.0f : dx[i] + term;
+				}
+		}
+	}
+}
+
+/* layernorm forward (ops.cpp:1003-1034) over R rows of D: float sums in column order. mean, inv_std: R floats. */
+void oracle_layernorm_forward(const float* x, size_t R, size_t D, const float* gm, const float* bt, float eps,
+		float* y, float* mean, float* inv_std) {
+	for (size_t r = 0; r < R; ++r) {
+		const float* row = x + r * D;
+		float sum = 0.0f;
+		for (size_t j = 0; j < D; ++j) sum += row[j];
+		const float mu = sum / (float)D;
+		float sq = 0.0f;
+		for (size_t j = 0; j < D; ++j) sq += (row[j] - mu) * (row[j] - mu);
+		const float inv = 1.0f / sqrtf(sq / (float)D + eps);
+		if (mean) mean[r] = mu;
+		if (inv_std) inv_std[r] = inv;
+		for (size_t j = 0; j < D; ++j) y[r * D + j] = (row[j] - mu) * inv * gm[j] + bt[j];
+	}
+}
+
+/* layernorm backward rule (ops.cpp:1035-1077). */
+void oracle_layernorm_backward(const float* g, const float* x, const float* gm, const float* mean,
+		const float* inv_std, size_t R, size_t D, float* dx, int dx_first, float* dgamma, int dgamma_first,
+		float* dbeta, int dbeta_first) {
+	if (dx)
+		for (size_t r = 0; r < R; ++r) {
+			const float mu = mean[r], inv = inv_std[r];
+			float a = 0.0f, b = 0.0f;
+			for (size_t j = 0; j < D; ++j) {
+				const float dxhat = g[r * D + j] * gm[j];
+				a += dxhat;
+				b += dxhat * ((x[r * D + j] - mu) * inv);
+			}
+			const float k = inv / (float)D, fd = (float)D;
+			for (size_t j = 0; j < D; ++j) {
+				const float dxhat = g[r * D + j] * gm[j];
+				const float term = k * (fd * dxhat - a - ((x[r * D + j] - mu) * inv) * b);
+				dx[r * D + j] = dx_first ? term + 0.0f : dx[r * D + j] + term;
+			}
+		}
+	if (dgamma || dbeta)
+		for (size_t j = 0; j < D; ++j) {
+			float sg = 0.0f, sb = 0.0f;
+			for (size_t r = 0; r < R; ++r) {
+				const float gv = g[r * D + j];
+				sg += gv * ((x[r * D + j] - mean[r]) * inv_std[r]);
+				sb += gv;
+			}
+			if (dgamma) dgamma[j] = dgamma_first ? 0.0f + sg : dgamma[j] + sg;
+			if (dbeta) dbeta[j] = dbeta_first ? 0.0f + sb : dbeta[j] + sb;
+		}
+}
+
+/* fp64 closed forms: batchnorm's normalised output over the channel's N*S elements (biased variance), and
+ * layernorm's over each row, without weights. */
+void oracle_batchnorm_f64(const float* x, size_t N, size_t C, size_t S, double eps, double* xhat) {
+	const size_t M = N * S;
+	for (size_t c = 0; c < C; ++c) {
+		double s = 0.0, q = 0.0;
+		for (size_t n = 0; n < N; ++n)
+			for (size_t t = 0; t < S; ++t) s += x[(n * C + c) * S + t];
+		const double mu = s / (double)M;
+		for (size_t n = 0; n < N; ++n)
+			for (size_t t = 0; t < S; ++t) {
+				const double d = x[(n * C + c) * S + t] - mu;
+				q += d * d;
+			}
+		const double inv = 1.0 / sqrt(q / (double)M + eps);
+		for (size_t n = 0; n < N; ++n)
+			for (size_t t = 0; t < S; ++t) xhat[(n * C + c) * S + t] = (x[(n * C + c) * S + t] - mu) * inv;
+	}
+}
+
+void oracle_layernorm_f64(const float* x, size_t R, size_t D, double eps, double* xhat) {
+	for (size_t r = 0; r < R; ++r) {
+		double s = 0.0, q = 0.0;
+		for (size_t j = 0; j < D; ++j) s += x[r * D + j];
+		const double mu = s / (double)D;
+		for (size_t j = 0; j < D; ++j) q += (x[r * D + j] - mu) * (x[r * D + j] - mu);
+		const double inv = 1.0 / sqrt(q / (double)D + eps);
+		for (size_t j = 0; j < D; ++j) xhat[r * D + j] = (x[r * D + j] - mu) * inv;
+	}
+}
+
 /* ---- max pooling ---- */
 
 /* maxpool2d forward (ops.cpp:1609-1684): per window, best = -inf and at = 0, then row by row a value replaces

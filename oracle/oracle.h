@@ -47,6 +47,20 @@ void oracle_linear_backward(const float* g, const float* x, const float* w, size
                             float* db, int db_first);
 void oracle_relu(const float* x, float* y, size_t count);
 
+/* ---- normalisation (src/autograd/ops.cpp:800-1078) ---- */
+void oracle_batchnorm_forward(const float* x, size_t N, size_t C, size_t S, const float* w, const float* b, float eps,
+                              int relu, float* y, unsigned char* alive, float* mean, float* var, float* inv_std);
+void oracle_batchnorm_backward(const float* g, const float* x, const unsigned char* alive, const float* w,
+                               const float* mean, const float* inv_std, size_t N, size_t C, size_t S, float* dx,
+                               int dx_first, float* dw, int dw_first, float* db, int db_first);
+void oracle_layernorm_forward(const float* x, size_t R, size_t D, const float* gm, const float* bt, float eps,
+                              float* y, float* mean, float* inv_std);
+void oracle_layernorm_backward(const float* g, const float* x, const float* gm, const float* mean,
+                               const float* inv_std, size_t R, size_t D, float* dx, int dx_first, float* dgamma,
+                               int dgamma_first, float* dbeta, int dbeta_first);
+void oracle_batchnorm_f64(const float* x, size_t N, size_t C, size_t S, double eps, double* xhat);
+void oracle_layernorm_f64(const float* x, size_t R, size_t D, double eps, double* xhat);
+
 /* ---- max pooling (src/autograd/ops.cpp:1609-1705) ---- */
 void oracle_maxpool2d_forward(const float* x, size_t planes, size_t H, size_t W, size_t k, size_t s, float* y,
                               uint32_t* argmax);

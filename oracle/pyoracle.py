@@ -84,6 +84,13 @@ class Oracle:
         L.oracle_attention_f64.argtypes = [_f, _f, _f, _sz, _sz, _sz, _sz, _sz, _f, C.c_int, _d, _d]
         L.oracle_mt19937_uniform.argtypes = [C.c_uint, C.c_float, C.c_float, _f, _sz]
         _u32 = C.POINTER(C.c_uint32)
+        L.oracle_batchnorm_forward.argtypes = [_f, _sz, _sz, _sz, _f, _f, C.c_float, C.c_int, _f, _u8, _f, _f, _f]
+        L.oracle_batchnorm_backward.argtypes = [_f, _f, _u8, _f, _f, _f, _sz, _sz, _sz, _f, C.c_int, _f, C.c_int, _f,
+                                                C.c_int]
+        L.oracle_layernorm_forward.argtypes = [_f, _sz, _sz, _f, _f, C.c_float, _f, _f, _f]
+        L.oracle_layernorm_backward.argtypes = [_f, _f, _f, _f, _f, _sz, _sz, _f, C.c_int, _f, C.c_int, _f, C.c_int]
+        L.oracle_batchnorm_f64.argtypes = [_f, _sz, _sz, _sz, C.c_double, _d]
+        L.oracle_layernorm_f64.argtypes = [_f, _sz, _sz, C.c_double, _d]
         L.oracle_maxpool2d_forward.argtypes = [_f, _sz, _sz, _sz, _sz, _sz, _f, _u32]
         L.oracle_maxpool2d_backward.argtypes = [_f, _u32, _sz, _sz, _sz, _sz, _sz, _f, C.c_int]
 
@@ -281,6 +288,84 @@ class Oracle:
                                            _fp(out), int(first))
         return out
 
+    # -- normalisation --
+    @staticmethod
+    def _nsc(x):
+        """(N, C, S) of a {N, C, ...} array."""
+        S = 1
+        for d in x.shape[2:]:
+            S *= d
+        return x.shape[0], x.shape[1], S
+
+    def batchnorm_forward(self, x, w, b, eps, relu=False):
+        """(y, alive or None, mean, var, inv_std) of nn::batchnorm in training mode on x {N, C, ...}."""
+        x = np.ascontiguousarray(x, np.float32)
+        N, Cc, S = self._nsc(x)
+        y = np.empty_like(x)
+        alive = np.empty(x.shape, np.uint8) if relu else None
+        mean, var, inv = (np.empty(Cc, np.float32) for _ in range(3))
+        self.lib.oracle_batchnorm_forward(_fp(x), N, Cc, S, _fp(np.ascontiguousarray(w, np.float32)),
+                                          _fp(np.ascontiguousarray(b, np.float32)), float(eps), int(relu), _fp(y),
+                                          _bp(alive), _fp(mean), _fp(var), _fp(inv))
+        return y, alive, mean, var, inv
+
+    def batchnorm_backward(self, g, x, alive, w, mean, inv_std, dx=None, dx_first=True, dw=None, dw_first=True,
+                           db=None, db_first=True, want=(True, True, True)):
+        """(dx, dw, db) of the backward rule; an output is None where `want` says so. Existing dx/dw/db arrays are
+        the buffers added to when the matching *_first is false."""
+        x = np.ascontiguousarray(x, np.float32)
+        N, Cc, S = self._nsc(x)
+        outs = []
+        for buf, shape, wanted in ((dx, x.shape, want[0]), (dw, (Cc,), want[1]), (db, (Cc,), want[2])):
+            outs.append((np.array(buf, np.float32, copy=True) if buf is not None else np.zeros(shape, np.float32))
+                        if wanted else None)
+        self.lib.oracle_batchnorm_backward(_fp(np.ascontiguousarray(g, np.float32)), _fp(x), _bp(alive),
+                                           _fp(np.ascontiguousarray(w, np.float32)), _fp(mean), _fp(inv_std), N, Cc, S,
+                                           _fp(outs[0]), int(dx_first), _fp(outs[1]), int(dw_first), _fp(outs[2]),
+                                           int(db_first))
+        return tuple(outs)
+
+    def layernorm_forward(self, x, gamma, beta, eps):
+        """(y, mean, inv_std) of nn::layernorm over the last axis."""
+        x = np.ascontiguousarray(x, np.float32)
+        D = x.shape[-1]
+        R = x.size // D
+        y = np.empty_like(x)
+        mean, inv = np.empty(R, np.float32), np.empty(R, np.float32)
+        self.lib.oracle_layernorm_forward(_fp(x), R, D, _fp(np.ascontiguousarray(gamma, np.float32)),
+                                          _fp(np.ascontiguousarray(beta, np.float32)), float(eps), _fp(y), _fp(mean),
+                                          _fp(inv))
+        return y, mean, inv
+
+    def layernorm_backward(self, g, x, gamma, mean, inv_std, dx=None, dx_first=True, dgamma=None, dgamma_first=True,
+                           dbeta=None, dbeta_first=True, want=(True, True, True)):
+        x = np.ascontiguousarray(x, np.float32)
+        D = x.shape[-1]
+        R = x.size // D
+        outs = []
+        for buf, shape, wanted in ((dx, x.shape, want[0]), (dgamma, (D,), want[1]), (dbeta, (D,), want[2])):
+            outs.append((np.array(buf, np.float32, copy=True) if buf is not None else np.zeros(shape, np.float32))
+                        if wanted else None)
+        self.lib.oracle_layernorm_backward(_fp(np.ascontiguousarray(g, np.float32)), _fp(x),
+                                           _fp(np.ascontiguousarray(gamma, np.float32)), _fp(mean), _fp(inv_std), R, D,
+                                           _fp(outs[0]), int(dx_first), _fp(outs[1]), int(dgamma_first), _fp(outs[2]),
+                                           int(dbeta_first))
+        return tuple(outs)
+
+    def batchnorm_f64(self, x, eps):
+        x = np.ascontiguousarray(x, np.float32)
+        N, Cc, S = self._nsc(x)
+        out = np.empty(x.shape, np.float64)
+        self.lib.oracle_batchnorm_f64(_fp(x), N, Cc, S, float(eps), _dp(out))
+        return out
+
+    def layernorm_f64(self, x, eps):
+        x = np.ascontiguousarray(x, np.float32)
+        D = x.shape[-1]
+        out = np.empty(x.shape, np.float64)
+        self.lib.oracle_layernorm_f64(_fp(x), x.size // D, D, float(eps), _dp(out))
+        return out
+
     def mt19937_uniform(self, seed, lo, hi, count):
         out = np.empty(count, np.float32)
         self.lib.oracle_mt19937_uniform(seed, lo, hi, _fp(out), count)
@@ -315,6 +400,13 @@ class Reference:
         L.nnref_time_maxpool2d.argtypes = [_f, _sz, _sz, _sz, _sz, _sz, _sz, _f, C.c_int, C.c_int, C.c_double, _d,
                                            C.POINTER(C.c_int), _d, _f, _f]
         L.nnref_matmul_backward.argtypes = [_f, _szp, C.c_int, _f, _szp, C.c_int, C.c_int, _f, C.c_int, _f, _f]
+        L.nnref_batchnorm.argtypes = [_f, _sz, _sz, _sz, _f, _f, C.c_float, C.c_int, _f, _f, _f, _f, C.c_int, _f, _f,
+                                      _f]
+        L.nnref_layernorm.argtypes = [_f, _sz, _sz, _f, _f, C.c_float, _f, _f, C.c_int, _f, _f, _f]
+        L.nnref_time_batchnorm.argtypes = [_f, _sz, _sz, _sz, _f, _f, C.c_float, C.c_int, _f, C.c_int, C.c_int,
+                                           C.c_double, _d, C.POINTER(C.c_int), _d, _f, _f]
+        L.nnref_time_layernorm.argtypes = [_f, _sz, _sz, _f, _f, C.c_float, _f, C.c_int, C.c_int, C.c_double, _d,
+                                           C.POINTER(C.c_int), _d, _f, _f]
         _fpp = C.POINTER(_f)
         timing = [C.c_int, C.c_int, C.c_double, _d]
         L.nnref_time_matmul.argtypes = [_f, _szp, C.c_int, _f, _szp, C.c_int, C.c_int, C.c_int] + timing + [_f]
@@ -463,6 +555,40 @@ class Reference:
             return rc, None, None
         return 0, y, (dx if g is not None else None)
 
+    def batchnorm(self, x, w, b, eps, relu=False, g=None, repeats=1, want=(True, True, True)):
+        """nn::batchnorm (training mode) on x {N, C, ...}: (rc, y, mean, var, (dx, dw, db) or None). With g, the node's
+        backward rule runs `repeats` times (fresh gradients first, then added); `want` picks the inputs that require
+        a gradient."""
+        x = np.ascontiguousarray(x, np.float32)
+        N, Cc, S = Oracle._nsc(x)
+        y = np.empty_like(x)
+        mean, var = np.empty(Cc, np.float32), np.empty(Cc, np.float32)
+        grads = [np.empty(x.shape, np.float32) if want[0] else None, np.empty(Cc, np.float32) if want[1] else None,
+                 np.empty(Cc, np.float32) if want[2] else None]
+        rc = self.lib.nnref_batchnorm(_fp(x), N, Cc, S, _fp(np.ascontiguousarray(w, np.float32)),
+                                      _fp(np.ascontiguousarray(b, np.float32)), float(eps), int(relu), _fp(y),
+                                      _fp(mean), _fp(var), _fp(np.ascontiguousarray(g, np.float32)) if g is not None
+                                      else None, int(repeats), *(_fp(t) for t in grads))
+        if rc != 0:
+            return rc, None, None, None, None
+        return 0, y, mean, var, (tuple(grads) if g is not None else None)
+
+    def layernorm(self, x, gamma, beta, eps, g=None, repeats=1, want=(True, True, True)):
+        """nn::layernorm over the last axis: (rc, y, (dx, dgamma, dbeta) or None), as batchnorm()."""
+        x = np.ascontiguousarray(x, np.float32)
+        D = x.shape[-1]
+        R = x.size // D
+        y = np.empty_like(x)
+        grads = [np.empty(x.shape, np.float32) if want[0] else None, np.empty(D, np.float32) if want[1] else None,
+                 np.empty(D, np.float32) if want[2] else None]
+        rc = self.lib.nnref_layernorm(_fp(x), R, D, _fp(np.ascontiguousarray(gamma, np.float32)),
+                                      _fp(np.ascontiguousarray(beta, np.float32)), float(eps), _fp(y),
+                                      _fp(np.ascontiguousarray(g, np.float32)) if g is not None else None,
+                                      int(repeats), *(_fp(t) for t in grads))
+        if rc != 0:
+            return rc, None, None
+        return 0, y, (tuple(grads) if g is not None else None)
+
     # ---- timing (the CPU baseline): nn-cpp's own ops on buffers built once, apps/bench/runner.cpp's method ----
     # Each returns (times_ms, outputs): the timed runs after `warmup` untimed ones (at least one run, at most
     # max_runs, stopping once budget_s seconds of runs have passed) and the last run's outputs.
@@ -534,6 +660,24 @@ class Reference:
         nf = C.c_int(0)
         nb = self.lib.nnref_time_maxpool2d(_fp(x), N, Cc, H, W, k, s, _fp(g), warmup, max_runs, budget_s, _dp(tf),
                                            C.byref(nf), _dp(tb), _fp(y), _fp(dx))
+        return (self._times(tf, nf.value), y), (self._times(tb, nb), dx)
+
+    def time_batchnorm(self, x, w, b, eps, relu, g, warmup, max_runs, budget_s):
+        N, Cc, S = Oracle._nsc(x)
+        y, dx = np.empty_like(x), np.empty_like(x)
+        tf, tb = np.empty(max_runs, np.float64), np.empty(max_runs, np.float64)
+        nf = C.c_int(0)
+        nb = self.lib.nnref_time_batchnorm(_fp(x), N, Cc, S, _fp(w), _fp(b), float(eps), int(relu), _fp(g), warmup,
+                                           max_runs, budget_s, _dp(tf), C.byref(nf), _dp(tb), _fp(y), _fp(dx))
+        return (self._times(tf, nf.value), y), (self._times(tb, nb), dx)
+
+    def time_layernorm(self, x, gamma, beta, eps, g, warmup, max_runs, budget_s):
+        D = x.shape[-1]
+        y, dx = np.empty_like(x), np.empty_like(x)
+        tf, tb = np.empty(max_runs, np.float64), np.empty(max_runs, np.float64)
+        nf = C.c_int(0)
+        nb = self.lib.nnref_time_layernorm(_fp(x), x.size // D, D, _fp(gamma), _fp(beta), float(eps), _fp(g), warmup,
+                                           max_runs, budget_s, _dp(tf), C.byref(nf), _dp(tb), _fp(y), _fp(dx))
         return (self._times(tf, nf.value), y), (self._times(tb, nb), dx)
 
     def time_attention(self, q, k, v, heads, causal, g, warmup, max_runs, budget_s):

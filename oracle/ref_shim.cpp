@@ -552,6 +552,98 @@ int nnref_time_maxpool2d(const float* x, size_t N, size_t C, size_t H, size_t W,
 	return runs;
 }
 
+// nn::batchnorm in training mode (ops.cpp:900-1001) on x {N, C, S}: y, and mean and var when not null; then, when
+// g is not null, the node's backward rule `repeats` times (first into fresh gradients, then added), the gradients
+// of x, weight and bias into dx, dw, db (each may be null: that input then needs no gradient).
+int nnref_batchnorm(const float* x, size_t N, size_t C, size_t S, const float* w, const float* b, float eps, int relu,
+		float* y, float* mean, float* var, const float* g, int repeats, float* dx, float* dw, float* db) {
+	return guard([&] {
+		const Value xv = Value::leaf(make(x, {N, C, S}), dx != nullptr);
+		const Value wv = Value::leaf(make(w, {C}), dw != nullptr);
+		const Value bv = Value::leaf(make(b, {C}), db != nullptr);
+		Tensor mu({C}), va({C});
+		const Value r = nn::batchnorm(xv, wv, bv, eps, &mu, &va, relu != 0);
+		put(r.data(), y);
+		if (mean) put(mu, mean);
+		if (var) put(va, var);
+		if (g) {
+			const Tensor gt = make(g, r.data().shape());
+			run_backward_rule(r, gt, {&xv, &wv, &bv});
+			for (int i = 1; i < repeats; ++i) r.impl()->backward_fn(gt);
+			if (dx) put(xv.grad(), dx);
+			if (dw) put(wv.grad(), dw);
+			if (db) put(bv.grad(), db);
+		}
+	});
+}
+
+// nn::layernorm (ops.cpp:1003-1078) over R rows of D, then its backward rule as nnref_batchnorm's.
+int nnref_layernorm(const float* x, size_t R, size_t D, const float* gm, const float* bt, float eps, float* y,
+		const float* g, int repeats, float* dx, float* dgamma, float* dbeta) {
+	return guard([&] {
+		const Value xv = Value::leaf(make(x, {R, D}), dx != nullptr);
+		const Value gv = Value::leaf(make(gm, {D}), dgamma != nullptr);
+		const Value bv = Value::leaf(make(bt, {D}), dbeta != nullptr);
+		const Value r = nn::layernorm(xv, gv, bv, eps);
+		put(r.data(), y);
+		if (g) {
+			const Tensor gt = make(g, r.data().shape());
+			run_backward_rule(r, gt, {&xv, &gv, &bv});
+			for (int i = 1; i < repeats; ++i) r.impl()->backward_fn(gt);
+			if (dx) put(xv.grad(), dx);
+			if (dgamma) put(gv.grad(), dgamma);
+			if (dbeta) put(bv.grad(), dbeta);
+		}
+	});
+}
+
+// Timing of nn::batchnorm (relu folded or not) and of its backward rule, as nnref_time_maxpool2d.
+int nnref_time_batchnorm(const float* x, size_t N, size_t C, size_t S, const float* w, const float* b, float eps,
+		int relu, const float* g, int warmup, int max_runs, double budget_s, double* times_fwd, int* runs_fwd,
+		double* times_bwd, float* y, float* dx) {
+	int runs = -1;
+	guard([&] {
+		const Value xv = Value::leaf(make(x, {N, C, S}), true);
+		const Value wv = Value::leaf(make(w, {C}), true);
+		const Value bv = Value::leaf(make(b, {C}), true);
+		{
+			nn::NoGradGuard ng;
+			Value r = Value::leaf(Tensor::empty({0}));
+			*runs_fwd = time_runs([&] { r = nn::batchnorm(xv, wv, bv, eps, nullptr, nullptr, relu != 0); }, warmup,
+			                      max_runs, budget_s, times_fwd);
+			put(r.data(), y);
+		}
+		const Value r = nn::batchnorm(xv, wv, bv, eps, nullptr, nullptr, relu != 0);
+		const Tensor gt = make(g, r.data().shape());
+		runs = time_runs([&] { run_backward_rule(r, gt, {&xv, &wv, &bv}); }, warmup, max_runs, budget_s, times_bwd);
+		put(xv.grad(), dx);
+	});
+	return runs;
+}
+
+// Timing of nn::layernorm and of its backward rule.
+int nnref_time_layernorm(const float* x, size_t R, size_t D, const float* gm, const float* bt, float eps,
+		const float* g, int warmup, int max_runs, double budget_s, double* times_fwd, int* runs_fwd,
+		double* times_bwd, float* y, float* dx) {
+	int runs = -1;
+	guard([&] {
+		const Value xv = Value::leaf(make(x, {R, D}), true);
+		const Value gv = Value::leaf(make(gm, {D}), true);
+		const Value bv = Value::leaf(make(bt, {D}), true);
+		{
+			nn::NoGradGuard ng;
+			Value r = Value::leaf(Tensor::empty({0}));
+			*runs_fwd = time_runs([&] { r = nn::layernorm(xv, gv, bv, eps); }, warmup, max_runs, budget_s, times_fwd);
+			put(r.data(), y);
+		}
+		const Value r = nn::layernorm(xv, gv, bv, eps);
+		const Tensor gt = make(g, r.data().shape());
+		runs = time_runs([&] { run_backward_rule(r, gt, {&xv, &gv, &bv}); }, warmup, max_runs, budget_s, times_bwd);
+		put(xv.grad(), dx);
+	});
+	return runs;
+}
+
 // nn-cpp's side of the bench models' training step (the counterpart of nn-cpp_amd/src/bench/workloads.cpp, with
 // apps/bench/runner.cpp:33-45's clock points): the forward pass, then zero_grad and the backward pass from the
 // logits' gradient g; no loss, no optimizer step.

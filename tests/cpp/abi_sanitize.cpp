@@ -357,6 +357,65 @@ void conv_pool() {
 	EXPECT(nnh_maxpool2d_backward(g.data(), am.data(), kHuge, kHuge, 8, 8, 2, 2, dx.data(), 1, nullptr), INV);
 }
 
+void norm() {
+	auto x = buf(2 * 3 * 16), y = buf(2 * 3 * 16), g = buf(2 * 3 * 16), dx = buf(2 * 3 * 16), w = buf(16), b = buf(16);
+	auto mean = buf(32), var = buf(32), inv = buf(32), dw = buf(16), db = buf(16);
+	std::vector<unsigned char> alive(2 * 3 * 16);
+	size_t bytes = 0;
+	EXPECT(nnh_batchnorm_workspace_size(2, 3, 16, &bytes), OK);
+	EXPECT(bytes >= 2 * 2 * 3 * sizeof(float) ? OK : INV, OK);
+	EXPECT(nnh_batchnorm_workspace_size(kHuge, kHuge, 16, &bytes), INV);
+	EXPECT(nnh_batchnorm_workspace_size(2, kMax, 1, &bytes), INV);
+	EXPECT(nnh_batchnorm_forward(x.data(), 2, 3, 16, w.data(), b.data(), 1e-5f, 1, y.data(), alive.data(), mean.data(),
+	                             var.data(), inv.data(), nullptr),
+	       HIP);
+	EXPECT(nnh_batchnorm_forward(x.data(), 2, 3, 16, w.data(), b.data(), 1e-5f, 0, y.data(), nullptr, nullptr,
+	                             var.data(), inv.data(), nullptr),
+	       INV);
+	EXPECT(nnh_batchnorm_forward(x.data(), 2, 3, 16, w.data(), b.data(), 1e-5f, 0, x.data(), nullptr, mean.data(),
+	                             var.data(), inv.data(), nullptr),
+	       ALIAS);
+	EXPECT(nnh_batchnorm_forward(x.data(), 2, 3, 16, w.data(), b.data(), 1e-5f, 0, y.data(), nullptr, mean.data(),
+	                             mean.data(), inv.data(), nullptr),
+	       ALIAS);
+	EXPECT(nnh_batchnorm_forward(x.data(), kHuge, kHuge, kHuge, w.data(), b.data(), 1e-5f, 0, y.data(), nullptr,
+	                             mean.data(), var.data(), inv.data(), nullptr),
+	       INV);
+	EXPECT(nnh_batchnorm_forward(nullptr, 2, 0, 16, nullptr, nullptr, 1e-5f, 0, nullptr, nullptr, nullptr, nullptr,
+	                             nullptr, nullptr),
+	       OK);
+	EXPECT(nnh_batchnorm_backward(g.data(), x.data(), alive.data(), w.data(), mean.data(), inv.data(), 2, 3, 16,
+	                              dx.data(), 1, dw.data(), 1, db.data(), 1, nullptr),
+	       HIP);
+	EXPECT(nnh_batchnorm_backward(g.data(), x.data(), nullptr, w.data(), mean.data(), inv.data(), 2, 3, 16, g.data(), 1,
+	                              dw.data(), 1, db.data(), 1, nullptr),
+	       ALIAS);
+	EXPECT(nnh_batchnorm_backward(g.data(), x.data(), nullptr, w.data(), nullptr, inv.data(), 2, 3, 16, dx.data(), 1,
+	                              nullptr, 1, nullptr, 1, nullptr),
+	       INV);
+	EXPECT(nnh_batchnorm_backward(g.data(), x.data(), nullptr, w.data(), mean.data(), inv.data(), 2, 3, 16, nullptr, 1,
+	                              nullptr, 1, nullptr, 1, nullptr),
+	       OK);
+	EXPECT(nnh_layernorm_forward(x.data(), 6, 16, w.data(), b.data(), 1e-5f, y.data(), mean.data(), inv.data(), nullptr),
+	       HIP);
+	EXPECT(nnh_layernorm_forward(x.data(), 6, 0, w.data(), b.data(), 1e-5f, y.data(), mean.data(), inv.data(), nullptr),
+	       INV);
+	EXPECT(nnh_layernorm_forward(x.data(), kHuge, kHuge, w.data(), b.data(), 1e-5f, y.data(), mean.data(), inv.data(),
+	                             nullptr),
+	       INV);
+	EXPECT(nnh_layernorm_forward(x.data(), 6, 16, w.data(), b.data(), 1e-5f, x.data(), mean.data(), inv.data(), nullptr),
+	       ALIAS);
+	EXPECT(nnh_layernorm_backward(g.data(), x.data(), w.data(), mean.data(), inv.data(), 6, 16, dx.data(), 1, dw.data(),
+	                              1, db.data(), 1, nullptr),
+	       HIP);
+	EXPECT(nnh_layernorm_backward(g.data(), x.data(), w.data(), mean.data(), inv.data(), 6, 16, dx.data(), 1, dw.data(),
+	                              1, dw.data(), 1, nullptr),
+	       ALIAS);
+	EXPECT(nnh_layernorm_backward(g.data(), x.data(), nullptr, mean.data(), inv.data(), 6, 16, dx.data(), 1, nullptr, 1,
+	                              nullptr, 1, nullptr),
+	       INV);
+}
+
 void misc() {
 	EXPECT(nnh_set_numerics(5), INV);
 	EXPECT(nnh_set_numerics(NNH_NUMERICS_SPLIT_DEPTH), OK);
@@ -378,6 +437,7 @@ int main() {
 		return 77;
 	}
 	gemm();
+	norm();
 	sizes();
 	matmul();
 	linear_relu();

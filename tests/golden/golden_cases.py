@@ -137,3 +137,41 @@ def pool_inputs(spec):
         x[-1, -1, 0:k, 0:k] = np.nan                             # the first window of the last plane: all NaN
         x[0, -1, H // 2, W // 2] = np.nan                        # a NaN among ordinary values
     return np.ascontiguousarray(x), np.ascontiguousarray(g), k, s
+
+
+# nn::batchnorm in training mode on {N, C, S...}: (N, C, spatial shape, relu, seed). Inputs: x from U[-3, 5], weight
+# from U[0.5, 1.5], bias from U[-1, 1], the upstream gradient from U[-1, 1].
+BATCHNORM_CASES = [
+    ("bn2d_4x3x5x5", (4, 3, (5, 5), 0, 71)),
+    ("bn2d_relu_4x3x5x5", (4, 3, (5, 5), 1, 72)),
+    ("bn1d_16x4", (16, 4, (), 0, 73)),
+    ("bn2d_relu_tail_3x2x3x7", (3, 2, (3, 7), 1, 74)),
+    ("bn2d_one_element_per_channel_1x3x1x1", (1, 3, (1, 1), 0, 75)),
+]
+
+
+def batchnorm_inputs(spec):
+    N, C, sp, relu, seed = spec
+    shape = (N, C) + tuple(sp)
+    x, w, b, g = synth.uniform_operands(seed, [shape, (C,), (C,), shape])
+    x = (x * 4 + 1).astype(np.float32)
+    w = (w * 0.5 + 1).astype(np.float32)
+    return np.ascontiguousarray(x), np.ascontiguousarray(w), np.ascontiguousarray(b), np.ascontiguousarray(g), relu
+
+
+# nn::layernorm over the last axis: (shape, seed). x from U[-2, 3], gamma U[0.5, 1.5], beta U[-1, 1].
+LAYERNORM_CASES = [
+    ("ln_2x7", ((2, 7), 76)),
+    ("ln_2x3x5", ((2, 3, 5), 77)),
+    ("ln_16x64", ((16, 64), 78)),
+    ("ln_3x1", ((3, 1), 79)),
+]
+
+
+def layernorm_inputs(spec):
+    shape, seed = spec
+    D = shape[-1]
+    x, gm, bt, g = synth.uniform_operands(seed, [shape, (D,), (D,), shape])
+    x = (x * 2.5 + 0.5).astype(np.float32)
+    gm = (gm * 0.5 + 1).astype(np.float32)
+    return np.ascontiguousarray(x), np.ascontiguousarray(gm), np.ascontiguousarray(bt), np.ascontiguousarray(g)

@@ -18,8 +18,9 @@ sys.path.insert(0, os.path.join(ROOT, "nn-cpp_amd"))
 sys.path.insert(0, os.path.join(ROOT, "oracle"))
 sys.path.insert(0, HERE)
 
-from golden_cases import (ATTENTION_CASES, CONV_CASES, LINEAR_CASES, MATMUL_CASES, POOL_CASES, SGEMM_CASES,  # noqa: E402
-                          attention_inputs, conv_inputs, linear_inputs, matmul_inputs, pool_inputs, sgemm_inputs)
+from golden_cases import (ATTENTION_CASES, BATCHNORM_CASES, CONV_CASES, LAYERNORM_CASES, LINEAR_CASES,  # noqa: E402
+                          MATMUL_CASES, POOL_CASES, SGEMM_CASES, attention_inputs, batchnorm_inputs, conv_inputs,
+                          layernorm_inputs, linear_inputs, matmul_inputs, pool_inputs, sgemm_inputs)
 from pyoracle import Reference  # noqa: E402
 
 
@@ -56,6 +57,19 @@ def main():
         rc, y, dx = ref.maxpool2d(x, k, s, g)
         assert rc == 0, name
         out[f"pool/{name}/y"], out[f"pool/{name}/dx"] = y, dx
+    for name, spec in BATCHNORM_CASES:
+        x, w, b, g, relu = batchnorm_inputs(spec)
+        rc, y, mean, var, (dx, dw, db) = ref.batchnorm(x, w, b, 1e-5, relu, g=g)
+        assert rc == 0, name
+        for key, val in (("y", y), ("mean", mean), ("var", var), ("dx", dx), ("dw", dw), ("db", db)):
+            out[f"batchnorm/{name}/{key}"] = val
+    for name, spec in LAYERNORM_CASES:
+        x, gm, bt, g = layernorm_inputs(spec)
+        D = x.shape[-1]
+        rc, y, (dx, dg, db) = ref.layernorm(x.reshape(-1, D), gm, bt, 1e-5, g=g.reshape(-1, D))
+        assert rc == 0, name
+        for key, val in (("y", y.reshape(x.shape)), ("dx", dx.reshape(x.shape)), ("dgamma", dg), ("dbeta", db)):
+            out[f"layernorm/{name}/{key}"] = val
     path = os.path.join(HERE, "reference_vectors.npz")
     np.savez_compressed(path, **out)
     print(f"wrote {len(out)} arrays to {path} ({os.path.getsize(path)} bytes)")

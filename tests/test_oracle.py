@@ -525,3 +525,124 @@ def test_split_depth_rule(oracle):
         oracle.set_numerics(0)
     assert not oracle.depth_cut(512, 512, 256) and oracle.depth_cut(40, 48, 1100)
     assert oracle.piece_depth(40, 48, 1100) == 128 and oracle.piece_depth(512, 512, 512) == 0
+
+
+# ---------------------------------------------------------------- normalisation (ops.cpp:800-1078)
+
+def test_golden_batchnorm_and_layernorm(oracle):
+    """The restatements reproduce nn-cpp's outputs stored in the golden fixture: y, mean, var and the three
+    gradients (fresh) of batchnorm with and without its folded ReLU, and layernorm's y and gradients."""
+    gc, g = golden()
+    for name, spec in gc.BATCHNORM_CASES:
+        x, w, b, gr, relu = gc.batchnorm_inputs(spec)
+        y, alive, mean, var, inv = oracle.batchnorm_forward(x, w, b, 1e-5, relu)
+        dx, dw, db = oracle.batchnorm_backward(gr, x, alive, w, mean, inv)
+        for key, val in (("y", y), ("mean", mean), ("var", var), ("dx", dx), ("dw", dw), ("db", db)):
+            assert val.tobytes() == g[f"batchnorm/{name}/{key}"].tobytes(), (name, key)
+    for name, spec in gc.LAYERNORM_CASES:
+        x, gm, bt, gr = gc.layernorm_inputs(spec)
+        y, mean, inv = oracle.layernorm_forward(x, gm, bt, 1e-5)
+        dx, dg, db = oracle.layernorm_backward(gr, x, gm, mean, inv)
+        for key, val in (("y", y), ("dx", dx), ("dgamma", dg), ("dbeta", db)):
+            assert val.tobytes() == g[f"layernorm/{name}/{key}"].tobytes(), (name, key)
+
+
+BN_SWEEP = [(4, 3, (5, 5)), (2, 5, (1, 1)), (3, 2, (17,)), (8, 4, (2, 3, 3)), (1, 1, ()), (64, 3, ()),
+            (5, 2, (8,)), (2, 3, (2049,)), (300, 2, (1,))]
+
+
+@pytest.mark.parametrize("shape", BN_SWEEP)
+@pytest.mark.parametrize("relu", [0, 1])
+def test_batchnorm_matches_nncpp(oracle, ref, shape, relu):
+    """Against nn-cpp's compiled nn::batchnorm: rows with and without an eight-element tail, one element per row,
+    many samples, rows longer than a staging chunk; the backward rule fresh and then added a second time."""
+    N, Cc, sp = shape
+    full = (N, Cc) + tuple(sp)
+    rng = np.random.default_rng(N * 31 + Cc + relu)
+    x = (rng.uniform(-3, 5, full)).astype(np.float32)
+    w = rng.uniform(0.5, 1.5, Cc).astype(np.float32)
+    b = rng.uniform(-1, 1, Cc).astype(np.float32)
+    g = rng.normal(size=full).astype(np.float32)
+    y, alive, mean, var, inv = oracle.batchnorm_forward(x, w, b, 1e-5, relu)
+    rc, yr, mr, vr, (dxr, dwr, dbr) = ref.batchnorm(x, w, b, 1e-5, relu, g=g)
+    assert rc == 0
+    assert y.tobytes() == yr.tobytes() and mean.tobytes() == mr.tobytes() and var.tobytes() == vr.tobytes()
+    dx, dw, db = oracle.batchnorm_backward(g, x, alive, w, mean, inv)
+    assert (dx.tobytes(), dw.tobytes(), db.tobytes()) == (dxr.tobytes(), dwr.tobytes(), dbr.tobytes())
+    rc, _, _, _, (dx2r, dw2r, db2r) = ref.batchnorm(x, w, b, 1e-5, relu, g=g, repeats=2)
+    dx2, dw2, db2 = oracle.batchnorm_backward(g, x, alive, w, mean, inv, dx, False, dw, False, db, False)
+    assert (dx2.tobytes(), dw2.tobytes(), db2.tobytes()) == (dx2r.tobytes(), dw2r.tobytes(), db2r.tobytes())
+
+
+@pytest.mark.parametrize("shape", [(5, 4), (3, 7, 64), (2, 1), (9, 33), (40, 30, 16), (2, 515)])
+def test_layernorm_matches_nncpp(oracle, ref, shape):
+    D = shape[-1]
+    rng = np.random.default_rng(sum(shape))
+    x = rng.uniform(-2, 3, shape).astype(np.float32)
+    gm = rng.uniform(0.5, 1.5, D).astype(np.float32)
+    bt = rng.uniform(-1, 1, D).astype(np.float32)
+    g = rng.normal(size=shape).astype(np.float32)
+    y, mean, inv = oracle.layernorm_forward(x, gm, bt, 1e-5)
+    rc, yr, (dxr, dgr, dbr) = ref.layernorm(x.reshape(-1, D), gm, bt, 1e-5, g=g.reshape(-1, D))
+    assert rc == 0 and y.tobytes() == yr.reshape(shape).tobytes()
+    dx, dg, db = oracle.layernorm_backward(g, x, gm, mean, inv)
+    assert (dx.tobytes(), dg.tobytes(), db.tobytes()) == (dxr.reshape(shape).tobytes(), dgr.tobytes(), dbr.tobytes())
+    rc, _, (dx2r, dg2r, db2r) = ref.layernorm(x.reshape(-1, D), gm, bt, 1e-5, g=g.reshape(-1, D), repeats=2)
+    dx2, dg2, db2 = oracle.layernorm_backward(g, x, gm, mean, inv, dx, False, dg, False, db, False)
+    assert (dx2.tobytes(), dg2.tobytes(), db2.tobytes()) == (dx2r.reshape(shape).tobytes(), dg2r.tobytes(),
+                                                             db2r.tobytes())
+
+
+def test_batchnorm_hand_values_and_fp64(oracle):
+    """Hand values (test_nn.cpp:527-537's batches): {0, 2} has mean 1 and biased variance 1, so with eps 0 the
+    output is exactly -1, 1; {4, 4} has mean 4 and variance 0. Then against the fp64 normalisation: every channel of
+    the output has mean 0 and variance 1 (test_nn.cpp:341-354's criterion), and y = xhat * w + b within a few ulps;
+    the gradients satisfy the identities of the exact backward: sum(dx) = 0 and sum(dx * xhat) = 0 per channel,
+    db = sum(g), dw = sum(g * xhat)."""
+    y, _, mean, var, _ = oracle.batchnorm_forward(np.array([[0], [2]], np.float32), np.ones(1, np.float32),
+                                                  np.zeros(1, np.float32), 0.0)
+    assert y.ravel().tolist() == [-1.0, 1.0] and mean.tolist() == [1.0] and var.tolist() == [1.0]
+    _, _, mean, var, _ = oracle.batchnorm_forward(np.array([[4], [4]], np.float32), np.ones(1, np.float32),
+                                                  np.zeros(1, np.float32), 1e-5)
+    assert mean.tolist() == [4.0] and var.tolist() == [0.0]
+    rng = np.random.default_rng(5)
+    x = rng.uniform(-3, 5, (8, 3, 5, 5)).astype(np.float32)
+    w = rng.uniform(0.5, 1.5, 3).astype(np.float32)
+    b = rng.uniform(-1, 1, 3).astype(np.float32)
+    g = rng.normal(size=x.shape).astype(np.float32)
+    y, _, mean, var, inv = oracle.batchnorm_forward(x, w, b, 1e-5)
+    xhat = oracle.batchnorm_f64(x, 1e-5)
+    ref64 = xhat * w[None, :, None, None] + b[None, :, None, None]
+    assert np.max(np.abs(y - ref64)) < 1e-5
+    yn = (y - b[None, :, None, None]) / w[None, :, None, None]
+    assert np.all(np.abs(yn.mean(axis=(0, 2, 3))) < 1e-3) and np.all(np.abs(yn.var(axis=(0, 2, 3)) - 1) < 1e-3)
+    dx, dw, db = oracle.batchnorm_backward(g, x, None, w, mean, inv)
+    assert np.max(np.abs(dx.astype(np.float64).sum(axis=(0, 2, 3)))) < 1e-3
+    assert np.max(np.abs((dx * xhat).sum(axis=(0, 2, 3)))) < 1e-3
+    assert np.allclose(db, g.astype(np.float64).sum(axis=(0, 2, 3)), atol=1e-4)
+    assert np.allclose(dw, (g * xhat).sum(axis=(0, 2, 3)), atol=1e-3)
+
+
+def test_layernorm_hand_values_and_fp64(oracle):
+    """test_transformer.cpp:64-80: the row 1, 2, 3, 4 comes out with mean 0 and variance 1, a constant row comes out
+    0, and equal rows come out equal whatever the leading shape; fp64 normalisation within a few ulps; dbeta is the
+    column sum of g and dgamma the column sum of g * xhat."""
+    ones, zeros = np.ones(4, np.float32), np.zeros(4, np.float32)
+    y, _, _ = oracle.layernorm_forward(np.array([[1, 2, 3, 4]], np.float32), ones, zeros, 1e-5)
+    assert abs(y.mean()) < 1e-4 and abs(((y - y.mean()) ** 2).mean() - 1) < 1e-4
+    c, _, _ = oracle.layernorm_forward(np.full((1, 4), 3, np.float32), ones, zeros, 1e-5)
+    assert np.all(c == 0)
+    rows, _, _ = oracle.layernorm_forward(np.tile(np.array([1, 2, 3, 4], np.float32), (2, 3, 1)), ones, zeros, 1e-5)
+    assert all(r.tobytes() == y.ravel().tobytes() for r in rows.reshape(-1, 4))
+    rng = np.random.default_rng(6)
+    x = rng.uniform(-2, 3, (40, 30, 16)).astype(np.float32)
+    gm = rng.uniform(0.5, 1.5, 16).astype(np.float32)
+    bt = rng.uniform(-1, 1, 16).astype(np.float32)
+    g = rng.normal(size=x.shape).astype(np.float32)
+    y, mean, inv = oracle.layernorm_forward(x, gm, bt, 1e-5)
+    xhat = oracle.layernorm_f64(x, 1e-5)
+    assert np.max(np.abs(y - (xhat * gm + bt))) < 1e-5
+    dx, dg, db = oracle.layernorm_backward(g, x, gm, mean, inv)
+    assert np.allclose(db, g.reshape(-1, 16).astype(np.float64).sum(0), atol=1e-3)
+    assert np.allclose(dg, (g * xhat).reshape(-1, 16).sum(0), atol=1e-3)
+    assert np.max(np.abs(dx.astype(np.float64).sum(-1))) < 1e-4
