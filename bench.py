@@ -533,6 +533,104 @@ def build_rows(report=False, split=False):
     return rows
 
 
+def build_next_rows():
+    """The memory-bound ops next to the path on nn-cpp's own workloads (not BASELINE configs): batchnorm with its
+    folded ReLU at cnn_fer's first Conv-BN-ReLU (x [64,16,48,48], apps/bench/workloads.cpp:185-199) and layernorm
+    over config 4's activations (x [32,256,512]) and transformer_tiny's ([16,64,64]), forward and backward. Inputs
+    are seeded U[-3,5] activations, U[0.5,1.5] scales, U[-1,1] shifts and N(0,1) output gradients; HBM-bound, the
+    algorithmic bytes count x (and g) read once and y (dx) written once, not the alive flags or the per-channel or
+    per-row statistics."""
+    import numpy as np
+    import torch
+
+    import nnh
+    from nnh import synth
+    L = nnh.lib()
+    dev = torch.device("cuda:0")
+    d = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+    st = lambda: nnh._stream(None)
+    P = nnh._ptr
+    rows = []
+    # batchnorm + ReLU, cnn_fer layer 1
+    N, Cc, H, W = 64, 16, 48, 48
+    S = H * W
+    hx = (synth.mt19937_uniform(41, N * Cc * S, -3.0, 5.0)).reshape(N, Cc, H, W)
+    hw = synth.mt19937_uniform(42, Cc, 0.5, 1.5)
+    hb = synth.mt19937_uniform(43, Cc, -1.0, 1.0)
+    hg = synth.normal(44, (N, Cc, H, W))
+    x, w, b, g = d(hx), d(hw), d(hb), d(hg)
+    y, dx = torch.empty_like(x), torch.empty_like(x)
+    alive = torch.empty(x.shape, dtype=torch.uint8, device=dev)
+    mean, var, inv = (torch.empty(Cc, device=dev) for _ in range(3))
+    dw, db = torch.empty(Cc, device=dev), torch.empty(Cc, device=dev)
+
+    def bn_fwd():
+        nnh.check(L.nnh_batchnorm_forward(P(x), N, Cc, S, P(w), P(b), 1e-5, 1, P(y), P(alive), P(mean), P(var), P(inv),
+                                          st()))
+
+    def bn_bwd():
+        nnh.check(L.nnh_batchnorm_backward(P(g), P(x), P(alive), P(w), P(mean), P(inv), N, Cc, S, P(dx), 1, P(dw), 1,
+                                           P(db), 1, st()))
+
+    bn_fwd()
+    bn_cache = {}
+
+    def bn_cpu(ref, wu, r, bud):
+        if (wu, r, bud) not in bn_cache:
+            bn_cache[(wu, r, bud)] = ref.time_batchnorm(hx, hw, hb, 1e-5, 1, hg, wu, r, bud)
+        return bn_cache[(wu, r, bud)]
+
+    xb = 4 * hx.size
+    rows.append(Row("next", "batchnorm_relu_forward", "nn::batchnorm + folded ReLU forward, cnn_fer layer 1: "
+                    "x [64,16,48,48] (training-mode batch statistics)", bn_fwd, lambda: [y], 0, nbytes=2 * xb,
+                    bound="hbm", cpu=lambda ref, wu, r, bud: (lambda f, bw: (f[0], [f[1]]))(*bn_cpu(ref, wu, r, bud)),
+                    est_ms=0.02))
+    rows.append(Row("next", "batchnorm_relu_backward", "nn::batchnorm + folded ReLU backward: dx, dweight, dbias",
+                    bn_bwd, lambda: [dx, dw, db], 0, nbytes=3 * xb, bound="hbm",
+                    cpu=lambda ref, wu, r, bud: (lambda f, bw: (bw[0], [bw[1], None, None]))(*bn_cpu(ref, wu, r, bud)),
+                    est_ms=0.02))
+    for key, shape, seed in (("layernorm_attention_acts", (32, 256, 512), 45), ("layernorm_transformer_tiny",
+                                                                               (16, 64, 64), 46)):
+        D = shape[-1]
+        R = int(np.prod(shape)) // D
+        hlx = synth.mt19937_uniform(seed, R * D, -3.0, 5.0).reshape(shape)
+        hgm = synth.mt19937_uniform(seed + 10, D, 0.5, 1.5)
+        hbt = synth.mt19937_uniform(seed + 20, D, -1.0, 1.0)
+        hlg = synth.normal(seed + 30, shape)
+        lx, gm, bt, lg = d(hlx), d(hgm), d(hbt), d(hlg)
+        ly, ldx = torch.empty_like(lx), torch.empty_like(lx)
+        lmean, linv = torch.empty(R, device=dev), torch.empty(R, device=dev)
+        dgm, dbt = torch.empty(D, device=dev), torch.empty(D, device=dev)
+
+        def ln_fwd(lx=lx, gm=gm, bt=bt, ly=ly, lmean=lmean, linv=linv, R=R, D=D):
+            nnh.check(L.nnh_layernorm_forward(P(lx), R, D, P(gm), P(bt), 1e-5, P(ly), P(lmean), P(linv), st()))
+
+        def ln_bwd(lg=lg, lx=lx, gm=gm, lmean=lmean, linv=linv, ldx=ldx, dgm=dgm, dbt=dbt, R=R, D=D):
+            nnh.check(L.nnh_layernorm_backward(P(lg), P(lx), P(gm), P(lmean), P(linv), R, D, P(ldx), 1, P(dgm), 1,
+                                               P(dbt), 1, st()))
+
+        ln_fwd()
+        cache = {}
+
+        def ln_cpu(ref, wu, r, bud, hlx=hlx, hgm=hgm, hbt=hbt, hlg=hlg, cache=cache):
+            if (wu, r, bud) not in cache:
+                cache[(wu, r, bud)] = ref.time_layernorm(hlx, hgm, hbt, 1e-5, hlg, wu, r, bud)
+            return cache[(wu, r, bud)]
+
+        lb = 4 * hlx.size
+        dims = "x".join(map(str, shape))
+        rows.append(Row("next", key + "_forward", f"nn::layernorm forward over the last axis of [{dims}]", ln_fwd,
+                        lambda ly=ly: [ly], 0, nbytes=2 * lb, bound="hbm",
+                        cpu=lambda ref, wu, r, bud, f=ln_cpu: (lambda a, bw: (a[0], [a[1]]))(*f(ref, wu, r, bud)),
+                        est_ms=0.02))
+        rows.append(Row("next", key + "_backward", f"nn::layernorm backward over [{dims}]: dx, dgamma, dbeta", ln_bwd,
+                        lambda ldx=ldx, dgm=dgm, dbt=dbt: [ldx, dgm, dbt], 0, nbytes=3 * lb, bound="hbm",
+                        cpu=lambda ref, wu, r, bud, f=ln_cpu: (lambda a, bw: (bw[0], [bw[1], None, None]))(
+                            *f(ref, wu, r, bud)),
+                        est_ms=0.03))
+    return rows
+
+
 def run_gpu_rows(rows):
     """Times every row on the GPU, checks that three runs give the same bits, and keeps one run's outputs on the
     host."""
@@ -749,7 +847,7 @@ def row_json(r):
 def report(with_cpu=True):
     """The config rows as a markdown table, with the fp64 checks (slow)."""
     import torch
-    rows = build_rows(report=True)
+    rows = build_rows(report=True) + build_next_rows()
     run_gpu_rows(rows)
     setup = run_cpu_rows(rows) if with_cpu else None
     for r in rows:
@@ -836,7 +934,7 @@ def main():
         split = args.row.endswith("_split")
         prev = nnh.set_numerics(nnh.NUMERICS_SPLIT_DEPTH if split else nnh.NUMERICS_NNCPP)
         try:
-            rows = build_rows(split=split)
+            rows = build_rows(split=split) + ([] if split else build_next_rows())
             keys = [r.key for r in rows]
             rows = [r for r in rows if r.key == args.row]
             if not rows:
@@ -934,14 +1032,18 @@ def main():
                                                     for g, w in zip(r.host_outs, e.host_outs))
                 r.result["maxabs_vs_nn_cpp"] = max(float(np.max(np.abs(g.astype(np.float64) - w)))
                                                    for g, w in zip(r.host_outs, e.host_outs))
+    next_rows = []
+    if not args.no_configs:
+        next_rows = build_next_rows()
+        run_gpu_rows(next_rows)
     headline = Row(5, "headline", f"nn::kernels::sgemm {m}^3", None, None, flops,
                    cpu=lambda ref, w, r, bud: ref.time_matmul(a, b, 0, 0, w, r, bud))
     setup = None
     if not args.no_cpu_baseline:
-        setup = run_cpu_rows(rows, headline)
+        setup = run_cpu_rows(rows + next_rows, headline)
     workloads = [] if args.no_configs else run_workloads(with_cpu=not args.no_cpu_baseline)
     if args.csv and rows:
-        write_csv(args.csv, rows, setup, workloads)
+        write_csv(args.csv, rows + next_rows, setup, workloads)
     cpu = None
     hb = headline.result.get("cpu_baseline")
     if hb:
@@ -996,6 +1098,7 @@ def main():
                 "bitwise_vs_two_ops": conv1_pool1.result.get("bitwise_vs_two_ops")}},
         "configs": [row_json(r) for r in rows],
         "configs_split_depth": [row_json(r) for r in split_rows],
+        "next_rows": [row_json(r) for r in next_rows],
         "workloads": [{k: ({kk: (round(vv, 4) if isinstance(vv, float) else vv) for kk, vv in v.items()}
                            if isinstance(v, dict) else (round(v, 2) if isinstance(v, float) else v))
                        for k, v in w.items()} for w in workloads],

@@ -4,8 +4,8 @@
 // against it reads the same:
 //   * Tensor and matmul(a, b, trans_a, trans_b)                  include/nn/tensor.hpp:47-510, 465-491
 //   * Value, NoGradGuard, grad_accum and backward                include/nn/autograd/value.hpp:41-228
-//   * matmul, linear, matmul_bt, relu, reshape, conv2d, conv2d_relu, maxpool2d, attention, scaled_masked_softmax
-//     (and conv2d_relu_maxpool2d, the two ops of a first layer in one call)
+//   * matmul, linear, matmul_bt, relu, reshape, conv2d, conv2d_relu, maxpool2d, batchnorm, layernorm, attention,
+//     scaled_masked_softmax (and conv2d_relu_maxpool2d, the two ops of a first layer in one call)
 //                                                                include/nn/autograd/ops.hpp:22-523
 // The difference is where the numbers live: a Tensor's storage is HBM, so a chain of ops (linear -> relu ->
 // linear, conv -> pool -> conv) never leaves the device; data crosses PCIe only in from_host / to_host. Every op
@@ -145,6 +145,12 @@ Value maxpool2d(const Value& x, size_t kernel_size, size_t stride);
 // network's first layer). No counterpart in the reference, whose Sequential runs the two modules in turn.
 Value conv2d_relu_maxpool2d(const Value& x, const Value& weight, const Value& bias, int stride, int padding,
                             size_t kernel_size, size_t pool_stride);
+// ops.hpp:114-115: batch normalisation in training mode over every axis but axis 1 of x {N, C, ...}; mean_out and
+// var_out (optional) receive the batch mean and biased variance {C}; fuse_relu clips the result at 0 in the same op.
+Value batchnorm(const Value& x, const Value& weight, const Value& bias, float eps, Tensor* mean_out = nullptr,
+                Tensor* var_out = nullptr, bool fuse_relu = false);
+// ops.hpp:130: layer normalisation over the last axis of x {..., D}, gamma and beta {D}.
+Value layernorm(const Value& x, const Value& gamma, const Value& beta, float eps);
 // ops.hpp:324: multi-head attention core; key_padding_mask {N, Tk} (0 = padded) or empty.
 Value attention(const Value& q, const Value& k, const Value& v, size_t heads, const Tensor& key_padding_mask,
                 bool causal);

@@ -443,6 +443,63 @@ Value conv2d_relu_maxpool2d(const Value& x, const Value& weight, const Value& bi
 	return pool_node(conv, kernel_size, pool_stride, std::move(p), std::move(arg));
 }
 
+Value batchnorm(const Value& x, const Value& weight, const Value& bias, float eps, Tensor* mean_out, Tensor* var_out,
+                bool fuse_relu) {
+	const auto& xs = x.data().shape();
+	// ops.cpp:901-907
+	if (xs.size() < 2) throw TensorShapeError("nn::hip: batchnorm needs a channel axis");
+	const size_t N = xs[0], C = xs[1];
+	size_t S = 1;
+	for (size_t i = 2; i < xs.size(); ++i) S *= xs[i];
+	if (weight.data().size() != C || bias.data().size() != C) throw TensorShapeError("nn::hip: batchnorm parameters");
+	Tensor y = Tensor::empty(xs);
+	Tensor mean = Tensor::empty({C}), var = Tensor::empty({C}), inv = Tensor::empty({C});
+	const bool keep = fuse_relu && NoGradGuard::grad_enabled() &&
+	                  (x.requires_grad() || weight.requires_grad() || bias.requires_grad());
+	std::shared_ptr<Block> alive = keep ? side_buffer(y.size()) : nullptr;
+	check(nnh_batchnorm_forward(x.data().data(), N, C, S, weight.data().data(), bias.data().data(), eps,
+	                            fuse_relu ? 1 : 0, y.data(), alive ? static_cast<unsigned char*>(alive->p) : nullptr,
+	                            mean.data(), var.data(), inv.data(), g_stream));
+	if (mean_out) *mean_out = mean;
+	if (var_out) *var_out = var;
+	return Value::node(std::move(y), {x, weight, bias}, [x, weight, bias, mean, inv, alive, N, C, S](const Tensor& g) {
+		// ops.cpp:960-1000: dx by grad_accum, then weight and bias (grad() +=, a fresh one zeroed first)
+		bool fx = false, fw = false, fb = false;
+		float* dx = grad_if(x, fx);
+		float* dw = grad_if(weight, fw);
+		float* db = grad_if(bias, fb);
+		if (!dx && !dw && !db) return;
+		check(nnh_batchnorm_backward(g.data(), x.data().data(),
+		                             alive ? static_cast<const unsigned char*>(alive->p) : nullptr,
+		                             weight.data().data(), mean.data(), inv.data(), N, C, S, dx, fx, dw, fw, db, fb,
+		                             g_stream));
+	});
+}
+
+Value layernorm(const Value& x, const Value& gamma, const Value& beta, float eps) {
+	const auto& xs = x.data().shape();
+	// ops.cpp:1004-1006
+	if (xs.empty() || gamma.data().size() != xs.back() || beta.data().size() != xs.back())
+		throw TensorShapeError("nn::hip: layernorm shapes");
+	const size_t D = xs.back();
+	if (D == 0) throw std::invalid_argument("nn::hip: layernorm over an empty axis");
+	const size_t R = x.data().size() / D;
+	Tensor y = Tensor::empty(xs);
+	Tensor mean = Tensor::empty({R}), inv = Tensor::empty({R});
+	check(nnh_layernorm_forward(x.data().data(), R, D, gamma.data().data(), beta.data().data(), eps, y.data(),
+	                            mean.data(), inv.data(), g_stream));
+	return Value::node(std::move(y), {x, gamma, beta}, [x, gamma, beta, mean, inv, R, D](const Tensor& g) {
+		// ops.cpp:1035-1077: dx by grad_accum, then gamma and beta (grad() +=)
+		bool fx = false, fg = false, fb = false;
+		float* dx = grad_if(x, fx);
+		float* dg = grad_if(gamma, fg);
+		float* db = grad_if(beta, fb);
+		if (!dx && !dg && !db) return;
+		check(nnh_layernorm_backward(g.data(), x.data().data(), gamma.data().data(), mean.data(), inv.data(), R, D, dx,
+		                             fx, dg, fg, db, fb, g_stream));
+	});
+}
+
 Value attention(const Value& q, const Value& k, const Value& v, size_t heads, const Tensor& key_padding_mask,
                 bool causal) {
 	const auto& qs = q.data().shape();

@@ -17,6 +17,8 @@
 // gamma/beta gradient sums run down columns in row order, one thread per column (ops.cpp:1063-1075).
 #include "norm.hpp"
 
+#include <algorithm>
+
 #include "fastdiv.hpp"
 
 namespace nnh {
@@ -197,17 +199,45 @@ __global__ void __launch_bounds__(256) bn_rows_kernel(const BnRowArgs a) {
 			const int lfull = (int)(full - s0 < len ? (full - s0 > 0 ? full - s0 : 0) : len);
 			if (r < nrows) {
 				const float* xr = xs + r * kPitch;
-#pragma unroll 8
-				for (int l = k; l < lfull; l += 8) {
+				const float* gr = gs + r * kPitch;
+				const unsigned char* fr = fs + r * kPitch;
+				// 16 steps of the lane's chain per batch: the batch's LDS reads are all issued before its adds
+				int l = k;
+				for (; l + 8 * 15 < lfull; l += 8 * 16) {
+					float xv[16], gv[16];
+					unsigned char fv[16];
+#pragma unroll
+					for (int u = 0; u < 16; ++u) {
+						xv[u] = xr[l + 8 * u];
+						if (MODE == kBwd) {
+							gv[u] = gr[l + 8 * u];
+							if (masked) fv[u] = fr[l + 8 * u];
+						}
+					}
+#pragma unroll
+					for (int u = 0; u < 16; ++u) {
+						if (MODE == kSum) {
+							acc0 = acc0 + xv[u];
+						} else if (MODE == kSq) {
+							const float d = xv[u] - mu;
+							acc0 = acc0 + d * d;
+						} else {
+							const float gm = masked ? (fv[u] ? gv[u] : 0.0f) : gv[u];
+							acc0 = acc0 + gm;
+							acc1 = acc1 + gm * (xv[u] - mu);
+						}
+					}
+				}
+				for (; l < lfull; l += 8) {
 					if (MODE == kSum) {
 						acc0 = acc0 + xr[l];
 					} else if (MODE == kSq) {
 						const float d = xr[l] - mu;
 						acc0 = acc0 + d * d;
 					} else {
-						const float gv = masked ? (fs[r * kPitch + l] ? gs[r * kPitch + l] : 0.0f) : gs[r * kPitch + l];
-						acc0 = acc0 + gv;
-						acc1 = acc1 + gv * (xr[l] - mu);
+						const float gm = masked ? (fr[l] ? gr[l] : 0.0f) : gr[l];
+						acc0 = acc0 + gm;
+						acc1 = acc1 + gm * (xr[l] - mu);
 					}
 				}
 			}
@@ -514,6 +544,305 @@ __global__ void __launch_bounds__(256) ln_backward_kernel(const LnBwdArgs a) {
 	if (a.dbeta) a.dbeta[col] = a.db_first ? 0.0f + sb : a.dbeta[col] + sb;
 }
 
+// ---- layernorm with its rows staged in LDS ----
+// A workgroup owns `rw` consecutive rows (a contiguous block of rw * D floats): its 256 threads copy the block into
+// LDS with 16-byte coalesced loads, all issued before the first LDS store (row pitch D + 1, so lane r walking row r
+// hits bank (r + j) mod 64), lane r of wave 0 runs row r's chains over LDS and writes its outputs back into its LDS
+// row, and the 256 threads copy the block out with coalesced stores. The LDS budget is 64 KB of floats (16384):
+// rw = min(64, 16384 / (D + 1)) rows for the forward, half of that for the backward (g and x).
+
+constexpr int kLnLdsFloats = 16384;
+constexpr int kLnLoadPer = kLnLdsFloats / 4 / 256;  // float4 loads per thread for a full block (16)
+
+__device__ __forceinline__ void ln_block_load(const float* __restrict__ src, int nr, int D, int pitch, int vec,
+                                              const FastDiv& dq, float* dst) {
+	const int tid = threadIdx.x;
+	const int total = nr * D;
+	if (vec) {
+		const int q4 = D >> 2, tot = total >> 2;
+		if (tot == 0) return;
+		f32x4 v[kLnLoadPer];
+#pragma unroll
+		for (int u = 0; u < kLnLoadPer; ++u) {
+			const int q = min(tid + 256 * u, tot - 1);
+			v[u] = *reinterpret_cast<const f32x4*>(src + 4 * q);
+		}
+#pragma unroll
+		for (int u = 0; u < kLnLoadPer; ++u) {
+			const int q = tid + 256 * u;
+			if (q < tot) {
+				const int r = (int)fdiv((unsigned)q, dq), c = 4 * (q - r * q4);
+#pragma unroll
+				for (int i = 0; i < 4; ++i) dst[r * pitch + c + i] = v[u][i];
+			}
+		}
+	} else {
+		for (int b = 0; b < total; b += 256 * 16) {
+			float v[16];
+#pragma unroll
+			for (int u = 0; u < 16; ++u) v[u] = src[min(b + tid + 256 * u, total - 1)];
+#pragma unroll
+			for (int u = 0; u < 16; ++u) {
+				const int e = b + tid + 256 * u;
+				if (e < total) {
+					const int r = (int)fdiv((unsigned)e, dq);
+					dst[r * pitch + e - r * D] = v[u];
+				}
+			}
+		}
+	}
+}
+
+// dst (global) = block in LDS; with add, dst = old + block (the backward's accumulate).
+__device__ __forceinline__ void ln_block_store(float* __restrict__ dst, int nr, int D, int pitch, int vec,
+                                               const FastDiv& dq, const float* src, bool add) {
+	const int tid = threadIdx.x;
+	const int total = nr * D;
+	if (vec) {
+		const int q4 = D >> 2, tot = total >> 2;
+		for (int q = tid; q < tot; q += 256) {
+			const int r = (int)fdiv((unsigned)q, dq), c = 4 * (q - r * q4);
+			f32x4 v;
+#pragma unroll
+			for (int i = 0; i < 4; ++i) v[i] = src[r * pitch + c + i];
+			if (add) {
+				const f32x4 o = *reinterpret_cast<const f32x4*>(dst + 4 * q);
+#pragma unroll
+				for (int i = 0; i < 4; ++i) v[i] = o[i] + v[i];
+			}
+			*reinterpret_cast<f32x4*>(dst + 4 * q) = v;
+		}
+	} else {
+		for (int e = tid; e < total; e += 256) {
+			const int r = (int)fdiv((unsigned)e, dq);
+			const float v = src[r * pitch + e - r * D];
+			dst[e] = add ? dst[e] + v : v;
+		}
+	}
+}
+
+struct LnArgs {
+	const float* x;
+	const float* g;       // backward: upstream gradient
+	const float* gm;
+	const float* bt;
+	const float* mean_in;  // backward
+	const float* inv_in;   // backward
+	float* y;              // forward: y; backward: dx
+	float* mean;           // forward
+	float* inv;            // forward
+	int64_t R;
+	int D, rw, vec, first;
+	float fd, eps;
+	FastDiv dq;            // D / 4 (vec) or D
+	FastDiv dd;            // D
+};
+
+// layernorm forward (ops.cpp:1017-1030) on rw rows per workgroup.
+__global__ void __launch_bounds__(256) ln_forward_lds_kernel(const LnArgs a) {
+	extern __shared__ __align__(16) float lds[];
+	const int pitch = a.D + 1;
+	const int64_t r0 = (int64_t)blockIdx.x * a.rw;
+	const int nr = (int)(a.R - r0 < a.rw ? a.R - r0 : a.rw);
+	ln_block_load(a.x + r0 * a.D, nr, a.D, pitch, a.vec, a.dq, lds);
+	__syncthreads();
+	const int r = threadIdx.x;
+	if (r < nr) {
+		float* row = lds + r * pitch;
+		const int D16 = a.D & ~15;
+		float sum = 0.0f;
+		for (int j = 0; j < D16; j += 16) {  // 16 LDS reads issued, then the 16 dependent adds
+			float v[16];
+#pragma unroll
+			for (int u = 0; u < 16; ++u) v[u] = row[j + u];
+#pragma unroll
+			for (int u = 0; u < 16; ++u) sum = sum + v[u];
+		}
+		for (int j = D16; j < a.D; ++j) sum = sum + row[j];
+		const float mu = sum / a.fd;
+		float sq = 0.0f;
+		for (int j = 0; j < D16; j += 16) {
+			float v[16];
+#pragma unroll
+			for (int u = 0; u < 16; ++u) v[u] = row[j + u];
+#pragma unroll
+			for (int u = 0; u < 16; ++u) sq = sq + (v[u] - mu) * (v[u] - mu);
+		}
+		for (int j = D16; j < a.D; ++j) sq = sq + (row[j] - mu) * (row[j] - mu);
+		const float inv = 1.0f / sqrtf(sq / a.fd + a.eps);
+		a.mean[r0 + r] = mu;
+		a.inv[r0 + r] = inv;
+		for (int j = 0; j < D16; j += 16) {
+			float v[16];
+#pragma unroll
+			for (int u = 0; u < 16; ++u) v[u] = row[j + u];
+#pragma unroll
+			for (int u = 0; u < 16; ++u) row[j + u] = (v[u] - mu) * inv * a.gm[j + u] + a.bt[j + u];
+		}
+		for (int j = D16; j < a.D; ++j) row[j] = (row[j] - mu) * inv * a.gm[j] + a.bt[j];
+	}
+	__syncthreads();
+	ln_block_store(a.y + r0 * a.D, nr, a.D, pitch, a.vec, a.dq, lds, false);
+}
+
+// layernorm backward's dx (ops.cpp:1043-1060) on rw rows per workgroup. g and x are staged in LDS; all 256 threads
+// form the products dxhat * ((x - mean) * inv_std) of the second sum elementwise, so the lane that owns a row only
+// runs its two addition chains (sa over g * gamma, sb over the products, both in column order); then all threads
+// write dx = k * (D * dxhat - sa - xhat * sb) elementwise, straight to HBM.
+__global__ void __launch_bounds__(256) ln_dx_lds_kernel(const LnArgs a) {
+	extern __shared__ __align__(16) float lds[];
+	const int pitch = a.D + 1;
+	float* gs = lds;
+	float* xs = gs + a.rw * pitch;
+	float* ps = xs + a.rw * pitch;
+	float* gms = ps + a.rw * pitch;
+	float* st = gms + a.D;  // per row: mean, inv_std, sa, sb
+	const int tid = threadIdx.x;
+	const int64_t r0 = (int64_t)blockIdx.x * a.rw;
+	const int nr = (int)(a.R - r0 < a.rw ? a.R - r0 : a.rw);
+	ln_block_load(a.g + r0 * a.D, nr, a.D, pitch, a.vec, a.dq, gs);
+	ln_block_load(a.x + r0 * a.D, nr, a.D, pitch, a.vec, a.dq, xs);
+	for (int j = tid; j < a.D; j += 256) gms[j] = a.gm[j];
+	if (tid < nr) {
+		st[4 * tid] = a.mean_in[r0 + tid];
+		st[4 * tid + 1] = a.inv_in[r0 + tid];
+	}
+	__syncthreads();
+	const int total = nr * a.D;
+	for (int e = tid; e < total; e += 256) {
+		const int r = (int)fdiv((unsigned)e, a.dd), j = e - r * a.D;
+		const float dxhat = gs[r * pitch + j] * gms[j];
+		ps[r * pitch + j] = dxhat * ((xs[r * pitch + j] - st[4 * r]) * st[4 * r + 1]);
+	}
+	__syncthreads();
+	if (tid < nr) {
+		const float* gr = gs + tid * pitch;
+		const float* pr = ps + tid * pitch;
+		const int D16 = a.D & ~15;
+		float sa = 0.0f, sb = 0.0f;
+		for (int j = 0; j < D16; j += 16) {  // the batch's LDS reads issued, then the two chains
+			float gv[16], mv[16], pv[16];
+#pragma unroll
+			for (int u = 0; u < 16; ++u) {
+				gv[u] = gr[j + u];
+				mv[u] = gms[j + u];
+				pv[u] = pr[j + u];
+			}
+#pragma unroll
+			for (int u = 0; u < 16; ++u) {
+				sa = sa + gv[u] * mv[u];
+				sb = sb + pv[u];
+			}
+		}
+		for (int j = D16; j < a.D; ++j) {
+			sa = sa + gr[j] * gms[j];
+			sb = sb + pr[j];
+		}
+		st[4 * tid + 2] = sa;
+		st[4 * tid + 3] = sb;
+	}
+	__syncthreads();
+	const float fd = a.fd;
+	float* dst = a.y + r0 * a.D;
+	for (int e = tid; e < total; e += 256) {
+		const int r = (int)fdiv((unsigned)e, a.dd), j = e - r * a.D;
+		const float mu = st[4 * r], inv = st[4 * r + 1], sa = st[4 * r + 2], sb = st[4 * r + 3];
+		const float k = inv / fd;
+		const float dxhat = gs[r * pitch + j] * gms[j];
+		const float term = k * (fd * dxhat - sa - ((xs[r * pitch + j] - mu) * inv) * sb);
+		dst[e] = a.first ? term + 0.0f : dst[e] + term;
+	}
+}
+
+// layernorm backward's dgamma and dbeta (ops.cpp:1061-1076): a workgroup owns 32 columns and streams the rows in
+// chunks of 64. Waves 1-4 produce: each thread loads 8 rows of its column (g, x, and the rows' mean and inv_std)
+// three chunks ahead in a register ring, and writes g * ((x - mean) * inv_std), formed exactly as the reference
+// forms it, and g into the chunk's LDS buffer. Wave 0 consumes one chunk behind: lanes 0-31 add the products down
+// their column in row order (dgamma's chain), lanes 32-63 add g (dbeta's chain). One barrier per chunk; two
+// buffers, since the buffer producers fill was last read one chunk before.
+constexpr int kLnCols = 32, kLnChunk = 64, kLnAhead = 3, kLnProducers = 256, kLnThreads = 64 + kLnProducers;
+constexpr int kLnPer = kLnChunk * kLnCols / kLnProducers;  // 8 rows per producer thread and chunk
+
+__global__ void __launch_bounds__(kLnThreads) ln_dgamma_kernel(const float* __restrict__ g,
+                                                               const float* __restrict__ x,
+                                                               const float* __restrict__ mean,
+                                                               const float* __restrict__ inv, int64_t R, int D,
+                                                               float* dgamma, int dg_first, float* dbeta,
+                                                               int db_first) {
+	__shared__ float buf[2][2][kLnChunk][kLnCols];
+	const int tid = threadIdx.x;
+	const int c0 = blockIdx.x * kLnCols;
+	const int64_t chunks = (R + kLnChunk - 1) / kLnChunk;
+	const bool producer = tid >= 64;
+	const int pt = tid - 64;
+	const int c = pt & (kLnCols - 1), rr = pt / kLnCols;  // rows rr + 8u of a chunk
+	const int col = min(c0 + c, D - 1);
+	float gv[kLnAhead][kLnPer], xv[kLnAhead][kLnPer], mv[kLnAhead][kLnPer], iv[kLnAhead][kLnPer];
+	auto load = [&](int64_t ch, int slot) {
+#pragma unroll
+		for (int u = 0; u < kLnPer; ++u) {
+			const int64_t r = min(ch * kLnChunk + rr + 8 * u, R - 1);
+			gv[slot][u] = g[r * D + col];
+			xv[slot][u] = x[r * D + col];
+			mv[slot][u] = mean[r];
+			iv[slot][u] = inv[r];
+		}
+	};
+	auto chain = [&](float& acc, int b, int n) {
+		const float* v = &buf[b][tid >> 5][0][tid & 31];
+		if (n == kLnChunk) {
+#pragma unroll
+			for (int i0 = 0; i0 < kLnChunk; i0 += 16) {  // 16 LDS reads issued, then 16 dependent adds
+				float t[16];
+#pragma unroll
+				for (int u = 0; u < 16; ++u) t[u] = v[(i0 + u) * kLnCols];
+#pragma unroll
+				for (int u = 0; u < 16; ++u) acc = acc + t[u];
+			}
+		} else {
+			for (int i = 0; i < n; ++i) acc = acc + v[i * kLnCols];
+		}
+	};
+	if (producer) {
+#pragma unroll
+		for (int k = 0; k < kLnAhead; ++k)
+			if (k < chunks) load(k, k);
+	}
+	float acc = 0.0f;
+	for (int64_t base = 0; base < chunks; base += kLnAhead) {
+#pragma unroll
+		for (int k = 0; k < kLnAhead; ++k) {
+			const int64_t ch = base + k;
+			if (ch >= chunks) break;
+			const int b = (int)(ch & 1);
+			if (producer) {
+#pragma unroll
+				for (int u = 0; u < kLnPer; ++u) {
+					const int row = rr + 8 * u;
+					buf[b][0][row][c] = gv[k][u] * ((xv[k][u] - mv[k][u]) * iv[k][u]);
+					buf[b][1][row][c] = gv[k][u];
+				}
+				if (ch + kLnAhead < chunks) load(ch + kLnAhead, k);
+			} else if (ch > 0) {
+				chain(acc, b ^ 1, kLnChunk);  // chunk ch - 1 is whole
+			}
+			__syncthreads();
+		}
+	}
+	if (!producer && chunks > 0) {
+		const int64_t last = chunks - 1;
+		chain(acc, (int)(last & 1), (int)(R - last * kLnChunk));
+	}
+	if (tid < 64 && c0 + (tid & 31) < D) {
+		const int j = c0 + (tid & 31);
+		if (tid < 32) {
+			if (dgamma) dgamma[j] = dg_first ? 0.0f + acc : dgamma[j] + acc;
+		} else {
+			if (dbeta) dbeta[j] = db_first ? 0.0f + acc : dbeta[j] + acc;
+		}
+	}
+}
+
 inline bool aligned16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }
 
 template <int MODE>
@@ -639,6 +968,26 @@ hipError_t batchnorm_backward(const float* gy, const float* x, const unsigned ch
 hipError_t layernorm_forward(const float* x, const float* gamma, const float* beta, int64_t R, int D, float fd,
                              float eps, float* y, float* mean, float* inv_std, hipStream_t s) {
 	if (R == 0) return hipSuccess;
+	const int rw = (int)std::min<int64_t>(std::min(64, kLnLdsFloats / (D + 1)), R);
+	if (rw >= 1 && R / rw < ((int64_t)1 << 31) && (int64_t)rw * D < ((int64_t)1 << 31)) {
+		LnArgs a{};
+		a.x = x;
+		a.gm = gamma;
+		a.bt = beta;
+		a.y = y;
+		a.mean = mean;
+		a.inv = inv_std;
+		a.R = R;
+		a.D = D;
+		a.rw = rw;
+		a.fd = fd;
+		a.eps = eps;
+		a.vec = D % 4 == 0 && aligned16(x) && aligned16(y);
+		a.dq = make_fastdiv((unsigned)(a.vec ? D / 4 : D));
+		hipLaunchKernelGGL(ln_forward_lds_kernel, dim3((unsigned)((R + rw - 1) / rw)), dim3(256),
+		                   (size_t)rw * (D + 1) * sizeof(float), s, a);
+		return hipGetLastError();
+	}
 	const int vec = D % 4 == 0 && aligned16(x) && aligned16(y) && aligned16(gamma) && aligned16(beta);
 	hipLaunchKernelGGL(ln_forward_kernel, dim3((unsigned)((R + 255) / 256)), dim3(256), 0, s, x, gamma, beta, R, D, fd,
 	                   eps, y, mean, inv_std, vec);
@@ -649,6 +998,34 @@ hipError_t layernorm_backward(const float* gy, const float* x, const float* gamm
                               const float* inv_std, int64_t R, int D, float fd, float* dx, int dx_first,
                               float* dgamma, int dgamma_first, float* dbeta, int dbeta_first, hipStream_t s) {
 	if (R == 0 && !dgamma && !dbeta) return hipSuccess;
+	const int rw = (int)std::min<int64_t>(std::min(64, (kLnLdsFloats - D) / (3 * (D + 1) + 4)), std::max<int64_t>(R, 1));
+	if (rw >= 1 && R / rw < ((int64_t)1 << 31) && (int64_t)rw * D < ((int64_t)1 << 31)) {
+		if (dx && R > 0) {
+			LnArgs a{};
+			a.g = gy;
+			a.x = x;
+			a.gm = gamma;
+			a.mean_in = mean;
+			a.inv_in = inv_std;
+			a.y = dx;
+			a.R = R;
+			a.D = D;
+			a.rw = rw;
+			a.fd = fd;
+			a.first = dx_first;
+			a.vec = D % 4 == 0 && aligned16(x) && aligned16(gy) && aligned16(dx);
+			a.dq = make_fastdiv((unsigned)(a.vec ? D / 4 : D));
+			a.dd = make_fastdiv((unsigned)D);
+			hipLaunchKernelGGL(ln_dx_lds_kernel, dim3((unsigned)((R + rw - 1) / rw)), dim3(256),
+			                   ((size_t)3 * rw * (D + 1) + D + 4 * rw) * sizeof(float), s, a);
+			const hipError_t e = hipGetLastError();
+			if (e != hipSuccess) return e;
+		}
+		if (dgamma || dbeta)
+			hipLaunchKernelGGL(ln_dgamma_kernel, dim3((unsigned)((D + kLnCols - 1) / kLnCols)), dim3(kLnThreads), 0, s, gy, x,
+			                   mean, inv_std, R, D, dgamma, dgamma_first, dbeta, dbeta_first);
+		return hipGetLastError();
+	}
 	LnBwdArgs a{};
 	a.g = gy;
 	a.x = x;

@@ -343,6 +343,31 @@ int nnref_softmax_step(const float* x, size_t N, size_t H, size_t Tq, size_t Tk,
 	});
 }
 
+// A Conv-BN-ReLU stack with a layer-normalised head (the ops of nn-cpp's cnn_fer and transformer models):
+// conv2d(c0 -> c1, 3x3, pad 1) -> batchnorm + ReLU folded -> maxpool2d(2, 2) -> conv2d(c1 -> c2) -> batchnorm ->
+// relu -> reshape {N, flat} -> layernorm -> linear(classes); then the backward pass from the output gradient g.
+// p: w1, b1, bn1 weight, bn1 bias, w2, b2, bn2 weight, bn2 bias, ln gamma, ln beta, w3, b3; grads likewise, then dx.
+int nnref_norm_step(const float* x, size_t N, size_t c0, size_t side, size_t c1, size_t c2, size_t classes,
+		const float* const* p, const float* g, float* y, float* const* grads, float* dx) {
+	return guard([&] {
+		const size_t flat = c2 * (side / 2) * (side / 2);
+		const Value xv = leaf_of(x, {N, c0, side, side});
+		const std::vector<std::vector<size_t>> shapes = {{c1, c0, 3, 3}, {c1}, {c1}, {c1}, {c2, c1, 3, 3}, {c2}, {c2},
+		                                                 {c2}, {flat}, {flat}, {classes, flat}, {classes}};
+		std::vector<Value> v;
+		for (size_t i = 0; i < shapes.size(); ++i) v.push_back(leaf_of(p[i], shapes[i]));
+		Value h = nn::batchnorm(nn::conv2d(xv, v[0], v[1], 1, 1), v[2], v[3], 1e-5f, nullptr, nullptr, true);
+		h = nn::maxpool2d(h, 2, 2);
+		h = nn::relu(nn::batchnorm(nn::conv2d(h, v[4], v[5], 1, 1), v[6], v[7], 1e-5f));
+		h = nn::layernorm(nn::reshape(h, {N, flat}), v[8], v[9], 1e-5f);
+		const Value r = nn::linear(h, v[10], v[11]);
+		probe_loss(r, g).backward();
+		put(r.data(), y);
+		for (size_t i = 0; i < v.size(); ++i) put(v[i].grad(), grads[i]);
+		put(xv.grad(), dx);
+	});
+}
+
 // ---- nn-cpp's modules, unchanged (src/nn/*.cpp): the callers of the path ----
 // Builds model `which` after nn::manual_seed(seed) (so parameters come from the modules' own initialisation),
 // runs forward on x, seeds the backward pass with g through probe_loss, and returns the output (out, n_out floats)

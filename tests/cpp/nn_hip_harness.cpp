@@ -149,6 +149,28 @@ int h_softmax(const float* x, size_t N, size_t H, size_t Tq, size_t Tk, float sc
 	});
 }
 
+// The Conv-BN-ReLU stack with a layer-normalised head of oracle/ref_shim.cpp's nnref_norm_step, through nn::hip.
+int h_norm_step(const float* x, size_t N, size_t c0, size_t side, size_t c1, size_t c2, size_t classes,
+                const float* const* p, const float* g, float* y, float* const* grads, float* dx) {
+	return guard([&] {
+		const size_t flat = c2 * (side / 2) * (side / 2);
+		Value xv = param(x, {N, c0, side, side});
+		const std::vector<std::vector<size_t>> shapes = {{c1, c0, 3, 3}, {c1}, {c1}, {c1}, {c2, c1, 3, 3}, {c2}, {c2},
+		                                                 {c2}, {flat}, {flat}, {classes, flat}, {classes}};
+		std::vector<Value> v;
+		for (size_t i = 0; i < shapes.size(); ++i) v.push_back(param(p[i], shapes[i]));
+		Value h = nn::hip::batchnorm(nn::hip::conv2d(xv, v[0], v[1], 1, 1), v[2], v[3], 1e-5f, nullptr, nullptr, true);
+		h = nn::hip::maxpool2d(h, 2, 2);
+		h = nn::hip::relu(nn::hip::batchnorm(nn::hip::conv2d(h, v[4], v[5], 1, 1), v[6], v[7], 1e-5f));
+		h = nn::hip::layernorm(nn::hip::reshape(h, {N, flat}), v[8], v[9], 1e-5f);
+		Value r = nn::hip::linear(h, v[10], v[11]);
+		r.backward(Tensor::from_host({N, classes}, g));
+		out(r.data(), y);
+		for (size_t i = 0; i < v.size(); ++i) out(v[i].grad(), grads[i]);
+		out(xv.grad(), dx);
+	});
+}
+
 // The shape errors nn-cpp throws: bit i of the result is set when case i threw nn::hip::TensorShapeError.
 int h_shape_errors(void) {
 	int bits = 0;
@@ -170,6 +192,12 @@ int h_shape_errors(void) {
 	expect(6, [] { nn::hip::attention(Value::leaf(Tensor({1, 4, 6})), Value::leaf(Tensor({1, 4, 6})),
 	                                  Value::leaf(Tensor({1, 4, 6})), 4, Tensor(), false); });  // 4 heads do not divide 6
 	expect(7, [] { Value::leaf(Tensor({2, 2})).backward(); });                               // not one element
+	expect(8, [] { nn::hip::batchnorm(Value::leaf(Tensor({4})), Value::leaf(Tensor({4})), Value::leaf(Tensor({4})),
+	                                  1e-5f); });                                          // no channel axis
+	expect(9, [] { nn::hip::batchnorm(Value::leaf(Tensor({2, 3, 4})), Value::leaf(Tensor({4})),
+	                                  Value::leaf(Tensor({3})), 1e-5f); });                // weight of the wrong size
+	expect(10, [] { nn::hip::layernorm(Value::leaf(Tensor({2, 5})), Value::leaf(Tensor({4})), Value::leaf(Tensor({5})),
+	                                   1e-5f); });                                         // gamma of the wrong size
 	return bits;
 }
 

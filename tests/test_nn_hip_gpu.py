@@ -128,6 +128,35 @@ def test_softmax_matches_nncpp(harness, ref, case):
 
 
 def test_shape_errors_throw_tensor_shape_error(harness):
-    """matmul, linear, conv2d, maxpool2d and attention with shapes nn-cpp rejects, and backward() on a non-scalar:
-    each throws nn::hip::TensorShapeError."""
-    assert harness.h_shape_errors() == 0xFF
+    """matmul, linear, conv2d, maxpool2d, attention, batchnorm and layernorm with shapes nn-cpp rejects, and
+    backward() on a non-scalar: each throws nn::hip::TensorShapeError."""
+    assert harness.h_shape_errors() == 0x7FF
+
+
+@pytest.mark.parametrize("dims", [(16, 1, 24, 8, 16, 7), (3, 2, 10, 5, 3, 4)])
+def test_norm_step_matches_nncpp(harness, ref, dims):
+    """conv2d -> batchnorm with the ReLU folded -> maxpool2d -> conv2d -> batchnorm -> relu -> reshape -> layernorm
+    -> linear, forward and every gradient (the ops of nn-cpp's cnn_fer and transformer workloads), through nn::hip
+    against nn-cpp's own ops."""
+    N, c0, side, c1, c2, classes = dims
+    flat = c2 * (side // 2) ** 2
+    shapes = [(c1, c0, 3, 3), (c1,), (c1,), (c1,), (c2, c1, 3, 3), (c2,), (c2,), (c2,), (flat,), (flat,),
+              (classes, flat), (classes,)]
+    params = [uni(110 + i, s, 0.5) for i, s in enumerate(shapes)]
+    for i in (2, 6, 8):  # scales near 1
+        params[i] = (params[i] + 1).astype(np.float32)
+    x = np.ascontiguousarray(synth.mt19937_uniform(109, N * c0 * side * side, 0, 1).reshape(N, c0, side, side))
+    g = synth.normal(108, (N, classes))
+    results = []
+    for fn in (harness.h_norm_step, ref.lib.nnref_norm_step):
+        y = np.empty((N, classes), np.float32)
+        grads = [np.empty_like(p) for p in params]
+        dx = np.empty_like(x)
+        rc = fn(fp(x), _sz(N), _sz(c0), _sz(side), _sz(c1), _sz(c2), _sz(classes), ptrs(params), fp(g), fp(y),
+                ptrs(grads), fp(dx))
+        assert rc == 0, (fn, rc)
+        results.append([y, dx] + grads)
+    names = ["y", "dx", "dw1", "db1", "dbn1_w", "dbn1_b", "dw2", "db2", "dbn2_w", "dbn2_b", "dln_g", "dln_b", "dw3",
+             "db3"]
+    for name, got, want in zip(names, *results):
+        assert_same(got, want, (name, dims))
