@@ -48,8 +48,14 @@ hipError_t mask_grad(const float* g, const unsigned char* alive, float* out, int
 // per-sample dcol = W^T gm and col2im in one kernel, dcol kept in LDS (same bits). first: dx = 0 + taps, else
 // dx += taps. conv_dx_fused_ok tells whether the geometry fits (Ho*Wo <= 256, or Ho*Wo <= 1024 with kh*kw <= 16).
 bool conv_dx_fused_ok(const ConvGeom& g, int64_t samples, int cout);
-hipError_t conv_dx_fused(const float* gm, const float* w, float* dx, const ConvGeom& g, int64_t samples, int cout,
-                         int first, hipStream_t s);
+// Per-sample bias sums and weight gradients of a convolution with K = Cin*kh*kw <= 16 on planes of up to 1024
+// output positions (conv_dwp.hip): gb[n][c] = lane_sum of the masked gradient row, gw[n][c][k] = its product with
+// column k of sample n, one fma chain per element; the masked gradient stays in LDS. Declines depth-cut products.
+bool conv_dwp_ok(const ConvGeom& g, int64_t samples, int cout);
+hipError_t conv_dwp(const float* g, const unsigned char* alive, const float* x, float* gb, float* gw,
+                    const ConvGeom& geo, int64_t samples, int cout, hipStream_t s);
+hipError_t conv_dx_fused(const float* gm, const unsigned char* alive, const float* w, float* dx, const ConvGeom& g,
+                         int64_t samples, int cout, int first, hipStream_t s);
 hipError_t masked_lane_sums(const float* g, const unsigned char* alive, float* out, int64_t rows, int64_t n, float* dst,
                             hipStream_t s);
 hipError_t lane_sums(const float* src, int64_t rows, int64_t n, float* dst, hipStream_t s);

@@ -39,7 +39,8 @@ constexpr DxShape kDxFirst{16, 16};
 using M16 = Mfma<kMf16>;
 
 struct DxArgs {
-	const float* g;   // masked output gradient {N, Cout, hw}
+	const float* g;   // output gradient {N, Cout, hw}, masked unless alive is given
+	const unsigned char* alive;  // the folded ReLU's flags: g is masked here (alive ? g : 0), or null
 	const float* w;   // {Cout, K}
 	float* dx;        // {N, Cin, H, W}
 	ConvGeom geo;
@@ -114,6 +115,7 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2)
 	float* wl = sm;                          // [kDxRows][kDxWLd]: W^T for a chunk of output channels
 	float* tile = sm + kDxRows * kDxWLd;     // [cg * khkw][hwp]: the group's dcol rows
 	const float* gn = a.g + (int64_t)n * a.cout * hw;
+	const unsigned char* an = a.alive ? a.alive + (int64_t)n * a.cout * hw : nullptr;
 
 	// 1. the chains
 	M16::Acc acc[kDxRows / 16];
@@ -125,8 +127,20 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2)
 	const bool pos_here = 64 * wave < hw;
 	// gradient rows co .. co+kDxACh-1 at this lane's position (rows clamped into range, never used past cout)
 	auto load_g = [&](float (&dst)[kDxACh], int co) {
+		if (an) {  // ops.cpp:1439-1443's mask, applied as the rows are read
+			unsigned char f[kDxACh];
 #pragma unroll
-		for (int u = 0; u < kDxACh; ++u) dst[u] = gn[(int64_t)min(co + u, a.cout - 1) * hw + pos];
+			for (int u = 0; u < kDxACh; ++u) {
+				const int64_t off = (int64_t)min(co + u, a.cout - 1) * hw + pos;
+				dst[u] = gn[off];
+				f[u] = an[off];
+			}
+#pragma unroll
+			for (int u = 0; u < kDxACh; ++u) dst[u] = f[u] ? dst[u] : 0.0f;
+		} else {
+#pragma unroll
+			for (int u = 0; u < kDxACh; ++u) dst[u] = gn[(int64_t)min(co + u, a.cout - 1) * hw + pos];
+		}
 	};
 	for (int cc = 0; cc < a.cout; cc += kDxCo) {
 		const int nco = min(kDxCo, a.cout - cc);
@@ -261,12 +275,13 @@ bool conv_dx_fused_ok(const ConvGeom& g, int64_t samples, int cout) {
 	return samples * groups < ((int64_t)1 << 31) && samples * cout * (int64_t)g.ho * g.wo < ((int64_t)1 << 40);
 }
 
-hipError_t conv_dx_fused(const float* gm, const float* w, float* dx, const ConvGeom& g, int64_t samples, int cout,
-                         int first, hipStream_t s) {
+hipError_t conv_dx_fused(const float* gm, const unsigned char* alive, const float* w, float* dx, const ConvGeom& g,
+                         int64_t samples, int cout, int first, hipStream_t s) {
 	if (!conv_dx_fused_ok(g, samples, cout)) return hipErrorInvalidValue;
 	const DxShape sh = dx_shape(g);
 	DxArgs a;
 	a.g = gm;
+	a.alive = alive;
 	a.w = w;
 	a.dx = dx;
 	a.geo = g;

@@ -240,15 +240,20 @@ int nnh_conv2d_backward(const float* g, const float* x, const float* w, const un
 	// 3x3, stride 1, padding 1 on small planes: one kernel takes the mask (ops.cpp:1439-1443), the per-sample bias
 	// sums (1445) and the per-sample weight gradients (1448-1449) with its operands in LDS
 	const bool dw3 = dw && conv_dw3_ok(geo, (int64_t)N, (int)Cout, g, alive, m);
+	// short column depth (a first layer): db and dW per sample from LDS, the mask applied as g is staged; the dx
+	// kernel then masks g itself, so the masked gradient is never written
+	const bool dwp = dw && !dw3 && (!dx || dx_fused) && conv_dwp_ok(geo, (int64_t)N, (int)Cout);
 	if (dw3) {
 		rc = hip_status(conv_dw3(g, alive, m, gb, x, gw, geo, (int64_t)N, (int)Cout, s), "conv2d mask, db, dw 3x3");
+	} else if (dwp) {
+		rc = hip_status(conv_dwp(g, alive, x, gb, gw, geo, (int64_t)N, (int)Cout, s), "conv2d db, dw");
 	} else if (alive) {  // ops.cpp:1439-1443, with the per-sample bias sums of ops.cpp:1445 in the same pass
 		rc = db ? hip_status(masked_lane_sums(g, alive, m, (int64_t)(N * Cout), (int64_t)hw, gb, s), "conv2d mask, db")
 		        : hip_status(mask_grad(g, alive, m, (int64_t)(N * Cout * hw), s), "conv2d mask");
 	} else if (db) {  // ops.cpp:1445
 		rc = hip_status(lane_sums(gm, (int64_t)(N * Cout), (int64_t)hw, gb, s), "conv2d db");
 	}
-	if (rc == NNH_OK && dw && !dw3) {  // ops.cpp:1448-1449: dW_n = g_n col_n^T with col_n gathered from x_n
+	if (rc == NNH_OK && dw && !dw3 && !dwp) {  // ops.cpp:1448-1449: dW_n = g_n col_n^T with col_n gathered from x_n
 		nnh_batch b{};
 		b.ndim = 1;
 		b.shape[0] = N;
@@ -270,7 +275,9 @@ int nnh_conv2d_backward(const float* g, const float* x, const float* w, const un
 	else if (rc == NNH_OK && db)
 		rc = hip_status(sum_rows(gb, (int64_t)N, (int64_t)Cout, db, db_first ? 0 : 2, s), "conv2d db");
 	if (rc == NNH_OK && dx && dx_fused) {  // ops.cpp:1452-1455, dcol kept on chip
-		rc = hip_status(conv_dx_fused(gm, w, dx, geo, (int64_t)N, (int)Cout, dx_first ? 1 : 0, s), "conv2d dx");
+		rc = hip_status(dwp ? conv_dx_fused(g, alive, w, dx, geo, (int64_t)N, (int)Cout, dx_first ? 1 : 0, s)
+		                    : conv_dx_fused(gm, nullptr, w, dx, geo, (int64_t)N, (int)Cout, dx_first ? 1 : 0, s),
+		                "conv2d dx");
 	} else if (rc == NNH_OK && dx) {  // ops.cpp:1452-1455
 		float* col = ws.at<float>(plan.off_col);
 		nnh_batch b{};

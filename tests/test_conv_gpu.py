@@ -331,3 +331,48 @@ def test_same_width_quad_path(gpu, oracle):
     nnh.check(rc)
     wy, _ = oracle.conv2d_forward(x, w, b, 1, 1, True)
     same(host(yv).reshape(wy.shape), wy, "unaligned y")
+
+
+# First layers: K = Cin*kh*kw <= 16 on planes of up to 1024 outputs take one kernel for db and dW per sample
+# (conv_dwp), with the mask applied as g is staged and dx masking g itself. (N, Cin, H, W, Cout, kh, kw, stride,
+# pad)
+DWP_CASES = [
+    (4, 1, 28, 28, 32, 3, 3, 1, 1),     # config 3's conv1
+    (3, 1, 13, 13, 10, 3, 3, 1, 1),     # 169 outputs (not a multiple of 4: element-wise staging), 10 channels
+    (2, 1, 32, 32, 8, 3, 3, 1, 1),      # 1024 outputs, the largest plane it takes
+    (2, 2, 9, 9, 12, 2, 2, 2, 0),       # stride 2, K = 8
+    (2, 1, 30, 30, 9, 4, 4, 1, 1),      # 16 taps
+    (2, 1, 48, 48, 16, 3, 3, 1, 1),     # 2304 outputs: beyond it, the mask + GEMM path
+]
+
+
+@pytest.mark.parametrize("case", DWP_CASES)
+def test_first_layer_weight_gradient_kernel(gpu, oracle, case):
+    """db and dW (and dx, fresh and accumulated) bitwise against the oracle, with and without the ReLU's flags, and
+    with only some of the gradients asked for."""
+    import torch
+
+    import nnh
+    N, Cin, H, W, Cout, kh, kw, s, p = case
+    x = synth.mt19937_uniform(N * 37 + Cin, N * Cin * H * W).reshape(N, Cin, H, W)
+    w = synth.normal(Cout + 27, (Cout, Cin, kh, kw))
+    b = synth.mt19937_uniform(Cout + 28, Cout)
+    for relu in (True, False):
+        y, alive = nnh.conv2d_forward(dev(x), dev(w), dev(b), s, p, relu)
+        _, wa = oracle.conv2d_forward(x, w, b, s, p, relu)
+        gr = synth.normal(Cout + 29, tuple(y.shape))
+        old = synth.normal(Cout + 30, x.shape)
+        for want_dx, want_db, first in ((True, True, True), (True, True, False), (False, False, True),
+                                        (False, True, True)):
+            dx = (torch.full(x.shape, float("nan"), device="cuda") if first else dev(old)) if want_dx else None
+            dw = torch.full(w.shape, float("nan"), device="cuda")
+            db = torch.full((Cout,), float("nan"), device="cuda") if want_db else None
+            nnh.conv2d_backward(dev(gr), dev(x), dev(w), alive if relu else None, s, p, dx, first, dw, True, db, True)
+            wdx, wdw, wdb = oracle.conv2d_backward(gr, x, w, wa if relu else None, s, p,
+                                                   dx=None if first else old, dx_first=first)
+            tag = (case, relu, want_dx, want_db, first)
+            same(host(dw), wdw, ("dw",) + tag)
+            if want_db:
+                same(host(db), wdb, ("db",) + tag)
+            if want_dx:
+                same(host(dx), wdx, ("dx",) + tag)
