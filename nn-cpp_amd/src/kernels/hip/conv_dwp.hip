@@ -11,9 +11,10 @@
 //     coalesced loads of g and 4-byte loads of the flags), the sample's input and, from it, the sample's K im2col
 //     columns (zeros in the padding) in LDS;
 //   * waves 0-1: lane c*K + k runs dW_n[c][k]'s chain, reading g'[c][p] and col[k][p] sixteen positions at a time,
-//     the next sixteen in flight while it multiplies and adds the current ones;
-//   * wave 2: the eight lanes of channel c run lane_sum's eight partial chains over g'[c], combine them as
-//     ((a0+a1)+(a2+a3))+((a4+a5)+(a6+a7)) and add the tail.
+//     the next 48 in flight while it multiplies and adds the current ones (the chain is otherwise bound by the LDS
+//     read latency, not by the fma's);
+//   * wave 2: two lanes per channel c run lane_sum's eight partial chains over g'[c] (four each, from 16-byte
+//     reads), combine them as ((a0+a1)+(a2+a3))+((a4+a5)+(a6+a7)) and add the tail.
 // Row pitches keep the lanes of one LDS read on distinct banks: g' rows 8 mod 64 apart (8 channels), column rows
 // 4 mod 64 apart (up to 16 taps). The per-sample results go to the workspace; the caller adds them over the
 // samples in order, as the reference does (1461-1462). The masked gradient is not written out: the dx kernel masks
@@ -148,12 +149,20 @@ __global__ void __launch_bounds__(kPwThreads) conv_dwp_kernel(const PwArgs a) {
 			const float* gr = gs + c * a.gpitch;
 			const float* cr = cs + k * a.cpitch;
 			float acc = 0.0f;
-			float ga[16], ca[16], gb2[16], cb2[16];
-			auto load = [&](float (&gx)[16], float (&cx)[16], int b) {
+			// a ring of four batches of 16 positions: three batches' LDS reads are in flight while one batch's fmas
+			// run (every read unconditional, at a batch index clamped into range; the remainder after the last
+			// whole group of four is already in the ring)
+			float g0[16], c0v[16], g1[16], c1v[16], g2[16], c2v[16], g3[16], c3v[16];
+			auto load = [&](float (&gx)[16], float (&cx)[16], int b) {  // 16-byte LDS reads (rows 16-byte aligned)
 #pragma unroll
-				for (int u = 0; u < 16; ++u) {
-					gx[u] = gr[16 * b + u];
-					cx[u] = cr[16 * b + u];
+				for (int q = 0; q < 4; ++q) {
+					const f32x4 gv = *reinterpret_cast<const f32x4*>(gr + 16 * b + 4 * q);
+					const f32x4 cv = *reinterpret_cast<const f32x4*>(cr + 16 * b + 4 * q);
+#pragma unroll
+					for (int i = 0; i < 4; ++i) {
+						gx[4 * q + i] = gv[i];
+						cx[4 * q + i] = cv[i];
+					}
 				}
 			};
 			auto fmas = [&](const float (&gx)[16], const float (&cx)[16]) {
@@ -161,42 +170,59 @@ __global__ void __launch_bounds__(kPwThreads) conv_dwp_kernel(const PwArgs a) {
 				for (int u = 0; u < 16; ++u) acc = __builtin_fmaf(gx[u], cx[u], acc);
 			};
 			if (nb > 0) {
-				// two batches of 16 positions in registers: the next one's reads are in flight while the current
-				// one's fmas run (every read unconditional, at a batch index clamped into range)
-				load(ga, ca, 0);
+				load(g0, c0v, 0);
+				load(g1, c1v, min(1, nb - 1));
+				load(g2, c2v, min(2, nb - 1));
 				int b = 0;
-				for (; b + 1 < nb; b += 2) {
-					load(gb2, cb2, b + 1);
-					fmas(ga, ca);
-					load(ga, ca, min(b + 2, nb - 1));
-					fmas(gb2, cb2);
+				for (; b + 4 <= nb; b += 4) {
+					load(g3, c3v, min(b + 3, nb - 1));
+					fmas(g0, c0v);
+					load(g0, c0v, min(b + 4, nb - 1));
+					fmas(g1, c1v);
+					load(g1, c1v, min(b + 5, nb - 1));
+					fmas(g2, c2v);
+					load(g2, c2v, min(b + 6, nb - 1));
+					fmas(g3, c3v);
 				}
-				if (b < nb) fmas(ga, ca);
+				if (b < nb) fmas(g0, c0v);
+				if (b + 1 < nb) fmas(g1, c1v);
+				if (b + 2 < nb) fmas(g2, c2v);
 			}
 			for (int p = 16 * nb; p < hw; ++p) acc = __builtin_fmaf(gr[p], cr[p], acc);
 			a.gw[(row0 + c) * K + k] = acc;
 		}
-	} else if (tid < 3 * 64 && a.gb) {
-		// 4. db_n[c] = lane_sum(g'[c]) (ops.cpp:804-812): lane j of channel c's group is partial a[j]
-		const int l = tid - 2 * 64, c = l >> 3, j = l & 7;
+	} else if (tid < 2 * 64 + 2 * kPwCg && a.gb) {
+		// 4. db_n[c] = lane_sum(g'[c]) (ops.cpp:804-812): lanes 2c and 2c + 1 of wave 2 hold the reference's
+		// partials a[0..3] and a[4..7] of channel c (elements 8i + 4h + q), read 16 bytes at a time; lane 2c combines
+		// them as ((a0+a1)+(a2+a3))+((a4+a5)+(a6+a7)) and adds the tail
+		const int l = tid - 2 * 64, c = l >> 1, h = l & 1;
 		const int full = hw & ~7;
-		const float* gr = gs + c * a.gpitch;
-		float acc = 0.0f;
-		int i = j;
-		for (; i + 8 * 15 < full; i += 8 * 16) {
-			float v[16];
+		const float* gr = gs + c * a.gpitch + 4 * h;
+		float p0 = 0.0f, p1 = 0.0f, p2 = 0.0f, p3 = 0.0f;
+		int i = 0;
+		for (; i + 8 * 7 < full; i += 8 * 8) {
+			f32x4 v[8];
 #pragma unroll
-			for (int u = 0; u < 16; ++u) v[u] = gr[i + 8 * u];
+			for (int u = 0; u < 8; ++u) v[u] = *reinterpret_cast<const f32x4*>(gr + i + 8 * u);
 #pragma unroll
-			for (int u = 0; u < 16; ++u) acc = acc + v[u];
+			for (int u = 0; u < 8; ++u) {
+				p0 = p0 + v[u][0];
+				p1 = p1 + v[u][1];
+				p2 = p2 + v[u][2];
+				p3 = p3 + v[u][3];
+			}
 		}
-		for (; i < full; i += 8) acc = acc + gr[i];
-		const int base = l & ~7;
-		float part[8];
-#pragma unroll
-		for (int u = 0; u < 8; ++u) part[u] = __shfl(acc, base + u);
-		if (j == 0 && c < nc) {
-			float t = ((part[0] + part[1]) + (part[2] + part[3])) + ((part[4] + part[5]) + (part[6] + part[7]));
+		for (; i < full; i += 8) {
+			const f32x4 v = *reinterpret_cast<const f32x4*>(gr + i);
+			p0 = p0 + v[0];
+			p1 = p1 + v[1];
+			p2 = p2 + v[2];
+			p3 = p3 + v[3];
+		}
+		const int other = (l | 1);
+		const float q0 = __shfl(p0, other), q1 = __shfl(p1, other), q2 = __shfl(p2, other), q3 = __shfl(p3, other);
+		if (h == 0 && c < nc) {
+			float t = ((p0 + p1) + (p2 + p3)) + ((q0 + q1) + (q2 + q3));
 			for (int p = full; p < hw; ++p) t = t + gr[p];
 			a.gb[row0 + c] = t;
 		}
