@@ -1,5 +1,6 @@
 // gemm.hip - instantiations, depth-cut reduction and launch logic of the fp32 MFMA GEMM.
 #include "gemm.hpp"
+#include "gemm_valu.hpp"
 
 #include <optional>
 
@@ -193,8 +194,13 @@ int64_t gemm_workspace_floats(const GemmCall& g) {
 	return cut_plan(g.m, g.n, g.k).pieces * g.m * g.n * g.batch_count;
 }
 
-int gemm_config_count() { return kNumConfigs; }
+// Configurations kNumConfigs .. kNumConfigs + kValuShapes - 1 are the VALU kernel's lane blocks (gemm_valu.hip).
+int gemm_config_count() { return kNumConfigs + kValuShapes; }
 const char* gemm_config_name(int config) {
+	if (config == kNumConfigs + kValu2x2) return "valu 32x32 (2x2 chains per lane)";
+	if (config == kNumConfigs + kValu1x2) return "valu 16x32 (1x2 chains per lane)";
+	if (config == kNumConfigs + kValu2x4) return "valu 32x64 (2x4 chains per lane)";
+	if (config == kNumConfigs + kValu1x4) return "valu 16x64 (1x4 chains per lane)";
 	return (config >= 0 && config < kNumConfigs) ? configs()[config].name : "";
 }
 
@@ -202,6 +208,12 @@ hipError_t gemm_launch(const GemmCall& g, hipStream_t s, int config, float* work
 	if (g.m == 0 || g.n == 0 || g.batch_count == 0) return hipSuccess;
 	hipError_t e = prepare_device();
 	if (e != hipSuccess) return e;
+	// the VALU kernel: forced, or chosen by shape, for a product it can take
+	const bool valu_ok = !g.gather && !g.rowsum && g.k > 0 && !depth_cut(g.m, g.n, g.k) && g.m < (1 << 30) &&
+	                     g.n < (1 << 30) && g.k < (1 << 30);
+	if (valu_ok && config >= kNumConfigs && config < kNumConfigs + kValuShapes)
+		return gemm_valu_launch(g, config - kNumConfigs, s);
+	if ((config < 0 || config >= kNumConfigs) && valu_ok && valu_takes(g)) return gemm_valu_launch(g, valu_shape(g), s);
 	if (config < 0 || config >= kNumConfigs) config = pick_config(g);
 	const Config& cf = configs()[config];
 

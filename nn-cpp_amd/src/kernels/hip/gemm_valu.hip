@@ -1,0 +1,313 @@
+// gemm_valu.hip - the fp32 GEMM on the vector ALUs, for products too small to fill the GPU with MFMA tiles.
+//
+// Under nn-cpp's contract every element of C is one fma chain over the depth (gemm.cpp:232-244), so a product that
+// cannot keep the matrix cores busy with independent chains runs at the latency of a dependent k = 1 MFMA, 44
+// cycles per step. A dependent v_fma_f32 takes about 6 cycles, and a wave's lanes each run their own chains: here
+// every lane owns an RM x RN block of C and runs its RM * RN chains interleaved, so the VALU issues back to back.
+//   * A workgroup (4 waves as 2 x 2, each 8 x 8 lanes) owns a (16 RM) x (16 RN) tile. The depth is staged in LDS
+//     in chunks of 256, both operands k-contiguous (op(A) rows, op(B) columns; the transposes happen on the way in),
+//     row pitch 260 floats: a wave's 16-byte reads of 8 distinct rows land on distinct banks. A chunk's fmas take
+//     longer than the next chunk's global loads, which are in registers meanwhile (one wait per chunk).
+//   * Per four depth steps a lane reads RM + RN 16-byte words and issues 4 RM RN fmas, in depth order per chain,
+//     the next group's reads in flight.
+//   * The accumulate rule, the epilogue and the edges are the MFMA kernel's: old C joins after the first 256 steps
+//     (Store::kAdd, gemm.cpp:245-252), then bias, ReLU and the alive flags; only the m x n window is written.
+// Every chain has exactly k steps (a partial last chunk runs element by element), so -0 results stay -0.
+// The caller sends here only products without a depth cut.
+#include "gemm_valu.hpp"
+
+namespace nnh {
+
+namespace {
+
+// VC: depth per LDS chunk (the chunk's fmas outlast the next chunk's global loads); row pitch VC + 4 floats, 4 mod 64:
+// 16-byte reads of rows 4 floats apart hit distinct banks.
+template <int RM, int RN, int VC>
+struct VShape {
+	static constexpr int BM = 16 * RM, BN = 16 * RN;
+	static constexpr int kVp = VC + 4;
+	static constexpr int kBuf = (BM + BN) * kVp;   // floats of one chunk buffer
+	static_assert((BM * VC) % 1024 == 0 && (BN * VC) % 1024 == 0, "tiles split evenly over 256 threads");
+};
+
+// One chunk of op(X) (X = A with rows m, or B with columns n) into registers. R is the tile's row count (BM or BN),
+// rows are the m (or n) index, the depth index runs along the LDS row. KCONTIG: element (r, p) at X[r * ld + p]
+// (A untransposed, B transposed); otherwise at X[p * ld + r]. Branch-free: every address is clamped into the
+// matrix, so nothing outside it is read and every load is in flight at once; the values read for rows past the
+// matrix feed chains that are never stored, those for depth indices past k are never used (a partial chunk runs
+// exactly its k steps). VEC (16-byte loads) needs ld a multiple of 4, a 16-byte aligned base, and the contiguous
+// extent (k, or the rows) a multiple of 4.
+template <int R, bool KCONTIG, bool VEC, int kVc>
+struct ChunkLoader {
+	static constexpr int kVp = kVc + 4;
+	static constexpr int kPer = R * kVc / 4 / 256;
+	__device__ __forceinline__ static void load(const float* __restrict__ x, int64_t ld, int r0, int rows, int k0,
+	                                            int kdim, f32x4 (&v)[kPer], int tid) {
+#pragma unroll
+		for (int u = 0; u < kPer; ++u) {
+			const int idx = tid + 256 * u;
+			int r, p;
+			if (KCONTIG) {
+				r = idx / (kVc / 4);
+				p = 4 * (idx % (kVc / 4));
+			} else {
+				p = idx / (R / 4);
+				r = 4 * (idx % (R / 4));
+			}
+			const int gr = r0 + r, gp = k0 + p;
+			if (KCONTIG) {
+				const float* src = x + (int64_t)min(gr, rows - 1) * ld;
+				if (VEC) {
+					v[u] = *reinterpret_cast<const f32x4*>(src + min(gp, kdim - 4));
+				} else {
+#pragma unroll
+					for (int e = 0; e < 4; ++e) v[u][e] = src[min(gp + e, kdim - 1)];
+				}
+			} else {
+				const float* src = x + (int64_t)min(gp, kdim - 1) * ld;
+				if (VEC) {
+					v[u] = *reinterpret_cast<const f32x4*>(src + min(gr, rows - 4));
+				} else {
+#pragma unroll
+					for (int e = 0; e < 4; ++e) v[u][e] = src[min(gr + e, rows - 1)];
+				}
+			}
+		}
+	}
+	// into the LDS tile dst[r][p] (pitch kVp)
+	__device__ __forceinline__ static void store(float* dst, const f32x4 (&v)[kPer], int tid) {
+#pragma unroll
+		for (int u = 0; u < kPer; ++u) {
+			const int idx = tid + 256 * u;
+			if (KCONTIG) {
+				const int r = idx / (kVc / 4), p = 4 * (idx % (kVc / 4));
+				*reinterpret_cast<f32x4*>(dst + r * kVp + p) = v[u];
+			} else {
+				const int p = idx / (R / 4), r = 4 * (idx % (R / 4));
+#pragma unroll
+				for (int e = 0; e < 4; ++e) dst[(r + e) * kVp + p] = v[u][e];
+			}
+		}
+	}
+};
+
+template <bool TA, bool TB, int RM, int RN, bool VEC, int kVc>
+__global__ void __launch_bounds__(256) sgemm_valu_kernel(const GemmArgs p) {
+	using S = VShape<RM, RN, kVc>;
+	using LA = ChunkLoader<S::BM, !TA, VEC, kVc>;
+	using LB = ChunkLoader<S::BN, TB, VEC, kVc>;
+	constexpr int kVp = S::kVp;
+	extern __shared__ __align__(16) float lds[];  // 2 * S::kBuf floats
+	const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+	const int tiles = p.tiles_m * p.tiles_n;
+	const int t = blockIdx.x % tiles, bi = blockIdx.x / tiles;
+	const int tm = t / p.tiles_n, tn = t - tm * p.tiles_n;
+	const int m0 = tm * S::BM, n0 = tn * S::BN;
+	int64_t oa = 0, ob = 0, oc = 0;
+	if (p.batch.ndim > 0) batch_offsets(p.batch, bi, oa, ob, oc);
+	const float* __restrict__ A = p.a + oa;
+	const float* __restrict__ B = p.b + ob;
+	// this lane's block: rows lr0 .. lr0 + RM - 1, columns lc0 .. lc0 + RN - 1 of the tile
+	const int lr0 = (wave >> 1) * 8 * RM + (lane >> 3) * RM;
+	const int lc0 = (wave & 1) * 8 * RN + (lane & 7) * RN;
+
+	float acc[RM][RN];
+#pragma unroll
+	for (int i = 0; i < RM; ++i)
+#pragma unroll
+		for (int j = 0; j < RN; ++j) acc[i][j] = 0.0f;
+
+	const int nch = (p.k + kVc - 1) / kVc;
+	// the next chunk's global loads are in registers while the current chunk runs from LDS
+	f32x4 ra[LA::kPer], rb[LB::kPer];
+	auto gload = [&](int ch) {
+		const int k0 = ch * kVc;
+		LA::load(A, p.lda, m0, p.m, k0, p.k, ra, tid);
+		LB::load(B, p.ldb, n0, p.n, k0, p.k, rb, tid);
+	};
+	auto lstore = [&](int buf) {
+		float* base = lds + buf * S::kBuf;
+		LA::store(base, ra, tid);
+		LB::store(base + S::BM * kVp, rb, tid);
+	};
+	// the old C joins the chain after the first 256 steps (kAccAfter: the end of chunk kAccAfter / VC - 1), or at
+	// the end of a shorter one
+	static_assert(kAccAfter % kVc == 0, "the accumulate point is a chunk boundary");
+	const bool acc_mode = p.accumulate != 0;
+	auto add_old = [&]() {
+#pragma unroll
+		for (int i = 0; i < RM; ++i)
+#pragma unroll
+			for (int j = 0; j < RN; ++j) {
+				const int row = m0 + lr0 + i, col = n0 + lc0 + j;
+				if (row < p.m && col < p.n) acc[i][j] = p.c[oc + (int64_t)row * p.ldc + col] + acc[i][j];
+			}
+	};
+	auto compute = [&](int ch) {
+		const float* As = lds + (ch & 1) * S::kBuf + lr0 * kVp;
+		const float* Bs = lds + (ch & 1) * S::kBuf + S::BM * kVp + lc0 * kVp;
+		const int kc = min(kVc, p.k - ch * kVc);
+		auto rd = [&](f32x4 (&a)[RM], f32x4 (&b)[RN], int q) {
+#pragma unroll
+			for (int i = 0; i < RM; ++i) a[i] = *reinterpret_cast<const f32x4*>(As + i * kVp + 4 * q);
+#pragma unroll
+			for (int j = 0; j < RN; ++j) b[j] = *reinterpret_cast<const f32x4*>(Bs + j * kVp + 4 * q);
+		};
+		auto fm = [&](const f32x4 (&a)[RM], const f32x4 (&b)[RN], int steps) {
+#pragma unroll
+			for (int u = 0; u < 4; ++u)
+				if (u < steps)
+#pragma unroll
+					for (int i = 0; i < RM; ++i)
+#pragma unroll
+						for (int j = 0; j < RN; ++j) acc[i][j] = __builtin_fmaf(a[i][u], b[j][u], acc[i][j]);
+		};
+		// runs of 16 groups of 4 depth steps; inside a run the next group's 16-byte reads are issued before this
+		// group's fmas
+		const int q_full = kc / 4;
+		int q0 = 0;
+		for (; q0 + 16 <= q_full; q0 += 16) {
+			f32x4 a0[RM], b0[RN], a1[RM], b1[RN];
+			rd(a0, b0, q0);
+#pragma unroll
+			for (int q = 0; q < 16; q += 2) {
+				rd(a1, b1, q0 + q + 1);
+				fm(a0, b0, 4);
+				if (q + 2 < 16) rd(a0, b0, q0 + q + 2);
+				fm(a1, b1, 4);
+			}
+		}
+		for (; q0 < q_full; ++q0) {
+			f32x4 a0[RM], b0[RN];
+			rd(a0, b0, q0);
+			fm(a0, b0, 4);
+		}
+		if (kc % 4) {  // the last 1-3 steps of the depth
+			f32x4 a0[RM], b0[RN];
+			rd(a0, b0, q_full);
+			fm(a0, b0, kc % 4);
+		}
+	};
+
+	gload(0);
+	lstore(0);
+	__syncthreads();
+	for (int ch = 0; ch < nch; ++ch) {
+		if (ch + 1 < nch) gload(ch + 1);
+		compute(ch);
+		if (ch == kAccAfter / kVc - 1 && acc_mode && p.k > kAccAfter) add_old();
+		if (ch + 1 < nch) lstore((ch + 1) & 1);
+		__syncthreads();
+	}
+
+	// epilogue
+	const bool add_old_at_end = acc_mode && p.k <= kAccAfter;
+	float* __restrict__ Cp = p.c + oc;
+	unsigned char* alive = p.ep.alive ? p.ep.alive + oc : nullptr;
+#pragma unroll
+	for (int i = 0; i < RM; ++i) {
+		const int row = m0 + lr0 + i;
+		if (row >= p.m) continue;
+#pragma unroll
+		for (int j = 0; j < RN; ++j) {
+			const int col = n0 + lc0 + j;
+			if (col >= p.n) continue;
+			const int64_t off = (int64_t)row * p.ldc + col;
+			float v = acc[i][j];
+			if (add_old_at_end) v = Cp[off] + v;
+			if (p.ep.bias_mode == kBiasCol) v = v + p.ep.bias[col];
+			else if (p.ep.bias_mode == kBiasRow) v = v + p.ep.bias[row];
+			if (p.ep.relu) {
+				const bool on = v > 0.0f;
+				if (alive) alive[off] = on ? 1 : 0;
+				v = on ? v : 0.0f;
+			}
+			Cp[off] = v;
+		}
+	}
+}
+
+typedef void (*ValuFn)(const GemmArgs);
+
+template <int RM, int RN, bool VEC, int VC>
+ValuFn valu_fn(int ta, int tb) {
+	if (!ta && !tb) return sgemm_valu_kernel<false, false, RM, RN, VEC, VC>;
+	if (!ta && tb) return sgemm_valu_kernel<false, true, RM, RN, VEC, VC>;
+	if (ta && !tb) return sgemm_valu_kernel<true, false, RM, RN, VEC, VC>;
+	return sgemm_valu_kernel<true, true, RM, RN, VEC, VC>;
+}
+
+struct ValuShape {
+	int rm, rn, vc;
+};
+// kValu2x2, kValu1x2, kValu2x4, kValu1x4
+constexpr ValuShape kShapes[kValuShapes] = {{2, 2, 256}, {1, 2, 256}, {2, 4, 128}, {1, 4, 128}};
+
+template <bool VEC>
+ValuFn valu_pick(int shape, int ta, int tb) {
+	switch (shape) {
+	case kValu2x2: return valu_fn<2, 2, VEC, 256>(ta, tb);
+	case kValu1x2: return valu_fn<1, 2, VEC, 256>(ta, tb);
+	case kValu2x4: return valu_fn<2, 4, VEC, 128>(ta, tb);
+	default: return valu_fn<1, 4, VEC, 128>(ta, tb);
+	}
+}
+
+}  // namespace
+
+int valu_shape(const GemmCall& g) {
+	(void)g;
+	return kValu1x2;
+}
+
+bool valu_takes(const GemmCall& g) {
+	if (g.gather || g.rowsum || g.k <= 0 || g.m <= 0 || g.n <= 0) return false;
+	if (depth_cut(g.m, g.n, g.k)) return false;
+	if (g.m >= (1 << 30) || g.n >= (1 << 30) || g.k >= (1 << 30)) return false;
+	// Measured against the MFMA tiles (device time, one MI355X): the 1 x 2 lane block is faster up to 2^17 outputs
+	// with a depth of 256 or more (256 x 512 x 784 NT 11.2 against 14.3 us, 256 x 10 x 256 5.3 against 7.4,
+	// 256 x 512 x 256 NN 5.5 against 6.4) and slower from 2^18 (512^3: 14.3-15.1 against 9.2-10.8; 64 x 4096 x 4096:
+	// 94.5 against 60.1), where the MFMA tiles have enough chains to overlap and this kernel's LDS reads bind it.
+	const double outputs = (double)g.m * (double)g.n * (double)g.batch_count;
+	return outputs <= 131072.0 && g.k >= 256;
+}
+
+hipError_t gemm_valu_launch(const GemmCall& g, int shape, hipStream_t s) {
+	GemmArgs p{};
+	p.a = g.a;
+	p.b = g.b;
+	p.c = g.c;
+	p.lda = g.lda;
+	p.ldb = g.ldb;
+	p.ldc = g.ldc;
+	p.m = (int)g.m;
+	p.n = (int)g.n;
+	p.k = (int)g.k;
+	p.accumulate = g.accumulate;
+	p.batch_count = (int)g.batch_count;
+	p.batch = g.batch;
+	p.ep = g.ep;
+	p.pieces = 1;
+	// 16-byte loads: leading dimensions, batch strides and bases 16-byte aligned, and each operand's contiguous
+	// extent (k for a k-contiguous one, else m or n) a multiple of 4
+	bool vec_ok = (g.lda % 4 == 0) && (g.ldb % 4 == 0) && reinterpret_cast<uintptr_t>(g.a) % 16 == 0 &&
+	              reinterpret_cast<uintptr_t>(g.b) % 16 == 0 && (g.ta ? g.m : g.k) % 4 == 0 &&
+	              (g.tb ? g.k : g.n) % 4 == 0;
+	for (int d = 0; d < g.batch.ndim; ++d) vec_ok = vec_ok && g.batch.sa[d] % 4 == 0 && g.batch.sb[d] % 4 == 0;
+	p.vec_ok = vec_ok ? 1 : 0;
+	if (shape < 0 || shape >= kValuShapes) return hipErrorInvalidValue;
+	const int rm = kShapes[shape].rm, rn = kShapes[shape].rn, vc = kShapes[shape].vc;
+	p.tiles_m = (int)((g.m + 16 * rm - 1) / (16 * rm));
+	p.tiles_n = (int)((g.n + 16 * rn - 1) / (16 * rn));
+	const int64_t blocks = (int64_t)p.tiles_m * p.tiles_n * g.batch_count;
+	if (blocks > 0x7fffffff) return hipErrorInvalidConfiguration;
+	const ValuFn fn = vec_ok ? valu_pick<true>(shape, g.ta, g.tb) : valu_pick<false>(shape, g.ta, g.tb);
+	const size_t lds = (size_t)2 * (16 * rm + 16 * rn) * (vc + 4) * sizeof(float);
+	hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize,
+	                                   (int)lds);
+	if (e != hipSuccess) return e;
+	hipLaunchKernelGGL(fn, dim3((unsigned)blocks), dim3(256), lds, s, p);
+	return hipGetLastError();
+}
+
+}  // namespace nnh

@@ -1,0 +1,23 @@
+// gemm_valu.hpp - the fp32 GEMM on the vector ALUs (gemm_valu.hip; internal to libnnh): one fma chain per C element
+// as the MFMA kernel, for products whose outputs cannot fill the GPU with MFMA chains.
+#pragma once
+
+#include "gemm.hpp"
+
+namespace nnh {
+
+// Lane blocks: 2 x 2 chains (32 x 32 workgroup tiles), 1 x 2 (16 x 32), 2 x 4 (32 x 64), 1 x 4 (16 x 64).
+constexpr int kValu2x2 = 0;
+constexpr int kValu1x2 = 1;
+constexpr int kValu2x4 = 2;
+constexpr int kValu1x4 = 3;
+constexpr int kValuShapes = 4;
+
+// Whether the shape-based choice sends this product to the VALU kernel (no gather, no row sums, no depth cut, at
+// most 2^17 outputs and a depth of 256 or more), and which lane block it takes.
+bool valu_takes(const GemmCall& g);
+int valu_shape(const GemmCall& g);
+// The launch (any product without gather, row sums or a depth cut; k > 0).
+hipError_t gemm_valu_launch(const GemmCall& g, int shape, hipStream_t s);
+
+}  // namespace nnh
