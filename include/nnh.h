@@ -329,6 +329,27 @@ int nnh_layernorm_backward(const float* g, const float* x, const float* gamma, c
                            size_t R, size_t D, float* dx, int dx_first, float* dgamma, int dgamma_first, float* dbeta,
                            int dbeta_first, void* stream);
 
+/* nn::add (src/autograd/ops.cpp:331-337 forward, src/tensor.cpp:543-545) for a right operand broadcast along the left
+ * one's leading axes: y[o][j] = a[o][j] + b[j] over outer x inner (equal shapes: outer 1). y may be a itself. The
+ * backward rule is nnh_add_to_grad for a and, for a broadcast b, nnh_tensor_sum0 (sum_to_shape) then the store. */
+int nnh_add_forward(const float* a, const float* b, size_t outer, size_t inner, float* y, void* stream);
+
+/* nn::gelu, the tanh form (ops.cpp:451-466): tanh_saved receives tanh(k (x + c x^3)) per element (the reference keeps
+ * it for the backward pass), with nn-cpp's own tanh and exp (src/kernels/vmath.cpp:24-105), bit for bit. */
+int nnh_gelu_forward(const float* x, size_t count, float* y, float* tanh_saved, void* stream);
+/* Its backward rule (ops.cpp:467-480); first: dx is fresh (term + 0.0f), else term is added. */
+int nnh_gelu_backward(const float* x, const float* tanh_saved, const float* g, size_t count, float* dx, int first,
+                      void* stream);
+
+/* nn::embedding (ops.cpp:1991-2015): y row i = weight row rows[i] for a weight {V, D}. The rows are the ids as int32,
+ * validated by the caller (nn-cpp throws TensorShapeError for an id that is negative, fractional or >= V; an id out
+ * of range here reads a clamped row). */
+int nnh_embedding_forward(const float* weight, size_t V, size_t D, const int* rows, size_t count, float* y,
+                          void* stream);
+/* Its backward rule: dweight (first: zero-filled first) += g row i at row rows[i], for i in order. */
+int nnh_embedding_backward(const float* g, const int* rows, size_t count, size_t V, size_t D, float* dweight, int first,
+                           void* stream);
+
 #ifdef __cplusplus
 }
 #endif

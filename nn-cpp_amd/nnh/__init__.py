@@ -104,6 +104,11 @@ _EXTRA_DECLS = {
     "nnh_batchnorm_workspace_size": [_sz, _sz, _sz, _szp],
     "nnh_layernorm_forward": [_vp, _sz, _sz, _vp, _vp, C.c_float, _vp, _vp, _vp, _vp],
     "nnh_layernorm_backward": [_vp, _vp, _vp, _vp, _vp, _sz, _sz, _vp, C.c_int, _vp, C.c_int, _vp, C.c_int, _vp],
+    "nnh_add_forward": [_vp, _vp, _sz, _sz, _vp, _vp],
+    "nnh_gelu_forward": [_vp, _sz, _vp, _vp, _vp],
+    "nnh_gelu_backward": [_vp, _vp, _vp, _sz, _vp, C.c_int, _vp],
+    "nnh_embedding_forward": [_vp, _sz, _sz, _vp, _sz, _vp, _vp],
+    "nnh_embedding_backward": [_vp, _vp, _sz, _sz, _sz, _vp, C.c_int, _vp],
 }
 
 

@@ -1,0 +1,172 @@
+// elementwise.hip - the transformer's element-wise ops around the GEMMs: add with a broadcast right operand,
+// GELU (tanh form) forward and backward, embedding lookup and its gradient (src/autograd/ops.cpp:331-337, 451-481,
+// 1991-2015).
+//
+// GELU's tanh is nn-cpp's own (src/kernels/vmath.cpp:24-105): Cephes expf with the reference's constants and
+// operation order (x = n ln2 + r, ln2 split in two, a degree-5 polynomial in r, 2^n by building the exponent
+// bits), tanh(z) = (e^(2z) - 1) / (e^(2z) + 1) with z clamped to +-9. Every operation rounds on its own (the file is
+// built with -ffp-contract=off), the division is correctly rounded, rintf rounds half to even as nearbyint and
+// _MM_FROUND_TO_NEAREST_INT do, so each element gets the reference's bits (its 8-lane AVX2 form gives the scalar
+// form's bits per lane).
+#include "elementwise.hpp"
+
+#include <cmath>
+
+namespace nnh {
+
+namespace {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr float kExpLo = -87.3f, kExpHi = 88.3f;
+constexpr float kLog2e = 1.44269504088896341f;
+constexpr float kLn2Hi = 0.693359375f, kLn2Lo = -2.12194440e-4f;
+constexpr float kP0 = 1.9875691500e-4f, kP1 = 1.3981999507e-3f, kP2 = 8.3334519073e-3f;
+constexpr float kP3 = 4.1665795894e-2f, kP4 = 1.6666665459e-1f, kP5 = 5.0000001201e-1f;
+constexpr float kTanhMax = 9.0f;
+constexpr float kGeluK = 0.7978845608f;  // sqrt(2 / pi), ops.cpp:452
+constexpr float kGeluC = 0.044715f;
+
+__device__ __forceinline__ float exp_one(float x) {
+	if (x != x) return x;
+	if (x < kExpLo) return 0.0f;
+	if (x > kExpHi) return INFINITY;
+	const float n = rintf(x * kLog2e);
+	float r = x - n * kLn2Hi;
+	r = r - n * kLn2Lo;
+	float p = kP0;
+	p = p * r + kP1;
+	p = p * r + kP2;
+	p = p * r + kP3;
+	p = p * r + kP4;
+	p = p * r + kP5;
+	const float e = (p * (r * r) + r) + 1.0f;
+	const float pow2 = __int_as_float((int)(((unsigned)((int)n + 127)) << 23));
+	return e * pow2;
+}
+
+__device__ __forceinline__ float tanh_one(float x) {
+	if (x != x) return x;
+	float z = x < -kTanhMax ? -kTanhMax : x;
+	z = kTanhMax < z ? kTanhMax : z;
+	const float e = exp_one(z + z);
+	return (e - 1.0f) / (e + 1.0f);
+}
+
+__global__ void __launch_bounds__(256) add_bcast_kernel(const float* __restrict__ a, const float* __restrict__ b,
+                                                        int64_t total, int64_t inner, float* __restrict__ y) {
+	const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+	if (i >= total) return;
+	y[i] = a[i] + b[i % inner];
+}
+
+__global__ void __launch_bounds__(256) add_bcast4_kernel(const f32x4* __restrict__ a, const f32x4* __restrict__ b,
+                                                         int64_t total4, int64_t inner4, f32x4* __restrict__ y) {
+	const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+	if (i >= total4) return;
+	const f32x4 u = a[i], v = b[i % inner4];
+	y[i] = f32x4{u[0] + v[0], u[1] + v[1], u[2] + v[2], u[3] + v[3]};
+}
+
+// ops.cpp:461-466: th = k (x + c x x x), tanh in place, y = 0.5 x (1 + th); th is kept for the backward pass.
+__global__ void __launch_bounds__(256) gelu_forward_kernel(const float* __restrict__ x, int64_t count,
+                                                           float* __restrict__ y, float* __restrict__ th) {
+	const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+	if (i >= count) return;
+	const float v = x[i];
+	const float t = tanh_one(kGeluK * (v + kGeluC * v * v * v));
+	th[i] = t;
+	y[i] = 0.5f * v * (1.0f + t);
+}
+
+// ops.cpp:467-480: dx (first: term + 0, else +=) with term = g (0.5 (1 + t) + 0.5 v (1 - t t) k (1 + 3 c v v)).
+__global__ void __launch_bounds__(256) gelu_backward_kernel(const float* __restrict__ x, const float* __restrict__ th,
+                                                            const float* __restrict__ g, int64_t count,
+                                                            float* __restrict__ dx, int first) {
+	const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+	if (i >= count) return;
+	const float v = x[i], t = th[i];
+	const float term = g[i] * (0.5f * (1.0f + t) + 0.5f * v * (1.0f - t * t) * kGeluK * (1.0f + 3.0f * kGeluC * v * v));
+	dx[i] = first ? term + 0.0f : dx[i] + term;
+}
+
+// ops.cpp:2006-2007: out row i = weight row rows[i] (rows clamped into the table; the caller validates them).
+__global__ void __launch_bounds__(256) embedding_forward_kernel(const float* __restrict__ w, int64_t V, int64_t D,
+                                                                const int* __restrict__ rows, int64_t count,
+                                                                float* __restrict__ out) {
+	const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
+	if (e >= count * D) return;
+	const int64_t i = e / D, d = e - i * D;
+	const int64_t r = min<int64_t>(max(rows[i], 0), V - 1);
+	out[e] = w[r * D + d];
+}
+
+// ops.cpp:2008-2014: the gradient table (first: zeros) gets, for i in order, the output gradient's row i added to
+// row rows[i]. Gather form: a thread per table element walks the rows in order (staged through LDS) and adds the
+// gradients of the tokens that picked its row, so the additions keep the reference's order with no atomics.
+__global__ void __launch_bounds__(256) embedding_backward_kernel(const float* __restrict__ g, const int* __restrict__ rows,
+                                                                 int64_t count, int64_t V, int64_t D,
+                                                                 float* __restrict__ dw, int first) {
+	__shared__ int ids[1024];
+	const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
+	const bool here = e < V * D;
+	const int64_t v = here ? e / D : 0, d = here ? e - v * D : 0;
+	float acc = (first || !here) ? 0.0f : dw[e];
+	for (int64_t i0 = 0; i0 < count; i0 += 1024) {
+		const int n = (int)min<int64_t>(1024, count - i0);
+		__syncthreads();
+		for (int t = threadIdx.x; t < n; t += 256) ids[t] = rows[i0 + t];
+		__syncthreads();
+		if (here)
+			for (int t = 0; t < n; ++t)
+				if (ids[t] == v) acc = acc + g[(i0 + t) * D + d];
+	}
+	if (here) dw[e] = acc;
+}
+
+inline unsigned blocks_of(int64_t n) { return (unsigned)((n + 255) / 256); }
+
+}  // namespace
+
+hipError_t add_bcast(const float* a, const float* b, int64_t outer, int64_t inner, float* y, hipStream_t s) {
+	const int64_t total = outer * inner;
+	if (total == 0) return hipSuccess;
+	if (inner % 4 == 0 && reinterpret_cast<uintptr_t>(a) % 16 == 0 && reinterpret_cast<uintptr_t>(b) % 16 == 0 &&
+	    reinterpret_cast<uintptr_t>(y) % 16 == 0)
+		hipLaunchKernelGGL(add_bcast4_kernel, dim3(blocks_of(total / 4)), dim3(256), 0, s,
+		                   reinterpret_cast<const f32x4*>(a), reinterpret_cast<const f32x4*>(b), total / 4, inner / 4,
+		                   reinterpret_cast<f32x4*>(y));
+	else
+		hipLaunchKernelGGL(add_bcast_kernel, dim3(blocks_of(total)), dim3(256), 0, s, a, b, total, inner, y);
+	return hipGetLastError();
+}
+
+hipError_t gelu_forward(const float* x, int64_t count, float* y, float* th, hipStream_t s) {
+	if (count == 0) return hipSuccess;
+	hipLaunchKernelGGL(gelu_forward_kernel, dim3(blocks_of(count)), dim3(256), 0, s, x, count, y, th);
+	return hipGetLastError();
+}
+
+hipError_t gelu_backward(const float* x, const float* th, const float* g, int64_t count, float* dx, int first,
+                         hipStream_t s) {
+	if (count == 0) return hipSuccess;
+	hipLaunchKernelGGL(gelu_backward_kernel, dim3(blocks_of(count)), dim3(256), 0, s, x, th, g, count, dx, first);
+	return hipGetLastError();
+}
+
+hipError_t embedding_forward(const float* w, int64_t V, int64_t D, const int* rows, int64_t count, float* out,
+                             hipStream_t s) {
+	if (count * D == 0) return hipSuccess;
+	hipLaunchKernelGGL(embedding_forward_kernel, dim3(blocks_of(count * D)), dim3(256), 0, s, w, V, D, rows, count, out);
+	return hipGetLastError();
+}
+
+hipError_t embedding_backward(const float* g, const int* rows, int64_t count, int64_t V, int64_t D, float* dw, int first,
+                              hipStream_t s) {
+	if (V * D == 0) return hipSuccess;
+	hipLaunchKernelGGL(embedding_backward_kernel, dim3(blocks_of(V * D)), dim3(256), 0, s, g, rows, count, V, D, dw,
+	                   first);
+	return hipGetLastError();
+}
+
+}  // namespace nnh

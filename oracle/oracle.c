@@ -422,6 +422,68 @@ void oracle_layernorm_f64(const float* x, size_t R, size_t D, double eps, double
 	}
 }
 
+/* ---- element-wise: GELU and embedding ---- */
+
+/* nn-cpp's exp_one and tanh_one (src/kernels/vmath.cpp:68-97): Cephes expf with the reference's constants; every
+ * operation rounds on its own (-ffp-contract=off). */
+static float vm_exp_one(float x) {
+	if (x != x) return x;
+	if (x < -87.3f) return 0.0f;
+	if (x > 88.3f) return HUGE_VALF;
+	const float n = nearbyintf(x * 1.44269504088896341f);
+	float r = x - n * 0.693359375f;
+	r = r - n * -2.12194440e-4f;
+	float p = 1.9875691500e-4f;
+	p = p * r + 1.3981999507e-3f;
+	p = p * r + 8.3334519073e-3f;
+	p = p * r + 4.1665795894e-2f;
+	p = p * r + 1.6666665459e-1f;
+	p = p * r + 5.0000001201e-1f;
+	const float e = (p * (r * r) + r) + 1.0f;
+	const uint32_t bits = (uint32_t)((int32_t)n + 127) << 23;
+	float pow2;
+	memcpy(&pow2, &bits, sizeof pow2);
+	return e * pow2;
+}
+
+float oracle_tanh_one(float x) {
+	if (x != x) return x;
+	float z = x < -9.0f ? -9.0f : x;
+	z = 9.0f < z ? 9.0f : z;
+	const float e = vm_exp_one(z + z);
+	return (e - 1.0f) / (e + 1.0f);
+}
+
+/* gelu forward (ops.cpp:451-466): th = tanh(k (x + c x x x)), y = 0.5 x (1 + th). */
+void oracle_gelu_forward(const float* x, size_t count, float* y, float* th) {
+	const float k = 0.7978845608f, c = 0.044715f;
+	for (size_t i = 0; i < count; ++i) {
+		const float t = oracle_tanh_one(k * (x[i] + c * x[i] * x[i] * x[i]));
+		th[i] = t;
+		y[i] = 0.5f * x[i] * (1.0f + t);
+	}
+}
+
+/* gelu backward rule (ops.cpp:467-480). */
+void oracle_gelu_backward(const float* x, const float* th, const float* g, size_t count, float* dx, int first) {
+	const float k = 0.7978845608f, c = 0.044715f;
+	for (size_t i = 0; i < count; ++i) {
+		const float v = x[i], t = th[i];
+		const float term = g[i] * (0.5f * (1.0f + t) + 0.5f * v * (1.0f - t * t) * k * (1.0f + 3.0f * c * v * v));
+		dx[i] = first ? term + 0.0f : dx[i] + term;
+	}
+}
+
+/* embedding backward rule (ops.cpp:2008-2014): a fresh table is zero-filled, then g row i is added to row rows[i]
+ * for i in order. */
+void oracle_embedding_backward(const float* g, const int32_t* rows, size_t count, size_t V, size_t D, float* dw,
+		int first) {
+	if (first)
+		for (size_t e = 0; e < V * D; ++e) dw[e] = 0.0f;
+	for (size_t i = 0; i < count; ++i)
+		for (size_t d = 0; d < D; ++d) dw[(size_t)rows[i] * D + d] += g[i * D + d];
+}
+
 /* ---- max pooling ---- */
 
 /* maxpool2d forward (ops.cpp:1609-1684): per window, best = -inf and at = 0, then row by row a value replaces

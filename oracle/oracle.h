@@ -61,6 +61,13 @@ void oracle_layernorm_backward(const float* g, const float* x, const float* gm, 
 void oracle_batchnorm_f64(const float* x, size_t N, size_t C, size_t S, double eps, double* xhat);
 void oracle_layernorm_f64(const float* x, size_t R, size_t D, double eps, double* xhat);
 
+/* ---- element-wise (src/autograd/ops.cpp:451-481, 1991-2015; src/kernels/vmath.cpp) ---- */
+float oracle_tanh_one(float x);
+void oracle_gelu_forward(const float* x, size_t count, float* y, float* th);
+void oracle_gelu_backward(const float* x, const float* th, const float* g, size_t count, float* dx, int first);
+void oracle_embedding_backward(const float* g, const int32_t* rows, size_t count, size_t V, size_t D, float* dw,
+                               int first);
+
 /* ---- max pooling (src/autograd/ops.cpp:1609-1705) ---- */
 void oracle_maxpool2d_forward(const float* x, size_t planes, size_t H, size_t W, size_t k, size_t s, float* y,
                               uint32_t* argmax);

@@ -91,6 +91,11 @@ class Oracle:
         L.oracle_layernorm_backward.argtypes = [_f, _f, _f, _f, _f, _sz, _sz, _f, C.c_int, _f, C.c_int, _f, C.c_int]
         L.oracle_batchnorm_f64.argtypes = [_f, _sz, _sz, _sz, C.c_double, _d]
         L.oracle_layernorm_f64.argtypes = [_f, _sz, _sz, C.c_double, _d]
+        L.oracle_tanh_one.argtypes = [C.c_float]
+        L.oracle_tanh_one.restype = C.c_float
+        L.oracle_gelu_forward.argtypes = [_f, _sz, _f, _f]
+        L.oracle_gelu_backward.argtypes = [_f, _f, _f, _sz, _f, C.c_int]
+        L.oracle_embedding_backward.argtypes = [_f, C.POINTER(C.c_int32), _sz, _sz, _sz, _f, C.c_int]
         L.oracle_maxpool2d_forward.argtypes = [_f, _sz, _sz, _sz, _sz, _sz, _f, _u32]
         L.oracle_maxpool2d_backward.argtypes = [_f, _u32, _sz, _sz, _sz, _sz, _sz, _f, C.c_int]
 
@@ -352,6 +357,28 @@ class Oracle:
                                            int(dbeta_first))
         return tuple(outs)
 
+    def gelu_forward(self, x):
+        """(y, th) of nn::gelu, th the tanh it keeps for the backward pass."""
+        x = np.ascontiguousarray(x, np.float32)
+        y, th = np.empty_like(x), np.empty_like(x)
+        self.lib.oracle_gelu_forward(_fp(x), x.size, _fp(y), _fp(th))
+        return y, th
+
+    def gelu_backward(self, x, th, g, dx=None, first=True):
+        x = np.ascontiguousarray(x, np.float32)
+        out = np.array(dx, np.float32, copy=True) if dx is not None else np.empty_like(x)
+        self.lib.oracle_gelu_backward(_fp(x), _fp(np.ascontiguousarray(th, np.float32)),
+                                      _fp(np.ascontiguousarray(g, np.float32)), x.size, _fp(out), int(first))
+        return out
+
+    def embedding_backward(self, g, rows, V, D, dw=None, first=True):
+        g = np.ascontiguousarray(g, np.float32)
+        rows = np.ascontiguousarray(rows, np.int32)
+        out = np.array(dw, np.float32, copy=True) if dw is not None else np.empty((V, D), np.float32)
+        self.lib.oracle_embedding_backward(_fp(g), rows.ctypes.data_as(C.POINTER(C.c_int32)), rows.size, V, D,
+                                           _fp(out), int(first))
+        return out
+
     def batchnorm_f64(self, x, eps):
         x = np.ascontiguousarray(x, np.float32)
         N, Cc, S = self._nsc(x)
@@ -403,6 +430,8 @@ class Reference:
         L.nnref_batchnorm.argtypes = [_f, _sz, _sz, _sz, _f, _f, C.c_float, C.c_int, _f, _f, _f, _f, C.c_int, _f, _f,
                                       _f]
         L.nnref_layernorm.argtypes = [_f, _sz, _sz, _f, _f, C.c_float, _f, _f, C.c_int, _f, _f, _f]
+        L.nnref_gelu.argtypes = [_f, _sz, _f, _f, C.c_int, _f]
+        L.nnref_embedding.argtypes = [_f, _sz, _sz, _f, _sz, _f, _f, C.c_int, _f]
         L.nnref_time_batchnorm.argtypes = [_f, _sz, _sz, _sz, _f, _f, C.c_float, C.c_int, _f, C.c_int, C.c_int,
                                            C.c_double, _d, C.POINTER(C.c_int), _d, _f, _f]
         L.nnref_time_layernorm.argtypes = [_f, _sz, _sz, _f, _f, C.c_float, _f, C.c_int, C.c_int, C.c_double, _d,
@@ -588,6 +617,26 @@ class Reference:
         if rc != 0:
             return rc, None, None
         return 0, y, (tuple(grads) if g is not None else None)
+
+    def gelu(self, x, g=None, repeats=1):
+        """(rc, y, dx or None) of nn::gelu and its backward rule."""
+        x = np.ascontiguousarray(x, np.float32)
+        y, dx = np.empty_like(x), np.empty_like(x)
+        rc = self.lib.nnref_gelu(_fp(x), x.size, _fp(y), _fp(np.ascontiguousarray(g, np.float32)) if g is not None
+                                 else None, int(repeats), _fp(dx))
+        return rc, y, (dx if g is not None else None)
+
+    def embedding(self, w, ids, g=None, repeats=1):
+        """(rc, y, dw or None) of nn::embedding; ids are floats, as nn-cpp takes them."""
+        w = np.ascontiguousarray(w, np.float32)
+        ids = np.ascontiguousarray(ids, np.float32)
+        V, D = w.shape
+        y = np.empty((ids.size, D), np.float32)
+        dw = np.empty_like(w)
+        rc = self.lib.nnref_embedding(_fp(w), V, D, _fp(ids), ids.size, _fp(y),
+                                      _fp(np.ascontiguousarray(g, np.float32)) if g is not None else None, int(repeats),
+                                      _fp(dw))
+        return rc, (y if rc == 0 else None), (dw if g is not None and rc == 0 else None)
 
     # ---- timing (the CPU baseline): nn-cpp's own ops on buffers built once, apps/bench/runner.cpp's method ----
     # Each returns (times_ms, outputs): the timed runs after `warmup` untimed ones (at least one run, at most

@@ -602,6 +602,38 @@ int nnref_batchnorm(const float* x, size_t N, size_t C, size_t S, const float* w
 	});
 }
 
+// nn::gelu (ops.cpp:451-481) on count elements: y, then (g not null) the backward rule `repeats` times into dx.
+int nnref_gelu(const float* x, size_t count, float* y, const float* g, int repeats, float* dx) {
+	return guard([&] {
+		const Value xv = Value::leaf(make(x, {count}), true);
+		const Value r = nn::gelu(xv);
+		put(r.data(), y);
+		if (g) {
+			const Tensor gt = make(g, {count});
+			run_backward_rule(r, gt, {&xv});
+			for (int i = 1; i < repeats; ++i) r.impl()->backward_fn(gt);
+			put(xv.grad(), dx);
+		}
+	});
+}
+
+// nn::embedding (ops.cpp:1991-2015): weight {V, D}, ids (floats, as nn-cpp takes them) {count}; y, then (g not null)
+// the weight gradient through the backward rule `repeats` times. Returns 2 where nn-cpp throws TensorShapeError.
+int nnref_embedding(const float* w, size_t V, size_t D, const float* ids, size_t count, float* y, const float* g,
+		int repeats, float* dw) {
+	return guard([&] {
+		const Value wv = Value::leaf(make(w, {V, D}), true);
+		const Value r = nn::embedding(wv, make(ids, {count}));
+		put(r.data(), y);
+		if (g) {
+			const Tensor gt = make(g, {count, D});
+			run_backward_rule(r, gt, {&wv});
+			for (int i = 1; i < repeats; ++i) r.impl()->backward_fn(gt);
+			put(wv.grad(), dw);
+		}
+	});
+}
+
 // nn::layernorm (ops.cpp:1003-1078) over R rows of D, then its backward rule as nnref_batchnorm's.
 int nnref_layernorm(const float* x, size_t R, size_t D, const float* gm, const float* bt, float eps, float* y,
 		const float* g, int repeats, float* dx, float* dgamma, float* dbeta) {

@@ -428,6 +428,39 @@ void misc() {
 	EXPECT(nnh_version() ? OK : INV, OK);
 }
 
+void elem() {
+	auto a = buf(64), b = buf(64), y = buf(64), th = buf(64);
+	std::vector<int> rows(8, 0);
+	EXPECT(nnh_add_forward(a.data(), b.data(), 4, 16, y.data(), nullptr), HIP);
+	EXPECT(nnh_add_forward(a.data(), b.data(), 4, 16, a.data(), nullptr), HIP);
+	EXPECT(nnh_add_forward(a.data(), b.data(), 4, 16, a.data() + 1, nullptr), ALIAS);
+	EXPECT(nnh_add_forward(a.data(), b.data(), 4, 16, b.data(), nullptr), ALIAS);
+	EXPECT(nnh_add_forward(a.data(), b.data(), kHuge, kHuge, y.data(), nullptr), INV);
+	EXPECT(nnh_add_forward(nullptr, nullptr, 0, 16, nullptr, nullptr), OK);
+	EXPECT(nnh_add_forward(a.data(), nullptr, 4, 16, y.data(), nullptr), INV);
+	EXPECT(nnh_gelu_forward(a.data(), 64, y.data(), th.data(), nullptr), HIP);
+	EXPECT(nnh_gelu_forward(a.data(), 64, y.data(), y.data(), nullptr), ALIAS);
+	EXPECT(nnh_gelu_forward(a.data(), 64, a.data(), th.data(), nullptr), ALIAS);
+	EXPECT(nnh_gelu_forward(a.data(), 64, y.data(), nullptr, nullptr), INV);
+	EXPECT(nnh_gelu_forward(nullptr, 0, nullptr, nullptr, nullptr), OK);
+	EXPECT(nnh_gelu_backward(a.data(), th.data(), b.data(), 64, y.data(), 1, nullptr), HIP);
+	EXPECT(nnh_gelu_backward(a.data(), th.data(), b.data(), 64, b.data(), 1, nullptr), HIP);
+	EXPECT(nnh_gelu_backward(a.data(), th.data(), b.data(), 64, th.data(), 1, nullptr), ALIAS);
+	EXPECT(nnh_gelu_backward(a.data(), th.data(), b.data(), 64, b.data() + 2, 1, nullptr), ALIAS);
+	EXPECT(nnh_gelu_backward(a.data(), th.data(), b.data(), kHuge, y.data(), 1, nullptr), INV);
+	EXPECT(nnh_embedding_forward(a.data(), 8, 8, rows.data(), 8, y.data(), nullptr), HIP);
+	EXPECT(nnh_embedding_forward(a.data(), 0, 8, rows.data(), 8, y.data(), nullptr), SHAPE);
+	EXPECT(nnh_embedding_forward(a.data(), 8, 8, rows.data(), 8, a.data(), nullptr), ALIAS);
+	EXPECT(nnh_embedding_forward(a.data(), 8, 8, nullptr, 8, y.data(), nullptr), INV);
+	EXPECT(nnh_embedding_forward(a.data(), 8, 8, rows.data(), kHuge, y.data(), nullptr), INV);
+	EXPECT(nnh_embedding_forward(a.data(), 8, 8, rows.data(), 0, y.data(), nullptr), OK);
+	EXPECT(nnh_embedding_backward(b.data(), rows.data(), 8, 8, 8, y.data(), 1, nullptr), HIP);
+	EXPECT(nnh_embedding_backward(b.data(), rows.data(), 8, 8, 8, b.data(), 1, nullptr), ALIAS);
+	EXPECT(nnh_embedding_backward(b.data(), rows.data(), 8, 8, 8, nullptr, 1, nullptr), INV);
+	EXPECT(nnh_embedding_backward(b.data(), rows.data(), 8, kHuge, kHuge, y.data(), 1, nullptr), INV);
+	EXPECT(nnh_embedding_backward(nullptr, nullptr, 0, 8, 8, y.data(), 1, nullptr), HIP);
+}
+
 }  // namespace
 
 int main() {
@@ -438,6 +471,7 @@ int main() {
 	}
 	gemm();
 	norm();
+	elem();
 	sizes();
 	matmul();
 	linear_relu();

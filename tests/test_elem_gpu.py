@@ -1,0 +1,152 @@
+"""The transformer's element-wise ops on the GPU (nnh_add_forward, nnh_gelu_*, nnh_embedding_*) against the
+oracle, bit for bit: GELU over a sweep that crosses the tanh clamp and every special value, fresh and added
+gradients; add with a broadcast row, on aligned and unaligned buffers and in place; embedding rows gathered and the
+gradient table built in token order with repeated ids, fresh and added to, over more tokens than one staging pass."""
+import numpy as np
+import pytest
+
+from helpers import assert_same
+
+pytestmark = pytest.mark.gpu
+
+
+def dev(a, offset=0):
+    """A device copy of a placed `offset` elements into a larger buffer (offset 1 breaks 16-byte alignment)."""
+    import torch
+    a = np.ascontiguousarray(a)
+    t = torch.empty(a.size + offset, dtype=torch.from_numpy(a[:0]).dtype, device="cuda")
+    t[offset:] = torch.from_numpy(a.ravel()).cuda()
+    return t
+
+
+def host(t, offset, shape):
+    return t[offset:].cpu().numpy().reshape(shape)
+
+
+def gelu_inputs(n, seed):
+    rng = np.random.default_rng(seed)
+    x = np.concatenate([rng.normal(size=n).astype(np.float32) * 3,
+                        np.linspace(-12, 12, 4001).astype(np.float32),
+                        np.array([0, -0.0, 1e-30, -1e-30, 1e4, -1e4, np.inf, -np.inf, np.nan], np.float32)])
+    return x, rng.normal(size=x.size).astype(np.float32)
+
+
+@pytest.mark.parametrize("n,offset", [(0, 0), (1, 0), (64 * 256, 0), (64 * 256, 1), (300000, 0)])
+def test_gelu_bitwise(gpu, oracle, n, offset):
+    import torch
+
+    import nnh
+    L = nnh.lib()
+    x, g = gelu_inputs(n, n)
+    want_y, want_th = oracle.gelu_forward(x)
+    xd, gd = dev(x, offset), dev(g, offset)
+    y, th = dev(np.full(x.size, np.nan, np.float32), offset), dev(np.full(x.size, np.nan, np.float32), offset)
+    nnh.check(L.nnh_gelu_forward(nnh._ptr(xd, offset), x.size, nnh._ptr(y, offset), nnh._ptr(th, offset),
+                                 nnh._stream(None)))
+    dx = dev(np.full(x.size, np.nan, np.float32), offset)
+    nnh.check(L.nnh_gelu_backward(nnh._ptr(xd, offset), nnh._ptr(th, offset), nnh._ptr(gd, offset), x.size,
+                                  nnh._ptr(dx, offset), 1, nnh._stream(None)))
+    torch.cuda.synchronize()
+    assert_same(host(y, offset, x.shape), want_y, "gelu y", nan_equal=True)
+    assert_same(host(th, offset, x.shape), want_th, "gelu tanh", nan_equal=True)
+    want_dx = oracle.gelu_backward(x, want_th, g)
+    assert_same(host(dx, offset, x.shape), want_dx, "gelu dx", nan_equal=True)
+    # added to an existing gradient (the second use of the same activation)
+    nnh.check(L.nnh_gelu_backward(nnh._ptr(xd, offset), nnh._ptr(th, offset), nnh._ptr(gd, offset), x.size,
+                                  nnh._ptr(dx, offset), 0, nnh._stream(None)))
+    torch.cuda.synchronize()
+    assert_same(host(dx, offset, x.shape), oracle.gelu_backward(x, want_th, g, want_dx, False), "gelu dx added",
+                nan_equal=True)
+
+
+def test_gelu_backward_in_place_over_g(gpu, oracle):
+    """dx may be g itself (each element reads its g before writing dx)."""
+    import torch
+
+    import nnh
+    L = nnh.lib()
+    x, g = gelu_inputs(5000, 3)
+    _, th = oracle.gelu_forward(x)
+    xd, thd, gd = dev(x), dev(th), dev(g)
+    nnh.check(L.nnh_gelu_backward(nnh._ptr(xd), nnh._ptr(thd), nnh._ptr(gd), x.size, nnh._ptr(gd), 1,
+                                  nnh._stream(None)))
+    torch.cuda.synchronize()
+    assert_same(gd.cpu().numpy(), oracle.gelu_backward(x, th, g), "gelu dx over g", nan_equal=True)
+
+
+@pytest.mark.parametrize("outer,inner,offset", [(1, 1, 0), (7, 3, 0), (512, 64, 0), (512, 64, 1), (64, 256, 0),
+                                                (3, 100003, 0), (1000, 4, 0)])
+def test_add_broadcast_bitwise(gpu, outer, inner, offset):
+    """y = a + b with b one row broadcast over the leading axes (nn::add's suffix broadcast): one rounding per
+    element, so numpy's float32 sum is the reference's."""
+    import torch
+
+    import nnh
+    L = nnh.lib()
+    rng = np.random.default_rng(outer * 7 + inner)
+    a = rng.normal(size=(outer, inner)).astype(np.float32)
+    b = rng.normal(size=inner).astype(np.float32)
+    ad, bd = dev(a, offset), dev(b, offset)
+    y = dev(np.full(a.shape, np.nan, np.float32), offset)
+    nnh.check(L.nnh_add_forward(nnh._ptr(ad, offset), nnh._ptr(bd, offset), outer, inner, nnh._ptr(y, offset),
+                                nnh._stream(None)))
+    torch.cuda.synchronize()
+    assert_same(host(y, offset, a.shape), a + b, "add")
+    # in place: y = a
+    nnh.check(L.nnh_add_forward(nnh._ptr(ad, offset), nnh._ptr(bd, offset), outer, inner, nnh._ptr(ad, offset),
+                                nnh._stream(None)))
+    torch.cuda.synchronize()
+    assert_same(host(ad, offset, a.shape), a + b, "add in place")
+
+
+def test_add_rejects_overlaps(gpu):
+    import torch
+
+    import nnh
+    L = nnh.lib()
+    t = torch.zeros(64, device="cuda")
+    with pytest.raises(nnh.NnhError):
+        nnh.check(L.nnh_add_forward(nnh._ptr(t), nnh._ptr(t, 32), 2, 16, nnh._ptr(t, 40), nnh._stream(None)))
+    with pytest.raises(nnh.NnhError):  # y shifted by one element against a
+        nnh.check(L.nnh_add_forward(nnh._ptr(t), nnh._ptr(t, 48), 2, 16, nnh._ptr(t, 1), nnh._stream(None)))
+
+
+@pytest.mark.parametrize("V,D,count,offset", [(64, 64, 512, 0), (64, 64, 4096, 0), (5, 3, 2500, 1), (1, 8, 10, 0),
+                                              (1000, 1, 3000, 0), (64, 64, 0, 0)])
+def test_embedding_bitwise(gpu, oracle, V, D, count, offset):
+    import torch
+
+    import nnh
+    L = nnh.lib()
+    rng = np.random.default_rng(V * 31 + count)
+    w = rng.normal(size=(V, D)).astype(np.float32)
+    rows = rng.integers(0, V, count).astype(np.int32)
+    g = rng.normal(size=(count, D)).astype(np.float32)
+    wd, rd, gd = dev(w, offset), dev(rows, offset), dev(g, offset)
+    y = dev(np.full((count, D), np.nan, np.float32), offset)
+    nnh.check(L.nnh_embedding_forward(nnh._ptr(wd, offset), V, D, nnh._ptr(rd, offset), count, nnh._ptr(y, offset),
+                                      nnh._stream(None)))
+    dw = dev(np.full((V, D), np.nan, np.float32), offset)
+    nnh.check(L.nnh_embedding_backward(nnh._ptr(gd, offset), nnh._ptr(rd, offset), count, V, D, nnh._ptr(dw, offset),
+                                       1, nnh._stream(None)))
+    torch.cuda.synchronize()
+    assert_same(host(y, offset, (count, D)), w[rows], "embedding y")
+    want = oracle.embedding_backward(g, rows, V, D)
+    assert_same(host(dw, offset, (V, D)), want, "embedding dw")
+    nnh.check(L.nnh_embedding_backward(nnh._ptr(gd, offset), nnh._ptr(rd, offset), count, V, D, nnh._ptr(dw, offset),
+                                       0, nnh._stream(None)))
+    torch.cuda.synchronize()
+    assert_same(host(dw, offset, (V, D)), oracle.embedding_backward(g, rows, V, D, want, False), "embedding dw added")
+
+
+def test_embedding_errors(gpu):
+    import torch
+
+    import nnh
+    L = nnh.lib()
+    t = torch.zeros(64, device="cuda")
+    r = torch.zeros(4, dtype=torch.int32, device="cuda")
+    with pytest.raises(nnh.ShapeError):  # an empty table has no row for any id
+        nnh.check(L.nnh_embedding_forward(nnh._ptr(t), 0, 4, nnh._ptr(r), 4, nnh._ptr(t), nnh._stream(None)))
+    with pytest.raises(nnh.NnhError):  # y over the table
+        nnh.check(L.nnh_embedding_forward(nnh._ptr(t), 4, 4, nnh._ptr(r), 2, nnh._ptr(t, 8), nnh._stream(None)))

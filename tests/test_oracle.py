@@ -646,3 +646,73 @@ def test_layernorm_hand_values_and_fp64(oracle):
     assert np.allclose(db, g.reshape(-1, 16).astype(np.float64).sum(0), atol=1e-3)
     assert np.allclose(dg, (g * xhat).reshape(-1, 16).sum(0), atol=1e-3)
     assert np.max(np.abs(dx.astype(np.float64).sum(-1))) < 1e-4
+
+
+# ---------------------------------------------------------------- element-wise: GELU, embedding
+
+def _gelu_inputs(seed=0):
+    rng = np.random.default_rng(seed)
+    x = np.concatenate([rng.normal(size=50000).astype(np.float32) * 3,
+                        np.linspace(-12, 12, 20001).astype(np.float32),  # both sides of the +-9 clamp of 2z
+                        np.array([0, -0.0, 1e-30, -1e-30, 1e4, -1e4, np.inf, -np.inf, np.nan], np.float32)])
+    return x, rng.normal(size=x.size).astype(np.float32)
+
+
+def _bits_nan_equal(a, b):
+    na, nb = np.isnan(a), np.isnan(b)
+    return np.array_equal(na, nb) and np.array_equal(a.view(np.uint32)[~na], b.view(np.uint32)[~nb])
+
+
+def test_gelu_matches_nncpp(oracle, ref):
+    """Against nn-cpp's compiled nn::gelu (its AVX2 eight-lane tanh for whole groups of eight and the scalar form for
+    the tail): forward, the saved tanh feeding the backward rule, fresh and added gradients."""
+    x, g = _gelu_inputs()
+    y, th = oracle.gelu_forward(x)
+    rc, yr, dxr = ref.gelu(x, g)
+    assert rc == 0 and _bits_nan_equal(y, yr)
+    dx = oracle.gelu_backward(x, th, g)
+    assert _bits_nan_equal(dx, dxr)
+    rc, _, dx2r = ref.gelu(x, g, repeats=2)
+    assert _bits_nan_equal(oracle.gelu_backward(x, th, g, dx, False), dx2r)
+
+
+def test_gelu_against_the_closed_form(oracle):
+    """y = x/2 (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))) in fp64 within 2e-6 of |y| + 1e-6 (the tanh is computed as
+    (e^2z - 1)/(e^2z + 1), which loses relative precision near 0); tanh(0) = 0, tanh(+-20) = +-1 exactly, NaN stays NaN;
+    the derivative against a central difference of the fp64 form."""
+    x, g = _gelu_inputs(1)
+    y, th = oracle.gelu_forward(x)
+    fin = np.isfinite(x) & (np.abs(x) < 100)
+    xd = x[fin].astype(np.float64)
+    want = 0.5 * xd * (1 + np.tanh(np.sqrt(2 / np.pi) * (xd + 0.044715 * xd ** 3)))
+    assert np.all(np.abs(y[fin] - want) <= 2e-6 * np.abs(want) + 1e-6)
+    assert oracle.lib.oracle_tanh_one(0.0) == 0.0 and oracle.lib.oracle_tanh_one(20.0) == 1.0
+    assert oracle.lib.oracle_tanh_one(-20.0) == -1.0 and np.isnan(oracle.lib.oracle_tanh_one(float("nan")))
+    f = lambda v: 0.5 * v * (1 + np.tanh(np.sqrt(2 / np.pi) * (v + 0.044715 * v ** 3)))
+    xs = np.linspace(-6, 6, 1001).astype(np.float32)
+    _, ths = oracle.gelu_forward(xs)
+    d = oracle.gelu_backward(xs, ths, np.ones_like(xs))
+    h = 1e-5
+    num = (f(xs.astype(np.float64) + h) - f(xs.astype(np.float64) - h)) / (2 * h)
+    assert np.max(np.abs(d - num)) < 1e-5
+
+
+def test_embedding_matches_nncpp(oracle, ref):
+    """Rows gathered; the gradient table gets the output rows added in token order (repeated ids included), fresh
+    and added; ids that nn-cpp rejects (fractional, negative, past the table) throw TensorShapeError there."""
+    rng = np.random.default_rng(2)
+    w = rng.normal(size=(64, 32)).astype(np.float32)
+    ids = rng.integers(0, 64, 500).astype(np.float32)
+    g = rng.normal(size=(500, 32)).astype(np.float32)
+    rc, y, dwr = ref.embedding(w, ids, g)
+    assert rc == 0 and np.array_equal(y, w[ids.astype(int)])
+    rows = ids.astype(np.int32)
+    dw = oracle.embedding_backward(g, rows, 64, 32)
+    assert dw.tobytes() == dwr.tobytes()
+    # hand values: two tokens on row 3 add in order, untouched rows are +0
+    small = oracle.embedding_backward(np.array([[1.0], [2.0], [-1.0]], np.float32), np.array([3, 3, 0], np.int32), 5, 1)
+    assert small.ravel().tolist() == [-1.0, 0.0, 0.0, 3.0, 0.0]
+    rc, _, dw2r = ref.embedding(w, ids, g, repeats=2)
+    assert oracle.embedding_backward(g, rows, 64, 32, dw, False).tobytes() == dw2r.tobytes()
+    for bad in (1.5, 64.0, -1.0):
+        assert ref.embedding(w, np.array([bad], np.float32))[0] == 2
