@@ -715,24 +715,18 @@ def run_cpu_rows(rows, headline=None):
     return setup
 
 
-WORKLOADS = [  # (name, model index of libnnh_workloads, batch, input shape, parameter shapes)
-    ("mlp_wide", 0, 256, (256, 784), [(1024, 784), (1024,), (1024, 1024), (1024,), (10, 1024), (10,)]),
-    ("cnn_mnist", 1, 32, (32, 1, 28, 28), [(8, 1, 3, 3), (8,), (16, 8, 3, 3), (16,), (128, 784), (128,), (10, 128),
-                                           (10,)]),
-]
-
-
 def run_workloads(with_cpu=True, seed=1, warmup=3, runs=15):
-    """nn-cpp's bench models (apps/bench/workloads.cpp:100-137): parameters reseeded from std::mt19937(seed) and the
-    input drawn from std::mt19937(seed + 1), as make_workload does; one training step's forward pass and its zero_grad
-    plus backward pass (from a fixed N(0,1) gradient of the logits; no loss, no optimizer step), timed as
-    runner.cpp:33-45 does, median of `runs` after `warmup`: on the GPU through nn::hip (libnnh_workloads.so), and
-    nn-cpp's own step on the CPU (one thread per physical core, pinned), the logits compared bit for bit."""
+    """nn-cpp's bench models (apps/bench/workloads.cpp:80-137; the definitions are nnh/workloads.py): parameters
+    reseeded from std::mt19937(seed) and the input drawn from std::mt19937(seed + 1), as make_workload does; one
+    training step's forward pass and its zero_grad plus backward pass (from a fixed N(0,1) gradient of the logits; no
+    loss, no optimizer step), timed as runner.cpp:33-45 does, median of `runs` after `warmup`: on the GPU through
+    nn::hip (libnnh_workloads.so), and nn-cpp's own step on the CPU (one thread per physical core, pinned), the logits
+    compared bit for bit."""
     import ctypes as C
 
     import numpy as np
 
-    from nnh import synth
+    from nnh import workloads as wl
     L = C.CDLL(os.path.join(ROOT, "nn-cpp_amd", "lib", "libnnh_workloads.so"))
     ref = None
     if with_cpu:
@@ -740,32 +734,25 @@ def run_workloads(with_cpu=True, seed=1, warmup=3, runs=15):
         from pyoracle import Reference, reference_available
         if reference_available():
             ref = Reference()
-    fp = lambda a: a.ctypes.data_as(C.POINTER(C.c_float))
-    dp = lambda a: a.ctypes.data_as(C.POINTER(C.c_double))
     out = []
-    for name, model, N, xshape, shapes in WORKLOADS:
-        params = synth.reseeded_parameters(seed, shapes)
-        x = synth.mt19937_uniform(seed + 1, int(np.prod(xshape)), 0.0, 1.0).reshape(xshape)
-        g = synth.normal(seed + 2, (N, 10))
-        pp = (C.POINTER(C.c_float) * len(params))(*[fp(p) for p in params])
-        res = {"workload": name, "batch": N}
+    for w in wl.WORKLOADS:
+        params, x, g = wl.inputs(w, seed)
+        res = {"workload": w.name, "batch": w.batch}
         for side, lib, fn in (("gpu", L, "nnh_bench_workload_step"), ("cpu", ref.lib if ref else None,
                                                                        "nnref_time_workload_step")):
             if lib is None:
                 continue
-            fwd, bwd = np.empty(runs), np.empty(runs)
-            logits = np.empty((N, 10), np.float32)
             if side == "cpu":
                 cores, _ = physical_cores()
                 saved = os.sched_getaffinity(0)
                 os.sched_setaffinity(0, cores)
                 ref.set_threads(len(cores))
             try:
-                rc = getattr(lib, fn)(model, fp(x), C.c_size_t(N), pp, fp(g), warmup, runs, dp(fwd), dp(bwd), fp(logits))
+                rc, fwd, bwd, logits, _ = wl.run_step(getattr(lib, fn), w, params, x, g, warmup, runs)
             finally:
                 if side == "cpu":
                     os.sched_setaffinity(0, saved)
-            assert rc == 0, (name, side, rc)
+            assert rc == 0, (w.name, side, rc)
             tot = list(fwd + bwd)
             res[side] = {"forward_ms": median(list(fwd)), "backward_ms": median(list(bwd)), "total_ms": median(tot),
                          "spread": spread(tot), "runs": runs}
@@ -778,9 +765,9 @@ def run_workloads(with_cpu=True, seed=1, warmup=3, runs=15):
             res["speedup_gpu"] = res["cpu"]["total_ms"] / res["gpu"]["total_ms"]
         for k in ("gpu_logits", "cpu_logits"):
             res.pop(k, None)
-        log(f"[workload] {name}: GPU forward {res['gpu']['forward_ms']:.3f} ms + backward {res['gpu']['backward_ms']:.3f}"
-            f" ms" + (f"; nn-cpp CPU {res['cpu']['total_ms']:.3f} ms; logits bitwise {res['bitwise_vs_nn_cpp']}"
-                      if "cpu" in res else ""))
+        log(f"[workload] {w.name}: GPU forward {res['gpu']['forward_ms']:.3f} ms + backward "
+            f"{res['gpu']['backward_ms']:.3f} ms" + (f"; nn-cpp CPU {res['cpu']['total_ms']:.3f} ms; logits bitwise "
+                                                     f"{res['bitwise_vs_nn_cpp']}" if "cpu" in res else ""))
         out.append(res)
     return out
 

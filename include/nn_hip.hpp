@@ -156,6 +156,18 @@ Value attention(const Value& q, const Value& k, const Value& v, size_t heads, co
                 bool causal);
 // ops.cpp:1298-1343: softmax over the last axis of {N, H, Tq, Tk} after scaling and masking.
 Value scaled_masked_softmax(const Value& x, float scale_by, const Tensor& key_padding_mask, bool causal);
+// ops.hpp:22 (ops.cpp:331-337): a + b, for b of a's shape or of a's trailing axes (broadcast along the leading
+// ones, as PositionalEncoding adds its table); b's gradient is then summed one leading axis at a time
+// (sum_to_shape, ops.cpp:35-53). Other broadcasts are refused with std::invalid_argument.
+Value add(const Value& a, const Value& b);
+// ops.hpp:195 (ops.cpp:451-481): GELU, tanh form.
+Value gelu(const Value& x);
+// ops.hpp:255 (ops.cpp:1991-2015): rows of weight {V, D} picked by float ids (whole numbers in [0, V), checked on the
+// host: TensorShapeError otherwise); the result has ids' shape plus D. The device-tensor form reads the ids back.
+Value embedding(const Value& weight, const std::vector<float>& ids, const std::vector<size_t>& ids_shape);
+Value embedding(const Value& weight, const Tensor& ids);
+// positional.cpp:15-25: the fixed sinusoidal table {max_len, dim}, computed in double on the host and stored as fp32.
+Tensor sinusoidal_table(size_t max_len, size_t dim);
 
 }  // namespace hip
 }  // namespace nn

@@ -27,15 +27,17 @@ def mt19937_uniform(seed, count, lo=-1.0, hi=1.0):
     return uniform_from_raw(mt19937_raw(seed, count), lo, hi)
 
 
-def reseeded_parameters(seed, shapes):
-    """apps/bench/workloads.cpp:24-38 reseed_parameters: one std::mt19937(seed) stream over the parameters in order;
-    a parameter of rank < 2 becomes zeros (no draws), any other U(+-1/sqrt(size / shape[0])) in row-major order."""
+def reseeded_parameters(seed, shapes, ones=()):
+    """apps/bench/workloads.cpp:28-43 reseed_parameters: one std::mt19937(seed) stream over the parameters in order;
+    a parameter of rank < 2 becomes zeros (no draws), or stays all ones when its index is in `ones` (keep_ones_rank1
+    for parameters initialised to one, as LayerNorm's gamma is); any other U(+-1/sqrt(size / shape[0])) in row-major
+    order."""
     sizes = [int(np.prod(s)) for s in shapes]
     raw = mt19937_raw(seed, sum(n for s, n in zip(shapes, sizes) if len(s) >= 2))
     out, off = [], 0
-    for s, n in zip(shapes, sizes):
+    for i, (s, n) in enumerate(zip(shapes, sizes)):
         if len(s) < 2:
-            out.append(np.zeros(s, np.float32))
+            out.append(np.ones(s, np.float32) if i in ones else np.zeros(s, np.float32))
             continue
         bound = np.float32(1.0) / np.sqrt(np.float32(n // s[0]))
         out.append(np.ascontiguousarray(uniform_from_raw(raw[off:off + n], -bound, bound).reshape(s)))
@@ -57,3 +59,10 @@ def uniform_operands(seed, shapes, lo=-1.0, hi=1.0):
 def normal(seed, shape):
     """N(0, 1) float32 values (numpy's PCG64 stream; both sides receive the same buffer)."""
     return np.random.default_rng(seed).standard_normal(size=shape, dtype=np.float32)
+
+
+def uniform_ids(seed, count, bits):
+    """std::uniform_int_distribution<int>(0, 2^bits - 1) over std::mt19937(seed), as libstdc++ 11 draws it
+    (multiply-shift: (r * 2^bits) >> 32, which for a power-of-two range keeps the top `bits` bits of each output and
+    never rejects), as floats: the token ids of apps/bench/workloads.cpp:85-87."""
+    return (mt19937_raw(seed, count) >> np.uint32(32 - bits)).astype(np.float32)

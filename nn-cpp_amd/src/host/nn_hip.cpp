@@ -551,5 +551,104 @@ Value scaled_masked_softmax(const Value& x, float scale_by, const Tensor& key_pa
 	});
 }
 
+Value add(const Value& a, const Value& b) {
+	const auto& as = a.data().shape();
+	const auto& bs = b.data().shape();
+	if (bs.size() > as.size() || !std::equal(bs.begin(), bs.end(), as.end() - bs.size()))
+		throw std::invalid_argument("nn::hip: add takes b of a's shape or of a's trailing axes");
+	const size_t inner = b.data().size(), total = a.data().size();
+	const size_t outer = inner ? total / inner : 0;
+	Tensor y = Tensor::empty(as);
+	check(nnh_add_forward(a.data().data(), b.data().data(), outer, inner, y.data(), g_stream));
+	return Value::node(std::move(y), {a, b}, [a, b](const Tensor& g) {
+		// ops.cpp:333-336 then accumulate_grad (ops.cpp:110-117): a, then b, each stored fresh or added to
+		bool first = false;
+		if (float* da = grad_if(a, first)) check(nnh_add_to_grad(da, g.data(), g.size(), first, g_stream));
+		float* db = grad_if(b, first);
+		if (!db) return;
+		const auto& gs = g.shape();
+		const size_t lead = gs.size() - b.data().ndim();
+		if (lead == 0) {
+			check(nnh_add_to_grad(db, g.data(), g.size(), first, g_stream));
+			return;
+		}
+		// sum_to_shape: Tensor::sum(0) once per leading axis, the last one straight into the gradient
+		Tensor cur = g;
+		for (size_t i = 0; i < lead; ++i) {
+			const std::vector<size_t> rest(cur.shape().begin() + 1, cur.shape().end());
+			if (i + 1 == lead) {
+				check(nnh_tensor_sum0(cur.data(), cur.shape()[0], numel(rest), db, first ? 1 : 2, g_stream));
+			} else {
+				Tensor next = Tensor::empty(rest);
+				check(nnh_tensor_sum0(cur.data(), cur.shape()[0], numel(rest), next.data(), 0, g_stream));
+				cur = next;
+			}
+		}
+	});
+}
+
+Value gelu(const Value& x) {
+	Tensor y = Tensor::empty(x.data().shape());
+	Tensor th = Tensor::empty(x.data().shape());  // tanh(k (x + c x^3)), kept for the backward rule
+	check(nnh_gelu_forward(x.data().data(), y.size(), y.data(), th.data(), g_stream));
+	return Value::node(std::move(y), {x}, [x, th](const Tensor& g) {
+		bool first = false;
+		float* dx = grad_if(x, first);
+		if (dx) check(nnh_gelu_backward(x.data().data(), th.data(), g.data(), g.size(), dx, first, g_stream));
+	});
+}
+
+Value embedding(const Value& weight, const std::vector<float>& ids, const std::vector<size_t>& ids_shape) {
+	const auto& ws = weight.data().shape();
+	// ops.cpp:1992-2001
+	if (ws.size() != 2) throw TensorShapeError("nn::hip: embedding weight must be {V, D}");
+	if (numel(ids_shape) != ids.size()) throw std::invalid_argument("nn::hip: embedding ids and their shape differ");
+	const size_t V = ws[0], D = ws[1];
+	if (ids.size() > (size_t)INT32_MAX || V > (size_t)INT32_MAX)
+		throw std::invalid_argument("nn::hip: embedding takes at most 2^31 - 1 ids and table rows");
+	std::vector<int> rows(ids.size());
+	for (size_t i = 0; i < ids.size(); ++i) {
+		const float f = ids[i];
+		if (!(f >= 0.0f) || f != std::floor(f) || f >= static_cast<float>(V))
+			throw TensorShapeError("nn::hip: embedding id out of range or not a whole number");
+		rows[i] = static_cast<int>(f);
+	}
+	std::vector<size_t> out = ids_shape;
+	out.push_back(D);
+	Tensor y = Tensor::empty(out);
+	std::shared_ptr<Block> rb = side_buffer(rows.size() * sizeof(int));
+	if (!rows.empty()) {
+		check_hip(hipMemcpyAsync(rb->p, rows.data(), rows.size() * sizeof(int), hipMemcpyHostToDevice, g_stream),
+		          "copy in");
+		synchronize();  // rows is released on return
+	}
+	const size_t count = rows.size();
+	check(nnh_embedding_forward(weight.data().data(), V, D, static_cast<const int*>(rb->p), count, y.data(), g_stream));
+	return Value::node(std::move(y), {weight}, [weight, rb, count, V, D](const Tensor& g) {
+		// ops.cpp:2008-2014: weight.grad() (zeroed when fresh) gets the rows added in token order
+		bool first = false;
+		float* dw = grad_if(weight, first);
+		if (dw) check(nnh_embedding_backward(g.data(), static_cast<const int*>(rb->p), count, V, D, dw, first, g_stream));
+	});
+}
+
+Value embedding(const Value& weight, const Tensor& ids) {
+	return embedding(weight, ids.to_host(), ids.shape());
+}
+
+Tensor sinusoidal_table(size_t max_len, size_t dim) {
+	// positional.cpp:15-25: angle = pos / 10000^((c - c % 2) / dim) in double; sin on even columns, cos on odd
+	std::vector<float> t(max_len * dim);
+	for (size_t pos = 0; pos < max_len; ++pos)
+		for (size_t c = 0; c < dim; ++c) {
+			const double angle = static_cast<double>(pos) /
+			                     std::pow(10000.0, static_cast<double>(c - c % 2) / static_cast<double>(dim));
+			t[pos * dim + c] = static_cast<float>(c % 2 == 0 ? std::sin(angle) : std::cos(angle));
+		}
+	Tensor out = Tensor::from_host({max_len, dim}, t.data());
+	synchronize();  // t is released on return
+	return out;
+}
+
 }  // namespace hip
 }  // namespace nn

@@ -432,6 +432,7 @@ class Reference:
         L.nnref_layernorm.argtypes = [_f, _sz, _sz, _f, _f, C.c_float, _f, _f, C.c_int, _f, _f, _f]
         L.nnref_gelu.argtypes = [_f, _sz, _f, _f, C.c_int, _f]
         L.nnref_embedding.argtypes = [_f, _sz, _sz, _f, _sz, _f, _f, C.c_int, _f]
+        L.nnref_transformer_tiny_layout.argtypes = [_szp, _sz, _szp]
         L.nnref_time_batchnorm.argtypes = [_f, _sz, _sz, _sz, _f, _f, C.c_float, C.c_int, _f, C.c_int, C.c_int,
                                            C.c_double, _d, C.POINTER(C.c_int), _d, _f, _f]
         L.nnref_time_layernorm.argtypes = [_f, _sz, _sz, _f, _f, C.c_float, _f, C.c_int, C.c_int, C.c_double, _d,
@@ -637,6 +638,18 @@ class Reference:
                                       _fp(np.ascontiguousarray(g, np.float32)) if g is not None else None, int(repeats),
                                       _fp(dw))
         return rc, (y if rc == 0 else None), (dw if g is not None and rc == 0 else None)
+
+    def transformer_tiny_layout(self):
+        """[(shape, starts_at_ones)] of nn-cpp's Transformer{64, 64, 4, 2, 64} parameters, in parameters() order."""
+        buf = (C.c_size_t * 512)()
+        n = C.c_size_t()
+        assert self.lib.nnref_transformer_tiny_layout(buf, 512, C.byref(n)) == 0
+        out, i = [], 0
+        for _ in range(n.value):
+            r = buf[i]
+            out.append((tuple(buf[i + 1:i + 1 + r]), bool(buf[i + 1 + r])))
+            i += r + 2
+        return out
 
     # ---- timing (the CPU baseline): nn-cpp's own ops on buffers built once, apps/bench/runner.cpp's method ----
     # Each returns (times_ms, outputs): the timed runs after `warmup` untimed ones (at least one run, at most

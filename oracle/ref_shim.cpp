@@ -18,6 +18,7 @@
 #include "nn/nn/linear.hpp"
 #include "nn/nn/pool2d.hpp"
 #include "nn/nn/sequential.hpp"
+#include "nn/nn/transformer.hpp"
 #include "nn/random.hpp"
 #include "nn/kernels/parallel.hpp"
 #include "nn/tensor.hpp"
@@ -701,19 +702,58 @@ int nnref_time_layernorm(const float* x, size_t R, size_t D, const float* gm, co
 	return runs;
 }
 
+// transformer_tiny's parameters as nn-cpp's Transformer{64, 64, 4, 2, 64} holds them, in parameters() order: for
+// each, its rank, its dimensions, and 1 when it starts at all ones (else 0). Writes at most cap values; *count
+// receives the number of parameters.
+int nnref_transformer_tiny_layout(size_t* out, size_t cap, size_t* count) {
+	return guard([&] {
+		nn::Transformer tf(nn::TransformerConfig{64, 64, 4, 2, 64});
+		const std::vector<Value> ps = tf.parameters();
+		*count = ps.size();
+		size_t n = 0;
+		auto push = [&](size_t v) {
+			if (n < cap) out[n] = v;
+			++n;
+		};
+		for (const Value& p : ps) {
+			const nn::Tensor& t = p.data();
+			push(t.ndim());
+			for (size_t d : t.shape()) push(d);
+			bool ones = true;
+			for (float v : t.data()) ones = ones && v == 1.0f;
+			push(ones ? 1 : 0);
+		}
+		if (n > cap) throw std::invalid_argument("layout buffer too small");
+	});
+}
+
 // nn-cpp's side of the bench models' training step (the counterpart of nn-cpp_amd/src/bench/workloads.cpp, with
 // apps/bench/runner.cpp:33-45's clock points): the forward pass, then zero_grad and the backward pass from the
-// logits' gradient g; no loss, no optimizer step.
+// logits' gradient g; no loss, no optimizer step. Model 2 is transformer_tiny: nn-cpp's own Transformer module
+// (apps/bench/workloads.cpp:80-92) with the given parameters copied in, its {N, T, V} logits flattened as
+// FlatTransformer does. grads (optional) receives each parameter's gradient of the last step.
 int nnref_time_workload_step(int model, const float* x, size_t N, const float* const* params, const float* g,
-		int warmup, int runs, double* fwd_ms, double* bwd_ms, float* logits) {
+		int warmup, int runs, double* fwd_ms, double* bwd_ms, float* logits, float* const* grads) {
 	return guard([&] {
 		static const std::vector<std::vector<size_t>> mlp = {{1024, 784}, {1024}, {1024, 1024}, {1024}, {10, 1024}, {10}};
 		static const std::vector<std::vector<size_t>> cnn = {{8, 1, 3, 3}, {8}, {16, 8, 3, 3}, {16}, {128, 784}, {128},
 			{10, 128}, {10}};
-		const auto& shapes = model == 0 ? mlp : cnn;
 		std::vector<Value> p;
-		for (size_t i = 0; i < shapes.size(); ++i) p.push_back(Value::leaf(make(params[i], shapes[i]), true));
-		const Value xv = Value::leaf(make(x, model == 0 ? std::vector<size_t>{N, 784} : std::vector<size_t>{N, 1, 28, 28}));
+		std::unique_ptr<nn::Transformer> tf;
+		if (model == 2) {
+			tf = std::make_unique<nn::Transformer>(nn::TransformerConfig{64, 64, 4, 2, 64});
+			p = tf->parameters();
+			for (size_t i = 0; i < p.size(); ++i) {
+				nn::Tensor& t = p[i].data();
+				std::memcpy(t.data().data(), params[i], t.size() * sizeof(float));
+			}
+		} else {
+			const auto& shapes = model == 0 ? mlp : cnn;
+			for (size_t i = 0; i < shapes.size(); ++i) p.push_back(Value::leaf(make(params[i], shapes[i]), true));
+		}
+		const std::vector<size_t> xs = model == 0 ? std::vector<size_t>{N, 784}
+			: model == 2 ? std::vector<size_t>{N, 64} : std::vector<size_t>{N, 1, 28, 28};
+		const Value xv = Value::leaf(make(x, xs));
 		for (int i = 0; i < warmup + runs; ++i) {
 			const auto t0 = Clock::now();
 			Value y = Value::leaf(Tensor::empty({0}));
@@ -721,6 +761,10 @@ int nnref_time_workload_step(int model, const float* x, size_t N, const float* c
 				Value h = nn::relu(nn::linear(xv, p[0], p[1]));
 				h = nn::relu(nn::linear(h, p[2], p[3]));
 				y = nn::linear(h, p[4], p[5]);
+			} else if (model == 2) {
+				const Value o = tf->forward(xv);
+				const std::vector<size_t>& os = o.data().shape();
+				y = nn::reshape(o, {os[0] * os[1], os[2]});
 			} else {
 				Value h = nn::maxpool2d(nn::conv2d_relu(xv, p[0], p[1], 1, 1), 2, 2);
 				h = nn::maxpool2d(nn::conv2d_relu(h, p[2], p[3], 1, 1), 2, 2);
@@ -735,7 +779,12 @@ int nnref_time_workload_step(int model, const float* x, size_t N, const float* c
 				fwd_ms[i - warmup] = std::chrono::duration<double, std::milli>(t1 - t0).count();
 				bwd_ms[i - warmup] = std::chrono::duration<double, std::milli>(t2 - t1).count();
 			}
-			if (i + 1 == warmup + runs) put(y.data(), logits);
+			if (i + 1 == warmup + runs) {
+				if (logits) put(y.data(), logits);
+				if (grads)
+					for (size_t j = 0; j < p.size(); ++j)
+						if (grads[j]) put(p[j].grad(), grads[j]);
+			}
 		}
 	});
 }

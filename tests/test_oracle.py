@@ -716,3 +716,33 @@ def test_embedding_matches_nncpp(oracle, ref):
     assert oracle.embedding_backward(g, rows, 64, 32, dw, False).tobytes() == dw2r.tobytes()
     for bad in (1.5, 64.0, -1.0):
         assert ref.embedding(w, np.array([bad], np.float32))[0] == 2
+
+
+# ---------------------------------------------------------------- transformer_tiny workload definition
+
+def test_transformer_tiny_layout_matches_nncpp(ref):
+    """The GPU harness's parameter list (nnh/workloads.py, nn-cpp_amd/src/bench/workloads.cpp) is nn-cpp's
+    Transformer{vocab 64, dim 64, heads 4, layers 2, max_len 64}: the same shapes in the same order, and the gammas
+    that reseed_parameters keeps at one are exactly the parameters that start at one."""
+    from nnh import workloads as wl
+    w = wl.by_name("transformer_tiny")
+    layout = ref.transformer_tiny_layout()
+    assert [s for s, _ in layout] == [tuple(s) for s in w.shapes]
+    assert [i for i, (s, ones) in enumerate(layout) if ones and len(s) < 2] == list(w.ones)
+
+
+def test_transformer_tiny_ids_and_reference_step(ref):
+    """make_transformer_tiny's ids are std::uniform_int_distribution<int>(0, 63) over std::mt19937(seed + 1): here the
+    top six bits of each draw, every id a whole number in [0, 64) with all 64 present; nn-cpp's own training step on
+    them runs, is deterministic, and gives finite logits and gradients."""
+    from nnh import workloads as wl
+    w = wl.by_name("transformer_tiny")
+    params, x, g = wl.inputs(w, 1)
+    assert x.shape == (16, 64) and np.all(x == np.floor(x)) and x.min() == 0 and x.max() == 63
+    assert len(np.unique(x)) == 64
+    assert all(np.all(params[i] == 1) for i in w.ones)
+    runs = [wl.run_step(ref.lib.nnref_time_workload_step, w, params, x, g, 0, 1, want_grads=True) for _ in range(2)]
+    for rc, _, _, logits, grads in runs:
+        assert rc == 0 and np.all(np.isfinite(logits)) and all(np.all(np.isfinite(a)) for a in grads)
+    assert runs[0][3].tobytes() == runs[1][3].tobytes()
+    assert all(a.tobytes() == b.tobytes() for a, b in zip(runs[0][4], runs[1][4]))
