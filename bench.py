@@ -900,6 +900,8 @@ def main():
     ap.add_argument("--row", default=None, metavar="KEY", help="time one configuration row only (its key, e.g. "
                     "conv1_forward, or matmul512_nt_split in the split-depth mode) and print its JSON: the command "
                     "the per-kernel profiles under profiles/ are taken with")
+    ap.add_argument("--workloads", action="store_true", help="only nn-cpp's bench models' training steps (GPU and "
+                    "nn-cpp CPU), one JSON line")
     ap.add_argument("--floor", action="store_true", help="launch-cost floor of this GPU: empty kernel, fills, copies")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="only run 5 device-to-device copies of MIB MiB (calibrates rocprofv3 FETCH_SIZE/WRITE_SIZE)")
@@ -913,6 +915,13 @@ def main():
         return
     if args.floor:
         floor()
+        return
+    if args.workloads:
+        import torch  # noqa: F401 (torch's HIP runtime first, as everywhere else)
+        res = run_workloads(with_cpu=not args.no_cpu_baseline)
+        print(json.dumps({"workloads": [{k: ({kk: (round(vv, 4) if isinstance(vv, float) else vv)
+                                                for kk, vv in v.items()} if isinstance(v, dict) else v)
+                                           for k, v in w.items()} for w in res]}), flush=True)
         return
     if args.row:
         import torch  # noqa: F401 (torch's HIP runtime first, as everywhere else; libnnh then shares it)

@@ -102,26 +102,61 @@ __global__ void __launch_bounds__(256) embedding_forward_kernel(const float* __r
 }
 
 // ops.cpp:2008-2014: the gradient table (first: zeros) gets, for i in order, the output gradient's row i added to
-// row rows[i]. Gather form: a thread per table element walks the rows in order (staged through LDS) and adds the
-// gradients of the tokens that picked its row, so the additions keep the reference's order with no atomics.
+// row rows[i]. Gather form, no atomics: a wave owns one table row and 64 of its columns (a lane per column). The
+// workgroup stages 1024 ids at a time in LDS; a wave tests 256 of them per window (four ballots), then walks the
+// matches in token order eight at a time: eight independent loads of the gradient rows, then eight ordered adds, so
+// a window costs one load latency instead of one per token.
+constexpr int kEmbIds = 1024, kEmbBatch = 8;
+
 __global__ void __launch_bounds__(256) embedding_backward_kernel(const float* __restrict__ g, const int* __restrict__ rows,
                                                                  int64_t count, int64_t V, int64_t D,
                                                                  float* __restrict__ dw, int first) {
-	__shared__ int ids[1024];
-	const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
-	const bool here = e < V * D;
-	const int64_t v = here ? e / D : 0, d = here ? e - v * D : 0;
-	float acc = (first || !here) ? 0.0f : dw[e];
-	for (int64_t i0 = 0; i0 < count; i0 += 1024) {
-		const int n = (int)min<int64_t>(1024, count - i0);
+	__shared__ int ids[kEmbIds];
+	const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+	const int64_t dchunks = (D + 63) / 64;
+	const int64_t item = (int64_t)blockIdx.x * 4 + wave;  // (row, 64-column chunk)
+	const bool here = item < V * dchunks;                  // wave-uniform
+	const int64_t v = here ? item / dchunks : 0;
+	const int64_t d = (here ? item - v * dchunks : 0) * 64 + lane;
+	const bool on = here && d < D;
+	float acc = (first || !on) ? 0.0f : dw[v * D + d];
+	for (int64_t i0 = 0; i0 < count; i0 += kEmbIds) {
+		const int n = (int)min<int64_t>(kEmbIds, count - i0);
 		__syncthreads();
 		for (int t = threadIdx.x; t < n; t += 256) ids[t] = rows[i0 + t];
 		__syncthreads();
-		if (here)
-			for (int t = 0; t < n; ++t)
-				if (ids[t] == v) acc = acc + g[(i0 + t) * D + d];
+		if (!here) continue;
+		for (int w0 = 0; w0 < n; w0 += 256) {
+			uint64_t mk[4];
+#pragma unroll
+			for (int q = 0; q < 4; ++q) {
+				const int t = w0 + q * 64 + lane;
+				mk[q] = __ballot(t < n && ids[t] == (int)v);
+			}
+			int qi = 0;
+			while (true) {
+				int tk[kEmbBatch];
+#pragma unroll
+				for (int j = 0; j < kEmbBatch; ++j) {
+					while (qi < 4 && !mk[qi]) ++qi;
+					if (qi < 4) {
+						tk[j] = w0 + qi * 64 + __builtin_ctzll(mk[qi]);
+						mk[qi] &= mk[qi] - 1;
+					} else {
+						tk[j] = -1;
+					}
+				}
+				if (tk[0] < 0) break;
+				float x[kEmbBatch];
+#pragma unroll
+				for (int j = 0; j < kEmbBatch; ++j)  // a clamped address for empty slots and idle lanes: no branch
+					x[j] = g[(tk[j] >= 0 && on) ? (i0 + tk[j]) * D + d : 0];
+#pragma unroll
+				for (int j = 0; j < kEmbBatch; ++j) acc = tk[j] >= 0 ? acc + x[j] : acc;
+			}
+		}
 	}
-	if (here) dw[e] = acc;
+	if (on) dw[v * D + d] = acc;
 }
 
 inline unsigned blocks_of(int64_t n) { return (unsigned)((n + 255) / 256); }
@@ -164,8 +199,9 @@ hipError_t embedding_forward(const float* w, int64_t V, int64_t D, const int* ro
 hipError_t embedding_backward(const float* g, const int* rows, int64_t count, int64_t V, int64_t D, float* dw, int first,
                               hipStream_t s) {
 	if (V * D == 0) return hipSuccess;
-	hipLaunchKernelGGL(embedding_backward_kernel, dim3(blocks_of(V * D)), dim3(256), 0, s, g, rows, count, V, D, dw,
-	                   first);
+	const int64_t waves = V * ((D + 63) / 64);
+	hipLaunchKernelGGL(embedding_backward_kernel, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, s, g, rows, count, V,
+	                   D, dw, first);
 	return hipGetLastError();
 }
 

@@ -67,6 +67,8 @@ int nnh_embedding_backward(const float* g, const int* rows, size_t count, size_t
 	if (!count_ok({V, D}, tab) || !count_ok({count, D}))
 		return fail(NNH_ERR_INVALID, "embedding backward: size out of range (above 2^60 elements)");
 	if (tab == 0) return NNH_OK;
+	if ((uint64_t)V * ((D + 63) / 64) / 4 >= ((uint64_t)1 << 31))  // a wave per row and 64 columns, four to a block
+		return fail(NNH_ERR_INVALID, "embedding backward: too many table rows for the grid");
 	if (!dweight || (count > 0 && D > 0 && (!g || !rows))) return fail(NNH_ERR_INVALID, "embedding backward: null pointer");
 	if (ranges_overlap(dweight, tab * 4, g, (uint64_t)count * D * 4) ||
 	    ranges_overlap(dweight, tab * 4, rows, (uint64_t)count * 4))

@@ -112,7 +112,8 @@ def test_add_rejects_overlaps(gpu):
 
 
 @pytest.mark.parametrize("V,D,count,offset", [(64, 64, 512, 0), (64, 64, 4096, 0), (5, 3, 2500, 1), (1, 8, 10, 0),
-                                              (1000, 1, 3000, 0), (64, 64, 0, 0)])
+                                              (1000, 1, 3000, 0), (64, 64, 0, 0), (7, 130, 2000, 0), (3, 64, 1500, 1),
+                                              (2, 200, 1025, 0)])
 def test_embedding_bitwise(gpu, oracle, V, D, count, offset):
     import torch
 
@@ -150,3 +151,22 @@ def test_embedding_errors(gpu):
         nnh.check(L.nnh_embedding_forward(nnh._ptr(t), 0, 4, nnh._ptr(r), 4, nnh._ptr(t), nnh._stream(None)))
     with pytest.raises(nnh.NnhError):  # y over the table
         nnh.check(L.nnh_embedding_forward(nnh._ptr(t), 4, 4, nnh._ptr(r), 2, nnh._ptr(t, 8), nnh._stream(None)))
+
+
+def test_embedding_backward_keeps_negative_zero(gpu, oracle):
+    """Added to an existing gradient of -0 with gradients of -0, every entry stays -0: tokens of other rows add
+    nothing (not even +0)."""
+    import torch
+
+    import nnh
+    L = nnh.lib()
+    V, D, count = 6, 70, 700
+    rows = np.random.default_rng(3).integers(0, V - 1, count).astype(np.int32)  # the last row gets no token
+    g = np.full((count, D), -0.0, np.float32)
+    old = np.full((V, D), -0.0, np.float32)
+    gd, rd, dw = dev(g), dev(rows), dev(old)
+    nnh.check(L.nnh_embedding_backward(nnh._ptr(gd), nnh._ptr(rd), count, V, D, nnh._ptr(dw), 0, nnh._stream(None)))
+    torch.cuda.synchronize()
+    want = oracle.embedding_backward(g, rows, V, D, old, False)
+    assert np.all(np.signbit(want))
+    assert_same(dw.cpu().numpy().reshape(V, D), want, "embedding dw of -0")
