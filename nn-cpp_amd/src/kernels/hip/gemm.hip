@@ -201,6 +201,9 @@ const char* gemm_config_name(int config) {
 	if (config == kNumConfigs + kValu1x2) return "valu 16x32 (1x2 chains per lane)";
 	if (config == kNumConfigs + kValu2x4) return "valu 32x64 (2x4 chains per lane)";
 	if (config == kNumConfigs + kValu1x4) return "valu 16x64 (1x4 chains per lane)";
+	if (config == kNumConfigs + kValuBc1) return "valu bcast 16x16 (1 chain per lane, A by DPP)";
+	if (config == kNumConfigs + kValuBc2) return "valu bcast 32x16 (2 chains per lane, A by DPP)";
+
 	return (config >= 0 && config < kNumConfigs) ? configs()[config].name : "";
 }
 

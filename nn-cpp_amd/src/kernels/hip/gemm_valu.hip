@@ -13,8 +13,11 @@
 //   * The accumulate rule, the epilogue and the edges are the MFMA kernel's: old C joins after the first 256 steps
 //     (Store::kAdd, gemm.cpp:245-252), then bias, ReLU and the alive flags; only the m x n window is written.
 // Every chain has exactly k steps (a partial last chunk runs element by element), so -0 results stay -0.
+// A second kernel below (sgemm_valu_bc_kernel) feeds op(A) through registers and DPP row broadcasts instead of LDS.
 // The caller sends here only products without a depth cut.
 #include "gemm_valu.hpp"
+
+#include <utility>
 
 namespace nnh {
 
@@ -227,6 +230,175 @@ __global__ void __launch_bounds__(256) sgemm_valu_kernel(const GemmArgs p) {
 	}
 }
 
+// ---- the row-broadcast variant: op(A) through registers and DPP, only op(B) through LDS ----
+//
+// The kernel above reads RM + RN LDS words per lane for RM * RN fmas, and the LDS is what binds it. Here a lane
+// (q, c) = (lane >> 4, lane & 15) of wave w owns RM chains: rows m0 + 4 RM w + 4 i + q (i < RM) of op(A) and column
+// n0 + c. op(A) never enters LDS: for each block of 16 depth steps, lane (q, j) holds op(A)[row(q, i)][k0 + j] in
+// register a[i] (one dword load per lane and chain), and the fma of step j takes it from lane j of the lane's
+// 16-lane row by a DPP row broadcast inside the instruction (v_fmac_f32_dpp ... row_newbcast:j). op(B)'s 16 columns
+// of a 256-deep chunk sit in LDS, shared by the four waves; a lane reads its column's 16 values of a block as four
+// 16-byte words, so a depth step costs one 4-byte LDS word per lane against RM fmas. A DPP read of a register
+// written by a VALU instruction less than two cycles before is a hazard, so the first broadcast fma of each chain
+// in a block is preceded by s_nop 1 in the same asm statement (the registers are loaded from memory, or at most
+// copied between chunks). The last partial block (k not a multiple of 16) takes its values by ds_bpermute
+// (__shfl) instead. Every chain runs exactly k steps, in depth order, from +0.
+
+template <int J, bool FIRST>
+__device__ __forceinline__ void fmac_bcast(float& acc, float a, float b) {
+	if (FIRST)
+		asm("s_nop 1\n\tv_fmac_f32_dpp %0, %1, %2 row_newbcast:%3 row_mask:0xf bank_mask:0xf"
+		    : "+v"(acc)
+		    : "v"(a), "v"(b), "i"(J));
+	else
+		asm("v_fmac_f32_dpp %0, %1, %2 row_newbcast:%3 row_mask:0xf bank_mask:0xf" : "+v"(acc) : "v"(a), "v"(b), "i"(J));
+}
+
+template <int RM, int... J>
+__device__ __forceinline__ void bcast_block(float (&acc)[RM], const float (&a)[RM], const float (&b)[16],
+                                            std::integer_sequence<int, J...>) {
+	(
+	    [&] {
+#pragma unroll
+		    for (int i = 0; i < RM; ++i) fmac_bcast<J, J == 0>(acc[i], a[i], b[J]);
+	    }(),
+	    ...);
+}
+
+constexpr int kBcVc = 256;           // depth per LDS chunk
+constexpr int kBcVp = kBcVc + 4;     // pitch: 16-byte reads of the 16 columns hit distinct banks
+
+template <bool TA, bool TB, int RM, bool VEC>
+__global__ void __launch_bounds__(256) sgemm_valu_bc_kernel(const GemmArgs p) {
+	constexpr int BN = 16, kBlocks = kBcVc / 16;
+	using LB = ChunkLoader<BN, TB, VEC, kBcVc>;
+	__shared__ __align__(16) float lds[2 * BN * kBcVp];
+	const int tid = threadIdx.x, lane = tid & 63;
+	const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+	const int q = lane >> 4, c = lane & 15;
+	const int tiles = p.tiles_m * p.tiles_n;
+	const int t = blockIdx.x % tiles, bi = blockIdx.x / tiles;
+	const int tm = t / p.tiles_n, tn = t - tm * p.tiles_n;
+	const int m0 = tm * 16 * RM, n0 = tn * BN;
+	int64_t oa = 0, ob = 0, oc = 0;
+	if (p.batch.ndim > 0) batch_offsets(p.batch, bi, oa, ob, oc);
+	const float* __restrict__ A = p.a + oa;
+	const float* __restrict__ B = p.b + ob;
+	const int rbase = m0 + wave * 4 * RM;
+	const int K = p.k;
+
+	float acc[RM];
+#pragma unroll
+	for (int i = 0; i < RM; ++i) acc[i] = 0.0f;
+
+	// op(A) of one chunk: a[b][i] = op(A)[row(q, i)][chunk k0 + 16 b + c], addresses clamped into the matrix
+	auto aload = [&](int ch, float (&a)[kBlocks][RM]) {
+#pragma unroll
+		for (int b = 0; b < kBlocks; ++b)
+#pragma unroll
+			for (int i = 0; i < RM; ++i) {
+				const int64_t row = min(rbase + 4 * i + q, p.m - 1);
+				const int64_t kk = min(ch * kBcVc + 16 * b + c, K - 1);
+				a[b][i] = TA ? A[kk * p.lda + row] : A[row * p.lda + kk];
+			}
+	};
+	f32x4 rb[LB::kPer];
+	float ac[kBlocks][RM], an[kBlocks][RM];
+	const int nch = (K + kBcVc - 1) / kBcVc;
+	const bool acc_mode = p.accumulate != 0;
+	auto add_old = [&]() {
+		const int col = n0 + c;
+#pragma unroll
+		for (int i = 0; i < RM; ++i) {
+			const int row = rbase + 4 * i + q;
+			if (row < p.m && col < p.n) acc[i] = p.c[oc + (int64_t)row * p.ldc + col] + acc[i];
+		}
+	};
+
+	aload(0, ac);
+	LB::load(B, p.ldb, n0, p.n, 0, K, rb, tid);
+	LB::store(lds, rb, tid);
+	__syncthreads();
+	for (int ch = 0; ch < nch; ++ch) {
+		if (ch + 1 < nch) {
+			aload(ch + 1, an);
+			LB::load(B, p.ldb, n0, p.n, (ch + 1) * kBcVc, K, rb, tid);
+		}
+		const float* Bs = lds + (ch & 1) * BN * kBcVp + c * kBcVp;
+		const int kc = __builtin_amdgcn_readfirstlane(min(kBcVc, K - ch * kBcVc));
+		auto bread = [&](int b, float (&bv)[16]) {
+#pragma unroll
+			for (int u = 0; u < 4; ++u) {
+				const f32x4 w = *reinterpret_cast<const f32x4*>(Bs + 16 * b + 4 * u);
+				bv[4 * u] = w[0];
+				bv[4 * u + 1] = w[1];
+				bv[4 * u + 2] = w[2];
+				bv[4 * u + 3] = w[3];
+			}
+		};
+		if (kc == kBcVc) {
+			// a whole chunk, straight-line: the next block's LDS words are in flight during this block's fmas
+			float bv0[16], bv1[16];
+			bread(0, bv0);
+#pragma unroll
+			for (int b = 0; b < kBlocks; b += 2) {
+				bread(b + 1, bv1);
+				bcast_block<RM>(acc, ac[b], bv0, std::make_integer_sequence<int, 16>{});
+				if (b + 2 < kBlocks) bread(b + 2, bv0);
+				bcast_block<RM>(acc, ac[b + 1], bv1, std::make_integer_sequence<int, 16>{});
+			}
+		} else {
+			const int nb = kc / 16, rem = kc % 16;
+#pragma unroll
+			for (int b = 0; b < kBlocks; ++b) {
+				if (b < nb) {
+					float bv[16];
+					bread(b, bv);
+					bcast_block<RM>(acc, ac[b], bv, std::make_integer_sequence<int, 16>{});
+				} else if (b == nb && rem) {
+					for (int j = 0; j < rem; ++j) {
+						const float bj = Bs[16 * b + j];
+#pragma unroll
+						for (int i = 0; i < RM; ++i)
+							acc[i] = __builtin_fmaf(__shfl(ac[b][i], (lane & 48) | j), bj, acc[i]);
+					}
+				}
+			}
+		}
+		if (ch == kAccAfter / kBcVc - 1 && acc_mode && K > kAccAfter) add_old();
+		if (ch + 1 < nch) LB::store(lds + ((ch + 1) & 1) * BN * kBcVp, rb, tid);
+		__syncthreads();
+		if (ch + 1 < nch) {
+#pragma unroll
+			for (int b = 0; b < kBlocks; ++b)
+#pragma unroll
+				for (int i = 0; i < RM; ++i) ac[b][i] = an[b][i];
+		}
+	}
+
+	const bool add_old_at_end = acc_mode && K <= kAccAfter;
+	float* __restrict__ Cp = p.c + oc;
+	unsigned char* alive = p.ep.alive ? p.ep.alive + oc : nullptr;
+	const int col = n0 + c;
+	if (col >= p.n) return;
+#pragma unroll
+	for (int i = 0; i < RM; ++i) {
+		const int row = rbase + 4 * i + q;
+		if (row >= p.m) continue;
+		const int64_t off = (int64_t)row * p.ldc + col;
+		float v = acc[i];
+		if (add_old_at_end) v = Cp[off] + v;
+		if (p.ep.bias_mode == kBiasCol) v = v + p.ep.bias[col];
+		else if (p.ep.bias_mode == kBiasRow) v = v + p.ep.bias[row];
+		if (p.ep.relu) {
+			const bool on = v > 0.0f;
+			if (alive) alive[off] = on ? 1 : 0;
+			v = on ? v : 0.0f;
+		}
+		Cp[off] = v;
+	}
+}
+
 typedef void (*ValuFn)(const GemmArgs);
 
 template <int RM, int RN, bool VEC, int VC>
@@ -237,11 +409,20 @@ ValuFn valu_fn(int ta, int tb) {
 	return sgemm_valu_kernel<true, true, RM, RN, VEC, VC>;
 }
 
+template <int RM, bool VEC>
+ValuFn valu_bc_fn(int ta, int tb) {
+	if (!ta && !tb) return sgemm_valu_bc_kernel<false, false, RM, VEC>;
+	if (!ta && tb) return sgemm_valu_bc_kernel<false, true, RM, VEC>;
+	if (ta && !tb) return sgemm_valu_bc_kernel<true, false, RM, VEC>;
+	return sgemm_valu_bc_kernel<true, true, RM, VEC>;
+}
+
 struct ValuShape {
-	int rm, rn, vc;
+	int rm, rn, vc;  // rn 0: the row-broadcast kernel (tile 16 rm x 16)
 };
-// kValu2x2, kValu1x2, kValu2x4, kValu1x4
-constexpr ValuShape kShapes[kValuShapes] = {{2, 2, 256}, {1, 2, 256}, {2, 4, 128}, {1, 4, 128}};
+// kValu2x2, kValu1x2, kValu2x4, kValu1x4, kValuBc1, kValuBc2
+constexpr ValuShape kShapes[kValuShapes] = {{2, 2, 256}, {1, 2, 256}, {2, 4, 128}, {1, 4, 128}, {1, 0, kBcVc},
+                                            {2, 0, kBcVc}};
 
 template <bool VEC>
 ValuFn valu_pick(int shape, int ta, int tb) {
@@ -249,27 +430,38 @@ ValuFn valu_pick(int shape, int ta, int tb) {
 	case kValu2x2: return valu_fn<2, 2, VEC, 256>(ta, tb);
 	case kValu1x2: return valu_fn<1, 2, VEC, 256>(ta, tb);
 	case kValu2x4: return valu_fn<2, 4, VEC, 128>(ta, tb);
-	default: return valu_fn<1, 4, VEC, 128>(ta, tb);
+	case kValu1x4: return valu_fn<1, 4, VEC, 128>(ta, tb);
+	case kValuBc1: return valu_bc_fn<1, VEC>(ta, tb);
+	default: return valu_bc_fn<2, VEC>(ta, tb);
 	}
 }
 
 }  // namespace
 
 int valu_shape(const GemmCall& g) {
-	(void)g;
-	return kValu1x2;
+	if (g.ta) return kValu1x2;
+	const double outputs = (double)g.m * (double)g.n * (double)g.batch_count;
+	return outputs <= 131072.0 ? kValuBc1 : kValuBc2;
 }
 
 bool valu_takes(const GemmCall& g) {
 	if (g.gather || g.rowsum || g.k <= 0 || g.m <= 0 || g.n <= 0) return false;
 	if (depth_cut(g.m, g.n, g.k)) return false;
 	if (g.m >= (1 << 30) || g.n >= (1 << 30) || g.k >= (1 << 30)) return false;
-	// Measured against the MFMA tiles (device time, one MI355X): the 1 x 2 lane block is faster up to 2^17 outputs
-	// with a depth of 256 or more (256 x 512 x 784 NT 11.2 against 14.3 us, 256 x 10 x 256 5.3 against 7.4,
-	// 256 x 512 x 256 NN 5.5 against 6.4) and slower from 2^18 (512^3: 14.3-15.1 against 9.2-10.8; 64 x 4096 x 4096:
-	// 94.5 against 60.1), where the MFMA tiles have enough chains to overlap and this kernel's LDS reads bind it.
+	// Measured against the MFMA tiles (device time, one MI355X, every configuration forced):
+	// * op(A) untransposed, the row-broadcast kernel: one chain per lane up to 2^17 outputs (256 x 512 x 784 NT 9.8
+	//   against 11.2 us for the 1 x 2 lane block and 14.3 for the best MFMA tile; 256 x 10 x 256 4.4 against 5.3;
+	//   256 x 512 x 256 NN 4.7 against 5.4), two chains per lane up to 2^18 outputs at depths up to 512 with op(B)
+	//   untransposed (512^3 NN 9.75 against 10.3, 256 x 784 x 512 NN 9.1 against 11.9; 512^3 NT 9.8 against the
+	//   MFMA tiles' 9.3); at 2^18 outputs and deeper it ties with the MFMA tiles (64 x 4096 x 4096: 58.6 against
+	//   59.8; 256 x 1024 x 1024 NT: 15.7 against 15.2), and from 2^20 they win (1024^3: 27 against 47).
+	// * op(A) transposed (its dword loads are strided), the 1 x 2 lane block, up to 2^17 outputs: slower than the
+	//   MFMA tiles from 2^18 (512^3 TN: 15.0 against 10.9), where they have enough chains to overlap their 44-cycle
+	//   steps and this kernel's LDS reads bind it.
 	const double outputs = (double)g.m * (double)g.n * (double)g.batch_count;
-	return outputs <= 131072.0 && g.k >= 256;
+	if (g.k < 256) return false;
+	if (g.ta) return outputs <= 131072.0;
+	return outputs <= 131072.0 || (outputs <= 262144.0 && g.k <= 512 && !g.tb);
 }
 
 hipError_t gemm_valu_launch(const GemmCall& g, int shape, hipStream_t s) {
@@ -297,11 +489,17 @@ hipError_t gemm_valu_launch(const GemmCall& g, int shape, hipStream_t s) {
 	p.vec_ok = vec_ok ? 1 : 0;
 	if (shape < 0 || shape >= kValuShapes) return hipErrorInvalidValue;
 	const int rm = kShapes[shape].rm, rn = kShapes[shape].rn, vc = kShapes[shape].vc;
-	p.tiles_m = (int)((g.m + 16 * rm - 1) / (16 * rm));
-	p.tiles_n = (int)((g.n + 16 * rn - 1) / (16 * rn));
+	const bool bc = rn == 0;
+	const int tile_m = 16 * rm, tile_n = bc ? 16 : 16 * rn;
+	p.tiles_m = (int)((g.m + tile_m - 1) / tile_m);
+	p.tiles_n = (int)((g.n + tile_n - 1) / tile_n);
 	const int64_t blocks = (int64_t)p.tiles_m * p.tiles_n * g.batch_count;
 	if (blocks > 0x7fffffff) return hipErrorInvalidConfiguration;
 	const ValuFn fn = vec_ok ? valu_pick<true>(shape, g.ta, g.tb) : valu_pick<false>(shape, g.ta, g.tb);
+	if (bc) {  // static LDS
+		hipLaunchKernelGGL(fn, dim3((unsigned)blocks), dim3(256), 0, s, p);
+		return hipGetLastError();
+	}
 	const size_t lds = (size_t)2 * (16 * rm + 16 * rn) * (vc + 4) * sizeof(float);
 	hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize,
 	                                   (int)lds);

@@ -11,10 +11,14 @@ constexpr int kValu2x2 = 0;
 constexpr int kValu1x2 = 1;
 constexpr int kValu2x4 = 2;
 constexpr int kValu1x4 = 3;
-constexpr int kValuShapes = 4;
+// The row-broadcast kernel (op(A) by DPP row broadcasts, only op(B) in LDS): RM chains per lane, tile 16 RM x 16.
+constexpr int kValuBc1 = 4;
+constexpr int kValuBc2 = 5;
+constexpr int kValuShapes = 6;
 
-// Whether the shape-based choice sends this product to the VALU kernel (no gather, no row sums, no depth cut, at
-// most 2^17 outputs and a depth of 256 or more), and which lane block it takes.
+// Whether the shape-based choice sends this product to a VALU kernel (no gather, no row sums, no depth cut, a depth
+// of 256 or more, at most 2^17 outputs, or 2^18 at depths up to 512 when neither operand is transposed), and which kernel
+// and lane block it takes.
 bool valu_takes(const GemmCall& g);
 int valu_shape(const GemmCall& g);
 // The launch (any product without gather, row sums or a depth cut; k > 0).

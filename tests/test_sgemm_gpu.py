@@ -174,7 +174,7 @@ def test_every_tile_configuration_gives_the_same_bits(gpu, oracle):
     n_cfg = len(nnh.gemm_configs())
     seed = 50000
     for (ta, tb, m, n, k, pad) in ((0, 0, 256, 256, 256, 0), (1, 1, 300, 200, 77, 1), (0, 1, 64, 512, 600, 0),
-                                   (1, 0, 512, 64, 2048, 0)):
+                                   (1, 0, 512, 64, 2048, 0), (1, 0, 70, 37, 529, 1), (0, 1, 33, 90, 16, 0)):
         p = Problem(ta, tb, m, n, k, pad, seed)
         seed += 1
         for acc in (0, 1):
