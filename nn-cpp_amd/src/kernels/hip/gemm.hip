@@ -223,6 +223,7 @@ hipError_t gemm_launch(const GemmCall& g, hipStream_t s, int config, float* work
 	if (g.gather && g.ta) return hipErrorInvalidValue;
 	if (g.rowsum && (depth_cut(g.m, g.n, g.k) || g.batch_count != 1 || g.gather || !g.ta || g.tb))
 		return hipErrorInvalidValue;
+	if (valu_pieces_takes(g)) return gemm_valu_pieces_launch(g, s);
 	if (pieces_kernel_takes(g)) return gemm_pieces_launch(g, s);
 	bool cut = false, interior = false;
 	GemmArgs p = make_args(g, cf, cut, interior);

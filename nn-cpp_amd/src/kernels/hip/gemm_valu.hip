@@ -399,6 +399,187 @@ __global__ void __launch_bounds__(256) sgemm_valu_bc_kernel(const GemmArgs p) {
 	}
 }
 
+// ---- cut products on the VALU: all pieces of an output in one lane ----
+//
+// A product with a depth cut is, per element, pieces of piece_k depth steps, each a chain from +0, added in piece
+// order, then the old C (gemm.cpp:453-485). Cut products are small (at most 2^16 outputs in nn-cpp's rule), and
+// their pieces are independent chains: a lane runs all NP of its output's pieces interleaved, so the latency of a
+// DPP-fed fma (about 17 cycles) hides behind the other chains. A workgroup owns 16 x 16 outputs (wave w, lane
+// (q, c): row m0 + 4 w + q, column n0 + c). op(A) comes by DPP row broadcasts as in the kernel above (one dword per
+// lane, piece and 16-step block, all loaded up front); op(B)'s 16 columns stay in LDS for the whole depth
+// (k-contiguous, pitch 4 mod 64 floats), staged once with every load in flight before the stores. A chain slot past
+// the last piece runs piece 0's addresses and is dropped; the last piece runs exactly its own (possibly shorter)
+// depth. The pieces are then added in order, the old C, bias and ReLU applied.
+
+constexpr int kPcMaxBlocks = 8;     // piece depth <= 128
+constexpr int kPcMaxK = 2048;       // op(B)'s 16 columns of the whole depth in LDS: <= 131 KB
+constexpr int kPcMaxPieces = 4;
+constexpr int kPcMaxOutputs = 1 << 16;
+
+inline int pc_pitch(int k) { return ((k + 63) / 64) * 64 + 4; }
+
+// four depth steps J0 .. J0 + 3 of a 16-step block, for every chain
+template <int NP, int J0, int... J>
+__device__ __forceinline__ void bcast_quad(float (&acc)[NP], const float (&a)[NP], const f32x4 (&b)[NP],
+                                           std::integer_sequence<int, J...>) {
+	(
+	    [&] {
+#pragma unroll
+		    for (int u = 0; u < NP; ++u) fmac_bcast<J0 + J, J0 + J == 0>(acc[u], a[u], b[u][J]);
+	    }(),
+	    ...);
+}
+
+template <bool TA, bool TB, int NP, bool VEC>
+__global__ void __launch_bounds__(256) sgemm_valu_pieces_kernel(const GemmArgs p) {
+	extern __shared__ __align__(16) float lds[];  // [16][pitch]: lds[cc * pitch + kk] = op(B)[kk][n0 + cc]
+	const int tid = threadIdx.x, lane = tid & 63;
+	const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+	const int q = lane >> 4, c = lane & 15;
+	const int tiles = p.tiles_m * p.tiles_n;
+	const int t = blockIdx.x % tiles, bi = blockIdx.x / tiles;
+	const int tm = t / p.tiles_n, tn = t - tm * p.tiles_n;
+	const int m0 = tm * 16, n0 = tn * 16;
+	int64_t oa = 0, ob = 0, oc = 0;
+	if (p.batch.ndim > 0) batch_offsets(p.batch, bi, oa, ob, oc);
+	const float* __restrict__ A = p.a + oa;
+	const float* __restrict__ B = p.b + ob;
+	const int K = p.k, P = p.pieces, pk = p.piece_k;
+	const int pitch = ((K + 63) / 64) * 64 + 4;
+	const int row = m0 + 4 * wave + q, col = n0 + c;
+	const int64_t rowc = min(row, p.m - 1);
+
+	int pce[NP], len[NP];  // the piece each chain slot runs (piece 0 for an empty slot) and its depth
+#pragma unroll
+	for (int u = 0; u < NP; ++u) {
+		pce[u] = u < P ? u : 0;
+		len[u] = u < P ? min(pk, K - u * pk) : pk;
+	}
+	float a[NP][kPcMaxBlocks];
+#pragma unroll
+	for (int u = 0; u < NP; ++u)
+#pragma unroll
+		for (int b = 0; b < kPcMaxBlocks; ++b) {
+			const int64_t kk = min(pce[u] * pk + 16 * b + c, K - 1);
+			a[u][b] = TA ? A[kk * p.lda + rowc] : A[rowc * p.lda + kk];
+		}
+
+	// op(B) into LDS, eight loads in flight per thread before their stores
+	if (VEC) {  // K (TB) or n (!TB) a multiple of 4, 16-byte rows
+		const int total = TB ? 16 * (K / 4) : K * 4;
+		for (int e0 = 0; e0 < total; e0 += 8 * 256) {
+			f32x4 v[8];
+#pragma unroll
+			for (int u = 0; u < 8; ++u) {
+				const int e = min(e0 + tid + 256 * u, total - 1);
+				if (TB) {
+					const int cc = e / (K / 4), k4 = 4 * (e - cc * (K / 4));
+					v[u] = *reinterpret_cast<const f32x4*>(B + (int64_t)min(n0 + cc, p.n - 1) * p.ldb + k4);
+				} else {
+					const int kk = e >> 2, c4 = 4 * (e & 3);
+					v[u] = *reinterpret_cast<const f32x4*>(B + (int64_t)kk * p.ldb + min(n0 + c4, p.n - 4));
+				}
+			}
+#pragma unroll
+			for (int u = 0; u < 8; ++u) {
+				const int e = e0 + tid + 256 * u;
+				if (e >= total) continue;
+				if (TB) {
+					const int cc = e / (K / 4), k4 = 4 * (e - cc * (K / 4));
+					*reinterpret_cast<f32x4*>(lds + cc * pitch + k4) = v[u];
+				} else {
+					const int kk = e >> 2, c4 = 4 * (e & 3);
+					// columns n0 + c4 .. + 3 came from min(n0 + c4, n - 4): shift back when clamped
+					const int sh = n0 + c4 - min(n0 + c4, p.n - 4);
+#pragma unroll
+					for (int x = 0; x < 4; ++x) lds[(c4 + x) * pitch + kk] = v[u][min(x + sh, 3)];
+				}
+			}
+		}
+	} else {
+		const int total = 16 * K;
+		for (int e0 = 0; e0 < total; e0 += 8 * 256) {
+			float v[8];
+#pragma unroll
+			for (int u = 0; u < 8; ++u) {
+				const int e = min(e0 + tid + 256 * u, total - 1);
+				int cc, kk;
+				if (TB) {
+					cc = e / K;
+					kk = e - cc * K;
+				} else {
+					kk = e >> 4;
+					cc = e & 15;
+				}
+				const int64_t gc = min(n0 + cc, p.n - 1);
+				v[u] = TB ? B[gc * p.ldb + kk] : B[(int64_t)kk * p.ldb + gc];
+			}
+#pragma unroll
+			for (int u = 0; u < 8; ++u) {
+				const int e = e0 + tid + 256 * u;
+				if (e >= total) continue;
+				const int cc = TB ? e / K : (e & 15), kk = TB ? e - (e / K) * K : (e >> 4);
+				lds[cc * pitch + kk] = v[u];
+			}
+		}
+	}
+	__syncthreads();
+
+	float acc[NP];
+#pragma unroll
+	for (int u = 0; u < NP; ++u) acc[u] = 0.0f;
+	const float* Bc = lds + c * pitch;
+#pragma unroll
+	for (int b = 0; b < kPcMaxBlocks; ++b) {
+		if (16 * b >= pk) break;
+		bool all_full = true;
+#pragma unroll
+		for (int u = 0; u < NP; ++u) all_full = all_full && 16 * (b + 1) <= len[u];
+		float av[NP];
+#pragma unroll
+		for (int u = 0; u < NP; ++u) av[u] = a[u][b];
+		if (all_full) {
+			f32x4 b0[NP], b1[NP];
+#pragma unroll
+			for (int u = 0; u < NP; ++u) b0[u] = *reinterpret_cast<const f32x4*>(Bc + pce[u] * pk + 16 * b);
+#pragma unroll
+			for (int u = 0; u < NP; ++u) b1[u] = *reinterpret_cast<const f32x4*>(Bc + pce[u] * pk + 16 * b + 4);
+			bcast_quad<NP, 0>(acc, av, b0, std::make_integer_sequence<int, 4>{});
+#pragma unroll
+			for (int u = 0; u < NP; ++u) b0[u] = *reinterpret_cast<const f32x4*>(Bc + pce[u] * pk + 16 * b + 8);
+			bcast_quad<NP, 4>(acc, av, b1, std::make_integer_sequence<int, 4>{});
+#pragma unroll
+			for (int u = 0; u < NP; ++u) b1[u] = *reinterpret_cast<const f32x4*>(Bc + pce[u] * pk + 16 * b + 12);
+			bcast_quad<NP, 8>(acc, av, b0, std::make_integer_sequence<int, 4>{});
+			bcast_quad<NP, 12>(acc, av, b1, std::make_integer_sequence<int, 4>{});
+		} else {
+			// the last piece ends inside this block or earlier: every chain on its own, by ds_bpermute
+#pragma unroll
+			for (int u = 0; u < NP; ++u) {
+				const int steps = min(16, len[u] - 16 * b);
+				const float* bp = Bc + pce[u] * pk + 16 * b;
+				for (int j = 0; j < steps; ++j) acc[u] = __builtin_fmaf(__shfl(av[u], (lane & 48) | j), bp[j], acc[u]);
+			}
+		}
+	}
+	if (row >= p.m || col >= p.n) return;
+	float v = acc[0];
+#pragma unroll
+	for (int u = 1; u < NP; ++u)
+		if (u < P) v = v + acc[u];
+	float* __restrict__ Cp = p.c + oc;
+	const int64_t off = (int64_t)row * p.ldc + col;
+	if (p.accumulate) v = Cp[off] + v;
+	if (p.ep.bias_mode == kBiasCol) v = v + p.ep.bias[col];
+	else if (p.ep.bias_mode == kBiasRow) v = v + p.ep.bias[row];
+	if (p.ep.relu) {
+		const bool on = v > 0.0f;
+		if (p.ep.alive) p.ep.alive[oc + off] = on ? 1 : 0;
+		v = on ? v : 0.0f;
+	}
+	Cp[off] = v;
+}
+
 typedef void (*ValuFn)(const GemmArgs);
 
 template <int RM, int RN, bool VEC, int VC>
@@ -501,6 +682,61 @@ hipError_t gemm_valu_launch(const GemmCall& g, int shape, hipStream_t s) {
 		return hipGetLastError();
 	}
 	const size_t lds = (size_t)2 * (16 * rm + 16 * rn) * (vc + 4) * sizeof(float);
+	hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize,
+	                                   (int)lds);
+	if (e != hipSuccess) return e;
+	hipLaunchKernelGGL(fn, dim3((unsigned)blocks), dim3(256), lds, s, p);
+	return hipGetLastError();
+}
+
+bool valu_pieces_takes(const GemmCall& g) {
+	// Measured against the MFMA pieces kernel (device time, one MI355X): config 2's 256 x 256 x 512 NT layer (four
+	// 128-deep pieces) is about 1 us faster here (the MLP forward 23.6 -> 22.5 us); with eight pieces per lane
+	// (transformer_tiny's 64 x 64 x 1024 weight gradients, the split mode's 256 x 10 x 256) or a transposed op(A)
+	// (strided dword loads) it was slower, so those stay on the MFMA kernel.
+	if (g.gather || g.rowsum || g.ta || g.m <= 0 || g.n <= 0 || g.k <= 0) return false;
+	if (g.m >= (1 << 30) || g.n >= (1 << 30) || g.k > kPcMaxK) return false;
+	const CutPlan plan = cut_plan(g.m, g.n, g.k);
+	if (plan.pieces < 2 || plan.pieces > kPcMaxPieces || plan.piece_k % 16 != 0 || plan.piece_k > 16 * kPcMaxBlocks)
+		return false;
+	return (double)g.m * (double)g.n * (double)g.batch_count <= (double)kPcMaxOutputs;
+}
+
+template <bool VEC>
+ValuFn valu_pieces_pick(int tb) {
+	return tb ? sgemm_valu_pieces_kernel<false, true, kPcMaxPieces, VEC>
+	          : sgemm_valu_pieces_kernel<false, false, kPcMaxPieces, VEC>;
+}
+
+hipError_t gemm_valu_pieces_launch(const GemmCall& g, hipStream_t s) {
+	if (!valu_pieces_takes(g)) return hipErrorInvalidValue;
+	const CutPlan plan = cut_plan(g.m, g.n, g.k);
+	GemmArgs p{};
+	p.a = g.a;
+	p.b = g.b;
+	p.c = g.c;
+	p.lda = g.lda;
+	p.ldb = g.ldb;
+	p.ldc = g.ldc;
+	p.m = (int)g.m;
+	p.n = (int)g.n;
+	p.k = (int)g.k;
+	p.accumulate = g.accumulate;
+	p.batch_count = (int)g.batch_count;
+	p.batch = g.batch;
+	p.ep = g.ep;
+	p.pieces = (int)plan.pieces;
+	p.piece_k = (int)plan.piece_k;
+	p.tiles_m = (int)((g.m + 15) / 16);
+	p.tiles_n = (int)((g.n + 15) / 16);
+	const int64_t blocks = (int64_t)p.tiles_m * p.tiles_n * g.batch_count;
+	if (blocks > 0x7fffffff) return hipErrorInvalidConfiguration;
+	// 16-byte staging of op(B): its contiguous extent (k for a transposed B, else n) a multiple of 4, ldb, the base
+	// and the batch strides 16-byte aligned
+	bool vec = g.ldb % 4 == 0 && reinterpret_cast<uintptr_t>(g.b) % 16 == 0 && (g.tb ? g.k : g.n) % 4 == 0;
+	for (int d = 0; d < g.batch.ndim; ++d) vec = vec && g.batch.sb[d] % 4 == 0;
+	const ValuFn fn = vec ? valu_pieces_pick<true>(g.tb) : valu_pieces_pick<false>(g.tb);
+	const size_t lds = (size_t)16 * pc_pitch(p.k) * sizeof(float);
 	hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize,
 	                                   (int)lds);
 	if (e != hipSuccess) return e;

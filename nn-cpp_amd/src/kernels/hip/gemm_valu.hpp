@@ -24,4 +24,9 @@ int valu_shape(const GemmCall& g);
 // The launch (any product without gather, row sums or a depth cut; k > 0).
 hipError_t gemm_valu_launch(const GemmCall& g, int shape, hipStream_t s);
 
+// Cut products (nn-cpp's depth cut, or the split-depth mode's) with op(A) untransposed, at most 4 pieces of at most
+// 128 steps and at most 2^16 outputs: every piece of an output as a chain in one lane, on the VALU.
+bool valu_pieces_takes(const GemmCall& g);
+hipError_t gemm_valu_pieces_launch(const GemmCall& g, hipStream_t s);
+
 }  // namespace nnh

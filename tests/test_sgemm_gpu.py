@@ -360,3 +360,56 @@ def test_depth_cut_in_one_launch(gpu, oracle, ta, tb):
                     assert np.array_equal(alive[:, :n], on.astype(np.uint8)), (mode, acc)
                     assert np.all(alive[:, n:] == 7)
                 assert bits_equal(got, want), (mode, relu, acc, first_diff(got, want))
+
+
+@pytest.mark.parametrize("tb", [0, 1])
+def test_four_piece_cuts_on_the_vector_alus(gpu, oracle, tb):
+    """nn-cpp's cut at a depth of 512 (four 128-deep pieces, e.g. config 2's 256 x 256 x 512 layer) runs every piece
+    of an output as a chain in one lane: ragged and tile-aligned m x n, 16-byte and element staging of B (pad),
+    accumulate, a batch sharing B, and each bias mode with ReLU and its mask. Every element against the oracle."""
+    import torch
+
+    import nnh
+    seed = 93000 + 100 * tb
+    for m, n, pad in ((256, 256, 0), (37, 90, 1), (128, 16, 0), (50, 41, 1), (16, 4096, 0)):
+        for acc in (0, 1):
+            p = Problem(0, tb, m, n, 512, pad, seed)
+            seed += 1
+            got, want = gpu_sgemm(p, acc), oracle_sgemm(oracle, p, acc)
+            assert bits_equal(got, want), ((m, n, pad), acc, first_diff(got, want))
+    m, n, k, count = 64, 32, 512, 8
+    for pad in (0, 1):
+        a, lda, b, ldb, c, ldc = _batched_cut_case(0, tb, m, n, k, pad, count, seed + pad)
+        batch = nnh.make_batch((count,), (a[0].size,), (0,), (c[0].size,))
+        for acc in (0, 1):
+            da, db, dc = (torch.from_numpy(x).cuda() for x in (a, b, np.array(c, copy=True)))
+            nnh.sgemm_batched(0, tb, m, n, k, da, lda, db, ldb, dc, ldc, acc, batch)
+            got = dc.cpu().numpy()
+            for i in range(count):
+                want = oracle.sgemm(0, tb, m, n, k, np.ascontiguousarray(a[i]), lda, b, ldb,
+                                    np.ascontiguousarray(c[i]), ldc, acc)
+                assert bits_equal(got[i], want), (pad, acc, i, first_diff(got[i], want))
+    m, n = 40, 60
+    p = Problem(0, tb, m, n, 512, 0, seed + 7)
+    bias_col = synth.mt19937_uniform(seed + 8, n, -1.0, 1.0)
+    bias_row = synth.mt19937_uniform(seed + 9, m, -1.0, 1.0)
+    for mode, bias in ((nnh.BIAS_NONE, None), (nnh.BIAS_COL, bias_col), (nnh.BIAS_ROW, bias_row)):
+        for relu in (False, True):
+            for acc in (0, 1):
+                dbias = torch.from_numpy(bias).cuda() if bias is not None else None
+                dalive = torch.full((m, p.ldc), 7, dtype=torch.uint8, device="cuda")
+                ep = nnh.make_epilogue(mode, dbias, relu, dalive if relu else None)
+                got = gpu_sgemm(p, acc, epilogue=ep)
+                want = oracle_sgemm(oracle, p, acc).copy()
+                v = want[:m, :n]
+                if mode == nnh.BIAS_COL:
+                    v += bias_col[None, :]
+                elif mode == nnh.BIAS_ROW:
+                    v += bias_row[:, None]
+                if relu:
+                    on = v > 0
+                    v[~on] = 0.0
+                    alive = dalive.cpu().numpy()
+                    assert np.array_equal(alive[:, :n], on.astype(np.uint8)), (mode, acc)
+                    assert np.all(alive[:, n:] == 7)
+                assert bits_equal(got, want), (mode, relu, acc, first_diff(got, want))
