@@ -212,6 +212,65 @@ hipError_t add_to_grad(float* dst, const float* src, int64_t count, int first, h
 	return hipGetLastError();
 }
 
+// Two leading axes summed one after the other (sum_to_shape on a {r0, r1, inner} gradient, ops.cpp:35-53, two
+// Tensor::sum(0) calls): t[b][j] = the sum over a of src[a][b][j], then s_j = the sum over b of t[b][j], each in
+// order from +0, then combined into dst as sum_rows does. One launch instead of two: a workgroup owns 16 columns;
+// its 256 threads (16 columns x 16 rows of b) run the first-stage chains, eight of them per thread at a time with
+// the loads of eight depth steps of all eight in flight, park them in LDS, and 16 lanes run the second stage.
+constexpr int kS2Cols = 16, kS2Rows = 16, kS2Chains = 8, kS2Steps = 8;
+
+__global__ void __launch_bounds__(256) sum_rows2_kernel(const float* __restrict__ src, int r0, int r1, int inner,
+                                                        float* __restrict__ dst, int combine) {
+	__shared__ float part[kSum2MaxR1 * (kS2Cols + 1)];
+	const int jj = threadIdx.x & (kS2Cols - 1), br = threadIdx.x / kS2Cols;
+	const int j = min((int)blockIdx.x * kS2Cols + jj, inner - 1);
+	const int64_t sa = (int64_t)r1 * inner;
+	for (int bp = 0; bp < r1; bp += kS2Rows * kS2Chains) {
+		float acc[kS2Chains];
+#pragma unroll
+		for (int c = 0; c < kS2Chains; ++c) acc[c] = 0.0f;
+		for (int a0 = 0; a0 < r0; a0 += kS2Steps) {
+			float v[kS2Chains][kS2Steps];
+#pragma unroll
+			for (int c = 0; c < kS2Chains; ++c)
+#pragma unroll
+				for (int u = 0; u < kS2Steps; ++u) {
+					const int b = min(bp + br + kS2Rows * c, r1 - 1), a = min(a0 + u, r0 - 1);
+					v[c][u] = src[a * sa + (int64_t)b * inner + j];
+				}
+#pragma unroll
+			for (int u = 0; u < kS2Steps; ++u)
+				if (a0 + u < r0)
+#pragma unroll
+					for (int c = 0; c < kS2Chains; ++c) acc[c] = acc[c] + v[c][u];
+		}
+#pragma unroll
+		for (int c = 0; c < kS2Chains; ++c) {
+			const int b = bp + br + kS2Rows * c;
+			if (b < r1) part[b * (kS2Cols + 1) + jj] = acc[c];
+		}
+	}
+	__syncthreads();
+	if (threadIdx.x >= kS2Cols || (int)blockIdx.x * kS2Cols + jj >= inner) return;
+	float s = 0.0f;
+	for (int b = 0; b < r1; ++b) s = s + part[b * (kS2Cols + 1) + jj];
+	if (combine == 0) dst[j] = s;
+	else if (combine == 1) dst[j] = s + 0.0f;
+	else dst[j] = dst[j] + s;
+}
+
+bool sum_rows2_fits(int64_t r0, int64_t r1, int64_t inner) {
+	return r0 > 0 && r1 > 0 && r1 <= kSum2MaxR1 && inner > 0 && r0 < (1 << 30) && inner < (1 << 30) &&
+	       r0 * r1 * inner < ((int64_t)1 << 62) / 4;
+}
+
+hipError_t sum_rows2(const float* src, int64_t r0, int64_t r1, int64_t inner, float* dst, int combine, hipStream_t s) {
+	if (!sum_rows2_fits(r0, r1, inner)) return hipErrorInvalidValue;
+	hipLaunchKernelGGL(sum_rows2_kernel, dim3((unsigned)((inner + kS2Cols - 1) / kS2Cols)), dim3(256), 0, s, src, (int)r0,
+	                   (int)r1, (int)inner, dst, combine);
+	return hipGetLastError();
+}
+
 hipError_t sum_rows(const float* src, int64_t rows, int64_t inner, float* dst, int combine, hipStream_t s) {
 	if (inner == 0) return hipSuccess;
 	if (lds_sum_fits(rows, inner)) {

@@ -11,6 +11,11 @@ hipError_t sum_rows(const float* src, int64_t rows, int64_t inner, float* dst, i
 // Two independent sum_rows in one launch (the same bits as two calls).
 hipError_t sum_rows_pair(const float* src0, int64_t rows0, int64_t inner0, float* dst0, int combine0,
                          const float* src1, int64_t rows1, int64_t inner1, float* dst1, int combine1, hipStream_t s);
+// sum_rows over the first axis of a {r0, r1, inner} tensor, then over the second (two Tensor::sum(0) in turn, the
+// same bits as two calls), in one launch, when r1 <= kSum2MaxR1; combine as sum_rows.
+constexpr int kSum2MaxR1 = 512;
+bool sum_rows2_fits(int64_t r0, int64_t r1, int64_t inner);
+hipError_t sum_rows2(const float* src, int64_t r0, int64_t r1, int64_t inner, float* dst, int combine, hipStream_t s);
 // Tensor::sum(axis) over {pre, d, post} into {pre, post} (combine as sum_rows).
 hipError_t sum_axis(const float* src, int64_t pre, int64_t d, int64_t post, float* dst, int combine, hipStream_t s);
 // dst = src + 0.0f (first) or dst += src, element by element (add_to_grad, ops.cpp:55-82).

@@ -132,6 +132,8 @@ int nnh_linear_backward(const float* g, const float* x, const float* w, const si
 		// s + 0.0f into a fresh gradient or added (ops.cpp:85-99)
 		const int combine = db_first ? 1 : 2;
 		if (nlead == 1) return hip_status(sum_rows(g, (int64_t)lead[0], (int64_t)n, db, combine, s), "bias gradient");
+		if (nlead == 2 && sum_rows2_fits((int64_t)lead[0], (int64_t)lead[1], (int64_t)n))
+			return hip_status(sum_rows2(g, (int64_t)lead[0], (int64_t)lead[1], (int64_t)n, db, combine, s), "bias gradient");
 		// suffix[d] = n * prod(lead[d+1 ..]): the row length left after reducing axes 0..d
 		std::vector<size_t> suffix(nlead);
 		suffix[nlead - 1] = n;

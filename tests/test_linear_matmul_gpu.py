@@ -119,14 +119,17 @@ def test_linear_bias_gradient_in_weight_product(gpu, oracle):
     other cases keep the separate Tensor::sum(0). Both combines (store s + 0.0f, add to the old db), edge and
     interior tiles, several row tiles, depths that are not a multiple of the depth tile, weight gradients large
     enough for the 64 x 64 and 128 x 128 tile configurations, a product that takes nn-cpp's depth cut (db
-    computed apart: 32 x 64 outputs, 1024 deep), a 3-D gradient (two sums), and special values in G."""
+    computed apart: 32 x 64 outputs, 1024 deep), 3-D gradients (two sums, in one launch up to 512 rows of the
+    second axis: transformer_tiny's {16, 64, 64}, {35, 500, 70}; past it, {2, 513, 33}, two launches), a 4-D
+    gradient (three sums), and special values in G."""
     import torch
 
     import nnh
     cases = [  # (batch rows M, in K, out n, leading shape)
         (300, 70, 40, None), (256, 784, 512, None), (256, 256, 10, None), (64, 128, 96, None),
         (37, 33, 129, None), (1024, 64, 32, None), (64, 1024, 1024, None), (16, 2048, 4096, None),
-        (6, 50, 70, (2, 3)),
+        (6, 50, 70, (2, 3)), (1024, 64, 64, (16, 64)), (35 * 500, 8, 70, (35, 500)), (2 * 513, 4, 33, (2, 513)),
+        (60, 6, 7, (3, 4, 5)),
     ]
     for ci, (M, K, n, lead) in enumerate(cases):
         x = synth.mt19937_uniform(1000 + ci, M * K).reshape(M, K)
