@@ -114,6 +114,10 @@ private:
 	std::shared_ptr<NodeImpl> impl_;
 };
 
+// Value::zero_grad over a list (Optimizer::zero_grad, src/optim/sgd.cpp:19-21): the same gradients, all their fills
+// in one launch.
+void zero_grad(const std::vector<Value>& values);
+
 // Ops record no graph while one is alive on the thread (value.hpp:24-40).
 class NoGradGuard {
 public:

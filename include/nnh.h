@@ -194,6 +194,11 @@ int nnh_relu_backward(const float* x, const float* g, float* dx, int first, size
  * existing one adds src, element by element. The first-write rule every backward pass uses; reshape's backward. */
 int nnh_add_to_grad(float* dst, const float* src, size_t count, int first, void* stream);
 
+/* Value::zero_grad over a list of values (Optimizer::zero_grad, src/optim/sgd.cpp:19-21; value.cpp:69-76): n device
+ * buffers of counts[i] floats filled with +0, every fill in one launch (32 buffers per launch). The buffers must not
+ * overlap one another. */
+int nnh_zero_many(float* const* buffers, const size_t* counts, size_t n, void* stream);
+
 /* Tensor::sum(0) of a {rows, inner} tensor (src/tensor.cpp:422-456): s_j = sum of src[a][j] over a in order,
  * from +0. combine 0: dst = s; 1: dst = s + 0.0f (a fresh gradient); 2: dst += s. */
 int nnh_tensor_sum0(const float* src, size_t rows, size_t inner, float* dst, int combine, void* stream);

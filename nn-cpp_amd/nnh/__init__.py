@@ -70,6 +70,7 @@ _EXTRA_DECLS = {
     "nnh_relu_forward": [_vp, _vp, _sz, _vp],
     "nnh_relu_backward": [_vp, _vp, _vp, C.c_int, _sz, _vp],
     "nnh_tensor_sum0": [_vp, _sz, _sz, _vp, C.c_int, _vp],
+    "nnh_zero_many": [_vp, _vp, _sz, _vp],
     "nnh_attention_forward": [_vp, _vp, _vp, _sz, _sz, _sz, _sz, _sz, _vp, C.c_int, _vp, _vp, _vp],
     "nnh_attention_backward": [_vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, _sz, _sz, _vp, C.c_int, _vp, C.c_int, _vp,
                                C.c_int, _vp, C.c_int, _vp],
@@ -291,6 +292,13 @@ def tensor_sum0(src, dst, combine=0, stream=None):
     rows = src.shape[0]
     inner = src.numel() // rows if rows else dst.numel()
     check(lib().nnh_tensor_sum0(_ptr(src), rows, inner, _ptr(dst), int(combine), _stream(stream)))
+
+
+def zero_many(tensors, stream=None):
+    """Every float32 device tensor in `tensors` filled with +0 in one launch per 32 (nnh_zero_many)."""
+    ptrs = (C.c_void_p * max(1, len(tensors)))(*[t.data_ptr() for t in tensors])
+    counts = (C.c_size_t * max(1, len(tensors)))(*[t.numel() for t in tensors])
+    check(lib().nnh_zero_many(C.cast(ptrs, C.c_void_p), C.cast(counts, C.c_void_p), len(tensors), _stream(stream)))
 
 
 def attention_forward(q, k, v, heads, mask=None, causal=False, stream=None):

@@ -109,7 +109,7 @@ int nnh_bench_workload_step(int model, const float* x, size_t N, const float* co
 			Value y = tf ? transformer_forward(ids, N, p, pe) : forward(model, xv, p);
 			nn::hip::synchronize();
 			const auto t1 = Clock::now();
-			for (const Value& v : p) v.zero_grad();
+			nn::hip::zero_grad(p);  // Optimizer::zero_grad: every parameter's zero_grad, in one launch
 			y.backward(seed);
 			nn::hip::synchronize();
 			const auto t2 = Clock::now();

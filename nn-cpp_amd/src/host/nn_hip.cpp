@@ -223,6 +223,32 @@ void Value::zero_grad() const {
 	impl_->grad_fresh = false;
 }
 
+void zero_grad(const std::vector<Value>& values) {
+	std::vector<float*> ptrs;
+	std::vector<size_t> counts;
+	for (const Value& v : values) {
+		NodeImpl* n = v.impl();
+		if (n->grad.shape() != n->data.shape()) n->grad = Tensor::empty(n->data.shape());
+		n->grad_fresh = false;
+		if (n->grad.size()) {
+			ptrs.push_back(n->grad.data());
+			counts.push_back(n->grad.size());
+		}
+	}
+	// one value listed twice: one fill
+	std::vector<size_t> order(ptrs.size());
+	for (size_t i = 0; i < order.size(); ++i) order[i] = i;
+	std::sort(order.begin(), order.end(), [&](size_t a, size_t b) { return ptrs[a] < ptrs[b]; });
+	std::vector<float*> up;
+	std::vector<size_t> uc;
+	for (size_t i : order)
+		if (up.empty() || up.back() != ptrs[i]) {
+			up.push_back(ptrs[i]);
+			uc.push_back(counts[i]);
+		}
+	check(nnh_zero_many(up.data(), uc.data(), up.size(), g_stream));
+}
+
 void Value::backward() const {
 	if (impl_->data.size() != 1) throw TensorShapeError("nn::hip: backward() needs a one-element value");
 	backward(Tensor(impl_->data.shape(), 1.0f));

@@ -195,7 +195,8 @@ int64_t gemm_workspace_floats(const GemmCall& g) {
 }
 
 // Configurations kNumConfigs .. kNumConfigs + kValuShapes - 1 are the VALU kernel's lane blocks (gemm_valu.hip).
-int gemm_config_count() { return kNumConfigs + kValuShapes; }
+// Configuration kNumConfigs + kValuShapes forces the VALU pieces kernel on a cut product it can take.
+int gemm_config_count() { return kNumConfigs + kValuShapes + 1; }
 const char* gemm_config_name(int config) {
 	if (config == kNumConfigs + kValu2x2) return "valu 32x32 (2x2 chains per lane)";
 	if (config == kNumConfigs + kValu1x2) return "valu 16x32 (1x2 chains per lane)";
@@ -203,6 +204,7 @@ const char* gemm_config_name(int config) {
 	if (config == kNumConfigs + kValu1x4) return "valu 16x64 (1x4 chains per lane)";
 	if (config == kNumConfigs + kValuBc1) return "valu bcast 16x16 (1 chain per lane, A by DPP)";
 	if (config == kNumConfigs + kValuBc2) return "valu bcast 32x16 (2 chains per lane, A by DPP)";
+	if (config == kNumConfigs + kValuShapes) return "valu pieces 16x16 (every piece of a cut output in one lane)";
 
 	return (config >= 0 && config < kNumConfigs) ? configs()[config].name : "";
 }
@@ -211,6 +213,7 @@ hipError_t gemm_launch(const GemmCall& g, hipStream_t s, int config, float* work
 	if (g.m == 0 || g.n == 0 || g.batch_count == 0) return hipSuccess;
 	hipError_t e = prepare_device();
 	if (e != hipSuccess) return e;
+	const bool force_pieces = config == kNumConfigs + kValuShapes;
 	// the VALU kernel: forced, or chosen by shape, for a product it can take
 	const bool valu_ok = !g.gather && !g.rowsum && g.k > 0 && !depth_cut(g.m, g.n, g.k) && g.m < (1 << 30) &&
 	                     g.n < (1 << 30) && g.k < (1 << 30);
@@ -223,7 +226,8 @@ hipError_t gemm_launch(const GemmCall& g, hipStream_t s, int config, float* work
 	if (g.gather && g.ta) return hipErrorInvalidValue;
 	if (g.rowsum && (depth_cut(g.m, g.n, g.k) || g.batch_count != 1 || g.gather || !g.ta || g.tb))
 		return hipErrorInvalidValue;
-	if (valu_pieces_takes(g)) return gemm_valu_pieces_launch(g, s);
+	if (force_pieces ? valu_pieces_ok(g) : valu_pieces_takes(g))
+		return gemm_valu_pieces_launch(g, s);
 	if (pieces_kernel_takes(g)) return gemm_pieces_launch(g, s);
 	bool cut = false, interior = false;
 	GemmArgs p = make_args(g, cf, cut, interior);

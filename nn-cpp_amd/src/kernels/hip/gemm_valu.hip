@@ -413,7 +413,7 @@ __global__ void __launch_bounds__(256) sgemm_valu_bc_kernel(const GemmArgs p) {
 
 constexpr int kPcMaxBlocks = 8;     // piece depth <= 128
 constexpr int kPcMaxK = 2048;       // op(B)'s 16 columns of the whole depth in LDS: <= 131 KB
-constexpr int kPcMaxPieces = 4;
+constexpr int kPcMaxPieces = 8;   // forced (a configuration index); the shape rule sends at most 4
 constexpr int kPcMaxOutputs = 1 << 16;
 
 inline int pc_pitch(int k) { return ((k + 63) / 64) * 64 + 4; }
@@ -430,7 +430,10 @@ __device__ __forceinline__ void bcast_quad(float (&acc)[NP], const float (&a)[NP
 	    ...);
 }
 
-template <bool TA, bool TB, int NP, bool VEC>
+// SPLIT (more than four pieces): the workgroup owns 4 x 16 outputs instead (lane (q, c): row m0 + q) and wave w runs
+// pieces w, w + 4 (NP = 2 chains per lane), so a small product spreads over four times the workgroups; the waves'
+// results meet in LDS and the first wave adds them in piece order.
+template <bool TA, bool TB, int NP, bool VEC, bool SPLIT>
 __global__ void __launch_bounds__(256) sgemm_valu_pieces_kernel(const GemmArgs p) {
 	extern __shared__ __align__(16) float lds[];  // [16][pitch]: lds[cc * pitch + kk] = op(B)[kk][n0 + cc]
 	const int tid = threadIdx.x, lane = tid & 63;
@@ -439,21 +442,22 @@ __global__ void __launch_bounds__(256) sgemm_valu_pieces_kernel(const GemmArgs p
 	const int tiles = p.tiles_m * p.tiles_n;
 	const int t = blockIdx.x % tiles, bi = blockIdx.x / tiles;
 	const int tm = t / p.tiles_n, tn = t - tm * p.tiles_n;
-	const int m0 = tm * 16, n0 = tn * 16;
+	const int m0 = tm * (SPLIT ? 4 : 16), n0 = tn * 16;
 	int64_t oa = 0, ob = 0, oc = 0;
 	if (p.batch.ndim > 0) batch_offsets(p.batch, bi, oa, ob, oc);
 	const float* __restrict__ A = p.a + oa;
 	const float* __restrict__ B = p.b + ob;
 	const int K = p.k, P = p.pieces, pk = p.piece_k;
 	const int pitch = ((K + 63) / 64) * 64 + 4;
-	const int row = m0 + 4 * wave + q, col = n0 + c;
+	const int row = SPLIT ? m0 + q : m0 + 4 * wave + q, col = n0 + c;
 	const int64_t rowc = min(row, p.m - 1);
 
 	int pce[NP], len[NP];  // the piece each chain slot runs (piece 0 for an empty slot) and its depth
 #pragma unroll
 	for (int u = 0; u < NP; ++u) {
-		pce[u] = u < P ? u : 0;
-		len[u] = u < P ? min(pk, K - u * pk) : pk;
+		const int pc = SPLIT ? wave + 4 * u : u;
+		pce[u] = pc < P ? pc : 0;
+		len[u] = pc < P ? min(pk, K - pc * pk) : pk;
 	}
 	float a[NP][kPcMaxBlocks];
 #pragma unroll
@@ -464,13 +468,13 @@ __global__ void __launch_bounds__(256) sgemm_valu_pieces_kernel(const GemmArgs p
 			a[u][b] = TA ? A[kk * p.lda + rowc] : A[rowc * p.lda + kk];
 		}
 
-	// op(B) into LDS, eight loads in flight per thread before their stores
+	// op(B) into LDS, sixteen loads in flight per thread before their stores
 	if (VEC) {  // K (TB) or n (!TB) a multiple of 4, 16-byte rows
 		const int total = TB ? 16 * (K / 4) : K * 4;
-		for (int e0 = 0; e0 < total; e0 += 8 * 256) {
-			f32x4 v[8];
+		for (int e0 = 0; e0 < total; e0 += 16 * 256) {
+			f32x4 v[16];
 #pragma unroll
-			for (int u = 0; u < 8; ++u) {
+			for (int u = 0; u < 16; ++u) {
 				const int e = min(e0 + tid + 256 * u, total - 1);
 				if (TB) {
 					const int cc = e / (K / 4), k4 = 4 * (e - cc * (K / 4));
@@ -481,7 +485,7 @@ __global__ void __launch_bounds__(256) sgemm_valu_pieces_kernel(const GemmArgs p
 				}
 			}
 #pragma unroll
-			for (int u = 0; u < 8; ++u) {
+			for (int u = 0; u < 16; ++u) {
 				const int e = e0 + tid + 256 * u;
 				if (e >= total) continue;
 				if (TB) {
@@ -562,11 +566,23 @@ __global__ void __launch_bounds__(256) sgemm_valu_pieces_kernel(const GemmArgs p
 			}
 		}
 	}
-	if (row >= p.m || col >= p.n) return;
-	float v = acc[0];
+	float v;
+	if (SPLIT) {
+		float* part = lds + 16 * pitch;  // [P][64]
 #pragma unroll
-	for (int u = 1; u < NP; ++u)
-		if (u < P) v = v + acc[u];
+		for (int u = 0; u < NP; ++u)
+			if (wave + 4 * u < P) part[(wave + 4 * u) * 64 + lane] = acc[u];
+		__syncthreads();
+		if (wave != 0) return;
+		v = part[lane];
+		for (int pc = 1; pc < P; ++pc) v = v + part[pc * 64 + lane];
+	} else {
+		v = acc[0];
+#pragma unroll
+		for (int u = 1; u < NP; ++u)
+			if (u < P) v = v + acc[u];
+	}
+	if (row >= p.m || col >= p.n) return;
 	float* __restrict__ Cp = p.c + oc;
 	const int64_t off = (int64_t)row * p.ldc + col;
 	if (p.accumulate) v = Cp[off] + v;
@@ -689,12 +705,8 @@ hipError_t gemm_valu_launch(const GemmCall& g, int shape, hipStream_t s) {
 	return hipGetLastError();
 }
 
-bool valu_pieces_takes(const GemmCall& g) {
-	// Measured against the MFMA pieces kernel (device time, one MI355X): config 2's 256 x 256 x 512 NT layer (four
-	// 128-deep pieces) is about 1 us faster here (the MLP forward 23.6 -> 22.5 us); with eight pieces per lane
-	// (transformer_tiny's 64 x 64 x 1024 weight gradients, the split mode's 256 x 10 x 256) or a transposed op(A)
-	// (strided dword loads) it was slower, so those stay on the MFMA kernel.
-	if (g.gather || g.rowsum || g.ta || g.m <= 0 || g.n <= 0 || g.k <= 0) return false;
+bool valu_pieces_ok(const GemmCall& g) {
+	if (g.gather || g.rowsum || g.m <= 0 || g.n <= 0 || g.k <= 0) return false;
 	if (g.m >= (1 << 30) || g.n >= (1 << 30) || g.k > kPcMaxK) return false;
 	const CutPlan plan = cut_plan(g.m, g.n, g.k);
 	if (plan.pieces < 2 || plan.pieces > kPcMaxPieces || plan.piece_k % 16 != 0 || plan.piece_k > 16 * kPcMaxBlocks)
@@ -702,14 +714,34 @@ bool valu_pieces_takes(const GemmCall& g) {
 	return (double)g.m * (double)g.n * (double)g.batch_count <= (double)kPcMaxOutputs;
 }
 
+bool valu_pieces_takes(const GemmCall& g) {
+	// Measured against the MFMA pieces kernel (device time, one MI355X, the kernel forced as configuration 18):
+	// * four pieces in a lane: config 2's 256 x 256 x 512 NT layer 1 us faster (the MLP forward 23.6 -> 22.5 us);
+	// * five to eight pieces split over the waves: transformer_tiny's weight gradients 64 x 64 x 1024 TN 8.4 against
+	//   9.0 us, 256 x 64 x 1024 and 64 x 256 x 1024 TN 8.6 against 9.2, 64 x 64 x 1024 NN 7.1 against 8.9,
+	//   128 x 128 x 768 TN 7.9 against 8.9 (eight pieces in one lane had been slower: 16.3 us);
+	// * up to four pieces with op(A) transposed (strided dword loads) stay on the MFMA kernel.
+	if (!valu_pieces_ok(g)) return false;
+	const int64_t pieces = cut_plan(g.m, g.n, g.k).pieces;
+	return pieces > 4 || !g.ta;
+}
+
+template <int NP, bool VEC, bool SPLIT>
+ValuFn valu_pieces_fn(int ta, int tb) {
+	if (!ta && !tb) return sgemm_valu_pieces_kernel<false, false, NP, VEC, SPLIT>;
+	if (!ta && tb) return sgemm_valu_pieces_kernel<false, true, NP, VEC, SPLIT>;
+	if (ta && !tb) return sgemm_valu_pieces_kernel<true, false, NP, VEC, SPLIT>;
+	return sgemm_valu_pieces_kernel<true, true, NP, VEC, SPLIT>;
+}
+
+// up to four pieces in one lane; five to eight split over the waves, two per lane
 template <bool VEC>
-ValuFn valu_pieces_pick(int tb) {
-	return tb ? sgemm_valu_pieces_kernel<false, true, kPcMaxPieces, VEC>
-	          : sgemm_valu_pieces_kernel<false, false, kPcMaxPieces, VEC>;
+ValuFn valu_pieces_pick(int pieces, int ta, int tb) {
+	return pieces <= 4 ? valu_pieces_fn<4, VEC, false>(ta, tb) : valu_pieces_fn<2, VEC, true>(ta, tb);
 }
 
 hipError_t gemm_valu_pieces_launch(const GemmCall& g, hipStream_t s) {
-	if (!valu_pieces_takes(g)) return hipErrorInvalidValue;
+	if (!valu_pieces_ok(g)) return hipErrorInvalidValue;
 	const CutPlan plan = cut_plan(g.m, g.n, g.k);
 	GemmArgs p{};
 	p.a = g.a;
@@ -727,7 +759,8 @@ hipError_t gemm_valu_pieces_launch(const GemmCall& g, hipStream_t s) {
 	p.ep = g.ep;
 	p.pieces = (int)plan.pieces;
 	p.piece_k = (int)plan.piece_k;
-	p.tiles_m = (int)((g.m + 15) / 16);
+	const bool split = p.pieces > 4;
+	p.tiles_m = (int)((g.m + (split ? 3 : 15)) / (split ? 4 : 16));
 	p.tiles_n = (int)((g.n + 15) / 16);
 	const int64_t blocks = (int64_t)p.tiles_m * p.tiles_n * g.batch_count;
 	if (blocks > 0x7fffffff) return hipErrorInvalidConfiguration;
@@ -735,8 +768,9 @@ hipError_t gemm_valu_pieces_launch(const GemmCall& g, hipStream_t s) {
 	// and the batch strides 16-byte aligned
 	bool vec = g.ldb % 4 == 0 && reinterpret_cast<uintptr_t>(g.b) % 16 == 0 && (g.tb ? g.k : g.n) % 4 == 0;
 	for (int d = 0; d < g.batch.ndim; ++d) vec = vec && g.batch.sb[d] % 4 == 0;
-	const ValuFn fn = vec ? valu_pieces_pick<true>(g.tb) : valu_pieces_pick<false>(g.tb);
-	const size_t lds = (size_t)16 * pc_pitch(p.k) * sizeof(float);
+	const ValuFn fn =
+	    vec ? valu_pieces_pick<true>(p.pieces, g.ta, g.tb) : valu_pieces_pick<false>(p.pieces, g.ta, g.tb);
+	const size_t lds = ((size_t)16 * pc_pitch(p.k) + (split ? (size_t)p.pieces * 64 : 0)) * sizeof(float);
 	hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize,
 	                                   (int)lds);
 	if (e != hipSuccess) return e;

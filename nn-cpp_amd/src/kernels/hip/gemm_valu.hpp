@@ -24,9 +24,11 @@ int valu_shape(const GemmCall& g);
 // The launch (any product without gather, row sums or a depth cut; k > 0).
 hipError_t gemm_valu_launch(const GemmCall& g, int shape, hipStream_t s);
 
-// Cut products (nn-cpp's depth cut, or the split-depth mode's) with op(A) untransposed, at most 4 pieces of at most
-// 128 steps and at most 2^16 outputs: every piece of an output as a chain in one lane, on the VALU.
+// Cut products (nn-cpp's depth cut, or the split-depth mode's) of at most 8 pieces of at most 128 steps and at most
+// 2^16 outputs, on the VALU: up to 4 pieces (op(A) untransposed) as chains in one lane, 5 to 8 split over the waves.
 bool valu_pieces_takes(const GemmCall& g);
+// Whether the kernel can take the product at all (any layout, up to 8 pieces): configuration kValuPiecesConfig.
+bool valu_pieces_ok(const GemmCall& g);
 hipError_t gemm_valu_pieces_launch(const GemmCall& g, hipStream_t s);
 
 }  // namespace nnh

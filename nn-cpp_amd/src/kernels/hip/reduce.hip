@@ -271,6 +271,23 @@ hipError_t sum_rows2(const float* src, int64_t r0, int64_t r1, int64_t inner, fl
 	return hipGetLastError();
 }
 
+// +0 into several buffers in one launch: job i covers elements start[i] .. start[i + 1] - 1 of the concatenation.
+__global__ void __launch_bounds__(256) zero_many_kernel(const ZeroJobs jobs) {
+	const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
+	if (e >= jobs.start[jobs.n]) return;
+	int i = 0;
+	while (e >= jobs.start[i + 1]) ++i;
+	jobs.p[i][e - jobs.start[i]] = 0.0f;
+}
+
+hipError_t zero_many(const ZeroJobs& jobs, hipStream_t s) {
+	const int64_t total = jobs.start[jobs.n];
+	if (total == 0) return hipSuccess;
+	if ((total + 255) / 256 > 0x7fffffff) return hipErrorInvalidConfiguration;
+	hipLaunchKernelGGL(zero_many_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, jobs);
+	return hipGetLastError();
+}
+
 hipError_t sum_rows(const float* src, int64_t rows, int64_t inner, float* dst, int combine, hipStream_t s) {
 	if (inner == 0) return hipSuccess;
 	if (lds_sum_fits(rows, inner)) {

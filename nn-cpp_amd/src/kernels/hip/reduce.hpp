@@ -18,6 +18,14 @@ bool sum_rows2_fits(int64_t r0, int64_t r1, int64_t inner);
 hipError_t sum_rows2(const float* src, int64_t r0, int64_t r1, int64_t inner, float* dst, int combine, hipStream_t s);
 // Tensor::sum(axis) over {pre, d, post} into {pre, post} (combine as sum_rows).
 hipError_t sum_axis(const float* src, int64_t pre, int64_t d, int64_t post, float* dst, int combine, hipStream_t s);
+// Up to kZeroJobs buffers filled with +0 in one launch (start[0] = 0, start[i + 1] - start[i] = buffer i's length).
+constexpr int kZeroJobs = 32;
+struct ZeroJobs {
+	float* p[kZeroJobs];
+	int64_t start[kZeroJobs + 1];
+	int n;
+};
+hipError_t zero_many(const ZeroJobs& jobs, hipStream_t s);
 // dst = src + 0.0f (first) or dst += src, element by element (add_to_grad, ops.cpp:55-82).
 hipError_t add_to_grad(float* dst, const float* src, int64_t count, int first, hipStream_t s);
 hipError_t relu_forward(const float* x, float* y, int64_t count, hipStream_t s);

@@ -185,6 +185,34 @@ int nnh_add_to_grad(float* dst, const float* src, size_t count, int first, void*
 	                  "add_to_grad");
 }
 
+int nnh_zero_many(float* const* buffers, const size_t* counts, size_t n, void* stream) {
+	if (n == 0) return NNH_OK;
+	if (!buffers || !counts) return fail(NNH_ERR_INVALID, "zero_many: null pointer");
+	uint64_t total = 0;
+	for (size_t i = 0; i < n; ++i) {
+		if (counts[i] > 0 && !buffers[i]) return fail(NNH_ERR_INVALID, "zero_many: null buffer");
+		if (counts[i] > ((uint64_t)1 << 60) || total + counts[i] > ((uint64_t)1 << 60))
+			return fail(NNH_ERR_INVALID, "zero_many: size out of range (above 2^60 elements)");
+		total += counts[i];
+	}
+	for (size_t i = 0; i < n; ++i)
+		for (size_t j = i + 1; j < n; ++j)
+			if (ranges_overlap(buffers[i], (uint64_t)counts[i] * 4, buffers[j], (uint64_t)counts[j] * 4))
+				return fail(NNH_ERR_ALIAS, "zero_many: buffers overlap");
+	hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+	for (size_t b = 0; b < n; b += kZeroJobs) {
+		ZeroJobs jobs{};
+		jobs.n = (int)std::min<size_t>(kZeroJobs, n - b);
+		for (int i = 0; i < jobs.n; ++i) {
+			jobs.p[i] = buffers[b + i];
+			jobs.start[i + 1] = jobs.start[i] + (int64_t)counts[b + i];
+		}
+		const hipError_t e = zero_many(jobs, s);
+		if (e != hipSuccess) return hip_status(e, "zero_many");
+	}
+	return NNH_OK;
+}
+
 int nnh_tensor_sum0(const float* src, size_t rows, size_t inner, float* dst, int combine, void* stream) {
 	if (inner == 0) return NNH_OK;
 	if (!dst || (rows > 0 && !src)) return fail(NNH_ERR_INVALID, "null pointer");

@@ -459,6 +459,17 @@ void elem() {
 	EXPECT(nnh_embedding_backward(b.data(), rows.data(), 8, 8, 8, nullptr, 1, nullptr), INV);
 	EXPECT(nnh_embedding_backward(b.data(), rows.data(), 8, kHuge, kHuge, y.data(), 1, nullptr), INV);
 	EXPECT(nnh_embedding_backward(nullptr, nullptr, 0, 8, 8, y.data(), 1, nullptr), HIP);
+	float* bufs[3] = {a.data(), b.data(), y.data()};
+	size_t counts[3] = {64, 64, 64};
+	EXPECT(nnh_zero_many(bufs, counts, 3, nullptr), HIP);
+	EXPECT(nnh_zero_many(nullptr, nullptr, 0, nullptr), OK);
+	EXPECT(nnh_zero_many(nullptr, counts, 3, nullptr), INV);
+	float* overlap[2] = {a.data(), a.data() + 10};
+	EXPECT(nnh_zero_many(overlap, counts, 2, nullptr), ALIAS);
+	float* withnull[2] = {a.data(), nullptr};
+	EXPECT(nnh_zero_many(withnull, counts, 2, nullptr), INV);
+	size_t huge[2] = {kHuge, 1};
+	EXPECT(nnh_zero_many(bufs, huge, 2, nullptr), INV);
 }
 
 }  // namespace

@@ -170,3 +170,36 @@ def test_embedding_backward_keeps_negative_zero(gpu, oracle):
     want = oracle.embedding_backward(g, rows, V, D, old, False)
     assert np.all(np.signbit(want))
     assert_same(dw.cpu().numpy().reshape(V, D), want, "embedding dw of -0")
+
+
+def test_zero_many(gpu):
+    """nnh_zero_many (an optimizer's zero_grad over its parameters in one launch per 32 buffers): 40 buffers of
+    sizes 0 to 70,001 carved from one allocation with gaps, every buffer +0 afterwards (no -0) and every gap
+    untouched; overlapping buffers are refused."""
+    import torch
+
+    import nnh
+    rng = np.random.default_rng(5)
+    sizes = [0, 1, 3, 64, 70001] + list(rng.integers(1, 5000, 35))
+    total = sum(sizes) + 7 * len(sizes)
+    base = torch.full((total,), -0.0, device="cuda")
+    views, gaps, off = [], [], 0
+    for n in sizes:
+        views.append(base[off:off + n])
+        off += n
+        gaps.append((off, off + 7))
+        off += 7
+    base[:] = torch.from_numpy(rng.normal(size=total).astype(np.float32)).cuda()
+    before = base.cpu().numpy().copy()
+    nnh.zero_many(views)
+    torch.cuda.synchronize()
+    after = base.cpu().numpy()
+    off = 0
+    for n in sizes:
+        seg = after[off:off + n]
+        assert np.all(seg == 0) and not np.any(np.signbit(seg)), n
+        off += n
+        assert np.array_equal(after[off:off + 7].view(np.uint32), before[off:off + 7].view(np.uint32))
+        off += 7
+    with pytest.raises(nnh.NnhError):
+        nnh.zero_many([base[0:10], base[5:20]])
