@@ -843,6 +843,58 @@ __global__ void __launch_bounds__(kLnThreads) ln_dgamma_kernel(const float* __re
 	}
 }
 
+// dgamma and dbeta for at most 1024 rows (transformer_tiny's 16 x 64 tokens): the same chains, one pass. A
+// workgroup of 1024 threads owns 16 columns; every thread loads 16 rows of its column (g, x, the rows' mean and
+// inv_std, all in flight at once) and parks g * ((x - mean) * inv_std) and g in LDS; then lanes 0-15 add the
+// products down their column in row order (dgamma) and lanes 16-31 the gradients (dbeta), 16 LDS reads ahead.
+constexpr int kLnSmallCols = 16, kLnSmallRows = 1024, kLnSmallThreads = 1024;
+
+__global__ void __launch_bounds__(kLnSmallThreads) ln_dgamma_small_kernel(
+    const float* __restrict__ g, const float* __restrict__ x, const float* __restrict__ mean,
+    const float* __restrict__ inv, int R, int D, float* dgamma, int dg_first, float* dbeta, int db_first) {
+	__shared__ float buf[2][kLnSmallRows][kLnSmallCols];
+	const int tid = threadIdx.x;
+	const int c = tid & (kLnSmallCols - 1), r0 = tid / kLnSmallCols;  // rows r0 + 64 u
+	const int c0 = blockIdx.x * kLnSmallCols;
+	const int col = min(c0 + c, D - 1);
+	constexpr int kPer = kLnSmallRows * kLnSmallCols / kLnSmallThreads;
+	float gv[kPer], xv[kPer], mv[kPer], iv[kPer];
+#pragma unroll
+	for (int u = 0; u < kPer; ++u) {
+		const int64_t r = min(r0 + 64 * u, R - 1);
+		gv[u] = g[r * D + col];
+		xv[u] = x[r * D + col];
+		mv[u] = mean[r];
+		iv[u] = inv[r];
+	}
+#pragma unroll
+	for (int u = 0; u < kPer; ++u) {
+		const int r = r0 + 64 * u;
+		buf[0][r][c] = gv[u] * ((xv[u] - mv[u]) * iv[u]);
+		buf[1][r][c] = gv[u];
+	}
+	__syncthreads();
+	if (tid >= 2 * kLnSmallCols) return;
+	const float* v = &buf[tid / kLnSmallCols][0][c];
+	float acc = 0.0f;
+	int i = 0;
+	for (; i + 16 <= R; i += 16) {
+		float t[16];
+#pragma unroll
+		for (int u = 0; u < 16; ++u) t[u] = v[(i + u) * kLnSmallCols];
+#pragma unroll
+		for (int u = 0; u < 16; ++u) acc = acc + t[u];
+	}
+	for (; i < R; ++i) acc = acc + v[i * kLnSmallCols];
+	if (c0 + c >= D) return;
+	const int j = c0 + c;
+	if (tid < kLnSmallCols) {
+		if (dgamma) dgamma[j] = dg_first ? 0.0f + acc : dgamma[j] + acc;
+	} else {
+		if (dbeta) dbeta[j] = db_first ? 0.0f + acc : dbeta[j] + acc;
+	}
+}
+
 inline bool aligned16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }
 
 template <int MODE>
@@ -968,7 +1020,8 @@ hipError_t batchnorm_backward(const float* gy, const float* x, const unsigned ch
 hipError_t layernorm_forward(const float* x, const float* gamma, const float* beta, int64_t R, int D, float fd,
                              float eps, float* y, float* mean, float* inv_std, hipStream_t s) {
 	if (R == 0) return hipSuccess;
-	const int rw = (int)std::min<int64_t>(std::min(64, kLnLdsFloats / (D + 1)), R);
+	// as many rows per workgroup as LDS holds, but few enough for about 256 workgroups when the rows are few
+	const int rw = (int)std::min<int64_t>(std::min<int64_t>(std::min(64, kLnLdsFloats / (D + 1)), R), std::max<int64_t>(1, (R + 255) / 256));
 	if (rw >= 1 && R / rw < ((int64_t)1 << 31) && (int64_t)rw * D < ((int64_t)1 << 31)) {
 		LnArgs a{};
 		a.x = x;
@@ -998,7 +1051,9 @@ hipError_t layernorm_backward(const float* gy, const float* x, const float* gamm
                               const float* inv_std, int64_t R, int D, float fd, float* dx, int dx_first,
                               float* dgamma, int dgamma_first, float* dbeta, int dbeta_first, hipStream_t s) {
 	if (R == 0 && !dgamma && !dbeta) return hipSuccess;
-	const int rw = (int)std::min<int64_t>(std::min(64, (kLnLdsFloats - D) / (3 * (D + 1) + 4)), std::max<int64_t>(R, 1));
+	const int rw = (int)std::min<int64_t>(std::min<int64_t>(std::min(64, (kLnLdsFloats - D) / (3 * (D + 1) + 4)),
+	                                                        std::max<int64_t>(R, 1)),
+	                                      std::max<int64_t>(1, (R + 255) / 256));
 	if (rw >= 1 && R / rw < ((int64_t)1 << 31) && (int64_t)rw * D < ((int64_t)1 << 31)) {
 		if (dx && R > 0) {
 			LnArgs a{};
@@ -1021,7 +1076,11 @@ hipError_t layernorm_backward(const float* gy, const float* x, const float* gamm
 			const hipError_t e = hipGetLastError();
 			if (e != hipSuccess) return e;
 		}
-		if (dgamma || dbeta)
+		if ((dgamma || dbeta) && R > 0 && R <= kLnSmallRows)
+			hipLaunchKernelGGL(ln_dgamma_small_kernel, dim3((unsigned)((D + kLnSmallCols - 1) / kLnSmallCols)),
+			                   dim3(kLnSmallThreads), 0, s, gy, x, mean, inv_std, (int)R, D, dgamma, dgamma_first, dbeta,
+			                   dbeta_first);
+		else if (dgamma || dbeta)
 			hipLaunchKernelGGL(ln_dgamma_kernel, dim3((unsigned)((D + kLnCols - 1) / kLnCols)), dim3(kLnThreads), 0, s, gy, x,
 			                   mean, inv_std, R, D, dgamma, dgamma_first, dbeta, dbeta_first);
 		return hipGetLastError();
