@@ -246,7 +246,6 @@ __global__ void __launch_bounds__(256) sgemm_valu_kernel(const GemmArgs p) {
 
 template <int J, bool FIRST>
 __device__ __forceinline__ void fmac_bcast(float& acc, float a, float b) {
-
 	if (FIRST)
 		asm("s_nop 1\n\tv_fmac_f32_dpp %0, %1, %2 row_newbcast:%3 row_mask:0xf bank_mask:0xf"
 		    : "+v"(acc)
