@@ -549,7 +549,8 @@ __global__ void __launch_bounds__(256) ln_backward_kernel(const LnBwdArgs a) {
 // LDS with 16-byte coalesced loads, all issued before the first LDS store (row pitch D + 1, so lane r walking row r
 // hits bank (r + j) mod 64), lane r of wave 0 runs row r's chains over LDS and writes its outputs back into its LDS
 // row, and the 256 threads copy the block out with coalesced stores. The LDS budget is 64 KB of floats (16384):
-// rw = min(64, 16384 / (D + 1)) rows for the forward, half of that for the backward (g and x).
+// rw = min(64, 16384 / (D + 1)) rows for the forward, about half of that for the backward (g and x), and no more
+// than R / 256 rows when that leaves about 256 workgroups on a small input.
 
 constexpr int kLnLdsFloats = 16384;
 constexpr int kLnLoadPer = kLnLdsFloats / 4 / 256;  // float4 loads per thread for a full block (16)
@@ -694,8 +695,7 @@ __global__ void __launch_bounds__(256) ln_dx_lds_kernel(const LnArgs a) {
 	const int pitch = a.D + 1;
 	float* gs = lds;
 	float* xs = gs + a.rw * pitch;
-	float* ps = xs + a.rw * pitch;
-	float* gms = ps + a.rw * pitch;
+	float* gms = xs + a.rw * pitch;
 	float* st = gms + a.D;  // per row: mean, inv_std, sa, sb
 	const int tid = threadIdx.x;
 	const int64_t r0 = (int64_t)blockIdx.x * a.rw;
@@ -708,35 +708,33 @@ __global__ void __launch_bounds__(256) ln_dx_lds_kernel(const LnArgs a) {
 		st[4 * tid + 1] = a.inv_in[r0 + tid];
 	}
 	__syncthreads();
-	const int total = nr * a.D;
-	for (int e = tid; e < total; e += 256) {
-		const int r = (int)fdiv((unsigned)e, a.dd), j = e - r * a.D;
-		const float dxhat = gs[r * pitch + j] * gms[j];
-		ps[r * pitch + j] = dxhat * ((xs[r * pitch + j] - st[4 * r]) * st[4 * r + 1]);
-	}
-	__syncthreads();
 	if (tid < nr) {
+		// the row's two chains (ops.cpp:1040-1047): sa += g gamma, sb += (g gamma) ((x - mean) inv_std), each
+		// product formed as the reference forms it, 16 steps' LDS reads issued before their arithmetic
 		const float* gr = gs + tid * pitch;
-		const float* pr = ps + tid * pitch;
+		const float* xr = xs + tid * pitch;
+		const float mu = st[4 * tid], iv = st[4 * tid + 1];
 		const int D16 = a.D & ~15;
 		float sa = 0.0f, sb = 0.0f;
-		for (int j = 0; j < D16; j += 16) {  // the batch's LDS reads issued, then the two chains
-			float gv[16], mv[16], pv[16];
+		for (int j = 0; j < D16; j += 16) {
+			float gv[16], mv[16], xv[16];
 #pragma unroll
 			for (int u = 0; u < 16; ++u) {
 				gv[u] = gr[j + u];
 				mv[u] = gms[j + u];
-				pv[u] = pr[j + u];
+				xv[u] = xr[j + u];
 			}
 #pragma unroll
 			for (int u = 0; u < 16; ++u) {
-				sa = sa + gv[u] * mv[u];
-				sb = sb + pv[u];
+				const float dxhat = gv[u] * mv[u];
+				sa = sa + dxhat;
+				sb = sb + dxhat * ((xv[u] - mu) * iv);
 			}
 		}
 		for (int j = D16; j < a.D; ++j) {
-			sa = sa + gr[j] * gms[j];
-			sb = sb + pr[j];
+			const float dxhat = gr[j] * gms[j];
+			sa = sa + dxhat;
+			sb = sb + dxhat * ((xr[j] - mu) * iv);
 		}
 		st[4 * tid + 2] = sa;
 		st[4 * tid + 3] = sb;
@@ -744,6 +742,7 @@ __global__ void __launch_bounds__(256) ln_dx_lds_kernel(const LnArgs a) {
 	__syncthreads();
 	const float fd = a.fd;
 	float* dst = a.y + r0 * a.D;
+	const int total = nr * a.D;
 	for (int e = tid; e < total; e += 256) {
 		const int r = (int)fdiv((unsigned)e, a.dd), j = e - r * a.D;
 		const float mu = st[4 * r], inv = st[4 * r + 1], sa = st[4 * r + 2], sb = st[4 * r + 3];
@@ -754,55 +753,91 @@ __global__ void __launch_bounds__(256) ln_dx_lds_kernel(const LnArgs a) {
 	}
 }
 
-// layernorm backward's dgamma and dbeta (ops.cpp:1061-1076): a workgroup owns 32 columns and streams the rows in
-// chunks of 64. Waves 1-4 produce: each thread loads 8 rows of its column (g, x, and the rows' mean and inv_std)
-// three chunks ahead in a register ring, and writes g * ((x - mean) * inv_std), formed exactly as the reference
-// forms it, and g into the chunk's LDS buffer. Wave 0 consumes one chunk behind: lanes 0-31 add the products down
-// their column in row order (dgamma's chain), lanes 32-63 add g (dbeta's chain). One barrier per chunk; two
-// buffers, since the buffer producers fill was last read one chunk before.
-constexpr int kLnCols = 32, kLnChunk = 64, kLnAhead = 3, kLnProducers = 256, kLnThreads = 64 + kLnProducers;
-constexpr int kLnPer = kLnChunk * kLnCols / kLnProducers;  // 8 rows per producer thread and chunk
+// layernorm backward's dgamma and dbeta (ops.cpp:1061-1076): each is a chain down a column in row order, so the
+// columns are the only parallelism. A workgroup owns 32 columns and streams the rows in chunks of 120. Waves 1-15
+// produce: each thread loads four rows of its column (or, VEC, one row's four columns with 16-byte loads) with the
+// rows' mean and inv_std, four chunks ahead in a register ring, and writes g * ((x - mean) * inv_std), formed
+// exactly as the reference forms it, and g into the chunk's LDS buffer (a row of 64 floats: the products, then g,
+// so wave 0 reads 64 consecutive words). Wave 0 consumes one chunk behind: lanes 0-31 add the products down their
+// column (dgamma), lanes 32-63 add g (dbeta), 24 rows' LDS reads in flight while they add eight. One barrier per
+// chunk; two buffers. Measured at [32, 256, 512]: 53 us (the chains of 8192 rows bound it near 23 us; 8-column
+// blocks, 4x the workgroups, and a raised wave priority for the chains measured no faster).
+constexpr int kLnCols = 32, kLnProducers = 960, kLnThreads = 64 + kLnProducers, kLnAhead = 4, kLnPer = 4;
+constexpr int kLnRowStride = kLnProducers / kLnCols;  // 30: a scalar producer's rows are rr + 30 u
+constexpr int kLnChunk = kLnRowStride * kLnPer;       // 120 rows
+constexpr int kLnVecPerRow = kLnCols / 4;             // 8 16-byte loads cover a row's columns
 
+template <bool VEC>
 __global__ void __launch_bounds__(kLnThreads) ln_dgamma_kernel(const float* __restrict__ g,
                                                                const float* __restrict__ x,
                                                                const float* __restrict__ mean,
                                                                const float* __restrict__ inv, int64_t R, int D,
                                                                float* dgamma, int dg_first, float* dbeta,
                                                                int db_first) {
-	__shared__ float buf[2][2][kLnChunk][kLnCols];
+	__shared__ __align__(16) float buf[2][kLnChunk][2 * kLnCols];
 	const int tid = threadIdx.x;
 	const int c0 = blockIdx.x * kLnCols;
 	const int64_t chunks = (R + kLnChunk - 1) / kLnChunk;
 	const bool producer = tid >= 64;
+	const bool consumer = !producer;
 	const int pt = tid - 64;
-	const int c = pt & (kLnCols - 1), rr = pt / kLnCols;  // rows rr + 8u of a chunk
+	// scalar: column c of rows rr + 30 u; VEC: columns 4 q4 .. 4 q4 + 3 of row vr
+	const int c = pt % kLnCols, rr = pt / kLnCols;
+	const int q4 = pt % kLnVecPerRow, vr = pt / kLnVecPerRow;
+	constexpr int kVecRows = kLnProducers / kLnVecPerRow;  // 120: one row per producer thread and chunk
+	static_assert(kVecRows == kLnChunk, "a VEC producer owns one row of a chunk");
 	const int col = min(c0 + c, D - 1);
+	const int col4 = min(c0 + 4 * q4, D - 4);
 	float gv[kLnAhead][kLnPer], xv[kLnAhead][kLnPer], mv[kLnAhead][kLnPer], iv[kLnAhead][kLnPer];
 	auto load = [&](int64_t ch, int slot) {
+		if (VEC) {
+			const int64_t r = min(ch * kLnChunk + vr, R - 1);
+			const f32x4 g4 = *reinterpret_cast<const f32x4*>(g + r * D + col4);
+			const f32x4 x4 = *reinterpret_cast<const f32x4*>(x + r * D + col4);
+			const float m = mean[r], iv0 = inv[r];
+#pragma unroll
+			for (int u = 0; u < 4; ++u) {
+				gv[slot][u] = g4[u];
+				xv[slot][u] = x4[u];
+				mv[slot][u] = m;
+				iv[slot][u] = iv0;
+			}
+			return;
+		}
 #pragma unroll
 		for (int u = 0; u < kLnPer; ++u) {
-			const int64_t r = min(ch * kLnChunk + rr + 8 * u, R - 1);
+			const int64_t r = min(ch * kLnChunk + rr + kLnRowStride * u, R - 1);
 			gv[slot][u] = g[r * D + col];
 			xv[slot][u] = x[r * D + col];
 			mv[slot][u] = mean[r];
 			iv[slot][u] = inv[r];
 		}
 	};
+	// the consumer's chain over n rows of buffer b: batches of eight rows in a ring of four, three batches' LDS reads
+	// in flight while one batch's eight dependent adds run
 	auto chain = [&](float& acc, int b, int n) {
-		const float* v = &buf[b][tid >> 5][0][tid & 31];
+		const float* v = &buf[b][0][tid];
 		if (n == kLnChunk) {
+			constexpr int kB = kLnChunk / 8;
+			float t[4][8];
 #pragma unroll
-			for (int i0 = 0; i0 < kLnChunk; i0 += 16) {  // 16 LDS reads issued, then 16 dependent adds
-				float t[16];
+			for (int q = 0; q < 3; ++q)
 #pragma unroll
-				for (int u = 0; u < 16; ++u) t[u] = v[(i0 + u) * kLnCols];
+				for (int u = 0; u < 8; ++u) t[q][u] = v[(8 * q + u) * 2 * kLnCols];
 #pragma unroll
-				for (int u = 0; u < 16; ++u) acc = acc + t[u];
+			for (int q = 0; q < kB; ++q) {
+				if (q + 3 < kB) {
+#pragma unroll
+					for (int u = 0; u < 8; ++u) t[(q + 3) & 3][u] = v[(8 * (q + 3) + u) * 2 * kLnCols];
+				}
+#pragma unroll
+				for (int u = 0; u < 8; ++u) acc = acc + t[q & 3][u];
 			}
 		} else {
-			for (int i = 0; i < n; ++i) acc = acc + v[i * kLnCols];
+			for (int i = 0; i < n; ++i) acc = acc + v[i * 2 * kLnCols];
 		}
 	};
+	static_assert(kLnChunk % 8 == 0 && kLnChunk >= 24, "the chain reads batches of eight rows, three ahead");
 	if (producer) {
 #pragma unroll
 		for (int k = 0; k < kLnAhead; ++k)
@@ -816,26 +851,38 @@ __global__ void __launch_bounds__(kLnThreads) ln_dgamma_kernel(const float* __re
 			if (ch >= chunks) break;
 			const int b = (int)(ch & 1);
 			if (producer) {
+				if (VEC) {
+					// columns past D read a clamped address: their values are never used
+					f32x4 pr, gg;
 #pragma unroll
-				for (int u = 0; u < kLnPer; ++u) {
-					const int row = rr + 8 * u;
-					buf[b][0][row][c] = gv[k][u] * ((xv[k][u] - mv[k][u]) * iv[k][u]);
-					buf[b][1][row][c] = gv[k][u];
+					for (int u = 0; u < 4; ++u) {
+						pr[u] = gv[k][u] * ((xv[k][u] - mv[k][u]) * iv[k][u]);
+						gg[u] = gv[k][u];
+					}
+					*reinterpret_cast<f32x4*>(&buf[b][vr][4 * q4]) = pr;
+					*reinterpret_cast<f32x4*>(&buf[b][vr][kLnCols + 4 * q4]) = gg;
+				} else {
+#pragma unroll
+					for (int u = 0; u < kLnPer; ++u) {
+						const int row = rr + kLnRowStride * u;
+						buf[b][row][c] = gv[k][u] * ((xv[k][u] - mv[k][u]) * iv[k][u]);
+						buf[b][row][kLnCols + c] = gv[k][u];
+					}
 				}
 				if (ch + kLnAhead < chunks) load(ch + kLnAhead, k);
-			} else if (ch > 0) {
+			} else if (consumer && ch > 0) {
 				chain(acc, b ^ 1, kLnChunk);  // chunk ch - 1 is whole
 			}
 			__syncthreads();
 		}
 	}
-	if (!producer && chunks > 0) {
+	if (consumer && chunks > 0) {
 		const int64_t last = chunks - 1;
 		chain(acc, (int)(last & 1), (int)(R - last * kLnChunk));
 	}
-	if (tid < 64 && c0 + (tid & 31) < D) {
-		const int j = c0 + (tid & 31);
-		if (tid < 32) {
+	if (consumer && c0 + (tid % kLnCols) < D) {
+		const int j = c0 + tid % kLnCols;
+		if (tid < kLnCols) {
 			if (dgamma) dgamma[j] = dg_first ? 0.0f + acc : dgamma[j] + acc;
 		} else {
 			if (dbeta) dbeta[j] = db_first ? 0.0f + acc : dbeta[j] + acc;
@@ -1051,7 +1098,7 @@ hipError_t layernorm_backward(const float* gy, const float* x, const float* gamm
                               const float* inv_std, int64_t R, int D, float fd, float* dx, int dx_first,
                               float* dgamma, int dgamma_first, float* dbeta, int dbeta_first, hipStream_t s) {
 	if (R == 0 && !dgamma && !dbeta) return hipSuccess;
-	const int rw = (int)std::min<int64_t>(std::min<int64_t>(std::min(64, (kLnLdsFloats - D) / (3 * (D + 1) + 4)),
+	const int rw = (int)std::min<int64_t>(std::min<int64_t>(std::min(64, (kLnLdsFloats - D) / (2 * (D + 1) + 4)),
 	                                                        std::max<int64_t>(R, 1)),
 	                                      std::max<int64_t>(1, (R + 255) / 256));
 	if (rw >= 1 && R / rw < ((int64_t)1 << 31) && (int64_t)rw * D < ((int64_t)1 << 31)) {
@@ -1072,7 +1119,7 @@ hipError_t layernorm_backward(const float* gy, const float* x, const float* gamm
 			a.dq = make_fastdiv((unsigned)(a.vec ? D / 4 : D));
 			a.dd = make_fastdiv((unsigned)D);
 			hipLaunchKernelGGL(ln_dx_lds_kernel, dim3((unsigned)((R + rw - 1) / rw)), dim3(256),
-			                   ((size_t)3 * rw * (D + 1) + D + 4 * rw) * sizeof(float), s, a);
+			                   ((size_t)2 * rw * (D + 1) + D + 4 * rw) * sizeof(float), s, a);
 			const hipError_t e = hipGetLastError();
 			if (e != hipSuccess) return e;
 		}
@@ -1080,9 +1127,12 @@ hipError_t layernorm_backward(const float* gy, const float* x, const float* gamm
 			hipLaunchKernelGGL(ln_dgamma_small_kernel, dim3((unsigned)((D + kLnSmallCols - 1) / kLnSmallCols)),
 			                   dim3(kLnSmallThreads), 0, s, gy, x, mean, inv_std, (int)R, D, dgamma, dgamma_first, dbeta,
 			                   dbeta_first);
+		else if ((dgamma || dbeta) && D % 4 == 0 && aligned16(gy) && aligned16(x))
+			hipLaunchKernelGGL(ln_dgamma_kernel<true>, dim3((unsigned)((D + kLnCols - 1) / kLnCols)), dim3(kLnThreads), 0, s,
+			                   gy, x, mean, inv_std, R, D, dgamma, dgamma_first, dbeta, dbeta_first);
 		else if (dgamma || dbeta)
-			hipLaunchKernelGGL(ln_dgamma_kernel, dim3((unsigned)((D + kLnCols - 1) / kLnCols)), dim3(kLnThreads), 0, s, gy, x,
-			                   mean, inv_std, R, D, dgamma, dgamma_first, dbeta, dbeta_first);
+			hipLaunchKernelGGL(ln_dgamma_kernel<false>, dim3((unsigned)((D + kLnCols - 1) / kLnCols)), dim3(kLnThreads), 0, s,
+			                   gy, x, mean, inv_std, R, D, dgamma, dgamma_first, dbeta, dbeta_first);
 		return hipGetLastError();
 	}
 	LnBwdArgs a{};

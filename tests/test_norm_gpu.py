@@ -197,7 +197,8 @@ def ln_inputs(shape, seed):
             rng.uniform(-1, 1, D).astype(np.float32), rng.normal(size=shape).astype(np.float32))
 
 
-LN_CASES = [(16, 64, 64), (40, 30, 16), (3, 7, 33), (2, 515), (1, 4), (300, 1), (256, 512), (1023, 17), (1025, 8)]
+LN_CASES = [(16, 64, 64), (40, 30, 16), (3, 7, 33), (2, 515), (1, 4), (300, 1), (256, 512), (1023, 17), (1025, 8),
+            (3001, 40), (8, 1024, 512), (1201, 7)]
 
 
 @pytest.mark.parametrize("shape", LN_CASES)
