@@ -296,6 +296,9 @@ def tensor_sum0(src, dst, combine=0, stream=None):
 
 def zero_many(tensors, stream=None):
     """Every float32 device tensor in `tensors` filled with +0 in one launch per 32 (nnh_zero_many)."""
+    import torch
+    for t in tensors:
+        assert t.dtype == torch.float32 and t.is_cuda and t.is_contiguous(), "zero_many takes contiguous float32 device tensors"
     ptrs = (C.c_void_p * max(1, len(tensors)))(*[t.data_ptr() for t in tensors])
     counts = (C.c_size_t * max(1, len(tensors)))(*[t.numel() for t in tensors])
     check(lib().nnh_zero_many(C.cast(ptrs, C.c_void_p), C.cast(counts, C.c_void_p), len(tensors), _stream(stream)))
