@@ -923,14 +923,32 @@ __global__ void __launch_bounds__(kLnSmallThreads) ln_dgamma_small_kernel(
 	__syncthreads();
 	if (tid >= 2 * kLnSmallCols) return;
 	const float* v = &buf[tid / kLnSmallCols][0][c];
-	float acc = 0.0f;
+	// rows in order, the next sixteen rows' reads in flight while sixteen are added
+	float acc = 0.0f, t0[16], t1[16];
 	int i = 0;
-	for (; i + 16 <= R; i += 16) {
-		float t[16];
+	bool have0 = R >= 16;  // t0 holds rows i .. i + 15
+	if (have0) {
 #pragma unroll
-		for (int u = 0; u < 16; ++u) t[u] = v[(i + u) * kLnSmallCols];
+		for (int u = 0; u < 16; ++u) t0[u] = v[u * kLnSmallCols];
+	}
+	while (i + 32 <= R) {
 #pragma unroll
-		for (int u = 0; u < 16; ++u) acc = acc + t[u];
+		for (int u = 0; u < 16; ++u) t1[u] = v[(i + 16 + u) * kLnSmallCols];
+#pragma unroll
+		for (int u = 0; u < 16; ++u) acc = acc + t0[u];
+		have0 = i + 48 <= R;
+		if (have0) {
+#pragma unroll
+			for (int u = 0; u < 16; ++u) t0[u] = v[(i + 32 + u) * kLnSmallCols];
+		}
+#pragma unroll
+		for (int u = 0; u < 16; ++u) acc = acc + t1[u];
+		i += 32;
+	}
+	if (have0 && i + 16 <= R) {
+#pragma unroll
+		for (int u = 0; u < 16; ++u) acc = acc + t0[u];
+		i += 16;
 	}
 	for (; i < R; ++i) acc = acc + v[i * kLnSmallCols];
 	if (c0 + c >= D) return;
