@@ -8,10 +8,12 @@
 //      memory one row per step), against up to 80 rows k in five 16-wide units (B operand: W[co][k], staged in LDS
 //      a chunk of 64 output channels at a time); the chains never leave the accumulators across chunks.
 //   2. The dcol tile goes to LDS, and each dx element of the group gathers its taps from there, in (ph, pw) order.
-// Same bits as the batched GEMM + col2im path, with no dcol in HBM. Two shapes of workgroup: 4 waves and up to 80
-// dcol rows (Ho*Wo <= 256, a deeper layer), and 16 waves and up to 16 rows (Ho*Wo <= 1024 and kh*kw <= 16, a first
-// layer such as 28 x 28 with Cin = 1, where one row of W^T per tap is all a sample needs). Otherwise the caller uses
-// the batched GEMM + col2im path.
+// Same bits as the batched GEMM + col2im path, with no dcol in HBM. Three shapes of workgroup: 4 waves and up to 80
+// dcol rows (Ho*Wo <= 256, a deeper layer); for a first layer (Ho*Wo <= 1024 and kh*kw <= 16, such as 28 x 28 with
+// Cin = 1, where one row of W^T per tap is all a sample needs), 4 waves and up to 16 rows on a band of dx rows when
+// the stride is 1 (the band's output rows, halo included, in 256 positions: a 28 x 28 plane is four bands of seven
+// rows, four workgroups a sample), else 16 waves and up to 16 rows on the whole plane. Otherwise the caller uses the
+// batched GEMM + col2im path.
 #include "conv.hpp"
 
 #include <algorithm>
@@ -35,6 +37,9 @@ struct DxShape {
 };
 constexpr DxShape kDxDeep{4, 80};
 constexpr DxShape kDxFirst{16, 16};
+constexpr DxShape kDxBand{4, 16};  // kDxFirst's rows on a band of a stride-1 plane's rows
+
+constexpr bool same_shape(const DxShape& a, const DxShape& b) { return a.nw == b.nw && a.rows == b.rows; }
 
 using M16 = Mfma<kMf16>;
 
@@ -45,14 +50,16 @@ struct DxArgs {
 	float* dx;        // {N, Cin, H, W}
 	ConvGeom geo;
 	int cout, cg, groups, total, first;
-	int hwp;          // LDS row stride of the dcol tile (a multiple of 4, > hw)
-	FastDiv plane, width, stride;  // division by H*W, W and the stride
+	int bands, band_rows;  // stride 1 only: a workgroup takes band_rows rows of dx (bands per sample), else 1 and H
+	int hwp;          // LDS row stride of the dcol tile (a multiple of 4, > the positions a workgroup computes)
+	FastDiv plane, width, stride;  // division by band_rows*W, W and the stride
 };
 
 // The taps of a 3x3, stride-1 convolution, unrolled: the same order and the same additions as gather_taps. The
 // nine reads are unconditional (positions clamped into the row) so that all are in flight at once; a tap outside
 // the output plane is dropped by a select, which leaves the sum exactly as skipping it would.
-__device__ __forceinline__ float gather_taps_3x3(const float* tile, const DxArgs& a, int c, int ih, int iw, float v) {
+__device__ __forceinline__ float gather_taps_3x3(const float* tile, const DxArgs& a, int q0, int q1, int c, int ih, int iw,
+                                                 float v) {
 	const ConvGeom& G = a.geo;
 	float x[9];
 	bool ok[9];
@@ -60,7 +67,7 @@ __device__ __forceinline__ float gather_taps_3x3(const float* tile, const DxArgs
 	for (int ph = 0; ph < 3; ++ph) {
 		const int qh = ih + G.pad - ph;
 		const bool row_ok = qh >= 0 && qh < G.ho;
-		const float* trow = tile + (c * 9 + ph * 3) * a.hwp + min(max(qh, 0), G.ho - 1) * G.wo;
+		const float* trow = tile + (c * 9 + ph * 3) * a.hwp + (min(max(qh, q0), q1 - 1) - q0) * G.wo;
 #pragma unroll
 		for (int pw = 0; pw < 3; ++pw) {
 			const int qw = iw + G.pad - pw;
@@ -73,9 +80,10 @@ __device__ __forceinline__ float gather_taps_3x3(const float* tile, const DxArgs
 	return v;
 }
 
-// The taps of dx element (ih, iw) of channel c from the dcol tile, in (ph, pw) order (col2im_fast_kernel's gather)
+// The taps of dx element (ih, iw) of channel c from the dcol tile, in (ph, pw) order (col2im_fast_kernel's gather);
+// the tile's first row is output row q0
 template <bool STRIDE1>
-__device__ __forceinline__ float gather_taps(const float* tile, const DxArgs& a, int c, int ih, int iw, float v) {
+__device__ __forceinline__ float gather_taps(const float* tile, const DxArgs& a, int q0, int c, int ih, int iw, float v) {
 	const ConvGeom& G = a.geo;
 	for (int ph = 0; ph < G.kh; ++ph) {
 		const int th = ih + G.pad - ph;
@@ -86,7 +94,7 @@ __device__ __forceinline__ float gather_taps(const float* tile, const DxArgs& a,
 			if (qh * G.stride != th) continue;
 		}
 		if (qh >= G.ho) continue;
-		const float* trow = tile + (c * G.kh + ph) * G.kw * a.hwp + qh * G.wo;
+		const float* trow = tile + (c * G.kh + ph) * G.kw * a.hwp + (qh - q0) * G.wo;
 		for (int pw = 0; pw < G.kw; ++pw) {
 			const int tw = iw + G.pad - pw;
 			int qw = tw;
@@ -109,9 +117,15 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2)
 	const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
 	const ConvGeom& G = a.geo;
 	const int khkw = G.kh * G.kw, hw = G.ho * G.wo, K = G.cin * khkw;
-	const int lid = xcd_remap(blockIdx.x, a.total);  // the channel groups of one sample share an XCD's L2
-	const int n = lid / a.groups, grp = lid - n * a.groups;
+	const int lid = xcd_remap(blockIdx.x, a.total);  // the channel groups and bands of one sample share an XCD's L2
+	const int gb = lid / a.bands, band = lid - gb * a.bands;
+	const int n = gb / a.groups, grp = gb - n * a.groups;
 	const int c0 = grp * a.cg, cg = min(a.cg, G.cin - c0), rows = cg * khkw, k0 = c0 * khkw;
+	// dx rows r0 .. r0 + band_rows - 1 take taps from output rows q0 .. q1 - 1 (stride 1: qh = ih + pad - ph)
+	const int r0 = band * a.band_rows;
+	const int q0 = a.bands > 1 ? max(0, r0 + G.pad - G.kh + 1) : 0;
+	const int q1 = a.bands > 1 ? min(G.ho, r0 + a.band_rows + G.pad) : G.ho;
+	const int p_lo = q0 * G.wo, np = (q1 - q0) * G.wo;  // the positions this workgroup computes
 	float* wl = sm;                          // [kDxRows][kDxWLd]: W^T for a chunk of output channels
 	float* tile = sm + kDxRows * kDxWLd;     // [cg * khkw][hwp]: the group's dcol rows
 	const float* gn = a.g + (int64_t)n * a.cout * hw;
@@ -123,8 +137,8 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2)
 	for (int u = 0; u < kDxRows / 16; ++u)
 #pragma unroll
 		for (int r = 0; r < M16::NV; ++r) acc[u][r] = 0.0f;
-	const int pos = min(64 * wave + M16::arow(lane), hw - 1);  // positions past hw compute values never stored
-	const bool pos_here = 64 * wave < hw;
+	const int pos = p_lo + min(64 * wave + M16::arow(lane), np - 1);  // positions past np compute values never stored
+	const bool pos_here = 64 * wave < np;
 	// gradient rows co .. co+kDxACh-1 at this lane's position (rows clamped into range, never used past cout)
 	auto load_g = [&](float (&dst)[kDxACh], int co) {
 		if (an) {  // ops.cpp:1439-1443's mask, applied as the rows are read
@@ -203,7 +217,7 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2)
 #pragma unroll
 			for (int t = 0; t < M16::NV / 4; ++t) {
 				const int p0 = 64 * wave + M16::crow(4 * t, lane);
-				if (k < rows && p0 < hw)
+				if (k < rows && p0 < np)
 					*reinterpret_cast<f32x4*>(tile + k * a.hwp + p0) =
 					    f32x4{acc[u][4 * t], acc[u][4 * t + 1], acc[u][4 * t + 2], acc[u][4 * t + 3]};
 			}
@@ -212,40 +226,63 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2)
 	__syncthreads();
 
 	// 2b. col2im for the group's channels: every dx element adds its taps in (ph, pw) order
-	const int plane = G.h * G.w;
-	float* dxn = a.dx + ((int64_t)n * G.cin + c0) * plane;
+	// elements e = (c, ih - r0, iw) over the group's channels and the band's rows; rows past H (a short last band)
+	// are computed at row H - 1 and not stored
+	const int plane = G.h * G.w, bplane = a.band_rows * G.w, total = cg * bplane;
+	float* dxn = a.dx + ((int64_t)n * G.cin + c0) * plane + r0 * G.w;
 	if (G.stride == 1 && G.kh == 3 && G.kw == 3) {  // uniform: two elements per thread at a time
-		const int total = cg * plane;
 		for (int e0 = tid; e0 < total; e0 += 2 * kThreads) {
-			int c[2], ih[2], iw[2];
+			int c[2], ih[2], iw[2], at[2];
+			bool keep[2];
 			float v[2];
 #pragma unroll
 			for (int h = 0; h < 2; ++h) {
 				const int e = min(e0 + kThreads * h, total - 1);  // a repeated element is computed, stored once
 				c[h] = (int)fdiv((unsigned)e, a.plane);
-				const int rem = e - c[h] * plane;
-				ih[h] = (int)fdiv((unsigned)rem, a.width);
-				iw[h] = rem - ih[h] * G.w;
-				v[h] = a.first ? 0.0f : dxn[e];
+				const int rem = e - c[h] * bplane, rr = (int)fdiv((unsigned)rem, a.width);
+				iw[h] = rem - rr * G.w;
+				ih[h] = min(r0 + rr, G.h - 1);
+				keep[h] = e0 + kThreads * h < total && r0 + rr < G.h;
+				at[h] = c[h] * plane + (ih[h] - r0) * G.w + iw[h];
+				v[h] = a.first ? 0.0f : dxn[at[h]];
 			}
 #pragma unroll
-			for (int h = 0; h < 2; ++h) v[h] = gather_taps_3x3(tile, a, c[h], ih[h], iw[h], v[h]);
-			dxn[e0] = v[0];
-			if (e0 + kThreads < total) dxn[e0 + kThreads] = v[1];
+			for (int h = 0; h < 2; ++h) v[h] = gather_taps_3x3(tile, a, q0, q1, c[h], ih[h], iw[h], v[h]);
+#pragma unroll
+			for (int h = 0; h < 2; ++h)
+				if (keep[h]) dxn[at[h]] = v[h];
 		}
 	} else {
-		for (int e = tid; e < cg * plane; e += kThreads) {
-			const int c = (int)fdiv((unsigned)e, a.plane), rem = e - c * plane;
-			const int ih = (int)fdiv((unsigned)rem, a.width), iw = rem - ih * G.w;
-			const float v0 = a.first ? 0.0f : dxn[e];
-			dxn[e] = G.stride != 1 ? gather_taps<false>(tile, a, c, ih, iw, v0) : gather_taps<true>(tile, a, c, ih, iw, v0);
+		for (int e = tid; e < total; e += kThreads) {
+			const int c = (int)fdiv((unsigned)e, a.plane), rem = e - c * bplane;
+			const int rr = (int)fdiv((unsigned)rem, a.width), iw = rem - rr * G.w, ih = r0 + rr;
+			if (ih >= G.h) continue;
+			const int at = c * plane + rr * G.w + iw;
+			const float v0 = a.first ? 0.0f : dxn[at];
+			dxn[at] = G.stride != 1 ? gather_taps<false>(tile, a, q0, c, ih, iw, v0)
+			                        : gather_taps<true>(tile, a, q0, c, ih, iw, v0);
 		}
 	}
 }
 
-int dx_hwp(const ConvGeom& g) { return (g.ho * g.wo + 3) / 4 * 4 + 4; }
+// Rows of dx per band for kDxBand, balanced over the bands, with a band's output rows (band rows + kh - 1 at most,
+// stride 1) within the workgroup's 64 * nw positions; 0 when not even one row fits
+int dx_band_rows(const ConvGeom& g) {
+	if (g.stride != 1 || g.h < 1 || g.wo < 1) return 0;
+	const int most = 64 * kDxBand.nw / g.wo - (g.kh - 1);
+	if (most < 1) return 0;
+	const int bands = (g.h + most - 1) / most;
+	return (g.h + bands - 1) / bands;
+}
 
-int dx_lds_bytes(const ConvGeom& g, const DxShape& sh, int cg) { return (sh.rows * kDxWLd + cg * g.kh * g.kw * dx_hwp(g)) * 4; }
+int dx_hwp(const ConvGeom& g, const DxShape& sh) {
+	const int positions = same_shape(sh, kDxBand) ? (dx_band_rows(g) + g.kh - 1) * g.wo : g.ho * g.wo;
+	return (positions + 3) / 4 * 4 + 4;
+}
+
+int dx_lds_bytes(const ConvGeom& g, const DxShape& sh, int cg) {
+	return (sh.rows * kDxWLd + cg * g.kh * g.kw * dx_hwp(g, sh)) * 4;
+}
 
 // Input channels per workgroup: as many as the shape's MFMA rows hold, fewer if the dcol tile would not fit LDS
 int dx_group(const ConvGeom& g, const DxShape& sh) {
@@ -258,6 +295,10 @@ int dx_group(const ConvGeom& g, const DxShape& sh) {
 DxShape dx_shape(const ConvGeom& g) {
 	const int64_t hw = (int64_t)g.ho * g.wo;
 	if (hw >= 1 && hw <= 64 * kDxDeep.nw && g.kh * g.kw <= kDxDeep.rows && dx_group(g, kDxDeep) >= 1) return kDxDeep;
+	// a first layer's plane in bands of rows: more workgroups than samples, each of four waves
+	if (hw >= 1 && hw <= 64 * kDxFirst.nw && g.kh * g.kw <= kDxBand.rows && dx_band_rows(g) >= 1 &&
+	    dx_group(g, kDxBand) >= 1)
+		return kDxBand;
 	if (hw >= 1 && hw <= 64 * kDxFirst.nw && g.kh * g.kw <= kDxFirst.rows && dx_group(g, kDxFirst) >= 1) return kDxFirst;
 	return DxShape{0, 0};
 }
@@ -272,7 +313,8 @@ bool conv_dx_fused_ok(const ConvGeom& g, int64_t samples, int cout) {
 	// channels when it takes the depth cut; this kernel runs one chain over all of them
 	if (depth_cut((int64_t)g.cin * g.kh * g.kw, (int64_t)g.ho * g.wo, cout)) return false;
 	const int64_t groups = (g.cin + dx_group(g, sh) - 1) / dx_group(g, sh);
-	return samples * groups < ((int64_t)1 << 31) && samples * cout * (int64_t)g.ho * g.wo < ((int64_t)1 << 40);
+	const int64_t bands = same_shape(sh, kDxBand) ? (g.h + dx_band_rows(g) - 1) / dx_band_rows(g) : 1;
+	return samples * groups * bands < ((int64_t)1 << 31) && samples * cout * (int64_t)g.ho * g.wo < ((int64_t)1 << 40);
 }
 
 hipError_t conv_dx_fused(const float* gm, const unsigned char* alive, const float* w, float* dx, const ConvGeom& g,
@@ -288,23 +330,22 @@ hipError_t conv_dx_fused(const float* gm, const unsigned char* alive, const floa
 	a.cout = cout;
 	a.cg = dx_group(g, sh);
 	a.groups = (g.cin + a.cg - 1) / a.cg;
-	a.total = (int)(samples * a.groups);
+	const bool band = same_shape(sh, kDxBand);
+	a.band_rows = band ? dx_band_rows(g) : g.h;
+	a.bands = (g.h + a.band_rows - 1) / a.band_rows;
+	a.total = (int)(samples * a.groups * a.bands);
 	a.first = first;
-	a.hwp = dx_hwp(g);
-	a.plane = make_fastdiv((unsigned)(g.h * g.w));
+	a.hwp = dx_hwp(g, sh);
+	a.plane = make_fastdiv((unsigned)(a.band_rows * g.w));
 	a.width = make_fastdiv((unsigned)g.w);
 	a.stride = make_fastdiv((unsigned)g.stride);
 	const int lds = dx_lds_bytes(g, sh, a.cg);
-	const void* fn = sh.nw == kDxDeep.nw ? reinterpret_cast<const void*>(conv_dx_fused_kernel<kDxDeep.nw, kDxDeep.rows>)
-	                                     : reinterpret_cast<const void*>(conv_dx_fused_kernel<kDxFirst.nw, kDxFirst.rows>);
-	hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+	void (*fn)(DxArgs) = same_shape(sh, kDxDeep)  ? conv_dx_fused_kernel<kDxDeep.nw, kDxDeep.rows>
+	                     : same_shape(sh, kDxBand) ? conv_dx_fused_kernel<kDxBand.nw, kDxBand.rows>
+	                                               : conv_dx_fused_kernel<kDxFirst.nw, kDxFirst.rows>;
+	hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize, lds);
 	if (e != hipSuccess) return e;
-	if (sh.nw == kDxDeep.nw)
-		hipLaunchKernelGGL((conv_dx_fused_kernel<kDxDeep.nw, kDxDeep.rows>), dim3((unsigned)a.total), dim3(64 * sh.nw), lds,
-		                   s, a);
-	else
-		hipLaunchKernelGGL((conv_dx_fused_kernel<kDxFirst.nw, kDxFirst.rows>), dim3((unsigned)a.total), dim3(64 * sh.nw),
-		                   lds, s, a);
+	hipLaunchKernelGGL(fn, dim3((unsigned)a.total), dim3(64 * sh.nw), lds, s, a);
 	return hipGetLastError();
 }
 

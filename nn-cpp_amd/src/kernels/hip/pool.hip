@@ -6,7 +6,8 @@
 // Backward: the reference zero-fills a fresh plane and adds g[i] at argmax[i] for i in output order. Here each
 // input element gathers instead, visiting the windows that contain it in output order (no atomics, one writer per
 // element). Offset 0 of a plane also receives the windows that kept offset 0 without containing it; when a plane
-// has such windows its thread walks every output of the plane in order.
+// has such windows its thread walks every output of the plane in order. 2 x 2 windows at stride 2 on even planes
+// (one window per element) take a kernel of their own, a wave per plane.
 #include "pool.hpp"
 
 #include <cmath>
@@ -85,7 +86,7 @@ struct PoolBwdArgs {
 	const uint32_t* arg;
 	float* dx;
 	int h, w, ho, wo, k, s, first;
-	FastDiv w_div, s_div;
+	FastDiv w_div, s_div, wo_div;
 };
 
 // One (n, c) plane per workgroup (ops.cpp:1686-1704). Only the first window contains offset 0, so a later window
@@ -126,6 +127,70 @@ __global__ void __launch_bounds__(256) maxpool_backward_kernel(const PoolBwdArgs
 				}
 		}
 		dx[e] = v;
+	}
+}
+
+// 2 x 2 windows at stride 2 on planes of even height and width: every element lies in exactly one window, so it gets
+// that window's g when the window picked it, and offset 0 also gets the later windows that kept offset 0 (nothing in
+// them beat -inf). A wave owns a plane and its lanes take kPool2Per windows each per pass, with every load of the
+// pass (argmax, g, the four old values) issued before the first use; the first pass looks for windows that kept
+// offset 0 with a ballot, and when a plane has any, lane 0 walks the plane's windows in order for offset 0.
+constexpr int kPool2Per = 4;
+
+__global__ void __launch_bounds__(256) maxpool2x2_backward_kernel(const PoolBwdArgs a, const int64_t planes) {
+	const int lane = threadIdx.x & 63;
+	const int64_t p = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+	if (p >= planes) return;
+	const int out = a.ho * a.wo;
+	const float* g = a.g + p * out;
+	const uint32_t* arg = a.arg + p * out;
+	float* dx = a.dx + p * a.h * a.w;
+	bool walk0 = false;
+	for (int i0 = 0; i0 < out; i0 += 64 * kPool2Per) {
+		uint32_t at[kPool2Per];
+		float gv[kPool2Per];
+		int base[kPool2Per];
+		float2 o0[kPool2Per], o1[kPool2Per];
+#pragma unroll
+		for (int j = 0; j < kPool2Per; ++j) {
+			const int i = min(i0 + 64 * j + lane, out - 1);  // a repeated window is computed, stored once
+			at[j] = arg[i];
+			gv[j] = g[i];
+			const int oh = (int)fdiv((unsigned)i, a.wo_div);
+			base[j] = 2 * oh * a.w + 2 * (i - oh * a.wo);
+			o0[j] = a.first ? make_float2(0.0f, 0.0f) : *reinterpret_cast<const float2*>(dx + base[j]);
+			o1[j] = a.first ? make_float2(0.0f, 0.0f) : *reinterpret_cast<const float2*>(dx + base[j] + a.w);
+		}
+		if (i0 == 0) {
+			bool kept0 = false;
+#pragma unroll
+			for (int j = 0; j < kPool2Per; ++j) {
+				const int i = 64 * j + lane;
+				kept0 = kept0 || (i > 0 && i < out && at[j] == 0u);
+			}
+			for (int i = 64 * kPool2Per + lane; i < out; i += 64) kept0 = kept0 || arg[i] == 0u;
+			walk0 = __ballot(kept0) != 0;
+		}
+#pragma unroll
+		for (int j = 0; j < kPool2Per; ++j) {
+			const uint32_t e = (uint32_t)base[j];
+			if (at[j] == e) o0[j].x = o0[j].x + gv[j];
+			if (at[j] == e + 1) o0[j].y = o0[j].y + gv[j];
+			if (at[j] == e + a.w) o1[j].x = o1[j].x + gv[j];
+			if (at[j] == e + a.w + 1) o1[j].y = o1[j].y + gv[j];
+		}
+		if (i0 == 0 && lane == 0 && walk0) {  // window 0 is lane 0's first: its offset 0 takes every kept-0 window
+			float v = a.first ? 0.0f : dx[0];
+			for (int i = 0; i < out; ++i)
+				if (arg[i] == 0u) v = v + g[i];
+			o0[0].x = v;
+		}
+#pragma unroll
+		for (int j = 0; j < kPool2Per; ++j)
+			if (i0 + 64 * j + lane < out) {
+				*reinterpret_cast<float2*>(dx + base[j]) = o0[j];
+				*reinterpret_cast<float2*>(dx + base[j] + a.w) = o1[j];
+			}
 	}
 }
 
@@ -172,9 +237,13 @@ hipError_t maxpool2d_backward(const float* g, const uint32_t* arg, float* dx, in
 	a.wo = (w - k) / s + 1;
 	a.w_div = make_fastdiv((unsigned)w);
 	a.s_div = make_fastdiv((unsigned)s);
+	a.wo_div = make_fastdiv((unsigned)a.wo);
 	if (planes == 0 || (int64_t)h * w == 0) return hipSuccess;
 	if (planes > 0x7fffffff) return hipErrorInvalidConfiguration;
-	hipLaunchKernelGGL(maxpool_backward_kernel, dim3((unsigned)planes), dim3(256), 0, st, a);
+	if (k == 2 && s == 2 && h % 2 == 0 && w % 2 == 0 && reinterpret_cast<uintptr_t>(dx) % 8 == 0)
+		hipLaunchKernelGGL(maxpool2x2_backward_kernel, dim3((unsigned)((planes + 3) / 4)), dim3(256), 0, st, a, planes);
+	else
+		hipLaunchKernelGGL(maxpool_backward_kernel, dim3((unsigned)planes), dim3(256), 0, st, a);
 	return hipGetLastError();
 }
 

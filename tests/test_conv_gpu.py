@@ -112,18 +112,20 @@ def test_direct_and_gemm_paths_match_the_oracle(gpu, oracle):
 
 
 # dx with dcol kept on chip (Ho*Wo <= 256): input-channel groups that do not divide Cin, Cout over several 64-wide
-# chunks with a ragged end, strides, rectangular and large kernels, output planes that do not fill a wave; and
-# Ho*Wo > 256, which takes the batched GEMM and col2im. (N, Cin, H, W, Cout, kh, kw, stride, pad)
+# chunks with a ragged end, strides, rectangular and large kernels, output planes that do not fill a wave; first-layer
+# planes (Ho*Wo <= 1024, kh*kw <= 16) in bands of dx rows or whole; and larger planes, which take the batched GEMM and
+# col2im. (N, Cin, H, W, Cout, kh, kw, stride, pad)
 DX_CASES = [
     (2, 13, 14, 14, 64, 3, 3, 1, 1),    # config 3 conv2's plane; 13 channels: groups of 8 and 5
     (3, 9, 9, 7, 150, 3, 3, 1, 1),      # Cout 150: chunks of 64, 64 and 22
     (2, 5, 11, 11, 7, 5, 5, 2, 2),      # stride 2, 25 taps: 3 channels per group
     (2, 4, 6, 10, 33, 2, 3, 1, 0),      # rectangular kernel, no padding
     (1, 3, 16, 16, 20, 9, 9, 1, 4),     # 81 taps: one channel per group does not fit 80 rows
-    (2, 6, 17, 17, 24, 3, 3, 1, 1),     # 289 outputs: the sixteen-wave shape, one channel per group
-    (2, 1, 28, 28, 32, 3, 3, 1, 1),     # config 3's conv1 plane (784 outputs): sixteen waves
+    (2, 6, 17, 17, 24, 3, 3, 1, 1),     # 289 outputs: bands of 9 and 8 dx rows, one channel per group
+    (2, 1, 28, 28, 32, 3, 3, 1, 1),     # config 3's conv1 plane (784 outputs): four bands of seven rows
+    (2, 3, 24, 20, 10, 3, 3, 1, 0),     # no padding, 396 outputs: two bands, the first row's taps from row 0 only
     (2, 2, 40, 40, 5, 3, 3, 2, 1),      # stride 2, 400 outputs: sixteen waves, the general tap gather
-    (1, 1, 30, 30, 9, 4, 4, 1, 1),      # 16 taps, 841 outputs: sixteen waves
+    (1, 1, 30, 30, 9, 4, 4, 1, 1),      # 16 taps, 841 outputs: six bands of five rows, the general tap gather
     (1, 2, 34, 34, 6, 3, 3, 1, 1),      # 1156 outputs: the GEMM + col2im path
     (2, 8, 8, 8, 512, 3, 3, 1, 1),      # dcol = W^T g (72 x 64 x 512) takes the depth cut: the GEMM + col2im path
 ]

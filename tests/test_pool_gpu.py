@@ -50,6 +50,7 @@ CASES = [
     (2, 2, 7, 9, 2, 2, 85, 1),
     (2, 4, 8, 12, 2, 2, 86, 1),       # the two-output kernel with -inf and NaN windows
     (1, 1, 1, 1, 1, 1, 87, 0),
+    (1, 2, 40, 36, 2, 2, 88, 1),      # 360 windows a plane: a kept-0 window past a wave's first pass
 ]
 
 
