@@ -63,6 +63,14 @@ __global__ void __launch_bounds__(kPwThreads) conv_dwp_kernel(const PwArgs a) {
 	float* gs = sm;                       // [kPwCg][gpitch]: masked gradient rows
 	float* cs = sm + kPwCg * a.gpitch;    // [K][cpitch]: the sample's im2col columns
 
+	// 0. the first batch of the sample's input x_n, loaded now so that its loads and the gradient rows' are in flight
+	// together (stored to LDS in step 2)
+	const float* xs = a.x + (int64_t)n * G.cin * G.h * G.w;
+	const int xtot = G.cin * G.h * G.w;
+	float xv[8];
+#pragma unroll
+	for (int u = 0; u < 8; ++u) xv[u] = xs[min(tid + kPwThreads * u, xtot - 1)];
+
 	// 1. masked gradient rows c0 .. c0 + nc - 1 of sample n: one contiguous block of nc * hw
 	const int64_t row0 = (int64_t)n * a.cout + c0;
 	const float* gsrc = a.g + row0 * hw;
@@ -96,18 +104,18 @@ __global__ void __launch_bounds__(kPwThreads) conv_dwp_kernel(const PwArgs a) {
 			gs[r * a.gpitch + p] = (!asrc || asrc[e]) ? v : 0.0f;
 		}
 	}
-	// 2. the sample's input x_n into LDS (every load of a batch issued before its stores)
+	// 2. the sample's input x_n into LDS (the first batch loaded in step 0; every load of a batch issued before its
+	// stores)
 	float* xl = cs + K * a.cpitch;  // [cin][h][w]
 	{
-		const float* xs = a.x + (int64_t)n * G.cin * G.h * G.w;
-		const int xtot = G.cin * G.h * G.w;
 		for (int b = 0; b < xtot; b += kPwThreads * 8) {
-			float v[8];
+			if (b > 0) {
 #pragma unroll
-			for (int u = 0; u < 8; ++u) v[u] = xs[min(b + tid + kPwThreads * u, xtot - 1)];
+				for (int u = 0; u < 8; ++u) xv[u] = xs[min(b + tid + kPwThreads * u, xtot - 1)];
+			}
 #pragma unroll
 			for (int u = 0; u < 8; ++u)
-				if (b + tid + kPwThreads * u < xtot) xl[b + tid + kPwThreads * u] = v[u];
+				if (b + tid + kPwThreads * u < xtot) xl[b + tid + kPwThreads * u] = xv[u];
 		}
 	}
 	__syncthreads();
