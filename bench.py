@@ -772,6 +772,17 @@ def run_workloads(with_cpu=True, seed=1, warmup=3, runs=15):
     return out
 
 
+def csv_size(key, cfg):
+    """The CSV's size column: run_matmul's n for the square products (runner.cpp:80-96), m x n x k for the other
+    config-5 products, the config number for the op rows."""
+    m = re.match(r"matmul(\d+)_[nt][nt]$", key)
+    if m:
+        return m.group(1)
+    if key.startswith("matmul_"):
+        return key[len("matmul_"):]
+    return str(cfg)
+
+
 def write_csv(path, rows, setup, workloads=()):
     """apps/bench/bench.cpp:112-113's columns, then the GPU columns; one line per GPU row and per CPU baseline."""
     cols = ["config", "label", "threads", "benchmark", "size", "forward_ms", "backward_ms", "optim_ms", "total_ms",
@@ -782,7 +793,7 @@ def write_csv(path, rows, setup, workloads=()):
     for r in rows:
         res = r.result
         back = "backward" in r.key
-        size = r.key.split("_", 1)[1] if r.key.startswith("matmul") else str(r.cfg)
+        size = csv_size(r.key, r.cfg)
         for label, ent, thr in (("gpu-mi355x", res, ""), ("native-pinned", res.get("cpu_baseline"), None),
                                 ("native-1thread", res.get("cpu_1thread"), None)):
             if not ent:
@@ -829,6 +840,68 @@ def row_json(r):
             out[k] = {"ms": round(e["ms"], 4), "threads": e["threads"], "runs": e["runs"],
                       "spread": round(e["spread"], 4), "speedup_gpu": round(e["ms"] / res["ms"], 1)}
     return out
+
+
+LINE_LIMIT = 4096  # bytes: the stdout line the driver parses stays well inside what it keeps of stdout
+
+
+def _r(v, nd):
+    return None if v is None else round(v, nd)
+
+
+def compact_row(row):
+    """One config row as the stdout line carries it (under its key): median device ms, roofline fraction, nn-cpp's pinned CPU
+    ms, and whether the outputs were the same bits over three GPU runs and against nn-cpp (against the exact mode's
+    outputs' bits are not asked of a split-depth row: there `bitwise` is the repeat check alone)."""
+    bits = row.get("bitwise_repeat", False) and row.get("bitwise_vs_nn_cpp", True)
+    if row["key"].endswith("_split"):
+        bits = row.get("bitwise_repeat", False)
+    out = {"ms": _r(row["ms"], 5), "frac": _r(row["roofline"]["frac"], 4), "bitwise": bool(bits)}
+    if not row["key"].endswith("_split"):
+        out["cpu_ms"] = _r((row.get("cpu_baseline") or {}).get("ms"), 3)
+    if "useful_frac" in row["roofline"]:
+        out["useful_frac"] = _r(row["roofline"]["useful_frac"], 4)
+    return out
+
+
+def compact_line(full, strict=True):
+    """The driver's JSON line from the full result: the headline keys, roofline and cpu_baseline, the fused-op
+    figure, and per row only compact_row's fields; the full rows go to a file and to stderr. Past LINE_LIMIT it
+    raises when strict, else first sheds the workloads, the split-depth rows and the fused-op object."""
+    keep = ("metric", "value", "unit", "n_gpus", "steps", "warmup", "settle_launches", "ms_per_step",
+            "higher_is_better", "scaling", "vs_baseline", "dtype", "data", "config", "roofline", "cpu_baseline")
+    line = {k: full.get(k) for k in keep}
+    line["data"] = DATA_SHORT
+    fo = full.get("fused_op")
+    if fo:
+        line["fused_op"] = {"workload": "conv1 conv2d_relu fwd (cfg 3), alive flags", "value": fo["value"],
+                            "unit": fo["unit"], "us": fo["us_per_launch"], "frac": fo["roofline"]["frac"],
+                            "fill_floor_us": (fo.get("fill_floor") or {}).get("us_per_launch"),
+                            "frac_of_fill_floor": (fo.get("fill_floor") or {}).get("conv1_frac_of_floor")}
+    line["configs"] = {r["key"]: compact_row(r) for r in full.get("configs", [])}
+    line["configs_split_depth"] = {r["key"]: compact_row(r) for r in full.get("configs_split_depth", [])}
+    line["workloads"] = [{"workload": w["workload"], "gpu_ms": _r(w.get("gpu", {}).get("total_ms"), 4),
+                          "cpu_ms": _r((w.get("cpu") or {}).get("total_ms"), 4),
+                          "bitwise": w.get("bitwise_vs_nn_cpp")} for w in full.get("workloads", [])]
+    if line["workloads"]:
+        line["workloads_note"] = WORKLOAD_NOTE
+    line["full_rows"] = full.get("full_rows")
+    text = json.dumps(line, separators=(",", ":"))
+    if len(text.encode()) > LINE_LIMIT and not strict:
+        # never lose the line: shed what the full rows also hold, least important first
+        for drop in ("workloads_note", "workloads", "configs_split_depth", "fused_op"):
+            line.pop(drop, None)
+            text = json.dumps(line, separators=(",", ":"))
+            if len(text.encode()) <= LINE_LIMIT:
+                break
+    if len(text.encode()) > LINE_LIMIT:
+        raise ValueError(f"bench line is {len(text.encode())} bytes, over {LINE_LIMIT}")
+    return text
+
+
+DATA_SHORT = "synthetic: nn-cpp's seeded std::mt19937 streams (N(0,1) via numpy PCG64); same buffers on both sides"
+WORKLOAD_NOTE = ("step = forward + zero_grad + backward from a fixed N(0,1) logits gradient, both sides; no loss, "
+                 "no optimizer step (runner.cpp's optim_ms)")
 
 
 def report(with_cpu=True):
@@ -885,7 +958,7 @@ def floor():
         print(f"| {name} | {ms * 1e3:.2f} | {gbps:.0f} | {gbps / PEAK_HBM_GBPS * 100:.1f}% |", flush=True)
 
 
-def main():
+def make_parser():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
@@ -895,6 +968,9 @@ def main():
     ap.add_argument("--no-configs", action="store_true", help="only the headline product (no per-config rows)")
     ap.add_argument("--no-split", action="store_true", help="no rows in the split-depth numerics mode")
     ap.add_argument("--csv", default=None, help="also write the rows as CSV (the reference's bench columns + GPU ones)")
+    ap.add_argument("--full-json", default=os.path.join("gpurun_out", "bench_full.json"), metavar="PATH",
+                    help="where the full rows (every field, split-depth, next rows, workloads) are written; the "
+                         "stdout line carries a compact form")
     ap.add_argument("--report", action="store_true", help="every BASELINE config as a markdown table with fp64 "
                     "checks (not the driver's JSON line)")
     ap.add_argument("--row", default=None, metavar="KEY", help="time one configuration row only (its key, e.g. "
@@ -905,7 +981,11 @@ def main():
     ap.add_argument("--floor", action="store_true", help="launch-cost floor of this GPU: empty kernel, fills, copies")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="only run 5 device-to-device copies of MIB MiB (calibrates rocprofv3 FETCH_SIZE/WRITE_SIZE)")
-    args = ap.parse_args()
+    return ap
+
+
+def main():
+    args = make_parser().parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (this build has no multi-GPU path); --gpus {args.gpus} is not "
               "supported", file=sys.stderr)
@@ -1045,17 +1125,16 @@ def main():
     if hb:
         cpu = {"value": round(flops / (hb["ms"] * 1e-3) / 1e12, 4), "unit": "TFLOP/s", "cores": hb["threads"],
                "kind": "reference",
-               "sample": (f"nn::matmul {m}x{n}x{k} (nn-cpp 2.0.0 NN_NATIVE AVX2/FMA build, -O3 -mavx2 -mfma "
-                          f"-ffp-contract=off) on the same seed-4 inputs, {hb['threads']} threads pinned one per "
-                          f"physical core of {setup['cpu']} (governor {setup['governor']}), median of {hb['runs']} "
-                          f"runs after {hb['warmup']} warm-up")}
+               "sample": (f"nn::matmul {m}^3, nn-cpp NN_NATIVE AVX2 build (oracle/_ref), same seed-4 inputs, "
+                          f"{hb['threads']} threads pinned 1/physical core of {setup['cpu']} ({setup['governor']}), "
+                          f"median of {hb['runs']} after {hb['warmup']} warm-up")}
     conv1 = next((r for r in rows if r.key == "conv1_forward"), None)
     conv1_na = next((r for r in rows if r.key == "conv1_forward_no_alive"), None)
     pool1 = next((r for r in rows if r.key == "pool1_forward"), None)
     conv1_pool1 = next((r for r in rows if r.key == "conv1_pool1_forward"), None)
     fill_gbps = None if fill_floor_ms is None else 4 * 128 * 32 * 784 / (fill_floor_ms * 1e-3) / 1e9
     out = {
-        "metric": "fp32 GEMM TFLOP/s @4096^3 (nn::kernels::sgemm replacement, bit-exact with nn-cpp)",
+        "metric": "fp32 GEMM TFLOP/s @4096^3 + % MI355X fp32 MFMA peak; fused-op GB/s",
         "value": round(value, 3),
         "unit": "TFLOP/s",
         "n_gpus": 1,
@@ -1098,8 +1177,19 @@ def main():
         "workloads": [{k: ({kk: (round(vv, 4) if isinstance(vv, float) else vv) for kk, vv in v.items()}
                            if isinstance(v, dict) else (round(v, 2) if isinstance(v, float) else v))
                        for k, v in w.items()} for w in workloads],
+        "workloads_note": WORKLOAD_NOTE,
+        "full_rows": args.full_json,
     }
-    print(json.dumps(out), flush=True)
+    full = json.dumps(out)
+    try:
+        os.makedirs(os.path.dirname(os.path.abspath(args.full_json)), exist_ok=True)
+        with open(args.full_json, "w") as fh:
+            fh.write(full + "\n")
+    except OSError as e:
+        log(f"full rows not written to {args.full_json}: {e}")
+        out["full_rows"] = None
+    log("full rows: " + full)
+    print(compact_line(out, strict=False), flush=True)
 
 
 if __name__ == "__main__":

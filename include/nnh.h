@@ -69,7 +69,11 @@ typedef struct nnh_epilogue {
  * buffers (src/kernels/gemm.cpp:354, 395, 416, 467).
  *
  * The *_workspace_size queries give, for the same shape arguments as the call, the bytes that call takes (at least
- * what it needs: where a kernel choice depends on pointer alignment, the larger of the two).
+ * what it needs: where a kernel choice depends on pointer alignment, the larger of the two; over both numerics
+ * modes, the larger of the two). One exception: nnh_sgemm_workspace_size cannot see leading dimensions, and a
+ * depth-cut product of at most 16 pieces called with lda or ldb of 2^24 or more needs pieces * m * n * batch_count
+ * floats of partials that it does not count (with a registered workspace smaller than that, the call returns
+ * NNH_ERR_WORKSPACE before launching anything).
  */
 int nnh_set_workspace(void* stream, void* workspace, size_t bytes);
 int nnh_sgemm_workspace_size(size_t m, size_t n, size_t k, size_t batch_count, size_t* bytes);
@@ -87,7 +91,7 @@ int nnh_attention_forward_workspace_size(size_t N, size_t Tq, size_t Tk, size_t 
 int nnh_attention_backward_workspace_size(size_t N, size_t Tq, size_t Tk, size_t D, size_t heads, size_t* bytes);
 
 /*
- * Numerics mode (process-wide; set it before issuing work). NNH_NUMERICS_NNCPP (the default): every result is
+ * Numerics mode. NNH_NUMERICS_NNCPP (the default): every result is
  * nn-cpp's bits, as described above. NNH_NUMERICS_SPLIT_DEPTH: every product with m n <= 2^18 and k >= 256 is
  * computed the way nn-cpp's depth cut computes its products (src/kernels/gemm.cpp:453-485), fused multiply-add
  * chains from +0 over consecutive slices of the depth, added in slice order, then stored or added to C, with a
@@ -97,10 +101,19 @@ int nnh_attention_backward_workspace_size(size_t N, size_t Tq, size_t Tk, size_t
  * compositions), within 4 K 2^-24 sum|a||b| of the exact product, and equal to the oracle's in the same mode; they
  * are no longer nn-cpp's bits for the products the rule cuts differently from nn-cpp.
  */
+#define NNH_NUMERICS_DEFAULT (-1)
 #define NNH_NUMERICS_NNCPP 0
 #define NNH_NUMERICS_SPLIT_DEPTH 1
+/* The process default, for streams without a mode of their own (no counterpart in nn-cpp, which has one
+ * arithmetic). */
 int nnh_set_numerics(int mode);
 int nnh_get_numerics(void);
+/* A stream's own mode (NNH_NUMERICS_DEFAULT: back to the process default), so that callers in one process can run
+ * different modes at once. A call reads its stream's mode once, when it enters the library, and runs wholly in it:
+ * a mode set while another thread enqueues work takes effect from that thread's next call. The *_workspace_size
+ * queries answer for both modes. */
+int nnh_set_stream_numerics(void* stream, int mode);
+int nnh_get_stream_numerics(void* stream);
 
 /* Message of the calling thread's last failed call ("" if none). */
 const char* nnh_last_error(void);

@@ -16,7 +16,7 @@ REPO_ROOT = os.path.dirname(PKG_ROOT)
 HEADER_PATH = os.path.join(REPO_ROOT, "include", "nnh.h")
 
 OK, ERR_INVALID, ERR_SHAPE, ERR_ALIAS, ERR_HIP, ERR_WORKSPACE = 0, 1, 2, 3, 4, 5
-NUMERICS_NNCPP, NUMERICS_SPLIT_DEPTH = 0, 1
+NUMERICS_DEFAULT, NUMERICS_NNCPP, NUMERICS_SPLIT_DEPTH = -1, 0, 1
 BIAS_NONE, BIAS_COL, BIAS_ROW = 0, 1, 2
 MAX_BATCH_DIMS = 4
 
@@ -110,6 +110,8 @@ _EXTRA_DECLS = {
     "nnh_gelu_backward": [_vp, _vp, _vp, _sz, _vp, C.c_int, _vp],
     "nnh_embedding_forward": [_vp, _sz, _sz, _vp, _sz, _vp, _vp],
     "nnh_embedding_backward": [_vp, _vp, _sz, _sz, _sz, _vp, C.c_int, _vp],
+    "nnh_set_stream_numerics": [_vp, C.c_int],
+    "nnh_get_stream_numerics": [_vp],
 }
 
 
@@ -119,6 +121,16 @@ def set_numerics(mode):
     prev = lib().nnh_get_numerics()
     check(lib().nnh_set_numerics(int(mode)))
     return prev
+
+
+def set_stream_numerics(mode, stream=None):
+    """The mode of every call on `stream` (torch's current stream by default); NUMERICS_DEFAULT clears it, and the
+    stream follows the process default again."""
+    check(lib().nnh_set_stream_numerics(_stream(stream), int(mode)))
+
+
+def get_stream_numerics(stream=None):
+    return lib().nnh_get_stream_numerics(_stream(stream))
 
 
 def workspace_size(name, *args):

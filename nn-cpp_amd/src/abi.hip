@@ -157,6 +157,7 @@ const char* nnh_version(void) { return "nnh 0.1.0 (gfx950 fp32 MFMA, bit-exact w
 
 int nnh_sgemm(int trans_a, int trans_b, size_t m, size_t n, size_t k, const float* a, size_t lda, const float* b,
               size_t ldb, float* c, size_t ldc, int accumulate, void* stream) {
+	NumericsScope numerics_scope(stream);
 	GemmCall g;
 	int rc = build_gemm(trans_a, trans_b, m, n, k, a, lda, b, ldb, c, ldc, accumulate, nullptr, nullptr, g);
 	if (rc != NNH_OK) return rc;
@@ -173,6 +174,7 @@ int nnh_sgemm_batched(int trans_a, int trans_b, size_t m, size_t n, size_t k, co
 int nnh_sgemm_config(int trans_a, int trans_b, size_t m, size_t n, size_t k, const float* a, size_t lda,
                      const float* b, size_t ldb, float* c, size_t ldc, int accumulate, const nnh_batch* batch,
                      const nnh_epilogue* epilogue, int config, void* stream) {
+	NumericsScope numerics_scope(stream);
 	GemmCall g;
 	int rc = build_gemm(trans_a, trans_b, m, n, k, a, lda, b, ldb, c, ldc, accumulate, batch, epilogue, g);
 	if (rc != NNH_OK) return rc;
@@ -186,17 +188,21 @@ int nnh_set_workspace(void* stream, void* workspace, size_t bytes) {
 }
 
 int nnh_sgemm_workspace_size(size_t m, size_t n, size_t k, size_t batch_count, size_t* bytes) {
-	return put_bytes(bytes, gemm_workspace_bytes(m, n, k, batch_count));
+	return query_both_modes(bytes, [&](size_t* bytes) {
+		return put_bytes(bytes, gemm_workspace_bytes(m, n, k, batch_count));
+	});
 }
 
 int nnh_matmul_workspace_size(const size_t* a_shape, int a_ndim, const size_t* b_shape, int b_ndim, int trans_a,
                               int trans_b, size_t* bytes) {
-	MatmulPlan plan;
-	const int rc = plan_matmul(a_shape, a_ndim, b_shape, b_ndim, trans_a, trans_b, plan);
-	if (rc != NNH_OK) return rc;
-	size_t count = 1;
-	for (int d = 0; d < plan.batch.ndim; ++d) count *= plan.batch.shape[d];
-	return put_bytes(bytes, gemm_workspace_bytes(plan.m, plan.n, plan.k, count));
+	return query_both_modes(bytes, [&](size_t* bytes) {
+		MatmulPlan plan;
+		const int rc = plan_matmul(a_shape, a_ndim, b_shape, b_ndim, trans_a, trans_b, plan);
+		if (rc != NNH_OK) return rc;
+		size_t count = 1;
+		for (int d = 0; d < plan.batch.ndim; ++d) count *= plan.batch.shape[d];
+		return put_bytes(bytes, gemm_workspace_bytes(plan.m, plan.n, plan.k, count));
+	});
 }
 
 int nnh_set_numerics(int mode) {
@@ -205,7 +211,16 @@ int nnh_set_numerics(int mode) {
 	return NNH_OK;
 }
 
-int nnh_get_numerics(void) { return numerics(); }
+int nnh_get_numerics(void) { return default_numerics(); }
+
+int nnh_set_stream_numerics(void* stream, int mode) {
+	if (mode != NNH_NUMERICS_DEFAULT && mode != NNH_NUMERICS_NNCPP && mode != NNH_NUMERICS_SPLIT_DEPTH)
+		return fail(NNH_ERR_INVALID, "no such numerics mode");
+	set_stream_numerics(stream, mode);
+	return NNH_OK;
+}
+
+int nnh_get_stream_numerics(void* stream) { return stream_numerics(stream); }
 
 int nnh_gemm_config_count(void) { return gemm_config_count(); }
 
@@ -224,6 +239,7 @@ int nnh_matmul_shape(const size_t* a_shape, int a_ndim, const size_t* b_shape, i
 
 int nnh_matmul(const float* a, const size_t* a_shape, int a_ndim, const float* b, const size_t* b_shape, int b_ndim,
                int trans_a, int trans_b, float* out, void* stream) {
+	NumericsScope numerics_scope(stream);
 	MatmulPlan plan;
 	int rc = plan_matmul(a_shape, a_ndim, b_shape, b_ndim, trans_a, trans_b, plan);
 	if (rc != NNH_OK) return rc;

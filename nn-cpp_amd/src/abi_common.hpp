@@ -74,6 +74,19 @@ int check_workspace(void* stream, size_t bytes);
 int maxpool_geometry(size_t H, size_t W, size_t kernel, size_t stride, size_t& ho, size_t& wo);
 // Stores a workspace query's answer.
 int put_bytes(size_t* out, size_t bytes);
+// A workspace query answers for both numerics modes, the larger of the two: the stream a caller sizes a workspace
+// for may run either mode. f(size_t* bytes) is the query in the current mode.
+template <class F>
+int query_both_modes(size_t* bytes, F&& f) {
+	size_t b[2] = {0, 0};
+	const int modes[2] = {kNumericsNnCpp, kNumericsSplitDepth};
+	for (int i = 0; i < 2; ++i) {
+		NumericsScope scope(modes[i], true);
+		const int rc = f(&b[i]);
+		if (rc != NNH_OK) return rc;
+	}
+	return put_bytes(bytes, b[0] > b[1] ? b[0] : b[1]);
+}
 
 // How nn::matmul(a, b, trans_a, trans_b) (src/tensor.cpp:571-641) maps onto one (batched) GEMM.
 struct MatmulPlan {

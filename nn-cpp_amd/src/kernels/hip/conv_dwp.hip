@@ -39,7 +39,9 @@ constexpr int kPwMaxLds = 96 * 1024;
 inline int pw_gpitch(int hw) { return (hw + 63) / 64 * 64 + 8; }
 inline int pw_cpitch(int hw) { return (hw + 63) / 64 * 64 + 4; }
 inline size_t pw_lds_bytes(int hw, int K, int64_t x_plane) {
-	return ((size_t)kPwCg * pw_gpitch(hw) + (size_t)K * pw_cpitch(hw) + (size_t)x_plane) * sizeof(float);
+	// at least one float for the plane: the column build reads element 0 of an empty plane (and discards it)
+	return ((size_t)kPwCg * pw_gpitch(hw) + (size_t)K * pw_cpitch(hw) + (size_t)(x_plane > 0 ? x_plane : 1)) *
+	       sizeof(float);
 }
 
 struct PwArgs {
@@ -68,8 +70,10 @@ __global__ void __launch_bounds__(kPwThreads) conv_dwp_kernel(const PwArgs a) {
 	const float* xs = a.x + (int64_t)n * G.cin * G.h * G.w;
 	const int xtot = G.cin * G.h * G.w;
 	float xv[8];
+	if (xtot > 0) {  // an empty plane (H or W = 0, outputs from the padding alone) has no x to read
 #pragma unroll
-	for (int u = 0; u < 8; ++u) xv[u] = xs[min(tid + kPwThreads * u, xtot - 1)];
+		for (int u = 0; u < 8; ++u) xv[u] = xs[min(tid + kPwThreads * u, xtot - 1)];
+	}
 
 	// 1. masked gradient rows c0 .. c0 + nc - 1 of sample n: one contiguous block of nc * hw
 	const int64_t row0 = (int64_t)n * a.cout + c0;

@@ -160,11 +160,45 @@ GemmArgs make_args(const GemmCall& g, const Config& cf, bool& cut, bool& interio
 }  // namespace
 
 namespace {
-std::atomic<int> g_numerics{kNumericsNnCpp};
+std::atomic<int> g_numerics{kNumericsNnCpp};  // the process default
+std::mutex g_stream_modes_mu;
+std::vector<std::pair<void*, int>> g_stream_modes;  // per-stream overrides (few streams: a short list)
+thread_local int t_call_numerics = -1;              // the mode of the call being issued on this thread, or -1
 }  // namespace
 
 int set_numerics(int mode) { return g_numerics.exchange(mode); }
-int numerics() { return g_numerics.load(std::memory_order_relaxed); }
+int default_numerics() { return g_numerics.load(std::memory_order_relaxed); }
+
+int set_stream_numerics(void* stream, int mode) {
+	std::lock_guard<std::mutex> lk(g_stream_modes_mu);
+	int prev = -1;
+	for (size_t i = 0; i < g_stream_modes.size(); ++i) {
+		if (g_stream_modes[i].first != stream) continue;
+		prev = g_stream_modes[i].second;
+		if (mode < 0) g_stream_modes.erase(g_stream_modes.begin() + (ptrdiff_t)i);
+		else g_stream_modes[i].second = mode;
+		return prev;
+	}
+	if (mode >= 0) g_stream_modes.emplace_back(stream, mode);
+	return prev;
+}
+
+int stream_numerics(void* stream) {
+	{
+		std::lock_guard<std::mutex> lk(g_stream_modes_mu);
+		for (const auto& e : g_stream_modes)
+			if (e.first == stream) return e.second;
+	}
+	return default_numerics();
+}
+
+int numerics() { return t_call_numerics >= 0 ? t_call_numerics : default_numerics(); }
+
+NumericsScope::NumericsScope(void* stream) : prev_(t_call_numerics) {
+	if (prev_ < 0) t_call_numerics = stream_numerics(stream);
+}
+NumericsScope::NumericsScope(int mode, bool) : prev_(t_call_numerics) { t_call_numerics = mode; }
+NumericsScope::~NumericsScope() { t_call_numerics = prev_; }
 
 CutPlan cut_plan(int64_t m, int64_t n, int64_t k) {
 	CutPlan c;

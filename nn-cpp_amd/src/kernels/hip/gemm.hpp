@@ -34,8 +34,26 @@ struct GemmCall {
 // m n <= 2^18 and k >= 256 is cut into pieces whose depth is chosen so that the product fills the GPU (below).
 constexpr int kNumericsNnCpp = 0;
 constexpr int kNumericsSplitDepth = 1;
-int set_numerics(int mode);  // returns the previous mode
+// The mode a call runs in is read once, where it enters the C ABI (NumericsScope): the stream's own mode
+// (set_stream_numerics) if it has one, else the process default (set_numerics). numerics() returns that mode for
+// the rest of the call on the calling thread, so every decision of one call (kernel choice, workspace size,
+// partial layout) sees one mode whatever other threads set meanwhile; outside a call it is the process default.
+int set_numerics(int mode);                      // process default; returns the previous one
+int default_numerics();
+int set_stream_numerics(void* stream, int mode); // mode < 0 clears the stream's own mode; returns the previous (-1: none)
+int stream_numerics(void* stream);               // the stream's mode, else the process default
 int numerics();
+class NumericsScope {
+public:
+	explicit NumericsScope(void* stream);  // nested in another scope on this thread: keeps the outer call's mode
+	NumericsScope(int mode, bool forced);  // a given mode (the workspace queries evaluate both)
+	~NumericsScope();
+	NumericsScope(const NumericsScope&) = delete;
+	NumericsScope& operator=(const NumericsScope&) = delete;
+
+private:
+	int prev_;
+};
 
 // How a product's depth is cut: `pieces` contiguous slices of `piece_k` depth indices (the last one shorter),
 // each a chain from +0, summed in piece order (acc = piece 0, acc += piece 1, ...), then stored or added to C.
@@ -60,7 +78,9 @@ bool pieces_kernel_takes(int64_t m, int64_t n, int64_t k, int64_t batch_count, b
 bool pieces_kernel_takes(const GemmCall& g);  // also: leading dimensions below 2^24
 hipError_t gemm_pieces_launch(const GemmCall& g, hipStream_t s);
 
-// Floats of workspace a call needs: the partial sums of a depth cut the pieces kernel does not take, else 0.
+// Floats of workspace a call needs: the partial sums of a depth cut the pieces kernel does not take, else 0. The
+// shape-only overload (plans and workspace queries) assumes leading dimensions below 2^24, which every op's own
+// products have (their leading dimensions are extents of tensors whose cut dimensions are below 2^24).
 int64_t gemm_workspace_floats(const GemmCall& g);
 int64_t gemm_workspace_floats(int64_t m, int64_t n, int64_t k, int64_t batch_count, bool gather = false);
 

@@ -67,6 +67,7 @@ size_t nnh_sgemm_noalloc_max_workspace(void) { return kScratchFloats * sizeof(fl
 
 int nnh_sgemm_noalloc(int trans_a, int trans_b, size_t m, size_t n, size_t k, const float* a, size_t lda,
                       const float* b, size_t ldb, float* c, size_t ldc, int accumulate, void* stream) {
+	NumericsScope numerics_scope(stream);
 	GemmCall g;
 	int rc = build_gemm(trans_a, trans_b, m, n, k, a, lda, b, ldb, c, ldc, accumulate, nullptr, nullptr, g);
 	if (rc != NNH_OK) return rc;

@@ -102,22 +102,27 @@ size_t attention_forward_ws(const AttnGeom& a) {
 extern "C" {
 
 int nnh_attention_forward_workspace_size(size_t N, size_t Tq, size_t Tk, size_t D, size_t heads, size_t* bytes) {
-	AttnGeom a;
-	const int rc = check_attention(N, Tq, Tk, D, heads, 0, a);
-	if (rc != NNH_OK) return rc;
-	return put_bytes(bytes, attention_forward_ws(a));
+	return query_both_modes(bytes, [&](size_t* bytes) {
+		AttnGeom a;
+		const int rc = check_attention(N, Tq, Tk, D, heads, 0, a);
+		if (rc != NNH_OK) return rc;
+		return put_bytes(bytes, attention_forward_ws(a));
+	});
 }
 
 int nnh_attention_backward_workspace_size(size_t N, size_t Tq, size_t Tk, size_t D, size_t heads, size_t* bytes) {
-	AttnGeom a;
-	const int rc = check_attention(N, Tq, Tk, D, heads, 0, a);
-	if (rc != NNH_OK) return rc;
-	return put_bytes(bytes, attention_backward_plan(a).total);
+	return query_both_modes(bytes, [&](size_t* bytes) {
+		AttnGeom a;
+		const int rc = check_attention(N, Tq, Tk, D, heads, 0, a);
+		if (rc != NNH_OK) return rc;
+		return put_bytes(bytes, attention_backward_plan(a).total);
+	});
 }
 
 int nnh_attention_forward(const float* q, const float* k, const float* v, size_t N, size_t Tq, size_t Tk, size_t D,
                           size_t heads, const float* key_padding_mask, int causal, float* out, float* probs,
                           void* stream) {
+	NumericsScope numerics_scope(stream);
 	AttnGeom a;
 	int rc = check_attention(N, Tq, Tk, D, heads, causal, a);
 	if (rc != NNH_OK) return rc;
@@ -160,6 +165,7 @@ int nnh_attention_backward(const float* g, const float* q, const float* k, const
                            size_t N, size_t Tq, size_t Tk, size_t D, size_t heads, const float* key_padding_mask,
                            int causal, float* dq, int dq_first, float* dk, int dk_first, float* dv, int dv_first,
                            void* stream) {
+	NumericsScope numerics_scope(stream);
 	AttnGeom a;
 	int rc = check_attention(N, Tq, Tk, D, heads, causal, a);
 	if (rc != NNH_OK) return rc;

@@ -117,24 +117,29 @@ extern "C" {
 
 int nnh_conv2d_forward_workspace_size(size_t N, size_t Cin, size_t H, size_t W, size_t Cout, size_t kh, size_t kw,
                                       int stride, int padding, size_t* bytes) {
-	ConvGeom g;
-	const int rc = conv_geometry(N, Cin, H, W, Cout, kh, kw, stride, padding, g);
-	if (rc != NNH_OK) return rc;
-	return put_bytes(bytes, conv_forward_ws(g, N, Cout));
+	return query_both_modes(bytes, [&](size_t* bytes) {
+		ConvGeom g;
+		const int rc = conv_geometry(N, Cin, H, W, Cout, kh, kw, stride, padding, g);
+		if (rc != NNH_OK) return rc;
+		return put_bytes(bytes, conv_forward_ws(g, N, Cout));
+	});
 }
 
 int nnh_conv2d_backward_workspace_size(size_t N, size_t Cin, size_t H, size_t W, size_t Cout, size_t kh, size_t kw,
                                        int stride, int padding, int with_alive, int want_dx, int want_dw, int want_db,
                                        size_t* bytes) {
-	ConvGeom g;
-	const int rc = conv_geometry(N, Cin, H, W, Cout, kh, kw, stride, padding, g);
-	if (rc != NNH_OK) return rc;
-	return put_bytes(bytes, conv_backward_plan(g, N, Cout, with_alive, want_dx, want_dw, want_db).total);
+	return query_both_modes(bytes, [&](size_t* bytes) {
+		ConvGeom g;
+		const int rc = conv_geometry(N, Cin, H, W, Cout, kh, kw, stride, padding, g);
+		if (rc != NNH_OK) return rc;
+		return put_bytes(bytes, conv_backward_plan(g, N, Cout, with_alive, want_dx, want_dw, want_db).total);
+	});
 }
 
 int nnh_conv2d_forward(const float* x, size_t N, size_t Cin, size_t H, size_t W, const float* w, size_t Cout,
                        size_t kh, size_t kw, const float* bias, int stride, int padding, int fuse_relu, float* y,
                        unsigned char* alive, void* stream) {
+	NumericsScope numerics_scope(stream);
 	ConvGeom g;
 	int rc = conv_geometry(N, Cin, H, W, Cout, kh, kw, stride, padding, g);
 	if (rc != NNH_OK) return rc;
@@ -167,6 +172,7 @@ int nnh_conv2d_relu_maxpool2d_forward(const float* x, size_t N, size_t Cin, size
                                       size_t Cout, size_t kh, size_t kw, const float* bias, int stride, int padding,
                                       size_t pool_kernel, size_t pool_stride, float* y, unsigned char* alive,
                                       float* pooled, unsigned int* argmax, void* stream) {
+	NumericsScope numerics_scope(stream);
 	ConvGeom g;
 	int rc = conv_geometry(N, Cin, H, W, Cout, kh, kw, stride, padding, g);
 	if (rc != NNH_OK) return rc;
@@ -197,6 +203,7 @@ int nnh_conv2d_relu_maxpool2d_forward(const float* x, size_t N, size_t Cin, size
 int nnh_conv2d_backward(const float* g, const float* x, const float* w, const unsigned char* alive, size_t N,
                         size_t Cin, size_t H, size_t W, size_t Cout, size_t kh, size_t kw, int stride, int padding,
                         float* dx, int dx_first, float* dw, int dw_first, float* db, int db_first, void* stream) {
+	NumericsScope numerics_scope(stream);
 	ConvGeom geo;
 	int rc = conv_geometry(N, Cin, H, W, Cout, kh, kw, stride, padding, geo);
 	if (rc != NNH_OK) return rc;

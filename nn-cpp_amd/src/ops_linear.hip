@@ -43,20 +43,25 @@ size_t linear_backward_ws(const size_t* lead, int nlead, size_t M, size_t K, siz
 extern "C" {
 
 int nnh_linear_forward_workspace_size(size_t M, size_t K, size_t n, size_t* bytes) {
-	return put_bytes(bytes, gemm_workspace_bytes(M, n, K, 1));
+	return query_both_modes(bytes, [&](size_t* bytes) {
+		return put_bytes(bytes, gemm_workspace_bytes(M, n, K, 1));
+	});
 }
 
 int nnh_linear_backward_workspace_size(const size_t* lead, int nlead, size_t K, size_t n, int want_dx, int want_dw,
                                        int want_db, size_t* bytes) {
-	if (nlead > 0 && !lead) return fail(NNH_ERR_INVALID, "lead is null");
-	if (nlead < 1) return fail(NNH_ERR_SHAPE, "linear input needs at least 2 dimensions");
-	size_t M = 0;
-	if (!product_fits(lead, nlead, M)) return fail(NNH_ERR_INVALID, "input size overflows");
-	return put_bytes(bytes, linear_backward_ws(lead, nlead, M, K, n, want_dx, want_dw, want_db));
+	return query_both_modes(bytes, [&](size_t* bytes) {
+		if (nlead > 0 && !lead) return fail(NNH_ERR_INVALID, "lead is null");
+		if (nlead < 1) return fail(NNH_ERR_SHAPE, "linear input needs at least 2 dimensions");
+		size_t M = 0;
+		if (!product_fits(lead, nlead, M)) return fail(NNH_ERR_INVALID, "input size overflows");
+		return put_bytes(bytes, linear_backward_ws(lead, nlead, M, K, n, want_dx, want_dw, want_db));
+	});
 }
 
 int nnh_linear_forward(const float* x, size_t M, size_t K, const float* w, size_t n, const float* bias, int relu,
                        float* y, void* stream) {
+	NumericsScope numerics_scope(stream);
 	if (M > 0 && n > 0 && !bias) return fail(NNH_ERR_INVALID, "bias is null");
 	nnh_epilogue ep{NNH_BIAS_COL, relu ? 1 : 0, bias, nullptr};
 	GemmCall g;
@@ -69,6 +74,7 @@ int nnh_linear_forward(const float* x, size_t M, size_t K, const float* w, size_
 int nnh_linear_backward(const float* g, const float* x, const float* w, const size_t* lead, int nlead, size_t K,
                         size_t n, float* dx, int dx_first, float* dw, int dw_first, float* db, int db_first,
                         void* stream) {
+	NumericsScope numerics_scope(stream);
 	if (nlead > 0 && !lead) return fail(NNH_ERR_INVALID, "lead is null");
 	if (nlead < 1) return fail(NNH_ERR_SHAPE, "linear input needs at least 2 dimensions");
 	size_t M = 0;

@@ -160,26 +160,29 @@ extern "C" {
 
 int nnh_matmul_backward_workspace_size(const size_t* a_shape, int a_ndim, const size_t* b_shape, int b_ndim,
                                        int b_transposed, int want_da, int want_db, size_t* bytes) {
-	Plan p;
-	const int rc = plan_backward(nullptr, nullptr, a_shape, a_ndim, nullptr, b_shape, b_ndim, b_transposed ? 1 : 0,
-	                             want_da, want_db, 0, 0, p);
-	if (rc != NNH_OK) return rc;
-	if (p.fold) {
-		const size_t K = b_transposed ? b_shape[1] : b_shape[0], n = b_transposed ? b_shape[0] : b_shape[1];
-		size_t M = 1;
-		for (int d = 0; d < a_ndim; ++d) M *= a_shape[d];
-		M = K ? M / K : 0;
-		return put_bytes(bytes, std::max(want_da ? gemm_workspace_bytes(M, K, n, 1) : 0,
-		                                 want_db ? (b_transposed ? gemm_workspace_bytes(n, K, M, 1)
-		                                                         : gemm_workspace_bytes(K, n, M, 1))
-		                                         : 0));
-	}
-	return put_bytes(bytes, p.total);
+	return query_both_modes(bytes, [&](size_t* bytes) {
+		Plan p;
+		const int rc = plan_backward(nullptr, nullptr, a_shape, a_ndim, nullptr, b_shape, b_ndim, b_transposed ? 1 : 0,
+		                             want_da, want_db, 0, 0, p);
+		if (rc != NNH_OK) return rc;
+		if (p.fold) {
+			const size_t K = b_transposed ? b_shape[1] : b_shape[0], n = b_transposed ? b_shape[0] : b_shape[1];
+			size_t M = 1;
+			for (int d = 0; d < a_ndim; ++d) M *= a_shape[d];
+			M = K ? M / K : 0;
+			return put_bytes(bytes, std::max(want_da ? gemm_workspace_bytes(M, K, n, 1) : 0,
+			                                 want_db ? (b_transposed ? gemm_workspace_bytes(n, K, M, 1)
+			                                                         : gemm_workspace_bytes(K, n, M, 1))
+			                                         : 0));
+		}
+		return put_bytes(bytes, p.total);
+	});
 }
 
 int nnh_matmul_backward(const float* g, const float* a, const size_t* a_shape, int a_ndim, const float* b,
                         const size_t* b_shape, int b_ndim, int b_transposed, float* da, int da_first, float* db,
                         int db_first, void* stream) {
+	NumericsScope numerics_scope(stream);
 	const int bt = b_transposed ? 1 : 0;
 	Plan p;
 	int rc = plan_backward(g, a, a_shape, a_ndim, b, b_shape, b_ndim, bt, da != nullptr, db != nullptr, da_first,

@@ -423,6 +423,30 @@ void misc() {
 	auto a = buf(64), b = buf(64), c = buf(64);
 	EXPECT(nnh_sgemm(0, 0, 4, 4, 4, a.data(), 4, b.data(), 4, c.data(), 4, 0, nullptr), HIP);
 	EXPECT(nnh_set_numerics(NNH_NUMERICS_NNCPP), OK);
+	// a stream's own mode, beside the process default
+	void* s1 = reinterpret_cast<void*>(uintptr_t(0x1000));
+	void* s2 = reinterpret_cast<void*>(uintptr_t(0x2000));
+	EXPECT(nnh_set_stream_numerics(s1, 7), INV);
+	EXPECT(nnh_set_stream_numerics(s1, NNH_NUMERICS_SPLIT_DEPTH), OK);
+	EXPECT(nnh_get_stream_numerics(s1) == NNH_NUMERICS_SPLIT_DEPTH ? OK : INV, OK);
+	EXPECT(nnh_get_stream_numerics(s2) == NNH_NUMERICS_NNCPP ? OK : INV, OK);
+	EXPECT(nnh_get_numerics() == NNH_NUMERICS_NNCPP ? OK : INV, OK);
+	EXPECT(nnh_set_stream_numerics(s2, NNH_NUMERICS_NNCPP), OK);
+	EXPECT(nnh_set_numerics(NNH_NUMERICS_SPLIT_DEPTH), OK);
+	EXPECT(nnh_get_stream_numerics(s2) == NNH_NUMERICS_NNCPP ? OK : INV, OK);
+	EXPECT(nnh_set_stream_numerics(s2, NNH_NUMERICS_DEFAULT), OK);
+	EXPECT(nnh_get_stream_numerics(s2) == NNH_NUMERICS_SPLIT_DEPTH ? OK : INV, OK);
+	EXPECT(nnh_set_stream_numerics(s1, NNH_NUMERICS_DEFAULT), OK);
+	EXPECT(nnh_set_stream_numerics(s1, NNH_NUMERICS_DEFAULT), OK);
+	EXPECT(nnh_set_numerics(NNH_NUMERICS_NNCPP), OK);
+	// the queries answer for both modes whatever the default: 64 x 64 x 4096 takes 32 pieces of partials in nn-cpp's
+	// mode, none in the split mode (16 pieces, one launch)
+	size_t q0 = 0, q1 = 0;
+	EXPECT(nnh_sgemm_workspace_size(64, 64, 4096, 1, &q0), OK);
+	EXPECT(nnh_set_numerics(NNH_NUMERICS_SPLIT_DEPTH), OK);
+	EXPECT(nnh_sgemm_workspace_size(64, 64, 4096, 1, &q1), OK);
+	EXPECT(nnh_set_numerics(NNH_NUMERICS_NNCPP), OK);
+	EXPECT(q0 == 32u * 64 * 64 * 4 && q1 == q0 ? OK : INV, OK);
 	EXPECT(nnh_set_workspace(nullptr, nullptr, 64), INV);
 	EXPECT(nnh_set_workspace(nullptr, c.data(), 64), HIP);
 	EXPECT(nnh_version() ? OK : INV, OK);

@@ -98,11 +98,12 @@ def test_matmul_shapes_and_errors_match_nncpp(ref):
 def test_workspace_queries_on_the_host():
     """The *_workspace_size queries need no device: nn-cpp's depth cut (gemm.cpp:453-458) decides the GEMM's partials,
     128-deep pieces of m n floats each where there are more than 16 pieces (up to 16, one launch adds them in LDS),
-    and the multi-step ops take the largest of their pieces."""
+    and the multi-step ops take the largest of their pieces. The queries answer for both numerics modes: the
+    split-depth mode's cuts have at most 16 pieces, so they add nothing here."""
     import nnh
     assert nnh.workspace_size("sgemm", 64, 64, 4096, 1) == 32 * 64 * 64 * 4
     assert nnh.workspace_size("sgemm", 40, 48, 2200, 3) == 18 * 40 * 48 * 4 * 3
-    assert nnh.workspace_size("sgemm", 512, 512, 512, 1) == 0          # m n > 2^16: no cut
+    assert nnh.workspace_size("sgemm", 512, 512, 512, 1) == 0          # m n > 2^16: no cut (split mode: 16 pieces)
     assert nnh.workspace_size("sgemm", 16, 16, 2048, 1) == 0           # m n k < 2^20: no cut
     assert nnh.workspace_size("sgemm", 256, 10, 1024, 1) == 0          # 8 pieces: one launch, no partials
     assert nnh.workspace_size("sgemm", 40, 48, 2048, 64) == 0          # 16 pieces: one launch

@@ -378,3 +378,39 @@ def test_first_layer_weight_gradient_kernel(gpu, oracle, case):
                 same(host(db), wdb, ("db",) + tag)
             if want_dx:
                 same(host(dx), wdx, ("dx",) + tag)
+
+
+@pytest.mark.parametrize("relu", [True, False])
+def test_empty_plane_with_padding(gpu, oracle, relu):
+    """H = W = 0 with padding 1 and a 1x1 kernel: every output tap is padding (ho = wo = 2), so y = bias, dW is +0
+    and db sums g (ops.cpp:1362 accepts the shape). The first-layer weight-gradient kernel takes this shape with no
+    x to read: dW and db only (dx is empty), fresh and accumulated."""
+    import ctypes as C
+
+    import torch
+
+    import nnh
+    N, Cin, Cout = 3, 1, 5
+    x = np.zeros((N, Cin, 0, 0), np.float32)
+    w = synth.normal(61, (Cout, Cin, 1, 1))
+    b = synth.mt19937_uniform(62, Cout, -1.0, 1.0)
+    wy, wa = oracle.conv2d_forward(x, w, b, 1, 1, relu)
+    xd = torch.zeros(1, device="cuda")  # a real allocation standing in for the empty plane (never read)
+    y = torch.full(wy.shape, float("nan"), device="cuda")
+    alive = torch.empty(wy.shape, dtype=torch.uint8, device="cuda") if relu else None
+    L, P, st = nnh.lib(), nnh._ptr, nnh._stream(None)
+    wd, bd = dev(w), dev(b)
+    nnh.check(L.nnh_conv2d_forward(P(xd), N, Cin, 0, 0, P(wd), Cout, 1, 1, P(bd), 1, 1, int(relu), P(y), P(alive), st))
+    same(host(y), wy, "y")
+    gr = synth.normal(63, wy.shape)
+    old_w, old_b = synth.normal(64, w.shape), synth.normal(65, (Cout,))
+    for first in (True, False):
+        dw = torch.full(w.shape, float("nan"), device="cuda") if first else dev(old_w)
+        db = torch.full((Cout,), float("nan"), device="cuda") if first else dev(old_b)
+        nnh.check(L.nnh_conv2d_backward(P(dev(gr)), P(xd), P(wd), P(alive), N, Cin, 0, 0, Cout, 1, 1, 1, 1, None,
+                                        1, P(dw), int(first), P(db), int(first), st))
+        _, wdw, wdb = oracle.conv2d_backward(gr, x, w, wa if relu else None, 1, 1)
+        if not first:
+            wdw, wdb = old_w + wdw, old_b + wdb
+        same(host(dw), wdw, ("dw", relu, first))
+        same(host(db), wdb, ("db", relu, first))

@@ -198,7 +198,10 @@ def ln_inputs(shape, seed):
 
 
 LN_CASES = [(16, 64, 64), (40, 30, 16), (3, 7, 33), (2, 515), (1, 4), (300, 1), (256, 512), (1023, 17), (1025, 8),
-            (3001, 40), (8, 1024, 512), (1201, 7)]
+            (3001, 40), (8, 1024, 512), (1201, 7),
+            # wide rows: from D = 5460 the backward's LDS block holds no row (ln_backward_kernel, a thread per row and
+            # per column); from D = 16384 the forward's neither (ln_forward_kernel)
+            (3, 5459), (3, 5460), (2, 8192), (2, 16383), (2, 16384), (3, 20000), (5, 16385)]
 
 
 @pytest.mark.parametrize("shape", LN_CASES)
@@ -238,6 +241,19 @@ def test_layernorm_unaligned_and_subsets(oracle):
         for name, ref_val, wanted in (("dx", dx, want[0]), ("dgamma", dg, want[1]), ("dbeta", db, want[2])):
             if wanted:
                 assert_same(got[name], ref_val, f"{name} with want={want}")
+
+
+@pytest.mark.parametrize("shape", [(3, 5461), (2, 16384)])
+def test_layernorm_wide_rows_unaligned(oracle, shape):
+    """The wide-row kernels on buffers one float past 16-byte alignment."""
+    x, gm, bt, g = ln_inputs(shape, 77)
+    y, mean, inv = oracle.layernorm_forward(x, gm, bt, EPS)
+    dx, dg, db = oracle.layernorm_backward(g, x, gm, mean, inv)
+    got = run_ln(x, gm, bt, g, offset=1)
+    assert_same(got["y"], y, f"{shape} unaligned y")
+    assert_same(got["dx"], dx, f"{shape} unaligned dx")
+    assert_same(got["dgamma"], dg, f"{shape} dgamma")
+    assert_same(got["dbeta"], db, f"{shape} dbeta")
 
 
 def test_norm_shape_errors():

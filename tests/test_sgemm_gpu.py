@@ -9,8 +9,8 @@ checked on sampled elements (the oracle recomputes each sampled element's whole 
 import numpy as np
 import pytest
 
-from helpers import (SENTINEL, UNDERFLOW_SHAPES, Problem, bits_equal, first_diff, gpu_sgemm, oracle_sgemm,
-                     underflow_problem, within_fp64_bound)
+from helpers import (SENTINEL, UNDERFLOW_SHAPES, Problem, assert_same, bits_equal, first_diff, gpu_sgemm,
+                     oracle_sgemm, underflow_problem, within_fp64_bound)
 from nnh import synth
 
 pytestmark = pytest.mark.gpu
@@ -219,6 +219,24 @@ def test_baseline_config5_sampled(gpu, oracle, m, n, k):
     got = dc.cpu().numpy()[rows, cols]
     want = oracle.sgemm_at(0, 0, m, n, k, a, k, b, n, 0, rows, cols)
     assert got.tobytes() == want.tobytes(), first_diff(got, want)
+
+
+@pytest.mark.parametrize("m,n,k", [(1024, 1024, 1024), (2048, 2048, 2048), (4096, 4096, 4096),
+                                   (8192, 8192, 8192), (64, 4096, 4096), (4096, 4096, 64)])
+def test_baseline_config5_whole_output_vs_nncpp(gpu, ref, m, n, k):
+    """BASELINE config 5 at full size, seed 4: every element of nn::matmul's output bit-identical to nn-cpp's own
+    compiled nn::matmul (oracle/_ref, its AVX2 build, multithreaded) on the same host buffers."""
+    import torch
+
+    import nnh
+    a, b = synth.uniform_operands(4, [(m, k), (k, n)])
+    rc, want = ref.matmul(a, b, False, False)
+    assert rc == 0
+    da, db = torch.from_numpy(a).cuda(), torch.from_numpy(b).cuda()
+    dc = torch.empty((m, n), device="cuda")
+    nnh.sgemm(0, 0, m, n, k, da, k, db, n, dc, n, 0)
+    got = dc.cpu().numpy()
+    assert_same(got, want, f"{m}x{n}x{k}")
 
 
 def _subnormal_problem(ta, tb, m, n, k, seed):

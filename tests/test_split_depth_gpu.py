@@ -124,3 +124,58 @@ def test_split_mode_is_reset_and_rejected_values(gpu):
     import nnh
     assert nnh.lib().nnh_get_numerics() == nnh.NUMERICS_NNCPP
     assert nnh.lib().nnh_set_numerics(7) == nnh.ERR_INVALID
+
+
+def test_two_streams_in_two_modes_at_once(gpu, oracle):
+    """A stream's own mode: two streams, one per mode, issue the same products from two threads at once; each
+    stream's outputs are its mode's bits (the oracle in that mode), and the process default is left as it was."""
+    import threading
+
+    import torch
+
+    import nnh
+    shapes = [(512, 512, 512), (64, 4096, 600), (256, 256, 512)]
+    probs = [Problem(0, 1, m, n, k, 0, 7300 + i) for i, (m, n, k) in enumerate(shapes)]
+    want = {}
+    for mode in (0, 1):
+        oracle.set_numerics(mode)
+        want[mode] = [oracle_sgemm(oracle, p, 0) for p in probs]
+    oracle.set_numerics(0)
+    assert not all(bits_equal(want[0][i], want[1][i]) for i in range(len(probs)))
+    streams = {0: torch.cuda.Stream(), 1: torch.cuda.Stream()}
+    nnh.set_stream_numerics(nnh.NUMERICS_NNCPP, streams[0])
+    nnh.set_stream_numerics(nnh.NUMERICS_SPLIT_DEPTH, streams[1])
+    default = nnh.lib().nnh_get_numerics()
+    try:
+        assert nnh.get_stream_numerics(streams[1]) == nnh.NUMERICS_SPLIT_DEPTH
+        ops = {mode: [(torch.from_numpy(p.a).cuda(), torch.from_numpy(p.b).cuda(), torch.empty((p.m, p.ldc),
+                                                                                                   device="cuda"))
+                      for p in probs] for mode in (0, 1)}
+        torch.cuda.synchronize()
+        errors = []
+
+        def issue(mode):
+            try:
+                with torch.cuda.stream(streams[mode]):
+                    for rep in range(20):
+                        for p, (a, b, c) in zip(probs, ops[mode]):
+                            nnh.sgemm(p.ta, p.tb, p.m, p.n, p.k, a, p.lda, b, p.ldb, c, p.ldc, 0,
+                                      stream=streams[mode])
+            except Exception as e:  # reported by the main thread
+                errors.append(e)
+
+        threads = [threading.Thread(target=issue, args=(mode,)) for mode in (0, 1)]
+        for t in threads:
+            t.start()
+        for t in threads:
+            t.join()
+        torch.cuda.synchronize()
+        assert not errors, errors
+        for mode in (0, 1):
+            for i, (p, (_, _, c)) in enumerate(zip(probs, ops[mode])):
+                assert bits_equal(host(c), want[mode][i][: p.m]), (mode, shapes[i])
+        assert nnh.lib().nnh_get_numerics() == default
+    finally:
+        nnh.set_stream_numerics(nnh.NUMERICS_DEFAULT, streams[0])
+        nnh.set_stream_numerics(nnh.NUMERICS_DEFAULT, streams[1])
+    assert nnh.get_stream_numerics(streams[1]) == default
