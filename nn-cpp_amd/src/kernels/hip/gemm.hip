@@ -53,10 +53,12 @@ const Config* configs() {
 		config_64x128x32(), config_128x128x32(), config_64x256x32(), config_128x64x32(),
 		config_128x256x16(), config_256x128x16(), config_64x128x64(), config_128x128x16(),
 		config_32x32x32_mf4(), config_64x64x32_mf4(), config_64x64x32_mf16(), config_128x64x32_mf16(),
+		config_32x32x32_mfk4(), config_64x64x32_mfk4(), config_128x64x32_mfk4(), config_128x128x32_mfk4(),
+		config_32x32x64_mfk4(), config_32x32x128_mfk4(),
 	};
 	return table;
 }
-constexpr int kNumConfigs = 12;
+constexpr int kNumConfigs = 18;
 
 // Raises each kernel's dynamic LDS limit once per device (gfx950 has 160 KiB per CU).
 hipError_t prepare_device() {
@@ -91,19 +93,24 @@ hipError_t prepare_device() {
 	return hipSuccess;
 }
 
-// Choice by measured device time on MI355X (every configuration on every BASELINE shape). Each output element
-// is a K-long chain of dependent MFMAs, and a dependent chain step costs about 64 cycles with 32x32x1 and 44
-// with 16x16x1 or 4x4x1, whose instructions also issue faster. Large products fill the GPU with 128 x 128 or
-// 128 x 64 tiles of 32x32x1 units (16-deep stages for A B, 32-deep when an operand is transposed); a million
-// outputs or more use 64 x 64 workgroups of 16x16x1 units; smaller products use 32 x 32 workgroups of 4x4x1
-// units, one wave per 16 x 16 block, so that as many chains as possible advance at once. Results never
-// depend on the choice.
+// Choice by measured device time on MI355X (every configuration on every BASELINE shape, and the MLP's). Each
+// output element is a K-long chain of dependent MFMAs: a dependent step costs about 64 cycles with 32x32x1 and 44
+// with 16x16x1 or 4x4x1, for one depth index, and 44 with 16x16x4 for four. Large products fill the GPU with
+// 128 x 128 or 128 x 64 tiles of 32x32x1 units (16-deep stages for A B, 32-deep when an operand is transposed);
+// from about 4 million outputs down to 2^20, 128 x 128 and then 64 x 64 workgroups of 16x16x4 units; smaller
+// products use 32 x 32 workgroups of 16x16x4 units (one wave per 16 x 16 block, as many chains as possible), with
+// 64-deep stages (128-deep with op(A) transposed and 512 or more deep, 32-deep up to 32). Measured (us, exact
+// mode): 512^3 NN 9.9 -> 7.1, TN 9.8 -> 6.7, NT 8.4 -> 7.0; 64 x 4096 x 4096 59.6 -> 35.7; 2048^3 168 -> 158.
+// Results never depend on the choice.
 enum {
 	kCfg128x128x32 = 1,
 	kCfg128x64x32 = 3,
 	kCfg128x128x16 = 7,
-	kCfg32x32x32Mf4 = 8,
-	kCfg64x64x32Mf16 = 10,
+	kCfg64x64x32Mfk4 = 13,
+	kCfg128x128x32Mfk4 = 15,
+	kCfg32x32x64Mfk4 = 16,
+	kCfg32x32x128Mfk4 = 17,
+	kCfg32x32x32Mfk4 = 12,
 };
 
 int pick_config(const GemmCall& g) {
@@ -112,9 +119,12 @@ int pick_config(const GemmCall& g) {
 	// 28.2 against 30.0 us), while 16-deep products keep the 16-deep tiles their depth divides
 	if (outputs >= 512.0 * 128 * 128 && !g.ta && !g.tb && g.k >= 32 && g.k <= 64 && g.k % 32 == 0) return kCfg128x64x32;
 	if (outputs >= 512.0 * 128 * 128) return (!g.ta && !g.tb) ? kCfg128x128x16 : kCfg128x128x32;
+	if (g.m >= 128 && g.n >= 128 && outputs >= 256.0 * 128 * 128) return kCfg128x128x32Mfk4;
+	// narrower products of that size (attention's batched 256 x 64 per head) keep 128 x 64 tiles
 	if (g.m >= 128 && outputs >= 512.0 * 128 * 64) return kCfg128x64x32;
-	if (outputs >= 1024.0 * 1024) return kCfg64x64x32Mf16;
-	return kCfg32x32x32Mf4;
+	if (outputs >= 1024.0 * 1024) return kCfg64x64x32Mfk4;
+	if (g.k <= 32) return kCfg32x32x32Mfk4;
+	return (g.ta && g.k >= 512) ? kCfg32x32x128Mfk4 : kCfg32x32x64Mfk4;
 }
 
 // The kernel arguments of one product on configuration cf; cut: the product takes nn-cpp's depth cut (the

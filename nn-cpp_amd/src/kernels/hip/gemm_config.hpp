@@ -69,5 +69,12 @@ Config config_32x32x32_mf4();
 Config config_64x64x32_mf4();
 Config config_64x64x32_mf16();
 Config config_128x64x32_mf16();
+// 16x16x4 MFMAs: four depth indices of every chain per instruction (the same fma chain)
+Config config_32x32x32_mfk4();
+Config config_64x64x32_mfk4();
+Config config_128x64x32_mfk4();
+Config config_128x128x32_mfk4();
+Config config_32x32x64_mfk4();
+Config config_32x32x128_mfk4();
 
 }  // namespace nnh

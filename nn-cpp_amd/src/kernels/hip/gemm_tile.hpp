@@ -42,7 +42,7 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x32 __attribute__((ext_vector_type(32)));
 
-enum MfmaKind : int { kMf32 = 0, kMf16 = 1, kMf4 = 2 };
+enum MfmaKind : int { kMf32 = 0, kMf16 = 1, kMf4 = 2, kMf16x4 = 3 };
 
 // Per MFMA kind: the unit tile, which row of A (column of B) lane l supplies, and where accumulator
 // register r of lane l sits in the unit (lane layouts measured on gfx950).
@@ -51,7 +51,7 @@ struct Mfma;
 
 template <>
 struct Mfma<kMf32> {
-	static constexpr int UM = 64, UN = 32, NV = 32;
+	static constexpr int UM = 64, UN = 32, NV = 32, DEPTH = 1;
 	using Acc = f32x32;
 	__device__ static int arow(int l) { return l; }
 	__device__ static int bcol(int l) { return l & 31; }
@@ -62,7 +62,7 @@ struct Mfma<kMf32> {
 
 template <>
 struct Mfma<kMf16> {
-	static constexpr int UM = 64, UN = 16, NV = 16;
+	static constexpr int UM = 64, UN = 16, NV = 16, DEPTH = 1;
 	using Acc = f32x16;
 	__device__ static int arow(int l) { return l; }
 	__device__ static int bcol(int l) { return l & 15; }
@@ -73,13 +73,30 @@ struct Mfma<kMf16> {
 
 template <>
 struct Mfma<kMf4> {
-	static constexpr int UM = 16, UN = 16, NV = 4;
+	static constexpr int UM = 16, UN = 16, NV = 4, DEPTH = 1;
 	using Acc = f32x4;
 	__device__ static int arow(int l) { return 4 * (l >> 4) + (l & 3); }
 	__device__ static int bcol(int l) { return 4 * ((l >> 2) & 3) + (l & 3); }
 	__host__ __device__ static constexpr int crow(int r, int l) { return 4 * (l >> 4) + r; }
 	__device__ static int ccol(int l) { return 4 * ((l >> 2) & 3) + (l & 3); }
 	__device__ static Acc mma(float a, float b, const Acc& c) { return __builtin_amdgcn_mfma_f32_4x4x1f32(a, b, c, 0, 0, 0); }
+};
+
+// 16x16x4: one 16 x 16 block over four depth indices per instruction. Lane l supplies A[l % 16][k0 + l / 16] and
+// B[k0 + l / 16][l % 16], and each output becomes fma(a3, b3, fma(a2, b2, fma(a1, b1, fma(a0, b0, c)))), the depth
+// indices in increasing order: measured on gfx950 bit-identical to four fmaf in sequence (on the same GPU's vector
+// ALUs) on 5 million outputs, zeros of both signs, infinities, NaN payloads and subnormals included. So one
+// instruction advances every chain of its block four steps of the reference's chain, in 44 cycles where the k = 1
+// MFMAs take 44 for one.
+template <>
+struct Mfma<kMf16x4> {
+	static constexpr int UM = 16, UN = 16, NV = 4, DEPTH = 4;
+	using Acc = f32x4;
+	__device__ static int arow(int l) { return l & 15; }
+	__device__ static int bcol(int l) { return l & 15; }
+	__host__ __device__ static constexpr int crow(int r, int l) { return 4 * (l >> 4) + r; }
+	__device__ static int ccol(int l) { return l & 15; }
+	__device__ static Acc mma(float a, float b, const Acc& c) { return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0); }
 };
 
 constexpr int kMaxBatchDims = 4;
@@ -178,16 +195,25 @@ __device__ __forceinline__ void load_tile(const float* __restrict__ g, int64_t l
 	}
 }
 
-template <int R, int CC, int S>
+// KPERM (a k-contiguous tile for the 16x16x4 MFMA): inside every 16 columns, column 4 t + e is stored at 4 e + t,
+// so that lane group e's operands of four consecutive MFMAs (depth 4 t + e, t = 0..3) are one 16-byte read.
+template <int R, int CC, int S, bool KPERM = false>
 __device__ __forceinline__ void store_tile(float* lds, const f32x4* v, int tid) {
 	constexpr int kVecPerRow = CC / 4;
 	constexpr int kPer = R * CC / 4 / 256;
+	static_assert(!KPERM || CC % 16 == 0, "the permutation works on 16 columns at a time");
 #pragma unroll
 	for (int i = 0; i < kPer; ++i) {
 		const int idx = tid + 256 * i;
 		const int r = idx / kVecPerRow;
 		const int c = (idx % kVecPerRow) * 4;
-		*reinterpret_cast<f32x4*>(lds + r * S + c) = v[i];
+		if constexpr (KPERM) {
+			const int base = r * S + (c & ~15) + ((c >> 2) & 3);
+#pragma unroll
+			for (int e = 0; e < 4; ++e) lds[base + 4 * e] = v[i][e];
+		} else {
+			*reinterpret_cast<f32x4*>(lds + r * S + c) = v[i];
+		}
 	}
 }
 
@@ -260,18 +286,27 @@ struct TileShape {
 	static constexpr int kWavesN = BN / WN;
 	static_assert((BM / WM) * (BN / WN) == 4, "4 waves per workgroup");
 	static_assert(WM % Mfma<MF>::UM == 0 && WN % Mfma<MF>::UN == 0, "wave tile must be whole MFMA units");
-	static_assert(kAccAfter % BK == 0 && BK % 4 == 0, "depth tile must divide 256");
+	static constexpr int D = Mfma<MF>::DEPTH;
+	static_assert(kAccAfter % BK == 0 && BK % (4 * D) == 0, "depth tile must divide 256 and hold whole fragment groups");
 	static constexpr int I = WM / Mfma<MF>::UM, J = WN / Mfma<MF>::UN;
 	// LDS strides (floats). K-major tiles get 4 floats of padding so that 64 lanes reading 16 bytes
-	// from 64 consecutive rows spread over the banks.
-	static constexpr int SA = TA ? BM : BK + 4;
-	static constexpr int SB = TB ? BK + 4 : BN;
+	// from 64 consecutive rows spread over the banks. With the 16x16x4 MFMA an M/N-major tile's rows get 16 floats
+	// more, so that the four lane groups (four depth rows, 16 consecutive columns each) read distinct banks.
+	static constexpr int kPadMN = D == 4 ? 16 : 0;
+	static constexpr int SA = TA ? BM + kPadMN : BK + 4;
+	static constexpr int SB = TB ? BK + 4 : BN + kPadMN;
 	static constexpr int kASize = TA ? BK * SA : BM * SA;
 	static constexpr int kBSize = TB ? BN * SB : BK * SB;
 	static constexpr int kStage = kASize + kBSize;
 	static constexpr int kLdsFloats = 2 * kStage;
 	static constexpr int LA = BM * BK / 4 / 256;
 	static constexpr int LB = BN * BK / 4 / 256;
+	// Depth tiles whose global loads are in flight ahead of the one in LDS (a ring of register sets). Small tiles
+	// do little MFMA work per depth tile, less than a load's latency, so they keep up to 4 tiles in flight; the
+	// large tiles keep one (their registers are spent on accumulators).
+	static constexpr int kPF = BM * BN <= 32 * 32 ? (LA + LB <= 2 ? 4 : (LA + LB <= 4 ? 2 : 1))
+	                                              : (MF == kMf16x4 && BM * BN <= 64 * 64 ? 2 : 1);
+	static_assert((kAccAfter / BK) % kPF == 0, "the accumulate split must fall on a ring boundary");
 };
 
 // Maps the hardware workgroup id to a logical tile id so that consecutive logical ids (which share
@@ -340,7 +375,8 @@ __device__ __forceinline__ void sgemm_tile_body(const GemmArgs& p, int block) {
 			for (int r = 0; r < U::NV; ++r) acc[i][j][r] = 0.0f;
 
 	const bool vec_ok = p.vec_ok != 0;
-	f32x4 ra[S::LA], rb[S::LB];
+	constexpr int PF = RS ? 1 : S::kPF;  // the row sums' registers leave no room for a ring
+	f32x4 ra[PF][S::LA], rb[PF][S::LB];
 	// implicit im2col: the side of each thread's B slots that is fixed over the depth loop (NN: its columns p,
 	// NT: its rows kk), computed once
 	constexpr int kGV = TB ? BK / 4 : BN / 4;  // 16-byte groups per row of the B tile
@@ -358,7 +394,7 @@ __device__ __forceinline__ void sgemm_tile_body(const GemmArgs& p, int block) {
 			}
 		}
 	}
-	auto load = [&](int kt) {
+	auto load = [&](int kt, f32x4* ra, f32x4* rb) {
 		const int k0 = k_lo + kt * BK;
 		if (!TA)  // A stored m x k: tile BM rows x BK
 			load_tile<BM, BK, EDGE>(A + (int64_t)m0 * p.lda + k0, p.lda, p.m - m0, k_hi - k0, vec_ok, ra, tid);
@@ -383,12 +419,13 @@ __device__ __forceinline__ void sgemm_tile_body(const GemmArgs& p, int block) {
 			load_tile<BK, BN, EDGE>(B + (int64_t)k0 * p.ldb + n0, p.ldb, k_hi - k0, p.n - n0, vec_ok, rb, tid, -0.0f);
 		}
 	};
-	auto store = [&](int buf) {
+	constexpr bool kPerm = U::DEPTH == 4;  // k-contiguous tiles stored permuted for the 16x16x4 fragments
+	auto store = [&](int buf, const f32x4* ra, const f32x4* rb) {
 		float* As = lds + buf * S::kStage;
 		float* Bs = As + S::kASize;
-		if (!TA) store_tile<BM, BK, S::SA>(As, ra, tid);
+		if (!TA) store_tile<BM, BK, S::SA, kPerm>(As, ra, tid);
 		else store_tile<BK, BM, S::SA>(As, ra, tid);
-		if (TB) store_tile<BN, BK, S::SB>(Bs, rb, tid);
+		if (TB) store_tile<BN, BK, S::SB, kPerm>(Bs, rb, tid);
 		else store_tile<BK, BN, S::SB>(Bs, rb, tid);
 	};
 
@@ -396,9 +433,36 @@ __device__ __forceinline__ void sgemm_tile_body(const GemmArgs& p, int block) {
 	auto c_row = [&](int i, int r, int ln) { return wm0 + U::UM * i + U::crow(r, ln); };
 	auto c_col = [&](int j, int ln) { return wn0 + U::UN * j + U::ccol(ln); };
 
-	// One depth tile from LDS buffer buf: fragments for depth group kk+4 are read while the MFMAs of
-	// group kk run (two register sets), and each element's chain advances one k per MFMA, in order.
+	// One depth tile from LDS buffer buf: fragments for depth group kk+KG are read while the MFMAs of
+	// group kk run (two register sets), and each element's chain advances one k per MFMA (four with 16x16x4), in
+	// order. A group is 4 depth indices (k = 1 MFMAs: element e of a fragment is depth kk + e) or 16 (16x16x4:
+	// element t of lane group g's fragment is depth kk + 4 t + g).
+	constexpr int KG = 4 * U::DEPTH;
 	auto read_frags = [&](const float* As, const float* Bs, int kk, f32x4* af, f32x4* bf) {
+		if constexpr (U::DEPTH == 4) {
+			const int g = lane >> 4;
+#pragma unroll
+			for (int i = 0; i < I; ++i) {
+				const int row = wm0 + U::UM * i + U::arow(lane);
+				if (!TA) {
+					af[i] = *reinterpret_cast<const f32x4*>(As + row * S::SA + kk + 4 * g);
+				} else {
+#pragma unroll
+					for (int t = 0; t < 4; ++t) af[i][t] = As[(kk + 4 * t + g) * S::SA + row];
+				}
+			}
+#pragma unroll
+			for (int j = 0; j < J; ++j) {
+				const int col = wn0 + U::UN * j + U::bcol(lane);
+				if (TB) {
+					bf[j] = *reinterpret_cast<const f32x4*>(Bs + col * S::SB + kk + 4 * g);
+				} else {
+#pragma unroll
+					for (int t = 0; t < 4; ++t) bf[j][t] = Bs[(kk + 4 * t + g) * S::SB + col];
+				}
+			}
+			return;
+		}
 #pragma unroll
 		for (int i = 0; i < I; ++i) {
 			const int row = wm0 + U::UM * i + U::arow(lane);
@@ -425,28 +489,32 @@ __device__ __forceinline__ void sgemm_tile_body(const GemmArgs& p, int block) {
 	// no branch; the first column tile's threads tid < BM store them. Depth past k is zero-filled by the edge
 	// loader, and adding +0 leaves the sum unchanged (it starts at +0, so it is never -0).
 	float rsum = 0.0f;
-	auto read_rowsum = [&](const float* As, int kk) {
-		f32x4 v;
+	auto read_rowsum = [&](const float* As, int kk, f32x4* v) {  // the group's KG depth values of the row
 #pragma unroll
-		for (int e = 0; e < 4; ++e) v[e] = As[(kk + e) * S::SA + (tid & (BM - 1))];
-		return v;
+		for (int d = 0; d < U::DEPTH; ++d)
+#pragma unroll
+			for (int e = 0; e < 4; ++e) v[d][e] = As[(kk + 4 * d + e) * S::SA + (tid & (BM - 1))];
 	};
 	auto mma_tile = [&](int buf) {
 		const float* As = lds + buf * S::kStage;
 		const float* Bs = As + S::kASize;
 		f32x4 af[2][I], bf[2][J];
-		[[maybe_unused]] f32x4 rs[2];
+		// row-sum values: read a group ahead with the fragments (k = 1 MFMAs: 4 per group), or, with 16x16x4 (16 per
+		// group), for the current group only, so that they do not cost the registers of a second set
+		constexpr int RSB = U::DEPTH == 4 ? 1 : 2;
+		[[maybe_unused]] f32x4 rs[RSB][U::DEPTH];
 		read_frags(As, Bs, 0, af[0], bf[0]);
-		if constexpr (RS) rs[0] = read_rowsum(As, 0);
+		if constexpr (RS && RSB == 2) read_rowsum(As, 0, rs[0]);
 #pragma unroll
-		for (int kk = 0; kk < BK; kk += 4) {
-			const int cur = (kk >> 2) & 1;
+		for (int kk = 0; kk < BK; kk += KG) {
+			const int cur = (kk / KG) & 1;
 			// issue the next group's LDS reads before this group's MFMAs, so their latency is hidden;
 			// the scheduling fences stop the compiler from sinking them back next to their uses
-			if (kk + 4 < BK) {
-				read_frags(As, Bs, kk + 4, af[cur ^ 1], bf[cur ^ 1]);
-				if constexpr (RS) rs[cur ^ 1] = read_rowsum(As, kk + 4);
+			if (kk + KG < BK) {
+				read_frags(As, Bs, kk + KG, af[cur ^ 1], bf[cur ^ 1]);
+				if constexpr (RS && RSB == 2) read_rowsum(As, kk + KG, rs[cur ^ 1]);
 			}
+			if constexpr (RS && RSB == 1) read_rowsum(As, kk, rs[0]);
 			__builtin_amdgcn_sched_barrier(0);
 #pragma unroll
 			for (int e = 0; e < 4; ++e)
@@ -457,28 +525,59 @@ __device__ __forceinline__ void sgemm_tile_body(const GemmArgs& p, int block) {
 						acc[i][j] = U::mma(af[cur][i][e], bf[cur][j][e], acc[i][j]);
 			if constexpr (RS) {
 #pragma unroll
-				for (int e = 0; e < 4; ++e) rsum = rsum + rs[cur][e];
+				for (int d = 0; d < U::DEPTH; ++d)
+#pragma unroll
+					for (int e = 0; e < 4; ++e) rsum = rsum + rs[RSB == 2 ? cur : 0][d][e];
 			}
 			__builtin_amdgcn_sched_barrier(0);
 		}
 	};
-	auto step = [&](int kt) {
-		if (kt + 1 < nkt) load(kt + 1);
+	// Step kt, with u = kt % PF known at compile time: register set u held tile kt (already in LDS) and now loads
+	// tile kt + PF (clamped to the last tile: a redundant load instead of a branch around it, so the compiler
+	// waits for each set by count); the MFMAs run on LDS buffer kt & 1; set (u + 1) % PF, tile kt + 1, goes to the
+	// other buffer.
+	auto step = [&](int kt, int u) {
+		if (PF > 1 || kt + 1 < nkt) load(min(kt + PF, nkt - 1), ra[u], rb[u]);
 		mma_tile(kt & 1);
-		if (kt + 1 < nkt) store((kt + 1) & 1);
+		if (kt + 1 < nkt) store((kt + 1) & 1, ra[(u + 1) % PF], rb[(u + 1) % PF]);
 		__syncthreads();
+	};
+	// The same step with no branch at all (the ring's loads are then waited for by count: a branch anywhere in the
+	// loop makes the compiler wait for every load at the merge): past the last tile the store writes a redundant
+	// tile into the buffer no MFMA reads any more (the epilogue reuses LDS only after the loop's last barrier).
+	auto step_full = [&](int kt, int u) {
+		load(min(kt + PF, nkt - 1), ra[u], rb[u]);
+		mma_tile(kt & 1);
+		store((kt + 1) & 1, ra[(u + 1) % PF], rb[(u + 1) % PF]);
+		__syncthreads();
+	};
+	// steps k0 .. k1 - 1 (k0 a multiple of PF): whole rounds of PF steps, then the rest
+	auto run = [&](int k0, int k1) {
+		int kt = k0;
+		if constexpr (PF > 1) {
+			for (; kt + PF <= k1; kt += PF) {
+#pragma unroll
+				for (int u = 0; u < PF; ++u) step_full(kt + u, u);
+			}
+		}
+		for (; kt < k1; kt += PF) {
+#pragma unroll
+			for (int u = 0; u < PF; ++u)
+				if (kt + u < k1) step(kt + u, u);
+		}
 	};
 
 	if (nkt > 0) {
-		load(0);
-		store(0);
+#pragma unroll
+		for (int u = 0; u < PF; ++u) load(min(u, nkt - 1), ra[u], rb[u]);
+		store(0, ra[0], rb[0]);
 		__syncthreads();
 	}
 	// With accumulate, old C joins the chain after the first 256 steps; the loop is split there so the
 	// accumulators never leave the matrix-core registers inside a loop.
 	const bool add_mid = acc_mode && acc_tile >= 0;
 	const int n1 = add_mid ? acc_tile + 1 : nkt;
-	for (int kt = 0; kt < n1; ++kt) step(kt);
+	run(0, n1);
 	if (add_mid) {
 		int lane_m = lane;
 		asm volatile("" : "+v"(lane_m));
@@ -493,7 +592,7 @@ __device__ __forceinline__ void sgemm_tile_body(const GemmArgs& p, int block) {
 						acc[i][j][r] = p.c[oc + (int64_t)row * p.ldc + col] + acc[i][j][r];
 				}
 	}
-	for (int kt = n1; kt < nkt; ++kt) step(kt);
+	run(n1, nkt);
 	if (RS && p.rowsum != nullptr && tn == 0 && p.pieces == 1 && tid < BM && m0 + tid < p.m) {
 		float* d = p.rowsum + m0 + tid;
 		*d = p.rowsum_combine == 0 ? rsum : (p.rowsum_combine == 1 ? rsum + 0.0f : *d + rsum);
@@ -524,7 +623,7 @@ __device__ __forceinline__ void sgemm_tile_body(const GemmArgs& p, int block) {
 		// time, and writes C as 16-byte stores of 4 consecutive columns; the epilogue is applied per element.
 		constexpr int kPerWave = S::kLdsFloats / 4;
 		constexpr int LS = WN + 4;
-		constexpr int RP = (MF == kMf4) ? 16 : (U::UM * LS <= kPerWave ? U::UM : (U::UM / 2 * LS <= kPerWave ? U::UM / 2 : 16));
+		constexpr int RP = (MF == kMf4 || MF == kMf16x4) ? 16 : (U::UM * LS <= kPerWave ? U::UM : (U::UM / 2 * LS <= kPerWave ? U::UM / 2 : 16));
 		static_assert(RP * LS <= kPerWave, "an epilogue pass must fit in the wave's LDS slice");
 		static_assert(passes_split_evenly<MF>(RP), "a register's pass must not depend on the lane");
 		constexpr int kChunks = RP * WN / 4;        // 4-column groups in one pass

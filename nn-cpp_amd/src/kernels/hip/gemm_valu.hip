@@ -655,10 +655,15 @@ bool valu_takes(const GemmCall& g) {
 	// * op(A) transposed (its dword loads are strided), the 1 x 2 lane block, up to 2^17 outputs: slower than the
 	//   MFMA tiles from 2^18 (512^3 TN: 15.0 against 10.9), where they have enough chains to overlap their 44-cycle
 	//   steps and this kernel's LDS reads bind it.
+	// Against the 16x16x4 tiles (four depth indices per chain step): the row-broadcast kernel keeps products up to 2^17
+	// outputs (256 x 512 x 784 NT 10.5 against 12.4 us, 256 x 10 x 256 4.3 against 6.4, 256 x 512 x 256 NN 4.8
+	// against 5.0); at 2^18 the tiles win (512^3 NN 7.1 against 9.9, 256 x 784 x 512 NN 9.4 against 9.6). With op(A)
+	// transposed the tiles win from 2^17 outputs (256 x 512 x 256 TN 4.7 against 5.5), the 1 x 2 lane block keeps the
+	// smaller ones (10 x 256 x 256 TN 6.8 against 7.5).
 	const double outputs = (double)g.m * (double)g.n * (double)g.batch_count;
 	if (g.k < 256) return false;
-	if (g.ta) return outputs <= 131072.0;
-	return outputs <= 131072.0 || (outputs <= 262144.0 && g.k <= 512 && !g.tb);
+	if (g.ta) return outputs <= 65536.0;
+	return outputs <= 131072.0;
 }
 
 hipError_t gemm_valu_launch(const GemmCall& g, int shape, hipStream_t s) {
