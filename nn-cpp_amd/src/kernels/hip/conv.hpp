@@ -56,6 +56,16 @@ hipError_t conv_dwp(const float* g, const unsigned char* alive, const float* x, 
                     const ConvGeom& geo, int64_t samples, int cout, hipStream_t s);
 hipError_t conv_dx_fused(const float* gm, const unsigned char* alive, const float* w, float* dx, const ConvGeom& g,
                          int64_t samples, int cout, int first, hipStream_t s);
+// The whole backward of a first layer (conv_first.hip: K = Cin*kh*kw <= 16, Cout <= 32, stride 1, Ho*Wo a multiple
+// of 4 up to 65536, 16-byte aligned g and 4-byte aligned flags) in one launch of one-wave workgroups, two kinds per
+// sample: the per-sample bias sums gb {N, Cout} (may be null) and weight gradients gw {N, Cout, K} as conv_dwp
+// computes them (same bits), and dx on bands of rows (may be null; first: dx = 0 + taps, else dx += taps) as
+// conv_dx_fused computes it, each masking g as it reads it. Declines depth-cut products.
+bool conv_first_bwd_ok(const ConvGeom& g, int64_t samples, int cout, bool dx, const float* gr,
+                       const unsigned char* alive);
+hipError_t conv_first_bwd(const float* g, const unsigned char* alive, const float* x, const float* w, float* gb,
+                          float* gw, float* dx, int dx_first, const ConvGeom& geo, int64_t samples, int cout,
+                          hipStream_t s);
 hipError_t masked_lane_sums(const float* g, const unsigned char* alive, float* out, int64_t rows, int64_t n, float* dst,
                             hipStream_t s);
 hipError_t lane_sums(const float* src, int64_t rows, int64_t n, float* dst, hipStream_t s);

@@ -249,9 +249,14 @@ int nnh_conv2d_backward(const float* g, const float* x, const float* w, const un
 	const bool dw3 = dw && conv_dw3_ok(geo, (int64_t)N, (int)Cout, g, alive, m);
 	// short column depth (a first layer): db and dW per sample from LDS, the mask applied as g is staged; the dx
 	// kernel then masks g itself, so the masked gradient is never written
-	const bool dwp = dw && !dw3 && (!dx || dx_fused) && conv_dwp_ok(geo, (int64_t)N, (int)Cout);
+	// a first layer's whole backward (K <= 16, Cout <= 32) in one workgroup per sample
+	const bool first = dw && !dw3 && conv_first_bwd_ok(geo, (int64_t)N, (int)Cout, dx != nullptr, g, alive);
+	const bool dwp = dw && !dw3 && !first && (!dx || dx_fused) && conv_dwp_ok(geo, (int64_t)N, (int)Cout);
 	if (dw3) {
 		rc = hip_status(conv_dw3(g, alive, m, gb, x, gw, geo, (int64_t)N, (int)Cout, s), "conv2d mask, db, dw 3x3");
+	} else if (first) {
+		rc = hip_status(conv_first_bwd(g, alive, x, w, gb, gw, dx, dx_first ? 1 : 0, geo, (int64_t)N, (int)Cout, s),
+		                "conv2d db, dw, dx");
 	} else if (dwp) {
 		rc = hip_status(conv_dwp(g, alive, x, gb, gw, geo, (int64_t)N, (int)Cout, s), "conv2d db, dw");
 	} else if (alive) {  // ops.cpp:1439-1443, with the per-sample bias sums of ops.cpp:1445 in the same pass
@@ -260,7 +265,7 @@ int nnh_conv2d_backward(const float* g, const float* x, const float* w, const un
 	} else if (db) {  // ops.cpp:1445
 		rc = hip_status(lane_sums(gm, (int64_t)(N * Cout), (int64_t)hw, gb, s), "conv2d db");
 	}
-	if (rc == NNH_OK && dw && !dw3 && !dwp) {  // ops.cpp:1448-1449: dW_n = g_n col_n^T with col_n gathered from x_n
+	if (rc == NNH_OK && dw && !dw3 && !dwp && !first) {  // ops.cpp:1448-1449: dW_n = g_n col_n^T with col_n gathered from x_n
 		nnh_batch b{};
 		b.ndim = 1;
 		b.shape[0] = N;
@@ -281,7 +286,9 @@ int nnh_conv2d_backward(const float* g, const float* x, const float* w, const un
 		rc = hip_status(sum_rows(gw, (int64_t)N, (int64_t)(Cout * K), dw, dw_first ? 0 : 2, s), "conv2d dw");
 	else if (rc == NNH_OK && db)
 		rc = hip_status(sum_rows(gb, (int64_t)N, (int64_t)Cout, db, db_first ? 0 : 2, s), "conv2d db");
-	if (rc == NNH_OK && dx && dx_fused) {  // ops.cpp:1452-1455, dcol kept on chip
+	if (rc == NNH_OK && dx && first) {
+		// computed with dW above
+	} else if (rc == NNH_OK && dx && dx_fused) {  // ops.cpp:1452-1455, dcol kept on chip
 		rc = hip_status(dwp ? conv_dx_fused(g, alive, w, dx, geo, (int64_t)N, (int)Cout, dx_first ? 1 : 0, s)
 		                    : conv_dx_fused(gm, nullptr, w, dx, geo, (int64_t)N, (int)Cout, dx_first ? 1 : 0, s),
 		                "conv2d dx");

@@ -335,16 +335,27 @@ def test_same_width_quad_path(gpu, oracle):
     same(host(yv).reshape(wy.shape), wy, "unaligned y")
 
 
-# First layers: K = Cin*kh*kw <= 16 on planes of up to 1024 outputs take one kernel for db and dW per sample
-# (conv_dwp), with the mask applied as g is staged and dx masking g itself. (N, Cin, H, W, Cout, kh, kw, stride,
+# First layers: K = Cin*kh*kw <= 16 with Cout <= 32, stride 1, Ho*Wo a multiple of 4 and a padded input plane of up
+# to 2048 floats take one kernel per sample for db, dW and dx (conv_first); other short-depth layers take the
+# per-sample db and dW kernel (conv_dwp) and a dx kernel that masks g itself. (N, Cin, H, W, Cout, kh, kw, stride,
 # pad)
 DWP_CASES = [
     (4, 1, 28, 28, 32, 3, 3, 1, 1),     # config 3's conv1
     (3, 1, 13, 13, 10, 3, 3, 1, 1),     # 169 outputs (not a multiple of 4: element-wise staging), 10 channels
-    (2, 1, 32, 32, 8, 3, 3, 1, 1),      # 1024 outputs, the largest plane it takes
-    (2, 2, 9, 9, 12, 2, 2, 2, 0),       # stride 2, K = 8
+    (2, 1, 32, 32, 8, 3, 3, 1, 1),      # 1024 outputs: three bands of dx rows
+    (2, 2, 9, 9, 12, 2, 2, 2, 0),       # stride 2, K = 8: conv_dwp
     (2, 1, 30, 30, 9, 4, 4, 1, 1),      # 16 taps
-    (2, 1, 48, 48, 16, 3, 3, 1, 1),     # 2304 outputs: beyond it, the mask + GEMM path
+    (2, 1, 48, 48, 16, 3, 3, 1, 1),     # 2304 outputs: beyond LDS, the mask + GEMM path
+    (3, 1, 27, 27, 32, 3, 3, 1, 1),     # 729 outputs, two dW chains, element-wise staging
+    (2, 2, 12, 12, 20, 2, 2, 1, 0),     # Cout 20: the second chain's last 12 rows are padding
+    (2, 16, 7, 7, 24, 1, 1, 1, 0),      # K = 16 from 16 input channels of a 1x1 kernel
+    (2, 1, 5, 6, 3, 3, 3, 1, 2),        # padding 2: outer output rows take taps from padding only
+    (2, 1, 2, 3, 5, 1, 1, 1, 0),        # 6 outputs: lane_sum's tail only
+    (2, 1, 4, 4, 31, 2, 2, 1, 0),       # 9 outputs, Cout 31
+    (2, 1, 20, 20, 64, 3, 3, 1, 1),     # Cout 64: conv_dwp
+    (2, 1, 6, 6, 12, 3, 3, 1, 1),       # 36 outputs: lane_sum's tail of 4, one chain wave idle (Cout 12)
+    (2, 16, 8, 8, 24, 1, 1, 1, 0),      # K = 16 from 16 input channels, one whole chunk of 64 outputs
+    (2, 2, 9, 9, 32, 2, 2, 1, 1),       # even kernel with padding: 100 outputs, two input channels to gather
 ]
 
 
