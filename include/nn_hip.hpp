@@ -23,8 +23,10 @@
 #include <hip/hip_runtime.h>
 
 #include <cstddef>
+#include <cstdint>
 #include <functional>
 #include <memory>
+#include <random>
 #include <stdexcept>
 #include <string>
 #include <vector>
@@ -43,6 +45,16 @@ public:
 	explicit HipError(const std::string& m) : std::runtime_error(m) {}
 };
 
+// nn-cpp's library-wide seeding (include/nn/random.hpp, src/random.cpp): manual_seed restarts every named stream;
+// derive_generator hands out the k-th generator of a stream, seeded from splitmix64(base ^ fnv1a(stream) ^
+// k * golden) through std::seed_seq as the reference does, so that parameters initialised here (Tensor::random,
+// Dropout's masks) equal the reference's after the same seed. Without a manual_seed the base comes from
+// std::random_device once.
+void manual_seed(uint64_t seed);
+bool is_seeded();
+uint64_t seed_epoch();
+std::mt19937 derive_generator(const std::string& stream);
+
 // The stream every op enqueues on (setting another first waits for the current one).
 void set_stream(hipStream_t s);
 hipStream_t current_stream();
@@ -60,6 +72,10 @@ public:
 	explicit Tensor(std::vector<size_t> shape, float value = 0.0f);  // filled with value
 	static Tensor empty(std::vector<size_t> shape);            // uninitialised (Tensor::empty, tensor.cpp:263)
 	static Tensor from_host(std::vector<size_t> shape, const float* data);
+	// Tensor::random (tensor.cpp:504-522): uniform in [lo, hi) from the "tensor.random" stream of manual_seed below,
+	// drawn on the host (std::mt19937 and std::uniform_real_distribution<float>) and copied in: after the same
+	// manual_seed and the same sequence of draws, the values nn-cpp's Tensor::random gives.
+	static Tensor random(std::vector<size_t> shape, float lo, float hi);
 	void to_host(float* out) const;
 	std::vector<float> to_host() const;
 
@@ -164,6 +180,12 @@ Value scaled_masked_softmax(const Value& x, float scale_by, const Tensor& key_pa
 // ones, as PositionalEncoding adds its table); b's gradient is then summed one leading axis at a time
 // (sum_to_shape, ops.cpp:35-53). Other broadcasts are refused with std::invalid_argument.
 Value add(const Value& a, const Value& b);
+// ops.hpp (ops.cpp:347-357): element-wise product of two tensors of one shape (other broadcasts are refused with
+// std::invalid_argument); Dropout multiplies by its mask with it.
+Value mul(const Value& a, const Value& b);
+// ops.cpp:592-608: rows start .. end - 1 of axis 0 (other axes are refused with std::invalid_argument); the gradient
+// adds into that band of x's (PositionalEncoding takes its first T rows with it).
+Value slice(const Value& x, int axis, size_t start, size_t end);
 // ops.hpp:195 (ops.cpp:451-481): GELU, tanh form.
 Value gelu(const Value& x);
 // ops.hpp:255 (ops.cpp:1991-2015): rows of weight {V, D} picked by float ids (whole numbers in [0, V), checked on the

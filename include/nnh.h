@@ -352,6 +352,13 @@ int nnh_layernorm_backward(const float* g, const float* x, const float* gamma, c
  * backward rule is nnh_add_to_grad for a and, for a broadcast b, nnh_tensor_sum0 (sum_to_shape) then the store. */
 int nnh_add_forward(const float* a, const float* b, size_t outer, size_t inner, float* y, void* stream);
 
+/* nn::mul (src/autograd/ops.cpp:347-357 forward, src/tensor.cpp:551-553) of two same-shaped tensors: y = a * b. y may
+ * be a or b itself. Its backward rule, per operand: d = g * other (the other operand), stored as the product + 0 into a
+ * fresh gradient (first), else added (accumulate_grad, ops.cpp:110-117). Dropout's mask multiply uses it
+ * (src/nn/dropout.cpp:22-33). */
+int nnh_mul_forward(const float* a, const float* b, size_t count, float* y, void* stream);
+int nnh_mul_backward(const float* g, const float* other, size_t count, float* d, int first, void* stream);
+
 /* nn::gelu, the tanh form (ops.cpp:451-466): tanh_saved receives tanh(k (x + c x^3)) per element (the reference keeps
  * it for the backward pass), with nn-cpp's own tanh and exp (src/kernels/vmath.cpp:24-105), bit for bit. */
 int nnh_gelu_forward(const float* x, size_t count, float* y, float* tanh_saved, void* stream);

@@ -106,6 +106,8 @@ _EXTRA_DECLS = {
     "nnh_layernorm_forward": [_vp, _sz, _sz, _vp, _vp, C.c_float, _vp, _vp, _vp, _vp],
     "nnh_layernorm_backward": [_vp, _vp, _vp, _vp, _vp, _sz, _sz, _vp, C.c_int, _vp, C.c_int, _vp, C.c_int, _vp],
     "nnh_add_forward": [_vp, _vp, _sz, _sz, _vp, _vp],
+    "nnh_mul_forward": [_vp, _vp, _sz, _vp, _vp],
+    "nnh_mul_backward": [_vp, _vp, _sz, _vp, C.c_int, _vp],
     "nnh_gelu_forward": [_vp, _sz, _vp, _vp, _vp],
     "nnh_gelu_backward": [_vp, _vp, _vp, _sz, _vp, C.c_int, _vp],
     "nnh_embedding_forward": [_vp, _sz, _sz, _vp, _sz, _vp, _vp],

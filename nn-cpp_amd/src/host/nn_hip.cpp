@@ -613,6 +613,39 @@ Value add(const Value& a, const Value& b) {
 	});
 }
 
+Value mul(const Value& a, const Value& b) {
+	if (a.data().shape() != b.data().shape())
+		throw std::invalid_argument("nn::hip: mul takes two tensors of one shape");
+	Tensor y = Tensor::empty(a.data().shape());
+	check(nnh_mul_forward(a.data().data(), b.data().data(), y.size(), y.data(), g_stream));
+	return Value::node(std::move(y), {a, b}, [a, b](const Tensor& g) {
+		// ops.cpp:349-356: a's term g * b, then b's term g * a, each through accumulate_grad
+		bool first = false;
+		if (float* da = grad_if(a, first)) check(nnh_mul_backward(g.data(), b.data().data(), g.size(), da, first, g_stream));
+		if (float* db = grad_if(b, first)) check(nnh_mul_backward(g.data(), a.data().data(), g.size(), db, first, g_stream));
+	});
+}
+
+Value slice(const Value& x, int axis, size_t start, size_t end) {
+	const auto& xs = x.data().shape();
+	if (axis != 0) throw std::invalid_argument("nn::hip: slice takes axis 0");
+	if (xs.empty() || start >= end || end > xs[0]) throw TensorShapeError("nn::hip: slice out of range");
+	const size_t inner = x.data().size() / xs[0];
+	std::vector<size_t> ys = xs;
+	ys[0] = end - start;
+	Tensor y = Tensor::empty(ys);
+	if (y.size())
+		check_hip(hipMemcpyAsync(y.data(), x.data().data() + start * inner, y.size() * 4, hipMemcpyDeviceToDevice,
+		                         g_stream),
+		          "slice");
+	return Value::node(std::move(y), {x}, [x, start, inner](const Tensor& g) {
+		// ops.cpp:603-607: x.grad() (zeroed when fresh), then the band adds g
+		if (!x.requires_grad()) return;
+		float* dx = x.grad().data() + start * inner;
+		check(nnh_add_to_grad(dx, g.data(), g.size(), 0, g_stream));
+	});
+}
+
 Value gelu(const Value& x) {
 	Tensor y = Tensor::empty(x.data().shape());
 	Tensor th = Tensor::empty(x.data().shape());  // tanh(k (x + c x^3)), kept for the backward rule

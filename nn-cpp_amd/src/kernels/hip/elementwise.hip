@@ -1,6 +1,6 @@
-// elementwise.hip - the transformer's element-wise ops around the GEMMs: add with a broadcast right operand,
-// GELU (tanh form) forward and backward, embedding lookup and its gradient (src/autograd/ops.cpp:331-337, 451-481,
-// 1991-2015).
+// elementwise.hip - the transformer's element-wise ops around the GEMMs: add with a broadcast right operand, mul
+// (Dropout's mask), GELU (tanh form) forward and backward, embedding lookup and its gradient
+// (src/autograd/ops.cpp:331-357, 451-481, 1991-2015).
 //
 // GELU's tanh is nn-cpp's own (src/kernels/vmath.cpp:24-105): Cephes expf with the reference's constants and
 // operation order (x = n ln2 + r, ln2 split in two, a degree-5 polynomial in r, 2^n by building the exponent
@@ -159,6 +159,23 @@ __global__ void __launch_bounds__(256) embedding_backward_kernel(const float* __
 	if (on) dw[v * D + d] = acc;
 }
 
+// nn::mul (tensor.cpp:551-553): y = a * b, element by element
+__global__ void __launch_bounds__(256) mul_kernel(const float* __restrict__ a, const float* __restrict__ b, int64_t count,
+                                                  float* __restrict__ y) {
+	const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+	if (i < count) y[i] = a[i] * b[i];
+}
+
+// mul's backward term for one operand (ops.cpp:347-357 through accumulate_grad): t = g * other, stored as t + 0 into a
+// fresh gradient, else added
+__global__ void __launch_bounds__(256) mul_grad_kernel(const float* __restrict__ g, const float* __restrict__ other,
+                                                       int64_t count, float* __restrict__ d, int first) {
+	const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+	if (i >= count) return;
+	const float t = g[i] * other[i];
+	d[i] = first ? t + 0.0f : d[i] + t;
+}
+
 inline unsigned blocks_of(int64_t n) { return (unsigned)((n + 255) / 256); }
 
 }  // namespace
@@ -173,6 +190,18 @@ hipError_t add_bcast(const float* a, const float* b, int64_t outer, int64_t inne
 		                   reinterpret_cast<f32x4*>(y));
 	else
 		hipLaunchKernelGGL(add_bcast_kernel, dim3(blocks_of(total)), dim3(256), 0, s, a, b, total, inner, y);
+	return hipGetLastError();
+}
+
+hipError_t mul(const float* a, const float* b, int64_t count, float* y, hipStream_t s) {
+	if (count == 0) return hipSuccess;
+	hipLaunchKernelGGL(mul_kernel, dim3(blocks_of(count)), dim3(256), 0, s, a, b, count, y);
+	return hipGetLastError();
+}
+
+hipError_t mul_grad(const float* g, const float* other, int64_t count, float* d, int first, hipStream_t s) {
+	if (count == 0) return hipSuccess;
+	hipLaunchKernelGGL(mul_grad_kernel, dim3(blocks_of(count)), dim3(256), 0, s, g, other, count, d, first);
 	return hipGetLastError();
 }
 

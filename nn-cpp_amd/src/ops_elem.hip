@@ -23,6 +23,27 @@ int nnh_add_forward(const float* a, const float* b, size_t outer, size_t inner, 
 	return hip_status(add_bcast(a, b, (int64_t)outer, (int64_t)inner, y, reinterpret_cast<hipStream_t>(stream)), "add");
 }
 
+int nnh_mul_forward(const float* a, const float* b, size_t count, float* y, void* stream) {
+	if (!count_ok({count})) return fail(NNH_ERR_INVALID, "mul: size out of range (above 2^60 elements)");
+	if (count == 0) return NNH_OK;
+	if (!a || !b || !y) return fail(NNH_ERR_INVALID, "mul: null pointer");
+	const uint64_t n = (uint64_t)count * 4;
+	// y may be a or b itself (element by element), never a partial overlap of either
+	if (partial_overlap(y, n, a, n) || partial_overlap(y, n, b, n)) return fail(NNH_ERR_ALIAS, "mul: y overlaps part of a or b");
+	return hip_status(mul(a, b, (int64_t)count, y, reinterpret_cast<hipStream_t>(stream)), "mul");
+}
+
+int nnh_mul_backward(const float* g, const float* other, size_t count, float* d, int first, void* stream) {
+	if (!count_ok({count})) return fail(NNH_ERR_INVALID, "mul backward: size out of range (above 2^60 elements)");
+	if (count == 0) return NNH_OK;
+	if (!g || !other || !d) return fail(NNH_ERR_INVALID, "mul backward: null pointer");
+	const uint64_t n = (uint64_t)count * 4;
+	if (ranges_overlap(d, n, other, n) || partial_overlap(d, n, g, n))
+		return fail(NNH_ERR_ALIAS, "mul backward: d overlaps the other operand or part of g");
+	return hip_status(mul_grad(g, other, (int64_t)count, d, first ? 1 : 0, reinterpret_cast<hipStream_t>(stream)),
+	                  "mul backward");
+}
+
 int nnh_gelu_forward(const float* x, size_t count, float* y, float* tanh_saved, void* stream) {
 	if (!count_ok({count})) return fail(NNH_ERR_INVALID, "gelu: size out of range (above 2^60 elements)");
 	if (count == 0) return NNH_OK;

@@ -14,6 +14,7 @@
 #include "nn/nn/activation.hpp"
 #include "nn/nn/attention.hpp"
 #include "nn/nn/conv2d.hpp"
+#include "nn/nn/dropout.hpp"
 #include "nn/nn/flatten.hpp"
 #include "nn/nn/linear.hpp"
 #include "nn/nn/pool2d.hpp"
@@ -380,6 +381,11 @@ int nnref_norm_step(const float* x, size_t N, size_t c0, size_t side, size_t c1,
 //   2: MultiHeadAttention(64, 4 heads) with dropout 0.1 in training mode: the composed path through matmul_bt,
 //      scaled_masked_softmax, dropout and a batched matmul (attention.cpp:36-47).
 //   3: Sequential of Linear(20,30), ReLU, Linear(30,5) on a 3-D input (Linear is not folded with ReLU).
+//   4: Transformer{vocab 11, dim 16, heads 2, layers 2, max_len 12, mlp_ratio 2, dropout 0, causal, learned
+//      positions} on float ids x (x's gradient stays zero: ids are not differentiated).
+//   5: Sequential of Linear(20,30), Dropout(0.25) in training mode, ReLU, Linear(30,5).
+//   6: Transformer{vocab 13, dim 24, heads 3, layers 1, max_len 9, mlp_ratio 4, dropout 0.1, non-causal, sinusoidal
+//      positions} in evaluation mode.
 int nnref_module_run(int which, unsigned seed, const float* x, const size_t* xs, int xn, const float* g, float* out,
 		size_t out_cap, float* grads, size_t grads_cap, size_t* n_out, size_t* n_grads) {
 	return guard([&] {
@@ -403,12 +409,25 @@ int nnref_module_run(int which, unsigned seed, const float* x, const size_t* xs,
 		} else if (which == 2) {
 			m = std::make_unique<nn::MultiHeadAttention>(64, 4, false, 0.1f);
 			m->train(true);
-		} else {
+		} else if (which == 3) {
 			auto s = std::make_unique<nn::Sequential>();
 			s->add(std::make_unique<nn::Linear>(20, 30));
 			s->add(std::make_unique<nn::ReLU>());
 			s->add(std::make_unique<nn::Linear>(30, 5));
 			m = std::move(s);
+		} else if (which == 4) {
+			m = std::make_unique<nn::Transformer>(nn::TransformerConfig{11, 16, 2, 2, 12, 2, 0.0f, true, true});
+		} else if (which == 5) {
+			auto s = std::make_unique<nn::Sequential>();
+			s->add(std::make_unique<nn::Linear>(20, 30));
+			s->add(std::make_unique<nn::Dropout>(0.25f));
+			s->add(std::make_unique<nn::ReLU>());
+			s->add(std::make_unique<nn::Linear>(30, 5));
+			m = std::move(s);
+			m->train(true);
+		} else {
+			m = std::make_unique<nn::Transformer>(nn::TransformerConfig{13, 24, 3, 1, 9, 4, 0.1f, false, false});
+			m->eval();
 		}
 		const Value xv = Value::leaf(make(x, shape_of(xs, xn)), true);
 		const Value y = m->forward(xv);
@@ -425,6 +444,19 @@ int nnref_module_run(int which, unsigned seed, const float* x, const size_t* xs,
 			off += p.grad().size();
 		}
 		*n_grads = off;
+	});
+}
+
+// n draws of nn::derive_generator(stream) after nn::manual_seed(seed), the k-th generator of the stream for k = 0 ..
+// gens - 1 in turn (n / gens draws each): the seeding the module layer's initial values come from.
+int nnref_random_draws(unsigned long long seed, const char* stream, int gens, size_t n, unsigned* out) {
+	return guard([&] {
+		nn::manual_seed(seed);
+		size_t o = 0;
+		for (int k = 0; k < gens; ++k) {
+			std::mt19937 gen = nn::derive_generator(stream);
+			for (size_t i = 0; i < n / gens; ++i) out[o++] = static_cast<unsigned>(gen());
+		}
 	});
 }
 

@@ -4,23 +4,34 @@
 // every op in between reads and writes HBM; outputs and gradients are copied back at the end.
 // Return codes: 0 ok, 2 nn::hip::TensorShapeError, 1 any other exception.
 #include <cstring>
+#include <string>
+#include <memory>
+#include <stdexcept>
 #include <vector>
 
 #include "nn_hip.hpp"
+#include "nn_hip_modules.hpp"
 
 using nn::hip::Tensor;
 using nn::hip::Value;
 
 namespace {
 
+std::string g_last_error;
+
 template <typename F>
 int guard(F f) {
 	try {
 		f();
 		return 0;
-	} catch (const nn::hip::TensorShapeError&) {
+	} catch (const nn::hip::TensorShapeError& e) {
+		g_last_error = e.what();
 		return 2;
+	} catch (const std::exception& e) {
+		g_last_error = e.what();
+		return 1;
 	} catch (...) {
+		g_last_error = "unknown exception";
 		return 1;
 	}
 }
@@ -34,6 +45,9 @@ void out(const Tensor& t, float* dst) {
 }  // namespace
 
 extern "C" {
+
+// The message of the last exception a harness entry caught.
+const char* h_last_error(void) { return g_last_error.c_str(); }
 
 // nn-cpp's cnn_mnist model (apps/bench/workloads.cpp:113-137 with Sequential's Conv2d + ReLU folding,
 // src/nn/sequential.cpp:16-28): conv2d_relu(c0 -> c1, 3x3, pad 1) -> maxpool2d(2, 2) -> conv2d_relu(c1 -> c2) ->
@@ -199,6 +213,98 @@ int h_shape_errors(void) {
 	expect(10, [] { nn::hip::layernorm(Value::leaf(Tensor({2, 5})), Value::leaf(Tensor({4})), Value::leaf(Tensor({5})),
 	                                   1e-5f); });                                         // gamma of the wrong size
 	return bits;
+}
+
+// nn::hip::mul forward and backward on count elements: y = a * b, then the gradients of a and b from g; same = 1
+// passes a as both operands (its gradient stored by the first term, added to by the second).
+int h_mul_step(const float* a, const float* b, size_t count, int same, const float* g, float* y, float* da, float* db) {
+	return guard([&] {
+		Value av = param(a, {count});
+		Value bv = same ? av : param(b, {count});
+		Value r = nn::hip::mul(av, bv);
+		r.backward(Tensor::from_host({count}, g));
+		out(r.data(), y);
+		out(av.grad(), da);
+		if (!same) out(bv.grad(), db);
+	});
+}
+
+// n draws of nn::hip::derive_generator(stream) after nn::hip::manual_seed(seed), generators k = 0 .. gens - 1 of the
+// stream in turn (n / gens draws each); host only, no device work.
+int h_random_draws(unsigned long long seed, const char* stream, int gens, size_t n, unsigned* outp) {
+	return guard([&] {
+		nn::hip::manual_seed(seed);
+		size_t o = 0;
+		for (int k = 0; k < gens; ++k) {
+			std::mt19937 gen = nn::hip::derive_generator(stream);
+			for (size_t i = 0; i < n / gens; ++i) outp[o++] = static_cast<unsigned>(gen());
+		}
+	});
+}
+
+// The module layer (include/nn_hip_modules.hpp): the models of oracle/ref_shim.cpp's nnref_module_run, built with
+// nn::hip's modules after nn::hip::manual_seed(seed), the same input x (shape xs) and the output gradient g; out
+// receives the output and grads every parameter's gradient in parameters() order, then x's. *n_out and *n_grads
+// receive the counts; capacities are checked.
+int h_module_run(int which, unsigned seed, const float* x, const size_t* xs, int xn, const float* g, float* outp,
+                 size_t out_cap, float* grads, size_t grads_cap, size_t* n_out, size_t* n_grads) {
+	return guard([&] {
+		namespace H = nn::hip;
+		H::manual_seed(seed);
+		std::unique_ptr<H::Module> m;
+		if (which == 0) {
+			auto s = std::make_unique<H::Sequential>();
+			s->add(std::make_unique<H::Conv2d>(1, 8, 3, 1, 1));
+			s->add(std::make_unique<H::ReLU>());
+			s->add(std::make_unique<H::MaxPool2d>(2, 2));
+			s->add(std::make_unique<H::Conv2d>(8, 16, 3, 1, 1));
+			s->add(std::make_unique<H::ReLU>());
+			s->add(std::make_unique<H::MaxPool2d>(2, 2));
+			s->add(std::make_unique<H::Flatten>());
+			s->add(std::make_unique<H::Linear>(784, 128));
+			s->add(std::make_unique<H::ReLU>());
+			s->add(std::make_unique<H::Linear>(128, 10));
+			m = std::move(s);
+		} else if (which == 1) {
+			m = std::make_unique<H::MultiHeadAttention>(64, 4, true);
+		} else if (which == 3) {
+			auto s = std::make_unique<H::Sequential>();
+			s->add(std::make_unique<H::Linear>(20, 30));
+			s->add(std::make_unique<H::ReLU>());
+			s->add(std::make_unique<H::Linear>(30, 5));
+			m = std::move(s);
+		} else if (which == 4) {
+			m = std::make_unique<H::Transformer>(H::TransformerConfig{11, 16, 2, 2, 12, 2, 0.0f, true, true});
+		} else if (which == 5) {
+			auto s = std::make_unique<H::Sequential>();
+			s->add(std::make_unique<H::Linear>(20, 30));
+			s->add(std::make_unique<H::Dropout>(0.25f));
+			s->add(std::make_unique<H::ReLU>());
+			s->add(std::make_unique<H::Linear>(30, 5));
+			m = std::move(s);
+			m->train(true);
+		} else if (which == 6) {
+			m = std::make_unique<H::Transformer>(H::TransformerConfig{13, 24, 3, 1, 9, 4, 0.1f, false, false});
+			m->eval();
+		} else {
+			throw std::invalid_argument("h_module_run: unknown model");
+		}
+		const Value xv = param(x, std::vector<size_t>(xs, xs + xn));
+		const Value y = m->forward(xv);
+		y.backward(Tensor::from_host(y.data().shape(), g));
+		if (y.data().size() > out_cap) throw std::runtime_error("capacity");
+		out(y.data(), outp);
+		*n_out = y.data().size();
+		std::vector<Value> ps = m->parameters();
+		ps.push_back(xv);
+		size_t off = 0;
+		for (const Value& p : ps) {
+			if (off + p.grad().size() > grads_cap) throw std::runtime_error("capacity");
+			out(p.grad(), grads + off);
+			off += p.grad().size();
+		}
+		*n_grads = off;
+	});
 }
 
 }  // extern "C"
