@@ -234,13 +234,14 @@ int64_t gemm_workspace_floats(int64_t m, int64_t n, int64_t k, int64_t batch_cou
 }
 
 int64_t gemm_workspace_floats(const GemmCall& g) {
-	if (!depth_cut(g.m, g.n, g.k) || pieces_kernel_takes(g)) return 0;
+	if (!depth_cut(g.m, g.n, g.k) || pieces_kernel_takes(g) || pieces4_takes(g)) return 0;
 	return cut_plan(g.m, g.n, g.k).pieces * g.m * g.n * g.batch_count;
 }
 
 // Configurations kNumConfigs .. kNumConfigs + kValuShapes - 1 are the VALU kernel's lane blocks (gemm_valu.hip).
-// Configuration kNumConfigs + kValuShapes forces the VALU pieces kernel on a cut product it can take.
-int gemm_config_count() { return kNumConfigs + kValuShapes + 1; }
+// Configuration kNumConfigs + kValuShapes forces the VALU pieces kernel on a cut product it can take, and
+// kNumConfigs + kValuShapes + 1 the 16x16x4 MFMA pieces kernel.
+int gemm_config_count() { return kNumConfigs + kValuShapes + 2; }
 const char* gemm_config_name(int config) {
 	if (config == kNumConfigs + kValu2x2) return "valu 32x32 (2x2 chains per lane)";
 	if (config == kNumConfigs + kValu1x2) return "valu 16x32 (1x2 chains per lane)";
@@ -249,6 +250,7 @@ const char* gemm_config_name(int config) {
 	if (config == kNumConfigs + kValuBc1) return "valu bcast 16x16 (1 chain per lane, A by DPP)";
 	if (config == kNumConfigs + kValuBc2) return "valu bcast 32x16 (2 chains per lane, A by DPP)";
 	if (config == kNumConfigs + kValuShapes) return "valu pieces 16x16 (every piece of a cut output in one lane)";
+	if (config == kNumConfigs + kValuShapes + 1) return "mfma pieces 16x16x4 (a wave per piece, 16x16 tiles)";
 
 	return (config >= 0 && config < kNumConfigs) ? configs()[config].name : "";
 }
@@ -258,6 +260,7 @@ hipError_t gemm_launch(const GemmCall& g, hipStream_t s, int config, float* work
 	hipError_t e = prepare_device();
 	if (e != hipSuccess) return e;
 	const bool force_pieces = config == kNumConfigs + kValuShapes;
+	const bool force_pieces4 = config == kNumConfigs + kValuShapes + 1;
 	// the VALU kernel: forced, or chosen by shape, for a product it can take
 	const bool valu_ok = !g.gather && !g.rowsum && g.k > 0 && !depth_cut(g.m, g.n, g.k) && g.m < (1 << 30) &&
 	                     g.n < (1 << 30) && g.k < (1 << 30);
@@ -268,7 +271,12 @@ hipError_t gemm_launch(const GemmCall& g, hipStream_t s, int config, float* work
 	const Config& cf = configs()[config];
 
 	if (g.gather && g.ta) return hipErrorInvalidValue;
-	if (g.rowsum && (depth_cut(g.m, g.n, g.k) || g.batch_count != 1 || g.gather || !g.ta || g.tb))
+	// the 16x16x4 pieces kernel: its own route, forced, or the only one for two-stage row sums (a forced VALU pieces
+	// configuration keeps the VALU kernel where that can take the product)
+	const bool p4 = g.rowsum ? pieces4_takes(g)
+	                         : force_pieces4 ? pieces_kernel_takes(g) : !force_pieces && pieces4_takes(g);
+	if (p4) return gemm_pieces4_launch(g, s);
+	if (g.rowsum && (g.rowsum_outer > 0 || depth_cut(g.m, g.n, g.k) || g.batch_count != 1 || g.gather || !g.ta || g.tb))
 		return hipErrorInvalidValue;
 	if (force_pieces ? valu_pieces_ok(g) : valu_pieces_takes(g))
 		return gemm_valu_pieces_launch(g, s);
@@ -307,7 +315,7 @@ hipError_t gemm_launch_pair(const GemmCall& g0, const GemmCall& g1, hipStream_t 
 	launched = false;
 	// g0 = A B and g1 = A^T B (row sums allowed), single matrices, no depth cut, both on one configuration that
 	// has the pair kernels
-	if (g0.ta || g0.tb || g0.gather || g0.rowsum || !g1.ta || g1.tb || g1.gather) return hipSuccess;
+	if (g0.ta || g0.tb || g0.gather || g0.rowsum || !g1.ta || g1.tb || g1.gather || g1.rowsum_outer > 0) return hipSuccess;
 	if (g0.batch_count != 1 || g1.batch_count != 1 || g0.batch.ndim != 0 || g1.batch.ndim != 0) return hipSuccess;
 	if (g0.m == 0 || g0.n == 0 || g1.m == 0 || g1.n == 0) return hipSuccess;
 	if (depth_cut(g0.m, g0.n, g0.k) || depth_cut(g1.m, g1.n, g1.k)) return hipSuccess;

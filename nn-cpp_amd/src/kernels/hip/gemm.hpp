@@ -28,6 +28,9 @@ struct GemmCall {
 	ColGather col{};
 	float* rowsum = nullptr;  // optional row sums of op(A) (GemmArgs::rowsum); A transposed, B not, one matrix, no depth cut
 	int rowsum_combine = 0;
+	// > 0: the row sums are two ordered sums instead (GemmArgs::rowsum_outer), on a cut product the 16x16x4 pieces
+	// kernel takes (pieces4_takes)
+	int64_t rowsum_outer = 0;
 };
 
 // Numerics modes (nnh_set_numerics). kNumericsNnCpp: nn-cpp's bits. kNumericsSplitDepth: every product with
@@ -77,6 +80,11 @@ bool depth_cut(int64_t m, int64_t n, int64_t k);
 bool pieces_kernel_takes(int64_t m, int64_t n, int64_t k, int64_t batch_count, bool gather_or_rowsum);
 bool pieces_kernel_takes(const GemmCall& g);  // also: leading dimensions below 2^24
 hipError_t gemm_pieces_launch(const GemmCall& g, hipStream_t s);
+// The same products on the 16x16x4 MFMA: 16 x 16 tiles, a wave per piece, operands loaded into registers. It is
+// the route of the cut products it takes (pieces4_takes: A transposed and B not, the weight gradient's layout, also
+// with two-stage row sums); a forced configuration runs it on any product pieces_kernel_takes.
+bool pieces4_takes(const GemmCall& g);
+hipError_t gemm_pieces4_launch(const GemmCall& g, hipStream_t s);
 
 // Floats of workspace a call needs: the partial sums of a depth cut the pieces kernel does not take, else 0. The
 // shape-only overload (plans and workspace queries) assumes leading dimensions below 2^24, which every op's own

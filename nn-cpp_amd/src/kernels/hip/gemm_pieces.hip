@@ -14,6 +14,7 @@
 // after a barrier each thread adds the pieces in
 // piece order for its outputs, and the store applies accumulate, bias and ReLU as the reference's does.
 #include <mutex>
+#include <type_traits>
 
 #include "gemm.hpp"
 #include "gemm_tile.hpp"
@@ -80,6 +81,22 @@ __device__ __forceinline__ void wave_lds_sync() {
 	__builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
 	__builtin_amdgcn_wave_barrier();
 	__builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// The store of one finished output (gemm.cpp:481-484) and the op's bias and ReLU (src/autograd/ops.cpp:726-730,
+// 1396-1409): v is the sum of the pieces; accumulate adds it to the old C.
+__device__ __forceinline__ void put_output(const GemmArgs& p, float* __restrict__ Cp, unsigned char* alive, int row,
+                                           int col, float v) {
+	const int64_t off = (int64_t)row * p.ldc + col;
+	float y = p.accumulate ? Cp[off] + v : v;
+	if (p.ep.bias_mode == kBiasCol) y = y + p.ep.bias[col];
+	else if (p.ep.bias_mode == kBiasRow) y = y + p.ep.bias[row];
+	if (p.ep.relu) {
+		const bool on = y > 0.0f;
+		if (alive) alive[off] = on ? 1 : 0;
+		y = on ? y : 0.0f;
+	}
+	Cp[off] = y;
 }
 
 template <bool TA, bool TB, bool VEC>
@@ -201,19 +218,184 @@ __global__ void __launch_bounds__(kMaxPieces * 64) sgemm_pieces_kernel(const Gem
 #pragma unroll
 		for (int e = 0; e < 4; ++e) {
 			const int row = m0 + 16 * (blk >> 1) + 4 * (l >> 4) + e;
-			if (row >= p.m) continue;
-			const int64_t off = (int64_t)row * p.ldc + col;
-			float y = p.accumulate ? Cp[off] + v[e] : v[e];
-			if (p.ep.bias_mode == kBiasCol) y = y + p.ep.bias[col];
-			else if (p.ep.bias_mode == kBiasRow) y = y + p.ep.bias[row];
-			if (p.ep.relu) {
-				const bool on = y > 0.0f;
-				if (alive) alive[off] = on ? 1 : 0;
-				y = on ? y : 0.0f;
-			}
-			Cp[off] = y;
+			if (row < p.m) put_output(p, Cp, alive, row, col, v[e]);
 		}
 	}
+}
+
+constexpr int kRsMaxInner = 256;  // inner indices of the two-stage row sums (stage-one results held in LDS)
+constexpr int kRsSteps = 16;      // outer indices whose loads are in flight together
+constexpr int kRsWaves = 2;       // row-sum waves
+constexpr int kRsMaxPieces = 10;  // pieces beside them: at most 12 waves, three a SIMD, room for the loads
+
+// The pieces of a 16 x 16 tile, parked in LDS by piece (done[q][row][column]), added in piece order and stored.
+__device__ __forceinline__ void finish_tile(const GemmArgs& p, int64_t oc, int m0, int n0, int tid, int nthreads,
+                                            const float* done) {
+	constexpr int kU = 16;
+	float* __restrict__ Cp = p.c + oc;
+	unsigned char* alive = p.ep.alive ? p.ep.alive + oc : nullptr;
+	for (int o = tid; o < kU * kU; o += nthreads) {
+		float v = done[o];
+		for (int q = 1; q < p.pieces; ++q) v = v + done[q * kU * kU + o];
+		const int row = m0 + o / kU, col = n0 + o % kU;
+		if (row < p.m && col < p.n) put_output(p, Cp, alive, row, col, v);
+	}
+}
+
+// Two-stage row sums of op(A) = A^T for rows m0 .. m0 + 15 (columns of A, k x m with leading dimension lda), by
+// kRsWaves waves: A's row index is o * r1 + i (outer o < r0, inner i < r1 = k / r0).
+// Stage one (Tensor::sum(0) over the outer axis, tensor.cpp:422-456): for each inner i, s1[i] = +0 + A[i] +
+// A[r1 + i] + ... in outer order, parked in LDS as part[i][16]. Lane l of row-sum wave w sums four columns
+// 4 (l % 4) .. + 3 (one 16-byte load per step) for inner indices i = ib + l / 4 + 16 (2 w + u), u < 2, with
+// kRsSteps outer steps of loads in flight.
+// Stage two (the second sum(0)), after the workgroup's barrier: rowsum = +0 + s1[0] + s1[1] + ... in inner order,
+// lane c of the first row-sum wave for row m0 + c; then the combine of GemmArgs::rowsum_combine.
+// The caller guarantees m and lda multiples of 4, A 16-byte aligned, r1 <= kRsMaxInner and k lda < 2^29 (every
+// byte offset into A below 2^31).
+__device__ __forceinline__ void rowsums_stage1(const GemmArgs& p, const float* __restrict__ A, int m0, int lane, int w,
+                                               float* part) {
+	const int r0 = p.rowsum_outer, r1 = p.k / p.rowsum_outer;
+	const int cq = lane & 3, il = lane >> 2;
+	// a column quad past m loads the last quad instead and is never summed in stage two
+	const int col = min(m0 + 4 * cq, p.m - 4);
+	const __amdgpu_buffer_rsrc_t res = rsrc(A);
+	for (int ib = 0; ib < r1; ib += 16 * 2 * kRsWaves) {
+		// byte offsets: the inner index and column per lane, the outer index in a scalar register
+		int voff[2];
+#pragma unroll
+		for (int u = 0; u < 2; ++u) voff[u] = (min(ib + il + 16 * (2 * w + u), r1 - 1) * (int)p.lda + col) * 4;
+		f32x4 acc[2];
+#pragma unroll
+		for (int u = 0; u < 2; ++u) acc[u] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+		for (int o0 = 0; o0 < r0; o0 += kRsSteps) {
+			f32x4 v[kRsSteps][2];
+#pragma unroll
+			for (int st = 0; st < kRsSteps; ++st) {
+				const int soff = min(o0 + st, r0 - 1) * r1 * (int)p.lda * 4;
+#pragma unroll
+				for (int u = 0; u < 2; ++u)
+					v[st][u] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(res, voff[u], soff, 0));
+			}
+#pragma unroll
+			for (int st = 0; st < kRsSteps; ++st)
+				if (o0 + st < r0)
+#pragma unroll
+					for (int u = 0; u < 2; ++u)
+#pragma unroll
+						for (int e = 0; e < 4; ++e) acc[u][e] = acc[u][e] + v[st][u][e];
+		}
+#pragma unroll
+		for (int u = 0; u < 2; ++u) {
+			const int i = ib + il + 16 * (2 * w + u);
+			if (i < r1) *reinterpret_cast<f32x4*>(part + i * 16 + 4 * cq) = acc[u];
+		}
+	}
+}
+
+__device__ __forceinline__ void rowsums_stage2(const GemmArgs& p, int m0, int lane, const float* part) {
+	const int r1 = p.k / p.rowsum_outer;
+	if (lane >= 16 || m0 + lane >= p.m) return;
+	float s = 0.0f;
+	for (int i0 = 0; i0 < r1; i0 += 16) {
+		float v[16];
+#pragma unroll
+		for (int e = 0; e < 16; ++e) v[e] = part[min(i0 + e, r1 - 1) * 16 + lane];
+#pragma unroll
+		for (int e = 0; e < 16; ++e)
+			if (i0 + e < r1) s = s + v[e];
+	}
+	float* dst = p.rowsum + m0 + lane;
+	if (p.rowsum_combine == 0) *dst = s;
+	else if (p.rowsum_combine == 1) *dst = s + 0.0f;
+	else *dst = *dst + s;
+}
+
+// The same cut on the 16x16x4 MFMA (Mfma<kMf16x4>: one instruction advances each chain of a 16 x 16 block four
+// depth steps, bit-identical to four fmaf in order). One workgroup owns a 16 x 16 tile of C and one wave per piece,
+// so a product with few outputs still spreads over many CUs (a 64 x 64 output is 16 workgroups). A wave loads its
+// operands straight into the instruction's lane layout, 128 depth indices at a time with all 64 loads in flight
+// (lane l supplies row or column l % 16 at depth 4 s + l / 16 of step s), with no LDS staging; past the piece's end
+// A is +0 and B is -0 as above. The finished pieces meet in LDS and are added in piece order.
+//
+// RS (A transposed, B not: a linear layer's weight gradient G^T X): two more waves in the workgroups of the first
+// column tile fold the two-stage row sums of op(A) = G^T for the tile's 16 rows, the bias gradient of a
+// three-dimensional G (GemmArgs::rowsum_outer), while the MFMA waves run: 16-byte loads of four columns, chains
+// over the outer index per inner index parked in LDS, then, after the barrier, one chain over the inner index per
+// row.
+
+template <bool TA, bool TB, bool RS>
+__global__ void __launch_bounds__(RS ? (kRsMaxPieces + kRsWaves) * 64 : kMaxPieces * 64) sgemm_pieces4_kernel(const GemmArgs p) {
+	static_assert(!RS || (TA && !TB), "row sums are compiled for the weight-gradient layout only");
+	constexpr int kU = 16;      // tile side
+	constexpr int kSub = 8;     // MFMA steps per 32-deep sub-slab (one buffer resource each)
+	constexpr int kSteps = 32;  // MFMA steps per chunk: 128 depth indices
+	__shared__ float done[kMaxPieces * kU * kU];
+	__shared__ float part[RS ? kRsMaxInner * kU : 1];
+	const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+	const int nthreads = blockDim.x;
+	const int tiles = p.tiles_m * p.tiles_n;
+	const int lid = xcd_remap((int)blockIdx.x, tiles * p.batch_count);
+	const int t = lid % tiles, bi = lid / tiles;
+	const int m0 = (t / p.tiles_n) * kU, n0 = (t % p.tiles_n) * kU;
+	int64_t oa = 0, ob = 0, oc = 0;
+	if (p.batch.ndim > 0) batch_offsets(p.batch, bi, oa, ob, oc);
+	const float* __restrict__ A = p.a + oa;
+	const float* __restrict__ B = p.b + ob;
+	const int lda = (int)p.lda, ldb = (int)p.ldb;
+	const int r = lane & 15, j = lane >> 4;
+	if (RS && wave >= p.pieces) {
+		if (n0 == 0) rowsums_stage1(p, A, m0, lane, wave - p.pieces, part);
+		__syncthreads();
+		if (n0 == 0 && wave == p.pieces) rowsums_stage2(p, m0, lane, part);
+		finish_tile(p, oc, m0, n0, tid, nthreads, done);
+		return;
+	}
+	const bool row_in = m0 + r < p.m, col_in = n0 + r < p.n;
+	const int k_lo = wave * p.piece_k, k_hi = min(p.k, k_lo + p.piece_k);
+	f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+	// one chunk of up to 128 depth indices: every load issued before the first MFMA; PART (the piece's last chunk
+	// shorter than 128) masks the depth and turns B's +0 fill past the end into -0 at the MFMA
+	auto chunk = [&](int kc, auto part_tag) {
+		constexpr bool PART = decltype(part_tag)::value;
+		const int kv = k_hi - kc;
+		float a[kSteps], b[kSteps];
+#pragma unroll
+		for (int q = 0; q < kSteps / kSub; ++q) {
+			// a sub-slab's offsets stay below 32 rows of a leading dimension (below 2^24)
+			const int k0 = 4 * kSub * q;
+			const __amdgpu_buffer_rsrc_t ares =
+			    rsrc(TA ? A + (int64_t)(kc + k0) * lda + m0 : A + (int64_t)m0 * lda + kc + k0);
+			const __amdgpu_buffer_rsrc_t bres =
+			    rsrc(TB ? B + (int64_t)n0 * ldb + kc + k0 : B + (int64_t)(kc + k0) * ldb + n0);
+#pragma unroll
+			for (int u = 0; u < kSub; ++u) {
+				const int d = 4 * u + j;
+				const bool din = !PART || k0 + d < kv;
+				const int aoff = row_in && din ? (TA ? d * lda + r : r * lda + d) * 4 : kOob;
+				const int boff = col_in && din ? (TB ? r * ldb + d : d * ldb + r) * 4 : kOob;
+				a[kSub * q + u] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(ares, aoff, 0, 0));
+				b[kSub * q + u] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(bres, boff, 0, 0));
+			}
+		}
+		__builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+		for (int s = 0; s < kSteps; ++s) {
+			float bv = b[s];
+			if (PART) bv = __builtin_bit_cast(float, __builtin_bit_cast(unsigned, bv) | (4 * s + j < kv ? 0u : 0x80000000u));
+			acc = Mfma<kMf16x4>::mma(a[s], bv, acc);
+		}
+		__builtin_amdgcn_sched_barrier(0);
+	};
+	for (int kc = k_lo; kc < k_hi; kc += 4 * kSteps) {
+		if (k_hi - kc >= 4 * kSteps) chunk(kc, std::false_type{});
+		else chunk(kc, std::true_type{});
+	}
+	// register e of lane l holds row 4 (l / 16) + e, column l % 16 of the tile
+	float* const mine = done + wave * kU * kU;
+#pragma unroll
+	for (int e = 0; e < 4; ++e) mine[(4 * j + e) * kU + r] = acc[e];
+	__syncthreads();
+	finish_tile(p, oc, m0, n0, tid, nthreads, done);
 }
 
 using PiecesFn = void (*)(const GemmArgs);
@@ -293,6 +475,57 @@ hipError_t gemm_pieces_launch(const GemmCall& g, hipStream_t s) {
 	if (blocks > 0x7fffffff) return hipErrorInvalidConfiguration;
 	const int f = (g.ta ? 2 : 0) + (g.tb ? 1 : 0);
 	hipLaunchKernelGGL(fns[vec ? 1 : 0][f], dim3((unsigned)blocks), dim3(p.pieces * 64), p.pieces * kPerWaveBytes, s, p);
+	return hipGetLastError();
+}
+
+bool pieces4_takes(const GemmCall& g) {
+	// Measured (device time on one MI355X, against the VALU pieces kernel that took these before): A transposed and
+	// B not, the weight gradient's layout, 64 x 64 x 1024 4.37 against 8.36 us, 256 x 64 x 1024 4.44 against 8.82,
+	// 128 x 128 x 768 4.31 against 8.12. A k-contiguous op(A) or op(B) (16 rows per load, one element each) is
+	// slower here than on the other kernels: 64 x 64 x 1024 NN 10.4 against 7.1, NT 16.9 against 6.6.
+	if (!g.ta || g.tb || g.gather || !pieces_kernel_takes(g.m, g.n, g.k, g.batch_count, false) || g.lda >= kMaxLd ||
+	    g.ldb >= kMaxLd)
+		return false;
+	if (!g.rowsum) return true;
+	// two-stage row sums: one matrix, the row-sum waves beside at most kRsMaxPieces piece waves, 16-byte loads of A
+	const CutPlan plan = cut_plan(g.m, g.n, g.k);
+	return g.rowsum_outer > 0 && g.k % g.rowsum_outer == 0 && g.k / g.rowsum_outer <= kRsMaxInner &&
+	       g.batch_count == 1 && plan.pieces <= kRsMaxPieces && g.m % 4 == 0 && g.lda % 4 == 0 &&
+	       g.k * g.lda < (int64_t(1) << 29) &&
+	       reinterpret_cast<uintptr_t>(g.a) % 16 == 0;
+}
+
+hipError_t gemm_pieces4_launch(const GemmCall& g, hipStream_t s) {
+	static const PiecesFn fns[5] = {sgemm_pieces4_kernel<false, false, false>, sgemm_pieces4_kernel<false, true, false>,
+	                                sgemm_pieces4_kernel<true, false, false>, sgemm_pieces4_kernel<true, true, false>,
+	                                sgemm_pieces4_kernel<true, false, true>};
+	if (g.rowsum ? !pieces4_takes(g) : !pieces_kernel_takes(g)) return hipErrorInvalidValue;
+	const CutPlan plan = cut_plan(g.m, g.n, g.k);
+	GemmArgs p{};
+	p.a = g.a;
+	p.b = g.b;
+	p.c = g.c;
+	p.lda = g.lda;
+	p.ldb = g.ldb;
+	p.ldc = g.ldc;
+	p.m = (int)g.m;
+	p.n = (int)g.n;
+	p.k = (int)g.k;
+	p.accumulate = g.accumulate;
+	p.tiles_m = (int)((g.m + 15) / 16);
+	p.tiles_n = (int)((g.n + 15) / 16);
+	p.batch_count = (int)g.batch_count;
+	p.batch = g.batch;
+	p.ep = g.ep;
+	p.pieces = (int)plan.pieces;
+	p.piece_k = (int)plan.piece_k;
+	p.rowsum = g.rowsum;
+	p.rowsum_combine = g.rowsum_combine;
+	p.rowsum_outer = (int)g.rowsum_outer;
+	const int64_t blocks = (int64_t)p.tiles_m * p.tiles_n * p.batch_count;
+	if (blocks > 0x7fffffff) return hipErrorInvalidConfiguration;
+	const int f = g.rowsum ? 4 : (g.ta ? 2 : 0) + (g.tb ? 1 : 0);
+	hipLaunchKernelGGL(fns[f], dim3((unsigned)blocks), dim3((p.pieces + (g.rowsum ? kRsWaves : 0)) * 64), 0, s, p);
 	return hipGetLastError();
 }
 

@@ -150,6 +150,10 @@ struct GemmArgs {
 	// combine: 0 store s, 1 store s + 0.0f, 2 rowsum[i] += s
 	float* rowsum;
 	int rowsum_combine;
+	// > 0 (the 16x16x4 pieces kernel only): rowsum[i] is two ordered sums instead, as Tensor::sum(0) applied twice
+	// to op(A)'s row i viewed as [rowsum_outer][k / rowsum_outer]: first over the outer index for each inner one,
+	// each from +0, then over the inner index from +0; combined as above
+	int rowsum_outer;
 };
 
 __device__ __forceinline__ void batch_offsets(const BatchDesc& d, int64_t bi, int64_t& oa, int64_t& ob,

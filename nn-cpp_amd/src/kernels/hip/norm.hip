@@ -891,66 +891,74 @@ __global__ void __launch_bounds__(kLnThreads) ln_dgamma_kernel(const float* __re
 }
 
 // dgamma and dbeta for at most 1024 rows (transformer_tiny's 16 x 64 tokens): the same chains, one pass. A
-// workgroup of 1024 threads owns 16 columns; every thread loads 16 rows of its column (g, x, the rows' mean and
-// inv_std, all in flight at once) and parks g * ((x - mean) * inv_std) and g in LDS; then lanes 0-15 add the
-// products down their column in row order (dgamma) and lanes 16-31 the gradients (dbeta), 16 LDS reads ahead.
-constexpr int kLnSmallCols = 16, kLnSmallRows = 1024, kLnSmallThreads = 1024;
+// workgroup of 1024 threads owns kLnSmallCols columns; every thread loads kLnSmallCols rows of its column (g, x,
+// the rows' mean and inv_std, all in flight at once) and parks g * ((x - mean) * inv_std) and g in LDS, column by
+// column; then one lane per column adds the products down it in row order (dgamma) and one the gradients
+// (dbeta), four rows per 16-byte LDS read and 32 rows read ahead of the adds. Four columns a workgroup spread the
+// loads over 16 CUs at D = 64 (a CU's address unit takes one row per lane and load). Rows past R are parked as +0:
+// a chain from +0 never holds -0 (x + (-x) rounds to +0, and no sum of finite floats underflows to zero), so adding
+// +0 leaves it unchanged.
+constexpr int kLnSmallCols = 4, kLnSmallRows = 1024, kLnSmallThreads = 1024;
+constexpr int kLnSmallPitch = kLnSmallRows + 4;  // a column's rows, padded against bank conflicts of the stores
 
 __global__ void __launch_bounds__(kLnSmallThreads) ln_dgamma_small_kernel(
     const float* __restrict__ g, const float* __restrict__ x, const float* __restrict__ mean,
     const float* __restrict__ inv, int R, int D, float* dgamma, int dg_first, float* dbeta, int db_first) {
-	__shared__ float buf[2][kLnSmallRows][kLnSmallCols];
+	__shared__ __align__(16) float buf[2][kLnSmallCols][kLnSmallPitch];
+	constexpr int kRowStep = kLnSmallThreads / kLnSmallCols;
 	const int tid = threadIdx.x;
-	const int c = tid & (kLnSmallCols - 1), r0 = tid / kLnSmallCols;  // rows r0 + 64 u
+	const int c = tid % kLnSmallCols, r0 = tid / kLnSmallCols;  // rows r0 + kRowStep u
 	const int c0 = blockIdx.x * kLnSmallCols;
 	const int col = min(c0 + c, D - 1);
-	constexpr int kPer = kLnSmallRows * kLnSmallCols / kLnSmallThreads;
+	constexpr int kPer = kLnSmallRows / kRowStep;
 	float gv[kPer], xv[kPer], mv[kPer], iv[kPer];
 #pragma unroll
 	for (int u = 0; u < kPer; ++u) {
-		const int64_t r = min(r0 + 64 * u, R - 1);
+		const int64_t r = min(r0 + kRowStep * u, R - 1);
 		gv[u] = g[r * D + col];
 		xv[u] = x[r * D + col];
 		mv[u] = mean[r];
 		iv[u] = inv[r];
 	}
+	// the chains read whole blocks of 32 rows
+	const int rpad = (R + 31) & ~31;
 #pragma unroll
 	for (int u = 0; u < kPer; ++u) {
-		const int r = r0 + 64 * u;
-		buf[0][r][c] = gv[u] * ((xv[u] - mv[u]) * iv[u]);
-		buf[1][r][c] = gv[u];
+		const int r = r0 + kRowStep * u;
+		if (r < rpad) {
+			const bool in = r < R;
+			buf[0][c][r] = in ? gv[u] * ((xv[u] - mv[u]) * iv[u]) : 0.0f;
+			buf[1][c][r] = in ? gv[u] : 0.0f;
+		}
 	}
 	__syncthreads();
 	if (tid >= 2 * kLnSmallCols) return;
-	const float* v = &buf[tid / kLnSmallCols][0][c];
-	// rows in order, the next sixteen rows' reads in flight while sixteen are added
-	float acc = 0.0f, t0[16], t1[16];
-	int i = 0;
-	bool have0 = R >= 16;  // t0 holds rows i .. i + 15
-	if (have0) {
+	const f32x4* v = reinterpret_cast<const f32x4*>(&buf[tid / kLnSmallCols][c][0]);
+	// rows in order: block b's eight reads in flight while block b - 1 is added
+	float acc = 0.0f;
+	f32x4 t[2][8];
 #pragma unroll
-		for (int u = 0; u < 16; ++u) t0[u] = v[u * kLnSmallCols];
-	}
-	while (i + 32 <= R) {
+	for (int e = 0; e < 8; ++e) t[0][e] = v[e];
+	for (int i = 0; i < rpad; i += 64) {
+		const bool more = i + 32 < rpad;
+		if (more) {
 #pragma unroll
-		for (int u = 0; u < 16; ++u) t1[u] = v[(i + 16 + u) * kLnSmallCols];
-#pragma unroll
-		for (int u = 0; u < 16; ++u) acc = acc + t0[u];
-		have0 = i + 48 <= R;
-		if (have0) {
-#pragma unroll
-			for (int u = 0; u < 16; ++u) t0[u] = v[(i + 32 + u) * kLnSmallCols];
+			for (int e = 0; e < 8; ++e) t[1][e] = v[(i + 32) / 4 + e];
 		}
 #pragma unroll
-		for (int u = 0; u < 16; ++u) acc = acc + t1[u];
-		i += 32;
-	}
-	if (have0 && i + 16 <= R) {
+		for (int e = 0; e < 8; ++e)
 #pragma unroll
-		for (int u = 0; u < 16; ++u) acc = acc + t0[u];
-		i += 16;
+			for (int q = 0; q < 4; ++q) acc = acc + t[0][e][q];
+		if (!more) break;
+		if (i + 64 < rpad) {
+#pragma unroll
+			for (int e = 0; e < 8; ++e) t[0][e] = v[(i + 64) / 4 + e];
+		}
+#pragma unroll
+		for (int e = 0; e < 8; ++e)
+#pragma unroll
+			for (int q = 0; q < 4; ++q) acc = acc + t[1][e][q];
 	}
-	for (; i < R; ++i) acc = acc + v[i * kLnSmallCols];
 	if (c0 + c >= D) return;
 	const int j = c0 + c;
 	if (tid < kLnSmallCols) {

@@ -105,6 +105,21 @@ int nnh_linear_backward(const float* g, const float* x, const float* w, const si
 		if (!g) return fail(NNH_ERR_INVALID, "G is null");
 		if (ranges_overlap(db, n * 4, g, (uint64_t)M * n * 4)) return fail(NNH_ERR_ALIAS, "db overlaps G");
 	}
+	// db of a three-dimensional G is the two ordered sums of sum_to_shape (first over axis 0, then axis 1, each
+	// from +0): folded into a cut dW product that runs on the 16x16x4 pieces kernel, which sums G's columns in one
+	// more wave while the product runs
+	bool db_in_pieces = false;
+	if (dw && db && nlead == 2 && M > 0 && K > 0 && n > 0 && depth_cut((int64_t)n, (int64_t)K, (int64_t)M) &&
+	    !ranges_overlap(db, n * 4, dw, (uint64_t)n * K * 4) && !ranges_overlap(db, n * 4, x, (uint64_t)M * K * 4)) {
+		GemmCall t = cw;
+		t.rowsum = db;
+		t.rowsum_combine = db_first ? 1 : 2;
+		t.rowsum_outer = (int64_t)lead[0];
+		if (pieces4_takes(t)) {
+			cw = t;
+			db_in_pieces = true;
+		}
+	}
 	{
 		const int rc = check_workspace(stream, linear_backward_ws(lead, nlead, M, K, n, dx, dw, db));
 		if (rc != NNH_OK) return rc;
@@ -133,7 +148,7 @@ int nnh_linear_backward(const float* g, const float* x, const float* w, const si
 			if (rc != NNH_OK) return rc;
 		}
 	}
-	if (db && n > 0 && !db_in_dw) {
+	if (db && n > 0 && !db_in_dw && !db_in_pieces) {
 		// accumulate_grad(bias, G): Tensor::sum(0) once per leading axis (ops.cpp:35-53), then stored as
 		// s + 0.0f into a fresh gradient or added (ops.cpp:85-99)
 		const int combine = db_first ? 1 : 2;

@@ -156,6 +156,42 @@ def test_linear_bias_gradient_in_weight_product(gpu, oracle):
                 assert_same(host(t), wv, (M, K, n, lead, first, key), nan_equal=(ci == 4))
 
 
+def test_linear_bias_gradient_in_cut_weight_product(gpu, oracle):
+    """A 3-D gradient whose weight product takes nn-cpp's depth cut runs dW on the 16x16x4 pieces kernel, and db
+    (sum_to_shape's two ordered sums: over axis 0 for each index of axis 1, then over axis 1, each from +0) is
+    folded into that launch: transformer_tiny's attention, fc1 and fc2 gradients ({16, 64} rows), 256 rows of the
+    second axis (the most the fold takes), ragged output tiles (n = 68, 20); past the fold's limits the separate
+    sums take over (257 rows of the second axis, n not a multiple of 4). Both combines, and special values in G
+    (-0 columns, infinities) whose sums keep their sign; every output against the oracle, bit for bit."""
+    import nnh
+    cases = [  # (leading shape, in K, out n)
+        ((16, 64), 64, 64), ((16, 64), 64, 256), ((16, 64), 256, 64), ((4, 256), 32, 68), ((2, 384), 80, 20),
+        ((5, 257), 32, 36), ((3, 200), 64, 30),
+    ]
+    for ci, (lead, K, n) in enumerate(cases):
+        M = lead[0] * lead[1]
+        x = synth.mt19937_uniform(2000 + ci, M * K).reshape(lead + (K,))
+        w = synth.mt19937_uniform(2100 + ci, n * K).reshape(n, K)
+        gr = synth.normal(2200 + ci, lead + (n,))
+        if ci == 3:
+            gr[:, :, 1] = -0.0
+            gr[1, 5, 2] = np.inf
+            gr[2, 7, 3], gr[3, 9, 3] = np.inf, -np.inf
+            gr[:, 3, 4] = -0.0
+        for first in (True, False):
+            dx0 = synth.mt19937_uniform(2300 + ci, M * K).reshape(lead + (K,))
+            dw0 = synth.mt19937_uniform(2400 + ci, n * K).reshape(n, K)
+            db0 = synth.mt19937_uniform(2500 + ci, n)
+            if ci == 3:
+                db0[1] = -0.0
+            dx, dw, db = dev(dx0), dev(dw0), dev(db0)
+            nnh.linear_backward(dev(gr), dev(x), dev(w), dx, first, dw, first, db, first)
+            want = oracle.linear_backward(gr, x, w, dx=dx0.copy(), dx_first=first, dw=dw0.copy(), dw_first=first,
+                                          db=db0.copy(), db_first=first)
+            for t, wv, key in zip((dx, dw, db), want, ("dx", "dw", "db")):
+                assert_same(host(t), wv, (lead, K, n, first, key), nan_equal=(ci == 3))
+
+
 def test_linear_backward_dx_dw_in_one_launch(gpu, oracle):
     """dX = G W and dW = G^T X of one Linear run in one launch when both pick the same small-tile configuration
     (4x4x1 and 16x16x1 tiles, interior and edge, with and without db inside dW). Buffers that overlap keep the

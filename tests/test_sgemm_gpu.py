@@ -326,15 +326,24 @@ def _batched_cut_case(ta, tb, m, n, k, pad, count, seed):
     return a, lda, b, ldb, c, ldc
 
 
+def _pieces4_config():
+    import nnh
+    return next(i for i, nm in enumerate(nnh.gemm_configs()) if nm.startswith("mfma pieces 16x16x4"))
+
+
+@pytest.mark.parametrize("force4", [0, 1])
 @pytest.mark.parametrize("ta,tb", [(0, 0), (1, 0), (0, 1), (1, 1)])
-def test_depth_cut_in_one_launch(gpu, oracle, ta, tb):
+def test_depth_cut_in_one_launch(gpu, oracle, ta, tb, force4):
     """Cut products of at most 16 pieces run as one launch, one wave per piece, that adds the pieces in LDS (no
-    partial sums in HBM): a batch of 64 products of 64 x 64 x 1200 (10 pieces) with B shared by the batch, 16-byte
-    and element loads, accumulate; 16 pieces (the most one launch takes); and one product of 40 x 50 x 1000
-    (8 pieces) with each bias mode and ReLU with its mask. Every element against the oracle, bit for bit."""
+    partial sums in HBM): a batch of 64 products of 64 x 64 x 1200 (10 pieces, the last one 48 deep) with B shared
+    by the batch, 16-byte and element loads, accumulate; 16 pieces (the most one launch takes); and one product of
+    40 x 50 x 1000 (8 pieces, ragged tiles) with each bias mode and ReLU with its mask. Every element against the
+    oracle, bit for bit; force4 runs them all on the 16x16x4 MFMA pieces kernel (four depth steps of every chain
+    per instruction), otherwise the kernel the shape is routed to."""
     import torch
 
     import nnh
+    cfg = _pieces4_config() if force4 else -1
     m, n, k, count = 64, 64, 1200, 64
     assert nnh.workspace_size("sgemm", m, n, k, count) == 0
     for pad in (0, 1):
@@ -342,7 +351,7 @@ def test_depth_cut_in_one_launch(gpu, oracle, ta, tb):
         batch = nnh.make_batch((count,), (a[0].size,), (0,), (c[0].size,))
         for acc in (0, 1):
             da, db, dc = (torch.from_numpy(x).cuda() for x in (a, b, np.array(c, copy=True)))
-            nnh.sgemm_batched(ta, tb, m, n, k, da, lda, db, ldb, dc, ldc, acc, batch)
+            nnh.sgemm_batched(ta, tb, m, n, k, da, lda, db, ldb, dc, ldc, acc, batch, None, cfg)
             got = dc.cpu().numpy()
             for i in range(count):
                 want = oracle.sgemm(ta, tb, m, n, k, np.ascontiguousarray(a[i]), lda, b, ldb,
@@ -351,7 +360,7 @@ def test_depth_cut_in_one_launch(gpu, oracle, ta, tb):
     p = Problem(ta, tb, 33, 70, 2048, 1, 90500 + 2 * ta + tb)
     assert nnh.workspace_size("sgemm", 33, 70, 2048, 1) == 0
     for acc in (0, 1):
-        got, want = gpu_sgemm(p, acc), oracle_sgemm(oracle, p, acc)
+        got, want = gpu_sgemm(p, acc, cfg), oracle_sgemm(oracle, p, acc)
         assert bits_equal(got, want), ("16 pieces", acc, first_diff(got, want))
     m, n, k = 40, 50, 1000
     assert nnh.workspace_size("sgemm", m, n, k, 1) == 0
@@ -364,7 +373,7 @@ def test_depth_cut_in_one_launch(gpu, oracle, ta, tb):
                 dbias = torch.from_numpy(bias).cuda() if bias is not None else None
                 dalive = torch.full((m, p.ldc), 7, dtype=torch.uint8, device="cuda")
                 ep = nnh.make_epilogue(mode, dbias, relu, dalive if relu else None)
-                got = gpu_sgemm(p, acc, epilogue=ep)
+                got = gpu_sgemm(p, acc, cfg, epilogue=ep)
                 want = oracle_sgemm(oracle, p, acc).copy()
                 v = want[:m, :n]
                 if mode == nnh.BIAS_COL:
