@@ -690,15 +690,14 @@ __global__ void __launch_bounds__(256) ln_forward_lds_kernel(const LnArgs a) {
 // form the products dxhat * ((x - mean) * inv_std) of the second sum elementwise, so the lane that owns a row only
 // runs its two addition chains (sa over g * gamma, sb over the products, both in column order); then all threads
 // write dx = k * (D * dxhat - sa - xhat * sb) elementwise, straight to HBM.
-__global__ void __launch_bounds__(256) ln_dx_lds_kernel(const LnArgs a) {
-	extern __shared__ __align__(16) float lds[];
+__device__ __forceinline__ void ln_dx_body(const LnArgs& a, int block, float* lds) {
 	const int pitch = a.D + 1;
 	float* gs = lds;
 	float* xs = gs + a.rw * pitch;
 	float* gms = xs + a.rw * pitch;
 	float* st = gms + a.D;  // per row: mean, inv_std, sa, sb
 	const int tid = threadIdx.x;
-	const int64_t r0 = (int64_t)blockIdx.x * a.rw;
+	const int64_t r0 = (int64_t)block * a.rw;
 	const int nr = (int)(a.R - r0 < a.rw ? a.R - r0 : a.rw);
 	ln_block_load(a.g + r0 * a.D, nr, a.D, pitch, a.vec, a.dq, gs);
 	ln_block_load(a.x + r0 * a.D, nr, a.D, pitch, a.vec, a.dq, xs);
@@ -751,6 +750,11 @@ __global__ void __launch_bounds__(256) ln_dx_lds_kernel(const LnArgs a) {
 		const float term = k * (fd * dxhat - sa - ((xs[r * pitch + j] - mu) * inv) * sb);
 		dst[e] = a.first ? term + 0.0f : dst[e] + term;
 	}
+}
+
+__global__ void __launch_bounds__(256) ln_dx_lds_kernel(const LnArgs a) {
+	extern __shared__ __align__(16) float lds[];
+	ln_dx_body(a, (int)blockIdx.x, lds);
 }
 
 // layernorm backward's dgamma and dbeta (ops.cpp:1061-1076): each is a chain down a column in row order, so the
@@ -891,34 +895,50 @@ __global__ void __launch_bounds__(kLnThreads) ln_dgamma_kernel(const float* __re
 }
 
 // dgamma and dbeta for at most 1024 rows (transformer_tiny's 16 x 64 tokens): the same chains, one pass. A
-// workgroup of 1024 threads owns kLnSmallCols columns; every thread loads kLnSmallCols rows of its column (g, x,
-// the rows' mean and inv_std, all in flight at once) and parks g * ((x - mean) * inv_std) and g in LDS, column by
-// column; then one lane per column adds the products down it in row order (dgamma) and one the gradients
-// (dbeta), four rows per 16-byte LDS read and 32 rows read ahead of the adds. Four columns a workgroup spread the
-// loads over 16 CUs at D = 64 (a CU's address unit takes one row per lane and load). Rows past R are parked as +0:
-// a chain from +0 never holds -0 (x + (-x) rounds to +0, and no sum of finite floats underflows to zero), so adding
-// +0 leaves it unchanged.
-constexpr int kLnSmallCols = 4, kLnSmallRows = 1024, kLnSmallThreads = 1024;
+// workgroup owns a few columns (four with 1024 threads alone, one with 256 threads beside dx, so that the loads
+// spread over many CUs); every thread loads its share of a column's rows (g, x, the rows' mean and inv_std, all in
+// flight at once) and parks g * ((x - mean) * inv_std) and g in LDS, column by column; then one lane per column adds
+// the products down it in row order (dgamma) and one the gradients (dbeta), four rows per 16-byte LDS read. Rows
+// past R are parked as +0: a chain from +0 never holds -0 (x + (-x) rounds to +0, and no sum of finite floats
+// underflows to zero), so adding +0 leaves it unchanged.
+constexpr int kLnSmallRows = 1024, kLnSmallThreads = 1024;
+constexpr int kLnSmallCols = 4;     // columns of a workgroup of the standalone kernel
+constexpr int kLnMergedCols = 1;    // columns of a 256-thread workgroup beside dx
 constexpr int kLnSmallPitch = kLnSmallRows + 4;  // a column's rows, padded against bank conflicts of the stores
+constexpr size_t kLnMergedLds = 2 * kLnMergedCols * kLnSmallPitch * sizeof(float);
 
-__global__ void __launch_bounds__(kLnSmallThreads) ln_dgamma_small_kernel(
-    const float* __restrict__ g, const float* __restrict__ x, const float* __restrict__ mean,
-    const float* __restrict__ inv, int R, int D, float* dgamma, int dg_first, float* dbeta, int db_first) {
-	__shared__ __align__(16) float buf[2][kLnSmallCols][kLnSmallPitch];
-	constexpr int kRowStep = kLnSmallThreads / kLnSmallCols;
-	const int tid = threadIdx.x;
-	const int c = tid % kLnSmallCols, r0 = tid / kLnSmallCols;  // rows r0 + kRowStep u
-	const int c0 = blockIdx.x * kLnSmallCols;
-	const int col = min(c0 + c, D - 1);
+struct LnSmallArgs {
+	const float* g;
+	const float* x;
+	const float* mean;
+	const float* inv;
+	int R, D;
+	float* dgamma;
+	int dg_first;
+	float* dbeta;
+	int db_first;
+	int blocks;  // workgroups of the column chains
+};
+
+// block: the workgroup's index among the chains' workgroups; THREADS its size, COLS its columns; buf:
+// 2 COLS kLnSmallPitch floats of LDS.
+template <int THREADS, int COLS>
+__device__ __forceinline__ void ln_dgamma_small_body(const LnSmallArgs& d, int block, float* buf) {
+	constexpr int kRowStep = THREADS / COLS;
 	constexpr int kPer = kLnSmallRows / kRowStep;
+	const int R = d.R, D = d.D;
+	const int tid = threadIdx.x;
+	const int c = tid % COLS, r0 = tid / COLS;  // rows r0 + kRowStep u
+	const int c0 = block * COLS;
+	const int col = min(c0 + c, D - 1);
 	float gv[kPer], xv[kPer], mv[kPer], iv[kPer];
 #pragma unroll
 	for (int u = 0; u < kPer; ++u) {
 		const int64_t r = min(r0 + kRowStep * u, R - 1);
-		gv[u] = g[r * D + col];
-		xv[u] = x[r * D + col];
-		mv[u] = mean[r];
-		iv[u] = inv[r];
+		gv[u] = d.g[r * D + col];
+		xv[u] = d.x[r * D + col];
+		mv[u] = d.mean[r];
+		iv[u] = d.inv[r];
 	}
 	// the chains read whole blocks of 32 rows
 	const int rpad = (R + 31) & ~31;
@@ -927,45 +947,58 @@ __global__ void __launch_bounds__(kLnSmallThreads) ln_dgamma_small_kernel(
 		const int r = r0 + kRowStep * u;
 		if (r < rpad) {
 			const bool in = r < R;
-			buf[0][c][r] = in ? gv[u] * ((xv[u] - mv[u]) * iv[u]) : 0.0f;
-			buf[1][c][r] = in ? gv[u] : 0.0f;
+			buf[c * kLnSmallPitch + r] = in ? gv[u] * ((xv[u] - mv[u]) * iv[u]) : 0.0f;
+			buf[(COLS + c) * kLnSmallPitch + r] = in ? gv[u] : 0.0f;
 		}
 	}
 	__syncthreads();
-	if (tid >= 2 * kLnSmallCols) return;
-	const f32x4* v = reinterpret_cast<const f32x4*>(&buf[tid / kLnSmallCols][c][0]);
-	// rows in order: block b's eight reads in flight while block b - 1 is added
+	if (tid >= 2 * COLS) return;
+	// lane c: column c's products (dgamma); lane COLS + c: its gradients (dbeta). Rows in order, 32 at a time; the
+	// reads of the next two blocks are in flight while one is added (a dependent add takes about six cycles).
+	const f32x4* v = reinterpret_cast<const f32x4*>(buf + tid * kLnSmallPitch);
+	const int nb = rpad / 32;
 	float acc = 0.0f;
-	f32x4 t[2][8];
+	f32x4 t[3][8];
 #pragma unroll
 	for (int e = 0; e < 8; ++e) t[0][e] = v[e];
-	for (int i = 0; i < rpad; i += 64) {
-		const bool more = i + 32 < rpad;
-		if (more) {
+	if (nb > 1) {
 #pragma unroll
-			for (int e = 0; e < 8; ++e) t[1][e] = v[(i + 32) / 4 + e];
+		for (int e = 0; e < 8; ++e) t[1][e] = v[8 + e];
+	}
+	for (int b = 0; b < nb; b += 3) {
+#pragma unroll
+		for (int k = 0; k < 3; ++k) {
+			if (b + k >= nb) break;
+			if (b + k + 2 < nb) {
+#pragma unroll
+				for (int e = 0; e < 8; ++e) t[(k + 2) % 3][e] = v[8 * (b + k + 2) + e];
+			}
+#pragma unroll
+			for (int e = 0; e < 8; ++e)
+#pragma unroll
+				for (int q = 0; q < 4; ++q) acc = acc + t[k][e][q];
 		}
-#pragma unroll
-		for (int e = 0; e < 8; ++e)
-#pragma unroll
-			for (int q = 0; q < 4; ++q) acc = acc + t[0][e][q];
-		if (!more) break;
-		if (i + 64 < rpad) {
-#pragma unroll
-			for (int e = 0; e < 8; ++e) t[0][e] = v[(i + 64) / 4 + e];
-		}
-#pragma unroll
-		for (int e = 0; e < 8; ++e)
-#pragma unroll
-			for (int q = 0; q < 4; ++q) acc = acc + t[1][e][q];
 	}
 	if (c0 + c >= D) return;
 	const int j = c0 + c;
-	if (tid < kLnSmallCols) {
-		if (dgamma) dgamma[j] = dg_first ? 0.0f + acc : dgamma[j] + acc;
+	if (tid < COLS) {
+		if (d.dgamma) d.dgamma[j] = d.dg_first ? 0.0f + acc : d.dgamma[j] + acc;
 	} else {
-		if (dbeta) dbeta[j] = db_first ? 0.0f + acc : dbeta[j] + acc;
+		if (d.dbeta) d.dbeta[j] = d.db_first ? 0.0f + acc : d.dbeta[j] + acc;
 	}
+}
+
+__global__ void __launch_bounds__(kLnSmallThreads) ln_dgamma_small_kernel(const LnSmallArgs d) {
+	__shared__ __align__(16) float buf[2 * kLnSmallCols * kLnSmallPitch];
+	ln_dgamma_small_body<kLnSmallThreads, kLnSmallCols>(d, (int)blockIdx.x, buf);
+}
+
+// dx and the column chains of one layernorm backward in one launch (up to 1024 rows): a workgroup per column for
+// the chains, first, so that the longest work starts first, then the dx row blocks beside them on the other CUs.
+__global__ void __launch_bounds__(256) ln_backward_small_kernel(const LnArgs a, const LnSmallArgs d) {
+	extern __shared__ __align__(16) float lds[];
+	if ((int)blockIdx.x < d.blocks) ln_dgamma_small_body<256, kLnMergedCols>(d, (int)blockIdx.x, lds);
+	else ln_dx_body(a, (int)blockIdx.x - d.blocks, lds);
 }
 
 inline bool aligned16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }
@@ -1128,31 +1161,39 @@ hipError_t layernorm_backward(const float* gy, const float* x, const float* gamm
 	                                                        std::max<int64_t>(R, 1)),
 	                                      std::max<int64_t>(1, (R + 255) / 256));
 	if (rw >= 1 && R / rw < ((int64_t)1 << 31) && (int64_t)rw * D < ((int64_t)1 << 31)) {
+		LnArgs a{};
+		a.g = gy;
+		a.x = x;
+		a.gm = gamma;
+		a.mean_in = mean;
+		a.inv_in = inv_std;
+		a.y = dx;
+		a.R = R;
+		a.D = D;
+		a.rw = rw;
+		a.fd = fd;
+		a.first = dx_first;
+		a.vec = D % 4 == 0 && aligned16(x) && aligned16(gy) && aligned16(dx);
+		a.dq = make_fastdiv((unsigned)(a.vec ? D / 4 : D));
+		a.dd = make_fastdiv((unsigned)D);
+		const size_t dx_lds = ((size_t)2 * rw * (D + 1) + D + 4 * rw) * sizeof(float);
+		const int64_t dx_blocks = (R + rw - 1) / rw;
+		const bool small = (dgamma || dbeta) && R > 0 && R <= kLnSmallRows;
+		LnSmallArgs d{gy, x, mean, inv_std, (int)R, D, dgamma, dgamma_first, dbeta, dbeta_first,
+		              (D + kLnMergedCols - 1) / kLnMergedCols};
+		if (dx && R > 0 && small && dx_blocks + d.blocks < ((int64_t)1 << 31)) {
+			hipLaunchKernelGGL(ln_backward_small_kernel, dim3((unsigned)(d.blocks + dx_blocks)), dim3(256),
+			                   std::max(dx_lds, kLnMergedLds), s, a, d);
+			return hipGetLastError();
+		}
+		d.blocks = (D + kLnSmallCols - 1) / kLnSmallCols;
 		if (dx && R > 0) {
-			LnArgs a{};
-			a.g = gy;
-			a.x = x;
-			a.gm = gamma;
-			a.mean_in = mean;
-			a.inv_in = inv_std;
-			a.y = dx;
-			a.R = R;
-			a.D = D;
-			a.rw = rw;
-			a.fd = fd;
-			a.first = dx_first;
-			a.vec = D % 4 == 0 && aligned16(x) && aligned16(gy) && aligned16(dx);
-			a.dq = make_fastdiv((unsigned)(a.vec ? D / 4 : D));
-			a.dd = make_fastdiv((unsigned)D);
-			hipLaunchKernelGGL(ln_dx_lds_kernel, dim3((unsigned)((R + rw - 1) / rw)), dim3(256),
-			                   ((size_t)2 * rw * (D + 1) + D + 4 * rw) * sizeof(float), s, a);
+			hipLaunchKernelGGL(ln_dx_lds_kernel, dim3((unsigned)dx_blocks), dim3(256), dx_lds, s, a);
 			const hipError_t e = hipGetLastError();
 			if (e != hipSuccess) return e;
 		}
-		if ((dgamma || dbeta) && R > 0 && R <= kLnSmallRows)
-			hipLaunchKernelGGL(ln_dgamma_small_kernel, dim3((unsigned)((D + kLnSmallCols - 1) / kLnSmallCols)),
-			                   dim3(kLnSmallThreads), 0, s, gy, x, mean, inv_std, (int)R, D, dgamma, dgamma_first, dbeta,
-			                   dbeta_first);
+		if (small)
+			hipLaunchKernelGGL(ln_dgamma_small_kernel, dim3((unsigned)d.blocks), dim3(kLnSmallThreads), 0, s, d);
 		else if ((dgamma || dbeta) && D % 4 == 0 && aligned16(gy) && aligned16(x))
 			hipLaunchKernelGGL(ln_dgamma_kernel<true>, dim3((unsigned)((D + kLnCols - 1) / kLnCols)), dim3(kLnThreads), 0, s,
 			                   gy, x, mean, inv_std, R, D, dgamma, dgamma_first, dbeta, dbeta_first);
