@@ -207,6 +207,11 @@ int nnh_relu_backward(const float* x, const float* g, float* dx, int first, size
  * existing one adds src, element by element. The first-write rule every backward pass uses; reshape's backward. */
 int nnh_add_to_grad(float* dst, const float* src, size_t count, int first, void* stream);
 
+/* nnh_add_to_grad into two gradients of one source in one launch: dst0 by first0's rule, then dst1 by first1's, the
+ * backward of an add node whose operands have the output's shape (ops.cpp:333-336; accumulate_grad for a, then b).
+ * The two gradients must not overlap each other or src (one node as both operands: two nnh_add_to_grad calls). */
+int nnh_add_to_grad2(float* dst0, int first0, float* dst1, int first1, const float* src, size_t count, void* stream);
+
 /* Value::zero_grad over a list of values (Optimizer::zero_grad, src/optim/sgd.cpp:19-21; value.cpp:69-76): n device
  * buffers of counts[i] floats filled with +0, every fill in one launch (32 buffers per launch). The buffers must not
  * overlap one another. */

@@ -97,6 +97,7 @@ _EXTRA_DECLS = {
     "nnh_matmul_backward": [_vp, _vp, _szp, C.c_int, _vp, _szp, C.c_int, C.c_int, _vp, C.c_int, _vp, C.c_int, _vp],
     "nnh_matmul_backward_workspace_size": [_szp, C.c_int, _szp, C.c_int, C.c_int, C.c_int, C.c_int, _szp],
     "nnh_add_to_grad": [_vp, _vp, _sz, C.c_int, _vp],
+    "nnh_add_to_grad2": [_vp, C.c_int, _vp, C.c_int, _vp, _sz, _vp],
     "nnh_im2col": [_vp, _sz, _sz, _sz, _sz, _sz, _sz, C.c_int, C.c_int, _vp, _vp],
     "nnh_col2im_add": [_vp, _sz, _sz, _sz, _sz, _sz, _sz, C.c_int, C.c_int, _vp, C.c_int, _vp],
     "nnh_batchnorm_forward": [_vp, _sz, _sz, _sz, _vp, _vp, C.c_float, C.c_int, _vp, _vp, _vp, _vp, _vp, _vp],

@@ -588,12 +588,20 @@ Value add(const Value& a, const Value& b) {
 	check(nnh_add_forward(a.data().data(), b.data().data(), outer, inner, y.data(), g_stream));
 	return Value::node(std::move(y), {a, b}, [a, b](const Tensor& g) {
 		// ops.cpp:333-336 then accumulate_grad (ops.cpp:110-117): a, then b, each stored fresh or added to
-		bool first = false;
-		if (float* da = grad_if(a, first)) check(nnh_add_to_grad(da, g.data(), g.size(), first, g_stream));
-		float* db = grad_if(b, first);
-		if (!db) return;
 		const auto& gs = g.shape();
 		const size_t lead = gs.size() - b.data().ndim();
+		bool first = false, first_b = false;
+		float* da = grad_if(a, first);
+		if (lead == 0 && da && a.impl() != b.impl()) {
+			// both operands of the output's shape: both gradients in one launch
+			if (float* db = grad_if(b, first_b)) {
+				check(nnh_add_to_grad2(da, first, db, first_b, g.data(), g.size(), g_stream));
+				return;
+			}
+		}
+		if (da) check(nnh_add_to_grad(da, g.data(), g.size(), first, g_stream));
+		float* db = grad_if(b, first);
+		if (!db) return;
 		if (lead == 0) {
 			check(nnh_add_to_grad(db, g.data(), g.size(), first, g_stream));
 			return;

@@ -103,15 +103,16 @@ __global__ void __launch_bounds__(256) embedding_forward_kernel(const float* __r
 
 // ops.cpp:2008-2014: the gradient table (first: zeros) gets, for i in order, the output gradient's row i added to
 // row rows[i]. Gather form, no atomics: a wave owns one table row and 64 of its columns (a lane per column). The
-// workgroup stages 1024 ids at a time in LDS; a wave tests 256 of them per window (four ballots), then walks the
-// matches in token order eight at a time: eight independent loads of the gradient rows, then eight ordered adds, so
-// a window costs one load latency instead of one per token.
-constexpr int kEmbIds = 1024, kEmbBatch = 8;
+// workgroup stages 1024 ids at a time in LDS; a wave finds its row's tokens among them (16 ballots) and lists them in
+// token order in its own LDS list, then walks the list sixteen tokens at a time: sixteen independent loads of the
+// gradient rows, then sixteen ordered adds, so the usual handful of tokens a row costs one load latency.
+constexpr int kEmbIds = 1024, kEmbBatch = 16;
 
 __global__ void __launch_bounds__(256) embedding_backward_kernel(const float* __restrict__ g, const int* __restrict__ rows,
                                                                  int64_t count, int64_t V, int64_t D,
                                                                  float* __restrict__ dw, int first) {
 	__shared__ int ids[kEmbIds];
+	__shared__ int list[4][kEmbIds];
 	const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
 	const int64_t dchunks = (D + 63) / 64;
 	const int64_t item = (int64_t)blockIdx.x * 4 + wave;  // (row, 64-column chunk)
@@ -120,40 +121,34 @@ __global__ void __launch_bounds__(256) embedding_backward_kernel(const float* __
 	const int64_t d = (here ? item - v * dchunks : 0) * 64 + lane;
 	const bool on = here && d < D;
 	float acc = (first || !on) ? 0.0f : dw[v * D + d];
+	int* const mine = list[wave];
 	for (int64_t i0 = 0; i0 < count; i0 += kEmbIds) {
 		const int n = (int)min<int64_t>(kEmbIds, count - i0);
 		__syncthreads();
 		for (int t = threadIdx.x; t < n; t += 256) ids[t] = rows[i0 + t];
 		__syncthreads();
 		if (!here) continue;
-		for (int w0 = 0; w0 < n; w0 += 256) {
-			uint64_t mk[4];
+		// this row's tokens of the chunk, in order
+		int nm = 0;
+		for (int w0 = 0; w0 < n; w0 += 64) {
+			const int t = w0 + lane;
+			const bool hit = t < n && ids[t] == (int)v;
+			const uint64_t mk = __ballot(hit);
+			if (hit) mine[nm + __builtin_amdgcn_mbcnt_hi((unsigned)(mk >> 32), __builtin_amdgcn_mbcnt_lo((unsigned)mk, 0))] = t;
+			nm += __builtin_popcountll(mk);
+		}
+		__builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+		__builtin_amdgcn_wave_barrier();
+		__builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+		for (int b0 = 0; b0 < nm; b0 += kEmbBatch) {
+			float x[kEmbBatch];
 #pragma unroll
-			for (int q = 0; q < 4; ++q) {
-				const int t = w0 + q * 64 + lane;
-				mk[q] = __ballot(t < n && ids[t] == (int)v);
+			for (int j = 0; j < kEmbBatch; ++j) {  // a clamped address for empty slots and idle lanes: no branch
+				const int tk = mine[min(b0 + j, nm - 1)];
+				x[j] = g[on ? (i0 + tk) * D + d : 0];
 			}
-			int qi = 0;
-			while (true) {
-				int tk[kEmbBatch];
 #pragma unroll
-				for (int j = 0; j < kEmbBatch; ++j) {
-					while (qi < 4 && !mk[qi]) ++qi;
-					if (qi < 4) {
-						tk[j] = w0 + qi * 64 + __builtin_ctzll(mk[qi]);
-						mk[qi] &= mk[qi] - 1;
-					} else {
-						tk[j] = -1;
-					}
-				}
-				if (tk[0] < 0) break;
-				float x[kEmbBatch];
-#pragma unroll
-				for (int j = 0; j < kEmbBatch; ++j)  // a clamped address for empty slots and idle lanes: no branch
-					x[j] = g[(tk[j] >= 0 && on) ? (i0 + tk[j]) * D + d : 0];
-#pragma unroll
-				for (int j = 0; j < kEmbBatch; ++j) acc = tk[j] >= 0 ? acc + x[j] : acc;
-			}
+			for (int j = 0; j < kEmbBatch; ++j) acc = b0 + j < nm ? acc + x[j] : acc;
 		}
 	}
 	if (on) dw[v * D + d] = acc;

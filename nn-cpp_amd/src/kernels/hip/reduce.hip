@@ -195,6 +195,16 @@ __global__ void __launch_bounds__(256) add_to_grad_kernel(float* __restrict__ ds
 	dst[i] = first ? src[i] + 0.0f : dst[i] + src[i];
 }
 
+// The same rule into two gradients of one source (an add node's two operands, in one launch): dst0, then dst1.
+__global__ void __launch_bounds__(256) add_to_grad2_kernel(float* __restrict__ dst0, int first0, float* __restrict__ dst1,
+                                                           int first1, const float* __restrict__ src, int64_t count) {
+	const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+	if (i >= count) return;
+	const float v = src[i];
+	dst0[i] = first0 ? v + 0.0f : dst0[i] + v;
+	dst1[i] = first1 ? v + 0.0f : dst1[i] + v;
+}
+
 }  // namespace
 
 hipError_t sum_axis(const float* src, int64_t pre, int64_t d, int64_t post, float* dst, int combine, hipStream_t s) {
@@ -209,6 +219,13 @@ hipError_t add_to_grad(float* dst, const float* src, int64_t count, int first, h
 	if (count == 0) return hipSuccess;
 	hipLaunchKernelGGL(add_to_grad_kernel, dim3((unsigned)((count + 255) / 256)), dim3(256), 0, s, dst, src, count,
 	                   first);
+	return hipGetLastError();
+}
+
+hipError_t add_to_grad2(float* dst0, int first0, float* dst1, int first1, const float* src, int64_t count, hipStream_t s) {
+	if (count == 0) return hipSuccess;
+	hipLaunchKernelGGL(add_to_grad2_kernel, dim3((unsigned)((count + 255) / 256)), dim3(256), 0, s, dst0, first0, dst1,
+	                   first1, src, count);
 	return hipGetLastError();
 }
 

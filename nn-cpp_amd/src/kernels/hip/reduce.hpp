@@ -28,6 +28,8 @@ struct ZeroJobs {
 hipError_t zero_many(const ZeroJobs& jobs, hipStream_t s);
 // dst = src + 0.0f (first) or dst += src, element by element (add_to_grad, ops.cpp:55-82).
 hipError_t add_to_grad(float* dst, const float* src, int64_t count, int first, hipStream_t s);
+// The same into two gradients that do not overlap each other or src: dst0's rule, then dst1's, in one launch.
+hipError_t add_to_grad2(float* dst0, int first0, float* dst1, int first1, const float* src, int64_t count, hipStream_t s);
 hipError_t relu_forward(const float* x, float* y, int64_t count, hipStream_t s);
 hipError_t relu_backward(const float* x, const float* g, float* dst, int64_t count, int first, hipStream_t s);
 

@@ -423,8 +423,10 @@ bool vec_ok(int tk, const void* a, const void* b) {
 hipError_t softmax_rows(const float* in, float* out, int64_t rows, int tk, int tq, int heads, float scale,
                         const float* pad, int causal, hipStream_t s) {
 	if (rows == 0 || tk == 0) return hipSuccess;
-	const int rb = min(32, rows_per_block(tk, 1));  // 32 rows (33 KB at tk = 256): four blocks share a CU
+	int rb = min(32, rows_per_block(tk, 1));  // 32 rows (33 KB at tk = 256): four blocks share a CU
 	if (rb == 0) return hipErrorInvalidValue;
+	// fewer rows a block while that leaves CUs idle (2048 rows of 64 keys: 8.9 -> us with 4 rows a block)
+	while (rb > 4 && (rows + rb - 1) / rb < 512) rb /= 2;
 	if (rows >= ((int64_t)1 << 31) || (int64_t)rb * tk >= ((int64_t)1 << 31)) return hipErrorInvalidValue;
 	const RowGeom g = row_geom(rows, tk, tq, heads, scale, pad, causal);
 	const bool vec = vec_ok(tk, in, out);
@@ -446,8 +448,9 @@ hipError_t softmax_rows(const float* in, float* out, int64_t rows, int tk, int t
 hipError_t softmax_backward_rows(const float* y, const float* g_in, float* out, int64_t rows, int tk, int tq,
                                  int heads, float scale, const float* pad, int causal, int mode, hipStream_t s) {
 	if (rows == 0 || tk == 0) return hipSuccess;
-	const int rb = min(16, rows_per_block(tk, 2));  // 16 rows (33 KB at tk = 256): four blocks share a CU
+	int rb = min(16, rows_per_block(tk, 2));  // 16 rows (33 KB at tk = 256): four blocks share a CU
 	if (rb == 0) return hipErrorInvalidValue;
+	while (rb > 4 && (rows + rb - 1) / rb < 512) rb /= 2;  // fewer rows a block while that leaves CUs idle
 	if (rows >= ((int64_t)1 << 31) || (int64_t)rb * tk >= ((int64_t)1 << 31)) return hipErrorInvalidValue;
 	const RowGeom g = row_geom(rows, tk, tq, heads, scale, pad, causal);
 	const bool vec = vec_ok(tk, y, g_in) && reinterpret_cast<uintptr_t>(out) % 16 == 0;

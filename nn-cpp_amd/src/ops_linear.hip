@@ -206,6 +206,18 @@ int nnh_add_to_grad(float* dst, const float* src, size_t count, int first, void*
 	                  "add_to_grad");
 }
 
+int nnh_add_to_grad2(float* dst0, int first0, float* dst1, int first1, const float* src, size_t count, void* stream) {
+	if (count == 0) return NNH_OK;
+	if (!dst0 || !dst1 || !src) return fail(NNH_ERR_INVALID, "null pointer");
+	if (count > kMaxElems) return fail(NNH_ERR_INVALID, "count out of range (above 2^60)");
+	const uint64_t b = count * 4;
+	if (ranges_overlap(dst0, b, dst1, b) || ranges_overlap(dst0, b, src, b) || ranges_overlap(dst1, b, src, b))
+		return fail(NNH_ERR_ALIAS, "add_to_grad2: the gradients overlap each other or src");
+	return hip_status(add_to_grad2(dst0, first0 ? 1 : 0, dst1, first1 ? 1 : 0, src, (int64_t)count,
+	                               reinterpret_cast<hipStream_t>(stream)),
+	                  "add_to_grad2");
+}
+
 int nnh_zero_many(float* const* buffers, const size_t* counts, size_t n, void* stream) {
 	if (n == 0) return NNH_OK;
 	if (!buffers || !counts) return fail(NNH_ERR_INVALID, "zero_many: null pointer");

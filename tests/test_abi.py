@@ -56,6 +56,18 @@ def test_output_aliasing_an_input_is_rejected():
     assert _sgemm(0, 0, 4, 4, 4, C.c_void_p(FAKE_A), 4, C.c_void_p(FAKE_B), 4, C.c_void_p(FAKE_B - 16), 4, 0, None) == nnh.ERR_ALIAS
 
 
+def test_add_to_grad2_refuses_overlapping_gradients():
+    """nnh_add_to_grad2 writes two gradients of one source in one launch: gradients that overlap each other or the
+    source are refused on the host (one node passed as both operands takes two nnh_add_to_grad calls)."""
+    L = nnh.lib()
+    f = L.nnh_add_to_grad2
+    a, b, s = C.c_void_p(FAKE_A), C.c_void_p(FAKE_B), C.c_void_p(FAKE_C)
+    assert f(a, 1, C.c_void_p(FAKE_A + 16), 0, s, 64, None) == nnh.ERR_ALIAS
+    assert f(a, 1, b, 1, C.c_void_p(FAKE_B + 4), 8, None) == nnh.ERR_ALIAS
+    assert f(a, 1, None, 1, s, 8, None) == nnh.ERR_INVALID
+    assert f(None, 1, None, 1, None, 0, None) == nnh.OK
+
+
 def test_empty_products_touch_nothing_and_need_no_device():
     """m == 0 or n == 0 returns before any device work (gemm.cpp:344); null pointers are then fine."""
     assert _sgemm(0, 0, 0, 5, 4, None, 4, None, 5, None, 5, 0, None) == nnh.OK

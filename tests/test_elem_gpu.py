@@ -2,6 +2,8 @@
 oracle, bit for bit: GELU over a sweep that crosses the tanh clamp and every special value, fresh and added
 gradients; add with a broadcast row, on aligned and unaligned buffers and in place; embedding rows gathered and the
 gradient table built in token order with repeated ids, fresh and added to, over more tokens than one staging pass."""
+import ctypes as C
+
 import numpy as np
 import pytest
 
@@ -203,3 +205,35 @@ def test_zero_many(gpu):
         off += 7
     with pytest.raises(nnh.NnhError):
         nnh.zero_many([base[0:10], base[5:20]])
+
+
+@pytest.mark.parametrize("n,first0,first1", [(1, 1, 1), (1000, 1, 0), (70001, 0, 1), (4096, 0, 0)])
+def test_add_to_grad2_matches_two_calls(gpu, n, first0, first1):
+    """nnh_add_to_grad2 (an add node's backward into both operands in one launch) gives each gradient the bits of its
+    own nnh_add_to_grad call: a fresh one stores src + 0 (-0 becomes +0), an existing one adds src. Signed zeros,
+    infinities and NaN in src and in the old gradients."""
+    import torch
+
+    import nnh
+    L = nnh.lib()
+    rng = np.random.default_rng(n)
+    src = rng.standard_normal(n).astype(np.float32)
+    old0 = rng.standard_normal(n).astype(np.float32)
+    old1 = rng.standard_normal(n).astype(np.float32)
+    if n > 8:
+        src[:4] = [-0.0, 0.0, np.inf, np.nan]
+        old0[4:6] = [-0.0, -np.inf]
+        old1[1:3] = [-0.0, np.inf]
+    ds = dev(src)
+    got = [dev(old0), dev(old1)]
+    want = [dev(old0), dev(old1)]
+    ptr = lambda t: C.c_void_p(t.data_ptr())
+    assert L.nnh_add_to_grad2(ptr(got[0]), first0, ptr(got[1]), first1, ptr(ds), n, None) == 0
+    assert L.nnh_add_to_grad(ptr(want[0]), ptr(ds), n, first0, None) == 0
+    assert L.nnh_add_to_grad(ptr(want[1]), ptr(ds), n, first1, None) == 0
+    torch.cuda.synchronize()
+    for i in range(2):
+        assert_same(got[i].cpu().numpy(), want[i].cpu().numpy(), ("gradient", i), nan_equal=True)
+    with np.errstate(all="ignore"):
+        ref0 = src + np.float32(0) if first0 else old0 + src
+    assert_same(got[0].cpu().numpy(), ref0, "gradient 0 vs numpy", nan_equal=True)
