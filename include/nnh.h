@@ -213,7 +213,7 @@ int nnh_add_to_grad(float* dst, const float* src, size_t count, int first, void*
 int nnh_add_to_grad2(float* dst0, int first0, float* dst1, int first1, const float* src, size_t count, void* stream);
 
 /* Value::zero_grad over a list of values (Optimizer::zero_grad, src/optim/sgd.cpp:19-21; value.cpp:69-76): n device
- * buffers of counts[i] floats filled with +0, every fill in one launch (32 buffers per launch). The buffers must not
+ * buffers of counts[i] floats filled with +0, every fill in one launch (64 buffers per launch). The buffers must not
  * overlap one another. */
 int nnh_zero_many(float* const* buffers, const size_t* counts, size_t n, void* stream);
 

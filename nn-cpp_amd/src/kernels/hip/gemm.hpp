@@ -82,7 +82,8 @@ bool pieces_kernel_takes(const GemmCall& g);  // also: leading dimensions below 
 hipError_t gemm_pieces_launch(const GemmCall& g, hipStream_t s);
 // The same products on the 16x16x4 MFMA: 16 x 16 tiles, a wave per piece, operands loaded into registers. It is
 // the route of the cut products it takes (pieces4_takes: A transposed and B not, the weight gradient's layout, also
-// with two-stage row sums); a forced configuration runs it on any product pieces_kernel_takes.
+// with two-stage row sums; other layouts when their k-contiguous operands allow 16-byte loads); a forced
+// configuration runs it on any product pieces_kernel_takes.
 bool pieces4_takes(const GemmCall& g);
 hipError_t gemm_pieces4_launch(const GemmCall& g, hipStream_t s);
 

@@ -323,12 +323,32 @@ __device__ __forceinline__ void rowsums_stage2(const GemmArgs& p, int m0, int la
 // over the outer index per inner index parked in LDS, then, after the barrier, one chain over the inner index per
 // row.
 
-template <bool TA, bool TB, bool RS>
+// v[e] of lane group g (lanes 16 g .. 16 g + 15) becomes what v[g] of lane group e held: a 4 x 4 transpose of the
+// lane groups' four registers, by two v_permlane32_swap (lane groups 2, 3 of one register with 0, 1 of another) and
+// two v_permlane16_swap (odd groups of one with even groups of another), each after the two wait states a VALU
+// result needs before a lane swap reads it. Written as assembly: the compiler's builtins for these swaps return the
+// first register's result for both at -O3 (hipcc of ROCm 7.2). The registers are taken from a whole-vector bit
+// cast: a bit cast of one element of a float vector read element 0 for all four in the same compiler.
+__device__ __forceinline__ void transpose4(f32x4& v) {
+	typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+	const u32x4 u = __builtin_bit_cast(u32x4, v);
+	unsigned x0 = u.x, x1 = u.y, x2 = u.z, x3 = u.w;
+	asm volatile(
+	    "s_nop 1\n\t"
+	    "v_permlane32_swap_b32 %0, %2\n\t"
+	    "v_permlane32_swap_b32 %1, %3\n\t"
+	    "s_nop 1\n\t"
+	    "v_permlane16_swap_b32 %0, %1\n\t"
+	    "v_permlane16_swap_b32 %2, %3\n\t"
+	    "s_nop 1"
+	    : "+v"(x0), "+v"(x1), "+v"(x2), "+v"(x3));
+	v = __builtin_bit_cast(f32x4, u32x4{x0, x1, x2, x3});
+}
+
+template <bool TA, bool TB, bool RS, bool VEC>
 __global__ void __launch_bounds__(RS ? (kRsMaxPieces + kRsWaves) * 64 : kMaxPieces * 64) sgemm_pieces4_kernel(const GemmArgs p) {
 	static_assert(!RS || (TA && !TB), "row sums are compiled for the weight-gradient layout only");
 	constexpr int kU = 16;      // tile side
-	constexpr int kSub = 8;     // MFMA steps per 32-deep sub-slab (one buffer resource each)
-	constexpr int kSteps = 32;  // MFMA steps per chunk: 128 depth indices
 	__shared__ float done[kMaxPieces * kU * kU];
 	__shared__ float part[RS ? kRsMaxInner * kU : 1];
 	const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -353,43 +373,73 @@ __global__ void __launch_bounds__(RS ? (kRsMaxPieces + kRsWaves) * 64 : kMaxPiec
 	const bool row_in = m0 + r < p.m, col_in = n0 + r < p.n;
 	const int k_lo = wave * p.piece_k, k_hi = min(p.k, k_lo + p.piece_k);
 	f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-	// one chunk of up to 128 depth indices: every load issued before the first MFMA; PART (the piece's last chunk
-	// shorter than 128) masks the depth and turns B's +0 fill past the end into -0 at the MFMA
-	auto chunk = [&](int kc, auto part_tag) {
+	// one chunk of G groups of 16 depth indices: every load issued before the first MFMA. Group h holds the operands
+	// of steps 4 h .. 4 h + 3. A k-contiguous operand (A not transposed, B transposed) takes, with VEC, one 16-byte
+	// load per group (lane group g: depths 16 h + 4 g .. + 3 of its row), transposed across the lane groups before
+	// the group's MFMAs (transpose4); otherwise one element per lane and step. PART (fewer than 16 indices left in
+	// the piece) loads element by element, masks the depth and turns B's +0 fill past the end into -0 at the MFMA.
+	constexpr bool KA = VEC && !TA, KB = VEC && TB;
+	auto chunk = [&](int kc, auto groups_tag, auto part_tag) {
+		constexpr int G = decltype(groups_tag)::value;
 		constexpr bool PART = decltype(part_tag)::value;
+		constexpr bool VA = KA && !PART, VB = KB && !PART;
 		const int kv = k_hi - kc;
-		float a[kSteps], b[kSteps];
+		f32x4 a[G], b[G];
 #pragma unroll
-		for (int q = 0; q < kSteps / kSub; ++q) {
-			// a sub-slab's offsets stay below 32 rows of a leading dimension (below 2^24)
-			const int k0 = 4 * kSub * q;
-			const __amdgpu_buffer_rsrc_t ares =
-			    rsrc(TA ? A + (int64_t)(kc + k0) * lda + m0 : A + (int64_t)m0 * lda + kc + k0);
-			const __amdgpu_buffer_rsrc_t bres =
-			    rsrc(TB ? B + (int64_t)n0 * ldb + kc + k0 : B + (int64_t)(kc + k0) * ldb + n0);
+		for (int h = 0; h < G; ++h) {
+			// a group's offsets stay below 16 rows of a leading dimension (below 2^24)
+			const int k0 = kc + 16 * h;
+			const __amdgpu_buffer_rsrc_t ares = rsrc(TA ? A + (int64_t)k0 * lda + m0 : A + (int64_t)m0 * lda + k0);
+			const __amdgpu_buffer_rsrc_t bres = rsrc(TB ? B + (int64_t)n0 * ldb + k0 : B + (int64_t)k0 * ldb + n0);
+			if (VA) a[h] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(ares, row_in ? (r * lda + 4 * j) * 4 : kOob, 0, 0));
+			if (VB) b[h] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(bres, col_in ? (r * ldb + 4 * j) * 4 : kOob, 0, 0));
 #pragma unroll
-			for (int u = 0; u < kSub; ++u) {
-				const int d = 4 * u + j;
-				const bool din = !PART || k0 + d < kv;
-				const int aoff = row_in && din ? (TA ? d * lda + r : r * lda + d) * 4 : kOob;
-				const int boff = col_in && din ? (TB ? r * ldb + d : d * ldb + r) * 4 : kOob;
-				a[kSub * q + u] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(ares, aoff, 0, 0));
-				b[kSub * q + u] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(bres, boff, 0, 0));
+			for (int e = 0; e < 4; ++e) {
+				const int d = 4 * e + j;
+				const bool din = !PART || d < kv;
+				if (!VA) {
+					const int aoff = row_in && din ? (TA ? d * lda + r : r * lda + d) * 4 : kOob;
+					a[h][e] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(ares, aoff, 0, 0));
+				}
+				if (!VB) {
+					const int boff = col_in && din ? (TB ? r * ldb + d : d * ldb + r) * 4 : kOob;
+					b[h][e] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(bres, boff, 0, 0));
+				}
 			}
 		}
 		__builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-		for (int s = 0; s < kSteps; ++s) {
-			float bv = b[s];
-			if (PART) bv = __builtin_bit_cast(float, __builtin_bit_cast(unsigned, bv) | (4 * s + j < kv ? 0u : 0x80000000u));
-			acc = Mfma<kMf16x4>::mma(a[s], bv, acc);
+		for (int h = 0; h < G; ++h) {
+			if (VA) transpose4(a[h]);
+			if (VB) transpose4(b[h]);
+#pragma unroll
+			for (int e = 0; e < 4; ++e) {
+				float bv = b[h][e];
+				if (PART) bv = __builtin_bit_cast(float, __builtin_bit_cast(unsigned, bv) | (4 * e + j < kv ? 0u : 0x80000000u));
+				acc = Mfma<kMf16x4>::mma(a[h][e], bv, acc);
+			}
 		}
 		__builtin_amdgcn_sched_barrier(0);
 	};
-	for (int kc = k_lo; kc < k_hi; kc += 4 * kSteps) {
-		if (k_hi - kc >= 4 * kSteps) chunk(kc, std::false_type{});
-		else chunk(kc, std::true_type{});
+	using I1 = std::integral_constant<int, 1>;
+	using I2 = std::integral_constant<int, 2>;
+	using I4 = std::integral_constant<int, 4>;
+	using I8 = std::integral_constant<int, 8>;
+	int kc = k_lo;
+	for (; k_hi - kc >= 128; kc += 128) chunk(kc, I8{}, std::false_type{});
+	if (k_hi - kc >= 64) {
+		chunk(kc, I4{}, std::false_type{});
+		kc += 64;
 	}
+	if (k_hi - kc >= 32) {
+		chunk(kc, I2{}, std::false_type{});
+		kc += 32;
+	}
+	if (k_hi - kc >= 16) {
+		chunk(kc, I1{}, std::false_type{});
+		kc += 16;
+	}
+	if (kc < k_hi) chunk(kc, I1{}, std::true_type{});
 	// register e of lane l holds row 4 (l / 16) + e, column l % 16 of the tile
 	float* const mine = done + wave * kU * kU;
 #pragma unroll
@@ -478,14 +528,35 @@ hipError_t gemm_pieces_launch(const GemmCall& g, hipStream_t s) {
 	return hipGetLastError();
 }
 
+// 16-byte loads of a k-contiguous operand (A not transposed, B transposed): its leading dimension and batch
+// strides multiples of 4 and its base 16-byte aligned (every chunk starts at a depth that is a multiple of 4).
+bool pieces4_vec(const GemmCall& g) {
+	bool vec = true;
+	if (!g.ta) {
+		vec = vec && g.lda % 4 == 0 && reinterpret_cast<uintptr_t>(g.a) % 16 == 0;
+		for (int d = 0; d < g.batch.ndim; ++d) vec = vec && g.batch.sa[d] % 4 == 0;
+	}
+	if (g.tb) {
+		vec = vec && g.ldb % 4 == 0 && reinterpret_cast<uintptr_t>(g.b) % 16 == 0;
+		for (int d = 0; d < g.batch.ndim; ++d) vec = vec && g.batch.sb[d] % 4 == 0;
+	}
+	return vec;
+}
+
 bool pieces4_takes(const GemmCall& g) {
-	// Measured (device time on one MI355X, against the VALU pieces kernel that took these before): A transposed and
-	// B not, the weight gradient's layout, 64 x 64 x 1024 4.37 against 8.36 us, 256 x 64 x 1024 4.44 against 8.82,
-	// 128 x 128 x 768 4.31 against 8.12. A k-contiguous op(A) or op(B) (16 rows per load, one element each) is
-	// slower here than on the other kernels: 64 x 64 x 1024 NN 10.4 against 7.1, NT 16.9 against 6.6.
-	if (!g.ta || g.tb || g.gather || !pieces_kernel_takes(g.m, g.n, g.k, g.batch_count, false) || g.lda >= kMaxLd ||
-	    g.ldb >= kMaxLd)
+	// Measured (device time on one MI355X, nn-cpp's cut, against the VALU pieces kernel that took these before):
+	// A transposed and B not (the weight gradient's layout) 64 x 64 x 1024 4.3 against 8.4 us, 256 x 64 x 1024 4.4
+	// against 8.8, 128 x 128 x 768 4.3 against 8.1; with 16-byte loads of k-contiguous operands 256 x 256 x 512 NT
+	// (config 2's second layer) 5.1 against 7.3, NN 4.5 against 7.4, 64 x 64 x 1024 NN 5.5 against 7.1, NT 6.7
+	// against 6.6, 64 x 64 x 1200 TT 6.2 against 10.6, 33 x 70 x 2048 NN 10.0 against 25.9. A k-contiguous operand
+	// without them (one element per lane and load) is slower than the other kernels (64 x 64 x 1024 NN 10.4, NT 16.9).
+	// At most 512 tiles of 16 x 16 (every product nn-cpp cuts has at most 256): beyond, a wave per piece and tile
+	// re-reads the operands too often (NUMERICS_SPLIT_DEPTH's 512 x 512 x 512 in 32-deep pieces 10.4 us, 64 x 4096 x
+	// 4096 in 256-deep pieces 59 us, against 7.0 and 33 us on the kernels below).
+	if (g.gather || !pieces_kernel_takes(g.m, g.n, g.k, g.batch_count, false) || g.lda >= kMaxLd || g.ldb >= kMaxLd)
 		return false;
+	if (((g.m + 15) / 16) * ((g.n + 15) / 16) * g.batch_count > 512) return false;
+	if ((!g.ta || g.tb) && !pieces4_vec(g)) return false;
 	if (!g.rowsum) return true;
 	// two-stage row sums: one matrix, the row-sum waves beside at most kRsMaxPieces piece waves, 16-byte loads of A
 	const CutPlan plan = cut_plan(g.m, g.n, g.k);
@@ -496,9 +567,13 @@ bool pieces4_takes(const GemmCall& g) {
 }
 
 hipError_t gemm_pieces4_launch(const GemmCall& g, hipStream_t s) {
-	static const PiecesFn fns[5] = {sgemm_pieces4_kernel<false, false, false>, sgemm_pieces4_kernel<false, true, false>,
-	                                sgemm_pieces4_kernel<true, false, false>, sgemm_pieces4_kernel<true, true, false>,
-	                                sgemm_pieces4_kernel<true, false, true>};
+	static const PiecesFn fns[2][5] = {
+	    {sgemm_pieces4_kernel<false, false, false, false>, sgemm_pieces4_kernel<false, true, false, false>,
+	     sgemm_pieces4_kernel<true, false, false, false>, sgemm_pieces4_kernel<true, true, false, false>,
+	     sgemm_pieces4_kernel<true, false, true, false>},
+	    {sgemm_pieces4_kernel<false, false, false, true>, sgemm_pieces4_kernel<false, true, false, true>,
+	     sgemm_pieces4_kernel<true, false, false, true>, sgemm_pieces4_kernel<true, true, false, true>,
+	     sgemm_pieces4_kernel<true, false, true, false>}};
 	if (g.rowsum ? !pieces4_takes(g) : !pieces_kernel_takes(g)) return hipErrorInvalidValue;
 	const CutPlan plan = cut_plan(g.m, g.n, g.k);
 	GemmArgs p{};
@@ -524,8 +599,10 @@ hipError_t gemm_pieces4_launch(const GemmCall& g, hipStream_t s) {
 	p.rowsum_outer = (int)g.rowsum_outer;
 	const int64_t blocks = (int64_t)p.tiles_m * p.tiles_n * p.batch_count;
 	if (blocks > 0x7fffffff) return hipErrorInvalidConfiguration;
+	const bool vec = pieces4_vec(g);
 	const int f = g.rowsum ? 4 : (g.ta ? 2 : 0) + (g.tb ? 1 : 0);
-	hipLaunchKernelGGL(fns[f], dim3((unsigned)blocks), dim3((p.pieces + (g.rowsum ? kRsWaves : 0)) * 64), 0, s, p);
+	hipLaunchKernelGGL(fns[vec ? 1 : 0][f], dim3((unsigned)blocks), dim3((p.pieces + (g.rowsum ? kRsWaves : 0)) * 64), 0,
+	                   s, p);
 	return hipGetLastError();
 }
 

@@ -292,9 +292,14 @@ hipError_t sum_rows2(const float* src, int64_t r0, int64_t r1, int64_t inner, fl
 __global__ void __launch_bounds__(256) zero_many_kernel(const ZeroJobs jobs) {
 	const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
 	if (e >= jobs.start[jobs.n]) return;
-	int i = 0;
-	while (e >= jobs.start[i + 1]) ++i;
-	jobs.p[i][e - jobs.start[i]] = 0.0f;
+	// the job whose range holds e: the last i with start[i] <= e (a binary search over the starts)
+	int lo = 0, hi = jobs.n - 1;
+	while (lo < hi) {
+		const int mid = (lo + hi + 1) >> 1;
+		if (jobs.start[mid] <= e) lo = mid;
+		else hi = mid - 1;
+	}
+	jobs.p[lo][e - jobs.start[lo]] = 0.0f;
 }
 
 hipError_t zero_many(const ZeroJobs& jobs, hipStream_t s) {

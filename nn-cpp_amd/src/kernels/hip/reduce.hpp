@@ -19,7 +19,7 @@ hipError_t sum_rows2(const float* src, int64_t r0, int64_t r1, int64_t inner, fl
 // Tensor::sum(axis) over {pre, d, post} into {pre, post} (combine as sum_rows).
 hipError_t sum_axis(const float* src, int64_t pre, int64_t d, int64_t post, float* dst, int combine, hipStream_t s);
 // Up to kZeroJobs buffers filled with +0 in one launch (start[0] = 0, start[i + 1] - start[i] = buffer i's length).
-constexpr int kZeroJobs = 32;
+constexpr int kZeroJobs = 64;
 struct ZeroJobs {
 	float* p[kZeroJobs];
 	int64_t start[kZeroJobs + 1];

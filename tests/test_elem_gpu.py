@@ -175,14 +175,14 @@ def test_embedding_backward_keeps_negative_zero(gpu, oracle):
 
 
 def test_zero_many(gpu):
-    """nnh_zero_many (an optimizer's zero_grad over its parameters in one launch per 32 buffers): 40 buffers of
-    sizes 0 to 70,001 carved from one allocation with gaps, every buffer +0 afterwards (no -0) and every gap
-    untouched; overlapping buffers are refused."""
+    """nnh_zero_many (an optimizer's zero_grad over its parameters in one launch per 64 buffers): 70 buffers of
+    sizes 0 to 70,001 carved from one allocation with gaps (two launches; empty buffers first, last and between),
+    every buffer +0 afterwards (no -0) and every gap untouched; overlapping buffers are refused."""
     import torch
 
     import nnh
     rng = np.random.default_rng(5)
-    sizes = [0, 1, 3, 64, 70001] + list(rng.integers(1, 5000, 35))
+    sizes = [0, 1, 3, 64, 70001] + list(rng.integers(1, 5000, 35)) + [0, 0] + list(rng.integers(1, 900, 27)) + [0]
     total = sum(sizes) + 7 * len(sizes)
     base = torch.full((total,), -0.0, device="cuda")
     views, gaps, off = [], [], 0

@@ -389,20 +389,29 @@ def test_depth_cut_in_one_launch(gpu, oracle, ta, tb, force4):
                 assert bits_equal(got, want), (mode, relu, acc, first_diff(got, want))
 
 
+def _valu_pieces_config():
+    import nnh
+    return next(i for i, nm in enumerate(nnh.gemm_configs()) if nm.startswith("valu pieces"))
+
+
+@pytest.mark.parametrize("force_valu", [0, 1])
 @pytest.mark.parametrize("tb", [0, 1])
-def test_four_piece_cuts_on_the_vector_alus(gpu, oracle, tb):
-    """nn-cpp's cut at a depth of 512 (four 128-deep pieces, e.g. config 2's 256 x 256 x 512 layer) runs every piece
-    of an output as a chain in one lane: ragged and tile-aligned m x n, 16-byte and element staging of B (pad),
-    accumulate, a batch sharing B, and each bias mode with ReLU and its mask. Every element against the oracle."""
+def test_four_piece_cuts(gpu, oracle, tb, force_valu):
+    """nn-cpp's cut at a depth of 512 (four 128-deep pieces, e.g. config 2's 256 x 256 x 512 layer): on the kernel
+    the shape is routed to (the 16x16x4 MFMA pieces kernel with 16-byte loads of its k-contiguous operands when
+    aligned, else the VALU pieces kernel), and forced onto the VALU pieces kernel (every piece of an output as a chain
+    in one lane). Ragged and tile-aligned m x n, aligned and padded rows (pad), accumulate, a batch sharing B, and each
+    bias mode with ReLU and its mask. Every element against the oracle."""
     import torch
 
     import nnh
+    cfg = _valu_pieces_config() if force_valu else -1
     seed = 93000 + 100 * tb
     for m, n, pad in ((256, 256, 0), (37, 90, 1), (128, 16, 0), (50, 41, 1), (16, 4096, 0)):
         for acc in (0, 1):
             p = Problem(0, tb, m, n, 512, pad, seed)
             seed += 1
-            got, want = gpu_sgemm(p, acc), oracle_sgemm(oracle, p, acc)
+            got, want = gpu_sgemm(p, acc, cfg), oracle_sgemm(oracle, p, acc)
             assert bits_equal(got, want), ((m, n, pad), acc, first_diff(got, want))
     m, n, k, count = 64, 32, 512, 8
     for pad in (0, 1):
@@ -410,7 +419,7 @@ def test_four_piece_cuts_on_the_vector_alus(gpu, oracle, tb):
         batch = nnh.make_batch((count,), (a[0].size,), (0,), (c[0].size,))
         for acc in (0, 1):
             da, db, dc = (torch.from_numpy(x).cuda() for x in (a, b, np.array(c, copy=True)))
-            nnh.sgemm_batched(0, tb, m, n, k, da, lda, db, ldb, dc, ldc, acc, batch)
+            nnh.sgemm_batched(0, tb, m, n, k, da, lda, db, ldb, dc, ldc, acc, batch, None, cfg)
             got = dc.cpu().numpy()
             for i in range(count):
                 want = oracle.sgemm(0, tb, m, n, k, np.ascontiguousarray(a[i]), lda, b, ldb,
@@ -426,7 +435,7 @@ def test_four_piece_cuts_on_the_vector_alus(gpu, oracle, tb):
                 dbias = torch.from_numpy(bias).cuda() if bias is not None else None
                 dalive = torch.full((m, p.ldc), 7, dtype=torch.uint8, device="cuda")
                 ep = nnh.make_epilogue(mode, dbias, relu, dalive if relu else None)
-                got = gpu_sgemm(p, acc, epilogue=ep)
+                got = gpu_sgemm(p, acc, cfg, epilogue=ep)
                 want = oracle_sgemm(oracle, p, acc).copy()
                 v = want[:m, :n]
                 if mode == nnh.BIAS_COL:
