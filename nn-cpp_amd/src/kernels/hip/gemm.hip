@@ -239,9 +239,10 @@ int64_t gemm_workspace_floats(const GemmCall& g) {
 }
 
 // Configurations kNumConfigs .. kNumConfigs + kValuShapes - 1 are the VALU kernel's lane blocks (gemm_valu.hip).
-// Configuration kNumConfigs + kValuShapes forces the VALU pieces kernel on a cut product it can take, and
-// kNumConfigs + kValuShapes + 1 the 16x16x4 MFMA pieces kernel.
-int gemm_config_count() { return kNumConfigs + kValuShapes + 2; }
+// Configuration kNumConfigs + kValuShapes forces the VALU pieces kernel on a cut product it can take,
+// kNumConfigs + kValuShapes + 1 the 16x16x4 MFMA pieces kernel, and kNumConfigs + kValuShapes + 2 the whole-depth
+// 16x16x4 chain kernel on a product that is not cut.
+int gemm_config_count() { return kNumConfigs + kValuShapes + 3; }
 const char* gemm_config_name(int config) {
 	if (config == kNumConfigs + kValu2x2) return "valu 32x32 (2x2 chains per lane)";
 	if (config == kNumConfigs + kValu1x2) return "valu 16x32 (1x2 chains per lane)";
@@ -251,6 +252,7 @@ const char* gemm_config_name(int config) {
 	if (config == kNumConfigs + kValuBc2) return "valu bcast 32x16 (2 chains per lane, A by DPP)";
 	if (config == kNumConfigs + kValuShapes) return "valu pieces 16x16 (every piece of a cut output in one lane)";
 	if (config == kNumConfigs + kValuShapes + 1) return "mfma pieces 16x16x4 (a wave per piece, 16x16 tiles)";
+	if (config == kNumConfigs + kValuShapes + 2) return "mfma chain 16x16x4 (32x32 tiles, no LDS)";
 
 	return (config >= 0 && config < kNumConfigs) ? configs()[config].name : "";
 }
@@ -266,6 +268,8 @@ hipError_t gemm_launch(const GemmCall& g, hipStream_t s, int config, float* work
 	                     g.n < (1 << 30) && g.k < (1 << 30);
 	if (valu_ok && config >= kNumConfigs && config < kNumConfigs + kValuShapes)
 		return gemm_valu_launch(g, config - kNumConfigs, s);
+	if (config == kNumConfigs + kValuShapes + 2 && chain4_ok(g)) return gemm_chain4_launch(g, s);
+	if (config < 0 && chain4_takes(g)) return gemm_chain4_launch(g, s);
 	if ((config < 0 || config >= kNumConfigs) && valu_ok && valu_takes(g)) return gemm_valu_launch(g, valu_shape(g), s);
 	if (config < 0 || config >= kNumConfigs) config = pick_config(g);
 	const Config& cf = configs()[config];

@@ -85,6 +85,10 @@ hipError_t gemm_pieces_launch(const GemmCall& g, hipStream_t s);
 // with two-stage row sums; other layouts when their k-contiguous operands allow 16-byte loads); a forced
 // configuration runs it on any product pieces_kernel_takes.
 bool pieces4_takes(const GemmCall& g);
+// Whole-depth products (no cut, no gather, no row sums) on the 16x16x4 MFMA without LDS (gemm_chain.hip).
+bool chain4_ok(const GemmCall& g);
+bool chain4_takes(const GemmCall& g);  // the shapes it is routed for (measured)
+hipError_t gemm_chain4_launch(const GemmCall& g, hipStream_t s);
 hipError_t gemm_pieces4_launch(const GemmCall& g, hipStream_t s);
 
 // Floats of workspace a call needs: the partial sums of a depth cut the pieces kernel does not take, else 0. The

@@ -17,6 +17,7 @@
 #include <type_traits>
 
 #include "gemm.hpp"
+#include "gemm_direct.hpp"
 #include "gemm_tile.hpp"
 
 namespace nnh {
@@ -37,14 +38,6 @@ static_assert(kT * kT <= kPerWave, "a finished piece fits in the staging");
 // one float per lane (consecutive lanes, consecutive banks).
 __device__ __forceinline__ int kslot(int r, int c) { return 8 * r + (c ^ ((r >> 1) & 7)); }
 
-// Operand loads through buffer resources: an element outside the matrix gets an offset past the resource's end,
-// which the hardware answers with 0 and no memory access. No branches around the loads, so the compiler keeps
-// several slabs of them in flight and waits for each by count.
-constexpr int kOob = 0x7fffffff;
-
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const float* base) {
-	return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), (short)0, kOob, 0x00020000);
-}
 
 // Four elements of a row-major matrix whose element (0, 0) is the resource's base: row r, columns c .. c + 3,
 // 0 outside rows_valid x cols_valid (-0 with NEG: the B operand's fill, so that a step past a piece's end
@@ -323,28 +316,6 @@ __device__ __forceinline__ void rowsums_stage2(const GemmArgs& p, int m0, int la
 // over the outer index per inner index parked in LDS, then, after the barrier, one chain over the inner index per
 // row.
 
-// v[e] of lane group g (lanes 16 g .. 16 g + 15) becomes what v[g] of lane group e held: a 4 x 4 transpose of the
-// lane groups' four registers, by two v_permlane32_swap (lane groups 2, 3 of one register with 0, 1 of another) and
-// two v_permlane16_swap (odd groups of one with even groups of another), each after the two wait states a VALU
-// result needs before a lane swap reads it. Written as assembly: the compiler's builtins for these swaps return the
-// first register's result for both at -O3 (hipcc of ROCm 7.2). The registers are taken from a whole-vector bit
-// cast: a bit cast of one element of a float vector read element 0 for all four in the same compiler.
-__device__ __forceinline__ void transpose4(f32x4& v) {
-	typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
-	const u32x4 u = __builtin_bit_cast(u32x4, v);
-	unsigned x0 = u.x, x1 = u.y, x2 = u.z, x3 = u.w;
-	asm volatile(
-	    "s_nop 1\n\t"
-	    "v_permlane32_swap_b32 %0, %2\n\t"
-	    "v_permlane32_swap_b32 %1, %3\n\t"
-	    "s_nop 1\n\t"
-	    "v_permlane16_swap_b32 %0, %1\n\t"
-	    "v_permlane16_swap_b32 %2, %3\n\t"
-	    "s_nop 1"
-	    : "+v"(x0), "+v"(x1), "+v"(x2), "+v"(x3));
-	v = __builtin_bit_cast(f32x4, u32x4{x0, x1, x2, x3});
-}
-
 template <bool TA, bool TB, bool RS, bool VEC>
 __global__ void __launch_bounds__(RS ? (kRsMaxPieces + kRsWaves) * 64 : kMaxPieces * 64) sgemm_pieces4_kernel(const GemmArgs p) {
 	static_assert(!RS || (TA && !TB), "row sums are compiled for the weight-gradient layout only");
@@ -382,43 +353,11 @@ __global__ void __launch_bounds__(RS ? (kRsMaxPieces + kRsWaves) * 64 : kMaxPiec
 	auto chunk = [&](int kc, auto groups_tag, auto part_tag) {
 		constexpr int G = decltype(groups_tag)::value;
 		constexpr bool PART = decltype(part_tag)::value;
-		constexpr bool VA = KA && !PART, VB = KB && !PART;
-		const int kv = k_hi - kc;
 		f32x4 a[G], b[G];
-#pragma unroll
-		for (int h = 0; h < G; ++h) {
-			// a group's offsets stay below 16 rows of a leading dimension (below 2^24)
-			const int k0 = kc + 16 * h;
-			const __amdgpu_buffer_rsrc_t ares = rsrc(TA ? A + (int64_t)k0 * lda + m0 : A + (int64_t)m0 * lda + k0);
-			const __amdgpu_buffer_rsrc_t bres = rsrc(TB ? B + (int64_t)n0 * ldb + k0 : B + (int64_t)k0 * ldb + n0);
-			if (VA) a[h] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(ares, row_in ? (r * lda + 4 * j) * 4 : kOob, 0, 0));
-			if (VB) b[h] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(bres, col_in ? (r * ldb + 4 * j) * 4 : kOob, 0, 0));
-#pragma unroll
-			for (int e = 0; e < 4; ++e) {
-				const int d = 4 * e + j;
-				const bool din = !PART || d < kv;
-				if (!VA) {
-					const int aoff = row_in && din ? (TA ? d * lda + r : r * lda + d) * 4 : kOob;
-					a[h][e] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(ares, aoff, 0, 0));
-				}
-				if (!VB) {
-					const int boff = col_in && din ? (TB ? r * ldb + d : d * ldb + r) * 4 : kOob;
-					b[h][e] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(bres, boff, 0, 0));
-				}
-			}
-		}
+		load_groups<TA, TB, KA && !PART, KB && !PART, PART, G>(A, lda, B, ldb, m0, n0, kc, k_hi - kc, r, j, row_in,
+		                                                       col_in, a, b);
 		__builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-		for (int h = 0; h < G; ++h) {
-			if (VA) transpose4(a[h]);
-			if (VB) transpose4(b[h]);
-#pragma unroll
-			for (int e = 0; e < 4; ++e) {
-				float bv = b[h][e];
-				if (PART) bv = __builtin_bit_cast(float, __builtin_bit_cast(unsigned, bv) | (4 * e + j < kv ? 0u : 0x80000000u));
-				acc = Mfma<kMf16x4>::mma(a[h][e], bv, acc);
-			}
-		}
+		mma_groups<KA && !PART, KB && !PART, PART, G>(a, b, k_hi - kc, j, acc);
 		__builtin_amdgcn_sched_barrier(0);
 	};
 	using I1 = std::integral_constant<int, 1>;

@@ -156,15 +156,25 @@ def test_depth_cut(gpu, oracle):
                     seed += 1
 
 
-def test_accumulate_adds_old_c_after_first_depth_block(gpu, oracle):
+def _chain4_config():
+    import nnh
+    return next(i for i, nm in enumerate(nnh.gemm_configs()) if nm.startswith("mfma chain 16x16x4"))
+
+
+@pytest.mark.parametrize("force_chain", [0, 1])
+def test_accumulate_adds_old_c_after_first_depth_block(gpu, oracle, force_chain):
     """With accumulate, nn-cpp adds the old C after the first 256 depth steps (Store::kAdd, then
-    kContinue): exercised at depths around 256 and 512, with and without the depth cut."""
+    kContinue): exercised at depths around 256 and 512, with and without the depth cut, aligned and padded rows;
+    force_chain runs the products that are not cut on the whole-depth 16x16x4 chain kernel (old C added between two
+    of its 128-deep chunks)."""
+    cfg = _chain4_config() if force_chain else -1
     seed = 40000
-    for k in (1, 255, 256, 257, 300, 511, 512, 513, 1000):
+    for k in (1, 15, 255, 256, 257, 300, 511, 512, 513, 1000):
         for (m, n) in ((129, 129), (300, 300)):
-            for ta, tb in ((0, 0), (1, 1)):
-                check(oracle, Problem(ta, tb, m, n, k, 1, seed), 1)
-                seed += 1
+            for ta, tb in ((0, 0), (1, 1), (0, 1), (1, 0)):
+                for pad in (0, 1):
+                    check(oracle, Problem(ta, tb, m, n, k, pad, seed), 1, cfg)
+                    seed += 1
 
 
 def test_every_tile_configuration_gives_the_same_bits(gpu, oracle):
