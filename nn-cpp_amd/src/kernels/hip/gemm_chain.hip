@@ -5,7 +5,8 @@
 // same bits as the tile kernels. A workgroup owns a 32 x 32 tile of C, a wave a 16 x 16 quarter of it; the two
 // waves of a tile row read the same rows of op(A), which the CU's cache serves once. A wave streams the depth in
 // chunks of 128 indices (all 16 or 64 loads of a chunk in flight), the next chunk's loads issued before the current
-// chunk's MFMAs, so a chain waits on memory once instead of once per LDS stage. Accumulate follows the reference's
+// chunk's MFMAs, so a chain waits on memory once instead of once per LDS stage; a k-contiguous operand is reordered
+// for the MFMA through the wave's own LDS slots (gemm_direct.hpp), with no barrier. Accumulate follows the reference's
 // order (kAccAfter): old C joins the chain after the first 256 steps, or is added at the end of a shorter one.
 #include <algorithm>
 #include <type_traits>
@@ -37,6 +38,10 @@ __global__ void __launch_bounds__(256) sgemm_chain4_kernel(const GemmArgs p) {
 	const int r = lane & 15, j = lane >> 4;
 	const bool row_in = m0 + r < p.m, col_in = n0 + r < p.n;
 	const int K = p.k;
+	// the wave's LDS slots for its k-contiguous operands (two groups each)
+	__shared__ __align__(16) float kst[(KA || KB) ? 4 * 2 * 2 * kKSlot : 1];
+	float* const la = kst + (KA || KB ? wave * 4 * kKSlot : 0);
+	float* const lb = la + 2 * kKSlot;
 	f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
 	// register e of lane l holds row 4 (l / 16) + e, column l % 16 of the quarter
 	const int col = n0 + r;
@@ -54,7 +59,7 @@ __global__ void __launch_bounds__(256) sgemm_chain4_kernel(const GemmArgs p) {
 		load_groups<TA, TB, KA, KB, false, kChunkGroups>(A, lda, B, ldb, m0, n0, kc, K - kc, r, j, row_in, col_in, a, b);
 	};
 	auto run8 = [&](f32x4 (&a)[kChunkGroups], f32x4 (&b)[kChunkGroups]) {
-		mma_groups<KA, KB, false, kChunkGroups>(a, b, 0, j, acc);
+		mma_groups<KA, KB, false, kChunkGroups>(a, b, 0, r, j, acc, la, lb);
 	};
 	// whole chunks, two register sets: chunk c + 1's loads in flight while chunk c's MFMAs run
 	const int n128 = K / 128;
@@ -84,7 +89,7 @@ __global__ void __launch_bounds__(256) sgemm_chain4_kernel(const GemmArgs p) {
 		load_groups<TA, TB, KA && !PART, KB && !PART, PART, G>(A, lda, B, ldb, m0, n0, kc, K - kc, r, j, row_in, col_in,
 		                                                       a, b);
 		__builtin_amdgcn_sched_barrier(0);
-		mma_groups<KA && !PART, KB && !PART, PART, G>(a, b, K - kc, j, acc);
+		mma_groups<KA && !PART, KB && !PART, PART, G>(a, b, K - kc, r, j, acc, la, lb);
 		__builtin_amdgcn_sched_barrier(0);
 	};
 	if (K - kc >= 64) {

@@ -22,32 +22,10 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const float* base) {
 	return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), (short)0, kOob, 0x00020000);
 }
 
-// v[e] of lane group g (lanes 16 g .. 16 g + 15) becomes what v[g] of lane group e held: a 4 x 4 transpose of the
-// lane groups' four registers, by two v_permlane32_swap (lane groups 2, 3 of one register with 0, 1 of another) and
-// two v_permlane16_swap (odd groups of one with even groups of another), each after the two wait states a VALU
-// result needs before a lane swap reads it. Written as assembly: the compiler's builtins for these swaps return the
-// first register's result for both at -O3 (hipcc of ROCm 7.2). The registers are taken from a whole-vector bit
-// cast: a bit cast of one element of a float vector read element 0 for all four in the same compiler.
-__device__ __forceinline__ void transpose4(f32x4& v) {
-	typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
-	const u32x4 u = __builtin_bit_cast(u32x4, v);
-	unsigned x0 = u.x, x1 = u.y, x2 = u.z, x3 = u.w;
-	asm volatile(
-	    "s_nop 1\n\t"
-	    "v_permlane32_swap_b32 %0, %2\n\t"
-	    "v_permlane32_swap_b32 %1, %3\n\t"
-	    "s_nop 1\n\t"
-	    "v_permlane16_swap_b32 %0, %1\n\t"
-	    "v_permlane16_swap_b32 %2, %3\n\t"
-	    "s_nop 1"
-	    : "+v"(x0), "+v"(x1), "+v"(x2), "+v"(x3));
-	v = __builtin_bit_cast(f32x4, u32x4{x0, x1, x2, x3});
-}
-
 // G groups of depth indices kc .. kc + 16 G - 1 of the 16 x 16 tile at (m0, n0): kv depth indices are left in the
 // chain from kc (PART: fewer than 16). A k-contiguous operand (A not transposed, B transposed) takes, with VA / VB,
-// one 16-byte load per group (lane group g: depths 16 h + 4 g .. + 3 of its row), transposed across the lane
-// groups by mma_groups; otherwise one element per lane and step. Rows and columns outside the matrix, and with PART
+// one 16-byte load per group (lane group g: depths 16 h + 4 g .. + 3 of its row), reordered through LDS by
+// mma_groups; otherwise one element per lane and step. Rows and columns outside the matrix, and with PART
 // depths past the chain's end, load +0 without touching memory. A group's offsets stay below 16 rows of a leading
 // dimension, which the caller keeps below 2^24.
 template <bool TA, bool TB, bool VA, bool VB, bool PART, int G>
@@ -76,20 +54,67 @@ __device__ __forceinline__ void load_groups(const float* A, int lda, const float
 	}
 }
 
-// The MFMA steps of G loaded groups, in depth order, into acc. PART: steps past the chain's end (depth offset kv
-// and beyond) multiply A's +0 by B's fill turned into -0, which leaves every sum as it was, -0 included.
+// Per-wave LDS staging of a k-contiguous operand's groups, in place of a transpose across lane groups (lane swaps
+// are VALU instructions, and VALU work of a wave between its dependent MFMAs lengthens every chain step: measured
+// 33 cycles per dependent 16x16x4 step alone, 53-56 with one four-swap transpose per four steps). A slot holds one
+// group, 16 rows of 16 depths at a pitch of 20 floats; depth 4 t + e of a row sits at 4 e + t, so that lane group g's
+// four depths of its row (4 s + g for the group's four steps s) are one 16-byte read. Lane (r, g) writes its 16-byte
+// load (depths 4 g .. 4 g + 3) as four 4-byte stores; the pitch puts the 64 lanes of each store on 64 banks.
+constexpr int kKPitch = 20;
+constexpr int kKSlot = 16 * kKPitch;  // floats of one slot
+
+__device__ __forceinline__ void kperm_write(float* slot, const f32x4& v, int r, int j) {
+#pragma unroll
+	for (int e = 0; e < 4; ++e) slot[r * kKPitch + 4 * e + j] = v[e];
+}
+
+__device__ __forceinline__ f32x4 kperm_read(const float* slot, int r, int j) {
+	return *reinterpret_cast<const f32x4*>(slot + r * kKPitch + 4 * j);
+}
+
+// Orders a wave's LDS accesses for the compiler (the LDS runs one wave's accesses in issue order).
+__device__ __forceinline__ void wave_lds_fence() {
+	__builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+	__builtin_amdgcn_wave_barrier();
+	__builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// The MFMA steps of G loaded groups, in depth order, into acc. VA / VB: that operand came as 16-byte loads and goes
+// through the wave's two LDS slots (la, lb: 2 kKSlot floats each), group h + 1's round trip issued before group h's
+// MFMAs. PART: steps past the chain's end (depth offset kv and beyond) multiply A's +0 by B's fill turned into -0,
+// which leaves every sum as it was, -0 included.
 template <bool VA, bool VB, bool PART, int G>
-__device__ __forceinline__ void mma_groups(f32x4* a, f32x4* b, int kv, int j, f32x4& acc) {
+__device__ __forceinline__ void mma_groups(f32x4* a, f32x4* b, int kv, int r, int j, f32x4& acc, float* la,
+                                           float* lb) {
+	f32x4 ca = a[0], cb = b[0];
+	if (VA || VB) {
+		if (VA) kperm_write(la, a[0], r, j);
+		if (VB) kperm_write(lb, b[0], r, j);
+		wave_lds_fence();
+		if (VA) ca = kperm_read(la, r, j);
+		if (VB) cb = kperm_read(lb, r, j);
+	}
 #pragma unroll
 	for (int h = 0; h < G; ++h) {
-		if (VA) transpose4(a[h]);
-		if (VB) transpose4(b[h]);
+		f32x4 na = ca, nb = cb;
+		if ((VA || VB) && h + 1 < G) {
+			float* sa = la + ((h + 1) & 1) * kKSlot;
+			float* sb = lb + ((h + 1) & 1) * kKSlot;
+			if (VA) kperm_write(sa, a[h + 1], r, j);
+			if (VB) kperm_write(sb, b[h + 1], r, j);
+			wave_lds_fence();
+			if (VA) na = kperm_read(sa, r, j);
+			if (VB) nb = kperm_read(sb, r, j);
+		}
+		const f32x4 av = VA ? ca : a[h], bw = VB ? cb : b[h];
 #pragma unroll
 		for (int e = 0; e < 4; ++e) {
-			float bv = b[h][e];
+			float bv = bw[e];
 			if (PART) bv = __builtin_bit_cast(float, __builtin_bit_cast(unsigned, bv) | (4 * e + j < kv ? 0u : 0x80000000u));
-			acc = Mfma<kMf16x4>::mma(a[h][e], bv, acc);
+			acc = Mfma<kMf16x4>::mma(av[e], bv, acc);
 		}
+		if (VA) ca = na;
+		if (VB) cb = nb;
 	}
 }
 

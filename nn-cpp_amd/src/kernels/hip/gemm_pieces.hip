@@ -346,10 +346,14 @@ __global__ void __launch_bounds__(RS ? (kRsMaxPieces + kRsWaves) * 64 : kMaxPiec
 	f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
 	// one chunk of G groups of 16 depth indices: every load issued before the first MFMA. Group h holds the operands
 	// of steps 4 h .. 4 h + 3. A k-contiguous operand (A not transposed, B transposed) takes, with VEC, one 16-byte
-	// load per group (lane group g: depths 16 h + 4 g .. + 3 of its row), transposed across the lane groups before
-	// the group's MFMAs (transpose4); otherwise one element per lane and step. PART (fewer than 16 indices left in
+	// load per group (lane group g: depths 16 h + 4 g .. + 3 of its row), reordered through the wave's LDS slots
+	// (gemm_direct.hpp); otherwise one element per lane and step. PART (fewer than 16 indices left in
 	// the piece) loads element by element, masks the depth and turns B's +0 fill past the end into -0 at the MFMA.
 	constexpr bool KA = VEC && !TA, KB = VEC && TB;
+	// the wave's LDS slots for its k-contiguous operands (two groups each)
+	__shared__ __align__(16) float kst[(KA || KB) ? kMaxPieces * 2 * 2 * kKSlot : 1];
+	float* const la = kst + (KA || KB ? wave * 4 * kKSlot : 0);
+	float* const lb = la + 2 * kKSlot;
 	auto chunk = [&](int kc, auto groups_tag, auto part_tag) {
 		constexpr int G = decltype(groups_tag)::value;
 		constexpr bool PART = decltype(part_tag)::value;
@@ -357,7 +361,7 @@ __global__ void __launch_bounds__(RS ? (kRsMaxPieces + kRsWaves) * 64 : kMaxPiec
 		load_groups<TA, TB, KA && !PART, KB && !PART, PART, G>(A, lda, B, ldb, m0, n0, kc, k_hi - kc, r, j, row_in,
 		                                                       col_in, a, b);
 		__builtin_amdgcn_sched_barrier(0);
-		mma_groups<KA && !PART, KB && !PART, PART, G>(a, b, k_hi - kc, j, acc);
+		mma_groups<KA && !PART, KB && !PART, PART, G>(a, b, k_hi - kc, r, j, acc, la, lb);
 		__builtin_amdgcn_sched_barrier(0);
 	};
 	using I1 = std::integral_constant<int, 1>;
