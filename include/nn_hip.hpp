@@ -152,6 +152,9 @@ Value matmul(const Value& a, const Value& b);
 Value matmul_bt(const Value& a, const Value& b);
 // ops.hpp:304: x W^T + b, x {..., K}, weight {N, K}, bias {N}.
 Value linear(const Value& x, const Value& weight, const Value& bias);
+// relu(linear(x, weight, bias)) with both forwards in one launch: the same two nodes, outputs and gradients. No
+// counterpart in the reference, whose model code calls the two ops in turn.
+Value linear_relu(const Value& x, const Value& weight, const Value& bias);
 Value relu(const Value& x);
 // ops.cpp:672-681: same elements, new shape (the Flatten module's op).
 Value reshape(const Value& x, std::vector<size_t> new_shape);

@@ -13,8 +13,8 @@
 //
 // Differences, each stated where it applies: MultiHeadAttention refuses dropout on its attention weights in training
 // mode (std::invalid_argument; the reference composes that path from ops this library does not have), and Sequential
-// also runs a Conv2d, ReLU, MaxPool2d triple as nn::hip::conv2d_relu_maxpool2d (the same two graph nodes and bits as
-// conv2d_relu then maxpool2d, with both forwards in one pass).
+// also runs a Conv2d, ReLU, MaxPool2d triple as nn::hip::conv2d_relu_maxpool2d and a Linear, ReLU pair as
+// nn::hip::linear_relu (the same graph nodes and bits as the ops in turn, with the forwards in one pass).
 #pragma once
 
 #include <memory>
@@ -63,11 +63,14 @@ public:
 	Value forward(const Value& input) override;
 };
 
-// linear.cpp: y = x W^T + b; W {out, in} uniform in +-1/sqrt(in), b zeros.
+// linear.cpp: y = x W^T + b; W {out, in} uniform in +-1/sqrt(in), b zeros. A following ReLU folds into linear_relu
+// (the reference's Sequential folds only Conv2d + ReLU; the nodes and bits are those of the two ops).
 class Linear : public Module {
 public:
 	Linear(size_t in_features, size_t out_features);
 	Value forward(const Value& input) override;
+	bool can_fuse_relu() const override { return true; }
+	Value forward_relu(const Value& input) override { return linear_relu(input, weight_, bias_); }
 	std::vector<Value> parameters() const override;
 	std::vector<std::pair<std::string, Value>> named_parameters() const override;
 	const Value& weight() const { return weight_; }

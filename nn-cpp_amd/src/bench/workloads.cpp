@@ -69,8 +69,8 @@ Value transformer_forward(const std::vector<float>& ids, size_t N, const std::ve
 
 Value forward(int model, const Value& x, const std::vector<Value>& p) {
 	if (model == 0) {
-		Value h = nn::hip::relu(nn::hip::linear(x, p[0], p[1]));
-		h = nn::hip::relu(nn::hip::linear(h, p[2], p[3]));
+		Value h = nn::hip::linear_relu(x, p[0], p[1]);
+		h = nn::hip::linear_relu(h, p[2], p[3]);
 		return nn::hip::linear(h, p[4], p[5]);
 	}
 	const size_t N = x.data().shape()[0];
@@ -78,7 +78,7 @@ Value forward(int model, const Value& x, const std::vector<Value>& p) {
 	Value h = nn::hip::conv2d_relu_maxpool2d(x, p[0], p[1], 1, 1, 2, 2);
 	h = nn::hip::conv2d_relu_maxpool2d(h, p[2], p[3], 1, 1, 2, 2);
 	h = nn::hip::reshape(h, {N, 784});
-	return nn::hip::linear(nn::hip::relu(nn::hip::linear(h, p[4], p[5])), p[6], p[7]);
+	return nn::hip::linear(nn::hip::linear_relu(h, p[4], p[5]), p[6], p[7]);
 }
 
 }  // namespace

@@ -393,7 +393,13 @@ Value pool_node(const Value& x, size_t kernel_size, size_t stride, Tensor y, std
 Value matmul(const Value& a, const Value& b) { return matmul_op(a, b, false); }
 Value matmul_bt(const Value& a, const Value& b) { return matmul_op(a, b, true); }
 
-Value linear(const Value& x, const Value& weight, const Value& bias) {
+namespace {
+
+// nn::linear's node (ops.cpp:714-745); with relu, its forward also applies the ReLU that follows it in the same
+// launch (the GEMM epilogue) and a relu node over it is returned: the same two nodes and bits as relu(linear(...)).
+// The linear node's own data is then the ReLU's output: no backward rule reads it (linear's reads x and W, relu's
+// masks with its output, y > 0 exactly where its input is), and the caller only holds the relu node.
+Value linear_op(const Value& x, const Value& weight, const Value& bias, bool relu) {
 	const auto& xs = x.data().shape();
 	const auto& ws = weight.data().shape();
 	// ops.cpp:717-719
@@ -404,8 +410,8 @@ Value linear(const Value& x, const Value& weight, const Value& bias) {
 	out.push_back(n);
 	Tensor y = Tensor::empty(out);
 	check(nnh_linear_forward(x.data().data(), K ? M : numel(std::vector<size_t>(xs.begin(), xs.end() - 1)), K,
-	                         weight.data().data(), n, bias.data().data(), 0, y.data(), g_stream));
-	return Value::node(std::move(y), {x, weight, bias}, [x, weight, bias, n, K](const Tensor& g) {
+	                         weight.data().data(), n, bias.data().data(), relu ? 1 : 0, y.data(), g_stream));
+	Value h = Value::node(y, {x, weight, bias}, [x, weight, bias, n, K](const Tensor& g) {
 		bool fx = false, fw = false, fb = false;
 		float* dx = grad_if(x, fx);
 		float* dw = grad_if(weight, fw);
@@ -415,7 +421,20 @@ Value linear(const Value& x, const Value& weight, const Value& bias) {
 		check(nnh_linear_backward(g.data(), x.data().data(), weight.data().data(), xs2.data(), (int)xs2.size() - 1, K, n,
 		                          dx, fx, dw, fw, db, fb, g_stream));
 	});
+	if (!relu) return h;
+	// ops.cpp:775-793 on h, masked with the output
+	return Value::node(y, {h}, [h, y](const Tensor& g) {
+		bool first = false;
+		float* dh = grad_if(h, first);
+		if (dh) check(nnh_relu_backward(y.data(), g.data(), dh, first, g.size(), g_stream));
+	});
 }
+
+}  // namespace
+
+Value linear(const Value& x, const Value& weight, const Value& bias) { return linear_op(x, weight, bias, false); }
+
+Value linear_relu(const Value& x, const Value& weight, const Value& bias) { return linear_op(x, weight, bias, true); }
 
 Value relu(const Value& x) {
 	Tensor y = Tensor::empty(x.data().shape());
