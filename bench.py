@@ -467,6 +467,49 @@ def build_rows(report=False, split=False):
                     pool1_bwd, lambda: [gxp], 0, nbytes=pool_bytes, bound="hbm",
                     cpu=lambda ref, w, r, bud: (lambda f, b: (b[0], [b[1]]))(*pool_cpu(ref, w, r, bud)),
                     est_ms=0.008))
+    # the packed forms (nnh.h): ReLU flags one bit per output, a pooled output's maximum as its 2-bit position in the
+    # window; the same values and gradients as the byte forms above (checked bit for bit in main)
+    y1p, bits1 = torch.empty_like(y1), torch.empty(N * 32 * 784 // 8, dtype=torch.uint8, device=dev)
+
+    def conv1_packed():
+        nnh.check(L.nnh_conv2d_relu_forward_packed(P(dxc), N, 1, 28, 28, P(dw1), 32, 3, 3, P(db1), 1, 1, P(y1p),
+                                                   P(bits1), st()))
+
+    conv1_packed()
+    rows.append(Row(3, "conv1_forward_packed", "conv2d_relu forward, conv1, alive flags packed one bit per output",
+                    conv1_packed, lambda: [y1p, bits1], conv1_flops, nbytes=conv1_bytes, bound="hbm",
+                    cpu=lambda ref, w, r, bud: (lambda f, b: (f[0], [f[1], None]))(*conv_cpu(1, ref, w, r, bud)),
+                    est_ms=0.006))
+    y1q, bits1q, x2q = torch.empty_like(y1), torch.empty_like(bits1), torch.empty_like(x2)
+    amax1 = torch.empty(N * 32 * 14 * 4, dtype=torch.uint8, device=dev)
+
+    def conv1_pool1_packed():
+        nnh.check(L.nnh_conv2d_relu_maxpool2d_forward_packed(P(dxc), N, 1, 28, 28, P(dw1), 32, 3, 3, P(db1), 1, 1,
+                                                             P(y1q), P(bits1q), P(x2q), P(amax1), st()))
+
+    conv1_pool1_packed()
+    rows.append(Row(3, "conv1_pool1_forward_packed", "conv1 and the 2x2 s2 maxpool in one pass, alive flags as bits "
+                    "and the window maxima as 2-bit positions", conv1_pool1_packed, lambda: [y1q, bits1q, x2q, amax1],
+                    conv1_flops, nbytes=conv1_bytes + 4 * hx2.size, bound="hbm", est_ms=0.006))
+    gx1p, gw1p, gb1p = torch.empty_like(dxc), torch.empty_like(dw1), torch.empty_like(db1)
+
+    def conv1_bwd_packed():
+        nnh.check(L.nnh_conv2d_backward_packed(P(g1), P(dxc), P(dw1), P(bits1), N, 1, 28, 28, 32, 3, 3, 1, 1, P(gx1p), 1,
+                                               P(gw1p), 1, P(gb1p), 1, st()))
+
+    rows.append(Row(3, "conv1_backward_packed", "conv2d_relu backward, conv1, from the packed flags: dx, dW, db",
+                    conv1_bwd_packed, lambda: [gx1p, gw1p, gb1p], 2 * conv1_flops, nbytes=conv1_bwd_bytes, bound="hbm",
+                    cpu=lambda ref, w, r, bud: (lambda f, b: (b[0], list(b[1])))(*conv_cpu(1, ref, w, r, bud)),
+                    est_ms=0.02))
+    gxpp = torch.empty_like(y1)
+
+    def pool1_bwd_packed():
+        nnh.check(L.nnh_maxpool2d_backward_packed(P(gp), P(amax1), N, 32, 28, 28, P(gxpp), 1, st()))
+
+    rows.append(Row(3, "pool1_backward_packed", "maxpool2d backward 2x2 s2 from the 2-bit window positions",
+                    pool1_bwd_packed, lambda: [gxpp], 0, nbytes=pool_bytes, bound="hbm",
+                    cpu=lambda ref, w, r, bud: (lambda f, b: (b[0], [b[1]]))(*pool_cpu(ref, w, r, bud)),
+                    est_ms=0.006))
     conv2_flops = 2.0 * N * 64 * 196 * 288
     rows.append(Row(3, "conv2_forward", "conv2d_relu forward, conv2: x [128,32,14,14] -> y [128,64,14,14], 3x3 s1 p1",
                     conv2, lambda: [y2], conv2_flops, nbytes=4 * (hx2.size + w2.size + 64 + N * 64 * 196),
@@ -664,6 +707,41 @@ def run_gpu_rows(rows):
         log(f"[cfg {r.cfg}] {r.key}: {ms * 1e3:.2f} us (spread {res['spread']:.3f}), "
             f"{achieved:.1f} {res['roofline']['unit']} = {res['roofline']['frac'] * 100:.1f}% of {r.bound} peak, "
             f"repeat bitwise {same}")
+
+
+def unpack_argmax2(a2, planes, h, w):
+    """The plane offsets of nnh.h's 2-bit window positions (2 x 2, stride 2): {planes, h / 2, w / 2} uint32."""
+    import numpy as np
+    ph, pw, rb = h // 2, w // 2, (w + 7) // 8
+    j = np.arange(pw)
+    slot = (a2.reshape(planes, ph, rb)[:, :, j // 4] >> (2 * (j % 4)).astype(np.uint8)) & 3
+    rows = 2 * np.arange(ph)[None, :, None] + slot // 2
+    return (rows * w + 2 * j[None, None, :] + slot % 2).astype(np.uint32)
+
+
+def packed_checks(by_key):
+    """Each packed row against its byte-form row, bit for bit: values and gradients equal, flags equal to the
+    bytes' np.packbits (little bit order), window positions decoding to the 32-bit offsets."""
+    import numpy as np
+    eq = lambda a, b: a.shape == b.shape and np.array_equal(a.view(np.uint8), b.view(np.uint8))
+    fused = by_key.get("conv1_pool1_forward")
+    pairs = {"conv1_forward_packed": "conv1_forward", "conv1_pool1_forward_packed": "conv1_pool1_forward",
+             "conv1_backward_packed": "conv1_backward", "pool1_backward_packed": "pool1_backward"}
+    for key, base in pairs.items():
+        r, b = by_key.get(key), by_key.get(base)
+        if r is None or b is None:
+            continue
+        h, w = r.host_outs, b.host_outs
+        if key == "conv1_forward_packed":
+            ok = eq(h[0], w[0]) and fused is not None and \
+                eq(h[1], np.packbits(fused.host_outs[1].reshape(-1), bitorder="little"))
+        elif key == "conv1_pool1_forward_packed":
+            ok = eq(h[0], w[0]) and eq(h[2], w[2]) and \
+                eq(h[1], np.packbits(w[1].reshape(-1), bitorder="little")) and \
+                eq(unpack_argmax2(h[3], 128 * 32, 28, 28).reshape(-1), w[3].view(np.uint32).reshape(-1))
+        else:
+            ok = len(h) == len(w) and all(eq(x, y) for x, y in zip(h, w))
+        r.result["bitwise_vs_byte_form"] = bool(ok)
 
 
 def run_cpu_rows(rows, headline=None):
@@ -874,17 +952,24 @@ def compact_line(full, strict=True):
     line["data"] = DATA_SHORT
     fo = full.get("fused_op")
     if fo:
-        line["fused_op"] = {"workload": "conv1 conv2d_relu fwd (cfg 3), alive flags", "value": fo["value"],
+        line["fused_op"] = {"workload": "conv1 fwd + alive (cfg 3)", "value": fo["value"],
                             "unit": fo["unit"], "us": fo["us_per_launch"], "frac": fo["roofline"]["frac"],
-                            "fill_floor_us": (fo.get("fill_floor") or {}).get("us_per_launch"),
                             "frac_of_fill_floor": (fo.get("fill_floor") or {}).get("conv1_frac_of_floor")}
-    line["configs"] = {r["key"]: compact_row(r) for r in full.get("configs", [])}
+        # the packed-flag rows: their times and whether all four gave the byte forms' bits (full rows: the rest)
+        packed = {r["key"]: r for r in full.get("configs", []) if r["key"].endswith("_packed")}
+        if packed:
+            short = {"conv1_forward_packed": "fwd", "conv1_pool1_forward_packed": "fwd_pool",
+                     "conv1_backward_packed": "bwd", "pool1_backward_packed": "pool_bwd"}
+            line["fused_op"]["packed_us"] = {short.get(k, k): _r(r["ms"] * 1e3, 2) for k, r in packed.items()}
+            line["fused_op"]["packed_us"]["bitwise"] = all(r.get("bitwise_vs_byte_form") is True and
+                                                           r.get("bitwise_repeat", False) for r in packed.values())
+    line["configs"] = {r["key"]: compact_row(r) for r in full.get("configs", []) if not r["key"].endswith("_packed")}
     line["configs_split_depth"] = {r["key"]: compact_row(r) for r in full.get("configs_split_depth", [])}
     line["workloads"] = [{"workload": w["workload"], "gpu_ms": _r(w.get("gpu", {}).get("total_ms"), 4),
                           "cpu_ms": _r((w.get("cpu") or {}).get("total_ms"), 4),
                           "bitwise": w.get("bitwise_vs_nn_cpp")} for w in full.get("workloads", [])]
     if line["workloads"]:
-        line["workloads_note"] = WORKLOAD_NOTE
+        line["workloads_note"] = WORKLOAD_NOTE_SHORT
     line["full_rows"] = full.get("full_rows")
     text = json.dumps(line, separators=(",", ":"))
     if len(text.encode()) > LINE_LIMIT and not strict:
@@ -899,9 +984,10 @@ def compact_line(full, strict=True):
     return text
 
 
-DATA_SHORT = "synthetic: nn-cpp's seeded std::mt19937 streams (N(0,1) via numpy PCG64); same buffers on both sides"
+DATA_SHORT = "synthetic: nn-cpp's seeded mt19937 streams (N(0,1): numpy PCG64); same buffers both sides"
 WORKLOAD_NOTE = ("step = forward + zero_grad + backward from a fixed N(0,1) logits gradient, both sides; no loss, "
                  "no optimizer step (runner.cpp's optim_ms)")
+WORKLOAD_NOTE_SHORT = "step = fwd + zero_grad + bwd from fixed N(0,1) logits grads; no loss, no optimizer step"
 
 
 def report(with_cpu=True):
@@ -1087,6 +1173,7 @@ def main():
             want = by_key["conv1_forward"].host_outs[:1] + [None] + by_key["pool1_forward"].host_outs
             fused.result["bitwise_vs_two_ops"] = all(w is None or np.array_equal(g.view(np.uint8), w.view(np.uint8))
                                                      for g, w in zip(fused.host_outs, want))
+        packed_checks(by_key)
         # the launch floor of conv1's output size on this GPU: a plain fill of y (12.85 MB)
         ny = 128 * 32 * 28 * 28
         fill_buf = torch.empty(ny, device=dev)
@@ -1170,7 +1257,10 @@ def main():
             "with_pool": None if conv1_pool1 is None or pool1 is None else {
                 "workload": conv1_pool1.workload, "us_per_launch": round(conv1_pool1.result["ms"] * 1e3, 3),
                 "separate_us": round((conv1.result["ms"] + pool1.result["ms"]) * 1e3, 3),
-                "bitwise_vs_two_ops": conv1_pool1.result.get("bitwise_vs_two_ops")}},
+                "bitwise_vs_two_ops": conv1_pool1.result.get("bitwise_vs_two_ops")},
+            "packed_flags": {r.key: {"us_per_launch": round(r.result["ms"] * 1e3, 3),
+                                     "bitwise_vs_byte_form": r.result.get("bitwise_vs_byte_form")}
+                             for r in rows if r.key.endswith("_packed")} or None},
         "configs": [row_json(r) for r in rows],
         "configs_split_depth": [row_json(r) for r in split_rows],
         "next_rows": [row_json(r) for r in next_rows],

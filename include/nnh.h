@@ -70,7 +70,8 @@ typedef struct nnh_epilogue {
  *
  * The *_workspace_size queries give, for the same shape arguments as the call, the bytes that call takes (at least
  * what it needs: where a kernel choice depends on pointer alignment, the larger of the two; over both numerics
- * modes, the larger of the two). One exception: nnh_sgemm_workspace_size cannot see leading dimensions, and a
+ * modes, the larger of the two; nnh_conv2d_backward_workspace_size with with_alive = 1 also covers
+ * nnh_conv2d_backward_packed). One exception: nnh_sgemm_workspace_size cannot see leading dimensions, and a
  * depth-cut product of at most 16 pieces called with lda or ldb of 2^24 or more needs pieces * m * n * batch_count
  * floats of partials that it does not count (with a registered workspace smaller than that, the call returns
  * NNH_ERR_WORKSPACE before launching anything).
@@ -284,6 +285,42 @@ int nnh_conv2d_relu_maxpool2d_forward(const float* x, size_t N, size_t Cin, size
 int nnh_conv2d_backward(const float* g, const float* x, const float* w, const unsigned char* alive, size_t N,
                         size_t Cin, size_t H, size_t W, size_t Cout, size_t kh, size_t kw, int stride, int padding,
                         float* dx, int dx_first, float* dw, int dw_first, float* db, int db_first, void* stream);
+
+/*
+ * Packed forms of the ReLU flags and of the 2 x 2 pool's offsets, for callers whose backward is the flags' only
+ * reader (no counterpart in the reference, which keeps one byte per flag and a 32-bit plane offset per window; the
+ * byte forms above are unchanged). alive_bits holds one bit per output in y's order: bit o of the flattened
+ * {N, Cout, Ho, Wo} index at byte o / 8, bit o % 8 (N Cout Ho Wo / 8 bytes). argmax2 holds each 2 x 2 window's
+ * maximum as its 2-bit position in the window (0 row 0 left, 1 row 0 right, 2 row 1 left, 3 row 1 right): window
+ * (ph, pw) of plane p at bits 2 (pw % 4) of byte (p (Ho / 2) + ph) ceil(Wo / 8) + pw / 4. Values, gradients and bits
+ * are those of the byte forms.
+ *
+ * nnh_conv2d_packed_supported: 1 when a geometry takes them, both the forward (with_pool: conv2d_relu then a 2 x 2
+ * stride-2 maxpool in one pass) and nnh_conv2d_backward_packed (a network's first layer: stride 1, "same" width,
+ * Cin kh kw <= 16, Cout <= 32, Ho Wo a multiple of 8, the padded input plane Cin (Ho + kh - 1) (Wo + kw - 1) at most
+ * 2048 floats; with the pool H even and W <= 256);
+ * pointers must also be aligned as each call states.
+ * nnh_conv2d_relu_forward_packed: nnh_conv2d_forward with fuse_relu = 1 and packed flags (x, y 16-byte aligned).
+ * nnh_conv2d_relu_maxpool2d_forward_packed: nnh_conv2d_relu_maxpool2d_forward (pool 2, stride 2) with packed flags and
+ * offsets (x, y 16-byte, pooled 8-byte aligned).
+ * nnh_conv2d_backward_packed: nnh_conv2d_backward with packed flags (g 16-byte aligned).
+ * nnh_maxpool2d_backward_packed: nnh_maxpool2d_backward (kernel 2, stride 2) from argmax2 (dx 8-byte aligned).
+ */
+int nnh_conv2d_packed_supported(size_t N, size_t Cin, size_t H, size_t W, size_t Cout, size_t kh, size_t kw, int stride,
+                                int padding, int with_pool);
+int nnh_conv2d_relu_forward_packed(const float* x, size_t N, size_t Cin, size_t H, size_t W, const float* w,
+                                   size_t Cout, size_t kh, size_t kw, const float* bias, int stride, int padding,
+                                   float* y, unsigned char* alive_bits, void* stream);
+int nnh_conv2d_relu_maxpool2d_forward_packed(const float* x, size_t N, size_t Cin, size_t H, size_t W, const float* w,
+                                             size_t Cout, size_t kh, size_t kw, const float* bias, int stride,
+                                             int padding, float* y, unsigned char* alive_bits, float* pooled,
+                                             unsigned char* argmax2, void* stream);
+int nnh_conv2d_backward_packed(const float* g, const float* x, const float* w, const unsigned char* alive_bits,
+                               size_t N, size_t Cin, size_t H, size_t W, size_t Cout, size_t kh, size_t kw, int stride,
+                               int padding, float* dx, int dx_first, float* dw, int dw_first, float* db, int db_first,
+                               void* stream);
+int nnh_maxpool2d_backward_packed(const float* g, const unsigned char* argmax2, size_t N, size_t C, size_t H, size_t W,
+                                  float* dx, int first, void* stream);
 
 /* im2col_sample over a batch (ops.cpp:188-212): col {N, Cin*kh*kw, Ho*Wo}, zeros where a tap is padding. */
 int nnh_im2col(const float* x, size_t N, size_t Cin, size_t H, size_t W, size_t kh, size_t kw, int stride, int padding,

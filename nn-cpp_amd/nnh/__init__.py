@@ -94,6 +94,14 @@ _EXTRA_DECLS = {
     "nnh_conv2d_relu_maxpool2d_forward": [_vp, _sz, _sz, _sz, _sz, _vp, _sz, _sz, _sz, _vp, C.c_int, C.c_int, _sz, _sz,
                                           _vp, _vp, _vp, _vp, _vp],
     "nnh_maxpool2d_backward": [_vp, _vp, _sz, _sz, _sz, _sz, _sz, _sz, _vp, C.c_int, _vp],
+    "nnh_conv2d_packed_supported": [_sz, _sz, _sz, _sz, _sz, _sz, _sz, C.c_int, C.c_int, C.c_int],
+    "nnh_conv2d_relu_forward_packed": [_vp, _sz, _sz, _sz, _sz, _vp, _sz, _sz, _sz, _vp, C.c_int, C.c_int, _vp, _vp,
+                                       _vp],
+    "nnh_conv2d_relu_maxpool2d_forward_packed": [_vp, _sz, _sz, _sz, _sz, _vp, _sz, _sz, _sz, _vp, C.c_int, C.c_int,
+                                                 _vp, _vp, _vp, _vp, _vp],
+    "nnh_conv2d_backward_packed": [_vp, _vp, _vp, _vp, _sz, _sz, _sz, _sz, _sz, _sz, _sz, C.c_int, C.c_int, _vp,
+                                   C.c_int, _vp, C.c_int, _vp, C.c_int, _vp],
+    "nnh_maxpool2d_backward_packed": [_vp, _vp, _sz, _sz, _sz, _sz, _vp, C.c_int, _vp],
     "nnh_matmul_backward": [_vp, _vp, _szp, C.c_int, _vp, _szp, C.c_int, C.c_int, _vp, C.c_int, _vp, C.c_int, _vp],
     "nnh_matmul_backward_workspace_size": [_szp, C.c_int, _szp, C.c_int, C.c_int, C.c_int, C.c_int, _szp],
     "nnh_add_to_grad": [_vp, _vp, _sz, C.c_int, _vp],
@@ -414,6 +422,59 @@ def conv2d_backward(g, x, w, alive, stride, pad, dx=None, dx_first=True, dw=None
     check(lib().nnh_conv2d_backward(_ptr(g), _ptr(x), _ptr(w), _ptr(alive), N, Cin, H, W, Cout, kh, kw, int(stride),
                                     int(pad), _ptr(dx), int(dx_first), _ptr(dw), int(dw_first), _ptr(db),
                                     int(db_first), _stream(stream)))
+
+
+def conv2d_packed_supported(x_shape, w_shape, stride, pad, with_pool=False):
+    """Whether nnh_conv2d_*_packed take this geometry (pointer alignment is the caller's part)."""
+    N, Cin, H, W = x_shape
+    Cout, _, kh, kw = w_shape
+    return bool(lib().nnh_conv2d_packed_supported(N, Cin, H, W, Cout, kh, kw, int(stride), int(pad), int(with_pool)))
+
+
+def conv2d_relu_forward_packed(x, w, bias, stride, pad, stream=None):
+    """nn::conv2d_relu with its flags packed one bit per output; returns (y, alive_bits as uint8)."""
+    import torch
+    N, Cin, H, W = x.shape
+    Cout, _, kh, kw = w.shape
+    ho, wo = conv_out(H, W, kh, kw, stride, pad)
+    y = torch.empty((N, Cout, max(ho, 0), max(wo, 0)), dtype=torch.float32, device=x.device)
+    bits = torch.empty(((y.numel() + 7) // 8,), dtype=torch.uint8, device=x.device)
+    check(lib().nnh_conv2d_relu_forward_packed(_ptr(x), N, Cin, H, W, _ptr(w), Cout, kh, kw, _ptr(bias), int(stride),
+                                               int(pad), _ptr(y), _ptr(bits), _stream(stream)))
+    return y, bits
+
+
+def conv2d_relu_maxpool2d_forward_packed(x, w, bias, stride, pad, stream=None):
+    """nn::conv2d_relu then a 2 x 2 stride-2 nn::maxpool2d, flags as bits and window maxima as 2-bit positions;
+    returns (y, alive_bits, pooled, argmax2), both packed arrays uint8."""
+    import torch
+    N, Cin, H, W = x.shape
+    Cout, _, kh, kw = w.shape
+    ho, wo = conv_out(H, W, kh, kw, stride, pad)
+    y = torch.empty((N, Cout, max(ho, 0), max(wo, 0)), dtype=torch.float32, device=x.device)
+    bits = torch.empty(((y.numel() + 7) // 8,), dtype=torch.uint8, device=x.device)
+    pooled = torch.empty((N, Cout, max(ho, 0) // 2, max(wo, 0) // 2), dtype=torch.float32, device=x.device)
+    amax2 = torch.empty((N * Cout * (max(ho, 0) // 2) * ((max(wo, 0) + 7) // 8),), dtype=torch.uint8, device=x.device)
+    check(lib().nnh_conv2d_relu_maxpool2d_forward_packed(_ptr(x), N, Cin, H, W, _ptr(w), Cout, kh, kw, _ptr(bias),
+                                                         int(stride), int(pad), _ptr(y), _ptr(bits), _ptr(pooled),
+                                                         _ptr(amax2), _stream(stream)))
+    return y, bits, pooled, amax2
+
+
+def conv2d_backward_packed(g, x, w, alive_bits, stride, pad, dx=None, dx_first=True, dw=None, dw_first=True, db=None,
+                           db_first=True, stream=None):
+    N, Cin, H, W = x.shape
+    Cout, _, kh, kw = w.shape
+    check(lib().nnh_conv2d_backward_packed(_ptr(g), _ptr(x), _ptr(w), _ptr(alive_bits), N, Cin, H, W, Cout, kh, kw,
+                                           int(stride), int(pad), _ptr(dx), int(dx_first), _ptr(dw), int(dw_first),
+                                           _ptr(db), int(db_first), _stream(stream)))
+
+
+def maxpool2d_backward_packed(g, argmax2, dx, first=True, stream=None):
+    """nn::maxpool2d's backward (kernel 2, stride 2) from 2-bit window positions into dx {N, C, H, W}."""
+    N, Cc, H, W = dx.shape
+    check(lib().nnh_maxpool2d_backward_packed(_ptr(g), _ptr(argmax2), N, Cc, H, W, _ptr(dx), int(first),
+                                              _stream(stream)))
 
 
 def im2col(x, kh, kw, stride, pad, stream=None):

@@ -340,9 +340,9 @@ bool keeps_alive(const Value& x, const Value& w, const Value& b, bool fuse_relu)
 	return fuse_relu && NoGradGuard::grad_enabled() && (x.requires_grad() || w.requires_grad() || b.requires_grad());
 }
 
-// The conv node over its forward's outputs y and alive.
+// The conv node over its forward's outputs y and alive (packed: one bit per output, nnh.h's packed form).
 Value conv_node(const Value& x, const Value& w, const Value& b, int stride, int padding, const ConvShape& c, Tensor y,
-                std::shared_ptr<Block> alive) {
+                std::shared_ptr<Block> alive, bool packed) {
 	return Value::node(std::move(y), {x, w, b}, [=](const Tensor& g) {
 		// ops.cpp:1418-1463: dx taken first (grad_accum), then db and dW (grad() +=, a fresh one zeroed first,
 		// which gives the sum itself)
@@ -351,20 +351,34 @@ Value conv_node(const Value& x, const Value& w, const Value& b, int stride, int 
 		float* db = grad_if(b, fb);
 		float* dw = grad_if(w, fw);
 		if (!dx && !dw && !db) return;
-		check(nnh_conv2d_backward(g.data(), x.data().data(), w.data().data(),
-		                          alive ? static_cast<const unsigned char*>(alive->p) : nullptr, c.N, c.Cin, c.H, c.W,
-		                          c.Cout, c.kh, c.kw, stride, padding, dx, fx, dw, fw, db, fb, g_stream));
+		const unsigned char* al = alive ? static_cast<const unsigned char*>(alive->p) : nullptr;
+		if (packed)
+			check(nnh_conv2d_backward_packed(g.data(), x.data().data(), w.data().data(), al, c.N, c.Cin, c.H, c.W, c.Cout,
+			                                 c.kh, c.kw, stride, padding, dx, fx, dw, fw, db, fb, g_stream));
+		else
+			check(nnh_conv2d_backward(g.data(), x.data().data(), w.data().data(), al, c.N, c.Cin, c.H, c.W, c.Cout, c.kh,
+			                          c.kw, stride, padding, dx, fx, dw, fw, db, fb, g_stream));
 	});
 }
+
+bool aligned16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }
 
 Value conv_op(const Value& x, const Value& w, const Value& b, int stride, int padding, bool fuse_relu) {
 	const ConvShape c = conv_shape(x, w, b, stride, padding);
 	Tensor y = Tensor::empty({c.N, c.Cout, c.ho, c.wo});
-	std::shared_ptr<Block> alive = keeps_alive(x, w, b, fuse_relu) ? side_buffer(y.size()) : nullptr;
-	check(nnh_conv2d_forward(x.data().data(), c.N, c.Cin, c.H, c.W, w.data().data(), c.Cout, c.kh, c.kw,
-	                         b.data().data(), stride, padding, fuse_relu, y.data(),
-	                         alive ? static_cast<unsigned char*>(alive->p) : nullptr, g_stream));
-	return conv_node(x, w, b, stride, padding, c, std::move(y), std::move(alive));
+	const bool keep = keeps_alive(x, w, b, fuse_relu);
+	// a first layer keeps its flags as bits (its backward is their only reader)
+	const bool packed = keep && aligned16(x.data().data()) && aligned16(y.data()) &&
+	                    nnh_conv2d_packed_supported(c.N, c.Cin, c.H, c.W, c.Cout, c.kh, c.kw, stride, padding, 0);
+	std::shared_ptr<Block> alive = keep ? side_buffer(packed ? (y.size() + 7) / 8 : y.size()) : nullptr;
+	unsigned char* al = alive ? static_cast<unsigned char*>(alive->p) : nullptr;
+	if (packed)
+		check(nnh_conv2d_relu_forward_packed(x.data().data(), c.N, c.Cin, c.H, c.W, w.data().data(), c.Cout, c.kh, c.kw,
+		                                     b.data().data(), stride, padding, y.data(), al, g_stream));
+	else
+		check(nnh_conv2d_forward(x.data().data(), c.N, c.Cin, c.H, c.W, w.data().data(), c.Cout, c.kh, c.kw,
+		                         b.data().data(), stride, padding, fuse_relu, y.data(), al, g_stream));
+	return conv_node(x, w, b, stride, padding, c, std::move(y), std::move(alive), packed);
 }
 
 // ops.cpp:1610-1617: the pooled shape, or TensorShapeError.
@@ -375,14 +389,19 @@ std::vector<size_t> pool_shape(const std::vector<size_t>& xs, size_t kernel_size
 	return {xs[0], xs[1], (xs[2] - kernel_size) / stride + 1, (xs[3] - kernel_size) / stride + 1};
 }
 
-// The pool node over its forward's output y and argmax.
-Value pool_node(const Value& x, size_t kernel_size, size_t stride, Tensor y, std::shared_ptr<Block> arg) {
+// The pool node over its forward's output y and argmax (packed: 2-bit window positions of a 2 x 2, stride-2 pool).
+Value pool_node(const Value& x, size_t kernel_size, size_t stride, Tensor y, std::shared_ptr<Block> arg,
+                bool packed = false) {
 	const auto& xs = x.data().shape();
 	const size_t N = xs[0], C = xs[1], H = xs[2], W = xs[3];
 	return Value::node(std::move(y), {x}, [=](const Tensor& g) {
 		bool first = false;
 		float* dx = grad_if(x, first);
-		if (dx)
+		if (!dx) return;
+		if (packed)
+			check(nnh_maxpool2d_backward_packed(g.data(), static_cast<const unsigned char*>(arg->p), N, C, H, W, dx, first,
+			                                    g_stream));
+		else
 			check(nnh_maxpool2d_backward(g.data(), static_cast<const unsigned int*>(arg->p), N, C, H, W, kernel_size,
 			                             stride, dx, first, g_stream));
 	});
@@ -478,13 +497,29 @@ Value conv2d_relu_maxpool2d(const Value& x, const Value& weight, const Value& bi
 	const std::vector<size_t> ys{c.N, c.Cout, c.ho, c.wo};
 	Tensor y = Tensor::empty(ys);
 	Tensor p = Tensor::empty(pool_shape(ys, kernel_size, pool_stride));
-	std::shared_ptr<Block> alive = keeps_alive(x, weight, bias, true) ? side_buffer(y.size()) : nullptr;
+	const bool keep = keeps_alive(x, weight, bias, true);
+	// a first layer keeps its flags as bits and the window maxima as 2-bit positions (the backward is their only
+	// reader)
+	const bool packed = keep && kernel_size == 2 && pool_stride == 2 && aligned16(x.data().data()) &&
+	                    aligned16(y.data()) &&
+	                    nnh_conv2d_packed_supported(c.N, c.Cin, c.H, c.W, c.Cout, c.kh, c.kw, stride, padding, 1);
+	if (packed) {
+		std::shared_ptr<Block> alive = side_buffer((y.size() + 7) / 8);
+		std::shared_ptr<Block> arg = side_buffer(c.N * c.Cout * (c.ho / 2) * ((c.wo + 7) / 8));
+		check(nnh_conv2d_relu_maxpool2d_forward_packed(x.data().data(), c.N, c.Cin, c.H, c.W, weight.data().data(), c.Cout,
+		                                               c.kh, c.kw, bias.data().data(), stride, padding, y.data(),
+		                                               static_cast<unsigned char*>(alive->p), p.data(),
+		                                               static_cast<unsigned char*>(arg->p), g_stream));
+		Value conv = conv_node(x, weight, bias, stride, padding, c, std::move(y), std::move(alive), true);
+		return pool_node(conv, kernel_size, pool_stride, std::move(p), std::move(arg), true);
+	}
+	std::shared_ptr<Block> alive = keep ? side_buffer(y.size()) : nullptr;
 	std::shared_ptr<Block> arg = side_buffer(p.size() * 4);
 	check(nnh_conv2d_relu_maxpool2d_forward(x.data().data(), c.N, c.Cin, c.H, c.W, weight.data().data(), c.Cout, c.kh,
 	                                        c.kw, bias.data().data(), stride, padding, kernel_size, pool_stride,
 	                                        y.data(), alive ? static_cast<unsigned char*>(alive->p) : nullptr, p.data(),
 	                                        static_cast<unsigned int*>(arg->p), g_stream));
-	Value conv = conv_node(x, weight, bias, stride, padding, c, std::move(y), std::move(alive));
+	Value conv = conv_node(x, weight, bias, stride, padding, c, std::move(y), std::move(alive), false);
 	return pool_node(conv, kernel_size, pool_stride, std::move(p), std::move(arg));
 }
 

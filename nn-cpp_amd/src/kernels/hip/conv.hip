@@ -117,7 +117,8 @@ __global__ void __launch_bounds__(256) conv_direct_kernel(const float* __restric
 template <int CG, int PAD, int ROWS>
 __global__ void __launch_bounds__(256) conv_same_quad_kernel(const float* __restrict__ x, const float* __restrict__ w,
                                                              const float* __restrict__ bias, float* __restrict__ y,
-                                                             unsigned char* __restrict__ alive, ConvGeom g, FastDiv qpr,
+                                                             unsigned char* __restrict__ alive,
+                                                             unsigned char* __restrict__ bits, ConvGeom g, FastDiv qpr,
                                                              FastDiv ho, FastDiv kh, int cout, int relu,
                                                              int total_quads) {
 	constexpr int KW = 2 * PAD + 1;
@@ -178,28 +179,34 @@ __global__ void __launch_bounds__(256) conv_same_quad_kernel(const float* __rest
 			}
 		}
 	}
-	if (!active) return;
 	const int64_t hw = (int64_t)g.ho * g.wo;
 	const int64_t p0 = (int64_t)oh * g.wo + ow0;
 #pragma unroll
 	for (int c = 0; c < CG; ++c) {
-		if (c0 + c >= cout) break;
+		if (c0 + c >= cout) break;  // uniform
 		const int64_t o = ((int64_t)n * cout + c0 + c) * hw + p0;
 		const float b = bias[c0 + c];
 		f32x4 out;
-		unsigned flags = 0;
+		unsigned flags = 0, nib = 0;
 #pragma unroll
 		for (int i = 0; i < 4; ++i) {
 			float val = acc[c][i] + b;
 			if (relu) {
 				const bool on = val > 0.0f;
 				flags |= (on ? 1u : 0u) << (8 * i);
+				nib |= (on ? 1u : 0u) << i;
 				val = on ? val : 0.0f;
 			}
 			out[i] = val;
 		}
-		*reinterpret_cast<f32x4*>(y + o) = out;
-		if (alive) *reinterpret_cast<unsigned*>(alive + o) = flags;
+		if (active) *reinterpret_cast<f32x4*>(y + o) = out;
+		if (active && alive) *reinterpret_cast<unsigned*>(alive + o) = flags;
+		if (bits) {
+			// one bit per output in y's order (bit o at byte o / 8): with Ho Wo a multiple of 8, quads 2 t and 2 t + 1
+			// (lanes of one wave) share a byte, which the even one writes
+			const unsigned partner = __shfl_down(nib, 1);
+			if (active && (q & 1) == 0) bits[o >> 3] = (unsigned char)(nib | (partner << 4));
+		}
 	}
 }
 
@@ -448,12 +455,12 @@ constexpr int kQuadMaxRows = 8;
 
 template <int CG, int PAD, int ROWS>
 hipError_t launch_quad_rows(const float* x, const float* w, const float* bias, float* y, unsigned char* alive,
-                            const ConvGeom& g, int total_quads, int cout, int relu, hipStream_t s) {
+                            unsigned char* bits, const ConvGeom& g, int total_quads, int cout, int relu, hipStream_t s) {
 	if constexpr (ROWS * (2 * PAD + 1) > 32) {
 		return hipErrorInvalidValue;
 	} else {
 		dim3 grid(blocks_for(total_quads), (unsigned)((cout + CG - 1) / CG));
-		hipLaunchKernelGGL((conv_same_quad_kernel<CG, PAD, ROWS>), grid, dim3(256), 0, s, x, w, bias, y, alive, g,
+		hipLaunchKernelGGL((conv_same_quad_kernel<CG, PAD, ROWS>), grid, dim3(256), 0, s, x, w, bias, y, alive, bits, g,
 		                   make_fastdiv((unsigned)(g.wo / 4)), make_fastdiv((unsigned)g.ho), make_fastdiv((unsigned)g.kh),
 		                   cout, relu, total_quads);
 		return hipGetLastError();
@@ -462,29 +469,29 @@ hipError_t launch_quad_rows(const float* x, const float* w, const float* bias, f
 
 template <int CG, int PAD>
 hipError_t launch_quad_pad(const float* x, const float* w, const float* bias, float* y, unsigned char* alive,
-                           const ConvGeom& g, int total_quads, int cout, int relu, hipStream_t s) {
+                           unsigned char* bits, const ConvGeom& g, int total_quads, int cout, int relu, hipStream_t s) {
 	switch (g.cin * g.kh) {
-		case 1: return launch_quad_rows<CG, PAD, 1>(x, w, bias, y, alive, g, total_quads, cout, relu, s);
-		case 2: return launch_quad_rows<CG, PAD, 2>(x, w, bias, y, alive, g, total_quads, cout, relu, s);
-		case 3: return launch_quad_rows<CG, PAD, 3>(x, w, bias, y, alive, g, total_quads, cout, relu, s);
-		case 4: return launch_quad_rows<CG, PAD, 4>(x, w, bias, y, alive, g, total_quads, cout, relu, s);
-		case 5: return launch_quad_rows<CG, PAD, 5>(x, w, bias, y, alive, g, total_quads, cout, relu, s);
-		case 6: return launch_quad_rows<CG, PAD, 6>(x, w, bias, y, alive, g, total_quads, cout, relu, s);
-		case 7: return launch_quad_rows<CG, PAD, 7>(x, w, bias, y, alive, g, total_quads, cout, relu, s);
-		case 8: return launch_quad_rows<CG, PAD, 8>(x, w, bias, y, alive, g, total_quads, cout, relu, s);
+		case 1: return launch_quad_rows<CG, PAD, 1>(x, w, bias, y, alive, bits, g, total_quads, cout, relu, s);
+		case 2: return launch_quad_rows<CG, PAD, 2>(x, w, bias, y, alive, bits, g, total_quads, cout, relu, s);
+		case 3: return launch_quad_rows<CG, PAD, 3>(x, w, bias, y, alive, bits, g, total_quads, cout, relu, s);
+		case 4: return launch_quad_rows<CG, PAD, 4>(x, w, bias, y, alive, bits, g, total_quads, cout, relu, s);
+		case 5: return launch_quad_rows<CG, PAD, 5>(x, w, bias, y, alive, bits, g, total_quads, cout, relu, s);
+		case 6: return launch_quad_rows<CG, PAD, 6>(x, w, bias, y, alive, bits, g, total_quads, cout, relu, s);
+		case 7: return launch_quad_rows<CG, PAD, 7>(x, w, bias, y, alive, bits, g, total_quads, cout, relu, s);
+		case 8: return launch_quad_rows<CG, PAD, 8>(x, w, bias, y, alive, bits, g, total_quads, cout, relu, s);
 		default: return hipErrorInvalidValue;
 	}
 }
 
 template <int CG>
 hipError_t launch_same_quad(const float* x, const float* w, const float* bias, float* y, unsigned char* alive,
-                            const ConvGeom& g, int total_quads, int cout, int relu, hipStream_t s) {
+                            unsigned char* bits, const ConvGeom& g, int total_quads, int cout, int relu, hipStream_t s) {
 	switch (g.pad) {
-		case 0: return launch_quad_pad<CG, 0>(x, w, bias, y, alive, g, total_quads, cout, relu, s);
-		case 1: return launch_quad_pad<CG, 1>(x, w, bias, y, alive, g, total_quads, cout, relu, s);
-		case 2: return launch_quad_pad<CG, 2>(x, w, bias, y, alive, g, total_quads, cout, relu, s);
-		case 3: return launch_quad_pad<CG, 3>(x, w, bias, y, alive, g, total_quads, cout, relu, s);
-		case 4: return launch_quad_pad<CG, 4>(x, w, bias, y, alive, g, total_quads, cout, relu, s);
+		case 0: return launch_quad_pad<CG, 0>(x, w, bias, y, alive, bits, g, total_quads, cout, relu, s);
+		case 1: return launch_quad_pad<CG, 1>(x, w, bias, y, alive, bits, g, total_quads, cout, relu, s);
+		case 2: return launch_quad_pad<CG, 2>(x, w, bias, y, alive, bits, g, total_quads, cout, relu, s);
+		case 3: return launch_quad_pad<CG, 3>(x, w, bias, y, alive, bits, g, total_quads, cout, relu, s);
+		case 4: return launch_quad_pad<CG, 4>(x, w, bias, y, alive, bits, g, total_quads, cout, relu, s);
 		default: return hipErrorInvalidValue;
 	}
 }
@@ -499,12 +506,14 @@ bool conv_same_quad_ok(const float* x, const float* y, const unsigned char* aliv
 }
 
 hipError_t conv_same_quad(const float* x, const float* w, const float* bias, float* y, unsigned char* alive,
-                          const ConvGeom& g, int64_t samples, int cout, int relu, int cg, hipStream_t s) {
+                          const ConvGeom& g, int64_t samples, int cout, int relu, int cg, hipStream_t s,
+                          unsigned char* bits) {
 	const int total_quads = (int)(samples * g.ho * (int64_t)(g.wo / 4));
 	if (total_quads == 0 || cout == 0) return hipSuccess;
+	if (bits && (!relu || ((int64_t)g.ho * g.wo) % 8 != 0)) return hipErrorInvalidValue;
 	switch (cg) {
-		case 4: return launch_same_quad<4>(x, w, bias, y, alive, g, total_quads, cout, relu, s);
-		case 8: return launch_same_quad<8>(x, w, bias, y, alive, g, total_quads, cout, relu, s);
+		case 4: return launch_same_quad<4>(x, w, bias, y, alive, bits, g, total_quads, cout, relu, s);
+		case 8: return launch_same_quad<8>(x, w, bias, y, alive, bits, g, total_quads, cout, relu, s);
 		default: return hipErrorInvalidValue;
 	}
 }

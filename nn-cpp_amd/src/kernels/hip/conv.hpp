@@ -38,10 +38,15 @@ bool conv_same_quad_ok(const float* x, const float* y, const unsigned char* aliv
 // launch (alive and argmax may be null).
 bool conv_relu_pool2_ok(const float* x, const float* y, const unsigned char* alive, const float* pooled,
                         const uint32_t* argmax, const ConvGeom& g, int64_t samples);
+// bits / amax2 (both or neither, alive and argmax then null, W <= 256): the packed flags and window slots
+// (conv_pool.hip states the layouts).
 hipError_t conv_relu_pool2(const float* x, const float* w, const float* bias, float* y, unsigned char* alive,
-                           float* pooled, uint32_t* argmax, const ConvGeom& g, int64_t samples, int cout, hipStream_t s);
+                           float* pooled, uint32_t* argmax, const ConvGeom& g, int64_t samples, int cout, hipStream_t s,
+                           unsigned char* bits = nullptr, unsigned char* amax2 = nullptr);
+// bits: the ReLU's flags packed one bit per output in y's order (byte o / 8, bit o % 8; Ho Wo a multiple of 8).
 hipError_t conv_same_quad(const float* x, const float* w, const float* bias, float* y, unsigned char* alive,
-                          const ConvGeom& g, int64_t samples, int cout, int relu, int cg, hipStream_t s);
+                          const ConvGeom& g, int64_t samples, int cout, int relu, int cg, hipStream_t s,
+                          unsigned char* bits = nullptr);
 hipError_t mask_grad(const float* g, const unsigned char* alive, float* out, int64_t total, hipStream_t s);
 // mask_grad and lane_sums in one pass: out = alive ? g : 0 over rows x n, dst[row] = lane_sum of out's row.
 // dx of nn::conv2d's backward from the masked output gradient gm {samples, cout, Ho*Wo} (ops.cpp:1452-1455): the
@@ -57,15 +62,15 @@ hipError_t conv_dwp(const float* g, const unsigned char* alive, const float* x, 
 hipError_t conv_dx_fused(const float* gm, const unsigned char* alive, const float* w, float* dx, const ConvGeom& g,
                          int64_t samples, int cout, int first, hipStream_t s);
 // The whole backward of a first layer (conv_first.hip: K = Cin*kh*kw <= 16, Cout <= 32, stride 1, Ho*Wo a multiple
-// of 4 up to 65536, 16-byte aligned g and 4-byte aligned flags) in one launch of one-wave workgroups, two kinds per
-// sample: the per-sample bias sums gb {N, Cout} (may be null) and weight gradients gw {N, Cout, K} as conv_dwp
-// computes them (same bits), and dx on bands of rows (may be null; first: dx = 0 + taps, else dx += taps) as
-// conv_dx_fused computes it, each masking g as it reads it. Declines depth-cut products.
+// of 4 up to 65536, 16-byte aligned g, flags 4-byte aligned bytes or, alive_bits, one bit per output in y's order)
+// in one launch, a workgroup per sample: the per-sample bias sums gb {N, Cout} (may be null) and weight gradients
+// gw {N, Cout, K}, and dx (may be null; first: dx = 0 + taps, else dx += taps), g masked as it is read. Declines
+// depth-cut products.
 bool conv_first_bwd_ok(const ConvGeom& g, int64_t samples, int cout, bool dx, const float* gr,
-                       const unsigned char* alive);
+                       const unsigned char* alive, bool alive_bits = false);
 hipError_t conv_first_bwd(const float* g, const unsigned char* alive, const float* x, const float* w, float* gb,
                           float* gw, float* dx, int dx_first, const ConvGeom& geo, int64_t samples, int cout,
-                          hipStream_t s);
+                          hipStream_t s, bool alive_bits = false);
 hipError_t masked_lane_sums(const float* g, const unsigned char* alive, float* out, int64_t rows, int64_t n, float* dst,
                             hipStream_t s);
 hipError_t lane_sums(const float* src, int64_t rows, int64_t n, float* dst, hipStream_t s);

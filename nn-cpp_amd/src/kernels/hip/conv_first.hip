@@ -43,8 +43,9 @@ constexpr int kFbRing = 6;                 // chunks of gradient loads in flight
 constexpr int kFbMaxPlane = 2048;
 constexpr size_t kFbMaxLds = 160 * 1024;
 
-// flag layouts: none, or one 4-byte word per quad of positions
-constexpr int kAlNone = 0, kAlWord = 1;
+// flag layouts: none, one byte per position (a 4-byte word per quad of positions), or one bit per position (bit o of
+// the flattened output index at byte o / 8, bit o % 8: a quad's flags are one nibble)
+constexpr int kAlNone = 0, kAlWord = 1, kAlBits = 2;
 
 struct FbArgs {
 	const float* g;               // output gradient {N, Cout, hw}
@@ -91,7 +92,15 @@ __global__ void __launch_bounds__(kFbThreads) conv_first_bwd_kernel(const FbArgs
 				const int p = min(ch * kFbChunk + 4 * (qi & 15), hw - 4);
 				const int64_t at = (row0 + min(row, a.cout - 1)) * hw + p;
 				v[u] = *reinterpret_cast<const f32x4*>(a.g + at);
-				f[u] = AL != kAlNone ? *reinterpret_cast<const unsigned*>(a.alive + at) : 0x01010101u;
+				if (AL == kAlWord) {
+					f[u] = *reinterpret_cast<const unsigned*>(a.alive + at);
+				} else if (AL == kAlBits) {
+					// the quad's nibble spread to one flag byte per position
+					const unsigned nb = (unsigned)(a.alive[at >> 3] >> (at & 4)) & 0xfu;
+					f[u] = (nb & 1u) | ((nb & 2u) << 7) | ((nb & 4u) << 14) | ((nb & 8u) << 21);
+				} else {
+					f[u] = 0x01010101u;
+				}
 			}
 		};
 		// chunk ch into slot ch % 2: the masked gradient (rows past cout and positions past hw are zero) and the
@@ -331,7 +340,8 @@ FbLayout fb_layout(const ConvGeom& g, bool dx) {
 }  // namespace
 
 bool conv_first_bwd_ok(const ConvGeom& g, int64_t samples, int cout, bool dx, const float* gr,
-                       const unsigned char* alive) {
+                       const unsigned char* alive, bool alive_bits) {
+	if (alive_bits) alive = nullptr;  // bits take any alignment
 	const int64_t hw = (int64_t)g.ho * g.wo, K = (int64_t)g.cin * g.kh * g.kw;
 	if (cout < 1 || cout > kFbMaxCo || samples < 1 || samples > 0x7fffffff || hw < 1 || K < 1 || K > kFbMaxK)
 		return false;
@@ -348,8 +358,8 @@ bool conv_first_bwd_ok(const ConvGeom& g, int64_t samples, int cout, bool dx, co
 
 hipError_t conv_first_bwd(const float* g, const unsigned char* alive, const float* x, const float* w, float* gb,
                           float* gw, float* dx, int dx_first, const ConvGeom& geo, int64_t samples, int cout,
-                          hipStream_t s) {
-	if (!conv_first_bwd_ok(geo, samples, cout, dx != nullptr, g, alive)) return hipErrorInvalidValue;
+                          hipStream_t s, bool alive_bits) {
+	if (!conv_first_bwd_ok(geo, samples, cout, dx != nullptr, g, alive, alive_bits)) return hipErrorInvalidValue;
 	const FbLayout l = fb_layout(geo, dx != nullptr);
 	FbArgs a{};
 	a.g = g;
@@ -381,12 +391,14 @@ hipError_t conv_first_bwd(const float* g, const unsigned char* alive, const floa
 	a.wp_div = make_fastdiv((unsigned)a.wp);
 	a.w_div = make_fastdiv((unsigned)geo.w);
 	using Kern = void (*)(FbArgs);
-	static const Kern kerns[2][2][2] = {
-	    {{conv_first_bwd_kernel<9, 4, kAlNone>, conv_first_bwd_kernel<9, 4, kAlWord>},
-	     {conv_first_bwd_kernel<9, 8, kAlNone>, conv_first_bwd_kernel<9, 8, kAlWord>}},
-	    {{conv_first_bwd_kernel<16, 4, kAlNone>, conv_first_bwd_kernel<16, 4, kAlWord>},
-	     {conv_first_bwd_kernel<16, 8, kAlNone>, conv_first_bwd_kernel<16, 8, kAlWord>}}};
-	const Kern k = kerns[a.K > 9][cout > 16][alive != nullptr];
+	static const Kern kerns[2][2][3] = {
+	    {{conv_first_bwd_kernel<9, 4, kAlNone>, conv_first_bwd_kernel<9, 4, kAlWord>, conv_first_bwd_kernel<9, 4, kAlBits>},
+	     {conv_first_bwd_kernel<9, 8, kAlNone>, conv_first_bwd_kernel<9, 8, kAlWord>, conv_first_bwd_kernel<9, 8, kAlBits>}},
+	    {{conv_first_bwd_kernel<16, 4, kAlNone>, conv_first_bwd_kernel<16, 4, kAlWord>,
+	      conv_first_bwd_kernel<16, 4, kAlBits>},
+	     {conv_first_bwd_kernel<16, 8, kAlNone>, conv_first_bwd_kernel<16, 8, kAlWord>,
+	      conv_first_bwd_kernel<16, 8, kAlBits>}}};
+	const Kern k = kerns[a.K > 9][cout > 16][alive == nullptr ? 0 : alive_bits ? 2 : 1];
 	const size_t lds = l.floats * sizeof(float);
 	hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(k), hipFuncAttributeMaxDynamicSharedMemorySize,
 	                                   (int)lds);

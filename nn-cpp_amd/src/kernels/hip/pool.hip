@@ -194,7 +194,47 @@ __global__ void __launch_bounds__(256) maxpool2x2_backward_kernel(const PoolBwdA
 	}
 }
 
+// The same backward from 2-bit window positions (the packed form the fused conv2d_relu + 2 x 2 pool writes: window
+// (pr, wc) of plane p at bits 2 (wc % 4) of byte (p ho + pr) rb + wc / 4, rb = ceil(w / 8)): every element gets its
+// window's g when the window picked it (from 0 when first, else added to its old value); a window's maximum is
+// always one of its own four elements there, so no window keeps the plane's offset 0. A thread per window.
+__global__ void __launch_bounds__(256) maxpool2x2_backward_slots_kernel(const float* __restrict__ g,
+                                                                        const unsigned char* __restrict__ slots,
+                                                                        float* __restrict__ dx, int h, int w, int first,
+                                                                        FastDiv wo_div, FastDiv out_div, int64_t total) {
+	const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+	if (t >= total) return;
+	const int wo = (int)wo_div.d, out = (int)out_div.d;
+	const int64_t p = t / out;
+	const int i = (int)(t - p * out);
+	const int pr = (int)fdiv((unsigned)i, wo_div), wc = i - pr * wo;
+	const int rb = (w + 7) >> 3;
+	const unsigned sl = (slots[(p * (h >> 1) + pr) * rb + (wc >> 2)] >> (2 * (wc & 3))) & 3u;
+	const float gv = g[t];
+	float* d = dx + p * h * w + (int64_t)(2 * pr) * w + 2 * wc;
+	float2 r0 = first ? make_float2(0.0f, 0.0f) : *reinterpret_cast<const float2*>(d);
+	float2 r1 = first ? make_float2(0.0f, 0.0f) : *reinterpret_cast<const float2*>(d + w);
+	if (sl == 0) r0.x = r0.x + gv;
+	if (sl == 1) r0.y = r0.y + gv;
+	if (sl == 2) r1.x = r1.x + gv;
+	if (sl == 3) r1.y = r1.y + gv;
+	*reinterpret_cast<float2*>(d) = r0;
+	*reinterpret_cast<float2*>(d + w) = r1;
+}
+
 }  // namespace
+
+hipError_t maxpool2x2_backward_slots(const float* g, const unsigned char* slots, float* dx, int64_t planes, int h, int w,
+                                     int first, hipStream_t st) {
+	if (planes == 0 || h == 0 || w == 0) return hipSuccess;
+	if (h % 2 != 0 || w % 2 != 0 || reinterpret_cast<uintptr_t>(dx) % 8 != 0) return hipErrorInvalidValue;
+	const int ho = h / 2, wo = w / 2;
+	const int64_t total = planes * ho * wo;
+	if ((total + 255) / 256 > 0x7fffffff) return hipErrorInvalidConfiguration;
+	hipLaunchKernelGGL(maxpool2x2_backward_slots_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, g, slots,
+	                   dx, h, w, first, make_fastdiv((unsigned)wo), make_fastdiv((unsigned)(ho * wo)), total);
+	return hipGetLastError();
+}
 
 hipError_t maxpool2d_forward(const float* x, float* y, uint32_t* arg, int64_t planes, int h, int w, int k, int s,
                              hipStream_t st) {

@@ -13,5 +13,9 @@ hipError_t maxpool2d_forward(const float* x, float* y, uint32_t* arg, int64_t pl
 // dx (first: from 0, else added to) += g at each output's argmax, in output order (ops.cpp:1686-1704).
 hipError_t maxpool2d_backward(const float* g, const uint32_t* arg, float* dx, int64_t planes, int h, int w, int k, int s,
                               int first, hipStream_t st);
+// Its 2 x 2, stride 2 form from 2-bit window positions (the fused conv2d_relu + pool's packed output; h and w even,
+// dx 8-byte aligned).
+hipError_t maxpool2x2_backward_slots(const float* g, const unsigned char* slots, float* dx, int64_t planes, int h, int w,
+                                     int first, hipStream_t st);
 
 }  // namespace nnh

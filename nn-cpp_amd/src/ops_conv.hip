@@ -86,11 +86,20 @@ struct BwdPlan {
 	bool dx_fused = false;
 };
 
-BwdPlan conv_backward_plan(const ConvGeom& geo, size_t N, size_t Cout, bool alive, bool dx, bool dw, bool db) {
+// packed: the flags are bits and the first-layer kernel runs the whole backward (it writes the per-sample weight
+// gradients even when dW is not asked for, and needs no masked copy).
+BwdPlan conv_backward_plan(const ConvGeom& geo, size_t N, size_t Cout, bool alive, bool dx, bool dw, bool db,
+                           bool packed = false) {
 	BwdPlan p;
 	const size_t hw = (size_t)geo.ho * geo.wo, K = (size_t)geo.cin * geo.kh * geo.kw;
 	if (N == 0 || (!dx && !dw && !db)) return p;
 	WorkspacePlan plan;
+	if (packed) {
+		p.off_gb = db ? plan.add(N * Cout * 4) : 0;
+		p.off_gw = plan.add(N * Cout * K * 4);
+		p.total = plan.total;
+		return p;
+	}
 	p.off_m = alive ? plan.add(N * Cout * hw * 4) : 0;
 	p.off_gb = db ? plan.add(N * Cout * 4) : 0;
 	p.off_gw = dw ? plan.add(N * Cout * K * 4) : 0;
@@ -111,9 +120,34 @@ size_t conv_forward_ws(const ConvGeom& g, size_t N, size_t Cout) {
 	return gemm_workspace_bytes(Cout, hw, K, N, true);
 }
 
+// Whether the packed flag (and pooling-offset) forms take a geometry: the forward's quad kernel (or, with the 2 x 2
+// pool, the fused kernel) writes them and the first-layer backward kernel reads them.
+bool packed_geometry(const ConvGeom& g, size_t N, size_t Cout, bool pool) {
+	const int64_t hw = (int64_t)g.ho * g.wo;
+	if (N == 0 || Cout == 0 || hw == 0) return false;
+	const bool fwd = pool ? conv_relu_pool2_ok(nullptr, nullptr, nullptr, nullptr, nullptr, g, (int64_t)N) && g.w <= 256
+	                      : conv_same_quad_ok(nullptr, nullptr, nullptr, g, (int64_t)N) && hw % 8 == 0 &&
+	                            (size_t)g.cin * g.kh * g.kw <= kDirectMaxK;
+	return fwd && conv_first_bwd_ok(g, (int64_t)N, (int)Cout, true, nullptr, nullptr, true);
+}
+
+int conv_backward_impl(const float* g, const float* x, const float* w, const unsigned char* alive, bool packed, size_t N,
+                       size_t Cin, size_t H, size_t W, size_t Cout, size_t kh, size_t kw, int stride, int padding,
+                       float* dx, int dx_first, float* dw, int dw_first, float* db, int db_first, void* stream);
+
 }  // namespace
 
 extern "C" {
+
+int nnh_conv2d_packed_supported(size_t N, size_t Cin, size_t H, size_t W, size_t Cout, size_t kh, size_t kw, int stride,
+                                int padding, int with_pool) {
+	ConvGeom g;
+	const std::string saved = g_last_error;
+	const bool ok = conv_geometry(N, Cin, H, W, Cout, kh, kw, stride, padding, g) == NNH_OK &&
+	                packed_geometry(g, N, Cout, with_pool != 0);
+	g_last_error = saved;
+	return ok ? 1 : 0;
+}
 
 int nnh_conv2d_forward_workspace_size(size_t N, size_t Cin, size_t H, size_t W, size_t Cout, size_t kh, size_t kw,
                                       int stride, int padding, size_t* bytes) {
@@ -132,7 +166,11 @@ int nnh_conv2d_backward_workspace_size(size_t N, size_t Cin, size_t H, size_t W,
 		ConvGeom g;
 		const int rc = conv_geometry(N, Cin, H, W, Cout, kh, kw, stride, padding, g);
 		if (rc != NNH_OK) return rc;
-		return put_bytes(bytes, conv_backward_plan(g, N, Cout, with_alive, want_dx, want_dw, want_db).total);
+		size_t total = conv_backward_plan(g, N, Cout, with_alive, want_dx, want_dw, want_db).total;
+		// with flags: also enough for nnh_conv2d_backward_packed where that takes the geometry
+		if (with_alive && packed_geometry(g, N, Cout, false))
+			total = std::max(total, conv_backward_plan(g, N, Cout, true, want_dx, want_dw, want_db, true).total);
+		return put_bytes(bytes, total);
 	});
 }
 
@@ -203,6 +241,74 @@ int nnh_conv2d_relu_maxpool2d_forward(const float* x, size_t N, size_t Cin, size
 int nnh_conv2d_backward(const float* g, const float* x, const float* w, const unsigned char* alive, size_t N,
                         size_t Cin, size_t H, size_t W, size_t Cout, size_t kh, size_t kw, int stride, int padding,
                         float* dx, int dx_first, float* dw, int dw_first, float* db, int db_first, void* stream) {
+	return conv_backward_impl(g, x, w, alive, false, N, Cin, H, W, Cout, kh, kw, stride, padding, dx, dx_first, dw,
+	                          dw_first, db, db_first, stream);
+}
+
+int nnh_conv2d_backward_packed(const float* g, const float* x, const float* w, const unsigned char* alive_bits,
+                               size_t N, size_t Cin, size_t H, size_t W, size_t Cout, size_t kh, size_t kw, int stride,
+                               int padding, float* dx, int dx_first, float* dw, int dw_first, float* db, int db_first,
+                               void* stream) {
+	if (N > 0 && (dx || dw || db) && !alive_bits) return fail(NNH_ERR_INVALID, "conv2d backward: null alive bits");
+	return conv_backward_impl(g, x, w, alive_bits, true, N, Cin, H, W, Cout, kh, kw, stride, padding, dx, dx_first, dw,
+	                          dw_first, db, db_first, stream);
+}
+
+int nnh_conv2d_relu_forward_packed(const float* x, size_t N, size_t Cin, size_t H, size_t W, const float* w,
+                                   size_t Cout, size_t kh, size_t kw, const float* bias, int stride, int padding,
+                                   float* y, unsigned char* alive_bits, void* stream) {
+	NumericsScope numerics_scope(stream);
+	ConvGeom g;
+	int rc = conv_geometry(N, Cin, H, W, Cout, kh, kw, stride, padding, g);
+	if (rc != NNH_OK) return rc;
+	const size_t hw = (size_t)g.ho * g.wo;
+	if (N == 0 || Cout == 0 || hw == 0) return NNH_OK;
+	if (!x || !w || !bias || !y || !alive_bits) return fail(NNH_ERR_INVALID, "conv2d_relu packed: null pointer");
+	if (!packed_geometry(g, N, Cout, false) || !conv_same_quad_ok(x, y, nullptr, g, (int64_t)N))
+		return fail(NNH_ERR_INVALID, "conv2d_relu packed: geometry or alignment not taken (nnh_conv2d_packed_supported, "
+		                             "16-byte aligned x and y)");
+	const uint64_t xb = (uint64_t)N * Cin * H * W * 4, yb = (uint64_t)N * Cout * hw * 4, bb = yb / 32;
+	if (ranges_overlap(y, yb, x, xb) || ranges_overlap(alive_bits, bb, x, xb) || ranges_overlap(alive_bits, bb, y, yb))
+		return fail(NNH_ERR_ALIAS, "conv2d_relu packed: outputs overlap each other or the input");
+	return hip_status(conv_same_quad(x, w, bias, y, nullptr, g, (int64_t)N, (int)Cout, 1, 4,
+	                                 reinterpret_cast<hipStream_t>(stream), alive_bits),
+	                  "conv2d_relu packed");
+}
+
+int nnh_conv2d_relu_maxpool2d_forward_packed(const float* x, size_t N, size_t Cin, size_t H, size_t W, const float* w,
+                                             size_t Cout, size_t kh, size_t kw, const float* bias, int stride,
+                                             int padding, float* y, unsigned char* alive_bits, float* pooled,
+                                             unsigned char* argmax2, void* stream) {
+	NumericsScope numerics_scope(stream);
+	ConvGeom g;
+	int rc = conv_geometry(N, Cin, H, W, Cout, kh, kw, stride, padding, g);
+	if (rc != NNH_OK) return rc;
+	const size_t hw = (size_t)g.ho * g.wo;
+	if (N == 0 || Cout == 0 || hw == 0) return NNH_OK;
+	if (!x || !w || !bias || !y || !alive_bits || !pooled || !argmax2)
+		return fail(NNH_ERR_INVALID, "conv2d_relu_maxpool2d packed: null pointer");
+	if (!packed_geometry(g, N, Cout, true) || !conv_relu_pool2_ok(x, y, nullptr, pooled, nullptr, g, (int64_t)N))
+		return fail(NNH_ERR_INVALID, "conv2d_relu_maxpool2d packed: geometry or alignment not taken "
+		                             "(nnh_conv2d_packed_supported, 16-byte aligned x and y, 8-byte aligned pooled)");
+	const uint64_t xb = (uint64_t)N * Cin * H * W * 4, yb = (uint64_t)N * Cout * hw * 4, bb = yb / 32;
+	const uint64_t pb = yb / 4, ab = (uint64_t)N * Cout * (g.h / 2) * ((g.w + 7) / 8);
+	if (ranges_overlap(y, yb, x, xb) || ranges_overlap(pooled, pb, x, xb) || ranges_overlap(pooled, pb, y, yb) ||
+	    ranges_overlap(argmax2, ab, x, xb) || ranges_overlap(argmax2, ab, y, yb) || ranges_overlap(argmax2, ab, pooled, pb) ||
+	    ranges_overlap(alive_bits, bb, pooled, pb) || ranges_overlap(alive_bits, bb, argmax2, ab) ||
+	    ranges_overlap(alive_bits, bb, y, yb) || ranges_overlap(alive_bits, bb, x, xb))
+		return fail(NNH_ERR_ALIAS, "conv2d_relu_maxpool2d packed: outputs overlap each other or the input");
+	return hip_status(conv_relu_pool2(x, w, bias, y, nullptr, pooled, nullptr, g, (int64_t)N, (int)Cout,
+	                                  reinterpret_cast<hipStream_t>(stream), alive_bits, argmax2),
+	                  "conv2d_relu_maxpool2d packed");
+}
+
+}  // extern "C"
+
+namespace {
+
+int conv_backward_impl(const float* g, const float* x, const float* w, const unsigned char* alive, bool packed, size_t N,
+                       size_t Cin, size_t H, size_t W, size_t Cout, size_t kh, size_t kw, int stride, int padding,
+                       float* dx, int dx_first, float* dw, int dw_first, float* db, int db_first, void* stream) {
 	NumericsScope numerics_scope(stream);
 	ConvGeom geo;
 	int rc = conv_geometry(N, Cin, H, W, Cout, kh, kw, stride, padding, geo);
@@ -219,7 +325,7 @@ int nnh_conv2d_backward(const float* g, const float* x, const float* w, const un
 	if (!g || !x || !w) return fail(NNH_ERR_INVALID, "conv2d backward: null pointer");
 	{
 		const uint64_t gb_ = (uint64_t)N * Cout * hw * 4, xb = (uint64_t)N * Cin * H * W * 4, wb = (uint64_t)Cout * K * 4;
-		const uint64_t ab = gb_ / 4;
+		const uint64_t ab = packed ? gb_ / 32 : gb_ / 4;
 		const void* ins[4] = {g, x, w, alive};
 		const uint64_t in_bytes[4] = {gb_, xb, wb, ab};
 		const void* outs[3] = {dx, dw, db};
@@ -233,7 +339,12 @@ int nnh_conv2d_backward(const float* g, const float* x, const float* w, const un
 					return fail(NNH_ERR_ALIAS, "conv2d backward: gradients overlap each other");
 		}
 	}
-	const BwdPlan plan = conv_backward_plan(geo, N, Cout, alive != nullptr, dx != nullptr, dw != nullptr, db != nullptr);
+	// packed flags: the first-layer kernel reads them (nnh_conv2d_packed_supported's backward half; g 16-byte aligned)
+	if (packed && !conv_first_bwd_ok(geo, (int64_t)N, (int)Cout, dx != nullptr, g, nullptr, true))
+		return fail(NNH_ERR_INVALID, "conv2d backward packed: geometry or alignment not taken "
+		                             "(nnh_conv2d_packed_supported, 16-byte aligned g)");
+	const BwdPlan plan =
+	    conv_backward_plan(geo, N, Cout, alive != nullptr, dx != nullptr, dw != nullptr, db != nullptr, packed);
 	rc = check_workspace(stream, plan.total);
 	if (rc != NNH_OK) return rc;
 	const bool dx_fused = plan.dx_fused;
@@ -242,20 +353,21 @@ int nnh_conv2d_backward(const float* g, const float* x, const float* w, const un
 	float* partials = plan.part ? ws.at<float>(plan.off_part) : nullptr;
 	float* m = alive ? ws.at<float>(plan.off_m) : nullptr;
 	float* gb = db ? ws.at<float>(plan.off_gb) : nullptr;
-	float* gw = dw ? ws.at<float>(plan.off_gw) : nullptr;
+	float* gw = dw || packed ? ws.at<float>(plan.off_gw) : nullptr;
 	const float* gm = alive ? m : g;
 	// 3x3, stride 1, padding 1 on small planes: one kernel takes the mask (ops.cpp:1439-1443), the per-sample bias
 	// sums (1445) and the per-sample weight gradients (1448-1449) with its operands in LDS
-	const bool dw3 = dw && conv_dw3_ok(geo, (int64_t)N, (int)Cout, g, alive, m);
+	const bool dw3 = !packed && dw && conv_dw3_ok(geo, (int64_t)N, (int)Cout, g, alive, m);
 	// short column depth (a first layer): db and dW per sample from LDS, the mask applied as g is staged; the dx
 	// kernel then masks g itself, so the masked gradient is never written
-	// a first layer's whole backward (K <= 16, Cout <= 32) in one workgroup per sample
-	const bool first = dw && !dw3 && conv_first_bwd_ok(geo, (int64_t)N, (int)Cout, dx != nullptr, g, alive);
+	// a first layer's whole backward (K <= 16, Cout <= 32) in one workgroup per sample (always with packed flags)
+	const bool first =
+	    packed || (dw && !dw3 && conv_first_bwd_ok(geo, (int64_t)N, (int)Cout, dx != nullptr, g, alive));
 	const bool dwp = dw && !dw3 && !first && (!dx || dx_fused) && conv_dwp_ok(geo, (int64_t)N, (int)Cout);
 	if (dw3) {
 		rc = hip_status(conv_dw3(g, alive, m, gb, x, gw, geo, (int64_t)N, (int)Cout, s), "conv2d mask, db, dw 3x3");
 	} else if (first) {
-		rc = hip_status(conv_first_bwd(g, alive, x, w, gb, gw, dx, dx_first ? 1 : 0, geo, (int64_t)N, (int)Cout, s),
+		rc = hip_status(conv_first_bwd(g, alive, x, w, gb, gw, dx, dx_first ? 1 : 0, geo, (int64_t)N, (int)Cout, s, packed),
 		                "conv2d db, dw, dx");
 	} else if (dwp) {
 		rc = hip_status(conv_dwp(g, alive, x, gb, gw, geo, (int64_t)N, (int)Cout, s), "conv2d db, dw");
@@ -307,6 +419,10 @@ int nnh_conv2d_backward(const float* g, const float* x, const float* w, const un
 	}
 	return rc;
 }
+
+}  // namespace
+
+extern "C" {
 
 int nnh_im2col(const float* x, size_t N, size_t Cin, size_t H, size_t W, size_t kh, size_t kw, int stride, int padding,
                float* col, void* stream) {

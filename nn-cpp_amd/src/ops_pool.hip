@@ -63,4 +63,24 @@ int nnh_maxpool2d_backward(const float* g, const unsigned int* argmax, size_t N,
 	                  "maxpool2d backward");
 }
 
+int nnh_maxpool2d_backward_packed(const float* g, const unsigned char* argmax2, size_t N, size_t C, size_t H, size_t W,
+                                  float* dx, int first, void* stream) {
+	if (!count_ok({N, C, H, W})) return fail(NNH_ERR_INVALID, "maxpool2d backward packed: size out of range");
+	size_t ho = 0, wo = 0;
+	int rc = maxpool_geometry(H, W, 2, 2, ho, wo);
+	if (rc != NNH_OK) return rc;
+	const size_t planes = N * C;
+	if (planes == 0) return NNH_OK;
+	if (!g || !argmax2 || !dx) return fail(NNH_ERR_INVALID, "maxpool2d backward packed: null pointer");
+	if (H % 2 != 0 || W % 2 != 0 || reinterpret_cast<uintptr_t>(dx) % 8 != 0)
+		return fail(NNH_ERR_INVALID, "maxpool2d backward packed: H and W must be even and dx 8-byte aligned");
+	const uint64_t xb = (uint64_t)planes * H * W * 4, yb = (uint64_t)planes * ho * wo * 4;
+	const uint64_t ab = (uint64_t)planes * (H / 2) * ((W + 7) / 8);
+	if (ranges_overlap(dx, xb, g, yb) || ranges_overlap(dx, xb, argmax2, ab))
+		return fail(NNH_ERR_ALIAS, "maxpool2d backward packed: dx overlaps g or argmax2");
+	return hip_status(maxpool2x2_backward_slots(g, argmax2, dx, (int64_t)planes, (int)H, (int)W, first ? 1 : 0,
+	                                            reinterpret_cast<hipStream_t>(stream)),
+	                  "maxpool2d backward packed");
+}
+
 }  // extern "C"

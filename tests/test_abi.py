@@ -68,6 +68,24 @@ def test_add_to_grad2_refuses_overlapping_gradients():
     assert f(None, 1, None, 1, None, 0, None) == nnh.OK
 
 
+def test_packed_flag_geometries_on_the_host():
+    """nnh_conv2d_packed_supported (no device needed): a first layer's geometry takes the packed flags; stride,
+    depth, channel count, plane size and (with the pool) odd heights or rows wider than 256 do not."""
+    ok = lambda xs, ws, s=1, p=1, pool=False: nnh.conv2d_packed_supported(xs, ws, s, p, pool)
+    assert ok((128, 1, 28, 28), (32, 1, 3, 3)) and ok((128, 1, 28, 28), (32, 1, 3, 3), pool=True)
+    assert ok((2, 1, 4, 256), (2, 1, 3, 3), pool=True)
+    assert not ok((2, 1, 4, 264), (2, 1, 3, 3), pool=True)      # a row wider than 256
+    assert not ok((2, 1, 9, 8), (4, 1, 3, 3), pool=True)        # an odd height
+    assert not ok((2, 1, 28, 28), (32, 1, 3, 3), s=2)           # stride 2
+    assert not ok((2, 2, 28, 28), (32, 2, 3, 3))                # Cin kh kw = 18 > 16
+    assert not ok((2, 1, 28, 28), (33, 1, 3, 3))                # Cout 33
+    assert not ok((2, 1, 6, 6), (4, 1, 3, 3))                   # 36 outputs per plane (not a multiple of 8)
+    assert not ok((2, 1, 48, 48), (4, 1, 3, 3))                 # a padded plane of 2500 floats
+    assert not ok((0, 1, 28, 28), (32, 1, 3, 3))                # no samples
+    L = nnh.lib()
+    assert L.nnh_conv2d_packed_supported(1, 1, 28, 28, 32, 3, 3, 1, 1, 0) == 1
+
+
 def test_empty_products_touch_nothing_and_need_no_device():
     """m == 0 or n == 0 returns before any device work (gemm.cpp:344); null pointers are then fine."""
     assert _sgemm(0, 0, 0, 5, 4, None, 4, None, 5, None, 5, 0, None) == nnh.OK

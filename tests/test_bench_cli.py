@@ -25,6 +25,7 @@ def bench():
 # every row key bench.py's default run produces (build_rows, then build_rows(split=True))
 ROW_KEYS = ["matmul512_nn", "matmul512_tn", "matmul512_nt", "mlp_forward", "mlp_backward", "conv1_forward",
             "conv1_forward_no_alive", "conv1_backward", "pool1_forward", "conv1_pool1_forward", "pool1_backward",
+            "conv1_forward_packed", "conv1_pool1_forward_packed", "conv1_backward_packed", "pool1_backward_packed",
             "conv2_forward", "conv2_backward", "attention_forward", "attention_backward", "attention_forward_causal",
             "attention_backward_causal", "matmul_1024x1024x1024", "matmul_2048x2048x2048", "matmul_4096x4096x4096",
             "matmul_8192x8192x8192", "matmul_64x4096x4096", "matmul_4096x4096x64"]
@@ -91,7 +92,9 @@ def test_stdout_line_fits_and_carries_the_contract(bench):
     assert line["roofline"]["traffic"] == 604138031.0
     assert set(line["roofline"]) >= {"bound", "achieved", "peak", "unit", "frac", "traffic"}
     assert set(line["cpu_baseline"]) >= {"value", "unit", "cores", "kind", "sample"}
-    assert list(line["configs"]) == ROW_KEYS
+    # the packed-flag rows travel as their time and check in fused_op
+    assert list(line["configs"]) == [k for k in ROW_KEYS if not k.endswith("_packed")]
+    assert list(line["fused_op"]["packed_us"]) == ["fwd", "fwd_pool", "bwd", "pool_bwd", "bitwise"]
     assert list(line["configs_split_depth"]) == SPLIT_KEYS
     for r in line["configs"].values():
         assert set(r) >= {"ms", "frac", "cpu_ms", "bitwise"}
