@@ -317,6 +317,23 @@ hipError_t gemm_launch(const GemmCall& g, hipStream_t s, int config, float* work
 
 hipError_t gemm_launch_pair(const GemmCall& g0, const GemmCall& g1, hipStream_t s, bool& launched) {
 	launched = false;
+	// a whole-depth A B on the chain kernel beside a cut A^T B (with or without two-stage row sums) on the pieces
+	// kernel: the kernels their own launches take, in one grid
+	if (chain_pieces_pair_takes(g0, g1)) {
+		hipError_t e = prepare_device();
+		if (e != hipSuccess) return e;
+		e = gemm_chain_pieces_pair_launch(g0, g1, s);
+		launched = e == hipSuccess;
+		return e;
+	}
+	// two products that each run on the chain kernel (a matmul's dA = G B or G B^T and dB = A^T G or G^T A)
+	if (chain4_pair_takes(g0, g1)) {
+		hipError_t e = prepare_device();
+		if (e != hipSuccess) return e;
+		e = gemm_chain4_pair_launch(g0, g1, s);
+		launched = e == hipSuccess;
+		return e;
+	}
 	// g0 = A B and g1 = A^T B (row sums allowed), single matrices, no depth cut, both on one configuration that
 	// has the pair kernels
 	if (g0.ta || g0.tb || g0.gather || g0.rowsum || !g1.ta || g1.tb || g1.gather || g1.rowsum_outer > 0) return hipSuccess;

@@ -89,7 +89,20 @@ bool pieces4_takes(const GemmCall& g);
 bool chain4_ok(const GemmCall& g);
 bool chain4_takes(const GemmCall& g);  // the shapes it is routed for (measured)
 hipError_t gemm_chain4_launch(const GemmCall& g, hipStream_t s);
+bool chain4_vec(const GemmCall& g);       // 16-byte loads of its k-contiguous operands
+GemmArgs chain4_args(const GemmCall& g);  // the chain kernel's arguments (32 x 32 tiles)
 hipError_t gemm_pieces4_launch(const GemmCall& g, hipStream_t s);
+// A B on the chain kernel and A^T B (row sums allowed) on the pieces kernel in one launch (gemm_pieces.hip): single
+// matrices, each taken by its own kernel's route (chain4_takes, a depth cut and pieces4_takes) and at most
+// 768 threads for the pieces' workgroup. The caller guarantees that neither product writes what the other reads or
+// writes.
+bool chain_pieces_pair_takes(const GemmCall& g0, const GemmCall& g1);
+// Two whole-depth products on the chain kernel in one launch (gemm_chain.hip): g0 = A B or A B^T and g1 = A^T B,
+// each one the chain kernel's own route takes (chain4_takes). The caller guarantees that neither product writes what
+// the other reads or writes.
+bool chain4_pair_takes(const GemmCall& g0, const GemmCall& g1);
+hipError_t gemm_chain4_pair_launch(const GemmCall& g0, const GemmCall& g1, hipStream_t s);
+hipError_t gemm_chain_pieces_pair_launch(const GemmCall& g0, const GemmCall& g1, hipStream_t s);
 
 // Floats of workspace a call needs: the partial sums of a depth cut the pieces kernel does not take, else 0. The
 // shape-only overload (plans and workspace queries) assumes leading dimensions below 2^24, which every op's own

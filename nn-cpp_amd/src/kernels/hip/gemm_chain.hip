@@ -19,116 +19,26 @@ namespace nnh {
 
 namespace {
 
-constexpr int kChunkGroups = 8;  // 128 depth indices
-
 template <bool TA, bool TB, bool VEC>
 __global__ void __launch_bounds__(256) sgemm_chain4_kernel(const GemmArgs p) {
-	constexpr bool KA = VEC && !TA, KB = VEC && TB;
-	const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-	const int tiles = p.tiles_m * p.tiles_n;
-	const int lid = xcd_remap((int)blockIdx.x, tiles * p.batch_count);
-	const int t = lid % tiles, bi = lid / tiles;
-	const int m0 = (t / p.tiles_n) * 32 + 16 * (wave >> 1), n0 = (t % p.tiles_n) * 32 + 16 * (wave & 1);
-	int64_t oa = 0, ob = 0, oc = 0;
-	if (p.batch.ndim > 0) batch_offsets(p.batch, bi, oa, ob, oc);
-	const float* __restrict__ A = p.a + oa;
-	const float* __restrict__ B = p.b + ob;
-	float* __restrict__ Cp = p.c + oc;
-	const int lda = (int)p.lda, ldb = (int)p.ldb;
-	const int r = lane & 15, j = lane >> 4;
-	const bool row_in = m0 + r < p.m, col_in = n0 + r < p.n;
-	const int K = p.k;
-	// the wave's LDS slots for its k-contiguous operands (two groups each)
-	__shared__ __align__(16) float kst[(KA || KB) ? 4 * 2 * 2 * kKSlot : 1];
-	float* const la = kst + (KA || KB ? wave * 4 * kKSlot : 0);
-	float* const lb = la + 2 * kKSlot;
-	f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-	// register e of lane l holds row 4 (l / 16) + e, column l % 16 of the quarter
-	const int col = n0 + r;
-	auto add_old = [&]() {
-#pragma unroll
-		for (int e = 0; e < 4; ++e) {
-			const int row = m0 + 4 * j + e;
-			if (row < p.m && col < p.n) acc[e] = Cp[(int64_t)row * p.ldc + col] + acc[e];
-		}
-	};
-	using G4 = std::integral_constant<int, 4>;
-	using G2 = std::integral_constant<int, 2>;
-	using G1 = std::integral_constant<int, 1>;
-	auto load8 = [&](int kc, f32x4 (&a)[kChunkGroups], f32x4 (&b)[kChunkGroups]) {
-		load_groups<TA, TB, KA, KB, false, kChunkGroups>(A, lda, B, ldb, m0, n0, kc, K - kc, r, j, row_in, col_in, a, b);
-	};
-	auto run8 = [&](f32x4 (&a)[kChunkGroups], f32x4 (&b)[kChunkGroups]) {
-		mma_groups<KA, KB, false, kChunkGroups>(a, b, 0, r, j, acc, la, lb);
-	};
-	// whole chunks, two register sets: chunk c + 1's loads in flight while chunk c's MFMAs run
-	const int n128 = K / 128;
-	const bool acc_mid = p.accumulate && K > kAccAfter;  // then n128 >= 2: old C joins after chunk 1
-	f32x4 a0[kChunkGroups], b0[kChunkGroups], a1[kChunkGroups], b1[kChunkGroups];
-	if (n128 > 0) load8(0, a0, b0);
-	int c = 0;
-	for (; c + 2 <= n128; c += 2) {
-		load8(128 * (c + 1), a1, b1);
-		__builtin_amdgcn_sched_barrier(0);
-		run8(a0, b0);
-		__builtin_amdgcn_sched_barrier(0);
-		// unconditional (the last pair reloads its second chunk, unused): no branch, so the waits stay counted
-		load8(128 * min(c + 2, n128 - 1), a0, b0);
-		__builtin_amdgcn_sched_barrier(0);
-		run8(a1, b1);
-		__builtin_amdgcn_sched_barrier(0);
-		if (c == 0 && acc_mid) add_old();
-	}
-	if (c < n128) run8(a0, b0);
-	// the rest of the depth: 64, 32, 16 indices, then fewer than 16
-	int kc = 128 * n128;
-	auto part = [&](auto groups_tag, auto part_tag) {
-		constexpr int G = decltype(groups_tag)::value;
-		constexpr bool PART = decltype(part_tag)::value;
-		f32x4 a[G], b[G];
-		load_groups<TA, TB, KA && !PART, KB && !PART, PART, G>(A, lda, B, ldb, m0, n0, kc, K - kc, r, j, row_in, col_in,
-		                                                       a, b);
-		__builtin_amdgcn_sched_barrier(0);
-		mma_groups<KA && !PART, KB && !PART, PART, G>(a, b, K - kc, r, j, acc, la, lb);
-		__builtin_amdgcn_sched_barrier(0);
-	};
-	if (K - kc >= 64) {
-		part(G4{}, std::false_type{});
-		kc += 64;
-	}
-	if (K - kc >= 32) {
-		part(G2{}, std::false_type{});
-		kc += 32;
-	}
-	if (K - kc >= 16) {
-		part(G1{}, std::false_type{});
-		kc += 16;
-	}
-	if (kc < K) part(G1{}, std::true_type{});
-	// the store (gemm.cpp:176-187, 245-252) and the op's bias and ReLU (src/autograd/ops.cpp:726-730, 1396-1409)
-	const bool add_old_at_end = p.accumulate && K <= kAccAfter;
-	unsigned char* alive = p.ep.alive ? p.ep.alive + oc : nullptr;
-#pragma unroll
-	for (int e = 0; e < 4; ++e) {
-		const int row = m0 + 4 * j + e;
-		if (row >= p.m || col >= p.n) continue;
-		const int64_t off = (int64_t)row * p.ldc + col;
-		float v = acc[e];
-		if (add_old_at_end) v = K > 0 ? Cp[off] + v : Cp[off];
-		if (p.ep.bias_mode == kBiasCol) v = v + p.ep.bias[col];
-		else if (p.ep.bias_mode == kBiasRow) v = v + p.ep.bias[row];
-		if (p.ep.relu) {
-			const bool on = v > 0.0f;
-			if (alive) alive[off] = on ? 1 : 0;
-			v = on ? v : 0.0f;
-		}
-		Cp[off] = v;
-	}
+	chain4_tile<TA, TB, VEC>(p, (int)blockIdx.x, __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6),
+	                         (int)threadIdx.x & 63);
+}
+
+// Two whole-depth products in one launch (a matmul's two operand gradients): workgroups below blocks0 take the first
+// product's tiles, the others the second's, each with the chains of its own launch.
+template <bool TA0, bool TB0, bool VEC0, bool TA1, bool TB1, bool VEC1>
+__global__ void __launch_bounds__(256) sgemm_chain4_pair_kernel(const GemmArgs p0, const GemmArgs p1, int blocks0) {
+	const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6), lane = (int)threadIdx.x & 63;
+	if ((int)blockIdx.x < blocks0) chain4_tile<TA0, TB0, VEC0>(p0, (int)blockIdx.x, wave, lane);
+	else chain4_tile<TA1, TB1, VEC1>(p1, (int)blockIdx.x - blocks0, wave, lane);
 }
 
 using ChainFn = void (*)(const GemmArgs);
 
 constexpr int64_t kMaxLd = int64_t(1) << 24;
+
+}  // namespace
 
 bool chain4_vec(const GemmCall& g) {
 	bool vec = true;
@@ -142,8 +52,6 @@ bool chain4_vec(const GemmCall& g) {
 	}
 	return vec;
 }
-
-}  // namespace
 
 bool chain4_ok(const GemmCall& g) {
 	return !g.gather && !g.rowsum && g.k > 0 && !depth_cut(g.m, g.n, g.k) && g.m < kMaxLd && g.n < kMaxLd &&
@@ -171,6 +79,15 @@ hipError_t gemm_chain4_launch(const GemmCall& g, hipStream_t s) {
 	    {sgemm_chain4_kernel<false, false, true>, sgemm_chain4_kernel<false, true, true>,
 	     sgemm_chain4_kernel<true, false, true>, sgemm_chain4_kernel<true, true, true>}};
 	if (!chain4_ok(g)) return hipErrorInvalidValue;
+	const GemmArgs p = chain4_args(g);
+	const int64_t blocks = (int64_t)p.tiles_m * p.tiles_n * p.batch_count;
+	if (blocks > 0x7fffffff) return hipErrorInvalidConfiguration;
+	const int f = (g.ta ? 2 : 0) + (g.tb ? 1 : 0);
+	hipLaunchKernelGGL(fns[chain4_vec(g) ? 1 : 0][f], dim3((unsigned)blocks), dim3(256), 0, s, p);
+	return hipGetLastError();
+}
+
+GemmArgs chain4_args(const GemmCall& g) {
 	GemmArgs p{};
 	p.a = g.a;
 	p.b = g.b;
@@ -189,10 +106,30 @@ hipError_t gemm_chain4_launch(const GemmCall& g, hipStream_t s) {
 	p.ep = g.ep;
 	p.pieces = 1;
 	p.piece_k = (int)g.k;
-	const int64_t blocks = (int64_t)p.tiles_m * p.tiles_n * p.batch_count;
-	if (blocks > 0x7fffffff) return hipErrorInvalidConfiguration;
-	const int f = (g.ta ? 2 : 0) + (g.tb ? 1 : 0);
-	hipLaunchKernelGGL(fns[chain4_vec(g) ? 1 : 0][f], dim3((unsigned)blocks), dim3(256), 0, s, p);
+	return p;
+}
+
+bool chain4_pair_takes(const GemmCall& g0, const GemmCall& g1) {
+	// the layouts of a matmul's gradients: dA = G B (NN) or G B^T (NT) beside dB = A^T G or G^T A (TN)
+	if (g0.ta || !g1.ta || g1.tb || !chain4_takes(g0) || !chain4_takes(g1)) return false;
+	const int64_t b0 = ((g0.m + 31) / 32) * ((g0.n + 31) / 32) * g0.batch_count;
+	const int64_t b1 = ((g1.m + 31) / 32) * ((g1.n + 31) / 32) * g1.batch_count;
+	return b0 > 0 && b1 > 0 && b0 + b1 <= 0x7fffffff;
+}
+
+hipError_t gemm_chain4_pair_launch(const GemmCall& g0, const GemmCall& g1, hipStream_t s) {
+	using PairFn = void (*)(const GemmArgs, const GemmArgs, int);
+	// [g0 transposes B][g0 16-byte loads]; g1 (A^T B) reads no k-contiguous operand, so its loads are the same either way
+	static const PairFn fns[2][2] = {
+	    {sgemm_chain4_pair_kernel<false, false, false, true, false, true>,
+	     sgemm_chain4_pair_kernel<false, false, true, true, false, true>},
+	    {sgemm_chain4_pair_kernel<false, true, false, true, false, true>,
+	     sgemm_chain4_pair_kernel<false, true, true, true, false, true>}};
+	if (!chain4_pair_takes(g0, g1)) return hipErrorInvalidValue;
+	const GemmArgs p0 = chain4_args(g0), p1 = chain4_args(g1);
+	const int b0 = p0.tiles_m * p0.tiles_n * p0.batch_count, b1 = p1.tiles_m * p1.tiles_n * p1.batch_count;
+	hipLaunchKernelGGL(fns[g0.tb ? 1 : 0][chain4_vec(g0) ? 1 : 0], dim3((unsigned)(b0 + b1)), dim3(256), 0, s, p0, p1,
+	                   b0);
 	return hipGetLastError();
 }
 

@@ -9,6 +9,9 @@
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
+#include <type_traits>
+
 #include "gemm_tile.hpp"
 
 namespace nnh {
@@ -115,6 +118,119 @@ __device__ __forceinline__ void mma_groups(f32x4* a, f32x4* b, int kv, int r, in
 		}
 		if (VA) ca = na;
 		if (VB) cb = nb;
+	}
+}
+
+// One 32 x 32 tile of a whole-depth product (the chain kernel, gemm_chain.hip; also the first product of the chain +
+// pieces pair launch, gemm_pieces.hip): waves 0-3 of the workgroup each own a 16 x 16 quarter, block is the tile's
+// index among the product's workgroups. Every output is one chain over the whole depth in order, four depth steps
+// per instruction; the wave streams the depth in chunks of kChainChunkGroups groups, the next chunk's loads issued
+// before the current chunk's MFMAs. Accumulate follows the reference's order (kAccAfter): old C joins the chain
+// after the first 256 steps, or is added at the end of a shorter one. No barrier: only the wave's own LDS slots.
+constexpr int kChainChunkGroups = 8;  // 128 depth indices
+
+template <bool TA, bool TB, bool VEC>
+__device__ __forceinline__ void chain4_tile(const GemmArgs& p, int block, int wave, int lane) {
+	constexpr int kChunkGroups = kChainChunkGroups;
+	constexpr bool KA = VEC && !TA, KB = VEC && TB;
+	const int tiles = p.tiles_m * p.tiles_n;
+	const int lid = xcd_remap(block, tiles * p.batch_count);
+	const int t = lid % tiles, bi = lid / tiles;
+	const int m0 = (t / p.tiles_n) * 32 + 16 * (wave >> 1), n0 = (t % p.tiles_n) * 32 + 16 * (wave & 1);
+	int64_t oa = 0, ob = 0, oc = 0;
+	if (p.batch.ndim > 0) batch_offsets(p.batch, bi, oa, ob, oc);
+	const float* __restrict__ A = p.a + oa;
+	const float* __restrict__ B = p.b + ob;
+	float* __restrict__ Cp = p.c + oc;
+	const int lda = (int)p.lda, ldb = (int)p.ldb;
+	const int r = lane & 15, j = lane >> 4;
+	const bool row_in = m0 + r < p.m, col_in = n0 + r < p.n;
+	const int K = p.k;
+	// the wave's LDS slots for its k-contiguous operands (two groups each)
+	__shared__ __align__(16) float kst[(KA || KB) ? 4 * 2 * 2 * kKSlot : 1];
+	float* const la = kst + (KA || KB ? wave * 4 * kKSlot : 0);
+	float* const lb = la + 2 * kKSlot;
+	f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+	// register e of lane l holds row 4 (l / 16) + e, column l % 16 of the quarter
+	const int col = n0 + r;
+	auto add_old = [&]() {
+#pragma unroll
+		for (int e = 0; e < 4; ++e) {
+			const int row = m0 + 4 * j + e;
+			if (row < p.m && col < p.n) acc[e] = Cp[(int64_t)row * p.ldc + col] + acc[e];
+		}
+	};
+	using G4 = std::integral_constant<int, 4>;
+	using G2 = std::integral_constant<int, 2>;
+	using G1 = std::integral_constant<int, 1>;
+	auto load8 = [&](int kc, f32x4 (&a)[kChunkGroups], f32x4 (&b)[kChunkGroups]) {
+		load_groups<TA, TB, KA, KB, false, kChunkGroups>(A, lda, B, ldb, m0, n0, kc, K - kc, r, j, row_in, col_in, a, b);
+	};
+	auto run8 = [&](f32x4 (&a)[kChunkGroups], f32x4 (&b)[kChunkGroups]) {
+		mma_groups<KA, KB, false, kChunkGroups>(a, b, 0, r, j, acc, la, lb);
+	};
+	// whole chunks, two register sets: chunk c + 1's loads in flight while chunk c's MFMAs run
+	const int n128 = K / 128;
+	const bool acc_mid = p.accumulate && K > kAccAfter;  // then n128 >= 2: old C joins after chunk 1
+	f32x4 a0[kChunkGroups], b0[kChunkGroups], a1[kChunkGroups], b1[kChunkGroups];
+	if (n128 > 0) load8(0, a0, b0);
+	int c = 0;
+	for (; c + 2 <= n128; c += 2) {
+		load8(128 * (c + 1), a1, b1);
+		__builtin_amdgcn_sched_barrier(0);
+		run8(a0, b0);
+		__builtin_amdgcn_sched_barrier(0);
+		// unconditional (the last pair reloads its second chunk, unused): no branch, so the waits stay counted
+		load8(128 * min(c + 2, n128 - 1), a0, b0);
+		__builtin_amdgcn_sched_barrier(0);
+		run8(a1, b1);
+		__builtin_amdgcn_sched_barrier(0);
+		if (c == 0 && acc_mid) add_old();
+	}
+	if (c < n128) run8(a0, b0);
+	// the rest of the depth: 64, 32, 16 indices, then fewer than 16
+	int kc = 128 * n128;
+	auto part = [&](auto groups_tag, auto part_tag) {
+		constexpr int G = decltype(groups_tag)::value;
+		constexpr bool PART = decltype(part_tag)::value;
+		f32x4 a[G], b[G];
+		load_groups<TA, TB, KA && !PART, KB && !PART, PART, G>(A, lda, B, ldb, m0, n0, kc, K - kc, r, j, row_in, col_in,
+		                                                       a, b);
+		__builtin_amdgcn_sched_barrier(0);
+		mma_groups<KA && !PART, KB && !PART, PART, G>(a, b, K - kc, r, j, acc, la, lb);
+		__builtin_amdgcn_sched_barrier(0);
+	};
+	if (K - kc >= 64) {
+		part(G4{}, std::false_type{});
+		kc += 64;
+	}
+	if (K - kc >= 32) {
+		part(G2{}, std::false_type{});
+		kc += 32;
+	}
+	if (K - kc >= 16) {
+		part(G1{}, std::false_type{});
+		kc += 16;
+	}
+	if (kc < K) part(G1{}, std::true_type{});
+	// the store (gemm.cpp:176-187, 245-252) and the op's bias and ReLU (src/autograd/ops.cpp:726-730, 1396-1409)
+	const bool add_old_at_end = p.accumulate && K <= kAccAfter;
+	unsigned char* alive = p.ep.alive ? p.ep.alive + oc : nullptr;
+#pragma unroll
+	for (int e = 0; e < 4; ++e) {
+		const int row = m0 + 4 * j + e;
+		if (row >= p.m || col >= p.n) continue;
+		const int64_t off = (int64_t)row * p.ldc + col;
+		float v = acc[e];
+		if (add_old_at_end) v = K > 0 ? Cp[off] + v : Cp[off];
+		if (p.ep.bias_mode == kBiasCol) v = v + p.ep.bias[col];
+		else if (p.ep.bias_mode == kBiasRow) v = v + p.ep.bias[row];
+		if (p.ep.relu) {
+			const bool on = v > 0.0f;
+			if (alive) alive[off] = on ? 1 : 0;
+			v = on ? v : 0.0f;
+		}
+		Cp[off] = v;
 	}
 }
 

@@ -13,6 +13,7 @@
 // -0 included (a chain from +0 ends at -0 when its products round to -0). A finished piece goes to an LDS slot;
 // after a barrier each thread adds the pieces in
 // piece order for its outputs, and the store applies accumulate, bias and ReLU as the reference's does.
+#include <algorithm>
 #include <mutex>
 #include <type_traits>
 
@@ -316,16 +317,19 @@ __device__ __forceinline__ void rowsums_stage2(const GemmArgs& p, int m0, int la
 // over the outer index per inner index parked in LDS, then, after the barrier, one chain over the inner index per
 // row.
 
+//
+// One workgroup's tile (block: its index among the product's workgroups) with nthreads threads: waves 0 .. pieces - 1
+// run the pieces, with RS the next kRsWaves waves the row sums, and any further waves only take part in the barrier
+// and the final sums.
 template <bool TA, bool TB, bool RS, bool VEC>
-__global__ void __launch_bounds__(RS ? (kRsMaxPieces + kRsWaves) * 64 : kMaxPieces * 64) sgemm_pieces4_kernel(const GemmArgs p) {
+__device__ __forceinline__ void pieces4_tile(const GemmArgs& p, int block, int tid, int nthreads) {
 	static_assert(!RS || (TA && !TB), "row sums are compiled for the weight-gradient layout only");
 	constexpr int kU = 16;      // tile side
 	__shared__ float done[kMaxPieces * kU * kU];
 	__shared__ float part[RS ? kRsMaxInner * kU : 1];
-	const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-	const int nthreads = blockDim.x;
+	const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
 	const int tiles = p.tiles_m * p.tiles_n;
-	const int lid = xcd_remap((int)blockIdx.x, tiles * p.batch_count);
+	const int lid = xcd_remap(block, tiles * p.batch_count);
 	const int t = lid % tiles, bi = lid / tiles;
 	const int m0 = (t / p.tiles_n) * kU, n0 = (t % p.tiles_n) * kU;
 	int64_t oa = 0, ob = 0, oc = 0;
@@ -334,10 +338,10 @@ __global__ void __launch_bounds__(RS ? (kRsMaxPieces + kRsWaves) * 64 : kMaxPiec
 	const float* __restrict__ B = p.b + ob;
 	const int lda = (int)p.lda, ldb = (int)p.ldb;
 	const int r = lane & 15, j = lane >> 4;
-	if (RS && wave >= p.pieces) {
-		if (n0 == 0) rowsums_stage1(p, A, m0, lane, wave - p.pieces, part);
+	if (wave >= p.pieces) {
+		if (RS && n0 == 0 && wave - p.pieces < kRsWaves) rowsums_stage1(p, A, m0, lane, wave - p.pieces, part);
 		__syncthreads();
-		if (n0 == 0 && wave == p.pieces) rowsums_stage2(p, m0, lane, part);
+		if (RS && n0 == 0 && wave == p.pieces) rowsums_stage2(p, m0, lane, part);
 		finish_tile(p, oc, m0, n0, tid, nthreads, done);
 		return;
 	}
@@ -389,6 +393,31 @@ __global__ void __launch_bounds__(RS ? (kRsMaxPieces + kRsWaves) * 64 : kMaxPiec
 	for (int e = 0; e < 4; ++e) mine[(4 * j + e) * kU + r] = acc[e];
 	__syncthreads();
 	finish_tile(p, oc, m0, n0, tid, nthreads, done);
+}
+
+template <bool TA, bool TB, bool RS, bool VEC>
+__global__ void __launch_bounds__(RS ? (kRsMaxPieces + kRsWaves) * 64 : kMaxPieces * 64) sgemm_pieces4_kernel(const GemmArgs p) {
+	pieces4_tile<TA, TB, RS, VEC>(p, (int)blockIdx.x, (int)threadIdx.x, (int)blockDim.x);
+}
+
+// A linear layer's two backward products in one launch (nnh_linear_backward's dX = G W and dW = G^T X, with or
+// without dW's two-stage row sums, db): workgroups below blocks0 take dX's 32 x 32 tiles on their first four waves
+// (chain4_tile: a whole-depth product, A and B not transposed), the others dW's 16 x 16 tiles (pieces4_tile: a cut
+// product, A transposed). Each output gets the chain it gets from its own kernel, so the bits are those of the two
+// launches; the caller guarantees that neither product writes what the other reads or writes. The workgroup has
+// max(256, pieces-tile threads) threads, at most kPairThreads.
+constexpr int kPairThreads = (kRsMaxPieces + kRsWaves) * 64;
+
+template <bool VEC0, bool RS1>
+__global__ void __launch_bounds__(kPairThreads) sgemm_chain_pieces_kernel(const GemmArgs p0, const GemmArgs p1,
+                                                                         int blocks0) {
+	const int tid = threadIdx.x;
+	if ((int)blockIdx.x < blocks0) {
+		const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+		if (wave < 4) chain4_tile<false, false, VEC0>(p0, (int)blockIdx.x, wave, tid & 63);
+		return;
+	}
+	pieces4_tile<true, false, RS1, !RS1>(p1, (int)blockIdx.x - blocks0, tid, (int)blockDim.x);
 }
 
 using PiecesFn = void (*)(const GemmArgs);
@@ -509,15 +538,9 @@ bool pieces4_takes(const GemmCall& g) {
 	       reinterpret_cast<uintptr_t>(g.a) % 16 == 0;
 }
 
-hipError_t gemm_pieces4_launch(const GemmCall& g, hipStream_t s) {
-	static const PiecesFn fns[2][5] = {
-	    {sgemm_pieces4_kernel<false, false, false, false>, sgemm_pieces4_kernel<false, true, false, false>,
-	     sgemm_pieces4_kernel<true, false, false, false>, sgemm_pieces4_kernel<true, true, false, false>,
-	     sgemm_pieces4_kernel<true, false, true, false>},
-	    {sgemm_pieces4_kernel<false, false, false, true>, sgemm_pieces4_kernel<false, true, false, true>,
-	     sgemm_pieces4_kernel<true, false, false, true>, sgemm_pieces4_kernel<true, true, false, true>,
-	     sgemm_pieces4_kernel<true, false, true, false>}};
-	if (g.rowsum ? !pieces4_takes(g) : !pieces_kernel_takes(g)) return hipErrorInvalidValue;
+namespace {
+
+GemmArgs pieces4_args(const GemmCall& g) {
 	const CutPlan plan = cut_plan(g.m, g.n, g.k);
 	GemmArgs p{};
 	p.a = g.a;
@@ -540,12 +563,53 @@ hipError_t gemm_pieces4_launch(const GemmCall& g, hipStream_t s) {
 	p.rowsum = g.rowsum;
 	p.rowsum_combine = g.rowsum_combine;
 	p.rowsum_outer = (int)g.rowsum_outer;
+	return p;
+}
+
+}  // namespace
+
+hipError_t gemm_pieces4_launch(const GemmCall& g, hipStream_t s) {
+	static const PiecesFn fns[2][5] = {
+	    {sgemm_pieces4_kernel<false, false, false, false>, sgemm_pieces4_kernel<false, true, false, false>,
+	     sgemm_pieces4_kernel<true, false, false, false>, sgemm_pieces4_kernel<true, true, false, false>,
+	     sgemm_pieces4_kernel<true, false, true, false>},
+	    {sgemm_pieces4_kernel<false, false, false, true>, sgemm_pieces4_kernel<false, true, false, true>,
+	     sgemm_pieces4_kernel<true, false, false, true>, sgemm_pieces4_kernel<true, true, false, true>,
+	     sgemm_pieces4_kernel<true, false, true, false>}};
+	if (g.rowsum ? !pieces4_takes(g) : !pieces_kernel_takes(g)) return hipErrorInvalidValue;
+	const GemmArgs p = pieces4_args(g);
 	const int64_t blocks = (int64_t)p.tiles_m * p.tiles_n * p.batch_count;
 	if (blocks > 0x7fffffff) return hipErrorInvalidConfiguration;
 	const bool vec = pieces4_vec(g);
 	const int f = g.rowsum ? 4 : (g.ta ? 2 : 0) + (g.tb ? 1 : 0);
 	hipLaunchKernelGGL(fns[vec ? 1 : 0][f], dim3((unsigned)blocks), dim3((p.pieces + (g.rowsum ? kRsWaves : 0)) * 64), 0,
 	                   s, p);
+	return hipGetLastError();
+}
+
+bool chain_pieces_pair_takes(const GemmCall& g0, const GemmCall& g1) {
+	if (g0.ta || g0.tb || !g1.ta || g1.tb || g0.batch_count != 1 || g1.batch_count != 1 || g0.batch.ndim != 0 ||
+	    g1.batch.ndim != 0 || g0.m <= 0 || g0.n <= 0 || g1.m <= 0 || g1.n <= 0)
+		return false;
+	// dW on the kernel its own launch takes; dX on the chain kernel where that is its own route, or where its chains
+	// are at most 256 deep (the pair runs about as long as its slower half)
+	if (!depth_cut(g1.m, g1.n, g1.k) || !pieces4_takes(g1)) return false;
+	if (!chain4_takes(g0) && !(chain4_ok(g0) && g0.k <= 256 && g0.m * g0.n <= (int64_t(1) << 20))) return false;
+	const int threads = (int)(cut_plan(g1.m, g1.n, g1.k).pieces + (g1.rowsum ? kRsWaves : 0)) * 64;
+	return threads <= kPairThreads && (int64_t)((g0.m + 31) / 32) * ((g0.n + 31) / 32) +
+	                                      ((g1.m + 15) / 16) * ((g1.n + 15) / 16) <= 0x7fffffff;
+}
+
+hipError_t gemm_chain_pieces_pair_launch(const GemmCall& g0, const GemmCall& g1, hipStream_t s) {
+	using PairFn = void (*)(const GemmArgs, const GemmArgs, int);
+	static const PairFn fns[2][2] = {{sgemm_chain_pieces_kernel<false, false>, sgemm_chain_pieces_kernel<false, true>},
+	                                 {sgemm_chain_pieces_kernel<true, false>, sgemm_chain_pieces_kernel<true, true>}};
+	if (!chain_pieces_pair_takes(g0, g1)) return hipErrorInvalidValue;
+	const GemmArgs p0 = chain4_args(g0), p1 = pieces4_args(g1);
+	const int b0 = p0.tiles_m * p0.tiles_n, b1 = p1.tiles_m * p1.tiles_n;
+	const int threads = std::max(256, (p1.pieces + (g1.rowsum ? kRsWaves : 0)) * 64);
+	hipLaunchKernelGGL(fns[chain4_vec(g0) ? 1 : 0][g1.rowsum ? 1 : 0], dim3((unsigned)(b0 + b1)), dim3(threads), 0, s,
+	                   p0, p1, b0);
 	return hipGetLastError();
 }
 

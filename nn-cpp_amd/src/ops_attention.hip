@@ -68,6 +68,24 @@ int gemm(int ta, int tb, size_t m, size_t n, size_t k, const float* A, size_t ld
 	return run_gemm(g, stream, -1, partials);
 }
 
+// Two products that write apart from each other and from what the other reads, in one launch where the pair
+// kernels take them (gemm_launch_pair), else in turn.
+int gemm2(int ta0, int tb0, size_t m0, size_t n0, size_t k0, const float* A0, size_t lda0, const float* B0, size_t ldb0,
+          float* C0, size_t ldc0, int acc0, const nnh_batch& batch0, int ta1, int tb1, size_t m1, size_t n1, size_t k1,
+          const float* A1, size_t lda1, const float* B1, size_t ldb1, float* C1, size_t ldc1, int acc1,
+          const nnh_batch& batch1, void* stream, float* partials) {
+	GemmCall g0, g1;
+	int rc = build_gemm(ta0, tb0, m0, n0, k0, A0, lda0, B0, ldb0, C0, ldc0, acc0, &batch0, nullptr, g0);
+	if (rc == NNH_OK) rc = build_gemm(ta1, tb1, m1, n1, k1, A1, lda1, B1, ldb1, C1, ldc1, acc1, &batch1, nullptr, g1);
+	if (rc != NNH_OK) return rc;
+	bool paired = false;
+	rc = hip_status(gemm_launch_pair(g0, g1, reinterpret_cast<hipStream_t>(stream), paired), "attention backward");
+	if (rc != NNH_OK || paired) return rc;
+	rc = run_gemm(g0, stream, -1, partials);
+	if (rc == NNH_OK) rc = run_gemm(g1, stream, -1, partials);
+	return rc;
+}
+
 // One workspace for nnh_attention_backward: dS, then the depth-cut partials the dV, dQ and dK products share
 // (they run in turn).
 struct BwdPlan {
@@ -194,21 +212,32 @@ int nnh_attention_backward(const float* g, const float* q, const float* k, const
 	float* partials = plan.part ? ws.at<float>(plan.off_part) : nullptr;
 	const bool fused = (dq || dk) && attention_fused_ok((int64_t)Tq, (int64_t)Tk, (int64_t)a.Dh, (int64_t)D, g, v, v, ds,
 	                                                    probs, key_padding_mask);
-	if (fused)  // dP = G_h V_h^T and the softmax backward in one kernel (ops.cpp:1286, 1289-1290)
-		rc = hip_status(attention_fused_dscores(g, v, probs, (int64_t)N, (int64_t)Tq, (int64_t)Tk, (int64_t)D,
-		                                        (int64_t)heads, key_padding_mask, causal, a.scale, ds, s),
-		                "attention backward");
-	else  // dP = G_h V_h^T (ops.cpp:1286)
-		rc = gemm(0, 1, Tq, Tk, a.Dh, g, D, v, D, ds, Tk, 0, head_batch(a, Tq, Tk, false, true, 0), stream, partials);
-	// dV (+)= P^T G_h (ops.cpp:1287): A = probs stored Tq x Tk, read transposed
-	if (rc == NNH_OK && dv) {
-		nnh_batch b = head_batch(a, 0, Tq, true, false, Tk);
-		rc = gemm(1, 0, Tk, a.Dh, Tq, probs, Tk, g, D, dv, D, !dv_first, b, stream, partials);
+	const uint64_t qb = (uint64_t)N * Tq * D * 4, kb = (uint64_t)N * Tk * D * 4, sb = (uint64_t)N * heads * Tq * Tk * 4;
+	if (!fused && (dq || dk) && dv && !ranges_overlap(dv, kb, ds, sb)) {
+		// dP = G_h V_h^T (ops.cpp:1286) and dV (+)= P^T G_h (ops.cpp:1287), which reads P, not dP
+		rc = gemm2(0, 1, Tq, Tk, a.Dh, g, D, v, D, ds, Tk, 0, head_batch(a, Tq, Tk, false, true, 0), 1, 0, Tk, a.Dh, Tq,
+		           probs, Tk, g, D, dv, D, !dv_first, head_batch(a, 0, Tq, true, false, Tk), stream, partials);
+	} else {
+		if (fused)  // dP = G_h V_h^T and the softmax backward in one kernel (ops.cpp:1286, 1289-1290)
+			rc = hip_status(attention_fused_dscores(g, v, probs, (int64_t)N, (int64_t)Tq, (int64_t)Tk, (int64_t)D,
+			                                        (int64_t)heads, key_padding_mask, causal, a.scale, ds, s),
+			                "attention backward");
+		else if (dq || dk)  // dP = G_h V_h^T (ops.cpp:1286)
+			rc = gemm(0, 1, Tq, Tk, a.Dh, g, D, v, D, ds, Tk, 0, head_batch(a, Tq, Tk, false, true, 0), stream, partials);
+		// dV (+)= P^T G_h (ops.cpp:1287): A = probs stored Tq x Tk, read transposed
+		if (rc == NNH_OK && dv) {
+			nnh_batch b = head_batch(a, 0, Tq, true, false, Tk);
+			rc = gemm(1, 0, Tk, a.Dh, Tq, probs, Tk, g, D, dv, D, !dv_first, b, stream, partials);
+		}
 	}
 	if (rc == NNH_OK && (dq || dk) && !fused)
 		rc = hip_status(softmax_backward_rows(probs, ds, ds, (int64_t)(N * heads * Tq), (int)Tk, (int)Tq, (int)heads,
 		                                      a.scale, key_padding_mask, causal, 0, s),
 		                "attention softmax backward");
+	// dQ (+)= dS K_h (ops.cpp:1291) and dK (+)= dS^T Q_h (ops.cpp:1292) in one launch when they are apart
+	if (rc == NNH_OK && dq && dk && !ranges_overlap(dq, qb, dk, kb))
+		return gemm2(0, 0, Tq, a.Dh, Tk, ds, Tk, k, D, dq, D, !dq_first, head_batch(a, 0, Tk, true, false, Tq), 1, 0, Tk,
+		             a.Dh, Tq, ds, Tk, q, D, dk, D, !dk_first, head_batch(a, 0, Tq, true, false, Tk), stream, partials);
 	// dQ (+)= dS K_h (ops.cpp:1291)
 	if (rc == NNH_OK && dq) {
 		nnh_batch b = head_batch(a, 0, Tk, true, false, Tq);

@@ -131,8 +131,9 @@ int nnh_linear_backward(const float* g, const float* x, const float* w, const si
 		const uint64_t bx = (uint64_t)M * K * 4, bw = (uint64_t)n * K * 4, bg = (uint64_t)M * n * 4;
 		const bool apart = !ranges_overlap(dx, bx, g, bg) && !ranges_overlap(dx, bx, w, bw) &&
 		                   !ranges_overlap(dx, bx, x, bx) && !ranges_overlap(dx, bx, dw, bw) &&
-		                   !ranges_overlap(dw, bw, w, bw) && (!db_in_dw || (!ranges_overlap(db, n * 4, dx, bx) &&
-		                                                                    !ranges_overlap(db, n * 4, w, bw)));
+		                   !ranges_overlap(dw, bw, w, bw) &&
+		                   (!(db_in_dw || db_in_pieces) ||
+		                    (!ranges_overlap(db, n * 4, dx, bx) && !ranges_overlap(db, n * 4, w, bw)));
 		if (apart) {
 			const int rc = hip_status(gemm_launch_pair(cx, cw, s, paired), "linear backward");
 			if (rc != NNH_OK) return rc;

@@ -129,13 +129,27 @@ int plan_backward(const float* g, const float* a, const size_t* as, int an, cons
 	return NNH_OK;
 }
 
+// The product of one gradient into out (the gradient itself when direct, else the scratch it is reduced from).
+int grad_call(const GradPlan& gp, float* out, GemmCall& call) {
+	const MatmulPlan& m = gp.mm;
+	return build_gemm(m.fold ? 0 : gp.ta, gp.tb, m.m, m.n, m.k, gp.left, m.lda, gp.right, m.ldb, out, m.n, 0,
+	                  m.batch.ndim ? &m.batch : nullptr, nullptr, call);
+}
+
+// The two gradients in one launch (gemm_launch_pair) when both go straight into their buffers, those do not overlap,
+// and the pair kernels take the products; launched tells whether it did (otherwise nothing was enqueued).
+int run_pair(const GemmCall& ca, float* da, uint64_t da_bytes, const GemmCall& cb, float* db, uint64_t db_bytes,
+             void* stream, bool& launched) {
+	launched = false;
+	if (ranges_overlap(da, da_bytes, db, db_bytes)) return NNH_OK;
+	return hip_status(gemm_launch_pair(ca, cb, reinterpret_cast<hipStream_t>(stream), launched), "matmul backward");
+}
+
 int run_grad(const GradPlan& gp, float* dst, int first, float* tmp, float* pp0, float* pp1, float* part, void* stream) {
 	hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-	float* out = gp.direct ? dst : tmp;
 	GemmCall call;
 	const MatmulPlan& m = gp.mm;
-	int rc = build_gemm(m.fold ? 0 : gp.ta, gp.tb, m.m, m.n, m.k, gp.left, m.lda, gp.right, m.ldb, out, m.n, 0,
-	                    m.batch.ndim ? &m.batch : nullptr, nullptr, call);
+	int rc = grad_call(gp, gp.direct ? dst : tmp, call);
 	if (rc != NNH_OK) return rc;
 	rc = run_gemm(call, stream, -1, part);
 	if (rc != NNH_OK || gp.direct) return rc;
@@ -221,6 +235,11 @@ int nnh_matmul_backward(const float* g, const float* a, const size_t* a_shape, i
 			        : build_gemm(1, 0, K, n, M, a, K, g, n, db, n, !db_first, nullptr, nullptr, cb);
 			if (rc != NNH_OK) return rc;
 		}
+		bool paired = false;
+		if (da && db) {
+			rc = run_pair(ca, da, (uint64_t)M * K * 4, cb, db, (uint64_t)K * n * 4, stream, paired);
+			if (rc != NNH_OK || paired) return rc;
+		}
 		if (da) rc = run_gemm(ca, stream, -1);
 		if (rc == NNH_OK && db) rc = run_gemm(cb, stream, -1);
 		return rc;
@@ -228,6 +247,17 @@ int nnh_matmul_backward(const float* g, const float* a, const size_t* a_shape, i
 	rc = check_workspace(stream, p.total);
 	if (rc != NNH_OK) return rc;
 	if (p.total == 0) {  // fresh gradients of the operands' own shapes, no depth cut: straight into them
+		if (da && db) {
+			GemmCall ca, cb;
+			rc = grad_call(p.ga, da, ca);
+			if (rc == NNH_OK) rc = grad_call(p.gb, db, cb);
+			if (rc != NNH_OK) return rc;
+			const uint64_t ab = numel(std::vector<size_t>(a_shape, a_shape + a_ndim)) * 4;
+			const uint64_t bb = numel(std::vector<size_t>(b_shape, b_shape + b_ndim)) * 4;
+			bool paired = false;
+			rc = run_pair(ca, da, ab, cb, db, bb, stream, paired);
+			if (rc != NNH_OK || paired) return rc;
+		}
 		if (da) rc = run_grad(p.ga, da, da_first, nullptr, nullptr, nullptr, nullptr, stream);
 		if (rc == NNH_OK && db) rc = run_grad(p.gb, db, db_first, nullptr, nullptr, nullptr, nullptr, stream);
 		return rc;

@@ -24,6 +24,8 @@ CASES = [
     ((2, 3, 16, 8), (2, 3, 16, 8), True),      # composed attention's scores: q_h k_h^T per (sample, head)
     ((2, 3, 16, 16), (2, 3, 16, 8), False),    # composed attention's output: P v_h
     ((3, 5, 600), (3, 600, 40), False),        # batched with a depth cut in dA? (5 x 600 x 40: no); dB 600x40x5
+    ((16, 4, 64, 16), (16, 4, 64, 16), True),  # transformer_tiny's scores: both gradients in one launch
+    ((16, 4, 64, 64), (16, 4, 64, 16), False), # and its P v_h
 ]
 
 
@@ -38,6 +40,8 @@ def host(t):
 
 @pytest.mark.parametrize("case", CASES)
 def test_matmul_backward_matches_nncpp(gpu, ref, case):
+    """Fresh gradients (where both run on the chain kernel, in one launch), then accumulated ones, against nn-cpp's
+    own backward rule."""
     import nnh
     import torch
     ash, bsh, bt = case
