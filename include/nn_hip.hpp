@@ -155,6 +155,12 @@ Value linear(const Value& x, const Value& weight, const Value& bias);
 // relu(linear(x, weight, bias)) with both forwards in one launch: the same two nodes, outputs and gradients. No
 // counterpart in the reference, whose model code calls the two ops in turn.
 Value linear_relu(const Value& x, const Value& weight, const Value& bias);
+// add(residual, linear(x, weight, bias)) with the add in the linear's epilogue (one kernel): the same two nodes and
+// bits. A residual of another shape runs the two ops.
+Value linear_add(const Value& x, const Value& weight, const Value& bias, const Value& residual);
+// linear(x, w_i, b_i) for each (w_i, b_i) of layers (an attention layer's q, k and v projections): the nodes and bits
+// of the separate calls, in one launch where the shapes allow.
+std::vector<Value> linear_many(const Value& x, const std::vector<std::pair<Value, Value>>& layers);
 Value relu(const Value& x);
 // ops.cpp:672-681: same elements, new shape (the Flatten module's op).
 Value reshape(const Value& x, std::vector<size_t> new_shape);

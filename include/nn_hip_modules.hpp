@@ -71,6 +71,8 @@ public:
 	Value forward(const Value& input) override;
 	bool can_fuse_relu() const override { return true; }
 	Value forward_relu(const Value& input) override { return linear_relu(input, weight_, bias_); }
+	// add(residual, forward(input)) in one kernel (linear_add)
+	Value forward_add(const Value& input, const Value& residual) { return linear_add(input, weight_, bias_, residual); }
 	std::vector<Value> parameters() const override;
 	std::vector<std::pair<std::string, Value>> named_parameters() const override;
 	const Value& weight() const { return weight_; }
@@ -172,11 +174,15 @@ public:
 	MultiHeadAttention(size_t dim, size_t heads, bool causal = false, float dropout = 0.0f);
 	Value forward(const Value& x) override;
 	Value attend(const Value& query, const Value& context, const Tensor& key_padding_mask = Tensor({0}));
+	// add(residual, forward(x)), the output projection's epilogue adding the residual (a transformer block's x +
+	// attn(ln1(x)))
+	Value forward_add(const Value& x, const Value& residual);
 	std::vector<Value> parameters() const override;
 	std::vector<std::pair<std::string, Value>> named_parameters() const override;
 	void train(bool mode = true) override;
 
 private:
+	Value attend_impl(const Value& query, const Value& context, const Tensor& key_padding_mask, const Value* residual);
 	size_t dim_, heads_;
 	bool causal_;
 	Linear q_, k_, v_, o_;

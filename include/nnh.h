@@ -185,6 +185,21 @@ int nnh_matmul_backward_workspace_size(const size_t* a_shape, int a_ndim, const 
  */
 int nnh_linear_forward(const float* x, size_t M, size_t K, const float* w, size_t n, const float* bias, int relu,
                        float* y, void* stream);
+/*
+ * nn::linear, then nn::add(residual, that) (ops.cpp:714-730, 333-336: a transformer block's residual connection) in
+ * one kernel: y = residual + (x w^T + bias), element by element the bits of the two ops. No single counterpart in
+ * the reference. residual is {M, n}, read before y is written, and may be y itself (not otherwise overlap it).
+ */
+int nnh_linear_forward_add(const float* x, size_t M, size_t K, const float* w, size_t n, const float* bias,
+                           const float* residual, float* y, void* stream);
+/*
+ * count (1 to 8) nn::linear forwards over one input (ops.cpp:714-730: an attention layer's q, k and v projections):
+ * y[i] {M, n[i]} = x w[i]^T + bias[i], the bits of count separate calls, in one launch where the shapes allow (two or
+ * three products, each at most 2^20 outputs and 256 deep). No single counterpart in the reference. No output may
+ * overlap x, another output, or any layer's weight or bias.
+ */
+int nnh_linear_forward_multi(const float* x, size_t M, size_t K, int count, const float* const* w, const size_t* n,
+                             const float* const* bias, float* const* y, void* stream);
 
 /*
  * nn::linear backward (ops.cpp:731-744) for upstream gradient g of shape lead[0..nlead-1] x n, where x has

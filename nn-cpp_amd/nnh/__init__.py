@@ -106,6 +106,8 @@ _EXTRA_DECLS = {
     "nnh_matmul_backward_workspace_size": [_szp, C.c_int, _szp, C.c_int, C.c_int, C.c_int, C.c_int, _szp],
     "nnh_add_to_grad": [_vp, _vp, _sz, C.c_int, _vp],
     "nnh_add_to_grad2": [_vp, C.c_int, _vp, C.c_int, _vp, _sz, _vp],
+    "nnh_linear_forward_add": [_vp, _sz, _sz, _vp, _sz, _vp, _vp, _vp, _vp],
+    "nnh_linear_forward_multi": [_vp, _sz, _sz, C.c_int, C.POINTER(_vp), _szp, C.POINTER(_vp), C.POINTER(_vp), _vp],
     "nnh_im2col": [_vp, _sz, _sz, _sz, _sz, _sz, _sz, C.c_int, C.c_int, _vp, _vp],
     "nnh_col2im_add": [_vp, _sz, _sz, _sz, _sz, _sz, _sz, C.c_int, C.c_int, _vp, C.c_int, _vp],
     "nnh_batchnorm_forward": [_vp, _sz, _sz, _sz, _vp, _vp, C.c_float, C.c_int, _vp, _vp, _vp, _vp, _vp, _vp],
@@ -289,6 +291,32 @@ def linear_forward(x, w, bias, relu=False, stream=None):
     n = w.shape[0]
     y = torch.empty(tuple(x.shape[:-1]) + (n,), dtype=torch.float32, device=x.device)
     check(lib().nnh_linear_forward(_ptr(x), M, K, _ptr(w), n, _ptr(bias), int(relu), _ptr(y), _stream(stream)))
+    return y
+
+
+def linear_forward_multi(x, layers, stream=None):
+    """Several nn::linear forwards over one input x; layers is [(w, bias), ...]; returns the outputs."""
+    import torch
+    K = x.shape[-1]
+    M = x.numel() // K if K else int(torch.tensor(x.shape[:-1]).prod())
+    ys = [torch.empty(tuple(x.shape[:-1]) + (w.shape[0],), dtype=torch.float32, device=x.device) for w, _ in layers]
+    cnt = len(layers)
+    arr = lambda ts: (_vp * cnt)(*[t.data_ptr() for t in ts])
+    ns = (C.c_size_t * cnt)(*[w.shape[0] for w, _ in layers])
+    check(lib().nnh_linear_forward_multi(_ptr(x), M, K, cnt, arr([w for w, _ in layers]), ns,
+                                         arr([b for _, b in layers]), arr(ys), _stream(stream)))
+    return ys
+
+
+def linear_forward_add(x, w, bias, residual, out=None, stream=None):
+    """nn::add(residual, nn::linear(x, w, bias)) in one kernel; returns y (out, which may be residual itself)."""
+    import torch
+    K = x.shape[-1]
+    M = x.numel() // K if K else int(torch.tensor(x.shape[:-1]).prod())
+    n = w.shape[0]
+    y = out if out is not None else torch.empty(tuple(x.shape[:-1]) + (n,), dtype=torch.float32, device=x.device)
+    check(lib().nnh_linear_forward_add(_ptr(x), M, K, _ptr(w), n, _ptr(bias), _ptr(residual), _ptr(y),
+                                       _stream(stream)))
     return y
 
 

@@ -57,11 +57,14 @@ Value transformer_forward(const std::vector<float>& ids, size_t N, const std::ve
 	size_t i = 1;
 	for (size_t l = 0; l < kLayers; ++l, i += 16) {
 		const Value a = nn::hip::layernorm(h, p[i], p[i + 1], 1e-5f);
-		const Value att = nn::hip::attention(nn::hip::linear(a, p[i + 2], p[i + 3]), nn::hip::linear(a, p[i + 4], p[i + 5]),
-		                                     nn::hip::linear(a, p[i + 6], p[i + 7]), kHeads, no_mask, true);
-		h = nn::hip::add(h, nn::hip::linear(att, p[i + 8], p[i + 9]));
+		// the q, k and v projections in one launch (the nodes and bits of three linear calls)
+		const std::vector<Value> qkv =
+		    nn::hip::linear_many(a, {{p[i + 2], p[i + 3]}, {p[i + 4], p[i + 5]}, {p[i + 6], p[i + 7]}});
+		const Value att = nn::hip::attention(qkv[0], qkv[1], qkv[2], kHeads, no_mask, true);
+		// add(h, linear(...)) with the add in the linear's epilogue: the same nodes and bits
+		h = nn::hip::linear_add(att, p[i + 8], p[i + 9], h);
 		const Value m = nn::hip::gelu(nn::hip::linear(nn::hip::layernorm(h, p[i + 10], p[i + 11], 1e-5f), p[i + 12], p[i + 13]));
-		h = nn::hip::add(h, nn::hip::linear(m, p[i + 14], p[i + 15]));
+		h = nn::hip::linear_add(m, p[i + 14], p[i + 15], h);
 	}
 	const Value o = nn::hip::linear(nn::hip::layernorm(h, p[i], p[i + 1], 1e-5f), p[i + 2], p[i + 3]);
 	return nn::hip::reshape(o, {N * kMaxLen, kVocab});

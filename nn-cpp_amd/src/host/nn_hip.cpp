@@ -418,6 +418,21 @@ namespace {
 // launch (the GEMM epilogue) and a relu node over it is returned: the same two nodes and bits as relu(linear(...)).
 // The linear node's own data is then the ReLU's output: no backward rule reads it (linear's reads x and W, relu's
 // masks with its output, y > 0 exactly where its input is), and the caller only holds the relu node.
+// The linear node over its forward's output y (ops.cpp:733-745).
+Value linear_node(const Value& x, const Value& weight, const Value& bias, const Tensor& y) {
+	const size_t n = weight.data().shape()[0], K = weight.data().shape()[1];
+	return Value::node(y, {x, weight, bias}, [x, weight, bias, n, K](const Tensor& g) {
+		bool fx = false, fw = false, fb = false;
+		float* dx = grad_if(x, fx);
+		float* dw = grad_if(weight, fw);
+		float* db = grad_if(bias, fb);
+		if (!dx && !dw && !db) return;
+		const auto& xs2 = x.data().shape();
+		check(nnh_linear_backward(g.data(), x.data().data(), weight.data().data(), xs2.data(), (int)xs2.size() - 1, K, n,
+		                          dx, fx, dw, fw, db, fb, g_stream));
+	});
+}
+
 Value linear_op(const Value& x, const Value& weight, const Value& bias, bool relu) {
 	const auto& xs = x.data().shape();
 	const auto& ws = weight.data().shape();
@@ -430,16 +445,7 @@ Value linear_op(const Value& x, const Value& weight, const Value& bias, bool rel
 	Tensor y = Tensor::empty(out);
 	check(nnh_linear_forward(x.data().data(), K ? M : numel(std::vector<size_t>(xs.begin(), xs.end() - 1)), K,
 	                         weight.data().data(), n, bias.data().data(), relu ? 1 : 0, y.data(), g_stream));
-	Value h = Value::node(y, {x, weight, bias}, [x, weight, bias, n, K](const Tensor& g) {
-		bool fx = false, fw = false, fb = false;
-		float* dx = grad_if(x, fx);
-		float* dw = grad_if(weight, fw);
-		float* db = grad_if(bias, fb);
-		if (!dx && !dw && !db) return;
-		const auto& xs2 = x.data().shape();
-		check(nnh_linear_backward(g.data(), x.data().data(), weight.data().data(), xs2.data(), (int)xs2.size() - 1, K, n,
-		                          dx, fx, dw, fw, db, fb, g_stream));
-	});
+	Value h = linear_node(x, weight, bias, y);
 	if (!relu) return h;
 	// ops.cpp:775-793 on h, masked with the output
 	return Value::node(y, {h}, [h, y](const Tensor& g) {
@@ -631,15 +637,10 @@ Value scaled_masked_softmax(const Value& x, float scale_by, const Tensor& key_pa
 	});
 }
 
-Value add(const Value& a, const Value& b) {
-	const auto& as = a.data().shape();
-	const auto& bs = b.data().shape();
-	if (bs.size() > as.size() || !std::equal(bs.begin(), bs.end(), as.end() - bs.size()))
-		throw std::invalid_argument("nn::hip: add takes b of a's shape or of a's trailing axes");
-	const size_t inner = b.data().size(), total = a.data().size();
-	const size_t outer = inner ? total / inner : 0;
-	Tensor y = Tensor::empty(as);
-	check(nnh_add_forward(a.data().data(), b.data().data(), outer, inner, y.data(), g_stream));
+namespace {
+
+// The add node over its forward's output y = a + b.
+Value add_node(const Value& a, const Value& b, Tensor y) {
 	return Value::node(std::move(y), {a, b}, [a, b](const Tensor& g) {
 		// ops.cpp:333-336 then accumulate_grad (ops.cpp:110-117): a, then b, each stored fresh or added to
 		const auto& gs = g.shape();
@@ -673,6 +674,72 @@ Value add(const Value& a, const Value& b) {
 			}
 		}
 	});
+}
+
+}  // namespace
+
+Value add(const Value& a, const Value& b) {
+	const auto& as = a.data().shape();
+	const auto& bs = b.data().shape();
+	if (bs.size() > as.size() || !std::equal(bs.begin(), bs.end(), as.end() - bs.size()))
+		throw std::invalid_argument("nn::hip: add takes b of a's shape or of a's trailing axes");
+	const size_t inner = b.data().size(), total = a.data().size();
+	const size_t outer = inner ? total / inner : 0;
+	Tensor y = Tensor::empty(as);
+	check(nnh_add_forward(a.data().data(), b.data().data(), outer, inner, y.data(), g_stream));
+	return add_node(a, b, std::move(y));
+}
+
+std::vector<Value> linear_many(const Value& x, const std::vector<std::pair<Value, Value>>& layers) {
+	const auto& xs = x.data().shape();
+	const size_t count = layers.size();
+	if (count == 0) return {};
+	if (count > 8) {
+		std::vector<Value> out;
+		for (const auto& l : layers) out.push_back(linear(x, l.first, l.second));
+		return out;
+	}
+	std::vector<Tensor> ys;
+	std::vector<const float*> w(count), b(count);
+	std::vector<float*> y(count);
+	std::vector<size_t> n(count);
+	const size_t K = xs.empty() ? 0 : xs.back();
+	for (size_t i = 0; i < count; ++i) {
+		const auto& ws = layers[i].first.data().shape();
+		// ops.cpp:717-719
+		if (xs.size() < 2 || ws.size() != 2 || xs.back() != ws[1] ||
+		    layers[i].second.data().shape() != std::vector<size_t>{ws[0]})
+			throw TensorShapeError("nn::hip: linear shapes");
+		std::vector<size_t> out(xs.begin(), xs.end() - 1);
+		out.push_back(ws[0]);
+		ys.push_back(Tensor::empty(out));
+		w[i] = layers[i].first.data().data();
+		b[i] = layers[i].second.data().data();
+		y[i] = ys.back().data();
+		n[i] = ws[0];
+	}
+	const size_t M = K ? x.data().size() / K : numel(std::vector<size_t>(xs.begin(), xs.end() - 1));
+	check(nnh_linear_forward_multi(x.data().data(), M, K, (int)count, w.data(), n.data(), b.data(), y.data(), g_stream));
+	std::vector<Value> out;
+	for (size_t i = 0; i < count; ++i) out.push_back(linear_node(x, layers[i].first, layers[i].second, ys[i]));
+	return out;
+}
+
+Value linear_add(const Value& x, const Value& weight, const Value& bias, const Value& residual) {
+	const auto& xs = x.data().shape();
+	const auto& ws = weight.data().shape();
+	// ops.cpp:717-719
+	if (xs.size() < 2 || ws.size() != 2 || xs.back() != ws[1] || bias.data().shape() != std::vector<size_t>{ws[0]})
+		throw TensorShapeError("nn::hip: linear shapes");
+	std::vector<size_t> out(xs.begin(), xs.end() - 1);
+	out.push_back(ws[0]);
+	if (residual.data().shape() != out) return add(residual, linear(x, weight, bias));
+	const size_t n = ws[0], K = ws[1], M = numel(out) / std::max<size_t>(n, 1);
+	Tensor y = Tensor::empty(out);
+	check(nnh_linear_forward_add(x.data().data(), M, K, weight.data().data(), n, bias.data().data(),
+	                             residual.data().data(), y.data(), g_stream));
+	// the linear node (whose backward does not read its data) and the add node over it, as add(residual, linear(..))
+	return add_node(residual, linear_node(x, weight, bias, y), y);
 }
 
 Value mul(const Value& a, const Value& b) {

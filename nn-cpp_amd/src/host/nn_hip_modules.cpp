@@ -204,7 +204,16 @@ MultiHeadAttention::MultiHeadAttention(size_t dim, size_t heads, bool causal, fl
 
 Value MultiHeadAttention::forward(const Value& x) { return attend(x, x); }
 
+Value MultiHeadAttention::forward_add(const Value& x, const Value& residual) {
+	return attend_impl(x, x, Tensor({0}), &residual);
+}
+
 Value MultiHeadAttention::attend(const Value& query, const Value& context, const Tensor& key_padding_mask) {
+	return attend_impl(query, context, key_padding_mask, nullptr);
+}
+
+Value MultiHeadAttention::attend_impl(const Value& query, const Value& context, const Tensor& key_padding_mask,
+                                      const Value* residual) {
 	const auto& qs = query.data().shape();
 	const auto& cs = context.data().shape();
 	if (qs.size() != 3 || cs.size() != 3 || qs[2] != dim_ || cs[2] != dim_ || qs[0] != cs[0])
@@ -215,9 +224,16 @@ Value MultiHeadAttention::attend(const Value& query, const Value& context, const
 	if (drop_.active())
 		throw std::invalid_argument(
 		    "nn::hip::MultiHeadAttention: dropout on the attention weights in training mode is not available");
-	// one op reads each head in place (attention.cpp:33-35)
-	return o_.forward(attention(q_.forward(query), k_.forward(context), v_.forward(context), heads_, key_padding_mask,
-	                            causal_));
+	// one op reads each head in place (attention.cpp:33-35); self-attention's three projections in one launch
+	Value a;
+	if (query.impl() == context.impl()) {
+		const std::vector<Value> qkv = linear_many(query, {{q_.weight(), q_.bias()}, {k_.weight(), k_.bias()},
+		                                                   {v_.weight(), v_.bias()}});
+		a = attention(qkv[0], qkv[1], qkv[2], heads_, key_padding_mask, causal_);
+	} else {
+		a = attention(q_.forward(query), k_.forward(context), v_.forward(context), heads_, key_padding_mask, causal_);
+	}
+	return residual ? o_.forward_add(a, *residual) : o_.forward(a);
 }
 
 std::vector<Value> MultiHeadAttention::parameters() const {
@@ -324,8 +340,11 @@ TransformerBlock::TransformerBlock(size_t dim, size_t heads, size_t mlp_ratio, f
 	  drop_(dropout) {}
 
 Value TransformerBlock::forward(const Value& x) {
-	const Value h = add(x, attn_.forward(ln1_.forward(x)));
-	return add(h, drop_.forward(fc2_.forward(act_.forward(fc1_.forward(ln2_.forward(h))))));
+	// x + attn(ln1(x)) and h + drop(fc2(...)) with each add in the producing linear's epilogue (the same nodes and
+	// bits); an active dropout between fc2 and the add keeps the ops apart
+	const Value h = attn_.forward_add(ln1_.forward(x), x);
+	const Value f = act_.forward(fc1_.forward(ln2_.forward(h)));
+	return drop_.active() ? add(h, drop_.forward(fc2_.forward(f))) : fc2_.forward_add(f, h);
 }
 
 std::vector<Value> TransformerBlock::parameters() const {

@@ -16,9 +16,10 @@ namespace nnh {
 namespace {
 
 __device__ __forceinline__ float finish(float v, int64_t row, int64_t col, int64_t off, const Epilogue& ep,
-                                        unsigned char* alive) {
+                                        unsigned char* alive, const float* res) {
 	if (ep.bias_mode == kBiasCol) v = v + ep.bias[col];
 	else if (ep.bias_mode == kBiasRow) v = v + ep.bias[row];
+	if (res) v = res[off] + v;
 	if (ep.relu) {
 		const bool on = v > 0.0f;
 		if (alive) alive[off] = on ? 1 : 0;
@@ -45,7 +46,7 @@ __global__ void __launch_bounds__(256) reduce_pieces_kernel(const float* __restr
 	const int64_t off = row * ldc + col;
 	float* cp = c + oc;
 	float v = accumulate ? cp[off] + acc : acc;
-	cp[off] = finish(v, row, col, off, ep, ep.alive ? ep.alive + oc : nullptr);
+	cp[off] = finish(v, row, col, off, ep, ep.alive ? ep.alive + oc : nullptr, ep.res ? ep.res + oc : nullptr);
 }
 
 const Config* configs() {
@@ -354,6 +355,16 @@ hipError_t gemm_launch_pair(const GemmCall& g0, const GemmCall& g1, hipStream_t 
 	hipLaunchKernelGGL(fn, dim3((unsigned)(b0 + b1)), dim3(256), std::max(cf.lds_bytes[0], cf.lds_bytes[2]), s, p0, p1,
 	                   (int)b0);
 	e = hipGetLastError();
+	launched = e == hipSuccess;
+	return e;
+}
+
+hipError_t gemm_launch_group(const GemmCall* g, int count, hipStream_t s, bool& launched) {
+	launched = false;
+	if (!chain4_group_takes(g, count)) return hipSuccess;
+	hipError_t e = prepare_device();
+	if (e != hipSuccess) return e;
+	e = gemm_chain4_group_launch(g, count, s);
 	launched = e == hipSuccess;
 	return e;
 }

@@ -101,6 +101,12 @@ bool chain_pieces_pair_takes(const GemmCall& g0, const GemmCall& g1);
 // each one the chain kernel's own route takes (chain4_takes). The caller guarantees that neither product writes what
 // the other reads or writes.
 bool chain4_pair_takes(const GemmCall& g0, const GemmCall& g1);
+// Two or three whole-depth products of one layout on the chain kernel in one launch (gemm_chain.hip: several linear
+// layers over one input), each at most 2^20 outputs and 256 deep. The caller guarantees that no product writes what
+// another reads or writes.
+constexpr int kChainGroupMax = 3;
+bool chain4_group_takes(const GemmCall* g, int count);
+hipError_t gemm_chain4_group_launch(const GemmCall* g, int count, hipStream_t s);
 hipError_t gemm_chain4_pair_launch(const GemmCall& g0, const GemmCall& g1, hipStream_t s);
 hipError_t gemm_chain_pieces_pair_launch(const GemmCall& g0, const GemmCall& g1, hipStream_t s);
 
@@ -118,6 +124,11 @@ hipError_t gemm_launch(const GemmCall& g, hipStream_t s, int config = -1, float*
 // pick the same small-tile configuration; launched tells whether it did (otherwise nothing was launched and the
 // caller runs them in turn). The caller guarantees that neither product writes what the other reads or writes.
 hipError_t gemm_launch_pair(const GemmCall& g0, const GemmCall& g1, hipStream_t s, bool& launched);
+
+// Two or three products in one launch where the chain kernel's group launch takes them (chain4_group_takes);
+// launched tells whether it did (otherwise nothing was launched and the caller runs them in turn). The caller
+// guarantees that no product writes what another reads or writes.
+hipError_t gemm_launch_group(const GemmCall* g, int count, hipStream_t s, bool& launched);
 
 int gemm_config_count();
 const char* gemm_config_name(int config);

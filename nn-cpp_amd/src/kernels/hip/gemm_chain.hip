@@ -34,6 +34,24 @@ __global__ void __launch_bounds__(256) sgemm_chain4_pair_kernel(const GemmArgs p
 	else chain4_tile<TA1, TB1, VEC1>(p1, (int)blockIdx.x - blocks0, wave, lane);
 }
 
+// Up to kChainGroupMax whole-depth products of one layout in one launch (several linear layers over one input):
+// product i takes the workgroups from start[i] on. The switch keeps each product's arguments a compile-time slot
+// of the kernel's argument block.
+struct ChainGroup {
+	GemmArgs p[kChainGroupMax];
+	int start[kChainGroupMax + 1];
+	int count;
+};
+
+template <bool TA, bool TB, bool VEC>
+__global__ void __launch_bounds__(256) sgemm_chain4_group_kernel(const ChainGroup g) {
+	const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6), lane = (int)threadIdx.x & 63;
+	const int b = (int)blockIdx.x;
+	if (b < g.start[1]) chain4_tile<TA, TB, VEC>(g.p[0], b, wave, lane);
+	else if (g.count < 3 || b < g.start[2]) chain4_tile<TA, TB, VEC>(g.p[1], b - g.start[1], wave, lane);
+	else chain4_tile<TA, TB, VEC>(g.p[2], b - g.start[2], wave, lane);
+}
+
 using ChainFn = void (*)(const GemmArgs);
 
 constexpr int64_t kMaxLd = int64_t(1) << 24;
@@ -130,6 +148,42 @@ hipError_t gemm_chain4_pair_launch(const GemmCall& g0, const GemmCall& g1, hipSt
 	const int b0 = p0.tiles_m * p0.tiles_n * p0.batch_count, b1 = p1.tiles_m * p1.tiles_n * p1.batch_count;
 	hipLaunchKernelGGL(fns[g0.tb ? 1 : 0][chain4_vec(g0) ? 1 : 0], dim3((unsigned)(b0 + b1)), dim3(256), 0, s, p0, p1,
 	                   b0);
+	return hipGetLastError();
+}
+
+bool chain4_group_takes(const GemmCall* g, int count) {
+	if (count < 2 || count > kChainGroupMax) return false;
+	int64_t blocks = 0;
+	for (int i = 0; i < count; ++i) {
+		if (!chain4_ok(g[i]) || g[i].ta != g[0].ta || g[i].tb != g[0].tb || g[i].m <= 0 || g[i].n <= 0 ||
+		    g[i].m * g[i].n * g[i].batch_count > (int64_t(1) << 20) || g[i].k > 256)
+			return false;
+		blocks += ((g[i].m + 31) / 32) * ((g[i].n + 31) / 32) * g[i].batch_count;
+	}
+	return blocks <= 0x7fffffff;
+}
+
+hipError_t gemm_chain4_group_launch(const GemmCall* g, int count, hipStream_t s) {
+	using GroupFn = void (*)(const ChainGroup);
+	static const GroupFn fns[2][4] = {
+	    {sgemm_chain4_group_kernel<false, false, false>, sgemm_chain4_group_kernel<false, true, false>,
+	     sgemm_chain4_group_kernel<true, false, false>, sgemm_chain4_group_kernel<true, true, false>},
+	    {sgemm_chain4_group_kernel<false, false, true>, sgemm_chain4_group_kernel<false, true, true>,
+	     sgemm_chain4_group_kernel<true, false, true>, sgemm_chain4_group_kernel<true, true, true>}};
+	if (!chain4_group_takes(g, count)) return hipErrorInvalidValue;
+	ChainGroup grp{};
+	grp.count = count;
+	bool vec = true;
+	int start = 0;
+	for (int i = 0; i < count; ++i) {
+		grp.p[i] = chain4_args(g[i]);
+		grp.start[i] = start;
+		start += grp.p[i].tiles_m * grp.p[i].tiles_n * grp.p[i].batch_count;
+		vec = vec && chain4_vec(g[i]);
+	}
+	for (int i = count; i <= kChainGroupMax; ++i) grp.start[i] = start;
+	const int f = (g[0].ta ? 2 : 0) + (g[0].tb ? 1 : 0);
+	hipLaunchKernelGGL(fns[vec ? 1 : 0][f], dim3((unsigned)start), dim3(256), 0, s, grp);
 	return hipGetLastError();
 }
 

@@ -225,6 +225,7 @@ __device__ __forceinline__ void chain4_tile(const GemmArgs& p, int block, int wa
 		if (add_old_at_end) v = K > 0 ? Cp[off] + v : Cp[off];
 		if (p.ep.bias_mode == kBiasCol) v = v + p.ep.bias[col];
 		else if (p.ep.bias_mode == kBiasRow) v = v + p.ep.bias[row];
+		if (p.ep.res) v = p.ep.res[oc + off] + v;
 		if (p.ep.relu) {
 			const bool on = v > 0.0f;
 			if (alive) alive[off] = on ? 1 : 0;

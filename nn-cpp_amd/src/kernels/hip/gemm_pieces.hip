@@ -85,6 +85,7 @@ __device__ __forceinline__ void put_output(const GemmArgs& p, float* __restrict_
 	float y = p.accumulate ? Cp[off] + v : v;
 	if (p.ep.bias_mode == kBiasCol) y = y + p.ep.bias[col];
 	else if (p.ep.bias_mode == kBiasRow) y = y + p.ep.bias[row];
+	if (p.ep.res) y = p.ep.res[(Cp - p.c) + off] + y;
 	if (p.ep.relu) {
 		const bool on = y > 0.0f;
 		if (alive) alive[off] = on ? 1 : 0;

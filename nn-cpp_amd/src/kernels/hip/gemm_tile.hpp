@@ -118,6 +118,8 @@ struct Epilogue {
 	int relu;
 	const float* bias;
 	unsigned char* alive;  // optional, addressed like C
+	// optional, addressed like C: added after the bias as res + v, the reference's add(residual, linear(...))
+	const float* res;
 };
 
 // Implicit im2col (src/autograd/ops.cpp:188-212): B is a sample's column matrix col[k][p] of a convolution,
@@ -633,7 +635,7 @@ __device__ __forceinline__ void sgemm_tile_body(const GemmArgs& p, int block) {
 		constexpr int kChunks = RP * WN / 4;        // 4-column groups in one pass
 		constexpr int kRowChunks = WN / 4;
 		float* st = lds + wave * kPerWave;
-		const bool plain = !add_old_at_end && p.ep.bias_mode == kBiasNone && !p.ep.relu;
+		const bool plain = !add_old_at_end && p.ep.bias_mode == kBiasNone && !p.ep.relu && !p.ep.res;
 #pragma unroll
 		for (int i = 0; i < I; ++i)
 #pragma unroll
@@ -674,6 +676,7 @@ __device__ __forceinline__ void sgemm_tile_body(const GemmArgs& p, int block) {
 					for (int e = 0; e < 4; ++e) {
 						if (p.ep.bias_mode == kBiasCol) v[e] = v[e] + p.ep.bias[col + e];
 						else if (p.ep.bias_mode == kBiasRow) v[e] = v[e] + p.ep.bias[row];
+						if (p.ep.res) v[e] = p.ep.res[oc + off + e] + v[e];
 						if (p.ep.relu) {
 							const bool on = v[e] > 0.0f;
 							if (alive) alive[off + e] = on ? 1 : 0;
@@ -701,6 +704,7 @@ __device__ __forceinline__ void sgemm_tile_body(const GemmArgs& p, int block) {
 				if (add_old_at_end) v = (p.k > 0) ? Cp[off] + v : Cp[off];
 				if (p.ep.bias_mode == kBiasCol) v = v + p.ep.bias[col];
 				else if (p.ep.bias_mode == kBiasRow) v = v + p.ep.bias[row];
+				if (p.ep.res) v = p.ep.res[oc + off] + v;
 				if (p.ep.relu) {
 					const bool on = v > 0.0f;
 					if (alive) alive[off] = on ? 1 : 0;

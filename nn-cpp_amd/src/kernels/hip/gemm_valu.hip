@@ -220,6 +220,7 @@ __global__ void __launch_bounds__(256) sgemm_valu_kernel(const GemmArgs p) {
 			if (add_old_at_end) v = Cp[off] + v;
 			if (p.ep.bias_mode == kBiasCol) v = v + p.ep.bias[col];
 			else if (p.ep.bias_mode == kBiasRow) v = v + p.ep.bias[row];
+			if (p.ep.res) v = p.ep.res[oc + off] + v;
 			if (p.ep.relu) {
 				const bool on = v > 0.0f;
 				if (alive) alive[off] = on ? 1 : 0;
@@ -390,6 +391,7 @@ __global__ void __launch_bounds__(256) sgemm_valu_bc_kernel(const GemmArgs p) {
 		if (add_old_at_end) v = Cp[off] + v;
 		if (p.ep.bias_mode == kBiasCol) v = v + p.ep.bias[col];
 		else if (p.ep.bias_mode == kBiasRow) v = v + p.ep.bias[row];
+		if (p.ep.res) v = p.ep.res[oc + off] + v;
 		if (p.ep.relu) {
 			const bool on = v > 0.0f;
 			if (alive) alive[off] = on ? 1 : 0;
@@ -588,6 +590,7 @@ __global__ void __launch_bounds__(256) sgemm_valu_pieces_kernel(const GemmArgs p
 	if (p.accumulate) v = Cp[off] + v;
 	if (p.ep.bias_mode == kBiasCol) v = v + p.ep.bias[col];
 	else if (p.ep.bias_mode == kBiasRow) v = v + p.ep.bias[row];
+	if (p.ep.res) v = p.ep.res[oc + off] + v;
 	if (p.ep.relu) {
 		const bool on = v > 0.0f;
 		if (p.ep.alive) p.ep.alive[oc + off] = on ? 1 : 0;

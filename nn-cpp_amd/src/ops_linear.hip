@@ -71,6 +71,54 @@ int nnh_linear_forward(const float* x, size_t M, size_t K, const float* w, size_
 	return run_gemm(g, stream, -1);
 }
 
+int nnh_linear_forward_multi(const float* x, size_t M, size_t K, int count, const float* const* w, const size_t* n,
+                             const float* const* bias, float* const* y, void* stream) {
+	NumericsScope numerics_scope(stream);
+	if (count < 1 || count > 8) return fail(NNH_ERR_INVALID, "linear multi: count must be 1 to 8");
+	if (!w || !n || !bias || !y) return fail(NNH_ERR_INVALID, "linear multi: null array");
+	GemmCall calls[8];
+	for (int i = 0; i < count; ++i) {
+		if (M > 0 && n[i] > 0 && !bias[i]) return fail(NNH_ERR_INVALID, "bias is null");
+		nnh_epilogue ep{NNH_BIAS_COL, 0, bias[i], nullptr};
+		const int rc = build_gemm(0, 1, M, n[i], K, x, K, w[i], K, y[i], n[i], 0, nullptr, &ep, calls[i]);
+		if (rc != NNH_OK) return rc;
+	}
+	// no output may overlap another output or another layer's weight or bias (build_gemm checked x and its own)
+	for (int i = 0; i < count; ++i)
+		for (int j = 0; j < count; ++j) {
+			if (i == j || M == 0 || n[i] == 0) continue;
+			const uint64_t yb = (uint64_t)M * n[i] * 4;
+			if ((j < i && n[j] > 0 && ranges_overlap(y[i], yb, y[j], (uint64_t)M * n[j] * 4)) ||
+			    ranges_overlap(y[i], yb, w[j], (uint64_t)n[j] * K * 4) || ranges_overlap(y[i], yb, bias[j], n[j] * 4))
+				return fail(NNH_ERR_ALIAS, "linear multi: an output overlaps another layer's output or parameters");
+		}
+	bool grouped = false;
+	if (count >= 2) {
+		const int rc = hip_status(gemm_launch_group(calls, count, reinterpret_cast<hipStream_t>(stream), grouped),
+		                          "linear multi");
+		if (rc != NNH_OK || grouped) return rc;
+	}
+	for (int i = 0; i < count; ++i) {
+		const int rc = run_gemm(calls[i], stream, -1);
+		if (rc != NNH_OK) return rc;
+	}
+	return NNH_OK;
+}
+
+int nnh_linear_forward_add(const float* x, size_t M, size_t K, const float* w, size_t n, const float* bias,
+                           const float* residual, float* y, void* stream) {
+	NumericsScope numerics_scope(stream);
+	if (M > 0 && n > 0 && (!bias || !residual)) return fail(NNH_ERR_INVALID, "bias or residual is null");
+	if (M > 0 && n > 0 && residual != y && ranges_overlap(residual, (uint64_t)M * n * 4, y, (uint64_t)M * n * 4))
+		return fail(NNH_ERR_ALIAS, "residual overlaps y other than in place");
+	nnh_epilogue ep{NNH_BIAS_COL, 0, bias, nullptr};
+	GemmCall g;
+	int rc = build_gemm(0, 1, M, n, K, x, K, w, K, y, n, 0, nullptr, &ep, g);
+	if (rc != NNH_OK) return rc;
+	g.ep.res = residual;
+	return run_gemm(g, stream, -1);
+}
+
 int nnh_linear_backward(const float* g, const float* x, const float* w, const size_t* lead, int nlead, size_t K,
                         size_t n, float* dx, int dx_first, float* dw, int dw_first, float* db, int db_first,
                         void* stream) {

@@ -99,6 +99,65 @@ def test_linear_golden(gpu):
             same(host(t), g[f"linear/{name}/{key}"], (name, key))
 
 
+def test_linear_forward_add(gpu, oracle):
+    """nnh_linear_forward_add: y = residual + linear(x, w, b), bit for bit the oracle's linear and then the float
+    add, on shapes each GEMM route takes (the tile kernel, the VALU kernel, the chain kernel, the pieces kernels and
+    a cut of more than 16 pieces with its partials), with -0, infinities and NaN in the residual, in place (y is the
+    residual), and refused when the residual overlaps y other than in place."""
+    import torch
+
+    import nnh
+    cases = [(1024, 64, 64), (1024, 256, 64), (256, 32, 64), (64, 1024, 64), (33, 2048, 70), (16, 4096, 16),
+             (512, 512, 512), (7, 5, 3)]
+    for ci, (M, K, n) in enumerate(cases):
+        x = synth.mt19937_uniform(3000 + ci, M * K).reshape(M, K)
+        w = synth.mt19937_uniform(3100 + ci, n * K).reshape(n, K)
+        b = synth.mt19937_uniform(3200 + ci, n)
+        r = synth.normal(3300 + ci, (M, n))
+        r[0, : min(n, 4)] = [-0.0, np.inf, -np.inf, np.nan][: min(n, 4)]
+        want = r + oracle.linear_forward(x, w, b)
+        got = nnh.linear_forward_add(dev(x), dev(w), dev(b), dev(r))
+        assert_same(host(got), want, ("linear + residual", M, K, n), nan_equal=True)
+        rd = dev(r)
+        nnh.linear_forward_add(dev(x), dev(w), dev(b), rd, out=rd)
+        assert_same(host(rd), want, ("in place", M, K, n), nan_equal=True)
+    L = nnh.lib()
+    buf = torch.zeros(2 * 64 * 64 + 64, device="cuda")
+    x, w, b = dev(np.ones((64, 64), np.float32)), dev(np.ones((64, 64), np.float32)), dev(np.ones(64, np.float32))
+    rc = L.nnh_linear_forward_add(nnh._ptr(x), 64, 64, nnh._ptr(w), 64, nnh._ptr(b), nnh._ptr(buf),
+                                  nnh._ptr(buf, 64), nnh._stream(None))
+    assert rc == nnh.ERR_ALIAS
+
+
+def test_linear_forward_multi(gpu, oracle):
+    """nnh_linear_forward_multi: several linear layers over one input, each output the oracle's linear bit for bit:
+    three projections of one width (one launch on the chain kernel), of different widths, with ragged tiles, a
+    single layer, four layers and a depth past the group's limit (each in turn); outputs that overlap are refused."""
+    import torch
+
+    import nnh
+    cases = [((16, 64, 64), [64, 64, 64]), ((100, 48), [64, 32, 16]), ((37, 20), [7, 9]), ((64, 64), [64]),
+             ((64, 64), [16, 16, 16, 16]), ((64, 512), [32, 32, 32])]
+    for ci, (xs, ns) in enumerate(cases):
+        K = xs[-1]
+        x = synth.mt19937_uniform(3400 + ci, int(np.prod(xs))).reshape(xs)
+        layers = [(synth.mt19937_uniform(3500 + 10 * ci + i, n * K).reshape(n, K),
+                   synth.mt19937_uniform(3600 + 10 * ci + i, n)) for i, n in enumerate(ns)]
+        ys = nnh.linear_forward_multi(dev(x), [(dev(w), dev(b)) for w, b in layers])
+        for i, (w, b) in enumerate(layers):
+            same(host(ys[i]), oracle.linear_forward(x, w, b), (xs, ns, i))
+    L = nnh.lib()
+    x, w, b = dev(np.ones((64, 64), np.float32)), dev(np.ones((64, 64), np.float32)), dev(np.ones(64, np.float32))
+    buf = torch.zeros(64 * 64 + 64 * 32, device="cuda")
+    vp = nnh._vp
+    ws = (vp * 2)(w.data_ptr(), w.data_ptr())
+    bs = (vp * 2)(b.data_ptr(), b.data_ptr())
+    ys = (vp * 2)(buf.data_ptr(), buf.data_ptr() + 4 * 64 * 32)
+    import ctypes as C
+    ns = (C.c_size_t * 2)(64, 64)
+    assert L.nnh_linear_forward_multi(nnh._ptr(x), 64, 64, 2, ws, ns, bs, ys, nnh._stream(None)) == nnh.ERR_ALIAS
+
+
 def test_linear_first_write_overwrites(gpu, oracle):
     """A fresh gradient is overwritten (sgemm without accumulate; bias s + 0.0f): garbage in the buffer
     must not leak into the result."""
