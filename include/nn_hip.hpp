@@ -104,6 +104,7 @@ struct NodeImpl {
 	Tensor grad;
 	bool grad_fresh = false;
 	bool requires_grad = false;
+	size_t consumers = 0;  // uses as a parent in the graph of the last backward() that reached this node
 	std::vector<Value> parents;
 	std::function<void(const Tensor&)> backward_fn;
 };
@@ -201,6 +202,11 @@ Value gelu(const Value& x);
 // host: TensorShapeError otherwise); the result has ids' shape plus D. The device-tensor form reads the ids back.
 Value embedding(const Value& weight, const std::vector<float>& ids, const std::vector<size_t>& ids_shape);
 Value embedding(const Value& weight, const Tensor& ids);
+// add(embedding(weight, ids), addend) with the addend (of the output's trailing axes: a transformer's positions)
+// added in the lookup's kernel: the nodes and bits of the two ops.
+Value embedding_add(const Value& weight, const std::vector<float>& ids, const std::vector<size_t>& ids_shape,
+                    const Value& addend);
+Value embedding_add(const Value& weight, const Tensor& ids, const Value& addend);
 // positional.cpp:15-25: the fixed sinusoidal table {max_len, dim}, computed in double on the host and stored as fp32.
 Tensor sinusoidal_table(size_t max_len, size_t dim);
 

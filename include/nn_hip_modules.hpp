@@ -146,6 +146,8 @@ class Embedding : public Module {
 public:
 	Embedding(size_t num_embeddings, size_t dim);
 	Value forward(const Value& ids) override;
+	// add(forward(ids), addend) in one kernel (embedding_add)
+	Value forward_add(const Value& ids, const Value& addend);
 	std::vector<Value> parameters() const override;
 	std::vector<std::pair<std::string, Value>> named_parameters() const override;
 
@@ -159,6 +161,8 @@ class PositionalEncoding : public Module {
 public:
 	PositionalEncoding(size_t max_len, size_t dim, bool learned = false);
 	Value forward(const Value& input) override;
+	// the addend forward adds to a {N, T, dim} input: the table's first T rows (the same node forward builds)
+	Value rows(size_t T);
 	std::vector<Value> parameters() const override;
 	std::vector<std::pair<std::string, Value>> named_parameters() const override;
 

@@ -428,6 +428,12 @@ int nnh_gelu_backward(const float* x, const float* tanh_saved, const float* g, s
  * of range here reads a clamped row). */
 int nnh_embedding_forward(const float* weight, size_t V, size_t D, const int* rows, size_t count, float* y,
                           void* stream);
+/* nn::embedding, then nn::add(that, addend) with the addend {addend_rows, D} broadcast over the leading rows (row i
+ * takes addend row i % addend_rows: a transformer's token embedding plus its positions, ops.cpp:1991-2015 and
+ * 333-336) in one kernel, the bits of the two ops. No single counterpart in the reference. addend_rows divides count;
+ * y overlaps none of the inputs. */
+int nnh_embedding_add_forward(const float* weight, size_t V, size_t D, const int* rows, size_t count,
+                              const float* addend, size_t addend_rows, float* y, void* stream);
 /* Its backward rule: dweight (first: zero-filled first) += g row i at row rows[i], for i in order. */
 int nnh_embedding_backward(const float* g, const int* rows, size_t count, size_t V, size_t D, float* dweight, int first,
                            void* stream);

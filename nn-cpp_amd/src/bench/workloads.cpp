@@ -53,7 +53,8 @@ const std::vector<std::vector<size_t>>& param_shapes(int model) {
 // (attention.cpp:31-35) and LayerNorm's default eps 1e-5; dropout 0 leaves every Dropout the identity.
 Value transformer_forward(const std::vector<float>& ids, size_t N, const std::vector<Value>& p, const Value& pe) {
 	const Tensor no_mask;
-	Value h = nn::hip::add(nn::hip::embedding(p[0], ids, {N, kMaxLen}), pe);
+	// add(embedding(...), pe) with the positions added in the lookup's kernel (the same nodes and bits)
+	Value h = nn::hip::embedding_add(p[0], ids, {N, kMaxLen}, pe);
 	size_t i = 1;
 	for (size_t l = 0; l < kLayers; ++l, i += 16) {
 		const Value a = nn::hip::layernorm(h, p[i], p[i + 1], 1e-5f);

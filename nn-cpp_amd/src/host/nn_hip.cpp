@@ -277,11 +277,15 @@ void Value::backward(const Tensor& seed) const {
 		for (const Value& p : v.impl()->parents)
 			if (!expanded.count(p.impl())) stack.push_back(p);
 	}
-	for (const Value& v : topo)
+	for (const Value& v : topo) {
+		v.impl()->consumers = 0;
 		if (v.impl()->backward_fn) {
 			if (v.impl()->grad.shape() != v.impl()->data.shape()) v.impl()->grad = Tensor::empty(v.impl()->data.shape());
 			v.impl()->grad_fresh = true;
 		}
+	}
+	for (const Value& v : topo)
+		for (const Value& p : v.impl()->parents) ++p.impl()->consumers;
 	if (impl_->grad.shape() != impl_->data.shape()) impl_->grad = Tensor::empty(impl_->data.shape());
 	if (seed.size())
 		check_hip(hipMemcpyAsync(impl_->grad.data(), seed.data(), seed.size() * 4, hipMemcpyDeviceToDevice, g_stream),
@@ -298,6 +302,17 @@ namespace {
 float* grad_if(const Value& v, bool& first) {
 	first = false;
 	return v.requires_grad() ? v.grad_accum(first).data() : nullptr;
+}
+
+// A pass-through rule (add, reshape) hands its gradient g to an operand that is an intermediate node, used only by
+// this node and not yet written: the operand's gradient takes g's storage (the values a store of g would give,
+// nothing is written to it later), instead of a copy. Returns whether it did.
+bool take_grad(const Value& v, const Tensor& g) {
+	NodeImpl* n = v.impl();
+	if (!n->requires_grad || !n->backward_fn || !n->grad_fresh || n->consumers != 1) return false;
+	n->grad = g.reshape(n->data.shape());
+	n->grad_fresh = false;
+	return true;
 }
 
 // A byte or uint32 side buffer an op keeps for its backward (conv's alive flags, pooling's argmax).
@@ -474,6 +489,7 @@ Value relu(const Value& x) {
 Value reshape(const Value& x, std::vector<size_t> new_shape) {
 	Tensor y = x.data().reshape(std::move(new_shape));
 	return Value::node(std::move(y), {x}, [x](const Tensor& g) {
+		if (take_grad(x, g)) return;
 		bool first = false;
 		float* dx = grad_if(x, first);
 		if (dx) check(nnh_add_to_grad(dx, g.data(), g.size(), first, g_stream));
@@ -646,7 +662,16 @@ Value add_node(const Value& a, const Value& b, Tensor y) {
 		const auto& gs = g.shape();
 		const size_t lead = gs.size() - b.data().ndim();
 		bool first = false, first_b = false;
-		float* da = grad_if(a, first);
+		// an operand used only here takes g's storage (a.impl() == b.impl() counts two uses)
+		const bool took_a = take_grad(a, g);
+		const bool took_b = lead == 0 && take_grad(b, g);
+		if (took_a || took_b) {
+			if (!took_a) {
+				if (float* da = grad_if(a, first)) check(nnh_add_to_grad(da, g.data(), g.size(), first, g_stream));
+			}
+			if (took_b) return;
+		}
+		float* da = took_a ? nullptr : grad_if(a, first);
 		if (lead == 0 && da && a.impl() != b.impl()) {
 			// both operands of the output's shape: both gradients in one launch
 			if (float* db = grad_if(b, first_b)) {
@@ -786,7 +811,11 @@ Value gelu(const Value& x) {
 	});
 }
 
-Value embedding(const Value& weight, const std::vector<float>& ids, const std::vector<size_t>& ids_shape) {
+namespace {
+
+// embedding, or embedding_add with addend (its rows broadcast over the ids), as the nodes of the separate ops
+Value embedding_op(const Value& weight, const std::vector<float>& ids, const std::vector<size_t>& ids_shape,
+                   const Value* addend) {
 	const auto& ws = weight.data().shape();
 	// ops.cpp:1992-2001
 	if (ws.size() != 2) throw TensorShapeError("nn::hip: embedding weight must be {V, D}");
@@ -811,13 +840,42 @@ Value embedding(const Value& weight, const std::vector<float>& ids, const std::v
 		synchronize();  // rows is released on return
 	}
 	const size_t count = rows.size();
-	check(nnh_embedding_forward(weight.data().data(), V, D, static_cast<const int*>(rb->p), count, y.data(), g_stream));
-	return Value::node(std::move(y), {weight}, [weight, rb, count, V, D](const Tensor& g) {
+	// the addend's shape must be trailing axes of the output's (add's rule), its rows dividing the ids' count
+	const bool fuse = addend && addend->data().ndim() >= 1 && addend->data().ndim() <= out.size() &&
+	                  std::equal(addend->data().shape().begin(), addend->data().shape().end(),
+	                             out.end() - addend->data().ndim()) &&
+	                  addend->data().size() > 0;
+	if (fuse)
+		check(nnh_embedding_add_forward(weight.data().data(), V, D, static_cast<const int*>(rb->p), count,
+		                                addend->data().data(), addend->data().size() / std::max<size_t>(D, 1), y.data(),
+		                                g_stream));
+	else
+		check(nnh_embedding_forward(weight.data().data(), V, D, static_cast<const int*>(rb->p), count, y.data(),
+		                            g_stream));
+	Value e = Value::node(y, {weight}, [weight, rb, count, V, D](const Tensor& g) {
 		// ops.cpp:2008-2014: weight.grad() (zeroed when fresh) gets the rows added in token order
 		bool first = false;
 		float* dw = grad_if(weight, first);
 		if (dw) check(nnh_embedding_backward(g.data(), static_cast<const int*>(rb->p), count, V, D, dw, first, g_stream));
 	});
+	if (!addend) return e;
+	// the embedding node (whose backward does not read its data) and the add node over it
+	return fuse ? add_node(e, *addend, y) : add(e, *addend);
+}
+
+}  // namespace
+
+Value embedding(const Value& weight, const std::vector<float>& ids, const std::vector<size_t>& ids_shape) {
+	return embedding_op(weight, ids, ids_shape, nullptr);
+}
+
+Value embedding_add(const Value& weight, const std::vector<float>& ids, const std::vector<size_t>& ids_shape,
+                    const Value& addend) {
+	return embedding_op(weight, ids, ids_shape, &addend);
+}
+
+Value embedding_add(const Value& weight, const Tensor& ids, const Value& addend) {
+	return embedding_add(weight, ids.to_host(), ids.shape(), addend);
 }
 
 Value embedding(const Value& weight, const Tensor& ids) {

@@ -173,6 +173,7 @@ Embedding::Embedding(size_t num_embeddings, size_t dim)
 	: weight_(Value::leaf(Tensor::random({num_embeddings, dim}, -bound(dim), bound(dim)), true)) {}
 
 Value Embedding::forward(const Value& ids) { return embedding(weight_, ids.data()); }
+Value Embedding::forward_add(const Value& ids, const Value& addend) { return embedding_add(weight_, ids.data(), addend); }
 std::vector<Value> Embedding::parameters() const { return {weight_}; }
 std::vector<std::pair<std::string, Value>> Embedding::named_parameters() const { return {{"weight", weight_}}; }
 
@@ -187,7 +188,11 @@ Value PositionalEncoding::forward(const Value& input) {
 	const auto& s = input.data().shape();
 	if (s.size() != 3 || s[1] > max_len_ || s[2] != dim_)
 		throw TensorShapeError("nn::hip: PositionalEncoding takes {N, T <= max_len, dim}");
-	return add(input, slice(pe_, 0, 0, s[1]));
+	return add(input, rows(s[1]));
+}
+Value PositionalEncoding::rows(size_t T) {
+	if (T > max_len_) throw TensorShapeError("nn::hip: PositionalEncoding takes {N, T <= max_len, dim}");
+	return slice(pe_, 0, 0, T);
 }
 std::vector<Value> PositionalEncoding::parameters() const {
 	return learned_ ? std::vector<Value>{pe_} : std::vector<Value>{};
@@ -376,7 +381,9 @@ Transformer::Transformer(const TransformerConfig& c)
 }
 
 Value Transformer::forward(const Value& ids) {
-	Value h = pos_.forward(embed_.forward(ids));
+	// pos(embed(ids)) with the positions added in the lookup's kernel for {N, T} ids (the same nodes and bits)
+	const auto& is = ids.data().shape();
+	Value h = is.size() == 2 ? embed_.forward_add(ids, pos_.rows(is[1])) : pos_.forward(embed_.forward(ids));
 	for (auto& b : blocks_) h = b->forward(h);
 	return head_.forward(ln_f_.forward(h));
 }

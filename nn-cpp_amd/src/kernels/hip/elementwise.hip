@@ -91,14 +91,18 @@ __global__ void __launch_bounds__(256) gelu_backward_kernel(const float* __restr
 }
 
 // ops.cpp:2006-2007: out row i = weight row rows[i] (rows clamped into the table; the caller validates them).
+// add (optional): add(embedding, addend) with the addend's rows broadcast over the ids (ops.cpp:333-336), row i
+// taking addend row i % add_rows: out = w[row] + addend, the add's bits.
 __global__ void __launch_bounds__(256) embedding_forward_kernel(const float* __restrict__ w, int64_t V, int64_t D,
                                                                 const int* __restrict__ rows, int64_t count,
-                                                                float* __restrict__ out) {
+                                                                float* __restrict__ out, const float* __restrict__ add,
+                                                                int64_t add_rows) {
 	const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
 	if (e >= count * D) return;
 	const int64_t i = e / D, d = e - i * D;
 	const int64_t r = min<int64_t>(max(rows[i], 0), V - 1);
-	out[e] = w[r * D + d];
+	const float v = w[r * D + d];
+	out[e] = add ? v + add[(i % add_rows) * D + d] : v;
 }
 
 // ops.cpp:2008-2014: the gradient table (first: zeros) gets, for i in order, the output gradient's row i added to
@@ -214,9 +218,10 @@ hipError_t gelu_backward(const float* x, const float* th, const float* g, int64_
 }
 
 hipError_t embedding_forward(const float* w, int64_t V, int64_t D, const int* rows, int64_t count, float* out,
-                             hipStream_t s) {
+                             hipStream_t s, const float* add, int64_t add_rows) {
 	if (count * D == 0) return hipSuccess;
-	hipLaunchKernelGGL(embedding_forward_kernel, dim3(blocks_of(count * D)), dim3(256), 0, s, w, V, D, rows, count, out);
+	hipLaunchKernelGGL(embedding_forward_kernel, dim3(blocks_of(count * D)), dim3(256), 0, s, w, V, D, rows, count, out,
+	                   add, add_rows);
 	return hipGetLastError();
 }
 

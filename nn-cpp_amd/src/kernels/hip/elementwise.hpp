@@ -18,8 +18,9 @@ hipError_t gelu_forward(const float* x, int64_t count, float* y, float* th, hipS
 hipError_t gelu_backward(const float* x, const float* th, const float* g, int64_t count, float* dx, int first,
                          hipStream_t s);
 // nn::embedding (ops.cpp:1991-2015) with validated rows (0 <= rows[i] < V).
+// add (optional): the addend {add_rows, D} broadcast over the ids and added after the lookup.
 hipError_t embedding_forward(const float* w, int64_t V, int64_t D, const int* rows, int64_t count, float* out,
-                             hipStream_t s);
+                             hipStream_t s, const float* add = nullptr, int64_t add_rows = 1);
 hipError_t embedding_backward(const float* g, const int* rows, int64_t count, int64_t V, int64_t D, float* dw, int first,
                               hipStream_t s);
 

@@ -67,6 +67,24 @@ int nnh_gelu_backward(const float* x, const float* tanh_saved, const float* g, s
 	                  "gelu backward");
 }
 
+int nnh_embedding_add_forward(const float* weight, size_t V, size_t D, const int* rows, size_t count,
+                              const float* addend, size_t addend_rows, float* y, void* stream) {
+	uint64_t out = 0;
+	if (!count_ok({V, D}) || !count_ok({count, D}, out) || !count_ok({addend_rows, D}))
+		return fail(NNH_ERR_INVALID, "embedding add: size out of range (above 2^60 elements)");
+	if (out == 0) return NNH_OK;
+	if (V == 0) return fail(NNH_ERR_SHAPE, "embedding: empty table");  // every id is out of range (ops.cpp:1999)
+	if (addend_rows == 0 || count % addend_rows != 0)
+		return fail(NNH_ERR_SHAPE, "embedding add: the addend's rows must divide the ids' count");
+	if (!weight || !rows || !y || !addend) return fail(NNH_ERR_INVALID, "embedding add: null pointer");
+	if (ranges_overlap(y, out * 4, weight, (uint64_t)V * D * 4) || ranges_overlap(y, out * 4, rows, (uint64_t)count * 4) ||
+	    ranges_overlap(y, out * 4, addend, (uint64_t)addend_rows * D * 4))
+		return fail(NNH_ERR_ALIAS, "embedding add: y overlaps the table, the rows or the addend");
+	return hip_status(embedding_forward(weight, (int64_t)V, (int64_t)D, rows, (int64_t)count, y,
+	                                    reinterpret_cast<hipStream_t>(stream), addend, (int64_t)addend_rows),
+	                  "embedding add");
+}
+
 int nnh_embedding_forward(const float* weight, size_t V, size_t D, const int* rows, size_t count, float* y,
                           void* stream) {
 	uint64_t out = 0;

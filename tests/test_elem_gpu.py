@@ -134,6 +134,16 @@ def test_embedding_bitwise(gpu, oracle, V, D, count, offset):
                                        1, nnh._stream(None)))
     torch.cuda.synchronize()
     assert_same(host(y, offset, (count, D)), w[rows], "embedding y")
+    # with an addend broadcast over the rows (a transformer's positions): the lookup, then the float add
+    T = max([t for t in range(1, 65) if count % t == 0] or [1])
+    pe = rng.normal(size=(T, D)).astype(np.float32)
+    ped = dev(pe, offset)
+    y2 = dev(np.full((count, D), np.nan, np.float32), offset)
+    nnh.check(L.nnh_embedding_add_forward(nnh._ptr(wd, offset), V, D, nnh._ptr(rd, offset), count, nnh._ptr(ped, offset),
+                                          T, nnh._ptr(y2, offset), nnh._stream(None)))
+    torch.cuda.synchronize()
+    if count:
+        assert_same(host(y2, offset, (count, D)), w[rows] + np.tile(pe, (count // T, 1)), "embedding + addend")
     want = oracle.embedding_backward(g, rows, V, D)
     assert_same(host(dw, offset, (V, D)), want, "embedding dw")
     nnh.check(L.nnh_embedding_backward(nnh._ptr(gd, offset), nnh._ptr(rd, offset), count, V, D, nnh._ptr(dw, offset),
@@ -153,6 +163,13 @@ def test_embedding_errors(gpu):
         nnh.check(L.nnh_embedding_forward(nnh._ptr(t), 0, 4, nnh._ptr(r), 4, nnh._ptr(t), nnh._stream(None)))
     with pytest.raises(nnh.NnhError):  # y over the table
         nnh.check(L.nnh_embedding_forward(nnh._ptr(t), 4, 4, nnh._ptr(r), 2, nnh._ptr(t, 8), nnh._stream(None)))
+    p = torch.zeros(64, device="cuda")
+    with pytest.raises(nnh.ShapeError):  # the addend's rows must divide the ids' count
+        nnh.check(L.nnh_embedding_add_forward(nnh._ptr(t), 4, 4, nnh._ptr(r), 4, nnh._ptr(p), 3, nnh._ptr(t, 32),
+                                              nnh._stream(None)))
+    with pytest.raises(nnh.NnhError):  # y over the addend
+        nnh.check(L.nnh_embedding_add_forward(nnh._ptr(t), 4, 4, nnh._ptr(r), 4, nnh._ptr(p), 2, nnh._ptr(p, 4),
+                                              nnh._stream(None)))
 
 
 def test_embedding_backward_keeps_negative_zero(gpu, oracle):
