@@ -116,6 +116,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) a
 	const float* vp = a.v + (int64_t)n * tk * a.d + h * kDh;
 	const float* padrow = a.pad ? a.pad + (int64_t)n * tk : nullptr;
 	if (tid < 32) table[tid] = kExp2Table[tid];
+	const bool pv4 = tk % 16 == 0;  // O = P V on the 16x16x4 MFMA (P kept in LDS in its permuted layout)
 
 	// 0, 1. S^T for keys 64w + l against queries 32u + (l & 31), u = 0, 1 (fma(k, q, acc) is the reference's
 	// fma(q, k, acc))
@@ -248,19 +249,119 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) a
 	{
 		float* pr = a.probs + ((int64_t)nh * a.tq + i0) * tk;
 		const unsigned quads = (unsigned)(nq * (tk / 4));
-		for (unsigned e = tid; e < quads; e += 256) {
-			const unsigned row = fdiv(e, a.quads);
-			const int j = (int)(e - row * a.quads.d) * 4;
-			float* o = sm + row * ldp + j;
-			const f32x4 x = *reinterpret_cast<const f32x4*>(o);
-			float y[4] = {x[0], x[1], x[2], x[3]};
-			div_n_by_row_sum(y, rowsum[row], rowinv[row]);
-			const f32x4 y4 = {y[0], y[1], y[2], y[3]};
-			*reinterpret_cast<f32x4*>(o) = y4;
-			*reinterpret_cast<f32x4*>(pr + (int64_t)row * tk + j) = y4;
+		if (pv4) {
+			// the 16x16x4 product below reads each row permuted, key j at j % 4 (Tk / 4) + j / 4: every quad is read
+			// and divided first, then, after a barrier, written back in that order (at most kRows Tk / 1024 quads a
+			// thread)
+			constexpr int kPer = kRows * kMaxKeys / 4 / 256;
+			f32x4 yv[kPer];
+#pragma unroll
+			for (int u = 0; u < kPer; ++u) {
+				const unsigned e = tid + 256 * u;
+				if (e < quads) {
+					const unsigned row = fdiv(e, a.quads);
+					const int j = (int)(e - row * a.quads.d) * 4;
+					const f32x4 x = *reinterpret_cast<const f32x4*>(sm + row * ldp + j);
+					float y[4] = {x[0], x[1], x[2], x[3]};
+					div_n_by_row_sum(y, rowsum[row], rowinv[row]);
+					yv[u] = f32x4{y[0], y[1], y[2], y[3]};
+					*reinterpret_cast<f32x4*>(pr + (int64_t)row * tk + j) = yv[u];
+				}
+			}
+			__syncthreads();
+#pragma unroll
+			for (int u = 0; u < kPer; ++u) {
+				const unsigned e = tid + 256 * u;
+				if (e < quads) {
+					const unsigned row = fdiv(e, a.quads);
+					const int jq = (int)(e - row * a.quads.d);
+#pragma unroll
+					for (int c = 0; c < 4; ++c) sm[row * ldp + c * (tk >> 2) + jq] = yv[u][c];
+				}
+			}
+		} else {
+			for (unsigned e = tid; e < quads; e += 256) {
+				const unsigned row = fdiv(e, a.quads);
+				const int j = (int)(e - row * a.quads.d) * 4;
+				float* o = sm + row * ldp + j;
+				const f32x4 x = *reinterpret_cast<const f32x4*>(o);
+				float y[4] = {x[0], x[1], x[2], x[3]};
+				div_n_by_row_sum(y, rowsum[row], rowinv[row]);
+				const f32x4 y4 = {y[0], y[1], y[2], y[3]};
+				*reinterpret_cast<f32x4*>(o) = y4;
+				*reinterpret_cast<f32x4*>(pr + (int64_t)row * tk + j) = y4;
+			}
 		}
 	}
 	__syncthreads();
+
+	if (pv4) {
+		// 3. O columns 16w .. 16w+15 for the 64 rows on the 16x16x4 MFMA (Mfma<kMf16x4>: four keys per instruction,
+		// bit for bit four fmas in key order): four 16-row tiles, four independent chains over every key. At step s
+		// lane (g, i) supplies P[16 t + i][4 s + g], read four steps at a time from the permuted rows (positions
+		// g Tk / 4 + s), and V[4 s + g][16 w + i], loaded 16 steps ahead.
+		using M4 = Mfma<kMf16x4>;
+		const int g = lane >> 4, il = lane & 15, q4 = tk >> 2;
+		M4::Acc acc4[4];
+#pragma unroll
+		for (int t = 0; t < 4; ++t) acc4[t] = M4::Acc{0.0f, 0.0f, 0.0f, 0.0f};
+		const float* vcol = vp + 16 * wave + il;
+		const float* pbase = sm + il * ldp + g * q4;
+		auto load_v = [&](float (&dst)[16], int s0) {  // steps s0 .. s0 + 15 (clamped rows are loaded, never used)
+#pragma unroll
+			for (int u = 0; u < 16; ++u) dst[u] = vcol[(int64_t)min(4 * (s0 + u) + g, tk - 1) * a.d];
+		};
+		auto load_p = [&](f32x4 (&dst)[4], int s0) {  // steps s0 .. s0 + 3 of the four tiles
+#pragma unroll
+			for (int t = 0; t < 4; ++t) dst[t] = *reinterpret_cast<const f32x4*>(pbase + 16 * t * ldp + min(s0, q4 - 4));
+		};
+		float v0[16], v1[16];
+		f32x4 pa[4], pb[4];
+		auto chunk = [&](const float (&v)[16], int s0) {  // 16 steps from s0, P one group of four steps ahead
+			load_p(pa, s0);
+#pragma unroll
+			for (int h4 = 0; h4 < 4; ++h4) {
+				f32x4 (&cur)[4] = (h4 & 1) ? pb : pa;
+				f32x4 (&nxt)[4] = (h4 & 1) ? pa : pb;
+				if (h4 < 3) load_p(nxt, s0 + 4 * (h4 + 1));
+#pragma unroll
+				for (int e = 0; e < 4; ++e)
+#pragma unroll
+					for (int t = 0; t < 4; ++t) acc4[t] = M4::mma(cur[t][e], v[4 * h4 + e], acc4[t]);
+			}
+		};
+		// tk % 16 == 0: q4 is a multiple of 4, whole groups of four steps; chunks of 16 steps, V two chunks ahead
+		load_v(v0, 0);
+		load_v(v1, 16);
+		int s0 = 0;
+		for (; s0 + 32 <= q4; s0 += 32) {
+			chunk(v0, s0);
+			load_v(v0, s0 + 32);
+			chunk(v1, s0 + 16);
+			load_v(v1, s0 + 48);
+		}
+		// the rest: fewer than 32 steps, in groups of four
+		for (; s0 < q4; s0 += 4) {
+			float vv[16];
+			f32x4 pp[4];
+			load_p(pp, s0);
+#pragma unroll
+			for (int e = 0; e < 4; ++e) vv[e] = vcol[(int64_t)(4 * (s0 + e) + g) * a.d];
+#pragma unroll
+			for (int e = 0; e < 4; ++e)
+#pragma unroll
+				for (int t = 0; t < 4; ++t) acc4[t] = M4::mma(pp[t][e], vv[e], acc4[t]);
+		}
+		float* op = a.out + ((int64_t)n * a.tq + i0) * a.d + h * kDh + 16 * wave + il;
+#pragma unroll
+		for (int t = 0; t < 4; ++t)
+#pragma unroll
+			for (int r = 0; r < 4; ++r) {
+				const int row = 16 * t + 4 * g + r;
+				if (row < nq) op[(int64_t)row * a.d] = acc4[t][r];
+			}
+		return;
+	}
 
 	// 3. O columns 16w .. 16w+15 for the 64 rows: the chain over every key in order
 	M16::Acc o;
