@@ -116,6 +116,11 @@ FUSED_SHAPES = [  # (N, Tq, Tk, heads, causal, masked)
     (2, 100, 100, 2, True, True),
     (1, 130, 252, 3, False, True),
     (2, 256, 256, 2, True, True),
+    # Tk a multiple of 16: O = P V on 16x16x4 (ragged and whole 64-row blocks, key counts that are not a multiple of
+    # 64)
+    (2, 48, 160, 2, False, True),
+    (1, 16, 16, 1, True, False),
+    (1, 112, 240, 1, False, False),
 ]
 # The three-launch path: key count not a multiple of 4, more than 256 keys, head width 32.
 UNFUSED_SHAPES = [  # (N, Tq, Tk, heads, Dh, causal, masked)
@@ -324,6 +329,30 @@ def test_head64_dq_dk_accumulate_subsets_and_one_node(gpu, oracle):
             L.oracle_attention_backward(_fp(g), _fp(x), _fp(x), _fp(x), _fp(px), N, T, T, D, H, _fp(mask), int(causal),
                                         _fp(want), int(dq_first), _fp(want), int(dk_first), _fp(want), int(dv_first))
             same(host(grad), want, (causal, dv_first, dq_first, dk_first, "one node"))
+
+
+def test_head64_dq_dk_accumulate_whole_blocks(gpu, oracle):
+    """dQ and dK of head width 64 with Tq and Tk multiples of 16 (whole 16-row tiles): added to old gradients and
+    stored fresh, causal and padded, against the oracle."""
+    import nnh
+    from pyoracle import _fp
+    L = oracle.lib
+    N, T, H = 2, 96, 2
+    D = 64 * H
+    q, k, v, mask = attention_case(130, N, T, T, D, True)
+    g = synth.normal(135, (N, T, D))
+    for causal in (False, True):
+        _, p = oracle.attention_forward(q, k, v, H, mask, causal)
+        for first in (False, True):
+            dq0, dk0 = synth.normal(136, q.shape), synth.normal(137, k.shape)
+            dq, dk = dev(dq0), dev(dk0)
+            nnh.attention_backward(dev(g), dev(q), dev(k), dev(v), dev(p), H, dev(mask), causal, dq, first, dk, first,
+                                   None, True)
+            wq, wk = dq0.copy(), dk0.copy()
+            L.oracle_attention_backward(_fp(g), _fp(q), _fp(k), _fp(v), _fp(p), N, T, T, D, H, _fp(mask), int(causal),
+                                        _fp(wq), int(first), _fp(wk), int(first), None, 1)
+            same(host(dq), wq, (causal, first, "dq"))
+            same(host(dk), wk, (causal, first, "dk"))
 
 
 def test_attention_hand_reference_and_masks(gpu):
