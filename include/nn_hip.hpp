@@ -159,6 +159,8 @@ Value linear_relu(const Value& x, const Value& weight, const Value& bias);
 // add(residual, linear(x, weight, bias)) with the add in the linear's epilogue (one kernel): the same two nodes and
 // bits. A residual of another shape runs the two ops.
 Value linear_add(const Value& x, const Value& weight, const Value& bias, const Value& residual);
+// gelu(linear(x, weight, bias)) with the GELU in the linear's epilogue: the same two nodes and bits.
+Value linear_gelu(const Value& x, const Value& weight, const Value& bias);
 // linear(x, w_i, b_i) for each (w_i, b_i) of layers (an attention layer's q, k and v projections): the nodes and bits
 // of the separate calls, in one launch where the shapes allow.
 std::vector<Value> linear_many(const Value& x, const std::vector<std::pair<Value, Value>>& layers);

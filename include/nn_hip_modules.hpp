@@ -73,6 +73,8 @@ public:
 	Value forward_relu(const Value& input) override { return linear_relu(input, weight_, bias_); }
 	// add(residual, forward(input)) in one kernel (linear_add)
 	Value forward_add(const Value& input, const Value& residual) { return linear_add(input, weight_, bias_, residual); }
+	// gelu(forward(input)) in one kernel (linear_gelu)
+	Value forward_gelu(const Value& input) { return linear_gelu(input, weight_, bias_); }
 	std::vector<Value> parameters() const override;
 	std::vector<std::pair<std::string, Value>> named_parameters() const override;
 	const Value& weight() const { return weight_; }

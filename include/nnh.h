@@ -193,6 +193,14 @@ int nnh_linear_forward(const float* x, size_t M, size_t K, const float* w, size_
 int nnh_linear_forward_add(const float* x, size_t M, size_t K, const float* w, size_t n, const float* bias,
                            const float* residual, float* y, void* stream);
 /*
+ * nn::linear, then nn::gelu on its output (ops.cpp:714-730, 451-466: a transformer block's fc1 and activation) in one
+ * kernel where the product has no depth cut: h {M, n} = x w^T + bias (the GELU's input, which its backward reads),
+ * y = gelu(h) and tanh_saved as nnh_gelu_forward leaves them, the bits of the two ops. No single counterpart in the
+ * reference. y and tanh_saved overlap neither each other, h, nor the inputs.
+ */
+int nnh_linear_gelu_forward(const float* x, size_t M, size_t K, const float* w, size_t n, const float* bias, float* h,
+                            float* y, float* tanh_saved, void* stream);
+/*
  * count (1 to 8) nn::linear forwards over one input (ops.cpp:714-730: an attention layer's q, k and v projections):
  * y[i] {M, n[i]} = x w[i]^T + bias[i], the bits of count separate calls, in one launch where the shapes allow (two or
  * three products, each at most 2^20 outputs and 256 deep). No single counterpart in the reference. No output may

@@ -107,6 +107,7 @@ _EXTRA_DECLS = {
     "nnh_add_to_grad": [_vp, _vp, _sz, C.c_int, _vp],
     "nnh_add_to_grad2": [_vp, C.c_int, _vp, C.c_int, _vp, _sz, _vp],
     "nnh_linear_forward_add": [_vp, _sz, _sz, _vp, _sz, _vp, _vp, _vp, _vp],
+    "nnh_linear_gelu_forward": [_vp, _sz, _sz, _vp, _sz, _vp, _vp, _vp, _vp, _vp],
     "nnh_embedding_add_forward": [_vp, _sz, _sz, _vp, _sz, _vp, _sz, _vp, _vp],
     "nnh_linear_forward_multi": [_vp, _sz, _sz, C.c_int, C.POINTER(_vp), _szp, C.POINTER(_vp), C.POINTER(_vp), _vp],
     "nnh_im2col": [_vp, _sz, _sz, _sz, _sz, _sz, _sz, C.c_int, C.c_int, _vp, _vp],

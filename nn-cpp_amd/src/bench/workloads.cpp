@@ -64,7 +64,8 @@ Value transformer_forward(const std::vector<float>& ids, size_t N, const std::ve
 		const Value att = nn::hip::attention(qkv[0], qkv[1], qkv[2], kHeads, no_mask, true);
 		// add(h, linear(...)) with the add in the linear's epilogue: the same nodes and bits
 		h = nn::hip::linear_add(att, p[i + 8], p[i + 9], h);
-		const Value m = nn::hip::gelu(nn::hip::linear(nn::hip::layernorm(h, p[i + 10], p[i + 11], 1e-5f), p[i + 12], p[i + 13]));
+		// gelu(linear(...)) with the GELU in the linear's epilogue (the same nodes and bits)
+		const Value m = nn::hip::linear_gelu(nn::hip::layernorm(h, p[i + 10], p[i + 11], 1e-5f), p[i + 12], p[i + 13]);
 		h = nn::hip::linear_add(m, p[i + 14], p[i + 15], h);
 	}
 	const Value o = nn::hip::linear(nn::hip::layernorm(h, p[i], p[i + 1], 1e-5f), p[i + 2], p[i + 3]);

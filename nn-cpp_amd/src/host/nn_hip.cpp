@@ -800,15 +800,39 @@ Value slice(const Value& x, int axis, size_t start, size_t end) {
 	});
 }
 
-Value gelu(const Value& x) {
-	Tensor y = Tensor::empty(x.data().shape());
-	Tensor th = Tensor::empty(x.data().shape());  // tanh(k (x + c x^3)), kept for the backward rule
-	check(nnh_gelu_forward(x.data().data(), y.size(), y.data(), th.data(), g_stream));
+namespace {
+
+// The GELU node over its forward's output y and the tanh it keeps for the backward rule.
+Value gelu_node(const Value& x, Tensor y, Tensor th) {
 	return Value::node(std::move(y), {x}, [x, th](const Tensor& g) {
 		bool first = false;
 		float* dx = grad_if(x, first);
 		if (dx) check(nnh_gelu_backward(x.data().data(), th.data(), g.data(), g.size(), dx, first, g_stream));
 	});
+}
+
+}  // namespace
+
+Value gelu(const Value& x) {
+	Tensor y = Tensor::empty(x.data().shape());
+	Tensor th = Tensor::empty(x.data().shape());  // tanh(k (x + c x^3)), kept for the backward rule
+	check(nnh_gelu_forward(x.data().data(), y.size(), y.data(), th.data(), g_stream));
+	return gelu_node(x, std::move(y), std::move(th));
+}
+
+Value linear_gelu(const Value& x, const Value& weight, const Value& bias) {
+	const auto& xs = x.data().shape();
+	const auto& ws = weight.data().shape();
+	// ops.cpp:717-719
+	if (xs.size() < 2 || ws.size() != 2 || xs.back() != ws[1] || bias.data().shape() != std::vector<size_t>{ws[0]})
+		throw TensorShapeError("nn::hip: linear shapes");
+	std::vector<size_t> out(xs.begin(), xs.end() - 1);
+	out.push_back(ws[0]);
+	const size_t n = ws[0], K = ws[1], M = numel(out) / std::max<size_t>(n, 1);
+	Tensor h = Tensor::empty(out), y = Tensor::empty(out), th = Tensor::empty(out);
+	check(nnh_linear_gelu_forward(x.data().data(), M, K, weight.data().data(), n, bias.data().data(), h.data(), y.data(),
+	                              th.data(), g_stream));
+	return gelu_node(linear_node(x, weight, bias, h), std::move(y), std::move(th));
 }
 
 namespace {

@@ -348,7 +348,7 @@ Value TransformerBlock::forward(const Value& x) {
 	// x + attn(ln1(x)) and h + drop(fc2(...)) with each add in the producing linear's epilogue (the same nodes and
 	// bits); an active dropout between fc2 and the add keeps the ops apart
 	const Value h = attn_.forward_add(ln1_.forward(x), x);
-	const Value f = act_.forward(fc1_.forward(ln2_.forward(h)));
+	const Value f = fc1_.forward_gelu(ln2_.forward(h));  // act_ is the GELU
 	return drop_.active() ? add(h, drop_.forward(fc2_.forward(f))) : fc2_.forward_add(f, h);
 }
 

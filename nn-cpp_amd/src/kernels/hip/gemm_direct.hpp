@@ -12,6 +12,7 @@
 #include <algorithm>
 #include <type_traits>
 
+#include "gelu_math.hpp"
 #include "gemm_tile.hpp"
 
 namespace nnh {
@@ -226,6 +227,11 @@ __device__ __forceinline__ void chain4_tile(const GemmArgs& p, int block, int wa
 		if (p.ep.bias_mode == kBiasCol) v = v + p.ep.bias[col];
 		else if (p.ep.bias_mode == kBiasRow) v = v + p.ep.bias[row];
 		if (p.ep.res) v = p.ep.res[oc + off] + v;
+		if (p.ep.gelu_y) {
+			float t;
+			p.ep.gelu_y[oc + off] = gelu_math::gelu_one(v, t);
+			p.ep.gelu_t[oc + off] = t;
+		}
 		if (p.ep.relu) {
 			const bool on = v > 0.0f;
 			if (alive) alive[off] = on ? 1 : 0;

@@ -120,6 +120,10 @@ struct Epilogue {
 	unsigned char* alive;  // optional, addressed like C
 	// optional, addressed like C: added after the bias as res + v, the reference's add(residual, linear(...))
 	const float* res;
+	// optional, addressed like C, the chain kernel only (gemm_direct.hpp): GELU of the stored value (ops.cpp:461-466)
+	// into gelu_y and its tanh into gelu_t, the reference's gelu(linear(...)) with C its input
+	float* gelu_y;
+	float* gelu_t;
 };
 
 // Implicit im2col (src/autograd/ops.cpp:188-212): B is a sample's column matrix col[k][p] of a convolution,

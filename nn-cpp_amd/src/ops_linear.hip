@@ -105,6 +105,31 @@ int nnh_linear_forward_multi(const float* x, size_t M, size_t K, int count, cons
 	return NNH_OK;
 }
 
+int nnh_linear_gelu_forward(const float* x, size_t M, size_t K, const float* w, size_t n, const float* bias, float* h,
+                            float* y, float* tanh_saved, void* stream) {
+	NumericsScope numerics_scope(stream);
+	if (M > 0 && n > 0 && (!bias || !y || !tanh_saved)) return fail(NNH_ERR_INVALID, "linear gelu: null pointer");
+	const uint64_t bytes = (uint64_t)M * n * 4;
+	if (M > 0 && n > 0 &&
+	    (ranges_overlap(y, bytes, h, bytes) || ranges_overlap(tanh_saved, bytes, h, bytes) ||
+	     ranges_overlap(tanh_saved, bytes, y, bytes) || ranges_overlap(y, bytes, x, (uint64_t)M * K * 4) ||
+	     ranges_overlap(tanh_saved, bytes, x, (uint64_t)M * K * 4) || ranges_overlap(y, bytes, w, (uint64_t)n * K * 4) ||
+	     ranges_overlap(tanh_saved, bytes, w, (uint64_t)n * K * 4)))
+		return fail(NNH_ERR_ALIAS, "linear gelu: the outputs overlap each other or the inputs");
+	nnh_epilogue ep{NNH_BIAS_COL, 0, bias, nullptr};
+	GemmCall g;
+	int rc = build_gemm(0, 1, M, n, K, x, K, w, K, h, n, 0, nullptr, &ep, g);
+	if (rc != NNH_OK || M == 0 || n == 0) return rc;
+	if (chain4_ok(g)) {  // the chain kernel applies the GELU in its epilogue
+		g.ep.gelu_y = y;
+		g.ep.gelu_t = tanh_saved;
+		return hip_status(gemm_chain4_launch(g, reinterpret_cast<hipStream_t>(stream)), "linear gelu");
+	}
+	rc = run_gemm(g, stream, -1);
+	if (rc != NNH_OK) return rc;
+	return nnh_gelu_forward(h, M * n, y, tanh_saved, stream);
+}
+
 int nnh_linear_forward_add(const float* x, size_t M, size_t K, const float* w, size_t n, const float* bias,
                            const float* residual, float* y, void* stream) {
 	NumericsScope numerics_scope(stream);

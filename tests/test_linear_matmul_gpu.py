@@ -129,6 +129,35 @@ def test_linear_forward_add(gpu, oracle):
     assert rc == nnh.ERR_ALIAS
 
 
+def test_linear_gelu_forward(gpu, oracle):
+    """nnh_linear_gelu_forward: h = linear(x, w, b) and the GELU of h (y and the kept tanh), bit for bit the oracle's
+    linear and gelu, with the GELU in the chain kernel's epilogue (transformer_tiny's fc1, ragged tiles, inputs past
+    tanh's clamp) and, for a product with a depth cut, as two launches; outputs that overlap are refused."""
+    import torch
+
+    import nnh
+    L, P, st = nnh.lib(), nnh._ptr, nnh._stream(None)
+    cases = [(1024, 64, 256), (37, 20, 70), (64, 1024, 64), (5, 3, 9)]
+    for ci, (M, K, n) in enumerate(cases):
+        x = synth.normal(3700 + ci, (M, K))
+        w = synth.normal(3800 + ci, (n, K))
+        b = synth.normal(3900 + ci, (n,))
+        if ci == 1:
+            b[0], b[1] = 40.0, -40.0  # outputs far past tanh's clamp of +-9
+        h0 = oracle.linear_forward(x, w, b)
+        y0, t0 = oracle.gelu_forward(h0)
+        h, y, t = (torch.full((M, n), float("nan"), device="cuda") for _ in range(3))
+        xd, wd, bd = dev(x), dev(w), dev(b)
+        nnh.check(L.nnh_linear_gelu_forward(P(xd), M, K, P(wd), n, P(bd), P(h), P(y), P(t), st))
+        same(host(h), h0, ("h", M, K, n))
+        same(host(y), y0, ("y", M, K, n))
+        same(host(t), t0, ("tanh", M, K, n))
+    buf = torch.zeros(3 * 64 * 64, device="cuda")
+    xd, wd, bd = dev(np.ones((64, 64), np.float32)), dev(np.ones((64, 64), np.float32)), dev(np.ones(64, np.float32))
+    assert L.nnh_linear_gelu_forward(P(xd), 64, 64, P(wd), 64, P(bd), P(buf), P(buf, 64), P(buf, 8192), st) == \
+        nnh.ERR_ALIAS
+
+
 def test_linear_forward_multi(gpu, oracle):
     """nnh_linear_forward_multi: several linear layers over one input, each output the oracle's linear bit for bit:
     three projections of one width (one launch on the chain kernel), of different widths, with ragged tiles, a
