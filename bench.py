@@ -907,7 +907,7 @@ def row_json(r):
         if k in res:
             out[k] = round(res[k], 3)
     out["roofline"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in res["roofline"].items()}
-    for k in ("bitwise_repeat", "bitwise_vs_nn_cpp", "bitwise_vs_two_ops"):
+    for k in ("bitwise_repeat", "bitwise_vs_nn_cpp", "bitwise_vs_two_ops", "bitwise_vs_byte_form"):
         if k in res:
             out[k] = res[k]
     if "maxabs_vs_nn_cpp" in res and not res.get("bitwise_vs_nn_cpp", True):

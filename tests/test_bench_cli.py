@@ -44,6 +44,8 @@ def full_row(key, i):
            "cpu_1thread": {"ms": 8020.4746123, "threads": 1, "runs": 1, "spread": 0.0, "speedup_gpu": 891.3}}
     if key.endswith("_causal"):
         row["roofline"]["useful_frac"] = 0.4012345
+    if key.endswith("_packed"):
+        row["bitwise_vs_byte_form"] = True
     return row
 
 
@@ -95,6 +97,7 @@ def test_stdout_line_fits_and_carries_the_contract(bench):
     # the packed-flag rows travel as their time and check in fused_op
     assert list(line["configs"]) == [k for k in ROW_KEYS if not k.endswith("_packed")]
     assert list(line["fused_op"]["packed_us"]) == ["fwd", "fwd_pool", "bwd", "pool_bwd", "bitwise"]
+    assert line["fused_op"]["packed_us"]["bitwise"] is True
     assert list(line["configs_split_depth"]) == SPLIT_KEYS
     for r in line["configs"].values():
         assert set(r) >= {"ms", "frac", "cpu_ms", "bitwise"}
