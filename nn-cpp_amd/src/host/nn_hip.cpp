@@ -280,16 +280,24 @@ void Value::backward(const Tensor& seed) const {
 	for (const Value& v : topo) {
 		v.impl()->consumers = 0;
 		if (v.impl()->backward_fn) {
-			if (v.impl()->grad.shape() != v.impl()->data.shape()) v.impl()->grad = Tensor::empty(v.impl()->data.shape());
+			// a buffer of its own every walk: an earlier walk may have left it sharing storage (take_grad, the seed)
+			v.impl()->grad = Tensor::empty(v.impl()->data.shape());
 			v.impl()->grad_fresh = true;
 		}
 	}
 	for (const Value& v : topo)
 		for (const Value& p : v.impl()->parents) ++p.impl()->consumers;
-	if (impl_->grad.shape() != impl_->data.shape()) impl_->grad = Tensor::empty(impl_->data.shape());
-	if (seed.size())
-		check_hip(hipMemcpyAsync(impl_->grad.data(), seed.data(), seed.size() * 4, hipMemcpyDeviceToDevice, g_stream),
-		          "seed");
+	if (impl_->backward_fn) {
+		// an intermediate output's gradient is the seed itself (shared storage, no copy): nothing writes it during the
+		// walk (only single-use pass-through operands take a gradient's storage, and no contribution reaches them
+		// later), and the next walk gives the node a buffer of its own again
+		impl_->grad = seed;
+	} else {
+		if (impl_->grad.shape() != impl_->data.shape()) impl_->grad = Tensor::empty(impl_->data.shape());
+		if (seed.size())
+			check_hip(hipMemcpyAsync(impl_->grad.data(), seed.data(), seed.size() * 4, hipMemcpyDeviceToDevice, g_stream),
+			          "seed");
+	}
 	impl_->grad_fresh = false;
 	for (auto it = topo.rbegin(); it != topo.rend(); ++it)
 		if (it->impl()->backward_fn) it->impl()->backward_fn(it->grad());
