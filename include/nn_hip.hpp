@@ -119,6 +119,8 @@ public:
 	Tensor& grad() const;                     // a fresh gradient is zeroed on first read
 	Tensor& grad_accum(bool& first) const;    // value.cpp:60-64: first = the buffer holds nothing yet
 	bool requires_grad() const;
+	// value.cpp's zero_grad: the gradient reads as zeros from here on; marked fresh rather than filled (no launch),
+	// the next backward rule's first write giving the bits of an add to zeros
 	void zero_grad() const;
 	// Value::backward (value.cpp:80-132) for a one-element value; the overload seeds the output gradient with
 	// `seed` (the output's shape) instead of ones, for a graph whose loss is formed elsewhere.
@@ -131,8 +133,7 @@ private:
 	std::shared_ptr<NodeImpl> impl_;
 };
 
-// Value::zero_grad over a list (Optimizer::zero_grad, src/optim/sgd.cpp:19-21): the same gradients, all their fills
-// in one launch.
+// Value::zero_grad over a list (Optimizer::zero_grad, src/optim/sgd.cpp:19-21): the same gradients, no launch.
 void zero_grad(const std::vector<Value>& values);
 
 // Ops record no graph while one is alive on the thread (value.hpp:24-40).

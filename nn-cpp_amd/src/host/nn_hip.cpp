@@ -217,36 +217,16 @@ Tensor& Value::grad_accum(bool& first) const {
 
 bool Value::requires_grad() const { return impl_->requires_grad; }
 
+// zero_grad marks the gradient fresh instead of filling it with zeros: the next backward rule stores its
+// contribution as nn-cpp adds it to zeros (every rule's first write is that sum: s + 0.0f, or a chain from +0, which
+// is never -0), and grad() fills a gradient no rule wrote with zeros when it is read. No launch.
 void Value::zero_grad() const {
-	if (impl_->grad.shape() != impl_->data.shape()) impl_->grad = Tensor(impl_->data.shape(), 0.0f);
-	else impl_->grad.zero_();
-	impl_->grad_fresh = false;
+	if (impl_->grad.shape() != impl_->data.shape()) impl_->grad = Tensor::empty(impl_->data.shape());
+	impl_->grad_fresh = true;
 }
 
 void zero_grad(const std::vector<Value>& values) {
-	std::vector<float*> ptrs;
-	std::vector<size_t> counts;
-	for (const Value& v : values) {
-		NodeImpl* n = v.impl();
-		if (n->grad.shape() != n->data.shape()) n->grad = Tensor::empty(n->data.shape());
-		n->grad_fresh = false;
-		if (n->grad.size()) {
-			ptrs.push_back(n->grad.data());
-			counts.push_back(n->grad.size());
-		}
-	}
-	// one value listed twice: one fill
-	std::vector<size_t> order(ptrs.size());
-	for (size_t i = 0; i < order.size(); ++i) order[i] = i;
-	std::sort(order.begin(), order.end(), [&](size_t a, size_t b) { return ptrs[a] < ptrs[b]; });
-	std::vector<float*> up;
-	std::vector<size_t> uc;
-	for (size_t i : order)
-		if (up.empty() || up.back() != ptrs[i]) {
-			up.push_back(ptrs[i]);
-			uc.push_back(counts[i]);
-		}
-	check(nnh_zero_many(up.data(), uc.data(), up.size(), g_stream));
+	for (const Value& v : values) v.zero_grad();
 }
 
 void Value::backward() const {
