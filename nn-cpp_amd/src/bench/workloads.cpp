@@ -114,7 +114,7 @@ int nnh_bench_workload_step(int model, const float* x, size_t N, const float* co
 			Value y = tf ? transformer_forward(ids, N, p, pe) : forward(model, xv, p);
 			nn::hip::synchronize();
 			const auto t1 = Clock::now();
-			nn::hip::zero_grad(p);  // Optimizer::zero_grad: every parameter's zero_grad, in one launch
+			nn::hip::zero_grad(p);  // Optimizer::zero_grad: marks every parameter's gradient fresh (no launch)
 			y.backward(seed);
 			nn::hip::synchronize();
 			const auto t2 = Clock::now();
