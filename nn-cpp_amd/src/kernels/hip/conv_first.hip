@@ -7,9 +7,9 @@
 // co in order from +0 of W[co][k] g'[co][p]; each dx element then adds its taps in (ph, pw) order, starting from 0 or
 // its old value). The caller sums db_n and dW_n over the samples in order.
 //
-// A workgroup of eight waves walks the sample's output positions in chunks of 64, one barrier per chunk, with each
+// A workgroup of twelve waves walks the sample's output positions in chunks of 64, one barrier per chunk, with each
 // wave in one role:
-//   * waves 4-7 stream the gradient from HBM (kFbRing chunks of loads in flight), mask it and write each chunk into
+//   * waves 4-11 stream the gradient from HBM (kFbRing chunks of loads in flight), mask it and write each chunk into
 //     one of two LDS slots, transposed by 16 positions (position 16 J + 4 t + e at 16 J + 4 e + t, so that one 16-byte
 //     read feeds four MFMA steps), together with the chunk's im2col columns taken from the input plane in LDS;
 //   * waves 0-1 run dW_n and db_n for 16 channels each as one 16x16x4 MFMA chain (four fmas in sequence per element
@@ -33,7 +33,7 @@ namespace nnh {
 
 namespace {
 
-constexpr int kFbThreads = 512;
+constexpr int kFbThreads = 768;
 constexpr int kFbMaxK = 16;
 constexpr int kFbMaxCo = 32;
 constexpr int kFbChunk = 64;               // output positions per chunk (four blocks of 16)
@@ -42,6 +42,14 @@ constexpr int kFbSlot = 48 * kFbPitch;     // 32 gradient rows and 16 column row
 constexpr int kFbRing = 6;                 // chunks of gradient loads in flight per staging lane
 constexpr int kFbMaxPlane = 2048;
 constexpr size_t kFbMaxLds = 160 * 1024;
+// staging lanes (waves 4 on): each builds kFbQuads gradient quads and kFbCols column values of every chunk. Eight
+// staging waves keep a chunk's build (masking, the transposed LDS writes, the im2col gathers) about as long as the
+// dW chain's 16 MFMAs, which four waves were not.
+constexpr int kFbStage = kFbThreads - 256;
+constexpr int kFbQuads = 32 * kFbChunk / 4 / kFbStage;
+constexpr int kFbCols = 16 * kFbChunk / kFbStage;
+static_assert(kFbQuads * kFbStage == 32 * kFbChunk / 4 && kFbCols * kFbStage == 16 * kFbChunk && kFbStage % 64 == 0,
+              "whole quads and columns per staging lane");
 
 // flag layouts: none, one byte per position (a 4-byte word per quad of positions), or one bit per position (bit o of
 // the flattened output index at byte o / 8, bit o % 8: a quad's flags are one nibble)
@@ -83,14 +91,30 @@ __global__ void __launch_bounds__(kFbThreads) conv_first_bwd_kernel(const FbArgs
 
 	// Every wave passes 2 + nchunks barriers below (and one more when dx is asked for), whatever its role.
 	if (wave >= 4) {
-		// ---- staging: lane st owns quads st and st + 256 of each chunk (row = quad / 16, positions 4 (quad % 16) ..)
+		// ---- staging: lane st owns quads st + kFbStage u of each chunk (row = quad / 16, positions 4 (quad % 16) ..)
 		const int st = tid - 256;
-		auto load = [&](int ch, f32x4(&v)[2], unsigned(&f)[2]) {
+		// the plane offsets of the columns this lane builds (column (wave - 4) + kFbStage / 64 u, the same in every
+		// chunk), read once with a wave-uniform index: a per-lane index into the argument block becomes a vector load
+		// whose wait would also drain the ring of gradient loads in flight
+		int koff[kFbCols];
 #pragma unroll
-			for (int u = 0; u < 2; ++u) {
-				const int qi = st + 256 * u, row = qi >> 4;
-				const int p = min(ch * kFbChunk + 4 * (qi & 15), hw - 4);
-				const int64_t at = (row0 + min(row, a.cout - 1)) * hw + p;
+		for (int u = 0; u < kFbCols; ++u) koff[u] = a.koff[min(wave - 4 + kFbStage / 64 * u, K - 1)];
+		// a lane's quads keep their rows (st / 16 + kFbStage / 16 u) and their place in the chunk (4 (st % 16)) in every
+		// chunk: the row offsets and the rows' liveness once
+		const int q4 = 4 * (st & 15);
+		int64_t roff[kFbQuads];
+		bool rlive[kFbQuads];
+#pragma unroll
+		for (int u = 0; u < kFbQuads; ++u) {
+			const int row = (st >> 4) + kFbStage / 16 * u;
+			rlive[u] = row < a.cout;
+			roff[u] = (row0 + min(row, a.cout - 1)) * hw;
+		}
+		auto load = [&](int ch, f32x4(&v)[kFbQuads], unsigned(&f)[kFbQuads]) {
+#pragma unroll
+			for (int u = 0; u < kFbQuads; ++u) {
+				const int p = min(ch * kFbChunk + q4, hw - 4);
+				const int64_t at = roff[u] + p;
 				v[u] = *reinterpret_cast<const f32x4*>(a.g + at);
 				if (AL == kAlWord) {
 					f[u] = *reinterpret_cast<const unsigned*>(a.alive + at);
@@ -105,35 +129,32 @@ __global__ void __launch_bounds__(kFbThreads) conv_first_bwd_kernel(const FbArgs
 		};
 		// chunk ch into slot ch % 2: the masked gradient (rows past cout and positions past hw are zero) and the
 		// columns
-		auto build = [&](int ch, const f32x4(&v)[2], const unsigned(&f)[2]) {
+		auto build = [&](int ch, const f32x4(&v)[kFbQuads], const unsigned(&f)[kFbQuads]) {
 			float* sl = slots + (ch & 1) * kFbSlot;
 #pragma unroll
-			for (int u = 0; u < 2; ++u) {
-				const int qi = st + 256 * u, row = qi >> 4, q = qi & 15;
-				const int p = ch * kFbChunk + 4 * q;
+			for (int u = 0; u < kFbQuads; ++u) {
+				const int qi = st + kFbStage * u, row = qi >> 4, q = qi & 15;
+				// hw is a multiple of 4, so a quad lies wholly before hw or wholly past it
+				const bool on = rlive[u] && ch * kFbChunk + q4 < hw;
 				float* d = sl + row * kFbPitch + 16 * (q >> 2) + (q & 3);
 #pragma unroll
-				for (int e = 0; e < 4; ++e)
-					d[4 * e] = (row < a.cout && p + e < hw && ((f[u] >> (8 * e)) & 0xffu)) ? v[u][e] : 0.0f;
+				for (int e = 0; e < 4; ++e) d[4 * e] = (on && ((f[u] >> (8 * e)) & 0xffu)) ? v[u][e] : 0.0f;
 			}
-			// column k of positions ch * 64 .. + 63: lane st takes values st + 256 u (k = value / 64, uniform in the
-			// wave); all reads are issued before the writes
-			float cv[4];
+			// column k of positions ch * 64 .. + 63: lane st takes values st + kFbStage u (k = value / 64 = (wave - 4) +
+			// kFbStage / 64 u, position value % 64 = lane); all reads are issued before the writes
+			float cv[kFbCols];
+			const unsigned pq = (unsigned)min(ch * kFbChunk + lane, hw - 1);
+			const int oh = (int)fdiv(pq, a.wo_div), ow = (int)pq - oh * G.wo;
 #pragma unroll
-			for (int u = 0; u < 4; ++u) {
-				const int vi = st + 256 * u, k = min(vi >> 6, K - 1);
-				const unsigned pq = (unsigned)min(ch * kFbChunk + (vi & 63), hw - 1);
-				const int oh = (int)fdiv(pq, a.wo_div), ow = (int)pq - oh * G.wo;
-				cv[u] = plane[a.koff[k] + oh * a.wp + ow];
-			}
+			for (int u = 0; u < kFbCols; ++u) cv[u] = plane[koff[u] + oh * a.wp + ow];
 #pragma unroll
-			for (int u = 0; u < 4; ++u) {
-				const int vi = st + 256 * u, k = vi >> 6, pl = vi & 63;
+			for (int u = 0; u < kFbCols; ++u) {
+				const int vi = st + kFbStage * u, k = vi >> 6, pl = vi & 63;
 				if (k < K) sl[(32 + k) * kFbPitch + fb_slot(pl)] = ch * kFbChunk + pl < hw ? cv[u] : 0.0f;
 			}
 		};
-		f32x4 rv[kFbRing][2];
-		unsigned rf[kFbRing][2];
+		f32x4 rv[kFbRing][kFbQuads];
+		unsigned rf[kFbRing][kFbQuads];
 #pragma unroll
 		for (int u = 0; u < kFbRing; ++u) load(u, rv[u], rf[u]);
 		__syncthreads();  // the plane is in LDS
