@@ -7,7 +7,7 @@
 // co in order from +0 of W[co][k] g'[co][p]; each dx element then adds its taps in (ph, pw) order, starting from 0 or
 // its old value). The caller sums db_n and dW_n over the samples in order.
 //
-// A workgroup of twelve waves walks the sample's output positions in chunks of 64, one barrier per chunk, with each
+// A workgroup of twelve waves walks the sample's output positions in chunks of 128, one barrier per chunk, with each
 // wave in one role:
 //   * waves 4-11 stream the gradient from HBM (kFbRing chunks of loads in flight), mask it and write each chunk into
 //     one of two LDS slots, transposed by 16 positions (position 16 J + 4 t + e at 16 J + 4 e + t, so that one 16-byte
@@ -36,7 +36,9 @@ namespace {
 constexpr int kFbThreads = 768;
 constexpr int kFbMaxK = 16;
 constexpr int kFbMaxCo = 32;
-constexpr int kFbChunk = 64;               // output positions per chunk (four blocks of 16)
+constexpr int kFbChunk = 128;              // output positions per chunk (eight blocks of 16)
+constexpr int kFbBlocks = kFbChunk / 16;
+constexpr int kFbRowQuads = kFbChunk / 4;  // quads of a gradient row in a chunk
 constexpr int kFbPitch = kFbChunk + 4;     // LDS pitch of a row of a chunk slot
 constexpr int kFbSlot = 48 * kFbPitch;     // 32 gradient rows and 16 column rows
 constexpr int kFbRing = 6;                 // chunks of gradient loads in flight per staging lane
@@ -48,8 +50,9 @@ constexpr size_t kFbMaxLds = 160 * 1024;
 constexpr int kFbStage = kFbThreads - 256;
 constexpr int kFbQuads = 32 * kFbChunk / 4 / kFbStage;
 constexpr int kFbCols = 16 * kFbChunk / kFbStage;
-static_assert(kFbQuads * kFbStage == 32 * kFbChunk / 4 && kFbCols * kFbStage == 16 * kFbChunk && kFbStage % 64 == 0,
-              "whole quads and columns per staging lane");
+static_assert(kFbQuads * kFbStage == 32 * kFbChunk / 4 && kFbCols * kFbStage == 16 * kFbChunk &&
+                  kFbStage % kFbChunk == 0 && kFbChunk % 64 == 0 && kFbStage % kFbRowQuads == 0,
+              "whole quads and columns per staging lane, a column's positions within one wave pair");
 
 // flag layouts: none, one byte per position (a 4-byte word per quad of positions), or one bit per position (bit o of
 // the flattened output index at byte o / 8, bit o % 8: a quad's flags are one nibble)
@@ -67,7 +70,7 @@ struct FbArgs {
 	ConvGeom geo;
 	int cout, K, hw, full, nchunks;
 	int hp, wp, plane, plane_pad; // zero-padded input plane: (ho-1) + kh rows, (wo-1) + kw columns
-	int dpitch;                   // LDS pitch of a dcol row (nchunks * 64)
+	int dpitch;                   // LDS pitch of a dcol row (nchunks * kFbChunk + 4)
 	int koff[kFbMaxK];            // column k = (ci, ph, pw) starts at plane offset (ci hp + ph) wp + pw (0 past K)
 	int tapc[kFbMaxK];            // tap t = (ph, pw): t dpitch - ph wo - pw (0 past kh kw)
 	FastDiv wo_div, plane_div, wp_div, w_div;
@@ -91,22 +94,25 @@ __global__ void __launch_bounds__(kFbThreads) conv_first_bwd_kernel(const FbArgs
 
 	// Every wave passes 2 + nchunks barriers below (and one more when dx is asked for), whatever its role.
 	if (wave >= 4) {
-		// ---- staging: lane st owns quads st + kFbStage u of each chunk (row = quad / 16, positions 4 (quad % 16) ..)
+		// ---- staging: lane st owns quads st + kFbStage u of each chunk (row = quad / kFbRowQuads, positions
+		// 4 (quad % kFbRowQuads) ..)
 		const int st = tid - 256;
-		// the plane offsets of the columns this lane builds (column (wave - 4) + kFbStage / 64 u, the same in every
-		// chunk), read once with a wave-uniform index: a per-lane index into the argument block becomes a vector load
-		// whose wait would also drain the ring of gradient loads in flight
+		// the columns this lane builds: value st + kFbStage u of a chunk is column (st + kFbStage u) / kFbChunk =
+		// kcol0 + kFbStage / kFbChunk u (wave-uniform) at position st % kFbChunk, the same in every chunk. Their plane
+		// offsets are read once with a wave-uniform index: a per-lane index into the argument block becomes a vector
+		// load whose wait would also drain the ring of gradient loads in flight
+		const int kcol0 = (wave - 4) * 64 / kFbChunk, pcol = st & (kFbChunk - 1);
 		int koff[kFbCols];
 #pragma unroll
-		for (int u = 0; u < kFbCols; ++u) koff[u] = a.koff[min(wave - 4 + kFbStage / 64 * u, K - 1)];
-		// a lane's quads keep their rows (st / 16 + kFbStage / 16 u) and their place in the chunk (4 (st % 16)) in every
-		// chunk: the row offsets and the rows' liveness once
-		const int q4 = 4 * (st & 15);
+		for (int u = 0; u < kFbCols; ++u) koff[u] = a.koff[min(kcol0 + kFbStage / kFbChunk * u, K - 1)];
+		// a lane's quads keep their rows (st / kFbRowQuads + kFbStage / kFbRowQuads u) and their place in the chunk
+		// (4 (st % kFbRowQuads)) in every chunk: the row offsets and the rows' liveness once
+		const int q4 = 4 * (st % kFbRowQuads);
 		int64_t roff[kFbQuads];
 		bool rlive[kFbQuads];
 #pragma unroll
 		for (int u = 0; u < kFbQuads; ++u) {
-			const int row = (st >> 4) + kFbStage / 16 * u;
+			const int row = st / kFbRowQuads + kFbStage / kFbRowQuads * u;
 			rlive[u] = row < a.cout;
 			roff[u] = (row0 + min(row, a.cout - 1)) * hw;
 		}
@@ -133,24 +139,23 @@ __global__ void __launch_bounds__(kFbThreads) conv_first_bwd_kernel(const FbArgs
 			float* sl = slots + (ch & 1) * kFbSlot;
 #pragma unroll
 			for (int u = 0; u < kFbQuads; ++u) {
-				const int qi = st + kFbStage * u, row = qi >> 4, q = qi & 15;
+				const int qi = st + kFbStage * u, row = qi / kFbRowQuads, q = qi % kFbRowQuads;
 				// hw is a multiple of 4, so a quad lies wholly before hw or wholly past it
 				const bool on = rlive[u] && ch * kFbChunk + q4 < hw;
 				float* d = sl + row * kFbPitch + 16 * (q >> 2) + (q & 3);
 #pragma unroll
 				for (int e = 0; e < 4; ++e) d[4 * e] = (on && ((f[u] >> (8 * e)) & 0xffu)) ? v[u][e] : 0.0f;
 			}
-			// column k of positions ch * 64 .. + 63: lane st takes values st + kFbStage u (k = value / 64 = (wave - 4) +
-			// kFbStage / 64 u, position value % 64 = lane); all reads are issued before the writes
+			// the columns' values at position ch * kFbChunk + pcol; all reads are issued before the writes
 			float cv[kFbCols];
-			const unsigned pq = (unsigned)min(ch * kFbChunk + lane, hw - 1);
+			const unsigned pq = (unsigned)min(ch * kFbChunk + pcol, hw - 1);
 			const int oh = (int)fdiv(pq, a.wo_div), ow = (int)pq - oh * G.wo;
 #pragma unroll
 			for (int u = 0; u < kFbCols; ++u) cv[u] = plane[koff[u] + oh * a.wp + ow];
 #pragma unroll
 			for (int u = 0; u < kFbCols; ++u) {
-				const int vi = st + kFbStage * u, k = vi >> 6, pl = vi & 63;
-				if (k < K) sl[(32 + k) * kFbPitch + fb_slot(pl)] = ch * kFbChunk + pl < hw ? cv[u] : 0.0f;
+				const int k = kcol0 + kFbStage / kFbChunk * u;
+				if (k < K) sl[(32 + k) * kFbPitch + fb_slot(pcol)] = ch * kFbChunk + pcol < hw ? cv[u] : 0.0f;
 			}
 		};
 		f32x4 rv[kFbRing][kFbQuads];
@@ -217,15 +222,15 @@ __global__ void __launch_bounds__(kFbThreads) conv_first_bwd_kernel(const FbArgs
 			for (int i = 0; i < nchunks; ++i) {
 				if (live) {
 					const float* sl = slots + (i & 1) * kFbSlot;
-					f32x4 av[4], bv[4];
+					f32x4 av[kFbBlocks], bv[kFbBlocks];
 #pragma unroll
-					for (int b = 0; b < 4; ++b) {
+					for (int b = 0; b < kFbBlocks; ++b) {
 						av[b] = *reinterpret_cast<const f32x4*>(sl + arow + 16 * b);
 						bv[b] = *reinterpret_cast<const f32x4*>(sl + brow + 16 * b);
 					}
 					if ((i + 1) * kFbChunk <= full) {
 #pragma unroll
-						for (int b = 0; b < 4; ++b)
+						for (int b = 0; b < kFbBlocks; ++b)
 #pragma unroll
 							for (int t = 0; t < 4; ++t) {
 								if (t & 1) part1 = part1 + av[b][t];
@@ -235,7 +240,7 @@ __global__ void __launch_bounds__(kFbThreads) conv_first_bwd_kernel(const FbArgs
 					} else {
 						// the chunk reaches past full: positions past hw multiply +0 by -0, past full skip the partials
 #pragma unroll
-						for (int b = 0; b < 4; ++b)
+						for (int b = 0; b < kFbBlocks; ++b)
 #pragma unroll
 							for (int t = 0; t < 4; ++t) {
 								const int p = i * kFbChunk + 16 * b + 4 * t + grp;
@@ -273,7 +278,7 @@ __global__ void __launch_bounds__(kFbThreads) conv_first_bwd_kernel(const FbArgs
 				}
 			}
 		} else {
-			// ---- dcol of the chunk's blocks b0 and b0 + 2 (b0 = wave - 2): lane (grp, i) supplies g'[4 t + grp][16 b +
+			// ---- dcol of the chunk's blocks b0 + 2 j (b0 = wave - 2): lane (grp, i) supplies g'[4 t + grp][16 b +
 			// i], lane (grp, j) W[4 t + grp][j]; D[4 grp + r][j] = dcol[j][16 b + 4 grp + r]. Chains over co from +0;
 			// steps past cout multiply +0 (the zero rows) by -0.
 			const int b0 = wave - 2, i16 = l16;
@@ -284,27 +289,30 @@ __global__ void __launch_bounds__(kFbThreads) conv_first_bwd_kernel(const FbArgs
 				wreg[t] = (a.dx && co < a.cout && i16 < K) ? a.w[(int64_t)co * K + i16] : -0.0f;
 			}
 			float* drow = dcb + min(i16, K) * a.dpitch;
-			const int sa = fb_slot(16 * b0 + i16), sb = fb_slot(16 * (b0 + 2) + i16);
+			constexpr int kJ = kFbBlocks / 2;
+			int sidx[kJ];
+#pragma unroll
+			for (int j = 0; j < kJ; ++j) sidx[j] = fb_slot(16 * (b0 + 2 * j) + i16);
 			for (int i = 0; i < nchunks; ++i) {
 				if (a.dx) {
 					const float* sl = slots + (i & 1) * kFbSlot + grp * kFbPitch;
-					float va[NS], vb[NS];
+					float vv[kJ][NS];
 #pragma unroll
-					for (int t = 0; t < NS; ++t) {
-						va[t] = sl[4 * t * kFbPitch + sa];
-						vb[t] = sl[4 * t * kFbPitch + sb];
-					}
-					f32x4 acc0 = {0.0f, 0.0f, 0.0f, 0.0f}, acc1 = {0.0f, 0.0f, 0.0f, 0.0f};
+					for (int j = 0; j < kJ; ++j)
 #pragma unroll
-					for (int t = 0; t < NS; ++t) {
-						acc0 = __builtin_amdgcn_mfma_f32_16x16x4f32(va[t], wreg[t], acc0, 0, 0, 0);
-						acc1 = __builtin_amdgcn_mfma_f32_16x16x4f32(vb[t], wreg[t], acc1, 0, 0, 0);
-					}
+						for (int t = 0; t < NS; ++t) vv[j][t] = sl[4 * t * kFbPitch + sidx[j]];
+					f32x4 acc[kJ];
 #pragma unroll
-					for (int r = 0; r < 4; ++r) {
-						drow[i * kFbChunk + 16 * b0 + 4 * grp + r] = acc0[r];
-						drow[i * kFbChunk + 16 * (b0 + 2) + 4 * grp + r] = acc1[r];
-					}
+					for (int j = 0; j < kJ; ++j) acc[j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+					for (int t = 0; t < NS; ++t)
+#pragma unroll
+						for (int j = 0; j < kJ; ++j)
+							acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv[j][t], wreg[t], acc[j], 0, 0, 0);
+#pragma unroll
+					for (int j = 0; j < kJ; ++j)
+#pragma unroll
+						for (int r = 0; r < 4; ++r) drow[i * kFbChunk + 16 * (b0 + 2 * j) + 4 * grp + r] = acc[j][r];
 				}
 				__syncthreads();
 			}
@@ -353,7 +361,9 @@ FbLayout fb_layout(const ConvGeom& g, bool dx) {
 	l.wp = g.wo - 1 + g.kw;
 	l.plane = g.cin * l.hp * l.wp;
 	l.plane_pad = (l.plane + 3) / 4 * 4;
-	l.dpitch = l.nchunks * kFbChunk;
+	// four floats past the chunks: a pitch that is a multiple of the 64 banks would put a dcol write's sixteen rows in
+	// one bank
+	l.dpitch = l.nchunks * kFbChunk + 4;
 	l.floats = 2 * (size_t)kFbSlot + (size_t)l.plane_pad + (dx ? (size_t)(l.K + 1) * l.dpitch : 0);
 	return l;
 }
