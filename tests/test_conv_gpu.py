@@ -187,15 +187,15 @@ def test_conv_shape_errors(gpu):
 
 
 def test_conv3x3_lds_path(gpu, oracle):
-    """3x3, stride 1, padding 1 on planes up to 14 x 14 with Cout a multiple of 32 and H*W a multiple of 4 runs
+    """3x3, stride 1, padding 1 on planes up to 14 x 14 with Cout a multiple of 16 and H*W a multiple of 4 runs
     as MFMA chains over the input held in LDS: tiny and rectangular planes, one to fifty input channels, several
-    32-channel groups, ReLU on and off, special values in x, w and the bias. A product that takes nn-cpp's depth
+    32-channel groups and a last group of 16 (cnn_mnist's conv2: 8 -> 16 channels), ReLU on and off, special values in x, w and the bias. A product that takes nn-cpp's depth
     cut (Cin = 60: K = 540, 32 x 64 outputs), H*W = 49 and an unaligned y take the GEMM path instead: same bits."""
     import torch
 
     import nnh
     cases = [(2, 32, 14, 14, 64), (3, 1, 2, 2, 32), (2, 7, 12, 10, 96), (1, 50, 14, 14, 32), (2, 3, 9, 4, 32),
-             (1, 60, 8, 8, 32), (2, 3, 7, 7, 32)]
+             (1, 60, 8, 8, 32), (2, 3, 7, 7, 32), (3, 8, 14, 14, 16), (2, 5, 14, 14, 48), (1, 2, 4, 4, 16)]
     for ci, (N, Cin, H, W, Cout) in enumerate(cases):
         x = synth.mt19937_uniform(300 + ci, N * Cin * H * W).reshape(N, Cin, H, W) * 2 - 1
         w = synth.normal(310 + ci, (Cout, Cin, 3, 3))
