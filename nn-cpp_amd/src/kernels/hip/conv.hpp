@@ -15,7 +15,7 @@ struct ConvGeom {
 hipError_t im2col(const float* x, float* col, const ConvGeom& g, int64_t samples, hipStream_t s);
 hipError_t col2im(const float* col, float* dx, const ConvGeom& g, int64_t samples, int first, hipStream_t s);
 // 3x3, stride 1, padding 1 convolutions of planes up to 14 x 14 as MFMA chains over the input held in LDS
-// (conv_fwd3.hip): whether it takes this forward (no depth cut, Cout a multiple of 16, 16-byte aligned y), and
+// (conv_fwd3.hip): whether it takes this forward (no depth cut, Cout a multiple of 32, 16-byte aligned y), and
 // the launch.
 bool conv_fwd3_ok(const ConvGeom& g, int64_t samples, int cout, const float* y, const unsigned char* alive);
 hipError_t conv_fwd3(const float* x, const float* w, const float* bias, float* y, unsigned char* alive,

@@ -4,7 +4,8 @@
 // The reference computes, per sample, dW_n = g_n col_n^T (sgemm F,T): each element dW_n[co][k] is the fma chain
 // over the output positions p = 0..hw-1 in order from +0 of g_n[co][p] * col_n[k][p], with k = (c, ph, pw) and
 // col_n[k][p] = x_n[c][oh + ph - 1][ow + pw - 1], or 0 in the padding. The caller then sums dW_n over the samples
-// in order. One workgroup here owns one sample, 64 output channels and half of the 16-wide groups of k:
+// in order. One workgroup here owns one sample, 64 output channels (a last group of 16, 32 or 48 when Cout is not a
+// multiple of 64: zero rows past Cout, nothing written for them) and half of the 16-wide groups of k:
 //   * the sample's (masked) gradient rows, [64][197], and its zero-padded input, [Cin][16][19], go to LDS;
 //   * the 64 channels are the A operand of 16x16x1 MFMA units (lane l: channel l), one unit per 16 values of k
 //     (lane l: k = 16 u + (l & 15), whose window offset c*304 + ph*19 + pw is fixed per lane), at most three units
@@ -89,8 +90,11 @@ __global__ void __launch_bounds__(256) conv_dw3_kernel(const D3Args a) {
 	//   gradient rows: thread t covers channel t >> 2 and its 16-byte groups (t & 3) + 4 j (hw % 4 == 0), masked
 	//   here by the ReLU's alive bytes (ops.cpp:1439-1443); the half that owns the channel also writes the masked
 	//   row out for the input gradient.
+	// a last group of fewer than 64 channels (Cout a multiple of 16) stages zero rows past Cout, from clamped
+	// addresses, and writes nothing for them
 	const int gco = tid >> 2, ngq = hw >> 2;
-	const int64_t grow = ((int64_t)n * a.cout + co0 + gco) * hw;  // this thread's gradient row
+	const bool glive = co0 + gco < a.cout;
+	const int64_t grow = ((int64_t)n * a.cout + co0 + min(gco, a.cout - 1 - co0)) * hw;  // this thread's gradient row
 	{
 		const int r = tid >> 4, q = tid & 15, ih = r - 1, iw = q - 1;
 		const bool in = ih >= 0 && ih < a.height && iw >= 0 && iw < a.width;
@@ -112,10 +116,14 @@ __global__ void __launch_bounds__(256) conv_dw3_kernel(const D3Args a) {
 #pragma unroll
 				for (int e = 0; e < 4; ++e) gv[j][e] = ((al[j] >> (8 * e)) & 0xffu) ? gv[j][e] : 0.0f;
 		}
+		if (!glive) {
+#pragma unroll
+			for (int j = 0; j < kD3GQ; ++j) gv[j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+		}
 #pragma unroll
 		for (int u = 0; u < CX; ++u)
 			if (u < a.cin) xs[u * kD3Plane + r * kD3Row + q] = in ? xv[u] : 0.0f;
-		const bool out = a.alive && (gco >> 5) == half;  // uniform per wave
+		const bool out = a.alive && (gco >> 5) == half && glive;  // uniform per wave (Cout is a multiple of 16)
 #pragma unroll
 		for (int j = 0; j < kD3GQ; ++j) {
 			const int gq = (tid & 3) + 4 * j;
@@ -148,7 +156,7 @@ __global__ void __launch_bounds__(256) conv_dw3_kernel(const D3Args a) {
 		float part[8];
 #pragma unroll
 		for (int j = 0; j < 8; ++j) part[j] = __shfl(t, (lane & ~7) + j);
-		if (k == 0) {
+		if (k == 0 && co0 + row < a.cout) {
 			float v = ((part[0] + part[1]) + (part[2] + part[3])) + ((part[4] + part[5]) + (part[6] + part[7]));
 			for (int i = full; i < hw; ++i) v = v + pr[i];
 			a.gb[(int64_t)n * a.cout + co0 + row] = v;
@@ -219,7 +227,8 @@ __global__ void __launch_bounds__(256) conv_dw3_kernel(const D3Args a) {
 		const int k = (g0 + wave + 4 * i) * 16 + M16::ccol(lane);
 		if (k >= K) continue;
 #pragma unroll
-		for (int r = 0; r < M16::NV; ++r) gwn[(int64_t)M16::crow(r, lane) * K + k] = acc[i][r];
+		for (int r = 0; r < M16::NV; ++r)
+			if (co0 + M16::crow(r, lane) < a.cout) gwn[(int64_t)M16::crow(r, lane) * K + k] = acc[i][r];
 	}
 	bias_sums();
 }
@@ -236,7 +245,8 @@ bool conv_dw3_ok(const ConvGeom& g, int64_t samples, int cout, const float* gr, 
 	    g.wo != g.w)
 		return false;
 	const int64_t hw = (int64_t)g.h * g.w, K = (int64_t)g.cin * 9;
-	if (cout % kD3Co != 0 || K > 2 * 4 * kD3Units * 16 || samples * (cout / kD3Co) * 2 > 0x7fffffff) return false;
+	if (cout % 16 != 0 || K > 2 * 4 * kD3Units * 16 || samples * ((cout + kD3Co - 1) / kD3Co) * 2 > 0x7fffffff)
+		return false;
 	// the gradient rows are staged (and the masked rows written) in 16-byte groups, with 4-byte groups of the mask
 	if (hw % 4 != 0 || reinterpret_cast<uintptr_t>(gr) % 16 != 0) return false;
 	if (alive && (reinterpret_cast<uintptr_t>(alive) % 4 != 0 || !gmo || reinterpret_cast<uintptr_t>(gmo) % 16 != 0))
@@ -273,8 +283,9 @@ hipError_t conv_dw3(const float* gr, const unsigned char* alive, float* gmo, flo
 	}
 	const int K = g.cin * 9;
 	const int units = (K + 15) / 16;
-	const int pairs = (int)(samples * (cout / kD3Co));
-	D3Args a{gr, alive, alive ? gmo : nullptr, gb, x, gw, g.cin, g.h, g.w, cout, cout / kD3Co, (units + 1) / 2, pairs};
+	const int cogroups = (cout + kD3Co - 1) / kD3Co;
+	const int pairs = (int)(samples * cogroups);
+	D3Args a{gr, alive, alive ? gmo : nullptr, gb, x, gw, g.cin, g.h, g.w, cout, cogroups, (units + 1) / 2, pairs};
 	static_assert(kD3GQ * 4 * 4 >= 14 * 14, "a thread's groups cover a gradient row of a 14 x 14 plane");
 	static_assert(2 * 4 * kD3Units * 16 / 9 <= 48, "every accepted depth has at most 48 input channels");
 	hipLaunchKernelGGL(kernels[g.cin <= 32 ? 0 : 1][g.w - 1], dim3((unsigned)(samples * a.cogroups * 2)), dim3(256),

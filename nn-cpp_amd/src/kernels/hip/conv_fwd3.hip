@@ -14,9 +14,7 @@
 //     operands are read while the previous channel's MFMAs run;
 //   * the epilogue adds the bias, applies the ReLU and writes y and the alive flags four positions per store.
 // Each output is the reference's chain, padding taps included as fma(w, 0, acc): the same bits as the
-// implicit-im2col GEMM. Taken when Cout is a multiple of 16, the product takes no depth cut and the buffers suit
-// 16-byte stores; in a last group of 16 channels the other unit's W rows are staged as zeros and its outputs are not
-// written.
+// implicit-im2col GEMM. Taken when the product takes no depth cut and the buffers suit 16-byte stores.
 #include "conv.hpp"
 
 #include <algorithm>
@@ -81,7 +79,7 @@ __global__ void __launch_bounds__(256) conv_fwd3_kernel(const F3Args a) {
 		for (int u = 0; u < kW; ++u) {
 			const int e = min(tid + 256 * u, nw - 1);
 			const int j = (int)fdiv((unsigned)e, a.spandiv[cb == 0 ? 0 : 1]), kk = e - j * (ce - cb) * 9;
-			wv[u] = co0 + j < a.cout ? wg[min(j, a.cout - 1 - co0) * K + cb * 9 + kk] : 0.0f;
+			wv[u] = wg[j * K + cb * 9 + kk];
 		}
 	};
 	auto store_half = [&](int cb, int ce) {
@@ -197,7 +195,7 @@ bool conv_fwd3_ok(const ConvGeom& g, int64_t samples, int cout, const float* y, 
 	if (g.kh != 3 || g.kw != 3 || g.stride != 1 || g.pad != 1 || g.h > 14 || g.w > 14 || g.ho != g.h || g.wo != g.w)
 		return false;
 	const int64_t hw = (int64_t)g.h * g.w, K = (int64_t)g.cin * 9;
-	if (hw % 4 != 0 || cout % 16 != 0 || samples * ((cout + kF3Co - 1) / kF3Co) > 0x7fffffff) return false;
+	if (hw % 4 != 0 || cout % kF3Co != 0 || samples * (cout / kF3Co) > 0x7fffffff) return false;
 	if (depth_cut(cout, hw, K)) return false;  // the reference splits such products into 128-deep pieces
 	if (f3_lds_bytes(g.cin) > (size_t)kF3MaxLds || g.cin > 80) return false;  // a half stages <= 40 channels
 	if (reinterpret_cast<uintptr_t>(y) % 16 != 0 || (alive && reinterpret_cast<uintptr_t>(alive) % 4 != 0)) return false;
@@ -225,7 +223,7 @@ hipError_t conv_fwd3(const float* x, const float* w, const float* bias, float* y
 		}
 	}
 	const int c1 = (g.cin + 1) / 2;
-	F3Args a{x, w, bias, y, alive, g.cin, g.h, g.w, cout, (cout + kF3Co - 1) / kF3Co, relu,
+	F3Args a{x, w, bias, y, alive, g.cin, g.h, g.w, cout, cout / kF3Co, relu,
 	         {make_fastdiv((unsigned)(c1 * 9)), make_fastdiv((unsigned)(std::max(g.cin - c1, 1) * 9))}};
 	if (c1 <= 16) hipLaunchKernelGGL(conv_fwd3_kernel<16>, dim3((unsigned)(samples * a.groups)), dim3(256), lds, s, a);
 	else hipLaunchKernelGGL(conv_fwd3_kernel<40>, dim3((unsigned)(samples * a.groups)), dim3(256), lds, s, a);
